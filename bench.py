@@ -1,0 +1,248 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantised-linear hot path on one MI355X.
+
+Headline (BASELINE.json metric "decode tok/s & GEMV HBM GB/s (int8/int4);
+prefill int8 TOPS vs MFMA peak", workload configs[1]): one step is one pass
+of the full int8 linear (outlier-aware activation quant + i8 dot + epilogue,
+Bundle::mm's I8 arm) at M=1 over the five (K,N) shapes of the isolated
+int8 sweep, inputs already resident in HBM.  `value` is the step's
+algorithmic bytes (N*K + 4N + 4K + 4N per shape) over its wall time on the
+GPU stream, in GB/s.  Weights are rotated over 3 replica sets (786 MB, over
+the 256 MB MALL) so repeats are served from HBM.
+
+Also reported (in "detail"): the GEMV kernel alone on pre-quantised input
+(its roofline), the M=2048 MFMA-bound shapes in TOPS, the int4 decode GEMV
+on Gemma-2 shapes, and the config-4 MoE layer.  The CPU baseline is the
+oracle's restatement of the reference's scalar int8 path (the
+`_scalar_i8_bench` build) on the host's cores, on a bounded sample.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+METRIC = "decode tok/s & GEMV HBM GB/s (int8/int4); prefill int8 TOPS vs MFMA peak"
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+
+
+def int8_linear_bytes(m, k, n):
+    return n * k + 4 * n + 4 * m * k + 4 * m * n
+
+
+def gemv_kernel_bytes(m, k, n):
+    # weights + scale + a8 + sa + 32 outliers (idx, val) per row + f32 out
+    return n * k + 4 * n + m * k + m * (4 + 32 * 8) + 4 * m * n
+
+
+def int4_bytes(m, k, n, g=32):
+    return n * k // 2 + 2 * n * ((k + g - 1) // g) + 4 * m * k + 4 * m * n
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--replicas", type=int, default=3)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-detail", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path "
+              "(collectives are out of scope); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import fieldrun_amd as fa
+    from fieldrun_amd import hip, synth
+
+    ctx = fa.Context(0)
+    stream = fa.lib.frq_get_stream(ctx.h)
+    log = lambda *a: print("[bench]", *a, file=sys.stderr, flush=True)
+
+    def time_loop(fn, iters, warm=3):
+        for i in range(warm):
+            fn(i)
+        hip.synchronize()
+        e0, e1 = hip.Event(), hip.Event()
+        e0.record(stream)
+        for i in range(iters):
+            fn(i)
+        e1.record(stream)
+        e1.synchronize()
+        ctx.sync()
+        return e0.elapsed_ms(e1) / iters
+
+    # ---------------- headline: M=1 int8 sweep, full linear ----------------
+    R = args.replicas
+    shapes = list(synth.SWEEP_KN)
+    weights, host_w0, acts, outs = [], [], [], []
+    t0 = time.time()
+    for si, (k, n) in enumerate(shapes):
+        reps = []
+        for r in range(R):
+            wt, scale = synth.int8_weight(n, k, synth.seed(1, r) + si)
+            reps.append(ctx.upload_i8(wt, scale))
+            if r == 0:
+                host_w0.append((wt, scale))
+        weights.append(reps)
+        a = synth.activations(1, k, synth.seed(1) + si)
+        acts.append((a, hip.DeviceArray.from_numpy(a)))
+        outs.append(hip.DeviceArray((1, n), np.float32))
+    log(f"uploaded {R} replicas of {len(shapes)} shapes in {time.time() - t0:.1f}s")
+
+    def step(i):
+        for si in range(len(shapes)):
+            w = weights[si][i % R]
+            w.mm_dev(acts[si][1].ptr, 1, outs[si].ptr)
+
+    for i in range(args.warmup):
+        step(i)
+    hip.synchronize()
+    e0, e1 = hip.Event(), hip.Event()
+    e0.record(stream)
+    for i in range(args.steps):
+        step(i)
+    e1.record(stream)
+    e1.synchronize()
+    ctx.sync()
+    ms_total = e0.elapsed_ms(e1)
+    ms_step = ms_total / args.steps
+    step_bytes = sum(int8_linear_bytes(1, k, n) for k, n in shapes)
+    value = step_bytes / (ms_step * 1e-3) / 1e9
+    log(f"M=1 sweep: {ms_step * 1e3:.1f} us/step, {value:.0f} GB/s")
+
+    # correctness spot check of the timed outputs against the oracle-free
+    # path: the host entry point (same kernels) on replica (steps-1) % R
+    detail = {"int8_m1_full_linear": {}, "int8_m1_gemv_kernel": {}}
+    for si, (k, n) in enumerate(shapes):
+        w = weights[si][0]
+        us = time_loop(lambda i, w=w, si=si: weights[si][i % R].mm_dev(acts[si][1].ptr, 1, outs[si].ptr), 30) * 1e3
+        detail["int8_m1_full_linear"][f"K{k}_N{n}"] = {
+            "us": round(us, 2), "GBps": round(int8_linear_bytes(1, k, n) / (us * 1e-6) / 1e9, 1)}
+
+    # ---------------- roofline: the GEMV kernel on pre-quantised input -------------
+    gemv_rows = {}
+    for si, (k, n) in enumerate(shapes):
+        kp = fa.quant_pitch(k)
+        a8 = hip.DeviceArray((1, kp), np.int8)
+        sa = hip.DeviceArray((1,), np.float32)
+        oi = hip.DeviceArray((1, 32), np.uint32)
+        ov = hip.DeviceArray((1, 32), np.float32)
+        ctx.quant_dev(acts[si][1].ptr, 1, k, a8.ptr, sa.ptr, oi.ptr, ov.ptr)
+        us = time_loop(lambda i, si=si: weights[si][i % R].mm_q_dev(a8.ptr, sa.ptr, oi.ptr, ov.ptr, 1,
+                                                                   outs[si].ptr), 60) * 1e3
+        gb = gemv_kernel_bytes(1, k, n) / (us * 1e-6) / 1e9
+        gemv_rows[(k, n)] = (us, gb)
+        detail["int8_m1_gemv_kernel"][f"K{k}_N{n}"] = {"us": round(us, 2), "GBps": round(gb, 1),
+                                                       "frac": round(gb / HBM_PEAK_GBS, 3)}
+        qus = time_loop(lambda i, si=si: ctx.quant_dev(acts[si][1].ptr, 1, k, a8.ptr, sa.ptr, oi.ptr,
+                                                       ov.ptr), 60) * 1e3
+        detail["int8_m1_gemv_kernel"][f"K{k}_N{n}"]["quant_us"] = round(qus, 2)
+    dom = max(shapes, key=lambda s: s[0] * s[1])  # (896, 151936): 136 MB per launch
+    us_dom, gb_dom = gemv_rows[dom]
+    roofline = {"bound": "hbm", "achieved": round(gb_dom, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gb_dom / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": f"gemv_i8_kernel (M=1, K={dom[0]}, N={dom[1]})",
+                "bytes_per_launch": gemv_kernel_bytes(1, *dom), "us_per_launch": round(us_dom, 2)}
+
+    if not args.no_detail:
+        # ---------------- prefill: M=2048 MFMA-bound shapes ----------------
+        detail["int8_m2048_gemm"] = {}
+        for (k, n) in [(4096, 14336), (14336, 4096)]:
+            wt, scale = synth.int8_weight(n, k, synth.seed(1, 7))
+            w = ctx.upload_i8(wt, scale)
+            del wt
+            a = synth.activations(2048, k, synth.seed(1, 8))
+            da = hip.DeviceArray.from_numpy(a)
+            do = hip.DeviceArray((2048, n), np.float32)
+            us = time_loop(lambda i: w.mm_dev(da.ptr, 2048, do.ptr), 10) * 1e3
+            kp = fa.quant_pitch(k)
+            a8 = hip.DeviceArray((2048, kp), np.int8)
+            sa = hip.DeviceArray((2048,), np.float32)
+            oi = hip.DeviceArray((2048, 32), np.uint32)
+            ov = hip.DeviceArray((2048, 32), np.float32)
+            ctx.quant_dev(da.ptr, 2048, k, a8.ptr, sa.ptr, oi.ptr, ov.ptr)
+            gus = time_loop(lambda i: w.mm_q_dev(a8.ptr, sa.ptr, oi.ptr, ov.ptr, 2048, do.ptr), 10) * 1e3
+            ops = 2.0 * 2048 * n * k
+            detail["int8_m2048_gemm"][f"K{k}_N{n}"] = {
+                "full_linear_us": round(us, 1), "full_linear_TOPS": round(ops / (us * 1e-6) / 1e12, 1),
+                "gemm_us": round(gus, 1), "gemm_TOPS": round(ops / (gus * 1e-6) / 1e12, 1),
+                "gemm_frac_int8_peak": round(ops / (gus * 1e-6) / 1e12 / INT8_PEAK_TOPS, 3)}
+            log(f"M=2048 K={k} N={n}: {detail['int8_m2048_gemm'][f'K{k}_N{n}']}")
+            w.free()
+        # ---------------- int4 decode GEMV (Gemma-2-2b shapes) ----------------
+        detail["int4_m1_gemv"] = {}
+        for (k, n) in [(2304, 9216), (9216, 2304), (2304, 2048)]:
+            reps = []
+            for r in range(3):
+                packed, s16, g = synth.int4_weight(n, k, synth.seed(2, r))
+                reps.append(ctx.upload_i4(packed, s16, k, g))
+            a = synth.activations(1, k, synth.seed(2, 9), outlier_scale=1.0)
+            da = hip.DeviceArray.from_numpy(a)
+            do = hip.DeviceArray((1, n), np.float32)
+            us = time_loop(lambda i: reps[i % 3].mm_dev(da.ptr, 1, do.ptr), 60) * 1e3
+            gb = int4_bytes(1, k, n) / (us * 1e-6) / 1e9
+            detail["int4_m1_gemv"][f"K{k}_N{n}"] = {"us": round(us, 2), "GBps": round(gb, 1),
+                                                    "frac": round(gb / HBM_PEAK_GBS, 3)}
+            for w in reps:
+                w.free()
+        # ---------------- MoE layer (config 4) ----------------
+        detail["moe_qwen3_layer"] = {}
+        E, d, mi, topk = 128, 2048, 768, 8
+        gate, gs, up, us_, down, ds = synth.moe_layer(E, d, mi, synth.seed(3))
+        bank = ctx.upload_moe_i8(gate, gs, up, us_, down, ds)
+        for T in (1, 512):
+            rng = np.random.default_rng(synth.seed(3, T))
+            x = hip.DeviceArray.from_numpy(rng.standard_normal((T, d), dtype=np.float32))
+            lg = hip.DeviceArray.from_numpy(rng.standard_normal((T, E), dtype=np.float32))
+            o = hip.DeviceArray((T, d), np.float32)
+            us = time_loop(lambda i: bank.forward_dev(x.ptr, T, lg.ptr, topk, True, None, o.ptr), 10) * 1e3
+            detail["moe_qwen3_layer"][f"T{T}"] = {"us": round(us, 1),
+                                                  "flops_TF": round(2 * T * topk * 3 * d * mi / (us * 1e-6) / 1e12, 2)}
+        bank.free()
+
+    # ---------------- CPU baseline (the oracle's scalar restatement) ----------------
+    cpu = None
+    if not args.no_cpu:
+        import oracle  # the CPU baseline leg: the reference's scalar i8 path restated in C
+
+        threads = min(os.cpu_count() or 1, 16)
+        t_end = time.time() + args.cpu_seconds
+        iters, t_start = 0, time.time()
+        while True:
+            for si, (k, n) in enumerate(shapes):
+                wt, scale = host_w0[si]
+                oracle.mm_i8_mt(acts[si][0], wt, scale, threads)
+            iters += 1
+            if time.time() >= t_end:
+                break
+        el = time.time() - t_start
+        cpu_gbs = iters * step_bytes / el / 1e9
+        cpu = {"value": round(cpu_gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+               "sample": f"{iters} passes of the M=1 int8 sweep (5 shapes, replica 0) in {el:.1f}s; "
+                         f"oracle fro_mm_i8_mt: scalar i8dot built -O3 -march=x86-64, rayon-style split over N"}
+        log(f"CPU baseline {cpu_gbs:.2f} GB/s on {threads} threads")
+
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "configs[1] isolated int8 linear sweep at M=1 (decode): full linear "
+                               "(outlier-aware per-token quant + i8 dot + scale epilogue) over "
+                               "(K,N) in " + str(shapes) + f", {R} weight replicas rotated",
+                   "m": 1, "shapes": [list(s) for s in shapes]},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "detail": detail,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,291 @@
+"""fieldrun_amd — MI355X (gfx950) quantised-linear hot path of fieldrun.
+
+Python binding of libfrq.so (include/frq.h) through ctypes.  The library is
+the product: there is no CPU fallback, and importing this package raises if
+libfrq.so has not been built (``python fieldrun_amd/build.py``).
+
+The classes mirror the reference's interface for this path
+(/root/reference/src/bundle.rs):
+
+  Weight.mm(a)            Bundle::mm(a, name) for one int8 / int4 weight
+                          (src/bundle.rs:644-919)
+  MoeBank.forward(...)    the routed expert branch of qwen3moe::moe_branch
+                          (src/qwen3moe.rs:120-158) / gemma4 (131-187)
+  MoeBank.expert_mm(...)  Bundle::expert_mm (src/bundle.rs:457-461)
+
+Errors the reference raises by panicking come back as FrqError carrying the
+library's status code and message.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libfrq.so")
+
+FRQ_OK, FRQ_ERR_ARG, FRQ_ERR_HIP, FRQ_ERR_NAN = 0, 1, 2, 3
+FRQ_ERR_DTYPE, FRQ_ERR_FORMAT, FRQ_ERR_MISSING, FRQ_ERR_NODEV = 4, 5, 6, 7
+FRQ_DT_I8, FRQ_DT_I4 = 1, 2
+FRQ_ACT_SILU, FRQ_ACT_GELU_TANH = 0, 1
+
+# name -> (restype, argtypes); every symbol include/frq.h declares
+_P, _S, _I = C.c_void_p, C.c_size_t, C.c_int
+SIGNATURES = {
+    "frq_last_error": (C.c_char_p, []),
+    "frq_version": (C.c_char_p, []),
+    "frq_device_count": (_I, []),
+    "frq_init": (_P, [_I]),
+    "frq_free": (None, [_P]),
+    "frq_set_stream": (_I, [_P, _P]),
+    "frq_get_stream": (_P, [_P]),
+    "frq_sync": (_I, [_P]),
+    "frq_upload_i8": (_P, [_P, _P, _P, _S, _S]),
+    "frq_upload_i8_bundle": (_P, [_P, _P, _P, _S, _S]),
+    "frq_upload_i4": (_P, [_P, _P, _P, _S, _S, _S]),
+    "frq_w_free": (None, [_P]),
+    "frq_w_info": (_I, [_P, _P, _P, _P, _P]),
+    "frq_mm": (_I, [_P, _P, _P, _S, _P]),
+    "frq_mm_dev": (_I, [_P, _P, _P, _S, _P]),
+    "frq_mm_i8_debug": (_I, [_P, _P, _P, _S, _P, _P, _P, _P, _P, _P]),
+    "frq_quant_pitch": (_S, [_S]),
+    "frq_quant_i8_dev": (_I, [_P, _P, _S, _S, _P, _P, _P, _P]),
+    "frq_mm_i8_q_dev": (_I, [_P, _P, _P, _P, _P, _P, _S, _P]),
+    "frq_moe_upload_i8": (_P, [_P, _S, _S, _S, _I, _P, _P, _P, _P, _P, _P]),
+    "frq_moe_free": (None, [_P]),
+    "frq_moe": (_I, [_P, _P, _P, _S, _P, _S, _I, _P, _P]),
+    "frq_moe_dev": (_I, [_P, _P, _P, _S, _P, _S, _I, _P, _P]),
+    "frq_moe_route": (_I, [_P, _P, _S, _S, _S, _I, _P, _P, _P]),
+    "frq_expert_mm": (_I, [_P, _P, _I, _S, _P, _S, _P]),
+}
+
+
+class FrqError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"frq error {code}: {msg}")
+        self.code = code
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} is missing: build it with `python fieldrun_amd/build.py` "
+            "(the HIP library is the only implementation; there is no CPU fallback)")
+    lib = C.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        f = getattr(lib, name)
+        f.restype = res
+        f.argtypes = args
+    return lib
+
+
+lib = _load()
+
+
+def _ptr(a: np.ndarray | None):
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def _check(rc: int):
+    if rc != FRQ_OK:
+        raise FrqError(rc, lib.frq_last_error().decode())
+
+
+def device_count() -> int:
+    return lib.frq_device_count()
+
+
+def quant_pitch(k: int) -> int:
+    return lib.frq_quant_pitch(k)
+
+
+class Context:
+    """One device, one stream, one workspace (frq_ctx)."""
+
+    def __init__(self, device: int = 0):
+        self.h = lib.frq_init(device)
+        if not self.h:
+            raise FrqError(FRQ_ERR_NODEV, lib.frq_last_error().decode())
+        self.device = device
+
+    def close(self):
+        if self.h:
+            lib.frq_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_stream(self, stream_handle: int | None):
+        _check(lib.frq_set_stream(self.h, stream_handle))
+
+    def sync(self):
+        _check(lib.frq_sync(self.h))
+
+    def quant_dev(self, a_ptr: int, m: int, k: int, a8_ptr: int, sa_ptr: int, oidx_ptr: int,
+                  oval_ptr: int):
+        """Activation quant of the I8 arm on device pointers (a8 pitch quant_pitch(k))."""
+        _check(lib.frq_quant_i8_dev(self.h, a_ptr, m, k, a8_ptr, sa_ptr, oidx_ptr, oval_ptr))
+
+    # ---- uploads ----
+    def upload_i8(self, wt_nk: np.ndarray, scale: np.ndarray) -> "Weight":
+        wt_nk = np.ascontiguousarray(wt_nk, dtype=np.int8)
+        scale = np.ascontiguousarray(scale, dtype=np.float32)
+        n, k = wt_nk.shape
+        h = lib.frq_upload_i8(self.h, _ptr(wt_nk), _ptr(scale), n, k)
+        if not h:
+            raise FrqError(FRQ_ERR_HIP, lib.frq_last_error().decode())
+        return Weight(self, h, FRQ_DT_I8, n, k)
+
+    def upload_i8_bundle(self, w_kn: np.ndarray, scale_f16: np.ndarray) -> "Weight":
+        w_kn = np.ascontiguousarray(w_kn, dtype=np.int8)
+        s = np.ascontiguousarray(scale_f16, dtype=np.float16).view(np.uint16)
+        k, n = w_kn.shape
+        h = lib.frq_upload_i8_bundle(self.h, _ptr(w_kn), _ptr(s), k, n)
+        if not h:
+            raise FrqError(FRQ_ERR_HIP, lib.frq_last_error().decode())
+        return Weight(self, h, FRQ_DT_I8, n, k)
+
+    def upload_i4(self, packed: np.ndarray, scale_f16: np.ndarray, k: int, g: int) -> "Weight":
+        packed = np.ascontiguousarray(packed, dtype=np.uint8)
+        s = np.ascontiguousarray(scale_f16, dtype=np.float16).view(np.uint16)
+        n = packed.shape[0]
+        h = lib.frq_upload_i4(self.h, _ptr(packed), _ptr(s), n, k, g)
+        if not h:
+            raise FrqError(FRQ_ERR_HIP, lib.frq_last_error().decode())
+        return Weight(self, h, FRQ_DT_I4, n, k, g)
+
+    def upload_moe_i8(self, gate, gate_scale, up, up_scale, down, down_scale,
+                      act: int = FRQ_ACT_SILU) -> "MoeBank":
+        """Lists over experts of (in,out) int8 arrays and f32 [out] scales."""
+        E = len(gate)
+        d, gw = gate[0].shape
+        mi = down[0].shape[0]
+        keep = []
+
+        def arr(lst, dt):
+            ptrs = (C.c_void_p * E)()
+            for i, a in enumerate(lst):
+                a = np.ascontiguousarray(a, dtype=dt)
+                keep.append(a)
+                ptrs[i] = a.ctypes.data
+            return ptrs
+
+        g_p, gs_p = arr(gate, np.int8), arr(gate_scale, np.float32)
+        d_p, ds_p = arr(down, np.int8), arr(down_scale, np.float32)
+        if act == FRQ_ACT_SILU:
+            u_p, us_p = arr(up, np.int8), arr(up_scale, np.float32)
+        else:
+            u_p = us_p = None
+        h = lib.frq_moe_upload_i8(self.h, E, d, mi, act, g_p, gs_p, u_p, us_p, d_p, ds_p)
+        if not h:
+            raise FrqError(FRQ_ERR_HIP, lib.frq_last_error().decode())
+        return MoeBank(self, h, E, d, mi, act)
+
+    def moe_route(self, logits: np.ndarray, topk: int, norm_topk: bool = True,
+                  per_expert_scale: np.ndarray | None = None):
+        logits = np.ascontiguousarray(logits, dtype=np.float32)
+        T, E = logits.shape
+        sel = np.empty((T, topk), np.int32)
+        w = np.empty((T, topk), np.float32)
+        pes = None if per_expert_scale is None else np.ascontiguousarray(per_expert_scale, np.float32)
+        _check(lib.frq_moe_route(self.h, _ptr(logits), T, E, topk, int(norm_topk), _ptr(pes),
+                                 _ptr(sel), _ptr(w)))
+        return sel, w
+
+
+class Weight:
+    """A weight resident in HBM (frq_w)."""
+
+    def __init__(self, ctx: Context, h, dtype: int, n: int, k: int, g: int = 0):
+        self.ctx, self.h, self.dtype, self.n, self.k, self.g = ctx, h, dtype, n, k, g
+
+    def free(self):
+        if self.h:
+            lib.frq_w_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def mm(self, a: np.ndarray) -> np.ndarray:
+        """Bundle::mm: (M,K) f32 -> (M,N) f32."""
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        if a.ndim != 2 or a.shape[1] != self.k:
+            raise FrqError(FRQ_ERR_ARG, f"activation shape {a.shape} does not match K={self.k}")
+        out = np.empty((a.shape[0], self.n), np.float32)
+        _check(lib.frq_mm(self.ctx.h, self.h, _ptr(a), a.shape[0], _ptr(out)))
+        return out
+
+    def mm_dev(self, a_ptr: int, m: int, out_ptr: int):
+        """Device-pointer variant, enqueued on the context stream."""
+        _check(lib.frq_mm_dev(self.ctx.h, self.h, a_ptr, m, out_ptr))
+
+    def mm_q_dev(self, a8_ptr: int, sa_ptr: int, oidx_ptr: int, oval_ptr: int, m: int, out_ptr: int):
+        """int8 dot + epilogue on a batch quantised by Context.quant_dev."""
+        _check(lib.frq_mm_i8_q_dev(self.ctx.h, self.h, a8_ptr, sa_ptr, oidx_ptr, oval_ptr, m, out_ptr))
+
+    def mm_debug(self, a: np.ndarray):
+        """int8: (out, acc, a8, sa, oidx, oval) — the reference's locals."""
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        m = a.shape[0]
+        out = np.empty((m, self.n), np.float32)
+        acc = np.empty((m, self.n), np.int32)
+        a8 = np.empty((m, self.k), np.int8)
+        sa = np.empty(m, np.float32)
+        oi = np.empty((m, 32), np.uint32)
+        ov = np.empty((m, 32), np.float32)
+        _check(lib.frq_mm_i8_debug(self.ctx.h, self.h, _ptr(a), m, _ptr(out), _ptr(acc),
+                                   _ptr(a8), _ptr(sa), _ptr(oi), _ptr(ov)))
+        return out, acc, a8, sa, oi, ov
+
+
+class MoeBank:
+    """All routed experts of one layer, resident in HBM (frq_moe_w)."""
+
+    def __init__(self, ctx, h, E, d, mi, act):
+        self.ctx, self.h, self.E, self.d, self.mi, self.act = ctx, h, E, d, mi, act
+
+    def free(self):
+        if self.h:
+            lib.frq_moe_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def forward(self, x: np.ndarray, logits: np.ndarray, topk: int, norm_topk: bool = True,
+                per_expert_scale: np.ndarray | None = None) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        logits = np.ascontiguousarray(logits, dtype=np.float32)
+        T = x.shape[0]
+        out = np.empty((T, self.d), np.float32)
+        pes = None if per_expert_scale is None else np.ascontiguousarray(per_expert_scale, np.float32)
+        _check(lib.frq_moe(self.ctx.h, self.h, _ptr(x), T, _ptr(logits), topk, int(norm_topk),
+                           _ptr(pes), _ptr(out)))
+        return out
+
+    def forward_dev(self, x_ptr, T, logits_ptr, topk, norm_topk, pes_ptr, out_ptr):
+        _check(lib.frq_moe_dev(self.ctx.h, self.h, x_ptr, T, logits_ptr, topk, int(norm_topk),
+                               pes_ptr, out_ptr))
+
+    def expert_mm(self, which: int, e: int, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out_dim = {0: self.mi if self.act == FRQ_ACT_SILU else 2 * self.mi, 1: self.mi, 2: self.d}[which]
+        y = np.empty((x.shape[0], out_dim), np.float32)
+        _check(lib.frq_expert_mm(self.ctx.h, self.h, which, e, _ptr(x), x.shape[0], _ptr(y)))
+        return y

@@ -1,0 +1,120 @@
+// frq_internal.h — shared definitions of the gfx950 kernel library.
+//
+// Device layouts (all in HBM, uploaded once):
+//   int8 weight  wt   (Np, Kp) i8 row-major, K contiguous; Kp = K rounded up
+//                     to 128 and Np = N rounded up to 256, padding zero.
+//                wkn  (Kp, Np) i8 row-major: the bundle's (in, out) layout,
+//                     read by the GEMM's outlier correction.
+//                scale (Np) f32.
+//   int4 weight  blk  64-row blocks: for block b, group gi, row r: the 16
+//                     bytes (32 nibbles) of row 64b+r, group gi, at
+//                     ((b*ng + gi)*64 + r)*16  (g == 32, K % 32 == 0), or
+//                     the bundle's own (N, ceil(K/2)) rows otherwise.
+//                scale (N, ng) f16 in the same blocked order / as stored.
+//   activations  a8   (Mp, Kp) i8 per call (workspace), sa (M) f32,
+//                     oidx/oval (M, 32) u32/f32, outliers in ascending channel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/frq.h"
+
+#define FRQ_T 32            // OUTLIER_T (src/bundle.rs:309)
+#define FRQ_KALIGN 128      // Kp alignment (a multiple of the GEMM k-step)
+#define FRQ_NALIGN 256      // Np alignment (a multiple of every N tile)
+#define FRQ_MALIGN 128      // Mp alignment of the a8 workspace (GEMM M tile)
+
+namespace frq {
+
+inline size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+
+// 128-bit streaming (non-temporal) load of a weight chunk.
+__device__ __forceinline__ int4 ntload16(const void* p) {
+    const v4i v = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p));
+    return make_int4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint4 ntload16u(const void* p) {
+    const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// IEEE binary16 -> binary32 (exact).
+__device__ __forceinline__ float h2f(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// ---- weights -------------------------------------------------------------
+struct Weight {
+    int dtype = 0;           // FRQ_DT_I8 / FRQ_DT_I4
+    int device = 0;
+    size_t n = 0, k = 0, g = 0;
+    size_t np = 0, kp = 0;   // padded dims (int8)
+    int8_t* wt = nullptr;    // int8 (Np, Kp)
+    int8_t* wkn = nullptr;   // int8 (Kp, Np): the bundle's (in, out) layout
+    float* scale = nullptr;  // int8 scale (Np)
+    uint8_t* q4 = nullptr;   // int4 blocked (64-row blocks), when i4_blocked
+    uint16_t* s4 = nullptr;  // int4 f16 scales, blocked
+    uint8_t* q4raw = nullptr;   // int4 packed (N, ceil(K/2)) as stored
+    uint16_t* s4raw = nullptr;  // int4 f16 scales (N, ceil(K/g)) as stored
+    int i4_blocked = 0;      // 1 when the blocked g=32 layout is used
+};
+
+struct MoeBank {
+    int device = 0;
+    size_t n_exp = 0, d = 0, mi = 0;
+    int act = 0;
+    size_t gw = 0;               // gate width: mi (SiLU) or 2*mi (gate_up)
+    int8_t* gate = nullptr;      // (E, d, gw) i8 (in,out) row-major per expert
+    float* gate_s = nullptr;     // (E, gw)
+    int8_t* up = nullptr;        // (E, d, mi)
+    float* up_s = nullptr;       // (E, mi)
+    int8_t* down = nullptr;      // (E, mi, d)
+    float* down_s = nullptr;     // (E, d)
+};
+
+// ---- kernel launchers (each returns hipError_t of the launch) ------------
+// Activation quant of M rows of K f32 (row pitch K) into a8 (pitch kp).
+hipError_t launch_quant(const float* a, size_t m, size_t k, size_t kp,
+                        int8_t* a8, float* sa, uint32_t* oidx, float* oval,
+                        int* err, hipStream_t s);
+// int8 GEMV for 1 <= m <= 4.
+hipError_t launch_gemv_i8(const Weight& w, size_t m, const int8_t* a8,
+                          const float* sa, const uint32_t* oidx,
+                          const float* oval, float* out, int32_t* acc,
+                          hipStream_t s);
+// Union of outlier channels per M tile and their 3-digit int8 split.
+size_t gemm_union_bytes(size_t m, size_t k);
+hipError_t launch_union(size_t m, size_t k, const uint32_t* oidx,
+                        const float* oval, void* ubuf, hipStream_t s);
+// int8 MFMA GEMM for m > 4.
+hipError_t launch_gemm_i8(const Weight& w, size_t m, const int8_t* a8,
+                          const float* sa, const uint32_t* oidx,
+                          const float* oval, const void* ubuf, float* out,
+                          int32_t* acc, hipStream_t s);
+// int4 linear (any m).
+hipError_t launch_i4(const Weight& w, size_t m, const float* a, float* out,
+                     float* wsf, hipStream_t s);
+size_t i4_ws_floats(const Weight& w, size_t m);
+// int4 (N, K/2) -> 64-row blocked layout (g == 32, K % 32 == 0).
+hipError_t launch_i4_block(const uint8_t* raw, const uint16_t* sraw, size_t n,
+                           size_t k, uint8_t* blk, uint16_t* sblk,
+                           hipStream_t s);
+// MoE.
+size_t moe_ws_bytes(const MoeBank& b, size_t T, size_t topk);
+hipError_t launch_moe(const MoeBank& b, const float* x, size_t T,
+                      const float* logits, size_t topk, int norm_topk,
+                      const float* pes, float* out, void* ws, int* err,
+                      hipStream_t s);
+hipError_t launch_moe_route(const float* logits, size_t T, size_t E,
+                            size_t topk, int norm_topk, const float* pes,
+                            int32_t* sel, float* w, int* err, hipStream_t s);
+hipError_t launch_expert_mm(const int8_t* q, const float* s, size_t inp,
+                            size_t out, const float* x, size_t m, float* y,
+                            hipStream_t st);
+
+}  // namespace frq

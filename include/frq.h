@@ -1,0 +1,169 @@
+/*
+ * frq.h — C ABI of the MI355X (gfx950) quantised-linear library (libfrq.so).
+ *
+ * This is the drop-in boundary for fieldrun's quantised-linear hot path.  A
+ * host (the reference's Rust Bundle through a thin FFI crate, the C++
+ * frq::Bundle in fieldrun_amd/csrc/bundle.cpp, or Python ctypes) uploads each
+ * weight once into HBM and then calls the linear / expert entry points with
+ * plain pointers and sizes.  No torch or HIP types appear in the signatures:
+ * streams and device buffers are passed as void*.
+ *
+ * Citations are to the reference crate (/root/reference, fieldrun 0.1.0).
+ *
+ * Conventions
+ *  - Every entry point returns an int status (FRQ_OK = 0) or a NULL handle;
+ *    frq_last_error() then returns a one-line message (thread-local).  The
+ *    reference panics in the same situations (src/bundle.rs:370, 378-380,
+ *    703, 737, 917); nothing unwinds across this ABI.
+ *  - A frq_ctx owns one HIP stream and a workspace on one device.  Calls on
+ *    one ctx must not overlap (one ctx per host thread, as the reference's
+ *    Bundle is shared `&self` across rayon workers, src/model.rs:258).
+ *    Weight handles (frq_w, frq_moe_w) are immutable after upload and may be
+ *    used from any ctx on the same device.
+ *  - "Host" entry points take host pointers, copy in, compute and copy out,
+ *    and return after the result is on the host.  "_dev" entry points take
+ *    device pointers, enqueue on the ctx stream and return immediately;
+ *    their data-dependent errors (NaN activations) are reported by the next
+ *    frq_sync().
+ */
+#ifndef FRQ_H
+#define FRQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    FRQ_OK = 0,
+    FRQ_ERR_ARG = 1,     /* bad argument / shape mismatch                  */
+    FRQ_ERR_HIP = 2,     /* HIP runtime error (allocation, launch, copy)   */
+    FRQ_ERR_NAN = 3,     /* NaN activation: bundle.rs:703/737 unwrap panic */
+    FRQ_ERR_DTYPE = 4,   /* weight dtype not valid for this call (:370,917) */
+    FRQ_ERR_FORMAT = 5,  /* bad bundle manifest (bundle.rs:316-321)        */
+    FRQ_ERR_MISSING = 6, /* missing array (bundle.rs:378-380)              */
+    FRQ_ERR_NODEV = 7    /* no HIP device / library built without GPU      */
+};
+
+enum { FRQ_DT_I8 = 1, FRQ_DT_I4 = 2 };
+enum { FRQ_ACT_SILU = 0, FRQ_ACT_GELU_TANH = 1 };
+
+typedef struct frq_ctx frq_ctx;
+typedef struct frq_w frq_w;
+typedef struct frq_moe_w frq_moe_w;
+
+/* Last error message of the calling thread ("" when none). */
+const char* frq_last_error(void);
+/* Library version string. */
+const char* frq_version(void);
+/* Number of visible HIP devices (0 when none). */
+int frq_device_count(void);
+
+/* Context: device selection plus a stream and workspace.  Stands in for the
+ * `--device gpu` arm of device::select (src/device.rs:40-87). */
+frq_ctx* frq_init(int device);
+void frq_free(frq_ctx* ctx);
+/* Enqueue on a caller stream (e.g. torch.cuda.current_stream().cuda_stream)
+ * instead of the ctx's own; NULL restores the ctx stream. */
+int frq_set_stream(frq_ctx* ctx, void* hip_stream);
+void* frq_get_stream(frq_ctx* ctx);
+/* Wait for the ctx stream; returns FRQ_ERR_NAN if a _dev call since the last
+ * sync saw a NaN activation, else FRQ_OK / FRQ_ERR_HIP. */
+int frq_sync(frq_ctx* ctx);
+
+/* ---- weight upload (one-time, into persistent HBM) ---------------------- */
+
+/* int8 weight from the loader's transposed store: wt (N,K) row-major
+ * (wt[j*K+kk] = W[kk,j]) and f32 per-output scale[N].  Replaces
+ * Bundle::i8_for_gpu (src/bundle.rs:521-526) as the upload hook. */
+frq_w* frq_upload_i8(frq_ctx* ctx, const int8_t* wt_nk, const float* scale,
+                     size_t n, size_t k);
+/* int8 weight straight from the bundle blob: w (in=K, out=N) row-major as
+ * written by put_i8 (src/convert.rs:344-360) and its f16 `__scale` [N].  The
+ * (K,N)->(N,K) transpose of Bundle::load (src/bundle.rs:345-355) and the
+ * f16->f32 upcast of arr1o (921-933) run on the device. */
+frq_w* frq_upload_i8_bundle(frq_ctx* ctx, const int8_t* w_kn,
+                            const uint16_t* scale_f16, size_t k, size_t n);
+/* Group-wise int4 weight as stored: packed (N, ceil(K/2)) bytes, even input
+ * index in the low nibble, and f16 scales (N, ceil(K/g)) (src/bundle.rs:
+ * 50-56, 356-360; src/convert.rs:189-216). */
+frq_w* frq_upload_i4(frq_ctx* ctx, const uint8_t* packed,
+                     const uint16_t* scale_f16, size_t n, size_t k, size_t g);
+void frq_w_free(frq_w* w);
+/* dtype (FRQ_DT_*), N (out), K (in), g (int4 group, 0 for int8). */
+int frq_w_info(const frq_w* w, int* dtype, size_t* n, size_t* k, size_t* g);
+
+/* ---- the linear: Bundle::mm (src/bundle.rs:644-919) ----------------------
+ * out (M,N) = a (M,K) @ W for an int8 weight (W8A8 with outlier-aware
+ * per-token activation quant, src/bundle.rs:688-756) or an int4 weight
+ * (W4A32, src/bundle.rs:760-799).  a and out are row-major f32. */
+int frq_mm(frq_ctx* ctx, const frq_w* w, const float* a, size_t m,
+           float* out);
+int frq_mm_dev(frq_ctx* ctx, const frq_w* w, const float* d_a, size_t m,
+               float* d_out);
+/* int8 only, host pointers: also returns the internals the reference keeps
+ * in locals — acc (M,N) i32 (the i8dot sums), a8 (M,K) i8, sa[M], and the
+ * min(32,K) outliers per row (oidx, oval; (M,32), ascending channel).  Any
+ * of the extra outputs may be NULL. */
+int frq_mm_i8_debug(frq_ctx* ctx, const frq_w* w, const float* a, size_t m,
+                    float* out, int32_t* acc, int8_t* a8, float* sa,
+                    uint32_t* oidx, float* oval);
+
+/* The int8 linear in its two reference steps, on device pointers (ctx
+ * stream).  frq_quant_i8_dev is the activation quant of the I8 arm
+ * (src/bundle.rs:699-708 == 732-743): a (M,K) f32 -> a8 (M, kp) i8 with row
+ * pitch kp = frq_quant_pitch(K) (padding zero), sa[M], and the min(32,K)
+ * outliers per row (oidx, oval; (M,32), ascending channel).
+ * frq_mm_i8_q_dev is the dot + epilogue (709-715 / 744-752) on such a
+ * quantised batch; frq_mm_dev == frq_quant_i8_dev + frq_mm_i8_q_dev. */
+size_t frq_quant_pitch(size_t k);
+int frq_quant_i8_dev(frq_ctx* ctx, const float* d_a, size_t m, size_t k,
+                     int8_t* d_a8, float* d_sa, uint32_t* d_oidx,
+                     float* d_oval);
+int frq_mm_i8_q_dev(frq_ctx* ctx, const frq_w* w, const int8_t* d_a8,
+                    const float* d_sa, const uint32_t* d_oidx,
+                    const float* d_oval, size_t m, float* d_out);
+
+/* ---- MoE experts: expert_f32 + expert_mm (src/bundle.rs:404-461) and the
+ * routed branch of src/qwen3moe.rs:120-158 / src/gemma4.rs:131-187 -------- */
+
+/* Upload all experts of one layer.  act FRQ_ACT_SILU: gate[e], up[e] are
+ * (in=d, out=mi) and down[e] (in=mi, out=d), i8 (in,out) row-major as the
+ * bundle stores them, scales f32 [out].  act FRQ_ACT_GELU_TANH: gate[e] is
+ * the packed gate_up (d, 2*mi) and up/up_scale are ignored. */
+frq_moe_w* frq_moe_upload_i8(frq_ctx* ctx, size_t n_exp, size_t d, size_t mi,
+                             int act, const int8_t* const* gate,
+                             const float* const* gate_scale,
+                             const int8_t* const* up,
+                             const float* const* up_scale,
+                             const int8_t* const* down,
+                             const float* const* down_scale);
+void frq_moe_free(frq_moe_w* m);
+
+/* Routed expert layer: softmax over the router logits (T,E), stable top-k,
+ * renormalise (norm_topk; per_expert_scale non-NULL selects the gemma4
+ * weighting p/sum*pes[e]), per-expert W8A32 matmuls with SwiGLU or
+ * gelu_tanh gating, weighted combine into out (T,d).  x, logits, out f32. */
+int frq_moe(frq_ctx* ctx, const frq_moe_w* m, const float* x, size_t T,
+            const float* logits, size_t topk, int norm_topk,
+            const float* per_expert_scale, float* out);
+int frq_moe_dev(frq_ctx* ctx, const frq_moe_w* m, const float* d_x, size_t T,
+                const float* d_logits, size_t topk, int norm_topk,
+                const float* d_per_expert_scale, float* d_out);
+/* Routing only (host pointers): sel (T,topk) expert ids in descending-p
+ * order, w (T,topk) combine weights. */
+int frq_moe_route(frq_ctx* ctx, const float* logits, size_t T, size_t E,
+                  size_t topk, int norm_topk, const float* per_expert_scale,
+                  int32_t* sel, float* w);
+/* One expert matmul, expert_mm (src/bundle.rs:457-461): y (M,out) =
+ * x (M,in) @ (q * scale) for expert `e` of bank `which` (0 gate/gate_up,
+ * 1 up, 2 down). */
+int frq_expert_mm(frq_ctx* ctx, const frq_moe_w* m, int which, size_t e,
+                  const float* x, size_t mrows, float* y);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,253 @@
+"""CPU oracle of fieldrun's quantised-linear hot path — TEST INFRASTRUCTURE.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+import this package.  It wraps oracle/libfrq_oracle.so (built from
+frq_oracle.c by oracle/Makefile), a C restatement of /root/reference
+src/bundle.rs, src/convert.rs and the MoE branches of src/qwen3moe.rs /
+src/gemma4.rs; each C function cites the reference lines it follows.  The
+pinning status of each function is listed in frq_oracle.h.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libfrq_oracle.so")
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return LIB_PATH
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        build()
+    lib = C.CDLL(LIB_PATH)
+    P, S, I, F = C.c_void_p, C.c_size_t, C.c_int, C.c_float
+    sig = {
+        "fro_f16_to_f32": (F, [C.c_uint16]),
+        "fro_f32_to_f16": (C.c_uint16, [F]),
+        "fro_f16_to_f32_n": (None, [P, P, S]),
+        "fro_put_i8": (None, [P, S, S, I, P, P]),
+        "fro_put_i4": (S, [P, S, S, I, P, P]),
+        "fro_put_embed_i8": (None, [P, S, S, P, P]),
+        "fro_i8_transpose": (None, [P, S, S, P]),
+        "fro_i8dot": (C.c_int32, [P, P, S]),
+        "fro_quant_row": (I, [P, S, P, P, P, P, P]),
+        "fro_mm_i8": (I, [P, S, S, P, P, S, P, P]),
+        "fro_mm_i8_mt": (I, [P, S, S, P, P, S, P, I]),
+        "fro_i4_dot": (F, [P, P, P, S, S]),
+        "fro_i4_dot_avx2": (F, [P, P, P, S, S]),
+        "fro_mm_i4": (I, [P, S, S, P, P, S, S, P]),
+        "fro_expert_mm_i8": (None, [P, S, P, P, S, S, P]),
+        "fro_sgemm": (None, [P, S, S, P, S, P]),
+        "fro_silu": (F, [F]),
+        "fro_gelu_tanh": (F, [F]),
+        "fro_moe_route": (None, [P, S, S, S, I, P, P, P, P]),
+        "fro_moe": (I, [P, S, S, P, S, S, I, P, S, I, P, P, P, P, P, P, P]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(lib, name)
+        f.restype = res
+        f.argtypes = args
+    return lib
+
+
+lib = _load()
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def _c(a, dt):
+    return np.ascontiguousarray(a, dtype=dt)
+
+
+class OracleNaN(RuntimeError):
+    """The reference panics (partial_cmp().unwrap()) on this input."""
+
+
+# ---- f16 ----
+def f16_to_f32(h: np.ndarray) -> np.ndarray:
+    h = _c(h, np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib.fro_f16_to_f32_n(_p(h), _p(out), h.size)
+    return out
+
+
+def f32_to_f16_bits(x: float) -> int:
+    return int(lib.fro_f32_to_f16(float(x)))
+
+
+# ---- quantisers (src/convert.rs) ----
+def put_i8(data: np.ndarray, transpose: bool):
+    """-> (w (in,out) int8, scale f16 bits [out] uint16)."""
+    data = _c(data, np.float32)
+    rows, cols = data.shape
+    out, inp = (rows, cols) if transpose else (cols, rows)
+    w = np.empty((inp, out), np.int8)
+    s = np.empty(out, np.uint16)
+    lib.fro_put_i8(_p(data), rows, cols, int(transpose), _p(w), _p(s))
+    return w, s
+
+
+def put_i4(data: np.ndarray, transpose: bool):
+    """-> (packed (out, ceil(in/2)) uint8, scale f16 bits (out, ng), g)."""
+    data = _c(data, np.float32)
+    rows, cols = data.shape
+    out, inp = (rows, cols) if transpose else (cols, rows)
+    g = min(32, max(inp, 1))
+    ng = (inp + g - 1) // g
+    packed = np.empty((out, (inp + 1) // 2), np.uint8)
+    s = np.empty((out, ng), np.uint16)
+    g2 = lib.fro_put_i4(_p(data), rows, cols, int(transpose), _p(packed), _p(s))
+    assert g2 == g
+    return packed, s, g
+
+
+def put_embed_i8(data: np.ndarray):
+    data = _c(data, np.float32)
+    v, d = data.shape
+    q = np.empty((v, d), np.int8)
+    s = np.empty(v, np.uint16)
+    lib.fro_put_embed_i8(_p(data), v, d, _p(q), _p(s))
+    return q, s
+
+
+def i8_transpose(w_kn: np.ndarray) -> np.ndarray:
+    w_kn = _c(w_kn, np.int8)
+    k, n = w_kn.shape
+    out = np.empty((n, k), np.int8)
+    lib.fro_i8_transpose(_p(w_kn), k, n, _p(out))
+    return out
+
+
+# ---- int8 path (src/bundle.rs:688-756, 1036-1053) ----
+def i8dot(a: np.ndarray, w: np.ndarray) -> int:
+    a, w = _c(a, np.int8), _c(w, np.int8)
+    return int(lib.fro_i8dot(_p(a), _p(w), a.size))
+
+
+def quant_row(a: np.ndarray):
+    """-> (a8, sa, oidx[:t], oval[:t]); raises OracleNaN like the reference."""
+    a = _c(a, np.float32)
+    k = a.size
+    a8 = np.empty(k, np.int8)
+    sa = C.c_float()
+    oi = np.zeros(32, np.uint32)
+    ov = np.zeros(32, np.float32)
+    t = C.c_size_t()
+    rc = lib.fro_quant_row(_p(a), k, _p(a8), C.byref(sa), _p(oi), _p(ov), C.byref(t))
+    if rc:
+        raise OracleNaN("NaN activation")
+    return a8, np.float32(sa.value), oi[: t.value].copy(), ov[: t.value].copy()
+
+
+def mm_i8(a: np.ndarray, wt_nk: np.ndarray, scale: np.ndarray, with_acc: bool = False):
+    a = _c(a, np.float32)
+    wt_nk, scale = _c(wt_nk, np.int8), _c(scale, np.float32)
+    m, k = a.shape
+    n = wt_nk.shape[0]
+    out = np.empty((m, n), np.float32)
+    acc = np.empty((m, n), np.int32) if with_acc else None
+    rc = lib.fro_mm_i8(_p(a), m, k, _p(wt_nk), _p(scale), n, _p(out), _p(acc))
+    if rc:
+        raise OracleNaN("NaN activation")
+    return (out, acc) if with_acc else out
+
+
+def mm_i8_mt(a, wt_nk, scale, nthreads: int):
+    a = _c(a, np.float32)
+    wt_nk, scale = _c(wt_nk, np.int8), _c(scale, np.float32)
+    m, k = a.shape
+    n = wt_nk.shape[0]
+    out = np.empty((m, n), np.float32)
+    rc = lib.fro_mm_i8_mt(_p(a), m, k, _p(wt_nk), _p(scale), n, _p(out), int(nthreads))
+    if rc:
+        raise OracleNaN("NaN activation")
+    return out
+
+
+# ---- int4 path (src/bundle.rs:90-113, 199-225, 760-799) ----
+def i4_dot(prow, a, scale, g, k):
+    prow, a, scale = _c(prow, np.uint8), _c(a, np.float32), _c(scale, np.float32)
+    return np.float32(lib.fro_i4_dot(_p(prow), _p(a), _p(scale), g, k))
+
+
+def i4_dot_avx2(prow, a, scale, g, k):
+    prow, a, scale = _c(prow, np.uint8), _c(a, np.float32), _c(scale, np.float32)
+    return np.float32(lib.fro_i4_dot_avx2(_p(prow), _p(a), _p(scale), g, k))
+
+
+def mm_i4(a, packed, scale_f32, k, g):
+    a = _c(a, np.float32)
+    packed, scale_f32 = _c(packed, np.uint8), _c(scale_f32, np.float32)
+    m = a.shape[0]
+    n = packed.shape[0]
+    out = np.empty((m, n), np.float32)
+    lib.fro_mm_i4(_p(a), m, k, _p(packed), _p(scale_f32), n, g, _p(out))
+    return out
+
+
+# ---- experts / MoE (src/bundle.rs:404-461, src/qwen3moe.rs:120-158) ----
+def expert_mm_i8(x, raw_in_out, scale):
+    x, raw_in_out, scale = _c(x, np.float32), _c(raw_in_out, np.int8), _c(scale, np.float32)
+    m = x.shape[0]
+    inp, out = raw_in_out.shape
+    y = np.empty((m, out), np.float32)
+    lib.fro_expert_mm_i8(_p(x), m, _p(raw_in_out), _p(scale), inp, out, _p(y))
+    return y
+
+
+def silu(x: float) -> float:
+    return float(lib.fro_silu(float(x)))
+
+
+def gelu_tanh(x: float) -> float:
+    return float(lib.fro_gelu_tanh(float(x)))
+
+
+def moe_route(logits, topk, norm_topk=True, per_expert_scale=None):
+    logits = _c(logits, np.float32)
+    T, E = logits.shape
+    sel = np.empty((T, topk), np.int32)
+    w = np.empty((T, topk), np.float32)
+    probs = np.empty((T, E), np.float32)
+    pes = None if per_expert_scale is None else _c(per_expert_scale, np.float32)
+    lib.fro_moe_route(_p(logits), T, E, topk, int(norm_topk), _p(pes), _p(sel), _p(w), _p(probs))
+    return sel, w, probs
+
+
+def moe(x, logits, topk, norm_topk, gate, gate_scale, up, up_scale, down, down_scale,
+        act=0, per_expert_scale=None):
+    x, logits = _c(x, np.float32), _c(logits, np.float32)
+    T, d = x.shape
+    E = logits.shape[1]
+    mi = down[0].shape[0]
+    keep = []
+
+    def arr(lst, dt):
+        ptrs = (C.c_void_p * E)()
+        for i, a in enumerate(lst):
+            a = _c(a, dt)
+            keep.append(a)
+            ptrs[i] = a.ctypes.data
+        return ptrs
+
+    gp, gsp = arr(gate, np.int8), arr(gate_scale, np.float32)
+    dp, dsp = arr(down, np.int8), arr(down_scale, np.float32)
+    if act == 0:
+        up_, usp = arr(up, np.int8), arr(up_scale, np.float32)
+    else:
+        up_ = usp = None
+    pes = None if per_expert_scale is None else _c(per_expert_scale, np.float32)
+    out = np.empty((T, d), np.float32)
+    lib.fro_moe(_p(x), T, d, _p(logits), E, topk, int(norm_topk), _p(pes), mi, act,
+                gp, gsp, up_, usp, dp, dsp, _p(out))
+    return out

@@ -1,0 +1,548 @@
+/*
+ * frq_oracle.c — CPU restatement of fieldrun's quantised-linear hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY (parity checker + CPU baseline); see
+ * frq_oracle.h for who may load it and how each function is pinned.
+ *
+ * Build: gcc -O3 -march=x86-64 -ffp-contract=off -fPIC -shared (oracle/Makefile).
+ * -march=x86-64 mirrors the reference's release target (no target-cpu
+ * override anywhere in its tree), -ffp-contract=off mirrors Rust, which never
+ * contracts a*b+c into an FMA unless the source calls mul_add/_mm*_fmadd.
+ *
+ * All citations are to /root/reference (fieldrun 0.1.0).
+ */
+#include "frq_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------ */
+/* f16 <-> f32.  The reference upcasts with half::f16::to_f32 / F16C         */
+/* (src/bundle.rs:921-933, 1131-1160; exact) and downcasts with               */
+/* half::f16::from_f32 (src/convert.rs:147-155; round-to-nearest-even).       */
+/* ------------------------------------------------------------------------ */
+static size_t nz(size_t x) { return x ? x : 1; }
+static uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+float fro_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1Fu;
+    uint32_t man = h & 0x3FFu;
+    if (exp == 0x1F) /* inf / nan: keep payload */
+        return u2f(sign | 0x7F800000u | (man << 13));
+    if (exp == 0) {
+        if (man == 0) return u2f(sign);
+        /* subnormal: value = man * 2^-24, exact in f32 */
+        float v = (float)man * 5.9604644775390625e-08f;
+        return sign ? -v : v;
+    }
+    return u2f(sign | ((exp + 112u) << 23) | (man << 13));
+}
+
+uint16_t fro_f32_to_f16(float f) {
+    uint32_t x = f2u(f);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t exp = (x >> 23) & 0xFFu;
+    uint32_t man = x & 0x7FFFFFu;
+    if (exp == 0xFF) {
+        if (man) return (uint16_t)(sign | 0x7E00u | (man >> 13));
+        return (uint16_t)(sign | 0x7C00u);
+    }
+    int32_t he = (int32_t)exp - 127 + 15;
+    if (he >= 0x1F) return (uint16_t)(sign | 0x7C00u);
+    if (he <= 0) {
+        if (14 - he > 24) return (uint16_t)sign;
+        man |= 0x800000u;
+        uint32_t hm = man >> (14 - he);
+        uint32_t rb = 1u << (13 - he);
+        /* round half to even: round bit set and (sticky or lsb) */
+        if ((man & rb) && (man & (3u * rb - 1u))) hm++;
+        return (uint16_t)(sign | hm);
+    }
+    uint32_t h = sign | ((uint32_t)he << 10) | (man >> 13);
+    uint32_t rb = 0x1000u;
+    if ((man & rb) && (man & (3u * rb - 1u))) h++;
+    return (uint16_t)h;
+}
+
+void fro_f16_to_f32_n(const uint16_t* src, float* dst, size_t n) {
+    for (size_t i = 0; i < n; i++) dst[i] = fro_f16_to_f32(src[i]);
+}
+
+/* Rust `f32::round_ties_even` (src/convert.rs:351, 208): rintf under the
+ * default FE_TONEAREST mode. */
+static float round_ties_even(float v) { return rintf(v); }
+
+static float clampf(float v, float lo, float hi) {
+    return v < lo ? lo : (v > hi ? hi : v);
+}
+
+/* put_i8: src/convert.rs:344-360.  scale_j = max(amax_j/127, 1e-8) (f32),
+ * q = clamp(round_ties_even(w/s), -127, 127), stored (in,out); the scale is
+ * written as f16 (put_f16, 147-155). */
+void fro_put_i8(const float* data, size_t rows, size_t cols, int transpose,
+                int8_t* w_in_out, uint16_t* scale_f16) {
+    size_t out = transpose ? rows : cols, inp = transpose ? cols : rows;
+#define AT(i, j) (transpose ? data[(j) * inp + (i)] : data[(i) * out + (j)])
+    float* sc = (float*)malloc(nz(out) * sizeof(float));
+    for (size_t j = 0; j < out; j++) {
+        float m = 0.0f;
+        for (size_t i = 0; i < inp; i++) m = fmaxf(m, fabsf(AT(i, j)));
+        float s = m / 127.0f;
+        sc[j] = s > 1e-8f ? s : 1e-8f; /* f32::max(x, 1e-8) */
+    }
+    for (size_t i = 0; i < inp; i++)
+        for (size_t j = 0; j < out; j++)
+            w_in_out[i * out + j] =
+                (int8_t)clampf(round_ties_even(AT(i, j) / sc[j]), -127.0f, 127.0f);
+    for (size_t j = 0; j < out; j++) scale_f16[j] = fro_f32_to_f16(sc[j]);
+    free(sc);
+#undef AT
+}
+
+/* put_i4: src/convert.rs:189-216.  g = min(32, in); scale (out, ng) =
+ * max(amax/7, 1e-8); q = clamp(round_ties_even(w/s), -7, 7) as a two's-
+ * complement nibble, even input index in the low nibble.  Returns g. */
+size_t fro_put_i4(const float* data, size_t rows, size_t cols, int transpose,
+                  uint8_t* packed, uint16_t* scale_f16) {
+    size_t out = transpose ? rows : cols, inp = transpose ? cols : rows;
+#define AT(i, j) (transpose ? data[(j) * inp + (i)] : data[(i) * out + (j)])
+    size_t g = 32 < nz(inp) ? 32 : nz(inp);
+    size_t ng = (inp + g - 1) / g, rb = (inp + 1) / 2;
+    float* sc = (float*)malloc(nz(out * ng) * sizeof(float));
+    for (size_t j = 0; j < out; j++)
+        for (size_t gi = 0; gi < ng; gi++) {
+            size_t lo = gi * g, hi = (gi + 1) * g < inp ? (gi + 1) * g : inp;
+            float m = 0.0f;
+            for (size_t i = lo; i < hi; i++) m = fmaxf(m, fabsf(AT(i, j)));
+            float s = m / 7.0f;
+            sc[j * ng + gi] = s > 1e-8f ? s : 1e-8f;
+        }
+    memset(packed, 0, out * rb);
+    for (size_t j = 0; j < out; j++)
+        for (size_t i = 0; i < inp; i++) {
+            float s = sc[j * ng + i / g];
+            int8_t q = (int8_t)clampf(round_ties_even(AT(i, j) / s), -7.0f, 7.0f);
+            uint8_t nib = (uint8_t)q & 0x0F;
+            packed[j * rb + i / 2] |= (i % 2 == 0) ? nib : (uint8_t)(nib << 4);
+        }
+    for (size_t i = 0; i < out * ng; i++) scale_f16[i] = fro_f32_to_f16(sc[i]);
+    free(sc);
+    return g;
+#undef AT
+}
+
+/* put_embed_i8: src/convert.rs:265-279 (row-major per-row int8). */
+void fro_put_embed_i8(const float* data, size_t vocab, size_t d, int8_t* q,
+                      uint16_t* scale_f16) {
+    for (size_t r = 0; r < vocab; r++) {
+        float m = 0.0f;
+        for (size_t c = 0; c < d; c++) m = fmaxf(m, fabsf(data[r * d + c]));
+        float s = m / 127.0f;
+        s = s > 1e-8f ? s : 1e-8f;
+        for (size_t c = 0; c < d; c++)
+            q[r * d + c] = (int8_t)clampf(round_ties_even(data[r * d + c] / s), -127.0f, 127.0f);
+        scale_f16[r] = fro_f32_to_f16(s);
+    }
+}
+
+/* Bundle::load i8 arm: src/bundle.rs:345-355, wt[j*k+kk] = raw[kk*n+j]. */
+void fro_i8_transpose(const int8_t* w_kn, size_t k, size_t n, int8_t* wt_nk) {
+    for (size_t kk = 0; kk < k; kk++)
+        for (size_t j = 0; j < n; j++) wt_nk[j * k + kk] = w_kn[kk * n + j];
+}
+
+/* i8dot scalar fallback: src/bundle.rs:1052 (the `_scalar_i8_bench` path,
+ * Cargo.toml:19-21).  Every SIMD variant equals it (1359-1382). */
+int32_t fro_i8dot(const int8_t* a, const int8_t* w, size_t n) {
+    int32_t s = 0;
+    for (size_t i = 0; i < n; i++) s += (int32_t)a[i] * (int32_t)w[i];
+    return s;
+}
+
+/* Rust `f as i32` saturates and maps NaN to 0. */
+static int32_t sat_i32(float v) {
+    if (v != v) return 0;
+    if (v >= 2147483647.0f) return 2147483647;
+    if (v <= -2147483648.0f) return (-2147483647 - 1);
+    return (int32_t)v;
+}
+
+/* Quickselect: the value at rank `r` (0-based) of v[0..n) in DESCENDING
+ * order; reorders v.  Stands in for select_nth_unstable_by
+ * (src/bundle.rs:702-705); only the value at rank t is used, which is
+ * unique even when the index permutation is not. */
+static float select_desc(float* v, size_t n, size_t r) {
+    size_t lo = 0, hi = n; /* rank r lies in [lo, hi) */
+    while (hi - lo > 1) {
+        float a = v[lo], b = v[lo + (hi - lo) / 2], c = v[hi - 1];
+        float p = (a < b) ? ((b < c) ? b : (a < c ? c : a)) : ((a < c) ? a : (b < c ? c : b));
+        /* 3-way partition: [lo,lt) > p, [lt,gt) == p, [gt,hi) < p */
+        size_t lt = lo, i = lo, gt = hi;
+        while (i < gt) {
+            float x = v[i];
+            if (x > p) { v[i] = v[lt]; v[lt] = x; lt++; i++; }
+            else if (x < p) { gt--; v[i] = v[gt]; v[gt] = x; }
+            else i++;
+        }
+        if (r < lt) hi = lt;
+        else if (r >= gt) lo = gt;
+        else return p;
+    }
+    return v[lo];
+}
+
+/* Outlier-aware per-token activation quant: src/bundle.rs:691 (t),
+ * 699-708 (M>1) == 732-743 (M==1), OUTLIER_T at 309.
+ *   bulk_max = (t+1)-th largest |a| (0 when t == k)
+ *   sa = bulk_max > 0 ? bulk_max/127 : 1
+ *   a8 = clamp(round(a/sa) as i32, -127, 127)   (round: half away from 0)
+ *   the t largest-|a| channels are zeroed and kept as (idx, a) outliers.
+ * The reference leaves the outliers in select_nth_unstable_by's order and
+ * breaks ties at |a| == bulk_max arbitrarily; here outliers are all channels
+ * with |a| > bulk_max plus the lowest-index ties, listed in ascending channel
+ * order (the corr summation order the GPU kernels also use). */
+int fro_quant_row(const float* a, size_t k, int8_t* a8, float* sa_out,
+                  uint32_t* oidx, float* oval, size_t* t_out) {
+    size_t t = FRO_OUTLIER_T < k ? FRO_OUTLIER_T : k;
+    float bulk = 0.0f;
+    if (t < k) {
+        for (size_t i = 0; i < k; i++)
+            if (a[i] != a[i]) return FRO_ERR_NAN; /* partial_cmp().unwrap() */
+        float* tmp = (float*)malloc(k * sizeof(float));
+        for (size_t i = 0; i < k; i++) tmp[i] = fabsf(a[i]);
+        bulk = select_desc(tmp, k, t);
+        free(tmp);
+    }
+    float sa = bulk > 0.0f ? bulk / 127.0f : 1.0f;
+    for (size_t i = 0; i < k; i++) {
+        int32_t q = sat_i32(roundf(a[i] / sa));
+        q = q < -127 ? -127 : (q > 127 ? 127 : q);
+        a8[i] = (int8_t)q;
+    }
+    size_t n = 0;
+    if (t == k) {
+        for (size_t i = 0; i < k; i++) { oidx[n] = (uint32_t)i; oval[n] = a[i]; a8[i] = 0; n++; }
+    } else {
+        size_t gt = 0;
+        for (size_t i = 0; i < k; i++) gt += fabsf(a[i]) > bulk;
+        size_t ties = t - gt; /* >= 1 by definition of the (t+1)-th value */
+        for (size_t i = 0; i < k && n < t; i++) {
+            float m = fabsf(a[i]);
+            if (m > bulk || (m == bulk && ties > 0)) {
+                if (m == bulk) ties--;
+                oidx[n] = (uint32_t)i; oval[n] = a[i]; a8[i] = 0; n++;
+            }
+        }
+    }
+    *sa_out = sa;
+    *t_out = t;
+    return FRO_OK;
+}
+
+/* Epilogue of the I8 arm: src/bundle.rs:709-715 / 745-751.
+ *   corr = sum over outliers of av * (wt[j,ch] as f32)   (fold from -0.0)
+ *   out  = scale[j] * (sa * (acc as f32) + corr)          (no FMA) */
+static void i8_row(const float* arow, size_t k, const int8_t* wt,
+                   const float* scale, size_t j0, size_t j1, const int8_t* a8,
+                   float sa, const uint32_t* oidx, const float* oval, size_t t,
+                   float* orow, int32_t* accrow) {
+    for (size_t j = j0; j < j1; j++) {
+        const int8_t* w = wt + j * k;
+        int32_t acc = fro_i8dot(a8, w, k);
+        float corr = -0.0f;
+        for (size_t o = 0; o < t; o++) corr = corr + oval[o] * (float)w[oidx[o]];
+        orow[j] = scale[j] * (sa * (float)acc + corr);
+        if (accrow) accrow[j] = acc;
+    }
+    (void)arow;
+}
+
+int fro_mm_i8(const float* a, size_t m, size_t k, const int8_t* wt,
+              const float* scale, size_t n, float* out, int32_t* acc) {
+    int8_t* a8 = (int8_t*)malloc(nz(k));
+    uint32_t oidx[FRO_OUTLIER_T];
+    float oval[FRO_OUTLIER_T], sa;
+    size_t t;
+    for (size_t i = 0; i < m; i++) {
+        int rc = fro_quant_row(a + i * k, k, a8, &sa, oidx, oval, &t);
+        if (rc) { free(a8); return rc; }
+        i8_row(a + i * k, k, wt, scale, 0, n, a8, sa, oidx, oval, t, out + i * n,
+               acc ? acc + i * n : NULL);
+    }
+    free(a8);
+    return FRO_OK;
+}
+
+/* Threaded variant with the reference's rayon split: M==1 fans out over
+ * output columns (src/bundle.rs:744-752), M>1 over rows (695-718). */
+typedef struct {
+    const float* a; size_t m, k, n; const int8_t* wt; const float* scale;
+    float* out; size_t lo, hi; int by_rows;
+    const int8_t* a8; float sa; const uint32_t* oidx; const float* oval; size_t t;
+    int rc;
+} mt_job;
+
+static void* mt_worker(void* p) {
+    mt_job* J = (mt_job*)p;
+    if (!J->by_rows) {
+        i8_row(J->a, J->k, J->wt, J->scale, J->lo, J->hi, J->a8, J->sa, J->oidx, J->oval,
+               J->t, J->out, NULL);
+        return NULL;
+    }
+    int8_t* a8 = (int8_t*)malloc(nz(J->k));
+    uint32_t oidx[FRO_OUTLIER_T];
+    float oval[FRO_OUTLIER_T], sa;
+    size_t t;
+    for (size_t i = J->lo; i < J->hi; i++) {
+        int rc = fro_quant_row(J->a + i * J->k, J->k, a8, &sa, oidx, oval, &t);
+        if (rc) { J->rc = rc; break; }
+        i8_row(J->a + i * J->k, J->k, J->wt, J->scale, 0, J->n, a8, sa, oidx, oval, t,
+               J->out + i * J->n, NULL);
+    }
+    free(a8);
+    return NULL;
+}
+
+int fro_mm_i8_mt(const float* a, size_t m, size_t k, const int8_t* wt,
+                 const float* scale, size_t n, float* out, int nthreads) {
+    if (nthreads < 1) nthreads = 1;
+    pthread_t th[256];
+    mt_job jobs[256];
+    if (nthreads > 256) nthreads = 256;
+    int8_t* a8 = NULL;
+    uint32_t oidx[FRO_OUTLIER_T];
+    float oval[FRO_OUTLIER_T], sa = 1.0f;
+    size_t t = 0;
+    int rc = FRO_OK;
+    if (m == 1) {
+        a8 = (int8_t*)malloc(nz(k));
+        rc = fro_quant_row(a, k, a8, &sa, oidx, oval, &t);
+        if (rc) { free(a8); return rc; }
+    }
+    size_t total = (m == 1) ? n : m;
+    for (int w = 0; w < nthreads; w++) {
+        mt_job* J = &jobs[w];
+        J->a = a; J->m = m; J->k = k; J->n = n; J->wt = wt; J->scale = scale;
+        J->out = out; J->by_rows = (m != 1);
+        J->lo = total * (size_t)w / (size_t)nthreads;
+        J->hi = total * (size_t)(w + 1) / (size_t)nthreads;
+        J->a8 = a8; J->sa = sa; J->oidx = oidx; J->oval = oval; J->t = t; J->rc = 0;
+        pthread_create(&th[w], NULL, mt_worker, J);
+    }
+    for (int w = 0; w < nthreads; w++) {
+        pthread_join(th[w], NULL);
+        if (jobs[w].rc) rc = jobs[w].rc;
+    }
+    free(a8);
+    return rc;
+}
+
+/* ------------------------------------------------------------------------ */
+/* int4 (W4A32)                                                              */
+/* ------------------------------------------------------------------------ */
+/* Sign-extended nibble i of a packed row: src/bundle.rs:61-66. */
+static int nib_s4(const uint8_t* prow, size_t i) {
+    uint8_t b = prow[i / 2];
+    uint8_t v = (i % 2 == 0) ? (b & 0x0F) : (b >> 4);
+    return (int)(int8_t)(uint8_t)(v << 4) >> 4;
+}
+
+/* i4_dot scalar fold: src/bundle.rs:90-113 (== jit.rs:362-378). */
+float fro_i4_dot(const uint8_t* prow, const float* a, const float* scale,
+                 size_t g, size_t k) {
+    float sum = 0.0f;
+    size_t gi = 0, kk = 0;
+    while (kk < k) {
+        size_t hi = kk + g < k ? kk + g : k;
+        float gsum = 0.0f;
+        for (; kk < hi; kk++) gsum = gsum + a[kk] * (float)nib_s4(prow, kk);
+        sum = sum + scale[gi] * gsum;
+        gi++;
+    }
+    return sum;
+}
+
+/* i4_dot_avx2: src/bundle.rs:199-225, the order the x86 production build
+ * takes (dispatch at 91-96).  Per group: 8 lane accumulators, each an FMA
+ * chain over the 8-nibble chunks (unpack8_nibbles 186-193 reads 4 bytes at
+ * kk/2, i.e. nibbles 2*(kk/2)..+8), then hsum256 (146-153):
+ * ((l0+l4)+(l2+l6)) + ((l1+l5)+(l3+l7)), then a scalar mul+add tail, then
+ * sum += scale*gsum. */
+float fro_i4_dot_avx2(const uint8_t* prow, const float* a, const float* scale,
+                      size_t g, size_t k) {
+    float sum = 0.0f;
+    size_t gi = 0, kk = 0;
+    while (kk < k) {
+        size_t hi = kk + g < k ? kk + g : k;
+        float l[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        while (kk + 8 <= hi) {
+            size_t base = (kk / 2) * 2;
+            for (int q = 0; q < 8; q++)
+                l[q] = fmaf((float)nib_s4(prow, base + (size_t)q), a[kk + (size_t)q], l[q]);
+            kk += 8;
+        }
+        float q0 = l[0] + l[4], q1 = l[1] + l[5], q2 = l[2] + l[6], q3 = l[3] + l[7];
+        float d0 = q0 + q2, d1 = q1 + q3;
+        float gsum = d0 + d1;
+        for (; kk < hi; kk++) gsum = gsum + a[kk] * (float)nib_s4(prow, kk);
+        sum = sum + scale[gi] * gsum;
+        gi++;
+    }
+    return sum;
+}
+
+/* f32 GEMM used where the reference calls ndarray's a.dot (matrixmultiply
+ * 0.3.10 sgemm, Cargo.lock:1207).  Its k-blocking order is not visible in
+ * the reference tree (parity unpinned); this is the sequential-k FMA order
+ * of one register-blocked micro-kernel pass. */
+void fro_sgemm(const float* x, size_t m, size_t k, const float* w, size_t n,
+               float* y) {
+    for (size_t i = 0; i < m; i++)
+        for (size_t j = 0; j < n; j++) {
+            float acc = 0.0f;
+            for (size_t kk = 0; kk < k; kk++) acc = fmaf(x[i * k + kk], w[kk * n + j], acc);
+            y[i * n + j] = acc;
+        }
+}
+
+/* Bundle::mm I4 arm: src/bundle.rs:760-799.  M==1 -> i4_dot per output
+ * column (767-776, AVX2 order on x86); M>1 -> dequantise
+ * w[kk,col] = s4 * scale[j, kk/g] (784-790) then a.dot(w). */
+int fro_mm_i4(const float* a, size_t m, size_t k, const uint8_t* packed,
+              const float* scale, size_t n, size_t g, float* out) {
+    size_t ng = (k + g - 1) / g, rb = (k + 1) / 2;
+    if (m == 1) {
+        for (size_t j = 0; j < n; j++)
+            out[j] = fro_i4_dot_avx2(packed + j * rb, a, scale + j * ng, g, k);
+        return FRO_OK;
+    }
+    float* wcol = (float*)malloc(nz(k) * sizeof(float));
+    for (size_t j = 0; j < n; j++) {
+        for (size_t kk = 0; kk < k; kk++)
+            wcol[kk] = (float)nib_s4(packed + j * rb, kk) * scale[j * ng + kk / g];
+        for (size_t i = 0; i < m; i++) {
+            float acc = 0.0f;
+            for (size_t kk = 0; kk < k; kk++) acc = fmaf(a[i * k + kk], wcol[kk], acc);
+            out[i * n + j] = acc;
+        }
+    }
+    free(wcol);
+    return FRO_OK;
+}
+
+/* expert_f32 i8 arm + expert_mm: src/bundle.rs:410-420, 457-461.
+ * v[i,j] = (raw[i,j] as f32) * scale[j]; y = x . v  (W8A32). */
+void fro_expert_mm_i8(const float* x, size_t m, const int8_t* raw,
+                      const float* scale, size_t inp, size_t out, float* y) {
+    float* v = (float*)malloc(nz(inp * out) * sizeof(float));
+    for (size_t i = 0; i < inp; i++)
+        for (size_t j = 0; j < out; j++) v[i * out + j] = (float)raw[i * out + j] * scale[j];
+    fro_sgemm(x, m, inp, v, out, y);
+    free(v);
+}
+
+/* silu: src/qwen3moe.rs:38-40. */
+float fro_silu(float x) { return x / (1.0f + expf(-x)); }
+
+/* gelu_tanh: src/gemma4.rs:61-64 (c = sqrt(2/pi) computed in f32). */
+float fro_gelu_tanh(float x) {
+    float c = sqrtf(2.0f / 3.14159274101257324f);
+    return 0.5f * x * (1.0f + tanhf(c * (x + 0.044715f * x * x * x)));
+}
+
+/* Routing.  qwen3moe: softmax_rows (src/qwen3moe.rs:42-52; max, exp,
+ * sequential sum, divide), stable sort desc (129; ties -> lower expert),
+ * truncate to topk (130), w = p/denom with denom the sum over the top-k in
+ * sorted order when norm_topk (131-134).  gemma4 (src/gemma4.rs:146-161)
+ * always renormalises and multiplies by per_expert_scale[e]. */
+typedef struct { float p; int32_t e; } pe_t;
+static int pe_cmp(const void* x, const void* y) {
+    const pe_t* a = (const pe_t*)x;
+    const pe_t* b = (const pe_t*)y;
+    if (a->p > b->p) return -1;
+    if (a->p < b->p) return 1;
+    return a->e < b->e ? -1 : (a->e > b->e);
+}
+
+void fro_moe_route(const float* logits, size_t T, size_t E, size_t topk,
+                   int norm_topk, const float* pes, int32_t* sel, float* w,
+                   float* probs) {
+    float* p = (float*)malloc(nz(E) * sizeof(float));
+    pe_t* v = (pe_t*)malloc(nz(E) * sizeof(pe_t));
+    for (size_t t = 0; t < T; t++) {
+        const float* row = logits + t * E;
+        float m = -INFINITY;
+        for (size_t e = 0; e < E; e++) m = fmaxf(m, row[e]);
+        float s = 0.0f;
+        for (size_t e = 0; e < E; e++) { p[e] = expf(row[e] - m); s = s + p[e]; }
+        for (size_t e = 0; e < E; e++) p[e] = p[e] / s;
+        if (probs) memcpy(probs + t * E, p, E * sizeof(float));
+        for (size_t e = 0; e < E; e++) { v[e].p = p[e]; v[e].e = (int32_t)e; }
+        qsort(v, E, sizeof(pe_t), pe_cmp); /* (p desc, e asc) == stable desc */
+        float denom = 1.0f;
+        if (norm_topk || pes) {
+            denom = -0.0f;
+            for (size_t i = 0; i < topk; i++) denom = denom + v[i].p;
+        }
+        for (size_t i = 0; i < topk; i++) {
+            sel[t * topk + i] = v[i].e;
+            float wi = v[i].p / denom;
+            if (pes) wi = wi * pes[v[i].e];
+            w[t * topk + i] = wi;
+        }
+    }
+    free(p);
+    free(v);
+}
+
+/* Routed expert layer: src/qwen3moe.rs:120-158 (act 0) and the expert part
+ * of src/gemma4.rs:162-185 (act 1).  For each active expert the tokens routed
+ * to it are gathered, gate/up (or packed gate_up) -> act -> down via
+ * expert_mm, and out[t,:] += w * down (mul then add).  The reference visits
+ * experts in HashMap order (random per process); here ascending expert id. */
+int fro_moe(const float* x, size_t T, size_t d, const float* logits, size_t E,
+            size_t topk, int norm_topk, const float* pes, size_t mi, int act,
+            const int8_t* const* gate, const float* const* gate_scale,
+            const int8_t* const* up, const float* const* up_scale,
+            const int8_t* const* down, const float* const* down_scale,
+            float* out) {
+    int32_t* sel = (int32_t*)malloc(nz(T * topk) * sizeof(int32_t));
+    float* w = (float*)malloc(nz(T * topk) * sizeof(float));
+    fro_moe_route(logits, T, E, topk, norm_topk, pes, sel, w, NULL);
+    memset(out, 0, T * d * sizeof(float));
+    size_t gw = act == 1 ? 2 * mi : mi;
+    float* rows = (float*)malloc(nz(T * d) * sizeof(float));
+    float* g = (float*)malloc(nz(T * gw) * sizeof(float));
+    float* u = (float*)malloc(nz(T * mi) * sizeof(float));
+    float* h = (float*)malloc(nz(T * mi) * sizeof(float));
+    float* dn = (float*)malloc(nz(T * d) * sizeof(float));
+    size_t* tok = (size_t*)malloc(nz(T) * sizeof(size_t));
+    float* tw = (float*)malloc(nz(T) * sizeof(float));
+    for (size_t e = 0; e < E; e++) {
+        size_t nt = 0;
+        for (size_t t = 0; t < T; t++)
+            for (size_t i = 0; i < topk; i++)
+                if ((size_t)sel[t * topk + i] == e) { tok[nt] = t; tw[nt] = w[t * topk + i]; nt++; }
+        if (!nt) continue;
+        for (size_t r = 0; r < nt; r++) memcpy(rows + r * d, x + tok[r] * d, d * sizeof(float));
+        fro_expert_mm_i8(rows, nt, gate[e], gate_scale[e], d, gw, g);
+        if (act == 0) {
+            fro_expert_mm_i8(rows, nt, up[e], up_scale[e], d, mi, u);
+            for (size_t i = 0; i < nt * mi; i++) h[i] = fro_silu(g[i]) * u[i];
+        } else {
+            for (size_t r = 0; r < nt; r++)
+                for (size_t c = 0; c < mi; c++)
+                    h[r * mi + c] = fro_gelu_tanh(g[r * gw + c]) * g[r * gw + c + mi];
+        }
+        fro_expert_mm_i8(h, nt, down[e], down_scale[e], mi, d, dn);
+        for (size_t r = 0; r < nt; r++)
+            for (size_t c = 0; c < d; c++)
+                out[tok[r] * d + c] = out[tok[r] * d + c] + tw[r] * dn[r * d + c];
+    }
+    free(sel); free(w); free(rows); free(g); free(u); free(h); free(dn); free(tok); free(tw);
+    return FRO_OK;
+}

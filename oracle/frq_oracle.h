@@ -1,0 +1,124 @@
+/*
+ * frq_oracle.h — CPU restatement of fieldrun's quantised-linear hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the parity checker for the HIP
+ * kernels in fieldrun_amd/csrc and the CPU baseline timed by bench.py. Only
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.
+ * The product library (libfrq.so) never links, loads or calls it.
+ *
+ * Every function restates one piece of /root/reference (Rust crate fieldrun
+ * 0.1.0); the file:line each follows is cited at its definition in
+ * frq_oracle.c.  Where the reference's own order is unspecified (the
+ * permutation left by select_nth_unstable_by, HashMap iteration order,
+ * matrixmultiply's internal k-blocking) the oracle fixes one deterministic
+ * order and says so; the GPU kernels are checked against that order.
+ *
+ * Pinning status of each function (what checks it beyond this restatement):
+ *   fro_f16_to_f32 / fro_f32_to_f16   exhaustive vs numpy float16 (IEEE)
+ *   fro_put_i8 / fro_put_i4           reference KAT int8_quant_roundtrip +
+ *                                     closed-form numpy quantiser
+ *   fro_i8dot                         reference KATs i8dot_matches_manual,
+ *                                     i8dot_simd_vs_scalar (xorshift vectors)
+ *                                     + int64 brute force
+ *   fro_quant_row / fro_mm_i8         closed-form invariants + brute-force
+ *                                     sort + f64 epilogue bound
+ *   fro_i4_dot / fro_i4_dot_avx2      reference KATs i4_q4a_dot_matches_manual
+ *                                     (=1.0), i4_q4a_dot_simd_vs_reference,
+ *                                     jit LCG vectors + f64 brute force
+ *   fro_mm_i4 (M>1), fro_expert_mm    f64 brute force only; the reference
+ *                                     has no test for these (its sgemm order
+ *                                     is matrixmultiply's): tolerance parity
+ *   fro_moe_route / fro_moe           closed-form softmax + brute-force
+ *                                     stable sort, f64 combine bound
+ */
+#ifndef FRQ_ORACLE_H
+#define FRQ_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FRO_OUTLIER_T 32
+
+#define FRO_OK 0
+#define FRO_ERR_NAN 3 /* reference panics in partial_cmp().unwrap() */
+
+/* IEEE binary16 <-> binary32 (half 2.7.1 semantics: RNE, exact upcast). */
+float fro_f16_to_f32(uint16_t h);
+uint16_t fro_f32_to_f16(float f);
+void fro_f16_to_f32_n(const uint16_t* src, float* dst, size_t n);
+
+/* BundleWriter quantisers. transpose=1: source is (out,in) nn.Linear. */
+void fro_put_i8(const float* data, size_t rows, size_t cols, int transpose,
+                int8_t* w_in_out, uint16_t* scale_f16);
+size_t fro_put_i4(const float* data, size_t rows, size_t cols, int transpose,
+                  uint8_t* packed, uint16_t* scale_f16);
+void fro_put_embed_i8(const float* data, size_t vocab, size_t d, int8_t* q,
+                      uint16_t* scale_f16);
+
+/* Bundle::load's i8 arm: (in=K, out=N) row-major -> (N,K). */
+void fro_i8_transpose(const int8_t* w_kn, size_t k, size_t n, int8_t* wt_nk);
+
+/* i8dot: scalar i8 x i8 -> i32. */
+int32_t fro_i8dot(const int8_t* a, const int8_t* w, size_t n);
+
+/* Outlier-aware activation quant of ONE row.  Writes a8[k], *sa, the t
+ * outliers (oidx, oval) in ascending channel order and *t = min(32,k).
+ * Returns FRO_ERR_NAN when the reference would panic. */
+int fro_quant_row(const float* a, size_t k, int8_t* a8, float* sa,
+                  uint32_t* oidx, float* oval, size_t* t);
+
+/* Bundle::mm I8 arm.  wt is (N,K), scale f32 [N].  acc (M,N) nullable. */
+int fro_mm_i8(const float* a, size_t m, size_t k, const int8_t* wt,
+              const float* scale, size_t n, float* out, int32_t* acc);
+/* Same with the reference's rayon split over nthreads worker threads. */
+int fro_mm_i8_mt(const float* a, size_t m, size_t k, const int8_t* wt,
+                 const float* scale, size_t n, float* out, int nthreads);
+
+/* i4_dot (scalar fold) and i4_dot_avx2 (the x86 production order). */
+float fro_i4_dot(const uint8_t* prow, const float* a, const float* scale,
+                 size_t g, size_t k);
+float fro_i4_dot_avx2(const uint8_t* prow, const float* a, const float* scale,
+                      size_t g, size_t k);
+/* Bundle::mm I4 arm: M==1 uses the AVX2 order, M>1 dequant + f32 GEMM.
+ * packed (N, ceil(K/2)), scale f32 (N, ceil(K/g)). */
+int fro_mm_i4(const float* a, size_t m, size_t k, const uint8_t* packed,
+              const float* scale, size_t n, size_t g, float* out);
+
+/* expert_f32 (i8 arm) + expert_mm: raw (in,out) i8, scale f32 [out]. */
+void fro_expert_mm_i8(const float* x, size_t m, const int8_t* raw,
+                      const float* scale, size_t inp, size_t out, float* y);
+/* f32 GEMM y(m,n) = x(m,k) . w(k,n), sequential-k FMA order. */
+void fro_sgemm(const float* x, size_t m, size_t k, const float* w, size_t n,
+               float* y);
+
+/* Nonlinearities used by the MoE branch. */
+float fro_silu(float x);
+float fro_gelu_tanh(float x);
+
+/* qwen3moe softmax_rows + stable top-k + renorm; gemma4 variant multiplies
+ * by per_expert_scale (nullable).  sel (T,topk) int32, w (T,topk) f32.
+ * probs (T,E) nullable: the softmax output. */
+void fro_moe_route(const float* logits, size_t T, size_t E, size_t topk,
+                   int norm_topk, const float* per_expert_scale, int32_t* sel,
+                   float* w, float* probs);
+
+/* Full routed expert layer (qwen3moe moe_branch minus the router mm).
+ * act 0: SwiGLU with separate gate/up (qwen3moe); act 1: gelu_tanh with a
+ * packed gate_up expert (gemma4).  Expert e's arrays: gate[e]/up[e] (in=d,
+ * out=mi) or gate[e] = gate_up (d, 2mi); down[e] (mi, d); i8 (in,out) with
+ * f32 scales.  Experts are combined in ascending expert order. */
+int fro_moe(const float* x, size_t T, size_t d, const float* logits, size_t E,
+            size_t topk, int norm_topk, const float* per_expert_scale,
+            size_t mi, int act, const int8_t* const* gate,
+            const float* const* gate_scale, const int8_t* const* up,
+            const float* const* up_scale, const int8_t* const* down,
+            const float* const* down_scale, float* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,184 @@
+"""Parity of the gfx950 int8 / int4 linear (libfrq.so through the C ABI)
+against the CPU oracle on the same seeded inputs.
+
+Bars: activation quant (a8, sa, outliers) and the i32 accumulators
+bit-exact; int8 f32 outputs bit-exact on the GEMV path (same operation
+order as the oracle) and on the MFMA path within
+  |gpu - oracle| <= 1e-6 * |scale| * (|sa*acc| + sum_t |av_t * w_t|)
+per element (the outlier correction runs on 24-bit fixed-point MFMA there);
+int4 within 1e-5 of sum |a*w| per element (north_star allows 1e-4).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from fieldrun_amd import synth, convert
+
+pytestmark = pytest.mark.gpu
+
+
+def case(m, k, n, seed, outliers=True):
+    a = synth.activations(m, k, seed, 20.0 if outliers else 1.0)
+    wt, scale = synth.int8_weight(n, k, seed)
+    return a, wt, scale
+
+
+def check_quant(a, a8, sa, oi, ov):
+    for i in range(a.shape[0]):
+        q8, qsa, qoi, qov = oracle.quant_row(a[i])
+        t = len(qoi)
+        assert np.array_equal(a8[i], q8), f"a8 row {i}"
+        assert sa[i].view(np.uint32) == np.float32(qsa).view(np.uint32), f"sa row {i}"
+        assert np.array_equal(oi[i, :t], qoi), f"oidx row {i}"
+        assert np.array_equal(ov[i, :t].view(np.uint32), qov.view(np.uint32)), f"oval row {i}"
+
+
+def corr_mag(a, wt, scale, acc):
+    mags = []
+    for i in range(a.shape[0]):
+        _, sa, oi, ov = oracle.quant_row(a[i])
+        c = np.abs(wt[:, oi].astype(np.float64)) @ np.abs(ov.astype(np.float64))
+        mags.append(np.abs(scale) * (np.abs(np.float64(sa) * acc[i].astype(np.float64)) + c))
+    return np.array(mags)
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 896, 4864), (1, 4864, 896), (2, 4096, 1000), (3, 1000, 257),
+                                   (4, 768, 3072), (1, 37, 5), (1, 33, 300), (2, 32, 64), (1, 1, 7),
+                                   (1, 14336, 512), (3, 18944, 64)])
+def test_i8_gemv_bit_exact(ctx, m, k, n):
+    a, wt, scale = case(m, k, n, 100 + m * 7 + k + n)
+    w = ctx.upload_i8(wt, scale)
+    out, acc, a8, sa, oi, ov = w.mm_debug(a)
+    check_quant(a, a8, sa, oi, ov)
+    ref, racc = oracle.mm_i8(a, wt, scale, with_acc=True)
+    assert np.array_equal(acc, racc)
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+    assert np.array_equal(w.mm(a).view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("m,k,n", [(5, 896, 4864), (16, 4096, 1024), (128, 896, 640), (130, 512, 300),
+                                   (64, 37, 50), (16, 14336, 256), (33, 4864, 896), (200, 128, 129)])
+def test_i8_gemm_acc_exact_out_within_tol(ctx, m, k, n):
+    a, wt, scale = case(m, k, n, 200 + m + k + n)
+    w = ctx.upload_i8(wt, scale)
+    out, acc, a8, sa, oi, ov = w.mm_debug(a)
+    check_quant(a, a8, sa, oi, ov)
+    ref, racc = oracle.mm_i8(a, wt, scale, with_acc=True)
+    assert np.array_equal(acc, racc)
+    mag = corr_mag(a, wt, scale, racc)
+    err = np.abs(out.astype(np.float64) - ref.astype(np.float64))
+    assert np.all(err <= 1e-6 * mag + 1e-30), float((err / (mag + 1e-30)).max())
+    rel = err.max(axis=1) / np.abs(ref).max(axis=1)
+    assert rel.max() <= 1e-5
+
+
+def test_i8_activation_edge_cases(ctx):
+    k, n = 200, 96
+    wt, scale = synth.int8_weight(n, k, 7)
+    w = ctx.upload_i8(wt, scale)
+    rows = [np.zeros(k), np.ones(k), -np.ones(k), np.round(np.linspace(-3, 3, k) * 2) / 2,
+            np.where(np.arange(k) % 3 == 0, 5.0, 1.0), np.full(k, 1e-40),
+            np.concatenate([[np.inf, -np.inf], np.ones(k - 2)]),
+            np.concatenate([[3e38, -3e38], np.linspace(0, 1, k - 2)])]
+    a = np.array(rows, np.float32)
+    for mm in (a[:4], a):  # GEMV path (M <= 4) and MFMA path (M = 8)
+        out, acc, a8, sa, oi, ov = w.mm_debug(mm)
+        check_quant(mm, a8, sa, oi, ov)
+        ref, racc = oracle.mm_i8(mm, wt, scale, with_acc=True)
+        assert np.array_equal(acc, racc)
+        assert np.array_equal(np.isnan(out), np.isnan(ref))
+        assert np.array_equal(np.isinf(out), np.isinf(ref))
+        fin = np.isfinite(ref)
+        assert np.array_equal(out[~fin & ~np.isnan(ref)], ref[~fin & ~np.isnan(ref)])
+        if len(mm) <= 4:
+            assert np.array_equal(out[fin], ref[fin])
+        else:
+            with np.errstate(invalid="ignore", over="ignore"):
+                mag = corr_mag(mm, wt, scale, racc)
+            ok = fin & np.isfinite(mag)
+            assert np.all(np.abs(out[ok].astype(np.float64) - ref[ok]) <= 1e-6 * mag[ok] + 1e-30)
+
+
+def test_i8_nan_is_an_error_like_the_reference(ctx):
+    import fieldrun_amd as fa
+    wt, scale = synth.int8_weight(64, 100, 8)
+    w = ctx.upload_i8(wt, scale)
+    for m in (1, 9):
+        a = np.ones((m, 100), np.float32)
+        a[m - 1, 50] = np.nan
+        with pytest.raises(fa.FrqError) as ei:
+            w.mm(a)
+        assert ei.value.code == fa.FRQ_ERR_NAN
+    # the context stays usable, and K <= 32 with NaN does not raise
+    a = np.ones((1, 100), np.float32)
+    assert np.array_equal(w.mm(a), oracle.mm_i8(a, wt, scale))
+    wt2, sc2 = synth.int8_weight(8, 20, 9)
+    w2 = ctx.upload_i8(wt2, sc2)
+    b = np.ones((1, 20), np.float32)
+    b[0, 3] = np.nan
+    assert np.all(np.isnan(w2.mm(b)) == np.isnan(oracle.mm_i8(b, wt2, sc2)))
+
+
+def test_i8_bundle_upload_matches_transposed(ctx):
+    rng = np.random.default_rng(5)
+    src = (rng.standard_normal((300, 700)) * 0.02).astype(np.float32)  # (out, in)
+    w_kn, s16 = convert.put_i8(src, transpose=True)
+    a = synth.activations(3, 700, 11)
+    wb = ctx.upload_i8_bundle(w_kn, s16)
+    wt = np.ascontiguousarray(oracle.i8_transpose(w_kn))
+    sc = s16.astype(np.float32)
+    wd = ctx.upload_i8(wt, sc)
+    ref = oracle.mm_i8(a, wt, sc)
+    assert np.array_equal(wb.mm(a).view(np.uint32), ref.view(np.uint32))
+    assert np.array_equal(wd.mm(a).view(np.uint32), ref.view(np.uint32))
+    a6 = synth.activations(6, 700, 12)
+    assert np.array_equal(wb.mm(a6), wd.mm(a6))
+
+
+@pytest.mark.parametrize("k,n", synth.SWEEP_KN)
+def test_i8_sweep_full_shapes(ctx, k, n):
+    """configs[1] shapes at full size: M=1 fully against the oracle, M=128
+    and M=2048 on sampled rows (rows are independent)."""
+    a, wt, scale = case(2048, k, n, synth.seed(1))
+    w = ctx.upload_i8(wt, scale)
+    out1, acc1, *_ = w.mm_debug(a[:1])
+    ref1, racc1 = oracle.mm_i8(a[:1], wt, scale, with_acc=True)
+    assert np.array_equal(acc1, racc1) and np.array_equal(out1, ref1)
+    rows = np.array([0, 1, 127, 1000, 2047])
+    for m in (128, 2048):
+        out, acc, *_ = w.mm_debug(a[:m])
+        r = rows[rows < m]
+        ref, racc = oracle.mm_i8(a[r], wt, scale, with_acc=True)
+        assert np.array_equal(acc[r], racc)
+        mag = corr_mag(a[r], wt, scale, racc)
+        assert np.all(np.abs(out[r].astype(np.float64) - ref) <= 1e-6 * mag + 1e-30)
+
+
+# ------------------------------------------------------------------ int4 ----
+def i4_mag(a, packed, s16, k, g):
+    nib = convert.unpack_i4(packed, k).astype(np.float64)
+    sc = s16.astype(np.float64)[:, np.arange(k) // g]
+    return np.abs(a.astype(np.float64)) @ np.abs(nib * sc).T
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 2048, 2304), (1, 9216, 2304), (1, 2304, 9216), (1, 100, 64),
+                                   (1, 70, 37), (1, 33, 100), (2, 300, 2304), (16, 512, 2304),
+                                   (5, 70, 37), (64, 256, 1024)])
+def test_i4_parity(ctx, m, n, k):
+    packed, s16, g = synth.int4_weight(n, k, 300 + n + k)
+    a = synth.activations(m, k, 400 + m, outlier_scale=1.0)
+    w = ctx.upload_i4(packed, s16, k, g)
+    out = w.mm(a)
+    ref = oracle.mm_i4(a, packed, s16.astype(np.float32), k, g)
+    blocked = (m == 1 and g == 32 and k % 32 == 0)
+    if blocked:
+        mag = i4_mag(a, packed, s16, k, g)
+        assert np.all(np.abs(out - ref) <= 1e-5 * mag + 1e-30)
+    else:  # same operation order as the oracle: bit-exact
+        assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+def test_i4_reference_kat_through_gpu(ctx):
+    """i4_q4a_dot_matches_manual (src/bundle.rs:1306-1314): [0xE1,0xF3] . 1s = 1.0."""
+    w = ctx.upload_i4(np.array([[0xE1, 0xF3]], np.uint8), np.array([[1.0]], np.float16), 4, 4)
+    assert w.mm(np.ones((1, 4), np.float32))[0, 0] == 1.0

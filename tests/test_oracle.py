@@ -1,0 +1,429 @@
+"""Pins the CPU oracle before anything is checked against it.
+
+Each check is independent of the oracle's own code: the reference's unit-test
+known answers (tests/golden/reference_kats.json, lifted from the Rust tests
+cited there), numpy's IEEE binary16 conversions, int64 / float64 brute force,
+and closed-form invariants chosen so that a dropped term, a wrong rounding
+mode, a wrong nibble order or a transposed operand fails one of them.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+
+KATS = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "reference_kats.json")))
+M64 = (1 << 64) - 1
+
+
+def xorshift_i8(seed, n):
+    """The PRNG of i8dot_simd_vs_scalar (src/bundle.rs:1364-1370)."""
+    s = seed
+    out = []
+    for _ in range(n):
+        s ^= (s << 13) & M64
+        s ^= s >> 7
+        s ^= (s << 17) & M64
+        v = s >> 56
+        out.append(v - 256 if v >= 128 else v)
+    return out, s
+
+
+def lcg_u32(seed, add, n):
+    """The LCG of src/jit.rs tests: s = s*6364136223846793005 + add; s>>33."""
+    s = seed
+    out = []
+    for _ in range(n):
+        s = (s * 6364136223846793005 + add) & M64
+        out.append(s >> 33)
+    return out, s
+
+
+def u32_to_unit(u):
+    # Rust: (next() as f32 / u32::MAX as f32) * 2.0 - 1.0 in f32
+    return np.float32(np.float32(u) / np.float32(4294967295.0))
+
+
+def round_half_away(x):
+    x = np.asarray(x, np.float32)
+    r = np.trunc(x)
+    frac = x - r  # exact
+    return r + np.where(np.abs(frac) >= 0.5, np.sign(x), 0).astype(np.float32)
+
+
+# ---------------------------------------------------------------- f16 ----
+def test_f16_to_f32_exhaustive():
+    """Every binary16 pattern (cf. f16_to_f32_simd_vs_scalar, bundle.rs:1384)."""
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = oracle.f16_to_f32(bits)
+    want = bits.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_f32_to_f16_matches_ieee_rne():
+    rng = np.random.default_rng(1)
+    xs = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * np.float32(10.0) ** rng.integers(-9, 6, 20000).astype(np.float32),
+        np.array([0.0, -0.0, 65504, 65520, 65519.99, 1e-8, 5.96e-8, 2.98e-8, 2.9802322e-8, 6.1e-5,
+                  np.inf, -np.inf, 1e30, -1e30], np.float32),
+        # exact ties between adjacent f16 values (RNE must pick even)
+        (np.arange(1, 2048, dtype=np.float32) + np.float32(0.5)) * np.float32(2.0 ** -10),
+    ]).astype(np.float32)
+    got = np.array([oracle.f32_to_f16_bits(x) for x in xs], np.uint16)
+    want = xs.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+# ---------------------------------------------------------- quantisers ----
+def test_put_i8_closed_form_and_kat():
+    rng = np.random.default_rng(2)
+    src = rng.standard_normal((37, 53)).astype(np.float32)  # (out, in) nn.Linear
+    w, s16 = oracle.put_i8(src, transpose=True)
+    sc = np.maximum(np.abs(src).max(axis=1) / np.float32(127.0), np.float32(1e-8)).astype(np.float32)
+    want = np.clip(np.rint(src / sc[:, None]), -127, 127).astype(np.int8).T
+    assert np.array_equal(w, want)
+    assert np.array_equal(s16, sc.astype(np.float16).view(np.uint16))
+    assert w.min() >= -127  # never -128 (convert.rs:349-354)
+    k = KATS["int8_quant_roundtrip"]
+    w, s16 = oracle.put_i8(np.array(k["data"], np.float32).reshape(k["rows"], k["cols"]), k["transpose"])
+    s = s16.view(np.float16).astype(np.float32)
+    rows = w.astype(np.float32) * s[None, :]  # weight_row(m, r) = wt[j*k+r]*scale[j]
+    assert np.allclose(rows, np.array(k["want_rows"]), atol=k["tol"])
+
+
+def test_put_i4_closed_form():
+    rng = np.random.default_rng(3)
+    for out, inp in [(5, 64), (7, 37), (3, 32), (2, 1)]:
+        src = rng.standard_normal((out, inp)).astype(np.float32)
+        packed, s16, g = oracle.put_i4(src, transpose=True)
+        assert g == min(32, inp)
+        ng = (inp + g - 1) // g
+        sc = np.zeros((out, ng), np.float32)
+        for gi in range(ng):
+            blk = src[:, gi * g:(gi + 1) * g]
+            sc[:, gi] = np.maximum(np.abs(blk).max(axis=1) / np.float32(7.0), np.float32(1e-8))
+        q = np.clip(np.rint(src / np.repeat(sc, g, axis=1)[:, :inp]), -7, 7).astype(np.int8)
+        # unpack: even input index = low nibble
+        lo = (packed & 0x0F).astype(np.int8)
+        hi = (packed >> 4).astype(np.int8)
+        nib = np.stack([lo, hi], axis=2).reshape(out, -1)[:, :inp]
+        nib = np.where(nib >= 8, nib - 16, nib)
+        assert np.array_equal(nib, q)
+        assert np.array_equal(s16, sc.astype(np.float16).view(np.uint16))
+
+
+def test_put_embed_i8_kat():
+    k = KATS["rowi8_embed_roundtrip"]
+    data = np.array(k["data"], np.float32).reshape(k["vocab"], k["d"])
+    q, s16 = oracle.put_embed_i8(data)
+    row = q[k["row"]].astype(np.float32) * s16.view(np.float16).astype(np.float32)[k["row"]]
+    assert np.all(np.abs(row - data[k["row"]]) < k["tol"])
+
+
+# ---------------------------------------------------------------- i8dot ----
+def test_i8dot_kats():
+    k = KATS["i8dot_matches_manual"]
+    a, w = np.array(k["a"], np.int8), np.array(k["w"], np.int8)
+    assert oracle.i8dot(a, w) == int(np.dot(a.astype(np.int64), w.astype(np.int64)))
+    k = KATS["i8dot_simd_vs_scalar"]
+    seed = int(k["xorshift_seed"], 16)
+    state = seed
+    for n in k["lengths"]:
+        vals, state = xorshift_i8(state, 2 * n)
+        a = np.array(vals[:n], np.int8)
+        w = np.array(vals[n:], np.int8)
+        # the Rust test draws a (n values) then w (n values) from one stream
+        assert oracle.i8dot(a, w) == int(np.dot(a.astype(np.int64), w.astype(np.int64))), n
+    wc = k["worst_case"]
+    a = np.full(wc["len"], wc["a"], np.int8)
+    w = np.full(wc["len"], wc["w"], np.int8)
+    assert oracle.i8dot(a, w) == 127 * -128 * 4864
+
+
+def test_i8_transpose():
+    rng = np.random.default_rng(4)
+    w = rng.integers(-127, 128, (13, 29), dtype=np.int8)
+    assert np.array_equal(oracle.i8_transpose(w), w.T)
+
+
+# ---------------------------------------------------------- quant_row ----
+def brute_quant(a):
+    """Closed-form restatement of src/bundle.rs:699-708 with sorted ties."""
+    a = np.asarray(a, np.float32)
+    k = a.size
+    t = min(32, k)
+    order = sorted(range(k), key=lambda i: (-abs(float(a[i])), i))
+    bulk = np.float32(abs(a[order[t]])) if t < k else np.float32(0.0)
+    sa = np.float32(bulk / np.float32(127.0)) if bulk > 0 else np.float32(1.0)
+    q = round_half_away(a / sa)
+    a8 = np.clip(np.nan_to_num(q, nan=0.0), -127, 127).astype(np.int8)
+    out_idx = sorted(order[:t])
+    a8[out_idx] = 0
+    return a8, sa, np.array(out_idx, np.uint32), a[out_idx]
+
+
+@pytest.mark.parametrize("k", [1, 5, 32, 33, 37, 64, 100, 896, 4096])
+def test_quant_row_matches_brute_force(k):
+    rng = np.random.default_rng(10 + k)
+    for trial in range(4):
+        a = rng.standard_normal(k).astype(np.float32)
+        if trial == 1 and k > 10:
+            a[rng.choice(k, max(1, k // 100), replace=False)] *= 20  # outlier channels
+        if trial == 2:
+            a = np.round(a * 4) / 4  # many exact ties in |a|
+        if trial == 3:
+            a[: k // 2] = 0.0
+        got = oracle.quant_row(a)
+        want = brute_quant(a)
+        for g, w in zip(got, want):
+            assert np.array_equal(np.asarray(g), np.asarray(w)), (k, trial)
+
+
+def test_quant_row_invariants_and_rounding():
+    rng = np.random.default_rng(11)
+    a = rng.standard_normal(4864).astype(np.float32) * 3
+    a8, sa, oi, ov = oracle.quant_row(a)
+    absa = np.abs(a)
+    srt = np.sort(absa)[::-1]
+    assert sa == np.float32(srt[32] / np.float32(127.0))  # (t+1)-th largest / 127
+    assert len(oi) == 32 and np.all(a8[oi] == 0) and np.array_equal(ov, a[oi])
+    assert set(oi.tolist()) == set(np.argsort(-absa, kind="stable")[:32].tolist())
+    assert np.all(np.abs(a8.astype(int)) <= 127)
+    assert np.all(np.diff(oi.astype(np.int64)) > 0)  # ascending channel order
+    # half-away-from-zero, not ties-to-even: a/sa == 2.5 -> 3, -2.5 -> -3
+    b = np.zeros(40, np.float32)
+    b[:33] = 127.0  # bulk_max 127 -> sa 1
+    b[33], b[34], b[35], b[36] = 2.5, -2.5, 0.5, 3.5
+    a8, sa, _, _ = oracle.quant_row(b)
+    assert sa == 1.0 and list(a8[33:37]) == [3, -3, 1, 4]
+
+
+def test_quant_row_special_cases():
+    a8, sa, oi, ov = oracle.quant_row(np.array([1.0, -2.0, 3.0], np.float32))  # t == K
+    assert sa == 1.0 and not a8.any() and list(oi) == [0, 1, 2]
+    a8, sa, oi, ov = oracle.quant_row(np.zeros(100, np.float32))  # bulk_max == 0
+    assert sa == 1.0 and not a8.any() and list(oi) == list(range(32))
+    x = np.ones(100, np.float32)
+    x[7] = np.nan
+    with pytest.raises(oracle.OracleNaN):
+        oracle.quant_row(x)
+    y = np.array([np.nan, 1.0], np.float32)  # t == K: no select, no panic
+    a8, sa, oi, ov = oracle.quant_row(y)
+    assert sa == 1.0 and np.isnan(ov[0])
+
+
+# ---------------------------------------------------------- I8 linear ----
+def test_mm_i8_f64_brute_force():
+    rng = np.random.default_rng(12)
+    m, k, n = 5, 300, 41
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    a[:, [3, 77, 150]] *= 20
+    wt = rng.integers(-127, 128, (n, k)).astype(np.int8)
+    scale = (rng.uniform(1e-4, 3e-4, n)).astype(np.float16).astype(np.float32)
+    out, acc = oracle.mm_i8(a, wt, scale, with_acc=True)
+    for i in range(m):
+        a8, sa, oi, ov = brute_quant(a[i])
+        acc64 = wt.astype(np.int64) @ a8.astype(np.int64)
+        assert np.array_equal(acc[i], acc64)
+        corr = (wt[:, oi].astype(np.float64) * ov.astype(np.float64)[None, :]).sum(axis=1)
+        ref = scale.astype(np.float64) * (np.float64(sa) * acc64 + corr)
+        mag = np.abs(scale) * (np.abs(np.float64(sa) * acc64) + np.abs(wt[:, oi] * ov[None, :]).sum(axis=1))
+        assert np.all(np.abs(out[i] - ref) <= 1e-6 * mag + 1e-30)
+    # rows are independent and the threaded variant uses the same arithmetic
+    assert np.array_equal(oracle.mm_i8_mt(a, wt, scale, 3), out)
+    assert np.array_equal(oracle.mm_i8_mt(a[:1], wt, scale, 4), out[:1])
+
+
+def test_mm_i8_nan_raises_like_reference():
+    wt = np.ones((4, 40), np.int8)
+    a = np.ones((2, 40), np.float32)
+    a[1, 5] = np.nan
+    with pytest.raises(oracle.OracleNaN):
+        oracle.mm_i8(a, wt, np.ones(4, np.float32))
+
+
+# ------------------------------------------------------------------ i4 ----
+def pack_nibbles(q):
+    q = np.asarray(q, np.int64) & 0xF
+    k = q.shape[-1]
+    if k % 2:
+        q = np.concatenate([q, np.zeros(q.shape[:-1] + (1,), np.int64)], axis=-1)
+    return (q[..., 0::2] | (q[..., 1::2] << 4)).astype(np.uint8)
+
+
+def test_i4_dot_kats():
+    k = KATS["i4_q4a_dot_matches_manual"]
+    for f in (oracle.i4_dot, oracle.i4_dot_avx2):
+        assert f(np.array(k["prow"], np.uint8), np.array(k["a"], np.float32),
+                 np.array(k["scale"], np.float32), k["g"], k["k"]) == k["want_i4"]
+    k = KATS["i4_q4a_dot_simd_vs_reference"]
+    kk, g = k["k"], k["g"]
+    ng = (kk + g - 1) // g
+    nibs = np.array([((i * 7 + 3) % 16) - 8 for i in range(kk)], np.int64)
+    prow = pack_nibbles(nibs)
+    a = np.sin(np.arange(kk, dtype=np.float32) * np.float32(0.13) - np.float32(2.0)).astype(np.float32)
+    scale = (np.float32(0.1) + np.arange(ng, dtype=np.float32) * np.float32(0.05)).astype(np.float32)
+    want = float((a.astype(np.float64) * nibs * scale[np.arange(kk) // g]).sum())
+    for f in (oracle.i4_dot, oracle.i4_dot_avx2):
+        assert abs(f(prow, a, scale, g, kk) - want) < k["tol"]
+
+
+@pytest.mark.parametrize("case", ["jit_i4_dot_matches_scalar", "jit_i4_dot_vec_matches_scalar"])
+def test_i4_dot_jit_lcg_vectors(case):
+    k = KATS[case]
+    cases = [(k["k"], k["g"])] if "cases" not in k else [tuple(c) for c in k["cases"]]
+    for kk, g in cases:
+        nb, ng = (kk + 1) // 2, (kk + g - 1) // g
+        vals, _ = lcg_u32(k["seed"], k["lcg_add"], nb + kk + ng)
+        prow = np.array([v & 0xFF for v in vals[:nb]], np.uint8)
+        a = np.array([u32_to_unit(v) * np.float32(2.0) - np.float32(1.0) for v in vals[nb:nb + kk]], np.float32)
+        scale = np.array([np.float32(0.01) + u32_to_unit(v) * np.float32(0.03) for v in vals[nb + kk:]], np.float32)
+        s = oracle.i4_dot(prow, a, scale, g, kk)
+        v = oracle.i4_dot_avx2(prow, a, scale, g, kk)
+        lo = (prow & 0xF).astype(np.int64)
+        hi = (prow >> 4).astype(np.int64)
+        nib = np.stack([lo, hi], 1).reshape(-1)[:kk]
+        nib = np.where(nib >= 8, nib - 16, nib)
+        want = float((a.astype(np.float64) * nib * scale[np.arange(kk) // g]).sum())
+        assert abs(s - v) < k["tol"] and abs(s - want) < 1e-4 and abs(v - want) < 1e-4
+
+
+def test_i4_avx2_order_is_the_documented_tree():
+    """g=8, one chunk: gsum = ((l0+l4)+(l2+l6))+((l1+l5)+(l3+l7)), l_q = w_q*a_q."""
+    a = np.array([1e8, 1.0, -1e8, 3.0, 0.5, 1.0, 0.25, 7.0], np.float32)
+    nib = np.array([1, 1, 1, 1, 1, 1, 1, 1])
+    prow = pack_nibbles(nib)
+    got = oracle.i4_dot_avx2(prow, a, np.array([1.0], np.float32), 8, 8)
+    l = a.astype(np.float32)
+    f = np.float32
+    want = f(f(f(l[0] + l[4]) + f(l[2] + l[6])) + f(f(l[1] + l[5]) + f(l[3] + l[7])))
+    assert got == want
+    seq = np.float32(0)
+    for x in l:
+        seq = np.float32(seq + x)
+    assert oracle.i4_dot(prow, a, np.array([1.0], np.float32), 8, 8) == seq
+
+
+def test_mm_i4_f64_brute_force():
+    rng = np.random.default_rng(13)
+    for m, k, n in [(1, 96, 7), (3, 96, 7), (4, 37, 5)]:
+        src = rng.standard_normal((n, k)).astype(np.float32)
+        packed, s16, g = oracle.put_i4(src, True)
+        scale = s16.view(np.float16).astype(np.float32)
+        a = rng.standard_normal((m, k)).astype(np.float32)
+        out = oracle.mm_i4(a, packed, scale, k, g)
+        lo = (packed & 0xF).astype(np.int64)
+        hi = (packed >> 4).astype(np.int64)
+        nib = np.stack([lo, hi], 2).reshape(n, -1)[:, :k]
+        nib = np.where(nib >= 8, nib - 16, nib)
+        w = nib * scale[:, np.arange(k) // g].astype(np.float64)  # (n, k)
+        ref = a.astype(np.float64) @ w.T
+        mag = np.abs(a.astype(np.float64)) @ np.abs(w.T)
+        assert np.all(np.abs(out - ref) <= 1e-5 * mag + 1e-12)
+
+
+# ------------------------------------------------------------ experts ----
+def test_expert_mm_and_sgemm_f64():
+    rng = np.random.default_rng(14)
+    x = rng.standard_normal((6, 64)).astype(np.float32)
+    raw = rng.integers(-127, 128, (64, 48)).astype(np.int8)
+    sc = rng.uniform(1e-3, 3e-3, 48).astype(np.float16).astype(np.float32)
+    y = oracle.expert_mm_i8(x, raw, sc)
+    v = raw.astype(np.float64) * sc.astype(np.float64)[None, :]
+    ref = x.astype(np.float64) @ v
+    assert np.all(np.abs(y - ref) <= 1e-5 * (np.abs(x) @ np.abs(v)) + 1e-12)
+
+
+def test_nonlinearities():
+    xs = np.linspace(-8, 8, 101).astype(np.float32)
+    s = np.array([oracle.silu(x) for x in xs])
+    assert np.allclose(s, xs / (1 + np.exp(-xs.astype(np.float64))), rtol=1e-6, atol=1e-7)
+    g = np.array([oracle.gelu_tanh(x) for x in xs])
+    x64 = xs.astype(np.float64)
+    want = 0.5 * x64 * (1 + np.tanh(np.sqrt(2 / np.pi) * (x64 + 0.044715 * x64 ** 3)))
+    assert np.allclose(g, want, rtol=1e-5, atol=1e-6)
+
+
+def test_moe_route_brute_force():
+    rng = np.random.default_rng(15)
+    T, E, k = 64, 128, 8
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    logits[3, 10] = logits[3, 20] = 9.0  # an exact tie: lower expert first
+    for norm in (True, False):
+        sel, w, probs = oracle.moe_route(logits, k, norm)
+        l64 = logits.astype(np.float64)
+        p64 = np.exp(l64 - l64.max(1, keepdims=True))
+        p64 /= p64.sum(1, keepdims=True)
+        assert np.allclose(probs, p64, rtol=2e-6, atol=1e-9)
+        for t in range(T):
+            order = sorted(range(E), key=lambda e: (-float(probs[t, e]), e))[:k]
+            assert list(sel[t]) == order
+            den = np.float32(sum(probs[t, order])) if norm else np.float32(1.0)
+            assert np.allclose(w[t], probs[t, order] / den, rtol=1e-6)
+        assert sel[3, 0] == 10 and sel[3, 1] == 20
+    pes = rng.uniform(0.5, 1.5, E).astype(np.float32)
+    sel, w2, probs = oracle.moe_route(logits, k, True, pes)
+    sel_n, w_n, _ = oracle.moe_route(logits, k, True)
+    assert np.array_equal(sel, sel_n)
+    assert np.allclose(w2, w_n * pes[sel], rtol=1e-6)
+
+
+def make_experts(rng, E, d, mi, act):
+    gw = mi if act == 0 else 2 * mi
+    gate = [rng.integers(-127, 128, (d, gw)).astype(np.int8) for _ in range(E)]
+    gs = [rng.uniform(1e-3, 2e-3, gw).astype(np.float32) for _ in range(E)]
+    up = [rng.integers(-127, 128, (d, mi)).astype(np.int8) for _ in range(E)]
+    us = [rng.uniform(1e-3, 2e-3, mi).astype(np.float32) for _ in range(E)]
+    down = [rng.integers(-127, 128, (mi, d)).astype(np.int8) for _ in range(E)]
+    ds = [rng.uniform(1e-3, 2e-3, d).astype(np.float32) for _ in range(E)]
+    return gate, gs, up, us, down, ds
+
+
+@pytest.mark.parametrize("act", [0, 1])
+def test_moe_f64_brute_force(act):
+    rng = np.random.default_rng(16 + act)
+    T, E, d, mi, k = 24, 8, 64, 32, 3
+    x = rng.standard_normal((T, d)).astype(np.float32)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    gate, gs, up, us, down, ds = make_experts(rng, E, d, mi, act)
+    pes = rng.uniform(0.5, 1.5, E).astype(np.float32) if act else None
+    out = oracle.moe(x, logits, k, True, gate, gs, up, us, down, ds, act, pes)
+    sel, w, _ = oracle.moe_route(logits, k, True, pes)
+    ref = np.zeros((T, d))
+    for t in range(T):
+        for i in range(k):
+            e = sel[t, i]
+            x64 = x[t].astype(np.float64)
+            g = x64 @ (gate[e] * gs[e][None, :].astype(np.float64))
+            if act == 0:
+                u = x64 @ (up[e] * us[e][None, :].astype(np.float64))
+                h = g / (1 + np.exp(-g)) * u
+            else:
+                gg, uu = g[:mi], g[mi:]
+                h = 0.5 * gg * (1 + np.tanh(np.sqrt(2 / np.pi) * (gg + 0.044715 * gg ** 3))) * uu
+            ref[t] += w[t, i] * (h @ (down[e] * ds[e][None, :].astype(np.float64)))
+    assert np.max(np.abs(out - ref)) <= 1e-5 * np.max(np.abs(ref))
+
+
+# ------------------------------------------- package quantisers vs oracle ----
+def test_package_quantisers_match_oracle():
+    from fieldrun_amd import convert
+    rng = np.random.default_rng(17)
+    for shape, tr in [((37, 53), True), ((64, 33), False), ((5, 1), True), ((3, 96), True)]:
+        src = (rng.standard_normal(shape) * 0.02).astype(np.float32)
+        w1, s1 = convert.put_i8(src, tr)
+        w2, s2 = oracle.put_i8(src, tr)
+        assert np.array_equal(w1, w2) and np.array_equal(s1.view(np.uint16), s2)
+        p1, t1, g1 = convert.put_i4(src, tr)
+        p2, t2, g2 = oracle.put_i4(src, tr)
+        assert g1 == g2 and np.array_equal(p1, p2) and np.array_equal(t1.view(np.uint16), t2)
+        k = src.shape[1] if tr else src.shape[0]
+        assert np.array_equal(convert.unpack_i4(p1, k).shape, (p1.shape[0], k))
+    e = rng.standard_normal((9, 17)).astype(np.float32)
+    q1, s1 = convert.put_embed_i8(e)
+    q2, s2 = oracle.put_embed_i8(e)
+    assert np.array_equal(q1, q2) and np.array_equal(s1.view(np.uint16), s2)
