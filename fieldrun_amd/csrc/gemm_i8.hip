@@ -70,7 +70,7 @@ __global__ __launch_bounds__(256) void union_kernel(
     __syncthreads();
     for (int i = tid; i < nrows * t; i += 256) {
         const uint32_t c = oidx[(size_t)(r0 + i / t) * FRQ_T + i % t];
-        atomicOr(&bitmap[c >> 5], 1u << (c & 31));
+        if (c < (uint32_t)K) atomicOr(&bitmap[c >> 5], 1u << (c & 31));
     }
     __syncthreads();
     // prefix popcount over words (contiguous chunk per thread)
@@ -129,7 +129,7 @@ __global__ __launch_bounds__(256) void union_kernel(
         for (uint32_t ch = 0; ch < nup; ch += 16) {
             uint32_t v0[4] = {0, 0, 0, 0}, v1[4] = {0, 0, 0, 0}, v2[4] = {0, 0, 0, 0};
             while (!fin && tid < nrows && q < t) {
-                const uint32_t c = oidx[(size_t)row * FRQ_T + q];
+                const uint32_t c = min(oidx[(size_t)row * FRQ_T + q], (uint32_t)(K - 1));
                 const uint32_t pos = wpre[c >> 5] + __popc(bitmap[c >> 5] & ((1u << (c & 31)) - 1u));
                 if (pos >= ch + 16) break;
                 float xf = rintf(oval[(size_t)row * FRQ_T + q] / so);
@@ -302,7 +302,8 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(
                     corr = -0.0f;
                     const int8_t* wrow = W + (size_t)j * Kp;
                     for (int q = 0; q < t; ++q)
-                        corr = corr + oval[(size_t)i * FRQ_T + q] * (float)wrow[oidx[(size_t)i * FRQ_T + q]];
+                        corr = corr + oval[(size_t)i * FRQ_T + q] *
+                                          (float)wrow[min(oidx[(size_t)i * FRQ_T + q], (uint32_t)(Kp - 1))];
                 }
                 out[(size_t)i * N + j] = scale[j] * (sai * (float)av + corr);
                 if (acc_dbg) acc_dbg[(size_t)i * N + j] = av;

@@ -120,7 +120,7 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(
             const int8_t* wrow = W + (size_t)j * Kp;
             float corr = -0.0f;
             for (int q = 0; q < t; ++q)
-                corr = corr + s_ov[m][q] * (float)wrow[s_oi[m][q]];
+                corr = corr + s_ov[m][q] * (float)wrow[min(s_oi[m][q], (uint32_t)(Kp - 1))];
             const float sam = sa[m];
             out[(size_t)m * N + j] = scale[j] * (sam * (float)total + corr);
             if (acc_dbg) acc_dbg[(size_t)m * N + j] = total;

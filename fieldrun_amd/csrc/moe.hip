@@ -101,8 +101,16 @@ __global__ __launch_bounds__(256) void route_kernel(
         m = fmaxf(m, __shfl_xor(m, off, 64));
         bad |= __shfl_xor(bad, off, 64);
     }
-    // sort_by(partial_cmp().unwrap()) panics on NaN: raise err, skip token
-    if (active && bad && lane == 0) atomicOr(err, 1);
+    // sort_by(partial_cmp().unwrap()) panics on NaN: raise err; the token
+    // gets experts 0..k-1 with weight 0 so the rest of the pipeline stays in
+    // bounds (the call reports FRQ_ERR_NAN)
+    if (active && bad && lane == 0) {
+        atomicOr(err, 1);
+        for (int i = 0; i < topk; ++i) {
+            sel[(size_t)t * topk + i] = i;
+            wout[(size_t)t * topk + i] = 0.0f;
+        }
+    }
     const bool go = active && !bad;
     for (int e = lane; e < E && go; e += 64) p[e] = expf(row[e] - m);
     __syncthreads();
@@ -162,7 +170,10 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(
     for (int e = tid; e < E; e += 1024) run[e] = 0;
     __syncthreads();
     // pass 1: counts
-    for (int i = tid; i < T * topk; i += 1024) atomicAdd(&run[sel[i]], 1u);
+    for (int i = tid; i < T * topk; i += 1024) {
+        const int e = sel[i];
+        if (e >= 0 && e < E) atomicAdd(&run[e], 1u);
+    }
     __syncthreads();
     if (tid == 0) {
         int acc = 0, nt = 0;
@@ -187,7 +198,7 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(
         __syncthreads();
         for (int i = tid; i < tn * topk; i += 1024) {
             const int tt = i / topk, e = sel[(size_t)t0 * topk + i];
-            atomicOr(&bm[(size_t)e * nwc + (tt >> 5)], 1u << (tt & 31));
+            if (e >= 0 && e < E) atomicOr(&bm[(size_t)e * nwc + (tt >> 5)], 1u << (tt & 31));
         }
         __syncthreads();
         for (int e = tid; e < E; e += 1024) {
@@ -201,6 +212,7 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(
         __syncthreads();
         for (int i = tid; i < tn * topk; i += 1024) {
             const int tt = i / topk, e = sel[(size_t)t0 * topk + i];
+            if (e < 0 || e >= E) continue;
             const uint32_t word = bm[(size_t)e * nwc + (tt >> 5)];
             const uint32_t rank = pre[(size_t)e * nwc + (tt >> 5)] + __popc(word & ((1u << (tt & 31)) - 1u));
             const int prow = (int)offl[e] + (int)rank;
@@ -308,6 +320,7 @@ __global__ void combine_kernel(const float* __restrict__ dn, const int32_t* __re
             const int ev = st[q];
             if (ev > last && ev < be) { be = ev; best = q; }
         }
+        if (best < 0) break;
         last = be;
         acc = acc + w[(size_t)t * topk + best] * dn[(size_t)pos[(size_t)t * topk + best] * d + c];
     }

@@ -154,7 +154,15 @@ __global__ __launch_bounds__(BLOCK) void quant_rows(
     uint32_t bulk = 0;
     if (t < K) {
         if (nan_flag) {
-            if (tid == 0) atomicOr(err, 1);
+            // the reference panics here; the call reports FRQ_ERR_NAN.  Write
+            // in-bounds placeholders (a8 = 0, sa = 1, outliers 0..t-1 with
+            // value 0) so the kernels queued after this one read valid data.
+            if (tid == 0) { atomicOr(err, 1); sa_out[row] = 1.0f; }
+            for (int k = tid; k < Kp; k += BLOCK) q[k] = 0;
+            for (int k = tid; k < FRQ_T; k += BLOCK) {
+                oidx[(size_t)row * FRQ_T + k] = k < t ? (uint32_t)k : 0u;
+                oval[(size_t)row * FRQ_T + k] = 0.0f;
+            }
             return;  // uniform across the block
         }
         // 2. lower bound tau0 from the thread maxima
@@ -200,7 +208,8 @@ __global__ __launch_bounds__(BLOCK) void quant_rows(
         uint32_t gt_total, ties_total;
         block_excl_scan<BLOCK>(gt, scan_lds, &gt_total);
         uint32_t tie_base = block_excl_scan<BLOCK>(ties, scan_lds, &ties_total);
-        const uint32_t need = (uint32_t)t - gt_total;  // ties to take (>= 1)
+        // ties to take (>= 1 when bulk is the exact (t+1)-th largest)
+        const uint32_t need = gt_total < (uint32_t)t ? (uint32_t)t - gt_total : 0u;
         uint32_t take = need > tie_base ? min(need - tie_base, ties) : 0u;
         uint32_t sel_total;
         uint32_t base = block_excl_scan<BLOCK>(gt + take, scan_lds, &sel_total);
@@ -211,7 +220,7 @@ __global__ __launch_bounds__(BLOCK) void quant_rows(
                 uint32_t b = absbits(v);
                 bool s = b > bulk;
                 if (b == bulk) { s = tie_seen < take; tie_seen++; }
-                if (s) {
+                if (s && base < (uint32_t)FRQ_T) {
                     sel_i[base] = (uint32_t)k;
                     sel_v[base] = v;
                     atomicOr(&bitmap[k >> 5], 1u << (k & 31));
