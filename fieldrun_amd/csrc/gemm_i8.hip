@@ -29,8 +29,7 @@ namespace frq {
 
 namespace {
 
-constexpr int BM = 128, BN = 128, BK = 128;
-constexpr int LP = BK + 16;          // LDS row pitch (bytes): conflict-free
+constexpr int BM = 128, BK = 128;   // union tile rows; union padding unit
 constexpr int UMAX = BM * FRQ_T;     // max union size per M tile
 constexpr float XMAX = 8323072.0f;   // 127 * 2^16
 
@@ -154,44 +153,58 @@ __global__ __launch_bounds__(256) void union_kernel(
 }
 
 // ---- the GEMM -------------------------------------------------------------
-__device__ __forceinline__ v4i mfma(const int4 a, const int4 b, v4i c) {
-    v4i av = {a.x, a.y, a.z, a.w}, bv = {b.x, b.y, b.z, b.w};
-    return __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, c, 0, 0, 0);
+// 128 x 256 output tile per 256-thread workgroup; waves 2 (M) x 2 (N), each
+// 64 x 128 = 4 x 8 blocks of v_mfma_i32_16x16x64_i8.  k-step 64; a ring of
+// NST stages in LDS filled by global_load_lds_dwordx4, each 1 KB LDS block
+// holding one 16-row x 64-byte MFMA operand in lane order (lane l = 16*g + r
+// -> row r, bytes 16g..16g+15), so every operand fetch is one conflict-free
+// ds_read_b128 at block*1024 + lane*16.
+constexpr int GBM = 128, GBN = 256, GBK = 64, NST = 3;
+constexpr int ABLK = GBM / 16, BBLK = GBN / 16, SBLK = ABLK + BBLK;  // 8 + 16 blocks
+constexpr int STAGE = SBLK * 1024;                                   // 24 KB
+
+typedef __attribute__((address_space(1))) void gvoid_t;
+typedef __attribute__((address_space(3))) void lvoid_t;
+
+__device__ __forceinline__ void dma16(const void* g, void* lds_base) {
+    __builtin_amdgcn_global_load_lds((gvoid_t*)g, (lvoid_t*)lds_base, 16, 0, 0);
 }
 
-// 16 x int4 of a 128x128-byte tile per thread-quad: thread tid owns rows
-// tid/8 + 32*i (i < 4), 16-byte column chunk tid%8.
-__device__ __forceinline__ void load_tile(const int8_t* __restrict__ g, size_t pitch,
-                                          int4 (&r)[4]) {
-    const int tid = threadIdx.x;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        r[i] = *reinterpret_cast<const int4*>(g + (size_t)(tid / 8 + 32 * i) * pitch + (tid % 8) * 16);
-}
-__device__ __forceinline__ void store_tile(int8_t* s, const int4 (&r)[4]) {
-    const int tid = threadIdx.x;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        *reinterpret_cast<int4*>(s + (tid / 8 + 32 * i) * LP + (tid % 8) * 16) = r[i];
+// s_waitcnt vmcnt(n) (gfx9 encoding; expcnt / lgkmcnt not waited on)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
 }
 
-__device__ __forceinline__ void mma_tile(const int8_t* As, const int8_t* Bs,
-                                         v4i (&acc)[4][4]) {
+__device__ __forceinline__ v4i mfma(const v4i a, const v4i b, v4i c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// Issue this wave's 6 block loads of k-step ks into LDS stage buffer `st`.
+__device__ __forceinline__ void issue_stage(const int8_t* __restrict__ A, const int8_t* __restrict__ W,
+                                            int Kp, int m0, int n0, int ks, int8_t* st) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int r = lane & 15, g = lane >> 4;
+    const size_t k0 = (size_t)ks * GBK + g * 16;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-        int4 af[4], bf[4];
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            af[b] = *reinterpret_cast<const int4*>(As + (wm * 64 + b * 16 + (lane & 15)) * LP + kb * 64 + (lane >> 4) * 16);
-            bf[b] = *reinterpret_cast<const int4*>(Bs + (wn * 64 + b * 16 + (lane & 15)) * LP + kb * 64 + (lane >> 4) * 16);
-        }
-#pragma unroll
-        for (int bm = 0; bm < 4; ++bm)
-#pragma unroll
-            for (int bn = 0; bn < 4; ++bn) acc[bm][bn] = mfma(af[bm], bf[bn], acc[bm][bn]);
+    for (int i = 0; i < SBLK / 4; ++i) {
+        const int t = wave + 4 * i;
+        const int8_t* src = t < ABLK ? A + (size_t)(m0 + 16 * t + r) * Kp + k0
+                                     : W + (size_t)(n0 + 16 * (t - ABLK) + r) * Kp + k0;
+        dma16(src, st + t * 1024);
     }
+}
+
+// Bijective XCD-aware tile order: workgroups on the same XCD (id % 8) take a
+// contiguous run of tiles ordered N-tile major, M-tile minor, so the A
+// panel is shared in that XCD's L2 and each weight panel is read once.
+__device__ __forceinline__ void tile_of(int b, int G, int MT, int& mt, int& nt) {
+    const int x = b & 7, j = b >> 3;
+    const int q = G >> 3, rem = G & 7;
+    const int start = x * q + min(x, rem);
+    const int tau = start + j;
+    nt = tau / MT;
+    mt = tau % MT;
 }
 
 __global__ __launch_bounds__(256) void gemm_i8_kernel(
@@ -200,115 +213,153 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(
     const float* __restrict__ sa, int M, int N, int Np, int Kp, int t,
     UnionView uv, const uint32_t* __restrict__ oidx,
     const float* __restrict__ oval, float* __restrict__ out,
-    int32_t* __restrict__ acc_dbg) {
-    __shared__ __attribute__((aligned(16))) int8_t As[BM * LP];
-    __shared__ __attribute__((aligned(16))) int8_t Bs[BN * LP];
+    int32_t* __restrict__ acc_dbg, int MT) {
+    __shared__ __attribute__((aligned(1024))) int8_t lds[NST * STAGE];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1;
-    const int n0 = blockIdx.x * BN, tile = blockIdx.y, m0 = tile * BM;
+    int mt, nt;
+    tile_of(blockIdx.x, gridDim.x, MT, mt, nt);
+    const int m0 = mt * GBM, n0 = nt * GBN;
+    const int S = Kp / GBK;
 
-    // ---- corr = so * C, C via three int8 digit GEMMs over the union ----
-    float accf[4][4][4];
+    v4i acc[4][8];
 #pragma unroll
     for (int a = 0; a < 4; ++a)
 #pragma unroll
-        for (int b = 0; b < 4; ++b)
+        for (int b = 0; b < 8; ++b) acc[a][b] = v4i{0, 0, 0, 0};
+
+    issue_stage(A, W, Kp, m0, n0, 0, lds);
+    if (S > 1) issue_stage(A, W, Kp, m0, n0, 1, lds + STAGE);
+    for (int s = 0; s < S; ++s) {
+        if (s + 1 < S) wait_vm<SBLK / 4>(); else wait_vm<0>();
+        __syncthreads();
+        if (s + 2 < S) issue_stage(A, W, Kp, m0, n0, s + 2, lds + ((s + 2) % NST) * STAGE);
+        const int8_t* st = lds + (s % NST) * STAGE;
+        v4i af[4], bf[8];
 #pragma unroll
-            for (int c = 0; c < 4; ++c) accf[a][b][c] = 0.0f;
-    const int nu = uv.nu[tile];
-    const int nup = (nu + BK - 1) / BK * BK;
-    const uint32_t* U = uv.u + (size_t)tile * UMAX;
-    for (int d = 2; d >= 0 && nu > 0; --d) {
-        v4i acc[4][4];
+        for (int bm = 0; bm < 4; ++bm)
+            af[bm] = *reinterpret_cast<const v4i*>(st + (wm * 4 + bm) * 1024 + lane * 16);
 #pragma unroll
-        for (int a = 0; a < 4; ++a)
+        for (int bn = 0; bn < 8; ++bn)
+            bf[bn] = *reinterpret_cast<const v4i*>(st + (ABLK + wn * 8 + bn) * 1024 + lane * 16);
 #pragma unroll
-            for (int b = 0; b < 4; ++b) acc[a][b] = v4i{0, 0, 0, 0};
-        const int8_t* Dd = uv.d + ((size_t)tile * 3 + d) * BM * UMAX;
-        for (int u0 = 0; u0 < nup; u0 += BK) {
-            int4 ra[4];
-            load_tile(Dd + u0, UMAX, ra);
-            // B^T chunk: channel U[u0+uu], columns n0..n0+127 from wkn
-            int4 rb[4];
+        for (int bm = 0; bm < 4; ++bm)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int uu = tid / 8 + 32 * i;
-                rb[i] = *reinterpret_cast<const int4*>(Wkn + (size_t)U[u0 + uu] * Np + n0 + (tid % 8) * 16);
-            }
-            __syncthreads();
-            store_tile(As, ra);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int uu = tid / 8 + 32 * i, jb = (tid % 8) * 16;
-                const uint32_t w4[4] = {(uint32_t)rb[i].x, (uint32_t)rb[i].y, (uint32_t)rb[i].z, (uint32_t)rb[i].w};
-#pragma unroll
-                for (int b = 0; b < 16; ++b) Bs[(jb + b) * LP + uu] = (int8_t)(w4[b >> 2] >> ((b & 3) * 8));
-            }
-            __syncthreads();
-            mma_tile(As, Bs, acc);
-        }
-#pragma unroll
-        for (int a = 0; a < 4; ++a)
-#pragma unroll
-            for (int b = 0; b < 4; ++b)
-#pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    accf[a][b][c] = accf[a][b][c] * 256.0f + (float)acc[a][b][c];
+            for (int bn = 0; bn < 8; ++bn) acc[bm][bn] = mfma(af[bm], bf[bn], acc[bm][bn]);
     }
 
-    // ---- acc = a8 . wt^T ----
-    v4i acc[4][4];
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-        for (int b = 0; b < 4; ++b) acc[a][b] = v4i{0, 0, 0, 0};
-    const int8_t* Ag = A + (size_t)m0 * Kp;
-    const int8_t* Bg = W + (size_t)n0 * Kp;
-    int4 ra[4], rb[4];
-    load_tile(Ag, Kp, ra);
-    load_tile(Bg, Kp, rb);
-    for (int k0 = 0; k0 < Kp; k0 += BK) {
-        __syncthreads();
-        store_tile(As, ra);
-        store_tile(Bs, rb);
-        __syncthreads();
-        if (k0 + BK < Kp) {
-            load_tile(Ag + k0 + BK, Kp, ra);
-            load_tile(Bg + k0 + BK, Kp, rb);
-        }
-        mma_tile(As, Bs, acc);
+    // ---- epilogue, one 32-column sub-tile (2 MFMA blocks) at a time:
+    // t = sa * acc, plus the outlier correction so * C from three int8 digit
+    // MFMAs over the tile's channel union, then out = scale * t.  Lane holds
+    // rows 4*(lane/16)+c and column lane%16 of each 16x16 block.
+    // per-row sa, so and the non-finite flag of the tile, in the last stage
+    // buffer (free in the epilogue)
+    float* meta = reinterpret_cast<float*>(lds + 2 * STAGE + 16 * 1024);
+    __syncthreads();
+    if (threadIdx.x < GBM) {
+        const int i = min(m0 + (int)threadIdx.x, M - 1);
+        meta[threadIdx.x] = sa[i];
+        meta[GBM + threadIdx.x] = uv.fin[i] ? 0.0f : uv.so[i];
+        meta[2 * GBM + threadIdx.x] = uv.fin[i] ? 1.0f : 0.0f;
     }
-
-    // ---- epilogue: lane holds rows 4*(lane/16)+c, column lane%16 of each
-    // 16x16 block ----
+    const int nu = uv.nu[mt];
+    const uint32_t* U = uv.u + (size_t)mt * UMAX;
+    const int r = lane & 15, g = lane >> 4;
+    int8_t* bt = lds + 24 * 1024;
+    // stage digit chunk u0 (3 x 8 DMA blocks) and W[:, U[u0..u0+63]]^T (16 blocks)
+    __syncthreads();
+    auto stage_chunk = [&](int u0) {
+        __syncthreads();
 #pragma unroll
-    for (int bm = 0; bm < 4; ++bm)
+        for (int i = 0; i < 6; ++i) {
+            const int tb = wave + 4 * i;  // digit tb/8, row block tb%8
+            const int8_t* src = uv.d + (((size_t)mt * 3 + tb / 8) * BM + 16 * (tb % 8) + r) * UMAX + u0 + g * 16;
+            dma16(src, lds + tb * 1024);
+        }
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int i = m0 + wm * 64 + bm * 16 + (lane >> 4) * 4 + c;
-            if (i >= M) continue;
-            const float sai = sa[i], soi = uv.so[i];
-            const int fin = uv.fin[i];
+        for (int i = 0; i < 4; ++i) {
+            const int idx = threadIdx.x + 256 * i;  // 64 channels x 16 chunks of 16 columns
+            const int uu = idx >> 4, cch = idx & 15;
+            const v4i w = *reinterpret_cast<const v4i*>(Wkn + (size_t)U[u0 + uu] * Np + n0 + cch * 16);
 #pragma unroll
-            for (int bn = 0; bn < 4; ++bn) {
-                const int j = n0 + wn * 64 + bn * 16 + (lane & 15);
-                if (j >= N) continue;
-                const int av = acc[bm][bn][c];
-                float corr;
-                if (!fin) {
-                    corr = soi * accf[bm][bn][c];
-                } else {
-                    corr = -0.0f;
-                    const int8_t* wrow = W + (size_t)j * Kp;
-                    for (int q = 0; q < t; ++q)
-                        corr = corr + oval[(size_t)i * FRQ_T + q] *
-                                          (float)wrow[min(oidx[(size_t)i * FRQ_T + q], (uint32_t)(Kp - 1))];
+            for (int b = 0; b < 16; ++b)
+                bt[cch * 1024 + ((uu >> 4) * 16 + b) * 16 + (uu & 15)] = (int8_t)((uint32_t)w[b >> 2] >> ((b & 3) * 8));
+        }
+        wait_vm<0>();
+        __syncthreads();
+    };
+    const bool one_chunk = nu <= GBK;
+    if (nu > 0 && one_chunk) stage_chunk(0);
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub) {
+        float tv[4][2][4];
+#pragma unroll
+        for (int bm = 0; bm < 4; ++bm)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int rl = wm * 64 + bm * 16 + (lane >> 4) * 4 + c;
+                const float sai = meta[rl];
+#pragma unroll
+                for (int x = 0; x < 2; ++x) {
+                    const int av = acc[bm][sub * 2 + x][c];
+                    if (acc_dbg) {
+                        const int i = m0 + rl;
+                        const int j = n0 + wn * 128 + (sub * 2 + x) * 16 + (lane & 15);
+                        if (i < M && j < N) acc_dbg[(size_t)i * N + j] = av;
+                    }
+                    tv[bm][x][c] = sai * (float)av;
                 }
-                out[(size_t)i * N + j] = scale[j] * (sai * (float)av + corr);
-                if (acc_dbg) acc_dbg[(size_t)i * N + j] = av;
+            }
+        for (int u0 = 0; u0 < nu; u0 += GBK) {
+            if (!one_chunk) stage_chunk(u0);
+            v4i bf2[2];
+#pragma unroll
+            for (int x = 0; x < 2; ++x)
+                bf2[x] = *reinterpret_cast<const v4i*>(bt + (wn * 8 + sub * 2 + x) * 1024 + lane * 16);
+            // tv += so * (C2 * 2^16 + C1 * 2^8 + C0); so is 0 on non-finite rows
+#pragma unroll
+            for (int d = 2; d >= 0; --d) {
+                const float wd = d == 2 ? 65536.0f : (d == 1 ? 256.0f : 1.0f);
+#pragma unroll
+                for (int bm = 0; bm < 4; ++bm) {
+                    const v4i af = *reinterpret_cast<const v4i*>(lds + (d * 8 + wm * 4 + bm) * 1024 + lane * 16);
+#pragma unroll
+                    for (int x = 0; x < 2; ++x) {
+                        const v4i cd = mfma(af, bf2[x], v4i{0, 0, 0, 0});
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) {
+                            const float so = meta[GBM + wm * 64 + bm * 16 + (lane >> 4) * 4 + c];
+                            tv[bm][x][c] = tv[bm][x][c] + (so * wd) * (float)cd[c];
+                        }
+                    }
+                }
             }
         }
+#pragma unroll
+        for (int bm = 0; bm < 4; ++bm)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int i = m0 + wm * 64 + bm * 16 + (lane >> 4) * 4 + c;
+                if (i >= M) continue;
+#pragma unroll
+                for (int x = 0; x < 2; ++x) {
+                    const int j = n0 + wn * 128 + (sub * 2 + x) * 16 + (lane & 15);
+                    if (j >= N) continue;
+                    float v = tv[bm][x][c];
+                    if (meta[2 * GBM + wm * 64 + bm * 16 + (lane >> 4) * 4 + c] != 0.0f) {
+                        // non-finite outlier: exact sequential corr
+                        float corr = -0.0f;
+                        const int8_t* wrow = W + (size_t)j * Kp;
+                        for (int q = 0; q < t; ++q)
+                            corr = corr + oval[(size_t)i * FRQ_T + q] *
+                                              (float)wrow[min(oidx[(size_t)i * FRQ_T + q], (uint32_t)(Kp - 1))];
+                        v = v + corr;
+                    }
+                    out[(size_t)i * N + j] = scale[j] * v;
+                }
+            }
+    }
 }
 
 }  // namespace
@@ -337,12 +388,11 @@ hipError_t launch_gemm_i8(const Weight& w, size_t m, const int8_t* a8,
                           const float* oval, const void* ubuf, float* out,
                           int32_t* acc, hipStream_t s) {
     // a8 holds round_up(m, 128) rows; wt / wkn are padded to (Np, Kp) / (Kp, Np)
-    const size_t tiles = (m + BM - 1) / BM;
+    const int MT = (int)((m + GBM - 1) / GBM), NT = (int)(w.np / GBN);
     const int t = (int)(w.k < FRQ_T ? w.k : FRQ_T);
-    dim3 grid((unsigned)(w.np / BN), (unsigned)tiles);
-    gemm_i8_kernel<<<grid, dim3(256), 0, s>>>(
+    gemm_i8_kernel<<<dim3((unsigned)(MT * NT)), dim3(256), 0, s>>>(
         a8, w.wt, w.wkn, w.scale, sa, (int)m, (int)w.n, (int)w.np, (int)w.kp, t,
-        union_view(const_cast<void*>(ubuf), m), oidx, oval, out, acc);
+        union_view(const_cast<void*>(ubuf), m), oidx, oval, out, acc, MT);
     return hipGetLastError();
 }
 

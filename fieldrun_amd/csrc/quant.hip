@@ -251,7 +251,216 @@ __global__ __launch_bounds__(BLOCK) void quant_rows(
     if (tid == 0) sa_out[row] = sa;
 }
 
+// ---------------------------------------------------------------------------
+// Fast path: K % 4 == 0, 32 < K <= BLOCK * NV4 * 4.  The row stays in
+// registers (float4 loads); the (t+1)-th largest is found from a handful of
+// candidates and the quotient a/sa uses r = RN(1/sa) plus one FMA residual
+// correction (Markstein: RN(q + (a - q*sa)*r) == RN(a/sa) for r = RN(1/sa)
+// away from under/overflow), which rows with extreme sa bypass.
+
+// Descending bitonic sort of one value per lane across the 64-lane wave.
+__device__ __forceinline__ uint32_t wave_sort_desc(uint32_t x) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int k = 2; k <= 64; k <<= 1)
+#pragma unroll
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            const uint32_t y = __shfl_xor(x, j, 64);
+            const bool lower = !(lane & j), desc = !(lane & k);
+            x = (lower == desc) ? max(x, y) : min(x, y);
+        }
+    return x;
+}
+
+// Ascending bitonic sort of one value per lane across the wave.
+__device__ __forceinline__ uint32_t wave_sort_asc(uint32_t x) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int k = 2; k <= 64; k <<= 1)
+#pragma unroll
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            const uint32_t y = __shfl_xor(x, j, 64);
+            const bool lower = !(lane & j), asc = !(lane & k);
+            x = (lower == asc) ? min(x, y) : max(x, y);
+        }
+    return x;
+}
+
+__device__ __forceinline__ int8_t q8(float a, float sa, float r, bool fast) {
+    float qt;
+    if (fast) {
+        const float q = a * r;
+        const float e = __builtin_fmaf(-q, sa, a);
+        qt = __builtin_fmaf(e, r, q);
+    } else {
+        qt = a / sa;
+    }
+    const float x = __builtin_roundf(qt);
+    return (x != x) ? (int8_t)0 : (int8_t)(x < -127.0f ? -127 : (x > 127.0f ? 127 : (int)x));
+}
+
+constexpr int FCAP = 2048;
+
+template <int BLOCK, int NV4>
+__global__ __launch_bounds__(BLOCK) void quant_rows_fast(
+    const float* __restrict__ A, int K, int Kp, int8_t* __restrict__ a8,
+    float* __restrict__ sa_out, uint32_t* __restrict__ oidx,
+    float* __restrict__ oval, int* __restrict__ err) {
+    constexpr int NW = BLOCK / 64;
+    __shared__ uint32_t wsel[NW], wtop[NW];
+    __shared__ uint32_t ncand;
+    __shared__ unsigned long long cand[FCAP];
+    __shared__ unsigned long long top[FRQ_T + 1];
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t bc[2];
+    __shared__ uint32_t scan_lds[NW + 1];
+    __shared__ uint32_t sel_i[FRQ_T];
+    extern __shared__ uint32_t bitmap[];  // ceil(Kp/32) words
+
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const float* a = A + (size_t)row * K;
+    int8_t* q = a8 + (size_t)row * Kp;
+    const int K4 = K >> 2;
+
+    float4 v[NV4];
+    uint32_t mx = 0;
+    int nan = 0;
+#pragma unroll
+    for (int i = 0; i < NV4; ++i) {
+        const int i4 = tid + BLOCK * i;
+        v[i] = i4 < K4 ? reinterpret_cast<const float4*>(a)[i4] : make_float4(0.f, 0.f, 0.f, 0.f);
+        const uint32_t b0 = absbits(v[i].x), b1 = absbits(v[i].y);
+        const uint32_t b2 = absbits(v[i].z), b3 = absbits(v[i].w);
+        nan |= (b0 > 0x7F800000u) | (b1 > 0x7F800000u) | (b2 > 0x7F800000u) | (b3 > 0x7F800000u);
+        mx = max(mx, max(max(b0, b1), max(b2, b3)));
+    }
+    for (int w = tid; w < (Kp + 31) / 32; w += BLOCK) bitmap[w] = 0u;
+    if (tid == 0) ncand = 0;
+    if (tid < FRQ_T) sel_i[tid] = 0u;
+    if (__syncthreads_or(nan)) {
+        if (tid == 0) { atomicOr(err, 1); sa_out[row] = 1.0f; }
+        for (int k = tid; k < Kp; k += BLOCK) q[k] = 0;
+        if (tid < FRQ_T) {
+            oidx[(size_t)row * FRQ_T + tid] = (uint32_t)tid;
+            oval[(size_t)row * FRQ_T + tid] = 0.0f;
+        }
+        return;
+    }
+    // threshold: the largest of the waves' 33rd-largest thread maxima; every
+    // element above the (t+1)-th largest of the row is >= it
+    const uint32_t srt = wave_sort_desc(mx);
+    const uint32_t w33 = __shfl(srt, FRQ_T, 64), wmx = __shfl(srt, 0, 64);
+    if (lane == 0) { wsel[wave] = w33; wtop[wave] = wmx; }
+    __syncthreads();
+    uint32_t tau = 0, rowmax = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) { tau = max(tau, wsel[w]); rowmax = max(rowmax, wtop[w]); }
+    // compact candidates: key = |a| bits << 32 | ~index (unique; larger key =
+    // larger |a|, ties to the lower index)
+#pragma unroll
+    for (int i = 0; i < NV4; ++i) {
+        const int base = 4 * (tid + BLOCK * i);
+        const float e4[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const uint32_t b = absbits(e4[c]);
+            if (base + c < K && b >= tau) {
+                const uint32_t slot = atomicAdd(&ncand, 1u);
+                if (slot < (uint32_t)FCAP)
+                    cand[slot] = ((unsigned long long)b << 32) | (0xFFFFFFFFu - (uint32_t)(base + c));
+            }
+        }
+    }
+    __syncthreads();
+    const uint32_t nc = ncand;
+    uint32_t bulk;
+    if (nc <= (uint32_t)FCAP) {
+        // exact rank of every candidate; the 33 largest keys land in top[]
+        for (uint32_t i = tid; i < nc; i += BLOCK) {
+            const unsigned long long key = cand[i];
+            uint32_t rank = 0;
+            for (uint32_t j = 0; j < nc; ++j) rank += cand[j] > key;
+            if (rank <= (uint32_t)FRQ_T) top[rank] = key;
+        }
+        __syncthreads();
+        bulk = (uint32_t)(top[FRQ_T] >> 32);
+        if (wave == 0) {
+            const uint32_t idx = lane < FRQ_T ? 0xFFFFFFFFu - (uint32_t)(top[lane] & 0xFFFFFFFFu) : 0xFFFFFFFFu;
+            const uint32_t si = wave_sort_asc(idx);
+            if (lane < FRQ_T) {
+                sel_i[lane] = si;
+                atomicOr(&bitmap[si >> 5], 1u << (si & 31));
+            }
+        }
+    } else {
+        // many near-equal magnitudes (e.g. constant rows): exact select over
+        // the row in global memory, outliers by ordered chunks
+        bulk = radix_select_desc<BLOCK>([&](int i) { return absbits(a[i]); }, K,
+                                        (uint32_t)FRQ_T, hist, bc);
+        const int C = (K + BLOCK - 1) / BLOCK;
+        const int lo = tid * C, hi = min(lo + C, K);
+        uint32_t gt = 0, ties = 0;
+        for (int k = lo; k < hi; ++k) {
+            const uint32_t b = absbits(a[k]);
+            gt += b > bulk;
+            ties += b == bulk;
+        }
+        uint32_t gt_total, ties_total, sel_total;
+        block_excl_scan<BLOCK>(gt, scan_lds, &gt_total);
+        const uint32_t tie_base = block_excl_scan<BLOCK>(ties, scan_lds, &ties_total);
+        const uint32_t need = gt_total < (uint32_t)FRQ_T ? (uint32_t)FRQ_T - gt_total : 0u;
+        const uint32_t take = need > tie_base ? min(need - tie_base, ties) : 0u;
+        uint32_t pos = block_excl_scan<BLOCK>(gt + take, scan_lds, &sel_total);
+        if (gt + take) {
+            uint32_t seen = 0;
+            for (int k = lo; k < hi; ++k) {
+                const uint32_t b = absbits(a[k]);
+                bool s = b > bulk;
+                if (b == bulk) { s = seen < take; seen++; }
+                if (s && pos < (uint32_t)FRQ_T) {
+                    sel_i[pos++] = (uint32_t)k;
+                    atomicOr(&bitmap[k >> 5], 1u << (k & 31));
+                }
+            }
+        }
+    }
+    __syncthreads();
+    const float bulkf = __uint_as_float(bulk);
+    const float sa = bulkf > 0.0f ? bulkf / 127.0f : 1.0f;
+    const float r = 1.0f / sa;
+    // Markstein correction needs no under/overflow in q*sa and the residual
+    const bool fast = sa >= 1e-30f && sa <= 1e30f && rowmax < 0x7A800000u;  // |a| < 2^118
+#pragma unroll
+    for (int i = 0; i < NV4; ++i) {
+        const int i4 = tid + BLOCK * i;
+        if (i4 < K4) {
+            const int base = 4 * i4;
+            const uint32_t bw = bitmap[base >> 5] >> (base & 31);
+            const uint32_t b0 = (bw & 1u) ? 0u : (uint8_t)q8(v[i].x, sa, r, fast);
+            const uint32_t b1 = (bw & 2u) ? 0u : (uint8_t)q8(v[i].y, sa, r, fast);
+            const uint32_t b2 = (bw & 4u) ? 0u : (uint8_t)q8(v[i].z, sa, r, fast);
+            const uint32_t b3 = (bw & 8u) ? 0u : (uint8_t)q8(v[i].w, sa, r, fast);
+            reinterpret_cast<uint32_t*>(q)[i4] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+        }
+    }
+    for (int i4 = K4 + tid; i4 < Kp / 4; i4 += BLOCK) reinterpret_cast<uint32_t*>(q)[i4] = 0u;
+    if (tid < FRQ_T) {
+        const uint32_t k = sel_i[tid];
+        oidx[(size_t)row * FRQ_T + tid] = k;
+        oval[(size_t)row * FRQ_T + tid] = a[k];
+    }
+    if (tid == 0) sa_out[row] = sa;
+}
+
 }  // namespace
+
+template <int NV4>
+static void launch_fast(const float* a, size_t m, size_t k, size_t kp, int8_t* a8, float* sa,
+                        uint32_t* oidx, float* oval, int* err, size_t lds, hipStream_t s) {
+    quant_rows_fast<256, NV4><<<dim3((unsigned)m), dim3(256), lds, s>>>(
+        a, (int)k, (int)kp, a8, sa, oidx, oval, err);
+}
 
 hipError_t launch_quant(const float* a, size_t m, size_t k, size_t kp,
                         int8_t* a8, float* sa, uint32_t* oidx, float* oval,
@@ -259,7 +468,17 @@ hipError_t launch_quant(const float* a, size_t m, size_t k, size_t kp,
     if (m == 0) return hipSuccess;
     const int t = (int)(k < FRQ_T ? k : FRQ_T);
     const size_t lds = (kp + 31) / 32 * sizeof(uint32_t);
-    if (lds > 96 * 1024) return hipErrorInvalidValue;
+    if (lds > 32 * 1024) return hipErrorInvalidValue;
+    if (k > FRQ_T && k % 4 == 0 && ((uintptr_t)a & 15) == 0 && k <= 256 * 20 * 4) {
+        const size_t nv4 = (k / 4 + 255) / 256;
+        if (nv4 <= 1) launch_fast<1>(a, m, k, kp, a8, sa, oidx, oval, err, lds, s);
+        else if (nv4 <= 2) launch_fast<2>(a, m, k, kp, a8, sa, oidx, oval, err, lds, s);
+        else if (nv4 <= 4) launch_fast<4>(a, m, k, kp, a8, sa, oidx, oval, err, lds, s);
+        else if (nv4 <= 8) launch_fast<8>(a, m, k, kp, a8, sa, oidx, oval, err, lds, s);
+        else if (nv4 <= 14) launch_fast<14>(a, m, k, kp, a8, sa, oidx, oval, err, lds, s);
+        else launch_fast<20>(a, m, k, kp, a8, sa, oidx, oval, err, lds, s);
+        return hipGetLastError();
+    }
     if (m < 64)
         quant_rows<1024><<<dim3((unsigned)m), dim3(1024), lds, s>>>(
             a, (int)k, (int)kp, t, a8, sa, oidx, oval, err);
