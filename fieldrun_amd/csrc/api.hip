@@ -28,6 +28,9 @@ struct frq_ctx {
     void* ws = nullptr;
     size_t ws_bytes = 0;
     int* err = nullptr;  // device word: kernels atomically OR 1 on NaN input
+    // arrival counters of split-K reductions (last workgroup folds); zeroed
+    // at init and left zero by every kernel that uses them
+    unsigned* tickets = nullptr;
 };
 
 namespace {
@@ -225,6 +228,8 @@ frq_ctx* frq_init(int device) {
     hipError_t e = hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipMalloc(&c->err, 256);
     if (e == hipSuccess) e = hipMemset(c->err, 0, 256);
+    if (e == hipSuccess) e = hipMalloc(&c->tickets, FRQ_TICKETS * sizeof(unsigned));
+    if (e == hipSuccess) e = hipMemset(c->tickets, 0, FRQ_TICKETS * sizeof(unsigned));
     if (e != hipSuccess) {
         hip_fail(e, "frq_init");
         if (c->own) (void)hipStreamDestroy(c->own);
@@ -241,6 +246,7 @@ void frq_free(frq_ctx* c) {
     (void)hipStreamSynchronize(c->stream);
     if (c->ws) (void)hipFree(c->ws);
     if (c->err) (void)hipFree(c->err);
+    if (c->tickets) (void)hipFree(c->tickets);
     if (c->own) (void)hipStreamDestroy(c->own);
     delete c;
 }
@@ -384,7 +390,7 @@ int frq_mm_dev(frq_ctx* c, const frq_w* wh, const float* d_a, size_t m, float* d
     }
     if (w.dtype == FRQ_DT_I4) {
         if (int rc = ws_reserve(c, i4_ws_floats(w, m) * sizeof(float) + 256)) return rc;
-        HIPCHK(launch_i4(w, m, d_a, d_out, (float*)c->ws, c->stream), "launch i4");
+        HIPCHK(launch_i4(w, m, d_a, d_out, (float*)c->ws, c->tickets, c->stream), "launch i4");
         return FRQ_OK;
     }
     return fail(FRQ_ERR_DTYPE, "unsupported weight dtype");
@@ -470,7 +476,7 @@ static int mm_host(frq_ctx* c, const frq_w* wh, const float* a, size_t m, float*
     if (i8) {
         if (int rc = run_i8(c, w, d_a, m, d_out, d_acc, scratch, &a8, &sa, &oi, &ov)) return rc;
     } else {
-        HIPCHK(launch_i4(w, m, d_a, d_out, (float*)scratch, c->stream), "launch i4");
+        HIPCHK(launch_i4(w, m, d_a, d_out, (float*)scratch, c->tickets, c->stream), "launch i4");
     }
     HIPCHK(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
     if (int rc = check_err_word(c)) return rc;

@@ -25,6 +25,7 @@
 #define FRQ_KALIGN 128      // Kp alignment (a multiple of the GEMM k-step)
 #define FRQ_NALIGN 256      // Np alignment (a multiple of every N tile)
 #define FRQ_MALIGN 128      // Mp alignment of the a8 workspace (GEMM M tile)
+#define FRQ_TICKETS (1 << 20)  // per-context split-K arrival counters
 
 namespace frq {
 
@@ -98,7 +99,7 @@ hipError_t launch_gemm_i8(const Weight& w, size_t m, const int8_t* a8,
                           int32_t* acc, hipStream_t s);
 // int4 linear (any m).
 hipError_t launch_i4(const Weight& w, size_t m, const float* a, float* out,
-                     float* wsf, hipStream_t s);
+                     float* wsf, unsigned* tickets, hipStream_t s);
 size_t i4_ws_floats(const Weight& w, size_t m);
 // int4 (N, K/2) -> 64-row blocked layout (g == 32, K % 32 == 0).
 hipError_t launch_i4_block(const uint8_t* raw, const uint16_t* sraw, size_t n,

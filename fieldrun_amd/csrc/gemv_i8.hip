@@ -151,6 +151,244 @@ hipError_t launch_m(const Weight& w, const int8_t* a8, const float* sa,
     return launch_t<M, 4, 256>(w, a8, sa, oidx, oval, out, acc, s);
 }
 
+// ---------------------------------------------------------------------------
+// GEMV v2: L lanes per weight row (8 when the row is at most 64 chunks of 16
+// bytes, else 64), each lane owning chunks sub, sub+L, ... (at most CPL).
+// The activations' chunks for those positions are loaded once into
+// registers; every row pass then issues all of a lane's weight loads at once.
+// The outlier correction reads W[j, ch] from the (K, Np) copy of the weight:
+// for a fixed outlier channel the workgroup's rows are consecutive bytes, so
+// those loads coalesce; they are issued before the weight stream and packed
+// four to a register.  Same operation order as the oracle (bit-exact).
+template <int M, int L, int CPL>
+__global__ __launch_bounds__(256) void gemv2_i8_kernel(
+    const int8_t* __restrict__ W, const int8_t* __restrict__ Wkn,
+    const float* __restrict__ scale, int N, int Np, int Kp, int t,
+    const int8_t* __restrict__ a8, const float* __restrict__ sa,
+    const uint32_t* __restrict__ oidx, const float* __restrict__ oval,
+    float* __restrict__ out, int32_t* __restrict__ acc_dbg, int passes) {
+    constexpr int RPP = 256 / L;  // rows per pass
+    __shared__ int accs[M][256];
+    const int tid = threadIdx.x;
+    const int sub = tid % L, rloc = tid / L;
+    const int nch = Kp >> 4;
+    const int RPW = RPP * passes;
+    const int j0 = blockIdx.x * RPW;
+
+    // outlier bytes of this thread's epilogue row(s), 4 per register
+    uint32_t wc[M][FRQ_T / 4];
+    if (tid < RPW) {
+        const int j = j0 + tid;  // < Np
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+            for (int q4 = 0; q4 < FRQ_T / 4; ++q4) {
+                uint32_t v = 0;
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    const int q = q4 * 4 + b;
+                    if (q < t) {
+                        const uint32_t ch = min(oidx[(size_t)m * FRQ_T + q], (uint32_t)(Kp - 1));
+                        v |= (uint32_t)(uint8_t)Wkn[(size_t)ch * Np + j] << (8 * b);
+                    }
+                }
+                wc[m][q4] = v;
+            }
+    }
+    int4 x[M][CPL];
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            const int c = sub + L * i;
+            x[m][i] = c < nch ? *reinterpret_cast<const int4*>(a8 + (size_t)m * Kp + 16 * c)
+                              : make_int4(0, 0, 0, 0);
+        }
+    for (int ps = 0; ps < passes; ++ps) {
+        const int row = j0 + ps * RPP + rloc;
+        const int8_t* wr = W + (size_t)row * Kp;
+        int4 w[CPL];
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            const int c = sub + L * i;
+            w[i] = c < nch ? ntload16(wr + 16 * c) : make_int4(0, 0, 0, 0);
+        }
+        int acc[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            acc[m] = 0;
+#pragma unroll
+            for (int i = 0; i < CPL; ++i) acc[m] = dot16(x[m][i], w[i], acc[m]);
+#pragma unroll
+            for (int off = L / 2; off >= 1; off >>= 1) acc[m] += __shfl_xor(acc[m], off, 64);
+        }
+        if (sub == 0) {
+#pragma unroll
+            for (int m = 0; m < M; ++m) accs[m][ps * RPP + rloc] = acc[m];
+        }
+    }
+    __syncthreads();
+    if (tid < RPW) {
+        const int j = j0 + tid;
+        if (j < N) {
+            const float sc = scale[j];
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const int total = accs[m][tid];
+                float corr = -0.0f;
+#pragma unroll
+                for (int q = 0; q < FRQ_T; ++q)
+                    if (q < t)
+                        corr = corr + oval[(size_t)m * FRQ_T + q] *
+                                          (float)(int8_t)(wc[m][q >> 2] >> (8 * (q & 3)));
+                out[(size_t)m * N + j] = sc * (sa[m] * (float)total + corr);
+                if (acc_dbg) acc_dbg[(size_t)m * N + j] = total;
+            }
+        }
+    }
+}
+
+template <int M, int L, int CPL>
+hipError_t launch_v2(const Weight& w, const int8_t* a8, const float* sa,
+                     const uint32_t* oidx, const float* oval, float* out,
+                     int32_t* acc, hipStream_t s) {
+    constexpr int RPP = 256 / L;
+    int passes = 1;
+    while (passes * 2 * RPP <= 256 && (size_t)RPP * passes * 2 * 2048 <= w.n) passes *= 2;
+    const int RPW = RPP * passes;
+    const unsigned grid = (unsigned)((w.n + RPW - 1) / RPW);
+    const int t = (int)(w.k < FRQ_T ? w.k : FRQ_T);
+    gemv2_i8_kernel<M, L, CPL><<<dim3(grid), dim3(256), 0, s>>>(
+        w.wt, w.wkn, w.scale, (int)w.n, (int)w.np, (int)w.kp, t, a8, sa, oidx, oval, out, acc,
+        passes);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// GEMV v3 (M == 1): persistent grid-stride over groups of RPP = 256/L rows,
+// the next group's weight chunks (and its outlier bytes) in flight while the
+// current group is reduced.  Outlier correction: lane (q, r4) reads the four
+// bytes W[row0+4r4 .. +3, ch_q] as one word of the (K, Np) copy, forms the
+// products av_q * w in LDS, and one thread per row adds its t products in
+// channel order (-0.0 start) — the oracle's order, so outputs stay bit-exact.
+template <int L, int CPL, bool DB>
+__global__ __launch_bounds__(256) void gemv3_i8_kernel(
+    const int8_t* __restrict__ W, const int8_t* __restrict__ Wkn,
+    const float* __restrict__ scale, int N, int Np, int Kp, int t,
+    const int8_t* __restrict__ a8, const float* __restrict__ sa,
+    const uint32_t* __restrict__ oidx, const float* __restrict__ oval,
+    float* __restrict__ out, int32_t* __restrict__ acc_dbg, int n_rg) {
+    constexpr int RPP = 256 / L;
+    constexpr int NQW = FRQ_T * (RPP / 4);  // outlier words per group
+    __shared__ int accs[2][RPP];
+    __shared__ float prod[2][RPP][FRQ_T + 1];
+    const int tid = threadIdx.x;
+    const int sub = tid % L, rloc = tid / L;
+    const int nch = Kp >> 4;
+    const float sam = sa[0];
+    int4 x[CPL];
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+        const int c = sub + L * i;
+        x[i] = c < nch ? *reinterpret_cast<const int4*>(a8 + 16 * c) : make_int4(0, 0, 0, 0);
+    }
+    // outlier word this thread fetches each group: channel q, rows 4*r4..
+    const int q = tid % FRQ_T, r4 = tid / FRQ_T;
+    const bool qw = tid < NQW && q < t;
+    const uint32_t chq = qw ? min(oidx[q], (uint32_t)(Kp - 1)) : 0u;
+    const float ovq = qw ? oval[q] : 0.0f;
+
+    int rg = blockIdx.x;
+    int4 w[CPL], wn[DB ? CPL : 1];
+    uint32_t ow = 0, own = 0;
+    auto load_group = [&](int g, int4* dst, uint32_t& o) {
+        const int8_t* wr = W + (size_t)(g * RPP + rloc) * Kp;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            const int c = sub + L * i;
+            dst[i] = c < nch ? *reinterpret_cast<const int4*>(wr + 16 * c) : make_int4(0, 0, 0, 0);
+        }
+        if (qw) o = *reinterpret_cast<const uint32_t*>(Wkn + (size_t)chq * Np + g * RPP + 4 * r4);
+    };
+    if (rg < n_rg) load_group(rg, w, ow);
+    int buf = 0;
+    while (rg < n_rg) {
+        const int rgn = rg + gridDim.x;
+        if (DB && rgn < n_rg) load_group(rgn, wn, own);
+        int acc = 0;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) acc = dot16(x[i], w[i], acc);
+#pragma unroll
+        for (int off = L / 2; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+        if (sub == 0) accs[buf][rloc] = acc;
+        if (qw) {
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                prod[buf][4 * r4 + b][q] = ovq * (float)(int8_t)(ow >> (8 * b));
+        }
+        __syncthreads();
+        if (tid < RPP) {
+            const int j = rg * RPP + tid;
+            if (j < N) {
+                float corr = -0.0f;
+                for (int qq = 0; qq < t; ++qq) corr = corr + prod[buf][tid][qq];
+                const int total = accs[buf][tid];
+                out[j] = scale[j] * (sam * (float)total + corr);
+                if (acc_dbg) acc_dbg[j] = total;
+            }
+        }
+        buf ^= 1;
+        if (DB) {
+#pragma unroll
+            for (int i = 0; i < CPL; ++i) w[i] = wn[i];
+            ow = own;
+        } else if (rgn < n_rg) {
+            load_group(rgn, w, ow);
+        }
+        rg = rgn;
+    }
+}
+
+template <int L, int CPL, bool DB>
+hipError_t launch_v3(const Weight& w, const int8_t* a8, const float* sa,
+                     const uint32_t* oidx, const float* oval, float* out,
+                     int32_t* acc, hipStream_t s) {
+    constexpr int RPP = 256 / L;
+    const int n_rg = (int)((w.n + RPP - 1) / RPP);  // rows < Np (RPP divides 256)
+    const int grid = n_rg < 2048 ? n_rg : 2048;
+    const int t = (int)(w.k < FRQ_T ? w.k : FRQ_T);
+    gemv3_i8_kernel<L, CPL, DB><<<dim3((unsigned)grid), dim3(256), 0, s>>>(
+        w.wt, w.wkn, w.scale, (int)w.n, (int)w.np, (int)w.kp, t, a8, sa, oidx, oval, out, acc, n_rg);
+    return hipGetLastError();
+}
+
+hipError_t launch_v3_m1(const Weight& w, const int8_t* a8, const float* sa,
+                        const uint32_t* oidx, const float* oval, float* out,
+                        int32_t* acc, hipStream_t s) {
+    const size_t nch = w.kp / 16;
+    if (nch <= 64) return launch_v3<8, 8, true>(w, a8, sa, oidx, oval, out, acc, s);
+    if (nch <= 128) return launch_v3<64, 2, true>(w, a8, sa, oidx, oval, out, acc, s);
+    if (nch <= 256) return launch_v3<64, 4, true>(w, a8, sa, oidx, oval, out, acc, s);
+    if (nch <= 512) return launch_v3<64, 8, true>(w, a8, sa, oidx, oval, out, acc, s);
+    if (nch <= 1024) return launch_v3<64, 16, false>(w, a8, sa, oidx, oval, out, acc, s);
+    if (nch <= 1280) return launch_v3<64, 20, false>(w, a8, sa, oidx, oval, out, acc, s);
+    return launch_m<1>(w, a8, sa, oidx, oval, out, acc, s);
+}
+
+template <int M>
+hipError_t launch_v2_m(const Weight& w, const int8_t* a8, const float* sa,
+                       const uint32_t* oidx, const float* oval, float* out,
+                       int32_t* acc, hipStream_t s) {
+    const size_t nch = w.kp / 16;
+    if (nch <= 64) return launch_v2<M, 8, 8>(w, a8, sa, oidx, oval, out, acc, s);
+    if (nch <= 128) return launch_v2<M, 64, 2>(w, a8, sa, oidx, oval, out, acc, s);
+    if (nch <= 256) return launch_v2<M, 64, 4>(w, a8, sa, oidx, oval, out, acc, s);
+    if (nch <= 512) return launch_v2<M, 64, 8>(w, a8, sa, oidx, oval, out, acc, s);
+    if (M <= 2 && nch <= 1024) return launch_v2<M, 64, 16>(w, a8, sa, oidx, oval, out, acc, s);
+    if (M == 1 && nch <= 1280) return launch_v2<M, 64, 20>(w, a8, sa, oidx, oval, out, acc, s);
+    return launch_m<M>(w, a8, sa, oidx, oval, out, acc, s);
+}
+
 }  // namespace
 
 hipError_t launch_gemv_i8(const Weight& w, size_t m, const int8_t* a8,
@@ -160,10 +398,10 @@ hipError_t launch_gemv_i8(const Weight& w, size_t m, const int8_t* a8,
     // rows j >= N read zero padding of the (Np, Kp) weight and are not stored
     if ((size_t)m * w.kp > 64 * 1024) return hipErrorInvalidValue;
     switch (m) {
-        case 1: return launch_m<1>(w, a8, sa, oidx, oval, out, acc, s);
-        case 2: return launch_m<2>(w, a8, sa, oidx, oval, out, acc, s);
-        case 3: return launch_m<3>(w, a8, sa, oidx, oval, out, acc, s);
-        case 4: return launch_m<4>(w, a8, sa, oidx, oval, out, acc, s);
+        case 1: return launch_v3_m1(w, a8, sa, oidx, oval, out, acc, s);
+        case 2: return launch_v2_m<2>(w, a8, sa, oidx, oval, out, acc, s);
+        case 3: return launch_v2_m<3>(w, a8, sa, oidx, oval, out, acc, s);
+        case 4: return launch_v2_m<4>(w, a8, sa, oidx, oval, out, acc, s);
         default: return hipErrorInvalidValue;
     }
 }

@@ -43,26 +43,34 @@ __device__ __forceinline__ float group_avx2(const uint4 w, const float* __restri
     return (q0 + q2) + (q1 + q3);
 }
 
+// One workgroup = one 64-row block x one segment of its groups.  Wave w of
+// the workgroup takes the segment's groups w, w+4, ...; lane = row.  The
+// four wave sums are added in wave order; with S > 1 segments the partials
+// go to the workspace and i4_fold adds them in segment order.
 __global__ __launch_bounds__(256) void i4_gemv_blocked(
     const uint8_t* __restrict__ blk, const uint16_t* __restrict__ sblk,
-    const float* __restrict__ a, int N, int ng, int S, int nblk,
-    float* __restrict__ part) {
-    const int wave_id = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (wave_id >= nblk * S) return;
-    const int b = wave_id / S, seg = wave_id % S;
+    const float* __restrict__ a, int N, int ng, int S,
+    float* __restrict__ part, float* __restrict__ out) {
+    __shared__ float wsum[4][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int b = blockIdx.x / S, seg = blockIdx.x % S;
     const int g0 = (int)((long)ng * seg / S), g1 = (int)((long)ng * (seg + 1) / S);
     const uint4* wp = reinterpret_cast<const uint4*>(blk) + ((size_t)b * ng) * 64 + lane;
     const uint16_t* sp = sblk + ((size_t)b * ng) * 64 + lane;
     float sum = 0.0f;
-    for (int gi = g0; gi < g1; ++gi) {
+    for (int gi = g0 + wave; gi < g1; gi += 4) {
         const uint4 w = ntload16u(wp + (size_t)gi * 64);
         const float sc = h2f(sp[(size_t)gi * 64]);
-        const float gs = group_avx2(w, a + 32 * gi);
-        sum = sum + sc * gs;
+        sum = sum + sc * group_avx2(w, a + 32 * gi);
     }
-    const int row = b * 64 + lane;
-    if (row < N) part[(size_t)seg * N + row] = sum;
+    wsum[wave][lane] = sum;
+    __syncthreads();
+    const int row = b * 64 + threadIdx.x;
+    if (threadIdx.x < 64 && row < N) {
+        const float p = ((wsum[0][lane] + wsum[1][lane]) + wsum[2][lane]) + wsum[3][lane];
+        if (S == 1) out[row] = p;
+        else part[(size_t)seg * N + row] = p;
+    }
 }
 
 __global__ void i4_fold(const float* __restrict__ part, int N, int S,
@@ -164,8 +172,9 @@ __global__ void i4_block_kernel(const uint8_t* __restrict__ raw,
 
 int pick_segments(size_t n, size_t ng) {
     const size_t nblk = (n + 63) / 64;
-    size_t s = (4096 + nblk - 1) / nblk;  // aim for >= 4096 waves
-    if (s > ng) s = ng;
+    size_t s = (512 + nblk - 1) / nblk;  // aim for >= 512 workgroups (2048 waves)
+    if (s > 8) s = 8;                    // the fold reads S partials per row
+    if (s > ng / 4) s = ng / 4;          // >= 4 groups (one per wave) per segment
     if (s < 1) s = 1;
     return (int)s;
 }
@@ -185,16 +194,16 @@ hipError_t launch_i4_block(const uint8_t* raw, const uint16_t* sraw, size_t n,
 }
 
 hipError_t launch_i4(const Weight& w, size_t m, const float* a, float* out,
-                     float* wsf, hipStream_t s) {
+                     float* wsf, unsigned* tickets, hipStream_t s) {
+    (void)tickets;
     if (m == 0) return hipSuccess;
     if (m == 1 && w.i4_blocked) {
         const int ng = (int)(w.k / 32), nblk = (int)((w.n + 63) / 64);
         const int S = pick_segments(w.n, (size_t)ng);
-        const unsigned waves = (unsigned)(nblk * S);
-        i4_gemv_blocked<<<dim3((waves + 3) / 4), dim3(256), 0, s>>>(
-            w.q4, w.s4, a, (int)w.n, ng, S, nblk, wsf);
+        i4_gemv_blocked<<<dim3((unsigned)(nblk * S)), dim3(256), 0, s>>>(
+            w.q4, w.s4, a, (int)w.n, ng, S, wsf, out);
         hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
+        if (e != hipSuccess || S == 1) return e;
         i4_fold<<<dim3((unsigned)((w.n + 255) / 256)), dim3(256), 0, s>>>(wsf, (int)w.n, S, out);
         return hipGetLastError();
     }

@@ -286,6 +286,33 @@ __device__ __forceinline__ uint32_t wave_sort_asc(uint32_t x) {
     return x;
 }
 
+// Top 64 of two descending 64-lists, a in lane order and b reversed
+// (lane l holds b[63-l]): max() forms a bitonic sequence, the half-cleaners
+// sort it descending.
+__device__ __forceinline__ uint32_t merge_top64(uint32_t a, uint32_t b_rev) {
+    const int lane = threadIdx.x & 63;
+    uint32_t c = max(a, b_rev);
+#pragma unroll
+    for (int j = 32; j > 0; j >>= 1) {
+        const uint32_t y = __shfl_xor(c, j, 64);
+        c = !(lane & j) ? max(c, y) : min(c, y);
+    }
+    return c;
+}
+
+__device__ __forceinline__ unsigned long long wave_sort_desc64(unsigned long long x) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int k = 2; k <= 64; k <<= 1)
+#pragma unroll
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            const unsigned long long y = __shfl_xor(x, j, 64);
+            const bool lower = !(lane & j), desc = !(lane & k);
+            x = (lower == desc) ? (x > y ? x : y) : (x < y ? x : y);
+        }
+    return x;
+}
+
 __device__ __forceinline__ int8_t q8(float a, float sa, float r, bool fast) {
     float qt;
     if (fast) {
@@ -307,7 +334,8 @@ __global__ __launch_bounds__(BLOCK) void quant_rows_fast(
     float* __restrict__ sa_out, uint32_t* __restrict__ oidx,
     float* __restrict__ oval, int* __restrict__ err) {
     constexpr int NW = BLOCK / 64;
-    __shared__ uint32_t wsel[NW], wtop[NW];
+    __shared__ uint32_t wsorted[NW][64];
+    __shared__ uint32_t tau_s[2];
     __shared__ uint32_t ncand;
     __shared__ unsigned long long cand[FCAP];
     __shared__ unsigned long long top[FRQ_T + 1];
@@ -347,15 +375,22 @@ __global__ __launch_bounds__(BLOCK) void quant_rows_fast(
         }
         return;
     }
-    // threshold: the largest of the waves' 33rd-largest thread maxima; every
-    // element above the (t+1)-th largest of the row is >= it
-    const uint32_t srt = wave_sort_desc(mx);
-    const uint32_t w33 = __shfl(srt, FRQ_T, 64), wmx = __shfl(srt, 0, 64);
-    if (lane == 0) { wsel[wave] = w33; wtop[wave] = wmx; }
+    // threshold tau = the 33rd largest thread maximum (per-wave bitonic sorts,
+    // merged in wave 0): at least 33 elements are >= tau, so every element
+    // above the (t+1)-th largest |a| is >= tau, and for iid rows only a few
+    // dozen elements pass
+    static_assert(NW == 4, "the threshold merge assumes 4 waves");
+    wsorted[wave][lane] = wave_sort_desc(mx);
     __syncthreads();
-    uint32_t tau = 0, rowmax = 0;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) { tau = max(tau, wsel[w]); rowmax = max(rowmax, wtop[w]); }
+    if (wave == 0) {
+        const uint32_t x = merge_top64(wsorted[0][lane], wsorted[1][63 - lane]);
+        const uint32_t y = merge_top64(wsorted[2][lane], wsorted[3][63 - lane]);
+        const uint32_t z = merge_top64(x, __shfl(y, 63 - lane, 64));
+        if (lane == FRQ_T) tau_s[0] = z;
+        if (lane == 0) tau_s[1] = z;
+    }
+    __syncthreads();
+    const uint32_t tau = tau_s[0], rowmax = tau_s[1];
     // compact candidates: key = |a| bits << 32 | ~index (unique; larger key =
     // larger |a|, ties to the lower index)
 #pragma unroll
@@ -375,15 +410,30 @@ __global__ __launch_bounds__(BLOCK) void quant_rows_fast(
     __syncthreads();
     const uint32_t nc = ncand;
     uint32_t bulk;
-    if (nc <= (uint32_t)FCAP) {
+    if (nc <= 64) {
+        // one wave sorts the candidates' keys; lanes 0..31 are the outliers,
+        // lane 32 holds the (t+1)-th largest
+        if (wave == 0) {
+            const unsigned long long key = wave_sort_desc64(lane < (int)nc ? cand[lane] : 0ull);
+            if (lane <= FRQ_T) top[lane] = key;
+        }
+        __syncthreads();
+    } else if (nc <= (uint32_t)FCAP) {
         // exact rank of every candidate; the 33 largest keys land in top[]
         for (uint32_t i = tid; i < nc; i += BLOCK) {
             const unsigned long long key = cand[i];
             uint32_t rank = 0;
-            for (uint32_t j = 0; j < nc; ++j) rank += cand[j] > key;
+            uint32_t j = 0;
+            for (; j + 4 <= nc; j += 4) {
+                const unsigned long long c0 = cand[j], c1 = cand[j + 1], c2 = cand[j + 2], c3 = cand[j + 3];
+                rank += (c0 > key) + (c1 > key) + (c2 > key) + (c3 > key);
+            }
+            for (; j < nc; ++j) rank += cand[j] > key;
             if (rank <= (uint32_t)FRQ_T) top[rank] = key;
         }
         __syncthreads();
+    }
+    if (nc <= (uint32_t)FCAP) {
         bulk = (uint32_t)(top[FRQ_T] >> 32);
         if (wave == 0) {
             const uint32_t idx = lane < FRQ_T ? 0xFFFFFFFFu - (uint32_t)(top[lane] & 0xFFFFFFFFu) : 0xFFFFFFFFu;
