@@ -44,6 +44,37 @@ __device__ __forceinline__ uint4 ntload16u(const void* p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// Lane exchange v[lane ^ J] in VALU instructions only (no LDS crossbar):
+// J = 1, 2 via DPP quad_perm; J = 4, 8 via DPP row_shl / row_shr (lane i
+// reads i+J / i-J within a 16-lane row) selected by lane bit; J = 16, 32 via
+// gfx950 v_permlane16_swap / v_permlane32_swap.
+template <int J>
+__device__ __forceinline__ uint32_t xshfl(uint32_t v) {
+    const int lane = threadIdx.x & 63;
+    if constexpr (J == 1) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);
+    } else if constexpr (J == 2) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);
+    } else if constexpr (J == 4 || J == 8) {
+        const uint32_t up = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x100 + J, 0xF, 0xF, false);
+        const uint32_t dn = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x110 + J, 0xF, 0xF, false);
+        return (lane & J) ? dn : up;
+    } else if constexpr (J == 16) {
+        const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (lane & 16) ? p[0] : p[1];
+    } else {
+        static_assert(J == 32, "xor distance");
+        const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return (lane & 32) ? p[0] : p[1];
+    }
+}
+
+template <int J>
+__device__ __forceinline__ unsigned long long xshfl64(unsigned long long v) {
+    const uint32_t lo = xshfl<J>((uint32_t)v), hi = xshfl<J>((uint32_t)(v >> 32));
+    return ((unsigned long long)hi << 32) | lo;
+}
+
 // IEEE binary16 -> binary32 (exact).
 __device__ __forceinline__ float h2f(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);

@@ -258,72 +258,76 @@ __global__ __launch_bounds__(BLOCK) void quant_rows(
 // correction (Markstein: RN(q + (a - q*sa)*r) == RN(a/sa) for r = RN(1/sa)
 // away from under/overflow), which rows with extreme sa bypass.
 
-// Descending bitonic sort of one value per lane across the 64-lane wave.
-__device__ __forceinline__ uint32_t wave_sort_desc(uint32_t x) {
+// Bitonic networks across the 64-lane wave on VALU lane exchanges.
+template <int J, int K, bool DESC, typename T, typename X>
+__device__ __forceinline__ T bstage(T x, X xs) {
     const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int k = 2; k <= 64; k <<= 1)
-#pragma unroll
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            const uint32_t y = __shfl_xor(x, j, 64);
-            const bool lower = !(lane & j), desc = !(lane & k);
-            x = (lower == desc) ? max(x, y) : min(x, y);
-        }
+    const T y = xs(x);
+    const bool lower = !(lane & J), dir = !(lane & K);
+    const bool keep_big = DESC ? (lower == dir) : (lower != dir);
+    return keep_big ? (x > y ? x : y) : (x < y ? x : y);
+}
+
+template <bool DESC, typename T, typename X1, typename X2, typename X4, typename X8, typename X16,
+          typename X32>
+__device__ __forceinline__ T bitonic64(T x, X1 s1, X2 s2, X4 s4, X8 s8, X16 s16, X32 s32) {
+    x = bstage<1, 2, DESC>(x, s1);
+    x = bstage<2, 4, DESC>(x, s2); x = bstage<1, 4, DESC>(x, s1);
+    x = bstage<4, 8, DESC>(x, s4); x = bstage<2, 8, DESC>(x, s2); x = bstage<1, 8, DESC>(x, s1);
+    x = bstage<8, 16, DESC>(x, s8); x = bstage<4, 16, DESC>(x, s4); x = bstage<2, 16, DESC>(x, s2);
+    x = bstage<1, 16, DESC>(x, s1);
+    x = bstage<16, 32, DESC>(x, s16); x = bstage<8, 32, DESC>(x, s8); x = bstage<4, 32, DESC>(x, s4);
+    x = bstage<2, 32, DESC>(x, s2); x = bstage<1, 32, DESC>(x, s1);
+    x = bstage<32, 64, DESC>(x, s32); x = bstage<16, 64, DESC>(x, s16); x = bstage<8, 64, DESC>(x, s8);
+    x = bstage<4, 64, DESC>(x, s4); x = bstage<2, 64, DESC>(x, s2); x = bstage<1, 64, DESC>(x, s1);
     return x;
 }
 
-// Ascending bitonic sort of one value per lane across the wave.
+__device__ __forceinline__ uint32_t wave_sort_desc(uint32_t x) {
+    return bitonic64<true>(x, xshfl<1>, xshfl<2>, xshfl<4>, xshfl<8>, xshfl<16>, xshfl<32>);
+}
 __device__ __forceinline__ uint32_t wave_sort_asc(uint32_t x) {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int k = 2; k <= 64; k <<= 1)
-#pragma unroll
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            const uint32_t y = __shfl_xor(x, j, 64);
-            const bool lower = !(lane & j), asc = !(lane & k);
-            x = (lower == asc) ? min(x, y) : max(x, y);
-        }
-    return x;
+    return bitonic64<false>(x, xshfl<1>, xshfl<2>, xshfl<4>, xshfl<8>, xshfl<16>, xshfl<32>);
+}
+__device__ __forceinline__ unsigned long long wave_sort_desc64(unsigned long long x) {
+    return bitonic64<true>(x, xshfl64<1>, xshfl64<2>, xshfl64<4>, xshfl64<8>, xshfl64<16>,
+                           xshfl64<32>);
 }
 
 // Top 64 of two descending 64-lists, a in lane order and b reversed
 // (lane l holds b[63-l]): max() forms a bitonic sequence, the half-cleaners
 // sort it descending.
 __device__ __forceinline__ uint32_t merge_top64(uint32_t a, uint32_t b_rev) {
-    const int lane = threadIdx.x & 63;
     uint32_t c = max(a, b_rev);
-#pragma unroll
-    for (int j = 32; j > 0; j >>= 1) {
-        const uint32_t y = __shfl_xor(c, j, 64);
-        c = !(lane & j) ? max(c, y) : min(c, y);
-    }
+    c = bstage<32, 64, true>(c, xshfl<32>);
+    c = bstage<16, 64, true>(c, xshfl<16>);
+    c = bstage<8, 64, true>(c, xshfl<8>);
+    c = bstage<4, 64, true>(c, xshfl<4>);
+    c = bstage<2, 64, true>(c, xshfl<2>);
+    c = bstage<1, 64, true>(c, xshfl<1>);
     return c;
 }
 
-__device__ __forceinline__ unsigned long long wave_sort_desc64(unsigned long long x) {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int k = 2; k <= 64; k <<= 1)
-#pragma unroll
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            const unsigned long long y = __shfl_xor(x, j, 64);
-            const bool lower = !(lane & j), desc = !(lane & k);
-            x = (lower == desc) ? (x > y ? x : y) : (x < y ? x : y);
-        }
-    return x;
+// round(q) half away from zero (Rust f32::round), clamped to [-127, 127];
+// q finite.  trunc + exact fraction: |q - trunc(q)| is exact in f32.
+__device__ __forceinline__ uint32_t rq8(float q) {
+    const float t = __builtin_truncf(q);
+    const float r = __builtin_fabsf(q - t) >= 0.5f ? t + __builtin_copysignf(1.0f, q) : t;
+    return (uint32_t)(uint8_t)(int8_t)(int)__builtin_amdgcn_fmed3f(r, -127.0f, 127.0f);
 }
 
-__device__ __forceinline__ int8_t q8(float a, float sa, float r, bool fast) {
-    float qt;
-    if (fast) {
-        const float q = a * r;
-        const float e = __builtin_fmaf(-q, sa, a);
-        qt = __builtin_fmaf(e, r, q);
-    } else {
-        qt = a / sa;
-    }
-    const float x = __builtin_roundf(qt);
-    return (x != x) ? (int8_t)0 : (int8_t)(x < -127.0f ? -127 : (x > 127.0f ? 127 : (int)x));
+// RN(a / sa) by r = RN(1/sa) and one FMA residual correction (Markstein).
+__device__ __forceinline__ float qdiv_fast(float a, float sa, float r) {
+    const float q = a * r;
+    const float e = __builtin_fmaf(-q, sa, a);
+    return __builtin_fmaf(e, r, q);
+}
+
+// Exact path for rows outside the fast path's range (IEEE divide; Rust `as
+// i32` saturation maps NaN to 0).
+__device__ __forceinline__ uint32_t q8_slow(float a, float sa) {
+    const float x = __builtin_roundf(a / sa);
+    return (x != x) ? 0u : (uint32_t)(uint8_t)(int8_t)(x < -127.0f ? -127 : (x > 127.0f ? 127 : (int)x));
 }
 
 constexpr int FCAP = 2048;
@@ -336,7 +340,7 @@ __global__ __launch_bounds__(BLOCK) void quant_rows_fast(
     constexpr int NW = BLOCK / 64;
     __shared__ uint32_t wsorted[NW][64];
     __shared__ uint32_t tau_s[2];
-    __shared__ uint32_t ncand;
+    __shared__ uint32_t wcnt_s[NW];
     __shared__ unsigned long long cand[FCAP];
     __shared__ unsigned long long top[FRQ_T + 1];
     __shared__ uint32_t hist[256];
@@ -352,19 +356,19 @@ __global__ __launch_bounds__(BLOCK) void quant_rows_fast(
     const int K4 = K >> 2;
 
     float4 v[NV4];
-    uint32_t mx = 0;
-    int nan = 0;
+#pragma unroll
+    for (int i = 0; i < NV4; ++i) {  // unconditional loads (clamped), then mask
+        const int i4 = tid + BLOCK * i;
+        v[i] = reinterpret_cast<const float4*>(a)[min(i4, K4 - 1)];
+    }
+    uint32_t mx = 0;  // max |a| bits; NaN shows as > 0x7F800000
 #pragma unroll
     for (int i = 0; i < NV4; ++i) {
-        const int i4 = tid + BLOCK * i;
-        v[i] = i4 < K4 ? reinterpret_cast<const float4*>(a)[i4] : make_float4(0.f, 0.f, 0.f, 0.f);
-        const uint32_t b0 = absbits(v[i].x), b1 = absbits(v[i].y);
-        const uint32_t b2 = absbits(v[i].z), b3 = absbits(v[i].w);
-        nan |= (b0 > 0x7F800000u) | (b1 > 0x7F800000u) | (b2 > 0x7F800000u) | (b3 > 0x7F800000u);
-        mx = max(mx, max(max(b0, b1), max(b2, b3)));
+        if (tid + BLOCK * i >= K4) v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        mx = max(mx, max(max(absbits(v[i].x), absbits(v[i].y)), max(absbits(v[i].z), absbits(v[i].w))));
     }
+    const int nan = mx > 0x7F800000u;
     for (int w = tid; w < (Kp + 31) / 32; w += BLOCK) bitmap[w] = 0u;
-    if (tid == 0) ncand = 0;
     if (tid < FRQ_T) sel_i[tid] = 0u;
     if (__syncthreads_or(nan)) {
         if (tid == 0) { atomicOr(err, 1); sa_out[row] = 1.0f; }
@@ -393,42 +397,66 @@ __global__ __launch_bounds__(BLOCK) void quant_rows_fast(
     const uint32_t tau = tau_s[0], rowmax = tau_s[1];
     // compact candidates: key = |a| bits << 32 | ~index (unique; larger key =
     // larger |a|, ties to the lower index)
+    // per-wave regions of cand[] (FCAP/4 keys each), offsets from ballots
+    constexpr int WCAP = FCAP / NW;
+    uint32_t wcount = 0;
 #pragma unroll
     for (int i = 0; i < NV4; ++i) {
-        const int base = 4 * (tid + BLOCK * i);
-        const float e4[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+        const uint32_t b0 = absbits(v[i].x), b1 = absbits(v[i].y);
+        const uint32_t b2 = absbits(v[i].z), b3 = absbits(v[i].w);
+        const bool any = max(max(b0, b1), max(b2, b3)) >= tau;
+        if (__builtin_amdgcn_ballot_w64(any)) {  // rare: wave-uniform skip
+            const uint32_t base = 4u * (uint32_t)(tid + BLOCK * i);
+            const uint32_t bb[4] = {b0, b1, b2, b3};
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const uint32_t b = absbits(e4[c]);
-            if (base + c < K && b >= tau) {
-                const uint32_t slot = atomicAdd(&ncand, 1u);
-                if (slot < (uint32_t)FCAP)
-                    cand[slot] = ((unsigned long long)b << 32) | (0xFFFFFFFFu - (uint32_t)(base + c));
+            for (int c = 0; c < 4; ++c) {
+                const bool hit = bb[c] >= tau && base + c < (uint32_t)K;
+                const unsigned long long m = __builtin_amdgcn_ballot_w64(hit);
+                const uint32_t below = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+                const uint32_t slot = wcount + below;
+                if (hit && slot < (uint32_t)WCAP)
+                    cand[wave * WCAP + slot] = ((unsigned long long)bb[c] << 32) | (0xFFFFFFFFu - (base + c));
+                wcount += (uint32_t)__builtin_popcountll(m);
             }
         }
     }
+    if (lane == 0) wcnt_s[wave] = wcount;
     __syncthreads();
-    const uint32_t nc = ncand;
+    // concatenate the four regions (keys are independent of order)
+    uint32_t wc[NW], woff[NW + 1];
+    bool overflow = false;
+    woff[0] = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+        wc[w] = wcnt_s[w];
+        overflow |= wc[w] > (uint32_t)WCAP;
+        woff[w + 1] = woff[w] + wc[w];
+    }
+    const uint32_t nc = overflow ? (uint32_t)FCAP + 1u : woff[NW];
+    auto cand_at = [&](uint32_t i) -> unsigned long long {
+        int w = 0;
+#pragma unroll
+        for (int x = 1; x < NW; ++x) w += i >= woff[x];
+        return cand[w * WCAP + (i - woff[w])];
+    };
     uint32_t bulk;
     if (nc <= 64) {
         // one wave sorts the candidates' keys; lanes 0..31 are the outliers,
         // lane 32 holds the (t+1)-th largest
         if (wave == 0) {
-            const unsigned long long key = wave_sort_desc64(lane < (int)nc ? cand[lane] : 0ull);
+            const unsigned long long key = wave_sort_desc64(lane < (int)nc ? cand_at(lane) : 0ull);
             if (lane <= FRQ_T) top[lane] = key;
         }
         __syncthreads();
     } else if (nc <= (uint32_t)FCAP) {
         // exact rank of every candidate; the 33 largest keys land in top[]
         for (uint32_t i = tid; i < nc; i += BLOCK) {
-            const unsigned long long key = cand[i];
+            const unsigned long long key = cand_at(i);
             uint32_t rank = 0;
-            uint32_t j = 0;
-            for (; j + 4 <= nc; j += 4) {
-                const unsigned long long c0 = cand[j], c1 = cand[j + 1], c2 = cand[j + 2], c3 = cand[j + 3];
-                rank += (c0 > key) + (c1 > key) + (c2 > key) + (c3 > key);
-            }
-            for (; j < nc; ++j) rank += cand[j] > key;
+#pragma unroll
+            for (int w = 0; w < NW; ++w)
+                for (uint32_t j = 0; j < wc[w]; ++j) rank += cand[w * WCAP + j] > key;
             if (rank <= (uint32_t)FRQ_T) top[rank] = key;
         }
         __syncthreads();
@@ -439,8 +467,9 @@ __global__ __launch_bounds__(BLOCK) void quant_rows_fast(
             const uint32_t idx = lane < FRQ_T ? 0xFFFFFFFFu - (uint32_t)(top[lane] & 0xFFFFFFFFu) : 0xFFFFFFFFu;
             const uint32_t si = wave_sort_asc(idx);
             if (lane < FRQ_T) {
-                sel_i[lane] = si;
-                atomicOr(&bitmap[si >> 5], 1u << (si & 31));
+                const uint32_t sk = min(si, (uint32_t)(K - 1));
+                sel_i[lane] = sk;
+                atomicOr(&bitmap[sk >> 5], 1u << (sk & 31));
             }
         }
     } else {
@@ -481,16 +510,31 @@ __global__ __launch_bounds__(BLOCK) void quant_rows_fast(
     const float r = 1.0f / sa;
     // Markstein correction needs no under/overflow in q*sa and the residual
     const bool fast = sa >= 1e-30f && sa <= 1e30f && rowmax < 0x7A800000u;  // |a| < 2^118
+    if (fast) {
 #pragma unroll
-    for (int i = 0; i < NV4; ++i) {
-        const int i4 = tid + BLOCK * i;
-        if (i4 < K4) {
+        for (int i = 0; i < NV4; ++i) {
+            const int i4 = tid + BLOCK * i;
+            if (i4 < K4) {
+                const int base = 4 * i4;
+                const uint32_t bw = bitmap[base >> 5] >> (base & 31);
+                uint32_t w = rq8(qdiv_fast(v[i].x, sa, r));
+                w |= rq8(qdiv_fast(v[i].y, sa, r)) << 8;
+                w |= rq8(qdiv_fast(v[i].z, sa, r)) << 16;
+                w |= rq8(qdiv_fast(v[i].w, sa, r)) << 24;
+                const uint32_t keep = ((bw & 1u) ? 0u : 0xFFu) | ((bw & 2u) ? 0u : 0xFF00u) |
+                                      ((bw & 4u) ? 0u : 0xFF0000u) | ((bw & 8u) ? 0u : 0xFF000000u);
+                reinterpret_cast<uint32_t*>(q)[i4] = w & keep;
+            }
+        }
+    } else {
+        for (int i4 = tid; i4 < K4; i4 += BLOCK) {
+            const float4 x = reinterpret_cast<const float4*>(a)[i4];
             const int base = 4 * i4;
             const uint32_t bw = bitmap[base >> 5] >> (base & 31);
-            const uint32_t b0 = (bw & 1u) ? 0u : (uint8_t)q8(v[i].x, sa, r, fast);
-            const uint32_t b1 = (bw & 2u) ? 0u : (uint8_t)q8(v[i].y, sa, r, fast);
-            const uint32_t b2 = (bw & 4u) ? 0u : (uint8_t)q8(v[i].z, sa, r, fast);
-            const uint32_t b3 = (bw & 8u) ? 0u : (uint8_t)q8(v[i].w, sa, r, fast);
+            const uint32_t b0 = (bw & 1u) ? 0u : q8_slow(x.x, sa);
+            const uint32_t b1 = (bw & 2u) ? 0u : q8_slow(x.y, sa);
+            const uint32_t b2 = (bw & 4u) ? 0u : q8_slow(x.z, sa);
+            const uint32_t b3 = (bw & 8u) ? 0u : q8_slow(x.w, sa);
             reinterpret_cast<uint32_t*>(q)[i4] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
         }
     }
