@@ -42,6 +42,59 @@ def int4_bytes(m, k, n, g=32):
     return n * k // 2 + 2 * n * ((k + g - 1) // g) + 4 * m * k + 4 * m * n
 
 
+DOM_SHAPE = (896, 151936)  # the headline's dominant GEMV launch (136 MB of weights)
+DOM_KERNEL = "gemv3_i8_kernel<8,8,true>"
+PMC_COPY_BYTES = 256 << 20
+PMC_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                           "gemv_i8_m1_K896_N151936_pmc.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the dominant kernel, from the committed
+    rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, each scaled by the
+    same counter's reading on a copy of known size); None if absent."""
+    try:
+        with open(PMC_SUMMARY) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
+def pmc_pass(fa, hip, synth, ctx, log):
+    """Counter-collection workload, run under `rocprofv3 --pmc`: 3 device
+    copies of PMC_COPY_BYTES (the calibration kernel), then 9 launches of
+    the dominant GEMV kernel on pre-quantised input (3 weight replicas)."""
+    src = hip.DeviceArray((PMC_COPY_BYTES,), np.uint8)
+    dst = hip.DeviceArray((PMC_COPY_BYTES,), np.uint8)
+    src.zero()
+    hip.synchronize()
+    for _ in range(3):
+        hip.copy_d2d(dst.ptr, src.ptr, PMC_COPY_BYTES)
+    hip.synchronize()
+    log(f"pmc: 3 copies of {PMC_COPY_BYTES} bytes")
+    k, n = DOM_SHAPE
+    reps = []
+    for r in range(3):
+        wt, scale = synth.int8_weight(n, k, synth.seed(1, r) + 2)
+        reps.append(ctx.upload_i8(wt, scale))
+    a = synth.activations(1, k, synth.seed(1) + 2)
+    da = hip.DeviceArray.from_numpy(a)
+    out = hip.DeviceArray((1, n), np.float32)
+    a8 = hip.DeviceArray((1, fa.quant_pitch(k)), np.int8)
+    sa = hip.DeviceArray((1,), np.float32)
+    oi = hip.DeviceArray((1, 32), np.uint32)
+    ov = hip.DeviceArray((1, 32), np.float32)
+    ctx.quant_dev(da.ptr, 1, k, a8.ptr, sa.ptr, oi.ptr, ov.ptr)
+    for i in range(9):
+        reps[i % 3].mm_q_dev(a8.ptr, sa.ptr, oi.ptr, ov.ptr, 1, out.ptr)
+    ctx.sync()
+    log(f"pmc: 9 launches of {DOM_KERNEL} at K={k} N={n}, "
+        f"{gemv_kernel_bytes(1, k, n)} algorithmic bytes each")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -51,6 +104,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-detail", action="store_true")
+    ap.add_argument("--pmc-pass", action="store_true",
+                    help="only the counter-collection workload (run under rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path "
@@ -63,6 +118,9 @@ def main():
     ctx = fa.Context(0)
     stream = fa.lib.frq_get_stream(ctx.h)
     log = lambda *a: print("[bench]", *a, file=sys.stderr, flush=True)
+    if args.pmc_pass:
+        pmc_pass(fa, hip, synth, ctx, log)
+        return
 
     def time_loop(fn, iters, warm=3):
         for i in range(warm):
@@ -143,11 +201,11 @@ def main():
         qus = time_loop(lambda i, si=si: ctx.quant_dev(acts[si][1].ptr, 1, k, a8.ptr, sa.ptr, oi.ptr,
                                                        ov.ptr), 60) * 1e3
         detail["int8_m1_gemv_kernel"][f"K{k}_N{n}"]["quant_us"] = round(qus, 2)
-    dom = max(shapes, key=lambda s: s[0] * s[1])  # (896, 151936): 136 MB per launch
+    dom = DOM_SHAPE
     us_dom, gb_dom = gemv_rows[dom]
     roofline = {"bound": "hbm", "achieved": round(gb_dom, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(gb_dom / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": f"gemv_i8_kernel (M=1, K={dom[0]}, N={dom[1]})",
+                "frac": round(gb_dom / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                "kernel": f"{DOM_KERNEL} (M=1, K={dom[0]}, N={dom[1]})",
                 "bytes_per_launch": gemv_kernel_bytes(1, *dom), "us_per_launch": round(us_dom, 2)}
 
     if not args.no_detail:

@@ -7,9 +7,10 @@
 // outliers of av * wt[j,ch].
 //
 // acc: LDS-tiled v_mfma_i32_16x16x64_i8 over a8 (Mp,Kp) x wt (Np,Kp), both
-// K-contiguous.  128x128 output tile per 256-thread workgroup, 2x2 waves of
-// 64x64 (4x4 MFMA blocks), k-step 128 (one 128-byte line per row), register
-// prefetch of the next k-step while the current one is multiplied.
+// K-contiguous.  128x256 output tile per 256-thread workgroup, 2x2 waves of
+// 64x128 (4x8 MFMA blocks), k-step 64; operands go HBM -> LDS directly
+// (global_load_lds, no register staging) through a 3-stage ring with one
+// barrier per k-step, and the tile order is XCD-aware (tile_of below).
 //
 // corr: 32 VALU multiply-adds per output would cost as much as the whole
 // MFMA GEMM, so corr also runs on the int8 MFMA.  For each 128-row M tile

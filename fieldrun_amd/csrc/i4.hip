@@ -16,8 +16,11 @@
 // same for every lane (scalar loads into SGPRs).  To fill the chip when N is
 // small the groups are split into S contiguous segments, one wave each; the
 // per-segment folds are combined in segment order by a second tiny kernel.
-// With S == 1 the result is bit-identical to i4_dot_avx2; with S > 1 the
-// fold over groups is re-associated at S points (within the 1e-4 tolerance).
+// Within a group the arithmetic is i4_dot_avx2's; the fold over groups is
+// re-associated (the 4 waves of a block take interleaved groups, combined in
+// wave order, and S > 1 segments), which stays within 1e-5 of sum |a*w|.
+// Shapes outside the blocked layout run i4_gemv_generic, bit-identical to
+// i4_dot_avx2.
 #include "frq_internal.h"
 
 namespace frq {

@@ -12,18 +12,31 @@
 // in ascending channel order.  A NaN in a row with t < K is the reference's
 // partial_cmp().unwrap() panic: the kernel raises *err.
 //
-// One workgroup per row.  The (t+1)-th largest is found without sorting:
-//   1. each thread's max |a| (coalesced sweep);
-//   2. tau0 = the (t+1)-th largest thread max (LDS radix select over BLOCK
-//      values).  At least t+1 elements are >= tau0, so bulk_max >= tau0;
-//   3. elements >= tau0 (typically a few dozen) are compacted into LDS and
-//      an 8-bit-digit radix select over them yields bulk_max exactly; if more
-//      than CAP survive (e.g. constant rows) the select runs over the whole
-//      row from global memory instead;
-//   4. the outliers are taken in channel order by contiguous per-thread
-//      chunks and block scans (ties, then selected counts) into an LDS list
-//      and a channel bitmap;
-//   5. a8 is written once, coalesced, with the outlier slots zero.
+// One workgroup per row; HBM traffic is one read of the f32 row and one
+// write of the i8 row.  The (t+1)-th largest is found without a full sort.
+//
+// quant_rows_fast (K % 4 == 0, 32 < K <= 20480, 16-byte aligned rows; every
+// shape of the hot path): 256 threads, the row held in registers (float4
+// loads, one coalesced sweep).
+//   1. each thread's max |a|;
+//   2. tau0 = the 33rd largest thread max: every wave sorts its 64 maxima
+//      with a bitonic network on DPP / permlane lane exchanges, wave 0
+//      merges the four lists keeping the top 64.  At least t+1 elements are
+//      >= tau0, so bulk_max >= tau0;
+//   3. the elements >= tau0 (a few dozen on real rows) are compacted into
+//      per-wave LDS regions with ballot + mbcnt (no atomics) as
+//      (|a| << 32 | ~channel) keys; up to 64 are sorted in one wave, up to
+//      2048 are ranked by counting, and beyond that (constant rows) a radix
+//      select over the row gives bulk_max;
+//   4. the t outliers (|a| > bulk_max, then ties at bulk_max lowest channel
+//      first) are put in channel order by a wave sort and marked in an LDS
+//      bitmap;
+//   5. a8 = round(a / sa) from the registers, the quotient taken as a
+//      Markstein-corrected product with RN(1/sa), packed four to a word, the
+//      outlier slots zero, written once, coalesced.
+// quant_rows (any other K or alignment): the same steps from global memory
+// with LDS radix selects (four 8-bit MSB-first digit passes) and block scans,
+// and an IEEE divide.
 // |a| is compared as its IEEE bit pattern, which orders non-negative floats.
 #include "frq_internal.h"
 

@@ -107,3 +107,8 @@ class Event:
 
 def synchronize():
     _chk(_hip.hipDeviceSynchronize(), "hipDeviceSynchronize")
+
+
+def copy_d2d(dst: int, src: int, nbytes: int):
+    """Device-to-device copy (the runtime's blit kernel), synchronous."""
+    _chk(_hip.hipMemcpy(dst, src, nbytes, D2D), "hipMemcpy D2D")

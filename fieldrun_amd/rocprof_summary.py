@@ -1,0 +1,155 @@
+"""Summarise rocprofv3 CSV output as short markdown.
+
+  python3 -m fieldrun_amd.rocprof_summary stats KERNEL_STATS_CSV [--command CMD]
+      per-kernel call count and durations from `rocprofv3 --kernel-trace
+      --stats --output-format csv` (the *_kernel_stats.csv file).
+
+  python3 -m fieldrun_amd.rocprof_summary trace KERNEL_TRACE_CSV [--command CMD]
+      the same per (kernel, workgroup count) from *_kernel_trace.csv, with
+      register / LDS / scratch use.
+
+  python3 -m fieldrun_amd.rocprof_summary pmc --fetch CSV --write CSV
+          --kernel NAME --copy-bytes N --algo-bytes B [--command-fetch CMD]
+          [--command-write CMD]
+      HBM traffic per launch of kernel NAME from two `rocprofv3 --pmc` runs
+      (FETCH_SIZE, then WRITE_SIZE; *_counter_collection.csv).  Each counter
+      (KiB per dispatch) is scaled by the factor that makes the same counter
+      read N bytes on the device-to-device copy of N bytes in the same run.
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import re
+import sys
+from collections import defaultdict
+
+
+def short_name(name: str) -> str:
+    """Kernel name without namespaces and parameter list, template args kept."""
+    depth, cut = 0, len(name)
+    for i, ch in enumerate(name):  # drop the trailing "(args)"
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0 and not name.startswith("(", i + 1):
+            if name[i:i + 21] == "(anonymous namespace)":
+                continue
+            cut = i
+            break
+    s = name[:cut].replace("(anonymous namespace)::", "")
+    s = re.sub(r"^(void\s+)", "", s)
+    s = re.sub(r"\bfrq::", "", s)
+    return s.replace(" ", "")
+
+
+def _rows(path: str):
+    with open(path, newline="") as f:
+        yield from csv.DictReader(f)
+
+
+def stats(args) -> str:
+    rows = list(_rows(args.csv))
+    out = []
+    if args.command:
+        out += ["Command:", "", "    " + args.command, ""]
+    out += ["| kernel | calls | avg us | min us | max us | % time |", "|---|---:|---:|---:|---:|---:|"]
+    rows.sort(key=lambda r: -float(r.get("TotalDurationNs", 0) or 0))
+    for r in rows[: args.top]:
+        out.append("| `%s` | %s | %.2f | %.2f | %.2f | %.1f |" % (
+            short_name(r["Name"]), r["Calls"], float(r["AverageNs"]) / 1e3,
+            float(r["MinNs"]) / 1e3, float(r["MaxNs"]) / 1e3, float(r["Percentage"])))
+    return "\n".join(out) + "\n"
+
+
+def trace(args) -> str:
+    """Per (kernel, grid) durations from *_kernel_trace.csv: launches of one
+    kernel at different shapes have different grids."""
+    acc = defaultdict(list)
+    meta = {}
+    for r in _rows(args.csv):
+        key = (short_name(r["Kernel_Name"]), int(r["Grid_Size_X"]) // max(1, int(r["Workgroup_Size_X"])))
+        acc[key].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        meta[key] = (r["VGPR_Count"], r["Accum_VGPR_Count"], r["SGPR_Count"], r["LDS_Block_Size"],
+                     r["Scratch_Size"])
+    out = []
+    if args.command:
+        out += ["Command:", "", "    " + args.command, ""]
+    out += ["| kernel | workgroups | calls | avg us | min us | max us | VGPR | AGPR | SGPR | LDS B | scratch B |",
+            "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    keys = sorted(acc, key=lambda k: -sum(acc[k]))[: args.top]
+    for k in keys:
+        v = acc[k]
+        out.append("| `%s` | %d | %d | %.2f | %.2f | %.2f | %s | %s | %s | %s | %s |" % (
+            k[0], k[1], len(v), sum(v) / len(v), min(v), max(v), *meta[k]))
+    return "\n".join(out) + "\n"
+
+
+def _per_kernel(path: str, counter: str):
+    """Mean counter value per dispatch, by short kernel name."""
+    acc = defaultdict(list)
+    for r in _rows(path):
+        if r.get("Counter_Name", "").strip() != counter:
+            continue
+        acc[short_name(r["Kernel_Name"])].append(float(r["Counter_Value"]))
+    return {k: (sum(v) / len(v), len(v)) for k, v in acc.items()}
+
+
+def _pick(table, pattern: str, what: str):
+    key = pattern.replace(" ", "")
+    hits = [k for k in table if key in k]
+    if len(hits) != 1:
+        sys.exit(f"{what}: {len(hits)} kernels match {pattern!r}: {sorted(table)}")
+    return hits[0], table[hits[0]]
+
+
+def pmc(args) -> str:
+    lines = []
+    total = 0.0
+    for counter, path, cmd in (("FETCH_SIZE", args.fetch, args.command_fetch),
+                               ("WRITE_SIZE", args.write, args.command_write)):
+        table = _per_kernel(path, counter)
+        cname, (cval, cn) = _pick(table, args.copy_kernel, counter + " copy")
+        kname, (kval, kn) = _pick(table, args.kernel, counter + " kernel")
+        factor = args.copy_bytes / (cval * 1024.0)
+        bytes_ = kval * 1024.0 * factor
+        total += bytes_
+        if cmd:
+            lines += [f"{counter} run:", "", "    " + cmd, ""]
+        lines += [f"- `{cname}` ({cn} dispatches of {args.copy_bytes} bytes): {counter} = {cval:.0f} KiB"
+                  f" per dispatch, scale factor {factor:.4f}",
+                  f"- `{kname}` ({kn} dispatches): {counter} = {kval:.0f} KiB per dispatch"
+                  f" -> {bytes_:.0f} bytes", ""]
+    lines += [f"Algorithmic bytes per launch: {args.algo_bytes}",
+              f"Measured HBM traffic / algorithmic: {total / args.algo_bytes:.3f}", "",
+              f"traffic_bytes_per_launch: {int(round(total))}"]
+    return "\n".join(lines) + "\n"
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    sub = ap.add_subparsers(dest="mode", required=True)
+    s = sub.add_parser("stats")
+    s.add_argument("csv")
+    s.add_argument("--command", default="")
+    s.add_argument("--top", type=int, default=25)
+    t = sub.add_parser("trace")
+    t.add_argument("csv")
+    t.add_argument("--command", default="")
+    t.add_argument("--top", type=int, default=40)
+    p = sub.add_parser("pmc")
+    p.add_argument("--fetch", required=True)
+    p.add_argument("--write", required=True)
+    p.add_argument("--kernel", required=True)
+    p.add_argument("--copy-kernel", default="copyBuffer")
+    p.add_argument("--copy-bytes", type=int, required=True)
+    p.add_argument("--algo-bytes", type=int, required=True)
+    p.add_argument("--command-fetch", default="")
+    p.add_argument("--command-write", default="")
+    a = ap.parse_args(argv)
+    sys.stdout.write({"stats": stats, "trace": trace, "pmc": pmc}[a.mode](a))
+
+
+if __name__ == "__main__":
+    main()

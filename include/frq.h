@@ -2,11 +2,11 @@
  * frq.h — C ABI of the MI355X (gfx950) quantised-linear library (libfrq.so).
  *
  * This is the drop-in boundary for fieldrun's quantised-linear hot path.  A
- * host (the reference's Rust Bundle through a thin FFI crate, the C++
- * frq::Bundle in fieldrun_amd/csrc/bundle.cpp, or Python ctypes) uploads each
- * weight once into HBM and then calls the linear / expert entry points with
- * plain pointers and sizes.  No torch or HIP types appear in the signatures:
- * streams and device buffers are passed as void*.
+ * host (the reference's Rust Bundle through a thin FFI crate, or Python
+ * ctypes as in fieldrun_amd/__init__.py) uploads each weight once into HBM
+ * and then calls the linear / expert entry points with plain pointers and
+ * sizes.  No torch or HIP types appear in the signatures: streams and device
+ * buffers are passed as void* / typed device pointers.
  *
  * Citations are to the reference crate (/root/reference, fieldrun 0.1.0).
  *
