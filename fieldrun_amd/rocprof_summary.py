@@ -86,14 +86,25 @@ def trace(args) -> str:
     return "\n".join(out) + "\n"
 
 
-def _per_kernel(path: str, counter: str):
-    """Mean counter value per dispatch, by short kernel name."""
+def _per_kernel(path: str, counter: str, largest_grid=()):
+    """Mean counter value per dispatch, by short kernel name.  For kernels
+    whose short name contains one of `largest_grid`, only the dispatches with
+    the largest grid count (the runtime's copy kernel also serves small
+    host<->device copies, which must not dilute the calibration)."""
     acc = defaultdict(list)
     for r in _rows(path):
         if r.get("Counter_Name", "").strip() != counter:
             continue
-        acc[short_name(r["Kernel_Name"])].append(float(r["Counter_Value"]))
-    return {k: (sum(v) / len(v), len(v)) for k, v in acc.items()}
+        acc[short_name(r["Kernel_Name"])].append((int(r.get("Grid_Size", 0) or 0),
+                                                  float(r["Counter_Value"])))
+    out = {}
+    for k, v in acc.items():
+        if any(p in k for p in largest_grid):
+            g = max(x[0] for x in v)
+            v = [x for x in v if x[0] == g]
+        vals = [x[1] for x in v]
+        out[k] = (sum(vals) / len(vals), len(vals))
+    return out
 
 
 def _pick(table, pattern: str, what: str):
@@ -109,7 +120,7 @@ def pmc(args) -> str:
     total = 0.0
     for counter, path, cmd in (("FETCH_SIZE", args.fetch, args.command_fetch),
                                ("WRITE_SIZE", args.write, args.command_write)):
-        table = _per_kernel(path, counter)
+        table = _per_kernel(path, counter, largest_grid=(args.copy_kernel,))
         cname, (cval, cn) = _pick(table, args.copy_kernel, counter + " copy")
         kname, (kval, kn) = _pick(table, args.kernel, counter + " kernel")
         factor = args.copy_bytes / (cval * 1024.0)
