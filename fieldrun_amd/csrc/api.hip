@@ -4,7 +4,7 @@
 // weight uploads, and dispatches Bundle::mm / expert_mm semantics
 // (/root/reference/src/bundle.rs:644-919, 404-461) onto the gfx950 kernels:
 //   int8, M <= 4 (decode)  -> quant kernel + int8 GEMV
-//   int8, M >  4           -> quant kernel + outlier union + int8 MFMA GEMM
+//   int8, M >  4           -> quant kernel (blocked a8) + int8 MFMA GEMM
 //   int4                   -> blocked W4A32 GEMV (M == 1) / batched kernel
 // Every failure becomes an int status plus frq_last_error(); nothing throws.
 #include <mutex>
@@ -85,12 +85,13 @@ struct Carve {
     }
 };
 
-// Bytes of per-call scratch for an int8 linear of m rows.
-size_t i8_scratch_bytes(const Weight& w, size_t m, bool gemm) {
+// Bytes of per-call scratch for an int8 linear of m rows (a second, row-major
+// a8 when the GEMM's blocked a8 must also be returned to the host).
+size_t i8_scratch_bytes(const Weight& w, size_t m, bool rowmajor_copy) {
     const size_t mp = round_up(m, FRQ_MALIGN);
     size_t b = round_up(mp * w.kp, 256) + round_up(mp * 4, 256) +
                2 * round_up(mp * FRQ_T * 4, 256);
-    if (gemm) b += round_up(gemm_union_bytes(m, w.k), 256);
+    if (rowmajor_copy) b += round_up(m * w.kp, 256);
     return b;
 }
 
@@ -98,7 +99,8 @@ bool use_gemv(const Weight& w, size_t m) {
     return m <= 4 && m * w.kp <= 60 * 1024;
 }
 
-// The int8 linear on device pointers; scratch carved from `sc`.
+// The int8 linear on device pointers; scratch carved from `sc`.  With a8o
+// set, *a8o is a row-major (pitch kp) copy of the quantised rows.
 int run_i8(frq_ctx* c, const Weight& w, const float* d_a, size_t m, float* d_out,
            int32_t* d_acc, char* scratch, int8_t** a8o, float** sao,
            uint32_t** oio, float** ovo) {
@@ -109,19 +111,21 @@ int run_i8(frq_ctx* c, const Weight& w, const float* d_a, size_t m, float* d_out
     float* sa = cv.take<float>(mp);
     uint32_t* oi = cv.take<uint32_t>(mp * FRQ_T);
     float* ov = cv.take<float>(mp * FRQ_T);
-    void* ub = gemm ? cv.take<char>(gemm_union_bytes(m, w.k)) : nullptr;
-    if (a8o) { *a8o = a8; *sao = sa; *oio = oi; *ovo = ov; }
+    int8_t* a8rm = (gemm && a8o) ? cv.take<int8_t>(m * w.kp) : a8;
+    if (a8o) { *a8o = a8rm; *sao = sa; *oio = oi; *ovo = ov; }
     if (w.k == 0) {
         HIPCHK(hipMemsetAsync(d_out, 0, m * w.n * sizeof(float), c->stream), "hipMemsetAsync");
         if (d_acc) HIPCHK(hipMemsetAsync(d_acc, 0, m * w.n * sizeof(int32_t), c->stream), "hipMemsetAsync");
         return FRQ_OK;
     }
-    HIPCHK(launch_quant(d_a, m, w.k, w.kp, a8, sa, oi, ov, c->err, c->stream), "launch quant");
     if (!gemm) {
+        HIPCHK(launch_quant(d_a, m, w.k, w.kp, a8, sa, oi, ov, c->err, c->stream), "launch quant");
         HIPCHK(launch_gemv_i8(w, m, a8, sa, oi, ov, d_out, d_acc, c->stream), "launch gemv_i8");
     } else {
-        HIPCHK(launch_union(m, w.k, oi, ov, ub, c->stream), "launch union");
-        HIPCHK(launch_gemm_i8(w, m, a8, sa, oi, ov, ub, d_out, d_acc, c->stream), "launch gemm_i8");
+        HIPCHK(launch_quant(d_a, m, w.k, w.kp, a8, sa, oi, ov, c->err, c->stream, mp), "launch quant");
+        HIPCHK(launch_gemm_i8(w, m, a8, sa, oi, ov, d_out, d_acc, c->stream), "launch gemm_i8");
+        if (a8rm != a8)  // the same quantisation, row-major, for the caller
+            HIPCHK(launch_quant(d_a, m, w.k, w.kp, a8rm, sa, oi, ov, c->err, c->stream), "launch quant");
     }
     return FRQ_OK;
 }
@@ -175,6 +179,7 @@ void free_weight(Weight& w) {
     DeviceGuard g(w.device);
     if (w.wt) (void)hipFree(w.wt);
     if (w.wkn) (void)hipFree(w.wkn);
+    if (w.wblk) (void)hipFree(w.wblk);
     if (w.scale) (void)hipFree(w.scale);
     if (w.q4) (void)hipFree(w.q4);
     if (w.s4) (void)hipFree(w.s4);
@@ -190,6 +195,7 @@ int alloc_i8(frq_ctx* c, Weight& w) {
     const size_t kpa = w.kp ? w.kp : FRQ_KALIGN;
     HIPCHK(hipMalloc(&w.wt, w.np * kpa), "hipMalloc(wt)");
     HIPCHK(hipMalloc(&w.wkn, w.np * kpa), "hipMalloc(wkn)");
+    HIPCHK(hipMalloc(&w.wblk, w.np * kpa), "hipMalloc(wblk)");
     HIPCHK(hipMalloc(&w.scale, w.np * sizeof(float)), "hipMalloc(scale)");
     HIPCHK(hipMemsetAsync(w.wt, 0, w.np * kpa, c->stream), "hipMemsetAsync");
     HIPCHK(hipMemsetAsync(w.wkn, 0, w.np * kpa, c->stream), "hipMemsetAsync");
@@ -286,6 +292,7 @@ frq_w* frq_upload_i8(frq_ctx* c, const int8_t* wt_nk, const float* scale,
     if (!rc && e == hipSuccess && n)
         e = hipMemcpyAsync(w.scale, scale, n * sizeof(float), hipMemcpyHostToDevice, c->stream);
     if (!rc && e == hipSuccess) e = transpose(w.wt, n, k, w.kp, w.wkn, w.np, c->stream);
+    if (!rc && e == hipSuccess) e = launch_blockify(w.wt, w.np, w.np, w.kp, w.kp, w.wblk, c->stream);
     if (!rc && e == hipSuccess) e = hipStreamSynchronize(c->stream);
     if (!rc && e != hipSuccess) rc = hip_fail(e, "frq_upload_i8");
     if (rc) { free_weight(w); delete h; return nullptr; }
@@ -310,6 +317,7 @@ frq_w* frq_upload_i8_bundle(frq_ctx* c, const int8_t* w_kn,
     if (!rc && n && k)
         e = hipMemcpy2DAsync(w.wkn, w.np, w_kn, n, n, k, hipMemcpyHostToDevice, c->stream);
     if (!rc && e == hipSuccess) e = transpose(w.wkn, k, n, w.np, w.wt, w.kp, c->stream);
+    if (!rc && e == hipSuccess) e = launch_blockify(w.wt, w.np, w.np, w.kp, w.kp, w.wblk, c->stream);
     if (!rc && e == hipSuccess && n) e = hipMalloc(&hs, n * sizeof(uint16_t));
     if (!rc && e == hipSuccess && n)
         e = hipMemcpyAsync(hs, scale_f16, n * sizeof(uint16_t), hipMemcpyHostToDevice, c->stream);
@@ -385,7 +393,7 @@ int frq_mm_dev(frq_ctx* c, const frq_w* wh, const float* d_a, size_t m, float* d
     if (!d_a || !d_out) return fail(FRQ_ERR_ARG, "null activation/output pointer");
     DeviceGuard g(c->device);
     if (w.dtype == FRQ_DT_I8) {
-        if (int rc = ws_reserve(c, i8_scratch_bytes(w, m, !use_gemv(w, m)))) return rc;
+        if (int rc = ws_reserve(c, i8_scratch_bytes(w, m, false))) return rc;
         return run_i8(c, w, d_a, m, d_out, nullptr, (char*)c->ws, nullptr, nullptr, nullptr, nullptr);
     }
     if (w.dtype == FRQ_DT_I4) {
@@ -433,15 +441,12 @@ int frq_mm_i8_q_dev(frq_ctx* c, const frq_w* wh, const int8_t* d_a8, const float
         HIPCHK(launch_gemv_i8(w, m, d_a8, d_sa, d_oidx, d_oval, d_out, nullptr, c->stream), "launch gemv_i8");
         return FRQ_OK;
     }
-    // the MFMA GEMM reads a8 rows up to round_up(m, 128): stage a padded copy
+    // the MFMA GEMM reads round_up(m, 128) rows of a8 in the blocked layout
     const size_t mp = round_up(m, FRQ_MALIGN);
-    const size_t a8b = round_up(mp * w.kp, 256);
-    if (int rc = ws_reserve(c, a8b + round_up(gemm_union_bytes(m, w.k), 256))) return rc;
+    if (int rc = ws_reserve(c, round_up(mp * w.kp, 256))) return rc;
     int8_t* a8 = (int8_t*)c->ws;
-    void* ub = (char*)c->ws + a8b;
-    HIPCHK(hipMemcpyAsync(a8, d_a8, m * w.kp, hipMemcpyDeviceToDevice, c->stream), "hipMemcpyAsync(a8)");
-    HIPCHK(launch_union(m, w.k, d_oidx, d_oval, ub, c->stream), "launch union");
-    HIPCHK(launch_gemm_i8(w, m, a8, d_sa, d_oidx, d_oval, ub, d_out, nullptr, c->stream), "launch gemm_i8");
+    HIPCHK(launch_blockify(d_a8, m, mp, w.kp, w.kp, a8, c->stream), "launch blockify");
+    HIPCHK(launch_gemm_i8(w, m, a8, d_sa, d_oidx, d_oval, d_out, nullptr, c->stream), "launch gemm_i8");
     return FRQ_OK;
 }
 
@@ -461,7 +466,7 @@ static int mm_host(frq_ctx* c, const frq_w* wh, const float* a, size_t m, float*
     const size_t in_b = round_up(m * w.k * sizeof(float) + 16, 256);
     const size_t out_b = round_up(m * w.n * sizeof(float), 256);
     const size_t acc_b = acc ? round_up(m * w.n * sizeof(int32_t), 256) : 0;
-    const size_t work = i8 ? i8_scratch_bytes(w, m, !use_gemv(w, m))
+    const size_t work = i8 ? i8_scratch_bytes(w, m, a8h && !use_gemv(w, m))
                            : round_up(i4_ws_floats(w, m) * sizeof(float) + 256, 256);
     if (int rc = ws_reserve(c, in_b + out_b + acc_b + work)) return rc;
     char* base = (char*)c->ws;

@@ -11,8 +11,12 @@
 //                     ((b*ng + gi)*64 + r)*16  (g == 32, K % 32 == 0), or
 //                     the bundle's own (N, ceil(K/2)) rows otherwise.
 //                scale (N, ng) f16 in the same blocked order / as stored.
-//   activations  a8   (Mp, Kp) i8 per call (workspace), sa (M) f32,
-//                     oidx/oval (M, 32) u32/f32, outliers in ascending channel.
+//                wblk (Np, Kp) i8 in the blocked MFMA-operand layout
+//                     (blk_off below), read by the GEMM's main loop.
+//   activations  a8   (Mp, Kp) i8 per call (workspace): row-major for the
+//                     GEMV, blocked (blk_off, R = Mp) for the GEMM; sa (M)
+//                     f32, oidx/oval (M, 32) u32/f32, outliers in ascending
+//                     channel.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -30,6 +34,15 @@
 namespace frq {
 
 inline size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+// Blocked MFMA-operand layout of an (R, Kp) int8 matrix (R % 16 == 0,
+// Kp % 64 == 0): the v_mfma_i32_16x16x64_i8 operand of rows 16rb..16rb+15
+// and k-bytes 64kb..64kb+63 is one contiguous 1 KB block in lane order
+// (lane 16g + r holds row r, k-bytes 16g..16g+15), blocks k-block major.
+__host__ __device__ inline size_t blk_off(size_t i, size_t k, size_t R) {
+    return ((k >> 6) * (R >> 4) + (i >> 4)) * 1024 + ((((k & 63) >> 4) << 4) + (i & 15)) * 16 +
+           (k & 15);
+}
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
@@ -88,6 +101,7 @@ struct Weight {
     size_t np = 0, kp = 0;   // padded dims (int8)
     int8_t* wt = nullptr;    // int8 (Np, Kp)
     int8_t* wkn = nullptr;   // int8 (Kp, Np): the bundle's (in, out) layout
+    int8_t* wblk = nullptr;  // int8 (Np, Kp) blocked (blk_off): the GEMM operand
     float* scale = nullptr;  // int8 scale (Np)
     uint8_t* q4 = nullptr;   // int4 blocked (64-row blocks), when i4_blocked
     uint16_t* s4 = nullptr;  // int4 f16 scales, blocked
@@ -110,24 +124,25 @@ struct MoeBank {
 };
 
 // ---- kernel launchers (each returns hipError_t of the launch) ------------
-// Activation quant of M rows of K f32 (row pitch K) into a8 (pitch kp).
+// Activation quant of M rows of K f32 (row pitch K) into a8: row-major with
+// pitch kp when mpb == 0, else blocked (blk_off) with R = mpb rows.
 hipError_t launch_quant(const float* a, size_t m, size_t k, size_t kp,
                         int8_t* a8, float* sa, uint32_t* oidx, float* oval,
-                        int* err, hipStream_t s);
+                        int* err, hipStream_t s, size_t mpb = 0);
 // int8 GEMV for 1 <= m <= 4.
 hipError_t launch_gemv_i8(const Weight& w, size_t m, const int8_t* a8,
                           const float* sa, const uint32_t* oidx,
                           const float* oval, float* out, int32_t* acc,
                           hipStream_t s);
-// Union of outlier channels per M tile and their 3-digit int8 split.
-size_t gemm_union_bytes(size_t m, size_t k);
-hipError_t launch_union(size_t m, size_t k, const uint32_t* oidx,
-                        const float* oval, void* ubuf, hipStream_t s);
-// int8 MFMA GEMM for m > 4.
-hipError_t launch_gemm_i8(const Weight& w, size_t m, const int8_t* a8,
+// (valid rows of an (R, kp) row-major int8 matrix, pitch) -> blocked
+// (blk_off, R rows); rows >= valid become zero.
+hipError_t launch_blockify(const int8_t* src, size_t valid, size_t R, size_t kp,
+                           size_t pitch, int8_t* dst, hipStream_t s);
+// int8 MFMA GEMM for m > 4 on blocked a8 (R = round_up(m, 128)).
+hipError_t launch_gemm_i8(const Weight& w, size_t m, const int8_t* a8b,
                           const float* sa, const uint32_t* oidx,
-                          const float* oval, const void* ubuf, float* out,
-                          int32_t* acc, hipStream_t s);
+                          const float* oval, float* out, int32_t* acc,
+                          hipStream_t s);
 // int4 linear (any m).
 hipError_t launch_i4(const Weight& w, size_t m, const float* a, float* out,
                      float* wsf, unsigned* tickets, hipStream_t s);

@@ -6,163 +6,43 @@
 // acc = i8dot(a8[i], wt[j]) in i32 (bit-exact), corr = sum over row i's
 // outliers of av * wt[j,ch].
 //
-// acc: LDS-tiled v_mfma_i32_16x16x64_i8 over a8 (Mp,Kp) x wt (Np,Kp), both
-// K-contiguous.  128x256 output tile per 256-thread workgroup, 2x2 waves of
-// 64x128 (4x8 MFMA blocks), k-step 64; operands go HBM -> LDS directly
-// (global_load_lds, no register staging) through a 3-stage ring with one
-// barrier per k-step, and the tile order is XCD-aware (tile_of below).
+// Operand layout ("blocked", both a8 and the weight copy wblk): the MFMA
+// operand of 16 rows x 64 k-bytes is one contiguous 1 KB block in lane order
+// (lane 16g + r holds row r, k-bytes 16g..16g+15), blocks ordered k-block
+// major: block (kb, rb) at (kb * R/16 + rb) * 1 KB.  Every global_load_lds
+// of the main loop therefore reads 1 KB of contiguous memory, and a k-step's
+// 8 (A) or 16 (B) blocks are consecutive.  (Loading the same operands from
+// row-major (R, Kp) arrays, 16 rows x 64 bytes per instruction, runs the
+// L2 -> LDS path at a third of the contiguous rate.)
 //
-// corr: 32 VALU multiply-adds per output would cost as much as the whole
-// MFMA GEMM, so corr also runs on the int8 MFMA.  For each 128-row M tile
-// the union U of its rows' outlier channels is formed (sorted) and each
-// outlier value is written as X = round(av / so[i]), |X| <= 127*2^16, with
-// so[i] = max|av| / (127*2^16), split into three signed int8 digits
-// X = d2*2^16 + d1*2^8 + d0.  Then C_d = D_d (BM x |U|) . W[:, U]^T is an
-// exact int32 MFMA GEMM per digit and corr = so * ((C2*256 + C1)*256 + C0).
-// W[:, U] is staged from the (K, Np) row-major copy of the weight (wkn), one
-// 128-byte row per channel, transposed into LDS.  The 24-bit split makes
-// corr differ from the reference's f32 sum by ~1e-7 relative; acc stays
-// bit-exact.  Rows with a non-finite outlier take the exact sequential
-// corr in the epilogue instead.
+// acc: 128 x BN output tile per 256-thread workgroup (BN = 256 or 128),
+// 2x2 waves of 64 x BN/2, v_mfma_i32_16x16x64_i8, k-step 64; operands go
+// HBM -> LDS directly (global_load_lds_dwordx4) through an NST-stage ring.
+// The ring's waits are explicit vmcnt counts before a raw s_barrier:
+// __syncthreads() would also drain every LDS-DMA load still in flight and
+// serialise the ring.  The tile order is XCD-aware (tile_of).
+//
+// corr: 32 VALU multiply-adds per output would cost as much as the MFMA GEMM
+// itself, so corr also runs on the int8 MFMA.  Per workgroup, after the main
+// loop, the union U of its 128 rows' outlier channels is built in LDS (a
+// channel bitmap and its prefix popcounts); each outlier value becomes
+// X = round(av / so[i]), |X| <= 127*2^16, so[i] = max|av| / (127*2^16),
+// split into three signed int8 digits X = d2*2^16 + d1*2^8 + d0.  Then
+// C_d = D_d (128 x |U|) . W[:, U]^T is an exact int32 MFMA product per digit
+// and corr = so * ((C2*256 + C1)*256 + C0).  W[:, U] is read from the (K, Np)
+// row-major weight copy (wkn): for a channel, the tile's columns are
+// contiguous bytes.  The 24-bit split makes corr differ from the reference's
+// f32 sum by ~1e-7 relative; acc stays bit-exact.  Rows with a non-finite
+// outlier take the exact sequential corr instead.
 #include "frq_internal.h"
 
 namespace frq {
 
 namespace {
 
-constexpr int BM = 128, BK = 128;   // union tile rows; union padding unit
-constexpr int UMAX = BM * FRQ_T;     // max union size per M tile
-constexpr float XMAX = 8323072.0f;   // 127 * 2^16
-
-struct UnionView {
-    int32_t* nu;     // [tiles]
-    uint32_t* u;     // [tiles][UMAX]
-    float* so;       // [Mp]
-    int32_t* fin;    // [Mp] 1 = non-finite outlier in row
-    int8_t* d;       // [tiles][3][BM][UMAX]
-};
-
-__host__ __device__ inline UnionView union_view(void* base, size_t m) {
-    const size_t tiles = (m + BM - 1) / BM, mp = tiles * BM;
-    char* p = (char*)base;
-    UnionView v;
-    v.nu = (int32_t*)p; p += round_up(tiles * 4, 256);
-    v.u = (uint32_t*)p; p += round_up(tiles * UMAX * 4, 256);
-    v.so = (float*)p; p += round_up(mp * 4, 256);
-    v.fin = (int32_t*)p; p += round_up(mp * 4, 256);
-    v.d = (int8_t*)p;
-    return v;
-}
-
-// ---- union of outlier channels + digit split, one workgroup per M tile --
-__global__ __launch_bounds__(256) void union_kernel(
-    const uint32_t* __restrict__ oidx, const float* __restrict__ oval, int M,
-    int K, int t, UnionView uv) {
-    extern __shared__ uint32_t sm[];
-    const int nw = (K + 31) / 32;
-    uint32_t* bitmap = sm;           // nw words
-    uint32_t* wpre = sm + nw;        // nw words: popcount prefix
-    __shared__ uint32_t scan_lds[5];
-
-    const int tile = blockIdx.x, tid = threadIdx.x;
-    const int r0 = tile * BM, nrows = min(BM, M - r0);
-    for (int w = tid; w < nw; w += 256) bitmap[w] = 0u;
-    __syncthreads();
-    for (int i = tid; i < nrows * t; i += 256) {
-        const uint32_t c = oidx[(size_t)(r0 + i / t) * FRQ_T + i % t];
-        if (c < (uint32_t)K) atomicOr(&bitmap[c >> 5], 1u << (c & 31));
-    }
-    __syncthreads();
-    // prefix popcount over words (contiguous chunk per thread)
-    const int C = (nw + 255) / 256;
-    const int lo = tid * C, hi = min(lo + C, nw);
-    uint32_t cnt = 0;
-    for (int w = lo; w < hi; ++w) cnt += __popc(bitmap[w]);
-    const int lane = tid & 63, wave = tid >> 6;
-    uint32_t incl = cnt;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        uint32_t y = __shfl_up(incl, off, 64);
-        if (lane >= off) incl += y;
-    }
-    if (lane == 63) scan_lds[wave] = incl;
-    __syncthreads();
-    if (tid == 0) {
-        uint32_t run = 0;
-        for (int w = 0; w < 4; ++w) { uint32_t c = scan_lds[w]; scan_lds[w] = run; run += c; }
-        scan_lds[4] = run;
-    }
-    __syncthreads();
-    uint32_t base = scan_lds[wave] + incl - cnt;
-    const uint32_t nu = scan_lds[4];
-    uint32_t* U = uv.u + (size_t)tile * UMAX;
-    for (int w = lo; w < hi; ++w) {
-        wpre[w] = base;
-        uint32_t bits = bitmap[w];
-        while (bits) {
-            const int b = __ffs(bits) - 1;
-            bits &= bits - 1;
-            U[base++] = (uint32_t)(w * 32 + b);
-        }
-    }
-    const uint32_t nup = (nu + BK - 1) / BK * BK;
-    for (uint32_t u = nu + tid; u < nup; u += 256) U[u] = 0u;  // digits are 0 there
-    if (tid == 0) uv.nu[tile] = (int32_t)nu;
-    __syncthreads();
-    // one thread per row: scale, flag and its three digit rows
-    if (tid < BM) {
-        const int row = r0 + tid;
-        float mx = 0.0f;
-        int fin = 0;
-        if (tid < nrows)
-            for (int q = 0; q < t; ++q) {
-                const float v = oval[(size_t)row * FRQ_T + q];
-                fin |= !(fabsf(v) <= 3.0e38f);
-                mx = fmaxf(mx, fabsf(v));
-            }
-        float so = mx > 0.0f ? mx / XMAX : 1.0f;
-        if (!(so >= 1.0e-30f) || !(so <= 1.0e30f)) fin = 1;  // keep digits exact
-        if (fin) so = 1.0f;
-        uv.so[row] = so;
-        uv.fin[row] = fin;
-        int q = 0;
-        for (uint32_t ch = 0; ch < nup; ch += 16) {
-            uint32_t v0[4] = {0, 0, 0, 0}, v1[4] = {0, 0, 0, 0}, v2[4] = {0, 0, 0, 0};
-            while (!fin && tid < nrows && q < t) {
-                const uint32_t c = min(oidx[(size_t)row * FRQ_T + q], (uint32_t)(K - 1));
-                const uint32_t pos = wpre[c >> 5] + __popc(bitmap[c >> 5] & ((1u << (c & 31)) - 1u));
-                if (pos >= ch + 16) break;
-                float xf = rintf(oval[(size_t)row * FRQ_T + q] / so);
-                xf = fminf(fmaxf(xf, -XMAX), XMAX);
-                const int X = (int)xf;
-                const int d0 = (int)(int8_t)(X & 0xFF);
-                const int X1 = (X - d0) >> 8;
-                const int d1 = (int)(int8_t)(X1 & 0xFF);
-                const int d2 = (X1 - d1) >> 8;
-                const int byte = (int)(pos - ch), wd = byte >> 2, sh = (byte & 3) * 8;
-                v0[wd] |= (uint32_t)(d0 & 0xFF) << sh;
-                v1[wd] |= (uint32_t)(d1 & 0xFF) << sh;
-                v2[wd] |= (uint32_t)(d2 & 0xFF) << sh;
-                ++q;
-            }
-            int8_t* drow = uv.d + ((size_t)tile * 3 * BM + tid) * UMAX + ch;
-            *reinterpret_cast<uint4*>(drow) = make_uint4(v0[0], v0[1], v0[2], v0[3]);
-            *reinterpret_cast<uint4*>(drow + (size_t)BM * UMAX) = make_uint4(v1[0], v1[1], v1[2], v1[3]);
-            *reinterpret_cast<uint4*>(drow + (size_t)2 * BM * UMAX) = make_uint4(v2[0], v2[1], v2[2], v2[3]);
-        }
-    }
-}
-
-// ---- the GEMM -------------------------------------------------------------
-// 128 x 256 output tile per 256-thread workgroup; waves 2 (M) x 2 (N), each
-// 64 x 128 = 4 x 8 blocks of v_mfma_i32_16x16x64_i8.  k-step 64; a ring of
-// NST stages in LDS filled by global_load_lds_dwordx4, each 1 KB LDS block
-// holding one 16-row x 64-byte MFMA operand in lane order (lane l = 16*g + r
-// -> row r, bytes 16g..16g+15), so every operand fetch is one conflict-free
-// ds_read_b128 at block*1024 + lane*16.
-constexpr int GBM = 128, GBN = 256, GBK = 64, NST = 3;
-constexpr int ABLK = GBM / 16, BBLK = GBN / 16, SBLK = ABLK + BBLK;  // 8 + 16 blocks
-constexpr int STAGE = SBLK * 1024;                                   // 24 KB
+constexpr int GBM = 128, GBK = 64;
+constexpr int CH = 64;              // union channels per correction chunk
+constexpr float XMAX = 8323072.0f;  // 127 * 2^16
 
 typedef __attribute__((address_space(1))) void gvoid_t;
 typedef __attribute__((address_space(3))) void lvoid_t;
@@ -181,24 +61,10 @@ __device__ __forceinline__ v4i mfma(const v4i a, const v4i b, v4i c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
 
-// Issue this wave's 6 block loads of k-step ks into LDS stage buffer `st`.
-__device__ __forceinline__ void issue_stage(const int8_t* __restrict__ A, const int8_t* __restrict__ W,
-                                            int Kp, int m0, int n0, int ks, int8_t* st) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int r = lane & 15, g = lane >> 4;
-    const size_t k0 = (size_t)ks * GBK + g * 16;
-#pragma unroll
-    for (int i = 0; i < SBLK / 4; ++i) {
-        const int t = wave + 4 * i;
-        const int8_t* src = t < ABLK ? A + (size_t)(m0 + 16 * t + r) * Kp + k0
-                                     : W + (size_t)(n0 + 16 * (t - ABLK) + r) * Kp + k0;
-        dma16(src, st + t * 1024);
-    }
-}
-
-// Bijective XCD-aware tile order: workgroups on the same XCD (id % 8) take a
-// contiguous run of tiles ordered N-tile major, M-tile minor, so the A
-// panel is shared in that XCD's L2 and each weight panel is read once.
+// Bijective XCD-aware tile order: workgroup b runs on XCD b % 8; the
+// workgroups of one XCD take a contiguous run of tiles ordered N-tile
+// major, M-tile minor, so an XCD's concurrent tiles share A k-slices and
+// each weight panel in its L2.
 __device__ __forceinline__ void tile_of(int b, int G, int MT, int& mt, int& nt) {
     const int x = b & 7, j = b >> 3;
     const int q = G >> 3, rem = G & 7;
@@ -208,193 +74,391 @@ __device__ __forceinline__ void tile_of(int b, int G, int MT, int& mt, int& nt) 
     mt = tau % MT;
 }
 
-__global__ __launch_bounds__(256) void gemm_i8_kernel(
-    const int8_t* __restrict__ A, const int8_t* __restrict__ W,
-    const int8_t* __restrict__ Wkn, const float* __restrict__ scale,
-    const float* __restrict__ sa, int M, int N, int Np, int Kp, int t,
-    UnionView uv, const uint32_t* __restrict__ oidx,
+// Block-exclusive prefix sum of one value per thread (256 threads).
+__device__ uint32_t excl_scan256(uint32_t v, uint32_t* sc /*5 words*/, uint32_t* total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint32_t incl = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t y = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += y;
+    }
+    if (lane == 63) sc[wave] = incl;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t run = 0;
+        for (int w = 0; w < 4; ++w) { const uint32_t c = sc[w]; sc[w] = run; run += c; }
+        sc[4] = run;
+    }
+    __syncthreads();
+    const uint32_t r = sc[wave] + incl - v;
+    *total = sc[4];
+    return r;
+}
+
+template <int BN, int NST>
+__global__ __launch_bounds__(256, 2) void gemm_i8_kernel(
+    const int8_t* __restrict__ Ab, const int8_t* __restrict__ Wb,
+    const int8_t* __restrict__ Wkn, const int8_t* __restrict__ Wrow,
+    const float* __restrict__ scale, const float* __restrict__ sa, int M, int Mp,
+    int N, int Np, int K, int Kp, int t, const uint32_t* __restrict__ oidx,
     const float* __restrict__ oval, float* __restrict__ out,
     int32_t* __restrict__ acc_dbg, int MT) {
-    __shared__ __attribute__((aligned(1024))) int8_t lds[NST * STAGE];
+    constexpr int ABLK = GBM / 16, BBLK = BN / 16, SBLK = ABLK + BBLK;
+    constexpr int STAGE = SBLK * 1024;
+    constexpr int TM = 4, TN = BN / 32;  // 16x16 blocks per wave (64 x BN/2)
+    constexpr int PW = SBLK / 4;         // DMA blocks per wave per stage
+    extern __shared__ __attribute__((aligned(1024))) int8_t lds[];
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave >> 1, wn = wave & 1;
     int mt, nt;
     tile_of(blockIdx.x, gridDim.x, MT, mt, nt);
-    const int m0 = mt * GBM, n0 = nt * GBN;
+    const int m0 = mt * GBM, n0 = nt * BN;
     const int S = Kp / GBK;
+    const size_t arb = (size_t)Mp / 16, wrb = (size_t)Np / 16;
 
-    v4i acc[4][8];
+    auto issue = [&](int ks, int8_t* st) {
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-        for (int b = 0; b < 8; ++b) acc[a][b] = v4i{0, 0, 0, 0};
-
-    issue_stage(A, W, Kp, m0, n0, 0, lds);
-    if (S > 1) issue_stage(A, W, Kp, m0, n0, 1, lds + STAGE);
-    for (int s = 0; s < S; ++s) {
-        if (s + 1 < S) wait_vm<SBLK / 4>(); else wait_vm<0>();
-        __syncthreads();
-        if (s + 2 < S) issue_stage(A, W, Kp, m0, n0, s + 2, lds + ((s + 2) % NST) * STAGE);
-        const int8_t* st = lds + (s % NST) * STAGE;
-        v4i af[4], bf[8];
-#pragma unroll
-        for (int bm = 0; bm < 4; ++bm)
-            af[bm] = *reinterpret_cast<const v4i*>(st + (wm * 4 + bm) * 1024 + lane * 16);
-#pragma unroll
-        for (int bn = 0; bn < 8; ++bn)
-            bf[bn] = *reinterpret_cast<const v4i*>(st + (ABLK + wn * 8 + bn) * 1024 + lane * 16);
-#pragma unroll
-        for (int bm = 0; bm < 4; ++bm)
-#pragma unroll
-            for (int bn = 0; bn < 8; ++bn) acc[bm][bn] = mfma(af[bm], bf[bn], acc[bm][bn]);
-    }
-
-    // ---- epilogue, one 32-column sub-tile (2 MFMA blocks) at a time:
-    // t = sa * acc, plus the outlier correction so * C from three int8 digit
-    // MFMAs over the tile's channel union, then out = scale * t.  Lane holds
-    // rows 4*(lane/16)+c and column lane%16 of each 16x16 block.
-    // per-row sa, so and the non-finite flag of the tile, in the last stage
-    // buffer (free in the epilogue)
-    float* meta = reinterpret_cast<float*>(lds + 2 * STAGE + 16 * 1024);
-    __syncthreads();
-    if (threadIdx.x < GBM) {
-        const int i = min(m0 + (int)threadIdx.x, M - 1);
-        meta[threadIdx.x] = sa[i];
-        meta[GBM + threadIdx.x] = uv.fin[i] ? 0.0f : uv.so[i];
-        meta[2 * GBM + threadIdx.x] = uv.fin[i] ? 1.0f : 0.0f;
-    }
-    const int nu = uv.nu[mt];
-    const uint32_t* U = uv.u + (size_t)mt * UMAX;
-    const int r = lane & 15, g = lane >> 4;
-    int8_t* bt = lds + 24 * 1024;
-    // stage digit chunk u0 (3 x 8 DMA blocks) and W[:, U[u0..u0+63]]^T (16 blocks)
-    __syncthreads();
-    auto stage_chunk = [&](int u0) {
-        __syncthreads();
-#pragma unroll
-        for (int i = 0; i < 6; ++i) {
-            const int tb = wave + 4 * i;  // digit tb/8, row block tb%8
-            const int8_t* src = uv.d + (((size_t)mt * 3 + tb / 8) * BM + 16 * (tb % 8) + r) * UMAX + u0 + g * 16;
-            dma16(src, lds + tb * 1024);
+        for (int i = 0; i < PW; ++i) {
+            const int tb = wave + 4 * i;  // wave-uniform
+            const int8_t* src = tb < ABLK
+                ? Ab + ((size_t)ks * arb + m0 / 16 + tb) * 1024 + lane * 16
+                : Wb + ((size_t)ks * wrb + n0 / 16 + (tb - ABLK)) * 1024 + lane * 16;
+            dma16(src, st + tb * 1024);
         }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int idx = threadIdx.x + 256 * i;  // 64 channels x 16 chunks of 16 columns
-            const int uu = idx >> 4, cch = idx & 15;
-            const v4i w = *reinterpret_cast<const v4i*>(Wkn + (size_t)U[u0 + uu] * Np + n0 + cch * 16);
-#pragma unroll
-            for (int b = 0; b < 16; ++b)
-                bt[cch * 1024 + ((uu >> 4) * 16 + b) * 16 + (uu & 15)] = (int8_t)((uint32_t)w[b >> 2] >> ((b & 3) * 8));
-        }
-        wait_vm<0>();
-        __syncthreads();
     };
-    const bool one_chunk = nu <= GBK;
-    if (nu > 0 && one_chunk) stage_chunk(0);
+
+    v4i acc[TM][TN];
 #pragma unroll
-    for (int sub = 0; sub < 4; ++sub) {
-        float tv[4][2][4];
+    for (int a = 0; a < TM; ++a)
 #pragma unroll
-        for (int bm = 0; bm < 4; ++bm)
+        for (int b = 0; b < TN; ++b) acc[a][b] = v4i{0, 0, 0, 0};
+
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int rl = wm * 64 + bm * 16 + (lane >> 4) * 4 + c;
-                const float sai = meta[rl];
+    for (int p = 0; p < NST - 1; ++p)
+        if (p < S) issue(p, lds + p * STAGE);
+    for (int s = 0; s < S; ++s) {
+        // stage s has landed once at most (stages issued after s) x PW loads
+        // of this wave are outstanding; then every wave's part is in LDS
+        const int ahead = min(S - 1 - s, NST - 2);
+        if (ahead >= 2) wait_vm<2 * PW>();
+        else if (ahead == 1) wait_vm<PW>();
+        else wait_vm<0>();
+        __builtin_amdgcn_s_barrier();
+        // the buffer refilled here held stage s-1, which every wave finished
+        // reading (its fragments feed MFMAs issued before this barrier)
+        if (s + NST - 1 < S) issue(s + NST - 1, lds + ((s + NST - 1) % NST) * STAGE);
+        const int8_t* st = lds + (s % NST) * STAGE;
+        v4i af[TM], bf[TN];
 #pragma unroll
-                for (int x = 0; x < 2; ++x) {
-                    const int av = acc[bm][sub * 2 + x][c];
-                    if (acc_dbg) {
-                        const int i = m0 + rl;
-                        const int j = n0 + wn * 128 + (sub * 2 + x) * 16 + (lane & 15);
-                        if (i < M && j < N) acc_dbg[(size_t)i * N + j] = av;
-                    }
-                    tv[bm][x][c] = sai * (float)av;
+        for (int bm = 0; bm < TM; ++bm)
+            af[bm] = *reinterpret_cast<const v4i*>(st + (wm * TM + bm) * 1024 + lane * 16);
+#pragma unroll
+        for (int bn = 0; bn < TN; ++bn)
+            bf[bn] = *reinterpret_cast<const v4i*>(st + (ABLK + wn * TN + bn) * 1024 + lane * 16);
+#pragma unroll
+        for (int bm = 0; bm < TM; ++bm)
+#pragma unroll
+            for (int bn = 0; bn < TN; ++bn) acc[bm][bn] = mfma(af[bm], bf[bn], acc[bm][bn]);
+    }
+    __syncthreads();  // every fragment read; the ring is free for the epilogue
+
+    // ---- epilogue ------------------------------------------------------------
+    // LDS carve (the ring is free): header 8 KB (bitmap, prefix, row meta,
+    // scan, chunk channels, column scales), digits 16 KB, union positions 8 KB, digit
+    // blocks D 24 KB (first used as per-channel flags), W[:, U] blocks BN KB/16.
+    const int nwk = Kp >> 5;                                   // <= 640 bitmap words
+    uint32_t* bitmap = reinterpret_cast<uint32_t*>(lds);       // [640]
+    uint32_t* wpre = bitmap + 640;                             // [640]
+    float* meta = reinterpret_cast<float*>(lds + 5120);        // sa, so, fin: [3][128]
+    uint32_t* scan = reinterpret_cast<uint32_t*>(lds + 6656);  // [8]
+    uint32_t* uch = reinterpret_cast<uint32_t*>(lds + 6688);   // chunk channels [CH]
+    float* scl = reinterpret_cast<float*>(lds + 7168);         // tile column scales [BN]
+    uint32_t* dig = reinterpret_cast<uint32_t*>(lds + 8192);   // [128][32] digits d2|d1|d0
+    uint16_t* dpos = reinterpret_cast<uint16_t*>(lds + 24576); // [128][32] union position
+    int8_t* D = lds + 32768;                                   // 3 x 8 blocks (CH = 64)
+    uint8_t* flag = reinterpret_cast<uint8_t*>(D);             // [Kp] before D is built
+    int8_t* WU = lds + 32768 + 24 * 1024;                      // BN/16 blocks
+
+    const int tid = threadIdx.x;
+    const int nrows = min(GBM, M - m0);
+    // every global operand of the epilogue in one batch of independent loads:
+    // thread (er, eh) takes outliers 16eh..16eh+15 of tile row er; the tile's
+    // column scales go to LDS
+    const int er = tid >> 1, eh = tid & 1;
+    const bool rv = er < nrows;
+    uint32_t oi_r[16];
+    float ov_r[16];
+    {
+        const size_t base = (size_t)(m0 + (rv ? er : 0)) * FRQ_T + eh * 16;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const uint4 x = *reinterpret_cast<const uint4*>(oidx + base + 4 * v);
+            const float4 y = *reinterpret_cast<const float4*>(oval + base + 4 * v);
+            oi_r[4 * v] = x.x; oi_r[4 * v + 1] = x.y; oi_r[4 * v + 2] = x.z; oi_r[4 * v + 3] = x.w;
+            ov_r[4 * v] = y.x; ov_r[4 * v + 1] = y.y; ov_r[4 * v + 2] = y.z; ov_r[4 * v + 3] = y.w;
+        }
+    }
+    const float sa_r = sa[min(m0 + er, M - 1)];
+    if (tid < BN) scl[tid] = scale[n0 + tid];  // Np-padded: in bounds
+    // valid outliers of this thread: q = 16eh + v < t
+    auto qv = [&](int v) { return rv && 16 * eh + v < t; };
+
+    // union of the tile's outlier channels: byte flags, then bitmap words
+    for (int i = tid; i < Kp / 16; i += 256) reinterpret_cast<uint4*>(flag)[i] = make_uint4(0, 0, 0, 0);
+    __syncthreads();
+#pragma unroll
+    for (int v = 0; v < 16; ++v)
+        if (qv(v) && oi_r[v] < (uint32_t)K) flag[oi_r[v]] = 1;
+    __syncthreads();
+    for (int w = tid; w < nwk; w += 256) {
+        const uint4 f0 = reinterpret_cast<const uint4*>(flag)[2 * w];
+        const uint4 f1 = reinterpret_cast<const uint4*>(flag)[2 * w + 1];
+        const uint32_t fw[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+        uint32_t bits = 0;
+#pragma unroll
+        for (int b = 0; b < 32; ++b) bits |= ((fw[b >> 2] >> (8 * (b & 3))) & 1u) << b;
+        bitmap[w] = bits;
+    }
+    __syncthreads();
+    {
+        const int C = (nwk + 255) / 256, lo = tid * C, hi = min(lo + C, nwk);
+        uint32_t cnt = 0;
+        for (int w = lo; w < hi; ++w) cnt += __popc(bitmap[w]);
+        uint32_t nu_total;
+        uint32_t base = excl_scan256(cnt, scan, &nu_total);
+        for (int w = lo; w < hi; ++w) { wpre[w] = base; base += __popc(bitmap[w]); }
+        if (tid == 0) scan[5] = nu_total;
+    }
+    // per row: sa, the digit scale so and the non-finite flag (the row's two
+    // threads are adjacent lanes)
+    float mx = 0.0f;
+    int fin = 0;
+#pragma unroll
+    for (int v = 0; v < 16; ++v)
+        if (qv(v)) {
+            fin |= !(fabsf(ov_r[v]) <= 3.0e38f);
+            mx = fmaxf(mx, fabsf(ov_r[v]));
+        }
+    mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+    fin |= __shfl_xor(fin, 1, 64);
+    float so = mx > 0.0f ? mx / XMAX : 1.0f;
+    if (!(so >= 1.0e-30f) || !(so <= 1.0e30f)) fin = 1;  // keep digits exact
+    if (eh == 0) {
+        meta[er] = sa_r;
+        meta[GBM + er] = fin ? 0.0f : so;
+        meta[2 * GBM + er] = fin ? 1.0f : 0.0f;
+    }
+    __syncthreads();
+    const int nu = (int)scan[5];
+    // union position and three int8 digits of each outlier
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        uint32_t dv = 0;
+        uint16_t p = 0xFFFF;
+        if (qv(v) && !fin) {
+            const uint32_t c = min(oi_r[v], (uint32_t)(K - 1));
+            p = (uint16_t)(wpre[c >> 5] + __popc(bitmap[c >> 5] & ((1u << (c & 31)) - 1u)));
+            float xf = rintf(ov_r[v] / so);
+            xf = fminf(fmaxf(xf, -XMAX), XMAX);
+            const int X = (int)xf;
+            const int d0 = (int)(int8_t)(X & 0xFF);
+            const int X1 = (X - d0) >> 8;
+            const int d1 = (int)(int8_t)(X1 & 0xFF);
+            const int d2 = (X1 - d1) >> 8;
+            dv = (uint32_t)(d0 & 0xFF) | ((uint32_t)(d1 & 0xFF) << 8) | ((uint32_t)(d2 & 0xFF) << 16);
+        }
+        dig[er * FRQ_T + 16 * eh + v] = dv;
+        dpos[er * FRQ_T + 16 * eh + v] = p;
+    }
+
+    if (acc_dbg) {
+#pragma unroll
+        for (int bm = 0; bm < TM; ++bm)
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int bn = 0; bn < TN; ++bn) {
+                    const int i = m0 + wm * 64 + bm * 16 + (lane >> 4) * 4 + c;
+                    const int j = n0 + wn * (BN / 2) + bn * 16 + (lane & 15);
+                    if (i < M && j < N) acc_dbg[(size_t)i * N + j] = acc[bm][bn][c];
                 }
+    }
+    // t = sa * acc for the whole wave tile, in place of acc
+    float tv[TM][TN][4];
+#pragma unroll
+    for (int bm = 0; bm < TM; ++bm)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float sai = meta[wm * 64 + bm * 16 + (lane >> 4) * 4 + c];
+#pragma unroll
+            for (int bn = 0; bn < TN; ++bn) tv[bm][bn][c] = sai * (float)acc[bm][bn][c];
+        }
+
+    // corr, one union chunk of CH channels at a time: D_d blocks (d, rb) hold
+    // rows 16rb.., chunk entries in lane order; WU block cb holds tile
+    // columns 16cb.., the chunk's channels in lane order
+    for (int u0 = 0; u0 < nu; u0 += CH) {
+        __syncthreads();  // dig/dpos written; the previous chunk's blocks consumed
+        for (int i = tid; i < 24 * 64; i += 256) reinterpret_cast<uint4*>(D)[i] = make_uint4(0, 0, 0, 0);
+        if (tid < CH) {
+            // the (u0 + tid)-th set bit of the bitmap: last word with wpre <= target
+            const uint32_t target = (uint32_t)(u0 + tid);
+            uint32_t ch = 0;
+            if (target < (uint32_t)nu) {
+                int lo = 0, hi = nwk - 1;
+                while (lo < hi) {
+                    const int mid = (lo + hi + 1) >> 1;
+                    if (wpre[mid] <= target) lo = mid; else hi = mid - 1;
+                }
+                uint32_t bits = bitmap[lo];
+                for (uint32_t k = target - wpre[lo]; k > 0; --k) bits &= bits - 1;
+                ch = bits ? (uint32_t)lo * 32 + (uint32_t)(__ffs(bits) - 1) : 0u;
+                ch = min(ch, (uint32_t)(K - 1));
             }
-        for (int u0 = 0; u0 < nu; u0 += GBK) {
-            if (!one_chunk) stage_chunk(u0);
-            v4i bf2[2];
+            uch[tid] = ch;
+        }
+        __syncthreads();
+        for (int i = tid; i < GBM * FRQ_T; i += 256) {
+            const int e = (int)dpos[i] - u0;
+            if (e < 0 || e >= CH) continue;
+            const int r = i / FRQ_T;
+            const uint32_t dv = dig[i];
+            const int off = ((16 * (e >> 4) + (r & 15)) * 16) + (e & 15);
 #pragma unroll
-            for (int x = 0; x < 2; ++x)
-                bf2[x] = *reinterpret_cast<const v4i*>(bt + (wn * 8 + sub * 2 + x) * 1024 + lane * 16);
-            // tv += so * (C2 * 2^16 + C1 * 2^8 + C0); so is 0 on non-finite rows
+            for (int d = 0; d < 3; ++d)
+                D[(d * 8 + (r >> 4)) * 1024 + off] = (int8_t)((dv >> (8 * d)) & 0xFF);
+        }
+        {
+            constexpr int NL = CH * (BN / 16) / 256;  // 16-byte loads per thread
+            v4i wv[NL];
 #pragma unroll
-            for (int d = 2; d >= 0; --d) {
-                const float wd = d == 2 ? 65536.0f : (d == 1 ? 256.0f : 1.0f);
+            for (int l = 0; l < NL; ++l) {
+                const int idx = tid + 256 * l, e = idx % CH, cb = idx / CH;
+                wv[l] = *reinterpret_cast<const v4i*>(Wkn + (size_t)uch[e] * Np + n0 + cb * 16);
+            }
 #pragma unroll
-                for (int bm = 0; bm < 4; ++bm) {
-                    const v4i af = *reinterpret_cast<const v4i*>(lds + (d * 8 + wm * 4 + bm) * 1024 + lane * 16);
+            for (int l = 0; l < NL; ++l) {
+                const int idx = tid + 256 * l, e = idx % CH, cb = idx / CH;
 #pragma unroll
-                    for (int x = 0; x < 2; ++x) {
-                        const v4i cd = mfma(af, bf2[x], v4i{0, 0, 0, 0});
+                for (int b = 0; b < 16; ++b)
+                    WU[cb * 1024 + ((16 * (e >> 4) + b) * 16) + (e & 15)] =
+                        (int8_t)((uint32_t)wv[l][b >> 2] >> ((b & 3) * 8));
+            }
+        }
+        __syncthreads();
+        // tv += so * (C2 * 2^16 + C1 * 2^8 + C0); so is 0 on non-finite rows
 #pragma unroll
-                        for (int c = 0; c < 4; ++c) {
-                            const float so = meta[GBM + wm * 64 + bm * 16 + (lane >> 4) * 4 + c];
-                            tv[bm][x][c] = tv[bm][x][c] + (so * wd) * (float)cd[c];
-                        }
-                    }
+        for (int bm = 0; bm < TM; ++bm) {
+            float sow[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) sow[c] = meta[GBM + wm * 64 + bm * 16 + (lane >> 4) * 4 + c];
+            v4i af[3];
+#pragma unroll
+            for (int d = 0; d < 3; ++d)
+                af[d] = *reinterpret_cast<const v4i*>(D + (d * 8 + wm * 4 + bm) * 1024 + lane * 16);
+#pragma unroll
+            for (int bn = 0; bn < TN; ++bn) {
+                const v4i bf = *reinterpret_cast<const v4i*>(WU + (wn * TN + bn) * 1024 + lane * 16);
+                const v4i c2 = mfma(af[2], bf, v4i{0, 0, 0, 0});
+                const v4i c1 = mfma(af[1], bf, v4i{0, 0, 0, 0});
+                const v4i c0 = mfma(af[0], bf, v4i{0, 0, 0, 0});
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    tv[bm][bn][c] = tv[bm][bn][c] + (sow[c] * 65536.0f) * (float)c2[c];
+                    tv[bm][bn][c] = tv[bm][bn][c] + (sow[c] * 256.0f) * (float)c1[c];
+                    tv[bm][bn][c] = tv[bm][bn][c] + sow[c] * (float)c0[c];
                 }
             }
         }
-#pragma unroll
-        for (int bm = 0; bm < 4; ++bm)
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int i = m0 + wm * 64 + bm * 16 + (lane >> 4) * 4 + c;
-                if (i >= M) continue;
-#pragma unroll
-                for (int x = 0; x < 2; ++x) {
-                    const int j = n0 + wn * 128 + (sub * 2 + x) * 16 + (lane & 15);
-                    if (j >= N) continue;
-                    float v = tv[bm][x][c];
-                    if (meta[2 * GBM + wm * 64 + bm * 16 + (lane >> 4) * 4 + c] != 0.0f) {
-                        // non-finite outlier: exact sequential corr
-                        float corr = -0.0f;
-                        const int8_t* wrow = W + (size_t)j * Kp;
-                        for (int q = 0; q < t; ++q)
-                            corr = corr + oval[(size_t)i * FRQ_T + q] *
-                                              (float)wrow[min(oidx[(size_t)i * FRQ_T + q], (uint32_t)(Kp - 1))];
-                        v = v + corr;
-                    }
-                    out[(size_t)i * N + j] = scale[j] * v;
-                }
-            }
     }
+
+    // out = scale * t; rows with a non-finite outlier add the exact sequential corr
+#pragma unroll
+    for (int bm = 0; bm < TM; ++bm)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int rl = wm * 64 + bm * 16 + (lane >> 4) * 4 + c;
+            const int i = m0 + rl;
+            if (i >= M) continue;
+            const bool exact = meta[2 * GBM + rl] != 0.0f;
+#pragma unroll
+            for (int bn = 0; bn < TN; ++bn) {
+                const int j = n0 + wn * (BN / 2) + bn * 16 + (lane & 15);
+                if (j >= N) continue;
+                float v = tv[bm][bn][c];
+                if (exact) {
+                    float corr = -0.0f;
+                    const int8_t* wr = Wrow + (size_t)j * Kp;
+                    for (int q = 0; q < t; ++q)
+                        corr = corr + oval[(size_t)i * FRQ_T + q] *
+                                          (float)wr[min(oidx[(size_t)i * FRQ_T + q], (uint32_t)(Kp - 1))];
+                    v = v + corr;
+                }
+                out[(size_t)i * N + j] = scl[wn * (BN / 2) + bn * 16 + (lane & 15)] * v;
+            }
+        }
+}
+
+// (R, Kp) row-major (pitch) -> blocked, R a multiple of 16; rows >= valid are zero.
+__global__ void blockify_kernel(const int8_t* __restrict__ src, size_t valid, size_t R,
+                                size_t Kp, size_t pitch, int8_t* __restrict__ dst) {
+    const size_t cpr = Kp / 16, total = R * cpr;
+    for (size_t idx = blockIdx.x * (size_t)blockDim.x + threadIdx.x; idx < total;
+         idx += (size_t)gridDim.x * blockDim.x) {
+        const size_t row = idx / cpr, c = idx % cpr;
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (row < valid) v = *reinterpret_cast<const uint4*>(src + row * pitch + c * 16);
+        *reinterpret_cast<uint4*>(dst + blk_off(row, c * 16, R)) = v;
+    }
+}
+
+template <int BN, int NST>
+hipError_t launch_t(const Weight& w, size_t m, const int8_t* a8b, const float* sa,
+                    const uint32_t* oidx, const float* oval, float* out, int32_t* acc,
+                    hipStream_t s) {
+    const int MT = (int)((m + GBM - 1) / GBM), NT = (int)(w.np / BN);
+    const size_t lds = (size_t)NST * (GBM + BN) / 16 * 1024;
+    const int t = (int)(w.k < FRQ_T ? w.k : FRQ_T);
+    auto kern = gemm_i8_kernel<BN, NST>;
+    static bool attr_set = false;  // per process; the attribute is per function
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)lds);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    kern<<<dim3((unsigned)(MT * NT)), dim3(256), lds, s>>>(
+        a8b, w.wblk, w.wkn, w.wt, w.scale, sa, (int)m, (int)round_up(m, GBM), (int)w.n,
+        (int)w.np, (int)w.k, (int)w.kp, t, oidx, oval, out, acc, MT);
+    return hipGetLastError();
 }
 
 }  // namespace
 
-size_t gemm_union_bytes(size_t m, size_t k) {
-    (void)k;
-    const size_t tiles = (m + BM - 1) / BM, mp = tiles * BM;
-    return round_up(tiles * 4, 256) + round_up(tiles * UMAX * 4, 256) +
-           2 * round_up(mp * 4, 256) + tiles * 3 * BM * UMAX;
-}
-
-hipError_t launch_union(size_t m, size_t k, const uint32_t* oidx,
-                        const float* oval, void* ubuf, hipStream_t s) {
-    const size_t tiles = (m + BM - 1) / BM;
-    const size_t nw = (k + 31) / 32;
-    const size_t lds = 2 * nw * sizeof(uint32_t);
-    if (lds > 60 * 1024) return hipErrorInvalidValue;
-    const int t = (int)(k < FRQ_T ? k : FRQ_T);
-    union_kernel<<<dim3((unsigned)tiles), dim3(256), lds, s>>>(
-        oidx, oval, (int)m, (int)k, t, union_view(ubuf, m));
+hipError_t launch_blockify(const int8_t* src, size_t valid, size_t R, size_t kp,
+                           size_t pitch, int8_t* dst, hipStream_t s) {
+    if (!R || !kp) return hipSuccess;
+    const size_t total = R * kp / 16;
+    const size_t g = (total + 255) / 256;
+    const unsigned grid = (unsigned)(g < 8192 ? g : 8192);
+    blockify_kernel<<<dim3(grid), dim3(256), 0, s>>>(src, valid, R, kp, pitch, dst);
     return hipGetLastError();
 }
 
-hipError_t launch_gemm_i8(const Weight& w, size_t m, const int8_t* a8,
+hipError_t launch_gemm_i8(const Weight& w, size_t m, const int8_t* a8b,
                           const float* sa, const uint32_t* oidx,
-                          const float* oval, const void* ubuf, float* out,
-                          int32_t* acc, hipStream_t s) {
-    // a8 holds round_up(m, 128) rows; wt / wkn are padded to (Np, Kp) / (Kp, Np)
-    const int MT = (int)((m + GBM - 1) / GBM), NT = (int)(w.np / GBN);
-    const int t = (int)(w.k < FRQ_T ? w.k : FRQ_T);
-    gemm_i8_kernel<<<dim3((unsigned)(MT * NT)), dim3(256), 0, s>>>(
-        a8, w.wt, w.wkn, w.scale, sa, (int)m, (int)w.n, (int)w.np, (int)w.kp, t,
-        union_view(const_cast<void*>(ubuf), m), oidx, oval, out, acc, MT);
-    return hipGetLastError();
+                          const float* oval, float* out, int32_t* acc,
+                          hipStream_t s) {
+    // a8b holds round_up(m, 128) blocked rows; wblk / wkn are padded to Np
+    // (a multiple of 256) and Kp (a multiple of 128); Kp <= 20480 keeps the
+    // channel bitmap within its 640 LDS words
+    if (w.kp > 20480 || !w.wblk) return hipErrorInvalidValue;
+    const size_t tiles256 = ((m + GBM - 1) / GBM) * (w.np / 256);
+    if (tiles256 >= 512) return launch_t<256, 3>(w, m, a8b, sa, oidx, oval, out, acc, s);
+    return launch_t<128, 4>(w, m, a8b, sa, oidx, oval, out, acc, s);
 }
 
 }  // namespace frq

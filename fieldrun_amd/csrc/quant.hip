@@ -133,7 +133,7 @@ template <int BLOCK>
 __global__ __launch_bounds__(BLOCK) void quant_rows(
     const float* __restrict__ A, int K, int Kp, int t, int8_t* __restrict__ a8,
     float* __restrict__ sa_out, uint32_t* __restrict__ oidx,
-    float* __restrict__ oval, int* __restrict__ err) {
+    float* __restrict__ oval, int* __restrict__ err, int mpb) {
     __shared__ uint32_t hist[256];
     __shared__ uint32_t bc[2];
     __shared__ uint32_t vals[CAP > BLOCK ? CAP : BLOCK];
@@ -146,7 +146,10 @@ __global__ __launch_bounds__(BLOCK) void quant_rows(
 
     const int row = blockIdx.x;
     const float* a = A + (size_t)row * K;
-    int8_t* q = a8 + (size_t)row * Kp;
+    // a8 byte k of this row: row-major (pitch Kp) or blocked (R = mpb)
+    auto qa = [&](int k) -> int8_t* {
+        return mpb ? a8 + blk_off((size_t)row, (size_t)k, (size_t)mpb) : a8 + (size_t)row * Kp + k;
+    };
     const int tid = threadIdx.x;
 
     if (tid == 0) { ncand = 0; nan_flag = 0; }
@@ -171,7 +174,7 @@ __global__ __launch_bounds__(BLOCK) void quant_rows(
             // in-bounds placeholders (a8 = 0, sa = 1, outliers 0..t-1 with
             // value 0) so the kernels queued after this one read valid data.
             if (tid == 0) { atomicOr(err, 1); sa_out[row] = 1.0f; }
-            for (int k = tid; k < Kp; k += BLOCK) q[k] = 0;
+            for (int k = tid; k < Kp; k += BLOCK) *qa(k) = 0;
             for (int k = tid; k < FRQ_T; k += BLOCK) {
                 oidx[(size_t)row * FRQ_T + k] = k < t ? (uint32_t)k : 0u;
                 oval[(size_t)row * FRQ_T + k] = 0.0f;
@@ -253,7 +256,7 @@ __global__ __launch_bounds__(BLOCK) void quant_rows(
             r = (x != x) ? (int8_t)0
                          : (int8_t)(x < -127.0f ? -127 : (x > 127.0f ? 127 : (int)x));
         }
-        q[k] = r;
+        *qa(k) = r;
     }
     uint32_t* oi = oidx + (size_t)row * FRQ_T;
     float* ov = oval + (size_t)row * FRQ_T;
@@ -349,7 +352,7 @@ template <int BLOCK, int NV4>
 __global__ __launch_bounds__(BLOCK) void quant_rows_fast(
     const float* __restrict__ A, int K, int Kp, int8_t* __restrict__ a8,
     float* __restrict__ sa_out, uint32_t* __restrict__ oidx,
-    float* __restrict__ oval, int* __restrict__ err) {
+    float* __restrict__ oval, int* __restrict__ err, int mpb) {
     constexpr int NW = BLOCK / 64;
     __shared__ uint32_t wsorted[NW][64];
     __shared__ uint32_t tau_s[2];
@@ -365,7 +368,10 @@ __global__ __launch_bounds__(BLOCK) void quant_rows_fast(
     const int row = blockIdx.x, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const float* a = A + (size_t)row * K;
-    int8_t* q = a8 + (size_t)row * Kp;
+    // a8 byte k of this row: row-major (pitch Kp) or blocked (R = mpb)
+    auto qa = [&](int k) -> int8_t* {
+        return mpb ? a8 + blk_off((size_t)row, (size_t)k, (size_t)mpb) : a8 + (size_t)row * Kp + k;
+    };
     const int K4 = K >> 2;
 
     float4 v[NV4];
@@ -385,7 +391,7 @@ __global__ __launch_bounds__(BLOCK) void quant_rows_fast(
     if (tid < FRQ_T) sel_i[tid] = 0u;
     if (__syncthreads_or(nan)) {
         if (tid == 0) { atomicOr(err, 1); sa_out[row] = 1.0f; }
-        for (int k = tid; k < Kp; k += BLOCK) q[k] = 0;
+        for (int k = tid; k < Kp; k += BLOCK) *qa(k) = 0;
         if (tid < FRQ_T) {
             oidx[(size_t)row * FRQ_T + tid] = (uint32_t)tid;
             oval[(size_t)row * FRQ_T + tid] = 0.0f;
@@ -536,7 +542,7 @@ __global__ __launch_bounds__(BLOCK) void quant_rows_fast(
                 w |= rq8(qdiv_fast(v[i].w, sa, r)) << 24;
                 const uint32_t keep = ((bw & 1u) ? 0u : 0xFFu) | ((bw & 2u) ? 0u : 0xFF00u) |
                                       ((bw & 4u) ? 0u : 0xFF0000u) | ((bw & 8u) ? 0u : 0xFF000000u);
-                reinterpret_cast<uint32_t*>(q)[i4] = w & keep;
+                *reinterpret_cast<uint32_t*>(qa(4 * i4)) = w & keep;
             }
         }
     } else {
@@ -548,10 +554,10 @@ __global__ __launch_bounds__(BLOCK) void quant_rows_fast(
             const uint32_t b1 = (bw & 2u) ? 0u : q8_slow(x.y, sa);
             const uint32_t b2 = (bw & 4u) ? 0u : q8_slow(x.z, sa);
             const uint32_t b3 = (bw & 8u) ? 0u : q8_slow(x.w, sa);
-            reinterpret_cast<uint32_t*>(q)[i4] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+            *reinterpret_cast<uint32_t*>(qa(4 * i4)) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
         }
     }
-    for (int i4 = K4 + tid; i4 < Kp / 4; i4 += BLOCK) reinterpret_cast<uint32_t*>(q)[i4] = 0u;
+    for (int i4 = K4 + tid; i4 < Kp / 4; i4 += BLOCK) *reinterpret_cast<uint32_t*>(qa(4 * i4)) = 0u;
     if (tid < FRQ_T) {
         const uint32_t k = sel_i[tid];
         oidx[(size_t)row * FRQ_T + tid] = k;
@@ -564,34 +570,35 @@ __global__ __launch_bounds__(BLOCK) void quant_rows_fast(
 
 template <int NV4>
 static void launch_fast(const float* a, size_t m, size_t k, size_t kp, int8_t* a8, float* sa,
-                        uint32_t* oidx, float* oval, int* err, size_t lds, hipStream_t s) {
+                        uint32_t* oidx, float* oval, int* err, size_t lds, hipStream_t s, int mpb) {
     quant_rows_fast<256, NV4><<<dim3((unsigned)m), dim3(256), lds, s>>>(
-        a, (int)k, (int)kp, a8, sa, oidx, oval, err);
+        a, (int)k, (int)kp, a8, sa, oidx, oval, err, mpb);
 }
 
 hipError_t launch_quant(const float* a, size_t m, size_t k, size_t kp,
                         int8_t* a8, float* sa, uint32_t* oidx, float* oval,
-                        int* err, hipStream_t s) {
+                        int* err, hipStream_t s, size_t mpb) {
     if (m == 0) return hipSuccess;
+    if (mpb && (mpb < m || mpb % 16 || kp % 64)) return hipErrorInvalidValue;
     const int t = (int)(k < FRQ_T ? k : FRQ_T);
     const size_t lds = (kp + 31) / 32 * sizeof(uint32_t);
     if (lds > 32 * 1024) return hipErrorInvalidValue;
     if (k > FRQ_T && k % 4 == 0 && ((uintptr_t)a & 15) == 0 && k <= 256 * 20 * 4) {
         const size_t nv4 = (k / 4 + 255) / 256;
-        if (nv4 <= 1) launch_fast<1>(a, m, k, kp, a8, sa, oidx, oval, err, lds, s);
-        else if (nv4 <= 2) launch_fast<2>(a, m, k, kp, a8, sa, oidx, oval, err, lds, s);
-        else if (nv4 <= 4) launch_fast<4>(a, m, k, kp, a8, sa, oidx, oval, err, lds, s);
-        else if (nv4 <= 8) launch_fast<8>(a, m, k, kp, a8, sa, oidx, oval, err, lds, s);
-        else if (nv4 <= 14) launch_fast<14>(a, m, k, kp, a8, sa, oidx, oval, err, lds, s);
-        else launch_fast<20>(a, m, k, kp, a8, sa, oidx, oval, err, lds, s);
+        if (nv4 <= 1) launch_fast<1>(a, m, k, kp, a8, sa, oidx, oval, err, lds, s, (int)mpb);
+        else if (nv4 <= 2) launch_fast<2>(a, m, k, kp, a8, sa, oidx, oval, err, lds, s, (int)mpb);
+        else if (nv4 <= 4) launch_fast<4>(a, m, k, kp, a8, sa, oidx, oval, err, lds, s, (int)mpb);
+        else if (nv4 <= 8) launch_fast<8>(a, m, k, kp, a8, sa, oidx, oval, err, lds, s, (int)mpb);
+        else if (nv4 <= 14) launch_fast<14>(a, m, k, kp, a8, sa, oidx, oval, err, lds, s, (int)mpb);
+        else launch_fast<20>(a, m, k, kp, a8, sa, oidx, oval, err, lds, s, (int)mpb);
         return hipGetLastError();
     }
     if (m < 64)
         quant_rows<1024><<<dim3((unsigned)m), dim3(1024), lds, s>>>(
-            a, (int)k, (int)kp, t, a8, sa, oidx, oval, err);
+            a, (int)k, (int)kp, t, a8, sa, oidx, oval, err, (int)mpb);
     else
         quant_rows<256><<<dim3((unsigned)m), dim3(256), lds, s>>>(
-            a, (int)k, (int)kp, t, a8, sa, oidx, oval, err);
+            a, (int)k, (int)kp, t, a8, sa, oidx, oval, err, (int)mpb);
     return hipGetLastError();
 }
 

@@ -182,3 +182,27 @@ def test_i4_reference_kat_through_gpu(ctx):
     """i4_q4a_dot_matches_manual (src/bundle.rs:1306-1314): [0xE1,0xF3] . 1s = 1.0."""
     w = ctx.upload_i4(np.array([[0xE1, 0xF3]], np.uint8), np.array([[1.0]], np.float16), 4, 4)
     assert w.mm(np.ones((1, 4), np.float32))[0, 0] == 1.0
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 896, 4864), (3, 4096, 300), (40, 896, 640), (300, 4864, 896)])
+def test_i8_device_entry_points_match_host(ctx, m, k, n):
+    """frq_quant_i8_dev + frq_mm_i8_q_dev (device pointers, row-major a8 of
+    pitch frq_quant_pitch(K)) give the same bits as frq_mm_i8_debug."""
+    import fieldrun_amd as fa
+    from fieldrun_amd import hip
+    a, wt, scale = case(m, k, n, 500 + m + k)
+    w = ctx.upload_i8(wt, scale)
+    out_h, _, a8_h, sa_h, oi_h, ov_h = w.mm_debug(a)
+    kp = fa.quant_pitch(k)
+    da = hip.DeviceArray.from_numpy(a)
+    a8 = hip.DeviceArray((m, kp), np.int8)
+    sa = hip.DeviceArray((m,), np.float32)
+    oi = hip.DeviceArray((m, 32), np.uint32)
+    ov = hip.DeviceArray((m, 32), np.float32)
+    out = hip.DeviceArray((m, n), np.float32)
+    ctx.quant_dev(da.ptr, m, k, a8.ptr, sa.ptr, oi.ptr, ov.ptr)
+    w.mm_q_dev(a8.ptr, sa.ptr, oi.ptr, ov.ptr, m, out.ptr)
+    ctx.sync()
+    assert np.array_equal(a8.numpy()[:, :k], a8_h)
+    assert np.array_equal(sa.numpy(), sa_h)
+    assert np.array_equal(out.numpy().view(np.uint32), out_h.view(np.uint32))
