@@ -351,9 +351,9 @@ frq_w* frq_upload_i4(frq_ctx* c, const uint8_t* packed,
     if (e == hipSuccess && n * ng)
         e = hipMemcpyAsync(w.s4raw, scale_f16, n * ng * 2, hipMemcpyHostToDevice, c->stream);
     if (e == hipSuccess && g == 32 && k % 32 == 0 && k > 0 && n > 0) {
-        const size_t nblk = (n + 63) / 64;
-        e = hipMalloc(&w.q4, nblk * 64 * rb);
-        if (e == hipSuccess) e = hipMalloc(&w.s4, nblk * 64 * ng * 2);
+        const size_t bytes = i4_blocked_bytes(n, k);  // scales: 1/8 of it
+        e = hipMalloc(&w.q4, bytes);
+        if (e == hipSuccess) e = hipMalloc(&w.s4, bytes / 8);
         if (e == hipSuccess) e = launch_i4_block(w.q4raw, w.s4raw, n, k, w.q4, w.s4, c->stream);
         if (e == hipSuccess) w.i4_blocked = 1;
     }

@@ -6,11 +6,13 @@
 //                wkn  (Kp, Np) i8 row-major: the bundle's (in, out) layout,
 //                     read by the GEMM's outlier correction.
 //                scale (Np) f32.
-//   int4 weight  blk  64-row blocks: for block b, group gi, row r: the 16
-//                     bytes (32 nibbles) of row 64b+r, group gi, at
-//                     ((b*ng + gi)*64 + r)*16  (g == 32, K % 32 == 0), or
-//                     the bundle's own (N, ceil(K/2)) rows otherwise.
-//                scale (N, ng) f16 in the same blocked order / as stored.
+//   int4 weight  q4   (g == 32, K % 32 == 0) the MFMA layout: for 16-row
+//                     block rb, group quad g4 and lane l = 16q + r, the 4
+//                     bytes (k = 8q..8q+7) of row 16rb + r in each of the 4
+//                     groups, 16 bytes at ((rb*ng4 + g4)*64 + l)*16; s4 the
+//                     f16 scales (rb, g4, r, 4 groups).
+//                q4raw/s4raw the bundle's (N, ceil(K/2)) rows and (N, ng)
+//                     f16 scales (generic shapes and the exact fallback).
 //                wblk (Np, Kp) i8 in the blocked MFMA-operand layout
 //                     (blk_off below), read by the GEMM's main loop.
 //   activations  a8   (Mp, Kp) i8 per call (workspace): row-major for the
@@ -103,11 +105,11 @@ struct Weight {
     int8_t* wkn = nullptr;   // int8 (Kp, Np): the bundle's (in, out) layout
     int8_t* wblk = nullptr;  // int8 (Np, Kp) blocked (blk_off): the GEMM operand
     float* scale = nullptr;  // int8 scale (Np)
-    uint8_t* q4 = nullptr;   // int4 blocked (64-row blocks), when i4_blocked
-    uint16_t* s4 = nullptr;  // int4 f16 scales, blocked
+    uint8_t* q4 = nullptr;   // int4 MFMA layout, when i4_blocked
+    uint16_t* s4 = nullptr;  // int4 f16 scales, MFMA layout
     uint8_t* q4raw = nullptr;   // int4 packed (N, ceil(K/2)) as stored
     uint16_t* s4raw = nullptr;  // int4 f16 scales (N, ceil(K/g)) as stored
-    int i4_blocked = 0;      // 1 when the blocked g=32 layout is used
+    int i4_blocked = 0;      // 1 when the MFMA layout (g == 32) is built
 };
 
 struct MoeBank {
@@ -147,7 +149,8 @@ hipError_t launch_gemm_i8(const Weight& w, size_t m, const int8_t* a8b,
 hipError_t launch_i4(const Weight& w, size_t m, const float* a, float* out,
                      float* wsf, unsigned* tickets, hipStream_t s);
 size_t i4_ws_floats(const Weight& w, size_t m);
-// int4 (N, K/2) -> 64-row blocked layout (g == 32, K % 32 == 0).
+// int4 (N, K/2) -> the MFMA layout (g == 32, K % 32 == 0); bytes of q4.
+size_t i4_blocked_bytes(size_t n, size_t k);
 hipError_t launch_i4_block(const uint8_t* raw, const uint16_t* sraw, size_t n,
                            size_t k, uint8_t* blk, uint16_t* sblk,
                            hipStream_t s);

@@ -9,18 +9,29 @@
 //    oracle's stand-in for matrixmultiply's sgemm is a sequential-k FMA chain
 //    per output, which the batched kernel below reproduces.
 //
-// Decode (M == 1, g == 32, K % 32 == 0) uses the blocked layout built at
-// upload: for each 64-row block and group, the 64 rows' 16-byte groups are
-// contiguous, so a wave (one row per lane) reads 1 KB per group with one
-// coalesced 128-bit load per lane, and the group's 32 activations are the
-// same for every lane (scalar loads into SGPRs).  To fill the chip when N is
-// small the groups are split into S contiguous segments, one wave each; the
-// per-segment folds are combined in segment order by a second tiny kernel.
-// Within a group the arithmetic is i4_dot_avx2's; the fold over groups is
-// re-associated (the 4 waves of a block take interleaved groups, combined in
-// wave order, and S > 1 segments), which stays within 1e-5 of sum |a*w|.
-// Shapes outside the blocked layout run i4_gemv_generic, bit-identical to
-// i4_dot_avx2.
+// Blocked shapes (g == 32, K % 32 == 0, 1 <= M <= 16) run on the int8
+// MFMA.  At upload the nibbles are re-laid out so that the B operand of
+// v_mfma_i32_16x16x32_i8 (16 weight rows x 32 k = one group) for four
+// consecutive groups is one 16-byte load per lane and a wave load is 1 KB of
+// contiguous memory; in registers each packed dword (8 nibbles) becomes two
+// dwords of sign-extended int8 with 8 VALU operations.  The f32 activations
+// of each (token, group) are written as X = round(a / s), s = max|a| /
+// (127 * 2^16), |X| <= 127 * 2^16, split into three int8 digits
+// X = d2*2^16 + d1*2^8 + d0; token m's digits are A rows 4m, 4m+1, 4m+2, so
+// one MFMA gives the exact integer group dots of 4 tokens, and
+//   gsum = s * (C2 * 2^16 + C1 * 2^8 + C0),   out += scale[j,g] * gsum.
+// The 24-bit fixed point per group keeps the result within ~1e-7 of
+// max|a| * sum|w| of the group (the reference's own sums differ between its
+// M == 1 and M > 1 arms by more); a (token, group) with a non-finite or
+// extreme activation takes the group sum in the reference arm's own order
+// instead (i4_dot_avx2 for M == 1, the dequantised a * (s4 * scale) chain
+// for M > 1).  The digits are written once per call by a small kernel
+// (L2-resident, read by every row block); K is split across the waves of
+// one workgroup and the parts are added in order through LDS: a split across
+// workgroups would need device-scope fences, which on this part write back
+// and invalidate the whole L2.
+// Other shapes run i4_gemv_generic (M == 1, bit-identical to i4_dot_avx2)
+// or i4_gemm_rows (M > 1).
 #include "frq_internal.h"
 
 namespace frq {
@@ -44,45 +55,6 @@ __device__ __forceinline__ float group_avx2(const uint4 w, const float* __restri
             l[q] = __builtin_fmaf(s4f(ws[c], q), a[8 * c + q], l[q]);
     const float q0 = l[0] + l[4], q1 = l[1] + l[5], q2 = l[2] + l[6], q3 = l[3] + l[7];
     return (q0 + q2) + (q1 + q3);
-}
-
-// One workgroup = one 64-row block x one segment of its groups.  Wave w of
-// the workgroup takes the segment's groups w, w+4, ...; lane = row.  The
-// four wave sums are added in wave order; with S > 1 segments the partials
-// go to the workspace and i4_fold adds them in segment order.
-__global__ __launch_bounds__(256) void i4_gemv_blocked(
-    const uint8_t* __restrict__ blk, const uint16_t* __restrict__ sblk,
-    const float* __restrict__ a, int N, int ng, int S,
-    float* __restrict__ part, float* __restrict__ out) {
-    __shared__ float wsum[4][64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int b = blockIdx.x / S, seg = blockIdx.x % S;
-    const int g0 = (int)((long)ng * seg / S), g1 = (int)((long)ng * (seg + 1) / S);
-    const uint4* wp = reinterpret_cast<const uint4*>(blk) + ((size_t)b * ng) * 64 + lane;
-    const uint16_t* sp = sblk + ((size_t)b * ng) * 64 + lane;
-    float sum = 0.0f;
-    for (int gi = g0 + wave; gi < g1; gi += 4) {
-        const uint4 w = ntload16u(wp + (size_t)gi * 64);
-        const float sc = h2f(sp[(size_t)gi * 64]);
-        sum = sum + sc * group_avx2(w, a + 32 * gi);
-    }
-    wsum[wave][lane] = sum;
-    __syncthreads();
-    const int row = b * 64 + threadIdx.x;
-    if (threadIdx.x < 64 && row < N) {
-        const float p = ((wsum[0][lane] + wsum[1][lane]) + wsum[2][lane]) + wsum[3][lane];
-        if (S == 1) out[row] = p;
-        else part[(size_t)seg * N + row] = p;
-    }
-}
-
-__global__ void i4_fold(const float* __restrict__ part, int N, int S,
-                        float* __restrict__ out) {
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= N) return;
-    float s = part[j];
-    for (int q = 1; q < S; ++q) s = s + part[(size_t)q * N + j];
-    out[j] = s;
 }
 
 // Generic M == 1 (any K, g): one thread per output row, i4_dot_avx2 order.
@@ -149,66 +121,572 @@ __global__ __launch_bounds__(256) void i4_gemm_rows(
         if (m0 + m < M) out[(size_t)(m0 + m) * N + j] = acc[m];
 }
 
-// Re-layout (N, K/2) packed + (N, ng) scales into 64-row blocks.
-__global__ void i4_block_kernel(const uint8_t* __restrict__ raw,
-                                const uint16_t* __restrict__ sraw, int N,
-                                int K, uint8_t* __restrict__ blk,
-                                uint16_t* __restrict__ sblk) {
-    const int ng = K / 32, nblk = (N + 63) / 64;
-    const size_t total = (size_t)nblk * ng * 64;
-    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
-         i += (size_t)gridDim.x * blockDim.x) {
-        const int r = (int)(i % 64);
-        const size_t bg = i / 64;
-        const int gi = (int)(bg % ng), b = (int)(bg / ng);
-        const int row = b * 64 + r;
-        uint4 v = make_uint4(0, 0, 0, 0);
-        uint16_t s = 0;
-        if (row < N) {
-            v = *reinterpret_cast<const uint4*>(raw + (size_t)row * (K / 2) + gi * 16);
-            s = sraw[(size_t)row * ng + gi];
+constexpr float XMAX4 = 8323072.0f;  // 127 * 2^16
+
+// Sign-extend the 8 nibbles of w (k = 0..7, low nibble first) into int8:
+// lo = bytes for k = 0,2,4,6, hi = k = 1,3,5,7.  Per byte, with y = x ^ 8:
+// ((y + 0x78) ^ 0x80) == x as a signed nibble, and y + 0x78 <= 0x87 never
+// carries into the next byte.
+__device__ __forceinline__ void nib_unpack(uint32_t w, uint32_t& lo, uint32_t& hi) {
+    const uint32_t y = w ^ 0x88888888u;
+    lo = ((y & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
+    hi = (((y >> 4) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
+}
+
+// Activation digits, four threads (chunks q = 0..3 of 8 k) per (token m <
+// 4*MT4, group g < 4*ng4).  The A operand of token group tg = m/4 and group
+// g = 4*g4 + gi is, for lane l, the 8 bytes at ((tg*ng4 + g4)*64 + l)*32 +
+// 8*gi (a lane's 4 groups of a quad are one 32-byte run); lane
+// 16q + 4(m%4) + d holds digit d of token m at k = 8q + {0,2,4,6,1,3,5,7}
+// (the nibble order of the unpacked weights), lane 16q + 4(m%4) + 3 is zero.
+// so[(m*ng4 + g4)*4 + gi] = s, -1 for a group that takes the exact path, 0
+// for padding tokens and groups.
+__global__ void i4_digits_kernel(const float* __restrict__ a, int M, int Mp, int K, int ng4,
+                                 uint8_t* __restrict__ adig, float* __restrict__ so_out) {
+    const int ng = K / 32, ngp = 4 * ng4;
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    const int mg = idx >> 2, q = idx & 3;  // the 4 threads of (m, g) are adjacent lanes
+    const bool act = mg < Mp * ngp;
+    const int m = act ? mg / ngp : 0, g = act ? mg % ngp : 0;
+    const bool real = act && m < M && g < ng;
+    float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (real) {
+        const float4* ap = reinterpret_cast<const float4*>(a + (size_t)m * K + (size_t)g * 32 + 8 * q);
+        const float4 x0 = ap[0], x1 = ap[1];
+        v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
+        v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+    }
+    float mx = 0.0f;
+    int nf = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        nf |= !(fabsf(v[k]) <= 3.0e38f);
+        mx = fmaxf(mx, fabsf(v[k]));
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+    nf |= __shfl_xor(nf, 1, 64);
+    nf |= __shfl_xor(nf, 2, 64);
+    if (!act) return;
+    // |group sum| <= 32 * 8 * mx stays finite for s <= 1e28
+    const float s = mx > 0.0f ? mx / XMAX4 : 1.0f;
+    const bool ok = real && !nf && s >= 1.0e-30f && s <= 1.0e28f;
+    uint32_t dw[3][2] = {{0, 0}, {0, 0}, {0, 0}};
+    if (ok) {
+        const float r = 1.0f / s;  // any rounding of a / s keeps |a - s X| <= ~s/2
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            float xf = rintf(v[j] * r);
+            xf = fminf(fmaxf(xf, -XMAX4), XMAX4);
+            const int X = (int)xf;
+            const int d0 = (int)(int8_t)(X & 0xFF);
+            const int X1 = (X - d0) >> 8;
+            const int d1 = (int)(int8_t)(X1 & 0xFF);
+            const int d2 = (X1 - d1) >> 8;
+            const int p = (j & 1) ? 4 + (j >> 1) : (j >> 1);  // byte within the lane's 8
+            const int wsel = p >> 2, sh = 8 * (p & 3);
+            dw[0][wsel] |= (uint32_t)(d2 & 0xFF) << sh;
+            dw[1][wsel] |= (uint32_t)(d1 & 0xFF) << sh;
+            dw[2][wsel] |= (uint32_t)(d0 & 0xFF) << sh;
         }
-        reinterpret_cast<uint4*>(blk)[i] = v;
-        sblk[i] = s;
+    }
+    const int g4 = g >> 2, gi = g & 3;
+    uint8_t* blk = adig + ((size_t)(m >> 2) * ng4 + g4) * 64 * 32 + 8 * gi;
+    const int l0 = 16 * q + 4 * (m & 3);
+#pragma unroll
+    for (int d = 0; d < 3; ++d)
+        *reinterpret_cast<uint2*>(blk + (l0 + d) * 32) = make_uint2(dw[d][0], dw[d][1]);
+    *reinterpret_cast<uint2*>(blk + (l0 + 3) * 32) = make_uint2(0u, 0u);
+    if (q == 0) so_out[((size_t)m * ng4 + g4) * 4 + gi] = real ? (ok ? s : -1.0f) : 0.0f;
+}
+
+// acc plus one group of a (token, weight row) in the reference arm's own
+// order, for activations the digits cannot carry (non-finite or extreme):
+// M == 1: scale * i4_dot_avx2 group sum; M > 1: a * (s4 * scale), k ascending.
+template <bool INL = false>
+__device__ __attribute__((noinline)) float exact_group(float acc, const uint8_t* wrow, const float* ag,
+                                                       float sc, bool m1);
+template <>
+__device__ __attribute__((noinline)) float exact_group<false>(float acc, const uint8_t* wrow, const float* ag,
+                                                              float sc, bool m1);
+__device__ __forceinline__ float exact_group_body(float acc, const uint8_t* wrow, const float* ag,
+                                                  float sc, bool m1) {
+    const uint4 wr = *reinterpret_cast<const uint4*>(wrow);
+    if (m1) return acc + sc * group_avx2(wr, ag);
+    const uint32_t ws[4] = {wr.x, wr.y, wr.z, wr.w};
+    float e = 0.0f;
+    for (int k = 0; k < 32; ++k) e = __builtin_fmaf(ag[k], s4f(ws[k >> 3], k & 7) * sc, e);
+    return acc + e;
+}
+template <>
+__device__ __attribute__((noinline)) float exact_group<false>(float acc, const uint8_t* wrow, const float* ag,
+                                                              float sc, bool m1) {
+    return exact_group_body(acc, wrow, ag, sc, m1);
+}
+
+// Dot of one group for the MT4 token groups of a wave, acc += scale * gsum.
+template <int MT4, bool INL = false>
+__device__ __forceinline__ void group_mfma(float (&acc)[MT4], uint32_t wd, float sc, const long* aop,
+                                           const float* so, int g, int row, int N, int K, int M,
+                                           const uint8_t* __restrict__ raw, const float* __restrict__ a,
+                                           int ml) {
+    uint32_t lo, hi;
+    nib_unpack(wd, lo, hi);
+    const long bop = (long)(((unsigned long long)hi << 32) | lo);
+#pragma unroll
+    for (int t = 0; t < MT4; ++t) {
+        const v4i cr = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop[t], bop, v4i{0, 0, 0, 0}, 0, 0, 0);
+        if (__builtin_amdgcn_ballot_w64(so[t] < 0.0f)) {  // wave-uniform, rare
+            if (so[t] < 0.0f && row < N) {
+                const uint8_t* wr = raw + (size_t)row * (K / 2) + (size_t)g * 16;
+                const float* ag = a + (size_t)(4 * t + ml) * K + (size_t)g * 32;
+                if constexpr (INL) acc[t] = exact_group_body(acc[t], wr, ag, sc, M == 1);
+                else acc[t] = exact_group<false>(acc[t], wr, ag, sc, M == 1);
+                continue;
+            }
+        }
+        const float gs = so[t] * ((float)cr[0] * 65536.0f + ((float)cr[1] * 256.0f + (float)cr[2]));
+        acc[t] = acc[t] + sc * gs;
     }
 }
 
-int pick_segments(size_t n, size_t ng) {
-    const size_t nblk = (n + 63) / 64;
-    size_t s = (512 + nblk - 1) / nblk;  // aim for >= 512 workgroups (2048 waves)
-    if (s > 8) s = 8;                    // the fold reads S partials per row
-    if (s > ng / 4) s = ng / 4;          // >= 4 groups (one per wave) per segment
-    if (s < 1) s = 1;
-    return (int)s;
+// int4 x f32 on the int8 MFMA.  A workgroup of KS waves covers 16-row
+// blocks rb = blockIdx.x, + gridDim.x, ...; wave ks owns the ks-th part (at
+// most GQ group quads) of K.  It loads that part's activation operands once
+// (only the lanes whose A rows carry a token's digit; with M == 1 the digit
+// scales are wave-uniform) and keeps them in registers; per block it issues
+// all of the part's weight loads at once.  The KS partial sums of a block are
+// added in part order through LDS.  MT4 = token groups of 4 (M <= 4 * MT4).
+template <int MT4, int KS, int GQ, bool M1>
+__global__ __launch_bounds__(64 * KS) void i4_mfma_kernel(
+    const uint8_t* __restrict__ q4m, const uint16_t* __restrict__ s4m,
+    const uint8_t* __restrict__ raw, const float* __restrict__ a,
+    const uint8_t* __restrict__ adig, const float* __restrict__ sog, int M, int K,
+    int N, int ng4, float* __restrict__ out) {
+    __shared__ float red[2][KS][MT4][64];
+    const int lane = threadIdx.x & 63;
+    const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nrb = (N + 15) / 16, ng = K / 32;
+    const int q0 = (int)((long)ng4 * ks / KS), q1 = (int)((long)ng4 * (ks + 1) / KS);
+    const int col = lane & 15, ml = M1 ? 0 : lane >> 4;
+    // resident activation operands and digit scales of this part
+    long ao[GQ][4][MT4];
+    float sv[GQ][4][MT4];
+#pragma unroll
+    for (int i = 0; i < GQ; ++i)
+#pragma unroll
+        for (int t = 0; t < MT4; ++t) {
+            const int mt = M1 ? 1 : min(M - 4 * t, 4);  // tokens in this token group
+            const bool need = ((col >> 2) < mt) && ((col & 3) < 3) && q0 + i < q1;
+            uint4 h0 = make_uint4(0, 0, 0, 0), h1 = make_uint4(0, 0, 0, 0);
+            if (need) {
+                const uint4* ap = reinterpret_cast<const uint4*>(adig + (((size_t)t * ng4 + q0 + i) * 64 + lane) * 32);
+                h0 = ap[0];
+                h1 = ap[1];
+            }
+            ao[i][0][t] = (long)(((unsigned long long)h0.y << 32) | h0.x);
+            ao[i][1][t] = (long)(((unsigned long long)h0.w << 32) | h0.z);
+            ao[i][2][t] = (long)(((unsigned long long)h1.y << 32) | h1.x);
+            ao[i][3][t] = (long)(((unsigned long long)h1.w << 32) | h1.z);
+            float4 s4v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (q0 + i < q1 && (M1 || 4 * t + ml < M))
+                s4v = *reinterpret_cast<const float4*>(sog + ((size_t)(4 * t + ml) * ng4 + q0 + i) * 4);
+            sv[i][0][t] = s4v.x; sv[i][1][t] = s4v.y; sv[i][2][t] = s4v.z; sv[i][3][t] = s4v.w;
+        }
+
+    int buf = 0;
+    for (int rb = blockIdx.x; rb < nrb; rb += gridDim.x) {  // workgroup-uniform
+        const int row = 16 * rb + col;
+        uint4 wq[GQ];
+        uint2 wsc[GQ];
+#pragma unroll
+        for (int i = 0; i < GQ; ++i)
+            if (q0 + i < q1) {
+                const size_t blk = (size_t)rb * ng4 + q0 + i;
+                wq[i] = *reinterpret_cast<const uint4*>(q4m + (blk * 64 + lane) * 16);
+                wsc[i] = *reinterpret_cast<const uint2*>(s4m + (blk * 16 + col) * 4);
+            }
+        float acc[MT4];
+#pragma unroll
+        for (int t = 0; t < MT4; ++t) acc[t] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < GQ; ++i) {
+            if (q0 + i >= q1) continue;  // no break, so the loop unrolls
+            const uint32_t wd[4] = {wq[i].x, wq[i].y, wq[i].z, wq[i].w};
+            const uint32_t sd[2] = {wsc[i].x, wsc[i].y};
+#pragma unroll
+            for (int gi = 0; gi < 4; ++gi) {
+                const int g = 4 * (q0 + i) + gi;
+                if (g >= ng) continue;  // zero padding groups of the last quad
+                const float sc = h2f((uint16_t)(sd[gi >> 1] >> (16 * (gi & 1))));
+                group_mfma<MT4>(acc, wd[gi], sc, ao[i][gi], sv[i][gi], g, row, N, K, M, raw, a, ml);
+            }
+        }
+        if (KS == 1) {
+#pragma unroll
+            for (int t = 0; t < MT4; ++t) {
+                const int m = 4 * t + (lane >> 4);
+                if (m < M && row < N) out[(size_t)m * N + row] = acc[t];
+            }
+            continue;
+        }
+        // parts of this block through LDS; the two buffers alternate between
+        // consecutive blocks, so one barrier per block suffices
+#pragma unroll
+        for (int t = 0; t < MT4; ++t) red[buf][ks][t][lane] = acc[t];
+        __syncthreads();
+        if (ks == 0) {
+#pragma unroll
+            for (int t = 0; t < MT4; ++t) {
+                float v = red[buf][0][t][lane];
+#pragma unroll
+                for (int q = 1; q < KS; ++q) v = v + red[buf][q][t][lane];
+                const int m = 4 * t + (lane >> 4);
+                if (m < M && row < N) out[(size_t)m * N + row] = v;
+            }
+        }
+        buf ^= 1;
+    }
+}
+
+// Fused M <= 4 path (one launch, one 16-row block per workgroup).  The
+// workgroup first writes the activation digits of all K into LDS in compact
+// form: for group g < 4*ng4 (groups past K are zero), chunk q (k = 8q..8q+7),
+// token m and digit d, the 8 bytes at (((g*4 + q)*M + m)*3 + d)*8, plus
+// so[g*M + m] (-1: a group the digits cannot carry), and one zero slot.
+// Then its KS waves, wave ks owning the ks-th part (at most GQ quads) of K,
+// issue all of their part's weight loads at once (before the digit pass, so
+// the latencies overlap); the A operand of a group is an 8-byte LDS read (the
+// zero slot for lanes whose A row 4m + d has m >= M or d == 3).  The KS
+// partial sums are added in part order through LDS.
+template <int M, int KS, int GQ>
+__global__ __launch_bounds__(64 * KS) void i4_fused_kernel(
+    const uint8_t* __restrict__ q4m, const uint16_t* __restrict__ s4m,
+    const uint8_t* __restrict__ raw, const float* __restrict__ a, int K, int N,
+    int ng4, float* __restrict__ out) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int ng = K / 32, ngp = 4 * ng4;
+    uint2* adl = reinterpret_cast<uint2*>(smem);  // [ngp*4*M*3 + 1 zero slot]
+    const int zslot = ngp * 4 * M * 3;
+    float* sol = reinterpret_cast<float*>(smem + (size_t)(zslot + 2) * 8);  // [ngp*M]
+    float* red = sol + ((ngp * M + 3) & ~3);                                // [KS][64]
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int ks = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+    // the weight loads of this wave's part do not depend on the digits: issue
+    // them first, so their latency overlaps the digit pass
+    const int rb = blockIdx.x;
+    const int q0 = (int)((long)ng4 * ks / KS), q1 = (int)((long)ng4 * (ks + 1) / KS);
+    const int nq = q1 - q0;  // <= GQ
+    const int col = lane & 15, ml = lane >> 4;
+    uint4 wq[GQ];
+    uint2 wsc[GQ];
+#pragma unroll
+    for (int i = 0; i < GQ; ++i)
+        if (i < nq) {
+            const size_t blk = (size_t)rb * ng4 + q0 + i;
+            wq[i] = *reinterpret_cast<const uint4*>(q4m + (blk * 64 + lane) * 16);
+            wsc[i] = *reinterpret_cast<const uint2*>(s4m + (blk * 16 + col) * 4);
+        }
+
+    // 1. digits: four adjacent threads per (m, g), one chunk q each; a
+    //    thread's items of a pass are loaded together, then digitised
+    constexpr int IPT = 2;
+    const int nitems = 4 * M * ngp;
+    if (tid == 0) adl[zslot] = make_uint2(0u, 0u);
+    for (int base = 0; base < nitems; base += 64 * KS * IPT) {  // uniform trip count
+        float v[IPT][8];
+#pragma unroll
+        for (int it = 0; it < IPT; ++it) {
+            const int idx = base + it * 64 * KS + tid;
+            const int mg = idx >> 2, q = idx & 3;
+            const int m = mg / ngp, g = mg % ngp;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[it][k] = 0.0f;
+            if (mg < M * ngp && g < ng) {
+                const float4* ap = reinterpret_cast<const float4*>(a + (size_t)m * K + (size_t)g * 32 + 8 * q);
+                const float4 x0 = ap[0], x1 = ap[1];
+                v[it][0] = x0.x; v[it][1] = x0.y; v[it][2] = x0.z; v[it][3] = x0.w;
+                v[it][4] = x1.x; v[it][5] = x1.y; v[it][6] = x1.z; v[it][7] = x1.w;
+            }
+        }
+#pragma unroll
+        for (int it = 0; it < IPT; ++it) {
+            const int idx = base + it * 64 * KS + tid;
+            const int mg = idx >> 2, q = idx & 3;
+            const bool act = mg < M * ngp;
+            const int m = act ? mg / ngp : 0, g = act ? mg % ngp : 0;
+            float mx = 0.0f;
+            int nf = 0;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                nf |= !(fabsf(v[it][k]) <= 3.0e38f);
+                mx = fmaxf(mx, fabsf(v[it][k]));
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+            nf |= __shfl_xor(nf, 1, 64);
+            nf |= __shfl_xor(nf, 2, 64);
+            if (!act) continue;
+            // |group sum| <= 32 * 8 * mx stays finite for s <= 1e28
+            const float sg = mx > 0.0f ? mx / XMAX4 : 1.0f;
+            const bool ok = !nf && sg >= 1.0e-30f && sg <= 1.0e28f;
+            uint32_t dw[3][2] = {{0, 0}, {0, 0}, {0, 0}};
+            if (ok) {
+                const float r = 1.0f / sg;  // any rounding of a / s keeps |a - s X| <= ~s/2
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    float xf = rintf(v[it][j] * r);
+                    xf = fminf(fmaxf(xf, -XMAX4), XMAX4);
+                    const int X = (int)xf;
+                    const int d0 = (int)(int8_t)(X & 0xFF);
+                    const int X1 = (X - d0) >> 8;
+                    const int d1 = (int)(int8_t)(X1 & 0xFF);
+                    const int d2 = (X1 - d1) >> 8;
+                    const int p = (j & 1) ? 4 + (j >> 1) : (j >> 1);
+                    const int wsel = p >> 2, sh = 8 * (p & 3);
+                    dw[0][wsel] |= (uint32_t)(d2 & 0xFF) << sh;
+                    dw[1][wsel] |= (uint32_t)(d1 & 0xFF) << sh;
+                    dw[2][wsel] |= (uint32_t)(d0 & 0xFF) << sh;
+                }
+            }
+#pragma unroll
+            for (int d = 0; d < 3; ++d) adl[((g * 4 + q) * M + m) * 3 + d] = make_uint2(dw[d][0], dw[d][1]);
+            if (q == 0) sol[g * M + m] = g < ng ? (ok ? sg : -1.0f) : 0.0f;
+        }
+    }
+    __syncthreads();
+
+    // 2. this workgroup's 16-row block, the groups of the wave's part in order
+    const int am = col >> 2, ad = col & 3;  // A row of this lane: token am, digit ad
+    const int row = 16 * rb + col;
+    const int mtok = ml < M ? ml : 0;       // token of this lane's result (lanes >= M: junk)
+    // LDS slot of the lane's A operand for group g: abase + g * 12M (the zero
+    // slot, stride 0, for lanes without a digit row)
+    const bool arow = am < M && ad < 3;
+    const int abase = arow ? (ml * M + am) * 3 + ad : zslot;
+    const int astep = arow ? 12 * M : 0;
+    const int g0 = 4 * q0;
+    // any group of the part that the digits cannot carry?  (wave-uniform)
+    int xg = 0;
+    for (int i = lane; i < 4 * nq * M; i += 64) xg |= sol[g0 * M + i] < 0.0f;
+    float acc = 0.0f;
+    if (__builtin_amdgcn_ballot_w64(xg) == 0) {
+        // fast path: straight-line digit MFMAs, four groups per weight quad
+#pragma unroll
+        for (int i = 0; i < GQ; ++i) {
+            if (i >= nq) continue;  // wave-uniform; no break, so the loop unrolls
+            const int gq = 4 * (q0 + i);
+            const uint32_t wd[4] = {wq[i].x, wq[i].y, wq[i].z, wq[i].w};
+            v4i cr[4];
+#pragma unroll
+            for (int gi = 0; gi < 4; ++gi) {
+                uint32_t lo, hi;
+                nib_unpack(wd[gi], lo, hi);
+                const long bop = (long)(((unsigned long long)hi << 32) | lo);
+                const uint2 av = adl[abase + (gq + gi) * astep];
+                const long aop = (long)(((unsigned long long)av.y << 32) | av.x);
+                cr[gi] = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, v4i{0, 0, 0, 0}, 0, 0, 0);
+            }
+            const uint32_t sd[2] = {wsc[i].x, wsc[i].y};
+#pragma unroll
+            for (int gi = 0; gi < 4; ++gi) {
+                const float sgi = sol[(gq + gi) * M + mtok];
+                const float sc = h2f((uint16_t)(sd[gi >> 1] >> (16 * (gi & 1))));
+                const float gs = sgi * ((float)cr[gi][0] * 65536.0f + ((float)cr[gi][1] * 256.0f + (float)cr[gi][2]));
+                acc = acc + sc * gs;
+            }
+        }
+    } else {
+        // some group needs the exact path: a compact loop over the part, the
+        // weights read again from global memory
+        for (int g = g0; g < min(4 * q1, ng); ++g) {
+            const size_t blk = (size_t)rb * ng4 + (g >> 2);
+            const uint32_t wd = *reinterpret_cast<const uint32_t*>(q4m + (blk * 64 + lane) * 16 + 4 * (g & 3));
+            const uint16_t sh = s4m[(blk * 16 + col) * 4 + (g & 3)];
+            const uint2 av = adl[abase + g * astep];
+            const long aop[1] = {(long)(((unsigned long long)av.y << 32) | av.x)};
+            const float so[1] = {sol[g * M + mtok]};
+            float a1[1] = {acc};
+            group_mfma<1, true>(a1, wd, h2f(sh), aop, so, g, row, N, K, M, raw, a, ml);
+            acc = a1[0];
+        }
+    }
+    if (KS == 1) {
+        if (ml < M && row < N) out[(size_t)ml * N + row] = acc;
+        return;
+    }
+    red[ks * 64 + lane] = acc;
+    __syncthreads();
+    if (ks == 0) {
+        float v = red[lane];
+#pragma unroll
+        for (int q = 1; q < KS; ++q) v = v + red[q * 64 + lane];
+        if (ml < M && row < N) out[(size_t)ml * N + row] = v;
+    }
+}
+
+// LDS bytes of the fused path (compact digits + zero slot + scales + reduction).
+size_t fused_lds(size_t m, size_t k, int ks) {
+    const size_t ngp = 4 * ((k / 32 + 3) / 4);
+    return (ngp * 4 * m * 3 + 2) * 8 + ((ngp * m + 3) & ~(size_t)3) * 4 + (size_t)ks * 64 * 4;
+}
+
+// (N, K/2) packed nibbles + (N, ng) f16 scales -> the MFMA layout: for row
+// block rb and group quad g4, lane l = 16q + r holds, for groups 4g4..4g4+3,
+// the 4 bytes of row 16rb + r at k = 8q..8q+7 of each group (16 bytes at
+// ((rb*ng4 + g4)*64 + l)*16), and the scales (rb, g4, r) as 4 halves.
+// Rows >= N and groups >= ng are zero.
+__global__ void i4_block_kernel(const uint8_t* __restrict__ raw, const uint16_t* __restrict__ sraw,
+                                int N, int K, int ng4, uint8_t* __restrict__ q4m,
+                                uint16_t* __restrict__ s4m) {
+    const int ng = K / 32, nrb = (N + 15) / 16;
+    const size_t total = (size_t)nrb * ng4 * 64;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const int l = (int)(i % 64);
+        const size_t bg = i / 64;
+        const int g4 = (int)(bg % ng4), rb = (int)(bg / ng4);
+        const int r = l & 15, q = l >> 4, row = 16 * rb + r;
+        uint32_t v[4] = {0, 0, 0, 0};
+        for (int gi = 0; gi < 4; ++gi) {
+            const int g = 4 * g4 + gi;
+            if (row < N && g < ng)
+                v[gi] = *reinterpret_cast<const uint32_t*>(raw + (size_t)row * (K / 2) + (size_t)g * 16 + 4 * q);
+        }
+        reinterpret_cast<uint4*>(q4m)[i] = make_uint4(v[0], v[1], v[2], v[3]);
+        if (q == 0) {
+            for (int gi = 0; gi < 4; ++gi) {
+                const int g = 4 * g4 + gi;
+                s4m[(bg * 16 + r) * 4 + gi] = (row < N && g < ng) ? sraw[(size_t)row * ng + g] : (uint16_t)0;
+            }
+        }
+    }
 }
 
 }  // namespace
 
+static bool mfma_fits(size_t k, size_t m);
+
+static bool fused_fits(size_t k, size_t m);
+
 size_t i4_ws_floats(const Weight& w, size_t m) {
-    if (m != 1 || !w.i4_blocked) return 0;
-    return (size_t)pick_segments(w.n, w.k / 32) * w.n;
+    if (!w.i4_blocked || fused_fits(w.k, m) || !mfma_fits(w.k, m)) return 0;
+    const size_t mp = round_up(m, 4), ng4 = (w.k / 32 + 3) / 4;
+    return (mp / 4) * ng4 * 64 * 32 / sizeof(float) + mp * ng4 * 4 + 64;  // digits + scales
+}
+
+size_t i4_blocked_bytes(size_t n, size_t k) {
+    return (n + 15) / 16 * ((k / 32 + 3) / 4) * 1024;
 }
 
 hipError_t launch_i4_block(const uint8_t* raw, const uint16_t* sraw, size_t n,
                            size_t k, uint8_t* blk, uint16_t* sblk,
                            hipStream_t s) {
-    i4_block_kernel<<<dim3(1024), dim3(256), 0, s>>>(raw, sraw, (int)n, (int)k, blk, sblk);
+    const int ng4 = (int)((k / 32 + 3) / 4);
+    i4_block_kernel<<<dim3(1024), dim3(256), 0, s>>>(raw, sraw, (int)n, (int)k, ng4, blk, sblk);
     return hipGetLastError();
+}
+
+template <int MT4, int KS, int GQ>
+static hipError_t launch_mfma_t(const Weight& w, size_t m, const float* a, const uint8_t* adig,
+                                const float* sog, float* out, hipStream_t s) {
+    const size_t ng4 = (w.k / 32 + 3) / 4, nrb = (w.n + 15) / 16;
+    // about 8 waves per CU on 256 CUs, the blocks spread evenly
+    const size_t want = 2048 / KS;
+    const size_t per = (nrb + want - 1) / want;
+    const size_t grid = (nrb + per - 1) / per;
+    if constexpr (MT4 == 1)
+        if (m == 1) {
+            i4_mfma_kernel<1, KS, GQ, true><<<dim3((unsigned)grid), dim3(64 * KS), 0, s>>>(
+                w.q4, w.s4, w.q4raw, a, adig, sog, (int)m, (int)w.k, (int)w.n, (int)ng4, out);
+            return hipGetLastError();
+        }
+    i4_mfma_kernel<MT4, KS, GQ, false><<<dim3((unsigned)grid), dim3(64 * KS), 0, s>>>(
+        w.q4, w.s4, w.q4raw, a, adig, sog, (int)m, (int)w.k, (int)w.n, (int)ng4, out);
+    return hipGetLastError();
+}
+
+// Group quads per K part (register budget: GQ * 4 * MT4 resident operands).
+constexpr int gq_of(int mt4) { return mt4 == 1 ? 9 : (mt4 == 2 ? 5 : 3); }
+
+// KS waves per workgroup, the fewest whose parts hold at most GQ quads.
+template <int MT4>
+static hipError_t launch_mfma(const Weight& w, size_t m, const float* a, const uint8_t* adig,
+                              const float* sog, float* out, hipStream_t s) {
+    constexpr int GQ = gq_of(MT4);
+    const size_t ng4 = (w.k / 32 + 3) / 4;
+    if (ng4 <= GQ) return launch_mfma_t<MT4, 1, GQ>(w, m, a, adig, sog, out, s);
+    if (ng4 <= 2 * GQ) return launch_mfma_t<MT4, 2, GQ>(w, m, a, adig, sog, out, s);
+    if (ng4 <= 4 * GQ) return launch_mfma_t<MT4, 4, GQ>(w, m, a, adig, sog, out, s);
+    if (ng4 <= 8 * GQ) return launch_mfma_t<MT4, 8, GQ>(w, m, a, adig, sog, out, s);
+    return hipErrorInvalidValue;  // mfma_fits() sends longer K to the generic path
+}
+
+// Shapes the MFMA path takes at m tokens: m <= 16 and K in at most 8 parts.
+static bool mfma_fits(size_t k, size_t m) {
+    if (m < 1 || m > 16) return false;
+    const size_t ng4 = (k / 32 + 3) / 4, mt4 = (m + 3) / 4;
+    return ng4 <= 8 * (size_t)gq_of((int)mt4);
+}
+
+template <int M, int KS>
+static hipError_t launch_fused_t(const Weight& w, const float* a, float* out, hipStream_t s) {
+    constexpr int GQ = 9;
+    const size_t ng4 = (w.k / 32 + 3) / 4, nrb = (w.n + 15) / 16;
+    const size_t lds = fused_lds(M, w.k, KS);
+    i4_fused_kernel<M, KS, GQ><<<dim3((unsigned)nrb), dim3(64 * KS), lds, s>>>(
+        w.q4, w.s4, w.q4raw, a, (int)w.k, (int)w.n, (int)ng4, out);
+    return hipGetLastError();
+}
+
+// KS waves per workgroup: parts of at most 5 group quads (more waves per CU
+// to overlap the MFMA -> VALU chains), at most 9 when K needs 16 parts.
+template <int M>
+static hipError_t launch_fused_m(const Weight& w, const float* a, float* out, hipStream_t s) {
+    const size_t ng4 = (w.k / 32 + 3) / 4;
+    if (ng4 <= 5) return launch_fused_t<M, 1>(w, a, out, s);
+    if (ng4 <= 10) return launch_fused_t<M, 2>(w, a, out, s);
+    if (ng4 <= 20) return launch_fused_t<M, 4>(w, a, out, s);
+    if (ng4 <= 40) return launch_fused_t<M, 8>(w, a, out, s);
+    return launch_fused_t<M, 16>(w, a, out, s);
+}
+
+// The fused path: M <= 4, K in at most 16 parts of 9 quads, digits within 64 KB of LDS.
+static bool fused_fits(size_t k, size_t m) {
+    const size_t ng4 = (k / 32 + 3) / 4;
+    return m >= 1 && m <= 4 && ng4 <= 144 && fused_lds(m, k, 16) <= 64 * 1024;
+}
+
+static hipError_t launch_fused(const Weight& w, size_t m, const float* a, float* out, hipStream_t s) {
+    switch (m) {
+        case 1: return launch_fused_m<1>(w, a, out, s);
+        case 2: return launch_fused_m<2>(w, a, out, s);
+        case 3: return launch_fused_m<3>(w, a, out, s);
+        default: return launch_fused_m<4>(w, a, out, s);
+    }
 }
 
 hipError_t launch_i4(const Weight& w, size_t m, const float* a, float* out,
                      float* wsf, unsigned* tickets, hipStream_t s) {
     (void)tickets;
     if (m == 0) return hipSuccess;
-    if (m == 1 && w.i4_blocked) {
-        const int ng = (int)(w.k / 32), nblk = (int)((w.n + 63) / 64);
-        const int S = pick_segments(w.n, (size_t)ng);
-        i4_gemv_blocked<<<dim3((unsigned)(nblk * S)), dim3(256), 0, s>>>(
-            w.q4, w.s4, a, (int)w.n, ng, S, wsf, out);
+    if (w.i4_blocked && fused_fits(w.k, m)) return launch_fused(w, m, a, out, s);
+    if (w.i4_blocked && mfma_fits(w.k, m)) {
+        const size_t mp = round_up(m, 4), ng4 = (w.k / 32 + 3) / 4;
+        uint8_t* adig = reinterpret_cast<uint8_t*>(wsf);
+        float* sog = reinterpret_cast<float*>(adig + (mp / 4) * ng4 * 64 * 32);
+        const size_t nth = 4 * mp * 4 * ng4;
+        i4_digits_kernel<<<dim3((unsigned)((nth + 255) / 256)), dim3(256), 0, s>>>(
+            a, (int)m, (int)mp, (int)w.k, (int)ng4, adig, sog);
         hipError_t e = hipGetLastError();
-        if (e != hipSuccess || S == 1) return e;
-        i4_fold<<<dim3((unsigned)((w.n + 255) / 256)), dim3(256), 0, s>>>(wsf, (int)w.n, S, out);
-        return hipGetLastError();
+        if (e != hipSuccess) return e;
+        switch (mp / 4) {
+            case 1: return launch_mfma<1>(w, m, a, adig, sog, out, s);
+            case 2: return launch_mfma<2>(w, m, a, adig, sog, out, s);
+            case 3: return launch_mfma<3>(w, m, a, adig, sog, out, s);
+            default: return launch_mfma<4>(w, m, a, adig, sog, out, s);
+        }
     }
     if (m == 1) {
         i4_gemv_generic<<<dim3((unsigned)((w.n + 255) / 256)), dim3(256), 0, s>>>(

@@ -163,19 +163,60 @@ def i4_mag(a, packed, s16, k, g):
 
 @pytest.mark.parametrize("m,n,k", [(1, 2048, 2304), (1, 9216, 2304), (1, 2304, 9216), (1, 100, 64),
                                    (1, 70, 37), (1, 33, 100), (2, 300, 2304), (16, 512, 2304),
-                                   (5, 70, 37), (64, 256, 1024)])
+                                   (5, 70, 37), (64, 256, 1024), (1, 100, 2336), (3, 1000, 2336),
+                                   (16, 2304, 9216), (7, 33, 64), (13, 4000, 96), (1, 151, 18944)])
 def test_i4_parity(ctx, m, n, k):
     packed, s16, g = synth.int4_weight(n, k, 300 + n + k)
     a = synth.activations(m, k, 400 + m, outlier_scale=1.0)
     w = ctx.upload_i4(packed, s16, k, g)
     out = w.mm(a)
     ref = oracle.mm_i4(a, packed, s16.astype(np.float32), k, g)
-    blocked = (m == 1 and g == 32 and k % 32 == 0)
-    if blocked:
+    blocked = (m <= 16 and g == 32 and k % 32 == 0)
+    if blocked:  # int8-MFMA path (24-bit fixed-point activations per group)
         mag = i4_mag(a, packed, s16, k, g)
         assert np.all(np.abs(out - ref) <= 1e-5 * mag + 1e-30)
     else:  # same operation order as the oracle: bit-exact
         assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+def test_i4_blocked_nonfinite_and_extreme_groups(ctx):
+    """Groups with inf / NaN / extreme activations take the exact AVX2-order
+    group sum on the MFMA path; the rest of the row stays within tolerance."""
+    k, n = 2304, 300
+    packed, s16, g = synth.int4_weight(n, k, 77)
+    a = synth.activations(4, k, 78, outlier_scale=1.0)
+    a[0, 40] = np.inf
+    a[1, 100] = -np.inf
+    a[2, 7] = np.nan
+    a[3, 200:232] = 1e-38  # a group of tiny values (digit scale out of range)
+    a[3, 500] = 3e38
+    w = ctx.upload_i4(packed, s16, k, g)
+    with np.errstate(invalid="ignore", over="ignore"):
+        out = w.mm(a)
+        ref = oracle.mm_i4(a, packed, s16.astype(np.float32), k, g)
+        mag = i4_mag(a, packed, s16, k, g)
+    assert np.array_equal(np.isnan(out), np.isnan(ref))
+    inf = np.isinf(ref)
+    assert np.array_equal(out[inf], ref[inf])
+    ok = np.isfinite(ref) & np.isfinite(mag)
+    assert np.all(np.abs(out[ok] - ref[ok]) <= 1e-5 * mag[ok] + 1e-30)
+
+
+def test_i4_repeated_calls_rearm_tickets(ctx):
+    """The split-K fold re-arms its per-row-block counters: back-to-back
+    calls of different shapes give the same results as fresh ones."""
+    shapes = [(1, 9216, 2304), (16, 2304, 9216), (1, 2048, 2304)]
+    ws, refs, acts = [], [], []
+    for i, (m, n, k) in enumerate(shapes):
+        packed, s16, g = synth.int4_weight(n, k, 900 + i)
+        a = synth.activations(m, k, 910 + i, outlier_scale=1.0)
+        w = ctx.upload_i4(packed, s16, k, g)
+        ws.append(w)
+        acts.append(a)
+        refs.append(w.mm(a))
+    for _ in range(3):
+        for w, a, r in zip(ws, acts, refs):
+            assert np.array_equal(w.mm(a).view(np.uint32), r.view(np.uint32))
 
 
 def test_i4_reference_kat_through_gpu(ctx):
