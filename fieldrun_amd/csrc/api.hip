@@ -545,6 +545,17 @@ frq_moe_w* frq_moe_upload_i8(frq_ctx* c, size_t n_exp, size_t d, size_t mi, int 
             if (e == hipSuccess) e = hipMemcpyAsync(b.up_s + x * mi, up_scale[x], mi * 4, hipMemcpyHostToDevice, c->stream);
         }
     }
+    // blocked MFMA-operand copies for the digit GEMM
+    b.kpd = round_up(d, 64);
+    b.kpm = round_up(mi, 64);
+    const size_t gwp = round_up(b.gw, 16), mip = round_up(mi, 16), dp = round_up(d, 16);
+    if (e == hipSuccess) e = hipMalloc(&b.gate_b, n_exp * gwp * b.kpd);
+    if (e == hipSuccess) e = launch_moe_block(b.gate, n_exp, d, b.gw, b.kpd, gwp, b.gate_b, c->stream);
+    if (e == hipSuccess && act == FRQ_ACT_SILU) e = hipMalloc(&b.up_b, n_exp * mip * b.kpd);
+    if (e == hipSuccess && act == FRQ_ACT_SILU)
+        e = launch_moe_block(b.up, n_exp, d, mi, b.kpd, mip, b.up_b, c->stream);
+    if (e == hipSuccess) e = hipMalloc(&b.down_b, n_exp * dp * b.kpm);
+    if (e == hipSuccess) e = launch_moe_block(b.down, n_exp, mi, d, b.kpm, dp, b.down_b, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     if (e != hipSuccess) {
         hip_fail(e, "frq_moe_upload_i8");
@@ -558,7 +569,8 @@ void frq_moe_free(frq_moe_w* h) {
     if (!h) return;
     MoeBank& b = h->b;
     DeviceGuard g(b.device);
-    for (void* p : {(void*)b.gate, (void*)b.gate_s, (void*)b.up, (void*)b.up_s, (void*)b.down, (void*)b.down_s})
+    for (void* p : {(void*)b.gate, (void*)b.gate_s, (void*)b.up, (void*)b.up_s, (void*)b.down, (void*)b.down_s,
+                    (void*)b.gate_b, (void*)b.up_b, (void*)b.down_b})
         if (p) (void)hipFree(p);
     delete h;
 }

@@ -123,6 +123,12 @@ struct MoeBank {
     float* up_s = nullptr;       // (E, mi)
     int8_t* down = nullptr;      // (E, mi, d)
     float* down_s = nullptr;     // (E, d)
+    // blocked MFMA-operand copies (blk_off, per expert (Np, Kp)): gate
+    // (gw rows of d), up (mi rows of d), down (d rows of mi)
+    size_t kpd = 0, kpm = 0;     // d and mi rounded up to 64
+    int8_t* gate_b = nullptr;
+    int8_t* up_b = nullptr;
+    int8_t* down_b = nullptr;
 };
 
 // ---- kernel launchers (each returns hipError_t of the launch) ------------
@@ -163,6 +169,9 @@ hipError_t launch_moe(const MoeBank& b, const float* x, size_t T,
 hipError_t launch_moe_route(const float* logits, size_t T, size_t E,
                             size_t topk, int norm_topk, const float* pes,
                             int32_t* sel, float* w, int* err, hipStream_t s);
+// (E, K, N) (in, out) int8 -> per expert blocked (np, kp) copies.
+hipError_t launch_moe_block(const int8_t* src, size_t E, size_t K, size_t N, size_t kp,
+                            size_t np, int8_t* dst, hipStream_t s);
 hipError_t launch_expert_mm(const int8_t* q, const float* s, size_t inp,
                             size_t out, const float* x, size_t m, float* y,
                             hipStream_t st);

@@ -3,8 +3,7 @@
 // Restates the routed branch of /root/reference/src/qwen3moe.rs:120-158
 // (act SiLU) and the expert part of src/gemma4.rs:131-187 (act gelu_tanh,
 // packed gate_up, per_expert_scale), with the experts' matmuls as in
-// expert_f32 / expert_mm (src/bundle.rs:404-461): W8A32, w = q * scale[j]
-// exactly in f32, then an f32 GEMM.
+// expert_f32 / expert_mm (src/bundle.rs:404-461): W8A32, y = x . (q * s[j]).
 //
 // Pipeline (all on the device, no host round trip):
 //   route     one wave per token: max, exp, sequential sum, divide
@@ -15,11 +14,20 @@
 //   dispatch  one workgroup: per-expert counts, offsets, and each (token,
 //             slot) pair's row in the expert-sorted permutation, tokens in
 //             ascending order within an expert (a per-expert token bitmap
-//             gives the rank); plus the list of (expert, row0) GEMM tiles.
-//   gemm      grouped GEMM over the tile list: rows gathered through the
-//             permutation, weights dequantised while staged into LDS, a
-//             sequential-k FMA chain per output (the oracle's sgemm order).
-//   act       h = silu(g) * u   or   gelu_tanh(g[:mi]) * g[mi:].
+//             gives the rank); plus the list of (expert, row0) tiles.
+//   digits    each token row of x as X = round(x / s), s = max|x| /
+//             (127 * 2^16), |X| <= 127 * 2^16, split into three int8 digits
+//             X = d2*2^16 + d1*2^8 + d0 (a 24-bit fixed point per row).
+//   gemm      grouped GEMM over the tile list on v_mfma_i32_16x16x64_i8: the
+//             A rows of a token group are its tokens' three digit rows, B is
+//             the expert's weight in the blocked MFMA-operand layout (built
+//             at upload), so C_d = D_d . Q is exact in int32 over all of K
+//             (|C| < 127 * 127 * K) and y = s * (C2*2^16 + C1*2^8 + C0) * s[j].
+//             The rounding of x to 24 bits keeps y within ~1e-7 of
+//             max|x| * sum|q*s|; a row with a non-finite or extreme value
+//             takes the reference's sequential f32 sum (expert_mm order).
+//   act       h = silu(g) * u   or   gelu_tanh(g[:mi]) * g[mi:], written
+//             directly as the digits (and f32 copy) the down GEMM reads.
 //   combine   out[t,:] = sum over t's experts in ascending expert id of
 //             w * down (mul then add from +0): the reference adds in HashMap
 //             order, which is random per process; ascending id is one of
@@ -30,7 +38,7 @@ namespace frq {
 
 namespace {
 
-constexpr int GBM = 32, GBN = 64, GKC = 32;
+constexpr float XMAXD = 8323072.0f;  // 127 * 2^16: |X| of a 24-bit row digit triple
 
 struct MoeWs {
     int32_t* sel;      // [T*k]
@@ -42,16 +50,27 @@ struct MoeWs {
     int32_t* tile_e;   // [ntile_max]
     int32_t* tile_r;   // [ntile_max]
     int32_t* ntile;    // [1]
+    int8_t* xd;        // [T][3][kpd] digits of x
+    float* xso;        // [T]      their scales (-1: exact row)
     float* g;          // [T*k, gw]
     float* u;          // [T*k, mi]
     float* h;          // [T*k, mi]
+    int8_t* hd;        // [T*k][3][kpm] digits of h
+    float* hso;        // [T*k]
     float* dn;         // [T*k, d]
 };
 
-size_t ntile_max(size_t T, size_t k, size_t E) { return T * k / GBM + E + 1; }
+// Tiles of tr rows per expert: sum over experts of ceil(cnt / tr) is at most
+// T*k / tr plus one per active expert.
+size_t ntile_max(size_t T, size_t k, size_t E, size_t tr) {
+    const size_t P = T * k;
+    return P / tr + (E < P ? E : P) + 1;
+}
+
+size_t moe_tile_rows(size_t T) { return T <= 4 ? 4 : 16; }
 
 MoeWs moe_view(void* base, const MoeBank& b, size_t T, size_t k) {
-    const size_t P = T * k, E = b.n_exp, nt = ntile_max(T, k, E);
+    const size_t P = T * k, E = b.n_exp, nt = ntile_max(T, k, E, moe_tile_rows(T));
     char* p = (char*)base;
     MoeWs v;
     auto take = [&](size_t bytes) { char* r = p; p += round_up(bytes, 256); return r; };
@@ -64,9 +83,13 @@ MoeWs moe_view(void* base, const MoeBank& b, size_t T, size_t k) {
     v.tile_e = (int32_t*)take(nt * 4);
     v.tile_r = (int32_t*)take(nt * 4);
     v.ntile = (int32_t*)take(4);
+    v.xd = (int8_t*)take(T * 3 * b.kpd);
+    v.xso = (float*)take(T * 4);
     v.g = (float*)take(P * b.gw * 4);
     v.u = (float*)take(P * b.mi * 4);
     v.h = (float*)take(P * b.mi * 4);
+    v.hd = (int8_t*)take(P * 3 * b.kpm);
+    v.hso = (float*)take(P * 4);
     v.dn = (float*)take(P * b.d * 4);
     return v;
 }
@@ -158,7 +181,7 @@ __global__ __launch_bounds__(256) void route_kernel(
 constexpr int TC = 1024;  // tokens per bitmap chunk
 
 __global__ __launch_bounds__(1024) void dispatch_kernel(
-    const int32_t* __restrict__ sel, int T, int topk, int E,
+    const int32_t* __restrict__ sel, int T, int topk, int E, int tr,
     MoeWs ws) {
     extern __shared__ uint32_t sm[];
     const int nwc = TC / 32;
@@ -182,7 +205,7 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(
             ws.cnt[e] = c;
             ws.off[e] = acc;
             offl[e] = (uint32_t)acc;
-            for (int r = 0; r < c; r += GBM) { ws.tile_e[nt] = e; ws.tile_r[nt] = r; ++nt; }
+            for (int r = 0; r < c; r += tr) { ws.tile_e[nt] = e; ws.tile_r[nt] = r; ++nt; }
             acc += c;
         }
         ws.off[E] = acc;
@@ -223,83 +246,190 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(
     }
 }
 
-// ---- grouped W8A32 GEMM: Y[prow, :] = X[row(prow), :] . (q[e] * s[e]) ------
-// X rows: gather ? x[ptok[prow]] : xin[prow]; weights (E, K, N) i8 row-major.
-__global__ __launch_bounds__(256) void grouped_gemm_kernel(
-    const float* __restrict__ xin, int gather, const int32_t* __restrict__ ptok,
-    const int8_t* __restrict__ q, const float* __restrict__ qs, int K, int N,
-    const int32_t* __restrict__ off, const int32_t* __restrict__ cnt,
-    const int32_t* __restrict__ tile_e, const int32_t* __restrict__ tile_r,
-    const int32_t* __restrict__ ntile, float* __restrict__ y) {
-    __shared__ float As[GKC][GBM + 4];
-    __shared__ float Bs[GKC][GBN];
-    const int tix = blockIdx.x;
-    if (tix >= ntile[0]) return;
-    const int e = tile_e[tix], r0 = tile_r[tix];
-    const int rows = min(GBM, cnt[e] - r0);
-    const int n0 = blockIdx.y * GBN;
+// ---- 24-bit row digits ------------------------------------------------------
+// Digits of one f32 row v[0..K) into D[3][Kp] (d2, d1, d0; zero padding) and
+// its scale; -1 when the row holds a non-finite value or its scale leaves
+// [1e-30, 1e28] (|y| <= 127 * 127 * K * s must stay finite).  256 threads.
+__device__ void row_digits(const float* __restrict__ v, int K, int Kp, int8_t* __restrict__ D,
+                           float* __restrict__ so_out, float* red) {
     const int tid = threadIdx.x;
-    const int tr = tid / 16, tc = tid % 16;   // 16 x 16 threads: 2 rows x 4 cols
-    const int8_t* qe = q + (size_t)e * K * N;
-    const float* se = qs + (size_t)e * N;
-    const int pbase = off[e] + r0;
-    float acc[2][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
-    for (int k0 = 0; k0 < K; k0 += GKC) {
-        // stage A^T (GKC x GBM) and dequantised B (GKC x GBN)
-        for (int i = tid; i < GKC * GBM; i += 256) {
-            const int r = i / GKC, kk = i % GKC;
-            float v = 0.0f;
-            if (r < rows && k0 + kk < K) {
-                const int prow = pbase + r;
-                const float* xr = gather ? xin + (size_t)ptok[prow] * K : xin + (size_t)prow * K;
-                v = xr[k0 + kk];
-            }
-            As[kk][r] = v;
-        }
-        for (int i = tid; i < GKC * GBN; i += 256) {
-            const int kk = i / GBN, c = i % GBN;
-            float v = 0.0f;
-            if (k0 + kk < K && n0 + c < N)
-                v = (float)qe[(size_t)(k0 + kk) * N + n0 + c] * se[n0 + c];
-            Bs[kk][c] = v;
-        }
-        __syncthreads();
-        const int kn = min(GKC, K - k0);
-        for (int kk = 0; kk < kn; ++kk) {
-            const float a0 = As[kk][tr * 2], a1 = As[kk][tr * 2 + 1];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const float b = Bs[kk][tc * 4 + c];
-                acc[0][c] = __builtin_fmaf(a0, b, acc[0][c]);
-                acc[1][c] = __builtin_fmaf(a1, b, acc[1][c]);
-            }
-        }
-        __syncthreads();
+    float mx = 0.0f;
+    int nf = 0;
+    for (int k = tid; k < K; k += 256) {
+        const float x = v[k];
+        nf |= !(fabsf(x) <= 3.0e38f);
+        mx = fmaxf(mx, fabsf(x));
     }
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-        const int rr = tr * 2 + r;
-        if (rr >= rows) continue;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int j = n0 + tc * 4 + c;
-            if (j < N) y[(size_t)(pbase + rr) * N + j] = acc[r][c];
-        }
+    for (int o = 32; o >= 1; o >>= 1) {
+        mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        nf |= __shfl_xor(nf, o, 64);
     }
+    if ((tid & 63) == 0) { red[tid >> 6] = mx; red[4 + (tid >> 6)] = (float)nf; }
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    nf = (red[4] + red[5] + red[6] + red[7]) != 0.0f;
+    const float s = mx > 0.0f ? mx / XMAXD : 1.0f;
+    const bool ok = !nf && s >= 1.0e-30f && s <= 1.0e28f;
+    const float r = 1.0f / s;  // any rounding of x / s keeps |x - s X| <= ~s/2
+    for (int k = tid; k < Kp; k += 256) {
+        int d2 = 0, d1 = 0, d0 = 0;
+        if (ok && k < K) {
+            float xf = rintf(v[k] * r);
+            xf = fminf(fmaxf(xf, -XMAXD), XMAXD);
+            const int X = (int)xf;
+            d0 = (int)(int8_t)(X & 0xFF);
+            const int X1 = (X - d0) >> 8;
+            d1 = (int)(int8_t)(X1 & 0xFF);
+            d2 = (X1 - d1) >> 8;
+        }
+        D[k] = (int8_t)d2;
+        D[Kp + k] = (int8_t)d1;
+        D[2 * Kp + k] = (int8_t)d0;
+    }
+    if (tid == 0) *so_out = ok ? s : -1.0f;
 }
 
-__global__ void act_kernel(const float* __restrict__ g, const float* __restrict__ u,
-                           int act, int mi, int gw, const int32_t* __restrict__ off,
-                           int E, float* __restrict__ h) {
-    const int P = off[E];
-    const size_t total = (size_t)P * mi;
-    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
-         i += (size_t)gridDim.x * blockDim.x) {
-        const size_t r = i / mi, c = i % mi;
-        if (act == FRQ_ACT_SILU)
-            h[i] = silu(g[r * gw + c]) * u[i];
-        else
-            h[i] = gelu_tanh(g[r * gw + c]) * g[r * gw + c + mi];
+// One workgroup per token row of x.
+__global__ __launch_bounds__(256) void x_digits_kernel(const float* __restrict__ x, int K, int Kp,
+                                                       int8_t* __restrict__ D, float* __restrict__ so) {
+    __shared__ float red[8];
+    const int r = blockIdx.x;
+    row_digits(x + (size_t)r * K, K, Kp, D + (size_t)r * 3 * Kp, so + r, red);
+}
+
+// h = silu(g) * u  or  gelu_tanh(g[:mi]) * g[mi:], one workgroup per
+// permuted row (rows >= off[E] are idle): the f32 row (for the exact path)
+// and its digits.
+__global__ __launch_bounds__(256) void act_digits_kernel(
+    const float* __restrict__ g, const float* __restrict__ u, int act, int mi, int gw, int kpm,
+    const int32_t* __restrict__ off, int E, float* __restrict__ h, int8_t* __restrict__ hd,
+    float* __restrict__ hso) {
+    __shared__ float red[8];
+    const int r = blockIdx.x;
+    if (r >= off[E]) return;  // uniform
+    const float* gr = g + (size_t)r * gw;
+    float* hr = h + (size_t)r * mi;
+    for (int c = threadIdx.x; c < mi; c += 256)
+        hr[c] = act == FRQ_ACT_SILU ? silu(gr[c]) * u[(size_t)r * mi + c] : gelu_tanh(gr[c]) * gr[c + mi];
+    __syncthreads();
+    row_digits(hr, mi, kpm, hd + (size_t)r * 3 * kpm, hso + r, red);
+}
+
+// ---- grouped digit GEMM: Y[prow, :] = X[src(prow), :] . (q[e] * s[e]) -------
+// Workgroup = (tile of 4*TG rows of one expert, CB column blocks of 16);
+// its KS waves split the k-blocks and add their int32 accumulators through
+// LDS (exact in any order).  A operand of token group t: lane 16g + 4tl + d
+// holds digit d of row 4t + tl, k-bytes 16g..16g+15 of the k-block; C lane
+// l holds rows 4(l/16) + c, i.e. row 4t + l/16, digit c.  src = ptok[prow]
+// when gather (rows of x), else prow (rows of h).
+template <int TG, int CB, int KS>
+__global__ __launch_bounds__(64 * KS) void moe_mm_kernel(
+    const int8_t* __restrict__ D, const float* __restrict__ dso, int Kp, int gather,
+    const int32_t* __restrict__ ptok, const int8_t* __restrict__ Wb, int Np,
+    const float* __restrict__ wsc, int N, const float* __restrict__ xf, int K,
+    const int8_t* __restrict__ wkn, const int32_t* __restrict__ off,
+    const int32_t* __restrict__ cnt, const int32_t* __restrict__ tile_e,
+    const int32_t* __restrict__ tile_r, const int32_t* __restrict__ ntile,
+    float* __restrict__ y) {
+    constexpr int TR = 4 * TG;
+    __shared__ v4i red[KS > 1 ? KS - 1 : 1][TG][CB][64];
+    const int tix = blockIdx.x;
+    if (tix >= ntile[0]) return;  // uniform
+    const int e = tile_e[tix], r0 = tile_r[tix];
+    const int rows = min(TR, cnt[e] - r0);
+    const int pbase = off[e] + r0;
+    const int nb0 = blockIdx.y * CB;
+    const int lane = threadIdx.x & 63;
+    const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nkb = Kp / 64;
+    const int kb0 = nkb * ks / KS, kb1 = nkb * (ks + 1) / KS;
+    const int rr = lane & 15, tl = rr >> 2, dg = rr & 3, kq = lane >> 4;
+    const int8_t* arow[TG];
+    bool aval[TG];
+#pragma unroll
+    for (int t = 0; t < TG; ++t) {
+        const int i = 4 * t + tl;
+        aval[t] = i < rows && dg < 3;
+        const int prow = pbase + min(i, rows - 1);
+        const int src = gather ? ptok[prow] : prow;
+        arow[t] = D + ((size_t)src * 3 + (dg < 3 ? dg : 0)) * Kp + 16 * kq;
+    }
+    const int8_t* wb = Wb + (size_t)e * Np * Kp + (size_t)nb0 * 1024 + lane * 16;
+    const size_t kstride = (size_t)(Np / 16) * 1024;
+    v4i acc[TG][CB];
+#pragma unroll
+    for (int t = 0; t < TG; ++t)
+#pragma unroll
+        for (int c = 0; c < CB; ++c) acc[t][c] = v4i{0, 0, 0, 0};
+    // U k-blocks per step, all of their loads issued before the MFMAs
+    constexpr int U = (TG + CB <= 2) ? 8 : 2;
+    for (int kb = kb0; kb < kb1; kb += U) {
+        v4i av[U][TG], bv[U][CB];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const bool in = kb + u < kb1;
+#pragma unroll
+            for (int t = 0; t < TG; ++t)
+                av[u][t] = (in && aval[t]) ? *reinterpret_cast<const v4i*>(arow[t] + (size_t)(kb + u) * 64)
+                                           : v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int c = 0; c < CB; ++c)
+                bv[u][c] = in ? *reinterpret_cast<const v4i*>(wb + (size_t)(kb + u) * kstride + (size_t)c * 1024)
+                              : v4i{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int t = 0; t < TG; ++t)
+#pragma unroll
+                for (int c = 0; c < CB; ++c)
+                    acc[t][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[u][t], bv[u][c], acc[t][c], 0, 0, 0);
+    }
+    if (KS > 1) {
+        if (ks > 0) {
+#pragma unroll
+            for (int t = 0; t < TG; ++t)
+#pragma unroll
+                for (int c = 0; c < CB; ++c) red[ks - 1][t][c][lane] = acc[t][c];
+        }
+        __syncthreads();
+        if (ks > 0) return;
+#pragma unroll
+        for (int q = 0; q < KS - 1; ++q)
+#pragma unroll
+            for (int t = 0; t < TG; ++t)
+#pragma unroll
+                for (int c = 0; c < CB; ++c) acc[t][c] += red[q][t][c][lane];
+    }
+    // y = s * (C2 * 2^16 + C1 * 2^8 + C0) * wsc[e, j]; rows whose digits do not
+    // carry them take the reference's sequential sum x . (q * s)
+    const int col = lane & 15, tok = lane >> 4;
+    const float* __restrict__ se = wsc + (size_t)e * N;
+#pragma unroll
+    for (int t = 0; t < TG; ++t) {
+        const int i = 4 * t + tok;
+        if (i >= rows) continue;
+        const int prow = pbase + i;
+        const int src = gather ? ptok[prow] : prow;
+        const float so = dso[src];
+#pragma unroll
+        for (int c = 0; c < CB; ++c) {
+            const int j = (nb0 + c) * 16 + col;
+            if (j >= N) continue;
+            float v;
+            if (so >= 0.0f) {
+                const v4i a4 = acc[t][c];
+                v = so * ((float)a4[0] * 65536.0f + ((float)a4[1] * 256.0f + (float)a4[2])) * se[j];
+            } else {
+                const float* xr = xf + (size_t)src * K;
+                const int8_t* qe = wkn + (size_t)e * K * N;
+                const float sj = se[j];
+                v = 0.0f;
+                for (int k = 0; k < K; ++k) v = __builtin_fmaf(xr[k], (float)qe[(size_t)k * N + j] * sj, v);
+            }
+            y[(size_t)prow * N + j] = v;
+        }
     }
 }
 
@@ -330,10 +460,11 @@ __global__ void combine_kernel(const float* __restrict__ dn, const int32_t* __re
 }  // namespace
 
 size_t moe_ws_bytes(const MoeBank& b, size_t T, size_t topk) {
-    const size_t P = T * topk, E = b.n_exp, nt = ntile_max(T, topk, E);
+    const size_t P = T * topk, E = b.n_exp, nt = ntile_max(T, topk, E, moe_tile_rows(T));
     auto r = [](size_t x) { return round_up(x, 256); };
-    return r(P * 4) * 4 + r(E * 4) + r((E + 1) * 4) + r(nt * 4) * 2 + r(4) +
-           r(P * b.gw * 4) + r(P * b.mi * 4) * 2 + r(P * b.d * 4);
+    return r(P * 4) * 4 + r(E * 4) + r((E + 1) * 4) + r(nt * 4) * 2 + r(4) + r(T * 3 * b.kpd) +
+           r(T * 4) + r(P * b.gw * 4) + r(P * b.mi * 4) * 2 + r(P * 3 * b.kpm) + r(P * 4) +
+           r(P * b.d * 4);
 }
 
 hipError_t launch_moe_route(const float* logits, size_t T, size_t E,
@@ -345,6 +476,25 @@ hipError_t launch_moe_route(const float* logits, size_t T, size_t E,
     return hipGetLastError();
 }
 
+// One grouped digit GEMM: decode (tiles of 4 rows) splits K over 4 waves per
+// 16-column block; prefill (tiles of 16 rows) takes 64 columns per 1-wave
+// workgroup.
+static hipError_t moe_mm(bool dec, unsigned nt, const int8_t* D, const float* dso, size_t kp,
+                         int gather, const MoeWs& ws, const int8_t* wb, size_t np, const float* wsc,
+                         size_t n, const float* xf, size_t k, const int8_t* wkn, float* y,
+                         hipStream_t s) {
+    if (dec) {
+        moe_mm_kernel<1, 1, 4><<<dim3(nt, (unsigned)(np / 16)), dim3(256), 0, s>>>(
+            D, dso, (int)kp, gather, ws.ptok, wb, (int)np, wsc, (int)n, xf, (int)k, wkn, ws.off,
+            ws.cnt, ws.tile_e, ws.tile_r, ws.ntile, y);
+    } else {
+        moe_mm_kernel<4, 4, 1><<<dim3(nt, (unsigned)((np / 16 + 3) / 4)), dim3(64), 0, s>>>(
+            D, dso, (int)kp, gather, ws.ptok, wb, (int)np, wsc, (int)n, xf, (int)k, wkn, ws.off,
+            ws.cnt, ws.tile_e, ws.tile_r, ws.ntile, y);
+    }
+    return hipGetLastError();
+}
+
 hipError_t launch_moe(const MoeBank& b, const float* x, size_t T,
                       const float* logits, size_t topk, int norm_topk,
                       const float* pes, float* out, void* wsp, int* err,
@@ -352,27 +502,53 @@ hipError_t launch_moe(const MoeBank& b, const float* x, size_t T,
     if (T == 0) return hipSuccess;
     MoeWs ws = moe_view(wsp, b, T, topk);
     const int E = (int)b.n_exp, d = (int)b.d, mi = (int)b.mi, gw = (int)b.gw;
+    const size_t tr = moe_tile_rows(T);
+    const bool dec = tr == 4;
     hipError_t e = launch_moe_route(logits, T, b.n_exp, topk, norm_topk, pes, ws.sel, ws.w, err, s);
     if (e != hipSuccess) return e;
     const size_t dlds = ((size_t)E * (TC / 32) * 2 + 2 * E) * sizeof(uint32_t);
-    dispatch_kernel<<<dim3(1), dim3(1024), dlds, s>>>(ws.sel, (int)T, (int)topk, E, ws);
+    dispatch_kernel<<<dim3(1), dim3(1024), dlds, s>>>(ws.sel, (int)T, (int)topk, E, (int)tr, ws);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    const unsigned nt = (unsigned)ntile_max(T, topk, b.n_exp);
-    grouped_gemm_kernel<<<dim3(nt, (unsigned)((gw + GBN - 1) / GBN)), dim3(256), 0, s>>>(
-        x, 1, ws.ptok, b.gate, b.gate_s, d, gw, ws.off, ws.cnt, ws.tile_e, ws.tile_r, ws.ntile, ws.g);
+    x_digits_kernel<<<dim3((unsigned)T), dim3(256), 0, s>>>(x, d, (int)b.kpd, ws.xd, ws.xso);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    if (b.act == FRQ_ACT_SILU) {
-        grouped_gemm_kernel<<<dim3(nt, (unsigned)((mi + GBN - 1) / GBN)), dim3(256), 0, s>>>(
-            x, 1, ws.ptok, b.up, b.up_s, d, mi, ws.off, ws.cnt, ws.tile_e, ws.tile_r, ws.ntile, ws.u);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
-    }
-    act_kernel<<<dim3(1024), dim3(256), 0, s>>>(ws.g, ws.u, b.act, mi, gw, ws.off, E, ws.h);
+    const unsigned nt = (unsigned)ntile_max(T, topk, b.n_exp, tr);
+    const size_t gwp = round_up(b.gw, 16), mip = round_up(b.mi, 16), dp = round_up(b.d, 16);
+    if ((e = moe_mm(dec, nt, ws.xd, ws.xso, b.kpd, 1, ws, b.gate_b, gwp, b.gate_s, b.gw, x, b.d,
+                    b.gate, ws.g, s)) != hipSuccess)
+        return e;
+    if (b.act == FRQ_ACT_SILU &&
+        (e = moe_mm(dec, nt, ws.xd, ws.xso, b.kpd, 1, ws, b.up_b, mip, b.up_s, b.mi, x, b.d, b.up,
+                    ws.u, s)) != hipSuccess)
+        return e;
+    act_digits_kernel<<<dim3((unsigned)(T * topk)), dim3(256), 0, s>>>(
+        ws.g, ws.u, b.act, mi, gw, (int)b.kpm, ws.off, E, ws.h, ws.hd, ws.hso);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    grouped_gemm_kernel<<<dim3(nt, (unsigned)((d + GBN - 1) / GBN)), dim3(256), 0, s>>>(
-        ws.h, 0, ws.ptok, b.down, b.down_s, mi, d, ws.off, ws.cnt, ws.tile_e, ws.tile_r, ws.ntile, ws.dn);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if ((e = moe_mm(dec, nt, ws.hd, ws.hso, b.kpm, 0, ws, b.down_b, dp, b.down_s, b.d, ws.h, b.mi,
+                    b.down, ws.dn, s)) != hipSuccess)
+        return e;
     combine_kernel<<<dim3((unsigned)((d + 255) / 256), (unsigned)T), dim3(256), 0, s>>>(
         ws.dn, ws.sel, ws.w, ws.pos, (int)topk, d, out);
+    return hipGetLastError();
+}
+
+// (K, N) (in, out) int8 expert weights -> blocked (Np, Kp) per expert
+// (zero padding), the MFMA B-operand layout of the digit GEMM.
+__global__ void moe_block_kernel(const int8_t* __restrict__ src, int E, int K, int N, int Kp,
+                                 int Np, int8_t* __restrict__ dst) {
+    const size_t per = (size_t)Np * Kp, total = (size_t)E * per;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const size_t e = i / per, rem = i % per;
+        const int n = (int)(rem / Kp), k = (int)(rem % Kp);
+        const int8_t v = (n < N && k < K) ? src[e * (size_t)K * N + (size_t)k * N + n] : (int8_t)0;
+        dst[e * per + blk_off((size_t)n, (size_t)k, (size_t)Np)] = v;
+    }
+}
+
+hipError_t launch_moe_block(const int8_t* src, size_t E, size_t K, size_t N, size_t kp,
+                            size_t np, int8_t* dst, hipStream_t s) {
+    moe_block_kernel<<<dim3(2048), dim3(256), 0, s>>>(src, (int)E, (int)K, (int)N, (int)kp,
+                                                      (int)np, dst);
     return hipGetLastError();
 }
 
