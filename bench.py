@@ -10,9 +10,13 @@ algorithmic bytes (N*K + 4N + 4K + 4N per shape) over its wall time on the
 GPU stream, in GB/s.  Weights are rotated over 3 replica sets (786 MB, over
 the 256 MB MALL) so repeats are served from HBM.
 
-Also reported (in "detail"): the GEMV kernel alone on pre-quantised input
-(its roofline), the M=2048 MFMA-bound shapes in TOPS, the int4 decode GEMV
-on Gemma-2 shapes, and the config-4 MoE layer.  The CPU baseline is the
+At M=1 the full linear is one kernel (linear_m1_kernel: the activation quant
+fused into the GEMV); `roofline` is that kernel at the step's dominant shape
+(K=896, N=151936, 136 MB of weights), its algorithmic bytes (weights, scales,
+f32 activation row, f32 outputs) over its average launch time on the
+library's stream.  Also reported (in "detail"): the GEMV kernel alone on
+pre-quantised input, the M=2048 MFMA-bound shapes in TOPS, the int4 decode
+GEMV on Gemma-2 shapes, and the config-4 MoE layer.  The CPU baseline is the
 oracle's restatement of the reference's scalar int8 path (the
 `_scalar_i8_bench` build) on the host's cores, on a bounded sample.
 """
@@ -42,11 +46,11 @@ def int4_bytes(m, k, n, g=32):
     return n * k // 2 + 2 * n * ((k + g - 1) // g) + 4 * m * k + 4 * m * n
 
 
-DOM_SHAPE = (896, 151936)  # the headline's dominant GEMV launch (136 MB of weights)
-DOM_KERNEL = "gemv3_i8_kernel<8,8,true>"
+DOM_SHAPE = (896, 151936)  # the headline's dominant launch (136 MB of weights)
+DOM_KERNEL = "linear_m1_kernel<8,8,true,1>"
 PMC_COPY_BYTES = 256 << 20
 PMC_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                           "gemv_i8_m1_K896_N151936_pmc.md")
+                           "linear_m1_K896_N151936_pmc.md")
 
 
 def measured_traffic():
@@ -66,7 +70,7 @@ def measured_traffic():
 def pmc_pass(fa, hip, synth, ctx, log):
     """Counter-collection workload, run under `rocprofv3 --pmc`: 3 device
     copies of PMC_COPY_BYTES (the calibration kernel), then 9 launches of
-    the dominant GEMV kernel on pre-quantised input (3 weight replicas)."""
+    the dominant kernel, the fused M=1 linear (3 weight replicas)."""
     src = hip.DeviceArray((PMC_COPY_BYTES,), np.uint8)
     dst = hip.DeviceArray((PMC_COPY_BYTES,), np.uint8)
     src.zero()
@@ -83,16 +87,11 @@ def pmc_pass(fa, hip, synth, ctx, log):
     a = synth.activations(1, k, synth.seed(1) + 2)
     da = hip.DeviceArray.from_numpy(a)
     out = hip.DeviceArray((1, n), np.float32)
-    a8 = hip.DeviceArray((1, fa.quant_pitch(k)), np.int8)
-    sa = hip.DeviceArray((1,), np.float32)
-    oi = hip.DeviceArray((1, 32), np.uint32)
-    ov = hip.DeviceArray((1, 32), np.float32)
-    ctx.quant_dev(da.ptr, 1, k, a8.ptr, sa.ptr, oi.ptr, ov.ptr)
     for i in range(9):
-        reps[i % 3].mm_q_dev(a8.ptr, sa.ptr, oi.ptr, ov.ptr, 1, out.ptr)
+        reps[i % 3].mm_dev(da.ptr, 1, out.ptr)
     ctx.sync()
     log(f"pmc: 9 launches of {DOM_KERNEL} at K={k} N={n}, "
-        f"{gemv_kernel_bytes(1, k, n)} algorithmic bytes each")
+        f"{int8_linear_bytes(1, k, n)} algorithmic bytes each")
 
 
 def main():
@@ -183,7 +182,7 @@ def main():
         detail["int8_m1_full_linear"][f"K{k}_N{n}"] = {
             "us": round(us, 2), "GBps": round(int8_linear_bytes(1, k, n) / (us * 1e-6) / 1e9, 1)}
 
-    # ---------------- roofline: the GEMV kernel on pre-quantised input -------------
+    # ---------------- the GEMV kernel alone on pre-quantised input -------------
     gemv_rows = {}
     for si, (k, n) in enumerate(shapes):
         kp = fa.quant_pitch(k)
@@ -201,12 +200,17 @@ def main():
         qus = time_loop(lambda i, si=si: ctx.quant_dev(acts[si][1].ptr, 1, k, a8.ptr, sa.ptr, oi.ptr,
                                                        ov.ptr), 60) * 1e3
         detail["int8_m1_gemv_kernel"][f"K{k}_N{n}"]["quant_us"] = round(qus, 2)
+    # ---------------- roofline: the dominant launch of the step -------------
+    # at M=1 the full linear is the single fused kernel: time it alone, 60
+    # launches over the weight replicas, HIP events on the library's stream
     dom = DOM_SHAPE
-    us_dom, gb_dom = gemv_rows[dom]
+    dsi = shapes.index(dom)
+    us_dom = time_loop(lambda i: weights[dsi][i % R].mm_dev(acts[dsi][1].ptr, 1, outs[dsi].ptr), 60) * 1e3
+    gb_dom = int8_linear_bytes(1, *dom) / (us_dom * 1e-6) / 1e9
     roofline = {"bound": "hbm", "achieved": round(gb_dom, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gb_dom / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                 "kernel": f"{DOM_KERNEL} (M=1, K={dom[0]}, N={dom[1]})",
-                "bytes_per_launch": gemv_kernel_bytes(1, *dom), "us_per_launch": round(us_dom, 2)}
+                "bytes_per_launch": int8_linear_bytes(1, *dom), "us_per_launch": round(us_dom, 2)}
 
     if not args.no_detail:
         # ---------------- prefill: M=2048 MFMA-bound shapes ----------------

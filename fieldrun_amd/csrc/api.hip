@@ -118,7 +118,10 @@ int run_i8(frq_ctx* c, const Weight& w, const float* d_a, size_t m, float* d_out
         if (d_acc) HIPCHK(hipMemsetAsync(d_acc, 0, m * w.n * sizeof(int32_t), c->stream), "hipMemsetAsync");
         return FRQ_OK;
     }
-    if (!gemm) {
+    if (m == 1 && linear_m1_ok(w, d_a)) {
+        HIPCHK(launch_linear_m1(w, d_a, d_out, d_acc, a8o ? a8 : nullptr, sa, oi, ov, c->err, c->stream),
+               "launch linear_m1");
+    } else if (!gemm) {
         HIPCHK(launch_quant(d_a, m, w.k, w.kp, a8, sa, oi, ov, c->err, c->stream), "launch quant");
         HIPCHK(launch_gemv_i8(w, m, a8, sa, oi, ov, d_out, d_acc, c->stream), "launch gemv_i8");
     } else {

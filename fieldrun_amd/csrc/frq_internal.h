@@ -142,6 +142,14 @@ hipError_t launch_gemv_i8(const Weight& w, size_t m, const int8_t* a8,
                           const float* sa, const uint32_t* oidx,
                           const float* oval, float* out, int32_t* acc,
                           hipStream_t s);
+// The whole int8 linear for one row (quant fused into the GEMV) when
+// linear_m1_ok: K > 32, K % 4 == 0, a 16-byte aligned, Kp <= 20480.  a8o (Kp
+// bytes, row-major) / sao / oio / ovo receive the quantisation when a8o is
+// set; gmax caps the persistent grid (0: the default for the shape).
+bool linear_m1_ok(const Weight& w, const float* a);
+hipError_t launch_linear_m1(const Weight& w, const float* a, float* out, int32_t* acc,
+                            int8_t* a8o, float* sao, uint32_t* oio, float* ovo, int* err,
+                            hipStream_t s, int gmax = 0);
 // (valid rows of an (R, kp) row-major int8 matrix, pitch) -> blocked
 // (blk_off, R rows); rows >= valid become zero.
 hipError_t launch_blockify(const int8_t* src, size_t valid, size_t R, size_t kp,

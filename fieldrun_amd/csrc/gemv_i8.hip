@@ -14,7 +14,9 @@
 // per token row, and reduce across the wave with DPP/shuffles and across the
 // group's waves through LDS.  The activations (M x Kp bytes) sit in LDS and
 // each 16-byte activation chunk is reused for the R weight rows.
-#include "frq_internal.h"
+#include "quant_core.h"
+
+#include <algorithm>
 
 namespace frq {
 
@@ -375,6 +377,168 @@ hipError_t launch_v3_m1(const Weight& w, const int8_t* a8, const float* sa,
     return launch_m<1>(w, a8, sa, oidx, oval, out, acc, s);
 }
 
+// ---------------------------------------------------------------------------
+// Fused M == 1 linear: activation quant + GEMV v3 in one launch.  Every
+// workgroup issues the loads of its first weight row group(s), reads the f32
+// activation row (K*4 bytes: L2 hits after the first workgroups) and runs
+// quant_core.h's selection and quantisation on it — the routine of the
+// standalone quant kernel, so all workgroups hold the same a8 / sa /
+// outliers bit for bit without communicating — then streams its row groups
+// as gemv3 does.  Workgroup 0 also writes a8 / sa / outliers when asked.
+// LDS: the bitmap, then one region that holds the candidate keys, then the
+// quantised row, then (with DB) the correction products.  Without DB (long
+// rows) the activation chunks are read from the quantised row in LDS at each
+// group instead of being held in registers, and the products follow it.
+// bytes of the fused linear's candidate-key / quantised-row region
+__host__ __device__ inline size_t lm1_urow(size_t kp) {
+    return kp > (size_t)qc::FCAP * 8 ? kp : (size_t)qc::FCAP * 8;
+}
+
+template <int L, int CPL, bool DB, int NV4>
+__global__ __launch_bounds__(256) void linear_m1_kernel(
+    const int8_t* __restrict__ W, const int8_t* __restrict__ Wkn,
+    const float* __restrict__ scale, int N, int Np, int Kp, int K,
+    const float* __restrict__ A, float* __restrict__ out, int32_t* __restrict__ acc_dbg,
+    int8_t* __restrict__ a8o, float* __restrict__ sao, uint32_t* __restrict__ oio,
+    float* __restrict__ ovo, int* __restrict__ err, int n_rg) {
+    constexpr int RPP = 256 / L;
+    constexpr int NQW = FRQ_T * (RPP / 4);  // outlier words per group
+    __shared__ qc::RowLds Q;
+    __shared__ int accs[2][RPP];
+    extern __shared__ __align__(16) unsigned char dyn[];
+    const int nbw = Kp >> 5;  // Kp % 128 == 0
+    uint32_t* bitmap = reinterpret_cast<uint32_t*>(dyn);
+    unsigned char* U = dyn + 4 * nbw;
+
+    const int tid = threadIdx.x;
+    const int sub = tid % L, rloc = tid / L;
+    const int nch = Kp >> 4, K4 = K >> 2;
+    const int G = (int)gridDim.x;
+    int rg = blockIdx.x;
+    int4 w[CPL], wn[DB ? CPL : 1];
+    // chunks past the row are clamped, not skipped (no branches between the
+    // loads); the activation chunk they meet is zero
+    auto load_w = [&](int g, int4* dst) {
+        const int8_t* wr = W + (size_t)(g * RPP + rloc) * Kp;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i)
+            dst[i] = *reinterpret_cast<const int4*>(wr + 16 * min(sub + L * i, nch - 1));
+    };
+    // the activation row first (loads retire in issue order), then the
+    // weight stream, in flight during the quant
+    // (rg < n_rg: the grid is at most n_rg; a workgroup without a second
+    // group loads the last one, shared in L2, so that no branch separates
+    // these loads from the row's and the quant waits for the row only)
+    float4 v[NV4];
+    qc::row_load<NV4>(A, K4, v);
+    load_w(rg, w);
+    if (DB) load_w(min(rg + G, n_rg - 1), wn);
+    const qc::RowSel s = qc::row_select<NV4>(A, K, v, Q, reinterpret_cast<unsigned long long*>(U),
+                                             bitmap, nbw);
+    uint32_t* a8w = reinterpret_cast<uint32_t*>(U);  // the candidate keys are dead
+    if (s.nan) {
+        // the reference panics; the call reports FRQ_ERR_NAN and computes on
+        // the standalone quant's placeholders (a8 = 0, sa = 1, zero outliers)
+        for (int i4 = tid; i4 < K4; i4 += 256) a8w[i4] = 0u;
+    } else {
+        qc::row_quantize<NV4>(v, K4, bitmap, s.sa, s.fast, [&](int i4, uint32_t x) { a8w[i4] = x; });
+    }
+    for (int i4 = K4 + tid; i4 < (Kp >> 2); i4 += 256) a8w[i4] = 0u;
+    __syncthreads();
+    const float sam = s.sa;
+    if (blockIdx.x == 0) {
+        if (s.nan && tid == 0) atomicOr(err, 1);
+        if (a8o) {
+            for (int c = tid; c < nch; c += 256)
+                reinterpret_cast<int4*>(a8o)[c] = reinterpret_cast<const int4*>(U)[c];
+            if (tid < FRQ_T) { oio[tid] = Q.sel_i[tid]; ovo[tid] = Q.sel_v[tid]; }
+            if (tid == 0) sao[0] = sam;
+        }
+    }
+    const int4* xs = reinterpret_cast<const int4*>(U);
+    int4 x[DB ? CPL : 1];
+    if (DB) {
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            const int c = sub + L * i;
+            x[i] = c < nch ? xs[c] : make_int4(0, 0, 0, 0);
+        }
+    }
+    // outlier word this thread fetches each group: channel q, rows 4*r4..
+    const int q = tid % FRQ_T, r4 = tid / FRQ_T;
+    const bool qw = tid < NQW;
+    const uint32_t chq = qw ? min(Q.sel_i[q], (uint32_t)(Kp - 1)) : 0u;
+    const float ovq = qw ? Q.sel_v[q] : 0.0f;
+    if (DB) __syncthreads();  // U holds the correction products from here on
+    float (*prod)[RPP][FRQ_T + 1] = reinterpret_cast<float (*)[RPP][FRQ_T + 1]>(
+        DB ? U : U + lm1_urow(Kp));
+    auto load_o = [&](int g) -> uint32_t {
+        return qw ? *reinterpret_cast<const uint32_t*>(Wkn + (size_t)chq * Np + g * RPP + 4 * r4) : 0u;
+    };
+    uint32_t ow = 0, own = 0;
+    if (rg < n_rg) ow = load_o(rg);
+    if (DB && rg + G < n_rg) own = load_o(rg + G);
+    int buf = 0;
+    bool first = true;
+    while (rg < n_rg) {
+        const int rgn = rg + G;
+        if (DB && !first && rgn < n_rg) {
+            load_w(rgn, wn);
+            own = load_o(rgn);
+        }
+        first = false;
+        int acc = 0;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            const int c = sub + L * i;
+            acc = dot16(DB ? x[i] : (c < nch ? xs[c] : make_int4(0, 0, 0, 0)), w[i], acc);
+        }
+#pragma unroll
+        for (int off = L / 2; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+        if (sub == 0) accs[buf][rloc] = acc;
+        if (qw) {
+#pragma unroll
+            for (int b = 0; b < 4; ++b) prod[buf][4 * r4 + b][q] = ovq * (float)(int8_t)(ow >> (8 * b));
+        }
+        __syncthreads();
+        if (tid < RPP) {
+            const int j = rg * RPP + tid;
+            if (j < N) {
+                float corr = -0.0f;
+#pragma unroll
+                for (int qq = 0; qq < FRQ_T; ++qq) corr = corr + prod[buf][tid][qq];
+                const int total = accs[buf][tid];
+                out[j] = scale[j] * (sam * (float)total + corr);
+                if (acc_dbg) acc_dbg[j] = total;
+            }
+        }
+        buf ^= 1;
+        if (DB) {
+#pragma unroll
+            for (int i = 0; i < CPL; ++i) w[i] = wn[i];
+            ow = own;
+        } else if (rgn < n_rg) {
+            load_w(rgn, w);
+            ow = load_o(rgn);
+        }
+        rg = rgn;
+    }
+}
+
+template <int L, int CPL, bool DB, int NV4>
+hipError_t launch_lm1(const Weight& w, const float* a, float* out, int32_t* acc, int8_t* a8o,
+                      float* sao, uint32_t* oio, float* ovo, int* err, int gmax, hipStream_t s) {
+    constexpr int RPP = 256 / L;
+    const int n_rg = (int)((w.n + RPP - 1) / RPP);  // rows < Np (RPP divides 256)
+    const int grid = n_rg < gmax ? n_rg : gmax;
+    const size_t prod = (size_t)2 * RPP * (FRQ_T + 1) * 4;
+    const size_t lds = w.kp / 8 + (DB ? std::max(lm1_urow(w.kp), prod) : lm1_urow(w.kp) + prod);
+    linear_m1_kernel<L, CPL, DB, NV4><<<dim3((unsigned)grid), dim3(256), lds, s>>>(
+        w.wt, w.wkn, w.scale, (int)w.n, (int)w.np, (int)w.kp, (int)w.k, a, out, acc, a8o, sao, oio,
+        ovo, err, n_rg);
+    return hipGetLastError();
+}
+
 template <int M>
 hipError_t launch_v2_m(const Weight& w, const int8_t* a8, const float* sa,
                        const uint32_t* oidx, const float* oval, float* out,
@@ -404,6 +568,26 @@ hipError_t launch_gemv_i8(const Weight& w, size_t m, const int8_t* a8,
         case 4: return launch_v2_m<4>(w, a8, sa, oidx, oval, out, acc, s);
         default: return hipErrorInvalidValue;
     }
+}
+
+bool linear_m1_ok(const Weight& w, const float* a) {
+    return w.k > FRQ_T && w.k % 4 == 0 && ((uintptr_t)a & 15) == 0 && w.kp / 16 <= 1280;
+}
+
+hipError_t launch_linear_m1(const Weight& w, const float* a, float* out, int32_t* acc,
+                            int8_t* a8o, float* sao, uint32_t* oio, float* ovo, int* err,
+                            hipStream_t s, int gmax) {
+    if (!linear_m1_ok(w, a)) return hipErrorInvalidValue;
+    const size_t nch = w.kp / 16;
+    // grid caps: about the workgroups resident at once (256 CUs times the
+    // occupancy each variant's registers allow), measured best on MI355X
+    const int g = gmax;
+    if (nch <= 64) return launch_lm1<8, 8, true, 1>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 768, s);
+    if (nch <= 128) return launch_lm1<64, 2, true, 2>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 1024, s);
+    if (nch <= 256) return launch_lm1<64, 4, true, 4>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 1024, s);
+    if (nch <= 512) return launch_lm1<64, 8, true, 8>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 512, s);
+    if (nch <= 1024) return launch_lm1<64, 16, false, 16>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 256, s);
+    return launch_lm1<64, 20, false, 20>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 256, s);
 }
 
 }  // namespace frq

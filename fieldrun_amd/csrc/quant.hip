@@ -1,133 +1,30 @@
 // quant.hip — outlier-aware per-token int8 activation quant (gfx950).
 //
 // Restates the I8 arm's activation quant of Bundle::mm
-// (/root/reference/src/bundle.rs:691, 699-708 == 732-743; OUTLIER_T 309):
-//   t        = min(32, K)
-//   bulk_max = the (t+1)-th largest |a| of the row (0 when t == K)
-//   sa       = bulk_max > 0 ? bulk_max / 127 : 1          (IEEE f32 divide)
-//   a8[k]    = clamp(round(a[k] / sa) as i32, -127, 127)  (round half away)
-//   the t largest-|a| channels get a8 = 0 and are kept as (idx, a) outliers.
-// Ties at |a| == bulk_max, which the reference leaves to
-// select_nth_unstable_by, go to the lowest channel index; outliers are listed
-// in ascending channel order.  A NaN in a row with t < K is the reference's
-// partial_cmp().unwrap() panic: the kernel raises *err.
+// (/root/reference/src/bundle.rs:691, 699-708 == 732-743; OUTLIER_T 309);
+// the rule, tie order and outlier order are stated in quant_core.h.  A NaN
+// in a row with t < K is the reference's partial_cmp().unwrap() panic: the
+// kernel raises *err.
 //
 // One workgroup per row; HBM traffic is one read of the f32 row and one
 // write of the i8 row.  The (t+1)-th largest is found without a full sort.
-//
 // quant_rows_fast (K % 4 == 0, 32 < K <= 20480, 16-byte aligned rows; every
-// shape of the hot path): 256 threads, the row held in registers (float4
-// loads, one coalesced sweep).
-//   1. each thread's max |a|;
-//   2. tau0 = the 33rd largest thread max: every wave sorts its 64 maxima
-//      with a bitonic network on DPP / permlane lane exchanges, wave 0
-//      merges the four lists keeping the top 64.  At least t+1 elements are
-//      >= tau0, so bulk_max >= tau0;
-//   3. the elements >= tau0 (a few dozen on real rows) are compacted into
-//      per-wave LDS regions with ballot + mbcnt (no atomics) as
-//      (|a| << 32 | ~channel) keys; up to 64 are sorted in one wave, up to
-//      2048 are ranked by counting, and beyond that (constant rows) a radix
-//      select over the row gives bulk_max;
-//   4. the t outliers (|a| > bulk_max, then ties at bulk_max lowest channel
-//      first) are put in channel order by a wave sort and marked in an LDS
-//      bitmap;
-//   5. a8 = round(a / sa) from the registers, the quotient taken as a
-//      Markstein-corrected product with RN(1/sa), packed four to a word, the
-//      outlier slots zero, written once, coalesced.
+// shape of the hot path): the row in registers, quant_core.h's row_select and
+// row_quantize, the a8 row written once, coalesced.
 // quant_rows (any other K or alignment): the same steps from global memory
 // with LDS radix selects (four 8-bit MSB-first digit passes) and block scans,
 // and an IEEE divide.
-// |a| is compared as its IEEE bit pattern, which orders non-negative floats.
-#include "frq_internal.h"
+#include "quant_core.h"
 
 namespace frq {
 
 namespace {
 
+using qc::absbits;
+using qc::block_excl_scan;
+using qc::radix_select_desc;
+
 constexpr int CAP = 1024;
-
-__device__ __forceinline__ uint32_t absbits(float v) {
-    return __float_as_uint(v) & 0x7FFFFFFFu;
-}
-
-// Exclusive scan of one uint per thread across the block; *total gets the sum.
-template <int BLOCK>
-__device__ uint32_t block_excl_scan(uint32_t v, uint32_t* lds /*BLOCK/64+1*/,
-                                    uint32_t* total) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    uint32_t incl = v;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        uint32_t y = __shfl_up(incl, off, 64);
-        if (lane >= off) incl += y;
-    }
-    if (lane == 63) lds[wave] = incl;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t run = 0;
-        for (int w = 0; w < BLOCK / 64; ++w) {
-            uint32_t c = lds[w];
-            lds[w] = run;
-            run += c;
-        }
-        lds[BLOCK / 64] = run;
-    }
-    __syncthreads();
-    uint32_t r = lds[wave] + incl - v;
-    *total = lds[BLOCK / 64];
-    __syncthreads();
-    return r;
-}
-
-// Value of descending rank `rank` (0 = largest) among n non-negative float
-// bit patterns given by get(i).  Four 8-bit MSB-first digit passes.
-template <int BLOCK, typename Get>
-__device__ uint32_t radix_select_desc(Get get, int n, uint32_t rank,
-                                      uint32_t* hist, uint32_t* bc) {
-    uint32_t prefix = 0, mask = 0;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-        for (int i = threadIdx.x; i < 256; i += BLOCK) hist[i] = 0;
-        __syncthreads();
-        for (int i = threadIdx.x; i < n; i += BLOCK) {
-            uint32_t v = get(i);
-            if ((v & mask) == prefix) atomicAdd(&hist[(v >> shift) & 255u], 1u);
-        }
-        __syncthreads();
-        if (threadIdx.x < 64) {
-            const int lane = threadIdx.x;
-            // lane owns digits 255-4l .. 252-4l (descending order)
-            uint32_t h0 = hist[255 - 4 * lane], h1 = hist[254 - 4 * lane];
-            uint32_t h2 = hist[253 - 4 * lane], h3 = hist[252 - 4 * lane];
-            uint32_t s = h0 + h1 + h2 + h3, incl = s;
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                uint32_t y = __shfl_up(incl, off, 64);
-                if (lane >= off) incl += y;
-            }
-            uint32_t c = incl - s;
-            if (c <= rank && rank < incl) {
-                int d;
-                if (rank < c + h0) {
-                    d = 255 - 4 * lane;
-                } else if (rank < c + h0 + h1) {
-                    c += h0; d = 254 - 4 * lane;
-                } else if (rank < c + h0 + h1 + h2) {
-                    c += h0 + h1; d = 253 - 4 * lane;
-                } else {
-                    c += h0 + h1 + h2; d = 252 - 4 * lane;
-                }
-                bc[0] = (uint32_t)d;
-                bc[1] = c;
-            }
-        }
-        __syncthreads();
-        prefix |= bc[0] << shift;
-        mask |= 255u << shift;
-        rank -= bc[1];
-        __syncthreads();
-    }
-    return prefix;
-}
 
 template <int BLOCK>
 __global__ __launch_bounds__(BLOCK) void quant_rows(
@@ -268,302 +165,42 @@ __global__ __launch_bounds__(BLOCK) void quant_rows(
 }
 
 // ---------------------------------------------------------------------------
-// Fast path: K % 4 == 0, 32 < K <= BLOCK * NV4 * 4.  The row stays in
-// registers (float4 loads); the (t+1)-th largest is found from a handful of
-// candidates and the quotient a/sa uses r = RN(1/sa) plus one FMA residual
-// correction (Markstein: RN(q + (a - q*sa)*r) == RN(a/sa) for r = RN(1/sa)
-// away from under/overflow), which rows with extreme sa bypass.
-
-// Bitonic networks across the 64-lane wave on VALU lane exchanges.
-template <int J, int K, bool DESC, typename T, typename X>
-__device__ __forceinline__ T bstage(T x, X xs) {
-    const int lane = threadIdx.x & 63;
-    const T y = xs(x);
-    const bool lower = !(lane & J), dir = !(lane & K);
-    const bool keep_big = DESC ? (lower == dir) : (lower != dir);
-    return keep_big ? (x > y ? x : y) : (x < y ? x : y);
-}
-
-template <bool DESC, typename T, typename X1, typename X2, typename X4, typename X8, typename X16,
-          typename X32>
-__device__ __forceinline__ T bitonic64(T x, X1 s1, X2 s2, X4 s4, X8 s8, X16 s16, X32 s32) {
-    x = bstage<1, 2, DESC>(x, s1);
-    x = bstage<2, 4, DESC>(x, s2); x = bstage<1, 4, DESC>(x, s1);
-    x = bstage<4, 8, DESC>(x, s4); x = bstage<2, 8, DESC>(x, s2); x = bstage<1, 8, DESC>(x, s1);
-    x = bstage<8, 16, DESC>(x, s8); x = bstage<4, 16, DESC>(x, s4); x = bstage<2, 16, DESC>(x, s2);
-    x = bstage<1, 16, DESC>(x, s1);
-    x = bstage<16, 32, DESC>(x, s16); x = bstage<8, 32, DESC>(x, s8); x = bstage<4, 32, DESC>(x, s4);
-    x = bstage<2, 32, DESC>(x, s2); x = bstage<1, 32, DESC>(x, s1);
-    x = bstage<32, 64, DESC>(x, s32); x = bstage<16, 64, DESC>(x, s16); x = bstage<8, 64, DESC>(x, s8);
-    x = bstage<4, 64, DESC>(x, s4); x = bstage<2, 64, DESC>(x, s2); x = bstage<1, 64, DESC>(x, s1);
-    return x;
-}
-
-__device__ __forceinline__ uint32_t wave_sort_desc(uint32_t x) {
-    return bitonic64<true>(x, xshfl<1>, xshfl<2>, xshfl<4>, xshfl<8>, xshfl<16>, xshfl<32>);
-}
-__device__ __forceinline__ uint32_t wave_sort_asc(uint32_t x) {
-    return bitonic64<false>(x, xshfl<1>, xshfl<2>, xshfl<4>, xshfl<8>, xshfl<16>, xshfl<32>);
-}
-__device__ __forceinline__ unsigned long long wave_sort_desc64(unsigned long long x) {
-    return bitonic64<true>(x, xshfl64<1>, xshfl64<2>, xshfl64<4>, xshfl64<8>, xshfl64<16>,
-                           xshfl64<32>);
-}
-
-// Top 64 of two descending 64-lists, a in lane order and b reversed
-// (lane l holds b[63-l]): max() forms a bitonic sequence, the half-cleaners
-// sort it descending.
-__device__ __forceinline__ uint32_t merge_top64(uint32_t a, uint32_t b_rev) {
-    uint32_t c = max(a, b_rev);
-    c = bstage<32, 64, true>(c, xshfl<32>);
-    c = bstage<16, 64, true>(c, xshfl<16>);
-    c = bstage<8, 64, true>(c, xshfl<8>);
-    c = bstage<4, 64, true>(c, xshfl<4>);
-    c = bstage<2, 64, true>(c, xshfl<2>);
-    c = bstage<1, 64, true>(c, xshfl<1>);
-    return c;
-}
-
-// round(q) half away from zero (Rust f32::round), clamped to [-127, 127];
-// q finite.  trunc + exact fraction: |q - trunc(q)| is exact in f32.
-__device__ __forceinline__ uint32_t rq8(float q) {
-    const float t = __builtin_truncf(q);
-    const float r = __builtin_fabsf(q - t) >= 0.5f ? t + __builtin_copysignf(1.0f, q) : t;
-    return (uint32_t)(uint8_t)(int8_t)(int)__builtin_amdgcn_fmed3f(r, -127.0f, 127.0f);
-}
-
-// RN(a / sa) by r = RN(1/sa) and one FMA residual correction (Markstein).
-__device__ __forceinline__ float qdiv_fast(float a, float sa, float r) {
-    const float q = a * r;
-    const float e = __builtin_fmaf(-q, sa, a);
-    return __builtin_fmaf(e, r, q);
-}
-
-// Exact path for rows outside the fast path's range (IEEE divide; Rust `as
-// i32` saturation maps NaN to 0).
-__device__ __forceinline__ uint32_t q8_slow(float a, float sa) {
-    const float x = __builtin_roundf(a / sa);
-    return (x != x) ? 0u : (uint32_t)(uint8_t)(int8_t)(x < -127.0f ? -127 : (x > 127.0f ? 127 : (int)x));
-}
-
-constexpr int FCAP = 2048;
-
-template <int BLOCK, int NV4>
-__global__ __launch_bounds__(BLOCK) void quant_rows_fast(
+// Fast path: K % 4 == 0, 32 < K <= 1024 * NV4, 16-byte aligned rows.
+template <int NV4>
+__global__ __launch_bounds__(qc::BLOCK) void quant_rows_fast(
     const float* __restrict__ A, int K, int Kp, int8_t* __restrict__ a8,
     float* __restrict__ sa_out, uint32_t* __restrict__ oidx,
     float* __restrict__ oval, int* __restrict__ err, int mpb) {
-    constexpr int NW = BLOCK / 64;
-    __shared__ uint32_t wsorted[NW][64];
-    __shared__ uint32_t tau_s[2];
-    __shared__ uint32_t wcnt_s[NW];
-    __shared__ unsigned long long cand[FCAP];
-    __shared__ unsigned long long top[FRQ_T + 1];
-    __shared__ uint32_t hist[256];
-    __shared__ uint32_t bc[2];
-    __shared__ uint32_t scan_lds[NW + 1];
-    __shared__ uint32_t sel_i[FRQ_T];
+    __shared__ qc::RowLds L;
+    __shared__ unsigned long long cand[qc::FCAP];
     extern __shared__ uint32_t bitmap[];  // ceil(Kp/32) words
 
     const int row = blockIdx.x, tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
     const float* a = A + (size_t)row * K;
     // a8 byte k of this row: row-major (pitch Kp) or blocked (R = mpb)
     auto qa = [&](int k) -> int8_t* {
         return mpb ? a8 + blk_off((size_t)row, (size_t)k, (size_t)mpb) : a8 + (size_t)row * Kp + k;
     };
     const int K4 = K >> 2;
-
     float4 v[NV4];
-#pragma unroll
-    for (int i = 0; i < NV4; ++i) {  // unconditional loads (clamped), then mask
-        const int i4 = tid + BLOCK * i;
-        v[i] = reinterpret_cast<const float4*>(a)[min(i4, K4 - 1)];
-    }
-    uint32_t mx = 0;  // max |a| bits; NaN shows as > 0x7F800000
-#pragma unroll
-    for (int i = 0; i < NV4; ++i) {
-        if (tid + BLOCK * i >= K4) v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-        mx = max(mx, max(max(absbits(v[i].x), absbits(v[i].y)), max(absbits(v[i].z), absbits(v[i].w))));
-    }
-    const int nan = mx > 0x7F800000u;
-    for (int w = tid; w < (Kp + 31) / 32; w += BLOCK) bitmap[w] = 0u;
-    if (tid < FRQ_T) sel_i[tid] = 0u;
-    if (__syncthreads_or(nan)) {
-        if (tid == 0) { atomicOr(err, 1); sa_out[row] = 1.0f; }
-        for (int k = tid; k < Kp; k += BLOCK) *qa(k) = 0;
-        if (tid < FRQ_T) {
-            oidx[(size_t)row * FRQ_T + tid] = (uint32_t)tid;
-            oval[(size_t)row * FRQ_T + tid] = 0.0f;
-        }
-        return;
-    }
-    // threshold tau = the 33rd largest thread maximum (per-wave bitonic sorts,
-    // merged in wave 0): at least 33 elements are >= tau, so every element
-    // above the (t+1)-th largest |a| is >= tau, and for iid rows only a few
-    // dozen elements pass
-    static_assert(NW == 4, "the threshold merge assumes 4 waves");
-    wsorted[wave][lane] = wave_sort_desc(mx);
-    __syncthreads();
-    if (wave == 0) {
-        const uint32_t x = merge_top64(wsorted[0][lane], wsorted[1][63 - lane]);
-        const uint32_t y = merge_top64(wsorted[2][lane], wsorted[3][63 - lane]);
-        const uint32_t z = merge_top64(x, __shfl(y, 63 - lane, 64));
-        if (lane == FRQ_T) tau_s[0] = z;
-        if (lane == 0) tau_s[1] = z;
-    }
-    __syncthreads();
-    const uint32_t tau = tau_s[0], rowmax = tau_s[1];
-    // compact candidates: key = |a| bits << 32 | ~index (unique; larger key =
-    // larger |a|, ties to the lower index)
-    // per-wave regions of cand[] (FCAP/4 keys each), offsets from ballots
-    constexpr int WCAP = FCAP / NW;
-    uint32_t wcount = 0;
-#pragma unroll
-    for (int i = 0; i < NV4; ++i) {
-        const uint32_t b0 = absbits(v[i].x), b1 = absbits(v[i].y);
-        const uint32_t b2 = absbits(v[i].z), b3 = absbits(v[i].w);
-        const bool any = max(max(b0, b1), max(b2, b3)) >= tau;
-        if (__builtin_amdgcn_ballot_w64(any)) {  // rare: wave-uniform skip
-            const uint32_t base = 4u * (uint32_t)(tid + BLOCK * i);
-            const uint32_t bb[4] = {b0, b1, b2, b3};
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const bool hit = bb[c] >= tau && base + c < (uint32_t)K;
-                const unsigned long long m = __builtin_amdgcn_ballot_w64(hit);
-                const uint32_t below = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
-                                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-                const uint32_t slot = wcount + below;
-                if (hit && slot < (uint32_t)WCAP)
-                    cand[wave * WCAP + slot] = ((unsigned long long)bb[c] << 32) | (0xFFFFFFFFu - (base + c));
-                wcount += (uint32_t)__builtin_popcountll(m);
-            }
-        }
-    }
-    if (lane == 0) wcnt_s[wave] = wcount;
-    __syncthreads();
-    // concatenate the four regions (keys are independent of order)
-    uint32_t wc[NW], woff[NW + 1];
-    bool overflow = false;
-    woff[0] = 0;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-        wc[w] = wcnt_s[w];
-        overflow |= wc[w] > (uint32_t)WCAP;
-        woff[w + 1] = woff[w] + wc[w];
-    }
-    const uint32_t nc = overflow ? (uint32_t)FCAP + 1u : woff[NW];
-    auto cand_at = [&](uint32_t i) -> unsigned long long {
-        int w = 0;
-#pragma unroll
-        for (int x = 1; x < NW; ++x) w += i >= woff[x];
-        return cand[w * WCAP + (i - woff[w])];
-    };
-    uint32_t bulk;
-    if (nc <= 64) {
-        // one wave sorts the candidates' keys; lanes 0..31 are the outliers,
-        // lane 32 holds the (t+1)-th largest
-        if (wave == 0) {
-            const unsigned long long key = wave_sort_desc64(lane < (int)nc ? cand_at(lane) : 0ull);
-            if (lane <= FRQ_T) top[lane] = key;
-        }
-        __syncthreads();
-    } else if (nc <= (uint32_t)FCAP) {
-        // exact rank of every candidate; the 33 largest keys land in top[]
-        for (uint32_t i = tid; i < nc; i += BLOCK) {
-            const unsigned long long key = cand_at(i);
-            uint32_t rank = 0;
-#pragma unroll
-            for (int w = 0; w < NW; ++w)
-                for (uint32_t j = 0; j < wc[w]; ++j) rank += cand[w * WCAP + j] > key;
-            if (rank <= (uint32_t)FRQ_T) top[rank] = key;
-        }
-        __syncthreads();
-    }
-    if (nc <= (uint32_t)FCAP) {
-        bulk = (uint32_t)(top[FRQ_T] >> 32);
-        if (wave == 0) {
-            const uint32_t idx = lane < FRQ_T ? 0xFFFFFFFFu - (uint32_t)(top[lane] & 0xFFFFFFFFu) : 0xFFFFFFFFu;
-            const uint32_t si = wave_sort_asc(idx);
-            if (lane < FRQ_T) {
-                const uint32_t sk = min(si, (uint32_t)(K - 1));
-                sel_i[lane] = sk;
-                atomicOr(&bitmap[sk >> 5], 1u << (sk & 31));
-            }
-        }
+    qc::row_load<NV4>(a, K4, v);
+    const qc::RowSel s = qc::row_select<NV4>(a, K, v, L, cand, bitmap, (Kp + 31) / 32);
+    if (s.nan) {
+        // the reference panics here; the call reports FRQ_ERR_NAN.  In-bounds
+        // placeholders (a8 = 0, sa = 1, outliers 0..31 with value 0) keep the
+        // kernels queued after this one on valid data.
+        if (tid == 0) atomicOr(err, 1);
+        for (int i4 = tid; i4 < K4; i4 += qc::BLOCK) *reinterpret_cast<uint32_t*>(qa(4 * i4)) = 0u;
     } else {
-        // many near-equal magnitudes (e.g. constant rows): exact select over
-        // the row in global memory, outliers by ordered chunks
-        bulk = radix_select_desc<BLOCK>([&](int i) { return absbits(a[i]); }, K,
-                                        (uint32_t)FRQ_T, hist, bc);
-        const int C = (K + BLOCK - 1) / BLOCK;
-        const int lo = tid * C, hi = min(lo + C, K);
-        uint32_t gt = 0, ties = 0;
-        for (int k = lo; k < hi; ++k) {
-            const uint32_t b = absbits(a[k]);
-            gt += b > bulk;
-            ties += b == bulk;
-        }
-        uint32_t gt_total, ties_total, sel_total;
-        block_excl_scan<BLOCK>(gt, scan_lds, &gt_total);
-        const uint32_t tie_base = block_excl_scan<BLOCK>(ties, scan_lds, &ties_total);
-        const uint32_t need = gt_total < (uint32_t)FRQ_T ? (uint32_t)FRQ_T - gt_total : 0u;
-        const uint32_t take = need > tie_base ? min(need - tie_base, ties) : 0u;
-        uint32_t pos = block_excl_scan<BLOCK>(gt + take, scan_lds, &sel_total);
-        if (gt + take) {
-            uint32_t seen = 0;
-            for (int k = lo; k < hi; ++k) {
-                const uint32_t b = absbits(a[k]);
-                bool s = b > bulk;
-                if (b == bulk) { s = seen < take; seen++; }
-                if (s && pos < (uint32_t)FRQ_T) {
-                    sel_i[pos++] = (uint32_t)k;
-                    atomicOr(&bitmap[k >> 5], 1u << (k & 31));
-                }
-            }
-        }
+        qc::row_quantize<NV4>(v, K4, bitmap, s.sa, s.fast,
+                              [&](int i4, uint32_t w) { *reinterpret_cast<uint32_t*>(qa(4 * i4)) = w; });
     }
-    __syncthreads();
-    const float bulkf = __uint_as_float(bulk);
-    const float sa = bulkf > 0.0f ? bulkf / 127.0f : 1.0f;
-    const float r = 1.0f / sa;
-    // Markstein correction needs no under/overflow in q*sa and the residual
-    const bool fast = sa >= 1e-30f && sa <= 1e30f && rowmax < 0x7A800000u;  // |a| < 2^118
-    if (fast) {
-#pragma unroll
-        for (int i = 0; i < NV4; ++i) {
-            const int i4 = tid + BLOCK * i;
-            if (i4 < K4) {
-                const int base = 4 * i4;
-                const uint32_t bw = bitmap[base >> 5] >> (base & 31);
-                uint32_t w = rq8(qdiv_fast(v[i].x, sa, r));
-                w |= rq8(qdiv_fast(v[i].y, sa, r)) << 8;
-                w |= rq8(qdiv_fast(v[i].z, sa, r)) << 16;
-                w |= rq8(qdiv_fast(v[i].w, sa, r)) << 24;
-                const uint32_t keep = ((bw & 1u) ? 0u : 0xFFu) | ((bw & 2u) ? 0u : 0xFF00u) |
-                                      ((bw & 4u) ? 0u : 0xFF0000u) | ((bw & 8u) ? 0u : 0xFF000000u);
-                *reinterpret_cast<uint32_t*>(qa(4 * i4)) = w & keep;
-            }
-        }
-    } else {
-        for (int i4 = tid; i4 < K4; i4 += BLOCK) {
-            const float4 x = reinterpret_cast<const float4*>(a)[i4];
-            const int base = 4 * i4;
-            const uint32_t bw = bitmap[base >> 5] >> (base & 31);
-            const uint32_t b0 = (bw & 1u) ? 0u : q8_slow(x.x, sa);
-            const uint32_t b1 = (bw & 2u) ? 0u : q8_slow(x.y, sa);
-            const uint32_t b2 = (bw & 4u) ? 0u : q8_slow(x.z, sa);
-            const uint32_t b3 = (bw & 8u) ? 0u : q8_slow(x.w, sa);
-            *reinterpret_cast<uint32_t*>(qa(4 * i4)) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
-        }
-    }
-    for (int i4 = K4 + tid; i4 < Kp / 4; i4 += BLOCK) *reinterpret_cast<uint32_t*>(qa(4 * i4)) = 0u;
+    for (int i4 = K4 + tid; i4 < Kp / 4; i4 += qc::BLOCK) *reinterpret_cast<uint32_t*>(qa(4 * i4)) = 0u;
     if (tid < FRQ_T) {
-        const uint32_t k = sel_i[tid];
-        oidx[(size_t)row * FRQ_T + tid] = k;
-        oval[(size_t)row * FRQ_T + tid] = a[k];
+        oidx[(size_t)row * FRQ_T + tid] = L.sel_i[tid];
+        oval[(size_t)row * FRQ_T + tid] = L.sel_v[tid];
     }
-    if (tid == 0) sa_out[row] = sa;
+    if (tid == 0) sa_out[row] = s.sa;
 }
 
 }  // namespace
@@ -571,7 +208,7 @@ __global__ __launch_bounds__(BLOCK) void quant_rows_fast(
 template <int NV4>
 static void launch_fast(const float* a, size_t m, size_t k, size_t kp, int8_t* a8, float* sa,
                         uint32_t* oidx, float* oval, int* err, size_t lds, hipStream_t s, int mpb) {
-    quant_rows_fast<256, NV4><<<dim3((unsigned)m), dim3(256), lds, s>>>(
+    quant_rows_fast<NV4><<<dim3((unsigned)m), dim3(256), lds, s>>>(
         a, (int)k, (int)kp, a8, sa, oidx, oval, err, mpb);
 }
 
