@@ -389,6 +389,21 @@ hipError_t launch_v3_m1(const Weight& w, const int8_t* a8, const float* sa,
 // quantised row, then (with DB) the correction products.  Without DB (long
 // rows) the activation chunks are read from the quantised row in LDS at each
 // group instead of being held in registers, and the products follow it.
+// Group order of the fused linear's grid-stride loop.  Workgroup b runs on
+// XCD b % 8 (round-robin dispatch) and visits virtual groups v = b + i*G
+// (G % 8 == 0, or a single visit), so v % 8 names the XCD.  The outlier
+// gather reads RPP bytes per channel per group from the (K, Np) copy; a
+// 128-byte line spans S = 128 / RPP consecutive groups.  Within each chunk
+// of 8 S groups, XCD x takes the S consecutive groups x S .. x S + S - 1, so
+// every line of the gather is fetched by one XCD, once; the partial chunk
+// at the end keeps the identity order.
+template <int RPP>
+__device__ __forceinline__ int xcd_group(int v, int n_rg) {
+    constexpr int S = 128 / RPP, C = 8 * S;
+    const int c = v / C, j = v % C;
+    return (c + 1) * C <= n_rg ? c * C + (j % 8) * S + j / 8 : v;
+}
+
 // bytes of the fused linear's candidate-key / quantised-row region
 __host__ __device__ inline size_t lm1_urow(size_t kp) {
     return kp > (size_t)qc::FCAP * 8 ? kp : (size_t)qc::FCAP * 8;
@@ -421,8 +436,7 @@ __global__ __launch_bounds__(256) void linear_m1_kernel(
     auto load_w = [&](int g, int4* dst) {
         const int8_t* wr = W + (size_t)(g * RPP + rloc) * Kp;
 #pragma unroll
-        for (int i = 0; i < CPL; ++i)
-            dst[i] = *reinterpret_cast<const int4*>(wr + 16 * min(sub + L * i, nch - 1));
+        for (int i = 0; i < CPL; ++i) dst[i] = ntload16(wr + 16 * min(sub + L * i, nch - 1));
     };
     // the activation row first (loads retire in issue order), then the
     // weight stream, in flight during the quant
@@ -431,8 +445,8 @@ __global__ __launch_bounds__(256) void linear_m1_kernel(
     // these loads from the row's and the quant waits for the row only)
     float4 v[NV4];
     qc::row_load<NV4>(A, K4, v);
-    load_w(rg, w);
-    if (DB) load_w(min(rg + G, n_rg - 1), wn);
+    load_w(xcd_group<RPP>(rg, n_rg), w);
+    if (DB) load_w(xcd_group<RPP>(min(rg + G, n_rg - 1), n_rg), wn);
     const qc::RowSel s = qc::row_select<NV4>(A, K, v, Q, reinterpret_cast<unsigned long long*>(U),
                                              bitmap, nbw);
     uint32_t* a8w = reinterpret_cast<uint32_t*>(U);  // the candidate keys are dead
@@ -475,16 +489,26 @@ __global__ __launch_bounds__(256) void linear_m1_kernel(
     auto load_o = [&](int g) -> uint32_t {
         return qw ? *reinterpret_cast<const uint32_t*>(Wkn + (size_t)chq * Np + g * RPP + 4 * r4) : 0u;
     };
-    uint32_t ow = 0, own = 0;
-    if (rg < n_rg) ow = load_o(rg);
-    if (DB && rg + G < n_rg) own = load_o(rg + G);
+    // the epilogue thread's scale comes with its group's loads (a dependent
+    // load in the epilogue would stall every group behind the barrier)
+    auto load_s = [&](int g) -> float { return tid < RPP ? scale[g * RPP + tid] : 0.0f; };
+    int gc = xcd_group<RPP>(rg, n_rg);  // rg < n_rg: the grid is at most n_rg
+    uint32_t ow = load_o(gc), own = 0;
+    float sc = load_s(gc), scn = 0.0f;
+    if (DB && rg + G < n_rg) {
+        const int g1 = xcd_group<RPP>(rg + G, n_rg);
+        own = load_o(g1);
+        scn = load_s(g1);
+    }
     int buf = 0;
     bool first = true;
     while (rg < n_rg) {
         const int rgn = rg + G;
+        const int gn = rgn < n_rg ? xcd_group<RPP>(rgn, n_rg) : 0;
         if (DB && !first && rgn < n_rg) {
-            load_w(rgn, wn);
-            own = load_o(rgn);
+            load_w(gn, wn);
+            own = load_o(gn);
+            scn = load_s(gn);
         }
         first = false;
         int acc = 0;
@@ -493,6 +517,9 @@ __global__ __launch_bounds__(256) void linear_m1_kernel(
             const int c = sub + L * i;
             acc = dot16(DB ? x[i] : (c < nch ? xs[c] : make_int4(0, 0, 0, 0)), w[i], acc);
         }
+        // single-buffered: the next group's weights go out as soon as the dot
+        // has consumed these, overlapping the reduction and the epilogue
+        if (!DB && rgn < n_rg) load_w(gn, w);
 #pragma unroll
         for (int off = L / 2; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
         if (sub == 0) accs[buf][rloc] = acc;
@@ -500,15 +527,19 @@ __global__ __launch_bounds__(256) void linear_m1_kernel(
 #pragma unroll
             for (int b = 0; b < 4; ++b) prod[buf][4 * r4 + b][q] = ovq * (float)(int8_t)(ow >> (8 * b));
         }
+        if (!DB && rgn < n_rg) {
+            own = load_o(gn);
+            scn = load_s(gn);
+        }
         __syncthreads();
         if (tid < RPP) {
-            const int j = rg * RPP + tid;
+            const int j = gc * RPP + tid;
             if (j < N) {
                 float corr = -0.0f;
 #pragma unroll
                 for (int qq = 0; qq < FRQ_T; ++qq) corr = corr + prod[buf][tid][qq];
                 const int total = accs[buf][tid];
-                out[j] = scale[j] * (sam * (float)total + corr);
+                out[j] = sc * (sam * (float)total + corr);
                 if (acc_dbg) acc_dbg[j] = total;
             }
         }
@@ -516,11 +547,10 @@ __global__ __launch_bounds__(256) void linear_m1_kernel(
         if (DB) {
 #pragma unroll
             for (int i = 0; i < CPL; ++i) w[i] = wn[i];
-            ow = own;
-        } else if (rgn < n_rg) {
-            load_w(rgn, w);
-            ow = load_o(rgn);
         }
+        ow = own;
+        sc = scn;
+        gc = gn;
         rg = rgn;
     }
 }
