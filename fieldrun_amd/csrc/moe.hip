@@ -34,6 +34,8 @@
 //             its orders.
 #include "frq_internal.h"
 
+#include <algorithm>
+
 namespace frq {
 
 namespace {
@@ -102,19 +104,22 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 }
 
 // ---- routing: one wave per token ----------------------------------------
-__global__ __launch_bounds__(256) void route_kernel(
-    const float* __restrict__ logits, int T, int E, int topk, int norm_topk,
-    const float* __restrict__ pes, int32_t* __restrict__ sel,
-    float* __restrict__ wout, int* __restrict__ err) {
-    extern __shared__ float sp[];  // [4][E]
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int t = blockIdx.x * 4 + wv;
-    const bool active = t < T;
-    float* p = sp + wv * E;
-    const float* row = logits + (size_t)(active ? t : 0) * E;
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
+// Routing of one token by one wave: softmax (max, exp, sequential sum,
+// divide), k rounds of arg-max by (p desc, expert asc), renormalised
+// weights.  p: E floats of LDS; picks go to pe / pw (k entries of LDS, pick
+// order).  Returns true (uniformly) when the row holds a NaN: the reference
+// panics; the picks are then experts 0..k-1 with weight 0.
+__device__ bool route_wave(const float* __restrict__ row, int E, int topk, int norm_topk,
+                           const float* __restrict__ pes, float* p, int* pe, float* pw) {
+    const int lane = threadIdx.x & 63;
     float m = -INFINITY;
     int bad = 0;
-    for (int e = lane; e < E && active; e += 64) {
+    for (int e = lane; e < E; e += 64) {
         const float v = row[e];
         bad |= (v != v);
         m = fmaxf(m, v);
@@ -124,30 +129,24 @@ __global__ __launch_bounds__(256) void route_kernel(
         m = fmaxf(m, __shfl_xor(m, off, 64));
         bad |= __shfl_xor(bad, off, 64);
     }
-    // sort_by(partial_cmp().unwrap()) panics on NaN: raise err; the token
-    // gets experts 0..k-1 with weight 0 so the rest of the pipeline stays in
-    // bounds (the call reports FRQ_ERR_NAN)
-    if (active && bad && lane == 0) {
-        atomicOr(err, 1);
-        for (int i = 0; i < topk; ++i) {
-            sel[(size_t)t * topk + i] = i;
-            wout[(size_t)t * topk + i] = 0.0f;
-        }
+    if (bad) {
+        for (int i = lane; i < topk; i += 64) { pe[i] = i; pw[i] = 0.0f; }
+        wave_sync();
+        return true;
     }
-    const bool go = active && !bad;
-    for (int e = lane; e < E && go; e += 64) p[e] = expf(row[e] - m);
-    __syncthreads();
+    for (int e = lane; e < E; e += 64) p[e] = expf(row[e] - m);
+    wave_sync();
     float s = 0.0f;  // sequential sum in expert order, as the reference
-    for (int e = 0; e < E && go; ++e) s = s + p[e];
-    __syncthreads();
-    for (int e = lane; e < E && go; e += 64) p[e] = p[e] / s;
-    __syncthreads();
+    for (int e = 0; e < E; ++e) s = s + p[e];
+    wave_sync();
+    for (int e = lane; e < E; e += 64) p[e] = p[e] / s;
+    wave_sync();
     // k rounds of arg-max by (p desc, e asc); taken experts get p = -1
     float denom = -0.0f;
     for (int i = 0; i < topk; ++i) {
         float bv = -2.0f;
         int be = 0x7FFFFFFF;
-        for (int e = lane; e < E && go; e += 64) {
+        for (int e = lane; e < E; e += 64) {
             const float v = p[e];
             if (v > bv || (v == bv && e < be)) { bv = v; be = e; }
         }
@@ -157,23 +156,42 @@ __global__ __launch_bounds__(256) void route_kernel(
             const int oe = __shfl_xor(be, off, 64);
             if (ov > bv || (ov == bv && oe < be)) { bv = ov; be = oe; }
         }
-        __syncthreads();
-        if (go && lane == 0) {
-            sel[(size_t)t * topk + i] = be;
-            wout[(size_t)t * topk + i] = bv;  // p for now
+        if (lane == 0) {
+            pe[i] = be;
+            pw[i] = bv;
             p[be] = -1.0f;
         }
-        __syncthreads();
+        wave_sync();
         denom = denom + bv;
     }
-    if (go && lane == 0) {
-        const bool renorm = norm_topk || pes != nullptr;
-        for (int i = 0; i < topk; ++i) {
-            const float pv = wout[(size_t)t * topk + i];
-            float wv2 = renorm ? pv / denom : pv;
-            if (pes) wv2 = wv2 * pes[sel[(size_t)t * topk + i]];
-            wout[(size_t)t * topk + i] = wv2;
-        }
+    // renormalised weights, one pick per lane (each the same operations as a
+    // sequential pass)
+    const bool renorm = norm_topk || pes != nullptr;
+    for (int i = lane; i < topk; i += 64) {
+        float w = renorm ? pw[i] / denom : pw[i];
+        if (pes) w = w * pes[pe[i]];
+        pw[i] = w;
+    }
+    wave_sync();
+    return false;
+}
+
+// One wave per token (4 per workgroup); every step stays inside the wave.
+__global__ __launch_bounds__(256) void route_kernel(
+    const float* __restrict__ logits, int T, int E, int topk, int norm_topk,
+    const float* __restrict__ pes, int32_t* __restrict__ sel,
+    float* __restrict__ wout, int* __restrict__ err) {
+    extern __shared__ float sp[];  // [4][E] probabilities, [4][topk] picks (expert, w)
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int t = blockIdx.x * 4 + wv;
+    if (t >= T) return;  // whole waves only
+    int* pe = reinterpret_cast<int*>(sp + 4 * E) + wv * topk;
+    float* pw = sp + 4 * E + 4 * topk + wv * topk;
+    const bool bad = route_wave(logits + (size_t)t * E, E, topk, norm_topk, pes, sp + wv * E, pe, pw);
+    if (bad && lane == 0) atomicOr(err, 1);
+    for (int i = lane; i < topk; i += 64) {
+        sel[(size_t)t * topk + i] = pe[i];
+        wout[(size_t)t * topk + i] = pw[i];
     }
 }
 
@@ -184,7 +202,7 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(
     const int32_t* __restrict__ sel, int T, int topk, int E, int tr,
     MoeWs ws) {
     extern __shared__ uint32_t sm[];
-    const int nwc = TC / 32;
+    const int nwc = (min(T, TC) + 31) / 32;  // bitmap words per expert and chunk
     uint32_t* bm = sm;                     // [E][nwc]
     uint32_t* run = sm + (size_t)E * nwc;  // [E] running count
     uint32_t* pre = run + E;               // [E][nwc] prefix popcounts
@@ -433,6 +451,152 @@ __global__ __launch_bounds__(64 * KS) void moe_mm_kernel(
     }
 }
 
+// ---- decode (T == 1): three launches ---------------------------------------
+// K1: every workgroup (slot s of the k picks in ascending expert id, 16
+// columns of gate or up) routes the token in its wave 0 and builds the
+// token's digit row in LDS itself (a few KB from L2, no launch in between),
+// then runs the digit GEMM of moe_mm_kernel<1,1,4> for its expert and
+// columns; workgroup (0,0) publishes the sorted picks (ws.sel / ws.w) and
+// the row count the act kernel reads.
+__global__ __launch_bounds__(256) void moe_dec_gu_kernel(
+    const float* __restrict__ x, int d, int kpd, const float* __restrict__ logits, int E, int topk,
+    int norm_topk, const float* __restrict__ pes, const int8_t* __restrict__ gate_b, int gwp,
+    const float* __restrict__ gate_s, int gw, const int8_t* __restrict__ gate,
+    const int8_t* __restrict__ up_b, int mip, const float* __restrict__ up_s, int mi,
+    const int8_t* __restrict__ up, int nbg, float* __restrict__ g, float* __restrict__ u, MoeWs ws,
+    int* __restrict__ err) {
+    constexpr int KS = 4;
+    extern __shared__ __attribute__((aligned(16))) float dsm[];
+    float* p = dsm;                                       // [E]
+    int* pe = reinterpret_cast<int*>(dsm + E);            // [topk] picks, pick order
+    float* pw = dsm + E + topk;
+    int* se = reinterpret_cast<int*>(dsm + E + 2 * topk);  // [topk] ascending expert id
+    float* sw = dsm + E + 3 * topk;
+    float* red = dsm + E + 4 * topk;                       // [8]
+    float* so_l = red + 8;                                 // [1]
+    int* bad_l = reinterpret_cast<int*>(red + 9);
+    int8_t* Dl = reinterpret_cast<int8_t*>(dsm + ((E + 4 * topk + 10 + 3) & ~3));  // [3][kpd]
+    __shared__ v4i rv[KS - 1][64];
+
+    const int slot = blockIdx.x, cbk = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    if (wave == 0) {
+        const bool bad = route_wave(logits, E, topk, norm_topk, pes, p, pe, pw);
+        for (int i = lane; i < topk; i += 64) {
+            int r = 0;
+            for (int j = 0; j < topk; ++j) r += pe[j] < pe[i];
+            se[r] = pe[i];
+            sw[r] = pw[i];
+        }
+        if (lane == 0) *bad_l = bad;
+    }
+    row_digits(x, d, kpd, Dl, so_l, red);
+    __syncthreads();
+    if (slot == 0 && cbk == 0) {
+        if (tid < topk) { ws.sel[tid] = se[tid]; ws.w[tid] = sw[tid]; }
+        if (tid == 0) {
+            ws.off[E] = topk;
+            if (*bad_l) atomicOr(err, 1);
+        }
+    }
+    const bool isg = cbk < nbg;
+    const int e = se[slot];
+    const int8_t* __restrict__ Wb = isg ? gate_b : up_b;
+    const int Np = isg ? gwp : mip, N = isg ? gw : mi, nb0 = isg ? cbk : cbk - nbg;
+    const int nkb = kpd / 64, kb0 = nkb * wave / KS, kb1 = nkb * (wave + 1) / KS;
+    const int rr = lane & 15, dg = rr & 3, kq = lane >> 4;
+    const bool aval = rr < 3;  // token 0, digits 0..2
+    const int8_t* arow = Dl + (dg < 3 ? dg : 0) * kpd + 16 * kq;
+    const int8_t* wb = Wb + (size_t)e * Np * kpd + (size_t)nb0 * 1024 + lane * 16;
+    const size_t kstride = (size_t)(Np / 16) * 1024;
+    v4i acc = v4i{0, 0, 0, 0};
+    constexpr int U = 8;
+    for (int kb = kb0; kb < kb1; kb += U) {
+        v4i av[U], bv[U];
+#pragma unroll
+        for (int q = 0; q < U; ++q) {
+            const bool in = kb + q < kb1;
+            av[q] = (in && aval) ? *reinterpret_cast<const v4i*>(arow + (size_t)(kb + q) * 64) : v4i{0, 0, 0, 0};
+            bv[q] = in ? *reinterpret_cast<const v4i*>(wb + (size_t)(kb + q) * kstride) : v4i{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int q = 0; q < U; ++q) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[q], bv[q], acc, 0, 0, 0);
+    }
+    if (wave > 0) rv[wave - 1][lane] = acc;
+    __syncthreads();
+    if (wave > 0 || lane >= 16) return;
+#pragma unroll
+    for (int q = 0; q < KS - 1; ++q) acc += rv[q][lane];
+    // lanes 0..15: row 0 (the token), digits in acc[0..2], column lane
+    const int j = nb0 * 16 + lane;
+    if (j >= N) return;
+    const float so = *so_l, sj = (isg ? gate_s : up_s)[(size_t)e * N + j];
+    float v;
+    if (so >= 0.0f) {
+        v = so * ((float)acc[0] * 65536.0f + ((float)acc[1] * 256.0f + (float)acc[2])) * sj;
+    } else {
+        const int8_t* qe = (isg ? gate : up) + (size_t)e * d * N;
+        v = 0.0f;
+        for (int k = 0; k < d; ++k) v = __builtin_fmaf(x[k], (float)qe[(size_t)k * N + j] * sj, v);
+    }
+    (isg ? g : u)[(size_t)slot * N + j] = v;
+}
+
+// K3: down GEMM of all k rows and the combine, one wave per slot (ascending
+// expert id) and 16 output columns per workgroup; the combine adds the
+// slots' w * down in that order from +0, as combine_kernel does.
+__global__ __launch_bounds__(1024) void moe_dec_down_kernel(
+    const int8_t* __restrict__ hd, const float* __restrict__ hso, int kpm, const float* __restrict__ h,
+    int mi, const int8_t* __restrict__ down_b, int dp, const float* __restrict__ down_s,
+    const int8_t* __restrict__ down, int d, const int32_t* __restrict__ sel, const float* __restrict__ wsel,
+    int topk, float* __restrict__ out) {
+    __shared__ float vs[16][16];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int slot = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nb0 = blockIdx.x;
+    const int e = sel[slot];
+    const int nkb = kpm / 64;
+    const int rr = lane & 15, dg = rr & 3, kq = lane >> 4;
+    const bool aval = rr < 3;
+    const int8_t* arow = hd + ((size_t)slot * 3 + (dg < 3 ? dg : 0)) * kpm + 16 * kq;
+    const int8_t* wb = down_b + (size_t)e * dp * kpm + (size_t)nb0 * 1024 + lane * 16;
+    const size_t kstride = (size_t)(dp / 16) * 1024;
+    v4i acc = v4i{0, 0, 0, 0};
+    constexpr int U = 8;
+    for (int kb = 0; kb < nkb; kb += U) {
+        v4i av[U], bv[U];
+#pragma unroll
+        for (int q = 0; q < U; ++q) {
+            const bool in = kb + q < nkb;
+            av[q] = (in && aval) ? *reinterpret_cast<const v4i*>(arow + (size_t)(kb + q) * 64) : v4i{0, 0, 0, 0};
+            bv[q] = in ? *reinterpret_cast<const v4i*>(wb + (size_t)(kb + q) * kstride) : v4i{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int q = 0; q < U; ++q) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[q], bv[q], acc, 0, 0, 0);
+    }
+    const int j = nb0 * 16 + lane;
+    if (lane < 16 && j < d) {
+        const float so = hso[slot], sj = down_s[(size_t)e * d + j];
+        float v;
+        if (so >= 0.0f) {
+            v = so * ((float)acc[0] * 65536.0f + ((float)acc[1] * 256.0f + (float)acc[2])) * sj;
+        } else {
+            const float* xr = h + (size_t)slot * mi;
+            const int8_t* qe = down + (size_t)e * mi * d;
+            v = 0.0f;
+            for (int k = 0; k < mi; ++k) v = __builtin_fmaf(xr[k], (float)qe[(size_t)k * d + j] * sj, v);
+        }
+        vs[slot][lane] = v;
+    }
+    __syncthreads();
+    if (tid < 16 && nb0 * 16 + tid < d) {
+        float a = 0.0f;
+        for (int q = 0; q < topk; ++q) a = a + wsel[q] * vs[q][tid];
+        out[nb0 * 16 + tid] = a;
+    }
+}
+
 __global__ void combine_kernel(const float* __restrict__ dn, const int32_t* __restrict__ sel,
                                const float* __restrict__ w, const int32_t* __restrict__ pos,
                                int topk, int d, float* __restrict__ out) {
@@ -470,7 +634,7 @@ size_t moe_ws_bytes(const MoeBank& b, size_t T, size_t topk) {
 hipError_t launch_moe_route(const float* logits, size_t T, size_t E,
                             size_t topk, int norm_topk, const float* pes,
                             int32_t* sel, float* w, int* err, hipStream_t s) {
-    const size_t lds = 4 * E * sizeof(float);
+    const size_t lds = 4 * (E + 2 * topk) * sizeof(float);
     route_kernel<<<dim3((unsigned)((T + 3) / 4)), dim3(256), lds, s>>>(
         logits, (int)T, (int)E, (int)topk, norm_topk, pes, sel, w, err);
     return hipGetLastError();
@@ -504,15 +668,33 @@ hipError_t launch_moe(const MoeBank& b, const float* x, size_t T,
     const int E = (int)b.n_exp, d = (int)b.d, mi = (int)b.mi, gw = (int)b.gw;
     const size_t tr = moe_tile_rows(T);
     const bool dec = tr == 4;
+    const size_t gwp = round_up(b.gw, 16), mip = round_up(b.mi, 16), dp = round_up(b.d, 16);
+    if (T == 1 && topk <= 16) {
+        // decode: route + digits + gate/up, act digits, down + combine
+        const int nbg = (int)(gwp / 16), nbu = b.act == FRQ_ACT_SILU ? (int)(mip / 16) : 0;
+        const size_t lds1 = ((size_t)((E + 4 * (int)topk + 10 + 3) & ~3)) * 4 + 3 * b.kpd;
+        moe_dec_gu_kernel<<<dim3((unsigned)topk, (unsigned)(nbg + nbu)), dim3(256), lds1, s>>>(
+            x, d, (int)b.kpd, logits, E, (int)topk, norm_topk, pes, b.gate_b, (int)gwp, b.gate_s, gw,
+            b.gate, b.up_b, (int)mip, b.up_s, mi, b.up, nbg, ws.g, ws.u, ws, err);
+        hipError_t e1 = hipGetLastError();
+        if (e1 != hipSuccess) return e1;
+        act_digits_kernel<<<dim3((unsigned)topk), dim3(256), 0, s>>>(
+            ws.g, ws.u, b.act, mi, gw, (int)b.kpm, ws.off, E, ws.h, ws.hd, ws.hso);
+        if ((e1 = hipGetLastError()) != hipSuccess) return e1;
+        moe_dec_down_kernel<<<dim3((unsigned)(dp / 16)), dim3((unsigned)(64 * topk)), 0, s>>>(
+            ws.hd, ws.hso, (int)b.kpm, ws.h, mi, b.down_b, (int)dp, b.down_s, b.down, d, ws.sel, ws.w,
+            (int)topk, out);
+        return hipGetLastError();
+    }
     hipError_t e = launch_moe_route(logits, T, b.n_exp, topk, norm_topk, pes, ws.sel, ws.w, err, s);
     if (e != hipSuccess) return e;
-    const size_t dlds = ((size_t)E * (TC / 32) * 2 + 2 * E) * sizeof(uint32_t);
+    const size_t nwc = (std::min(T, (size_t)TC) + 31) / 32;
+    const size_t dlds = ((size_t)E * nwc * 2 + 2 * E) * sizeof(uint32_t);
     dispatch_kernel<<<dim3(1), dim3(1024), dlds, s>>>(ws.sel, (int)T, (int)topk, E, (int)tr, ws);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     x_digits_kernel<<<dim3((unsigned)T), dim3(256), 0, s>>>(x, d, (int)b.kpd, ws.xd, ws.xso);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const unsigned nt = (unsigned)ntile_max(T, topk, b.n_exp, tr);
-    const size_t gwp = round_up(b.gw, 16), mip = round_up(b.mi, 16), dp = round_up(b.d, 16);
     if ((e = moe_mm(dec, nt, ws.xd, ws.xso, b.kpd, 1, ws, b.gate_b, gwp, b.gate_s, b.gw, x, b.d,
                     b.gate, ws.g, s)) != hipSuccess)
         return e;
