@@ -409,17 +409,19 @@ __host__ __device__ inline size_t lm1_urow(size_t kp) {
     return kp > (size_t)qc::FCAP * 8 ? kp : (size_t)qc::FCAP * 8;
 }
 
-template <int L, int CPL, bool DB, int NV4>
-__global__ __launch_bounds__(256) void linear_m1_kernel(
+template <int L, int CPL, bool DB, int NV4, int NT>
+__global__ __launch_bounds__(NT) void linear_m1_kernel(
     const int8_t* __restrict__ W, const int8_t* __restrict__ Wkn,
     const float* __restrict__ scale, int N, int Np, int Kp, int K,
     const float* __restrict__ A, float* __restrict__ out, int32_t* __restrict__ acc_dbg,
     int8_t* __restrict__ a8o, float* __restrict__ sao, uint32_t* __restrict__ oio,
     float* __restrict__ ovo, int* __restrict__ err, int n_rg) {
-    constexpr int RPP = 256 / L;
+    constexpr int RPP = NT / L;
+    constexpr int LW = L < 64 ? L : 64, WPR = L / LW;  // lanes per wave of a row, waves per row
     constexpr int NQW = FRQ_T * (RPP / 4);  // outlier words per group
-    __shared__ qc::RowLds Q;
-    __shared__ int accs[2][RPP];
+    static_assert(NQW <= NT && RPP % 4 == 0, "one outlier word per thread");
+    __shared__ qc::RowLdsT<NT> Q;
+    __shared__ int accs[2][RPP * WPR];
     extern __shared__ __align__(16) unsigned char dyn[];
     const int nbw = Kp >> 5;  // Kp % 128 == 0
     uint32_t* bitmap = reinterpret_cast<uint32_t*>(dyn);
@@ -444,26 +446,26 @@ __global__ __launch_bounds__(256) void linear_m1_kernel(
     // group loads the last one, shared in L2, so that no branch separates
     // these loads from the row's and the quant waits for the row only)
     float4 v[NV4];
-    qc::row_load<NV4>(A, K4, v);
+    qc::row_load<NV4, NT>(A, K4, v);
     load_w(xcd_group<RPP>(rg, n_rg), w);
     if (DB) load_w(xcd_group<RPP>(min(rg + G, n_rg - 1), n_rg), wn);
-    const qc::RowSel s = qc::row_select<NV4>(A, K, v, Q, reinterpret_cast<unsigned long long*>(U),
+    const qc::RowSel s = qc::row_select<NV4, NT>(A, K, v, Q, reinterpret_cast<unsigned long long*>(U),
                                              bitmap, nbw);
     uint32_t* a8w = reinterpret_cast<uint32_t*>(U);  // the candidate keys are dead
     if (s.nan) {
         // the reference panics; the call reports FRQ_ERR_NAN and computes on
         // the standalone quant's placeholders (a8 = 0, sa = 1, zero outliers)
-        for (int i4 = tid; i4 < K4; i4 += 256) a8w[i4] = 0u;
+        for (int i4 = tid; i4 < K4; i4 += NT) a8w[i4] = 0u;
     } else {
-        qc::row_quantize<NV4>(v, K4, bitmap, s.sa, s.fast, [&](int i4, uint32_t x) { a8w[i4] = x; });
+        qc::row_quantize<NV4, NT>(v, K4, bitmap, s.sa, s.fast, [&](int i4, uint32_t x) { a8w[i4] = x; });
     }
-    for (int i4 = K4 + tid; i4 < (Kp >> 2); i4 += 256) a8w[i4] = 0u;
+    for (int i4 = K4 + tid; i4 < (Kp >> 2); i4 += NT) a8w[i4] = 0u;
     __syncthreads();
     const float sam = s.sa;
     if (blockIdx.x == 0) {
         if (s.nan && tid == 0) atomicOr(err, 1);
         if (a8o) {
-            for (int c = tid; c < nch; c += 256)
+            for (int c = tid; c < nch; c += NT)
                 reinterpret_cast<int4*>(a8o)[c] = reinterpret_cast<const int4*>(U)[c];
             if (tid < FRQ_T) { oio[tid] = Q.sel_i[tid]; ovo[tid] = Q.sel_v[tid]; }
             if (tid == 0) sao[0] = sam;
@@ -521,8 +523,8 @@ __global__ __launch_bounds__(256) void linear_m1_kernel(
         // has consumed these, overlapping the reduction and the epilogue
         if (!DB && rgn < n_rg) load_w(gn, w);
 #pragma unroll
-        for (int off = L / 2; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
-        if (sub == 0) accs[buf][rloc] = acc;
+        for (int off = LW / 2; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+        if (sub % LW == 0) accs[buf][rloc * WPR + sub / LW] = acc;
         if (qw) {
 #pragma unroll
             for (int b = 0; b < 4; ++b) prod[buf][4 * r4 + b][q] = ovq * (float)(int8_t)(ow >> (8 * b));
@@ -538,7 +540,9 @@ __global__ __launch_bounds__(256) void linear_m1_kernel(
                 float corr = -0.0f;
 #pragma unroll
                 for (int qq = 0; qq < FRQ_T; ++qq) corr = corr + prod[buf][tid][qq];
-                const int total = accs[buf][tid];
+                int total = accs[buf][tid * WPR];
+#pragma unroll
+                for (int h = 1; h < WPR; ++h) total += accs[buf][tid * WPR + h];
                 out[j] = sc * (sam * (float)total + corr);
                 if (acc_dbg) acc_dbg[j] = total;
             }
@@ -555,15 +559,15 @@ __global__ __launch_bounds__(256) void linear_m1_kernel(
     }
 }
 
-template <int L, int CPL, bool DB, int NV4>
+template <int L, int CPL, bool DB, int NV4, int NT = 256>
 hipError_t launch_lm1(const Weight& w, const float* a, float* out, int32_t* acc, int8_t* a8o,
                       float* sao, uint32_t* oio, float* ovo, int* err, int gmax, hipStream_t s) {
-    constexpr int RPP = 256 / L;
+    constexpr int RPP = NT / L;
     const int n_rg = (int)((w.n + RPP - 1) / RPP);  // rows < Np (RPP divides 256)
     const int grid = n_rg < gmax ? n_rg : gmax;
     const size_t prod = (size_t)2 * RPP * (FRQ_T + 1) * 4;
     const size_t lds = w.kp / 8 + (DB ? std::max(lm1_urow(w.kp), prod) : lm1_urow(w.kp) + prod);
-    linear_m1_kernel<L, CPL, DB, NV4><<<dim3((unsigned)grid), dim3(256), lds, s>>>(
+    linear_m1_kernel<L, CPL, DB, NV4, NT><<<dim3((unsigned)grid), dim3(NT), lds, s>>>(
         w.wt, w.wkn, w.scale, (int)w.n, (int)w.np, (int)w.kp, (int)w.k, a, out, acc, a8o, sao, oio,
         ovo, err, n_rg);
     return hipGetLastError();
@@ -616,8 +620,11 @@ hipError_t launch_linear_m1(const Weight& w, const float* a, float* out, int32_t
     if (nch <= 128) return launch_lm1<64, 2, true, 2>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 1024, s);
     if (nch <= 256) return launch_lm1<64, 4, true, 4>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 1024, s);
     if (nch <= 512) return launch_lm1<64, 8, true, 8>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 512, s);
-    if (nch <= 1024) return launch_lm1<64, 16, false, 16>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 256, s);
-    return launch_lm1<64, 20, false, 20>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 256, s);
+    // long rows: 1024 threads (a quarter of the quant per thread), every
+    // workgroup's first group in flight during the quant
+    // (128 lanes, two waves, per row: 8 rows per group)
+    if (nch <= 1024) return launch_lm1<128, 8, false, 4, 1024>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 256, s);
+    return launch_lm1<128, 10, false, 5, 1024>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 256, s);
 }
 
 }  // namespace frq

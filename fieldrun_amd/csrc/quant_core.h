@@ -12,14 +12,16 @@
 // select_nth_unstable_by, go to the lowest channel index; outliers are listed
 // in ascending channel order.
 //
-// The routines here cover rows with K % 4 == 0 and 32 < K <= 1024 * NV4, the
-// row held as v[i] = a[4 (tid + 256 i) ..] (float4, zero past K):
+// The routines here cover rows with K % 4 == 0 and 32 < K <= 4 NT NV4 for a
+// workgroup of NT = 256 or 1024 threads, the row held as
+// v[i] = a[4 (tid + NT i) ..] (float4, entries past K ignored):
 //   row_select:   1. each thread's max |a|;
-//                 2. tau = the 33rd largest thread max: every wave sorts its
-//                    64 maxima with a bitonic network on DPP / permlane lane
-//                    exchanges, and every wave merges the four lists keeping
-//                    the top 64.  At least t+1 elements are >= tau, so
-//                    bulk_max >= tau;
+//                 2. tau: with 4 waves the 33rd largest thread max (every
+//                    wave sorts its 64 maxima with a bitonic network on DPP /
+//                    permlane lane exchanges, and every wave merges the four
+//                    lists keeping the top 64); with 16 waves the 33rd
+//                    largest of the waves' top-3 lane maxima.  At least t+1
+//                    elements are >= tau, so bulk_max >= tau;
 //                 3. the elements >= tau (a few dozen on real rows) are
 //                    compacted into per-wave LDS regions with ballot + mbcnt
 //                    as keys (|a|, -channel, sign); each key's rank is counted
@@ -207,22 +209,25 @@ __device__ __forceinline__ uint32_t key_bits(unsigned long long key) {
     return (uint32_t)(key >> 32) | ((uint32_t)key << 31);
 }
 
-// LDS of one row's selection (besides the candidate keys and the bitmap,
-// which the caller places so that it can reuse their space).
-struct RowLds {
+// LDS of one row's selection by NT threads (besides the candidate keys and
+// the bitmap, which the caller places so that it can reuse their space).
+template <int NT>
+struct RowLdsT {
+    static constexpr int W = NT / 64;
     unsigned long long top[FRQ_T + 1];
     uint32_t hist[256];
-    uint32_t scan[NW + 1];
-    uint32_t ws[NW][64];
-    uint32_t wn[NW];
-    uint32_t wcnt[NW];
+    uint32_t scan[W + 1];
+    uint32_t ws[W][64];
+    uint32_t wn[W];
+    uint32_t wcnt[W];
     uint32_t bc[2];
     uint32_t sel_i[FRQ_T];
     float sel_v[FRQ_T];
     uint32_t rank[64];
     uint32_t cch[64];
-    unsigned long long ck[NW][64];
+    unsigned long long ck[W][64];
 };
+using RowLds = RowLdsT<BLOCK>;
 
 struct RowSel {
     float sa;
@@ -235,9 +240,11 @@ struct RowSel {
 // here.  Ends with a barrier; then sel_i / sel_v hold the 32 outliers in
 // channel order and bitmap marks them, and cand is free.  A NaN row returns
 // nan (uniformly) with sel_i[q] = q, sel_v[q] = 0 and an empty bitmap.
-template <int NV4>
-__device__ RowSel row_select(const float* __restrict__ a, int K, const float4 (&v)[NV4], RowLds& L,
+template <int NV4, int NT = BLOCK>
+__device__ RowSel row_select(const float* __restrict__ a, int K, const float4 (&v)[NV4], RowLdsT<NT>& L,
                              unsigned long long* cand, uint32_t* bitmap, int nbw) {
+    constexpr int NW = NT / 64, BLOCK = NT;
+    static_assert(NW == 4 || NW == 16, "4 or 16 waves");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int K4 = K >> 2;
     uint32_t mx = 0;  // max |a| bits; NaN shows as > 0x7F800000
@@ -246,26 +253,39 @@ __device__ RowSel row_select(const float* __restrict__ a, int K, const float4 (&
         const uint32_t m4 = max(max(absbits(v[i].x), absbits(v[i].y)), max(absbits(v[i].z), absbits(v[i].w)));
         mx = max(mx, tid + BLOCK * i < K4 ? m4 : 0u);
     }
-    // threshold tau = the 33rd largest thread maximum: at least 33 elements
-    // are >= tau, so every element above the (t+1)-th largest |a| is >= tau,
-    // and for iid rows only a few dozen elements pass.  Every wave sorts its
-    // 64 maxima; after one barrier every wave merges the four lists itself
-    // (no second barrier).  The NaN check rides on the same barrier.
-    static_assert(NW == 4, "the threshold merge assumes 4 waves");
+    // threshold tau, every element above the (t+1)-th largest |a| is >= tau.
+    // 4 waves: tau = the 33rd largest thread maximum (at least 33 elements
+    // are >= tau; for iid rows only a few dozen pass): every wave sorts its
+    // 64 maxima, and after one barrier every wave merges the four lists
+    // itself.  16 waves: tau = the 33rd largest of the waves' top-3 lane
+    // maxima (48 distinct elements, sorted in every wave).  The NaN check
+    // rides on the same barrier.
     const bool wnan = __builtin_amdgcn_ballot_w64(mx > 0x7F800000u) != 0;  // NaN bits
-    L.ws[wave][lane] = wave_sort_desc(mx);
+    const uint32_t srt = wave_sort_desc(mx);
+    if (NW == 4 || lane < 3) L.ws[wave][lane] = srt;
     if (lane == 0) L.wn[wave] = wnan;
     for (int w = tid; w < nbw; w += BLOCK) bitmap[w] = 0u;
     if (tid < 64) L.rank[tid] = 0u;
     __syncthreads();
-    if (L.wn[0] | L.wn[1] | L.wn[2] | L.wn[3]) {
+    uint32_t anynan = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) anynan |= L.wn[w];
+    if (anynan) {
         if (tid < FRQ_T) { L.sel_i[tid] = (uint32_t)tid; L.sel_v[tid] = 0.0f; }
         __syncthreads();
         return {1.0f, false, true};
     }
-    const uint32_t mx01 = merge_top64(L.ws[0][lane], L.ws[1][63 - lane]);
-    const uint32_t mx23 = merge_top64(L.ws[2][lane], L.ws[3][63 - lane]);
-    const uint32_t tau = __builtin_amdgcn_readlane(merge_top64(mx01, __shfl(mx23, 63 - lane, 64)), FRQ_T);
+    uint32_t tau;
+    if constexpr (NW == 4) {
+        const uint32_t mx01 = merge_top64(L.ws[0][lane], L.ws[1][63 - lane]);
+        const uint32_t mx23 = merge_top64(L.ws[2][lane], L.ws[3][63 - lane]);
+        tau = __builtin_amdgcn_readlane(merge_top64(mx01, __shfl(mx23, 63 - lane, 64)), FRQ_T);
+    } else {
+        // the 33rd largest of the waves' top-3 lane maxima: 48 distinct
+        // elements, so at least 33 elements are >= it
+        const uint32_t t3 = lane < 3 * NW ? L.ws[lane / 3][lane % 3] : 0u;
+        tau = __builtin_amdgcn_readlane(wave_sort_desc(t3), FRQ_T);
+    }
     // compact candidates into per-wave regions of cand[] (FCAP/4 keys each),
     // offsets from ballots
     constexpr int WCAP = FCAP / NW;
@@ -313,20 +333,21 @@ __device__ RowSel row_select(const float* __restrict__ a, int K, const float4 (&
     if (nc <= (uint32_t)FCAP) {
         if (nc <= 64) {
             // rank of lane l's key among the nc (distinct) keys: wave w
-            // counts the keys 16w .. 16w+15 above it, the four counts summed
-            // in LDS; ranks 0..32 go to top[]
+            // counts the keys KPW w .. KPW w + KPW-1 above it, the counts
+            // summed in LDS; ranks 0..32 go to top[]
             // (each wave gathers the keys into its own contiguous copy first,
-            // so that its 16 reads share one base; keys are > 0, and the
-            // slots past nc hold 0)
+            // so that its reads share one base; keys are > 0, and the slots
+            // past nc hold 0)
+            constexpr int KPW = 64 / NW;
             const bool valid = lane < (int)nc;
             const unsigned long long key = valid ? cand_at(lane) : 0ull;
             L.ck[wave][lane] = key;
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
-            const unsigned long long* kq = &L.ck[__builtin_amdgcn_readfirstlane(wave)][16 * __builtin_amdgcn_readfirstlane(wave)];
+            const unsigned long long* kq = &L.ck[__builtin_amdgcn_readfirstlane(wave)][KPW * __builtin_amdgcn_readfirstlane(wave)];
             uint32_t part = 0;
 #pragma unroll
-            for (int jj = 0; jj < 16; ++jj) part += kq[jj] > key;
+            for (int jj = 0; jj < KPW; ++jj) part += kq[jj] > key;
             if (valid && part) atomicAdd(&L.rank[lane], part);
             __syncthreads();
             if (wave == 0) {
@@ -419,9 +440,10 @@ __device__ RowSel row_select(const float* __restrict__ a, int K, const float4 (&
 
 // Step 5: the quantised word of float4 i4 (channels 4 i4 .. 4 i4 + 3) goes to
 // st(i4, word), bytes in channel order, outlier slots zero; i4 < K/4 only.
-template <int NV4, typename St>
+template <int NV4, int NT = BLOCK, typename St>
 __device__ __forceinline__ void row_quantize(const float4 (&v)[NV4], int K4, const uint32_t* bitmap,
                                              float sa, bool fast, St st) {
+    constexpr int BLOCK = NT;
     const int tid = threadIdx.x;
     const float r = 1.0f / sa;
 #pragma unroll
@@ -449,8 +471,9 @@ __device__ __forceinline__ void row_quantize(const float4 (&v)[NV4], int K4, con
 // past K/4 repeat the last float4 (clamped addresses, no branches, so that
 // loads issued after these need not wait for them); row_select and
 // row_quantize ignore them.
-template <int NV4>
+template <int NV4, int NT = BLOCK>
 __device__ __forceinline__ void row_load(const float* __restrict__ a, int K4, float4 (&v)[NV4]) {
+    constexpr int BLOCK = NT;
     const int tid = threadIdx.x;
 #pragma unroll
     for (int i = 0; i < NV4; ++i) v[i] = reinterpret_cast<const float4*>(a)[min(tid + BLOCK * i, K4 - 1)];
