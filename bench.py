@@ -47,7 +47,7 @@ def int4_bytes(m, k, n, g=32):
 
 
 DOM_SHAPE = (896, 151936)  # the headline's dominant launch (136 MB of weights)
-DOM_KERNEL = "linear_m1_kernel<8,8,true,1>"
+DOM_KERNEL = "linear_m1_kernel<8,8,true,1,256>"
 PMC_COPY_BYTES = 256 << 20
 PMC_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                            "linear_m1_K896_N151936_pmc.md")
