@@ -213,6 +213,31 @@ def main():
                 "bytes_per_launch": int8_linear_bytes(1, *dom), "us_per_launch": round(us_dom, 2)}
 
     if not args.no_detail:
+        # ---------------- the sweep's other M (full linear and GEMM-only) ----------------
+        # decode batches (M=4, 16: HBM-bound, GB/s) and M=128 (HBM-bound at
+        # these K, N); weights rotated over the same replicas
+        detail["int8_sweep_m"] = {}
+        for m in (4, 16, 128):
+            row = {}
+            for si, (k, n) in enumerate(shapes):
+                a = synth.activations(m, k, synth.seed(1, 20 + m) + si)
+                da = hip.DeviceArray.from_numpy(a)
+                do = hip.DeviceArray((m, n), np.float32)
+                us = time_loop(lambda i, si=si: weights[si][i % R].mm_dev(da.ptr, m, do.ptr), 30) * 1e3
+                kp = fa.quant_pitch(k)
+                a8 = hip.DeviceArray((m, kp), np.int8)
+                sa = hip.DeviceArray((m,), np.float32)
+                oi = hip.DeviceArray((m, 32), np.uint32)
+                ov = hip.DeviceArray((m, 32), np.float32)
+                ctx.quant_dev(da.ptr, m, k, a8.ptr, sa.ptr, oi.ptr, ov.ptr)
+                gus = time_loop(lambda i, si=si: weights[si][i % R].mm_q_dev(a8.ptr, sa.ptr, oi.ptr, ov.ptr, m,
+                                                                            do.ptr), 30) * 1e3
+                row[f"K{k}_N{n}"] = {"full_linear_us": round(us, 2),
+                                     "full_linear_GBps": round(int8_linear_bytes(m, k, n) / (us * 1e-6) / 1e9, 1),
+                                     "gemm_only_us": round(gus, 2),
+                                     "gemm_only_GBps": round(gemv_kernel_bytes(m, k, n) / (gus * 1e-6) / 1e9, 1)}
+            detail["int8_sweep_m"][f"M{m}"] = row
+            log(f"M={m}: {row}")
         # ---------------- prefill: M=2048 MFMA-bound shapes ----------------
         detail["int8_m2048_gemm"] = {}
         for (k, n) in [(4096, 14336), (14336, 4096)]:

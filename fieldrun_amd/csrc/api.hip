@@ -3,8 +3,10 @@
 // Owns device selection, streams, the per-context workspace and the one-time
 // weight uploads, and dispatches Bundle::mm / expert_mm semantics
 // (/root/reference/src/bundle.rs:644-919, 404-461) onto the gfx950 kernels:
-//   int8, M <= 4 (decode)  -> quant kernel + int8 GEMV
-//   int8, M >  4           -> quant kernel (blocked a8) + int8 MFMA GEMM
+//   int8, M == 1           -> fused quant + GEMV (one launch)
+//   int8, 2 <= M <= 16     -> quant kernel + skinny MFMA kernel (weights
+//                             streamed once; bit-exact epilogue)
+//   int8, M >  16          -> quant kernel (blocked a8) + int8 MFMA GEMM
 //   int4                   -> blocked W4A32 GEMV (M == 1) / batched kernel
 // Every failure becomes an int status plus frq_last_error(); nothing throws.
 #include <mutex>
@@ -95,8 +97,11 @@ size_t i8_scratch_bytes(const Weight& w, size_t m, bool rowmajor_copy) {
     return b;
 }
 
+// Decode batches (m <= 16) take the row-major a8 and the HBM-bound kernels;
+// larger m the blocked a8 and the MFMA GEMM.
 bool use_gemv(const Weight& w, size_t m) {
-    return m <= 4 && m * w.kp <= 60 * 1024;
+    (void)w;
+    return m <= 16;
 }
 
 // The int8 linear on device pointers; scratch carved from `sc`.  With a8o
@@ -123,7 +128,10 @@ int run_i8(frq_ctx* c, const Weight& w, const float* d_a, size_t m, float* d_out
                "launch linear_m1");
     } else if (!gemm) {
         HIPCHK(launch_quant(d_a, m, w.k, w.kp, a8, sa, oi, ov, c->err, c->stream), "launch quant");
-        HIPCHK(launch_gemv_i8(w, m, a8, sa, oi, ov, d_out, d_acc, c->stream), "launch gemv_i8");
+        if (m == 1)
+            HIPCHK(launch_gemv_i8(w, m, a8, sa, oi, ov, d_out, d_acc, c->stream), "launch gemv_i8");
+        else
+            HIPCHK(launch_skinny_i8(w, m, a8, sa, oi, ov, d_out, d_acc, c->stream), "launch skinny_i8");
     } else {
         HIPCHK(launch_quant(d_a, m, w.k, w.kp, a8, sa, oi, ov, c->err, c->stream, mp), "launch quant");
         HIPCHK(launch_gemm_i8(w, m, a8, sa, oi, ov, d_out, d_acc, c->stream), "launch gemm_i8");
@@ -441,7 +449,11 @@ int frq_mm_i8_q_dev(frq_ctx* c, const frq_w* wh, const int8_t* d_a8, const float
         return FRQ_OK;
     }
     if (use_gemv(w, m)) {
-        HIPCHK(launch_gemv_i8(w, m, d_a8, d_sa, d_oidx, d_oval, d_out, nullptr, c->stream), "launch gemv_i8");
+        if (m == 1)
+            HIPCHK(launch_gemv_i8(w, m, d_a8, d_sa, d_oidx, d_oval, d_out, nullptr, c->stream), "launch gemv_i8");
+        else
+            HIPCHK(launch_skinny_i8(w, m, d_a8, d_sa, d_oidx, d_oval, d_out, nullptr, c->stream),
+                   "launch skinny_i8");
         return FRQ_OK;
     }
     // the MFMA GEMM reads round_up(m, 128) rows of a8 in the blocked layout

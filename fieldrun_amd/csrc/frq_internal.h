@@ -54,6 +54,9 @@ __device__ __forceinline__ int4 ntload16(const void* p) {
     const v4i v = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p));
     return make_int4(v.x, v.y, v.z, v.w);
 }
+__device__ __forceinline__ v4i ntload_v4i(const void* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p));
+}
 __device__ __forceinline__ uint4 ntload16u(const void* p) {
     const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
     return make_uint4(v.x, v.y, v.z, v.w);
@@ -150,6 +153,11 @@ bool linear_m1_ok(const Weight& w, const float* a);
 hipError_t launch_linear_m1(const Weight& w, const float* a, float* out, int32_t* acc,
                             int8_t* a8o, float* sao, uint32_t* oio, float* ovo, int* err,
                             hipStream_t s, int gmax = 0);
+// int8 linear for 1 <= m <= 16 on row-major a8 (pitch kp) from the blocked
+// weight copy; outputs bit-exact to the reference's M > 1 order.
+hipError_t launch_skinny_i8(const Weight& w, size_t m, const int8_t* a8, const float* sa,
+                            const uint32_t* oidx, const float* oval, float* out, int32_t* acc,
+                            hipStream_t s);
 // (valid rows of an (R, kp) row-major int8 matrix, pitch) -> blocked
 // (blk_off, R rows); rows >= valid become zero.
 hipError_t launch_blockify(const int8_t* src, size_t valid, size_t R, size_t kp,
