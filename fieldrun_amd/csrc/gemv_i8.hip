@@ -1,7 +1,7 @@
-// gemv_i8.hip — int8 W8A8 GEMV for decode shapes (1 <= M <= 4), gfx950.
+// gemv_i8.hip — int8 W8A8 GEMV for single-token decode (M == 1), gfx950.
 //
-// Restates the M==1 arm of Bundle::mm's I8 path and its M>1 twin
-// (/root/reference/src/bundle.rs:744-752, 709-715):
+// Restates the M==1 arm of Bundle::mm's I8 path
+// (/root/reference/src/bundle.rs:744-752):
 //   acc  = i8dot(a8, wt[j])                    i32, exact (1036-1053)
 //   corr = sum over outliers of av * (wt[j,ch] as f32), ascending channel,
 //          folded from -0.0 (Rust f32 Sum)
@@ -151,119 +151,6 @@ hipError_t launch_m(const Weight& w, const int8_t* a8, const float* sa,
     if (nch <= 64) return launch_t<M, 4, 64>(w, a8, sa, oidx, oval, out, acc, s);
     if (nch <= 256) return launch_t<M, 4, 128>(w, a8, sa, oidx, oval, out, acc, s);
     return launch_t<M, 4, 256>(w, a8, sa, oidx, oval, out, acc, s);
-}
-
-// ---------------------------------------------------------------------------
-// GEMV v2: L lanes per weight row (8 when the row is at most 64 chunks of 16
-// bytes, else 64), each lane owning chunks sub, sub+L, ... (at most CPL).
-// The activations' chunks for those positions are loaded once into
-// registers; every row pass then issues all of a lane's weight loads at once.
-// The outlier correction reads W[j, ch] from the (K, Np) copy of the weight:
-// for a fixed outlier channel the workgroup's rows are consecutive bytes, so
-// those loads coalesce; they are issued before the weight stream and packed
-// four to a register.  Same operation order as the oracle (bit-exact).
-template <int M, int L, int CPL>
-__global__ __launch_bounds__(256) void gemv2_i8_kernel(
-    const int8_t* __restrict__ W, const int8_t* __restrict__ Wkn,
-    const float* __restrict__ scale, int N, int Np, int Kp, int t,
-    const int8_t* __restrict__ a8, const float* __restrict__ sa,
-    const uint32_t* __restrict__ oidx, const float* __restrict__ oval,
-    float* __restrict__ out, int32_t* __restrict__ acc_dbg, int passes) {
-    constexpr int RPP = 256 / L;  // rows per pass
-    __shared__ int accs[M][256];
-    const int tid = threadIdx.x;
-    const int sub = tid % L, rloc = tid / L;
-    const int nch = Kp >> 4;
-    const int RPW = RPP * passes;
-    const int j0 = blockIdx.x * RPW;
-
-    // outlier bytes of this thread's epilogue row(s), 4 per register
-    uint32_t wc[M][FRQ_T / 4];
-    if (tid < RPW) {
-        const int j = j0 + tid;  // < Np
-#pragma unroll
-        for (int m = 0; m < M; ++m)
-#pragma unroll
-            for (int q4 = 0; q4 < FRQ_T / 4; ++q4) {
-                uint32_t v = 0;
-#pragma unroll
-                for (int b = 0; b < 4; ++b) {
-                    const int q = q4 * 4 + b;
-                    if (q < t) {
-                        const uint32_t ch = min(oidx[(size_t)m * FRQ_T + q], (uint32_t)(Kp - 1));
-                        v |= (uint32_t)(uint8_t)Wkn[(size_t)ch * Np + j] << (8 * b);
-                    }
-                }
-                wc[m][q4] = v;
-            }
-    }
-    int4 x[M][CPL];
-#pragma unroll
-    for (int m = 0; m < M; ++m)
-#pragma unroll
-        for (int i = 0; i < CPL; ++i) {
-            const int c = sub + L * i;
-            x[m][i] = c < nch ? *reinterpret_cast<const int4*>(a8 + (size_t)m * Kp + 16 * c)
-                              : make_int4(0, 0, 0, 0);
-        }
-    for (int ps = 0; ps < passes; ++ps) {
-        const int row = j0 + ps * RPP + rloc;
-        const int8_t* wr = W + (size_t)row * Kp;
-        int4 w[CPL];
-#pragma unroll
-        for (int i = 0; i < CPL; ++i) {
-            const int c = sub + L * i;
-            w[i] = c < nch ? ntload16(wr + 16 * c) : make_int4(0, 0, 0, 0);
-        }
-        int acc[M];
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-            acc[m] = 0;
-#pragma unroll
-            for (int i = 0; i < CPL; ++i) acc[m] = dot16(x[m][i], w[i], acc[m]);
-#pragma unroll
-            for (int off = L / 2; off >= 1; off >>= 1) acc[m] += __shfl_xor(acc[m], off, 64);
-        }
-        if (sub == 0) {
-#pragma unroll
-            for (int m = 0; m < M; ++m) accs[m][ps * RPP + rloc] = acc[m];
-        }
-    }
-    __syncthreads();
-    if (tid < RPW) {
-        const int j = j0 + tid;
-        if (j < N) {
-            const float sc = scale[j];
-#pragma unroll
-            for (int m = 0; m < M; ++m) {
-                const int total = accs[m][tid];
-                float corr = -0.0f;
-#pragma unroll
-                for (int q = 0; q < FRQ_T; ++q)
-                    if (q < t)
-                        corr = corr + oval[(size_t)m * FRQ_T + q] *
-                                          (float)(int8_t)(wc[m][q >> 2] >> (8 * (q & 3)));
-                out[(size_t)m * N + j] = sc * (sa[m] * (float)total + corr);
-                if (acc_dbg) acc_dbg[(size_t)m * N + j] = total;
-            }
-        }
-    }
-}
-
-template <int M, int L, int CPL>
-hipError_t launch_v2(const Weight& w, const int8_t* a8, const float* sa,
-                     const uint32_t* oidx, const float* oval, float* out,
-                     int32_t* acc, hipStream_t s) {
-    constexpr int RPP = 256 / L;
-    int passes = 1;
-    while (passes * 2 * RPP <= 256 && (size_t)RPP * passes * 2 * 2048 <= w.n) passes *= 2;
-    const int RPW = RPP * passes;
-    const unsigned grid = (unsigned)((w.n + RPW - 1) / RPW);
-    const int t = (int)(w.k < FRQ_T ? w.k : FRQ_T);
-    gemv2_i8_kernel<M, L, CPL><<<dim3(grid), dim3(256), 0, s>>>(
-        w.wt, w.wkn, w.scale, (int)w.n, (int)w.np, (int)w.kp, t, a8, sa, oidx, oval, out, acc,
-        passes);
-    return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
@@ -573,20 +460,6 @@ hipError_t launch_lm1(const Weight& w, const float* a, float* out, int32_t* acc,
     return hipGetLastError();
 }
 
-template <int M>
-hipError_t launch_v2_m(const Weight& w, const int8_t* a8, const float* sa,
-                       const uint32_t* oidx, const float* oval, float* out,
-                       int32_t* acc, hipStream_t s) {
-    const size_t nch = w.kp / 16;
-    if (nch <= 64) return launch_v2<M, 8, 8>(w, a8, sa, oidx, oval, out, acc, s);
-    if (nch <= 128) return launch_v2<M, 64, 2>(w, a8, sa, oidx, oval, out, acc, s);
-    if (nch <= 256) return launch_v2<M, 64, 4>(w, a8, sa, oidx, oval, out, acc, s);
-    if (nch <= 512) return launch_v2<M, 64, 8>(w, a8, sa, oidx, oval, out, acc, s);
-    if (M <= 2 && nch <= 1024) return launch_v2<M, 64, 16>(w, a8, sa, oidx, oval, out, acc, s);
-    if (M == 1 && nch <= 1280) return launch_v2<M, 64, 20>(w, a8, sa, oidx, oval, out, acc, s);
-    return launch_m<M>(w, a8, sa, oidx, oval, out, acc, s);
-}
-
 }  // namespace
 
 hipError_t launch_gemv_i8(const Weight& w, size_t m, const int8_t* a8,
@@ -595,13 +468,8 @@ hipError_t launch_gemv_i8(const Weight& w, size_t m, const int8_t* a8,
                           hipStream_t s) {
     // rows j >= N read zero padding of the (Np, Kp) weight and are not stored
     if ((size_t)m * w.kp > 64 * 1024) return hipErrorInvalidValue;
-    switch (m) {
-        case 1: return launch_v3_m1(w, a8, sa, oidx, oval, out, acc, s);
-        case 2: return launch_v2_m<2>(w, a8, sa, oidx, oval, out, acc, s);
-        case 3: return launch_v2_m<3>(w, a8, sa, oidx, oval, out, acc, s);
-        case 4: return launch_v2_m<4>(w, a8, sa, oidx, oval, out, acc, s);
-        default: return hipErrorInvalidValue;
-    }
+    if (m != 1) return hipErrorInvalidValue;
+    return launch_v3_m1(w, a8, sa, oidx, oval, out, acc, s);
 }
 
 bool linear_m1_ok(const Weight& w, const float* a) {
