@@ -87,6 +87,13 @@ struct Carve {
     }
 };
 
+// Decode batches (m <= 16) take the row-major a8 and the HBM-bound kernels;
+// larger m the blocked a8 and the MFMA GEMM.
+bool use_gemv(const Weight& w, size_t m) {
+    (void)w;
+    return m <= 16;
+}
+
 // Bytes of per-call scratch for an int8 linear of m rows (a second, row-major
 // a8 when the GEMM's blocked a8 must also be returned to the host).
 size_t i8_scratch_bytes(const Weight& w, size_t m, bool rowmajor_copy) {
@@ -94,14 +101,8 @@ size_t i8_scratch_bytes(const Weight& w, size_t m, bool rowmajor_copy) {
     size_t b = round_up(mp * w.kp, 256) + round_up(mp * 4, 256) +
                2 * round_up(mp * FRQ_T * 4, 256);
     if (rowmajor_copy) b += round_up(m * w.kp, 256);
+    if (!use_gemv(w, m)) b += round_up(gemm_ws_bytes(m, w.kp), 256);
     return b;
-}
-
-// Decode batches (m <= 16) take the row-major a8 and the HBM-bound kernels;
-// larger m the blocked a8 and the MFMA GEMM.
-bool use_gemv(const Weight& w, size_t m) {
-    (void)w;
-    return m <= 16;
 }
 
 // The int8 linear on device pointers; scratch carved from `sc`.  With a8o
@@ -117,6 +118,7 @@ int run_i8(frq_ctx* c, const Weight& w, const float* d_a, size_t m, float* d_out
     uint32_t* oi = cv.take<uint32_t>(mp * FRQ_T);
     float* ov = cv.take<float>(mp * FRQ_T);
     int8_t* a8rm = (gemm && a8o) ? cv.take<int8_t>(m * w.kp) : a8;
+    void* gws = gemm ? cv.take<char>(gemm_ws_bytes(m, w.kp)) : nullptr;
     if (a8o) { *a8o = a8rm; *sao = sa; *oio = oi; *ovo = ov; }
     if (w.k == 0) {
         HIPCHK(hipMemsetAsync(d_out, 0, m * w.n * sizeof(float), c->stream), "hipMemsetAsync");
@@ -134,7 +136,7 @@ int run_i8(frq_ctx* c, const Weight& w, const float* d_a, size_t m, float* d_out
             HIPCHK(launch_skinny_i8(w, m, a8, sa, oi, ov, d_out, d_acc, c->stream), "launch skinny_i8");
     } else {
         HIPCHK(launch_quant(d_a, m, w.k, w.kp, a8, sa, oi, ov, c->err, c->stream, mp), "launch quant");
-        HIPCHK(launch_gemm_i8(w, m, a8, sa, oi, ov, d_out, d_acc, c->stream), "launch gemm_i8");
+        HIPCHK(launch_gemm_i8(w, m, a8, sa, oi, ov, d_out, d_acc, gws, c->stream), "launch gemm_i8");
         if (a8rm != a8)  // the same quantisation, row-major, for the caller
             HIPCHK(launch_quant(d_a, m, w.k, w.kp, a8rm, sa, oi, ov, c->err, c->stream), "launch quant");
     }
@@ -458,10 +460,11 @@ int frq_mm_i8_q_dev(frq_ctx* c, const frq_w* wh, const int8_t* d_a8, const float
     }
     // the MFMA GEMM reads round_up(m, 128) rows of a8 in the blocked layout
     const size_t mp = round_up(m, FRQ_MALIGN);
-    if (int rc = ws_reserve(c, round_up(mp * w.kp, 256))) return rc;
+    if (int rc = ws_reserve(c, round_up(mp * w.kp, 256) + gemm_ws_bytes(m, w.kp))) return rc;
     int8_t* a8 = (int8_t*)c->ws;
+    void* gws = (char*)c->ws + round_up(mp * w.kp, 256);
     HIPCHK(launch_blockify(d_a8, m, mp, w.kp, w.kp, a8, c->stream), "launch blockify");
-    HIPCHK(launch_gemm_i8(w, m, a8, d_sa, d_oidx, d_oval, d_out, nullptr, c->stream), "launch gemm_i8");
+    HIPCHK(launch_gemm_i8(w, m, a8, d_sa, d_oidx, d_oval, d_out, nullptr, gws, c->stream), "launch gemm_i8");
     return FRQ_OK;
 }
 

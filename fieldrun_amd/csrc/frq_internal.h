@@ -94,6 +94,12 @@ __device__ __forceinline__ unsigned long long xshfl64(unsigned long long v) {
 }
 
 // IEEE binary16 -> binary32 (exact).
+// Orders a wave's LDS accesses before and after (no other wave waits).
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
 __device__ __forceinline__ float h2f(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);
 }
@@ -162,10 +168,13 @@ hipError_t launch_skinny_i8(const Weight& w, size_t m, const int8_t* a8, const f
 // (blk_off, R rows); rows >= valid become zero.
 hipError_t launch_blockify(const int8_t* src, size_t valid, size_t R, size_t kp,
                            size_t pitch, int8_t* dst, hipStream_t s);
-// int8 MFMA GEMM for m > 4 on blocked a8 (R = round_up(m, 128)).
+// int8 MFMA GEMM for m > 16 on blocked a8 (R = round_up(m, 128)).
+// ws: gemm_ws_bytes(m, kp) bytes of device workspace (the per-row-tile
+// outlier union and digit blocks).
+size_t gemm_ws_bytes(size_t m, size_t kp);
 hipError_t launch_gemm_i8(const Weight& w, size_t m, const int8_t* a8b,
                           const float* sa, const uint32_t* oidx,
-                          const float* oval, float* out, int32_t* acc,
+                          const float* oval, float* out, int32_t* acc, void* ws,
                           hipStream_t s);
 // int4 linear (any m).
 hipError_t launch_i4(const Weight& w, size_t m, const float* a, float* out,

@@ -23,18 +23,24 @@
 // serialise the ring.  The tile order is XCD-aware (tile_of).
 //
 // corr: 32 VALU multiply-adds per output would cost as much as the MFMA GEMM
-// itself, so corr also runs on the int8 MFMA.  Per workgroup, after the main
-// loop, the union U of its 128 rows' outlier channels is built in LDS (a
-// channel bitmap and its prefix popcounts); each outlier value becomes
-// X = round(av / so[i]), |X| <= 127*2^16, so[i] = max|av| / (127*2^16),
-// split into three signed int8 digits X = d2*2^16 + d1*2^8 + d0.  Then
-// C_d = D_d (128 x |U|) . W[:, U]^T is an exact int32 MFMA product per digit
-// and corr = so * ((C2*256 + C1)*256 + C0).  W[:, U] is read from the (K, Np)
-// row-major weight copy (wkn): for a channel, the tile's columns are
-// contiguous bytes.  The 24-bit split makes corr differ from the reference's
-// f32 sum by ~1e-7 relative; acc stays bit-exact.  Rows with a non-finite
-// outlier take the exact sequential corr instead.
+// itself, so corr also runs on the int8 MFMA.  A pre-pass (gemm_prep_kernel)
+// works once per 128-row tile, for every column tile at once: the union U of
+// the tile's outlier channels (ascending, padded to a multiple of 64 with
+// channel 0), each row's digit scale so[i] = max|av| / (127*2^16), and each
+// outlier value as X = round(av / so[i]), |X| <= 127*2^16, split into three
+// signed int8 digits X = d2*2^16 + d1*2^8 + d0, laid out as MFMA A blocks
+// D_d (128 x |U|, 64 union channels per chunk).  In the GEMM's epilogue a
+// column tile gathers W[:, U] from the (K, Np) row-major copy (wkn: for a
+// channel the tile's columns are contiguous bytes), transposes it into B
+// blocks in LDS with byte permutes, and C_d = D_d . W[:, U]^T is an exact
+// int32 MFMA product per digit: corr = so * ((C2*256 + C1)*256 + C0).  The
+// 24-bit split makes corr differ from the reference's f32 sum by ~1e-7
+// relative; acc stays bit-exact.  Rows with a non-finite outlier take the
+// exact sequential corr instead.  The f32 tile leaves through LDS, one wave
+// slab of 16 rows at a time, as whole-row 16-byte stores.
 #include "frq_internal.h"
+
+#include <algorithm>
 
 namespace frq {
 
@@ -42,7 +48,8 @@ namespace {
 
 constexpr int GBM = 128, GBK = 64;
 constexpr int CH = 64;              // union channels per correction chunk
-constexpr float XMAX = 8323072.0f;  // 127 * 2^16
+// correction A blocks of one chunk: (hi, lo) x two 32-entry halves x 8 row blocks
+constexpr int DCH = 2 * 2 * (GBM / 16) * 1024;
 
 typedef __attribute__((address_space(1))) void gvoid_t;
 typedef __attribute__((address_space(3))) void lvoid_t;
@@ -96,14 +103,178 @@ __device__ uint32_t excl_scan256(uint32_t v, uint32_t* sc /*5 words*/, uint32_t*
     return r;
 }
 
+// The tile's union capacity: at most 128 rows x 32 outliers, at most Kp.
+__host__ __device__ inline int union_cap(int kp) {
+    const int u = kp < GBM * FRQ_T ? kp : GBM * FRQ_T;
+    return (u + CH - 1) / CH * CH;
+}
+
+// Per 128-row tile (blockIdx.x): the union of its rows' outlier channels,
+// per-row digit scales, and the digit blocks of chunks blockIdx.y,
+// blockIdx.y + gridDim.y, ...  Outputs: nu[mt]; uch[mt][cap] (union
+// channels ascending, then channel 0 up to the next multiple of 64);
+// so[Mp] (0 on rows that take the exact corr), fin[Mp] (1 on those rows);
+// D[mt][cap / 64][3][8][1 KB]: block (d, rb) of chunk c holds digit d of
+// rows 16rb.. against union entries 64c.., in MFMA A order (lane 16g + r:
+// row r, entries 16g..16g+15).
+__global__ __launch_bounds__(256) void gemm_prep_kernel(
+    int M, int K, int Kp, int t, const uint32_t* __restrict__ oidx,
+    const float* __restrict__ oval, int cap, int* __restrict__ nu_out,
+    uint32_t* __restrict__ uch, float* __restrict__ so_out, float* __restrict__ fin_out,
+    int8_t* __restrict__ D) {
+    __shared__ uint32_t bitmap[640], wpre[640], scan[8];
+    __shared__ __attribute__((aligned(16))) int8_t Dl[DCH];
+    const int tid = threadIdx.x, mt = blockIdx.x, m0 = mt * GBM;
+    const int nrows = min(GBM, M - m0);
+    // thread (er, eh) takes outliers 16eh..16eh+15 of tile row er
+    const int er = tid >> 1, eh = tid & 1;
+    const bool rv = er < nrows;
+    uint32_t oi_r[16];
+    float ov_r[16];
+    {
+        const size_t base = (size_t)(m0 + (rv ? er : 0)) * FRQ_T + eh * 16;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const uint4 x = *reinterpret_cast<const uint4*>(oidx + base + 4 * v);
+            const float4 y = *reinterpret_cast<const float4*>(oval + base + 4 * v);
+            oi_r[4 * v] = x.x; oi_r[4 * v + 1] = x.y; oi_r[4 * v + 2] = x.z; oi_r[4 * v + 3] = x.w;
+            ov_r[4 * v] = y.x; ov_r[4 * v + 1] = y.y; ov_r[4 * v + 2] = y.z; ov_r[4 * v + 3] = y.w;
+        }
+    }
+    // valid outliers of this thread: q = 16eh + v < t, channel inside the row
+    auto qv = [&](int v) { return rv && 16 * eh + v < t && oi_r[v] < (uint32_t)K; };
+
+    // the row's digit scale and non-finite flag first, while the bitmap is
+    // built below (its two threads are adjacent lanes)
+    float mx = 0.0f;
+    int fin = 0;
+#pragma unroll
+    for (int v = 0; v < 16; ++v)
+        if (rv && 16 * eh + v < t) {
+            fin |= !(fabsf(ov_r[v]) <= 3.0e38f);
+            mx = fmaxf(mx, fabsf(ov_r[v]));
+        }
+    mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+    fin |= __shfl_xor(fin, 1, 64);
+    // so = 2^(E - 15) with mx = m * 2^E, m in [0.5, 1): av / so is exact and
+    // below 2^15 in magnitude; rows whose values are not finite, or so tiny
+    // that 1/so leaves the f32 range, take the exact corr
+    int E = 0;
+    (void)frexpf(mx, &E);
+    if (mx > 0.0f && E < -100) fin = 1;
+    const bool sc = mx > 0.0f && !fin;
+    const float so = sc ? ldexpf(1.0f, E - 15) : 1.0f, rso = sc ? ldexpf(1.0f, 15 - E) : 1.0f;
+
+    const int nwk = Kp >> 5;  // <= 640 bitmap words
+    for (int w = tid; w < nwk; w += 256) bitmap[w] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int v = 0; v < 16; ++v)
+        if (qv(v)) atomicOr(&bitmap[oi_r[v] >> 5], 1u << (oi_r[v] & 31));
+    __syncthreads();
+    {
+        const int C = (nwk + 255) / 256, lo = tid * C, hi = min(lo + C, nwk);
+        uint32_t cnt = 0;
+        for (int w = lo; w < hi; ++w) cnt += __popc(bitmap[w]);
+        uint32_t nu_total;
+        uint32_t base = excl_scan256(cnt, scan, &nu_total);
+        for (int w = lo; w < hi; ++w) { wpre[w] = base; base += __popc(bitmap[w]); }
+        if (tid == 0) scan[5] = nu_total;
+    }
+    __syncthreads();
+    const int nu = (int)scan[5];
+    // union position and the f16 pair (hi, lo) of av / so, hi + lo within
+    // 2^-22 of it (rows taking the exact corr get none)
+    int pos[16];
+    uint32_t dig[16];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        pos[v] = -1;
+        dig[v] = 0u;
+        if (qv(v) && !fin) {
+            const uint32_t c = oi_r[v];
+            pos[v] = (int)(wpre[c >> 5] + __popc(bitmap[c >> 5] & ((1u << (c & 31)) - 1u)));
+            const float x = ov_r[v] * rso;  // exact: rso = 1 / so, a power of two
+            const _Float16 hi = (_Float16)x;
+            const _Float16 lo = (_Float16)(x - (float)hi);
+            dig[v] = (uint32_t)__builtin_bit_cast(uint16_t, hi) |
+                     ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
+        }
+    }
+    if (blockIdx.y == 0) {
+        uint32_t* ut = uch + (size_t)mt * cap;
+        if (tid == 0) nu_out[mt] = nu;
+        if (eh == 0) {
+            so_out[m0 + er] = rv ? so : 1.0f;
+            fin_out[m0 + er] = (rv && fin) ? 1.0f : 0.0f;
+        }
+        // every union channel is some outlier's: equal values where shared
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+            if (qv(v)) {
+                const uint32_t c = oi_r[v];
+                ut[wpre[c >> 5] + __popc(bitmap[c >> 5] & ((1u << (c & 31)) - 1u))] = c;
+            }
+        for (int p = nu + tid; p < (nu + CH - 1) / CH * CH; p += 256) ut[p] = 0u;
+    }
+    const int nch = (nu + CH - 1) / CH;
+    for (int c = blockIdx.y; c < nch; c += gridDim.y) {
+        for (int i = tid; i < DCH / 16; i += 256) reinterpret_cast<uint4*>(Dl)[i] = make_uint4(0, 0, 0, 0);
+        __syncthreads();
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int e = pos[v] - CH * c;
+            if (e >= 0 && e < CH) {
+                // entry e: half e / 32, lane group (e / 8) % 4, element e % 8
+                const int off = (16 * ((e >> 3) & 3) + (er & 15)) * 8 + (e & 7);
+                uint16_t* dl = reinterpret_cast<uint16_t*>(Dl);
+#pragma unroll
+                for (int p = 0; p < 2; ++p)
+                    dl[((p * 2 + (e >> 5)) * 8 + (er >> 4)) * 512 + off] = (uint16_t)(dig[v] >> (16 * p));
+            }
+        }
+        __syncthreads();
+        int8_t* dst = D + ((size_t)mt * (cap / CH) + c) * DCH;
+        for (int i = tid; i < DCH / 16; i += 256)
+            reinterpret_cast<uint4*>(dst)[i] = reinterpret_cast<const uint4*>(Dl)[i];
+        __syncthreads();
+    }
+}
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+
+// Two signed bytes of w (sel 0x04010400: bytes 0, 1; 0x04030402: bytes 2, 3)
+// as an exact f16 pair: 0x6400 | (b ^ 0x80) is 1024 + b + 128.
+__device__ __forceinline__ uint32_t i8x2_to_f16x2(uint32_t w, uint32_t sel) {
+    const uint32_t m = __builtin_amdgcn_perm(0x64646464u, w ^ 0x80808080u, sel);
+    const v2h h = __builtin_bit_cast(v2h, m) - (v2h){(_Float16)1152.0f, (_Float16)1152.0f};
+    return __builtin_bit_cast(uint32_t, h);
+}
+
+// 4x4 byte transpose: out[y] byte x = in[x] byte y.
+__device__ __forceinline__ void tr4(const uint32_t* in, uint32_t* out) {
+    const uint32_t t0 = __builtin_amdgcn_perm(in[1], in[0], 0x05010400u);
+    const uint32_t t1 = __builtin_amdgcn_perm(in[1], in[0], 0x07030602u);
+    const uint32_t t2 = __builtin_amdgcn_perm(in[3], in[2], 0x05010400u);
+    const uint32_t t3 = __builtin_amdgcn_perm(in[3], in[2], 0x07030602u);
+    out[0] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
+    out[1] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
+    out[2] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
+    out[3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
+}
+
 template <int BN, int NST>
 __global__ __launch_bounds__(256, 2) void gemm_i8_kernel(
     const int8_t* __restrict__ Ab, const int8_t* __restrict__ Wb,
     const int8_t* __restrict__ Wkn, const int8_t* __restrict__ Wrow,
     const float* __restrict__ scale, const float* __restrict__ sa, int M, int Mp,
-    int N, int Np, int K, int Kp, int t, const uint32_t* __restrict__ oidx,
+    int N, int Np, int Kp, int t, const uint32_t* __restrict__ oidx,
     const float* __restrict__ oval, float* __restrict__ out,
-    int32_t* __restrict__ acc_dbg, int MT) {
+    int32_t* __restrict__ acc_dbg, int MT, int cap, const int* __restrict__ nu_g,
+    const uint32_t* __restrict__ uch, const float* __restrict__ so_g,
+    const float* __restrict__ fin_g, const int8_t* __restrict__ D) {
     constexpr int ABLK = GBM / 16, BBLK = BN / 16, SBLK = ABLK + BBLK;
     constexpr int STAGE = SBLK * 1024;
     constexpr int TM = 4, TN = BN / 32;  // 16x16 blocks per wave (64 x BN/2)
@@ -166,113 +337,45 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_kernel(
     __syncthreads();  // every fragment read; the ring is free for the epilogue
 
     // ---- epilogue ------------------------------------------------------------
-    // LDS carve (the ring is free): header 8 KB (bitmap, prefix, row meta,
-    // scan, chunk channels, column scales), digits 16 KB, union positions 8 KB, digit
-    // blocks D 24 KB (first used as per-channel flags), W[:, U] blocks BN KB/16.
-    const int nwk = Kp >> 5;                                   // <= 640 bitmap words
-    uint32_t* bitmap = reinterpret_cast<uint32_t*>(lds);       // [640]
-    uint32_t* wpre = bitmap + 640;                             // [640]
-    float* meta = reinterpret_cast<float*>(lds + 5120);        // sa, so, fin: [3][128]
-    uint32_t* scan = reinterpret_cast<uint32_t*>(lds + 6656);  // [8]
-    uint32_t* uch = reinterpret_cast<uint32_t*>(lds + 6688);   // chunk channels [CH]
-    float* scl = reinterpret_cast<float*>(lds + 7168);         // tile column scales [BN]
-    uint32_t* dig = reinterpret_cast<uint32_t*>(lds + 8192);   // [128][32] digits d2|d1|d0
-    uint16_t* dpos = reinterpret_cast<uint16_t*>(lds + 24576); // [128][32] union position
-    int8_t* D = lds + 32768;                                   // 3 x 8 blocks (CH = 64)
-    uint8_t* flag = reinterpret_cast<uint8_t*>(D);             // [Kp] before D is built
-    int8_t* WU = lds + 32768 + 24 * 1024;                      // BN/16 blocks
+    // LDS carve (the ring is free): W[:, U] as f16 B blocks (2 x BN/16 x
+    // 1 KB), row meta (sa, so, exact flag), column scales, and one 16-row
+    // f32 slab per wave.
+    constexpr int SP = BN / 2 + 4;  // slab pitch (floats)
+    constexpr int WUB = BN * CH * 2;
+    static_assert(WUB + 4 * (3 * GBM + BN + 4 * 16 * SP) <= NST * STAGE, "epilogue LDS exceeds the ring");
+    int8_t* WU = lds;
+    float* meta = reinterpret_cast<float*>(lds + WUB);  // [3][128]
+    float* scl = meta + 3 * GBM;                            // [BN]
+    float* slab = scl + BN + 16 * SP * wave;                // [16][SP]
 
     const int tid = threadIdx.x;
-    const int nrows = min(GBM, M - m0);
-    // every global operand of the epilogue in one batch of independent loads:
-    // thread (er, eh) takes outliers 16eh..16eh+15 of tile row er; the tile's
-    // column scales go to LDS
-    const int er = tid >> 1, eh = tid & 1;
-    const bool rv = er < nrows;
-    uint32_t oi_r[16];
-    float ov_r[16];
-    {
-        const size_t base = (size_t)(m0 + (rv ? er : 0)) * FRQ_T + eh * 16;
+    const int nu = __builtin_amdgcn_readfirstlane(nu_g[mt]);
+    const int nch = (nu + CH - 1) / CH;
+    // the W[:, U] gather: unit (eg, cq) = union entries 8eg..8eg+7 of chunk c
+    // at tile columns 4cq..4cq+3 (one dword of a wkn row each); UPT units
+    // per thread
+    constexpr int NQ = BN / 4, UPT = 8 * NQ / 256;
+    const uint32_t* ut = uch + (size_t)mt * cap;
+    uint32_t gw[8 * UPT];
+    auto gather = [&](int c) {
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const uint4 x = *reinterpret_cast<const uint4*>(oidx + base + 4 * v);
-            const float4 y = *reinterpret_cast<const float4*>(oval + base + 4 * v);
-            oi_r[4 * v] = x.x; oi_r[4 * v + 1] = x.y; oi_r[4 * v + 2] = x.z; oi_r[4 * v + 3] = x.w;
-            ov_r[4 * v] = y.x; ov_r[4 * v + 1] = y.y; ov_r[4 * v + 2] = y.z; ov_r[4 * v + 3] = y.w;
+        for (int u = 0; u < UPT; ++u) {
+            const int un = tid + 256 * u, cq = un % NQ, eg = un / NQ;
+            const uint4 q0 = *reinterpret_cast<const uint4*>(ut + c * CH + 8 * eg);
+            const uint4 q1 = *reinterpret_cast<const uint4*>(ut + c * CH + 8 * eg + 4);
+            const uint32_t chs[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+            for (int x = 0; x < 8; ++x)
+                gw[8 * u + x] = *reinterpret_cast<const uint32_t*>(Wkn + (size_t)chs[x] * Np + n0 + 4 * cq);
         }
+    };
+    if (nch > 0) gather(0);
+    if (tid < GBM) {
+        meta[tid] = sa[min(m0 + tid, M - 1)];
+        meta[GBM + tid] = so_g[m0 + tid];
+        meta[2 * GBM + tid] = fin_g[m0 + tid];
     }
-    const float sa_r = sa[min(m0 + er, M - 1)];
     if (tid < BN) scl[tid] = scale[n0 + tid];  // Np-padded: in bounds
-    // valid outliers of this thread: q = 16eh + v < t
-    auto qv = [&](int v) { return rv && 16 * eh + v < t; };
-
-    // union of the tile's outlier channels: byte flags, then bitmap words
-    for (int i = tid; i < Kp / 16; i += 256) reinterpret_cast<uint4*>(flag)[i] = make_uint4(0, 0, 0, 0);
-    __syncthreads();
-#pragma unroll
-    for (int v = 0; v < 16; ++v)
-        if (qv(v) && oi_r[v] < (uint32_t)K) flag[oi_r[v]] = 1;
-    __syncthreads();
-    for (int w = tid; w < nwk; w += 256) {
-        const uint4 f0 = reinterpret_cast<const uint4*>(flag)[2 * w];
-        const uint4 f1 = reinterpret_cast<const uint4*>(flag)[2 * w + 1];
-        const uint32_t fw[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
-        uint32_t bits = 0;
-#pragma unroll
-        for (int b = 0; b < 32; ++b) bits |= ((fw[b >> 2] >> (8 * (b & 3))) & 1u) << b;
-        bitmap[w] = bits;
-    }
-    __syncthreads();
-    {
-        const int C = (nwk + 255) / 256, lo = tid * C, hi = min(lo + C, nwk);
-        uint32_t cnt = 0;
-        for (int w = lo; w < hi; ++w) cnt += __popc(bitmap[w]);
-        uint32_t nu_total;
-        uint32_t base = excl_scan256(cnt, scan, &nu_total);
-        for (int w = lo; w < hi; ++w) { wpre[w] = base; base += __popc(bitmap[w]); }
-        if (tid == 0) scan[5] = nu_total;
-    }
-    // per row: sa, the digit scale so and the non-finite flag (the row's two
-    // threads are adjacent lanes)
-    float mx = 0.0f;
-    int fin = 0;
-#pragma unroll
-    for (int v = 0; v < 16; ++v)
-        if (qv(v)) {
-            fin |= !(fabsf(ov_r[v]) <= 3.0e38f);
-            mx = fmaxf(mx, fabsf(ov_r[v]));
-        }
-    mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-    fin |= __shfl_xor(fin, 1, 64);
-    float so = mx > 0.0f ? mx / XMAX : 1.0f;
-    if (!(so >= 1.0e-30f) || !(so <= 1.0e30f)) fin = 1;  // keep digits exact
-    if (eh == 0) {
-        meta[er] = sa_r;
-        meta[GBM + er] = fin ? 0.0f : so;
-        meta[2 * GBM + er] = fin ? 1.0f : 0.0f;
-    }
-    __syncthreads();
-    const int nu = (int)scan[5];
-    // union position and three int8 digits of each outlier
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-        uint32_t dv = 0;
-        uint16_t p = 0xFFFF;
-        if (qv(v) && !fin) {
-            const uint32_t c = min(oi_r[v], (uint32_t)(K - 1));
-            p = (uint16_t)(wpre[c >> 5] + __popc(bitmap[c >> 5] & ((1u << (c & 31)) - 1u)));
-            float xf = rintf(ov_r[v] / so);
-            xf = fminf(fmaxf(xf, -XMAX), XMAX);
-            const int X = (int)xf;
-            const int d0 = (int)(int8_t)(X & 0xFF);
-            const int X1 = (X - d0) >> 8;
-            const int d1 = (int)(int8_t)(X1 & 0xFF);
-            const int d2 = (X1 - d1) >> 8;
-            dv = (uint32_t)(d0 & 0xFF) | ((uint32_t)(d1 & 0xFF) << 8) | ((uint32_t)(d2 & 0xFF) << 16);
-        }
-        dig[er * FRQ_T + 16 * eh + v] = dv;
-        dpos[er * FRQ_T + 16 * eh + v] = p;
-    }
 
     if (acc_dbg) {
 #pragma unroll
@@ -286,120 +389,142 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_kernel(
                     if (i < M && j < N) acc_dbg[(size_t)i * N + j] = acc[bm][bn][c];
                 }
     }
-    // t = sa * acc for the whole wave tile, in place of acc
-    float tv[TM][TN][4];
-#pragma unroll
-    for (int bm = 0; bm < TM; ++bm)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const float sai = meta[wm * 64 + bm * 16 + (lane >> 4) * 4 + c];
-#pragma unroll
-            for (int bn = 0; bn < TN; ++bn) tv[bm][bn][c] = sai * (float)acc[bm][bn][c];
-        }
-
-    // corr, one union chunk of CH channels at a time: D_d blocks (d, rb) hold
-    // rows 16rb.., chunk entries in lane order; WU block cb holds tile
-    // columns 16cb.., the chunk's channels in lane order
-    for (int u0 = 0; u0 < nu; u0 += CH) {
-        __syncthreads();  // dig/dpos written; the previous chunk's blocks consumed
-        for (int i = tid; i < 24 * 64; i += 256) reinterpret_cast<uint4*>(D)[i] = make_uint4(0, 0, 0, 0);
-        if (tid < CH) {
-            // the (u0 + tid)-th set bit of the bitmap: last word with wpre <= target
-            const uint32_t target = (uint32_t)(u0 + tid);
-            uint32_t ch = 0;
-            if (target < (uint32_t)nu) {
-                int lo = 0, hi = nwk - 1;
-                while (lo < hi) {
-                    const int mid = (lo + hi + 1) >> 1;
-                    if (wpre[mid] <= target) lo = mid; else hi = mid - 1;
-                }
-                uint32_t bits = bitmap[lo];
-                for (uint32_t k = target - wpre[lo]; k > 0; --k) bits &= bits - 1;
-                ch = bits ? (uint32_t)lo * 32 + (uint32_t)(__ffs(bits) - 1) : 0u;
-                ch = min(ch, (uint32_t)(K - 1));
-            }
-            uch[tid] = ch;
-        }
-        __syncthreads();
-        for (int i = tid; i < GBM * FRQ_T; i += 256) {
-            const int e = (int)dpos[i] - u0;
-            if (e < 0 || e >= CH) continue;
-            const int r = i / FRQ_T;
-            const uint32_t dv = dig[i];
-            const int off = ((16 * (e >> 4) + (r & 15)) * 16) + (e & 15);
-#pragma unroll
-            for (int d = 0; d < 3; ++d)
-                D[(d * 8 + (r >> 4)) * 1024 + off] = (int8_t)((dv >> (8 * d)) & 0xFF);
-        }
-        {
-            constexpr int NL = CH * (BN / 16) / 256;  // 16-byte loads per thread
-            v4i wv[NL];
-#pragma unroll
-            for (int l = 0; l < NL; ++l) {
-                const int idx = tid + 256 * l, e = idx % CH, cb = idx / CH;
-                wv[l] = *reinterpret_cast<const v4i*>(Wkn + (size_t)uch[e] * Np + n0 + cb * 16);
-            }
-#pragma unroll
-            for (int l = 0; l < NL; ++l) {
-                const int idx = tid + 256 * l, e = idx % CH, cb = idx / CH;
-#pragma unroll
-                for (int b = 0; b < 16; ++b)
-                    WU[cb * 1024 + ((16 * (e >> 4) + b) * 16) + (e & 15)] =
-                        (int8_t)((uint32_t)wv[l][b >> 2] >> ((b & 3) * 8));
-            }
-        }
-        __syncthreads();
-        // tv += so * (C2 * 2^16 + C1 * 2^8 + C0); so is 0 on non-finite rows
-#pragma unroll
-        for (int bm = 0; bm < TM; ++bm) {
-            float sow[4];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) sow[c] = meta[GBM + wm * 64 + bm * 16 + (lane >> 4) * 4 + c];
-            v4i af[3];
-#pragma unroll
-            for (int d = 0; d < 3; ++d)
-                af[d] = *reinterpret_cast<const v4i*>(D + (d * 8 + wm * 4 + bm) * 1024 + lane * 16);
-#pragma unroll
-            for (int bn = 0; bn < TN; ++bn) {
-                const v4i bf = *reinterpret_cast<const v4i*>(WU + (wn * TN + bn) * 1024 + lane * 16);
-                const v4i c2 = mfma(af[2], bf, v4i{0, 0, 0, 0});
-                const v4i c1 = mfma(af[1], bf, v4i{0, 0, 0, 0});
-                const v4i c0 = mfma(af[0], bf, v4i{0, 0, 0, 0});
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    tv[bm][bn][c] = tv[bm][bn][c] + (sow[c] * 65536.0f) * (float)c2[c];
-                    tv[bm][bn][c] = tv[bm][bn][c] + (sow[c] * 256.0f) * (float)c1[c];
-                    tv[bm][bn][c] = tv[bm][bn][c] + sow[c] * (float)c0[c];
-                }
-            }
-        }
-    }
-
-    // out = scale * t; rows with a non-finite outlier add the exact sequential corr
+    __syncthreads();  // meta, scl
+    // t = (sa * acc) / so for the whole wave tile, in place of acc (so is a
+    // power of two: exact both ways)
+    v4f tv[TM][TN];
 #pragma unroll
     for (int bm = 0; bm < TM; ++bm)
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const int rl = wm * 64 + bm * 16 + (lane >> 4) * 4 + c;
-            const int i = m0 + rl;
-            if (i >= M) continue;
-            const bool exact = meta[2 * GBM + rl] != 0.0f;
+            const float sai = meta[rl], rso = 1.0f / meta[GBM + rl];
 #pragma unroll
-            for (int bn = 0; bn < TN; ++bn) {
-                const int j = n0 + wn * (BN / 2) + bn * 16 + (lane & 15);
-                if (j >= N) continue;
-                float v = tv[bm][bn][c];
-                if (exact) {
-                    float corr = -0.0f;
-                    const int8_t* wr = Wrow + (size_t)j * Kp;
-                    for (int q = 0; q < t; ++q)
-                        corr = corr + oval[(size_t)i * FRQ_T + q] *
-                                          (float)wr[min(oidx[(size_t)i * FRQ_T + q], (uint32_t)(Kp - 1))];
-                    v = v + corr;
-                }
-                out[(size_t)i * N + j] = scl[wn * (BN / 2) + bn * 16 + (lane & 15)] * v;
+            for (int bn = 0; bn < TN; ++bn) tv[bm][bn][c] = (sai * (float)acc[bm][bn][c]) * rso;
+        }
+
+    // corr, one union chunk of 64 channels at a time: t += (hi + lo) . W[:, U]
+    // on the f16 MFMA (32 entries per instruction), straight into t
+    const int8_t* Dt = D + (size_t)mt * (cap / CH) * DCH + (wm * TM) * 1024 + lane * 16;
+    for (int c = 0; c < nch; ++c) {
+        // A fragments of one 16-row block at a time, the next one in flight:
+        // [part (hi, lo)][half]
+        const int8_t* Dc = Dt + (size_t)c * DCH;
+        v4i af[2][4];
+#pragma unroll
+        for (int x = 0; x < 4; ++x) af[0][x] = *reinterpret_cast<const v4i*>(Dc + (x * 8) * 1024);
+        // the gathered bytes -> f16 B blocks: half h, column block cb, lane
+        // 16g + r = column 16cb + r, entries 32h + 8g .. +7
+#pragma unroll
+        for (int u = 0; u < UPT; ++u) {
+            const int un = tid + 256 * u, cq = un % NQ, eg = un / NQ;  // entries 8eg..8eg+7
+            uint32_t o[4][2];
+#pragma unroll
+            for (int z = 0; z < 2; ++z) {
+                uint32_t tmp[4];
+                tr4(gw + 8 * u + 4 * z, tmp);
+#pragma unroll
+                for (int y = 0; y < 4; ++y) o[y][z] = tmp[y];
+            }
+#pragma unroll
+            for (int y = 0; y < 4; ++y) {
+                const int j = 4 * cq + y;
+                uint4 hv;
+                hv.x = i8x2_to_f16x2(o[y][0], 0x04010400u);
+                hv.y = i8x2_to_f16x2(o[y][0], 0x04030402u);
+                hv.z = i8x2_to_f16x2(o[y][1], 0x04010400u);
+                hv.w = i8x2_to_f16x2(o[y][1], 0x04030402u);
+                *reinterpret_cast<uint4*>(WU + ((eg >> 2) * (BN / 16) + (j >> 4)) * 1024 +
+                                          (16 * (eg & 3) + (j & 15)) * 16) = hv;
             }
         }
+        __syncthreads();
+        if (c + 1 < nch) gather(c + 1);  // in flight during this chunk's MFMAs
+#pragma unroll
+        for (int bm = 0; bm < TM; ++bm) {
+            if (bm + 1 < TM) {
+#pragma unroll
+                for (int x = 0; x < 4; ++x)
+                    af[(bm + 1) & 1][x] = *reinterpret_cast<const v4i*>(Dc + (x * 8 + bm + 1) * 1024);
+            }
+#pragma unroll
+            for (int bn = 0; bn < TN; ++bn) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const v4i bf = *reinterpret_cast<const v4i*>(WU + (h * (BN / 16) + wn * TN + bn) * 1024 + lane * 16);
+#pragma unroll
+                    for (int pp = 0; pp < 2; ++pp)
+                        tv[bm][bn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            __builtin_bit_cast(v8h, af[bm & 1][pp * 2 + h]), __builtin_bit_cast(v8h, bf), tv[bm][bn], 0, 0, 0);
+                }
+            }
+        }
+        __syncthreads();  // WU read by every wave before the next chunk's writes
+    }
+
+    // out = scale * t * so (rows with a non-finite outlier add the exact
+    // sequential corr first), through the wave's LDS slab: 16 rows at a time,
+    // written back as 16-byte runs of whole rows
+    const bool vec = (N & 3) == 0;
+    bool wexact = false;  // any exact-corr row among the wave's 64
+#pragma unroll
+    for (int bm = 0; bm < TM; ++bm)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) wexact |= meta[2 * GBM + wm * 64 + bm * 16 + (lane >> 4) * 4 + q] != 0.0f;
+    wexact = __builtin_amdgcn_ballot_w64(wexact) != 0;
+    const int cbase = n0 + wn * (BN / 2);
+    constexpr int Q4 = BN / 8, NIT = 16 * Q4 / 64;  // float4 runs per slab row, per lane
+#pragma unroll
+    for (int bm = 0; bm < TM; ++bm) {
+        const int rbase = m0 + wm * 64 + bm * 16;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int rs = (lane >> 4) * 4 + q;  // slab row
+            const int rl = wm * 64 + bm * 16 + rs;
+            const float so = meta[GBM + rl];
+#pragma unroll
+            for (int bn = 0; bn < TN; ++bn) {
+                const int cl = bn * 16 + (lane & 15);  // slab column
+                float v = tv[bm][bn][q] * so;
+                if (wexact && meta[2 * GBM + rl] != 0.0f && rbase + rs < M) {
+                    const int i = rbase + rs, j = min(cbase + cl, N - 1);
+                    float corr = -0.0f;
+                    const int8_t* wr = Wrow + (size_t)j * Kp;
+                    for (int qq = 0; qq < t; ++qq)
+                        corr = corr + oval[(size_t)i * FRQ_T + qq] *
+                                          (float)wr[min(oidx[(size_t)i * FRQ_T + qq], (uint32_t)(Kp - 1))];
+                    v = v + corr;
+                }
+                slab[rs * SP + cl] = scl[wn * (BN / 2) + cl] * v;
+            }
+        }
+        wave_sync();
+        float4 vv[NIT];
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+            const int idx = it * 64 + lane;
+            vv[it] = *reinterpret_cast<const float4*>(slab + (idx / Q4) * SP + 4 * (idx % Q4));
+        }
+        if (vec && rbase + 16 <= M && cbase + BN / 2 <= N) {  // wave-uniform
+#pragma unroll
+            for (int it = 0; it < NIT; ++it) {
+                const int idx = it * 64 + lane;
+                *reinterpret_cast<float4*>(out + (size_t)(rbase + idx / Q4) * N + cbase + 4 * (idx % Q4)) = vv[it];
+            }
+        } else {
+#pragma unroll
+            for (int it = 0; it < NIT; ++it) {
+                const int idx = it * 64 + lane, i = rbase + idx / Q4, j = cbase + 4 * (idx % Q4);
+                if (i >= M) continue;
+                float* o = out + (size_t)i * N + j;
+                if (j < N) o[0] = vv[it].x;
+                if (j + 1 < N) o[1] = vv[it].y;
+                if (j + 2 < N) o[2] = vv[it].z;
+                if (j + 3 < N) o[3] = vv[it].w;
+            }
+        }
+        wave_sync();  // the slab is read before the next 16 rows overwrite it
+    }
 }
 
 // (R, Kp) row-major (pitch) -> blocked, R a multiple of 16; rows >= valid are zero.
@@ -415,10 +540,35 @@ __global__ void blockify_kernel(const int8_t* __restrict__ src, size_t valid, si
     }
 }
 
+// The pre-pass outputs, carved from the caller's workspace.
+struct Prep {
+    int cap = 0;
+    int* nu = nullptr;
+    uint32_t* uch = nullptr;
+    float* so = nullptr;
+    float* fin = nullptr;
+    int8_t* D = nullptr;
+};
+
+size_t al256(size_t x) { return (x + 255) / 256 * 256; }
+
+Prep carve_prep(void* ws, size_t mp, size_t kp) {
+    Prep p;
+    const size_t mt = mp / GBM;
+    p.cap = union_cap((int)kp);
+    char* c = static_cast<char*>(ws);
+    p.nu = reinterpret_cast<int*>(c); c += al256(mt * 4);
+    p.uch = reinterpret_cast<uint32_t*>(c); c += al256(mt * p.cap * 4);
+    p.so = reinterpret_cast<float*>(c); c += al256(mp * 4);
+    p.fin = reinterpret_cast<float*>(c); c += al256(mp * 4);
+    p.D = reinterpret_cast<int8_t*>(c);
+    return p;
+}
+
 template <int BN, int NST>
 hipError_t launch_t(const Weight& w, size_t m, const int8_t* a8b, const float* sa,
                     const uint32_t* oidx, const float* oval, float* out, int32_t* acc,
-                    hipStream_t s) {
+                    const Prep& p, hipStream_t s) {
     const int MT = (int)((m + GBM - 1) / GBM), NT = (int)(w.np / BN);
     const size_t lds = (size_t)NST * (GBM + BN) / 16 * 1024;
     const int t = (int)(w.k < FRQ_T ? w.k : FRQ_T);
@@ -431,8 +581,8 @@ hipError_t launch_t(const Weight& w, size_t m, const int8_t* a8b, const float* s
         attr_set = true;
     }
     kern<<<dim3((unsigned)(MT * NT)), dim3(256), lds, s>>>(
-        a8b, w.wblk, w.wkn, w.wt, w.scale, sa, (int)m, (int)round_up(m, GBM), (int)w.n,
-        (int)w.np, (int)w.k, (int)w.kp, t, oidx, oval, out, acc, MT);
+        a8b, w.wblk, w.wkn, w.wt, w.scale, sa, (int)m, MT * GBM, (int)w.n, (int)w.np, (int)w.kp, t,
+        oidx, oval, out, acc, MT, p.cap, p.nu, p.uch, p.so, p.fin, p.D);
     return hipGetLastError();
 }
 
@@ -448,17 +598,32 @@ hipError_t launch_blockify(const int8_t* src, size_t valid, size_t R, size_t kp,
     return hipGetLastError();
 }
 
+size_t gemm_ws_bytes(size_t m, size_t kp) {
+    const size_t mp = round_up(m, GBM), mt = mp / GBM, cap = (size_t)union_cap((int)kp);
+    return al256(mt * 4) + al256(mt * cap * 4) + 2 * al256(mp * 4) + mt * (cap / CH) * DCH;
+}
+
 hipError_t launch_gemm_i8(const Weight& w, size_t m, const int8_t* a8b,
                           const float* sa, const uint32_t* oidx,
-                          const float* oval, float* out, int32_t* acc,
+                          const float* oval, float* out, int32_t* acc, void* ws,
                           hipStream_t s) {
     // a8b holds round_up(m, 128) blocked rows; wblk / wkn are padded to Np
     // (a multiple of 256) and Kp (a multiple of 128); Kp <= 20480 keeps the
-    // channel bitmap within its 640 LDS words
-    if (w.kp > 20480 || !w.wblk) return hipErrorInvalidValue;
-    const size_t tiles256 = ((m + GBM - 1) / GBM) * (w.np / 256);
-    if (tiles256 >= 512) return launch_t<256, 3>(w, m, a8b, sa, oidx, oval, out, acc, s);
-    return launch_t<128, 4>(w, m, a8b, sa, oidx, oval, out, acc, s);
+    // channel bitmap within its 640 LDS words; ws holds gemm_ws_bytes(m, Kp)
+    if (w.kp > 20480 || !w.wblk || !ws) return hipErrorInvalidValue;
+    const size_t mp = round_up(m, GBM);
+    const Prep p = carve_prep(ws, mp, w.kp);
+    const int MT = (int)(mp / GBM), nchmax = p.cap / CH;
+    const int t = (int)(w.k < FRQ_T ? w.k : FRQ_T);
+    // chunk groups: enough workgroups to build a dense union's chunks in
+    // parallel; each one builds the (cheap) union itself
+    const int ncg = std::max(1, std::min(nchmax, 256 / MT));
+    gemm_prep_kernel<<<dim3((unsigned)MT, (unsigned)ncg), dim3(256), 0, s>>>(
+        (int)m, (int)w.k, (int)w.kp, t, oidx, oval, p.cap, p.nu, p.uch, p.so, p.fin, p.D);
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    const size_t tiles256 = (size_t)MT * (w.np / 256);
+    if (tiles256 >= 512) return launch_t<256, 3>(w, m, a8b, sa, oidx, oval, out, acc, p, s);
+    return launch_t<128, 4>(w, m, a8b, sa, oidx, oval, out, acc, p, s);
 }
 
 }  // namespace frq

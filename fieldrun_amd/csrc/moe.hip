@@ -104,11 +104,6 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 }
 
 // ---- routing: one wave per token ----------------------------------------
-__device__ __forceinline__ void wave_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-}
-
 // Routing of one token by one wave: softmax (max, exp, sequential sum,
 // divide), k rounds of arg-max by (p desc, expert asc), renormalised
 // weights.  p: E floats of LDS; picks go to pe / pw (k entries of LDS, pick
