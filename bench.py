@@ -247,14 +247,18 @@ def main():
             a = synth.activations(2048, k, synth.seed(1, 8))
             da = hip.DeviceArray.from_numpy(a)
             do = hip.DeviceArray((2048, n), np.float32)
-            us = time_loop(lambda i: w.mm_dev(da.ptr, 2048, do.ptr), 10) * 1e3
+            # ~150 us launches: 10 warm-up launches, then the median of three
+            # trials of 20 (single trials of 10 vary by ~15% on the clock)
+            def med3(fn):
+                return float(np.median([time_loop(fn, 20, warm=10 if r == 0 else 0) for r in range(3)])) * 1e3
+            us = med3(lambda i: w.mm_dev(da.ptr, 2048, do.ptr))
             kp = fa.quant_pitch(k)
             a8 = hip.DeviceArray((2048, kp), np.int8)
             sa = hip.DeviceArray((2048,), np.float32)
             oi = hip.DeviceArray((2048, 32), np.uint32)
             ov = hip.DeviceArray((2048, 32), np.float32)
             ctx.quant_dev(da.ptr, 2048, k, a8.ptr, sa.ptr, oi.ptr, ov.ptr)
-            gus = time_loop(lambda i: w.mm_q_dev(a8.ptr, sa.ptr, oi.ptr, ov.ptr, 2048, do.ptr), 10) * 1e3
+            gus = med3(lambda i: w.mm_q_dev(a8.ptr, sa.ptr, oi.ptr, ov.ptr, 2048, do.ptr))
             ops = 2.0 * 2048 * n * k
             detail["int8_m2048_gemm"][f"K{k}_N{n}"] = {
                 "full_linear_us": round(us, 1), "full_linear_TOPS": round(ops / (us * 1e-6) / 1e12, 1),

@@ -101,7 +101,7 @@ size_t i8_scratch_bytes(const Weight& w, size_t m, bool rowmajor_copy) {
     size_t b = round_up(mp * w.kp, 256) + round_up(mp * 4, 256) +
                2 * round_up(mp * FRQ_T * 4, 256);
     if (rowmajor_copy) b += round_up(m * w.kp, 256);
-    if (!use_gemv(w, m)) b += round_up(gemm_ws_bytes(m, w.kp), 256);
+    if (!use_gemv(w, m)) b += round_up(gemm_ws_bytes(m, w.kp, w.np), 256);
     return b;
 }
 
@@ -118,7 +118,7 @@ int run_i8(frq_ctx* c, const Weight& w, const float* d_a, size_t m, float* d_out
     uint32_t* oi = cv.take<uint32_t>(mp * FRQ_T);
     float* ov = cv.take<float>(mp * FRQ_T);
     int8_t* a8rm = (gemm && a8o) ? cv.take<int8_t>(m * w.kp) : a8;
-    void* gws = gemm ? cv.take<char>(gemm_ws_bytes(m, w.kp)) : nullptr;
+    void* gws = gemm ? cv.take<char>(gemm_ws_bytes(m, w.kp, w.np)) : nullptr;
     if (a8o) { *a8o = a8rm; *sao = sa; *oio = oi; *ovo = ov; }
     if (w.k == 0) {
         HIPCHK(hipMemsetAsync(d_out, 0, m * w.n * sizeof(float), c->stream), "hipMemsetAsync");
@@ -460,7 +460,7 @@ int frq_mm_i8_q_dev(frq_ctx* c, const frq_w* wh, const int8_t* d_a8, const float
     }
     // the MFMA GEMM reads round_up(m, 128) rows of a8 in the blocked layout
     const size_t mp = round_up(m, FRQ_MALIGN);
-    if (int rc = ws_reserve(c, round_up(mp * w.kp, 256) + gemm_ws_bytes(m, w.kp))) return rc;
+    if (int rc = ws_reserve(c, round_up(mp * w.kp, 256) + gemm_ws_bytes(m, w.kp, w.np))) return rc;
     int8_t* a8 = (int8_t*)c->ws;
     void* gws = (char*)c->ws + round_up(mp * w.kp, 256);
     HIPCHK(launch_blockify(d_a8, m, mp, w.kp, w.kp, a8, c->stream), "launch blockify");

@@ -169,9 +169,9 @@ hipError_t launch_skinny_i8(const Weight& w, size_t m, const int8_t* a8, const f
 hipError_t launch_blockify(const int8_t* src, size_t valid, size_t R, size_t kp,
                            size_t pitch, int8_t* dst, hipStream_t s);
 // int8 MFMA GEMM for m > 16 on blocked a8 (R = round_up(m, 128)).
-// ws: gemm_ws_bytes(m, kp) bytes of device workspace (the per-row-tile
-// outlier union and digit blocks).
-size_t gemm_ws_bytes(size_t m, size_t kp);
+// ws: gemm_ws_bytes(m, kp, np) bytes of device workspace (the per-row-tile
+// outlier union and correction operands, split-K partial tiles).
+size_t gemm_ws_bytes(size_t m, size_t kp, size_t np);
 hipError_t launch_gemm_i8(const Weight& w, size_t m, const int8_t* a8b,
                           const float* sa, const uint32_t* oidx,
                           const float* oval, float* out, int32_t* acc, void* ws,

@@ -265,7 +265,11 @@ __device__ __forceinline__ void tr4(const uint32_t* in, uint32_t* out) {
     out[3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
 }
 
-template <int BN, int NST>
+// MODE 0: the whole K range, then the epilogue.  MODE 1 (split K): workgroup
+// b runs k-split b % nsplit of tile b / nsplit and stores its int32 tile to
+// part.  MODE 2: one workgroup per tile adds the tile's nsplit partial tiles
+// in split order (exact) and runs the epilogue.
+template <int BN, int NST, int MODE>
 __global__ __launch_bounds__(256, 2) void gemm_i8_kernel(
     const int8_t* __restrict__ Ab, const int8_t* __restrict__ Wb,
     const int8_t* __restrict__ Wkn, const int8_t* __restrict__ Wrow,
@@ -274,30 +278,40 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_kernel(
     const float* __restrict__ oval, float* __restrict__ out,
     int32_t* __restrict__ acc_dbg, int MT, int cap, const int* __restrict__ nu_g,
     const uint32_t* __restrict__ uch, const float* __restrict__ so_g,
-    const float* __restrict__ fin_g, const int8_t* __restrict__ D) {
+    const float* __restrict__ fin_g, const int8_t* __restrict__ D, int32_t* __restrict__ part,
+    int nsplit) {
     constexpr int ABLK = GBM / 16, BBLK = BN / 16, SBLK = ABLK + BBLK;
     constexpr int STAGE = SBLK * 1024;
     constexpr int TM = 4, TN = BN / 32;  // 16x16 blocks per wave (64 x BN/2)
-    constexpr int PW = SBLK / 4;         // DMA blocks per wave per stage
+    // DMA blocks per wave per stage: waves below SBLK % 4 take one more; the
+    // ring's waits count the smaller number (waiting longer is safe)
+    constexpr int PW = SBLK / 4, PWX = (SBLK + 3) / 4;
     extern __shared__ __attribute__((aligned(1024))) int8_t lds[];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave >> 1, wn = wave & 1;
     int mt, nt;
-    tile_of(blockIdx.x, gridDim.x, MT, mt, nt);
+    const int tb = MODE == 1 ? (int)blockIdx.x / nsplit : (int)blockIdx.x;
+    const int sp = MODE == 1 ? (int)blockIdx.x % nsplit : 0;
+    tile_of(tb, MODE == 1 ? (int)gridDim.x / nsplit : (int)gridDim.x, MT, mt, nt);
     const int m0 = mt * GBM, n0 = nt * BN;
-    const int S = Kp / GBK;
+    const int SK = Kp / GBK;  // k-steps of the whole row
+    // this workgroup's k-steps: [k0, k0 + S)
+    const int k0 = MODE == 1 ? SK * sp / nsplit : 0;
+    const int S = MODE == 0 ? SK : MODE == 1 ? SK * (sp + 1) / nsplit - k0 : 0;
     const size_t arb = (size_t)Mp / 16, wrb = (size_t)Np / 16;
 
     auto issue = [&](int ks, int8_t* st) {
 #pragma unroll
-        for (int i = 0; i < PW; ++i) {
-            const int tb = wave + 4 * i;  // wave-uniform
-            const int8_t* src = tb < ABLK
-                ? Ab + ((size_t)ks * arb + m0 / 16 + tb) * 1024 + lane * 16
-                : Wb + ((size_t)ks * wrb + n0 / 16 + (tb - ABLK)) * 1024 + lane * 16;
-            dma16(src, st + tb * 1024);
+        for (int i = 0; i < PWX; ++i) {
+            const int bl = wave + 4 * i;  // wave-uniform
+            if (PWX == PW || bl < SBLK) {
+                const int8_t* src = bl < ABLK
+                    ? Ab + ((size_t)(k0 + ks) * arb + m0 / 16 + bl) * 1024 + lane * 16
+                    : Wb + ((size_t)(k0 + ks) * wrb + n0 / 16 + (bl - ABLK)) * 1024 + lane * 16;
+                dma16(src, st + bl * 1024);
+            }
         }
     };
 
@@ -334,6 +348,25 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_kernel(
 #pragma unroll
             for (int bn = 0; bn < TN; ++bn) acc[bm][bn] = mfma(af[bm], bf[bn], acc[bm][bn]);
     }
+    // a k-split's int32 tile, 16 bytes per lane per block, 4 KB per block
+    // over the workgroup
+    int32_t* pt = part + ((size_t)(MODE == 1 ? blockIdx.x : tb * nsplit) * (TM * TN) * 256 + threadIdx.x) * 4;
+    if constexpr (MODE == 1) {
+#pragma unroll
+        for (int bm = 0; bm < TM; ++bm)
+#pragma unroll
+            for (int bn = 0; bn < TN; ++bn)
+                *reinterpret_cast<v4i*>(pt + (size_t)(bm * TN + bn) * 1024) = acc[bm][bn];
+        return;
+    }
+    if constexpr (MODE == 2) {
+        for (int q = 0; q < nsplit; ++q)
+#pragma unroll
+            for (int bm = 0; bm < TM; ++bm)
+#pragma unroll
+                for (int bn = 0; bn < TN; ++bn)
+                    acc[bm][bn] += *reinterpret_cast<const v4i*>(pt + ((size_t)q * TM * TN + bm * TN + bn) * 1024);
+    }
     __syncthreads();  // every fragment read; the ring is free for the epilogue
 
     // ---- epilogue ------------------------------------------------------------
@@ -354,13 +387,15 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_kernel(
     // the W[:, U] gather: unit (eg, cq) = union entries 8eg..8eg+7 of chunk c
     // at tile columns 4cq..4cq+3 (one dword of a wkn row each); UPT units
     // per thread
-    constexpr int NQ = BN / 4, UPT = 8 * NQ / 256;
+    constexpr int NQ = BN / 4, UPT = (8 * NQ + 255) / 256;
     const uint32_t* ut = uch + (size_t)mt * cap;
     uint32_t gw[8 * UPT];
     auto gather = [&](int c) {
 #pragma unroll
         for (int u = 0; u < UPT; ++u) {
-            const int un = tid + 256 * u, cq = un % NQ, eg = un / NQ;
+            int un = tid + 256 * u;
+            if ((8 * NQ) % 256) un = min(un, 8 * NQ - 1);  // spare units repeat the last
+            const int cq = un % NQ, eg = un / NQ;
             const uint4 q0 = *reinterpret_cast<const uint4*>(ut + c * CH + 8 * eg);
             const uint4 q1 = *reinterpret_cast<const uint4*>(ut + c * CH + 8 * eg + 4);
             const uint32_t chs[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
@@ -418,6 +453,7 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_kernel(
 #pragma unroll
         for (int u = 0; u < UPT; ++u) {
             const int un = tid + 256 * u, cq = un % NQ, eg = un / NQ;  // entries 8eg..8eg+7
+            if ((8 * NQ) % 256 && un >= 8 * NQ) continue;
             uint32_t o[4][2];
 #pragma unroll
             for (int z = 0; z < 2; ++z) {
@@ -541,6 +577,34 @@ __global__ void blockify_kernel(const int8_t* __restrict__ src, size_t valid, si
 }
 
 // The pre-pass outputs, carved from the caller's workspace.
+// The launch shape: tile width and the number of k-splits.
+struct Plan {
+    int bn = 128;
+    int split = 1;
+};
+
+Plan plan_of(size_t m, size_t kp, size_t np) {
+    Plan pl;
+    const long MT = (long)((m + GBM - 1) / GBM);
+    // tile width: two workgroups per CU run at once (512 slots); a launch
+    // takes ceil(tiles / 512) rounds of a tile's time, about BN + 150 column
+    // units (main loop plus a fixed share: the epilogue, whose correction
+    // chunks cost much the same at either width)
+    long best = -1;
+    for (int cand : {256, 224, 128}) {
+        if (np % cand) continue;
+        const long tiles = MT * (long)(np / cand);
+        const long cost = (tiles + 511) / 512 * (cand + 150);
+        if (best < 0 || cost < best) { best = cost; pl.bn = cand; }
+    }
+    // fewer tiles than CUs: split K over more workgroups, at least four
+    // k-steps each, up to the 512 slots
+    const long tiles = MT * (long)(np / pl.bn), ks = (long)(kp / GBK);
+    if (tiles < 256 && ks >= 8)
+        pl.split = (int)std::max(1L, std::min(512 / tiles, ks / 4));
+    return pl;
+}
+
 struct Prep {
     int cap = 0;
     int* nu = nullptr;
@@ -548,6 +612,7 @@ struct Prep {
     float* so = nullptr;
     float* fin = nullptr;
     int8_t* D = nullptr;
+    int32_t* part = nullptr;  // split-K partial tiles
 };
 
 size_t al256(size_t x) { return (x + 255) / 256 * 256; }
@@ -561,18 +626,19 @@ Prep carve_prep(void* ws, size_t mp, size_t kp) {
     p.uch = reinterpret_cast<uint32_t*>(c); c += al256(mt * p.cap * 4);
     p.so = reinterpret_cast<float*>(c); c += al256(mp * 4);
     p.fin = reinterpret_cast<float*>(c); c += al256(mp * 4);
-    p.D = reinterpret_cast<int8_t*>(c);
+    p.D = reinterpret_cast<int8_t*>(c); c += al256(mt * (p.cap / CH) * DCH);
+    p.part = reinterpret_cast<int32_t*>(c);
     return p;
 }
 
-template <int BN, int NST>
-hipError_t launch_t(const Weight& w, size_t m, const int8_t* a8b, const float* sa,
+template <int BN, int NST, int MODE>
+hipError_t launch_k(const Weight& w, size_t m, const int8_t* a8b, const float* sa,
                     const uint32_t* oidx, const float* oval, float* out, int32_t* acc,
-                    const Prep& p, hipStream_t s) {
+                    const Prep& p, int split, hipStream_t s) {
     const int MT = (int)((m + GBM - 1) / GBM), NT = (int)(w.np / BN);
     const size_t lds = (size_t)NST * (GBM + BN) / 16 * 1024;
     const int t = (int)(w.k < FRQ_T ? w.k : FRQ_T);
-    auto kern = gemm_i8_kernel<BN, NST>;
+    auto kern = gemm_i8_kernel<BN, NST, MODE>;
     static bool attr_set = false;  // per process; the attribute is per function
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -580,10 +646,21 @@ hipError_t launch_t(const Weight& w, size_t m, const int8_t* a8b, const float* s
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    kern<<<dim3((unsigned)(MT * NT)), dim3(256), lds, s>>>(
+    const unsigned grid = (unsigned)(MT * NT * (MODE == 1 ? split : 1));
+    kern<<<dim3(grid), dim3(256), lds, s>>>(
         a8b, w.wblk, w.wkn, w.wt, w.scale, sa, (int)m, MT * GBM, (int)w.n, (int)w.np, (int)w.kp, t,
-        oidx, oval, out, acc, MT, p.cap, p.nu, p.uch, p.so, p.fin, p.D);
+        oidx, oval, out, acc, MT, p.cap, p.nu, p.uch, p.so, p.fin, p.D, p.part, split);
     return hipGetLastError();
+}
+
+template <int BN, int NST>
+hipError_t launch_t(const Weight& w, size_t m, const int8_t* a8b, const float* sa,
+                    const uint32_t* oidx, const float* oval, float* out, int32_t* acc,
+                    const Prep& p, int split, hipStream_t s) {
+    if (split <= 1) return launch_k<BN, NST, 0>(w, m, a8b, sa, oidx, oval, out, acc, p, 1, s);
+    if (hipError_t e = launch_k<BN, NST, 1>(w, m, a8b, sa, oidx, oval, out, acc, p, split, s); e != hipSuccess)
+        return e;
+    return launch_k<BN, NST, 2>(w, m, a8b, sa, oidx, oval, out, acc, p, split, s);
 }
 
 }  // namespace
@@ -598,9 +675,11 @@ hipError_t launch_blockify(const int8_t* src, size_t valid, size_t R, size_t kp,
     return hipGetLastError();
 }
 
-size_t gemm_ws_bytes(size_t m, size_t kp) {
+size_t gemm_ws_bytes(size_t m, size_t kp, size_t np) {
     const size_t mp = round_up(m, GBM), mt = mp / GBM, cap = (size_t)union_cap((int)kp);
-    return al256(mt * 4) + al256(mt * cap * 4) + 2 * al256(mp * 4) + mt * (cap / CH) * DCH;
+    const Plan pl = plan_of(m, kp, np);
+    const size_t part = pl.split > 1 ? (size_t)pl.split * mp * np * 4 : 0;
+    return al256(mt * 4) + al256(mt * cap * 4) + 2 * al256(mp * 4) + al256(mt * (cap / CH) * DCH) + part;
 }
 
 hipError_t launch_gemm_i8(const Weight& w, size_t m, const int8_t* a8b,
@@ -609,7 +688,8 @@ hipError_t launch_gemm_i8(const Weight& w, size_t m, const int8_t* a8b,
                           hipStream_t s) {
     // a8b holds round_up(m, 128) blocked rows; wblk / wkn are padded to Np
     // (a multiple of 256) and Kp (a multiple of 128); Kp <= 20480 keeps the
-    // channel bitmap within its 640 LDS words; ws holds gemm_ws_bytes(m, Kp)
+    // channel bitmap within its 640 LDS words; ws holds
+    // gemm_ws_bytes(m, Kp, Np)
     if (w.kp > 20480 || !w.wblk || !ws) return hipErrorInvalidValue;
     const size_t mp = round_up(m, GBM);
     const Prep p = carve_prep(ws, mp, w.kp);
@@ -621,9 +701,10 @@ hipError_t launch_gemm_i8(const Weight& w, size_t m, const int8_t* a8b,
     gemm_prep_kernel<<<dim3((unsigned)MT, (unsigned)ncg), dim3(256), 0, s>>>(
         (int)m, (int)w.k, (int)w.kp, t, oidx, oval, p.cap, p.nu, p.uch, p.so, p.fin, p.D);
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-    const size_t tiles256 = (size_t)MT * (w.np / 256);
-    if (tiles256 >= 512) return launch_t<256, 3>(w, m, a8b, sa, oidx, oval, out, acc, p, s);
-    return launch_t<128, 4>(w, m, a8b, sa, oidx, oval, out, acc, p, s);
+    const Plan pl = plan_of(m, w.kp, w.np);
+    if (pl.bn == 256) return launch_t<256, 3>(w, m, a8b, sa, oidx, oval, out, acc, p, pl.split, s);
+    if (pl.bn == 224) return launch_t<224, 3>(w, m, a8b, sa, oidx, oval, out, acc, p, pl.split, s);
+    return launch_t<128, 4>(w, m, a8b, sa, oidx, oval, out, acc, p, pl.split, s);
 }
 
 }  // namespace frq

@@ -59,7 +59,8 @@ def test_i8_gemv_bit_exact(ctx, m, k, n):
 
 
 @pytest.mark.parametrize("m,k,n", [(5, 896, 4864), (16, 4096, 1024), (128, 896, 640), (130, 512, 300),
-                                   (64, 37, 50), (16, 14336, 256), (33, 4864, 896), (200, 128, 129)])
+                                   (64, 37, 50), (16, 14336, 256), (33, 4864, 896), (200, 128, 129),
+                                   (128, 14336, 512), (2048, 128, 14336)])
 def test_i8_gemm_acc_exact_out_within_tol(ctx, m, k, n):
     a, wt, scale = case(m, k, n, 200 + m + k + n)
     w = ctx.upload_i8(wt, scale)
