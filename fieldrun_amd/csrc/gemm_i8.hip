@@ -149,11 +149,12 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(
     float mx = 0.0f;
     int fin = 0;
 #pragma unroll
-    for (int v = 0; v < 16; ++v)
-        if (rv && 16 * eh + v < t) {
-            fin |= !(fabsf(ov_r[v]) <= 3.0e38f);
-            mx = fmaxf(mx, fabsf(ov_r[v]));
-        }
+    for (int v = 0; v < 16; ++v) {
+        const bool in = rv && 16 * eh + v < t;
+        const float av = fabsf(ov_r[v]);
+        fin |= in && !(av <= 3.0e38f);
+        mx = in ? fmaxf(mx, av) : mx;
+    }
     mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
     fin |= __shfl_xor(fin, 1, 64);
     // so = 2^(E - 15) with mx = m * 2^E, m in [0.5, 1): av / so is exact and
@@ -165,17 +166,30 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(
     const bool sc = mx > 0.0f && !fin;
     const float so = sc ? ldexpf(1.0f, E - 15) : 1.0f, rso = sc ? ldexpf(1.0f, 15 - E) : 1.0f;
 
+    // the union as byte flags (plain stores: the rows share channels, and
+    // atomics on a few hot words would serialise), then bitmap words
     const int nwk = Kp >> 5;  // <= 640 bitmap words
-    for (int w = tid; w < nwk; w += 256) bitmap[w] = 0u;
+    uint8_t* flag = reinterpret_cast<uint8_t*>(Dl);  // Kp bytes, before Dl holds digits
+    for (int i = tid; i < Kp / 16; i += 256) reinterpret_cast<uint4*>(flag)[i] = make_uint4(0, 0, 0, 0);
     __syncthreads();
 #pragma unroll
     for (int v = 0; v < 16; ++v)
-        if (qv(v)) atomicOr(&bitmap[oi_r[v] >> 5], 1u << (oi_r[v] & 31));
+        if (qv(v)) flag[oi_r[v]] = 1;
     __syncthreads();
     {
         const int C = (nwk + 255) / 256, lo = tid * C, hi = min(lo + C, nwk);
         uint32_t cnt = 0;
-        for (int w = lo; w < hi; ++w) cnt += __popc(bitmap[w]);
+        for (int w = lo; w < hi; ++w) {
+            const uint4 f0 = reinterpret_cast<const uint4*>(flag)[2 * w];
+            const uint4 f1 = reinterpret_cast<const uint4*>(flag)[2 * w + 1];
+            const uint32_t fw[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+            uint32_t bits = 0;
+#pragma unroll
+            for (int d = 0; d < 8; ++d)
+                bits |= ((fw[d] & 1u) | ((fw[d] >> 7) & 2u) | ((fw[d] >> 14) & 4u) | ((fw[d] >> 21) & 8u)) << (4 * d);
+            bitmap[w] = bits;
+            cnt += __popc(bits);
+        }
         uint32_t nu_total;
         uint32_t base = excl_scan256(cnt, scan, &nu_total);
         for (int w = lo; w < hi; ++w) { wpre[w] = base; base += __popc(bitmap[w]); }
@@ -183,17 +197,24 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(
     }
     __syncthreads();
     const int nu = (int)scan[5];
-    // union position and the f16 pair (hi, lo) of av / so, hi + lo within
-    // 2^-22 of it (rows taking the exact corr get none)
-    int pos[16];
+    // union position of each valid outlier (upos), and for rows that take
+    // the MFMA corr (pos) the f16 pair (hi, lo) of av / so, hi + lo within
+    // 2^-22 of it; branch-free, so the 32 LDS reads are in flight together
+    int upos[16], pos[16];
     uint32_t dig[16];
+    {
+        uint32_t wp[16], bw[16];
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-        pos[v] = -1;
-        dig[v] = 0u;
-        if (qv(v) && !fin) {
+        for (int v = 0; v < 16; ++v) {
+            const uint32_t w = qv(v) ? oi_r[v] >> 5 : 0u;
+            wp[v] = wpre[w];
+            bw[v] = bitmap[w];
+        }
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
             const uint32_t c = oi_r[v];
-            pos[v] = (int)(wpre[c >> 5] + __popc(bitmap[c >> 5] & ((1u << (c & 31)) - 1u)));
+            upos[v] = qv(v) ? (int)(wp[v] + __popc(bw[v] & ((1u << (c & 31)) - 1u))) : -1;
+            pos[v] = fin ? -1 : upos[v];
             const float x = ov_r[v] * rso;  // exact: rso = 1 / so, a power of two
             const _Float16 hi = (_Float16)x;
             const _Float16 lo = (_Float16)(x - (float)hi);
@@ -211,10 +232,7 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(
         // every union channel is some outlier's: equal values where shared
 #pragma unroll
         for (int v = 0; v < 16; ++v)
-            if (qv(v)) {
-                const uint32_t c = oi_r[v];
-                ut[wpre[c >> 5] + __popc(bitmap[c >> 5] & ((1u << (c & 31)) - 1u))] = c;
-            }
+            if (upos[v] >= 0) ut[upos[v]] = oi_r[v];
         for (int p = nu + tid; p < (nu + CH - 1) / CH * CH; p += 256) ut[p] = 0u;
     }
     const int nch = (nu + CH - 1) / CH;
