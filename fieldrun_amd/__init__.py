@@ -12,6 +12,9 @@ The classes mirror the reference's interface for this path
   MoeBank.forward(...)    the routed expert branch of qwen3moe::moe_branch
                           (src/qwen3moe.rs:120-158) / gemma4 (131-187)
   MoeBank.expert_mm(...)  Bundle::expert_mm (src/bundle.rs:457-461)
+  RowTable.rowdot_f32(x)  Bundle::rowdot_f32 (src/bundle.rs:958-987), the
+                          unembed over an f32 / f16 / rowi8 (vocab, d) table,
+                          and rowdot_f32_subset (995-1015)
 
 Errors the reference raises by panicking come back as FrqError carrying the
 library's status code and message.
@@ -28,7 +31,7 @@ LIB_PATH = os.path.join(_HERE, "libfrq.so")
 
 FRQ_OK, FRQ_ERR_ARG, FRQ_ERR_HIP, FRQ_ERR_NAN = 0, 1, 2, 3
 FRQ_ERR_DTYPE, FRQ_ERR_FORMAT, FRQ_ERR_MISSING, FRQ_ERR_NODEV = 4, 5, 6, 7
-FRQ_DT_I8, FRQ_DT_I4 = 1, 2
+FRQ_DT_I8, FRQ_DT_I4, FRQ_DT_F32, FRQ_DT_F16, FRQ_DT_ROWI8 = 1, 2, 3, 4, 5
 FRQ_ACT_SILU, FRQ_ACT_GELU_TANH = 0, 1
 
 # name -> (restype, argtypes); every symbol include/frq.h declares
@@ -45,6 +48,7 @@ SIGNATURES = {
     "frq_upload_i8": (_P, [_P, _P, _P, _S, _S]),
     "frq_upload_i8_bundle": (_P, [_P, _P, _P, _S, _S]),
     "frq_upload_i4": (_P, [_P, _P, _P, _S, _S, _S]),
+    "frq_upload_rows": (_P, [_P, _I, _P, _P, _S, _S]),
     "frq_w_free": (None, [_P]),
     "frq_w_info": (_I, [_P, _P, _P, _P, _P]),
     "frq_mm": (_I, [_P, _P, _P, _S, _P]),
@@ -59,6 +63,10 @@ SIGNATURES = {
     "frq_moe_dev": (_I, [_P, _P, _P, _S, _P, _S, _I, _P, _P]),
     "frq_moe_route": (_I, [_P, _P, _S, _S, _S, _I, _P, _P, _P]),
     "frq_expert_mm": (_I, [_P, _P, _I, _S, _P, _S, _P]),
+    "frq_rowdot_f32": (_I, [_P, _P, _P, _P]),
+    "frq_rowdot_f32_dev": (_I, [_P, _P, _P, _P]),
+    "frq_rowdot_f32_subset": (_I, [_P, _P, _P, _P, _S, _P]),
+    "frq_rowdot_f32_subset_dev": (_I, [_P, _P, _P, _P, _S, _P]),
 }
 
 
@@ -163,6 +171,25 @@ class Context:
             raise FrqError(FRQ_ERR_HIP, lib.frq_last_error().decode())
         return Weight(self, h, FRQ_DT_I4, n, k, g)
 
+    def upload_rows(self, kind: str, data: np.ndarray, scale: np.ndarray | None = None) -> "RowTable":
+        """A row-major (rows, d) embedding table for rowdot_f32: kind 'f32'
+        (float32 data), 'f16' (float16 data) or 'rowi8' (int8 data plus the
+        f32 row scale, the upcast `__scale` sibling)."""
+        if kind == "f32":
+            dt, data = FRQ_DT_F32, np.ascontiguousarray(data, dtype=np.float32)
+        elif kind == "f16":
+            dt, data = FRQ_DT_F16, np.ascontiguousarray(data, dtype=np.float16).view(np.uint16)
+        elif kind == "rowi8":
+            dt, data = FRQ_DT_ROWI8, np.ascontiguousarray(data, dtype=np.int8)
+        else:
+            raise FrqError(FRQ_ERR_DTYPE, f"unknown row table kind {kind!r}")
+        sc = None if scale is None else np.ascontiguousarray(scale, dtype=np.float32)
+        rows, d = data.shape
+        h = lib.frq_upload_rows(self.h, dt, _ptr(data), _ptr(sc), rows, d)
+        if not h:
+            raise FrqError(FRQ_ERR_ARG, lib.frq_last_error().decode())
+        return RowTable(self, h, dt, rows, d)
+
     def upload_moe_i8(self, gate, gate_scale, up, up_scale, down, down_scale,
                       act: int = FRQ_ACT_SILU) -> "MoeBank":
         """Lists over experts of (in,out) int8 arrays and f32 [out] scales."""
@@ -249,6 +276,36 @@ class Weight:
         _check(lib.frq_mm_i8_debug(self.ctx.h, self.h, _ptr(a), m, _ptr(out), _ptr(acc),
                                    _ptr(a8), _ptr(sa), _ptr(oi), _ptr(ov)))
         return out, acc, a8, sa, oi, ov
+
+
+class RowTable(Weight):
+    """A row-major embedding / unembedding table resident in HBM (frq_w)."""
+
+    def rowdot_f32(self, x: np.ndarray) -> np.ndarray:
+        """Bundle::rowdot_f32: out[r] = dot(W[r], x) for every row."""
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+        if x.shape[0] != self.k:
+            raise FrqError(FRQ_ERR_ARG, f"x has {x.shape[0]} entries, the rows {self.k}")
+        out = np.empty(self.n, np.float32)
+        _check(lib.frq_rowdot_f32(self.ctx.h, self.h, _ptr(x), _ptr(out)))
+        return out
+
+    def rowdot_f32_dev(self, x_ptr: int, out_ptr: int):
+        _check(lib.frq_rowdot_f32_dev(self.ctx.h, self.h, x_ptr, out_ptr))
+
+    def rowdot_f32_subset(self, x: np.ndarray, cand) -> np.ndarray:
+        """Bundle::rowdot_f32_subset: out[i] = dot(W[cand[i]], x); ids outside
+        [0, rows) score -inf."""
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+        if x.shape[0] != self.k:
+            raise FrqError(FRQ_ERR_ARG, f"x has {x.shape[0]} entries, the rows {self.k}")
+        cand = np.ascontiguousarray(cand, dtype=np.int64).reshape(-1)
+        out = np.empty(cand.shape[0], np.float32)
+        _check(lib.frq_rowdot_f32_subset(self.ctx.h, self.h, _ptr(x), _ptr(cand), cand.shape[0], _ptr(out)))
+        return out
+
+    def rowdot_f32_subset_dev(self, x_ptr: int, cand_ptr: int, ncand: int, out_ptr: int):
+        _check(lib.frq_rowdot_f32_subset_dev(self.ctx.h, self.h, x_ptr, cand_ptr, ncand, out_ptr))
 
 
 class MoeBank:

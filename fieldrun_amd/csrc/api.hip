@@ -198,6 +198,7 @@ void free_weight(Weight& w) {
     if (w.s4) (void)hipFree(w.s4);
     if (w.q4raw) (void)hipFree(w.q4raw);
     if (w.s4raw) (void)hipFree(w.s4raw);
+    if (w.rowp) (void)hipFree(w.rowp);
     w = Weight{};
 }
 
@@ -380,6 +381,49 @@ frq_w* frq_upload_i4(frq_ctx* c, const uint8_t* packed,
     return h;
 }
 
+frq_w* frq_upload_rows(frq_ctx* c, int dtype, const void* data, const float* scale, size_t rows,
+                       size_t d) {
+    if (check_ctx(c)) return nullptr;
+    if (dtype != FRQ_DT_F32 && dtype != FRQ_DT_F16 && dtype != FRQ_DT_ROWI8) {
+        fail(FRQ_ERR_DTYPE, "frq_upload_rows: dtype must be FRQ_DT_F32, FRQ_DT_F16 or FRQ_DT_ROWI8");
+        return nullptr;
+    }
+    if ((!data && rows * d) || (dtype == FRQ_DT_ROWI8 && !scale && rows)) {
+        fail(FRQ_ERR_ARG, "frq_upload_rows: null data or scale");
+        return nullptr;
+    }
+    if (rows > (size_t)INT32_MAX || d > (size_t)INT32_MAX) {
+        fail(FRQ_ERR_ARG, "frq_upload_rows: rows and d must fit in int32");
+        return nullptr;
+    }
+    DeviceGuard gd(c->device);
+    frq_w* h = new (std::nothrow) frq_w;
+    if (!h) { fail(FRQ_ERR_ARG, "out of host memory"); return nullptr; }
+    Weight& w = h->w;
+    w.dtype = dtype; w.device = c->device; w.n = rows; w.k = d;
+    const size_t es = dtype == FRQ_DT_F32 ? 4 : (dtype == FRQ_DT_F16 ? 2 : 1);
+    w.rpitch = row_pitch(dtype, d);
+    // at least one (zero) row: invalid subset ids read row 0 before scoring -inf
+    const size_t bytes = (rows ? rows : 1) * w.rpitch + 128;
+    hipError_t e = hipMalloc(&w.rowp, bytes);
+    if (e == hipSuccess) e = hipMemsetAsync(w.rowp, 0, bytes, c->stream);
+    if (e == hipSuccess && rows * d)
+        e = hipMemcpy2DAsync(w.rowp, w.rpitch, data, d * es, d * es, rows, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess && dtype == FRQ_DT_ROWI8) {
+        e = hipMalloc(&w.scale, rows * 4 + 16);
+        if (e == hipSuccess && rows)
+            e = hipMemcpyAsync(w.scale, scale, rows * 4, hipMemcpyHostToDevice, c->stream);
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) {
+        hip_fail(e, "frq_upload_rows");
+        free_weight(w);
+        delete h;
+        return nullptr;
+    }
+    return h;
+}
+
 void frq_w_free(frq_w* w) {
     if (!w) return;
     free_weight(w->w);
@@ -522,6 +566,71 @@ int frq_mm_i8_debug(frq_ctx* c, const frq_w* w, const float* a, size_t m, float*
                     int32_t* acc, int8_t* a8, float* sa, uint32_t* oidx, float* oval) {
     if (w && w->w.dtype != FRQ_DT_I8) return fail(FRQ_ERR_DTYPE, "frq_mm_i8_debug: not an int8 weight");
     return mm_host(c, w, a, m, out, acc, a8, sa, oidx, oval);
+}
+
+// ---- the unembed -------------------------------------------------------------
+
+static int rowdot_check(frq_ctx* c, const frq_w* wh) {
+    if (int rc = check_ctx(c)) return rc;
+    if (!wh) return fail(FRQ_ERR_ARG, "null weight");
+    const Weight& w = wh->w;
+    if (w.dtype != FRQ_DT_F32 && w.dtype != FRQ_DT_F16 && w.dtype != FRQ_DT_ROWI8)
+        return fail(FRQ_ERR_DTYPE, "rowdot_f32: not a row table (column-major quant unembed unsupported)");
+    if (w.device != c->device) return fail(FRQ_ERR_ARG, "weight lives on another device");
+    return FRQ_OK;
+}
+
+int frq_rowdot_f32_dev(frq_ctx* c, const frq_w* wh, const float* d_x, float* d_out) {
+    if (int rc = rowdot_check(c, wh)) return rc;
+    const Weight& w = wh->w;
+    if (!w.n) return FRQ_OK;
+    if ((!d_x && w.k) || !d_out) return fail(FRQ_ERR_ARG, "null pointer");
+    DeviceGuard g(c->device);
+    HIPCHK(launch_rowdot(w, d_x, nullptr, w.n, d_out, c->stream), "launch rowdot");
+    return FRQ_OK;
+}
+
+int frq_rowdot_f32_subset_dev(frq_ctx* c, const frq_w* wh, const float* d_x, const int64_t* d_cand,
+                              size_t ncand, float* d_out) {
+    if (int rc = rowdot_check(c, wh)) return rc;
+    const Weight& w = wh->w;
+    if (!ncand) return FRQ_OK;
+    if ((!d_x && w.k) || !d_cand || !d_out) return fail(FRQ_ERR_ARG, "null pointer");
+    DeviceGuard g(c->device);
+    HIPCHK(launch_rowdot(w, d_x, d_cand, ncand, d_out, c->stream), "launch rowdot");
+    return FRQ_OK;
+}
+
+static int rowdot_host(frq_ctx* c, const frq_w* wh, const float* x, const int64_t* cand, size_t nout,
+                       float* out) {
+    if (int rc = rowdot_check(c, wh)) return rc;
+    const Weight& w = wh->w;
+    if (!nout) return FRQ_OK;
+    if ((!x && w.k) || !out) return fail(FRQ_ERR_ARG, "null pointer");
+    DeviceGuard g(c->device);
+    const size_t xb = round_up(w.k * 4 + 16, 256), cb = cand ? round_up(nout * 8, 256) : 0;
+    if (int rc = ws_reserve(c, xb + cb + round_up(nout * 4, 256))) return rc;
+    char* base = (char*)c->ws;
+    float* d_x = (float*)base;
+    int64_t* d_cand = cand ? (int64_t*)(base + xb) : nullptr;
+    float* d_out = (float*)(base + xb + cb);
+    if (w.k) HIPCHK(hipMemcpyAsync(d_x, x, w.k * 4, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync(x)");
+    if (cand) HIPCHK(hipMemcpyAsync(d_cand, cand, nout * 8, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync(cand)");
+    HIPCHK(launch_rowdot(w, d_x, d_cand, nout, d_out, c->stream), "launch rowdot");
+    HIPCHK(hipMemcpyAsync(out, d_out, nout * 4, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync(out)");
+    HIPCHK(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return FRQ_OK;
+}
+
+int frq_rowdot_f32(frq_ctx* c, const frq_w* wh, const float* x, float* out) {
+    if (int rc = rowdot_check(c, wh)) return rc;
+    return rowdot_host(c, wh, x, nullptr, wh->w.n, out);
+}
+
+int frq_rowdot_f32_subset(frq_ctx* c, const frq_w* wh, const float* x, const int64_t* cand, size_t ncand,
+                          float* out) {
+    if (ncand && !cand) return fail(FRQ_ERR_ARG, "null candidate ids");
+    return rowdot_host(c, wh, x, ncand ? cand : nullptr, ncand, out);
 }
 
 // ---- MoE -----------------------------------------------------------------------

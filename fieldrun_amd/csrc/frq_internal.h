@@ -106,7 +106,7 @@ __device__ __forceinline__ float h2f(uint16_t h) {
 
 // ---- weights -------------------------------------------------------------
 struct Weight {
-    int dtype = 0;           // FRQ_DT_I8 / FRQ_DT_I4
+    int dtype = 0;           // FRQ_DT_*
     int device = 0;
     size_t n = 0, k = 0, g = 0;
     size_t np = 0, kp = 0;   // padded dims (int8)
@@ -119,6 +119,8 @@ struct Weight {
     uint8_t* q4raw = nullptr;   // int4 packed (N, ceil(K/2)) as stored
     uint16_t* s4raw = nullptr;  // int4 f16 scales (N, ceil(K/g)) as stored
     int i4_blocked = 0;      // 1 when the MFMA layout (g == 32) is built
+    uint8_t* rowp = nullptr; // row tables: (n, k) rows, each padded to rpitch bytes
+    size_t rpitch = 0;       //   (a multiple of 128); rowi8 scales in `scale`
 };
 
 struct MoeBank {
@@ -176,6 +178,12 @@ hipError_t launch_gemm_i8(const Weight& w, size_t m, const int8_t* a8b,
                           const float* sa, const uint32_t* oidx,
                           const float* oval, float* out, int32_t* acc, void* ws,
                           hipStream_t s);
+// Row tables (FRQ_DT_F32 / F16 / ROWI8): bytes per padded row, and
+// out[i] = dot(W[row i], x) for nout rows (cand == nullptr: rows 0..nout-1;
+// else the candidate ids, invalid ones -inf).
+size_t row_pitch(int dtype, size_t d);
+hipError_t launch_rowdot(const Weight& w, const float* x, const int64_t* cand, size_t nout, float* out,
+                         hipStream_t s);
 // int4 linear (any m).
 hipError_t launch_i4(const Weight& w, size_t m, const float* a, float* out,
                      float* wsf, unsigned* tickets, hipStream_t s);

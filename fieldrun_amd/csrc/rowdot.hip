@@ -1,0 +1,173 @@
+// rowdot.hip — the row-major unembed dot Bundle::rowdot_f32, gfx950.
+//
+// Restates /root/reference/src/bundle.rs:958-987 (rowdot_f32) and 995-1015
+// (rowdot_f32_subset): out[r] = dot(W[r], x) for a (rows, d) matrix stored
+// row-major as f32, f16, or rowi8 with an f32 scale per row, in the
+// reference's operation order, bit for bit:
+//   f32 / f16      a fold of w * x (w.to_f32() for f16; a mul, then an
+//                  add) from -0.0 (Rust's f32 Sum), k ascending;
+//   rowi8, full    s * rowi8_dot_avx2 (158-178), the order of the x86
+//                  build (AVX2 + FMA hosts, 975-978): eight lane
+//                  accumulators from +0.0, lane q an FMA chain over
+//                  k = 8i + q, then hsum256 ((l0+l4)+(l2+l6)) + ((l1+l5)+
+//                  (l3+l7)) (146-153), then a mul + add tail from 8*(d/8);
+//   rowi8, subset  s * the fold from -0.0 (1009-1012).
+// The subset form scores rows cand[i]; an id < 0 or >= rows gives -inf.
+//
+// HBM-bound: the matrix streams once.  One lane per row keeps each row's
+// chain in order.  A wave owns 64 rows and walks d in 128-byte chunks: the
+// chunk tile (64 rows x 128 B) is loaded coalesced (8 lanes per row, 16 B
+// each), staged through the wave's padded LDS tile (row stride 144 B, so the
+// lanes' row reads are conflict-free), and each lane reads back its own row;
+// the next chunk's loads are in flight meanwhile.  x is wave-uniform: its
+// reads are scalar loads.  Rows are padded to a multiple of 128 bytes at
+// upload, so chunk loads never run past a row.
+#include "frq_internal.h"
+
+namespace frq {
+
+namespace {
+
+constexpr int TP = 144;  // LDS tile row stride (bytes)
+
+template <int DT, bool SUB>  // DT: 0 f32, 1 f16, 2 rowi8
+__global__ __launch_bounds__(256) void rowdot_kernel(
+    const uint8_t* __restrict__ W, const float* __restrict__ rs, int rows, int d, size_t pitch,
+    const float* __restrict__ x, const int64_t* __restrict__ cand, int nout, float* __restrict__ out) {
+    constexpr int ES = DT == 0 ? 4 : (DT == 1 ? 2 : 1);  // bytes per element
+    constexpr int CE = 128 / ES;                         // elements per chunk
+    __shared__ __attribute__((aligned(16))) uint8_t tile[4][64 * TP];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int o0 = ((int)blockIdx.x * 4 + wave) * 64;
+    if (o0 >= nout) return;  // wave-uniform; no block-wide barrier below
+    uint8_t* tw = tile[wave];
+
+    // the row an output scores (row 0 stands in for invalid ones)
+    auto row_of = [&](int o, bool& ok) -> int {
+        ok = o < nout;
+        if constexpr (SUB) {
+            const int64_t c = ok ? cand[o] : 0;
+            ok = ok && c >= 0 && c < (int64_t)rows;
+            return ok ? (int)c : 0;
+        } else {
+            return ok ? o : 0;
+        }
+    };
+    // load instruction i of a chunk: lane l reads 16 bytes (l % 8) of the
+    // row of output o0 + 8i + l / 8
+    const uint8_t* src[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        bool ok;
+        const int r = row_of(o0 + 8 * i + (lane >> 3), ok);
+        src[i] = W + (size_t)r * pitch + (lane & 7) * 16;
+    }
+    bool own_ok;
+    const int own_row = row_of(o0 + lane, own_ok);
+
+    const int nch = (int)(pitch / 128);
+    uint4 cur[8], nxt[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) cur[i] = nch ? ntload16u(src[i]) : make_uint4(0, 0, 0, 0);
+
+    float acc = -0.0f;  // the fold (f32, f16, subset rowi8)
+    float l8[8] = {0, 0, 0, 0, 0, 0, 0, 0};  // the AVX2 lanes (full rowi8)
+    for (int c = 0; c < nch; ++c) {
+        if (c + 1 < nch) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) nxt[i] = ntload16u(src[i] + (size_t)(c + 1) * 128);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            *reinterpret_cast<uint4*>(tw + (8 * i + (lane >> 3)) * TP + (lane & 7) * 16) = cur[i];
+        wave_sync();
+        uint32_t v[32];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint4 q = *reinterpret_cast<const uint4*>(tw + lane * TP + 16 * j);
+            v[4 * j] = q.x; v[4 * j + 1] = q.y; v[4 * j + 2] = q.z; v[4 * j + 3] = q.w;
+        }
+        wave_sync();  // the tile is read before the next chunk is written
+        const int k0 = c * CE;
+        if constexpr (DT == 0) {
+#pragma unroll
+            for (int e = 0; e < CE; ++e)
+                if (k0 + e < d) acc = acc + __builtin_bit_cast(float, v[e]) * x[k0 + e];
+        } else if constexpr (DT == 1) {
+#pragma unroll
+            for (int e = 0; e < CE; ++e)
+                if (k0 + e < d) acc = acc + h2f((uint16_t)(v[e >> 1] >> (16 * (e & 1)))) * x[k0 + e];
+        } else if constexpr (SUB) {
+#pragma unroll
+            for (int e = 0; e < CE; ++e)
+                if (k0 + e < d)
+                    acc = acc + (float)(int8_t)(v[e >> 2] >> (8 * (e & 3))) * x[k0 + e];
+        } else {
+            // full 8-element groups only; the tail follows the lane sum
+#pragma unroll
+            for (int gi = 0; gi < CE / 8; ++gi) {
+                const int kb = k0 + 8 * gi;
+                if (kb + 8 <= d) {
+#pragma unroll
+                    for (int q = 0; q < 8; ++q)
+                        l8[q] = __builtin_fmaf((float)(int8_t)(v[2 * gi + (q >> 2)] >> (8 * (q & 3))), x[kb + q], l8[q]);
+                }
+            }
+            if (c == nch - 1) {
+                const float q0 = l8[0] + l8[4], q1 = l8[1] + l8[5], q2 = l8[2] + l8[6], q3 = l8[3] + l8[7];
+                acc = (q0 + q2) + (q1 + q3);
+                const int kt = d & ~7;  // the tail lies in this chunk
+#pragma unroll
+                for (int e = 0; e < CE; ++e)
+                    if (k0 + e >= kt && k0 + e < d)
+                        acc = acc + (float)(int8_t)(v[e >> 2] >> (8 * (e & 3))) * x[k0 + e];
+            }
+        }
+        if (c + 1 < nch) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) cur[i] = nxt[i];
+        }
+    }
+    if constexpr (DT == 2) {
+        if (!SUB && nch == 0) acc = 0.0f;  // d == 0: hsum of zero lanes
+        acc = rs[own_row] * acc;
+    }
+    const int o = o0 + lane;
+    if (o < nout) out[o] = own_ok ? acc : -__builtin_inff();
+}
+
+template <int DT>
+hipError_t launch_dt(const Weight& w, const float* x, const int64_t* cand, size_t nout, float* out,
+                     hipStream_t s) {
+    const unsigned grid = (unsigned)((nout + 255) / 256);
+    if (cand)
+        rowdot_kernel<DT, true><<<dim3(grid), dim3(256), 0, s>>>(
+            w.rowp, w.scale, (int)w.n, (int)w.k, w.rpitch, x, cand, (int)nout, out);
+    else
+        rowdot_kernel<DT, false><<<dim3(grid), dim3(256), 0, s>>>(
+            w.rowp, w.scale, (int)w.n, (int)w.k, w.rpitch, x, nullptr, (int)nout, out);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+size_t row_pitch(int dtype, size_t d) {
+    const size_t es = dtype == FRQ_DT_F32 ? 4 : (dtype == FRQ_DT_F16 ? 2 : 1);
+    return (d * es + 127) / 128 * 128;
+}
+
+hipError_t launch_rowdot(const Weight& w, const float* x, const int64_t* cand, size_t nout, float* out,
+                         hipStream_t s) {
+    if (!nout) return hipSuccess;
+    if (nout > (size_t)INT32_MAX - 256 || w.n > (size_t)INT32_MAX || w.k > (size_t)INT32_MAX)
+        return hipErrorInvalidValue;
+    switch (w.dtype) {
+        case FRQ_DT_F32: return launch_dt<0>(w, x, cand, nout, out, s);
+        case FRQ_DT_F16: return launch_dt<1>(w, x, cand, nout, out, s);
+        case FRQ_DT_ROWI8: return launch_dt<2>(w, x, cand, nout, out, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace frq

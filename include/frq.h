@@ -47,7 +47,13 @@ enum {
     FRQ_ERR_NODEV = 7    /* no HIP device / library built without GPU      */
 };
 
-enum { FRQ_DT_I8 = 1, FRQ_DT_I4 = 2 };
+enum {
+    FRQ_DT_I8 = 1,    /* int8 linear weight (W8A8)                        */
+    FRQ_DT_I4 = 2,    /* group-wise int4 linear weight (W4A32)            */
+    FRQ_DT_F32 = 3,   /* row-major f32 rows (embed / unembed)             */
+    FRQ_DT_F16 = 4,   /* row-major f16 rows                               */
+    FRQ_DT_ROWI8 = 5  /* row-major int8 rows + f32 scale per row          */
+};
 enum { FRQ_ACT_SILU = 0, FRQ_ACT_GELU_TANH = 1 };
 
 typedef struct frq_ctx frq_ctx;
@@ -91,8 +97,15 @@ frq_w* frq_upload_i8_bundle(frq_ctx* ctx, const int8_t* w_kn,
  * 50-56, 356-360; src/convert.rs:189-216). */
 frq_w* frq_upload_i4(frq_ctx* ctx, const uint8_t* packed,
                      const uint16_t* scale_f16, size_t n, size_t k, size_t g);
+/* Row-major (rows, d) embedding/unembedding table as stored: FRQ_DT_F32
+ * (float data), FRQ_DT_F16 (uint16_t f16 bits) or FRQ_DT_ROWI8 (int8 data
+ * plus scale[rows], the f32 upcast of the `__scale` sibling that
+ * Bundle::rowdot_f32 reads with arr1o).  Replaces the F32 / F16 / RowI8
+ * arrays of Bundle::load (src/bundle.rs:366-369) for rowdot_f32. */
+frq_w* frq_upload_rows(frq_ctx* ctx, int dtype, const void* data,
+                       const float* scale, size_t rows, size_t d);
 void frq_w_free(frq_w* w);
-/* dtype (FRQ_DT_*), N (out), K (in), g (int4 group, 0 for int8). */
+/* dtype (FRQ_DT_*), N (out; rows), K (in; d), g (int4 group, else 0). */
 int frq_w_info(const frq_w* w, int* dtype, size_t* n, size_t* k, size_t* g);
 
 /* ---- the linear: Bundle::mm (src/bundle.rs:644-919) ----------------------
@@ -125,6 +138,23 @@ int frq_quant_i8_dev(frq_ctx* ctx, const float* d_a, size_t m, size_t k,
 int frq_mm_i8_q_dev(frq_ctx* ctx, const frq_w* w, const int8_t* d_a8,
                     const float* d_sa, const uint32_t* d_oidx,
                     const float* d_oval, size_t m, float* d_out);
+
+/* ---- the unembed: Bundle::rowdot_f32 (src/bundle.rs:958-987) -----------
+ * out[r] = dot(W[r], x) for every row of a frq_upload_rows table (out has
+ * rows entries, x has d), bit-identical to the reference's order (f32/f16:
+ * a fold from -0.0; rowi8: scale * rowi8_dot_avx2, 158-178).  Other weight
+ * dtypes are FRQ_ERR_DTYPE (the reference panics, 983). */
+int frq_rowdot_f32(frq_ctx* ctx, const frq_w* w, const float* x, float* out);
+int frq_rowdot_f32_dev(frq_ctx* ctx, const frq_w* w, const float* d_x,
+                       float* d_out);
+/* Bundle::rowdot_f32_subset (src/bundle.rs:995-1015): out[i] =
+ * dot(W[cand[i]], x) for ncand candidate ids (rowi8: scale * the fold from
+ * -0.0, 1011); an id < 0 or >= rows gives -inf. */
+int frq_rowdot_f32_subset(frq_ctx* ctx, const frq_w* w, const float* x,
+                          const int64_t* cand, size_t ncand, float* out);
+int frq_rowdot_f32_subset_dev(frq_ctx* ctx, const frq_w* w, const float* d_x,
+                              const int64_t* d_cand, size_t ncand,
+                              float* d_out);
 
 /* ---- MoE experts: expert_f32 + expert_mm (src/bundle.rs:404-461) and the
  * routed branch of src/qwen3moe.rs:120-158 / src/gemma4.rs:131-187 -------- */

@@ -50,6 +50,8 @@ def _load():
         "fro_gelu_tanh": (F, [F]),
         "fro_moe_route": (None, [P, S, S, S, I, P, P, P, P]),
         "fro_moe": (I, [P, S, S, P, S, S, I, P, S, I, P, P, P, P, P, P, P]),
+        "fro_rowdot_f32": (None, [I, P, P, S, S, P, P]),
+        "fro_rowdot_f32_subset": (None, [I, P, P, S, S, P, P, S, P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -250,4 +252,35 @@ def moe(x, logits, topk, norm_topk, gate, gate_scale, up, up_scale, down, down_s
     out = np.empty((T, d), np.float32)
     lib.fro_moe(_p(x), T, d, _p(logits), E, topk, int(norm_topk), _p(pes), mi, act,
                 gp, gsp, up_, usp, dp, dsp, _p(out))
+    return out
+
+
+# ---- the unembed row dot ----
+ROW_DTYPES = {"f32": (3, np.float32), "f16": (4, np.uint16), "rowi8": (5, np.int8)}
+
+
+def rowdot_f32(kind: str, data, x, scale=None):
+    """Bundle::rowdot_f32 over a (rows, d) table; kind 'f32' (float data),
+    'f16' (uint16 f16 bits) or 'rowi8' (int8 + f32 scale per row)."""
+    code, dt = ROW_DTYPES[kind]
+    data = _c(data, dt)
+    rows, d = data.shape
+    x = _c(x, np.float32)
+    sc = _c(scale, np.float32) if scale is not None else None
+    out = np.empty(rows, np.float32)
+    lib.fro_rowdot_f32(code, _p(data), _p(sc), rows, d, _p(x), _p(out))
+    return out
+
+
+def rowdot_f32_subset(kind: str, data, x, cand, scale=None):
+    """Bundle::rowdot_f32_subset: out[i] = dot(W[cand[i]], x), -inf for ids
+    outside [0, rows)."""
+    code, dt = ROW_DTYPES[kind]
+    data = _c(data, dt)
+    rows, d = data.shape
+    x = _c(x, np.float32)
+    cand = _c(cand, np.int64)
+    sc = _c(scale, np.float32) if scale is not None else None
+    out = np.empty(len(cand), np.float32)
+    lib.fro_rowdot_f32_subset(code, _p(data), _p(sc), rows, d, _p(x), _p(cand), len(cand), _p(out))
     return out

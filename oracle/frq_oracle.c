@@ -546,3 +546,59 @@ int fro_moe(const float* x, size_t T, size_t d, const float* logits, size_t E,
     free(sel); free(w); free(rows); free(g); free(u); free(h); free(dn); free(tok); free(tw);
     return FRO_OK;
 }
+
+/* ------------------------------------------------------------------------ */
+/* The unembed row dot: Bundle::rowdot_f32 (src/bundle.rs:958-987) and       */
+/* rowdot_f32_subset (995-1015).                                             */
+/* ------------------------------------------------------------------------ */
+/* One row.  f32 (dtype 3) / f16 (4): the iterator fold of w * x from -0.0
+ * (Rust 1.89's f32 Sum; rust-version in the reference's Cargo.toml), a mul
+ * then an add (967-968).  rowi8 (5), full: scale * rowi8_dot_avx2 (158-178),
+ * the order the x86 build takes (975-978): 8 lane accumulators from +0.0,
+ * lane q an FMA chain over k = 8i + q, hsum256 (146-153), then a mul + add
+ * tail.  rowi8, subset (or a host without AVX2+FMA, 980): scale * the fold
+ * from -0.0 (1011). */
+static float row_dot(int dtype, const void* data, const float* scale, size_t r,
+                     size_t d, const float* x, int avx2) {
+    if (dtype == 3) {
+        const float* w = (const float*)data + r * d;
+        float s = -0.0f;
+        for (size_t k = 0; k < d; k++) s = s + w[k] * x[k];
+        return s;
+    }
+    if (dtype == 4) {
+        const uint16_t* w = (const uint16_t*)data + r * d;
+        float s = -0.0f;
+        for (size_t k = 0; k < d; k++) s = s + fro_f16_to_f32(w[k]) * x[k];
+        return s;
+    }
+    const int8_t* w = (const int8_t*)data + r * d;
+    if (!avx2) {
+        float s = -0.0f;
+        for (size_t k = 0; k < d; k++) s = s + (float)w[k] * x[k];
+        return scale[r] * s;
+    }
+    float l[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    size_t kk = 0;
+    for (; kk + 8 <= d; kk += 8)
+        for (int q = 0; q < 8; q++) l[q] = fmaf((float)w[kk + (size_t)q], x[kk + (size_t)q], l[q]);
+    float q0 = l[0] + l[4], q1 = l[1] + l[5], q2 = l[2] + l[6], q3 = l[3] + l[7];
+    float sum = (q0 + q2) + (q1 + q3);
+    for (; kk < d; kk++) sum = sum + (float)w[kk] * x[kk];
+    return scale[r] * sum;
+}
+
+void fro_rowdot_f32(int dtype, const void* data, const float* scale, size_t rows,
+                    size_t d, const float* x, float* out) {
+    for (size_t r = 0; r < rows; r++) out[r] = row_dot(dtype, data, scale, r, d, x, 1);
+}
+
+void fro_rowdot_f32_subset(int dtype, const void* data, const float* scale,
+                           size_t rows, size_t d, const float* x,
+                           const int64_t* cand, size_t ncand, float* out) {
+    for (size_t i = 0; i < ncand; i++) {
+        const int64_t c = cand[i];
+        out[i] = (c < 0 || (uint64_t)c >= rows) ? -INFINITY
+                                                : row_dot(dtype, data, scale, (size_t)c, d, x, 0);
+    }
+}

@@ -30,6 +30,11 @@
  *                                     is matrixmultiply's): tolerance parity
  *   fro_moe_route / fro_moe           closed-form softmax + brute-force
  *                                     stable sort, f64 combine bound
+ *   fro_rowdot_f32 / _subset          exact small-integer dots (any order),
+ *                                     f64 bound, and order-revealing cases
+ *                                     whose f32 result follows by hand from
+ *                                     the fold / the eight-lane AVX2 order;
+ *                                     the reference has no test for these
  */
 #ifndef FRQ_ORACLE_H
 #define FRQ_ORACLE_H
@@ -117,6 +122,15 @@ int fro_moe(const float* x, size_t T, size_t d, const float* logits, size_t E,
             const float* const* gate_scale, const int8_t* const* up,
             const float* const* up_scale, const int8_t* const* down,
             const float* const* down_scale, float* out);
+
+/* Bundle::rowdot_f32 / rowdot_f32_subset over a row-major (rows, d) table:
+ * dtype 3 f32 (float data), 4 f16 (uint16 bits), 5 rowi8 (int8 data +
+ * scale[rows]). Subset ids < 0 or >= rows give -inf. */
+void fro_rowdot_f32(int dtype, const void* data, const float* scale, size_t rows,
+                    size_t d, const float* x, float* out);
+void fro_rowdot_f32_subset(int dtype, const void* data, const float* scale,
+                           size_t rows, size_t d, const float* x,
+                           const int64_t* cand, size_t ncand, float* out);
 
 #ifdef __cplusplus
 }

@@ -427,3 +427,78 @@ def test_package_quantisers_match_oracle():
     q1, s1 = convert.put_embed_i8(e)
     q2, s2 = oracle.put_embed_i8(e)
     assert np.array_equal(q1, q2) and np.array_equal(s1.view(np.uint16), s2)
+
+
+# ---- the unembed row dot (src/bundle.rs:958-1015) ----
+# The reference has no test for rowdot_f32; the oracle is pinned by exact
+# small-integer dots (every order gives the same sum), an f64 bound, and
+# inputs whose f32 result follows by hand from the order.
+
+@pytest.mark.parametrize("kind", ["f32", "f16", "rowi8"])
+@pytest.mark.parametrize("d", [0, 1, 7, 8, 9, 64, 131])
+def test_rowdot_exact_integer_dots(kind, d):
+    rng = np.random.default_rng(100 + d)
+    rows = 5
+    wi = rng.integers(-8, 9, (rows, d))
+    x = rng.integers(-8, 9, d).astype(np.float32)
+    exact = (wi.astype(np.int64) @ x.astype(np.int64)).astype(np.float64)
+    scale = np.full(rows, 0.5, np.float32)
+    if kind == "f32":
+        data, want = wi.astype(np.float32), exact
+    elif kind == "f16":
+        data, want = wi.astype(np.float16).view(np.uint16), exact
+    else:
+        data, want = wi.astype(np.int8), exact * 0.5
+    got = oracle.rowdot_f32(kind, data, x, scale if kind == "rowi8" else None)
+    assert np.array_equal(got.astype(np.float64), want)
+    sub = oracle.rowdot_f32_subset(kind, data, x, [4, 0, -1, rows, 2], scale if kind == "rowi8" else None)
+    assert np.array_equal(sub[[0, 1, 4]].astype(np.float64), want[[4, 0, 2]])
+    assert np.isneginf(sub[2]) and np.isneginf(sub[3])
+
+
+def test_rowdot_f64_bound():
+    rng = np.random.default_rng(7)
+    rows, d = 40, 777
+    x = rng.standard_normal(d).astype(np.float32)
+    w16 = (rng.standard_normal((rows, d)) * 0.02).astype(np.float16)
+    w8 = rng.integers(-127, 128, (rows, d)).astype(np.int8)
+    s8 = rng.uniform(1e-4, 3e-4, rows).astype(np.float32)
+    for kind, data, sc, wf in [("f16", w16.view(np.uint16), None, w16.astype(np.float64)),
+                               ("rowi8", w8, s8, w8.astype(np.float64) * s8[:, None].astype(np.float64))]:
+        got = oracle.rowdot_f32(kind, data, x, sc).astype(np.float64)
+        ref = wf @ x.astype(np.float64)
+        bound = d * 2.0 ** -23 * (np.abs(wf) @ np.abs(x.astype(np.float64))) + 1e-30
+        assert np.all(np.abs(got - ref) <= bound)
+
+
+def test_rowdot_order_fold_vs_avx2_lanes():
+    # x = [2^24, 1 x 8], w = 1: the fold (f32, f16, rowi8 subset) drops every
+    # +1 (2^24 + 1 rounds to even 2^24): 2^24.  rowi8_dot_avx2: lane 0 holds
+    # 2^24, lanes 1..7 one each; hsum: (2^24+1 -> 2^24) + (1+1) + ... =
+    # 2^24 + 6, then the tail (k = 8) + 1 -> 2^24 + 7, rounded to even 2^24 + 8.
+    x = np.array([2.0 ** 24] + [1.0] * 8, np.float32)
+    one = np.ones((1, 9))
+    sc = np.ones(1, np.float32)
+    assert oracle.rowdot_f32("f32", one.astype(np.float32), x)[0] == 2.0 ** 24
+    assert oracle.rowdot_f32("f16", one.astype(np.float16).view(np.uint16), x)[0] == 2.0 ** 24
+    assert oracle.rowdot_f32("rowi8", one.astype(np.int8), x, sc)[0] == 2.0 ** 24 + 8
+    assert oracle.rowdot_f32_subset("rowi8", one.astype(np.int8), x, [0], sc)[0] == 2.0 ** 24
+    # eight full lanes, no tail: x = [2^24, 1 x 63]: lane 0 stays 2^24, lanes
+    # 1..7 hold 8 each: ((2^24 + 8) + 16) + (16 + 16) = 2^24 + 56, exact
+    x = np.array([2.0 ** 24] + [1.0] * 63, np.float32)
+    assert oracle.rowdot_f32("rowi8", np.ones((1, 64), np.int8), x, sc)[0] == 2.0 ** 24 + 56
+    assert oracle.rowdot_f32("f32", np.ones((1, 64), np.float32), x)[0] == 2.0 ** 24
+
+
+def test_rowdot_empty_rows_keep_the_fold_sign():
+    # Rust 1.89's f32 Sum folds from -0.0: an empty f32 / f16 / subset dot is
+    # -0.0; the AVX2 lanes start at +0.0
+    x = np.zeros(0, np.float32)
+    for kind, data in [("f32", np.zeros((2, 0), np.float32)), ("f16", np.zeros((2, 0), np.uint16))]:
+        got = oracle.rowdot_f32(kind, data, x)
+        assert np.all(got == 0) and np.all(np.signbit(got))
+    sc = np.ones(2, np.float32)
+    got = oracle.rowdot_f32("rowi8", np.zeros((2, 0), np.int8), x, sc)
+    assert np.all(got == 0) and not np.any(np.signbit(got))
+    sub = oracle.rowdot_f32_subset("rowi8", np.zeros((2, 0), np.int8), x, [1], sc)
+    assert sub[0] == 0 and np.signbit(sub[0])
