@@ -282,6 +282,30 @@ def main():
                                                     "frac": round(gb / HBM_PEAK_GBS, 3)}
             for w in reps:
                 w.free()
+        # ---------------- unembed row dot (Bundle::rowdot_f32) ----------------
+        # the tied f16 unembed of Gemma-2 (256000 x 2304, 1.18 GB: beyond the
+        # MALL, one table suffices) and its rowi8 form, the GPT-2 f16 head
+        detail["unembed_rowdot"] = {}
+        for name, rows, d, kind in [("gemma2_f16", 256000, 2304, "f16"), ("gemma2_rowi8", 256000, 2304, "rowi8"),
+                                    ("gpt2_f16", 50257, 768, "f16")]:
+            rng = np.random.default_rng(synth.seed(2, 30))
+            if kind == "f16":
+                data = (rng.standard_normal((rows, d), dtype=np.float32) * np.float32(0.02)).astype(np.float16)
+                sc, es = None, 2
+            else:
+                data = rng.integers(-127, 128, (rows, d), dtype=np.int8)
+                sc, es = rng.uniform(1e-4, 3e-4, rows).astype(np.float16).astype(np.float32), 1
+            t = ctx.upload_rows(kind, data, sc)
+            del data
+            x = hip.DeviceArray.from_numpy(rng.standard_normal(d).astype(np.float32))
+            o = hip.DeviceArray((rows,), np.float32)
+            us = time_loop(lambda i: t.rowdot_f32_dev(x.ptr, o.ptr), 30) * 1e3
+            nbytes = rows * d * es + (4 * rows if kind == "rowi8" else 0) + 4 * d + 4 * rows
+            gb = nbytes / (us * 1e-6) / 1e9
+            detail["unembed_rowdot"][name] = {"us": round(us, 2), "GBps": round(gb, 1),
+                                              "frac": round(gb / HBM_PEAK_GBS, 3)}
+            log(f"rowdot {name}: {detail['unembed_rowdot'][name]}")
+            t.free()
         # ---------------- MoE layer (config 4) ----------------
         detail["moe_qwen3_layer"] = {}
         E, d, mi, topk = 128, 2048, 768, 8

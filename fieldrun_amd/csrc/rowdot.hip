@@ -19,10 +19,12 @@
 // chunk tile (64 rows x 128 B) is loaded coalesced (8 lanes per row, 16 B
 // each), staged through the wave's padded LDS tile (row stride 144 B, so the
 // lanes' row reads are conflict-free), and each lane reads back its own row;
-// the next chunk's loads are in flight meanwhile.  x is wave-uniform: its
+// the next one or two chunks' loads are in flight meanwhile.  x is wave-uniform: its
 // reads are scalar loads.  Rows are padded to a multiple of 128 bytes at
 // upload, so chunk loads never run past a row.
 #include "frq_internal.h"
+
+#include <type_traits>
 
 namespace frq {
 
@@ -30,7 +32,7 @@ namespace {
 
 constexpr int TP = 144;  // LDS tile row stride (bytes)
 
-template <int DT, bool SUB>  // DT: 0 f32, 1 f16, 2 rowi8
+template <int DT, bool SUB, int DEPTH>  // DT: 0 f32, 1 f16, 2 rowi8; DEPTH chunks in registers
 __global__ __launch_bounds__(256) void rowdot_kernel(
     const uint8_t* __restrict__ W, const float* __restrict__ rs, int rows, int d, size_t pitch,
     const float* __restrict__ x, const int64_t* __restrict__ cand, int nout, float* __restrict__ out) {
@@ -67,20 +69,47 @@ __global__ __launch_bounds__(256) void rowdot_kernel(
     const int own_row = row_of(o0 + lane, own_ok);
 
     const int nch = (int)(pitch / 128);
-    uint4 cur[8], nxt[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) cur[i] = nch ? ntload16u(src[i]) : make_uint4(0, 0, 0, 0);
-
     float acc = -0.0f;  // the fold (f32, f16, subset rowi8)
     float l8[8] = {0, 0, 0, 0, 0, 0, 0, 0};  // the AVX2 lanes (full rowi8)
-    for (int c = 0; c < nch; ++c) {
-        if (c + 1 < nch) {
+    auto load = [&](uint4 (&b)[8], int c) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) nxt[i] = ntload16u(src[i] + (size_t)(c + 1) * 128);
+        for (int i = 0; i < 8; ++i) b[i] = ntload16u(src[i] + (size_t)c * 128);
+    };
+    // the elements k0 .. k0 + CE of this lane's row, in order; CHECK: only
+    // those below d (the last, partial chunk)
+    auto run = [&](const uint32_t (&v)[32], int k0, auto check) {
+        constexpr bool CHECK = decltype(check)::value;
+        if constexpr (DT == 0) {
+#pragma unroll
+            for (int e = 0; e < CE; ++e)
+                if (!CHECK || k0 + e < d) acc = acc + __builtin_bit_cast(float, v[e]) * x[k0 + e];
+        } else if constexpr (DT == 1) {
+#pragma unroll
+            for (int e = 0; e < CE; ++e)
+                if (!CHECK || k0 + e < d) acc = acc + h2f((uint16_t)(v[e >> 1] >> (16 * (e & 1)))) * x[k0 + e];
+        } else if constexpr (SUB) {
+#pragma unroll
+            for (int e = 0; e < CE; ++e)
+                if (!CHECK || k0 + e < d)
+                    acc = acc + (float)(int8_t)(v[e >> 2] >> (8 * (e & 3))) * x[k0 + e];
+        } else {
+            // full 8-element groups only; the tail follows the lane sum
+#pragma unroll
+            for (int gi = 0; gi < CE / 8; ++gi) {
+                const int kb = k0 + 8 * gi;
+                if (!CHECK || kb + 8 <= d) {
+#pragma unroll
+                    for (int q = 0; q < 8; ++q)
+                        l8[q] = __builtin_fmaf((float)(int8_t)(v[2 * gi + (q >> 2)] >> (8 * (q & 3))), x[kb + q], l8[q]);
+                }
+            }
         }
+    };
+    // one chunk: through the tile, then this lane's row
+    auto consume = [&](const uint4 (&b)[8], int c) {
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-            *reinterpret_cast<uint4*>(tw + (8 * i + (lane >> 3)) * TP + (lane & 7) * 16) = cur[i];
+            *reinterpret_cast<uint4*>(tw + (8 * i + (lane >> 3)) * TP + (lane & 7) * 16) = b[i];
         wave_sync();
         uint32_t v[32];
 #pragma unroll
@@ -90,43 +119,49 @@ __global__ __launch_bounds__(256) void rowdot_kernel(
         }
         wave_sync();  // the tile is read before the next chunk is written
         const int k0 = c * CE;
-        if constexpr (DT == 0) {
-#pragma unroll
-            for (int e = 0; e < CE; ++e)
-                if (k0 + e < d) acc = acc + __builtin_bit_cast(float, v[e]) * x[k0 + e];
-        } else if constexpr (DT == 1) {
-#pragma unroll
-            for (int e = 0; e < CE; ++e)
-                if (k0 + e < d) acc = acc + h2f((uint16_t)(v[e >> 1] >> (16 * (e & 1)))) * x[k0 + e];
-        } else if constexpr (SUB) {
-#pragma unroll
-            for (int e = 0; e < CE; ++e)
-                if (k0 + e < d)
-                    acc = acc + (float)(int8_t)(v[e >> 2] >> (8 * (e & 3))) * x[k0 + e];
-        } else {
-            // full 8-element groups only; the tail follows the lane sum
-#pragma unroll
-            for (int gi = 0; gi < CE / 8; ++gi) {
-                const int kb = k0 + 8 * gi;
-                if (kb + 8 <= d) {
-#pragma unroll
-                    for (int q = 0; q < 8; ++q)
-                        l8[q] = __builtin_fmaf((float)(int8_t)(v[2 * gi + (q >> 2)] >> (8 * (q & 3))), x[kb + q], l8[q]);
-                }
-            }
+        if (k0 + CE <= d) run(v, k0, std::false_type{});  // wave-uniform
+        else run(v, k0, std::true_type{});
+        if constexpr (DT == 2 && !SUB) {
             if (c == nch - 1) {
                 const float q0 = l8[0] + l8[4], q1 = l8[1] + l8[5], q2 = l8[2] + l8[6], q3 = l8[3] + l8[7];
                 acc = (q0 + q2) + (q1 + q3);
                 const int kt = d & ~7;  // the tail lies in this chunk
+                if (kt < d) {
 #pragma unroll
-                for (int e = 0; e < CE; ++e)
-                    if (k0 + e >= kt && k0 + e < d)
-                        acc = acc + (float)(int8_t)(v[e >> 2] >> (8 * (e & 3))) * x[k0 + e];
+                    for (int e = 0; e < CE; ++e)
+                        if (k0 + e >= kt && k0 + e < d)
+                            acc = acc + (float)(int8_t)(v[e >> 2] >> (8 * (e & 3))) * x[k0 + e];
+                }
             }
         }
-        if (c + 1 < nch) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) cur[i] = nxt[i];
+    };
+    // DEPTH - 1 chunks in flight ahead of the one consumed: a ring of DEPTH
+    // register buffers, rotated by unrolling (static indices).  Every load
+    // is issued unconditionally (the index clamped to the last chunk, whose
+    // re-reads hit L2), so the waits before a buffer's use count exactly
+    // the loads issued after it.
+    uint4 b0[8], b1[8], b2[8];
+    if (nch > 0) {
+        const int last = nch - 1;
+        load(b0, 0);
+        load(b1, min(1, last));
+        if constexpr (DEPTH == 2) {
+            for (int c = 0; c < nch; c += 2) {
+                consume(b0, c);
+                load(b0, min(c + 2, last));
+                if (c + 1 < nch) consume(b1, c + 1);
+                load(b1, min(c + 3, last));
+            }
+        } else {
+            load(b2, min(2, last));
+            for (int c = 0; c < nch; c += 3) {
+                consume(b0, c);
+                load(b0, min(c + 3, last));
+                if (c + 1 < nch) consume(b1, c + 1);
+                load(b1, min(c + 4, last));
+                if (c + 2 < nch) consume(b2, c + 2);
+                load(b2, min(c + 5, last));
+            }
         }
     }
     if constexpr (DT == 2) {
@@ -141,12 +176,24 @@ template <int DT>
 hipError_t launch_dt(const Weight& w, const float* x, const int64_t* cand, size_t nout, float* out,
                      hipStream_t s) {
     const unsigned grid = (unsigned)((nout + 255) / 256);
-    if (cand)
-        rowdot_kernel<DT, true><<<dim3(grid), dim3(256), 0, s>>>(
-            w.rowp, w.scale, (int)w.n, (int)w.k, w.rpitch, x, cand, (int)nout, out);
-    else
-        rowdot_kernel<DT, false><<<dim3(grid), dim3(256), 0, s>>>(
-            w.rowp, w.scale, (int)w.n, (int)w.k, w.rpitch, x, nullptr, (int)nout, out);
+    // fewer waves than about four per SIMD: keep three chunks in flight per
+    // wave (latency-bound), else two (the occupancy carries the load)
+    const bool deep = nout < 4 * 1024 * 64;
+    if (cand) {
+        if (deep)
+            rowdot_kernel<DT, true, 3><<<dim3(grid), dim3(256), 0, s>>>(
+                w.rowp, w.scale, (int)w.n, (int)w.k, w.rpitch, x, cand, (int)nout, out);
+        else
+            rowdot_kernel<DT, true, 2><<<dim3(grid), dim3(256), 0, s>>>(
+                w.rowp, w.scale, (int)w.n, (int)w.k, w.rpitch, x, cand, (int)nout, out);
+    } else {
+        if (deep)
+            rowdot_kernel<DT, false, 3><<<dim3(grid), dim3(256), 0, s>>>(
+                w.rowp, w.scale, (int)w.n, (int)w.k, w.rpitch, x, nullptr, (int)nout, out);
+        else
+            rowdot_kernel<DT, false, 2><<<dim3(grid), dim3(256), 0, s>>>(
+                w.rowp, w.scale, (int)w.n, (int)w.k, w.rpitch, x, nullptr, (int)nout, out);
+    }
     return hipGetLastError();
 }
 
