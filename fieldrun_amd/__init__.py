@@ -12,6 +12,9 @@ The classes mirror the reference's interface for this path
   MoeBank.forward(...)    the routed expert branch of qwen3moe::moe_branch
                           (src/qwen3moe.rs:120-158) / gemma4 (131-187)
   MoeBank.expert_mm(...)  Bundle::expert_mm (src/bundle.rs:457-461)
+  Bundle.load(stem)       Bundle::load (src/bundle.rs:314-376): manifest +
+                          mapped blob; Bundle.mm / rowdot_f32 / expert bank
+                          upload each array once onto the context's device
   RowTable.rowdot_f32(x)  Bundle::rowdot_f32 (src/bundle.rs:958-987), the
                           unembed over an f32 / f16 / rowi8 (vocab, d) table,
                           and rowdot_f32_subset (995-1015)
@@ -67,6 +70,12 @@ SIGNATURES = {
     "frq_rowdot_f32_dev": (_I, [_P, _P, _P, _P]),
     "frq_rowdot_f32_subset": (_I, [_P, _P, _P, _P, _S, _P]),
     "frq_rowdot_f32_subset_dev": (_I, [_P, _P, _P, _P, _S, _P]),
+    "frq_bundle_open": (_I, [C.c_char_p, _P]),
+    "frq_bundle_close": (None, [_P]),
+    "frq_bundle_header": (_I, [_P, _P, _S, _P, _P, _P, _P]),
+    "frq_bundle_array": (_I, [_P, C.c_char_p, _P, _S, _P, _P, _P, _P, _P]),
+    "frq_bundle_weight": (_I, [_P, _P, C.c_char_p, _P]),
+    "frq_bundle_moe": (_I, [_P, _P, C.c_char_p, _S, _I, _P]),
 }
 
 
@@ -346,3 +355,116 @@ class MoeBank:
         y = np.empty((x.shape[0], out_dim), np.float32)
         _check(lib.frq_expert_mm(self.ctx.h, self.h, which, e, _ptr(x), x.shape[0], _ptr(y)))
         return y
+
+
+class Bundle:
+    """A fieldrun bundle (<stem>.fieldrun.json + .fieldrun.bin) opened by the
+    library's reader (Bundle::load, src/bundle.rs:314-376).  Arrays are views
+    of the mapped blob; mm / rowdot_f32 upload a weight on first use onto the
+    context's device (the resident set of the GPU path) and call the
+    kernels."""
+
+    def __init__(self, stem: str, ctx: "Context | None" = None):
+        self.h = None
+        out = C.c_void_p()
+        _check(lib.frq_bundle_open(os.fspath(stem).encode(), C.byref(out)))
+        self.h = out.value
+        self.ctx = ctx
+        self._dev = {}
+        arch = C.create_string_buffer(64)
+        nc, nf = C.c_size_t(0), C.c_size_t(0)
+        _check(lib.frq_bundle_header(self.h, arch, 64, None, C.byref(nc), None, C.byref(nf)))
+        cfg = (C.c_int64 * max(nc.value, 1))()
+        cff = (C.c_double * max(nf.value, 1))()
+        _check(lib.frq_bundle_header(self.h, arch, 64, cfg, C.byref(nc), cff, C.byref(nf)))
+        self.arch = arch.value.decode()
+        self.config = [int(cfg[i]) for i in range(nc.value)]
+        self.config_f = [float(cff[i]) for i in range(nf.value)]
+
+    @classmethod
+    def load(cls, stem: str, ctx: "Context | None" = None) -> "Bundle":
+        return cls(stem, ctx)
+
+    def close(self):
+        for w in self._dev.values():
+            w.free()
+        self._dev = {}
+        if self.h:
+            lib.frq_bundle_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def info(self, name: str):
+        """(dtype, shape, group, nbytes) of a stored array."""
+        dt = C.create_string_buffer(16)
+        shape = (C.c_size_t * 8)()
+        nd, grp, data, nb = C.c_size_t(8), C.c_size_t(0), C.c_void_p(), C.c_size_t(0)
+        _check(lib.frq_bundle_array(self.h, name.encode(), dt, 16, shape, C.byref(nd), C.byref(grp),
+                                    C.byref(data), C.byref(nb)))
+        return dt.value.decode(), tuple(shape[i] for i in range(nd.value)), grp.value, nb.value
+
+    def arr(self, name: str) -> np.ndarray:
+        """The stored bytes of an array as a read-only numpy view in its stored
+        type (f32, f16 bits as float16, i8 / rowi8 as int8, i4 / q4a packed
+        bytes as uint8)."""
+        dt, shape, _, nb = self.info(name)
+        data = C.c_void_p()
+        nd = C.c_size_t(0)
+        _check(lib.frq_bundle_array(self.h, name.encode(), None, 0, None, C.byref(nd), None, C.byref(data), None))
+        np_dt = {"f32": np.float32, "f16": np.float16, "i8": np.int8, "rowi8": np.int8}.get(dt, np.uint8)
+        if nb == 0:
+            return np.zeros(shape if np_dt is not np.uint8 else (0,), np_dt)
+        buf = (C.c_uint8 * nb).from_address(data.value)
+        a = np.frombuffer(buf, np.uint8).view(np_dt)
+        if dt in ("i4", "q4a"):
+            a = a.reshape(shape[0], -1)
+        else:
+            a = a.reshape(shape)
+        a.flags.writeable = False
+        return a
+
+    def dims(self, name: str):
+        """Bundle::dims: the logical (rows, cols) of a 2-D array."""
+        _, shape, _, _ = self.info(name)
+        return shape[0], shape[1]
+
+    def weight(self, name: str):
+        """The device copy of an array (uploaded once, owned by the bundle)."""
+        if name not in self._dev:
+            if self.ctx is None:
+                raise FrqError(FRQ_ERR_ARG, "this bundle was opened without a device context")
+            out = C.c_void_p()
+            _check(lib.frq_bundle_weight(self.ctx.h, self.h, name.encode(), C.byref(out)))
+            h = out.value
+            dtype, n, k, g = C.c_int(0), C.c_size_t(0), C.c_size_t(0), C.c_size_t(0)
+            _check(lib.frq_w_info(h, C.byref(dtype), C.byref(n), C.byref(k), C.byref(g)))
+            cls = RowTable if dtype.value in (FRQ_DT_F32, FRQ_DT_F16, FRQ_DT_ROWI8) else Weight
+            self._dev[name] = cls(self.ctx, h, dtype.value, n.value, k.value, g.value)
+        return self._dev[name]
+
+    def mm(self, a: np.ndarray, name: str) -> np.ndarray:
+        """Bundle::mm(a, name) for an i8 / i4 linear, on the device."""
+        return self.weight(name).mm(a)
+
+    def rowdot_f32(self, name: str, x: np.ndarray) -> np.ndarray:
+        """Bundle::rowdot_f32(name, x) over an f32 / f16 / rowi8 table."""
+        return self.weight(name).rowdot_f32(x)
+
+    def rowdot_f32_subset(self, name: str, x: np.ndarray, cand) -> np.ndarray:
+        return self.weight(name).rowdot_f32_subset(x, cand)
+
+    def moe(self, prefix: str, n_exp: int, act: int = FRQ_ACT_SILU) -> "MoeBank":
+        """The routed expert bank of one MoE layer ({prefix}experts.{e}.*)."""
+        if self.ctx is None:
+            raise FrqError(FRQ_ERR_ARG, "this bundle was opened without a device context")
+        out = C.c_void_p()
+        _check(lib.frq_bundle_moe(self.ctx.h, self.h, prefix.encode(), n_exp, act, C.byref(out)))
+        h = out.value
+        _, shape, _, _ = self.info(prefix + "experts.0.down")
+        mi, d = shape
+        return MoeBank(self.ctx, h, n_exp, d, mi, act)

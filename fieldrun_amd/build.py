@@ -15,7 +15,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libfrq.so")
-SOURCES = ["api.hip", "quant.hip", "gemv_i8.hip", "skinny_i8.hip", "gemm_i8.hip", "i4.hip", "moe.hip", "rowdot.hip"]
+SOURCES = ["api.hip", "quant.hip", "gemv_i8.hip", "skinny_i8.hip", "gemm_i8.hip", "i4.hip", "moe.hip", "rowdot.hip",
+           "bundle.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",

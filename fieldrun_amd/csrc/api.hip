@@ -38,9 +38,11 @@ struct frq_ctx {
 namespace {
 
 thread_local std::string g_err;
+thread_local int g_code = FRQ_OK;
 
 int fail(int code, const std::string& msg) {
     g_err = msg;
+    g_code = code;
     return code;
 }
 int hip_fail(hipError_t e, const char* what) {
@@ -218,6 +220,11 @@ int alloc_i8(frq_ctx* c, Weight& w) {
 }
 
 }  // namespace
+
+namespace frq {
+int set_error(int code, const std::string& msg) { return fail(code, msg); }
+int last_code() { return g_code; }
+}  // namespace frq
 
 extern "C" {
 

@@ -21,6 +21,8 @@
 //                     channel.
 #pragma once
 
+#include <string>
+
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -178,6 +180,11 @@ hipError_t launch_gemm_i8(const Weight& w, size_t m, const int8_t* a8b,
                           const float* sa, const uint32_t* oidx,
                           const float* oval, float* out, int32_t* acc, void* ws,
                           hipStream_t s);
+// Sets the calling thread's frq_last_error() message and returns code.
+int set_error(int code, const std::string& msg);
+// The status of the calling thread's last failure.
+int last_code();
+
 // Row tables (FRQ_DT_F32 / F16 / ROWI8): bytes per padded row, and
 // out[i] = dot(W[row i], x) for nout rows (cand == nullptr: rows 0..nout-1;
 // else the candidate ids, invalid ones -inf).

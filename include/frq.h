@@ -59,6 +59,7 @@ enum { FRQ_ACT_SILU = 0, FRQ_ACT_GELU_TANH = 1 };
 typedef struct frq_ctx frq_ctx;
 typedef struct frq_w frq_w;
 typedef struct frq_moe_w frq_moe_w;
+typedef struct frq_bundle frq_bundle;
 
 /* Last error message of the calling thread ("" when none). */
 const char* frq_last_error(void);
@@ -192,6 +193,41 @@ int frq_moe_route(frq_ctx* ctx, const float* logits, size_t T, size_t E,
  * 1 up, 2 down). */
 int frq_expert_mm(frq_ctx* ctx, const frq_moe_w* m, int which, size_t e,
                   const float* x, size_t mrows, float* y);
+
+/* ---- the bundle: Bundle::load (src/bundle.rs:314-376, FORMAT.md) --------
+ * frq_bundle_open reads <stem>.fieldrun.json and maps <stem>.fieldrun.bin
+ * read-only (host only, no device): FRQ_ERR_FORMAT for a manifest the
+ * reference refuses (format != "fieldrun-bundle", version != 1, an array
+ * beyond the blob), FRQ_ERR_ARG for I/O errors; *out is the bundle or NULL. */
+int frq_bundle_open(const char* stem, frq_bundle** out);
+void frq_bundle_close(frq_bundle* b);
+/* arch (NUL-terminated, truncated to arch_cap), config / config_f: up to
+ * *n entries copied, *n set to the manifest's count. */
+int frq_bundle_header(const frq_bundle* b, char* arch, size_t arch_cap,
+                      int64_t* config, size_t* n_config, double* config_f,
+                      size_t* n_config_f);
+/* One array as stored (expert arrays included): dtype string, shape (up
+ * to *ndim dims copied, *ndim set), int4 group (0 when absent), a pointer
+ * into the mapped blob (valid until frq_bundle_close) and its byte count.
+ * FRQ_ERR_MISSING when absent (src/bundle.rs:378-380). */
+int frq_bundle_array(const frq_bundle* b, const char* name, char* dtype,
+                     size_t dtype_cap, size_t* shape, size_t* ndim,
+                     size_t* group, const void** data, size_t* bytes);
+/* Upload one array onto ctx's device in its stored precision: an i8 linear
+ * (with its f16 __scale, as frq_upload_i8_bundle), an i4 linear (with its
+ * f16 (out, ceil(in/g)) __scale and group, default 32), a rowi8 table (f16
+ * row scales) or a 2-D f16 / f32 table (as frq_upload_rows).  The caller
+ * owns *out (frq_w_free).  FRQ_ERR_MISSING for an absent array or scale,
+ * FRQ_ERR_FORMAT when a size does not match its shape, FRQ_ERR_DTYPE for a
+ * dtype with no device form here. */
+int frq_bundle_weight(frq_ctx* ctx, const frq_bundle* b, const char* name,
+                      frq_w** out);
+/* The routed expert bank of one MoE layer: n_exp experts named
+ * {prefix}experts.{e}.gate / .up / .down (FRQ_ACT_SILU, qwen3moe) or
+ * .gate_up / .down (FRQ_ACT_GELU_TANH, gemma4), int8 (in, out) with f16
+ * __scale siblings (src/qwen3moe.rs:148-152, src/gemma4.rs:174-181). */
+int frq_bundle_moe(frq_ctx* ctx, const frq_bundle* b, const char* prefix,
+                   size_t n_exp, int act, frq_moe_w** out);
 
 #ifdef __cplusplus
 }
