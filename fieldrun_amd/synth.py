@@ -68,3 +68,57 @@ def moe_layer(E: int, d: int, mi: int, s: int, act: int = 0, std: float = 0.02):
             w, sc = lin(mi, d); up.append(w); us.append(sc)
         w, sc = lin(d, mi); down.append(w); ds.append(sc)
     return gate, gs, up, us, down, ds
+
+
+# ---- synthetic random-init bundles in the reference format (the BASELINE
+# configs; array names and layouts as src/convert.rs writes them) ----------
+
+def write_gpt2_bundle(stem: str, s: int, n_layer: int = 12, n_head: int = 12, d: int = 768,
+                      n_pos: int = 1024, vocab: int = 50257, std: float = 0.02) -> dict:
+    """a GPT-2-small-shaped int8 bundle (convert_gpt2,
+    src/convert.rs:505-545 with dtype int8): wte / wpe / ln_f in f16, LN
+    gains 1 and biases 0, the four Conv1D linears per layer int8 from
+    (in, out) sources with f16 biases.  Weights ~ N(0, std)."""
+    from .bundle import BundleWriter, manifest
+    rng = np.random.default_rng(s)
+    nrm = lambda *shape: (rng.standard_normal(shape, dtype=np.float32) * np.float32(std))
+    w = BundleWriter(stem)
+    w.put_embed("wte", nrm(vocab, d), "f16", "int8")
+    w.put_small("wpe", nrm(n_pos, d), None, "int8")
+    w.put_small("ln_f.weight", np.ones(d, np.float32), None, "int8")
+    w.put_small("ln_f.bias", np.zeros(d, np.float32), None, "int8")
+    for l in range(n_layer):
+        for ln in ("ln_1", "ln_2"):
+            w.put_small(f"h{l}.{ln}.weight", np.ones(d, np.float32), None, "int8")
+            w.put_small(f"h{l}.{ln}.bias", np.zeros(d, np.float32), None, "int8")
+        for name, (i, o) in (("attn.c_attn", (d, 3 * d)), ("attn.c_proj", (d, d)),
+                             ("mlp.c_fc", (d, 4 * d)), ("mlp.c_proj", (4 * d, d))):
+            w.put_i8(f"h{l}.{name}.weight", nrm(i, o), False)
+            w.put_small(f"h{l}.{name}.bias", np.zeros(o, np.float32), None, "int8")
+    m = manifest("gpt2", [n_layer, n_head, d, n_pos, vocab])
+    w.finish(m)
+    return m
+
+
+def write_qwen3moe_layer_bundle(stem: str, s: int, n_exp: int = 128, d: int = 2048, mi: int = 768,
+                                topk: int = 8, std: float = 0.02) -> dict:
+    """one Qwen3-MoE routed layer as convert_qwen3moe writes it
+    (src/convert.rs:872-936, dtype int8): the router l0.gate and the experts
+    l0.experts.{e}.gate / .up / .down, each put_lin from an (out, in)
+    Linear source -> int8 (in, out) + f16 __scale.  The manifest's config
+    follows that converter's vector for a one-layer model (Qwen3-30B-A3B
+    attention dims, all of its arrays but the MoE layer absent)."""
+    from .bundle import BundleWriter, manifest
+    rng = np.random.default_rng(s)
+    nrm = lambda *shape: (rng.standard_normal(shape, dtype=np.float32) * np.float32(std))
+    w = BundleWriter(stem)
+    w.put_lin("l0.gate", nrm(n_exp, d), "int8")
+    for e in range(n_exp):
+        w.put_lin(f"l0.experts.{e}.gate", nrm(mi, d), "int8")
+        w.put_lin(f"l0.experts.{e}.up", nrm(mi, d), "int8")
+        w.put_lin(f"l0.experts.{e}.down", nrm(d, mi), "int8")
+    nh, nkv, hd, vocab = 32, 4, 128, 151936
+    cfg = [1, nh, nkv, hd, d, 6144, vocab, 0, n_exp, topk, mi, 1, 1, 0]
+    m = manifest("qwen3moe", cfg, [1e6, 1e-6])
+    w.finish(m)
+    return m

@@ -149,3 +149,43 @@ def test_reader_json_details(tmp_path):
     dt, shape, group, nb = b.info("embéd\t")
     assert (dt, shape, group, nb) == ("f32", (2, 8), 0, 64)
     b.close()
+
+
+def test_config_bundles_follow_the_converters(tmp_path):
+    """The synthetic config bundles carry the names, dtypes and stored
+    shapes convert_gpt2 (src/convert.rs:505-545) and convert_qwen3moe
+    (872-938, one MoE layer) write for an int8 build."""
+    from fieldrun_amd import synth
+    stem = str(tmp_path / "g")
+    synth.write_gpt2_bundle(stem, 1, n_layer=2, n_head=2, d=32, n_pos=8, vocab=40)
+    m = json.load(open(stem + ".fieldrun.json"))
+    assert (m["arch"], m["config"]) == ("gpt2", [2, 2, 32, 8, 40])
+    dt = {a["name"]: (a["dtype"], a["shape"]) for a in m["arrays"]}
+    want = {"wte": ("f16", [40, 32]), "wpe": ("f16", [8, 32]),
+            "ln_f.weight": ("f16", [32]), "ln_f.bias": ("f16", [32])}
+    for l in range(2):
+        for ln in ("ln_1", "ln_2"):
+            want[f"h{l}.{ln}.weight"] = want[f"h{l}.{ln}.bias"] = ("f16", [32])
+        for name, (i, o) in (("attn.c_attn", (32, 96)), ("attn.c_proj", (32, 32)),
+                             ("mlp.c_fc", (32, 128)), ("mlp.c_proj", (128, 32))):
+            want[f"h{l}.{name}.weight"] = ("i8", [i, o])
+            want[f"h{l}.{name}.weight__scale"] = ("f16", [o])
+            want[f"h{l}.{name}.bias"] = ("f16", [o])
+    assert dt == want
+    b = fa.Bundle(stem)
+    assert np.all(b.arr("h1.ln_2.weight") == 1) and np.all(b.arr("h0.attn.c_proj.bias") == 0)
+    b.close()
+
+    stem = str(tmp_path / "q")
+    synth.write_qwen3moe_layer_bundle(stem, 1, n_exp=3, d=64, mi=16, topk=2)
+    m = json.load(open(stem + ".fieldrun.json"))
+    assert m["arch"] == "qwen3moe" and m["config_f"] == [1e6, 1e-6]
+    # [nl, nh, nkv, hd, d, ffn, vocab, tie, n_exp, topk, moe_inter, norm_topk, moe flag l0, window]
+    assert m["config"] == [1, 32, 4, 128, 64, 6144, 151936, 0, 3, 2, 16, 1, 1, 0]
+    dt = {a["name"]: (a["dtype"], a["shape"]) for a in m["arrays"]}
+    want = {"l0.gate": ("i8", [64, 3]), "l0.gate__scale": ("f16", [3])}
+    for e in range(3):
+        for fr, (i, o) in (("gate", (64, 16)), ("up", (64, 16)), ("down", (16, 64))):
+            want[f"l0.experts.{e}.{fr}"] = ("i8", [i, o])
+            want[f"l0.experts.{e}.{fr}__scale"] = ("f16", [o])
+    assert dt == want

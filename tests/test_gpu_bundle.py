@@ -104,3 +104,50 @@ def test_bundle_upload_errors(ctx, stem):
         b.moe("l9.", 2)
     assert e.value.code == fa.FRQ_ERR_MISSING
     b.close()
+
+
+def test_gpt2_config_bundle_on_device(ctx, tmp_path):
+    """configs[0]'s shapes (GPT-2 small, one layer): each Conv1D linear read
+    from the bundle and run on the device gives the oracle's bits, and the
+    tied f16 wte unembed is the reference's rowdot_f32."""
+    stem = str(tmp_path / "gpt2")
+    synth.write_gpt2_bundle(stem, 5, n_layer=1)
+    b = fa.Bundle(stem, ctx)
+    for name in ("attn.c_attn", "attn.c_proj", "mlp.c_fc", "mlp.c_proj"):
+        w = f"h0.{name}.weight"
+        k, n = b.dims(w)
+        wt = np.ascontiguousarray(b.arr(w).T)
+        sc = b.arr(w + "__scale").astype(np.float32)
+        for m in (1, 8):
+            a = synth.activations(m, k, 17 * m + n)
+            assert same_bits(b.mm(a, w), oracle.mm_i8(a, wt, sc)), (name, m)
+    x = np.random.default_rng(6).standard_normal(768).astype(np.float32)
+    assert same_bits(b.rowdot_f32("wte", x), oracle.rowdot_f32("f16", b.arr("wte").view(np.uint16), x))
+    b.close()
+
+
+def test_qwen3moe_config_bundle_on_device(ctx, tmp_path):
+    """configs[3]'s expert shapes (Qwen3-30B-A3B: d 2048, moe_inter 768, top
+    8) with 16 experts: the router is the bundle's int8 l0.gate through mm,
+    and the routed layer from the bundle's expert bank matches the oracle."""
+    E, d, mi, k = 16, 2048, 768, 8
+    stem = str(tmp_path / "q")
+    synth.write_qwen3moe_layer_bundle(stem, 6, n_exp=E, d=d, mi=mi, topk=k)
+    b = fa.Bundle(stem, ctx)
+    x = np.random.default_rng(8).standard_normal((6, d)).astype(np.float32)
+    rt = np.ascontiguousarray(b.arr("l0.gate").T)
+    logits = b.mm(x, "l0.gate")
+    assert same_bits(logits, oracle.mm_i8(x, rt, b.arr("l0.gate__scale").astype(np.float32)))
+    bank = b.moe("l0.", E, fa.FRQ_ACT_SILU)
+    lst = lambda fr: [b.arr(f"l0.experts.{e}.{fr}") for e in range(E)]
+    scs = lambda fr: [b.arr(f"l0.experts.{e}.{fr}__scale").astype(np.float32) for e in range(E)]
+    out = bank.forward(x, logits, k, True)
+    ref = oracle.moe(x, logits, k, True, lst("gate"), scs("gate"), lst("up"), scs("up"),
+                     lst("down"), scs("down"), 0, None)
+    sel, _ = ctx.moe_route(logits, k, True)
+    rsel, _, _ = oracle.moe_route(logits, k, True)
+    same = np.all(np.sort(sel, 1) == np.sort(rsel, 1), axis=1)
+    assert same.sum() >= 5
+    err = np.abs(out[same] - ref[same]).max()
+    assert err <= 1e-5 * np.abs(ref).max(), err
+    b.close()
