@@ -76,6 +76,13 @@ SIGNATURES = {
     "frq_bundle_array": (_I, [_P, C.c_char_p, _P, _S, _P, _P, _P, _P, _P]),
     "frq_bundle_weight": (_I, [_P, _P, C.c_char_p, _P]),
     "frq_bundle_moe": (_I, [_P, _P, C.c_char_p, _S, _I, _P]),
+    "frq_gpt2_load": (_I, [_P, _P, _I, _P]),
+    "frq_gpt2_free": (None, [_P]),
+    "frq_gpt2_info": (_I, [_P, _P, _P, _P, _P, _P]),
+    "frq_gpt2_set_graphs": (_I, [_P, _I]),
+    "frq_gpt2_generate": (_I, [_P, _P, _P, _S, _S, _P, _P]),
+    "frq_gpt2_predict": (_I, [_P, _P, _P, _S, _P, _P]),
+    "frq_libm_f32": (_I, [_P, _I, _P, _S, _P]),
 }
 
 
@@ -468,3 +475,65 @@ class Bundle:
         _, shape, _, _ = self.info(prefix + "experts.0.down")
         mi, d = shape
         return MoeBank(self.ctx, h, n_exp, d, mi, act)
+
+
+class Gpt2:
+    """Gpt2 of src/composition.rs on the device: Gpt2::new over an arch
+    "gpt2" bundle (52-56), Model::generate (317-341; kv_int8: the int8
+    cache, 251-270) and Model::predict (304-308), every step resident in
+    HBM.  `bundle` is a Bundle opened with this context."""
+
+    def __init__(self, bundle: "Bundle", kv_int8: bool = False, ctx: "Context | None" = None):
+        self.ctx = ctx or bundle.ctx
+        if self.ctx is None:
+            raise FrqError(FRQ_ERR_ARG, "this bundle was opened without a device context")
+        self.h = None
+        out = C.c_void_p()
+        _check(lib.frq_gpt2_load(self.ctx.h, bundle.h, int(kv_int8), C.byref(out)))
+        self.h = out.value
+        dims = [C.c_size_t(0) for _ in range(5)]
+        _check(lib.frq_gpt2_info(self.h, *[C.byref(v) for v in dims]))
+        self.n_layer, self.n_head, self.d, self.n_pos, self.vocab = (v.value for v in dims)
+        self.kv_int8 = bool(kv_int8)
+
+    def free(self):
+        if self.h:
+            lib.frq_gpt2_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def set_graphs(self, on: bool):
+        _check(lib.frq_gpt2_set_graphs(self.h, int(on)))
+
+    def generate(self, prompt, n_new: int, with_logits: bool = False):
+        prompt = np.ascontiguousarray(prompt, dtype=np.int64)
+        out = np.empty(n_new, np.int64)
+        lg = np.empty((n_new, self.vocab), np.float32) if with_logits else None
+        _check(lib.frq_gpt2_generate(self.ctx.h, self.h, _ptr(prompt), len(prompt), n_new, _ptr(out),
+                                     None if lg is None else _ptr(lg)))
+        return (out, lg) if with_logits else out
+
+    def predict(self, ids, with_logits: bool = False):
+        ids = np.ascontiguousarray(ids, dtype=np.int64)
+        tok = np.zeros(1, np.int64)
+        lg = np.empty(self.vocab, np.float32) if with_logits else None
+        _check(lib.frq_gpt2_predict(self.ctx.h, self.h, _ptr(ids), len(ids), _ptr(tok),
+                                    None if lg is None else _ptr(lg)))
+        return (int(tok[0]), lg) if with_logits else int(tok[0])
+
+
+LIBM_FNS = {"expf": 0, "expm1f": 1, "tanhf": 2}
+
+
+def libm_f32(fn: str, x: np.ndarray, ctx: "Context | None" = None) -> np.ndarray:
+    """The library's f32 expf / expm1f / tanhf (the libm algorithms the
+    reference's f32::exp / f32::tanh reach), on ctx's device or the host."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    _check(lib.frq_libm_f32(None if ctx is None else ctx.h, LIBM_FNS[fn], _ptr(x), x.size, _ptr(out)))
+    return out

@@ -224,6 +224,9 @@ int alloc_i8(frq_ctx* c, Weight& w) {
 namespace frq {
 int set_error(int code, const std::string& msg) { return fail(code, msg); }
 int last_code() { return g_code; }
+int ctx_device(const frq_ctx* c) { return c->device; }
+int* ctx_err(frq_ctx* c) { return c->err; }
+const Weight* weight_of(const frq_w* w) { return &w->w; }
 }  // namespace frq
 
 extern "C" {

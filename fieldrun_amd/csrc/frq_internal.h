@@ -180,6 +180,12 @@ hipError_t launch_gemm_i8(const Weight& w, size_t m, const int8_t* a8b,
                           const float* sa, const uint32_t* oidx,
                           const float* oval, float* out, int32_t* acc, void* ws,
                           hipStream_t s);
+// Context and weight internals, for engines built on the entry points: the
+// context's device, its NaN error word (reported by frq_sync) and a
+// weight's device layout.
+int ctx_device(const frq_ctx* c);
+int* ctx_err(frq_ctx* c);
+const Weight* weight_of(const frq_w* w);
 // Sets the calling thread's frq_last_error() message and returns code.
 int set_error(int code, const std::string& msg);
 // The status of the calling thread's last failure.

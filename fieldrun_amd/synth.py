@@ -73,6 +73,11 @@ def moe_layer(E: int, d: int, mi: int, s: int, act: int = 0, std: float = 0.02):
 # ---- synthetic random-init bundles in the reference format (the BASELINE
 # configs; array names and layouts as src/convert.rs writes them) ----------
 
+def gpt2_prompt(n: int, vocab: int, s: int) -> np.ndarray:
+    """A seeded uniform-random prompt of n token ids in [0, vocab)."""
+    return np.random.default_rng(s).integers(0, vocab, n).astype(np.int64)
+
+
 def write_gpt2_bundle(stem: str, s: int, n_layer: int = 12, n_head: int = 12, d: int = 768,
                       n_pos: int = 1024, vocab: int = 50257, std: float = 0.02) -> dict:
     """a GPT-2-small-shaped int8 bundle (convert_gpt2,

@@ -60,6 +60,7 @@ typedef struct frq_ctx frq_ctx;
 typedef struct frq_w frq_w;
 typedef struct frq_moe_w frq_moe_w;
 typedef struct frq_bundle frq_bundle;
+typedef struct frq_gpt2 frq_gpt2;
 
 /* Last error message of the calling thread ("" when none). */
 const char* frq_last_error(void);
@@ -228,6 +229,39 @@ int frq_bundle_weight(frq_ctx* ctx, const frq_bundle* b, const char* name,
  * __scale siblings (src/qwen3moe.rs:148-152, src/gemma4.rs:174-181). */
 int frq_bundle_moe(frq_ctx* ctx, const frq_bundle* b, const char* prefix,
                    size_t n_exp, int act, frq_moe_w** out);
+
+/* ---- GPT-2 decode: Gpt2 (src/composition.rs) on the device --------------
+ * frq_gpt2_load is Gpt2::new (52-56) over an arch "gpt2" bundle (config
+ * [n_layer, n_head, n_embd, n_positions, vocab]; arrays as convert_gpt2
+ * writes them, src/convert.rs:505-545): the int8 / int4 linears, the f16
+ * wte table (embedding rows and the tied unembed), wpe, the layernorms and
+ * biases go to ctx's device with a KV cache of n_positions rows per layer
+ * (kv_int8: int8 with an f32 scale per position and head, as
+ * forward_block_q, 214-249).  FRQ_ERR_FORMAT / FRQ_ERR_MISSING /
+ * FRQ_ERR_DTYPE for a bundle that does not match. */
+int frq_gpt2_load(frq_ctx* ctx, const frq_bundle* b, int kv_int8, frq_gpt2** out);
+void frq_gpt2_free(frq_gpt2* g);
+int frq_gpt2_info(const frq_gpt2* g, size_t* n_layer, size_t* n_head, size_t* d, size_t* n_pos,
+                  size_t* vocab);
+/* Model::generate for Gpt2 (317-341 / 251-270): n_new greedy tokens after
+ * the prompt (prefill, then one cached decode step per token) into out;
+ * logits (n_new, vocab), nullable, receives the logits each token was
+ * chosen from.  FRQ_ERR_ARG for an id outside the vocabulary or a position
+ * past n_positions (the reference panics on those rows), FRQ_ERR_NAN for
+ * NaN activations or logits.  Calls on one model must not overlap. */
+int frq_gpt2_generate(frq_ctx* ctx, frq_gpt2* g, const int64_t* prompt, size_t n_prompt, size_t n_new,
+                      int64_t* out, float* logits);
+/* Model::predict (304-308): the next token after ids (logits nullable). */
+int frq_gpt2_predict(frq_ctx* ctx, frq_gpt2* g, const int64_t* ids, size_t n, int64_t* token,
+                     float* logits);
+/* Decode steps run as one captured HIP graph per generate call (replayed
+ * per token) unless switched off here; the results are the same. */
+int frq_gpt2_set_graphs(frq_gpt2* g, int on);
+/* The f32 libm functions the decode kernels use (fn 0 expf, 1 expm1f, 2
+ * tanhf), bit-identical to the libm behind Rust's f32::exp / f32::tanh
+ * (glibc's expf and fdlibm's expm1f / tanhf): out[i] = f(x[i]) for n host
+ * values, on ctx's device, or on the host when ctx is NULL. */
+int frq_libm_f32(frq_ctx* ctx, int fn, const float* x, size_t n, float* out);
 
 #ifdef __cplusplus
 }

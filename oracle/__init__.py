@@ -52,6 +52,11 @@ def _load():
         "fro_moe": (I, [P, S, S, P, S, S, I, P, S, I, P, P, P, P, P, P, P]),
         "fro_rowdot_f32": (None, [I, P, P, S, S, P, P]),
         "fro_rowdot_f32_subset": (None, [I, P, P, S, S, P, P, S, P]),
+        "fro_layernorm": (None, [P, S, S, P, P, P]),
+        "fro_nd_sum": (F, [P, S]),
+        "fro_libm_f32": (None, [I, P, S, P]),
+        "fro_gpt2_generate": (I, [P, P, S, S, I, I, P, P]),
+        "fro_gpt2_predict": (I, [P, P, S, I, P, P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -283,4 +288,109 @@ def rowdot_f32_subset(kind: str, data, x, cand, scale=None):
     sc = _c(scale, np.float32) if scale is not None else None
     out = np.empty(len(cand), np.float32)
     lib.fro_rowdot_f32_subset(code, _p(data), _p(sc), rows, d, _p(x), _p(cand), len(cand), _p(out))
+    return out
+
+
+# ---- GPT-2 with a KV cache (src/composition.rs) ----
+def read_bundle(stem: str):
+    """(manifest, {name: array}) of a fieldrun bundle, read with numpy from
+    the manifest and a memory map of the blob (FORMAT.md v1): f32 / f16 /
+    i8 / rowi8 arrays in their stored type and shape, i4 / q4a as packed
+    uint8 rows.  Test-side: independent of the library's reader."""
+    import json
+    m = json.load(open(stem + ".fieldrun.json"))
+    blob = np.memmap(stem + ".fieldrun.bin", np.uint8, "r")
+    out = {}
+    for a in m["arrays"]:
+        dt = {"f32": np.float32, "f16": np.float16, "i8": np.int8, "rowi8": np.int8}.get(a.get("dtype", "f32"), np.uint8)
+        raw = blob[a["offset"]:a["offset"] + a["bytes"]]
+        v = np.frombuffer(raw, dt)
+        out[a["name"]] = v.reshape(a["shape"]) if dt is not np.uint8 else v.reshape(a["shape"][0], -1)
+    return m, out
+
+
+class _Gpt2W(C.Structure):
+    _fields_ = [("n_layer", C.c_size_t), ("n_head", C.c_size_t), ("d", C.c_size_t), ("n_pos", C.c_size_t),
+                ("vocab", C.c_size_t), ("wte", C.c_void_p), ("wpe", C.c_void_p), ("ln_f_g", C.c_void_p),
+                ("ln_f_b", C.c_void_p), ("ln_g", C.c_void_p), ("ln_b", C.c_void_p), ("wt", C.c_void_p),
+                ("scale", C.c_void_p), ("bias", C.c_void_p)]
+
+
+class Gpt2:
+    """The oracle's GPT-2 over a bundle's arrays (Gpt2::new,
+    composition.rs:52-56: config [n_layer, n_head, d, n_pos, vocab]).  f16
+    vectors are upcast exactly; each int8 linear is stored transposed to the
+    (N, K) order Bundle::load keeps (src/bundle.rs:345-355)."""
+
+    def __init__(self, manifest, arrs, nthreads: int = 8):
+        L, H, d, npos, vocab = (int(c) for c in manifest["config"][:5])
+        f32 = lambda n: np.ascontiguousarray(arrs[n], np.float32)
+        self.keep = []
+
+        def ptrs(lst):
+            self.keep.extend(lst)
+            arr = (C.c_void_p * max(len(lst), 1))(*[a.ctypes.data for a in lst])
+            self.keep.append(arr)
+            return C.cast(arr, C.c_void_p)
+
+        self.wte = np.ascontiguousarray(arrs["wte"]).view(np.uint16)
+        self.wpe, self.lnfg, self.lnfb = f32("wpe"), f32("ln_f.weight"), f32("ln_f.bias")
+        lg, lb, wt, sc, bi = [], [], [], [], []
+        for l in range(L):
+            for ln in ("ln_1", "ln_2"):
+                lg.append(f32(f"h{l}.{ln}.weight"))
+                lb.append(f32(f"h{l}.{ln}.bias"))
+            for name in ("attn.c_attn", "attn.c_proj", "mlp.c_fc", "mlp.c_proj"):
+                w = f"h{l}.{name}.weight"
+                wt.append(np.ascontiguousarray(arrs[w].T))
+                sc.append(f32(w + "__scale"))
+                bi.append(f32(f"h{l}.{name}.bias"))
+        self.s = _Gpt2W(L, H, d, npos, vocab, self.wte.ctypes.data, self.wpe.ctypes.data,
+                        self.lnfg.ctypes.data, self.lnfb.ctypes.data, ptrs(lg), ptrs(lb), ptrs(wt),
+                        ptrs(sc), ptrs(bi))
+        self.vocab, self.nthreads = vocab, nthreads
+
+    def generate(self, prompt, n_new: int, kv_int8: bool = False, with_logits: bool = False):
+        prompt = _c(prompt, np.int64)
+        out = np.empty(n_new, np.int64)
+        lg = np.empty((n_new, self.vocab), np.float32) if with_logits else None
+        rc = lib.fro_gpt2_generate(C.byref(self.s), _p(prompt), len(prompt), n_new, int(kv_int8),
+                                   self.nthreads, _p(out), _p(lg))
+        if rc == 3:
+            raise OracleNaN("NaN in activations or logits")
+        if rc:
+            raise IndexError("token or position beyond the bundle's tables")
+        return (out, lg) if with_logits else out
+
+    def predict(self, ids, with_logits: bool = False):
+        ids = _c(ids, np.int64)
+        tok = np.zeros(1, np.int64)
+        lg = np.empty(self.vocab, np.float32) if with_logits else None
+        rc = lib.fro_gpt2_predict(C.byref(self.s), _p(ids), len(ids), self.nthreads, _p(tok), _p(lg))
+        if rc == 3:
+            raise OracleNaN("NaN in activations or logits")
+        if rc:
+            raise IndexError("token or position beyond the bundle's tables")
+        return (int(tok[0]), lg) if with_logits else int(tok[0])
+
+
+def nd_sum(x) -> float:
+    x = _c(x, np.float32)
+    return float(lib.fro_nd_sum(_p(x), x.size))
+
+
+def layernorm(x, g, b):
+    x = _c(x, np.float32)
+    x2 = x.reshape(-1, x.shape[-1])
+    out = np.empty_like(x2)
+    lib.fro_layernorm(_p(x2), x2.shape[0], x2.shape[1], _p(_c(g, np.float32)), _p(_c(b, np.float32)), _p(out))
+    return out.reshape(x.shape)
+
+
+def libm_f32(fn: str, x) -> np.ndarray:
+    """The system libm's expf / expm1f / tanhf: what the reference's f32 math
+    calls."""
+    x = _c(x, np.float32)
+    out = np.empty_like(x)
+    lib.fro_libm_f32({"expf": 0, "expm1f": 1, "tanhf": 2}[fn], _p(x), x.size, _p(out))
     return out

@@ -602,3 +602,271 @@ void fro_rowdot_f32_subset(int dtype, const void* data, const float* scale,
                                                 : row_dot(dtype, data, scale, (size_t)c, d, x, 0);
     }
 }
+
+/* ------------------------------------------------------------------------ */
+/* GPT-2 greedy decode with a KV cache: Gpt2::generate (src/composition.rs:  */
+/* 317-341; int8 cache 251-270), forward_block (175-209), forward_block_q    */
+/* (214-249), head_argmax (296-300), layernorm / gelu / softmax_rows (20-50).*/
+/* ------------------------------------------------------------------------ */
+
+/* ndarray 0.16.1 ArrayBase::sum over a contiguous row: numeric_util::
+ * unrolled_fold (eight partial sums p0..p7 from 0, combined as acc += p0+p4,
+ * p1+p5, p2+p6, p3+p7, then the < 8 tail in order).  layernorm's mean
+ * (composition.rs:24) goes through it. */
+float fro_nd_sum(const float* x, size_t n) {
+    float p[8] = {0, 0, 0, 0, 0, 0, 0, 0}, acc = 0.0f;
+    size_t i = 0;
+    for (; i + 8 <= n; i += 8)
+        for (int q = 0; q < 8; q++) p[q] = p[q] + x[i + q];
+    acc = acc + (p[0] + p[4]);
+    acc = acc + (p[1] + p[5]);
+    acc = acc + (p[2] + p[6]);
+    acc = acc + (p[3] + p[7]);
+    for (; i < n; i++) acc = acc + x[i];
+    return acc;
+}
+
+/* layernorm (composition.rs:20-33): eps 1e-5, mean by nd_sum, variance a
+ * fold from -0.0 (Iterator::sum), (v - mu) * inv * g + b with no FMA. */
+void fro_layernorm(const float* x, size_t m, size_t d, const float* g, const float* b, float* out) {
+    const float n = (float)d;
+    for (size_t r = 0; r < m; r++) {
+        const float* row = x + r * d;
+        const float mu = fro_nd_sum(row, d) / n;
+        float var = -0.0f;
+        for (size_t i = 0; i < d; i++) var = var + (row[i] - mu) * (row[i] - mu);
+        var = var / n;
+        const float inv = 1.0f / sqrtf(var + 1e-5f);
+        for (size_t i = 0; i < d; i++) out[r * d + i] = (row[i] - mu) * inv * g[i] + b[i];
+    }
+}
+
+/* softmax_rows (composition.rs:40-50) on one row. */
+static void softmax_row(float* v, size_t n) {
+    float mx = -INFINITY;
+    for (size_t j = 0; j < n; j++) mx = fmaxf(mx, v[j]);
+    float s = 0.0f;
+    for (size_t j = 0; j < n; j++) { v[j] = expf(v[j] - mx); s = s + v[j]; }
+    for (size_t j = 0; j < n; j++) v[j] = v[j] / s;
+}
+
+typedef struct {
+    const fro_gpt2_t* g;
+    int nthreads;
+    int kv8;
+    size_t total;
+    float** kc; float** vc;          /* f32 cache (total, d) per layer */
+    int8_t** kq; int8_t** vq;        /* int8 cache (total, d) per layer */
+    float** ks; float** vs;          /* int8 cache scales (total, n_head) */
+} g2_run;
+
+/* q8 of forward_block_q (composition.rs:220): (v / sc).round() clamped. */
+static int8_t kv_q8(float v, float sc) {
+    float q = roundf(v / sc);
+    if (q != q) return 0; /* Rust's `as i8` saturates NaN to 0 */
+    if (q < -127.0f) q = -127.0f;
+    if (q > 127.0f) q = 127.0f;
+    return (int8_t)q;
+}
+
+/* forward_block / forward_block_q: m rows at absolute positions cur..cur+m
+ * through every layer; x (m, d) in, the pre-final-LN hidden states out (in
+ * place).  The attention products are matrixmultiply sgemms in the
+ * reference; here each is a sequential-k FMA chain (fro_sgemm's order). */
+static int g2_block(g2_run* R, float* x, size_t m, size_t cur) {
+    const fro_gpt2_t* g = R->g;
+    const size_t d = g->d, H = g->n_head, hd = d / H, klen = cur + m;
+    float* a = (float*)malloc(nz(m * d * 4));
+    float* qkv = (float*)malloc(nz(m * 3 * d * 4));
+    float* att = (float*)malloc(nz(m * d * 4));
+    float* y = (float*)malloc(nz(m * 4 * d * 4));
+    float* hm = (float*)malloc(nz(m * 4 * d * 4));
+    float* sc = (float*)malloc(nz(m * klen * 4));
+    float* kh = (float*)malloc(nz(klen * hd * 4));
+    float* vh = (float*)malloc(nz(klen * hd * 4));
+    const float rs = sqrtf((float)hd);
+    int rc = FRO_OK;
+    for (size_t l = 0; l < g->n_layer && !rc; l++) {
+        const int8_t* const* W = g->wt + 4 * l;
+        const float* const* S = g->scale + 4 * l;
+        const float* const* B = g->bias + 4 * l;
+        fro_layernorm(x, m, d, g->ln_g[2 * l], g->ln_b[2 * l], a);
+        if ((rc = fro_mm_i8_mt(a, m, d, W[0], S[0], 3 * d, qkv, R->nthreads))) break;
+        for (size_t i = 0; i < m; i++)
+            for (size_t c = 0; c < 3 * d; c++) qkv[i * 3 * d + c] = qkv[i * 3 * d + c] + B[0][c];
+        for (size_t i = 0; i < m; i++) {  /* append K/V (quantised per head for int8) */
+            const size_t pos = cur + i;
+            const float* kr = qkv + i * 3 * d + d;
+            const float* vr = qkv + i * 3 * d + 2 * d;
+            if (!R->kv8) {
+                memcpy(R->kc[l] + pos * d, kr, d * 4);
+                memcpy(R->vc[l] + pos * d, vr, d * 4);
+            } else {
+                for (size_t h = 0; h < H; h++) {
+                    float mk = 0.0f, mv = 0.0f;
+                    for (size_t c = 0; c < hd; c++) {
+                        mk = fmaxf(mk, fabsf(kr[h * hd + c]));
+                        mv = fmaxf(mv, fabsf(vr[h * hd + c]));
+                    }
+                    float sck = mk / 127.0f, scv = mv / 127.0f;
+                    if (!(sck > 0.0f)) sck = 1.0f;
+                    if (!(scv > 0.0f)) scv = 1.0f;
+                    R->ks[l][pos * H + h] = sck;
+                    R->vs[l][pos * H + h] = scv;
+                    for (size_t c = 0; c < hd; c++) {
+                        R->kq[l][pos * d + h * hd + c] = kv_q8(kr[h * hd + c], sck);
+                        R->vq[l][pos * d + h * hd + c] = kv_q8(vr[h * hd + c], scv);
+                    }
+                }
+            }
+        }
+        for (size_t h = 0; h < H; h++) {
+            for (size_t j = 0; j < klen; j++)
+                for (size_t c = 0; c < hd; c++) {
+                    if (!R->kv8) {
+                        kh[j * hd + c] = R->kc[l][j * d + h * hd + c];
+                        vh[j * hd + c] = R->vc[l][j * d + h * hd + c];
+                    } else {
+                        kh[j * hd + c] = (float)R->kq[l][j * d + h * hd + c] * R->ks[l][j * H + h];
+                        vh[j * hd + c] = (float)R->vq[l][j * d + h * hd + c] * R->vs[l][j * H + h];
+                    }
+                }
+            for (size_t i = 0; i < m; i++) {
+                const float* q = qkv + i * 3 * d + h * hd;
+                float* s = sc + i * klen;
+                for (size_t j = 0; j < klen; j++) {
+                    float acc = 0.0f;
+                    for (size_t c = 0; c < hd; c++) acc = fmaf(q[c], kh[j * hd + c], acc);
+                    s[j] = acc / rs;
+                }
+                for (size_t j = cur + i + 1; j < klen; j++) s[j] = -1e10f;  /* causal mask */
+                softmax_row(s, klen);
+                for (size_t c = 0; c < hd; c++) {
+                    float acc = 0.0f;
+                    for (size_t j = 0; j < klen; j++) acc = fmaf(s[j], vh[j * hd + c], acc);
+                    att[i * d + h * hd + c] = acc;
+                }
+            }
+        }
+        if ((rc = fro_mm_i8_mt(att, m, d, W[1], S[1], d, y, R->nthreads))) break;
+        for (size_t i = 0; i < m * d; i++) x[i] = x[i] + (y[i] + B[1][i % d]);
+        fro_layernorm(x, m, d, g->ln_g[2 * l + 1], g->ln_b[2 * l + 1], a);
+        if ((rc = fro_mm_i8_mt(a, m, d, W[2], S[2], 4 * d, hm, R->nthreads))) break;
+        for (size_t i = 0; i < m * 4 * d; i++) hm[i] = fro_gelu_tanh(hm[i] + B[2][i % (4 * d)]);
+        if ((rc = fro_mm_i8_mt(hm, m, 4 * d, W[3], S[3], d, y, R->nthreads))) break;
+        for (size_t i = 0; i < m * d; i++) x[i] = x[i] + (y[i] + B[3][i % d]);
+    }
+    free(a); free(qkv); free(att); free(y); free(hm); free(sc); free(kh); free(vh);
+    return rc;
+}
+
+typedef struct { const fro_gpt2_t* g; const float* x; float* out; size_t lo, hi; } g2_head_job;
+static void* g2_head_worker(void* p) {
+    g2_head_job* J = (g2_head_job*)p;
+    fro_rowdot_f32(FRO_DT_F16, J->g->wte + J->lo * J->g->d, NULL, J->hi - J->lo, J->g->d, J->x, J->out + J->lo);
+    return NULL;
+}
+
+/* head_argmax (composition.rs:296-300): ln_f of the last row, the tied
+ * unembed rowdot_f32("wte") over f16 rows, then Iterator::max_by with
+ * partial_cmp (the last of equal maxima; a NaN panics -> FRO_ERR_NAN). */
+static int g2_head(g2_run* R, const float* xlast, float* logits, int64_t* tok) {
+    const fro_gpt2_t* g = R->g;
+    float* xf = (float*)malloc(nz(g->d * 4));
+    fro_layernorm(xlast, 1, g->d, g->ln_f_g, g->ln_f_b, xf);
+    int nt = R->nthreads < 1 ? 1 : (R->nthreads > 64 ? 64 : R->nthreads);
+    pthread_t th[64];
+    g2_head_job jobs[64];
+    for (int w = 0; w < nt; w++) {
+        jobs[w] = (g2_head_job){g, xf, logits, g->vocab * (size_t)w / nt, g->vocab * (size_t)(w + 1) / nt};
+        pthread_create(&th[w], NULL, g2_head_worker, &jobs[w]);
+    }
+    for (int w = 0; w < nt; w++) pthread_join(th[w], NULL);
+    free(xf);
+    size_t best = 0;
+    for (size_t r = 0; r < g->vocab; r++) {
+        if (isnan(logits[r])) return FRO_ERR_NAN;
+        if (logits[r] >= logits[best]) best = r;
+    }
+    *tok = (int64_t)best;
+    return FRO_OK;
+}
+
+/* rows_f32("wte", ids) + rows_f32("wpe", pos) (bundle.rs:936-955). */
+static int g2_embed(const fro_gpt2_t* g, const int64_t* ids, size_t m, size_t pos0, float* x) {
+    for (size_t t = 0; t < m; t++) {
+        if (ids[t] < 0 || (size_t)ids[t] >= g->vocab || pos0 + t >= g->n_pos) return FRO_ERR_ARG;
+        for (size_t c = 0; c < g->d; c++)
+            x[t * g->d + c] = fro_f16_to_f32(g->wte[(size_t)ids[t] * g->d + c]) + g->wpe[(pos0 + t) * g->d + c];
+    }
+    return FRO_OK;
+}
+
+int fro_gpt2_generate(const fro_gpt2_t* g, const int64_t* prompt, size_t n_prompt, size_t n_new, int kv_int8,
+                      int nthreads, int64_t* out, float* logits) {
+    if (!n_prompt || !n_new) return FRO_ERR_ARG;
+    const size_t d = g->d, L = g->n_layer, total = n_prompt + n_new;
+    g2_run R = {g, nthreads, kv_int8, total, NULL, NULL, NULL, NULL, NULL, NULL};
+    R.kc = (float**)calloc(L, sizeof(float*)); R.vc = (float**)calloc(L, sizeof(float*));
+    R.kq = (int8_t**)calloc(L, sizeof(int8_t*)); R.vq = (int8_t**)calloc(L, sizeof(int8_t*));
+    R.ks = (float**)calloc(L, sizeof(float*)); R.vs = (float**)calloc(L, sizeof(float*));
+    for (size_t l = 0; l < L; l++) {
+        if (!kv_int8) {
+            R.kc[l] = (float*)calloc(total * d, 4); R.vc[l] = (float*)calloc(total * d, 4);
+        } else {
+            R.kq[l] = (int8_t*)calloc(total * d, 1); R.vq[l] = (int8_t*)calloc(total * d, 1);
+            R.ks[l] = (float*)calloc(total * g->n_head, 4); R.vs[l] = (float*)calloc(total * g->n_head, 4);
+        }
+    }
+    float* x = (float*)malloc(nz(n_prompt * d * 4));
+    float* lg = (float*)malloc(nz(g->vocab * 4));
+    int64_t next = 0;
+    int rc = g2_embed(g, prompt, n_prompt, 0, x);
+    if (!rc) rc = g2_block(&R, x, n_prompt, 0);
+    if (!rc) rc = g2_head(&R, x + (n_prompt - 1) * d, lg, &next);
+    size_t pos = n_prompt;
+    for (size_t s = 0; !rc; s++) {
+        out[s] = next;
+        if (logits) memcpy(logits + s * g->vocab, lg, g->vocab * 4);
+        if (s + 1 == n_new) break;
+        rc = g2_embed(g, &next, 1, pos, x);
+        if (!rc) rc = g2_block(&R, x, 1, pos);
+        if (!rc) rc = g2_head(&R, x, lg, &next);
+        pos++;
+    }
+    for (size_t l = 0; l < L; l++) {
+        free(R.kc[l]); free(R.vc[l]); free(R.kq[l]); free(R.vq[l]); free(R.ks[l]); free(R.vs[l]);
+    }
+    free(R.kc); free(R.vc); free(R.kq); free(R.vq); free(R.ks); free(R.vs);
+    free(x); free(lg);
+    return rc;
+}
+
+/* Model::predict for Gpt2 (composition.rs:304-308): the whole sequence,
+ * no cache, the last row's argmax.  hidden() (61-96) is forward_block at
+ * cur = 0 over the full sequence (the cache it fills is unused). */
+int fro_gpt2_predict(const fro_gpt2_t* g, const int64_t* ids, size_t n, int nthreads, int64_t* tok, float* logits) {
+    if (!n) return FRO_ERR_ARG;
+    int64_t t = 0;
+    float* lg = logits ? logits : (float*)malloc(nz(g->vocab * 4));
+    const size_t d = g->d, L = g->n_layer;
+    g2_run R = {g, nthreads, 0, n, NULL, NULL, NULL, NULL, NULL, NULL};
+    R.kc = (float**)calloc(L, sizeof(float*)); R.vc = (float**)calloc(L, sizeof(float*));
+    for (size_t l = 0; l < L; l++) { R.kc[l] = (float*)calloc(n * d, 4); R.vc[l] = (float*)calloc(n * d, 4); }
+    float* x = (float*)malloc(nz(n * d * 4));
+    int rc = g2_embed(g, ids, n, 0, x);
+    if (!rc) rc = g2_block(&R, x, n, 0);
+    if (!rc) rc = g2_head(&R, x + (n - 1) * d, lg, &t);
+    *tok = t;
+    for (size_t l = 0; l < L; l++) { free(R.kc[l]); free(R.vc[l]); }
+    free(R.kc); free(R.vc); free(x);
+    if (!logits) free(lg);
+    return rc;
+}
+
+/* The libm calls of the reference's f32 math: Rust's f32::exp reaches the
+ * platform expf (llvm.exp.f32 lowers to the libcall), f32::tanh calls tanhf
+ * (std's cmath binding), both from the system libm. */
+void fro_libm_f32(int fn, const float* x, size_t n, float* out) {
+    for (size_t i = 0; i < n; i++) out[i] = fn == 0 ? expf(x[i]) : (fn == 1 ? expm1f(x[i]) : tanhf(x[i]));
+}

@@ -30,6 +30,14 @@
  *                                     is matrixmultiply's): tolerance parity
  *   fro_moe_route / fro_moe           closed-form softmax + brute-force
  *                                     stable sort, f64 combine bound
+ *   fro_nd_sum / fro_layernorm        hand-derived order case (the eight-lane
+ *                                     fold vs a sequential sum), exact-integer
+ *                                     rows vs f64, constant rows
+ *   fro_gpt2_generate / _predict      an independent f64 numpy forward (tolerance),
+ *                                     predict(prefix) == the cached decode step
+ *                                     bit for bit (composition.rs:313-316 says the
+ *                                     cache is exact); matrixmultiply's order for
+ *                                     the attention products is parity unpinned
  *   fro_rowdot_f32 / _subset          exact small-integer dots (any order),
  *                                     f64 bound, and order-revealing cases
  *                                     whose f32 result follows by hand from
@@ -49,7 +57,9 @@ extern "C" {
 #define FRO_OUTLIER_T 32
 
 #define FRO_OK 0
+#define FRO_ERR_ARG 1 /* an index the reference would panic on          */
 #define FRO_ERR_NAN 3 /* reference panics in partial_cmp().unwrap() */
+#define FRO_DT_F16 4
 
 /* IEEE binary16 <-> binary32 (half 2.7.1 semantics: RNE, exact upcast). */
 float fro_f16_to_f32(uint16_t h);
@@ -131,6 +141,40 @@ void fro_rowdot_f32(int dtype, const void* data, const float* scale, size_t rows
 void fro_rowdot_f32_subset(int dtype, const void* data, const float* scale,
                            size_t rows, size_t d, const float* x,
                            const int64_t* cand, size_t ncand, float* out);
+
+/* GPT-2 with a KV cache (src/composition.rs).  Weights as the bundle holds
+ * them after Bundle::load: wte f16 bits (vocab, d), wpe f32 (n_pos, d); per
+ * layer l: ln_g/ln_b[2l] = ln_1, [2l+1] = ln_2 (f32 [d]); wt/scale/bias
+ * [4l + 0..3] = attn.c_attn, attn.c_proj, mlp.c_fc, mlp.c_proj with wt the
+ * (N, K) transposed int8 store, scale and bias f32 [N]. */
+typedef struct {
+    size_t n_layer, n_head, d, n_pos, vocab;
+    const uint16_t* wte;
+    const float* wpe;
+    const float* ln_f_g;
+    const float* ln_f_b;
+    const float* const* ln_g;
+    const float* const* ln_b;
+    const int8_t* const* wt;
+    const float* const* scale;
+    const float* const* bias;
+} fro_gpt2_t;
+
+/* The system libm's expf (fn 0), expm1f (1), tanhf (2) over n values. */
+void fro_libm_f32(int fn, const float* x, size_t n, float* out);
+/* ndarray 0.16.1 ArrayBase::sum of a contiguous f32 row (unrolled_fold). */
+float fro_nd_sum(const float* x, size_t n);
+/* layernorm (composition.rs:20-33) over m rows of d. */
+void fro_layernorm(const float* x, size_t m, size_t d, const float* g, const float* b, float* out);
+/* Gpt2::generate (composition.rs:317-341; kv_int8: 251-270): n_new greedy
+ * tokens after the prompt; logits (n_new, vocab) nullable: the logits each
+ * token was chosen from.  FRO_ERR_ARG for a token / position beyond the
+ * tables (the reference's index panic), FRO_ERR_NAN for NaN activations or
+ * logits. */
+int fro_gpt2_generate(const fro_gpt2_t* g, const int64_t* prompt, size_t n_prompt, size_t n_new, int kv_int8,
+                      int nthreads, int64_t* out, float* logits);
+/* Model::predict (composition.rs:304-308). */
+int fro_gpt2_predict(const fro_gpt2_t* g, const int64_t* ids, size_t n, int nthreads, int64_t* tok, float* logits);
 
 #ifdef __cplusplus
 }
