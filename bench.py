@@ -16,7 +16,10 @@ fused into the GEMV); `roofline` is that kernel at the step's dominant shape
 f32 activation row, f32 outputs) over its average launch time on the
 library's stream.  Also reported (in "detail"): the GEMV kernel alone on
 pre-quantised input, the M=2048 MFMA-bound shapes in TOPS, the int4 decode
-GEMV on Gemma-2 shapes, and the config-4 MoE layer.  The CPU baseline is the
+GEMV on Gemma-2 shapes, the unembed row dot, the config-4 MoE layer, and
+config 0 end to end: GPT-2 small greedy decode (tok/s, f32 and int8 KV
+caches) with the oracle's CPU rate and token check beside it.  The CPU
+baseline is the
 oracle's restatement of the reference's scalar int8 path (the
 `_scalar_i8_bench` build) on the host's cores, on a bounded sample.
 """
@@ -103,6 +106,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-detail", action="store_true")
+    ap.add_argument("--no-graphs", action="store_true",
+                    help="GPT-2 decode steps launched eagerly rather than from a captured graph (the same "
+                         "kernels; rocprofv3's kernel trace does not survive graph capture on this image)")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="only the counter-collection workload (run under rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -320,6 +326,52 @@ def main():
             detail["moe_qwen3_layer"][f"T{T}"] = {"us": round(us, 1),
                                                   "flops_TF": round(2 * T * topk * 3 * d * mi / (us * 1e-6) / 1e12, 2)}
         bank.free()
+        # ---------------- GPT-2 greedy decode (config 0) ----------------
+        # GPT-2 small int8, random init, 32-token seeded prompt, 128 greedy
+        # tokens (Gpt2::generate), whole call timed on the host clock; the
+        # decode rate excludes the prefill (generate(128) - generate(1))
+        import tempfile
+        detail["gpt2_decode"] = {}
+        with tempfile.TemporaryDirectory() as tmp:
+            stem = os.path.join(tmp, "gpt2")
+            synth.write_gpt2_bundle(stem, 1234)
+            b = fa.Bundle(stem, ctx)
+            prompt = synth.gpt2_prompt(32, 50257, 7)
+            for kv8 in (False, True):
+                g = fa.Gpt2(b, kv8)
+                g.set_graphs(not args.no_graphs)
+                g.generate(prompt, 128)
+                runs = {}
+                for n_new in (1, 128):
+                    ts = []
+                    for _ in range(3):
+                        t0 = time.perf_counter()
+                        g.generate(prompt, n_new)
+                        ts.append(time.perf_counter() - t0)
+                    runs[n_new] = sorted(ts)[1]
+                dec_ms = (runs[128] - runs[1]) / 127 * 1e3
+                detail["gpt2_decode"]["kv_int8" if kv8 else "kv_f32"] = {
+                    "tok_s": round(128 / runs[128], 1), "decode_ms_per_token": round(dec_ms, 4),
+                    "decode_tok_s": round(1e3 / dec_ms, 1), "prefill_plus_first_ms": round(runs[1] * 1e3, 3)}
+                log(f"gpt2 decode kv_int8={kv8}: {detail['gpt2_decode']['kv_int8' if kv8 else 'kv_f32']}")
+                g.free()
+            if not args.no_cpu:
+                import oracle  # the reference's GPT-2 restated in C (the CPU rate beside the device's)
+
+                m_, arrs = oracle.read_bundle(stem)
+                threads = min(os.cpu_count() or 1, 16)
+                ref = oracle.Gpt2(m_, arrs, nthreads=threads)
+                g = fa.Gpt2(b)
+                t0 = time.perf_counter()
+                rt = ref.generate(prompt, 16)
+                el = time.perf_counter() - t0
+                same = bool(np.array_equal(rt, g.generate(prompt, 16)))
+                detail["gpt2_decode"]["cpu_oracle"] = {"tok_s": round(16 / el, 2), "threads": threads,
+                                                       "sample": "16 tokens after the 32-token prompt",
+                                                       "tokens_identical": same}
+                log(f"gpt2 oracle: {detail['gpt2_decode']['cpu_oracle']}")
+                g.free()
+            b.close()
 
     # ---------------- CPU baseline (the oracle's scalar restatement) ----------------
     cpu = None

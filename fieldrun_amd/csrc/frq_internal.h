@@ -197,6 +197,11 @@ int last_code();
 size_t row_pitch(int dtype, size_t d);
 hipError_t launch_rowdot(const Weight& w, const float* x, const int64_t* cand, size_t nout, float* out,
                          hipStream_t s);
+// The full-table form that also folds the argmax (the last index of the
+// largest value) into *best as (order-preserving value bits << 32 | row);
+// *best must start at 0.  A NaN output sets *err.
+hipError_t launch_rowdot_argmax(const Weight& w, const float* x, float* out, unsigned long long* best, int* err,
+                                hipStream_t s);
 // int4 linear (any m).
 hipError_t launch_i4(const Weight& w, size_t m, const float* a, float* out,
                      float* wsf, unsigned* tickets, hipStream_t s);

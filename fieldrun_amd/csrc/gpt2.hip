@@ -74,19 +74,83 @@ __global__ __launch_bounds__(NT) void embed_kernel(const uint8_t* __restrict__ w
     for (int c = threadIdx.x; c < d; c += NT) x[(size_t)t * d + c] = h2f(row[c]) + pe[c];
 }
 
+// acc + p[0] + p[1] + ... + p[n-1] in index order, in the calling lane,
+// over LDS (p 16-byte aligned): loads run one 32-value batch ahead of the
+// adds (unconditional, the index clamped to the last batch) so the chain
+// waits on the adds, not on LDS latency.
+__device__ float seq_sum(const float* p, int n, float acc) {
+    constexpr int B = 8;  // float4 per batch
+    const int nb = n / (4 * B);
+    const float4* p4 = reinterpret_cast<const float4*>(p);
+    float4 b0[B], b1[B];
+    auto ld = [&](float4 (&b)[B], int k) {
+#pragma unroll
+        for (int u = 0; u < B; ++u) b[u] = p4[k * B + u];
+    };
+    auto add = [&](const float4 (&b)[B]) {
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+            acc = acc + b[u].x;
+            acc = acc + b[u].y;
+            acc = acc + b[u].z;
+            acc = acc + b[u].w;
+        }
+    };
+    if (nb > 0) {
+        ld(b0, 0);
+        ld(b1, min(1, nb - 1));
+        for (int k = 0; k < nb; k += 2) {
+            add(b0);
+            ld(b0, min(k + 2, nb - 1));
+            if (k + 1 < nb) add(b1);
+            ld(b1, min(k + 3, nb - 1));
+        }
+    }
+    for (int i = nb * 4 * B; i < n; ++i) acc = acc + p[i];
+    return acc;
+}
+// The same over p[0], p[8], p[16], ... (n values): one of ndarray's eight
+// partial sums.
+__device__ float seq_sum8(const float* p, int n, float acc) {
+    constexpr int B = 16;
+    const int nb = n / B;
+    float b0[B], b1[B];
+    auto ld = [&](float (&b)[B], int k) {
+#pragma unroll
+        for (int u = 0; u < B; ++u) b[u] = p[(k * B + u) * 8];
+    };
+    auto add = [&](const float (&b)[B]) {
+#pragma unroll
+        for (int u = 0; u < B; ++u) acc = acc + b[u];
+    };
+    if (nb > 0) {
+        ld(b0, 0);
+        ld(b1, min(1, nb - 1));
+        for (int k = 0; k < nb; k += 2) {
+            add(b0);
+            ld(b0, min(k + 2, nb - 1));
+            if (k + 1 < nb) add(b1);
+            ld(b1, min(k + 3, nb - 1));
+        }
+    }
+    for (int i = nb * B; i < n; ++i) acc = acc + p[i * 8];
+    return acc;
+}
+
 // x[r] = x[r] + (y[r] + bias) (when y is set), then out[r] = layernorm(x[r])
 // for rows row0 .. row0 + gridDim.x, in layernorm's order (composition.rs:
 // 20-33): mu = row.sum() / n with ndarray 0.16's sum (eight partial sums
 // p0..p7 over the leading multiple of 8, combined acc += p0+p4, p1+p5,
 // p2+p6, p3+p7 from 0, then the tail in order), var = the fold from -0.0 of
 // (v - mu)^2 in index order / n, inv = 1 / sqrt(var + 1e-5), out =
-// (v - mu) * inv * g + b.  The chains run in one lane each; the row and the
-// squares sit in LDS (2d floats).
+// (v - mu) * inv * g + b.  The chains run in one lane each (eight for the
+// partial sums); the row and the squares sit in LDS (2d floats).
 __global__ __launch_bounds__(NT) void resid_ln_kernel(float* __restrict__ x, const float* __restrict__ y,
                                                       const float* __restrict__ bias, const float* __restrict__ g,
                                                       const float* __restrict__ b, float* __restrict__ out, int d,
                                                       int row0) {
-    extern __shared__ float xs[];  // row (d), squares (d)
+    extern __shared__ float4 lds4[];
+    float* xs = reinterpret_cast<float*>(lds4);  // row (d), squares (d)
     __shared__ float part[8], stat[2];
     float* sq = xs + d;
     const size_t r = (size_t)(row0 + blockIdx.x) * d;
@@ -100,11 +164,7 @@ __global__ __launch_bounds__(NT) void resid_ln_kernel(float* __restrict__ x, con
     }
     __syncthreads();
     const int n8 = d & ~7;
-    if (threadIdx.x < 8) {
-        float p = 0.0f;
-        for (int i = threadIdx.x; i < n8; i += 8) p = p + xs[i];
-        part[threadIdx.x] = p;
-    }
+    if (threadIdx.x < 8) part[threadIdx.x] = seq_sum8(xs + threadIdx.x, n8 / 8, 0.0f);
     __syncthreads();
     if (threadIdx.x == 0) {
         float acc = 0.0f;
@@ -119,19 +179,7 @@ __global__ __launch_bounds__(NT) void resid_ln_kernel(float* __restrict__ x, con
     const float mu = stat[0];
     for (int c = threadIdx.x; c < d; c += NT) sq[c] = (xs[c] - mu) * (xs[c] - mu);
     __syncthreads();
-    if (threadIdx.x == 0) {
-        float v = -0.0f;
-        int i = 0;
-        for (; i + 4 <= d; i += 4) {
-            const float4 q = *reinterpret_cast<const float4*>(sq + i);
-            v = v + q.x;
-            v = v + q.y;
-            v = v + q.z;
-            v = v + q.w;
-        }
-        for (; i < d; ++i) v = v + sq[i];
-        stat[1] = v / (float)d;
-    }
+    if (threadIdx.x == 0) stat[1] = seq_sum(sq, d, -0.0f) / (float)d;
     __syncthreads();
     const float inv = 1.0f / sqrtf(stat[1] + 1e-5f);
     for (int c = threadIdx.x; c < d; c += NT) out[r + c] = (xs[c] - mu) * inv * g[c] + b[c];
@@ -182,26 +230,63 @@ __global__ __launch_bounds__(NT) void qkv_kernel(float* __restrict__ qkv, const 
 // Causal attention of row i (position cur + i) and head h over cache rows
 // 0 .. cur + i (forward_block 189-201): s_j = (q . k_j) / sqrt(hd) as a
 // sequential FMA chain over the head dims (one thread per key), softmax
-// (max, expf, sum, divide), then out_c = sum_j p_j v_jc as a sequential FMA
-// chain over j (one lane per output dim).  Keys past cur + i carry the
-// reference's -1e10 mask: it joins the max, and its exp is exactly 0 (for
-// any max above -1e10 + 104), so those keys add nothing and are skipped.
-// LDS: hd + klen_max floats.
-template <bool KV8>
-__global__ __launch_bounds__(NT) void attn_kernel(const float* __restrict__ qkv, int d, int H, int hd,
-                                                  const int* __restrict__ curp, const float* __restrict__ kc,
-                                                  const float* __restrict__ vc, const int8_t* __restrict__ kq,
-                                                  const int8_t* __restrict__ vq, const float* __restrict__ ks,
-                                                  const float* __restrict__ vs, float rs, float* __restrict__ att) {
-    extern __shared__ float sh[];
+// (max, expf, the sum in key order, divide), then out_c = sum_j p_j v_jc as
+// a sequential FMA chain over j (one lane per output dim, its loads a
+// 16-key batch ahead).  Keys past cur + i carry the reference's -1e10
+// mask: it joins the max, and its exp is exactly 0 (for any max above
+// -1e10 + 104), so those keys add nothing and are skipped.
+// FUSED (decode, one row): the block also adds the bias to its head's q, k,
+// v and appends k, v to cache row cur (as qkv_kernel), before attending.
+// LDS: q (hd), p and the int8 value scales (pstride each).
+template <bool KV8, bool FUSED>
+__global__ __launch_bounds__(NT) void attn_kernel(const float* __restrict__ qkv, const float* __restrict__ bias,
+                                                  int d, int H, int hd, const int* __restrict__ curp,
+                                                  float* __restrict__ kc, float* __restrict__ vc,
+                                                  int8_t* __restrict__ kq, int8_t* __restrict__ vq,
+                                                  float* __restrict__ ks, float* __restrict__ vs, float rs,
+                                                  int pstride, float* __restrict__ att) {
+    extern __shared__ float4 lds4[];
+    float* q = reinterpret_cast<float*>(lds4);
+    float* p = q + ((hd + 3) & ~3);
+    float* sv = p + pstride;  // pstride >= max(klen_max, 2 hd), a multiple of 4
     __shared__ float red[4];
     const int h = blockIdx.x, i = blockIdx.y;
-    const int nk = *curp + i + 1;
-    float* q = sh;
-    float* p = sh + hd;
-    const float* qsrc = qkv + (size_t)i * 3 * d + (size_t)h * hd;
-    for (int c = threadIdx.x; c < hd; c += NT) q[c] = qsrc[c];
-    __syncthreads();
+    const int cur = *curp;
+    const int nk = cur + i + 1;
+    const float* row = qkv + (size_t)i * 3 * d + (size_t)h * hd;
+    if constexpr (FUSED) {
+        const size_t pos = (size_t)cur;
+        float* kv = p;  // the new k (hd) and v (hd), staged for the int8 scales
+        for (int t = threadIdx.x; t < 3 * hd; t += NT) {
+            const int part = t / hd, c = t - part * hd;
+            const size_t col = (size_t)part * d + (size_t)h * hd + c;
+            const float v = row[(size_t)part * d + c] + bias[col];
+            if (part == 0) q[c] = v;
+            else if constexpr (!KV8) (part == 1 ? kc : vc)[pos * d + (size_t)h * hd + c] = v;
+            else kv[(part - 1) * hd + c] = v;
+        }
+        if constexpr (KV8) {
+            __syncthreads();
+            const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+            if (wave < 2) {  // wave 0: k, wave 1: v (forward_block_q 224-235)
+                const float* src = kv + wave * hd;
+                float mx = 0.0f;
+                for (int c = lane; c < hd; c += 64) mx = fmaxf(mx, fabsf(src[c]));
+                mx = wave_max(mx);
+                float sc = mx / 127.0f;
+                if (!(sc > 0.0f)) sc = 1.0f;
+                int8_t* dq = (wave ? vq : kq) + pos * d + (size_t)h * hd;
+                for (int c = lane; c < hd; c += 64) {
+                    const float r = roundf(src[c] / sc);
+                    dq[c] = r != r ? (int8_t)0 : (int8_t)fminf(fmaxf(r, -127.0f), 127.0f);
+                }
+                if (lane == 0) (wave ? vs : ks)[pos * H + h] = sc;
+            }
+        }
+    } else {
+        for (int c = threadIdx.x; c < hd; c += NT) q[c] = row[c];
+    }
+    __syncthreads();  // q, and (FUSED) the new cache row, visible to the block
     float mx = -INFINITY;
     for (int j = threadIdx.x; j < nk; j += NT) {
         float acc = 0.0f;
@@ -217,6 +302,7 @@ __global__ __launch_bounds__(NT) void attn_kernel(const float* __restrict__ qkv,
         } else {
             const int8_t* kr = kq + (size_t)j * d + (size_t)h * hd;
             const float sk = ks[(size_t)j * H + h];
+            sv[j] = vs[(size_t)j * H + h];
             for (int c = 0; c < hd; c += 4) {
                 const char4 k4 = *reinterpret_cast<const char4*>(kr + c);
                 acc = __builtin_fmaf(q[c], (float)k4.x * sk, acc);
@@ -225,35 +311,54 @@ __global__ __launch_bounds__(NT) void attn_kernel(const float* __restrict__ qkv,
                 acc = __builtin_fmaf(q[c + 3], (float)k4.w * sk, acc);
             }
         }
-        const float s = acc / rs;
-        p[j] = s;
-        mx = fmaxf(mx, s);
+        const float sj = acc / rs;
+        p[j] = sj;
+        mx = fmaxf(mx, sj);
     }
     mx = block_max(mx, red);
-    if (nk < *curp + (int)gridDim.y) mx = fmaxf(mx, -1e10f);  // a masked entry joins the max
+    if (nk < cur + (int)gridDim.y) mx = fmaxf(mx, -1e10f);  // a masked entry joins the max
     for (int j = threadIdx.x; j < nk; j += NT) p[j] = libm::frq_expf(p[j] - mx);
     __syncthreads();
-    if (threadIdx.x == 0) {  // the sum in key order (masked exps are +0)
-        float sum = 0.0f;
-        for (int j = 0; j < nk; ++j) sum = sum + p[j];
-        red[0] = sum;
-    }
+    if (threadIdx.x == 0) red[0] = seq_sum(p, nk, 0.0f);  // masked exps are +0
     __syncthreads();
     const float sum = red[0];
     for (int j = threadIdx.x; j < nk; j += NT) p[j] = p[j] / sum;
     __syncthreads();
-    // one lane per output dim, the waves splitting the dims
+    // out_c: one lane per dim; the value loads (coalesced over the lanes)
+    // run one 16-key batch ahead of the chain
+    constexpr int B = 16;
     for (int c = threadIdx.x; c < hd; c += NT) {
         float acc = 0.0f;
-        if constexpr (!KV8) {
-            const float* vr = vc + (size_t)h * hd + c;
-            for (int j = 0; j < nk; ++j) acc = __builtin_fmaf(p[j], vr[(size_t)j * d], acc);
-        } else {
-            const int8_t* vr = vq + (size_t)h * hd + c;
-            const float* sv = vs + h;
-            for (int j = 0; j < nk; ++j) acc = __builtin_fmaf(p[j], (float)vr[(size_t)j * d] * sv[(size_t)j * H], acc);
+        const size_t col = (size_t)h * hd + c;
+        const int nb = nk / B;
+        float v0[B], v1[B];
+        auto ld = [&](float (&v)[B], int k) {
+#pragma unroll
+            for (int u = 0; u < B; ++u) {
+                const size_t j = (size_t)(k * B + u);
+                if constexpr (!KV8) v[u] = vc[j * d + col];
+                else v[u] = (float)vq[j * d + col] * sv[j];
+            }
+        };
+        auto fma_b = [&](const float (&v)[B], int k) {
+#pragma unroll
+            for (int u = 0; u < B; ++u) acc = __builtin_fmaf(p[k * B + u], v[u], acc);
+        };
+        if (nb > 0) {
+            ld(v0, 0);
+            ld(v1, min(1, nb - 1));
+            for (int k = 0; k < nb; k += 2) {
+                fma_b(v0, k);
+                ld(v0, min(k + 2, nb - 1));
+                if (k + 1 < nb) fma_b(v1, k + 1);
+                ld(v1, min(k + 3, nb - 1));
+            }
         }
-        att[(size_t)i * d + (size_t)h * hd + c] = acc;
+        for (int j = nb * B; j < nk; ++j) {
+            const float v = KV8 ? (float)vq[(size_t)j * d + col] * sv[j] : vc[(size_t)j * d + col];
+            acc = __builtin_fmaf(p[j], v, acc);
+        }
+        att[(size_t)i * d + col] = acc;
     }
 }
 
@@ -266,38 +371,17 @@ __global__ __launch_bounds__(NT) void bias_gelu_kernel(float* __restrict__ hm, c
     }
 }
 
-// head_argmax's max_by(partial_cmp) (composition.rs:299): the LAST index of
-// the maximum; a NaN logit panics there -> the context's error word.  The
-// token goes to out[cur + m - P]; then cur += m.
-constexpr int AT = 1024;
-__global__ __launch_bounds__(AT) void argmax_kernel(const float* __restrict__ lg, int n, int* __restrict__ curp,
-                                                    int m, int P, int64_t* __restrict__ out, int* __restrict__ err) {
-    __shared__ float bv[AT / 64];
-    __shared__ int bi[AT / 64];
-    float v = -INFINITY;
-    int idx = -1;
-    bool nan = false;
-    for (int r = threadIdx.x; r < n; r += AT) {
-        const float x = lg[r];
-        nan |= x != x;
-        if (idx < 0 || x >= v) { v = x; idx = r; }
-    }
-    // (v, idx) pairs: the larger value, ties to the larger index
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(v, o);
-        const int oi = __shfl_xor(idx, o);
-        if (oi >= 0 && (idx < 0 || ov > v || (ov == v && oi > idx))) { v = ov; idx = oi; }
-    }
-    if ((threadIdx.x & 63) == 0) { bv[threadIdx.x >> 6] = v; bi[threadIdx.x >> 6] = idx; }
-    if (nan) atomicOr(err, 1);
-    __syncthreads();
+// head_argmax's max_by(partial_cmp) (composition.rs:299): the unembed
+// folded the argmax (the LAST index of the maximum) into *best; a NaN logit
+// (a panic there) set the error word.  The token goes to out[cur + m - P],
+// then cur += m and *best is cleared for the next step.
+__global__ void argmax_done_kernel(unsigned long long* __restrict__ best, int* __restrict__ curp, int m, int P,
+                                   int64_t* __restrict__ out) {
     if (threadIdx.x == 0) {
-        for (int w = 1; w < AT / 64; ++w)
-            if (bi[w] >= 0 && (idx < 0 || bv[w] > v || (bv[w] == v && bi[w] > idx))) { v = bv[w]; idx = bi[w]; }
         const int cur = *curp;
-        out[cur + m - P] = idx < 0 ? 0 : idx;
+        out[cur + m - P] = (int64_t)(uint32_t)(*best & 0xffffffffull);
         *curp = cur + m;
+        *best = 0ull;
     }
 }
 
@@ -331,6 +415,7 @@ struct frq_gpt2 {
     int8_t *kq = nullptr, *vq = nullptr;
     float *x = nullptr, *a = nullptr, *qkv = nullptr, *att = nullptr, *y = nullptr, *hm = nullptr, *logits = nullptr;
     int* cur = nullptr;
+    unsigned long long* best = nullptr;  // the unembed's folded argmax
     int64_t *tok = nullptr, *ids = nullptr;
     ~frq_gpt2() {
         for (frq_w* w : lin) frq_w_free(w);
@@ -421,7 +506,8 @@ int check_lin(const frq_w* w, size_t k, size_t n, const std::string& name) {
     return FRQ_OK;
 }
 
-size_t attn_lds(const frq_gpt2* g) { return (g->hd + g->npos) * sizeof(float); }
+size_t attn_pstride(const frq_gpt2* g) { return (std::max(g->npos, 2 * g->hd) + 3) & ~(size_t)3; }
+size_t attn_lds(const frq_gpt2* g) { return (((g->hd + 3) & ~(size_t)3) + 2 * attn_pstride(g)) * sizeof(float); }
 
 // One forward block (m rows at device position cur; rel: the row's token
 // is the previous argmax) through the head: the argmax token and cur += m.
@@ -455,24 +541,37 @@ int gpt2_block(frq_ctx* c, frq_gpt2* g, size_t m, int rel, int P, float* logits_
     GCHK(ln(nullptr, nullptr, g->ln_of(0, 0), g->ln_of(0, 1), (int)m, 0), "launch layernorm");
     for (size_t l = 0; l < g->L; ++l) {
         if (int rc = mm(g->lin[4 * l], g->a, g->d, g->qkv, 3 * g->d)) return rc;
-        if (g->kv8)
-            qkv_kernel<true><<<dim3((unsigned)m), dim3(NT), 0, s>>>(
-                g->qkv, g->bias_of(l, 0), d, H, hd, g->cur, nullptr, nullptr, g->kq + l * g->npos * g->d,
-                g->vq + l * g->npos * g->d, g->ks + l * g->npos * g->H, g->vs + l * g->npos * g->H);
-        else
-            qkv_kernel<false><<<dim3((unsigned)m), dim3(NT), 0, s>>>(
-                g->qkv, g->bias_of(l, 0), d, H, hd, g->cur, g->kc + l * g->npos * g->d, g->vc + l * g->npos * g->d,
-                nullptr, nullptr, nullptr, nullptr);
-        GCHK(hipGetLastError(), "launch qkv");
+        float* kc = g->kv8 ? nullptr : g->kc + l * g->npos * g->d;
+        float* vc = g->kv8 ? nullptr : g->vc + l * g->npos * g->d;
+        int8_t* kq = g->kv8 ? g->kq + l * g->npos * g->d : nullptr;
+        int8_t* vq = g->kv8 ? g->vq + l * g->npos * g->d : nullptr;
+        float* ks = g->kv8 ? g->ks + l * g->npos * g->H : nullptr;
+        float* vs = g->kv8 ? g->vs + l * g->npos * g->H : nullptr;
         const dim3 ag((unsigned)H, (unsigned)m);
-        if (g->kv8)
-            attn_kernel<true><<<ag, dim3(NT), attn_lds(g), s>>>(
-                g->qkv, d, H, hd, g->cur, nullptr, nullptr, g->kq + l * g->npos * g->d, g->vq + l * g->npos * g->d,
-                g->ks + l * g->npos * g->H, g->vs + l * g->npos * g->H, rs, g->att);
-        else
-            attn_kernel<false><<<ag, dim3(NT), attn_lds(g), s>>>(
-                g->qkv, d, H, hd, g->cur, g->kc + l * g->npos * g->d, g->vc + l * g->npos * g->d, nullptr, nullptr,
-                nullptr, nullptr, rs, g->att);
+        const size_t lds = attn_lds(g);
+        const int np = (int)attn_pstride(g);
+        if (m == 1) {  // decode: bias, cache append and attention in one launch per head
+            if (g->kv8)
+                attn_kernel<true, true><<<ag, dim3(NT), lds, s>>>(g->qkv, g->bias_of(l, 0), d, H, hd, g->cur, kc,
+                                                                  vc, kq, vq, ks, vs, rs, np, g->att);
+            else
+                attn_kernel<false, true><<<ag, dim3(NT), lds, s>>>(g->qkv, g->bias_of(l, 0), d, H, hd, g->cur, kc,
+                                                                   vc, kq, vq, ks, vs, rs, np, g->att);
+        } else {
+            if (g->kv8)
+                qkv_kernel<true><<<dim3((unsigned)m), dim3(NT), 0, s>>>(g->qkv, g->bias_of(l, 0), d, H, hd, g->cur,
+                                                                        kc, vc, kq, vq, ks, vs);
+            else
+                qkv_kernel<false><<<dim3((unsigned)m), dim3(NT), 0, s>>>(g->qkv, g->bias_of(l, 0), d, H, hd, g->cur,
+                                                                         kc, vc, kq, vq, ks, vs);
+            GCHK(hipGetLastError(), "launch qkv");
+            if (g->kv8)
+                attn_kernel<true, false><<<ag, dim3(NT), lds, s>>>(g->qkv, nullptr, d, H, hd, g->cur, kc, vc, kq, vq,
+                                                                   ks, vs, rs, np, g->att);
+            else
+                attn_kernel<false, false><<<ag, dim3(NT), lds, s>>>(g->qkv, nullptr, d, H, hd, g->cur, kc, vc, kq,
+                                                                    vq, ks, vs, rs, np, g->att);
+        }
         GCHK(hipGetLastError(), "launch attention");
         if (int rc = mm(g->lin[4 * l + 1], g->att, g->d, g->y, g->d)) return rc;
         GCHK(ln(g->y, g->bias_of(l, 1), g->ln_of(l, 2), g->ln_of(l, 3), (int)m, 0), "launch layernorm");
@@ -488,8 +587,8 @@ int gpt2_block(frq_ctx* c, frq_gpt2* g, size_t m, int rel, int P, float* logits_
             GCHK(ln(g->y, g->bias_of(l, 3), g->lnf_g, g->lnf_b, 1, (int)m - 1), "launch layernorm");
     }
     float* lg = logits_out ? logits_out : g->logits;
-    if (int rc = frq_rowdot_f32_dev(c, g->wte, g->a + (m - 1) * g->d, lg)) return rc;
-    argmax_kernel<<<dim3(1), dim3(AT), 0, s>>>(lg, (int)g->vocab, g->cur, (int)m, P, g->tok, ctx_err(c));
+    GCHK(launch_rowdot_argmax(wt, g->a + (m - 1) * g->d, lg, g->best, ctx_err(c), s), "launch rowdot");
+    argmax_done_kernel<<<dim3(1), dim3(64), 0, s>>>(g->best, g->cur, (int)m, P, g->tok);
     GCHK(hipGetLastError(), "launch argmax");
     return FRQ_OK;
 }
@@ -635,7 +734,7 @@ int frq_gpt2_load(frq_ctx* c, const frq_bundle* b, int kv_int8, frq_gpt2** out) 
         o_kc = take(L * N * d * 4); o_vc = take(L * N * d * 4);
     }
     const size_t o_x = take(N * d * 4), o_a = take(N * d * 4), o_qkv = take(N * 3 * d * 4), o_att = take(N * d * 4),
-                 o_y = take(N * d * 4), o_h = take(N * 4 * d * 4), o_lg = take(V * 4), o_cur = take(4),
+                 o_y = take(N * d * 4), o_h = take(N * 4 * d * 4), o_lg = take(V * 4), o_cur = take(4), o_best = take(8),
                  o_tok = take(N * 8), o_ids = take(N * 8);
     DevSwitch dv(g->device);
     hipStream_t s = (hipStream_t)frq_get_stream(c);
@@ -659,6 +758,7 @@ int frq_gpt2_load(frq_ctx* c, const frq_bundle* b, int kv_int8, frq_gpt2** out) 
     g->qkv = reinterpret_cast<float*>(m + o_qkv); g->att = reinterpret_cast<float*>(m + o_att);
     g->y = reinterpret_cast<float*>(m + o_y); g->hm = reinterpret_cast<float*>(m + o_h);
     g->logits = reinterpret_cast<float*>(m + o_lg); g->cur = reinterpret_cast<int*>(m + o_cur);
+    g->best = reinterpret_cast<unsigned long long*>(m + o_best);
     g->tok = reinterpret_cast<int64_t*>(m + o_tok); g->ids = reinterpret_cast<int64_t*>(m + o_ids);
     GCHK(hipStreamSynchronize(s), "hipStreamSynchronize");  // hv is released on return
     *out = g.release();

@@ -32,16 +32,29 @@ namespace {
 
 constexpr int TP = 144;  // LDS tile row stride (bytes)
 
-template <int DT, bool SUB, int DEPTH>  // DT: 0 f32, 1 f16, 2 rowi8; DEPTH chunks in registers
-__global__ __launch_bounds__(256) void rowdot_kernel(
+// The argmax of the full-table form (ARG): each wave folds its 64 outputs'
+// keys (order-preserving bits of the value, -0 as +0, above the row id, so
+// ties go to the larger id) into *best with a 64-bit atomic max; a NaN
+// output sets *err.
+__device__ __forceinline__ unsigned long long argmax_key(float v, int row) {
+    uint32_t u = __builtin_bit_cast(uint32_t, v);
+    if (u == 0x80000000u) u = 0;
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)u << 32) | (uint32_t)row;
+}
+
+template <int DT, bool SUB, int DEPTH, int WPB, bool ARG>  // DT: 0 f32, 1 f16, 2 rowi8; DEPTH chunks in
+                                                          // registers; WPB waves per block
+__global__ __launch_bounds__(64 * WPB) void rowdot_kernel(
     const uint8_t* __restrict__ W, const float* __restrict__ rs, int rows, int d, size_t pitch,
-    const float* __restrict__ x, const int64_t* __restrict__ cand, int nout, float* __restrict__ out) {
+    const float* __restrict__ x, const int64_t* __restrict__ cand, int nout, float* __restrict__ out,
+    unsigned long long* __restrict__ best, int* __restrict__ err) {
     constexpr int ES = DT == 0 ? 4 : (DT == 1 ? 2 : 1);  // bytes per element
     constexpr int CE = 128 / ES;                         // elements per chunk
-    __shared__ __attribute__((aligned(16))) uint8_t tile[4][64 * TP];
+    __shared__ __attribute__((aligned(16))) uint8_t tile[WPB][64 * TP];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int o0 = ((int)blockIdx.x * 4 + wave) * 64;
+    const int o0 = ((int)blockIdx.x * WPB + wave) * 64;
     if (o0 >= nout) return;  // wave-uniform; no block-wide barrier below
     uint8_t* tw = tile[wave];
 
@@ -170,30 +183,37 @@ __global__ __launch_bounds__(256) void rowdot_kernel(
     }
     const int o = o0 + lane;
     if (o < nout) out[o] = own_ok ? acc : -__builtin_inff();
+    if constexpr (ARG) {
+        unsigned long long key = o < nout ? argmax_key(acc, o) : 0ull;
+        const bool nan = o < nout && acc != acc;
+#pragma unroll
+        for (int sh = 32; sh > 0; sh >>= 1) {
+            const unsigned long long ok = __shfl_xor(key, sh);
+            key = ok > key ? ok : key;
+        }
+        if (__builtin_amdgcn_ballot_w64(nan) && lane == 0) atomicOr(err, 1);
+        if (lane == 0) atomicMax(best, key);
+    }
 }
 
-template <int DT>
+template <int DT, bool ARG>
 hipError_t launch_dt(const Weight& w, const float* x, const int64_t* cand, size_t nout, float* out,
-                     hipStream_t s) {
-    const unsigned grid = (unsigned)((nout + 255) / 256);
+                     unsigned long long* best, int* err, hipStream_t s) {
     // fewer waves than about four per SIMD: keep three chunks in flight per
     // wave (latency-bound), else two (the occupancy carries the load)
     const bool deep = nout < 4 * 1024 * 64;
+    const unsigned g4 = (unsigned)((nout + 255) / 256);
+#define FRQ_ROWDOT(SUBV, DEPTHV, WPBV)                                                                   \
+    rowdot_kernel<DT, SUBV, DEPTHV, WPBV, ARG><<<dim3(g4), dim3(64 * WPBV), 0, s>>>(                   \
+        w.rowp, w.scale, (int)w.n, (int)w.k, w.rpitch, x, cand, (int)nout, out, best, err)
     if (cand) {
-        if (deep)
-            rowdot_kernel<DT, true, 3><<<dim3(grid), dim3(256), 0, s>>>(
-                w.rowp, w.scale, (int)w.n, (int)w.k, w.rpitch, x, cand, (int)nout, out);
-        else
-            rowdot_kernel<DT, true, 2><<<dim3(grid), dim3(256), 0, s>>>(
-                w.rowp, w.scale, (int)w.n, (int)w.k, w.rpitch, x, cand, (int)nout, out);
+        if (deep) FRQ_ROWDOT(true, 3, 4);
+        else FRQ_ROWDOT(true, 2, 4);
     } else {
-        if (deep)
-            rowdot_kernel<DT, false, 3><<<dim3(grid), dim3(256), 0, s>>>(
-                w.rowp, w.scale, (int)w.n, (int)w.k, w.rpitch, x, nullptr, (int)nout, out);
-        else
-            rowdot_kernel<DT, false, 2><<<dim3(grid), dim3(256), 0, s>>>(
-                w.rowp, w.scale, (int)w.n, (int)w.k, w.rpitch, x, nullptr, (int)nout, out);
+        if (deep) FRQ_ROWDOT(false, 3, 4);
+        else FRQ_ROWDOT(false, 2, 4);
     }
+#undef FRQ_ROWDOT
     return hipGetLastError();
 }
 
@@ -210,9 +230,21 @@ hipError_t launch_rowdot(const Weight& w, const float* x, const int64_t* cand, s
     if (nout > (size_t)INT32_MAX - 256 || w.n > (size_t)INT32_MAX || w.k > (size_t)INT32_MAX)
         return hipErrorInvalidValue;
     switch (w.dtype) {
-        case FRQ_DT_F32: return launch_dt<0>(w, x, cand, nout, out, s);
-        case FRQ_DT_F16: return launch_dt<1>(w, x, cand, nout, out, s);
-        case FRQ_DT_ROWI8: return launch_dt<2>(w, x, cand, nout, out, s);
+        case FRQ_DT_F32: return launch_dt<0, false>(w, x, cand, nout, out, nullptr, nullptr, s);
+        case FRQ_DT_F16: return launch_dt<1, false>(w, x, cand, nout, out, nullptr, nullptr, s);
+        case FRQ_DT_ROWI8: return launch_dt<2, false>(w, x, cand, nout, out, nullptr, nullptr, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_rowdot_argmax(const Weight& w, const float* x, float* out, unsigned long long* best, int* err,
+                                hipStream_t s) {
+    if (!w.n) return hipSuccess;
+    if (w.n > (size_t)INT32_MAX - 256 || w.k > (size_t)INT32_MAX) return hipErrorInvalidValue;
+    switch (w.dtype) {
+        case FRQ_DT_F32: return launch_dt<0, true>(w, x, nullptr, w.n, out, best, err, s);
+        case FRQ_DT_F16: return launch_dt<1, true>(w, x, nullptr, w.n, out, best, err, s);
+        case FRQ_DT_ROWI8: return launch_dt<2, true>(w, x, nullptr, w.n, out, best, err, s);
         default: return hipErrorInvalidValue;
     }
 }
