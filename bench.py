@@ -16,7 +16,7 @@ fused into the GEMV); `roofline` is that kernel at the step's dominant shape
 f32 activation row, f32 outputs) over its average launch time on the
 library's stream.  Also reported (in "detail"): the GEMV kernel alone on
 pre-quantised input, the M=2048 MFMA-bound shapes in TOPS, the int4 decode
-GEMV on Gemma-2 shapes, the unembed row dot, the config-4 MoE layer, and
+GEMV and the affine-int4 (q4a) GEMV on Gemma-2 shapes, the unembed row dot, the config-4 MoE layer, and
 config 0 end to end: GPT-2 small greedy decode (tok/s, f32 and int8 KV
 caches) with the oracle's CPU rate and token check beside it.  The CPU
 baseline is the
@@ -47,6 +47,11 @@ def gemv_kernel_bytes(m, k, n):
 
 def int4_bytes(m, k, n, g=32):
     return n * k // 2 + 2 * n * ((k + g - 1) // g) + 4 * m * k + 4 * m * n
+
+
+def q4a_bytes(m, k, n, g=32):
+    # packed nibbles + the f16 scale and min of each group + f32 in / out
+    return n * ((k + 1) // 2) + 4 * n * ((k + g - 1) // g) + 4 * m * k + 4 * m * n
 
 
 DOM_SHAPE = (896, 151936)  # the headline's dominant launch (136 MB of weights)
@@ -118,7 +123,7 @@ def main():
         sys.exit(2)
 
     import fieldrun_amd as fa
-    from fieldrun_amd import hip, synth
+    from fieldrun_amd import convert, hip, synth
 
     ctx = fa.Context(0)
     stream = fa.lib.frq_get_stream(ctx.h)
@@ -286,6 +291,25 @@ def main():
             gb = int4_bytes(1, k, n) / (us * 1e-6) / 1e9
             detail["int4_m1_gemv"][f"K{k}_N{n}"] = {"us": round(us, 2), "GBps": round(gb, 1),
                                                     "frac": round(gb / HBM_PEAK_GBS, 3)}
+            for w in reps:
+                w.free()
+        # ---------------- affine int4 (q4a) decode GEMV, same shapes ----------------
+        detail["q4a_m1_gemv"] = {}
+        for (k, n) in [(2304, 9216), (9216, 2304), (2304, 2048)]:
+            reps = []
+            for r in range(3):
+                rng = np.random.default_rng(synth.seed(5, r))
+                wsrc = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02))
+                packed, s16, m16, g = convert.put_q4a(wsrc, True)
+                del wsrc
+                reps.append(ctx.upload_q4a(packed, s16, m16, k, g))
+            a = synth.activations(1, k, synth.seed(5, 9), outlier_scale=1.0)
+            da = hip.DeviceArray.from_numpy(a)
+            do = hip.DeviceArray((1, n), np.float32)
+            us = time_loop(lambda i: reps[i % 3].mm_dev(da.ptr, 1, do.ptr), 60) * 1e3
+            gb = q4a_bytes(1, k, n, g) / (us * 1e-6) / 1e9
+            detail["q4a_m1_gemv"][f"K{k}_N{n}"] = {"us": round(us, 2), "GBps": round(gb, 1),
+                                                   "frac": round(gb / HBM_PEAK_GBS, 3)}
             for w in reps:
                 w.free()
         # ---------------- unembed row dot (Bundle::rowdot_f32) ----------------

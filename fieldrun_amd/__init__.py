@@ -34,7 +34,7 @@ LIB_PATH = os.path.join(_HERE, "libfrq.so")
 
 FRQ_OK, FRQ_ERR_ARG, FRQ_ERR_HIP, FRQ_ERR_NAN = 0, 1, 2, 3
 FRQ_ERR_DTYPE, FRQ_ERR_FORMAT, FRQ_ERR_MISSING, FRQ_ERR_NODEV = 4, 5, 6, 7
-FRQ_DT_I8, FRQ_DT_I4, FRQ_DT_F32, FRQ_DT_F16, FRQ_DT_ROWI8 = 1, 2, 3, 4, 5
+FRQ_DT_I8, FRQ_DT_I4, FRQ_DT_F32, FRQ_DT_F16, FRQ_DT_ROWI8, FRQ_DT_Q4A = 1, 2, 3, 4, 5, 6
 FRQ_ACT_SILU, FRQ_ACT_GELU_TANH = 0, 1
 
 # name -> (restype, argtypes); every symbol include/frq.h declares
@@ -76,6 +76,7 @@ SIGNATURES = {
     "frq_bundle_array": (_I, [_P, C.c_char_p, _P, _S, _P, _P, _P, _P, _P]),
     "frq_bundle_weight": (_I, [_P, _P, C.c_char_p, _P]),
     "frq_bundle_moe": (_I, [_P, _P, C.c_char_p, _S, _I, _P]),
+    "frq_upload_q4a": (_P, [_P, _P, _P, _P, _S, _S, _S]),
     "frq_gpt2_load": (_I, [_P, _P, _I, _P]),
     "frq_gpt2_free": (None, [_P]),
     "frq_gpt2_info": (_I, [_P, _P, _P, _P, _P, _P]),
@@ -186,6 +187,19 @@ class Context:
         if not h:
             raise FrqError(FRQ_ERR_HIP, lib.frq_last_error().decode())
         return Weight(self, h, FRQ_DT_I4, n, k, g)
+
+    def upload_q4a(self, packed: np.ndarray, scale_f16: np.ndarray, min_f16: np.ndarray, k: int,
+                   g: int) -> "Weight":
+        """Affine int4: packed (N, ceil(K/2)) unsigned nibbles, f16 scale and
+        min (N, ceil(K/g)); w = scale*q + min."""
+        packed = np.ascontiguousarray(packed, dtype=np.uint8)
+        s = np.ascontiguousarray(scale_f16, dtype=np.float16).view(np.uint16)
+        mn = np.ascontiguousarray(min_f16, dtype=np.float16).view(np.uint16)
+        n = packed.shape[0]
+        h = lib.frq_upload_q4a(self.h, _ptr(packed), _ptr(s), _ptr(mn), n, k, g)
+        if not h:
+            raise FrqError(FRQ_ERR_HIP, lib.frq_last_error().decode())
+        return Weight(self, h, FRQ_DT_Q4A, n, k, g)
 
     def upload_rows(self, kind: str, data: np.ndarray, scale: np.ndarray | None = None) -> "RowTable":
         """A row-major (rows, d) embedding table for rowdot_f32: kind 'f32'

@@ -11,6 +11,7 @@ against the oracle's restatement of convert.rs):
   put_small             176-178   f32 if dtype == "f32", else f16
   put_lin               181-190   (out, in) source -> int8 / int4 / f16 / f32
   put_i4                196-216   group-wise int4 (out, in) packed + f16 scales
+  put_q4a               223-260   affine group int4 + f16 scales and mins
   put_embed_i8 / _embed 265-291   row-major per-row int8 (rowi8) or small
   put_i8                344-360   per-output-column int8 (in, out) + f16 scales
   finish                362-365   the manifest with "arrays" appended
@@ -83,13 +84,27 @@ class BundleWriter:
         self.entry(name, "i4", (out, inp), n, group=g)
         self.put_f16(name + "__scale", s16.astype(np.float32))
 
+    def put_q4a(self, name: str, data, transpose: bool):
+        """Affine group int4 (convert.rs:223-260): stored (out, in) packed
+        unsigned nibbles with the "group" field and f16 (out, ng) __scale and
+        __min siblings."""
+        packed, s16, m16, g = convert.put_q4a(data, transpose)
+        out = packed.shape[0]
+        inp = np.asarray(data).shape[1] if transpose else np.asarray(data).shape[0]
+        n = self._write(np.ascontiguousarray(packed))
+        self.entry(name, "q4a", (out, inp), n, group=g)
+        self.put_f16(name + "__scale", s16.astype(np.float32))
+        self.put_f16(name + "__min", m16.astype(np.float32))
+
     def put_lin(self, name: str, data, dtype: str):
-        """A weight linear from an (out, in) source: "int8" / "int4", or f16 /
-        f32 transposed to (in, out)."""
+        """A weight linear from an (out, in) source: "int8" / "int4" / "q4a",
+        or f16 / f32 transposed to (in, out)."""
         if dtype == "int8":
             return self.put_i8(name, data, True)
         if dtype == "int4":
             return self.put_i4(name, data, True)
+        if dtype == "q4a":
+            return self.put_q4a(name, data, True)
         self.put_small(name, np.ascontiguousarray(np.asarray(data, np.float32).T), None, dtype)
 
     def put_embed_i8(self, name: str, data):

@@ -46,6 +46,31 @@ def put_i4(data: np.ndarray, transpose: bool):
     return packed, sc.astype(np.float16), g
 
 
+def put_q4a(data: np.ndarray, transpose: bool):
+    """Affine group int4 (src/convert.rs:223-260) -> (packed (out, ceil(in/2))
+    uint8 unsigned nibbles, scale float16 (out, ng), min float16 (out, ng), g):
+    per group scale = max((max - min) / 15, 1e-8), q = clamp(round_ties_even(
+    (v - min) / scale), 0, 15) from the f32 scale and min."""
+    w = _as_out_in(data, transpose)
+    out, inp = w.shape
+    g = min(32, max(inp, 1))
+    ng = (inp + g - 1) // g
+    pad = ng * g - inp
+    wv = w.reshape(out, -1)
+    mn = np.stack([wv[:, i * g:min((i + 1) * g, inp)].min(axis=1) for i in range(ng)], axis=1) if inp else \
+        np.zeros((out, 0), np.float32)
+    mx = np.stack([wv[:, i * g:min((i + 1) * g, inp)].max(axis=1) for i in range(ng)], axis=1) if inp else \
+        np.zeros((out, 0), np.float32)
+    sc = np.maximum((mx - mn) / np.float32(15.0), np.float32(1e-8)).astype(np.float32)
+    rep = lambda v: np.repeat(v, g, axis=1)[:, :inp]
+    q = np.clip(np.rint((w - rep(mn)) / rep(sc)), 0, 15).astype(np.int64)
+    del pad
+    if inp % 2:
+        q = np.pad(q, ((0, 0), (0, 1)))
+    packed = (q[:, 0::2] | (q[:, 1::2] << 4)).astype(np.uint8)
+    return packed, sc.astype(np.float16), mn.astype(np.float32).astype(np.float16), g
+
+
 def put_embed_i8(data: np.ndarray):
     """-> (q (vocab, d) int8, scale float16 [vocab])."""
     data = np.asarray(data, np.float32)

@@ -12,6 +12,7 @@
 #include <mutex>
 #include <new>
 #include <string>
+#include <vector>
 
 #include "frq_internal.h"
 
@@ -201,6 +202,7 @@ void free_weight(Weight& w) {
     if (w.q4raw) (void)hipFree(w.q4raw);
     if (w.s4raw) (void)hipFree(w.s4raw);
     if (w.rowp) (void)hipFree(w.rowp);
+    if (w.q4a_sm) (void)hipFree(w.q4a_sm);
     w = Weight{};
 }
 
@@ -391,6 +393,38 @@ frq_w* frq_upload_i4(frq_ctx* c, const uint8_t* packed,
     return h;
 }
 
+frq_w* frq_upload_q4a(frq_ctx* c, const uint8_t* packed, const uint16_t* scale_f16, const uint16_t* min_f16,
+                      size_t n, size_t k, size_t g) {
+    if (check_ctx(c) || g == 0 || (n * k && (!packed || !scale_f16 || !min_f16))) {
+        fail(FRQ_ERR_ARG, "frq_upload_q4a: null argument or zero group");
+        return nullptr;
+    }
+    DeviceGuard gd(c->device);
+    frq_w* h = new (std::nothrow) frq_w;
+    if (!h) { fail(FRQ_ERR_ARG, "out of host memory"); return nullptr; }
+    Weight& w = h->w;
+    w.dtype = FRQ_DT_Q4A; w.device = c->device; w.n = n; w.k = k; w.g = g;
+    const size_t rb = (k + 1) / 2, ng = (k + g - 1) / g;
+    w.rpitch = q4a_pitch(k);
+    std::vector<uint32_t> sm(n * ng);
+    for (size_t i = 0; i < n * ng; ++i) sm[i] = (uint32_t)scale_f16[i] | ((uint32_t)min_f16[i] << 16);
+    hipError_t e = hipMalloc(&w.q4raw, n * w.rpitch + 16);
+    if (e == hipSuccess) e = hipMalloc(&w.q4a_sm, n * ng * 4 + 16);
+    if (e == hipSuccess) e = hipMemsetAsync(w.q4raw, 0, n * w.rpitch + 16, c->stream);
+    if (e == hipSuccess && n * rb)
+        e = hipMemcpy2DAsync(w.q4raw, w.rpitch, packed, rb, rb, n, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess && n * ng)
+        e = hipMemcpyAsync(w.q4a_sm, sm.data(), n * ng * 4, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);  // sm is released on return
+    if (e != hipSuccess) {
+        hip_fail(e, "frq_upload_q4a");
+        free_weight(w);
+        delete h;
+        return nullptr;
+    }
+    return h;
+}
+
 frq_w* frq_upload_rows(frq_ctx* c, int dtype, const void* data, const float* scale, size_t rows,
                        size_t d) {
     if (check_ctx(c)) return nullptr;
@@ -468,6 +502,10 @@ int frq_mm_dev(frq_ctx* c, const frq_w* wh, const float* d_a, size_t m, float* d
         HIPCHK(launch_i4(w, m, d_a, d_out, (float*)c->ws, c->tickets, c->stream), "launch i4");
         return FRQ_OK;
     }
+    if (w.dtype == FRQ_DT_Q4A) {
+        HIPCHK(launch_q4a(w, m, d_a, d_out, c->stream), "launch q4a");
+        return FRQ_OK;
+    }
     return fail(FRQ_ERR_DTYPE, "unsupported weight dtype");
 }
 
@@ -532,7 +570,7 @@ static int mm_host(frq_ctx* c, const frq_w* wh, const float* a, size_t m, float*
     if ((!a && w.k) || !out) return fail(FRQ_ERR_ARG, "null activation/output pointer");
     DeviceGuard g(c->device);
     const bool i8 = w.dtype == FRQ_DT_I8;
-    if (!i8 && w.dtype != FRQ_DT_I4) return fail(FRQ_ERR_DTYPE, "unsupported weight dtype");
+    if (!i8 && w.dtype != FRQ_DT_I4 && w.dtype != FRQ_DT_Q4A) return fail(FRQ_ERR_DTYPE, "unsupported weight dtype");
     if (!i8 && (acc || a8h || sah || oih || ovh))
         return fail(FRQ_ERR_DTYPE, "debug outputs exist for int8 weights only");
     const size_t in_b = round_up(m * w.k * sizeof(float) + 16, 256);
@@ -552,6 +590,8 @@ static int mm_host(frq_ctx* c, const frq_w* wh, const float* a, size_t m, float*
     int8_t* a8 = nullptr; float* sa = nullptr; uint32_t* oi = nullptr; float* ov = nullptr;
     if (i8) {
         if (int rc = run_i8(c, w, d_a, m, d_out, d_acc, scratch, &a8, &sa, &oi, &ov)) return rc;
+    } else if (w.dtype == FRQ_DT_Q4A) {
+        HIPCHK(launch_q4a(w, m, d_a, d_out, c->stream), "launch q4a");
     } else {
         HIPCHK(launch_i4(w, m, d_a, d_out, (float*)scratch, c->tickets, c->stream), "launch i4");
     }

@@ -507,6 +507,22 @@ static frq_w* bundle_weight(frq_ctx* ctx, const frq_bundle* b, const char* name)
         }
         return frq_upload_i4(ctx, data, f16_words(b, sc, tmp), n, k, g);
     }
+    if (s->dtype == "q4a") {  // Bundle::load 361-364 (group default 64); __scale and __min per mm (803-804)
+        if (!need(b, nm, "q4a", 2)) return nullptr;
+        const size_t n = s->shape[0], k = s->shape[1], g = s->group ? s->group : 64;
+        const std::string mn = nm + "__min";
+        const ArrSpec* sc = find(b, sn);
+        if (!sc) return nullptr;
+        const ArrSpec* mi = find(b, mn);
+        if (!mi) return nullptr;
+        const size_t want = n * ((k + g - 1) / g) * 2;
+        if (sc->dtype != "f16" || sc->bytes != want || mi->dtype != "f16" || mi->bytes != want) {
+            frq::set_error(FRQ_ERR_FORMAT, nm + ": f16 (out, ceil(in/group)) __scale and __min expected");
+            return nullptr;
+        }
+        std::vector<uint16_t> tmp2;
+        return frq_upload_q4a(ctx, data, f16_words(b, sc, tmp), f16_words(b, mi, tmp2), n, k, g);
+    }
     if (s->dtype == "rowi8") {
         if (!need(b, nm, "rowi8", 2)) return nullptr;
         const ArrSpec* sc = need(b, sn, "f16", 1);

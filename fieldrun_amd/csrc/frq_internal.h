@@ -21,6 +21,7 @@
 //                     channel.
 #pragma once
 
+#include <algorithm>
 #include <string>
 
 #include <hip/hip_runtime.h>
@@ -122,7 +123,9 @@ struct Weight {
     uint16_t* s4raw = nullptr;  // int4 f16 scales (N, ceil(K/g)) as stored
     int i4_blocked = 0;      // 1 when the MFMA layout (g == 32) is built
     uint8_t* rowp = nullptr; // row tables: (n, k) rows, each padded to rpitch bytes
-    size_t rpitch = 0;       //   (a multiple of 128); rowi8 scales in `scale`
+    size_t rpitch = 0;       //   (a multiple of 128); rowi8 scales in `scale`;
+                             //   q4a: the q4raw row pitch (a multiple of 16)
+    uint32_t* q4a_sm = nullptr;  // q4a: (N, ng) words, f16 scale | f16 min << 16
 };
 
 struct MoeBank {
@@ -211,6 +214,9 @@ size_t i4_blocked_bytes(size_t n, size_t k);
 hipError_t launch_i4_block(const uint8_t* raw, const uint16_t* sraw, size_t n,
                            size_t k, uint8_t* blk, uint16_t* sblk,
                            hipStream_t s);
+// Affine int4 (q4a) linear (any m): packed rows in q4raw at pitch rpitch.
+size_t q4a_pitch(size_t k);
+hipError_t launch_q4a(const Weight& w, size_t m, const float* a, float* out, hipStream_t s);
 // MoE.
 size_t moe_ws_bytes(const MoeBank& b, size_t T, size_t topk);
 hipError_t launch_moe(const MoeBank& b, const float* x, size_t T,

@@ -499,7 +499,8 @@ int check_lin(const frq_w* w, size_t k, size_t n, const std::string& name) {
     int dt = 0;
     size_t wn = 0, wk = 0, g = 0;
     if (int rc = frq_w_info(w, &dt, &wn, &wk, &g)) return rc;
-    if (dt != FRQ_DT_I8 && dt != FRQ_DT_I4) return set_error(FRQ_ERR_DTYPE, name + ": not an int8 / int4 linear");
+    if (dt != FRQ_DT_I8 && dt != FRQ_DT_I4 && dt != FRQ_DT_Q4A)
+        return set_error(FRQ_ERR_DTYPE, name + ": not an int8 / int4 / q4a linear");
     if (wk != k || wn != n)
         return set_error(FRQ_ERR_FORMAT, name + ": shape (" + std::to_string(wk) + ", " + std::to_string(wn) +
                                              "), expected (" + std::to_string(k) + ", " + std::to_string(n) + ")");

@@ -1,0 +1,192 @@
+// q4a.hip — group-wise affine int4 (q4a) linears, gfx950.
+//
+// Restates Bundle::mm's Q4A arm (/root/reference/src/bundle.rs:802-845):
+// w[k, j] = scale[j, k/g] * q + min[j, k/g], q the unsigned nibble of the
+// packed (N, ceil(K/2)) rows (even k in the low nibble).
+//   M == 1: out[j] = q4a_dot_avx2(row j) (231-258), the x86 production
+//           order: per group two sets of eight lane accumulators over the
+//           8-nibble chunks from the group's start (q lanes FMA chains of
+//           q * a, a lanes add chains of a), each folded by hsum256
+//           ((l0+l4)+(l2+l6)) + ((l1+l5)+(l3+l7)), a mul+add tail, then
+//           sum += scale*qsum + min*asum across the groups in order.
+//   M > 1:  the dequantised weight (scale*q + min, a mul then an add) and a
+//           sequential-k FMA chain per output (the order the oracle takes
+//           for ndarray's sgemm).
+// Both bit-exact to the oracle.
+//
+// M == 1 layout of the work: the groups of a row are independent until the
+// final in-order sum, so a thread takes one (row, group) pair at a time —
+// adjacent threads read adjacent groups, so the packed bytes and the scale /
+// min words arrive coalesced — and leaves scale*qsum + min*asum in LDS; one
+// lane per row then adds its row's groups in order.  Rows are stored with a
+// 16-byte pitch and the f16 scale and min of a group side by side in one
+// 32-bit word (scale low, min high).
+#include "frq_internal.h"
+
+namespace frq {
+
+namespace {
+
+constexpr int QT = 256;
+
+__device__ __forceinline__ float q4a_group(const uint8_t* __restrict__ prow, const float* __restrict__ a, int kk,
+                                           int hi, uint32_t sm) {
+    float l[8] = {0, 0, 0, 0, 0, 0, 0, 0}, m[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (; kk + 8 <= hi; kk += 8) {
+        const int base = kk & ~1;  // unpack8_nibbles reads from byte kk / 2
+        const uint8_t* pb = prow + (base >> 1);
+        const uint32_t w = (uint32_t)pb[0] | ((uint32_t)pb[1] << 8) | ((uint32_t)pb[2] << 16) | ((uint32_t)pb[3] << 24);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const float av = a[kk + q];
+            l[q] = __builtin_fmaf((float)((w >> (4 * q)) & 15u), av, l[q]);
+            m[q] = m[q] + av;
+        }
+    }
+    float qsum = ((l[0] + l[4]) + (l[2] + l[6])) + ((l[1] + l[5]) + (l[3] + l[7]));
+    float asum = ((m[0] + m[4]) + (m[2] + m[6])) + ((m[1] + m[5]) + (m[3] + m[7]));
+    for (; kk < hi; ++kk) {
+        const uint8_t byte = prow[kk >> 1];
+        const float q = (float)((kk & 1) ? (byte >> 4) : (byte & 15));
+        qsum = qsum + a[kk] * q;
+        asum = asum + a[kk];
+    }
+    return h2f((uint16_t)(sm & 0xffffu)) * qsum + h2f((uint16_t)(sm >> 16)) * asum;
+}
+
+// The same for a group of 32 * G4 nibbles whose bytes start 16-byte
+// aligned, from registers: G4 16-byte loads of nibbles, the activations from
+// the workgroup's LDS copy (as, padded 4 floats per 32 so the lanes, which
+// take adjacent groups, fall on different banks).
+template <int G4>
+__device__ __forceinline__ float q4a_group_vec(const uint8_t* __restrict__ pg, const float* __restrict__ as, int k0,
+                                               uint32_t sm) {
+    float l[8] = {0, 0, 0, 0, 0, 0, 0, 0}, m[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int h = 0; h < G4; ++h) {
+        const uint4 w4 = *reinterpret_cast<const uint4*>(pg + 16 * h);
+        const uint32_t ws[4] = {w4.x, w4.y, w4.z, w4.w};
+        const float* ab = as + (k0 + 32 * h) / 32 * 36;  // 32 activations at a 36-float stride
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float4 a0 = *reinterpret_cast<const float4*>(ab + 8 * c);
+            const float4 a1 = *reinterpret_cast<const float4*>(ab + 8 * c + 4);
+            const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                l[q] = __builtin_fmaf((float)((ws[c] >> (4 * q)) & 15u), av[q], l[q]);
+                m[q] = m[q] + av[q];
+            }
+        }
+    }
+    const float qsum = ((l[0] + l[4]) + (l[2] + l[6])) + ((l[1] + l[5]) + (l[3] + l[7]));
+    const float asum = ((m[0] + m[4]) + (m[2] + m[6])) + ((m[1] + m[5]) + (m[3] + m[7]));
+    return h2f((uint16_t)(sm & 0xffffu)) * qsum + h2f((uint16_t)(sm >> 16)) * asum;
+}
+
+// M == 1: a workgroup owns `rb` rows; cg (LDS) holds their rb * ng group
+// terms.  G4 > 0: g == 32 * G4 and the rows' 16-byte pitch keep every group
+// aligned, and the activation row is staged in LDS first; G4 == 0: any g,
+// byte loads and activations from global memory.
+template <int G4>
+__global__ __launch_bounds__(QT) void q4a_gemv_kernel(const uint8_t* __restrict__ packed, size_t pitch,
+                                                      const uint32_t* __restrict__ sm, int N, int K, int g, int rb,
+                                                      const float* __restrict__ a, float* __restrict__ out) {
+    extern __shared__ float4 lds4[];
+    float* cg = reinterpret_cast<float*>(lds4);
+    const int ng = (K + g - 1) / g;
+    const int r0 = blockIdx.x * rb;
+    const int nr = min(rb, N - r0);
+    const int items = nr * ng;
+    if constexpr (G4 > 0) {
+        float* as = cg + ((rb * ng + 3) & ~3);
+        for (int i = threadIdx.x; i < K / 4; i += QT)
+            *reinterpret_cast<float4*>(as + (4 * i) / 32 * 36 + (4 * i) % 32) = reinterpret_cast<const float4*>(a)[i];
+        __syncthreads();
+        for (int p = threadIdx.x; p < items; p += QT) {
+            const int r = p / ng, gi = p - r * ng;
+            const int j = r0 + r;
+            cg[p] = q4a_group_vec<G4>(packed + (size_t)j * pitch + (size_t)gi * 16 * G4, as, gi * g,
+                                      sm[(size_t)j * ng + gi]);
+        }
+    } else {
+        for (int p = threadIdx.x; p < items; p += QT) {
+            const int r = p / ng, gi = p - r * ng;
+            const int j = r0 + r;
+            const int kk = gi * g, hi = min(kk + g, K);
+            cg[p] = q4a_group(packed + (size_t)j * pitch, a, kk, hi, sm[(size_t)j * ng + gi]);
+        }
+    }
+    __syncthreads();
+    for (int r = threadIdx.x; r < nr; r += QT) {
+        float sum = 0.0f;
+        const float* c = cg + r * ng;
+        for (int gi = 0; gi < ng; ++gi) sum = sum + c[gi];
+        out[r0 + r] = sum;
+    }
+}
+
+// M > 1: one thread per output column j and up to MT token rows.
+template <int MT>
+__global__ __launch_bounds__(QT) void q4a_gemm_rows(const uint8_t* __restrict__ packed, size_t pitch,
+                                                    const uint32_t* __restrict__ sm, int N, int K, int g,
+                                                    const float* __restrict__ a, int M, float* __restrict__ out) {
+    const int j = blockIdx.x * QT + threadIdx.x;
+    const int m0 = blockIdx.y * MT;
+    if (j >= N) return;
+    const int ng = (K + g - 1) / g;
+    const uint8_t* prow = packed + (size_t)j * pitch;
+    const uint32_t* srow = sm + (size_t)j * ng;
+    float acc[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
+    for (int kk = 0; kk < K; ++kk) {
+        const uint8_t byte = prow[kk >> 1];
+        const uint32_t s = srow[kk / g];
+        const float w = h2f((uint16_t)(s & 0xffffu)) * (float)((kk & 1) ? (byte >> 4) : (byte & 15)) +
+                        h2f((uint16_t)(s >> 16));
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+            if (m0 + m < M) acc[m] = __builtin_fmaf(a[(size_t)(m0 + m) * K + kk], w, acc[m]);
+    }
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+        if (m0 + m < M) out[(size_t)(m0 + m) * N + j] = acc[m];
+}
+
+}  // namespace
+
+size_t q4a_pitch(size_t k) { return round_up((k + 1) / 2, 16); }
+
+hipError_t launch_q4a(const Weight& w, size_t m, const float* a, float* out, hipStream_t s) {
+    if (m == 0 || w.n == 0) return hipSuccess;
+    if (w.n > (size_t)INT32_MAX || w.k > (size_t)INT32_MAX || m > (size_t)INT32_MAX) return hipErrorInvalidValue;
+    const int ng = (int)((w.k + w.g - 1) / w.g);
+    if (m == 1) {
+        if (ng > 8192) return hipErrorInvalidValue;  // one row's group terms must fit in LDS
+        // rows per workgroup: the group terms in <= 32 KB of LDS, and enough
+        // workgroups to spread over the CUs
+        int rb = (int)std::min<size_t>(64, std::max<size_t>(1, 8192 / (size_t)std::max(ng, 1)));
+        while (rb > 8 && (w.n + rb - 1) / rb < 512) rb /= 2;
+        const unsigned grid = (unsigned)((w.n + rb - 1) / rb);
+        const size_t cgb = (((size_t)rb * ng + 3) & ~(size_t)3) * sizeof(float);
+        const size_t asb = (w.k / 32) * 36 * sizeof(float);
+        const bool vec = w.k % 32 == 0 && (w.g == 32 || w.g == 64) && cgb + asb <= 64 * 1024;
+        if (vec && w.g == 32)
+            q4a_gemv_kernel<1><<<dim3(grid), dim3(QT), cgb + asb, s>>>(w.q4raw, w.rpitch, w.q4a_sm, (int)w.n,
+                                                                      (int)w.k, (int)w.g, rb, a, out);
+        else if (vec)
+            q4a_gemv_kernel<2><<<dim3(grid), dim3(QT), cgb + asb, s>>>(w.q4raw, w.rpitch, w.q4a_sm, (int)w.n,
+                                                                      (int)w.k, (int)w.g, rb, a, out);
+        else
+            q4a_gemv_kernel<0><<<dim3(grid), dim3(QT), cgb, s>>>(w.q4raw, w.rpitch, w.q4a_sm, (int)w.n, (int)w.k,
+                                                                (int)w.g, rb, a, out);
+        return hipGetLastError();
+    }
+    dim3 grid((unsigned)((w.n + QT - 1) / QT), (unsigned)((m + 15) / 16));
+    q4a_gemm_rows<16><<<grid, dim3(QT), 0, s>>>(w.q4raw, w.rpitch, w.q4a_sm, (int)w.n, (int)w.k, (int)w.g, a, (int)m,
+                                                 out);
+    return hipGetLastError();
+}
+
+}  // namespace frq

@@ -52,7 +52,8 @@ enum {
     FRQ_DT_I4 = 2,    /* group-wise int4 linear weight (W4A32)            */
     FRQ_DT_F32 = 3,   /* row-major f32 rows (embed / unembed)             */
     FRQ_DT_F16 = 4,   /* row-major f16 rows                               */
-    FRQ_DT_ROWI8 = 5  /* row-major int8 rows + f32 scale per row          */
+    FRQ_DT_ROWI8 = 5, /* row-major int8 rows + f32 scale per row          */
+    FRQ_DT_Q4A = 6    /* group-wise affine int4 linear (W4A32, scale+min) */
 };
 enum { FRQ_ACT_SILU = 0, FRQ_ACT_GELU_TANH = 1 };
 
@@ -99,6 +100,13 @@ frq_w* frq_upload_i8_bundle(frq_ctx* ctx, const int8_t* w_kn,
  * 50-56, 356-360; src/convert.rs:189-216). */
 frq_w* frq_upload_i4(frq_ctx* ctx, const uint8_t* packed,
                      const uint16_t* scale_f16, size_t n, size_t k, size_t g);
+/* Group-wise affine int4 (q4a) weight as stored: packed (N, ceil(K/2))
+ * unsigned nibbles (even input index low) and f16 scale and min, each
+ * (N, ceil(K/g)); w = scale*q + min (src/bundle.rs:68-77, 361-364;
+ * src/convert.rs:223-260).  frq_mm runs the Q4A arm of Bundle::mm
+ * (802-845): M == 1 in q4a_dot_avx2's order, M > 1 dequantise + GEMM. */
+frq_w* frq_upload_q4a(frq_ctx* ctx, const uint8_t* packed, const uint16_t* scale_f16,
+                      const uint16_t* min_f16, size_t n, size_t k, size_t g);
 /* Row-major (rows, d) embedding/unembedding table as stored: FRQ_DT_F32
  * (float data), FRQ_DT_F16 (uint16_t f16 bits) or FRQ_DT_ROWI8 (int8 data
  * plus scale[rows], the f32 upcast of the `__scale` sibling that

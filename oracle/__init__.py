@@ -55,6 +55,10 @@ def _load():
         "fro_layernorm": (None, [P, S, S, P, P, P]),
         "fro_nd_sum": (F, [P, S]),
         "fro_libm_f32": (None, [I, P, S, P]),
+        "fro_put_q4a": (S, [P, S, S, I, P, P, P]),
+        "fro_q4a_dot": (F, [P, P, P, P, S, S]),
+        "fro_q4a_dot_avx2": (F, [P, P, P, P, S, S]),
+        "fro_mm_q4a": (I, [P, S, S, P, P, P, S, S, P]),
         "fro_gpt2_generate": (I, [P, P, S, S, I, I, P, P]),
         "fro_gpt2_predict": (I, [P, P, S, I, P, P]),
     }
@@ -393,4 +397,41 @@ def libm_f32(fn: str, x) -> np.ndarray:
     x = _c(x, np.float32)
     out = np.empty_like(x)
     lib.fro_libm_f32({"expf": 0, "expm1f": 1, "tanhf": 2}[fn], _p(x), x.size, _p(out))
+    return out
+
+
+# ---- affine int4 (q4a) ----
+def put_q4a(data: np.ndarray, transpose: bool):
+    """put_q4a (src/convert.rs:223-260): (packed (out, ceil(in/2)) u8,
+    scale f16 bits, min f16 bits (out, ng), g)."""
+    data = _c(data, np.float32)
+    rows, cols = data.shape
+    out, inp = (rows, cols) if transpose else (cols, rows)
+    g = min(32, max(inp, 1))
+    ng = (inp + g - 1) // g
+    packed = np.empty((out, (inp + 1) // 2), np.uint8)
+    s16 = np.empty((out, ng), np.uint16)
+    m16 = np.empty((out, ng), np.uint16)
+    g = lib.fro_put_q4a(_p(data), rows, cols, int(transpose), _p(packed), _p(s16), _p(m16))
+    return packed, s16, m16, g
+
+
+def q4a_dot(prow, a, scale, mins, g, k):
+    return lib.fro_q4a_dot(_p(_c(prow, np.uint8)), _p(_c(a, np.float32)), _p(_c(scale, np.float32)),
+                           _p(_c(mins, np.float32)), g, k)
+
+
+def q4a_dot_avx2(prow, a, scale, mins, g, k):
+    return lib.fro_q4a_dot_avx2(_p(_c(prow, np.uint8)), _p(_c(a, np.float32)), _p(_c(scale, np.float32)),
+                                _p(_c(mins, np.float32)), g, k)
+
+
+def mm_q4a(a, packed, scale_f32, min_f32, k, g):
+    """Bundle::mm's Q4A arm: a (M, K) f32 -> (M, N)."""
+    a = _c(a, np.float32)
+    packed = _c(packed, np.uint8)
+    n = packed.shape[0]
+    out = np.empty((a.shape[0], n), np.float32)
+    lib.fro_mm_q4a(_p(a), a.shape[0], k, _p(packed), _p(_c(scale_f32, np.float32)), _p(_c(min_f32, np.float32)),
+                   n, g, _p(out))
     return out

@@ -870,3 +870,126 @@ int fro_gpt2_predict(const fro_gpt2_t* g, const int64_t* ids, size_t n, int nthr
 void fro_libm_f32(int fn, const float* x, size_t n, float* out) {
     for (size_t i = 0; i < n; i++) out[i] = fn == 0 ? expf(x[i]) : (fn == 1 ? expm1f(x[i]) : tanhf(x[i]));
 }
+
+/* ------------------------------------------------------------------------ */
+/* Affine int4 (q4a): w = scale*q + min, q an unsigned nibble                */
+/* ------------------------------------------------------------------------ */
+static unsigned nib_u4(const uint8_t* prow, size_t i) {
+    uint8_t b = prow[i / 2];
+    return (i % 2 == 0) ? (b & 0x0Fu) : (b >> 4);
+}
+
+/* put_q4a: src/convert.rs:223-260.  g = min(Q4A_GROUP = 32, in) (33-36);
+ * per (out j, group): mn / mx folds from +-inf, scale = max((mx - mn) / 15,
+ * 1e-8), min = mn; q = clamp(round_ties_even((v - min) / scale), 0, 15)
+ * from the f32 scale / min; scale and min stored f16 (put_f16, RNE). */
+size_t fro_put_q4a(const float* data, size_t rows, size_t cols, int transpose, uint8_t* packed,
+                   uint16_t* scale_f16, uint16_t* min_f16) {
+    size_t out = transpose ? rows : cols, inp = transpose ? cols : rows;
+#define AT(i, j) (transpose ? data[(j) * inp + (i)] : data[(i) * out + (j)])
+    size_t g = 32 < nz(inp) ? 32 : nz(inp);
+    size_t ng = (inp + g - 1) / g, rb = (inp + 1) / 2;
+    float* sc = (float*)malloc(nz(out * ng) * sizeof(float));
+    float* mnv = (float*)malloc(nz(out * ng) * sizeof(float));
+    for (size_t j = 0; j < out; j++)
+        for (size_t gi = 0; gi < ng; gi++) {
+            size_t lo = gi * g, hi = (gi + 1) * g < inp ? (gi + 1) * g : inp;
+            float mn = INFINITY, mx = -INFINITY;
+            for (size_t i = lo; i < hi; i++) { mn = fminf(mn, AT(i, j)); mx = fmaxf(mx, AT(i, j)); }
+            float s = (mx - mn) / 15.0f;
+            sc[j * ng + gi] = fmaxf(s, 1e-8f);
+            mnv[j * ng + gi] = mn;
+        }
+    memset(packed, 0, out * rb);
+    for (size_t j = 0; j < out; j++)
+        for (size_t i = 0; i < inp; i++) {
+            size_t gi = j * ng + i / g;
+            uint8_t q = (uint8_t)clampf(round_ties_even((AT(i, j) - mnv[gi]) / sc[gi]), 0.0f, 15.0f);
+            packed[j * rb + i / 2] |= (i % 2 == 0) ? q : (uint8_t)(q << 4);
+        }
+    for (size_t i = 0; i < out * ng; i++) {
+        scale_f16[i] = fro_f32_to_f16(sc[i]);
+        min_f16[i] = fro_f32_to_f16(mnv[i]);
+    }
+    free(sc);
+    free(mnv);
+    return g;
+#undef AT
+}
+
+/* q4a_dot, the scalar form (src/bundle.rs:118-143): per group qsum += a*q,
+ * asum += a; sum += scale*qsum + min*asum. */
+float fro_q4a_dot(const uint8_t* prow, const float* a, const float* scale, const float* mins, size_t g, size_t k) {
+    float sum = 0.0f;
+    size_t gi = 0, kk = 0;
+    while (kk < k) {
+        size_t hi = kk + g < k ? kk + g : k;
+        float qsum = 0.0f, asum = 0.0f;
+        for (; kk < hi; kk++) {
+            qsum = qsum + a[kk] * (float)nib_u4(prow, kk);
+            asum = asum + a[kk];
+        }
+        sum = sum + (scale[gi] * qsum + mins[gi] * asum);
+        gi++;
+    }
+    return sum;
+}
+
+/* q4a_dot_avx2 (src/bundle.rs:231-258), the x86 production order (dispatch
+ * 121-124): per group two sets of 8 lane accumulators, q lanes an FMA chain
+ * (q * a), a lanes an add chain, over the 8-nibble chunks read from byte
+ * kk/2 (unpack8_nibbles); each set through hsum256; a mul+add tail; then
+ * sum += scale*qsum + min*asum. */
+float fro_q4a_dot_avx2(const uint8_t* prow, const float* a, const float* scale, const float* mins, size_t g,
+                       size_t k) {
+    float sum = 0.0f;
+    size_t gi = 0, kk = 0;
+    while (kk < k) {
+        size_t hi = kk + g < k ? kk + g : k;
+        float l[8] = {0, 0, 0, 0, 0, 0, 0, 0}, m[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        while (kk + 8 <= hi) {
+            size_t base = (kk / 2) * 2;
+            for (int q = 0; q < 8; q++) {
+                l[q] = fmaf((float)nib_u4(prow, base + (size_t)q), a[kk + (size_t)q], l[q]);
+                m[q] = m[q] + a[kk + (size_t)q];
+            }
+            kk += 8;
+        }
+        float qsum = ((l[0] + l[4]) + (l[2] + l[6])) + ((l[1] + l[5]) + (l[3] + l[7]));
+        float asum = ((m[0] + m[4]) + (m[2] + m[6])) + ((m[1] + m[5]) + (m[3] + m[7]));
+        for (; kk < hi; kk++) {
+            qsum = qsum + a[kk] * (float)nib_u4(prow, kk);
+            asum = asum + a[kk];
+        }
+        sum = sum + (scale[gi] * qsum + mins[gi] * asum);
+        gi++;
+    }
+    return sum;
+}
+
+/* Bundle::mm Q4A arm: src/bundle.rs:802-845.  M==1 -> q4a_dot per output
+ * column (AVX2 order); M>1 -> w[kk,col] = scale*q + min (f32, mul then
+ * add, 826-829) then a.dot(w) (the sequential-k FMA order of fro_sgemm). */
+int fro_mm_q4a(const float* a, size_t m, size_t k, const uint8_t* packed, const float* scale, const float* mins,
+               size_t n, size_t g, float* out) {
+    size_t ng = (k + g - 1) / g, rb = (k + 1) / 2;
+    if (m == 1) {
+        for (size_t j = 0; j < n; j++)
+            out[j] = fro_q4a_dot_avx2(packed + j * rb, a, scale + j * ng, mins + j * ng, g, k);
+        return FRO_OK;
+    }
+    float* wcol = (float*)malloc(nz(k) * sizeof(float));
+    for (size_t j = 0; j < n; j++) {
+        for (size_t kk = 0; kk < k; kk++) {
+            size_t gi = j * ng + kk / g;
+            wcol[kk] = scale[gi] * (float)nib_u4(packed + j * rb, kk) + mins[gi];
+        }
+        for (size_t i = 0; i < m; i++) {
+            float acc = 0.0f;
+            for (size_t kk = 0; kk < k; kk++) acc = fmaf(a[i * k + kk], wcol[kk], acc);
+            out[i * n + j] = acc;
+        }
+    }
+    free(wcol);
+    return FRO_OK;
+}

@@ -25,6 +25,12 @@
  *   fro_i4_dot / fro_i4_dot_avx2      reference KATs i4_q4a_dot_matches_manual
  *                                     (=1.0), i4_q4a_dot_simd_vs_reference,
  *                                     jit LCG vectors + f64 brute force
+ *   fro_q4a_dot / _avx2 / fro_mm_q4a  reference KATs i4_q4a_dot_matches_manual
+ *                                     (=12.5) and i4_q4a_dot_simd_vs_reference,
+ *                                     f64 brute force, exact small-integer
+ *                                     cases, hand-derived lane-order case;
+ *                                     fro_put_q4a by closed forms (min/max
+ *                                     nibbles, reconstruction bound)
  *   fro_mm_i4 (M>1), fro_expert_mm    f64 brute force only; the reference
  *                                     has no test for these (its sgemm order
  *                                     is matrixmultiply's): tolerance parity
@@ -102,6 +108,16 @@ float fro_i4_dot_avx2(const uint8_t* prow, const float* a, const float* scale,
  * packed (N, ceil(K/2)), scale f32 (N, ceil(K/g)). */
 int fro_mm_i4(const float* a, size_t m, size_t k, const uint8_t* packed,
               const float* scale, size_t n, size_t g, float* out);
+
+/* Affine int4 (q4a): packed (N, ceil(K/2)) unsigned nibbles, scale and min
+ * (N, ceil(K/g)).  put_q4a returns g (min(32, in)). */
+size_t fro_put_q4a(const float* data, size_t rows, size_t cols, int transpose, uint8_t* packed,
+                   uint16_t* scale_f16, uint16_t* min_f16);
+float fro_q4a_dot(const uint8_t* prow, const float* a, const float* scale, const float* mins, size_t g, size_t k);
+float fro_q4a_dot_avx2(const uint8_t* prow, const float* a, const float* scale, const float* mins, size_t g,
+                       size_t k);
+int fro_mm_q4a(const float* a, size_t m, size_t k, const uint8_t* packed, const float* scale, const float* mins,
+               size_t n, size_t g, float* out);
 
 /* expert_f32 (i8 arm) + expert_mm: raw (in,out) i8, scale f32 [out]. */
 void fro_expert_mm_i8(const float* x, size_t m, const int8_t* raw,

@@ -502,3 +502,90 @@ def test_rowdot_empty_rows_keep_the_fold_sign():
     assert np.all(got == 0) and not np.any(np.signbit(got))
     sub = oracle.rowdot_f32_subset("rowi8", np.zeros((2, 0), np.int8), x, [1], sc)
     assert sub[0] == 0 and np.signbit(sub[0])
+
+
+# ---- affine int4 (q4a): src/bundle.rs:118-143, 231-258, 802-845; convert.rs:223-260 ----
+def test_q4a_dot_kats():
+    k = KATS["i4_q4a_dot_matches_manual"]   # unsigned nibbles [1, 14, 3, 15], w = 0.5 q - 1
+    for f in (oracle.q4a_dot, oracle.q4a_dot_avx2):
+        got = f(np.array(k["prow"], np.uint8), np.array(k["a"], np.float32), np.array(k["q4a_scale"], np.float32),
+                np.array(k["q4a_min"], np.float32), k["g"], k["k"])
+        assert abs(got - k["want_q4a"]) < k["q4a_tol"]
+        assert got == 12.5   # every step is exact here
+    k = KATS["i4_q4a_dot_simd_vs_reference"]
+    kk, g = k["k"], k["g"]
+    ng = (kk + g - 1) // g
+    nibs = np.array([((i * 7 + 3) % 16) - 8 for i in range(kk)], np.int64)
+    prow = pack_nibbles(nibs)
+    a = np.sin(np.arange(kk, dtype=np.float32) * np.float32(0.13) - np.float32(2.0)).astype(np.float32)
+    scale = (np.float32(0.1) + np.arange(ng, dtype=np.float32) * np.float32(0.05)).astype(np.float32)
+    mins = (np.float32(-0.3) + np.arange(ng, dtype=np.float32) * np.float32(0.1)).astype(np.float32)
+    u = nibs & 0xF
+    want = float((a.astype(np.float64) * (scale[np.arange(kk) // g] * u + mins[np.arange(kk) // g])).sum())
+    for f in (oracle.q4a_dot, oracle.q4a_dot_avx2):
+        assert abs(f(prow, a, scale, mins, g, kk) - want) < k["tol"]
+
+
+def test_q4a_dot_avx2_lane_order():
+    # one group of 16, every nibble 1, scale 1, min 0; a0 = 2^24, a1 = a5 = 1.
+    # The AVX2 order puts a1 and a5 in lanes 1 and 5: (l1 + l5) = 2 and
+    # 2^24 + 2 is exact.  The scalar fold adds them to 2^24 one at a time and
+    # loses both (2^24 + 1 ties to even, 2^24).
+    a = np.zeros(16, np.float32)
+    a[0], a[1], a[5] = 2.0 ** 24, 1.0, 1.0
+    prow = pack_nibbles(np.ones(16, np.int64))
+    one, zero = np.ones(1, np.float32), np.zeros(1, np.float32)
+    assert oracle.q4a_dot_avx2(prow, a, one, zero, 16, 16) == 2.0 ** 24 + 2
+    assert oracle.q4a_dot(prow, a, one, zero, 16, 16) == 2.0 ** 24
+    # a group of 13 starting at an odd k: the chunk reads nibbles from byte kk / 2
+    # (so from k - 1), as unpack8_nibbles does; then a 5-element tail
+    k, g = 26, 13
+    rng = np.random.default_rng(3)
+    q = rng.integers(0, 16, k)
+    a = rng.integers(-4, 5, k).astype(np.float32)
+    prow = pack_nibbles(q)
+    s, m = np.array([0.5, 0.25], np.float32), np.array([1.0, -2.0], np.float32)
+    # group 1 (k = 13..25): chunk k = 13..20 pairs a[13+i] with nibble 12+i
+    qs = sum(a[13 + i] * q[12 + i] for i in range(8)) + sum(a[21 + i] * q[21 + i] for i in range(5))
+    as_ = a[13:].sum()
+    g0 = (a[:8] * q[:8]).sum() + (a[8:13] * q[8:13]).sum()
+    want = np.float32(0.5 * g0 + 1.0 * a[:13].sum()) + np.float32(0.25 * qs - 2.0 * as_)
+    assert oracle.q4a_dot_avx2(prow, a, s, m, g, k) == want     # small integers: every step exact
+
+
+def test_q4a_exact_small_integers_and_gemm():
+    rng = np.random.default_rng(7)
+    n, k, g = 24, 96, 32
+    q = rng.integers(0, 16, (n, k))
+    packed = pack_nibbles(q)
+    s = (2.0 ** rng.integers(-3, 2, (n, k // g))).astype(np.float32)
+    m = rng.integers(-4, 4, (n, k // g)).astype(np.float32)
+    a = rng.integers(-8, 9, (3, k)).astype(np.float32)
+    w = s[:, np.arange(k) // g] * q + m[:, np.arange(k) // g]          # exact
+    want = a.astype(np.float64) @ w.T.astype(np.float64)
+    for mm in (1, 3):
+        assert np.array_equal(oracle.mm_q4a(a[:mm], packed, s, m, k, g), want[:mm].astype(np.float32))
+
+
+def test_put_q4a_closed_forms():
+    from fieldrun_amd import convert
+    rng = np.random.default_rng(5)
+    w = (rng.standard_normal((40, 70)) * 0.1).astype(np.float32)        # (out, in)
+    packed, s16, m16, g = oracle.put_q4a(w, True)
+    assert g == 32 and packed.shape == (40, 35) and s16.shape == (40, 3)
+    q = np.stack([packed & 15, packed >> 4], axis=2).reshape(40, -1)[:, :70].astype(np.int64)
+    for j in range(40):
+        for gi in range(3):
+            seg = w[j, gi * 32:(gi + 1) * 32]
+            qs = q[j, gi * 32:(gi + 1) * 32]
+            assert qs[np.argmin(seg)] == 0 and qs[np.argmax(seg)] == 15   # the ends map to 0 and 15
+            sc = max((np.float32(seg.max()) - np.float32(seg.min())) / np.float32(15), np.float32(1e-8))
+            assert s16.view(np.float16)[j, gi] == np.float16(sc)
+            assert m16.view(np.float16)[j, gi] == np.float16(seg.min())
+            assert np.abs(sc * qs + seg.min() - seg).max() <= sc * 0.5001
+    # the package's numpy quantiser writes the same bytes
+    p2, s2, m2, g2 = convert.put_q4a(w, True)
+    assert g2 == g and np.array_equal(p2, packed)
+    assert np.array_equal(s2.view(np.uint16), s16) and np.array_equal(m2.view(np.uint16), m16)
+    p3, s3, m3, _ = convert.put_q4a(np.ascontiguousarray(w.T), False)
+    assert np.array_equal(p3, packed) and np.array_equal(s3, s2) and np.array_equal(m3, m2)
