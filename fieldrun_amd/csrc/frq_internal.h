@@ -107,6 +107,42 @@ __device__ __forceinline__ float h2f(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);
 }
 
+// acc + p[0] + p[1] + ... + p[n-1] in index order, in the calling lane,
+// over LDS (p 16-byte aligned): loads run one 32-value batch ahead of the
+// adds (unconditional, the index clamped to the last batch) so the chain
+// waits on the adds, not on LDS latency.
+__device__ inline float lds_seq_sum(const float* p, int n, float acc) {
+    constexpr int B = 8;  // float4 per batch
+    const int nb = n / (4 * B);
+    const float4* p4 = reinterpret_cast<const float4*>(p);
+    float4 b0[B], b1[B];
+    auto ld = [&](float4 (&b)[B], int k) {
+#pragma unroll
+        for (int u = 0; u < B; ++u) b[u] = p4[k * B + u];
+    };
+    auto add = [&](const float4 (&b)[B]) {
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+            acc = acc + b[u].x;
+            acc = acc + b[u].y;
+            acc = acc + b[u].z;
+            acc = acc + b[u].w;
+        }
+    };
+    if (nb > 0) {
+        ld(b0, 0);
+        ld(b1, min(1, nb - 1));
+        for (int k = 0; k < nb; k += 2) {
+            add(b0);
+            ld(b0, min(k + 2, nb - 1));
+            if (k + 1 < nb) add(b1);
+            ld(b1, min(k + 3, nb - 1));
+        }
+    }
+    for (int i = nb * 4 * B; i < n; ++i) acc = acc + p[i];
+    return acc;
+}
+
 // ---- weights -------------------------------------------------------------
 struct Weight {
     int dtype = 0;           // FRQ_DT_*
@@ -209,6 +245,9 @@ hipError_t launch_rowdot_argmax(const Weight& w, const float* x, float* out, uns
 hipError_t launch_i4(const Weight& w, size_t m, const float* a, float* out,
                      float* wsf, unsigned* tickets, hipStream_t s);
 size_t i4_ws_floats(const Weight& w, size_t m);
+// int4 at M == 1 in i4_dot_avx2's order (bit-exact) with coalesced loads, for
+// K % 32 == 0 and g in {32, 64}; hipErrorNotSupported for other shapes.
+hipError_t launch_i4_terms(const Weight& w, const float* a, float* out, hipStream_t s);
 // int4 (N, K/2) -> the MFMA layout (g == 32, K % 32 == 0); bytes of q4.
 size_t i4_blocked_bytes(size_t n, size_t k);
 hipError_t launch_i4_block(const uint8_t* raw, const uint16_t* sraw, size_t n,

@@ -74,41 +74,6 @@ __global__ __launch_bounds__(NT) void embed_kernel(const uint8_t* __restrict__ w
     for (int c = threadIdx.x; c < d; c += NT) x[(size_t)t * d + c] = h2f(row[c]) + pe[c];
 }
 
-// acc + p[0] + p[1] + ... + p[n-1] in index order, in the calling lane,
-// over LDS (p 16-byte aligned): loads run one 32-value batch ahead of the
-// adds (unconditional, the index clamped to the last batch) so the chain
-// waits on the adds, not on LDS latency.
-__device__ float seq_sum(const float* p, int n, float acc) {
-    constexpr int B = 8;  // float4 per batch
-    const int nb = n / (4 * B);
-    const float4* p4 = reinterpret_cast<const float4*>(p);
-    float4 b0[B], b1[B];
-    auto ld = [&](float4 (&b)[B], int k) {
-#pragma unroll
-        for (int u = 0; u < B; ++u) b[u] = p4[k * B + u];
-    };
-    auto add = [&](const float4 (&b)[B]) {
-#pragma unroll
-        for (int u = 0; u < B; ++u) {
-            acc = acc + b[u].x;
-            acc = acc + b[u].y;
-            acc = acc + b[u].z;
-            acc = acc + b[u].w;
-        }
-    };
-    if (nb > 0) {
-        ld(b0, 0);
-        ld(b1, min(1, nb - 1));
-        for (int k = 0; k < nb; k += 2) {
-            add(b0);
-            ld(b0, min(k + 2, nb - 1));
-            if (k + 1 < nb) add(b1);
-            ld(b1, min(k + 3, nb - 1));
-        }
-    }
-    for (int i = nb * 4 * B; i < n; ++i) acc = acc + p[i];
-    return acc;
-}
 // The same over p[0], p[8], p[16], ... (n values): one of ndarray's eight
 // partial sums.
 __device__ float seq_sum8(const float* p, int n, float acc) {
@@ -179,7 +144,7 @@ __global__ __launch_bounds__(NT) void resid_ln_kernel(float* __restrict__ x, con
     const float mu = stat[0];
     for (int c = threadIdx.x; c < d; c += NT) sq[c] = (xs[c] - mu) * (xs[c] - mu);
     __syncthreads();
-    if (threadIdx.x == 0) stat[1] = seq_sum(sq, d, -0.0f) / (float)d;
+    if (threadIdx.x == 0) stat[1] = lds_seq_sum(sq, d, -0.0f) / (float)d;
     __syncthreads();
     const float inv = 1.0f / sqrtf(stat[1] + 1e-5f);
     for (int c = threadIdx.x; c < d; c += NT) out[r + c] = (xs[c] - mu) * inv * g[c] + b[c];
@@ -319,7 +284,7 @@ __global__ __launch_bounds__(NT) void attn_kernel(const float* __restrict__ qkv,
     if (nk < cur + (int)gridDim.y) mx = fmaxf(mx, -1e10f);  // a masked entry joins the max
     for (int j = threadIdx.x; j < nk; j += NT) p[j] = libm::frq_expf(p[j] - mx);
     __syncthreads();
-    if (threadIdx.x == 0) red[0] = seq_sum(p, nk, 0.0f);  // masked exps are +0
+    if (threadIdx.x == 0) red[0] = lds_seq_sum(p, nk, 0.0f);  // masked exps are +0
     __syncthreads();
     const float sum = red[0];
     for (int j = threadIdx.x; j < nk; j += NT) p[j] = p[j] / sum;

@@ -90,6 +90,71 @@ __global__ void i4_gemv_generic(const uint8_t* __restrict__ packed,
     out[j] = sum;
 }
 
+// M == 1 in i4_dot_avx2's order, fast: a group's term scale * gsum is
+// independent of the others until the in-order sum, so a thread takes one
+// (row, group) at a time (adjacent threads adjacent groups: the G4 16-byte
+// nibble loads and the f16 scales arrive coalesced), the activations come
+// from the workgroup's LDS copy (padded 4 floats per 32 against bank
+// conflicts), and one lane per row adds its row's terms in order.  Needs
+// K % 32 == 0 (16-byte aligned rows) and g == 32 G4.
+template <int G4>
+__global__ __launch_bounds__(256) void i4_gemv_terms(const uint8_t* __restrict__ packed,
+                                                     const uint16_t* __restrict__ scale, int N, int K, int rb,
+                                                     const float* __restrict__ a, float* __restrict__ out) {
+    extern __shared__ float4 lds4[];
+    float* cg = reinterpret_cast<float*>(lds4);
+    constexpr int g = 32 * G4;
+    const int ng = K / g, pitch = K / 2;
+    const int r0 = blockIdx.x * rb;
+    const int nr = min(rb, N - r0);
+    const int items = nr * ng;
+    const int ngp = (ng + 3) & ~3;  // row stride of the terms: 16-byte aligned rows
+    float* as = cg + rb * ngp;
+    for (int i = threadIdx.x; i < K / 4; i += 256)
+        *reinterpret_cast<float4*>(as + (4 * i) / 32 * 36 + (4 * i) % 32) = reinterpret_cast<const float4*>(a)[i];
+    __syncthreads();
+    // the next item's nibbles and scale load while this one computes (the
+    // index clamped to the last item, so every load is unconditional)
+    auto fetch = [&](int p, uint4 (&w)[G4], float& sc) {
+        const int r = p / ng, gi = p - r * ng;
+        const uint8_t* pg = packed + (size_t)(r0 + r) * pitch + (size_t)gi * 16 * G4;
+#pragma unroll
+        for (int h = 0; h < G4; ++h) w[h] = *reinterpret_cast<const uint4*>(pg + 16 * h);
+        sc = h2f(scale[(size_t)(r0 + r) * ng + gi]);
+    };
+    if (threadIdx.x < items) {
+        uint4 wn[G4];
+        float sn;
+        fetch(threadIdx.x, wn, sn);
+        for (int p = threadIdx.x; p < items; p += 256) {
+            uint4 wc[G4];
+#pragma unroll
+            for (int h = 0; h < G4; ++h) wc[h] = wn[h];
+            const float sc = sn;
+            fetch(min(p + 256, items - 1), wn, sn);
+            const int rr = p / ng, gi = p - rr * ng;
+            float l[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+            for (int h = 0; h < G4; ++h) {
+                const uint32_t ws[4] = {wc[h].x, wc[h].y, wc[h].z, wc[h].w};
+                const float* ab = as + (gi * g + 32 * h) / 32 * 36;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const float4 a0 = *reinterpret_cast<const float4*>(ab + 8 * c);
+                    const float4 a1 = *reinterpret_cast<const float4*>(ab + 8 * c + 4);
+                    const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) l[q] = __builtin_fmaf(s4f(ws[c], q), av[q], l[q]);
+                }
+            }
+            const float q0 = l[0] + l[4], q1 = l[1] + l[5], q2 = l[2] + l[6], q3 = l[3] + l[7];
+            cg[rr * ngp + gi] = sc * ((q0 + q2) + (q1 + q3));
+        }
+    }
+    __syncthreads();
+    for (int r = threadIdx.x; r < nr; r += 256) out[r0 + r] = lds_seq_sum(cg + r * ngp, ng, 0.0f);
+}
+
 // M > 1: dequantise w = s4 * scale (f32, exact) and run a sequential-k FMA
 // chain per output (the oracle's sgemm order).  One thread per column j and
 // up to 16 token rows; the token rows' activations are uniform across the
@@ -667,10 +732,32 @@ static hipError_t launch_fused(const Weight& w, size_t m, const float* a, float*
     }
 }
 
+// The exact M == 1 kernel when the shape allows it (else hipErrorNotSupported).
+hipError_t launch_i4_terms(const Weight& w, const float* a, float* out, hipStream_t s) {
+    if (w.k % 32 || (w.g != 32 && w.g != 64) || w.k > (size_t)INT32_MAX || w.n > (size_t)INT32_MAX)
+        return hipErrorNotSupported;
+    const int ng = (int)(w.k / w.g);
+    int rb = std::min(64, std::max(1, 8192 / std::max(ng, 1)));
+    while (rb > 8 && (w.n + rb - 1) / rb < 512) rb /= 2;
+    const size_t cgb = (size_t)rb * ((ng + 3) & ~3) * sizeof(float);
+    const size_t asb = (w.k / 32) * 36 * sizeof(float);
+    if (cgb + asb > 64 * 1024) return hipErrorNotSupported;
+    const unsigned grid = (unsigned)((w.n + rb - 1) / rb);
+    if (w.g == 32)
+        i4_gemv_terms<1><<<dim3(grid), dim3(256), cgb + asb, s>>>(w.q4raw, w.s4raw, (int)w.n, (int)w.k, rb, a, out);
+    else
+        i4_gemv_terms<2><<<dim3(grid), dim3(256), cgb + asb, s>>>(w.q4raw, w.s4raw, (int)w.n, (int)w.k, rb, a, out);
+    return hipGetLastError();
+}
+
 hipError_t launch_i4(const Weight& w, size_t m, const float* a, float* out,
                      float* wsf, unsigned* tickets, hipStream_t s) {
     (void)tickets;
     if (m == 0) return hipSuccess;
+    if (m == 1) {  // the reference's decode order, bit for bit, where the shape allows
+        const hipError_t e = launch_i4_terms(w, a, out, s);
+        if (e != hipErrorNotSupported) return e;
+    }
     if (w.i4_blocked && fused_fits(w.k, m)) return launch_fused(w, m, a, out, s);
     if (w.i4_blocked && mfma_fits(w.k, m)) {
         const size_t mp = round_up(m, 4), ng4 = (w.k / 32 + 3) / 4;

@@ -54,18 +54,17 @@ __device__ __forceinline__ float q4a_group(const uint8_t* __restrict__ prow, con
     return h2f((uint16_t)(sm & 0xffffu)) * qsum + h2f((uint16_t)(sm >> 16)) * asum;
 }
 
-// The same for a group of 32 * G4 nibbles whose bytes start 16-byte
-// aligned, from registers: G4 16-byte loads of nibbles, the activations from
+// The same for a group of 32 * G4 nibbles held in registers (G4 16-byte
+// words, loaded by the caller), the activations from
 // the workgroup's LDS copy (as, padded 4 floats per 32 so the lanes, which
 // take adjacent groups, fall on different banks).
 template <int G4>
-__device__ __forceinline__ float q4a_group_vec(const uint8_t* __restrict__ pg, const float* __restrict__ as, int k0,
+__device__ __forceinline__ float q4a_group_vec(const uint4 (&wv)[G4], const float* __restrict__ as, int k0,
                                                uint32_t sm) {
     float l[8] = {0, 0, 0, 0, 0, 0, 0, 0}, m[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
     for (int h = 0; h < G4; ++h) {
-        const uint4 w4 = *reinterpret_cast<const uint4*>(pg + 16 * h);
-        const uint32_t ws[4] = {w4.x, w4.y, w4.z, w4.w};
+        const uint32_t ws[4] = {wv[h].x, wv[h].y, wv[h].z, wv[h].w};
         const float* ab = as + (k0 + 32 * h) / 32 * 36;  // 32 activations at a 36-float stride
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
@@ -98,32 +97,45 @@ __global__ __launch_bounds__(QT) void q4a_gemv_kernel(const uint8_t* __restrict_
     const int r0 = blockIdx.x * rb;
     const int nr = min(rb, N - r0);
     const int items = nr * ng;
+    const int ngp = (ng + 3) & ~3;  // row stride of the terms: 16-byte aligned rows
     if constexpr (G4 > 0) {
-        float* as = cg + ((rb * ng + 3) & ~3);
+        float* as = cg + rb * ngp;
         for (int i = threadIdx.x; i < K / 4; i += QT)
             *reinterpret_cast<float4*>(as + (4 * i) / 32 * 36 + (4 * i) % 32) = reinterpret_cast<const float4*>(a)[i];
         __syncthreads();
-        for (int p = threadIdx.x; p < items; p += QT) {
+        // the next item's nibbles and scale / min load while this one
+        // computes (the index clamped to the last item: unconditional loads)
+        auto fetch = [&](int p, uint4 (&w)[G4], uint32_t& s) {
             const int r = p / ng, gi = p - r * ng;
-            const int j = r0 + r;
-            cg[p] = q4a_group_vec<G4>(packed + (size_t)j * pitch + (size_t)gi * 16 * G4, as, gi * g,
-                                      sm[(size_t)j * ng + gi]);
+            const uint8_t* pg = packed + (size_t)(r0 + r) * pitch + (size_t)gi * 16 * G4;
+#pragma unroll
+            for (int h = 0; h < G4; ++h) w[h] = *reinterpret_cast<const uint4*>(pg + 16 * h);
+            s = sm[(size_t)(r0 + r) * ng + gi];
+        };
+        if ((int)threadIdx.x < items) {
+            uint4 wn[G4];
+            uint32_t sn;
+            fetch(threadIdx.x, wn, sn);
+            for (int p = threadIdx.x; p < items; p += QT) {
+                uint4 wc[G4];
+#pragma unroll
+                for (int h = 0; h < G4; ++h) wc[h] = wn[h];
+                const uint32_t sc = sn;
+                fetch(min(p + QT, items - 1), wn, sn);
+                const int rr = p / ng, gi = p - rr * ng;
+                cg[rr * ngp + gi] = q4a_group_vec<G4>(wc, as, gi * g, sc);
+            }
         }
     } else {
         for (int p = threadIdx.x; p < items; p += QT) {
             const int r = p / ng, gi = p - r * ng;
             const int j = r0 + r;
             const int kk = gi * g, hi = min(kk + g, K);
-            cg[p] = q4a_group(packed + (size_t)j * pitch, a, kk, hi, sm[(size_t)j * ng + gi]);
+            cg[r * ngp + gi] = q4a_group(packed + (size_t)j * pitch, a, kk, hi, sm[(size_t)j * ng + gi]);
         }
     }
     __syncthreads();
-    for (int r = threadIdx.x; r < nr; r += QT) {
-        float sum = 0.0f;
-        const float* c = cg + r * ng;
-        for (int gi = 0; gi < ng; ++gi) sum = sum + c[gi];
-        out[r0 + r] = sum;
-    }
+    for (int r = threadIdx.x; r < nr; r += QT) out[r0 + r] = lds_seq_sum(cg + r * ngp, ng, 0.0f);
 }
 
 // M > 1: one thread per output column j and up to MT token rows.
@@ -169,7 +181,7 @@ hipError_t launch_q4a(const Weight& w, size_t m, const float* a, float* out, hip
         int rb = (int)std::min<size_t>(64, std::max<size_t>(1, 8192 / (size_t)std::max(ng, 1)));
         while (rb > 8 && (w.n + rb - 1) / rb < 512) rb /= 2;
         const unsigned grid = (unsigned)((w.n + rb - 1) / rb);
-        const size_t cgb = (((size_t)rb * ng + 3) & ~(size_t)3) * sizeof(float);
+        const size_t cgb = (size_t)rb * ((ng + 3) & ~3) * sizeof(float);
         const size_t asb = (w.k / 32) * 36 * sizeof(float);
         const bool vec = w.k % 32 == 0 && (w.g == 32 || w.g == 64) && cgb + asb <= 64 * 1024;
         if (vec && w.g == 32)

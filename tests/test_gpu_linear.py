@@ -250,3 +250,16 @@ def test_i8_device_entry_points_match_host(ctx, m, k, n):
     assert np.array_equal(a8.numpy()[:, :k], a8_h)
     assert np.array_equal(sa.numpy(), sa_h)
     assert np.array_equal(out.numpy().view(np.uint32), out_h.view(np.uint32))
+
+
+@pytest.mark.parametrize("n,k", [(9216, 2304), (2304, 9216), (2048, 2304), (1000, 4096), (7, 64)])
+def test_i4_m1_bit_exact_avx2_order(ctx, n, k):
+    """M == 1 int4 with K % 32 == 0 and g = 32: bit-identical to
+    i4_dot_avx2's order (src/bundle.rs:199-225), the x86 production path."""
+    packed, s16, g = synth.int4_weight(n, k, n + k)
+    w = ctx.upload_i4(packed, s16, k, g)
+    a = synth.activations(1, k, k, outlier_scale=1.0)
+    got = w.mm(a)
+    ref = oracle.mm_i4(a, packed, s16.astype(np.float32), k, g)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    w.free()
