@@ -84,6 +84,12 @@ SIGNATURES = {
     "frq_gpt2_generate": (_I, [_P, _P, _P, _S, _S, _P, _P]),
     "frq_gpt2_predict": (_I, [_P, _P, _P, _S, _P, _P]),
     "frq_libm_f32": (_I, [_P, _I, _P, _S, _P]),
+    "frq_gemma_load": (_I, [_P, _P, _I, _P]),
+    "frq_gemma_free": (None, [_P]),
+    "frq_gemma_info": (_I, [_P, _P, _P, _P]),
+    "frq_gemma_set_graphs": (_I, [_P, _I]),
+    "frq_gemma_generate": (_I, [_P, _P, _P, _S, _S, _P, _P]),
+    "frq_gemma_predict": (_I, [_P, _P, _P, _S, _P, _P]),
 }
 
 
@@ -551,3 +557,51 @@ def libm_f32(fn: str, x: np.ndarray, ctx: "Context | None" = None) -> np.ndarray
     out = np.empty_like(x)
     _check(lib.frq_libm_f32(None if ctx is None else ctx.h, LIBM_FNS[fn], _ptr(x), x.size, _ptr(out)))
     return out
+
+
+class Gemma:
+    """Gemma of src/gemma.rs on the device: Gemma::new over an arch "gemma"
+    bundle (52-60), Model::generate (403-431; kv_int8: 364-384) and
+    Model::predict (436-441), every step resident in HBM."""
+
+    def __init__(self, bundle: "Bundle", kv_int8: bool = False, ctx: "Context | None" = None):
+        self.ctx = ctx or bundle.ctx
+        if self.ctx is None:
+            raise FrqError(FRQ_ERR_ARG, "this bundle was opened without a device context")
+        self.h = None
+        out = C.c_void_p()
+        _check(lib.frq_gemma_load(self.ctx.h, bundle.h, int(kv_int8), C.byref(out)))
+        self.h = out.value
+        dims = [C.c_size_t(0) for _ in range(3)]
+        _check(lib.frq_gemma_info(self.h, *[C.byref(v) for v in dims]))
+        self.n_layer, self.d, self.vocab = (v.value for v in dims)
+
+    def free(self):
+        if self.h:
+            lib.frq_gemma_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def set_graphs(self, on: bool):
+        _check(lib.frq_gemma_set_graphs(self.h, int(on)))
+
+    def generate(self, prompt, n_new: int, with_logits: bool = False):
+        prompt = np.ascontiguousarray(prompt, dtype=np.int64)
+        out = np.empty(n_new, np.int64)
+        lg = np.empty((n_new, self.vocab), np.float32) if with_logits else None
+        _check(lib.frq_gemma_generate(self.ctx.h, self.h, _ptr(prompt), len(prompt), n_new, _ptr(out),
+                                      None if lg is None else _ptr(lg)))
+        return (out, lg) if with_logits else out
+
+    def predict(self, ids, with_logits: bool = False):
+        ids = np.ascontiguousarray(ids, dtype=np.int64)
+        tok = np.zeros(1, np.int64)
+        lg = np.empty(self.vocab, np.float32) if with_logits else None
+        _check(lib.frq_gemma_predict(self.ctx.h, self.h, _ptr(ids), len(ids), _ptr(tok),
+                                     None if lg is None else _ptr(lg)))
+        return (int(tok[0]), lg) if with_logits else int(tok[0])

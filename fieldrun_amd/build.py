@@ -16,7 +16,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libfrq.so")
 SOURCES = ["api.hip", "quant.hip", "gemv_i8.hip", "skinny_i8.hip", "gemm_i8.hip", "i4.hip", "moe.hip", "rowdot.hip",
-           "bundle.hip", "gpt2.hip", "q4a.hip"]
+           "bundle.hip", "gpt2.hip", "q4a.hip", "gemma.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",

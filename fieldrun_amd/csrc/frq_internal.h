@@ -248,6 +248,9 @@ size_t i4_ws_floats(const Weight& w, size_t m);
 // int4 at M == 1 in i4_dot_avx2's order (bit-exact) with coalesced loads, for
 // K % 32 == 0 and g in {32, 64}; hipErrorNotSupported for other shapes.
 hipError_t launch_i4_terms(const Weight& w, const float* a, float* out, hipStream_t s);
+// int4 in the reference's orders for any m (M == 1 i4_dot_avx2, M > 1 the
+// dequantise + sequential-k GEMM): the paths decode engines use.
+hipError_t launch_i4_exact(const Weight& w, size_t m, const float* a, float* out, hipStream_t s);
 // int4 (N, K/2) -> the MFMA layout (g == 32, K % 32 == 0); bytes of q4.
 size_t i4_blocked_bytes(size_t n, size_t k);
 hipError_t launch_i4_block(const uint8_t* raw, const uint16_t* sraw, size_t n,

@@ -1,0 +1,778 @@
+// gemma.hip — Gemma-2 greedy decode on the device with a KV cache, gfx950.
+//
+// Restates Gemma of /root/reference/src/gemma.rs: new (52-60), norm (66-77,
+// RMSNorm with the (1 + w) gain baked at export), rope (79-94),
+// forward_block (242-291), forward_block_q (293-363, the int8 cache),
+// head_argmax (386-390) and generate (403-431).  Per layer, m rows at
+// positions cur .. cur+m-1:
+//   a    = norm(x, input_layernorm)            (fused into the previous step)
+//   qkv  = mm(a, [q_proj | k_proj | v_proj])   (one launch: the three weights'
+//                                               output columns side by side)
+//   q, k = rope(q, k); k, v -> cache (int8: per kv-head scale)
+//   att  = softmax(softcap(q k^T * qscalar^-0.5), causal, sliding on even
+//          layers) v, grouped-query (head h reads kv head h / (H / nkv))
+//   x    = x + norm(mm(att, o_proj), post_attention_layernorm)
+//   a    = norm(x, pre_feedforward_layernorm)
+//   gu   = mm(a, [gate_proj | up_proj]);  h = gelu_tanh(gate) * up
+//   x    = x + norm(mm(h, down_proj), post_feedforward_layernorm)
+// then norm(x, "norm") and the tied f16 unembed with its argmax.
+// Every step follows the reference's f32 order, so tokens and logits are
+// the reference's bit for bit: the RMSNorm sum of squares is the fold from
+// -0.0 in index order; the RoPE cos / sin are the host libm's (the table is
+// computed on the host, where the reference computes them); scores and
+// values are sequential FMA chains; the soft-cap and GELU use the libm
+// tanhf restatement, the softmax the expf one and a key-order sum; the
+// linears take their reference-order kernels (int4: i4_dot_avx2's order at
+// M = 1, dequantise + sequential GEMM above; int8: the bit-exact M <= 16
+// path, in chunks).
+#include "frq_internal.h"
+#include "libm_f32.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <vector>
+
+namespace frq {
+namespace {
+
+constexpr int GT = 256;
+
+__device__ __forceinline__ float gwave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ float gblock_max(float v, float* red) {
+    v = gwave_max(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// rows_f32("embed", ids) * escale (gemma.rs:424, 429): row t is token ids[t]
+// (rel: ids[cur - P + t], the token the last argmax wrote).
+__global__ __launch_bounds__(GT) void gm_embed_kernel(const uint8_t* __restrict__ tab, size_t pitch, int d,
+                                                      float escale, const int64_t* __restrict__ ids, int rel, int P,
+                                                      const int* __restrict__ curp, float* __restrict__ x) {
+    const int t = blockIdx.x;
+    const int64_t id = ids[rel ? *curp - P + t : t];
+    const uint16_t* row = reinterpret_cast<const uint16_t*>(tab + (size_t)id * pitch);
+    for (int c = threadIdx.x; c < d; c += GT) x[(size_t)t * d + c] = h2f(row[c]) * escale;
+}
+
+// One row's norm (gemma.rs:66-77) from LDS v (d values) into dst: ms = the
+// fold from -0.0 of v*v in index order / n (one lane, its LDS loads a batch
+// ahead), inv = 1 / sqrt(ms + eps), dst = v * inv * w.
+__device__ void rms_row(const float* v, float* sq, const float* __restrict__ w, int d, float eps, float* dst,
+                        float* stat) {
+    for (int c = threadIdx.x; c < d; c += GT) sq[c] = v[c] * v[c];
+    __syncthreads();
+    if (threadIdx.x == 0) stat[0] = lds_seq_sum(sq, d, -0.0f) / (float)d;
+    __syncthreads();
+    const float inv = 1.0f / sqrtf(stat[0] + eps);
+    for (int c = threadIdx.x; c < d; c += GT) dst[c] = v[c] * inv * w[c];
+    __syncthreads();
+}
+
+// Row r = row0 + blockIdx.x.  y set: x += norm(y, wpost); then out =
+// norm(x, wnext).  LDS: three rows of d floats.
+__global__ __launch_bounds__(GT) void gm_norm_kernel(float* __restrict__ x, const float* __restrict__ y,
+                                                     const float* __restrict__ wpost, const float* __restrict__ wnext,
+                                                     float* __restrict__ out, int d, float eps, int row0) {
+    extern __shared__ float4 lds4[];
+    float* v = reinterpret_cast<float*>(lds4);
+    float* sq = v + d;
+    float* t = sq + d;
+    __shared__ float stat[1];
+    const size_t r = (size_t)(row0 + blockIdx.x) * d;
+    if (y) {
+        for (int c = threadIdx.x; c < d; c += GT) v[c] = y[r + c];
+        __syncthreads();
+        rms_row(v, sq, wpost, d, eps, t, stat);
+        for (int c = threadIdx.x; c < d; c += GT) {
+            const float nx = x[r + c] + t[c];
+            x[r + c] = nx;
+            v[c] = nx;
+        }
+    } else {
+        for (int c = threadIdx.x; c < d; c += GT) v[c] = x[r + c];
+    }
+    __syncthreads();
+    rms_row(v, sq, wnext, d, eps, t, stat);
+    for (int c = threadIdx.x; c < d; c += GT) out[r + c] = t[c];
+}
+
+// rope (gemma.rs:79-94) on one head of hd values at absolute position pos,
+// in place: (a, b) = (x[j], x[j + half]) -> (a c - b s, b c + a s) with the
+// host-computed cos / sin of pos * inv[j].
+__device__ __forceinline__ void rope_pair(float* xh, int j, int half, const float2* __restrict__ cs) {
+    const float2 t = cs[j];
+    const float a = xh[j], b = xh[j + half];
+    xh[j] = a * t.x - b * t.y;
+    xh[j + half] = b * t.x + a * t.y;
+}
+
+// The int8 cache quantiser of forward_block_q (314-324): sc = (max|v| /
+// 127).max(1e-8), q = clamp(round(v / sc)) (NaN -> 0), by one wave.
+__device__ void kv_quant_wave(const float* src, int hd, int8_t* dq, float* sdst) {
+    const int lane = threadIdx.x & 63;
+    float mx = 0.0f;
+    for (int c = lane; c < hd; c += 64) mx = fmaxf(mx, fabsf(src[c]));
+    mx = gwave_max(mx);
+    const float sc = fmaxf(mx / 127.0f, 1e-8f);
+    for (int c = lane; c < hd; c += 64) {
+        const float r = roundf(src[c] / sc);
+        dq[c] = r != r ? (int8_t)0 : (int8_t)fminf(fmaxf(r, -127.0f), 127.0f);
+    }
+    if (lane == 0) *sdst = sc;
+}
+
+// Prefill: rope the q and k heads of row i in the qkv buffer and append k,
+// v to cache row cur + i.  qkv row: [q (H hd) | k (KV hd) | v (KV hd)].
+template <bool KV8>
+__global__ __launch_bounds__(GT) void gm_qkv_kernel(float* __restrict__ qkv, int H, int KV, int hd,
+                                                    const int* __restrict__ curp, const float2* __restrict__ cs,
+                                                    float* __restrict__ kc, float* __restrict__ vc,
+                                                    int8_t* __restrict__ kq, int8_t* __restrict__ vq,
+                                                    float* __restrict__ ks, float* __restrict__ vs) {
+    const int i = blockIdx.x, half = hd / 2, kvd = KV * hd;
+    const size_t pos = (size_t)(*curp + i);
+    float* row = qkv + (size_t)i * (H + 2 * KV) * hd;
+    const float2* csp = cs + pos * half;
+    for (int t = threadIdx.x; t < (H + KV) * half; t += GT) rope_pair(row + (t / half) * hd, t % half, half, csp);
+    __syncthreads();
+    if constexpr (!KV8) {
+        for (int c = threadIdx.x; c < kvd; c += GT) {
+            kc[pos * kvd + c] = row[H * hd + c];
+            vc[pos * kvd + c] = row[(H + KV) * hd + c];
+        }
+    } else {
+        const int wave = threadIdx.x >> 6;
+        for (int u = wave; u < 2 * KV; u += GT / 64) {
+            const int kind = u >= KV, kh = kind ? u - KV : u;
+            kv_quant_wave(row + (H + kind * KV + kh) * hd, hd, (kind ? vq : kq) + pos * kvd + (size_t)kh * hd,
+                          (kind ? vs : ks) + pos * KV + kh);
+        }
+    }
+}
+
+// Attention of row i (position cur + i), query head h over kv head h / rep
+// (forward_block 252-277): s_j = (q . k_j) * qscale as a sequential FMA
+// chain, attn_cap * tanh(s / attn_cap), keys past the position or (even
+// layers) window or more behind it masked at -1e30 (their exps are 0, the
+// mask joins the max), softmax (expf, key-order sum, divide), then the
+// value chain.  FUSED (decode): the block ropes its q head and its kv
+// head's k from the qkv row and appends k, v to the cache first (blocks of
+// one kv group write the same bytes).  LDS: q (hd), k / v staging (2 hd),
+// p and the int8 value scales (pstride each).
+template <bool KV8, bool FUSED>
+__global__ __launch_bounds__(GT) void gm_attn_kernel(const float* __restrict__ qkv, int H, int KV, int hd,
+                                                     const int* __restrict__ curp, const float2* __restrict__ cs,
+                                                     float* __restrict__ kc, float* __restrict__ vc,
+                                                     int8_t* __restrict__ kq, int8_t* __restrict__ vq,
+                                                     float* __restrict__ ks, float* __restrict__ vs, float qscale,
+                                                     float cap, int sliding, int window, int pstride,
+                                                     float* __restrict__ att) {
+    extern __shared__ float4 lds4[];
+    float* q = reinterpret_cast<float*>(lds4);
+    float* kvs = q + ((hd + 3) & ~3);
+    float* p = kvs + 2 * ((hd + 3) & ~3);
+    float* sv = p + pstride;
+    __shared__ float red[4];
+    const int h = blockIdx.x, i = blockIdx.y, rep = H / KV, kv = h / rep, half = hd / 2, kvd = KV * hd;
+    const int cur = *curp, ab = cur + i, klen = cur + (int)gridDim.y;
+    const float* row = qkv + (size_t)i * (H + 2 * KV) * hd;
+    if constexpr (FUSED) {
+        const size_t pos = (size_t)ab;
+        for (int c = threadIdx.x; c < hd; c += GT) {
+            q[c] = row[h * hd + c];
+            kvs[c] = row[(H + kv) * hd + c];
+            kvs[((hd + 3) & ~3) + c] = row[(H + KV + kv) * hd + c];
+        }
+        __syncthreads();
+        const float2* csp = cs + pos * half;
+        for (int t = threadIdx.x; t < 2 * half; t += GT) rope_pair(t < half ? q : kvs, t % half, half, csp);
+        __syncthreads();
+        const float* vsrc = kvs + ((hd + 3) & ~3);
+        if constexpr (!KV8) {
+            for (int c = threadIdx.x; c < hd; c += GT) {
+                kc[pos * kvd + (size_t)kv * hd + c] = kvs[c];
+                vc[pos * kvd + (size_t)kv * hd + c] = vsrc[c];
+            }
+        } else {
+            const int wave = threadIdx.x >> 6;
+            if (wave < 2)
+                kv_quant_wave(wave ? vsrc : kvs, hd, (wave ? vq : kq) + pos * kvd + (size_t)kv * hd,
+                              (wave ? vs : ks) + pos * KV + kv);
+        }
+    } else {
+        for (int c = threadIdx.x; c < hd; c += GT) q[c] = row[h * hd + c];
+    }
+    __syncthreads();
+    const int j0 = (sliding && ab >= window) ? ab - window + 1 : 0;
+    const int nk = ab + 1;
+    float mx = -INFINITY;
+    for (int j = j0 + threadIdx.x; j < nk; j += GT) {
+        float acc = 0.0f;
+        if constexpr (!KV8) {
+            const float* kr = kc + (size_t)j * kvd + (size_t)kv * hd;
+            for (int c = 0; c < hd; c += 4) {
+                const float4 k4 = *reinterpret_cast<const float4*>(kr + c);
+                acc = __builtin_fmaf(q[c], k4.x, acc);
+                acc = __builtin_fmaf(q[c + 1], k4.y, acc);
+                acc = __builtin_fmaf(q[c + 2], k4.z, acc);
+                acc = __builtin_fmaf(q[c + 3], k4.w, acc);
+            }
+        } else {
+            const int8_t* kr = kq + (size_t)j * kvd + (size_t)kv * hd;
+            const float sk = ks[(size_t)j * KV + kv];
+            sv[j] = vs[(size_t)j * KV + kv];
+            for (int c = 0; c < hd; c += 4) {
+                const char4 k4 = *reinterpret_cast<const char4*>(kr + c);
+                acc = __builtin_fmaf(q[c], (float)k4.x * sk, acc);
+                acc = __builtin_fmaf(q[c + 1], (float)k4.y * sk, acc);
+                acc = __builtin_fmaf(q[c + 2], (float)k4.z * sk, acc);
+                acc = __builtin_fmaf(q[c + 3], (float)k4.w * sk, acc);
+            }
+        }
+        float sj = acc * qscale;
+        if (cap > 0.0f) sj = cap * libm::frq_tanhf(sj / cap);
+        p[j] = sj;
+        mx = fmaxf(mx, sj);
+    }
+    mx = gblock_max(mx, red);
+    if (j0 > 0 || nk < klen) mx = fmaxf(mx, -1e30f);  // a masked entry joins the max
+    for (int j = j0 + threadIdx.x; j < nk; j += GT) p[j] = libm::frq_expf(p[j] - mx);
+    __syncthreads();
+    if (threadIdx.x == 0) {  // key order; the masked exps are +0 (j < j0 add nothing to +0)
+        float sum = 0.0f;
+        for (int j = j0; j < nk; ++j) sum = sum + p[j];
+        red[0] = sum;
+    }
+    __syncthreads();
+    const float sum = red[0];
+    for (int j = j0 + threadIdx.x; j < nk; j += GT) p[j] = p[j] / sum;
+    __syncthreads();
+    constexpr int B = 16;
+    for (int c = threadIdx.x; c < hd; c += GT) {
+        float acc = 0.0f;
+        const size_t col = (size_t)kv * hd + c;
+        const int n = nk - j0, nb = n / B;
+        float v0[B], v1[B];
+        auto ld = [&](float (&v)[B], int k) {
+#pragma unroll
+            for (int u = 0; u < B; ++u) {
+                const size_t j = (size_t)(j0 + k * B + u);
+                if constexpr (!KV8) v[u] = vc[j * kvd + col];
+                else v[u] = (float)vq[j * kvd + col] * sv[j];
+            }
+        };
+        auto fma_b = [&](const float (&v)[B], int k) {
+#pragma unroll
+            for (int u = 0; u < B; ++u) acc = __builtin_fmaf(p[j0 + k * B + u], v[u], acc);
+        };
+        if (nb > 0) {
+            ld(v0, 0);
+            ld(v1, min(1, nb - 1));
+            for (int k = 0; k < nb; k += 2) {
+                fma_b(v0, k);
+                ld(v0, min(k + 2, nb - 1));
+                if (k + 1 < nb) fma_b(v1, k + 1);
+                ld(v1, min(k + 3, nb - 1));
+            }
+        }
+        for (int j = j0 + nb * B; j < nk; ++j) {
+            const float v = KV8 ? (float)vq[(size_t)j * kvd + col] * sv[j] : vc[(size_t)j * kvd + col];
+            acc = __builtin_fmaf(p[j], v, acc);
+        }
+        att[(size_t)i * H * hd + (size_t)h * hd + c] = acc;
+    }
+}
+
+// h = gelu_tanh(gate) * up over m rows of the [gate | up] buffer.
+__global__ __launch_bounds__(GT) void gm_geglu_kernel(const float* __restrict__ gu, int ffn, size_t total,
+                                                      float c, float* __restrict__ hm) {
+    for (size_t i = (size_t)blockIdx.x * GT + threadIdx.x; i < total; i += (size_t)gridDim.x * GT) {
+        const size_t r = i / ffn, col = i - r * ffn;
+        const float x = gu[r * 2 * ffn + col];
+        hm[i] = 0.5f * x * (1.0f + libm::frq_tanhf(c * (x + 0.044715f * x * x * x))) * gu[r * 2 * ffn + ffn + col];
+    }
+}
+
+// The token the unembed's folded argmax chose goes to out[cur + m - P];
+// cur += m; the key is cleared.
+__global__ void gm_argmax_done_kernel(unsigned long long* __restrict__ best, int* __restrict__ curp, int m, int P,
+                                      int64_t* __restrict__ out) {
+    if (threadIdx.x == 0) {
+        const int cur = *curp;
+        out[cur + m - P] = (int64_t)(uint32_t)(*best & 0xffffffffull);
+        *curp = cur + m;
+        *best = 0ull;
+    }
+}
+
+}  // namespace
+}  // namespace frq
+
+using namespace frq;
+
+struct frq_gemma {
+    int device = 0;
+    size_t L = 0, H = 0, KV = 0, hd = 0, d = 0, ffn = 0, vocab = 0;
+    size_t window = 4096;
+    float theta = 0, eps = 0, cap = 0, qscale = 0, escale = 0;
+    int kv8 = 0, graphs = 1;
+    std::vector<float> inv;          // RoPE inverse frequencies
+    std::vector<frq_w*> qkv, o, gu, down;
+    frq_w* embed = nullptr;
+    float* norms = nullptr;          // 4 per layer + the final norm, f32 (d each)
+    // sized to the largest call so far: positions (cache, RoPE table) and rows
+    size_t cap_pos = 0, cap_rows = 0;
+    char* buf = nullptr;
+    float2* cs = nullptr;
+    float *kc = nullptr, *vc = nullptr, *ks = nullptr, *vs = nullptr;
+    int8_t *kq = nullptr, *vq = nullptr;
+    float *x = nullptr, *a = nullptr, *qkvb = nullptr, *att = nullptr, *ob = nullptr, *gub = nullptr, *hm = nullptr,
+          *logits = nullptr;
+    int* cur = nullptr;
+    unsigned long long* best = nullptr;
+    int64_t *tok = nullptr, *ids = nullptr;
+    ~frq_gemma() {
+        for (auto* v : {&qkv, &o, &gu, &down})
+            for (frq_w* w : *v) frq_w_free(w);
+        frq_w_free(embed);
+        if (norms) (void)hipFree(norms);
+        if (buf) (void)hipFree(buf);
+    }
+    const float* norm_of(size_t l, int j) const { return norms + (4 * l + j) * d; }
+    const float* final_norm() const { return norms + 4 * L * d; }
+};
+
+namespace {
+
+int gfail(hipError_t e, const char* what) { return set_error(FRQ_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e)); }
+#define GMCHK(expr, what)                              \
+    do {                                               \
+        hipError_t e_ = (expr);                        \
+        if (e_ != hipSuccess) return gfail(e_, what);  \
+    } while (0)
+
+struct GDev {
+    int prev = -1;
+    explicit GDev(int d) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != d) (void)hipSetDevice(d);
+    }
+    ~GDev() {
+        if (prev >= 0) (void)hipSetDevice(prev);
+    }
+};
+
+// Two or three linears with the same input concatenated along the output:
+// the stored arrays' output rows (int4 / q4a: rows of the (out, in) store;
+// int8: columns of the (in, out) store) side by side, scales likewise.
+int concat_linear(frq_ctx* c, const frq_bundle* b, const std::vector<std::string>& names, size_t k, frq_w** out) {
+    struct Arr {
+        std::string dt;
+        size_t shape[4], nd = 4, grp = 0, bytes = 0;
+        const void* data = nullptr;
+    };
+    auto get = [&](const std::string& nm, Arr& a) {
+        char dt[16];
+        const int rc = frq_bundle_array(b, nm.c_str(), dt, sizeof dt, a.shape, &a.nd, &a.grp, &a.data, &a.bytes);
+        a.dt = dt;
+        return rc;
+    };
+    std::vector<Arr> w(names.size()), s(names.size()), mn(names.size());
+    size_t ntot = 0;
+    for (size_t i = 0; i < names.size(); ++i) {
+        if (int rc = get(names[i], w[i])) return rc;
+        if (int rc = get(names[i] + "__scale", s[i])) return rc;
+        if (w[i].dt != w[0].dt || w[i].nd != 2) return set_error(FRQ_ERR_FORMAT, names[i] + ": mixed or bad dtype");
+        if (w[i].dt == "q4a")
+            if (int rc = get(names[i] + "__min", mn[i])) return rc;
+        const bool i8 = w[i].dt == "i8";
+        const size_t kin = i8 ? w[i].shape[0] : w[i].shape[1];
+        if (kin != k) return set_error(FRQ_ERR_FORMAT, names[i] + ": input width " + std::to_string(kin));
+        if (s[i].dt != "f16") return set_error(FRQ_ERR_FORMAT, names[i] + "__scale: f16 expected");
+        ntot += i8 ? w[i].shape[1] : w[i].shape[0];
+    }
+    const std::string dt = w[0].dt;
+    if (dt == "i8") {
+        std::vector<int8_t> cat(k * ntot);
+        std::vector<uint16_t> sc(ntot);
+        size_t off = 0;
+        for (size_t i = 0; i < names.size(); ++i) {
+            const size_t n = w[i].shape[1];
+            const int8_t* src = static_cast<const int8_t*>(w[i].data);
+            for (size_t r = 0; r < k; ++r) std::memcpy(&cat[r * ntot + off], src + r * n, n);
+            std::memcpy(&sc[off], s[i].data, n * 2);
+            off += n;
+        }
+        *out = frq_upload_i8_bundle(c, cat.data(), sc.data(), k, ntot);
+    } else if (dt == "i4" || dt == "q4a") {
+        const size_t g = w[0].grp ? w[0].grp : (dt == "i4" ? 32 : 64), rb = (k + 1) / 2, ng = (k + g - 1) / g;
+        std::vector<uint8_t> cat(ntot * rb);
+        std::vector<uint16_t> sc(ntot * ng), mv(dt == "q4a" ? ntot * ng : 0);
+        size_t off = 0;
+        for (size_t i = 0; i < names.size(); ++i) {
+            const size_t n = w[i].shape[0];
+            if ((w[i].grp ? w[i].grp : g) != g) return set_error(FRQ_ERR_FORMAT, names[i] + ": group differs");
+            std::memcpy(&cat[off * rb], w[i].data, n * rb);
+            std::memcpy(&sc[off * ng], s[i].data, n * ng * 2);
+            if (dt == "q4a") std::memcpy(&mv[off * ng], mn[i].data, n * ng * 2);
+            off += n;
+        }
+        *out = dt == "i4" ? frq_upload_i4(c, cat.data(), sc.data(), ntot, k, g)
+                          : frq_upload_q4a(c, cat.data(), sc.data(), mv.data(), ntot, k, g);
+    } else {
+        return set_error(FRQ_ERR_DTYPE, names[0] + ": gemma linears must be i8, i4 or q4a");
+    }
+    return *out ? FRQ_OK : last_code();
+}
+
+int one_linear(frq_ctx* c, const frq_bundle* b, const std::string& name, size_t k, size_t n, frq_w** out) {
+    if (int rc = frq_bundle_weight(c, b, name.c_str(), out)) return rc;
+    int dt = 0;
+    size_t wn = 0, wk = 0, g = 0;
+    (void)frq_w_info(*out, &dt, &wn, &wk, &g);
+    if (dt != FRQ_DT_I8 && dt != FRQ_DT_I4 && dt != FRQ_DT_Q4A)
+        return set_error(FRQ_ERR_DTYPE, name + ": gemma linears must be i8, i4 or q4a");
+    if (wk != k || wn != n) return set_error(FRQ_ERR_FORMAT, name + ": unexpected shape");
+    return FRQ_OK;
+}
+
+// Bundle::mm in the reference's order for m rows.
+int gm_mm(frq_ctx* c, const frq_w* wh, const float* in, size_t m, float* outp) {
+    const Weight& w = *weight_of(wh);
+    hipStream_t s = (hipStream_t)frq_get_stream(c);
+    if (w.dtype == FRQ_DT_I4) {
+        GMCHK(launch_i4_exact(w, m, in, outp, s), "launch i4");
+        return FRQ_OK;
+    }
+    if (w.dtype == FRQ_DT_Q4A) {
+        GMCHK(launch_q4a(w, m, in, outp, s), "launch q4a");
+        return FRQ_OK;
+    }
+    if (m <= 16) return frq_mm_dev(c, wh, in, m, outp);
+    const size_t nch = (m + 15) / 16;  // int8: the bit-exact multi-row path in chunks of 8..16 rows
+    size_t r0 = 0;
+    for (size_t i = 0; i < nch; ++i) {
+        const size_t rows = m / nch + (i < m % nch ? 1 : 0);
+        if (int rc = frq_mm_dev(c, wh, in + r0 * w.k, rows, outp + r0 * w.n)) return rc;
+        r0 += rows;
+    }
+    return FRQ_OK;
+}
+
+size_t gm_pstride(const frq_gemma* g) { return (g->cap_pos + 3) & ~(size_t)3; }
+size_t gm_attn_lds(const frq_gemma* g) { return (3 * ((g->hd + 3) & ~(size_t)3) + 2 * gm_pstride(g)) * sizeof(float); }
+
+// Device buffers for up to npos positions and rows prompt rows; the RoPE
+// table cos / sin(pos * inv[j]) from the host libm (the reference's f32
+// cos / sin).
+int gm_reserve(frq_ctx* c, frq_gemma* g, size_t npos, size_t rows) {
+    if (npos <= g->cap_pos && rows <= g->cap_rows) return FRQ_OK;
+    hipStream_t s = (hipStream_t)frq_get_stream(c);
+    GMCHK(hipStreamSynchronize(s), "hipStreamSynchronize");
+    if (g->buf) (void)hipFree(g->buf);
+    g->buf = nullptr;
+    g->cap_pos = std::max(npos, g->cap_pos);
+    g->cap_rows = std::max(rows, g->cap_rows);
+    if (gm_attn_lds(g) > 64 * 1024)
+        return set_error(FRQ_ERR_ARG, "gemma: " + std::to_string(g->cap_pos) +
+                                          " positions exceed this build's attention scores in LDS");
+    const size_t N = g->cap_pos, R = g->cap_rows, L = g->L, kvd = g->KV * g->hd, half = g->hd / 2;
+    size_t off = 0;
+    auto take = [&](size_t bytes) { const size_t o = off; off += round_up(bytes, 256); return o; };
+    const size_t o_cs = take(N * half * sizeof(float2));
+    size_t o_kc, o_vc, o_ks = 0, o_vs = 0;
+    if (g->kv8) {
+        o_kc = take(L * N * kvd); o_vc = take(L * N * kvd);
+        o_ks = take(L * N * g->KV * 4); o_vs = take(L * N * g->KV * 4);
+    } else {
+        o_kc = take(L * N * kvd * 4); o_vc = take(L * N * kvd * 4);
+    }
+    const size_t o_x = take(R * g->d * 4), o_a = take(R * g->d * 4),
+                 o_qkv = take(R * (g->H + 2 * g->KV) * g->hd * 4), o_att = take(R * g->H * g->hd * 4),
+                 o_o = take(R * g->d * 4), o_gu = take(R * 2 * g->ffn * 4), o_hm = take(R * g->ffn * 4),
+                 o_lg = take(g->vocab * 4), o_cur = take(4), o_best = take(8), o_tok = take(N * 8), o_ids = take(R * 8);
+    GMCHK(hipMalloc(&g->buf, off), "hipMalloc(gemma)");
+    char* m = g->buf;
+    GMCHK(hipMemsetAsync(m, 0, off, s), "hipMemsetAsync(gemma)");
+    std::vector<float2> cs(N * half);
+    for (size_t pos = 0; pos < N; ++pos)
+        for (size_t j = 0; j < half; ++j) {
+            const float ang = (float)pos * g->inv[j];
+            cs[pos * half + j] = make_float2(cosf(ang), sinf(ang));
+        }
+    GMCHK(hipMemcpyAsync(m + o_cs, cs.data(), cs.size() * sizeof(float2), hipMemcpyHostToDevice, s), "hipMemcpyAsync");
+    g->cs = reinterpret_cast<float2*>(m + o_cs);
+    g->kc = g->kv8 ? nullptr : reinterpret_cast<float*>(m + o_kc);
+    g->vc = g->kv8 ? nullptr : reinterpret_cast<float*>(m + o_vc);
+    g->kq = g->kv8 ? reinterpret_cast<int8_t*>(m + o_kc) : nullptr;
+    g->vq = g->kv8 ? reinterpret_cast<int8_t*>(m + o_vc) : nullptr;
+    g->ks = g->kv8 ? reinterpret_cast<float*>(m + o_ks) : nullptr;
+    g->vs = g->kv8 ? reinterpret_cast<float*>(m + o_vs) : nullptr;
+    g->x = reinterpret_cast<float*>(m + o_x); g->a = reinterpret_cast<float*>(m + o_a);
+    g->qkvb = reinterpret_cast<float*>(m + o_qkv); g->att = reinterpret_cast<float*>(m + o_att);
+    g->ob = reinterpret_cast<float*>(m + o_o); g->gub = reinterpret_cast<float*>(m + o_gu);
+    g->hm = reinterpret_cast<float*>(m + o_hm); g->logits = reinterpret_cast<float*>(m + o_lg);
+    g->cur = reinterpret_cast<int*>(m + o_cur); g->best = reinterpret_cast<unsigned long long*>(m + o_best);
+    g->tok = reinterpret_cast<int64_t*>(m + o_tok); g->ids = reinterpret_cast<int64_t*>(m + o_ids);
+    GMCHK(hipStreamSynchronize(s), "hipStreamSynchronize");  // cs is released on return
+    return FRQ_OK;
+}
+
+int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_out) {
+    hipStream_t s = (hipStream_t)frq_get_stream(c);
+    const int d = (int)g->d, H = (int)g->H, KV = (int)g->KV, hd = (int)g->hd, ffn = (int)g->ffn;
+    const Weight& et = *weight_of(g->embed);
+    const size_t nlds = 3 * g->d * sizeof(float);
+    auto norm = [&](const float* y, const float* wpost, const float* wnext, int rows, int row0) {
+        gm_norm_kernel<<<dim3(rows), dim3(GT), nlds, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, row0);
+        return hipGetLastError();
+    };
+    gm_embed_kernel<<<dim3((unsigned)m), dim3(GT), 0, s>>>(et.rowp, et.rpitch, d, g->escale, rel ? g->tok : g->ids,
+                                                           rel, P, g->cur, g->x);
+    GMCHK(hipGetLastError(), "launch embed");
+    GMCHK(norm(nullptr, nullptr, g->norm_of(0, 0), (int)m, 0), "launch norm");
+    const size_t kvd = g->KV * g->hd;
+    for (size_t l = 0; l < g->L; ++l) {
+        if (int rc = gm_mm(c, g->qkv[l], g->a, m, g->qkvb)) return rc;
+        float* kc = g->kv8 ? nullptr : g->kc + l * g->cap_pos * kvd;
+        float* vc = g->kv8 ? nullptr : g->vc + l * g->cap_pos * kvd;
+        int8_t* kq = g->kv8 ? g->kq + l * g->cap_pos * kvd : nullptr;
+        int8_t* vq = g->kv8 ? g->vq + l * g->cap_pos * kvd : nullptr;
+        float* ks = g->kv8 ? g->ks + l * g->cap_pos * g->KV : nullptr;
+        float* vs = g->kv8 ? g->vs + l * g->cap_pos * g->KV : nullptr;
+        const dim3 ag((unsigned)H, (unsigned)m);
+        const size_t lds = gm_attn_lds(g);
+        const int ps = (int)gm_pstride(g), sl = l % 2 == 0 ? 1 : 0, win = (int)g->window;
+        if (m == 1) {
+            if (g->kv8)
+                gm_attn_kernel<true, true><<<ag, dim3(GT), lds, s>>>(g->qkvb, H, KV, hd, g->cur, g->cs, kc, vc, kq,
+                                                                     vq, ks, vs, g->qscale, g->cap, sl, win, ps,
+                                                                     g->att);
+            else
+                gm_attn_kernel<false, true><<<ag, dim3(GT), lds, s>>>(g->qkvb, H, KV, hd, g->cur, g->cs, kc, vc, kq,
+                                                                      vq, ks, vs, g->qscale, g->cap, sl, win, ps,
+                                                                      g->att);
+        } else {
+            if (g->kv8)
+                gm_qkv_kernel<true><<<dim3((unsigned)m), dim3(GT), 0, s>>>(g->qkvb, H, KV, hd, g->cur, g->cs, kc, vc,
+                                                                           kq, vq, ks, vs);
+            else
+                gm_qkv_kernel<false><<<dim3((unsigned)m), dim3(GT), 0, s>>>(g->qkvb, H, KV, hd, g->cur, g->cs, kc,
+                                                                            vc, kq, vq, ks, vs);
+            GMCHK(hipGetLastError(), "launch qkv");
+            if (g->kv8)
+                gm_attn_kernel<true, false><<<ag, dim3(GT), lds, s>>>(g->qkvb, H, KV, hd, g->cur, g->cs, kc, vc, kq,
+                                                                      vq, ks, vs, g->qscale, g->cap, sl, win, ps,
+                                                                      g->att);
+            else
+                gm_attn_kernel<false, false><<<ag, dim3(GT), lds, s>>>(g->qkvb, H, KV, hd, g->cur, g->cs, kc, vc,
+                                                                       kq, vq, ks, vs, g->qscale, g->cap, sl, win,
+                                                                       ps, g->att);
+        }
+        GMCHK(hipGetLastError(), "launch attention");
+        if (int rc = gm_mm(c, g->o[l], g->att, m, g->ob)) return rc;
+        GMCHK(norm(g->ob, g->norm_of(l, 1), g->norm_of(l, 2), (int)m, 0), "launch norm");
+        if (int rc = gm_mm(c, g->gu[l], g->a, m, g->gub)) return rc;
+        const size_t tot = m * g->ffn;
+        gm_geglu_kernel<<<dim3((unsigned)std::min<size_t>((tot + GT - 1) / GT, 4096)), dim3(GT), 0, s>>>(
+            g->gub, ffn, tot, sqrtf(2.0f / 3.14159274101257324f), g->hm);
+        GMCHK(hipGetLastError(), "launch geglu");
+        if (int rc = gm_mm(c, g->down[l], g->hm, m, g->ob)) return rc;
+        if (l + 1 < g->L)
+            GMCHK(norm(g->ob, g->norm_of(l, 3), g->norm_of(l + 1, 0), (int)m, 0), "launch norm");
+        else  // only the last row feeds the head
+            GMCHK(norm(g->ob, g->norm_of(l, 3), g->final_norm(), 1, (int)m - 1), "launch norm");
+    }
+    float* lg = logits_out ? logits_out : g->logits;
+    GMCHK(launch_rowdot_argmax(et, g->a + (m - 1) * g->d, lg, g->best, ctx_err(c), s), "launch unembed");
+    gm_argmax_done_kernel<<<dim3(1), dim3(64), 0, s>>>(g->best, g->cur, (int)m, P, g->tok);
+    GMCHK(hipGetLastError(), "launch argmax");
+    return FRQ_OK;
+}
+
+int gm_run(frq_ctx* c, frq_gemma* g, const int64_t* prompt, size_t P, size_t n_new, int64_t* out, float* logits) {
+    if (!c || !g) return set_error(FRQ_ERR_ARG, "null context / model");
+    if (ctx_device(c) != g->device) return set_error(FRQ_ERR_ARG, "model lives on another device");
+    if (!P || !n_new) return set_error(FRQ_ERR_ARG, "empty prompt or no tokens asked for");
+    if (!prompt || !out) return set_error(FRQ_ERR_ARG, "null prompt / output");
+    for (size_t i = 0; i < P; ++i)
+        if (prompt[i] < 0 || (size_t)prompt[i] >= g->vocab)
+            return set_error(FRQ_ERR_ARG, "token id " + std::to_string(prompt[i]) + " beyond the vocabulary");
+    GDev dv(g->device);
+    if (int rc = gm_reserve(c, g, P + n_new, P)) return rc;
+    hipStream_t s = (hipStream_t)frq_get_stream(c);
+    float* lgd = nullptr;
+    if (logits) GMCHK(hipMalloc(&lgd, n_new * g->vocab * sizeof(float)), "hipMalloc(logits)");
+    struct Free {
+        float* p;
+        ~Free() { if (p) (void)hipFree(p); }
+    } fr{lgd};
+    GMCHK(hipMemcpyAsync(g->ids, prompt, P * sizeof(int64_t), hipMemcpyHostToDevice, s), "hipMemcpyAsync(prompt)");
+    GMCHK(hipMemsetAsync(g->cur, 0, sizeof(int), s), "hipMemsetAsync(cur)");
+    if (int rc = gm_block(c, g, P, 0, (int)P, lgd)) return rc;
+    if (g->graphs && !logits && n_new > 2 && s != nullptr) {
+        hipGraph_t gr = nullptr;
+        hipGraphExec_t ex = nullptr;
+        GMCHK(hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed), "hipStreamBeginCapture");
+        const int rc = gm_block(c, g, 1, 1, (int)P, nullptr);
+        const hipError_t e = hipStreamEndCapture(s, &gr);
+        if (rc) { if (gr) (void)hipGraphDestroy(gr); return rc; }
+        GMCHK(e, "hipStreamEndCapture");
+        const hipError_t ei = hipGraphInstantiate(&ex, gr, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(gr);
+        GMCHK(ei, "hipGraphInstantiate");
+        hipError_t el = hipSuccess;
+        for (size_t t = 1; t < n_new && el == hipSuccess; ++t) el = hipGraphLaunch(ex, s);
+        (void)hipGraphExecDestroy(ex);
+        GMCHK(el, "hipGraphLaunch");
+    } else {
+        for (size_t t = 1; t < n_new; ++t)
+            if (int rc = gm_block(c, g, 1, 1, (int)P, lgd ? lgd + t * g->vocab : nullptr)) return rc;
+    }
+    GMCHK(hipMemcpyAsync(out, g->tok, n_new * sizeof(int64_t), hipMemcpyDeviceToHost, s), "hipMemcpyAsync(tokens)");
+    if (logits)
+        GMCHK(hipMemcpyAsync(logits, lgd, n_new * g->vocab * sizeof(float), hipMemcpyDeviceToHost, s),
+              "hipMemcpyAsync(logits)");
+    return frq_sync(c);
+}
+
+float f16_host(uint16_t h) {
+    const uint32_t sg = (uint32_t)(h >> 15) << 31, e = (h >> 10) & 31, mt = h & 1023;
+    uint32_t bits;
+    if (e == 0) {
+        if (!mt) bits = sg;
+        else {
+            int sh = 0;
+            uint32_t mm = mt;
+            while (!(mm & 1024)) { mm <<= 1; ++sh; }
+            bits = sg | ((uint32_t)(113 - sh) << 23) | ((mm & 1023) << 13);
+        }
+    } else if (e == 31) {
+        bits = sg | 0x7F800000u | (mt << 13);
+    } else {
+        bits = sg | ((e + 112) << 23) | (mt << 13);
+    }
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f;
+}
+
+int norm_vec(const frq_bundle* b, const std::string& name, size_t d, float* dst) {
+    char dt[16];
+    size_t shape[4], nd = 4, grp = 0, bytes = 0;
+    const void* data = nullptr;
+    if (int rc = frq_bundle_array(b, name.c_str(), dt, sizeof dt, shape, &nd, &grp, &data, &bytes)) return rc;
+    const std::string t = dt;
+    if (nd != 1 || shape[0] != d || (t != "f16" && t != "f32"))
+        return set_error(FRQ_ERR_FORMAT, name + ": expected " + std::to_string(d) + " f16 / f32 values");
+    if (t == "f32") std::memcpy(dst, data, d * 4);
+    else for (size_t i = 0; i < d; ++i) dst[i] = f16_host(static_cast<const uint16_t*>(data)[i]);
+    return FRQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int frq_gemma_load(frq_ctx* c, const frq_bundle* b, int kv_int8, frq_gemma** out) {
+    if (!out) return set_error(FRQ_ERR_ARG, "null output handle");
+    *out = nullptr;
+    if (!c || !b) return set_error(FRQ_ERR_ARG, "null context / bundle");
+    char arch[32];
+    int64_t cfg[8];
+    double cff[8];
+    size_t nc = 8, nf = 8;
+    if (int rc = frq_bundle_header(b, arch, sizeof arch, cfg, &nc, cff, &nf)) return rc;
+    if (std::string(arch) != "gemma") return set_error(FRQ_ERR_FORMAT, std::string("not a gemma bundle: ") + arch);
+    if (nc < 7 || nf < 6)
+        return set_error(FRQ_ERR_FORMAT, "gemma config needs [n_layer, H, nkv, hd, d, ffn, vocab, tied] and "
+                                         "config_f [theta, eps, attn_cap, final_cap, qscalar, escale]");
+    for (int i = 0; i < 7; ++i)
+        if (cfg[i] <= 0) return set_error(FRQ_ERR_FORMAT, "gemma config entries must be positive");
+    auto g = std::make_unique<frq_gemma>();
+    g->device = ctx_device(c);
+    g->L = cfg[0]; g->H = cfg[1]; g->KV = cfg[2]; g->hd = cfg[3]; g->d = cfg[4]; g->ffn = cfg[5]; g->vocab = cfg[6];
+    g->kv8 = kv_int8 ? 1 : 0;
+    if (g->H % g->KV || g->hd % 4 || g->d % 4 || g->d > 8192 || g->hd > 1024)
+        return set_error(FRQ_ERR_ARG, "gemma shape outside this build's kernels (H % nkv, head dim and d % 4, "
+                                      "d <= 8192)");
+    // Gemma::new (52-60): f32 of the f64 config values; RoPE frequencies and
+    // the query scale through the host libm's powf, as the reference
+    const float theta = (float)cff[0], qscalar = (float)cff[4];
+    g->theta = theta; g->eps = (float)cff[1]; g->cap = (float)cff[2]; g->escale = (float)cff[5];
+    g->qscale = powf(qscalar, -0.5f);
+    for (size_t j = 0; j < g->hd / 2; ++j) g->inv.push_back(1.0f / powf(theta, 2.0f * (float)j / (float)g->hd));
+    const size_t L = g->L, d = g->d, qd = g->H * g->hd, kvd = g->KV * g->hd;
+    (void)kvd;
+    for (size_t l = 0; l < L; ++l) {
+        const std::string p = "l" + std::to_string(l) + ".";
+        frq_w* w = nullptr;
+        if (int rc = concat_linear(c, b, {p + "self_attn.q_proj", p + "self_attn.k_proj", p + "self_attn.v_proj"}, d, &w))
+            return rc;
+        g->qkv.push_back(w);
+        if (int rc = one_linear(c, b, p + "self_attn.o_proj", qd, d, &w)) return rc;
+        g->o.push_back(w);
+        if (int rc = concat_linear(c, b, {p + "mlp.gate_proj", p + "mlp.up_proj"}, d, &w)) return rc;
+        g->gu.push_back(w);
+        if (int rc = one_linear(c, b, p + "mlp.down_proj", g->ffn, d, &w)) return rc;
+        g->down.push_back(w);
+    }
+    if (int rc = frq_bundle_weight(c, b, "embed", &g->embed)) return rc;
+    {
+        int dt = 0;
+        size_t n = 0, k = 0, gg = 0;
+        (void)frq_w_info(g->embed, &dt, &n, &k, &gg);
+        if (dt != FRQ_DT_F16 || n != g->vocab || k != d)
+            return set_error(FRQ_ERR_FORMAT, "embed: expected an f16 (vocab, d) table");
+    }
+    std::vector<float> hv((4 * L + 1) * d);
+    static const char* nn[4] = {"input_layernorm", "post_attention_layernorm", "pre_feedforward_layernorm",
+                                "post_feedforward_layernorm"};
+    for (size_t l = 0; l < L; ++l)
+        for (int j = 0; j < 4; ++j)
+            if (int rc = norm_vec(b, "l" + std::to_string(l) + "." + nn[j], d, &hv[(4 * l + j) * d])) return rc;
+    if (int rc = norm_vec(b, "norm", d, &hv[4 * L * d])) return rc;
+    GDev dv(g->device);
+    hipStream_t s = (hipStream_t)frq_get_stream(c);
+    GMCHK(hipMalloc(&g->norms, hv.size() * 4), "hipMalloc(norms)");
+    GMCHK(hipMemcpyAsync(g->norms, hv.data(), hv.size() * 4, hipMemcpyHostToDevice, s), "hipMemcpyAsync(norms)");
+    GMCHK(hipStreamSynchronize(s), "hipStreamSynchronize");
+    *out = g.release();
+    return FRQ_OK;
+}
+
+void frq_gemma_free(frq_gemma* g) { delete g; }
+
+int frq_gemma_set_graphs(frq_gemma* g, int on) {
+    if (!g) return set_error(FRQ_ERR_ARG, "null model");
+    g->graphs = on ? 1 : 0;
+    return FRQ_OK;
+}
+
+int frq_gemma_info(const frq_gemma* g, size_t* n_layer, size_t* d, size_t* vocab) {
+    if (!g) return set_error(FRQ_ERR_ARG, "null model");
+    if (n_layer) *n_layer = g->L;
+    if (d) *d = g->d;
+    if (vocab) *vocab = g->vocab;
+    return FRQ_OK;
+}
+
+int frq_gemma_generate(frq_ctx* c, frq_gemma* g, const int64_t* prompt, size_t n_prompt, size_t n_new,
+                       int64_t* out, float* logits) {
+    return gm_run(c, g, prompt, n_prompt, n_new, out, logits);
+}
+
+int frq_gemma_predict(frq_ctx* c, frq_gemma* g, const int64_t* ids, size_t n, int64_t* token, float* logits) {
+    return gm_run(c, g, ids, n, 1, token, logits);
+}
+
+}  // extern "C"

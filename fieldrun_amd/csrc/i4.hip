@@ -750,6 +750,20 @@ hipError_t launch_i4_terms(const Weight& w, const float* a, float* out, hipStrea
     return hipGetLastError();
 }
 
+hipError_t launch_i4_exact(const Weight& w, size_t m, const float* a, float* out, hipStream_t s) {
+    if (m == 0 || w.n == 0) return hipSuccess;
+    if (m == 1) {
+        const hipError_t e = launch_i4_terms(w, a, out, s);
+        if (e != hipErrorNotSupported) return e;
+        i4_gemv_generic<<<dim3((unsigned)((w.n + 255) / 256)), dim3(256), 0, s>>>(
+            w.q4raw, w.s4raw, (int)w.n, (int)w.k, (int)w.g, a, out);
+        return hipGetLastError();
+    }
+    dim3 grid((unsigned)((w.n + 255) / 256), (unsigned)((m + 15) / 16));
+    i4_gemm_rows<16><<<grid, dim3(256), 0, s>>>(w.q4raw, w.s4raw, (int)w.n, (int)w.k, (int)w.g, a, (int)m, out);
+    return hipGetLastError();
+}
+
 hipError_t launch_i4(const Weight& w, size_t m, const float* a, float* out,
                      float* wsf, unsigned* tickets, hipStream_t s) {
     (void)tickets;

@@ -127,3 +127,55 @@ def write_qwen3moe_layer_bundle(stem: str, s: int, n_exp: int = 128, d: int = 20
     m = manifest("qwen3moe", cfg, [1e6, 1e-6])
     w.finish(m)
     return m
+
+
+def write_gemma2_bundle(stem: str, s: int, n_layer: int = 26, n_head: int = 8, n_kv: int = 4, hd: int = 256,
+                        d: int = 2304, ffn: int = 9216, vocab: int = 256000, std: float = 0.02,
+                        dtype: str = "int4", norm_std: float = 0.0, raw: bool = False) -> dict:
+    """a Gemma-2-2b-shaped bundle as convert_gemma writes it
+    (src/convert.rs:636-657 via write_layers 1266-1300): the f16 embed (tied
+    unembed), the RMSNorm gains with the +1 baked in (1 + w, w = 0 at init,
+    or N(0, norm_std)), and the seven projections per layer put_lin from
+    (out, in) sources in `dtype` ("int4" groups of 32, "int8", "q4a").
+    config [nl, H, nkv, hd, d, ffn, vocab, tied]; config_f [theta, eps,
+    attn_cap, final_cap, query_pre_attn_scalar, sqrt(d)] as Gemma-2-2b.
+    raw: the int4 linears as seeded random nibbles with f16 scales written
+    directly (the configs[2] size in seconds rather than minutes)."""
+    from .bundle import BundleWriter, manifest
+    rng = np.random.default_rng(s)
+    nrm = lambda *shape: (rng.standard_normal(shape, dtype=np.float32) * np.float32(std))
+    gain = lambda: (np.float32(1.0) + rng.standard_normal(d, dtype=np.float32) * np.float32(norm_std)
+                    if norm_std else np.ones(d, np.float32))
+    w = BundleWriter(stem)
+    if raw:  # the f16 embed in row chunks (no full-size f32 temporary)
+        rows = []
+        for r0 in range(0, vocab, 8192):
+            rows.append(nrm(min(8192, vocab - r0), d).astype(np.float16))
+        emb = np.concatenate(rows)
+        nb = w._write(np.ascontiguousarray(emb.view(np.uint16)))
+        w.entry("embed", "f16", emb.shape, nb)
+        del emb, rows
+    else:
+        w.put_embed("embed", nrm(vocab, d), "f16", dtype)
+    w.put_small("norm", gain(), None, dtype)
+    shapes = {"self_attn.q_proj": (n_head * hd, d), "self_attn.k_proj": (n_kv * hd, d),
+              "self_attn.v_proj": (n_kv * hd, d), "self_attn.o_proj": (d, n_head * hd),
+              "mlp.gate_proj": (ffn, d), "mlp.up_proj": (ffn, d), "mlp.down_proj": (d, ffn)}
+    for l in range(n_layer):
+        for nm in ("input_layernorm", "post_attention_layernorm", "pre_feedforward_layernorm",
+                   "post_feedforward_layernorm"):
+            w.put_small(f"l{l}.{nm}", gain(), None, dtype)
+        for proj, (o, i) in shapes.items():
+            if raw:  # seeded random nibbles and f16 group scales, written as stored
+                g = 32
+                packed = rng.integers(0, 256, (o, (i + 1) // 2), dtype=np.uint8)
+                s16 = rng.uniform(0.5, 1.0, (o, (i + g - 1) // g)).astype(np.float32) * np.float32(std / 2.5)
+                nb = w._write(np.ascontiguousarray(packed))
+                w.entry(f"l{l}.{proj}", "i4", (o, i), nb, group=g)
+                w.put_f16(f"l{l}.{proj}__scale", s16)
+            else:
+                w.put_lin(f"l{l}.{proj}", nrm(o, i), dtype)
+    m = manifest("gemma", [n_layer, n_head, n_kv, hd, d, ffn, vocab, 1],
+                 [10000.0, 1e-6, 50.0, 30.0, float(hd), float(np.sqrt(d))])
+    w.finish(m)
+    return m

@@ -62,6 +62,7 @@ typedef struct frq_w frq_w;
 typedef struct frq_moe_w frq_moe_w;
 typedef struct frq_bundle frq_bundle;
 typedef struct frq_gpt2 frq_gpt2;
+typedef struct frq_gemma frq_gemma;
 
 /* Last error message of the calling thread ("" when none). */
 const char* frq_last_error(void);
@@ -265,6 +266,24 @@ int frq_gpt2_predict(frq_ctx* ctx, frq_gpt2* g, const int64_t* ids, size_t n, in
 /* Decode steps run as one captured HIP graph per generate call (replayed
  * per token) unless switched off here; the results are the same. */
 int frq_gpt2_set_graphs(frq_gpt2* g, int on);
+/* ---- Gemma-2 decode: Gemma (src/gemma.rs) on the device -----------------
+ * frq_gemma_load is Gemma::new (52-60) over an arch "gemma" bundle (config
+ * [n_layer, H, nkv, hd, d, ffn, vocab, tied], config_f [theta, eps,
+ * attn_cap, final_cap, query_pre_attn_scalar, escale]; arrays as
+ * convert_gemma writes them, src/convert.rs:636-657): int4 / int8 / q4a
+ * linears (q|k|v and gate|up uploaded side by side), the f16 embed (rows and
+ * the tied unembed), the RMSNorm gains; kv_int8: the int8 cache of
+ * forward_block_q (293-363).  generate / predict as Model::generate
+ * (403-431) / predict (436-441): tokens and logits as the reference's.
+ * The cache and the RoPE table grow to the longest call. */
+int frq_gemma_load(frq_ctx* ctx, const frq_bundle* b, int kv_int8, frq_gemma** out);
+void frq_gemma_free(frq_gemma* g);
+int frq_gemma_info(const frq_gemma* g, size_t* n_layer, size_t* d, size_t* vocab);
+int frq_gemma_generate(frq_ctx* ctx, frq_gemma* g, const int64_t* prompt, size_t n_prompt, size_t n_new,
+                       int64_t* out, float* logits);
+int frq_gemma_predict(frq_ctx* ctx, frq_gemma* g, const int64_t* ids, size_t n, int64_t* token,
+                      float* logits);
+int frq_gemma_set_graphs(frq_gemma* g, int on);
 /* The f32 libm functions the decode kernels use (fn 0 expf, 1 expm1f, 2
  * tanhf), bit-identical to the libm behind Rust's f32::exp / f32::tanh
  * (glibc's expf and fdlibm's expm1f / tanhf): out[i] = f(x[i]) for n host

@@ -59,6 +59,9 @@ def _load():
         "fro_q4a_dot": (F, [P, P, P, P, S, S]),
         "fro_q4a_dot_avx2": (F, [P, P, P, P, S, S]),
         "fro_mm_q4a": (I, [P, S, S, P, P, P, S, S, P]),
+        "fro_mm_i4_mt": (I, [P, S, S, P, P, S, S, P, I]),
+        "fro_rmsnorm": (None, [P, S, S, P, F, P]),
+        "fro_gemma_generate": (I, [P, P, S, S, I, I, P, P]),
         "fro_gpt2_generate": (I, [P, P, S, S, I, I, P, P]),
         "fro_gpt2_predict": (I, [P, P, S, I, P, P]),
     }
@@ -434,4 +437,89 @@ def mm_q4a(a, packed, scale_f32, min_f32, k, g):
     out = np.empty((a.shape[0], n), np.float32)
     lib.fro_mm_q4a(_p(a), a.shape[0], k, _p(packed), _p(_c(scale_f32, np.float32)), _p(_c(min_f32, np.float32)),
                    n, g, _p(out))
+    return out
+
+
+# ---- Gemma-2 with a KV cache (src/gemma.rs) ----
+class _Lin(C.Structure):
+    _fields_ = [("dtype", C.c_int), ("n", C.c_size_t), ("k", C.c_size_t), ("g", C.c_size_t),
+                ("packed", C.c_void_p), ("wt", C.c_void_p), ("scale", C.c_void_p), ("mins", C.c_void_p)]
+
+
+class _GemmaW(C.Structure):
+    _fields_ = [("n_layer", C.c_size_t), ("n_head", C.c_size_t), ("n_kv", C.c_size_t), ("hd", C.c_size_t),
+                ("d", C.c_size_t), ("ffn", C.c_size_t), ("vocab", C.c_size_t), ("window", C.c_size_t),
+                ("theta", C.c_float), ("eps", C.c_float), ("attn_cap", C.c_float), ("qscale", C.c_float),
+                ("escale", C.c_float), ("embed", C.c_void_p), ("norm", C.c_void_p), ("norms", C.c_void_p),
+                ("lin", C.c_void_p)]
+
+
+class Gemma:
+    """The oracle's Gemma-2 over a bundle's arrays (Gemma::new, gemma.rs:
+    52-60: config [n_layer, H, nkv, hd, d, ffn, vocab, tied], config_f
+    [theta, eps, attn_cap, final_cap, qscalar, escale], window 4096).
+    Linears as Bundle::load keeps them: int4 packed + f32 scales, int8
+    transposed to (N, K)."""
+
+    def __init__(self, manifest, arrs, nthreads: int = 8):
+        L, H, KV, hd, d, ffn, vocab = (int(c) for c in manifest["config"][:7])
+        theta, eps, cap, _fcap, qscalar, escale = (float(c) for c in manifest["config_f"][:6])
+        f32 = lambda n: np.ascontiguousarray(arrs[n], np.float32)
+        self.keep = []
+        norms = []
+        lins = (_Lin * (7 * L))()
+        names = ["self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj", "mlp.gate_proj",
+                 "mlp.up_proj", "mlp.down_proj"]
+        info = {e["name"]: e for e in manifest["arrays"]}
+        for l in range(L):
+            for nm in ("input_layernorm", "post_attention_layernorm", "pre_feedforward_layernorm",
+                       "post_feedforward_layernorm"):
+                norms.append(f32(f"l{l}.{nm}"))
+            for j, nm in enumerate(names):
+                a = arrs[f"l{l}.{nm}"]
+                sc = f32(f"l{l}.{nm}__scale")
+                ent = info[f"l{l}.{nm}"]
+                if ent.get("dtype") == "i8":       # stored (in, out)
+                    wt = np.ascontiguousarray(a.T)
+                    lins[7 * l + j] = _Lin(1, wt.shape[0], wt.shape[1], 0, None, wt.ctypes.data, sc.ctypes.data,
+                                           None)
+                    self.keep.append(wt)
+                else:                              # i4 / q4a stored (out, in) packed
+                    n, k = ent["shape"]
+                    q4a = ent.get("dtype") == "q4a"
+                    g = ent.get("group") or (64 if q4a else 32)
+                    pk = np.ascontiguousarray(a)
+                    mn = f32(f"l{l}.{nm}__min") if q4a else None
+                    lins[7 * l + j] = _Lin(3 if q4a else 2, n, k, g, pk.ctypes.data, None, sc.ctypes.data,
+                                           None if mn is None else mn.ctypes.data)
+                    self.keep += [pk, mn]
+                self.keep.append(sc)
+        self.keep.extend(norms)
+        nptr = (C.c_void_p * len(norms))(*[n.ctypes.data for n in norms])
+        self.keep += [lins, nptr]
+        self.embed = np.ascontiguousarray(arrs["embed"]).view(np.uint16)
+        self.norm = f32("norm")
+        self.s = _GemmaW(L, H, KV, hd, d, ffn, vocab, 4096, np.float32(theta), np.float32(eps), np.float32(cap),
+                         np.float32(np.float32(qscalar) ** np.float32(-0.5)), np.float32(escale),
+                         self.embed.ctypes.data, self.norm.ctypes.data, C.cast(nptr, C.c_void_p),
+                         C.cast(lins, C.c_void_p))
+        self.vocab, self.nthreads = vocab, nthreads
+
+    def generate(self, prompt, n_new: int, kv_int8: bool = False, with_logits: bool = False):
+        prompt = _c(prompt, np.int64)
+        out = np.empty(n_new, np.int64)
+        lg = np.empty((n_new, self.vocab), np.float32) if with_logits else None
+        rc = lib.fro_gemma_generate(C.byref(self.s), _p(prompt), len(prompt), n_new, int(kv_int8),
+                                    self.nthreads, _p(out), _p(lg))
+        if rc == 3:
+            raise OracleNaN("NaN in activations or logits")
+        if rc:
+            raise IndexError("token beyond the vocabulary")
+        return (out, lg) if with_logits else out
+
+
+def rmsnorm(x, w, eps: float):
+    x = _c(x, np.float32)
+    out = np.empty_like(x)
+    lib.fro_rmsnorm(_p(x), x.shape[0], x.shape[1], _p(_c(w, np.float32)), eps, _p(out))
     return out

@@ -993,3 +993,265 @@ int fro_mm_q4a(const float* a, size_t m, size_t k, const uint8_t* packed, const 
     free(wcol);
     return FRO_OK;
 }
+
+/* fro_mm_i4 with the output columns split over nthreads threads (each
+ * column's arithmetic as fro_mm_i4's: identical results). */
+typedef struct { const float* a; size_t m, k; const uint8_t* packed; const float* scale; size_t n, g; float* out;
+                 size_t lo, hi; } i4_job;
+static void* i4_worker(void* p) {
+    i4_job* J = (i4_job*)p;
+    size_t ng = (J->k + J->g - 1) / J->g, rb = (J->k + 1) / 2;
+    if (J->m == 1) {
+        for (size_t j = J->lo; j < J->hi; j++)
+            J->out[j] = fro_i4_dot_avx2(J->packed + j * rb, J->a, J->scale + j * ng, J->g, J->k);
+        return NULL;
+    }
+    float* wcol = (float*)malloc(nz(J->k) * sizeof(float));
+    for (size_t j = J->lo; j < J->hi; j++) {
+        for (size_t kk = 0; kk < J->k; kk++)
+            wcol[kk] = (float)nib_s4(J->packed + j * rb, kk) * J->scale[j * ng + kk / J->g];
+        for (size_t i = 0; i < J->m; i++) {
+            float acc = 0.0f;
+            for (size_t kk = 0; kk < J->k; kk++) acc = fmaf(J->a[i * J->k + kk], wcol[kk], acc);
+            J->out[i * J->n + j] = acc;
+        }
+    }
+    free(wcol);
+    return NULL;
+}
+int fro_mm_i4_mt(const float* a, size_t m, size_t k, const uint8_t* packed, const float* scale, size_t n, size_t g,
+                 float* out, int nthreads) {
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > 256) nthreads = 256;
+    pthread_t th[256];
+    i4_job jobs[256];
+    for (int w = 0; w < nthreads; w++) {
+        jobs[w] = (i4_job){a, m, k, packed, scale, n, g, out, n * (size_t)w / nthreads, n * (size_t)(w + 1) / nthreads};
+        pthread_create(&th[w], NULL, i4_worker, &jobs[w]);
+    }
+    for (int w = 0; w < nthreads; w++) pthread_join(th[w], NULL);
+    return FRO_OK;
+}
+
+static int lin_mm(const fro_lin_t* L, const float* a, size_t m, float* out, int nthreads) {
+    if (L->dtype == 2) return fro_mm_i4_mt(a, m, L->k, L->packed, L->scale, L->n, L->g, out, nthreads);
+    if (L->dtype == 3) return fro_mm_q4a(a, m, L->k, L->packed, L->scale, L->mins, L->n, L->g, out);
+    return fro_mm_i8_mt(a, m, L->k, L->wt, L->scale, L->n, out, nthreads);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Gemma-2 greedy decode with a KV cache: Gemma (src/gemma.rs): norm 66-77,  */
+/* rope 79-94, forward_block 242-291, forward_block_q 293-363, head_argmax   */
+/* 386-390, generate 403-431 (kv_int8: generate_kv_int8 364-384).            */
+/* ------------------------------------------------------------------------ */
+
+/* RMSNorm with the +1 baked gain (gemma.rs:66-77): ms = the fold from -0.0
+ * of v*v / n, inv = 1 / sqrt(ms + eps), v * inv * w. */
+void fro_rmsnorm(const float* x, size_t m, size_t d, const float* w, float eps, float* out) {
+    for (size_t r = 0; r < m; r++) {
+        const float* row = x + r * d;
+        float ms = -0.0f;
+        for (size_t i = 0; i < d; i++) ms = ms + row[i] * row[i];
+        ms = ms / (float)d;
+        const float inv = 1.0f / sqrtf(ms + eps);
+        for (size_t i = 0; i < d; i++) out[r * d + i] = row[i] * inv * w[i];
+    }
+}
+
+typedef struct {
+    const fro_gemma_t* g;
+    int nthreads, kv8;
+    float* inv;                       /* RoPE inverse frequencies (hd / 2) */
+    float** kc; float** vc;           /* f32 cache (total, nkv*hd) per layer */
+    int8_t** kq; int8_t** vq;
+    float** ks; float** vs;           /* (total, nkv) */
+} gm_run;
+
+/* rope (gemma.rs:79-94) on n_heads heads of m rows at positions pos0.. */
+static void gm_rope(const gm_run* R, float* x, size_t m, size_t n_heads, size_t pos0) {
+    const size_t hd = R->g->hd, half = hd / 2;
+    for (size_t i = 0; i < m; i++) {
+        float* row = x + i * n_heads * hd;
+        for (size_t h = 0; h < n_heads; h++)
+            for (size_t j = 0; j < half; j++) {
+                const float ang = (float)(pos0 + i) * R->inv[j];
+                const float c = cosf(ang), s = sinf(ang);
+                const float a = row[h * hd + j], b = row[h * hd + j + half];
+                row[h * hd + j] = a * c - b * s;
+                row[h * hd + j + half] = b * c + a * s;
+            }
+    }
+}
+
+static int gm_block(gm_run* R, float* x, size_t m, size_t cur) {
+    const fro_gemma_t* g = R->g;
+    const size_t d = g->d, H = g->n_head, KV = g->n_kv, hd = g->hd, rep = H / KV, kvd = KV * hd, klen = cur + m;
+    float* a = (float*)malloc(nz(m * d * 4));
+    float* q = (float*)malloc(nz(m * H * hd * 4));
+    float* k = (float*)malloc(nz(m * kvd * 4));
+    float* v = (float*)malloc(nz(m * kvd * 4));
+    float* att = (float*)malloc(nz(m * H * hd * 4));
+    float* o = (float*)malloc(nz(m * d * 4));
+    float* gate = (float*)malloc(nz(m * g->ffn * 4));
+    float* up = (float*)malloc(nz(m * g->ffn * 4));
+    float* sc = (float*)malloc(nz(klen * 4));
+    float* kh = (float*)malloc(nz(klen * hd * 4));
+    float* vh = (float*)malloc(nz(klen * hd * 4));
+    int rc = FRO_OK;
+    for (size_t l = 0; l < g->n_layer && !rc; l++) {
+        const fro_lin_t* L = g->lin + 7 * l;
+        const float* const* N = g->norms + 4 * l;
+        fro_rmsnorm(x, m, d, N[0], g->eps, a);
+        if ((rc = lin_mm(&L[0], a, m, q, R->nthreads)) || (rc = lin_mm(&L[1], a, m, k, R->nthreads)) ||
+            (rc = lin_mm(&L[2], a, m, v, R->nthreads)))
+            break;
+        gm_rope(R, q, m, H, cur);
+        gm_rope(R, k, m, KV, cur);
+        for (size_t i = 0; i < m; i++) {  /* append K/V */
+            const size_t pos = cur + i;
+            if (!R->kv8) {
+                memcpy(R->kc[l] + pos * kvd, k + i * kvd, kvd * 4);
+                memcpy(R->vc[l] + pos * kvd, v + i * kvd, kvd * 4);
+            } else {
+                for (size_t kh_ = 0; kh_ < KV; kh_++) {
+                    const float* kr = k + i * kvd + kh_ * hd;
+                    const float* vr = v + i * kvd + kh_ * hd;
+                    float mk = 0.0f, mv = 0.0f;
+                    for (size_t c = 0; c < hd; c++) { mk = fmaxf(mk, fabsf(kr[c])); mv = fmaxf(mv, fabsf(vr[c])); }
+                    const float sck = fmaxf(mk / 127.0f, 1e-8f), scv = fmaxf(mv / 127.0f, 1e-8f);
+                    R->ks[l][pos * KV + kh_] = sck;
+                    R->vs[l][pos * KV + kh_] = scv;
+                    for (size_t c = 0; c < hd; c++) {
+                        R->kq[l][pos * kvd + kh_ * hd + c] = kv_q8(kr[c], sck);
+                        R->vq[l][pos * kvd + kh_ * hd + c] = kv_q8(vr[c], scv);
+                    }
+                }
+            }
+        }
+        const int sliding = l % 2 == 0;
+        for (size_t h = 0; h < H; h++) {
+            const size_t kv = h / rep;
+            for (size_t j = 0; j < klen; j++)
+                for (size_t c = 0; c < hd; c++) {
+                    if (!R->kv8) {
+                        kh[j * hd + c] = R->kc[l][j * kvd + kv * hd + c];
+                        vh[j * hd + c] = R->vc[l][j * kvd + kv * hd + c];
+                    } else {
+                        kh[j * hd + c] = (float)R->kq[l][j * kvd + kv * hd + c] * R->ks[l][j * KV + kv];
+                        vh[j * hd + c] = (float)R->vq[l][j * kvd + kv * hd + c] * R->vs[l][j * KV + kv];
+                    }
+                }
+            for (size_t i = 0; i < m; i++) {
+                const float* qr = q + i * H * hd + h * hd;
+                const size_t abs_ = cur + i;
+                for (size_t j = 0; j < klen; j++) {
+                    float acc = 0.0f;
+                    for (size_t c = 0; c < hd; c++) acc = fmaf(qr[c], kh[j * hd + c], acc);
+                    float s = acc * g->qscale;
+                    if (g->attn_cap > 0.0f) s = g->attn_cap * tanhf(s / g->attn_cap);
+                    if (j > abs_ || (sliding && abs_ >= g->window && j <= abs_ - g->window)) s = -1e30f;
+                    sc[j] = s;
+                }
+                softmax_row(sc, klen);
+                for (size_t c = 0; c < hd; c++) {
+                    float acc = 0.0f;
+                    for (size_t j = 0; j < klen; j++) acc = fmaf(sc[j], vh[j * hd + c], acc);
+                    att[i * H * hd + h * hd + c] = acc;
+                }
+            }
+        }
+        if ((rc = lin_mm(&L[3], att, m, o, R->nthreads))) break;
+        fro_rmsnorm(o, m, d, N[1], g->eps, a);
+        for (size_t i = 0; i < m * d; i++) x[i] = x[i] + a[i];
+        fro_rmsnorm(x, m, d, N[2], g->eps, a);
+        if ((rc = lin_mm(&L[4], a, m, gate, R->nthreads)) || (rc = lin_mm(&L[5], a, m, up, R->nthreads))) break;
+        for (size_t i = 0; i < m * g->ffn; i++) gate[i] = fro_gelu_tanh(gate[i]) * up[i];
+        if ((rc = lin_mm(&L[6], gate, m, o, R->nthreads))) break;
+        fro_rmsnorm(o, m, d, N[3], g->eps, a);
+        for (size_t i = 0; i < m * d; i++) x[i] = x[i] + a[i];
+    }
+    free(a); free(q); free(k); free(v); free(att); free(o); free(gate); free(up); free(sc); free(kh); free(vh);
+    return rc;
+}
+
+typedef struct { const fro_gemma_t* g; const float* x; float* out; size_t lo, hi; } gm_head_job;
+static void* gm_head_worker(void* p) {
+    gm_head_job* J = (gm_head_job*)p;
+    fro_rowdot_f32(FRO_DT_F16, J->g->embed + J->lo * J->g->d, NULL, J->hi - J->lo, J->g->d, J->x, J->out + J->lo);
+    return NULL;
+}
+
+/* the final norm of the last row, then head_argmax (gemma.rs:386-390) */
+static int gm_head(gm_run* R, const float* xlast, float* logits, int64_t* tok) {
+    const fro_gemma_t* g = R->g;
+    float* xf = (float*)malloc(nz(g->d * 4));
+    fro_rmsnorm(xlast, 1, g->d, g->norm, g->eps, xf);
+    int nt = R->nthreads < 1 ? 1 : (R->nthreads > 64 ? 64 : R->nthreads);
+    pthread_t th[64];
+    gm_head_job jobs[64];
+    for (int w = 0; w < nt; w++) {
+        jobs[w] = (gm_head_job){g, xf, logits, g->vocab * (size_t)w / nt, g->vocab * (size_t)(w + 1) / nt};
+        pthread_create(&th[w], NULL, gm_head_worker, &jobs[w]);
+    }
+    for (int w = 0; w < nt; w++) pthread_join(th[w], NULL);
+    free(xf);
+    size_t best = 0;
+    for (size_t r = 0; r < g->vocab; r++) {
+        if (isnan(logits[r])) return FRO_ERR_NAN;
+        if (logits[r] >= logits[best]) best = r;
+    }
+    *tok = (int64_t)best;
+    return FRO_OK;
+}
+
+static int gm_embed(const fro_gemma_t* g, const int64_t* ids, size_t m, float* x) {
+    for (size_t t = 0; t < m; t++) {
+        if (ids[t] < 0 || (size_t)ids[t] >= g->vocab) return FRO_ERR_ARG;
+        for (size_t c = 0; c < g->d; c++) x[t * g->d + c] = fro_f16_to_f32(g->embed[(size_t)ids[t] * g->d + c]) * g->escale;
+    }
+    return FRO_OK;
+}
+
+int fro_gemma_generate(const fro_gemma_t* g, const int64_t* prompt, size_t n_prompt, size_t n_new, int kv_int8,
+                       int nthreads, int64_t* out, float* logits) {
+    if (!n_prompt || !n_new) return FRO_ERR_ARG;
+    const size_t d = g->d, L = g->n_layer, total = n_prompt + n_new, kvd = g->n_kv * g->hd;
+    gm_run R;
+    memset(&R, 0, sizeof R);
+    R.g = g; R.nthreads = nthreads; R.kv8 = kv_int8;
+    R.inv = (float*)malloc(nz(g->hd / 2 * 4));
+    for (size_t j = 0; j < g->hd / 2; j++) R.inv[j] = 1.0f / powf(g->theta, 2.0f * (float)j / (float)g->hd);
+    R.kc = (float**)calloc(L, sizeof(float*)); R.vc = (float**)calloc(L, sizeof(float*));
+    R.kq = (int8_t**)calloc(L, sizeof(int8_t*)); R.vq = (int8_t**)calloc(L, sizeof(int8_t*));
+    R.ks = (float**)calloc(L, sizeof(float*)); R.vs = (float**)calloc(L, sizeof(float*));
+    for (size_t l = 0; l < L; l++) {
+        if (!kv_int8) {
+            R.kc[l] = (float*)calloc(total * kvd, 4); R.vc[l] = (float*)calloc(total * kvd, 4);
+        } else {
+            R.kq[l] = (int8_t*)calloc(total * kvd, 1); R.vq[l] = (int8_t*)calloc(total * kvd, 1);
+            R.ks[l] = (float*)calloc(total * g->n_kv, 4); R.vs[l] = (float*)calloc(total * g->n_kv, 4);
+        }
+    }
+    float* x = (float*)malloc(nz(n_prompt * d * 4));
+    float* lg = (float*)malloc(nz(g->vocab * 4));
+    int64_t next = 0;
+    int rc = gm_embed(g, prompt, n_prompt, x);
+    if (!rc) rc = gm_block(&R, x, n_prompt, 0);
+    if (!rc) rc = gm_head(&R, x + (n_prompt - 1) * d, lg, &next);
+    size_t pos = n_prompt;
+    for (size_t s = 0; !rc; s++) {
+        out[s] = next;
+        if (logits) memcpy(logits + s * g->vocab, lg, g->vocab * 4);
+        if (s + 1 == n_new) break;
+        rc = gm_embed(g, &next, 1, x);
+        if (!rc) rc = gm_block(&R, x, 1, pos);
+        if (!rc) rc = gm_head(&R, x, lg, &next);
+        pos++;
+    }
+    for (size_t l = 0; l < L; l++) {
+        free(R.kc[l]); free(R.vc[l]); free(R.kq[l]); free(R.vq[l]); free(R.ks[l]); free(R.vs[l]);
+    }
+    free(R.kc); free(R.vc); free(R.kq); free(R.vq); free(R.ks); free(R.vs); free(R.inv);
+    free(x); free(lg);
+    return rc;
+}

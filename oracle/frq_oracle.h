@@ -192,6 +192,41 @@ int fro_gpt2_generate(const fro_gpt2_t* g, const int64_t* prompt, size_t n_promp
 /* Model::predict (composition.rs:304-308). */
 int fro_gpt2_predict(const fro_gpt2_t* g, const int64_t* ids, size_t n, int nthreads, int64_t* tok, float* logits);
 
+/* fro_mm_i4 over nthreads threads (columns split; identical results). */
+int fro_mm_i4_mt(const float* a, size_t m, size_t k, const uint8_t* packed, const float* scale, size_t n, size_t g,
+                 float* out, int nthreads);
+
+/* A linear as Bundle::load keeps it: dtype 1 int8 (wt (N,K) transposed,
+ * scale f32 [N]), 2 int4 (packed (N, ceil(K/2)), scale f32 (N, ng), g) or
+ * 3 q4a (as int4 plus mins f32 (N, ng)). */
+typedef struct {
+    int dtype;
+    size_t n, k, g;
+    const uint8_t* packed;
+    const int8_t* wt;
+    const float* scale;
+    const float* mins;
+} fro_lin_t;
+
+/* Gemma-2 (src/gemma.rs).  norms[4l + 0..3]: input, post_attention,
+ * pre_feedforward, post_feedforward (f32, the +1 baked); lin[7l + 0..6]:
+ * q, k, v, o, gate, up, down. qscale = query_pre_attn_scalar^-0.5. */
+typedef struct {
+    size_t n_layer, n_head, n_kv, hd, d, ffn, vocab, window;
+    float theta, eps, attn_cap, qscale, escale;
+    const uint16_t* embed;      /* (vocab, d) f16 bits: embedding and tied unembed */
+    const float* norm;          /* final norm */
+    const float* const* norms;
+    const fro_lin_t* lin;
+} fro_gemma_t;
+
+/* RMSNorm with the baked (1 + w) gain (gemma.rs:66-77) over m rows. */
+void fro_rmsnorm(const float* x, size_t m, size_t d, const float* w, float eps, float* out);
+/* Gemma::generate (gemma.rs:403-431; kv_int8: 364-384): n_new greedy
+ * tokens, logits (n_new, vocab) nullable. */
+int fro_gemma_generate(const fro_gemma_t* g, const int64_t* prompt, size_t n_prompt, size_t n_new, int kv_int8,
+                       int nthreads, int64_t* out, float* logits);
+
 #ifdef __cplusplus
 }
 #endif
