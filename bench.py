@@ -18,7 +18,8 @@ library's stream.  Also reported (in "detail"): the GEMV kernel alone on
 pre-quantised input, the M=2048 MFMA-bound shapes in TOPS, the int4 decode
 GEMV and the affine-int4 (q4a) GEMV on Gemma-2 shapes, the unembed row dot, the config-4 MoE layer, and
 config 0 end to end: GPT-2 small greedy decode (tok/s, f32 and int8 KV
-caches) with the oracle's CPU rate and token check beside it.  The CPU
+caches) with the oracle's CPU rate and token check beside it, and config 2:
+Gemma-2-2b int4 greedy decode (256 tokens after a 64-token prompt).  The CPU
 baseline is the
 oracle's restatement of the reference's scalar int8 path (the
 `_scalar_i8_bench` build) on the host's cores, on a bounded sample.
@@ -395,6 +396,44 @@ def main():
                                                        "tokens_identical": same}
                 log(f"gpt2 oracle: {detail['gpt2_decode']['cpu_oracle']}")
                 g.free()
+            b.close()
+        # ---------------- Gemma-2-2b int4 greedy decode (config 2) ----------------
+        # 26 layers, int4 g=32 (seeded random nibbles and f16 scales), f16 embed
+        # and tied unembed, 64-token seeded prompt, 256 greedy tokens, batch 1
+        detail["gemma2_decode"] = {}
+        with tempfile.TemporaryDirectory() as tmp:
+            stem = os.path.join(tmp, "gemma2")
+            synth.write_gemma2_bundle(stem, 2, raw=True)
+            b = fa.Bundle(stem, ctx)
+            g = fa.Gemma(b)
+            g.set_graphs(not args.no_graphs)
+            prompt = synth.gpt2_prompt(64, 256000, 7)
+            g.generate(prompt, 8)
+            runs = {}
+            for n_new in (1, 256):
+                t0 = time.perf_counter()
+                g.generate(prompt, n_new)
+                runs[n_new] = time.perf_counter() - t0
+            dec_ms = (runs[256] - runs[1]) / 255 * 1e3
+            detail["gemma2_decode"]["int4_kv_f32"] = {
+                "tok_s": round(256 / runs[256], 1), "decode_ms_per_token": round(dec_ms, 3),
+                "decode_tok_s": round(1e3 / dec_ms, 1), "prefill_plus_first_ms": round(runs[1] * 1e3, 1)}
+            log(f"gemma2 decode: {detail['gemma2_decode']['int4_kv_f32']}")
+            if not args.no_cpu:
+                import oracle  # the reference's Gemma restated in C (the CPU rate beside the device's)
+
+                m_, arrs = oracle.read_bundle(stem)
+                threads = min(os.cpu_count() or 1, 16)
+                ref = oracle.Gemma(m_, arrs, nthreads=threads)
+                t0 = time.perf_counter()
+                rt = ref.generate(prompt[:8], 4)
+                el = time.perf_counter() - t0
+                same = bool(np.array_equal(rt, g.generate(prompt[:8], 4)))
+                detail["gemma2_decode"]["cpu_oracle"] = {"seconds": round(el, 2), "threads": threads,
+                                                         "sample": "8-token prompt, 4 tokens (prefill-dominated)",
+                                                         "tokens_identical": same}
+                log(f"gemma2 oracle: {detail['gemma2_decode']['cpu_oracle']}")
+            g.free()
             b.close()
 
     # ---------------- CPU baseline (the oracle's scalar restatement) ----------------

@@ -129,15 +129,24 @@ __device__ inline float lds_seq_sum(const float* p, int n, float acc) {
             acc = acc + b[u].w;
         }
     };
+    // two batches a trip, both consumed unconditionally, the odd last batch
+    // after the loop; the scheduling barriers keep each batch's loads where
+    // they are issued, a batch ahead of their adds (the scheduler would
+    // otherwise sink them down to the use)
     if (nb > 0) {
         ld(b0, 0);
         ld(b1, min(1, nb - 1));
-        for (int k = 0; k < nb; k += 2) {
+        __builtin_amdgcn_sched_barrier(0);
+        int k = 0;
+        for (; k + 2 <= nb; k += 2) {
             add(b0);
             ld(b0, min(k + 2, nb - 1));
-            if (k + 1 < nb) add(b1);
+            __builtin_amdgcn_sched_barrier(0);
+            add(b1);
             ld(b1, min(k + 3, nb - 1));
+            __builtin_amdgcn_sched_barrier(0);
         }
+        if (k < nb) add(b0);
     }
     for (int i = nb * 4 * B; i < n; ++i) acc = acc + p[i];
     return acc;

@@ -88,15 +88,20 @@ __device__ float seq_sum8(const float* p, int n, float acc) {
 #pragma unroll
         for (int u = 0; u < B; ++u) acc = acc + b[u];
     };
-    if (nb > 0) {
+    if (nb > 0) {  // as lds_seq_sum: loads pinned a batch ahead of their adds
         ld(b0, 0);
         ld(b1, min(1, nb - 1));
-        for (int k = 0; k < nb; k += 2) {
+        __builtin_amdgcn_sched_barrier(0);
+        int k = 0;
+        for (; k + 2 <= nb; k += 2) {
             add(b0);
             ld(b0, min(k + 2, nb - 1));
-            if (k + 1 < nb) add(b1);
+            __builtin_amdgcn_sched_barrier(0);
+            add(b1);
             ld(b1, min(k + 3, nb - 1));
+            __builtin_amdgcn_sched_barrier(0);
         }
+        if (k < nb) add(b0);
     }
     for (int i = nb * B; i < n; ++i) acc = acc + p[i * 8];
     return acc;
@@ -309,15 +314,20 @@ __global__ __launch_bounds__(NT) void attn_kernel(const float* __restrict__ qkv,
 #pragma unroll
             for (int u = 0; u < B; ++u) acc = __builtin_fmaf(p[k * B + u], v[u], acc);
         };
-        if (nb > 0) {
+        if (nb > 0) {  // both batches of a trip consumed unconditionally, loads pinned a batch ahead
             ld(v0, 0);
             ld(v1, min(1, nb - 1));
-            for (int k = 0; k < nb; k += 2) {
+            __builtin_amdgcn_sched_barrier(0);
+            int k = 0;
+            for (; k + 2 <= nb; k += 2) {
                 fma_b(v0, k);
                 ld(v0, min(k + 2, nb - 1));
-                if (k + 1 < nb) fma_b(v1, k + 1);
+                __builtin_amdgcn_sched_barrier(0);
+                fma_b(v1, k + 1);
                 ld(v1, min(k + 3, nb - 1));
+                __builtin_amdgcn_sched_barrier(0);
             }
+            if (k < nb) fma_b(v0, k);
         }
         for (int j = nb * B; j < nk; ++j) {
             const float v = KV8 ? (float)vq[(size_t)j * d + col] * sv[j] : vc[(size_t)j * d + col];
