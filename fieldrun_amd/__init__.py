@@ -85,6 +85,7 @@ SIGNATURES = {
     "frq_gpt2_predict": (_I, [_P, _P, _P, _S, _P, _P]),
     "frq_libm_f32": (_I, [_P, _I, _P, _S, _P]),
     "frq_gemma_load": (_I, [_P, _P, _I, _P]),
+    "frq_rope_load": (_I, [_P, _P, _I, _P]),
     "frq_gemma_free": (None, [_P]),
     "frq_gemma_info": (_I, [_P, _P, _P, _P]),
     "frq_gemma_set_graphs": (_I, [_P, _I]),
@@ -564,13 +565,15 @@ class Gemma:
     bundle (52-60), Model::generate (403-431; kv_int8: 364-384) and
     Model::predict (436-441), every step resident in HBM."""
 
+    _loader = "frq_gemma_load"
+
     def __init__(self, bundle: "Bundle", kv_int8: bool = False, ctx: "Context | None" = None):
         self.ctx = ctx or bundle.ctx
         if self.ctx is None:
             raise FrqError(FRQ_ERR_ARG, "this bundle was opened without a device context")
         self.h = None
         out = C.c_void_p()
-        _check(lib.frq_gemma_load(self.ctx.h, bundle.h, int(kv_int8), C.byref(out)))
+        _check(getattr(lib, self._loader)(self.ctx.h, bundle.h, int(kv_int8), C.byref(out)))
         self.h = out.value
         dims = [C.c_size_t(0) for _ in range(3)]
         _check(lib.frq_gemma_info(self.h, *[C.byref(v) for v in dims]))
@@ -605,3 +608,11 @@ class Gemma:
         _check(lib.frq_gemma_predict(self.ctx.h, self.h, _ptr(ids), len(ids), _ptr(tok),
                                      None if lg is None else _ptr(lg)))
         return (int(tok[0]), lg) if with_logits else int(tok[0])
+
+
+class Rope(Gemma):
+    """Rope of src/rope.rs (Llama / Qwen2.5 / Qwen3 / Mistral) on the device:
+    Rope::new over an arch "rope" bundle (56-64), Model::generate
+    (1147-1170) and predict (730-734), in the same engine as Gemma."""
+
+    _loader = "frq_rope_load"

@@ -77,7 +77,8 @@ __device__ void rms_row(const float* v, float* sq, const float* __restrict__ w, 
     __syncthreads();
 }
 
-// Row r = row0 + blockIdx.x.  y set: x += norm(y, wpost); then out =
+// Row r = row0 + blockIdx.x.  y set: x += norm(y, wpost) (gemma's post-norm
+// before the residual) or, wpost NULL, x += y (rope.rs); then out =
 // norm(x, wnext).  LDS: three rows of d floats.
 __global__ __launch_bounds__(GT) void gm_norm_kernel(float* __restrict__ x, const float* __restrict__ y,
                                                      const float* __restrict__ wpost, const float* __restrict__ wnext,
@@ -88,12 +89,18 @@ __global__ __launch_bounds__(GT) void gm_norm_kernel(float* __restrict__ x, cons
     float* t = sq + d;
     __shared__ float stat[1];
     const size_t r = (size_t)(row0 + blockIdx.x) * d;
-    if (y) {
+    if (y && wpost) {
         for (int c = threadIdx.x; c < d; c += GT) v[c] = y[r + c];
         __syncthreads();
         rms_row(v, sq, wpost, d, eps, t, stat);
         for (int c = threadIdx.x; c < d; c += GT) {
             const float nx = x[r + c] + t[c];
+            x[r + c] = nx;
+            v[c] = nx;
+        }
+    } else if (y) {  // rope.rs: x = x + y, no post-norm
+        for (int c = threadIdx.x; c < d; c += GT) {
+            const float nx = x[r + c] + y[r + c];
             x[r + c] = nx;
             v[c] = nx;
         }
@@ -130,6 +137,16 @@ __device__ void kv_quant_wave(const float* src, int hd, int8_t* dq, float* sdst)
     if (lane == 0) *sdst = sc;
 }
 
+// Rope::head_norm (rope.rs:72-87) on one head of hd values in place, by the
+// calling lane: ms = the fold from -0.0 of v*v / hd, v * inv * w.
+__device__ void head_norm_lane(float* v, int hd, const float* __restrict__ w, float eps) {
+    float ms = -0.0f;
+    for (int c = 0; c < hd; ++c) ms = ms + v[c] * v[c];
+    ms = ms / (float)hd;
+    const float inv = 1.0f / sqrtf(ms + eps);
+    for (int c = 0; c < hd; ++c) v[c] = v[c] * inv * w[c];
+}
+
 // Prefill: rope the q and k heads of row i in the qkv buffer and append k,
 // v to cache row cur + i.  qkv row: [q (H hd) | k (KV hd) | v (KV hd)].
 template <bool KV8>
@@ -137,11 +154,21 @@ __global__ __launch_bounds__(GT) void gm_qkv_kernel(float* __restrict__ qkv, int
                                                     const int* __restrict__ curp, const float2* __restrict__ cs,
                                                     float* __restrict__ kc, float* __restrict__ vc,
                                                     int8_t* __restrict__ kq, int8_t* __restrict__ vq,
-                                                    float* __restrict__ ks, float* __restrict__ vs) {
+                                                    float* __restrict__ ks, float* __restrict__ vs,
+                                                    const float* __restrict__ bias, const float* __restrict__ qn,
+                                                    const float* __restrict__ kn, float eps) {
     const int i = blockIdx.x, half = hd / 2, kvd = KV * hd;
     const size_t pos = (size_t)(*curp + i);
     float* row = qkv + (size_t)i * (H + 2 * KV) * hd;
     const float2* csp = cs + pos * half;
+    if (bias) {  // proj: y + bias (rope.rs:110-117)
+        for (int c = threadIdx.x; c < (H + 2 * KV) * hd; c += GT) row[c] = row[c] + bias[c];
+        __syncthreads();
+    }
+    if (qn) {  // the QK-norm, a lane per head
+        for (int t = threadIdx.x; t < H + KV; t += GT) head_norm_lane(row + t * hd, hd, t < H ? qn : kn, eps);
+        __syncthreads();
+    }
     for (int t = threadIdx.x; t < (H + KV) * half; t += GT) rope_pair(row + (t / half) * hd, t % half, half, csp);
     __syncthreads();
     if constexpr (!KV8) {
@@ -175,7 +202,9 @@ __global__ __launch_bounds__(GT) void gm_attn_kernel(const float* __restrict__ q
                                                      int8_t* __restrict__ kq, int8_t* __restrict__ vq,
                                                      float* __restrict__ ks, float* __restrict__ vs, float qscale,
                                                      float cap, int sliding, int window, int pstride,
-                                                     float* __restrict__ att) {
+                                                     float* __restrict__ att, int div,
+                                                     const float* __restrict__ bias, const float* __restrict__ qn,
+                                                     const float* __restrict__ kn, float eps) {
     extern __shared__ float4 lds4[];
     float* q = reinterpret_cast<float*>(lds4);
     float* kvs = q + ((hd + 3) & ~3);
@@ -188,11 +217,22 @@ __global__ __launch_bounds__(GT) void gm_attn_kernel(const float* __restrict__ q
     if constexpr (FUSED) {
         const size_t pos = (size_t)ab;
         for (int c = threadIdx.x; c < hd; c += GT) {
-            q[c] = row[h * hd + c];
-            kvs[c] = row[(H + kv) * hd + c];
-            kvs[((hd + 3) & ~3) + c] = row[(H + KV + kv) * hd + c];
+            float qv = row[h * hd + c], kv_ = row[(H + kv) * hd + c], vv = row[(H + KV + kv) * hd + c];
+            if (bias) {  // proj: y + bias (rope.rs:110-117)
+                qv = qv + bias[h * hd + c];
+                kv_ = kv_ + bias[(H + kv) * hd + c];
+                vv = vv + bias[(H + KV + kv) * hd + c];
+            }
+            q[c] = qv;
+            kvs[c] = kv_;
+            kvs[((hd + 3) & ~3) + c] = vv;
         }
         __syncthreads();
+        if (qn) {  // the QK-norm of this q head and kv head (two lanes)
+            if (threadIdx.x == 0) head_norm_lane(q, hd, qn, eps);
+            if (threadIdx.x == 64) head_norm_lane(kvs, hd, kn, eps);
+            __syncthreads();
+        }
         const float2* csp = cs + pos * half;
         for (int t = threadIdx.x; t < 2 * half; t += GT) rope_pair(t < half ? q : kvs, t % half, half, csp);
         __syncthreads();
@@ -238,7 +278,7 @@ __global__ __launch_bounds__(GT) void gm_attn_kernel(const float* __restrict__ q
                 acc = __builtin_fmaf(q[c + 3], (float)k4.w * sk, acc);
             }
         }
-        float sj = acc * qscale;
+        float sj = div ? acc / qscale : acc * qscale;  // rope.rs: / sqrt(hd); gemma.rs: * qscalar^-0.5
         if (cap > 0.0f) sj = cap * libm::frq_tanhf(sj / cap);
         p[j] = sj;
         mx = fmaxf(mx, sj);
@@ -297,13 +337,16 @@ __global__ __launch_bounds__(GT) void gm_attn_kernel(const float* __restrict__ q
     }
 }
 
-// h = gelu_tanh(gate) * up over m rows of the [gate | up] buffer.
+// h = act(gate) * up over m rows of the [gate | up] buffer: gelu_tanh
+// (gemma.rs:31-34) or, silu, x / (1 + exp(-x)) (rope.rs:39-41).
 __global__ __launch_bounds__(GT) void gm_geglu_kernel(const float* __restrict__ gu, int ffn, size_t total,
-                                                      float c, float* __restrict__ hm) {
+                                                      float c, float* __restrict__ hm, int silu) {
     for (size_t i = (size_t)blockIdx.x * GT + threadIdx.x; i < total; i += (size_t)gridDim.x * GT) {
         const size_t r = i / ffn, col = i - r * ffn;
         const float x = gu[r * 2 * ffn + col];
-        hm[i] = 0.5f * x * (1.0f + libm::frq_tanhf(c * (x + 0.044715f * x * x * x))) * gu[r * 2 * ffn + ffn + col];
+        const float a = silu ? x / (1.0f + libm::frq_expf(-x))
+                             : 0.5f * x * (1.0f + libm::frq_tanhf(c * (x + 0.044715f * x * x * x)));
+        hm[i] = a * gu[r * 2 * ffn + ffn + col];
     }
 }
 
@@ -330,10 +373,14 @@ struct frq_gemma {
     size_t window = 4096;
     float theta = 0, eps = 0, cap = 0, qscale = 0, escale = 0;
     int kv8 = 0, graphs = 1;
+    int arch = 0;                    // 0 gemma (gemma.rs), 1 the Llama / Qwen family (rope.rs)
     std::vector<float> inv;          // RoPE inverse frequencies
     std::vector<frq_w*> qkv, o, gu, down;
     frq_w* embed = nullptr;
+    frq_w* unembed = nullptr;        // rope, untied: lm_head (else the embed table)
     float* norms = nullptr;          // 4 per layer + the final norm, f32 (d each)
+    float* qkvbias = nullptr;        // rope: (H + 2 nkv) hd per layer, or NULL
+    float* qknorm = nullptr;         // rope (Qwen3): q_norm, k_norm (hd each) per layer, or NULL
     // sized to the largest call so far: positions (cache, RoPE table) and rows
     size_t cap_pos = 0, cap_rows = 0;
     char* buf = nullptr;
@@ -349,10 +396,18 @@ struct frq_gemma {
         for (auto* v : {&qkv, &o, &gu, &down})
             for (frq_w* w : *v) frq_w_free(w);
         frq_w_free(embed);
+        frq_w_free(unembed);
         if (norms) (void)hipFree(norms);
+        if (qkvbias) (void)hipFree(qkvbias);
+        if (qknorm) (void)hipFree(qknorm);
         if (buf) (void)hipFree(buf);
     }
     const float* norm_of(size_t l, int j) const { return norms + (4 * l + j) * d; }
+    // the post-norms before the residuals (gemma); rope has none
+    const float* post_of(size_t l, int j) const { return arch == 0 ? norm_of(l, j) : nullptr; }
+    const float* bias_of(size_t l) const { return qkvbias ? qkvbias + l * (H + 2 * KV) * hd : nullptr; }
+    const float* qn_of(size_t l) const { return qknorm ? qknorm + l * 2 * hd : nullptr; }
+    const float* kn_of(size_t l) const { return qknorm ? qknorm + l * 2 * hd + hd : nullptr; }
     const float* final_norm() const { return norms + 4 * L * d; }
 };
 
@@ -556,49 +611,55 @@ int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_o
         float* vs = g->kv8 ? g->vs + l * g->cap_pos * g->KV : nullptr;
         const dim3 ag((unsigned)H, (unsigned)m);
         const size_t lds = gm_attn_lds(g);
-        const int ps = (int)gm_pstride(g), sl = l % 2 == 0 ? 1 : 0, win = (int)g->window;
+        const int ps = (int)gm_pstride(g), sl = (g->arch == 0 && l % 2 == 0) ? 1 : 0, win = (int)g->window;
+        const float* qb = g->bias_of(l);
+        const float* qn = g->qn_of(l);
+        const float* kn = g->kn_of(l);
+        const int div = g->arch == 1;
         if (m == 1) {
             if (g->kv8)
                 gm_attn_kernel<true, true><<<ag, dim3(GT), lds, s>>>(g->qkvb, H, KV, hd, g->cur, g->cs, kc, vc, kq,
                                                                      vq, ks, vs, g->qscale, g->cap, sl, win, ps,
-                                                                     g->att);
+                                                                     g->att, div, qb, qn, kn, g->eps);
             else
                 gm_attn_kernel<false, true><<<ag, dim3(GT), lds, s>>>(g->qkvb, H, KV, hd, g->cur, g->cs, kc, vc, kq,
                                                                       vq, ks, vs, g->qscale, g->cap, sl, win, ps,
-                                                                      g->att);
+                                                                      g->att, div, qb, qn, kn, g->eps);
         } else {
             if (g->kv8)
                 gm_qkv_kernel<true><<<dim3((unsigned)m), dim3(GT), 0, s>>>(g->qkvb, H, KV, hd, g->cur, g->cs, kc, vc,
-                                                                           kq, vq, ks, vs);
+                                                                           kq, vq, ks, vs, qb, qn, kn, g->eps);
             else
                 gm_qkv_kernel<false><<<dim3((unsigned)m), dim3(GT), 0, s>>>(g->qkvb, H, KV, hd, g->cur, g->cs, kc,
-                                                                            vc, kq, vq, ks, vs);
+                                                                            vc, kq, vq, ks, vs, qb, qn, kn, g->eps);
             GMCHK(hipGetLastError(), "launch qkv");
             if (g->kv8)
                 gm_attn_kernel<true, false><<<ag, dim3(GT), lds, s>>>(g->qkvb, H, KV, hd, g->cur, g->cs, kc, vc, kq,
                                                                       vq, ks, vs, g->qscale, g->cap, sl, win, ps,
-                                                                      g->att);
+                                                                      g->att, div, nullptr, nullptr, nullptr, g->eps);
             else
                 gm_attn_kernel<false, false><<<ag, dim3(GT), lds, s>>>(g->qkvb, H, KV, hd, g->cur, g->cs, kc, vc,
                                                                        kq, vq, ks, vs, g->qscale, g->cap, sl, win,
-                                                                       ps, g->att);
+                                                                       ps, g->att, div, nullptr, nullptr, nullptr,
+                                                                       g->eps);
         }
         GMCHK(hipGetLastError(), "launch attention");
         if (int rc = gm_mm(c, g->o[l], g->att, m, g->ob)) return rc;
-        GMCHK(norm(g->ob, g->norm_of(l, 1), g->norm_of(l, 2), (int)m, 0), "launch norm");
+        GMCHK(norm(g->ob, g->post_of(l, 1), g->norm_of(l, 2), (int)m, 0), "launch norm");
         if (int rc = gm_mm(c, g->gu[l], g->a, m, g->gub)) return rc;
         const size_t tot = m * g->ffn;
         gm_geglu_kernel<<<dim3((unsigned)std::min<size_t>((tot + GT - 1) / GT, 4096)), dim3(GT), 0, s>>>(
-            g->gub, ffn, tot, sqrtf(2.0f / 3.14159274101257324f), g->hm);
+            g->gub, ffn, tot, sqrtf(2.0f / 3.14159274101257324f), g->hm, g->arch == 1 ? 1 : 0);
         GMCHK(hipGetLastError(), "launch geglu");
         if (int rc = gm_mm(c, g->down[l], g->hm, m, g->ob)) return rc;
         if (l + 1 < g->L)
-            GMCHK(norm(g->ob, g->norm_of(l, 3), g->norm_of(l + 1, 0), (int)m, 0), "launch norm");
+            GMCHK(norm(g->ob, g->post_of(l, 3), g->norm_of(l + 1, 0), (int)m, 0), "launch norm");
         else  // only the last row feeds the head
-            GMCHK(norm(g->ob, g->norm_of(l, 3), g->final_norm(), 1, (int)m - 1), "launch norm");
+            GMCHK(norm(g->ob, g->post_of(l, 3), g->final_norm(), 1, (int)m - 1), "launch norm");
     }
     float* lg = logits_out ? logits_out : g->logits;
-    GMCHK(launch_rowdot_argmax(et, g->a + (m - 1) * g->d, lg, g->best, ctx_err(c), s), "launch unembed");
+    const Weight& ut = g->unembed ? *weight_of(g->unembed) : et;
+    GMCHK(launch_rowdot_argmax(ut, g->a + (m - 1) * g->d, lg, g->best, ctx_err(c), s), "launch unembed");
     gm_argmax_done_kernel<<<dim3(1), dim3(64), 0, s>>>(g->best, g->cur, (int)m, P, g->tok);
     GMCHK(hipGetLastError(), "launch argmax");
     return FRQ_OK;
@@ -688,7 +749,7 @@ int norm_vec(const frq_bundle* b, const std::string& name, size_t d, float* dst)
 
 extern "C" {
 
-int frq_gemma_load(frq_ctx* c, const frq_bundle* b, int kv_int8, frq_gemma** out) {
+static int decoder_load(frq_ctx* c, const frq_bundle* b, int kv_int8, int want_arch, frq_gemma** out) {
     if (!out) return set_error(FRQ_ERR_ARG, "null output handle");
     *out = nullptr;
     if (!c || !b) return set_error(FRQ_ERR_ARG, "null context / bundle");
@@ -697,24 +758,36 @@ int frq_gemma_load(frq_ctx* c, const frq_bundle* b, int kv_int8, frq_gemma** out
     double cff[8];
     size_t nc = 8, nf = 8;
     if (int rc = frq_bundle_header(b, arch, sizeof arch, cfg, &nc, cff, &nf)) return rc;
-    if (std::string(arch) != "gemma") return set_error(FRQ_ERR_FORMAT, std::string("not a gemma bundle: ") + arch);
-    if (nc < 7 || nf < 6)
-        return set_error(FRQ_ERR_FORMAT, "gemma config needs [n_layer, H, nkv, hd, d, ffn, vocab, tied] and "
-                                         "config_f [theta, eps, attn_cap, final_cap, qscalar, escale]");
+    const char* name = want_arch == 0 ? "gemma" : "rope";
+    if (std::string(arch) != name)
+        return set_error(FRQ_ERR_FORMAT, std::string("not a ") + name + " bundle: " + arch);
+    if (nc < 8 || nf < (want_arch == 0 ? 6u : 2u))
+        return set_error(FRQ_ERR_FORMAT, want_arch == 0
+                                             ? "gemma config needs [n_layer, H, nkv, hd, d, ffn, vocab, tied] and "
+                                               "config_f [theta, eps, attn_cap, final_cap, qscalar, escale]"
+                                             : "rope config needs [n_layer, H, nkv, hd, d, ffn, vocab, tied] and "
+                                               "config_f [theta, eps]");
     for (int i = 0; i < 7; ++i)
         if (cfg[i] <= 0) return set_error(FRQ_ERR_FORMAT, "gemma config entries must be positive");
     auto g = std::make_unique<frq_gemma>();
     g->device = ctx_device(c);
     g->L = cfg[0]; g->H = cfg[1]; g->KV = cfg[2]; g->hd = cfg[3]; g->d = cfg[4]; g->ffn = cfg[5]; g->vocab = cfg[6];
     g->kv8 = kv_int8 ? 1 : 0;
+    g->arch = want_arch;
     if (g->H % g->KV || g->hd % 4 || g->d % 4 || g->d > 8192 || g->hd > 1024)
         return set_error(FRQ_ERR_ARG, "gemma shape outside this build's kernels (H % nkv, head dim and d % 4, "
                                       "d <= 8192)");
     // Gemma::new (52-60): f32 of the f64 config values; RoPE frequencies and
     // the query scale through the host libm's powf, as the reference
-    const float theta = (float)cff[0], qscalar = (float)cff[4];
-    g->theta = theta; g->eps = (float)cff[1]; g->cap = (float)cff[2]; g->escale = (float)cff[5];
-    g->qscale = powf(qscalar, -0.5f);
+    const float theta = (float)cff[0];
+    g->theta = theta; g->eps = (float)cff[1];
+    if (want_arch == 0) {
+        g->cap = (float)cff[2]; g->escale = (float)cff[5];
+        g->qscale = powf((float)cff[4], -0.5f);
+    } else {  // Rope::new (rope.rs:56-64): scores / sqrt(hd), no scale, no soft-cap
+        g->cap = 0.0f; g->escale = 1.0f;
+        g->qscale = sqrtf((float)g->hd);
+    }
     for (size_t j = 0; j < g->hd / 2; ++j) g->inv.push_back(1.0f / powf(theta, 2.0f * (float)j / (float)g->hd));
     const size_t L = g->L, d = g->d, qd = g->H * g->hd, kvd = g->KV * g->hd;
     (void)kvd;
@@ -731,28 +804,78 @@ int frq_gemma_load(frq_ctx* c, const frq_bundle* b, int kv_int8, frq_gemma** out
         if (int rc = one_linear(c, b, p + "mlp.down_proj", g->ffn, d, &w)) return rc;
         g->down.push_back(w);
     }
-    if (int rc = frq_bundle_weight(c, b, "embed", &g->embed)) return rc;
-    {
+    auto table = [&](const char* nm, frq_w** w) -> int {
+        if (int rc = frq_bundle_weight(c, b, nm, w)) return rc;
         int dt = 0;
         size_t n = 0, k = 0, gg = 0;
-        (void)frq_w_info(g->embed, &dt, &n, &k, &gg);
+        (void)frq_w_info(*w, &dt, &n, &k, &gg);
         if (dt != FRQ_DT_F16 || n != g->vocab || k != d)
-            return set_error(FRQ_ERR_FORMAT, "embed: expected an f16 (vocab, d) table");
-    }
-    std::vector<float> hv((4 * L + 1) * d);
+            return set_error(FRQ_ERR_FORMAT, std::string(nm) + ": expected an f16 (vocab, d) table");
+        return FRQ_OK;
+    };
+    if (int rc = table("embed", &g->embed)) return rc;
+    // the unembed: gemma ties it; rope reads lm_head unless tied (rope.rs:306-308)
+    if (want_arch == 1 && cfg[7] == 0)
+        if (int rc = table("lm_head", &g->unembed)) return rc;
+    std::vector<float> hv((4 * L + 1) * d, 0.0f);
     static const char* nn[4] = {"input_layernorm", "post_attention_layernorm", "pre_feedforward_layernorm",
                                 "post_feedforward_layernorm"};
+    static const char* rn[4] = {"in_ln", nullptr, "post_ln", nullptr};
     for (size_t l = 0; l < L; ++l)
-        for (int j = 0; j < 4; ++j)
-            if (int rc = norm_vec(b, "l" + std::to_string(l) + "." + nn[j], d, &hv[(4 * l + j) * d])) return rc;
+        for (int j = 0; j < 4; ++j) {
+            const char* nm = want_arch == 0 ? nn[j] : rn[j];
+            if (nm)
+                if (int rc = norm_vec(b, "l" + std::to_string(l) + "." + nm, d, &hv[(4 * l + j) * d])) return rc;
+        }
     if (int rc = norm_vec(b, "norm", d, &hv[4 * L * d])) return rc;
+    // rope: q / k / v biases (Qwen2.5) and the per-head q / k norms (Qwen3),
+    // all present or all absent per kind
+    std::vector<float> bias, qkn;
+    auto has = [&](const std::string& nm) {
+        size_t nd = 0;
+        return frq_bundle_array(b, nm.c_str(), nullptr, 0, nullptr, &nd, nullptr, nullptr, nullptr) == FRQ_OK;
+    };
+    if (want_arch == 1 && has("l0.self_attn.q_proj.bias")) {
+        const size_t w = (g->H + 2 * g->KV) * g->hd;
+        bias.assign(L * w, 0.0f);
+        for (size_t l = 0; l < L; ++l) {
+            const std::string p = "l" + std::to_string(l) + ".self_attn.";
+            if (int rc = norm_vec(b, p + "q_proj.bias", g->H * g->hd, &bias[l * w])) return rc;
+            if (int rc = norm_vec(b, p + "k_proj.bias", g->KV * g->hd, &bias[l * w + g->H * g->hd])) return rc;
+            if (int rc = norm_vec(b, p + "v_proj.bias", g->KV * g->hd, &bias[l * w + (g->H + g->KV) * g->hd]))
+                return rc;
+        }
+    }
+    if (want_arch == 1 && has("l0.self_attn.q_norm")) {
+        qkn.assign(L * 2 * g->hd, 0.0f);
+        for (size_t l = 0; l < L; ++l) {
+            const std::string p = "l" + std::to_string(l) + ".self_attn.";
+            if (int rc = norm_vec(b, p + "q_norm", g->hd, &qkn[l * 2 * g->hd])) return rc;
+            if (int rc = norm_vec(b, p + "k_norm", g->hd, &qkn[l * 2 * g->hd + g->hd])) return rc;
+        }
+    }
     GDev dv(g->device);
     hipStream_t s = (hipStream_t)frq_get_stream(c);
-    GMCHK(hipMalloc(&g->norms, hv.size() * 4), "hipMalloc(norms)");
-    GMCHK(hipMemcpyAsync(g->norms, hv.data(), hv.size() * 4, hipMemcpyHostToDevice, s), "hipMemcpyAsync(norms)");
+    auto up = [&](const std::vector<float>& v, float** dst) -> int {
+        if (v.empty()) return FRQ_OK;
+        GMCHK(hipMalloc(dst, v.size() * 4), "hipMalloc(vectors)");
+        GMCHK(hipMemcpyAsync(*dst, v.data(), v.size() * 4, hipMemcpyHostToDevice, s), "hipMemcpyAsync(vectors)");
+        return FRQ_OK;
+    };
+    if (int rc = up(hv, &g->norms)) return rc;
+    if (int rc = up(bias, &g->qkvbias)) return rc;
+    if (int rc = up(qkn, &g->qknorm)) return rc;
     GMCHK(hipStreamSynchronize(s), "hipStreamSynchronize");
     *out = g.release();
     return FRQ_OK;
+}
+
+int frq_gemma_load(frq_ctx* c, const frq_bundle* b, int kv_int8, frq_gemma** out) {
+    return decoder_load(c, b, kv_int8, 0, out);
+}
+
+int frq_rope_load(frq_ctx* c, const frq_bundle* b, int kv_int8, frq_gemma** out) {
+    return decoder_load(c, b, kv_int8, 1, out);
 }
 
 void frq_gemma_free(frq_gemma* g) { delete g; }

@@ -179,3 +179,57 @@ def write_gemma2_bundle(stem: str, s: int, n_layer: int = 26, n_head: int = 8, n
                  [10000.0, 1e-6, 50.0, 30.0, float(hd), float(np.sqrt(d))])
     w.finish(m)
     return m
+
+
+def write_rope_bundle(stem: str, s: int, n_layer: int = 28, n_head: int = 28, n_kv: int = 4, hd: int = 128,
+                      d: int = 3584, ffn: int = 18944, vocab: int = 152064, std: float = 0.02, dtype: str = "int8",
+                      qkv_bias: bool = True, qk_norm: bool = False, tied: bool = False, norm_std: float = 0.0,
+                      theta: float = 1e6, eps: float = 1e-6, raw: bool = False) -> dict:
+    """a Llama / Qwen2.5-7B-shaped bundle as convert_rope writes
+    it (src/convert.rs:619-634 via write_layers 1266-1310): f16 embed (and
+    lm_head unless tied), in_ln / post_ln RMSNorm weights (1 at init, or
+    1 + N(0, norm_std); no +1 bake), q/k/v biases (Qwen2.5) and per-head
+    q/k norms (Qwen3) when asked, the seven projections put_lin from (out,
+    in) sources in `dtype`.  raw: int8 linears as seeded random bytes with
+    f16 per-column scales written as stored (the 7B size in seconds)."""
+    from .bundle import BundleWriter, manifest
+    rng = np.random.default_rng(s)
+    nrm = lambda *shape: (rng.standard_normal(shape, dtype=np.float32) * np.float32(std))
+    gain = lambda n: (np.float32(1.0) + rng.standard_normal(n, dtype=np.float32) * np.float32(norm_std)
+                      if norm_std else np.ones(n, np.float32))
+    w = BundleWriter(stem)
+
+    def table(name):
+        rows = [nrm(min(8192, vocab - r0), d).astype(np.float16) for r0 in range(0, vocab, 8192)]
+        t = np.concatenate(rows)
+        nb = w._write(np.ascontiguousarray(t.view(np.uint16)))
+        w.entry(name, "f16", t.shape, nb)
+
+    table("embed")
+    w.put_small("norm", gain(d), None, dtype)
+    if not tied:
+        table("lm_head")
+    shapes = {"self_attn.q_proj": (n_head * hd, d), "self_attn.k_proj": (n_kv * hd, d),
+              "self_attn.v_proj": (n_kv * hd, d), "self_attn.o_proj": (d, n_head * hd),
+              "mlp.gate_proj": (ffn, d), "mlp.up_proj": (ffn, d), "mlp.down_proj": (d, ffn)}
+    for l in range(n_layer):
+        w.put_small(f"l{l}.in_ln", gain(d), None, dtype)
+        w.put_small(f"l{l}.post_ln", gain(d), None, dtype)
+        for proj, (o, i) in shapes.items():
+            if raw and dtype == "int8":
+                q = rng.integers(-127, 128, (i, o), dtype=np.int8)
+                nb = w._write(np.ascontiguousarray(q))
+                w.entry(f"l{l}.{proj}", "i8", (i, o), nb)
+                w.put_f16(f"l{l}.{proj}__scale", rng.uniform(0.5, 1.0, o).astype(np.float32) * np.float32(std / 40))
+            else:
+                w.put_lin(f"l{l}.{proj}", nrm(o, i), dtype)
+        if qkv_bias:
+            for proj in ("q_proj", "k_proj", "v_proj"):
+                o = shapes[f"self_attn.{proj}"][0]
+                w.put_small(f"l{l}.self_attn.{proj}.bias", nrm(o), None, dtype)
+        if qk_norm:
+            w.put_small(f"l{l}.self_attn.q_norm", gain(hd), None, dtype)
+            w.put_small(f"l{l}.self_attn.k_norm", gain(hd), None, dtype)
+    m = manifest("rope", [n_layer, n_head, n_kv, hd, d, ffn, vocab, int(tied)], [theta, eps])
+    w.finish(m)
+    return m

@@ -284,6 +284,14 @@ int frq_gemma_generate(frq_ctx* ctx, frq_gemma* g, const int64_t* prompt, size_t
 int frq_gemma_predict(frq_ctx* ctx, frq_gemma* g, const int64_t* ids, size_t n, int64_t* token,
                       float* logits);
 int frq_gemma_set_graphs(frq_gemma* g, int on);
+/* Rope::new (src/rope.rs:56-64) over an arch "rope" bundle (Llama / Qwen2.5
+ * / Qwen3 / Mistral: config [n_layer, H, nkv, hd, d, ffn, vocab, tied],
+ * config_f [theta, eps]; arrays as convert_rope writes them,
+ * src/convert.rs:619-634: in_ln / post_ln, optional q/k/v biases and q/k
+ * norms, lm_head unless tied) into the same engine: generate, predict,
+ * free and set_graphs are the frq_gemma_* calls (Model::generate,
+ * rope.rs:1147-1170; predict 730-734). */
+int frq_rope_load(frq_ctx* ctx, const frq_bundle* b, int kv_int8, frq_gemma** out);
 /* The f32 libm functions the decode kernels use (fn 0 expf, 1 expm1f, 2
  * tanhf), bit-identical to the libm behind Rust's f32::exp / f32::tanh
  * (glibc's expf and fdlibm's expm1f / tanhf): out[i] = f(x[i]) for n host

@@ -451,19 +451,26 @@ class _GemmaW(C.Structure):
                 ("d", C.c_size_t), ("ffn", C.c_size_t), ("vocab", C.c_size_t), ("window", C.c_size_t),
                 ("theta", C.c_float), ("eps", C.c_float), ("attn_cap", C.c_float), ("qscale", C.c_float),
                 ("escale", C.c_float), ("embed", C.c_void_p), ("norm", C.c_void_p), ("norms", C.c_void_p),
-                ("lin", C.c_void_p)]
+                ("lin", C.c_void_p), ("arch", C.c_int), ("bias", C.c_void_p), ("qk_norm", C.c_void_p),
+                ("unembed", C.c_void_p)]
 
 
 class Gemma:
-    """The oracle's Gemma-2 over a bundle's arrays (Gemma::new, gemma.rs:
-    52-60: config [n_layer, H, nkv, hd, d, ffn, vocab, tied], config_f
-    [theta, eps, attn_cap, final_cap, qscalar, escale], window 4096).
-    Linears as Bundle::load keeps them: int4 packed + f32 scales, int8
-    transposed to (N, K)."""
+    """The oracle's Gemma-2 (arch "gemma": Gemma::new, gemma.rs:52-60) or
+    Llama / Qwen (arch "rope": Rope::new, rope.rs:56-64) over a bundle's
+    arrays: config [n_layer, H, nkv, hd, d, ffn, vocab, tied]; config_f
+    [theta, eps, attn_cap, final_cap, qscalar, escale] (gemma, window 4096)
+    or [theta, eps] (rope).  Linears as Bundle::load keeps them: int4 / q4a
+    packed + f32 scales (and mins), int8 transposed to (N, K)."""
 
     def __init__(self, manifest, arrs, nthreads: int = 8):
         L, H, KV, hd, d, ffn, vocab = (int(c) for c in manifest["config"][:7])
-        theta, eps, cap, _fcap, qscalar, escale = (float(c) for c in manifest["config_f"][:6])
+        rope = manifest["arch"] == "rope"
+        if rope:
+            theta, eps = (float(c) for c in manifest["config_f"][:2])
+            cap, qscalar, escale = 0.0, float(hd), 1.0
+        else:
+            theta, eps, cap, _fcap, qscalar, escale = (float(c) for c in manifest["config_f"][:6])
         f32 = lambda n: np.ascontiguousarray(arrs[n], np.float32)
         self.keep = []
         norms = []
@@ -471,10 +478,20 @@ class Gemma:
         names = ["self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj", "mlp.gate_proj",
                  "mlp.up_proj", "mlp.down_proj"]
         info = {e["name"]: e for e in manifest["arrays"]}
+        biases, qkn = [], []
         for l in range(L):
-            for nm in ("input_layernorm", "post_attention_layernorm", "pre_feedforward_layernorm",
-                       "post_feedforward_layernorm"):
-                norms.append(f32(f"l{l}.{nm}"))
+            if rope:
+                norms += [f32(f"l{l}.in_ln"), None, f32(f"l{l}.post_ln"), None]
+                for nm in ("q_proj", "k_proj", "v_proj"):
+                    bn = f"l{l}.self_attn.{nm}.bias"
+                    biases.append(f32(bn) if bn in arrs else None)
+                for nm in ("q_norm", "k_norm"):
+                    qn = f"l{l}.self_attn.{nm}"
+                    qkn.append(f32(qn) if qn in arrs else None)
+            else:
+                for nm in ("input_layernorm", "post_attention_layernorm", "pre_feedforward_layernorm",
+                           "post_feedforward_layernorm"):
+                    norms.append(f32(f"l{l}.{nm}"))
             for j, nm in enumerate(names):
                 a = arrs[f"l{l}.{nm}"]
                 sc = f32(f"l{l}.{nm}__scale")
@@ -494,15 +511,19 @@ class Gemma:
                                            None if mn is None else mn.ctypes.data)
                     self.keep += [pk, mn]
                 self.keep.append(sc)
-        self.keep.extend(norms)
-        nptr = (C.c_void_p * len(norms))(*[n.ctypes.data for n in norms])
-        self.keep += [lins, nptr]
+        self.keep.extend(norms + biases + qkn)
+        ptrs = lambda lst: (C.c_void_p * max(len(lst), 1))(*[None if a is None else a.ctypes.data for a in lst])
+        nptr, bptr, qptr = ptrs(norms), ptrs(biases), ptrs(qkn)
+        self.keep += [lins, nptr, bptr, qptr]
         self.embed = np.ascontiguousarray(arrs["embed"]).view(np.uint16)
+        tied = int(manifest["config"][7]) != 0
+        self.unembed = None if (not rope or tied) else np.ascontiguousarray(arrs["lm_head"]).view(np.uint16)
         self.norm = f32("norm")
         self.s = _GemmaW(L, H, KV, hd, d, ffn, vocab, 4096, np.float32(theta), np.float32(eps), np.float32(cap),
                          np.float32(np.float32(qscalar) ** np.float32(-0.5)), np.float32(escale),
                          self.embed.ctypes.data, self.norm.ctypes.data, C.cast(nptr, C.c_void_p),
-                         C.cast(lins, C.c_void_p))
+                         C.cast(lins, C.c_void_p), int(rope), C.cast(bptr, C.c_void_p), C.cast(qptr, C.c_void_p),
+                         None if self.unembed is None else self.unembed.ctypes.data)
         self.vocab, self.nthreads = vocab, nthreads
 
     def generate(self, prompt, n_new: int, kv_int8: bool = False, with_logits: bool = False):
@@ -516,6 +537,9 @@ class Gemma:
         if rc:
             raise IndexError("token beyond the vocabulary")
         return (out, lg) if with_logits else out
+
+
+Rope = Gemma  # the Llama / Qwen family rides the same restatement (arch "rope")
 
 
 def rmsnorm(x, w, eps: float):

@@ -1083,6 +1083,23 @@ static void gm_rope(const gm_run* R, float* x, size_t m, size_t n_heads, size_t 
     }
 }
 
+/* Rope::head_norm (rope.rs:72-87): per head of hd, ms = the fold from -0.0
+ * of v*v / hd, inv = 1 / sqrt(ms + eps), v * inv * w[c]. */
+static void gm_head_norm(float* x, size_t m, size_t n_heads, size_t hd, const float* w, float eps) {
+    for (size_t i = 0; i < m; i++)
+        for (size_t h = 0; h < n_heads; h++) {
+            float* v = x + (i * n_heads + h) * hd;
+            float ms = -0.0f;
+            for (size_t c = 0; c < hd; c++) ms = ms + v[c] * v[c];
+            ms = ms / (float)hd;
+            const float inv = 1.0f / sqrtf(ms + eps);
+            for (size_t c = 0; c < hd; c++) v[c] = v[c] * inv * w[c];
+        }
+}
+
+/* silu (rope.rs:39-41): x / (1 + exp(-x)). */
+static float gm_silu(float x) { return x / (1.0f + expf(-x)); }
+
 static int gm_block(gm_run* R, float* x, size_t m, size_t cur) {
     const fro_gemma_t* g = R->g;
     const size_t d = g->d, H = g->n_head, KV = g->n_kv, hd = g->hd, rep = H / KV, kvd = KV * hd, klen = cur + m;
@@ -1105,6 +1122,17 @@ static int gm_block(gm_run* R, float* x, size_t m, size_t cur) {
         if ((rc = lin_mm(&L[0], a, m, q, R->nthreads)) || (rc = lin_mm(&L[1], a, m, k, R->nthreads)) ||
             (rc = lin_mm(&L[2], a, m, v, R->nthreads)))
             break;
+        if (g->arch == 1) {  /* proj: + bias (rope.rs:110-117), then the QK-norm */
+            const float* const* B = g->bias + 3 * l;
+            float* outs[3] = {q, k, v};
+            const size_t wid[3] = {H * hd, kvd, kvd};
+            for (int t = 0; t < 3; t++)
+                if (B[t])
+                    for (size_t i = 0; i < m; i++)
+                        for (size_t c = 0; c < wid[t]; c++) outs[t][i * wid[t] + c] = outs[t][i * wid[t] + c] + B[t][c];
+            if (g->qk_norm[2 * l]) gm_head_norm(q, m, H, hd, g->qk_norm[2 * l], g->eps);
+            if (g->qk_norm[2 * l + 1]) gm_head_norm(k, m, KV, hd, g->qk_norm[2 * l + 1], g->eps);
+        }
         gm_rope(R, q, m, H, cur);
         gm_rope(R, k, m, KV, cur);
         for (size_t i = 0; i < m; i++) {  /* append K/V */
@@ -1128,7 +1156,7 @@ static int gm_block(gm_run* R, float* x, size_t m, size_t cur) {
                 }
             }
         }
-        const int sliding = l % 2 == 0;
+        const int sliding = g->arch == 0 && l % 2 == 0;
         for (size_t h = 0; h < H; h++) {
             const size_t kv = h / rep;
             for (size_t j = 0; j < klen; j++)
@@ -1147,8 +1175,8 @@ static int gm_block(gm_run* R, float* x, size_t m, size_t cur) {
                 for (size_t j = 0; j < klen; j++) {
                     float acc = 0.0f;
                     for (size_t c = 0; c < hd; c++) acc = fmaf(qr[c], kh[j * hd + c], acc);
-                    float s = acc * g->qscale;
-                    if (g->attn_cap > 0.0f) s = g->attn_cap * tanhf(s / g->attn_cap);
+                    float s = g->arch == 1 ? acc / sqrtf((float)hd) : acc * g->qscale;
+                    if (g->arch == 0 && g->attn_cap > 0.0f) s = g->attn_cap * tanhf(s / g->attn_cap);
                     if (j > abs_ || (sliding && abs_ >= g->window && j <= abs_ - g->window)) s = -1e30f;
                     sc[j] = s;
                 }
@@ -1161,14 +1189,23 @@ static int gm_block(gm_run* R, float* x, size_t m, size_t cur) {
             }
         }
         if ((rc = lin_mm(&L[3], att, m, o, R->nthreads))) break;
-        fro_rmsnorm(o, m, d, N[1], g->eps, a);
-        for (size_t i = 0; i < m * d; i++) x[i] = x[i] + a[i];
+        if (N[1]) {  /* gemma: the post-norm before the residual; rope: x + o */
+            fro_rmsnorm(o, m, d, N[1], g->eps, a);
+            for (size_t i = 0; i < m * d; i++) x[i] = x[i] + a[i];
+        } else {
+            for (size_t i = 0; i < m * d; i++) x[i] = x[i] + o[i];
+        }
         fro_rmsnorm(x, m, d, N[2], g->eps, a);
         if ((rc = lin_mm(&L[4], a, m, gate, R->nthreads)) || (rc = lin_mm(&L[5], a, m, up, R->nthreads))) break;
-        for (size_t i = 0; i < m * g->ffn; i++) gate[i] = fro_gelu_tanh(gate[i]) * up[i];
+        for (size_t i = 0; i < m * g->ffn; i++)
+            gate[i] = (g->arch == 1 ? gm_silu(gate[i]) : fro_gelu_tanh(gate[i])) * up[i];
         if ((rc = lin_mm(&L[6], gate, m, o, R->nthreads))) break;
-        fro_rmsnorm(o, m, d, N[3], g->eps, a);
-        for (size_t i = 0; i < m * d; i++) x[i] = x[i] + a[i];
+        if (N[3]) {
+            fro_rmsnorm(o, m, d, N[3], g->eps, a);
+            for (size_t i = 0; i < m * d; i++) x[i] = x[i] + a[i];
+        } else {
+            for (size_t i = 0; i < m * d; i++) x[i] = x[i] + o[i];
+        }
     }
     free(a); free(q); free(k); free(v); free(att); free(o); free(gate); free(up); free(sc); free(kh); free(vh);
     return rc;
@@ -1177,7 +1214,8 @@ static int gm_block(gm_run* R, float* x, size_t m, size_t cur) {
 typedef struct { const fro_gemma_t* g; const float* x; float* out; size_t lo, hi; } gm_head_job;
 static void* gm_head_worker(void* p) {
     gm_head_job* J = (gm_head_job*)p;
-    fro_rowdot_f32(FRO_DT_F16, J->g->embed + J->lo * J->g->d, NULL, J->hi - J->lo, J->g->d, J->x, J->out + J->lo);
+    const uint16_t* tab = J->g->unembed ? J->g->unembed : J->g->embed;
+    fro_rowdot_f32(FRO_DT_F16, tab + J->lo * J->g->d, NULL, J->hi - J->lo, J->g->d, J->x, J->out + J->lo);
     return NULL;
 }
 

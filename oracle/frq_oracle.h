@@ -218,12 +218,23 @@ typedef struct {
     const float* norm;          /* final norm */
     const float* const* norms;
     const fro_lin_t* lin;
+    /* the Llama / Qwen family (src/rope.rs) when arch == 1: no embedding
+     * scale, norms[4l + 0] = in_ln and [4l + 2] = post_ln (1 and 3 NULL: a
+     * plain residual), scores / sqrt(hd) (qscale unused), no soft-cap or
+     * window, SiLU; bias[3l + 0..2] q / k / v biases (NULL when absent),
+     * qk_norm[2l + 0..1] per-head q / k norms (NULL when absent); unembed
+     * the lm_head (NULL: embed). */
+    int arch;
+    const float* const* bias;
+    const float* const* qk_norm;
+    const uint16_t* unembed;
 } fro_gemma_t;
 
 /* RMSNorm with the baked (1 + w) gain (gemma.rs:66-77) over m rows. */
 void fro_rmsnorm(const float* x, size_t m, size_t d, const float* w, float eps, float* out);
-/* Gemma::generate (gemma.rs:403-431; kv_int8: 364-384): n_new greedy
- * tokens, logits (n_new, vocab) nullable. */
+/* Gemma::generate (gemma.rs:403-431; kv_int8: 364-384) or, arch 1,
+ * Rope::generate (src/rope.rs:1147-1170, forward_block 391-437): n_new
+ * greedy tokens, logits (n_new, vocab) nullable. */
 int fro_gemma_generate(const fro_gemma_t* g, const int64_t* prompt, size_t n_prompt, size_t n_new, int kv_int8,
                        int nthreads, int64_t* out, float* logits);
 

@@ -12,7 +12,11 @@ from fieldrun_amd import synth
 
 def f64_gemma(m, arrs, prompt, n_new):
     L, H, KV, hd, d, ffn, V = m["config"][:7]
-    theta, eps, cap, _fc, qscalar, escale = m["config_f"][:6]
+    rope_arch = m["arch"] == "rope"
+    if rope_arch:  # rope.rs: no embedding scale, no soft-cap / window / post-norms, SiLU
+        (theta, eps), cap, qscalar, escale = m["config_f"][:2], 0.0, float(hd), 1.0
+    else:
+        theta, eps, cap, _fc, qscalar, escale = m["config_f"][:6]
     rep, half, window = H // KV, hd // 2, 4096
     f = lambda n: arrs[n].astype(np.float64)
     emb = f("embed")
@@ -27,6 +31,17 @@ def f64_gemma(m, arrs, prompt, n_new):
     def norm(x, name):
         ms = (x * x).mean(-1, keepdims=True)
         return x / np.sqrt(ms + eps) * f(name)
+
+    def proj(a, name):
+        y = mm(a, name)
+        return y + f(name + ".bias") if name + ".bias" in arrs else y
+
+    def head_norm(x, name, nh):
+        if name not in arrs:
+            return x
+        x = x.reshape(x.shape[0], nh, hd)
+        x = x / np.sqrt((x * x).mean(-1, keepdims=True) + eps) * f(name)
+        return x.reshape(x.shape[0], nh * hd)
 
     def rope(x, nh, pos0):
         x = x.copy()
@@ -46,35 +61,43 @@ def f64_gemma(m, arrs, prompt, n_new):
         mr = x.shape[0]
         for l in range(L):
             p = f"l{l}."
-            a = norm(x, p + "input_layernorm")
-            q = rope(mm(a, p + "self_attn.q_proj"), H, cur)
-            k = rope(mm(a, p + "self_attn.k_proj"), KV, cur)
-            v = mm(a, p + "self_attn.v_proj")
+            a = norm(x, p + ("in_ln" if rope_arch else "input_layernorm"))
+            q = rope(head_norm(proj(a, p + "self_attn.q_proj"), p + "self_attn.q_norm", H), H, cur)
+            k = rope(head_norm(proj(a, p + "self_attn.k_proj"), p + "self_attn.k_norm", KV), KV, cur)
+            v = proj(a, p + "self_attn.v_proj")
             K[l] = np.concatenate([K[l], k])
             Vc[l] = np.concatenate([Vc[l], v])
             att = np.zeros((mr, H * hd))
             for h in range(H):
                 kv = h // rep
                 s = q[:, h * hd:(h + 1) * hd] @ K[l][:, kv * hd:(kv + 1) * hd].T / np.sqrt(qscalar)
-                s = cap * np.tanh(s / cap)
+                if cap > 0:
+                    s = cap * np.tanh(s / cap)
                 for i in range(mr):
                     ab = cur + i
                     s[i, ab + 1:] = -np.inf
-                    if l % 2 == 0 and ab >= window:
+                    if not rope_arch and l % 2 == 0 and ab >= window:
                         s[i, :ab - window + 1] = -np.inf
                 s = np.exp(s - s.max(1, keepdims=True))
                 s /= s.sum(1, keepdims=True)
                 att[:, h * hd:(h + 1) * hd] = s @ Vc[l][:, kv * hd:(kv + 1) * hd]
-            x = x + norm(mm(att, p + "self_attn.o_proj"), p + "post_attention_layernorm")
-            a2 = norm(x, p + "pre_feedforward_layernorm")
+            o = mm(att, p + "self_attn.o_proj")
+            x = x + (o if rope_arch else norm(o, p + "post_attention_layernorm"))
+            a2 = norm(x, p + ("post_ln" if rope_arch else "pre_feedforward_layernorm"))
             gt, up = mm(a2, p + "mlp.gate_proj"), mm(a2, p + "mlp.up_proj")
-            c = np.sqrt(2 / np.pi)
-            hm = 0.5 * gt * (1 + np.tanh(c * (gt + 0.044715 * gt ** 3))) * up
-            x = x + norm(mm(hm, p + "mlp.down_proj"), p + "post_feedforward_layernorm")
+            if rope_arch:
+                hm = gt / (1 + np.exp(-gt)) * up
+            else:
+                c = np.sqrt(2 / np.pi)
+                hm = 0.5 * gt * (1 + np.tanh(c * (gt + 0.044715 * gt ** 3))) * up
+            dn = mm(hm, p + "mlp.down_proj")
+            x = x + (dn if rope_arch else norm(dn, p + "post_feedforward_layernorm"))
         return x
 
+    un = f("lm_head") if (rope_arch and not m["config"][7]) else emb
+
     def head(x):
-        lg = emb @ norm(x[-1:], "norm")[0]
+        lg = un @ norm(x[-1:], "norm")[0]
         return int(np.flatnonzero(lg == lg.max())[-1]), lg
 
     x = block(emb[prompt] * escale, 0)
@@ -119,3 +142,18 @@ def test_rmsnorm_closed_forms():
     x = np.random.default_rng(2).integers(-20, 20, (4, d)).astype(np.float32)
     ref = x / np.sqrt((x.astype(np.float64) ** 2).mean(1, keepdims=True) + 1e-6) * w
     assert np.allclose(oracle.rmsnorm(x, w, 1e-6), ref, rtol=3e-7, atol=1e-7)
+
+
+@pytest.mark.parametrize("kw", [dict(qkv_bias=True), dict(qkv_bias=False, qk_norm=True, tied=True)])
+def test_oracle_rope_matches_f64_model(tmp_path, kw):
+    stem = str(tmp_path / "r")
+    synth.write_rope_bundle(stem, 4, n_layer=2, n_head=4, n_kv=2, hd=32, d=128, ffn=256, vocab=500, std=0.1,
+                            norm_std=0.1, dtype="int4", **kw)
+    m, arrs = oracle.read_bundle(stem)
+    g = oracle.Rope(m, arrs, nthreads=4)
+    prompt = synth.gpt2_prompt(6, 500, 2)
+    toks, lg = g.generate(prompt, 10, with_logits=True)
+    rt, rlg = f64_gemma(m, arrs, prompt, 10)
+    assert np.array_equal(toks, rt)
+    assert np.abs(lg - rlg).max() <= 2e-5 * np.abs(rlg).max()
+    assert len(set(toks.tolist())) > 3
