@@ -19,7 +19,8 @@ pre-quantised input, the M=2048 MFMA-bound shapes in TOPS, the int4 decode
 GEMV and the affine-int4 (q4a) GEMV on Gemma-2 shapes, the unembed row dot, the config-4 MoE layer, and
 config 0 end to end: GPT-2 small greedy decode (tok/s, f32 and int8 KV
 caches) with the oracle's CPU rate and token check beside it, and config 2:
-Gemma-2-2b int4 greedy decode (256 tokens after a 64-token prompt).  The CPU
+Gemma-2-2b int4 greedy decode (256 tokens after a 64-token prompt), and
+config 4: Qwen2.5-7B int8, a 2048-token prefill then 128 greedy tokens.  The CPU
 baseline is the
 oracle's restatement of the reference's scalar int8 path (the
 `_scalar_i8_bench` build) on the host's cores, on a bounded sample.
@@ -433,6 +434,33 @@ def main():
                                                          "sample": "8-token prompt, 4 tokens (prefill-dominated)",
                                                          "tokens_identical": same}
                 log(f"gemma2 oracle: {detail['gemma2_decode']['cpu_oracle']}")
+            g.free()
+            b.close()
+
+        # ---------------- Qwen2.5-7B int8 prefill + greedy decode (config 4) ----------------
+        # 28 layers, d 3584, 28 / 4 heads of 128, ffn 18944, vocab 152064, int8
+        # per-column scales (seeded random bytes), q/k/v biases, untied f16
+        # head; 2048-token seeded prompt, then 128 greedy tokens, batch 1
+        detail["rope_decode"] = {}
+        with tempfile.TemporaryDirectory() as tmp:
+            stem = os.path.join(tmp, "qwen25")
+            synth.write_rope_bundle(stem, 6, raw=True)
+            b = fa.Bundle(stem, ctx)
+            g = fa.Rope(b)
+            g.set_graphs(not args.no_graphs)
+            prompt = synth.gpt2_prompt(2048, 152064, 9)
+            g.generate(prompt[:16], 4)
+            runs = {}
+            for n_new in (1, 128):
+                t0 = time.perf_counter()
+                g.generate(prompt, n_new)
+                runs[n_new] = time.perf_counter() - t0
+            dec_ms = (runs[128] - runs[1]) / 127 * 1e3
+            detail["rope_decode"]["qwen25_7b_int8"] = {
+                "prefill_tok_s": round(2048 / runs[1], 1), "prefill_plus_first_ms": round(runs[1] * 1e3, 1),
+                "decode_ms_per_token": round(dec_ms, 3), "decode_tok_s": round(1e3 / dec_ms, 1),
+                "total_s_2048_plus_128": round(runs[128], 3)}
+            log(f"qwen2.5-7b: {detail['rope_decode']['qwen25_7b_int8']}")
             g.free()
             b.close()
 
