@@ -288,9 +288,10 @@ __global__ __launch_bounds__(GT) void gm_attn_kernel(const float* __restrict__ q
     for (int j = j0 + threadIdx.x; j < nk; j += GT) p[j] = libm::frq_expf(p[j] - mx);
     __syncthreads();
     if (threadIdx.x == 0) {  // key order; the masked exps are +0 (j < j0 add nothing to +0)
+        const int ja = min((j0 + 3) & ~3, nk);  // p + ja 16-byte aligned for the batched chain
         float sum = 0.0f;
-        for (int j = j0; j < nk; ++j) sum = sum + p[j];
-        red[0] = sum;
+        for (int j = j0; j < ja; ++j) sum = sum + p[j];
+        red[0] = lds_seq_sum(p + ja, nk - ja, sum);
     }
     __syncthreads();
     const float sum = red[0];
@@ -334,6 +335,183 @@ __global__ __launch_bounds__(GT) void gm_attn_kernel(const float* __restrict__ q
             acc = __builtin_fmaf(p[j], v, acc);
         }
         att[(size_t)i * H * hd + (size_t)h * hd + c] = acc;
+    }
+}
+
+// ---- decode attention for long caches, split into three launches ----
+// The scores of the keys are independent (each a sequential FMA chain over
+// the head dims), so they spread over many blocks; the softmax sum and the
+// value chains stay one lane each, in key order.  Same arithmetic as
+// gm_attn_kernel<.., true>, so the same bits.
+
+// 1. Block b < H: bias, QK-norm and RoPE of q head b into qr; block H + kh:
+// the same for k head kh (no norm on v), then k, v appended at cache row cur.
+template <bool KV8>
+__global__ __launch_bounds__(GT) void gm_dec_prep_kernel(const float* __restrict__ qkv, int H, int KV, int hd,
+                                                         const int* __restrict__ curp, const float2* __restrict__ cs,
+                                                         float* __restrict__ kc, float* __restrict__ vc,
+                                                         int8_t* __restrict__ kq, int8_t* __restrict__ vq,
+                                                         float* __restrict__ ks, float* __restrict__ vs,
+                                                         const float* __restrict__ bias, const float* __restrict__ qn,
+                                                         const float* __restrict__ kn, float eps,
+                                                         float* __restrict__ qr) {
+    extern __shared__ float4 lds4[];
+    float* hv = reinterpret_cast<float*>(lds4);  // this head's vector (and v after it)
+    const int b = blockIdx.x, half = hd / 2, kvd = KV * hd, hd4 = (hd + 3) & ~3;
+    const bool isq = b < H;
+    const int head = isq ? b : b - H;
+    const size_t pos = (size_t)*curp;
+    const int col0 = isq ? head * hd : (H + head) * hd;
+    for (int c = threadIdx.x; c < hd; c += GT) {
+        float v = qkv[col0 + c];
+        if (bias) v = v + bias[col0 + c];
+        hv[c] = v;
+        if (!isq) {
+            float w = qkv[(H + KV + head) * hd + c];
+            if (bias) w = w + bias[(H + KV + head) * hd + c];
+            hv[hd4 + c] = w;
+        }
+    }
+    __syncthreads();
+    if (qn) {
+        if (threadIdx.x == 0) head_norm_lane(hv, hd, isq ? qn : kn, eps);
+        __syncthreads();
+    }
+    const float2* csp = cs + pos * half;
+    for (int j = threadIdx.x; j < half; j += GT) rope_pair(hv, j, half, csp);
+    __syncthreads();
+    if (isq) {
+        for (int c = threadIdx.x; c < hd; c += GT) qr[head * hd + c] = hv[c];
+    } else if constexpr (!KV8) {
+        for (int c = threadIdx.x; c < hd; c += GT) {
+            kc[pos * kvd + (size_t)head * hd + c] = hv[c];
+            vc[pos * kvd + (size_t)head * hd + c] = hv[hd4 + c];
+        }
+    } else {
+        const int wave = threadIdx.x >> 6;
+        if (wave < 2)
+            kv_quant_wave(hv + wave * hd4, hd, (wave ? vq : kq) + pos * kvd + (size_t)head * hd,
+                          (wave ? vs : ks) + pos * KV + head);
+    }
+}
+
+// 2. Scores: grid (H, key chunks of GT): thread j of chunk z scores key
+// z GT + j of the window [j0, cur] into sc[h * pstride + j].
+template <bool KV8>
+__global__ __launch_bounds__(GT) void gm_dec_score_kernel(const float* __restrict__ qr, int H, int KV, int hd,
+                                                          const int* __restrict__ curp, const float* __restrict__ kc,
+                                                          const int8_t* __restrict__ kq, const float* __restrict__ ks,
+                                                          float qscale, float cap, int sliding, int window, int div,
+                                                          int pstride, float* __restrict__ sc) {
+    extern __shared__ float4 lds4[];
+    float* q = reinterpret_cast<float*>(lds4);
+    const int h = blockIdx.x, kv = h / (H / KV), kvd = KV * hd;
+    const int ab = *curp, nk = ab + 1, j0 = (sliding && ab >= window) ? ab - window + 1 : 0;
+    const int j = blockIdx.y * GT + threadIdx.x;
+    if ((int)(blockIdx.y * GT) >= nk) return;  // block-uniform: past the cache
+    for (int c = threadIdx.x; c < hd; c += GT) q[c] = qr[h * hd + c];
+    __syncthreads();
+    if (j < j0 || j >= nk) return;
+    float acc = 0.0f;
+    if constexpr (!KV8) {
+        const float* kr = kc + (size_t)j * kvd + (size_t)kv * hd;
+        for (int c = 0; c < hd; c += 4) {
+            const float4 k4 = *reinterpret_cast<const float4*>(kr + c);
+            acc = __builtin_fmaf(q[c], k4.x, acc);
+            acc = __builtin_fmaf(q[c + 1], k4.y, acc);
+            acc = __builtin_fmaf(q[c + 2], k4.z, acc);
+            acc = __builtin_fmaf(q[c + 3], k4.w, acc);
+        }
+    } else {
+        const int8_t* kr = kq + (size_t)j * kvd + (size_t)kv * hd;
+        const float sk = ks[(size_t)j * KV + kv];
+        for (int c = 0; c < hd; c += 4) {
+            const char4 k4 = *reinterpret_cast<const char4*>(kr + c);
+            acc = __builtin_fmaf(q[c], (float)k4.x * sk, acc);
+            acc = __builtin_fmaf(q[c + 1], (float)k4.y * sk, acc);
+            acc = __builtin_fmaf(q[c + 2], (float)k4.z * sk, acc);
+            acc = __builtin_fmaf(q[c + 3], (float)k4.w * sk, acc);
+        }
+    }
+    float sj = div ? acc / qscale : acc * qscale;
+    if (cap > 0.0f) sj = cap * libm::frq_tanhf(sj / cap);
+    sc[(size_t)h * pstride + j] = sj;
+}
+
+// 3. Per head: max, exp, the key-order sum, divide, then the value chains.
+template <bool KV8>
+__global__ __launch_bounds__(GT) void gm_dec_value_kernel(const float* __restrict__ sc, int H, int KV, int hd,
+                                                          const int* __restrict__ curp, const float* __restrict__ vc,
+                                                          const int8_t* __restrict__ vq, const float* __restrict__ vs,
+                                                          int sliding, int window, int pstride,
+                                                          float* __restrict__ att) {
+    extern __shared__ float4 lds4[];
+    float* p = reinterpret_cast<float*>(lds4);
+    float* sv = p + pstride;
+    __shared__ float red[4];
+    const int h = blockIdx.x, kv = h / (H / KV), kvd = KV * hd;
+    const int ab = *curp, nk = ab + 1, j0 = (sliding && ab >= window) ? ab - window + 1 : 0;
+    float mx = -INFINITY;
+    for (int j = j0 + threadIdx.x; j < nk; j += GT) {
+        const float v = sc[(size_t)h * pstride + j];
+        p[j] = v;
+        mx = fmaxf(mx, v);
+        if constexpr (KV8) sv[j] = vs[(size_t)j * KV + kv];
+    }
+    mx = gblock_max(mx, red);
+    if (j0 > 0) mx = fmaxf(mx, -1e30f);  // a masked entry joins the max
+    for (int j = j0 + threadIdx.x; j < nk; j += GT) p[j] = libm::frq_expf(p[j] - mx);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        // key order from j0: the few keys before the next 16-byte boundary
+        // one at a time, the rest through the batched LDS chain
+        const int ja = min((j0 + 3) & ~3, nk);
+        float sum = 0.0f;
+        for (int j = j0; j < ja; ++j) sum = sum + p[j];
+        red[0] = lds_seq_sum(p + ja, nk - ja, sum);
+    }
+    __syncthreads();
+    const float sum = red[0];
+    for (int j = j0 + threadIdx.x; j < nk; j += GT) p[j] = p[j] / sum;
+    __syncthreads();
+    constexpr int B = 16;
+    for (int c = threadIdx.x; c < hd; c += GT) {
+        float acc = 0.0f;
+        const size_t col = (size_t)kv * hd + c;
+        const int n = nk - j0, nb = n / B;
+        float v0[B], v1[B];
+        auto ld = [&](float (&v)[B], int k) {
+#pragma unroll
+            for (int u = 0; u < B; ++u) {
+                const size_t j = (size_t)(j0 + k * B + u);
+                if constexpr (!KV8) v[u] = vc[j * kvd + col];
+                else v[u] = (float)vq[j * kvd + col] * sv[j];
+            }
+        };
+        auto fma_b = [&](const float (&v)[B], int k) {
+#pragma unroll
+            for (int u = 0; u < B; ++u) acc = __builtin_fmaf(p[j0 + k * B + u], v[u], acc);
+        };
+        if (nb > 0) {
+            ld(v0, 0);
+            ld(v1, min(1, nb - 1));
+            __builtin_amdgcn_sched_barrier(0);
+            int k = 0;
+            for (; k + 2 <= nb; k += 2) {
+                fma_b(v0, k);
+                ld(v0, min(k + 2, nb - 1));
+                __builtin_amdgcn_sched_barrier(0);
+                fma_b(v1, k + 1);
+                ld(v1, min(k + 3, nb - 1));
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (k < nb) fma_b(v0, k);
+        }
+        for (int j = j0 + nb * B; j < nk; ++j) {
+            const float v = KV8 ? (float)vq[(size_t)j * kvd + col] * sv[j] : vc[(size_t)j * kvd + col];
+            acc = __builtin_fmaf(p[j], v, acc);
+        }
+        att[(size_t)h * hd + c] = acc;
     }
 }
 
@@ -392,6 +570,7 @@ struct frq_gemma {
     int* cur = nullptr;
     unsigned long long* best = nullptr;
     int64_t *tok = nullptr, *ids = nullptr;
+    float *qr = nullptr, *sc = nullptr;  // long-cache decode attention: roped q, scores
     ~frq_gemma() {
         for (auto* v : {&qkv, &o, &gu, &down})
             for (frq_w* w : *v) frq_w_free(w);
@@ -559,7 +738,8 @@ int gm_reserve(frq_ctx* c, frq_gemma* g, size_t npos, size_t rows) {
     const size_t o_x = take(R * g->d * 4), o_a = take(R * g->d * 4),
                  o_qkv = take(R * (g->H + 2 * g->KV) * g->hd * 4), o_att = take(R * g->H * g->hd * 4),
                  o_o = take(R * g->d * 4), o_gu = take(R * 2 * g->ffn * 4), o_hm = take(R * g->ffn * 4),
-                 o_lg = take(g->vocab * 4), o_cur = take(4), o_best = take(8), o_tok = take(N * 8), o_ids = take(R * 8);
+                 o_lg = take(g->vocab * 4), o_cur = take(4), o_best = take(8), o_tok = take(N * 8), o_ids = take(R * 8),
+                 o_qr = take(g->H * g->hd * 4), o_sc = take(g->H * gm_pstride(g) * 4);
     GMCHK(hipMalloc(&g->buf, off), "hipMalloc(gemma)");
     char* m = g->buf;
     GMCHK(hipMemsetAsync(m, 0, off, s), "hipMemsetAsync(gemma)");
@@ -583,6 +763,7 @@ int gm_reserve(frq_ctx* c, frq_gemma* g, size_t npos, size_t rows) {
     g->hm = reinterpret_cast<float*>(m + o_hm); g->logits = reinterpret_cast<float*>(m + o_lg);
     g->cur = reinterpret_cast<int*>(m + o_cur); g->best = reinterpret_cast<unsigned long long*>(m + o_best);
     g->tok = reinterpret_cast<int64_t*>(m + o_tok); g->ids = reinterpret_cast<int64_t*>(m + o_ids);
+    g->qr = reinterpret_cast<float*>(m + o_qr); g->sc = reinterpret_cast<float*>(m + o_sc);
     GMCHK(hipStreamSynchronize(s), "hipStreamSynchronize");  // cs is released on return
     return FRQ_OK;
 }
@@ -616,7 +797,27 @@ int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_o
         const float* qn = g->qn_of(l);
         const float* kn = g->kn_of(l);
         const int div = g->arch == 1;
-        if (m == 1) {
+        if (m == 1 && g->cap_pos > 512) {  // long caches: the three-launch decode attention
+            const int hd4 = (hd + 3) & ~3;
+            const size_t plds = (size_t)2 * hd4 * sizeof(float);
+            const dim3 sg((unsigned)H, (unsigned)((g->cap_pos + GT - 1) / GT));
+            const size_t vlds = (size_t)2 * ps * sizeof(float);
+            if (g->kv8) {
+                gm_dec_prep_kernel<true><<<dim3((unsigned)(H + KV)), dim3(GT), plds, s>>>(
+                    g->qkvb, H, KV, hd, g->cur, g->cs, kc, vc, kq, vq, ks, vs, qb, qn, kn, g->eps, g->qr);
+                gm_dec_score_kernel<true><<<sg, dim3(GT), hd4 * sizeof(float), s>>>(
+                    g->qr, H, KV, hd, g->cur, kc, kq, ks, g->qscale, g->cap, sl, win, div, ps, g->sc);
+                gm_dec_value_kernel<true><<<dim3((unsigned)H), dim3(GT), vlds, s>>>(g->sc, H, KV, hd, g->cur, vc, vq,
+                                                                                    vs, sl, win, ps, g->att);
+            } else {
+                gm_dec_prep_kernel<false><<<dim3((unsigned)(H + KV)), dim3(GT), plds, s>>>(
+                    g->qkvb, H, KV, hd, g->cur, g->cs, kc, vc, kq, vq, ks, vs, qb, qn, kn, g->eps, g->qr);
+                gm_dec_score_kernel<false><<<sg, dim3(GT), hd4 * sizeof(float), s>>>(
+                    g->qr, H, KV, hd, g->cur, kc, kq, ks, g->qscale, g->cap, sl, win, div, ps, g->sc);
+                gm_dec_value_kernel<false><<<dim3((unsigned)H), dim3(GT), vlds, s>>>(g->sc, H, KV, hd, g->cur, vc,
+                                                                                     vq, vs, sl, win, ps, g->att);
+            }
+        } else if (m == 1) {
             if (g->kv8)
                 gm_attn_kernel<true, true><<<ag, dim3(GT), lds, s>>>(g->qkvb, H, KV, hd, g->cur, g->cs, kc, vc, kq,
                                                                      vq, ks, vs, g->qscale, g->cap, sl, win, ps,

@@ -106,3 +106,24 @@ def test_config2_gemma2_2b_int4(ctx, tmp_path):
     assert same_bits(lg, rlg), first_diff(lg, rlg)
     g.free()
     b.close()
+
+
+@pytest.mark.parametrize("kv_int8", [False, True])
+def test_gemma_long_cache_decode(ctx, tmp_path, kv_int8):
+    """The three-launch decode attention (caches past 512 positions) with
+    Gemma's soft-cap: the same bits as the oracle."""
+    stem = str(tmp_path / "g")
+    synth.write_gemma2_bundle(stem, 13, n_layer=2, n_head=4, n_kv=2, hd=32, d=128, ffn=256, vocab=500, std=0.05,
+                              norm_std=0.1)
+    m, arrs = oracle.read_bundle(stem)
+    ref = oracle.Gemma(m, arrs, nthreads=16)
+    b = fa.Bundle(stem, ctx)
+    g = fa.Gemma(b, kv_int8)
+    prompt = synth.gpt2_prompt(600, 500, 14)
+    toks, lg = g.generate(prompt, 6, with_logits=True)
+    rt, rlg = ref.generate(prompt, 6, kv_int8=kv_int8, with_logits=True)
+    assert np.array_equal(toks, rt)
+    assert same_bits(lg, rlg), first_diff(lg, rlg)
+    assert np.array_equal(g.generate(prompt, 6), toks)
+    g.free()
+    b.close()

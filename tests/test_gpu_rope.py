@@ -89,3 +89,25 @@ def test_config4_width_two_layers(ctx, tmp_path):
     assert same_bits(lg, rlg), first_diff(lg, rlg)
     g.free()
     b.close()
+
+
+@pytest.mark.parametrize("kv_int8", [False, True])
+def test_rope_long_cache_decode(ctx, tmp_path, kv_int8):
+    """Caches past 512 positions take the three-launch decode attention
+    (scores over many blocks, then the key-order softmax and value chains):
+    the same bits as the oracle."""
+    stem = str(tmp_path / "r")
+    synth.write_rope_bundle(stem, 12, n_layer=2, n_head=4, n_kv=2, hd=32, d=128, ffn=256, vocab=500, std=0.1,
+                            norm_std=0.1, dtype="int8", qk_norm=True)
+    m, arrs = oracle.read_bundle(stem)
+    ref = oracle.Rope(m, arrs, nthreads=16)
+    b = fa.Bundle(stem, ctx)
+    g = fa.Rope(b, kv_int8)
+    prompt = synth.gpt2_prompt(600, 500, 13)
+    toks, lg = g.generate(prompt, 6, with_logits=True)
+    rt, rlg = ref.generate(prompt, 6, kv_int8=kv_int8, with_logits=True)
+    assert np.array_equal(toks, rt)
+    assert same_bits(lg, rlg), first_diff(lg, rlg)
+    assert np.array_equal(g.generate(prompt, 6), toks)
+    g.free()
+    b.close()
