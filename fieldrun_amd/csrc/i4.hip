@@ -31,7 +31,7 @@
 // workgroups would need device-scope fences, which on this part write back
 // and invalidate the whole L2.
 // Other shapes run i4_gemv_generic (M == 1, bit-identical to i4_dot_avx2)
-// or i4_gemm_rows (M > 1).
+// or, M > 1, i4_rows_chain (K and g multiples of 32) or i4_gemm_rows.
 #include "frq_internal.h"
 
 namespace frq {
@@ -184,6 +184,60 @@ __global__ __launch_bounds__(256) void i4_gemm_rows(
 #pragma unroll
     for (int m = 0; m < MT; ++m)
         if (m0 + m < M) out[(size_t)(m0 + m) * N + j] = acc[m];
+}
+
+// The same chain with one thread per (column j, token row blockIdx.y), for
+// K % 32 == 0, g % 32 == 0 and 16-byte aligned activation rows: the thread
+// reads its packed row 32 nibbles (16 bytes) at a time and the token's 32
+// activations (uniform across the workgroup) with them, one chunk ahead of
+// the chain, so the K-long FMA chain is the only serial part.  The order per
+// output is i4_gemm_rows' (kk ascending, w = s4 * scale), bit for bit.
+__global__ __launch_bounds__(256) void i4_rows_chain(const uint8_t* __restrict__ packed,
+                                                     const uint16_t* __restrict__ scale, int N, int K, int g,
+                                                     const float* __restrict__ a, float* __restrict__ out) {
+    const int j = blockIdx.x * 256 + threadIdx.x, m = blockIdx.y;
+    const int jj = min(j, N - 1);  // clamped: the loads stay unconditional, the store is guarded
+    const int nc = K / 32, ng = K / g;
+    const uint4* prow = reinterpret_cast<const uint4*>(packed + (size_t)jj * (K / 2));
+    const uint16_t* srow = scale + (size_t)jj * ng;
+    const float4* arow = reinterpret_cast<const float4*>(a + (size_t)m * K);
+    struct Chunk {
+        uint4 w;
+        float s;
+        float4 av[8];
+    };
+    auto ld = [&](Chunk& c, int i) {
+        c.w = prow[i];
+        c.s = h2f(srow[(32 * i) / g]);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) c.av[u] = arow[8 * i + u];
+    };
+    float acc = 0.0f;
+    auto chain = [&](const Chunk& c) {
+        const uint32_t ws[4] = {c.w.x, c.w.y, c.w.z, c.w.w};
+#pragma unroll
+        for (int c4 = 0; c4 < 4; ++c4) {
+            const float x[8] = {c.av[2 * c4].x, c.av[2 * c4].y, c.av[2 * c4].z, c.av[2 * c4].w,
+                                c.av[2 * c4 + 1].x, c.av[2 * c4 + 1].y, c.av[2 * c4 + 1].z, c.av[2 * c4 + 1].w};
+#pragma unroll
+            for (int q = 0; q < 8; ++q) acc = __builtin_fmaf(x[q], s4f(ws[c4], q) * c.s, acc);
+        }
+    };
+    Chunk c0, c1;
+    ld(c0, 0);
+    ld(c1, min(1, nc - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    int i = 0;
+    for (; i + 2 <= nc; i += 2) {
+        chain(c0);
+        ld(c0, min(i + 2, nc - 1));
+        __builtin_amdgcn_sched_barrier(0);
+        chain(c1);
+        ld(c1, min(i + 3, nc - 1));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (i < nc) chain(c0);
+    if (j < N) out[(size_t)m * N + j] = acc;
 }
 
 constexpr float XMAX4 = 8323072.0f;  // 127 * 2^16
@@ -756,6 +810,11 @@ hipError_t launch_i4_exact(const Weight& w, size_t m, const float* a, float* out
         const hipError_t e = launch_i4_terms(w, a, out, s);
         if (e != hipErrorNotSupported) return e;
         i4_gemv_generic<<<dim3((unsigned)((w.n + 255) / 256)), dim3(256), 0, s>>>(
+            w.q4raw, w.s4raw, (int)w.n, (int)w.k, (int)w.g, a, out);
+        return hipGetLastError();
+    }
+    if (w.k % 32 == 0 && w.g % 32 == 0 && ((uintptr_t)a & 15) == 0 && m <= 65535) {
+        i4_rows_chain<<<dim3((unsigned)((w.n + 255) / 256), (unsigned)m), dim3(256), 0, s>>>(
             w.q4raw, w.s4raw, (int)w.n, (int)w.k, (int)w.g, a, out);
         return hipGetLastError();
     }

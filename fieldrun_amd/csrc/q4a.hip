@@ -11,7 +11,8 @@
 //           sum += scale*qsum + min*asum across the groups in order.
 //   M > 1:  the dequantised weight (scale*q + min, a mul then an add) and a
 //           sequential-k FMA chain per output (the order the oracle takes
-//           for ndarray's sgemm).
+//           for ndarray's sgemm): q4a_rows_chain, a thread per (row, token),
+//           where K and g are multiples of 32, else q4a_gemm_rows.
 // Both bit-exact to the oracle.
 //
 // M == 1 layout of the work: the groups of a row are independent until the
@@ -166,6 +167,61 @@ __global__ __launch_bounds__(QT) void q4a_gemm_rows(const uint8_t* __restrict__ 
         if (m0 + m < M) out[(size_t)(m0 + m) * N + j] = acc[m];
 }
 
+// M > 1 with K % 32 == 0, g % 32 == 0 and 16-byte aligned activation rows:
+// one thread per (column j, token row blockIdx.y), the packed row read 16
+// bytes (32 nibbles) and the token's 32 activations (uniform across the
+// workgroup) at a time, one chunk ahead of the chain.  The order per output
+// is q4a_gemm_rows' (kk ascending, w = scale * q + min), bit for bit.
+__global__ __launch_bounds__(QT) void q4a_rows_chain(const uint8_t* __restrict__ packed, size_t pitch,
+                                                     const uint32_t* __restrict__ sm, int N, int K, int g,
+                                                     const float* __restrict__ a, float* __restrict__ out) {
+    const int j = blockIdx.x * QT + threadIdx.x, m = blockIdx.y;
+    const int jj = min(j, N - 1);  // clamped: the loads stay unconditional, the store is guarded
+    const int nc = K / 32, ng = K / g;
+    const uint4* prow = reinterpret_cast<const uint4*>(packed + (size_t)jj * pitch);
+    const uint32_t* srow = sm + (size_t)jj * ng;
+    const float4* arow = reinterpret_cast<const float4*>(a + (size_t)m * K);
+    struct Chunk {
+        uint4 w;
+        uint32_t s;
+        float4 av[8];
+    };
+    auto ld = [&](Chunk& c, int i) {
+        c.w = prow[i];
+        c.s = srow[(32 * i) / g];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) c.av[u] = arow[8 * i + u];
+    };
+    float acc = 0.0f;
+    auto chain = [&](const Chunk& c) {
+        const uint32_t ws[4] = {c.w.x, c.w.y, c.w.z, c.w.w};
+        const float sc = h2f((uint16_t)(c.s & 0xffffu)), mn = h2f((uint16_t)(c.s >> 16));
+#pragma unroll
+        for (int c4 = 0; c4 < 4; ++c4) {
+            const float x[8] = {c.av[2 * c4].x, c.av[2 * c4].y, c.av[2 * c4].z, c.av[2 * c4].w,
+                                c.av[2 * c4 + 1].x, c.av[2 * c4 + 1].y, c.av[2 * c4 + 1].z, c.av[2 * c4 + 1].w};
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                acc = __builtin_fmaf(x[q], sc * (float)((ws[c4] >> (4 * q)) & 15u) + mn, acc);
+        }
+    };
+    Chunk c0, c1;
+    ld(c0, 0);
+    ld(c1, min(1, nc - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    int i = 0;
+    for (; i + 2 <= nc; i += 2) {
+        chain(c0);
+        ld(c0, min(i + 2, nc - 1));
+        __builtin_amdgcn_sched_barrier(0);
+        chain(c1);
+        ld(c1, min(i + 3, nc - 1));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (i < nc) chain(c0);
+    if (j < N) out[(size_t)m * N + j] = acc;
+}
+
 }  // namespace
 
 size_t q4a_pitch(size_t k) { return round_up((k + 1) / 2, 16); }
@@ -193,6 +249,11 @@ hipError_t launch_q4a(const Weight& w, size_t m, const float* a, float* out, hip
         else
             q4a_gemv_kernel<0><<<dim3(grid), dim3(QT), cgb, s>>>(w.q4raw, w.rpitch, w.q4a_sm, (int)w.n, (int)w.k,
                                                                 (int)w.g, rb, a, out);
+        return hipGetLastError();
+    }
+    if (w.k % 32 == 0 && w.g % 32 == 0 && ((uintptr_t)a & 15) == 0 && m <= 65535) {
+        q4a_rows_chain<<<dim3((unsigned)((w.n + QT - 1) / QT), (unsigned)m), dim3(QT), 0, s>>>(
+            w.q4raw, w.rpitch, w.q4a_sm, (int)w.n, (int)w.k, (int)w.g, a, out);
         return hipGetLastError();
     }
     dim3 grid((unsigned)((w.n + QT - 1) / QT), (unsigned)((m + 15) / 16));
