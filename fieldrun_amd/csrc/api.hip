@@ -146,6 +146,32 @@ int run_i8(frq_ctx* c, const Weight& w, const float* d_a, size_t m, float* d_out
     return FRQ_OK;
 }
 
+bool rows_exact_ok(const frq_w* wh, size_t m) {
+    const Weight& w = wh->w;
+    return w.dtype == FRQ_DT_I8 && m > 16 && m <= 65535 && w.k > 0 && w.wblk && w.wkn && w.kp <= 20480 &&
+           !use_gemv(w, m);
+}
+
+int rows_exact(frq_ctx* c, const frq_w* wh, const float* d_a, size_t m, float* d_out) {
+    if (!rows_exact_ok(wh, m)) return fail(FRQ_ERR_ARG, "mm_i8_rows_exact: shape not supported");
+    const Weight& w = wh->w;
+    DeviceGuard g(c->device);
+    const size_t base = i8_scratch_bytes(w, m, false);
+    if (int rc = ws_reserve(c, base + round_up(m * w.n * sizeof(int32_t), 256))) return rc;
+    const size_t mp = round_up(m, FRQ_MALIGN);
+    Carve cv{(char*)c->ws};
+    int8_t* a8 = cv.take<int8_t>(mp * w.kp);
+    float* sa = cv.take<float>(mp);
+    uint32_t* oi = cv.take<uint32_t>(mp * FRQ_T);
+    float* ov = cv.take<float>(mp * FRQ_T);
+    void* gws = cv.take<char>(gemm_ws_bytes(m, w.kp, w.np));
+    int32_t* acc = reinterpret_cast<int32_t*>((char*)c->ws + base);
+    HIPCHK(launch_quant(d_a, m, w.k, w.kp, a8, sa, oi, ov, c->err, c->stream, mp), "launch quant");
+    HIPCHK(launch_gemm_i8(w, m, a8, sa, oi, ov, d_out, acc, gws, c->stream), "launch gemm_i8");
+    HIPCHK(launch_i8_exact_epilogue(w, m, sa, oi, ov, acc, d_out, c->stream), "launch i8 epilogue");
+    return FRQ_OK;
+}
+
 int check_err_word(frq_ctx* c) {
     int h = 0;
     HIPCHK(hipMemcpy(&h, c->err, sizeof(int), hipMemcpyDeviceToHost), "hipMemcpy(err)");
@@ -229,6 +255,10 @@ int last_code() { return g_code; }
 int ctx_device(const frq_ctx* c) { return c->device; }
 int* ctx_err(frq_ctx* c) { return c->err; }
 const Weight* weight_of(const frq_w* w) { return &w->w; }
+bool i8_rows_exact_ok(const frq_w* w, size_t m) { return rows_exact_ok(w, m); }
+int mm_i8_rows_exact(frq_ctx* c, const frq_w* w, const float* d_a, size_t m, float* d_out) {
+    return rows_exact(c, w, d_a, m, d_out);
+}
 }  // namespace frq
 
 extern "C" {

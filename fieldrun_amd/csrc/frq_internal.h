@@ -228,12 +228,22 @@ hipError_t launch_gemm_i8(const Weight& w, size_t m, const int8_t* a8b,
                           const float* sa, const uint32_t* oidx,
                           const float* oval, float* out, int32_t* acc, void* ws,
                           hipStream_t s);
+// out = scale * (sa * acc + corr) from the GEMM's i32 sums with the
+// reference's sequential outlier correction (the skinny kernel's order)
+hipError_t launch_i8_exact_epilogue(const Weight& w, size_t m, const float* sa, const uint32_t* oidx,
+                                    const float* oval, const int32_t* acc, float* out, hipStream_t s);
 // Context and weight internals, for engines built on the entry points: the
 // context's device, its NaN error word (reported by frq_sync) and a
 // weight's device layout.
 int ctx_device(const frq_ctx* c);
 int* ctx_err(frq_ctx* c);
 const Weight* weight_of(const frq_w* w);
+// The int8 linear over m > 16 rows bit for bit as the skinny path gives it
+// (the reference's M > 1 arm), in one pass: the MFMA GEMM's exact i32 sums
+// and the sequential outlier correction.  i8_rows_exact_ok says whether the
+// weight allows it (an int8 weight with its blocked copy, m > 16).
+bool i8_rows_exact_ok(const frq_w* w, size_t m);
+int mm_i8_rows_exact(frq_ctx* c, const frq_w* w, const float* d_a, size_t m, float* d_out);
 // Sets the calling thread's frq_last_error() message and returns code.
 int set_error(int code, const std::string& msg);
 // The status of the calling thread's last failure.

@@ -681,6 +681,38 @@ hipError_t launch_t(const Weight& w, size_t m, const int8_t* a8b, const float* s
     return launch_k<BN, NST, 2>(w, m, a8b, sa, oidx, oval, out, acc, p, split, s);
 }
 
+// out[i, j] = scale[j] * (sa[i] * (acc[i, j] as f32) + corr), corr the
+// reference's M > 1 sum over row i's outliers (ascending channel, from -0.0,
+// each product rounded before its add: bundle.rs:732-743), from the GEMM's
+// exact i32 sums: the skinny kernel's arithmetic, bit for bit.  A thread takes
+// four adjacent columns of one row (blockIdx.y); an outlier's four weights
+// are one 32-bit word of the (Kp, Np) copy, the row's outliers uniform loads.
+__global__ __launch_bounds__(256) void i8_exact_epilogue(const int8_t* __restrict__ wkn, int Np, int Kp,
+                                                         const float* __restrict__ scale, int N, int t,
+                                                         const float* __restrict__ sa,
+                                                         const uint32_t* __restrict__ oidx,
+                                                         const float* __restrict__ oval,
+                                                         const int32_t* __restrict__ acc, float* __restrict__ out) {
+    const int i = blockIdx.y, j0 = 4 * (blockIdx.x * 256 + threadIdx.x);
+    if (j0 >= N) return;
+    const uint32_t* oi = oidx + (size_t)i * FRQ_T;
+    const float* ov = oval + (size_t)i * FRQ_T;
+    float corr[4] = {-0.0f, -0.0f, -0.0f, -0.0f};
+    for (int q = 0; q < t; ++q) {
+        const uint32_t ch = min(oi[q], (uint32_t)(Kp - 1));
+        const uint32_t wq = *reinterpret_cast<const uint32_t*>(wkn + (size_t)ch * Np + j0);  // j0 + 3 < Np
+        const float o = ov[q];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) corr[b] = corr[b] + o * (float)(int8_t)(wq >> (8 * b));
+    }
+    const float s = sa[i];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        const int j = j0 + b;
+        if (j < N) out[(size_t)i * N + j] = scale[j] * (s * (float)acc[(size_t)i * N + j] + corr[b]);
+    }
+}
+
 }  // namespace
 
 hipError_t launch_blockify(const int8_t* src, size_t valid, size_t R, size_t kp,
@@ -723,6 +755,17 @@ hipError_t launch_gemm_i8(const Weight& w, size_t m, const int8_t* a8b,
     if (pl.bn == 256) return launch_t<256, 3>(w, m, a8b, sa, oidx, oval, out, acc, p, pl.split, s);
     if (pl.bn == 224) return launch_t<224, 3>(w, m, a8b, sa, oidx, oval, out, acc, p, pl.split, s);
     return launch_t<128, 4>(w, m, a8b, sa, oidx, oval, out, acc, p, pl.split, s);
+}
+
+hipError_t launch_i8_exact_epilogue(const Weight& w, size_t m, const float* sa, const uint32_t* oidx,
+                                    const float* oval, const int32_t* acc, float* out, hipStream_t s) {
+    if (m == 0 || w.n == 0) return hipSuccess;
+    if (!w.wkn || m > 65535 || w.np % 4 || w.np < w.n || w.kp == 0) return hipErrorInvalidValue;
+    const int t = (int)(w.k < FRQ_T ? w.k : FRQ_T);
+    const size_t n4 = (w.n + 3) / 4;
+    i8_exact_epilogue<<<dim3((unsigned)((n4 + 255) / 256), (unsigned)m), dim3(256), 0, s>>>(
+        w.wkn, (int)w.np, (int)w.kp, w.scale, (int)w.n, t, sa, oidx, oval, acc, out);
+    return hipGetLastError();
 }
 
 }  // namespace frq

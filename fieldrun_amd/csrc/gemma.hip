@@ -697,6 +697,7 @@ int gm_mm(frq_ctx* c, const frq_w* wh, const float* in, size_t m, float* outp) {
         return FRQ_OK;
     }
     if (m <= 16) return frq_mm_dev(c, wh, in, m, outp);
+    if (i8_rows_exact_ok(wh, m)) return mm_i8_rows_exact(c, wh, in, m, outp);
     const size_t nch = (m + 15) / 16;  // int8: the bit-exact multi-row path in chunks of 8..16 rows
     size_t r0 = 0;
     for (size_t i = 0; i < nch; ++i) {

@@ -497,11 +497,13 @@ int gpt2_block(frq_ctx* c, frq_gpt2* g, size_t m, int rel, int P, float* logits_
                                                                               row0);
         return hipGetLastError();
     };
-    // Bundle::mm over m rows; m > 16 in chunks of 8..16 rows (the bit-exact
-    // multi-row path; every row is quantised and reduced on its own, so the
-    // chunks give the whole product's rows)
+    // Bundle::mm over m rows; m > 16 through the MFMA GEMM with the exact
+    // epilogue, else in chunks of 8..16 rows (the bit-exact multi-row path;
+    // every row is quantised and reduced on its own, so the chunks give the
+    // whole product's rows)
     auto mm = [&](frq_w* w, const float* in, size_t K, float* o, size_t N) -> int {
         if (m <= 16) return frq_mm_dev(c, w, in, m, o);
+        if (i8_rows_exact_ok(w, m)) return mm_i8_rows_exact(c, w, in, m, o);
         const size_t nch = (m + 15) / 16;
         size_t r0 = 0;
         for (size_t i = 0; i < nch; ++i) {
