@@ -338,6 +338,191 @@ __global__ __launch_bounds__(GT) void gm_attn_kernel(const float* __restrict__ q
     }
 }
 
+// ---- multi-row attention, one workgroup per (kv head, query row) ----
+// The R = H / KV query heads that share a kv head read the same key and
+// value rows, so one workgroup takes all R for its query row: each key row
+// is loaded once for R score chains, each value element once for up to RC
+// (head, dim) chains.  The arithmetic per output is gm_attn_kernel<.., false>'s
+// (score = sequential FMA chain over the head dims, softmax max / exp /
+// key-order sum / divide, value chain in key order), so the bits are the same.
+// Needs GT % hd == 0 and R <= RC * (GT / hd).
+template <bool KV8>
+__global__ __launch_bounds__(GT) void gm_attn_group_kernel(const float* __restrict__ qkv, int H, int KV, int hd,
+                                                           const int* __restrict__ curp,
+                                                           const float* __restrict__ kc, const float* __restrict__ vc,
+                                                           const int8_t* __restrict__ kq, const int8_t* __restrict__ vq,
+                                                           const float* __restrict__ ks, const float* __restrict__ vs,
+                                                           float qscale, float cap, int sliding, int window,
+                                                           int pstride, float* __restrict__ att, int div) {
+    constexpr int RMAX = 16, RC = 4;
+    extern __shared__ float4 lds4[];
+    const int R = H / KV, hd4 = (hd + 3) & ~3, kvd = KV * hd;
+    float* q = reinterpret_cast<float*>(lds4);  // R rows of hd4
+    float* p = q + R * hd4;                     // R rows of pstride
+    float* sv = p + (size_t)R * pstride;
+    __shared__ float red[RMAX][GT / 64];
+    const int kv = blockIdx.x, i = blockIdx.y;
+    const int cur = *curp, ab = cur + i, klen = cur + (int)gridDim.y;
+    const float* row = qkv + (size_t)i * (H + 2 * KV) * hd;
+    for (int t = threadIdx.x; t < R * hd; t += GT) q[(t / hd) * hd4 + t % hd] = row[(kv * R + t / hd) * hd + t % hd];
+    __syncthreads();
+    const int j0 = (sliding && ab >= window) ? ab - window + 1 : 0;
+    const int nk = ab + 1;
+    float mx[RMAX];
+#pragma unroll
+    for (int r = 0; r < RMAX; ++r) mx[r] = -INFINITY;
+    for (int j = j0 + threadIdx.x; j < nk; j += GT) {
+        float acc[RMAX];
+#pragma unroll
+        for (int r = 0; r < RMAX; ++r) acc[r] = 0.0f;
+        if constexpr (!KV8) {
+            const float* kr = kc + (size_t)j * kvd + (size_t)kv * hd;
+            for (int c = 0; c < hd; c += 4) {
+                const float4 k4 = *reinterpret_cast<const float4*>(kr + c);
+#pragma unroll
+                for (int r = 0; r < RMAX; ++r) {
+                    if (r < R) {
+                        const float* qr = q + r * hd4;
+                        acc[r] = __builtin_fmaf(qr[c], k4.x, acc[r]);
+                        acc[r] = __builtin_fmaf(qr[c + 1], k4.y, acc[r]);
+                        acc[r] = __builtin_fmaf(qr[c + 2], k4.z, acc[r]);
+                        acc[r] = __builtin_fmaf(qr[c + 3], k4.w, acc[r]);
+                    }
+                }
+            }
+        } else {
+            const int8_t* kr = kq + (size_t)j * kvd + (size_t)kv * hd;
+            const float sk = ks[(size_t)j * KV + kv];
+            sv[j] = vs[(size_t)j * KV + kv];
+            for (int c = 0; c < hd; c += 4) {
+                const char4 k4 = *reinterpret_cast<const char4*>(kr + c);
+                const float k0 = (float)k4.x * sk, k1 = (float)k4.y * sk, k2 = (float)k4.z * sk,
+                            k3 = (float)k4.w * sk;
+#pragma unroll
+                for (int r = 0; r < RMAX; ++r) {
+                    if (r < R) {
+                        const float* qr = q + r * hd4;
+                        acc[r] = __builtin_fmaf(qr[c], k0, acc[r]);
+                        acc[r] = __builtin_fmaf(qr[c + 1], k1, acc[r]);
+                        acc[r] = __builtin_fmaf(qr[c + 2], k2, acc[r]);
+                        acc[r] = __builtin_fmaf(qr[c + 3], k3, acc[r]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < RMAX; ++r) {
+            if (r < R) {
+                float sj = div ? acc[r] / qscale : acc[r] * qscale;
+                if (cap > 0.0f) sj = cap * libm::frq_tanhf(sj / cap);
+                p[(size_t)r * pstride + j] = sj;
+                mx[r] = fmaxf(mx[r], sj);
+            }
+        }
+    }
+    // block max per head (max is exact in any order)
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int r = 0; r < RMAX; ++r) {
+        if (r < R) {
+            float v = mx[r];
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+            if (lane == 0) red[r][wave] = v;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < RMAX; ++r) {
+        if (r < R) {
+            float v = red[r][0];
+#pragma unroll
+            for (int w = 1; w < GT / 64; ++w) v = fmaxf(v, red[r][w]);
+            if (j0 > 0 || nk < klen) v = fmaxf(v, -1e30f);  // a masked entry joins the max
+            mx[r] = v;
+        }
+    }
+    __syncthreads();  // red is reused for the sums
+    for (int j = j0 + threadIdx.x; j < nk; j += GT) {
+#pragma unroll
+        for (int r = 0; r < RMAX; ++r)
+            if (r < R) p[(size_t)r * pstride + j] = libm::frq_expf(p[(size_t)r * pstride + j] - mx[r]);
+    }
+    __syncthreads();
+    if (threadIdx.x < R) {  // one lane per head, in key order; the lanes run in step
+        const float* pr = p + (size_t)threadIdx.x * pstride;
+        const int ja = min((j0 + 3) & ~3, nk);
+        float sum = 0.0f;
+        for (int j = j0; j < ja; ++j) sum = sum + pr[j];
+        red[threadIdx.x][0] = lds_seq_sum(pr + ja, nk - ja, sum);
+    }
+    __syncthreads();
+    for (int j = j0 + threadIdx.x; j < nk; j += GT) {
+#pragma unroll
+        for (int r = 0; r < RMAX; ++r)
+            if (r < R) p[(size_t)r * pstride + j] = p[(size_t)r * pstride + j] / red[r][0];
+    }
+    __syncthreads();
+    // value chains: thread t takes dim c = t % hd of heads t / hd, t / hd + GT / hd, ...
+    const int c = threadIdx.x % hd, r0 = threadIdx.x / hd, rs = GT / hd;
+    const size_t col = (size_t)kv * hd + c;
+    float acc[RC];
+#pragma unroll
+    for (int u = 0; u < RC; ++u) acc[u] = 0.0f;
+    constexpr int B = 16;
+    const int n = nk - j0, nb = n / B;
+    float v0[B], v1[B];
+    auto ld = [&](float (&v)[B], int k) {
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+            const size_t j = (size_t)(j0 + k * B + u);
+            if constexpr (!KV8) v[u] = vc[j * kvd + col];
+            else v[u] = (float)vq[j * kvd + col] * sv[j];
+        }
+    };
+    auto fma_b = [&](const float (&v)[B], int k) {
+#pragma unroll
+        for (int w = 0; w < RC; ++w) {
+            const int r = r0 + w * rs;
+            if (r < R) {
+                const float* pr = p + (size_t)r * pstride + j0 + k * B;
+#pragma unroll
+                for (int u = 0; u < B; ++u) acc[w] = __builtin_fmaf(pr[u], v[u], acc[w]);
+            }
+        }
+    };
+    if (r0 < R) {
+        if (nb > 0) {  // both batches of a trip consumed unconditionally, loads pinned a batch ahead
+            ld(v0, 0);
+            ld(v1, min(1, nb - 1));
+            __builtin_amdgcn_sched_barrier(0);
+            int k = 0;
+            for (; k + 2 <= nb; k += 2) {
+                fma_b(v0, k);
+                ld(v0, min(k + 2, nb - 1));
+                __builtin_amdgcn_sched_barrier(0);
+                fma_b(v1, k + 1);
+                ld(v1, min(k + 3, nb - 1));
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (k < nb) fma_b(v0, k);
+        }
+        for (int j = j0 + nb * B; j < nk; ++j) {
+            const float v = KV8 ? (float)vq[(size_t)j * kvd + col] * sv[j] : vc[(size_t)j * kvd + col];
+#pragma unroll
+            for (int w = 0; w < RC; ++w) {
+                const int r = r0 + w * rs;
+                if (r < R) acc[w] = __builtin_fmaf(p[(size_t)r * pstride + j], v, acc[w]);
+            }
+        }
+#pragma unroll
+        for (int w = 0; w < RC; ++w) {
+            const int r = r0 + w * rs;
+            if (r < R) att[(size_t)i * H * hd + (size_t)(kv * R + r) * hd + c] = acc[w];
+        }
+    }
+}
+
 // ---- decode attention for long caches, split into three launches ----
 // The scores of the keys are independent (each a sequential FMA chain over
 // the head dims), so they spread over many blocks; the softmax sum and the
@@ -835,7 +1020,21 @@ int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_o
                 gm_qkv_kernel<false><<<dim3((unsigned)m), dim3(GT), 0, s>>>(g->qkvb, H, KV, hd, g->cur, g->cs, kc,
                                                                             vc, kq, vq, ks, vs, qb, qn, kn, g->eps);
             GMCHK(hipGetLastError(), "launch qkv");
-            if (g->kv8)
+            // the heads of a kv group in one workgroup where the shape and LDS allow
+            const int R = H / KV;
+            const size_t glds = ((size_t)R * (((size_t)hd + 3) & ~(size_t)3) + (size_t)R * ps + (g->kv8 ? (size_t)ps : 0)) * sizeof(float);
+            const bool grouped = R > 1 && R <= 16 && GT % hd == 0 && R <= 4 * (GT / hd) && glds + 1024 <= 160 * 1024 &&
+                                 m <= 65535;
+            if (grouped) {
+                auto kern = g->kv8 ? gm_attn_group_kernel<true> : gm_attn_group_kernel<false>;
+                if (glds > 64 * 1024)
+                    GMCHK(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                              (int)glds),
+                          "hipFuncSetAttribute");
+                kern<<<dim3((unsigned)KV, (unsigned)m), dim3(GT), glds, s>>>(g->qkvb, H, KV, hd, g->cur, kc, vc, kq,
+                                                                             vq, ks, vs, g->qscale, g->cap, sl, win,
+                                                                             ps, g->att, div);
+            } else if (g->kv8)
                 gm_attn_kernel<true, false><<<ag, dim3(GT), lds, s>>>(g->qkvb, H, KV, hd, g->cur, g->cs, kc, vc, kq,
                                                                       vq, ks, vs, g->qscale, g->cap, sl, win, ps,
                                                                       g->att, div, nullptr, nullptr, nullptr, g->eps);
