@@ -30,7 +30,8 @@ def same_bits(a, b):
 
 
 @pytest.mark.parametrize("n,k,g", [(9216, 2304, 32), (2304, 9216, 32), (2048, 2304, 32), (300, 37, 16),
-                                   (257, 100, 64), (64, 26, 13), (1000, 4096, 64), (33, 8, 32)])
+                                   (257, 100, 64), (64, 26, 13), (1000, 4096, 64), (33, 8, 32),
+                                   (512, 1024, 32), (300, 2048, 64)])
 @pytest.mark.parametrize("m", [1, 3, 16, 20])
 def test_q4a_mm_bit_exact(ctx, n, k, g, m):
     if m > 1 and n * k > 4_000_000:
