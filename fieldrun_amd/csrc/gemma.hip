@@ -659,12 +659,14 @@ __global__ __launch_bounds__(GT) void gm_dec_value_kernel(const float* __restric
     const float sum = red[0];
     for (int j = j0 + threadIdx.x; j < nk; j += GT) p[j] = p[j] / sum;
     __syncthreads();
+    // three batches of B keys in flight (48 loads a wave, within the 63 the
+    // wave's vector-memory counter tracks): the cache is read from L2 / HBM
     constexpr int B = 16;
     for (int c = threadIdx.x; c < hd; c += GT) {
         float acc = 0.0f;
         const size_t col = (size_t)kv * hd + c;
         const int n = nk - j0, nb = n / B;
-        float v0[B], v1[B];
+        float v0[B], v1[B], v2[B];
         auto ld = [&](float (&v)[B], int k) {
 #pragma unroll
             for (int u = 0; u < B; ++u) {
@@ -680,17 +682,22 @@ __global__ __launch_bounds__(GT) void gm_dec_value_kernel(const float* __restric
         if (nb > 0) {
             ld(v0, 0);
             ld(v1, min(1, nb - 1));
+            ld(v2, min(2, nb - 1));
             __builtin_amdgcn_sched_barrier(0);
             int k = 0;
-            for (; k + 2 <= nb; k += 2) {
+            for (; k + 3 <= nb; k += 3) {
                 fma_b(v0, k);
-                ld(v0, min(k + 2, nb - 1));
+                ld(v0, min(k + 3, nb - 1));
                 __builtin_amdgcn_sched_barrier(0);
                 fma_b(v1, k + 1);
-                ld(v1, min(k + 3, nb - 1));
+                ld(v1, min(k + 4, nb - 1));
+                __builtin_amdgcn_sched_barrier(0);
+                fma_b(v2, k + 2);
+                ld(v2, min(k + 5, nb - 1));
                 __builtin_amdgcn_sched_barrier(0);
             }
             if (k < nb) fma_b(v0, k);
+            if (k + 1 < nb) fma_b(v1, k + 1);
         }
         for (int j = j0 + nb * B; j < nk; ++j) {
             const float v = KV8 ? (float)vq[(size_t)j * kvd + col] * sv[j] : vc[(size_t)j * kvd + col];
