@@ -91,13 +91,14 @@ def test_config4_width_two_layers(ctx, tmp_path):
     b.close()
 
 
+@pytest.mark.parametrize("hd", [32, 128])
 @pytest.mark.parametrize("kv_int8", [False, True])
-def test_rope_long_cache_decode(ctx, tmp_path, kv_int8):
+def test_rope_long_cache_decode(ctx, tmp_path, kv_int8, hd):
     """Caches past 512 positions take the three-launch decode attention
     (scores over many blocks, then the key-order softmax and value chains):
     the same bits as the oracle."""
     stem = str(tmp_path / "r")
-    synth.write_rope_bundle(stem, 12, n_layer=2, n_head=4, n_kv=2, hd=32, d=128, ffn=256, vocab=500, std=0.1,
+    synth.write_rope_bundle(stem, 12, n_layer=2, n_head=4, n_kv=2, hd=hd, d=4 * hd, ffn=256, vocab=500, std=0.1,
                             norm_std=0.1, dtype="int8", qk_norm=True)
     m, arrs = oracle.read_bundle(stem)
     ref = oracle.Rope(m, arrs, nthreads=16)
