@@ -484,7 +484,11 @@ hipError_t launch_linear_m1(const Weight& w, const float* a, float* out, int32_t
     // grid caps: about the workgroups resident at once (256 CUs times the
     // occupancy each variant's registers allow), measured best on MI355X
     const int g = gmax;
-    if (nch <= 64) return launch_lm1<8, 8, true, 1>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 768, s);
+    // short rows: 8 lanes a row (32-row groups) when N is large, 16 lanes
+    // (16-row groups: twice the groups, a shorter quant-bound tail) below
+    if (nch <= 64 && w.n >= 65536)
+        return launch_lm1<8, 8, true, 1>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 768, s);
+    if (nch <= 64) return launch_lm1<16, 4, true, 1>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 768, s);
     if (nch <= 128) return launch_lm1<64, 2, true, 2>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 1024, s);
     if (nch <= 256) return launch_lm1<64, 4, true, 4>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 1024, s);
     if (nch <= 512) return launch_lm1<64, 8, true, 8>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 512, s);
