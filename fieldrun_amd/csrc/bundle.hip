@@ -371,10 +371,19 @@ const ArrSpec* find(const frq_bundle* b, const std::string& name) {
     return &it->second;
 }
 
-size_t prod(const std::vector<size_t>& s) {
+// Product of the dims, false when it overflows size_t (a crafted manifest
+// could otherwise wrap it onto the array's byte count).
+bool prod(const std::vector<size_t>& s, size_t* out) {
     size_t n = 1;
-    for (size_t x : s) n *= x;
-    return n;
+    for (size_t x : s)
+        if (__builtin_mul_overflow(n, x, &n)) return false;
+    *out = n;
+    return true;
+}
+
+// Bytes of an (n, ceil(k/g)) f16 table, false on overflow.
+bool group_table_bytes(size_t n, size_t k, size_t g, size_t* out) {
+    return g && !__builtin_mul_overflow(n, k / g + (k % g != 0), out) && !__builtin_mul_overflow(*out, (size_t)2, out);
 }
 
 // The array, checked to be `dt` with `ndim` dims and `bytes` of content.
@@ -385,10 +394,16 @@ const ArrSpec* need(const frq_bundle* b, const std::string& name, const char* dt
         frq::set_error(FRQ_ERR_FORMAT, name + ": expected a " + std::to_string(ndim) + "-D " + dt + " array");
         return nullptr;
     }
-    size_t want = prod(s->shape);
-    if (!std::strcmp(dt, "f16")) want *= 2;
-    else if (!std::strcmp(dt, "f32")) want *= 4;
-    else if (!std::strcmp(dt, "i4") || !std::strcmp(dt, "q4a")) want = s->shape[0] * ((s->shape[1] + 1) / 2);
+    size_t want = 0;
+    bool ok = prod(s->shape, &want);
+    if (!std::strcmp(dt, "f16")) ok = ok && !__builtin_mul_overflow(want, (size_t)2, &want);
+    else if (!std::strcmp(dt, "f32")) ok = ok && !__builtin_mul_overflow(want, (size_t)4, &want);
+    else if (!std::strcmp(dt, "i4") || !std::strcmp(dt, "q4a"))
+        ok = ok && !__builtin_mul_overflow(s->shape[0], s->shape[1] / 2 + (s->shape[1] & 1), &want);
+    if (!ok) {
+        frq::set_error(FRQ_ERR_FORMAT, name + ": shape overflows the address space");
+        return nullptr;
+    }
     if (s->bytes != want) {
         frq::set_error(FRQ_ERR_FORMAT, name + ": " + std::to_string(s->bytes) + " bytes for its shape (" +
                                            std::to_string(want) + " expected)");
@@ -501,7 +516,8 @@ static frq_w* bundle_weight(frq_ctx* ctx, const frq_bundle* b, const char* name)
         const size_t n = s->shape[0], k = s->shape[1], g = s->group ? s->group : 32;
         const ArrSpec* sc = find(b, sn);
         if (!sc) return nullptr;
-        if (sc->dtype != "f16" || sc->bytes != n * ((k + g - 1) / g) * 2) {
+        size_t want = 0;
+        if (sc->dtype != "f16" || !group_table_bytes(n, k, g, &want) || sc->bytes != want) {
             frq::set_error(FRQ_ERR_FORMAT, sn + ": f16 (out, ceil(in/group)) scales expected");
             return nullptr;
         }
@@ -515,8 +531,9 @@ static frq_w* bundle_weight(frq_ctx* ctx, const frq_bundle* b, const char* name)
         if (!sc) return nullptr;
         const ArrSpec* mi = find(b, mn);
         if (!mi) return nullptr;
-        const size_t want = n * ((k + g - 1) / g) * 2;
-        if (sc->dtype != "f16" || sc->bytes != want || mi->dtype != "f16" || mi->bytes != want) {
+        size_t want = 0;
+        if (sc->dtype != "f16" || !group_table_bytes(n, k, g, &want) || sc->bytes != want || mi->dtype != "f16" ||
+            mi->bytes != want) {
             frq::set_error(FRQ_ERR_FORMAT, nm + ": f16 (out, ceil(in/group)) __scale and __min expected");
             return nullptr;
         }

@@ -23,21 +23,27 @@
 // serialise the ring.  The tile order is XCD-aware (tile_of).
 //
 // corr: 32 VALU multiply-adds per output would cost as much as the MFMA GEMM
-// itself, so corr also runs on the int8 MFMA.  A pre-pass (gemm_prep_kernel)
-// works once per 128-row tile, for every column tile at once: the union U of
-// the tile's outlier channels (ascending, padded to a multiple of 64 with
-// channel 0), each row's digit scale so[i] = max|av| / (127*2^16), and each
-// outlier value as X = round(av / so[i]), |X| <= 127*2^16, split into three
-// signed int8 digits X = d2*2^16 + d1*2^8 + d0, laid out as MFMA A blocks
-// D_d (128 x |U|, 64 union channels per chunk).  In the GEMM's epilogue a
-// column tile gathers W[:, U] from the (K, Np) row-major copy (wkn: for a
-// channel the tile's columns are contiguous bytes), transposes it into B
-// blocks in LDS with byte permutes, and C_d = D_d . W[:, U]^T is an exact
-// int32 MFMA product per digit: corr = so * ((C2*256 + C1)*256 + C0).  The
-// 24-bit split makes corr differ from the reference's f32 sum by ~1e-7
-// relative; acc stays bit-exact.  Rows with a non-finite outlier take the
-// exact sequential corr instead.  The f32 tile leaves through LDS, one wave
-// slab of 16 rows at a time, as whole-row 16-byte stores.
+// itself, so corr runs on the f16 MFMA.  A pre-pass (gemm_prep_kernel) works
+// once per 128-row tile, for every column tile at once: the union U of the
+// tile's outlier channels (ascending, padded to a multiple of 64 with
+// channel 0), each row's power-of-two scale so[i] = 2^(E-15) (max|av| =
+// m * 2^E), and each outlier value x = av / so[i] (exact, |x| < 2^15) as an
+// f16 pair hi = f16(x), lo = f16(x - hi), laid out as MFMA A blocks (128 x
+// |U|, 64 union channels per chunk).  In the GEMM's epilogue a column tile
+// gathers W[:, U] from the (Kp, Np) row-major copy (wkn: for a channel the
+// tile's columns are contiguous bytes), turns the bytes into f16 B blocks in
+// LDS with byte permutes (every int8 is exact in f16), and
+// v_mfma_f32_16x16x32_f16 adds (hi + lo) . W[:, U]^T straight into the f32
+// tile, which holds sa * acc / so (a power-of-two scaling, exact); the tile
+// is scaled back by so at the end.  hi + lo is within 2^-22 |x|, so corr
+// differs from the reference's f32 sum by ~1e-7 relative; acc stays
+// bit-exact.  Rows with a non-finite or vanishing outlier take the exact
+// sequential corr instead.  The f32 tile leaves through LDS, one wave slab
+// of 16 rows at a time, as whole-row 16-byte stores.
+//
+// i8_exact_epilogue (for the decode engines, whose greedy tokens need the
+// reference's bits) takes the GEMM's exact int32 sums instead and adds the
+// outlier correction as the reference's sequential f32 sum.
 #include "frq_internal.h"
 
 #include <algorithm>
@@ -110,13 +116,13 @@ __host__ __device__ inline int union_cap(int kp) {
 }
 
 // Per 128-row tile (blockIdx.x): the union of its rows' outlier channels,
-// per-row digit scales, and the digit blocks of chunks blockIdx.y,
-// blockIdx.y + gridDim.y, ...  Outputs: nu[mt]; uch[mt][cap] (union
-// channels ascending, then channel 0 up to the next multiple of 64);
+// per-row power-of-two scales, and the f16 (hi, lo) A blocks of chunks
+// blockIdx.y, blockIdx.y + gridDim.y, ...  Outputs: nu[mt]; uch[mt][cap]
+// (union channels ascending, then channel 0 up to the next multiple of 64);
 // so[Mp] (0 on rows that take the exact corr), fin[Mp] (1 on those rows);
-// D[mt][cap / 64][3][8][1 KB]: block (d, rb) of chunk c holds digit d of
-// rows 16rb.. against union entries 64c.., in MFMA A order (lane 16g + r:
-// row r, entries 16g..16g+15).
+// D[mt][cap / 64][DCH bytes]: for chunk c the (hi, lo) x two 32-entry
+// halves x 8 row-block f16 A blocks of rows 16rb.. against union entries
+// 64c.., in MFMA A order.
 __global__ __launch_bounds__(256) void gemm_prep_kernel(
     int M, int K, int Kp, int t, const uint32_t* __restrict__ oidx,
     const float* __restrict__ oval, int cap, int* __restrict__ nu_out,

@@ -900,24 +900,63 @@ int gm_mm(frq_ctx* c, const frq_w* wh, const float* in, size_t m, float* outp) {
     return FRQ_OK;
 }
 
-size_t gm_pstride(const frq_gemma* g) { return (g->cap_pos + 3) & ~(size_t)3; }
-size_t gm_attn_lds(const frq_gemma* g) { return (3 * ((g->hd + 3) & ~(size_t)3) + 2 * gm_pstride(g)) * sizeof(float); }
+size_t gm_pstride_n(size_t npos) { return (npos + 3) & ~(size_t)3; }
+size_t gm_pstride(const frq_gemma* g) { return gm_pstride_n(g->cap_pos); }
+// LDS of the one-launch attention (gm_attn_kernel: q, two hd-vectors and
+// two score rows of the padded position count); the long-cache value
+// kernel needs the two score rows only, so this bounds both.
+size_t gm_attn_lds_n(size_t hd, size_t npos) {
+    return (3 * ((hd + 3) & ~(size_t)3) + 2 * gm_pstride_n(npos)) * sizeof(float);
+}
+size_t gm_attn_lds(const frq_gemma* g) { return gm_attn_lds_n(g->hd, g->cap_pos); }
+constexpr size_t GM_LDS_MAX = 160 * 1024;  // gfx950's LDS per workgroup
+
+// Dynamic LDS above the default 64 KB for the kernels whose need grows with
+// the cache length.
+hipError_t gm_allow_lds(size_t lds) {
+    if (lds <= 64 * 1024) return hipSuccess;
+    const void* ks[] = {(const void*)gm_attn_kernel<false, false>, (const void*)gm_attn_kernel<false, true>,
+                        (const void*)gm_attn_kernel<true, false>, (const void*)gm_attn_kernel<true, true>,
+                        (const void*)gm_dec_value_kernel<false>, (const void*)gm_dec_value_kernel<true>};
+    for (const void* k : ks)
+        if (hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds)) return e;
+    return hipSuccess;
+}
+
+// Points every buffer of the model at nothing and the capacities at zero:
+// the state after a failed reserve, so the next call reserves again.
+void gm_drop_buffers(frq_gemma* g) {
+    if (g->buf) (void)hipFree(g->buf);
+    g->buf = nullptr;
+    g->cap_pos = g->cap_rows = 0;
+    g->cs = nullptr;
+    g->kc = g->vc = g->ks = g->vs = nullptr;
+    g->kq = g->vq = nullptr;
+    g->x = g->a = g->qkvb = g->att = g->ob = g->gub = g->hm = g->logits = nullptr;
+    g->cur = nullptr;
+    g->best = nullptr;
+    g->tok = g->ids = nullptr;
+    g->qr = g->sc = nullptr;
+}
 
 // Device buffers for up to npos positions and rows prompt rows; the RoPE
 // table cos / sin(pos * inv[j]) from the host libm (the reference's f32
-// cos / sin).
+// cos / sin).  A request the attention cannot serve is refused before
+// anything changes; any later failure leaves the model with no buffers
+// (capacities 0), never with pointers into freed memory.
 int gm_reserve(frq_ctx* c, frq_gemma* g, size_t npos, size_t rows) {
-    if (npos <= g->cap_pos && rows <= g->cap_rows) return FRQ_OK;
+    if (npos <= g->cap_pos && rows <= g->cap_rows && g->buf) return FRQ_OK;
+    const size_t N = std::max(npos, g->cap_pos), R = std::max(rows, g->cap_rows);
+    const size_t need = gm_attn_lds_n(g->hd, N);
+    if (need > GM_LDS_MAX)
+        return set_error(FRQ_ERR_ARG, "gemma: " + std::to_string(N) +
+                                          " positions exceed the attention scores' LDS (" + std::to_string(need) +
+                                          " > " + std::to_string(GM_LDS_MAX) + " bytes)");
     hipStream_t s = (hipStream_t)frq_get_stream(c);
     GMCHK(hipStreamSynchronize(s), "hipStreamSynchronize");
-    if (g->buf) (void)hipFree(g->buf);
-    g->buf = nullptr;
-    g->cap_pos = std::max(npos, g->cap_pos);
-    g->cap_rows = std::max(rows, g->cap_rows);
-    if (gm_attn_lds(g) > 64 * 1024)
-        return set_error(FRQ_ERR_ARG, "gemma: " + std::to_string(g->cap_pos) +
-                                          " positions exceed this build's attention scores in LDS");
-    const size_t N = g->cap_pos, R = g->cap_rows, L = g->L, kvd = g->KV * g->hd, half = g->hd / 2;
+    gm_drop_buffers(g);
+    GMCHK(gm_allow_lds(need), "hipFuncSetAttribute");
+    const size_t L = g->L, kvd = g->KV * g->hd, half = g->hd / 2;
     size_t off = 0;
     auto take = [&](size_t bytes) { const size_t o = off; off += round_up(bytes, 256); return o; };
     const size_t o_cs = take(N * half * sizeof(float2));
@@ -932,17 +971,28 @@ int gm_reserve(frq_ctx* c, frq_gemma* g, size_t npos, size_t rows) {
                  o_qkv = take(R * (g->H + 2 * g->KV) * g->hd * 4), o_att = take(R * g->H * g->hd * 4),
                  o_o = take(R * g->d * 4), o_gu = take(R * 2 * g->ffn * 4), o_hm = take(R * g->ffn * 4),
                  o_lg = take(g->vocab * 4), o_cur = take(4), o_best = take(8), o_tok = take(N * 8), o_ids = take(R * 8),
-                 o_qr = take(g->H * g->hd * 4), o_sc = take(g->H * gm_pstride(g) * 4);
-    GMCHK(hipMalloc(&g->buf, off), "hipMalloc(gemma)");
-    char* m = g->buf;
-    GMCHK(hipMemsetAsync(m, 0, off, s), "hipMemsetAsync(gemma)");
+                 o_qr = take(g->H * g->hd * 4), o_sc = take(g->H * gm_pstride_n(N) * 4);
+    char* m = nullptr;
+    GMCHK(hipMalloc(&m, off), "hipMalloc(gemma)");
+    if (hipError_t e = hipMemsetAsync(m, 0, off, s)) {
+        (void)hipFree(m);
+        return gfail(e, "hipMemsetAsync(gemma)");
+    }
     std::vector<float2> cs(N * half);
     for (size_t pos = 0; pos < N; ++pos)
         for (size_t j = 0; j < half; ++j) {
             const float ang = (float)pos * g->inv[j];
             cs[pos * half + j] = make_float2(cosf(ang), sinf(ang));
         }
-    GMCHK(hipMemcpyAsync(m + o_cs, cs.data(), cs.size() * sizeof(float2), hipMemcpyHostToDevice, s), "hipMemcpyAsync");
+    hipError_t e = hipMemcpyAsync(m + o_cs, cs.data(), cs.size() * sizeof(float2), hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);  // cs is released on return
+    if (e != hipSuccess) {
+        (void)hipFree(m);
+        return gfail(e, "hipMemcpyAsync(gemma RoPE table)");
+    }
+    g->buf = m;
+    g->cap_pos = N;
+    g->cap_rows = R;
     g->cs = reinterpret_cast<float2*>(m + o_cs);
     g->kc = g->kv8 ? nullptr : reinterpret_cast<float*>(m + o_kc);
     g->vc = g->kv8 ? nullptr : reinterpret_cast<float*>(m + o_vc);
@@ -957,7 +1007,6 @@ int gm_reserve(frq_ctx* c, frq_gemma* g, size_t npos, size_t rows) {
     g->cur = reinterpret_cast<int*>(m + o_cur); g->best = reinterpret_cast<unsigned long long*>(m + o_best);
     g->tok = reinterpret_cast<int64_t*>(m + o_tok); g->ids = reinterpret_cast<int64_t*>(m + o_ids);
     g->qr = reinterpret_cast<float*>(m + o_qr); g->sc = reinterpret_cast<float*>(m + o_sc);
-    GMCHK(hipStreamSynchronize(s), "hipStreamSynchronize");  // cs is released on return
     return FRQ_OK;
 }
 

@@ -33,6 +33,7 @@
 //             order, which is random per process; ascending id is one of
 //             its orders.
 #include "frq_internal.h"
+#include "libm_f32.h"
 
 #include <algorithm>
 
@@ -96,11 +97,14 @@ MoeWs moe_view(void* base, const MoeBank& b, size_t T, size_t k) {
     return v;
 }
 
-__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+// The gates and the softmax use the restated glibc expf / fdlibm tanhf
+// (libm_f32.h), which Rust's f32::exp / f32::tanh reach on the reference's
+// host, so route weights and gated activations are the reference's bits.
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + libm::frq_expf(-x)); }
 
 __device__ __forceinline__ float gelu_tanh(float x) {
     const float c = sqrtf(2.0f / 3.14159274101257324f);
-    return 0.5f * x * (1.0f + tanhf(c * (x + 0.044715f * x * x * x)));
+    return 0.5f * x * (1.0f + libm::frq_tanhf(c * (x + 0.044715f * x * x * x)));
 }
 
 // ---- routing: one wave per token ----------------------------------------
@@ -129,7 +133,7 @@ __device__ bool route_wave(const float* __restrict__ row, int E, int topk, int n
         wave_sync();
         return true;
     }
-    for (int e = lane; e < E; e += 64) p[e] = expf(row[e] - m);
+    for (int e = lane; e < E; e += 64) p[e] = libm::frq_expf(row[e] - m);
     wave_sync();
     float s = 0.0f;  // sequential sum in expert order, as the reference
     for (int e = 0; e < E; ++e) s = s + p[e];

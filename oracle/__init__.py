@@ -50,6 +50,7 @@ def _load():
         "fro_gelu_tanh": (F, [F]),
         "fro_moe_route": (None, [P, S, S, S, I, P, P, P, P]),
         "fro_moe": (I, [P, S, S, P, S, S, I, P, S, I, P, P, P, P, P, P, P]),
+        "fro_moe_mt": (I, [P, S, S, P, S, S, I, P, S, I, P, P, P, P, P, P, P, I]),
         "fro_rowdot_f32": (None, [I, P, P, S, S, P, P]),
         "fro_rowdot_f32_subset": (None, [I, P, P, S, S, P, P, S, P]),
         "fro_layernorm": (None, [P, S, S, P, P, P]),
@@ -239,7 +240,9 @@ def moe_route(logits, topk, norm_topk=True, per_expert_scale=None):
 
 
 def moe(x, logits, topk, norm_topk, gate, gate_scale, up, up_scale, down, down_scale,
-        act=0, per_expert_scale=None):
+        act=0, per_expert_scale=None, nthreads: int = 1):
+    """The routed expert layer (fro_moe; fro_moe_mt when nthreads > 1, the
+    same output: experts' matmuls in parallel, one ascending-id combine)."""
     x, logits = _c(x, np.float32), _c(logits, np.float32)
     T, d = x.shape
     E = logits.shape[1]
@@ -262,8 +265,12 @@ def moe(x, logits, topk, norm_topk, gate, gate_scale, up, up_scale, down, down_s
         up_ = usp = None
     pes = None if per_expert_scale is None else _c(per_expert_scale, np.float32)
     out = np.empty((T, d), np.float32)
-    lib.fro_moe(_p(x), T, d, _p(logits), E, topk, int(norm_topk), _p(pes), mi, act,
-                gp, gsp, up_, usp, dp, dsp, _p(out))
+    if nthreads > 1:
+        lib.fro_moe_mt(_p(x), T, d, _p(logits), E, topk, int(norm_topk), _p(pes), mi, act,
+                       gp, gsp, up_, usp, dp, dsp, _p(out), int(nthreads))
+    else:
+        lib.fro_moe(_p(x), T, d, _p(logits), E, topk, int(norm_topk), _p(pes), mi, act,
+                    gp, gsp, up_, usp, dp, dsp, _p(out))
     return out
 
 

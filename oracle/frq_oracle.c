@@ -503,48 +503,99 @@ void fro_moe_route(const float* logits, size_t T, size_t E, size_t topk,
  * of src/gemma4.rs:162-185 (act 1).  For each active expert the tokens routed
  * to it are gathered, gate/up (or packed gate_up) -> act -> down via
  * expert_mm, and out[t,:] += w * down (mul then add).  The reference visits
- * experts in HashMap order (random per process); here ascending expert id. */
-int fro_moe(const float* x, size_t T, size_t d, const float* logits, size_t E,
-            size_t topk, int norm_topk, const float* pes, size_t mi, int act,
-            const int8_t* const* gate, const float* const* gate_scale,
-            const int8_t* const* up, const float* const* up_scale,
-            const int8_t* const* down, const float* const* down_scale,
-            float* out) {
-    int32_t* sel = (int32_t*)malloc(nz(T * topk) * sizeof(int32_t));
-    float* w = (float*)malloc(nz(T * topk) * sizeof(float));
-    fro_moe_route(logits, T, E, topk, norm_topk, pes, sel, w, NULL);
-    memset(out, 0, T * d * sizeof(float));
-    size_t gw = act == 1 ? 2 * mi : mi;
+ * experts in HashMap order (random per process); here ascending expert id.
+ * fro_moe_mt runs the experts' matmuls on nthreads threads (each expert's
+ * rows are independent) and then combines on one thread in ascending expert
+ * id, so its output is the same for any thread count. */
+typedef struct {
+    const float* x; size_t T, d, topk, mi, E; int act;
+    const int32_t* sel; const float* w;
+    const int8_t* const* gate; const float* const* gate_scale;
+    const int8_t* const* up; const float* const* up_scale;
+    const int8_t* const* down; const float* const* down_scale;
+    float* dn;  /* (T*topk, d): the down output of (t, slot) */
+    int w0, nw;
+} moe_job;
+
+static void* moe_worker(void* arg) {
+    const moe_job* J = (const moe_job*)arg;
+    const size_t T = J->T, d = J->d, topk = J->topk, mi = J->mi;
+    const size_t gw = J->act == 1 ? 2 * mi : mi;
     float* rows = (float*)malloc(nz(T * d) * sizeof(float));
     float* g = (float*)malloc(nz(T * gw) * sizeof(float));
     float* u = (float*)malloc(nz(T * mi) * sizeof(float));
     float* h = (float*)malloc(nz(T * mi) * sizeof(float));
     float* dn = (float*)malloc(nz(T * d) * sizeof(float));
     size_t* tok = (size_t*)malloc(nz(T) * sizeof(size_t));
-    float* tw = (float*)malloc(nz(T) * sizeof(float));
-    for (size_t e = 0; e < E; e++) {
+    for (size_t e = (size_t)J->w0; e < J->E; e += (size_t)J->nw) {
         size_t nt = 0;
         for (size_t t = 0; t < T; t++)
             for (size_t i = 0; i < topk; i++)
-                if ((size_t)sel[t * topk + i] == e) { tok[nt] = t; tw[nt] = w[t * topk + i]; nt++; }
+                if ((size_t)J->sel[t * topk + i] == e) tok[nt++] = t * topk + i;
         if (!nt) continue;
-        for (size_t r = 0; r < nt; r++) memcpy(rows + r * d, x + tok[r] * d, d * sizeof(float));
-        fro_expert_mm_i8(rows, nt, gate[e], gate_scale[e], d, gw, g);
-        if (act == 0) {
-            fro_expert_mm_i8(rows, nt, up[e], up_scale[e], d, mi, u);
+        for (size_t r = 0; r < nt; r++) memcpy(rows + r * d, J->x + tok[r] / topk * d, d * sizeof(float));
+        fro_expert_mm_i8(rows, nt, J->gate[e], J->gate_scale[e], d, gw, g);
+        if (J->act == 0) {
+            fro_expert_mm_i8(rows, nt, J->up[e], J->up_scale[e], d, mi, u);
             for (size_t i = 0; i < nt * mi; i++) h[i] = fro_silu(g[i]) * u[i];
         } else {
             for (size_t r = 0; r < nt; r++)
                 for (size_t c = 0; c < mi; c++)
                     h[r * mi + c] = fro_gelu_tanh(g[r * gw + c]) * g[r * gw + c + mi];
         }
-        fro_expert_mm_i8(h, nt, down[e], down_scale[e], mi, d, dn);
-        for (size_t r = 0; r < nt; r++)
-            for (size_t c = 0; c < d; c++)
-                out[tok[r] * d + c] = out[tok[r] * d + c] + tw[r] * dn[r * d + c];
+        fro_expert_mm_i8(h, nt, J->down[e], J->down_scale[e], mi, d, dn);
+        for (size_t r = 0; r < nt; r++) memcpy(J->dn + tok[r] * d, dn + r * d, d * sizeof(float));
     }
-    free(sel); free(w); free(rows); free(g); free(u); free(h); free(dn); free(tok); free(tw);
+    free(rows); free(g); free(u); free(h); free(dn); free(tok);
+    return NULL;
+}
+
+int fro_moe_mt(const float* x, size_t T, size_t d, const float* logits, size_t E,
+               size_t topk, int norm_topk, const float* pes, size_t mi, int act,
+               const int8_t* const* gate, const float* const* gate_scale,
+               const int8_t* const* up, const float* const* up_scale,
+               const int8_t* const* down, const float* const* down_scale,
+               float* out, int nthreads) {
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > 64) nthreads = 64;
+    int32_t* sel = (int32_t*)malloc(nz(T * topk) * sizeof(int32_t));
+    float* w = (float*)malloc(nz(T * topk) * sizeof(float));
+    float* dn = (float*)malloc(nz(T * topk * d) * sizeof(float));
+    fro_moe_route(logits, T, E, topk, norm_topk, pes, sel, w, NULL);
+    moe_job jobs[64];
+    pthread_t th[64];
+    for (int i = 0; i < nthreads; i++) {
+        moe_job J = {x, T, d, topk, mi, E, act, sel, w, gate, gate_scale, up, up_scale,
+                     down, down_scale, dn, i, nthreads};
+        jobs[i] = J;
+    }
+    if (nthreads == 1) {
+        moe_worker(&jobs[0]);
+    } else {
+        for (int i = 0; i < nthreads; i++) pthread_create(&th[i], NULL, moe_worker, &jobs[i]);
+        for (int i = 0; i < nthreads; i++) pthread_join(th[i], NULL);
+    }
+    memset(out, 0, T * d * sizeof(float));
+    for (size_t e = 0; e < E; e++)
+        for (size_t t = 0; t < T; t++)
+            for (size_t i = 0; i < topk; i++)
+                if ((size_t)sel[t * topk + i] == e) {
+                    const float tw = w[t * topk + i];
+                    const float* r = dn + (t * topk + i) * d;
+                    for (size_t c = 0; c < d; c++) out[t * d + c] = out[t * d + c] + tw * r[c];
+                }
+    free(sel); free(w); free(dn);
     return FRO_OK;
+}
+
+int fro_moe(const float* x, size_t T, size_t d, const float* logits, size_t E,
+            size_t topk, int norm_topk, const float* pes, size_t mi, int act,
+            const int8_t* const* gate, const float* const* gate_scale,
+            const int8_t* const* up, const float* const* up_scale,
+            const int8_t* const* down, const float* const* down_scale,
+            float* out) {
+    return fro_moe_mt(x, T, d, logits, E, topk, norm_topk, pes, mi, act, gate, gate_scale, up,
+                      up_scale, down, down_scale, out, 1);
 }
 
 /* ------------------------------------------------------------------------ */

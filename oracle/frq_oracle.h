@@ -148,6 +148,12 @@ int fro_moe(const float* x, size_t T, size_t d, const float* logits, size_t E,
             const float* const* gate_scale, const int8_t* const* up,
             const float* const* up_scale, const int8_t* const* down,
             const float* const* down_scale, float* out);
+int fro_moe_mt(const float* x, size_t T, size_t d, const float* logits, size_t E,
+            size_t topk, int norm_topk, const float* per_expert_scale,
+            size_t mi, int act, const int8_t* const* gate,
+            const float* const* gate_scale, const int8_t* const* up,
+            const float* const* up_scale, const int8_t* const* down,
+            const float* const* down_scale, float* out, int nthreads);
 
 /* Bundle::rowdot_f32 / rowdot_f32_subset over a row-major (rows, d) table:
  * dtype 3 f32 (float data), 4 f16 (uint16 bits), 5 rowi8 (int8 data +

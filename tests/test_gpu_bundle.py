@@ -151,3 +151,29 @@ def test_qwen3moe_config_bundle_on_device(ctx, tmp_path):
     err = np.abs(out[same] - ref[same]).max()
     assert err <= 1e-5 * np.abs(ref).max(), err
     b.close()
+
+
+@pytest.mark.parametrize("dtype,shape", [("i8", [1 << 33, 1 << 31]), ("i4", [1 << 32, 1 << 36]),
+                                         ("q4a", [1 << 32, 1 << 36])])
+def test_bundle_shape_overflow_is_a_format_error(ctx, tmp_path, dtype, shape):
+    """A manifest whose shape products wrap around 2^64 onto the arrays'
+    byte counts (0 here: for int4, 2^32 * 2^35 packed bytes and 2^32 * 2^31
+    * 2 scale bytes) is refused before any upload reads the blob."""
+    import json
+    stem = str(tmp_path / "o")
+    with open(stem + ".fieldrun.bin", "wb") as f:
+        f.write(b"\0" * 64)
+    arrays = [{"name": "w", "dtype": dtype, "shape": shape, "offset": 0, "bytes": 0},
+              {"name": "w__scale", "dtype": "f16", "shape": [shape[1] if dtype == "i8" else shape[0], 1 << 31],
+               "offset": 0, "bytes": 0},
+              {"name": "w__min", "dtype": "f16", "shape": [shape[0], 1 << 31], "offset": 0, "bytes": 0}]
+    if dtype != "i8":
+        arrays[0]["group"] = 32
+    m = {"format": "fieldrun-bundle", "version": 1, "arch": "rope", "config": [1], "arrays": arrays}
+    with open(stem + ".fieldrun.json", "w") as f:
+        json.dump(m, f)
+    b = fa.Bundle(stem, ctx)
+    with pytest.raises(fa.FrqError) as e:
+        b.weight("w")
+    assert e.value.code == fa.FRQ_ERR_FORMAT
+    b.close()

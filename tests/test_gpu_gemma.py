@@ -127,3 +127,48 @@ def test_gemma_long_cache_decode(ctx, tmp_path, kv_int8):
     assert np.array_equal(g.generate(prompt, 6), toks)
     g.free()
     b.close()
+
+
+def test_gemma_refused_length_leaves_model_usable(ctx, small):
+    """A generate whose cache the attention cannot hold is refused with
+    FRQ_ERR_ARG before anything changes; the same handle then still decodes
+    bit for bit (before and after a successful call)."""
+    m, arrs = oracle.read_bundle(small)
+    ref = oracle.Gemma(m, arrs, nthreads=8)
+    prompt = synth.gpt2_prompt(5, 500, 21)
+    rt, rlg = ref.generate(prompt, 4, with_logits=True)
+    b = fa.Bundle(small, ctx)
+    g = fa.Gemma(b)
+    for first in (True, False):
+        if not first:
+            toks, lg = g.generate(prompt, 4, with_logits=True)
+            assert np.array_equal(toks, rt) and same_bits(lg, rlg)
+        with pytest.raises(fa.FrqError) as e:
+            g.generate(prompt, 40000)
+        assert e.value.code == fa.FRQ_ERR_ARG
+        toks, lg = g.generate(prompt, 4, with_logits=True)
+        assert np.array_equal(toks, rt)
+        assert same_bits(lg, rlg), first_diff(lg, rlg)
+    g.free()
+    b.close()
+
+
+def test_gemma_cache_past_64k_of_scores(ctx, tmp_path):
+    """A cache of 8300 positions (Gemma-2's 8192-token context and more):
+    the one-launch prefill attention (one query head per kv head, so not the
+    grouped kernel) and the long-cache decode split hold more than 64 KB of
+    scores in LDS; tokens and logits bit for bit."""
+    stem = str(tmp_path / "l")
+    synth.write_gemma2_bundle(stem, 17, n_layer=2, n_head=2, n_kv=2, hd=16, d=32, ffn=64, vocab=300, std=0.1,
+                              norm_std=0.1)
+    m, arrs = oracle.read_bundle(stem)
+    ref = oracle.Gemma(m, arrs, nthreads=16)
+    b = fa.Bundle(stem, ctx)
+    g = fa.Gemma(b)
+    prompt = synth.gpt2_prompt(8300, 300, 6)
+    toks, lg = g.generate(prompt, 3, with_logits=True)
+    rt, rlg = ref.generate(prompt, 3, with_logits=True)
+    assert np.array_equal(toks, rt)
+    assert same_bits(lg, rlg), first_diff(lg, rlg)
+    g.free()
+    b.close()

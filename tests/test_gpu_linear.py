@@ -46,7 +46,8 @@ def corr_mag(a, wt, scale, acc):
                                    (4, 768, 3072), (1, 37, 5), (1, 33, 300), (2, 32, 64), (1, 1, 7),
                                    (1, 14336, 512), (3, 18944, 64), (1, 18944, 300), (1, 9000, 77),
                                    (1, 20480, 40), (5, 896, 4864), (8, 4864, 896), (16, 4096, 1024),
-                                   (16, 14336, 256), (11, 33, 300), (16, 1000, 3000), (2, 896, 40000)])
+                                   (16, 14336, 256), (11, 33, 300), (16, 1000, 3000), (2, 896, 40000),
+                                   (1, 24576, 300), (1, 30001, 64), (1, 65536, 33)])
 def test_i8_gemv_bit_exact(ctx, m, k, n):
     a, wt, scale = case(m, k, n, 100 + m * 7 + k + n)
     w = ctx.upload_i8(wt, scale)

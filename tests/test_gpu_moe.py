@@ -1,9 +1,11 @@
 """Parity of the gfx950 routed-expert layer against the CPU oracle.
 
-Routing: selected experts identical (ties -> lower expert id, as the stable
-sort in src/qwen3moe.rs:129), weights within 1e-6 relative (exp differs by
-at most an ulp between the device and the host libm).  expert_mm: bit-exact
-(same sequential-k FMA order).  Layer output: within 1e-5 of max|out|.
+Routing: selected experts identical and combine weights bit-identical (the
+device runs the restated glibc expf, as Rust's f32::exp reaches it; ties ->
+lower expert id, as the stable sort in src/qwen3moe.rs:129).  expert_mm:
+bit-exact (same sequential-k FMA order).  Layer output: every element within
+1e-5 of the sum of the magnitudes of its terms (moe_term_bound), for every
+token, with every token's expert set identical to the oracle's.
 """
 import numpy as np
 import pytest
@@ -15,13 +17,44 @@ import fieldrun_amd as fa
 pytestmark = pytest.mark.gpu
 
 
-def near_tie(probs_row, sel_a, sel_b):
-    """True when two selections differ only across an (ulp-level) tie."""
-    if set(sel_a) == set(sel_b):
-        return True
-    k = len(sel_a)
-    srt = np.sort(probs_row)[::-1]
-    return abs(float(srt[k - 1]) - float(srt[k])) <= 4e-7 * float(srt[k - 1])
+def _silu(g):
+    return g / (1.0 + np.exp(-g))
+
+
+def _gelu(g):
+    return 0.5 * g * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (g + 0.044715 * g ** 3)))
+
+
+def moe_term_bound(x, sel, w, gate, gs, up, us, down, ds, act):
+    """f64 bound per output element (t, c): sum over t's experts of |w| *
+    sum_j (|h_j| + dh_j) * |down[j, c]|, where dh_j bounds how far an
+    error of the gate / up sums (relative to the magnitudes of their terms)
+    moves h_j = act(g_j) * u_j.  The device rounds each row to 24 bits
+    before its exact integer products; the reference sums in f32."""
+    T, d = x.shape
+    B = np.zeros((T, d))
+    X = x.astype(np.float64)
+    for e in range(len(gate)):
+        tok, slot = np.nonzero(sel == e)
+        if not len(tok):
+            continue
+        Xe, Ae = X[tok], np.abs(X[tok])
+        G = gate[e].astype(np.float64) * gs[e]
+        g, Sg = Xe @ G, Ae @ np.abs(G)
+        if act == 0:
+            U = up[e].astype(np.float64) * us[e]
+            u, Su = Xe @ U, Ae @ np.abs(U)
+            a = _silu(g)
+            h = a * u
+            dh = 1.1 * np.abs(u) * Sg + np.abs(a) * Su
+        else:
+            mi = G.shape[1] // 2
+            a = _gelu(g[:, :mi])
+            h = a * g[:, mi:]
+            dh = 1.2 * np.abs(g[:, mi:]) * Sg[:, :mi] + np.abs(a) * Sg[:, mi:]
+        D = np.abs(down[e].astype(np.float64) * ds[e])
+        np.add.at(B, tok, np.abs(w[tok, slot])[:, None] * ((np.abs(h) + dh) @ D))
+    return B
 
 
 @pytest.mark.parametrize("T,E,k,norm", [(1, 128, 8, True), (512, 128, 8, True), (37, 60, 4, False),
@@ -32,17 +65,14 @@ def test_route_parity(ctx, T, E, k, norm):
     if T > 3:
         logits[2, 1] = logits[2, E - 2] = 7.0  # exact tie: the lower expert first
     sel, w = ctx.moe_route(logits, k, norm)
-    rsel, rw, probs = oracle.moe_route(logits, k, norm)
-    for t in range(T):
-        if not np.array_equal(sel[t], rsel[t]):
-            assert near_tie(probs[t], sel[t], rsel[t]), t
-        else:
-            assert np.allclose(w[t], rw[t], rtol=1e-6, atol=0)
+    rsel, rw, _ = oracle.moe_route(logits, k, norm)
+    assert np.array_equal(sel, rsel)
+    assert np.array_equal(w.view(np.uint32), rw.view(np.uint32))
     pes = rng.uniform(0.5, 1.5, E).astype(np.float32)
     sel2, w2 = ctx.moe_route(logits, k, True, pes)
     rsel2, rw2, _ = oracle.moe_route(logits, k, True, pes)
-    same = np.all(sel2 == rsel2, axis=1)
-    assert np.allclose(w2[same], rw2[same], rtol=1e-6)
+    assert np.array_equal(sel2, rsel2)
+    assert np.array_equal(w2.view(np.uint32), rw2.view(np.uint32))
 
 
 def test_route_nan_is_an_error(ctx):
@@ -71,7 +101,8 @@ def test_expert_mm_bit_exact(ctx, act):
 @pytest.mark.parametrize("T,E,d,mi,k,act", [(1, 16, 256, 64, 4, 0), (40, 16, 256, 64, 4, 0),
                                             (7, 8, 128, 32, 8, 1), (1, 128, 2048, 768, 8, 0),
                                             (64, 128, 2048, 768, 8, 0), (1, 8, 128, 32, 8, 1),
-                                            (1, 60, 256, 64, 4, 0), (1, 32, 320, 96, 16, 1)])
+                                            (1, 60, 256, 64, 4, 0), (1, 32, 320, 96, 16, 1),
+                                            (512, 128, 2048, 768, 8, 0)])
 def test_moe_layer_parity(ctx, T, E, d, mi, k, act):
     gate, gs, up, us, down, ds = synth.moe_layer(E, d, mi, synth.seed(3) + T + act, act)
     bank = ctx.upload_moe_i8(gate, gs, up, us, down, ds, act)
@@ -80,13 +111,13 @@ def test_moe_layer_parity(ctx, T, E, d, mi, k, act):
     logits = rng.standard_normal((T, E)).astype(np.float32)
     pes = rng.uniform(0.5, 1.5, E).astype(np.float32) if act else None
     out = bank.forward(x, logits, k, True, pes)
-    ref = oracle.moe(x, logits, k, True, gate, gs, up, us, down, ds, act, pes)
-    sel, _ = ctx.moe_route(logits, k, True, pes)
-    rsel, _, _ = oracle.moe_route(logits, k, True, pes)
-    same = np.all(np.sort(sel, 1) == np.sort(rsel, 1), axis=1)
-    assert same.mean() > 0.95
-    err = np.abs(out[same] - ref[same]).max()
-    assert err <= 1e-5 * np.abs(ref).max(), err
+    ref = oracle.moe(x, logits, k, True, gate, gs, up, us, down, ds, act, pes, nthreads=16)
+    sel, w = ctx.moe_route(logits, k, True, pes)
+    rsel, rw, _ = oracle.moe_route(logits, k, True, pes)
+    assert np.array_equal(sel, rsel)
+    B = moe_term_bound(x, rsel, rw, gate, gs, up, us, down, ds, act)
+    err = np.abs(out.astype(np.float64) - ref)
+    assert np.all(err <= 1e-5 * B), float((err / np.maximum(B, 1e-300)).max())
 
 
 @pytest.mark.parametrize("act", [0, 1])
@@ -106,26 +137,30 @@ def test_moe_decode_matches_batched_row(ctx, act):
     assert np.array_equal(one[0].view(np.uint32), many[0].view(np.uint32))
 
 
-def test_moe_decode_extreme_row_takes_exact_path(ctx):
-    """A token row whose digit scale leaves the exact range (|x| ~ 3e38)
-    takes the reference's sequential expert sum in the decode kernels."""
+@pytest.mark.parametrize("T", [1, 3])
+def test_moe_extreme_row_takes_exact_path(ctx, T):
+    """A token row whose digit scale leaves the exact range (one |x| of
+    1e35) takes the reference's sequential expert sum, in the decode
+    kernels (T == 1) and in the batched pipeline.  Input channel 7 has zero
+    weights in every gate / up matrix, so the row's outputs stay finite and
+    the exact path's arithmetic is compared value by value."""
     E, d, mi, k = 16, 256, 64, 4
     gate, gs, up, us, down, ds = synth.moe_layer(E, d, mi, synth.seed(3) + 91, 0)
+    for e in range(E):
+        gate[e][7, :] = 0
+        up[e][7, :] = 0
     bank = ctx.upload_moe_i8(gate, gs, up, us, down, ds, 0)
     rng = np.random.default_rng(11)
-    x = (rng.standard_normal((1, d)) * 1e-3).astype(np.float32)
-    x[0, 7] = np.float32(3.0e38)
-    logits = rng.standard_normal((1, E)).astype(np.float32)
+    x = rng.standard_normal((T, d)).astype(np.float32)
+    x[0, 7] = np.float32(1.0e35)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
     out = bank.forward(x, logits, k, True)
     ref = oracle.moe(x, logits, k, True, gate, gs, up, us, down, ds, 0, None)
-    # (this row overflows the SiLU * up product: every output is inf or NaN,
-    # position for position as in the reference)
-    assert np.array_equal(np.isnan(out), np.isnan(ref))
-    inf = np.isinf(ref)
-    assert np.array_equal(out[inf], ref[inf])
-    fin = np.isfinite(ref)
-    if fin.any():
-        assert np.abs(out[fin] - ref[fin]).max() <= 1e-5 * np.abs(ref[fin]).max()
+    assert np.all(np.isfinite(ref)) and np.all(np.isfinite(out))
+    rsel, rw, _ = oracle.moe_route(logits, k, True)
+    B = moe_term_bound(np.where(np.abs(x) > 1e30, 0, x), rsel, rw, gate, gs, up, us, down, ds, 0)
+    err = np.abs(out.astype(np.float64) - ref)
+    assert np.all(err <= 1e-5 * B), float((err / np.maximum(B, 1e-300)).max())
 
 
 def test_moe_decode_nan_logits_is_an_error(ctx):

@@ -407,6 +407,11 @@ def test_moe_f64_brute_force(act):
                 h = 0.5 * gg * (1 + np.tanh(np.sqrt(2 / np.pi) * (gg + 0.044715 * gg ** 3))) * uu
             ref[t] += w[t, i] * (h @ (down[e] * ds[e][None, :].astype(np.float64)))
     assert np.max(np.abs(out - ref)) <= 1e-5 * np.max(np.abs(ref))
+    # the threaded restatement (experts in parallel, one ascending-id
+    # combine) gives the same bits for any thread count
+    for nt in (2, 3, 8):
+        o2 = oracle.moe(x, logits, k, True, gate, gs, up, us, down, ds, act, pes, nthreads=nt)
+        assert np.array_equal(o2.view(np.uint32), out.view(np.uint32))
 
 
 # ------------------------------------------- package quantisers vs oracle ----
