@@ -56,6 +56,7 @@ SIGNATURES = {
     "frq_w_info": (_I, [_P, _P, _P, _P, _P]),
     "frq_mm": (_I, [_P, _P, _P, _S, _P]),
     "frq_mm_dev": (_I, [_P, _P, _P, _S, _P]),
+    "frq_mm_dev_noalloc": (_I, [_P, _P, _P, _S, _P]),
     "frq_mm_i8_debug": (_I, [_P, _P, _P, _S, _P, _P, _P, _P, _P, _P]),
     "frq_quant_pitch": (_S, [_S]),
     "frq_quant_i8_dev": (_I, [_P, _P, _S, _S, _P, _P, _P, _P]),
@@ -295,6 +296,12 @@ class Weight:
     def mm_dev(self, a_ptr: int, m: int, out_ptr: int):
         """Device-pointer variant, enqueued on the context stream."""
         _check(lib.frq_mm_dev(self.ctx.h, self.h, a_ptr, m, out_ptr))
+
+    def mm_dev_noalloc(self, a_ptr: int, m: int, out_ptr: int):
+        """mm_dev with no device allocation: the scratch is the library's
+        static per-GPU array (frq_mm_dev_noalloc; shared by every call on
+        the GPU, so overlapping calls race)."""
+        _check(lib.frq_mm_dev_noalloc(self.ctx.h, self.h, a_ptr, m, out_ptr))
 
     def mm_q_dev(self, a8_ptr: int, sa_ptr: int, oidx_ptr: int, oval_ptr: int, m: int, out_ptr: int):
         """int8 dot + epilogue on a batch quantised by Context.quant_dev."""

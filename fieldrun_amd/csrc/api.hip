@@ -36,7 +36,37 @@ struct frq_ctx {
     unsigned* tickets = nullptr;
 };
 
+// Scratch of frq_mm_dev_noalloc: one static array per GPU (each device that
+// loads the library holds its own copy until the process ends).  Host code
+// never uses the array's name as an address: frq_init resolves the device
+// address once per device with hipGetSymbolAddress and keeps it in
+// g_scratch_ptr, and only that pointer reaches kernels.
+static __device__ __align__(256) char scratch[FRQ_NOALLOC_SCRATCH_BYTES];
+
 namespace {
+
+constexpr int FRQ_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[FRQ_MAX_DEVICES];  // scratch's address on each device, null until resolved
+
+// With `dev` current: resolve scratch's device address once for this device.
+hipError_t scratch_setup(int dev) {
+    if (dev < 0 || dev >= FRQ_MAX_DEVICES) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[dev]) return hipSuccess;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress((void**)&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    g_scratch_ptr[dev] = p;
+    return hipSuccess;
+}
+
+void* scratch_of(int dev) {
+    if (dev < 0 || dev >= FRQ_MAX_DEVICES) return nullptr;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    return g_scratch_ptr[dev];
+}
 
 thread_local std::string g_err;
 thread_local int g_code = FRQ_OK;
@@ -292,6 +322,7 @@ frq_ctx* frq_init(int device) {
     if (e == hipSuccess) e = hipMemset(c->err, 0, 256);
     if (e == hipSuccess) e = hipMalloc(&c->tickets, FRQ_TICKETS * sizeof(unsigned));
     if (e == hipSuccess) e = hipMemset(c->tickets, 0, FRQ_TICKETS * sizeof(unsigned));
+    if (e == hipSuccess) e = scratch_setup(device);
     if (e != hipSuccess) {
         hip_fail(e, "frq_init");
         if (c->own) (void)hipStreamDestroy(c->own);
@@ -530,6 +561,39 @@ int frq_mm_dev(frq_ctx* c, const frq_w* wh, const float* d_a, size_t m, float* d
     if (w.dtype == FRQ_DT_I4) {
         if (int rc = ws_reserve(c, i4_ws_floats(w, m) * sizeof(float) + 256)) return rc;
         HIPCHK(launch_i4(w, m, d_a, d_out, (float*)c->ws, c->tickets, c->stream), "launch i4");
+        return FRQ_OK;
+    }
+    if (w.dtype == FRQ_DT_Q4A) {
+        HIPCHK(launch_q4a(w, m, d_a, d_out, c->stream), "launch q4a");
+        return FRQ_OK;
+    }
+    return fail(FRQ_ERR_DTYPE, "unsupported weight dtype");
+}
+
+int frq_mm_dev_noalloc(frq_ctx* c, const frq_w* wh, const float* d_a, size_t m, float* d_out) {
+    if (int rc = check_ctx(c)) return rc;
+    if (!wh) return fail(FRQ_ERR_ARG, "null weight");
+    const Weight& w = wh->w;
+    if (w.device != c->device) return fail(FRQ_ERR_ARG, "weight lives on another device");
+    if (m == 0 || w.n == 0) return FRQ_OK;
+    if (!d_a || !d_out) return fail(FRQ_ERR_ARG, "null activation/output pointer");
+    char* sp = static_cast<char*>(scratch_of(c->device));
+    if (!sp) return fail(FRQ_ERR_HIP, "frq_mm_dev_noalloc: the static scratch of this device is not set up");
+    auto too_big = [&](size_t need) {
+        return fail(FRQ_ERR_ARG, "frq_mm_dev_noalloc: this call needs " + std::to_string(need) +
+                                     " bytes of scratch, the static scratch holds " +
+                                     std::to_string((size_t)FRQ_NOALLOC_SCRATCH_BYTES));
+    };
+    DeviceGuard g(c->device);
+    if (w.dtype == FRQ_DT_I8) {
+        const size_t need = i8_scratch_bytes(w, m, false);
+        if (need > FRQ_NOALLOC_SCRATCH_BYTES) return too_big(need);
+        return run_i8(c, w, d_a, m, d_out, nullptr, sp, nullptr, nullptr, nullptr, nullptr);
+    }
+    if (w.dtype == FRQ_DT_I4) {
+        const size_t need = i4_ws_floats(w, m) * sizeof(float) + 256;
+        if (need > FRQ_NOALLOC_SCRATCH_BYTES) return too_big(need);
+        HIPCHK(launch_i4(w, m, d_a, d_out, reinterpret_cast<float*>(sp), c->tickets, c->stream), "launch i4");
         return FRQ_OK;
     }
     if (w.dtype == FRQ_DT_Q4A) {

@@ -127,6 +127,20 @@ int frq_mm(frq_ctx* ctx, const frq_w* w, const float* a, size_t m,
            float* out);
 int frq_mm_dev(frq_ctx* ctx, const frq_w* w, const float* d_a, size_t m,
                float* d_out);
+/* No counterpart in the reference.  frq_mm_dev that allocates nothing, for
+ * callers that cannot call hipMalloc (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid allocation).  The per-call scratch
+ * (quantised rows, outliers, the GEMM pre-pass, int4 digit rows) lives in
+ * one static device array of FRQ_NOALLOC_SCRATCH_BYTES per GPU, which the
+ * library holds until the process ends; a call that needs more is refused
+ * with FRQ_ERR_ARG (every int8 batch up to 16 rows fits, and larger batches
+ * whose GEMM pre-pass and split-K tiles fit).  The array keeps the last
+ * call's contents, and every call on one GPU shares it: calls that overlap
+ * on one GPU (two streams, two contexts or two threads) race.  Results are
+ * frq_mm_dev's. */
+#define FRQ_NOALLOC_SCRATCH_BYTES (32u << 20)
+int frq_mm_dev_noalloc(frq_ctx* ctx, const frq_w* w, const float* d_a, size_t m,
+                       float* d_out);
 /* int8 only, host pointers: also returns the internals the reference keeps
  * in locals — acc (M,N) i32 (the i8dot sums), a8 (M,K) i8, sa[M], and the
  * min(32,K) outliers per row (oidx, oval; (M,32), ascending channel).  Any
