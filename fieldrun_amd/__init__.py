@@ -85,6 +85,7 @@ SIGNATURES = {
     "frq_gpt2_generate": (_I, [_P, _P, _P, _S, _S, _P, _P]),
     "frq_gpt2_predict": (_I, [_P, _P, _P, _S, _P, _P]),
     "frq_libm_f32": (_I, [_P, _I, _P, _S, _P]),
+    "frq_seq_fold_f32": (_I, [_P, _P, _S, _S, C.c_float, _P]),
     "frq_gemma_load": (_I, [_P, _P, _I, _P]),
     "frq_rope_load": (_I, [_P, _P, _I, _P]),
     "frq_gemma_free": (None, [_P]),
@@ -553,6 +554,16 @@ class Gpt2:
         _check(lib.frq_gpt2_predict(self.ctx.h, self.h, _ptr(ids), len(ids), _ptr(tok),
                                     None if lg is None else _ptr(lg)))
         return (int(tok[0]), lg) if with_logits else int(tok[0])
+
+
+def seq_fold_f32(ctx: "Context", x: np.ndarray, init: float = -0.0) -> np.ndarray:
+    """out[r] = init + x[r, 0] + ... + x[r, n-1] in f32 index order (the
+    reference's iterator sum), by the device's speculative segmented fold
+    (frq_seq_fold_f32, the decode kernels' RMSNorm and softmax sums)."""
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+    out = np.empty(x.shape[0], np.float32)
+    _check(lib.frq_seq_fold_f32(ctx.h, _ptr(x), x.shape[0], x.shape[1], C.c_float(init), _ptr(out)))
+    return out
 
 
 LIBM_FNS = {"expf": 0, "expm1f": 1, "tanhf": 2}

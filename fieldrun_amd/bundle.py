@@ -36,9 +36,12 @@ class BundleWriter:
         self.offset = 0
 
     def _write(self, raw: bytes | np.ndarray):
-        b = raw.tobytes() if isinstance(raw, np.ndarray) else raw
-        self._bin.write(b)
-        return len(b)
+        if isinstance(raw, np.ndarray):  # the array's own bytes, no copy
+            raw = np.ascontiguousarray(raw)
+            self._bin.write(memoryview(raw.reshape(-1).view(np.uint8)))
+            return raw.nbytes
+        self._bin.write(raw)
+        return len(raw)
 
     def entry(self, name: str, dtype: str, shape, nbytes: int, group: int | None = None):
         e = {"name": name, "dtype": dtype, "shape": [int(s) for s in shape], "offset": self.offset,

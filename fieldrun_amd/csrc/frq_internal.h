@@ -152,6 +152,115 @@ __device__ inline float lds_seq_sum(const float* p, int n, float acc) {
     return acc;
 }
 
+// lds_seq_sum with two chains in the calling lane: a0 and a1 each get
+// p[0] + ... + p[n-1] added in index order (one LDS load feeds both).
+__device__ inline void lds_seq_sum2(const float* p, int n, float& a0, float& a1) {
+    constexpr int B = 8;
+    const int nb = n / (4 * B);
+    const float4* p4 = reinterpret_cast<const float4*>(p);
+    float4 b0[B], b1[B];
+    auto ld = [&](float4 (&b)[B], int k) {
+#pragma unroll
+        for (int u = 0; u < B; ++u) b[u] = p4[k * B + u];
+    };
+    auto add = [&](const float4 (&b)[B]) {
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+            a0 = a0 + b[u].x; a1 = a1 + b[u].x;
+            a0 = a0 + b[u].y; a1 = a1 + b[u].y;
+            a0 = a0 + b[u].z; a1 = a1 + b[u].z;
+            a0 = a0 + b[u].w; a1 = a1 + b[u].w;
+        }
+    };
+    if (nb > 0) {
+        ld(b0, 0);
+        ld(b1, min(1, nb - 1));
+        __builtin_amdgcn_sched_barrier(0);
+        int k = 0;
+        for (; k + 2 <= nb; k += 2) {
+            add(b0);
+            ld(b0, min(k + 2, nb - 1));
+            __builtin_amdgcn_sched_barrier(0);
+            add(b1);
+            ld(b1, min(k + 3, nb - 1));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (k < nb) add(b0);
+    }
+    for (int i = nb * 4 * B; i < n; ++i) {
+        a0 = a0 + p[i];
+        a1 = a1 + p[i];
+    }
+}
+
+// LDS floats of seq_sum_spec<NT>'s scratch (8-byte aligned).
+constexpr int seq_sum_spec_scratch(int nt) { return (nt / 64) * 128 + 2 * (nt / 64) + 4; }
+
+// init + p[0] + p[1] + ... + p[n-1], the sequential f32 fold in index order
+// (p in LDS, 16-byte aligned), bit-identical to lds_seq_sum, by all NT
+// threads of the workgroup (every thread calls it and gets the result) in
+// about 64/NT of its time.  Each of the NT/64 waves takes one contiguous
+// segment.  Segment 0 is folded from init.  Segment k > 0 is folded from 128
+// start values at once, two chains per lane: the f32 values within 64 steps
+// (one unit in the last place each) either side of f32(init + the exact
+// sum of the earlier segments, added in double).  The true start of segment
+// k is the fold's value at its first index, which differs from that
+// estimate only by the accumulated rounding, a few dozen units in the last
+// place on activation rows.  Then one thread chains the segments: when
+// segment k's true start (segment k-1's true end) is among its candidates,
+// bit for bit, that candidate's end is segment k's true end, by
+// determinism; otherwise (rows whose rounding drifts further, constant rows,
+// non-finite values) it folds segment k again from the true start.  The
+// result never depends on the estimates, only the time does.
+template <int NT>
+__device__ float seq_sum_spec(const float* p, int n, float init, float* sc) {
+    constexpr int S = NT / 64, C = 128;
+    const int tid = threadIdx.x, lane = tid & 63, k = tid >> 6;
+    float* ends = sc;                                      // [S][C] candidate ends
+    double* psum = reinterpret_cast<double*>(sc + S * C);  // [S] segment sums
+    float* res = sc + S * C + 2 * S;                       // [1] the result
+    if (n < 64 * S) {  // short: the plain chain
+        if (tid == 0) res[0] = lds_seq_sum(p, n, init);
+        __syncthreads();
+        const float r = res[0];
+        __syncthreads();
+        return r;
+    }
+    const int L = ((n + S - 1) / S + 3) & ~3;  // segment length, a multiple of 4
+    const int lo = k * L, hi = min(n, lo + L);
+    double ps = 0.0;
+    for (int i = lo + lane; i < hi; i += 64) ps += (double)p[i];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ps += __shfl_xor(ps, off, 64);
+    if (lane == 0) psum[k] = ps;
+    __syncthreads();
+    double pre = (double)init;
+    for (int kk = 0; kk < k; ++kk) pre += psum[kk];
+    const uint32_t eb = __float_as_uint((float)pre);
+    float c0 = k == 0 ? init : __uint_as_float(eb + (uint32_t)lane - (uint32_t)(C / 2));
+    float c1 = k == 0 ? init : __uint_as_float(eb + (uint32_t)lane + 64u - (uint32_t)(C / 2));
+    if (lo < hi) lds_seq_sum2(p + lo, hi - lo, c0, c1);
+    ends[k * C + lane] = c0;
+    ends[k * C + lane + 64] = c1;
+    __syncthreads();
+    if (tid == 0) {
+        float s = ends[0];
+        double pp = (double)init;
+        for (int kk = 1; kk < S; ++kk) {
+            pp += psum[kk - 1];
+            const int64_t d = (int64_t)__float_as_uint(s) - (int64_t)__float_as_uint((float)pp) + C / 2;
+            const int lo2 = kk * L, hi2 = min(n, lo2 + L);
+            if (d >= 0 && d < C) s = ends[kk * C + (int)d];
+            else if (lo2 < hi2) s = lds_seq_sum(p + lo2, hi2 - lo2, s);
+        }
+        res[0] = s;
+    }
+    __syncthreads();
+    const float r = res[0];
+    __syncthreads();  // the scratch may be reused by the caller
+    return r;
+}
+
 // ---- weights -------------------------------------------------------------
 struct Weight {
     int dtype = 0;           // FRQ_DT_*

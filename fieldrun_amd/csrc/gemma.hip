@@ -63,53 +63,75 @@ __global__ __launch_bounds__(GT) void gm_embed_kernel(const uint8_t* __restrict_
     for (int c = threadIdx.x; c < d; c += GT) x[(size_t)t * d + c] = h2f(row[c]) * escale;
 }
 
+// Threads of the norm kernel: eight waves, so the fold runs as eight
+// speculative segments (seq_sum_spec).
+constexpr int NORM_NT = 512;
+
 // One row's norm (gemma.rs:66-77) from LDS v (d values) into dst: ms = the
-// fold from -0.0 of v*v in index order / n (one lane, its LDS loads a batch
-// ahead), inv = 1 / sqrt(ms + eps), dst = v * inv * w.
+// fold from -0.0 of v*v in index order / n (seq_sum_spec: bit-identical to
+// the one-lane chain), inv = 1 / sqrt(ms + eps), dst = v * inv * w.
 __device__ void rms_row(const float* v, float* sq, const float* __restrict__ w, int d, float eps, float* dst,
-                        float* stat) {
-    for (int c = threadIdx.x; c < d; c += GT) sq[c] = v[c] * v[c];
+                        float* fsc) {
+    for (int c = threadIdx.x; c < d; c += NORM_NT) sq[c] = v[c] * v[c];
     __syncthreads();
-    if (threadIdx.x == 0) stat[0] = lds_seq_sum(sq, d, -0.0f) / (float)d;
-    __syncthreads();
-    const float inv = 1.0f / sqrtf(stat[0] + eps);
-    for (int c = threadIdx.x; c < d; c += GT) dst[c] = v[c] * inv * w[c];
+    const float ms = seq_sum_spec<NORM_NT>(sq, d, -0.0f, fsc) / (float)d;
+    const float inv = 1.0f / sqrtf(ms + eps);
+    for (int c = threadIdx.x; c < d; c += NORM_NT) dst[c] = v[c] * inv * w[c];
     __syncthreads();
 }
 
 // Row r = row0 + blockIdx.x.  y set: x += norm(y, wpost) (gemma's post-norm
 // before the residual) or, wpost NULL, x += y (rope.rs); then out =
-// norm(x, wnext).  LDS: three rows of d floats.
-__global__ __launch_bounds__(GT) void gm_norm_kernel(float* __restrict__ x, const float* __restrict__ y,
-                                                     const float* __restrict__ wpost, const float* __restrict__ wnext,
-                                                     float* __restrict__ out, int d, float eps, int row0) {
+// norm(x, wnext).  LDS: three rows of d floats (each 16-byte aligned) and
+// the fold's scratch.
+__host__ __device__ inline size_t gm_norm_lds(int d) {
+    return (3 * (size_t)((d + 3) & ~3) + seq_sum_spec_scratch(NORM_NT)) * sizeof(float);
+}
+__global__ __launch_bounds__(NORM_NT) void gm_norm_kernel(float* __restrict__ x, const float* __restrict__ y,
+                                                          const float* __restrict__ wpost,
+                                                          const float* __restrict__ wnext, float* __restrict__ out,
+                                                          int d, float eps, int row0) {
     extern __shared__ float4 lds4[];
+    const int dp = (d + 3) & ~3;
     float* v = reinterpret_cast<float*>(lds4);
-    float* sq = v + d;
-    float* t = sq + d;
-    __shared__ float stat[1];
+    float* sq = v + dp;
+    float* t = sq + dp;
+    float* fsc = t + dp;
     const size_t r = (size_t)(row0 + blockIdx.x) * d;
     if (y && wpost) {
-        for (int c = threadIdx.x; c < d; c += GT) v[c] = y[r + c];
+        for (int c = threadIdx.x; c < d; c += NORM_NT) v[c] = y[r + c];
         __syncthreads();
-        rms_row(v, sq, wpost, d, eps, t, stat);
-        for (int c = threadIdx.x; c < d; c += GT) {
+        rms_row(v, sq, wpost, d, eps, t, fsc);
+        for (int c = threadIdx.x; c < d; c += NORM_NT) {
             const float nx = x[r + c] + t[c];
             x[r + c] = nx;
             v[c] = nx;
         }
     } else if (y) {  // rope.rs: x = x + y, no post-norm
-        for (int c = threadIdx.x; c < d; c += GT) {
+        for (int c = threadIdx.x; c < d; c += NORM_NT) {
             const float nx = x[r + c] + y[r + c];
             x[r + c] = nx;
             v[c] = nx;
         }
     } else {
-        for (int c = threadIdx.x; c < d; c += GT) v[c] = x[r + c];
+        for (int c = threadIdx.x; c < d; c += NORM_NT) v[c] = x[r + c];
     }
     __syncthreads();
-    rms_row(v, sq, wnext, d, eps, t, stat);
-    for (int c = threadIdx.x; c < d; c += GT) out[r + c] = t[c];
+    rms_row(v, sq, wnext, d, eps, t, fsc);
+    for (int c = threadIdx.x; c < d; c += NORM_NT) out[r + c] = t[c];
+}
+
+// Checking hook of seq_sum_spec: out[r] = init + x[r][0] + ... + x[r][n-1],
+// the sequential f32 fold, one workgroup per row (the norm kernel's shape).
+__global__ __launch_bounds__(NORM_NT) void seq_fold_kernel(const float* __restrict__ x, int n, float init,
+                                                           float* __restrict__ out) {
+    extern __shared__ float4 lds4[];
+    float* v = reinterpret_cast<float*>(lds4);
+    float* fsc = v + ((n + 3) & ~3);
+    for (int c = threadIdx.x; c < n; c += NORM_NT) v[c] = x[(size_t)blockIdx.x * n + c];
+    __syncthreads();
+    const float r = seq_sum_spec<NORM_NT>(v, n, init, fsc);
+    if (threadIdx.x == 0) out[blockIdx.x] = r;
 }
 
 // rope (gemma.rs:79-94) on one head of hd values at absolute position pos,
@@ -287,14 +309,13 @@ __global__ __launch_bounds__(GT) void gm_attn_kernel(const float* __restrict__ q
     if (j0 > 0 || nk < klen) mx = fmaxf(mx, -1e30f);  // a masked entry joins the max
     for (int j = j0 + threadIdx.x; j < nk; j += GT) p[j] = libm::frq_expf(p[j] - mx);
     __syncthreads();
-    if (threadIdx.x == 0) {  // key order; the masked exps are +0 (j < j0 add nothing to +0)
-        const int ja = min((j0 + 3) & ~3, nk);  // p + ja 16-byte aligned for the batched chain
-        float sum = 0.0f;
-        for (int j = j0; j < ja; ++j) sum = sum + p[j];
-        red[0] = lds_seq_sum(p + ja, nk - ja, sum);
-    }
-    __syncthreads();
-    const float sum = red[0];
+    // the sum in key order (the masked exps are +0: j < j0 add nothing to
+    // +0): the keys before the next 16-byte boundary in every thread, the
+    // rest by the whole workgroup's speculative segmented fold
+    const int ja = min((j0 + 3) & ~3, nk);
+    float head = 0.0f;
+    for (int j = j0; j < ja; ++j) head = head + p[j];
+    const float sum = seq_sum_spec<GT>(p + ja, nk - ja, head, sv + pstride);
     for (int j = j0 + threadIdx.x; j < nk; j += GT) p[j] = p[j] / sum;
     __syncthreads();
     constexpr int B = 16;
@@ -647,16 +668,12 @@ __global__ __launch_bounds__(GT) void gm_dec_value_kernel(const float* __restric
     if (j0 > 0) mx = fmaxf(mx, -1e30f);  // a masked entry joins the max
     for (int j = j0 + threadIdx.x; j < nk; j += GT) p[j] = libm::frq_expf(p[j] - mx);
     __syncthreads();
-    if (threadIdx.x == 0) {
-        // key order from j0: the few keys before the next 16-byte boundary
-        // one at a time, the rest through the batched LDS chain
-        const int ja = min((j0 + 3) & ~3, nk);
-        float sum = 0.0f;
-        for (int j = j0; j < ja; ++j) sum = sum + p[j];
-        red[0] = lds_seq_sum(p + ja, nk - ja, sum);
-    }
-    __syncthreads();
-    const float sum = red[0];
+    // key order from j0: the few keys before the next 16-byte boundary in
+    // every thread, the rest by the workgroup's speculative segmented fold
+    const int ja = min((j0 + 3) & ~3, nk);
+    float head = 0.0f;
+    for (int j = j0; j < ja; ++j) head = head + p[j];
+    const float sum = seq_sum_spec<GT>(p + ja, nk - ja, head, sv + pstride);
     for (int j = j0 + threadIdx.x; j < nk; j += GT) p[j] = p[j] / sum;
     __syncthreads();
     // three batches of B keys in flight (48 loads a wave, within the 63 the
@@ -906,7 +923,7 @@ size_t gm_pstride(const frq_gemma* g) { return gm_pstride_n(g->cap_pos); }
 // two score rows of the padded position count); the long-cache value
 // kernel needs the two score rows only, so this bounds both.
 size_t gm_attn_lds_n(size_t hd, size_t npos) {
-    return (3 * ((hd + 3) & ~(size_t)3) + 2 * gm_pstride_n(npos)) * sizeof(float);
+    return (3 * ((hd + 3) & ~(size_t)3) + 2 * gm_pstride_n(npos) + seq_sum_spec_scratch(GT)) * sizeof(float);
 }
 size_t gm_attn_lds(const frq_gemma* g) { return gm_attn_lds_n(g->hd, g->cap_pos); }
 constexpr size_t GM_LDS_MAX = 160 * 1024;  // gfx950's LDS per workgroup
@@ -956,6 +973,10 @@ int gm_reserve(frq_ctx* c, frq_gemma* g, size_t npos, size_t rows) {
     GMCHK(hipStreamSynchronize(s), "hipStreamSynchronize");
     gm_drop_buffers(g);
     GMCHK(gm_allow_lds(need), "hipFuncSetAttribute");
+    if (gm_norm_lds((int)g->d) > 64 * 1024)
+        GMCHK(hipFuncSetAttribute((const void*)gm_norm_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)gm_norm_lds((int)g->d)),
+              "hipFuncSetAttribute(norm)");
     const size_t L = g->L, kvd = g->KV * g->hd, half = g->hd / 2;
     size_t off = 0;
     auto take = [&](size_t bytes) { const size_t o = off; off += round_up(bytes, 256); return o; };
@@ -1014,9 +1035,9 @@ int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_o
     hipStream_t s = (hipStream_t)frq_get_stream(c);
     const int d = (int)g->d, H = (int)g->H, KV = (int)g->KV, hd = (int)g->hd, ffn = (int)g->ffn;
     const Weight& et = *weight_of(g->embed);
-    const size_t nlds = 3 * g->d * sizeof(float);
+    const size_t nlds = gm_norm_lds(d);
     auto norm = [&](const float* y, const float* wpost, const float* wnext, int rows, int row0) {
-        gm_norm_kernel<<<dim3(rows), dim3(GT), nlds, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, row0);
+        gm_norm_kernel<<<dim3(rows), dim3(NORM_NT), nlds, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, row0);
         return hipGetLastError();
     };
     gm_embed_kernel<<<dim3((unsigned)m), dim3(GT), 0, s>>>(et.rowp, et.rpitch, d, g->escale, rel ? g->tok : g->ids,
@@ -1043,7 +1064,7 @@ int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_o
             const int hd4 = (hd + 3) & ~3;
             const size_t plds = (size_t)2 * hd4 * sizeof(float);
             const dim3 sg((unsigned)H, (unsigned)((g->cap_pos + GT - 1) / GT));
-            const size_t vlds = (size_t)2 * ps * sizeof(float);
+            const size_t vlds = ((size_t)2 * ps + seq_sum_spec_scratch(GT)) * sizeof(float);
             if (g->kv8) {
                 gm_dec_prep_kernel<true><<<dim3((unsigned)(H + KV)), dim3(GT), plds, s>>>(
                     g->qkvb, H, KV, hd, g->cur, g->cs, kc, vc, kq, vq, ks, vs, qb, qn, kn, g->eps, g->qr);
@@ -1358,6 +1379,31 @@ int frq_gemma_generate(frq_ctx* c, frq_gemma* g, const int64_t* prompt, size_t n
 
 int frq_gemma_predict(frq_ctx* c, frq_gemma* g, const int64_t* ids, size_t n, int64_t* token, float* logits) {
     return gm_run(c, g, ids, n, 1, token, logits);
+}
+
+int frq_seq_fold_f32(frq_ctx* c, const float* x, size_t rows, size_t n, float init, float* out) {
+    if (!c) return set_error(FRQ_ERR_ARG, "null context");
+    if (!rows) return FRQ_OK;
+    if ((!x && n) || !out) return set_error(FRQ_ERR_ARG, "null input / output");
+    const size_t lds = (((n + 3) & ~(size_t)3) + seq_sum_spec_scratch(NORM_NT)) * sizeof(float);
+    if (lds > GM_LDS_MAX || rows > 65535) return set_error(FRQ_ERR_ARG, "row too long for the fold's LDS");
+    GDev dv(ctx_device(c));
+    hipStream_t s = (hipStream_t)frq_get_stream(c);
+    float* dx = nullptr;
+    GMCHK(hipMalloc(&dx, (rows * n + rows) * sizeof(float)), "hipMalloc(fold)");
+    struct Free {
+        float* p;
+        ~Free() { (void)hipFree(p); }
+    } fr{dx};
+    if (lds > 64 * 1024)
+        GMCHK(hipFuncSetAttribute((const void*)seq_fold_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+              "hipFuncSetAttribute");
+    if (n) GMCHK(hipMemcpyAsync(dx, x, rows * n * sizeof(float), hipMemcpyHostToDevice, s), "hipMemcpyAsync");
+    seq_fold_kernel<<<dim3((unsigned)rows), dim3(NORM_NT), lds, s>>>(dx, (int)n, init, dx + rows * n);
+    GMCHK(hipGetLastError(), "launch fold");
+    GMCHK(hipMemcpyAsync(out, dx + rows * n, rows * sizeof(float), hipMemcpyDeviceToHost, s), "hipMemcpyAsync");
+    GMCHK(hipStreamSynchronize(s), "hipStreamSynchronize");
+    return FRQ_OK;
 }
 
 }  // extern "C"

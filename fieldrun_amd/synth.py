@@ -129,6 +129,27 @@ def write_qwen3moe_layer_bundle(stem: str, s: int, n_exp: int = 128, d: int = 20
     return m
 
 
+def _parallel(jobs, workers: int = 8):
+    """Run the zero-argument jobs on a thread pool, results in job order
+    (numpy's bulk generators release the GIL, so seeded chunks come out
+    several times faster; each job owns its generator, so the bytes do not
+    depend on the thread count or the scheduling)."""
+    from concurrent.futures import ThreadPoolExecutor
+    with ThreadPoolExecutor(workers) as ex:
+        return list(ex.map(lambda f: f(), jobs))
+
+
+def _f16_table_chunks(ss, rows: int, d: int, std: float):
+    """A (rows, d) table of N(0, std) values in f16, 8192-row chunks each
+    drawn from its own child of the seed sequence ss."""
+    def chunk(r0, child):
+        g = np.random.default_rng(child)
+        return (g.standard_normal((min(8192, rows - r0), d), dtype=np.float32) * np.float32(std)).astype(np.float16)
+    starts = list(range(0, rows, 8192))
+    kids = ss.spawn(len(starts))
+    return np.concatenate(_parallel([lambda r0=r0, c=c: chunk(r0, c) for r0, c in zip(starts, kids)]))
+
+
 def write_gemma2_bundle(stem: str, s: int, n_layer: int = 26, n_head: int = 8, n_kv: int = 4, hd: int = 256,
                         d: int = 2304, ffn: int = 9216, vocab: int = 256000, std: float = 0.02,
                         dtype: str = "int4", norm_std: float = 0.0, raw: bool = False) -> dict:
@@ -147,34 +168,38 @@ def write_gemma2_bundle(stem: str, s: int, n_layer: int = 26, n_head: int = 8, n
     gain = lambda: (np.float32(1.0) + rng.standard_normal(d, dtype=np.float32) * np.float32(norm_std)
                     if norm_std else np.ones(d, np.float32))
     w = BundleWriter(stem)
+    ss = np.random.SeedSequence([s, 2])  # the raw tensors' streams (one child per chunk / matrix)
     if raw:  # the f16 embed in row chunks (no full-size f32 temporary)
-        rows = []
-        for r0 in range(0, vocab, 8192):
-            rows.append(nrm(min(8192, vocab - r0), d).astype(np.float16))
-        emb = np.concatenate(rows)
+        emb = _f16_table_chunks(ss, vocab, d, std)
         nb = w._write(np.ascontiguousarray(emb.view(np.uint16)))
         w.entry("embed", "f16", emb.shape, nb)
-        del emb, rows
+        del emb
     else:
         w.put_embed("embed", nrm(vocab, d), "f16", dtype)
     w.put_small("norm", gain(), None, dtype)
     shapes = {"self_attn.q_proj": (n_head * hd, d), "self_attn.k_proj": (n_kv * hd, d),
               "self_attn.v_proj": (n_kv * hd, d), "self_attn.o_proj": (d, n_head * hd),
               "mlp.gate_proj": (ffn, d), "mlp.up_proj": (ffn, d), "mlp.down_proj": (d, ffn)}
+    def nibbles(o, i, child, g=32):  # seeded random nibbles and f16 group scales, as stored
+        r = np.random.default_rng(child)
+        packed = r.integers(0, 256, (o, (i + 1) // 2), dtype=np.uint8)
+        return packed, r.uniform(0.5, 1.0, (o, (i + g - 1) // g)).astype(np.float32) * np.float32(std / 2.5)
+
     for l in range(n_layer):
         for nm in ("input_layernorm", "post_attention_layernorm", "pre_feedforward_layernorm",
                    "post_feedforward_layernorm"):
             w.put_small(f"l{l}.{nm}", gain(), None, dtype)
-        for proj, (o, i) in shapes.items():
-            if raw:  # seeded random nibbles and f16 group scales, written as stored
-                g = 32
-                packed = rng.integers(0, 256, (o, (i + 1) // 2), dtype=np.uint8)
-                s16 = rng.uniform(0.5, 1.0, (o, (i + g - 1) // g)).astype(np.float32) * np.float32(std / 2.5)
+        if raw:
+            kids = ss.spawn(len(shapes))
+            mats = _parallel([lambda o=o, i=i, c=c: nibbles(o, i, c) for (o, i), c in zip(shapes.values(), kids)])
+            for (proj, (o, i)), (packed, s16) in zip(shapes.items(), mats):
                 nb = w._write(np.ascontiguousarray(packed))
-                w.entry(f"l{l}.{proj}", "i4", (o, i), nb, group=g)
+                w.entry(f"l{l}.{proj}", "i4", (o, i), nb, group=32)
                 w.put_f16(f"l{l}.{proj}__scale", s16)
-            else:
-                w.put_lin(f"l{l}.{proj}", nrm(o, i), dtype)
+            del mats
+            continue
+        for proj, (o, i) in shapes.items():
+            w.put_lin(f"l{l}.{proj}", nrm(o, i), dtype)
     m = manifest("gemma", [n_layer, n_head, n_kv, hd, d, ffn, vocab, 1],
                  [10000.0, 1e-6, 50.0, 30.0, float(hd), float(np.sqrt(d))])
     w.finish(m)
@@ -198,12 +223,17 @@ def write_rope_bundle(stem: str, s: int, n_layer: int = 28, n_head: int = 28, n_
     gain = lambda n: (np.float32(1.0) + rng.standard_normal(n, dtype=np.float32) * np.float32(norm_std)
                       if norm_std else np.ones(n, np.float32))
     w = BundleWriter(stem)
+    ss = np.random.SeedSequence([s, 4])  # the large tensors' streams (one child per chunk / matrix)
 
     def table(name):
-        rows = [nrm(min(8192, vocab - r0), d).astype(np.float16) for r0 in range(0, vocab, 8192)]
-        t = np.concatenate(rows)
+        t = _f16_table_chunks(ss, vocab, d, std)
         nb = w._write(np.ascontiguousarray(t.view(np.uint16)))
         w.entry(name, "f16", t.shape, nb)
+
+    def raw_i8(o, i, child):  # seeded random bytes (in, out) and f16 per-column scales, as stored
+        r = np.random.default_rng(child)
+        return (r.integers(-127, 128, (i, o), dtype=np.int8),
+                r.uniform(0.5, 1.0, o).astype(np.float32) * np.float32(std / 40))
 
     table("embed")
     w.put_small("norm", gain(d), None, dtype)
@@ -215,13 +245,16 @@ def write_rope_bundle(stem: str, s: int, n_layer: int = 28, n_head: int = 28, n_
     for l in range(n_layer):
         w.put_small(f"l{l}.in_ln", gain(d), None, dtype)
         w.put_small(f"l{l}.post_ln", gain(d), None, dtype)
-        for proj, (o, i) in shapes.items():
-            if raw and dtype == "int8":
-                q = rng.integers(-127, 128, (i, o), dtype=np.int8)
+        if raw and dtype == "int8":
+            kids = ss.spawn(len(shapes))
+            mats = _parallel([lambda o=o, i=i, c=c: raw_i8(o, i, c) for (o, i), c in zip(shapes.values(), kids)])
+            for (proj, (o, i)), (q, sc) in zip(shapes.items(), mats):
                 nb = w._write(np.ascontiguousarray(q))
                 w.entry(f"l{l}.{proj}", "i8", (i, o), nb)
-                w.put_f16(f"l{l}.{proj}__scale", rng.uniform(0.5, 1.0, o).astype(np.float32) * np.float32(std / 40))
-            else:
+                w.put_f16(f"l{l}.{proj}__scale", sc)
+            del mats
+        else:
+            for proj, (o, i) in shapes.items():
                 w.put_lin(f"l{l}.{proj}", nrm(o, i), dtype)
         if qkv_bias:
             for proj in ("q_proj", "k_proj", "v_proj"):

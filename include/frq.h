@@ -311,6 +311,12 @@ int frq_rope_load(frq_ctx* ctx, const frq_bundle* b, int kv_int8, frq_gemma** ou
  * (glibc's expf and fdlibm's expm1f / tanhf): out[i] = f(x[i]) for n host
  * values, on ctx's device, or on the host when ctx is NULL. */
 int frq_libm_f32(frq_ctx* ctx, int fn, const float* x, size_t n, float* out);
+/* Checking hook of the decode kernels' sequential fold (RMSNorm mean
+ * squares, softmax sums; the Rust iterator sum, a fold in index order):
+ * out[r] = init + x[r][0] + ... + x[r][n-1] in f32, computed on ctx's
+ * device by the speculative segmented fold the kernels use.  x is (rows, n)
+ * row-major on the host. */
+int frq_seq_fold_f32(frq_ctx* ctx, const float* x, size_t rows, size_t n, float init, float* out);
 
 #ifdef __cplusplus
 }

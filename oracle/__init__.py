@@ -41,6 +41,8 @@ def _load():
         "fro_quant_row": (I, [P, S, P, P, P, P, P]),
         "fro_mm_i8": (I, [P, S, S, P, P, S, P, P]),
         "fro_mm_i8_mt": (I, [P, S, S, P, P, S, P, I]),
+        "fro_i8dot_avx512bw": (C.c_int32, [P, P, S]),
+        "fro_set_i8dot": (I, [I]),
         "fro_i4_dot": (F, [P, P, P, S, S]),
         "fro_i4_dot_avx2": (F, [P, P, P, S, S]),
         "fro_mm_i4": (I, [P, S, S, P, P, S, S, P]),
@@ -175,6 +177,18 @@ def mm_i8(a: np.ndarray, wt_nk: np.ndarray, scale: np.ndarray, with_acc: bool = 
     if rc:
         raise OracleNaN("NaN activation")
     return (out, acc) if with_acc else out
+
+
+def set_i8dot(variant: str) -> bool:
+    """The i8 dot of the oracle's int8 linears: "scalar" (the reference's
+    `_scalar_i8_bench` build; default) or "avx512bw" (i8dot_avx512bw, the
+    production x86 dispatch).  False when the host lacks AVX-512BW."""
+    return bool(lib.fro_set_i8dot({"scalar": 0, "avx512bw": 1}[variant]))
+
+
+def i8dot_avx512bw(a: np.ndarray, w: np.ndarray) -> int:
+    a, w = _c(a, np.int8), _c(w, np.int8)
+    return int(lib.fro_i8dot_avx512bw(_p(a), _p(w), a.size))
 
 
 def mm_i8_mt(a, wt_nk, scale, nthreads: int):

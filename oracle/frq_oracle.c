@@ -13,6 +13,7 @@
  */
 #include "frq_oracle.h"
 
+#include <immintrin.h>
 #include <math.h>
 #include <pthread.h>
 #include <stdlib.h>
@@ -163,6 +164,42 @@ int32_t fro_i8dot(const int8_t* a, const int8_t* w, size_t n) {
     return s;
 }
 
+/* i8dot_avx512bw: src/bundle.rs:1107-1126, the dot the production x86 build
+ * dispatches to when the host has avx512bw + avx512f (1044-1047): 32 lanes
+ * a step (sign-extend to i16, madd to 16 i32 pairwise sums, add), a
+ * horizontal add of the 16 lanes, then the scalar tail.  Integer and
+ * overflow-free at these lengths, so it equals fro_i8dot (the reference's
+ * own test, 1359-1382).  Used for the CPU baseline's second figure. */
+__attribute__((target("avx512bw,avx512f")))
+int32_t fro_i8dot_avx512bw(const int8_t* a, const int8_t* w, size_t n) {
+    const size_t chunks = n / 32;
+    __m512i acc = _mm512_setzero_si512();
+    for (size_t c = 0; c < chunks; c++) {
+        const __m256i av = _mm256_loadu_si256((const __m256i*)(a + c * 32));
+        const __m256i wv = _mm256_loadu_si256((const __m256i*)(w + c * 32));
+        acc = _mm512_add_epi32(acc, _mm512_madd_epi16(_mm512_cvtepi8_epi16(av), _mm512_cvtepi8_epi16(wv)));
+    }
+    int32_t s = _mm512_reduce_add_epi32(acc);
+    for (size_t k = chunks * 32; k < n; k++) s += (int32_t)a[k] * (int32_t)w[k];
+    return s;
+}
+
+/* The dot the int8 linears below use: the scalar fallback (the
+ * `_scalar_i8_bench` build, the default here) or, after
+ * fro_set_i8dot(1) on a host with AVX-512BW, i8dot_avx512bw. */
+static int32_t (*g_i8dot)(const int8_t*, const int8_t*, size_t) = fro_i8dot;
+
+int fro_set_i8dot(int variant) {
+    if (variant == 1) {
+        __builtin_cpu_init();
+        if (!__builtin_cpu_supports("avx512bw") || !__builtin_cpu_supports("avx512f")) return 0;
+        g_i8dot = fro_i8dot_avx512bw;
+        return 1;
+    }
+    g_i8dot = fro_i8dot;
+    return 1;
+}
+
 /* Rust `f as i32` saturates and maps NaN to 0. */
 static int32_t sat_i32(float v) {
     if (v != v) return 0;
@@ -252,7 +289,7 @@ static void i8_row(const float* arow, size_t k, const int8_t* wt,
                    float* orow, int32_t* accrow) {
     for (size_t j = j0; j < j1; j++) {
         const int8_t* w = wt + j * k;
-        int32_t acc = fro_i8dot(a8, w, k);
+        int32_t acc = g_i8dot(a8, w, k);
         float corr = -0.0f;
         for (size_t o = 0; o < t; o++) corr = corr + oval[o] * (float)w[oidx[o]];
         orow[j] = scale[j] * (sa * (float)acc + corr);

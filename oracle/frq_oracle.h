@@ -85,6 +85,12 @@ void fro_i8_transpose(const int8_t* w_kn, size_t k, size_t n, int8_t* wt_nk);
 
 /* i8dot: scalar i8 x i8 -> i32. */
 int32_t fro_i8dot(const int8_t* a, const int8_t* w, size_t n);
+/* i8dot_avx512bw (src/bundle.rs:1107-1126); needs a host with AVX-512BW. */
+int32_t fro_i8dot_avx512bw(const int8_t* a, const int8_t* w, size_t n);
+/* The dot of the int8 linears: 0 the scalar fallback (default), 1
+ * i8dot_avx512bw.  Returns 0 (and changes nothing) when the host lacks
+ * AVX-512BW.  Integer results are the same either way; only speed differs. */
+int fro_set_i8dot(int variant);
 
 /* Outlier-aware activation quant of ONE row.  Writes a8[k], *sa, the t
  * outliers (oidx, oval) in ascending channel order and *t = min(32,k).

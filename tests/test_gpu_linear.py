@@ -141,8 +141,8 @@ def test_i8_bundle_upload_matches_transposed(ctx):
 
 @pytest.mark.parametrize("k,n", synth.SWEEP_KN)
 def test_i8_sweep_full_shapes(ctx, k, n):
-    """configs[1] shapes at full size: M=1 fully against the oracle, M=128
-    and M=2048 on sampled rows (rows are independent)."""
+    """configs[1] shapes at full size: M=1, 4 and 16 fully against the
+    oracle, M=128 and M=2048 on sampled rows (rows are independent)."""
     a, wt, scale = case(2048, k, n, synth.seed(1))
     w = ctx.upload_i8(wt, scale)
     out1, acc1, *_ = w.mm_debug(a[:1])
@@ -156,6 +156,11 @@ def test_i8_sweep_full_shapes(ctx, k, n):
         assert np.array_equal(acc[r], racc)
         mag = corr_mag(a[r], wt, scale, racc)
         assert np.all(np.abs(out[r].astype(np.float64) - ref) <= 1e-6 * mag + 1e-30)
+    # the decode batches (M = 4 and 16): every row bit-exact (the multi-row
+    # MFMA path keeps the reference's epilogue order)
+    for m in (4, 16):
+        ref = oracle.mm_i8_mt(a[:m], wt, scale, 16)
+        assert np.array_equal(w.mm(a[:m]).view(np.uint32), ref.view(np.uint32)), m
 
 
 # ------------------------------------------------------------------ int4 ----

@@ -144,6 +144,40 @@ def test_i8dot_kats():
     assert oracle.i8dot(a, w) == 127 * -128 * 4864
 
 
+def test_i8dot_avx512bw_equals_scalar():
+    """i8dot_avx512bw (src/bundle.rs:1107-1126) against the scalar dot on the
+    reference test's xorshift vectors and lengths (1359-1382), the worst
+    case, and random lengths around the 32-lane step; and the int8 linear
+    gives the same bits with either dot."""
+    if not oracle.set_i8dot("avx512bw"):
+        pytest.skip("host without AVX-512BW")
+    oracle.set_i8dot("scalar")
+    k = KATS["i8dot_simd_vs_scalar"]
+    state = int(k["xorshift_seed"], 16)
+    for n in k["lengths"]:
+        vals, state = xorshift_i8(state, 2 * n)
+        a, w = np.array(vals[:n], np.int8), np.array(vals[n:], np.int8)
+        assert oracle.i8dot_avx512bw(a, w) == oracle.i8dot(a, w), n
+    wc = k["worst_case"]
+    a, w = np.full(wc["len"], wc["a"], np.int8), np.full(wc["len"], wc["w"], np.int8)
+    assert oracle.i8dot_avx512bw(a, w) == 127 * -128 * 4864
+    rng = np.random.default_rng(12)
+    for n in (0, 1, 31, 32, 33, 63, 64, 65, 4095, 18944):
+        a = rng.integers(-128, 128, n, dtype=np.int8)
+        w = rng.integers(-128, 128, n, dtype=np.int8)
+        assert oracle.i8dot_avx512bw(a, w) == int(np.dot(a.astype(np.int64), w.astype(np.int64))), n
+    x = (rng.standard_normal((3, 896)) * np.where(rng.random(896) < 0.01, 20.0, 1.0)).astype(np.float32)
+    wt = rng.integers(-127, 128, (300, 896), dtype=np.int8)
+    sc = rng.uniform(1e-4, 3e-4, 300).astype(np.float32)
+    ref = oracle.mm_i8_mt(x, wt, sc, 3)
+    try:
+        assert oracle.set_i8dot("avx512bw")
+        got = oracle.mm_i8_mt(x, wt, sc, 3)
+    finally:
+        oracle.set_i8dot("scalar")
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
 def test_i8_transpose():
     rng = np.random.default_rng(4)
     w = rng.integers(-127, 128, (13, 29), dtype=np.int8)
