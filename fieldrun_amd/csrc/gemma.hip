@@ -27,6 +27,7 @@
 // path, in chunks).
 #include "frq_internal.h"
 #include "libm_f32.h"
+#include "quant_core.h"
 
 #include <algorithm>
 #include <cmath>
@@ -70,13 +71,14 @@ constexpr int NORM_NT = 512;
 // One row's norm (gemma.rs:66-77) from LDS v (d values) into dst: ms = the
 // fold from -0.0 of v*v in index order / n (seq_sum_spec: bit-identical to
 // the one-lane chain), inv = 1 / sqrt(ms + eps), dst = v * inv * w.
+template <int NT>
 __device__ void rms_row(const float* v, float* sq, const float* __restrict__ w, int d, float eps, float* dst,
                         float* fsc) {
-    for (int c = threadIdx.x; c < d; c += NORM_NT) sq[c] = v[c] * v[c];
+    for (int c = threadIdx.x; c < d; c += NT) sq[c] = v[c] * v[c];
     __syncthreads();
-    const float ms = seq_sum_spec<NORM_NT>(sq, d, -0.0f, fsc) / (float)d;
+    const float ms = seq_sum_spec<NT>(sq, d, -0.0f, fsc) / (float)d;
     const float inv = 1.0f / sqrtf(ms + eps);
-    for (int c = threadIdx.x; c < d; c += NORM_NT) dst[c] = v[c] * inv * w[c];
+    for (int c = threadIdx.x; c < d; c += NT) dst[c] = v[c] * inv * w[c];
     __syncthreads();
 }
 
@@ -84,41 +86,199 @@ __device__ void rms_row(const float* v, float* sq, const float* __restrict__ w, 
 // before the residual) or, wpost NULL, x += y (rope.rs); then out =
 // norm(x, wnext).  LDS: three rows of d floats (each 16-byte aligned) and
 // the fold's scratch.
-__host__ __device__ inline size_t gm_norm_lds(int d) {
-    return (3 * (size_t)((d + 3) & ~3) + seq_sum_spec_scratch(NORM_NT)) * sizeof(float);
+template <int NT>
+__host__ __device__ inline size_t gm_norm_lds_t(int d) {
+    return (3 * (size_t)((d + 3) & ~3) + seq_sum_spec_scratch(NT)) * sizeof(float);
 }
-__global__ __launch_bounds__(NORM_NT) void gm_norm_kernel(float* __restrict__ x, const float* __restrict__ y,
-                                                          const float* __restrict__ wpost,
-                                                          const float* __restrict__ wnext, float* __restrict__ out,
-                                                          int d, float eps, int row0) {
-    extern __shared__ float4 lds4[];
+__host__ __device__ inline size_t gm_norm_lds(int d) { return gm_norm_lds_t<NORM_NT>(d); }
+
+// The norm kernel's body for NT threads; the normalised row is left in LDS
+// (returned) as well as written to out.
+template <int NT>
+__device__ float* gm_norm_body(float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ wpost,
+                               const float* __restrict__ wnext, float* __restrict__ out, int d, float eps,
+                               size_t r, float* lds) {
     const int dp = (d + 3) & ~3;
-    float* v = reinterpret_cast<float*>(lds4);
+    float* v = lds;
     float* sq = v + dp;
     float* t = sq + dp;
     float* fsc = t + dp;
-    const size_t r = (size_t)(row0 + blockIdx.x) * d;
     if (y && wpost) {
-        for (int c = threadIdx.x; c < d; c += NORM_NT) v[c] = y[r + c];
+        for (int c = threadIdx.x; c < d; c += NT) v[c] = y[r + c];
         __syncthreads();
-        rms_row(v, sq, wpost, d, eps, t, fsc);
-        for (int c = threadIdx.x; c < d; c += NORM_NT) {
+        rms_row<NT>(v, sq, wpost, d, eps, t, fsc);
+        for (int c = threadIdx.x; c < d; c += NT) {
             const float nx = x[r + c] + t[c];
             x[r + c] = nx;
             v[c] = nx;
         }
     } else if (y) {  // rope.rs: x = x + y, no post-norm
-        for (int c = threadIdx.x; c < d; c += NORM_NT) {
+        for (int c = threadIdx.x; c < d; c += NT) {
             const float nx = x[r + c] + y[r + c];
             x[r + c] = nx;
             v[c] = nx;
         }
     } else {
-        for (int c = threadIdx.x; c < d; c += NORM_NT) v[c] = x[r + c];
+        for (int c = threadIdx.x; c < d; c += NT) v[c] = x[r + c];
     }
     __syncthreads();
-    rms_row(v, sq, wnext, d, eps, t, fsc);
-    for (int c = threadIdx.x; c < d; c += NORM_NT) out[r + c] = t[c];
+    rms_row<NT>(v, sq, wnext, d, eps, t, fsc);
+    for (int c = threadIdx.x; c < d; c += NT) out[r + c] = t[c];
+    return t;
+}
+
+__global__ __launch_bounds__(NORM_NT) void gm_norm_kernel(float* __restrict__ x, const float* __restrict__ y,
+                                                          const float* __restrict__ wpost,
+                                                          const float* __restrict__ wnext, float* __restrict__ out,
+                                                          int d, float eps, int row0) {
+    extern __shared__ float4 lds4[];
+    gm_norm_body<NORM_NT>(x, y, wpost, wnext, out, d, eps, (size_t)(row0 + blockIdx.x) * d,
+                          reinterpret_cast<float*>(lds4));
+}
+
+// The norm kernel with the row in registers: float4 q = tid + NORM_NT i of
+// the row (d % 4 == 0, d <= 4 NORM_NT NV); every global load (y, x and both
+// gains) is issued up front, the squares go to LDS for the fold.  The
+// arithmetic is gm_norm_body's, operation for operation.  LDS: d floats and
+// the fold's scratch.
+__host__ __device__ inline size_t gm_norm2_lds(int d) {
+    return ((size_t)((d + 3) & ~3) + seq_sum_spec_scratch(NORM_NT)) * sizeof(float);
+}
+template <int NV>
+__global__ __launch_bounds__(NORM_NT) void gm_norm2_kernel(float* __restrict__ x, const float* __restrict__ y,
+                                                           const float* __restrict__ wpost,
+                                                           const float* __restrict__ wnext, float* __restrict__ out,
+                                                           int d, float eps, int row0) {
+    extern __shared__ float4 lds4[];
+    float4* sq4 = lds4;
+    float* sq = reinterpret_cast<float*>(lds4);
+    float* fsc = sq + ((d + 3) & ~3);
+    const int tid = threadIdx.x, d4 = d >> 2;
+    const size_t r = (size_t)(row0 + blockIdx.x) * d;
+    const float4* x4 = reinterpret_cast<const float4*>(x + r);
+    const float4* y4 = y ? reinterpret_cast<const float4*>(y + r) : nullptr;
+    const float4* wp4 = reinterpret_cast<const float4*>(wpost);
+    const float4* wn4 = reinterpret_cast<const float4*>(wnext);
+    float4 xv[NV], yv[NV], wpv[NV], wnv[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int q = min(tid + NORM_NT * i, d4 - 1);  // clamped: unconditional loads
+        xv[i] = x4[q];
+        wnv[i] = wn4[q];
+        if (y) yv[i] = y4[q];
+        if (y && wpost) wpv[i] = wp4[q];
+    }
+    auto valid = [&](int i) { return tid + NORM_NT * i < d4; };
+    auto mul = [](float4 a, float4 b) { return make_float4(a.x * b.x, a.y * b.y, a.z * b.z, a.w * b.w); };
+    auto scl = [](float4 a, float s) { return make_float4(a.x * s, a.y * s, a.z * s, a.w * s); };
+    auto add = [](float4 a, float4 b) { return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w); };
+    // inv = 1 / sqrt(the fold of v*v / d + eps) of the row held in v
+    auto inv_of = [&](const float4 (&v)[NV]) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
+            if (valid(i)) sq4[tid + NORM_NT * i] = mul(v[i], v[i]);
+        __syncthreads();
+        const float ms = seq_sum_spec<NORM_NT>(sq, d, -0.0f, fsc) / (float)d;
+        return 1.0f / sqrtf(ms + eps);
+    };
+    float4 nv[NV];
+    if (y && wpost) {  // gemma: x += norm(y, wpost)
+        const float iy = inv_of(yv);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) nv[i] = add(xv[i], mul(scl(yv[i], iy), wpv[i]));
+    } else if (y) {  // rope.rs: x = x + y
+#pragma unroll
+        for (int i = 0; i < NV; ++i) nv[i] = add(xv[i], yv[i]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) nv[i] = xv[i];
+    }
+    if (y) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
+            if (valid(i)) reinterpret_cast<float4*>(x + r)[tid + NORM_NT * i] = nv[i];
+    }
+    const float inv = inv_of(nv);
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+        if (valid(i)) reinterpret_cast<float4*>(out + r)[tid + NORM_NT * i] = mul(scl(nv[i], inv), wnv[i]);
+}
+
+// ---- the int8 decode linears' activation quant, fused into the kernel that
+// produces the row (the norm before q|k|v and gate|up, the activation before
+// down), so the linear that follows streams its weights with no quant of
+// its own (frq_mm_i8_q_dev).  The quant is quant_core.h's, by 16 waves:
+// the same bytes as the standalone quant and the fused M == 1 linear.
+constexpr int QNT = 1024;
+constexpr int FRQ_QMAXK = 4 * QNT * 5;  // K of the fused quant (NV4 <= 5)
+
+struct Q8 {  // one quantised activation row as frq_mm_i8_q_dev takes it
+    int8_t* a8;    // kp bytes, channels past K zero
+    float* sa;
+    uint32_t* oi;  // the 32 outliers, ascending channel
+    float* ov;
+    int kp;
+};
+
+// The row (K floats of LDS, 16-byte aligned, K % 4 == 0, 32 < K <= 4096 NV4)
+// quantised into q by the QNT threads; a NaN row sets *err and writes the
+// standalone quant's placeholders.
+template <int NV4>
+__device__ void quant_lds_row(const float* row, int K, const Q8& q, int* err) {
+    __shared__ qc::RowLdsT<QNT> L;
+    __shared__ unsigned long long cand[qc::FCAP];
+    __shared__ uint32_t bitmap[FRQ_QMAXK / 32];
+    const int tid = threadIdx.x, K4 = K >> 2;
+    float4 v[NV4];
+#pragma unroll
+    for (int i = 0; i < NV4; ++i) v[i] = reinterpret_cast<const float4*>(row)[min(tid + QNT * i, K4 - 1)];
+    const qc::RowSel sel = qc::row_select<NV4, QNT>(row, K, v, L, cand, bitmap, (q.kp + 31) / 32);
+    uint32_t* a8w = reinterpret_cast<uint32_t*>(q.a8);
+    if (sel.nan) {  // the reference panics here; the call reports FRQ_ERR_NAN
+        if (tid == 0) atomicOr(err, 1);
+        for (int i4 = tid; i4 < K4; i4 += QNT) a8w[i4] = 0u;
+    } else {
+        qc::row_quantize<NV4, QNT>(v, K4, bitmap, sel.sa, sel.fast, [&](int i4, uint32_t w) { a8w[i4] = w; });
+    }
+    for (int i4 = K4 + tid; i4 < q.kp / 4; i4 += QNT) a8w[i4] = 0u;
+    if (tid < FRQ_T) {
+        q.oi[tid] = L.sel_i[tid];
+        q.ov[tid] = L.sel_v[tid];
+    }
+    if (tid == 0) *q.sa = sel.sa;
+}
+
+// gm_norm_kernel for one decode row, the normalised row also quantised.
+template <int NV4>
+__global__ __launch_bounds__(QNT) void gm_norm_quant_kernel(float* __restrict__ x, const float* __restrict__ y,
+                                                            const float* __restrict__ wpost,
+                                                            const float* __restrict__ wnext,
+                                                            float* __restrict__ out, int d, float eps, int row0,
+                                                            Q8 q, int* __restrict__ err) {
+    extern __shared__ float4 lds4[];
+    const float* t = gm_norm_body<QNT>(x, y, wpost, wnext, out, d, eps, (size_t)(row0 + blockIdx.x) * d,
+                                       reinterpret_cast<float*>(lds4));
+    quant_lds_row<NV4>(t, d, q, err);
+}
+
+// The down linear's input for one decode row, act(gate) * up as
+// gm_geglu_kernel computes it (also written to hm), quantised.
+template <int NV4>
+__global__ __launch_bounds__(QNT) void gm_act_quant_kernel(const float* __restrict__ gu, int ffn, float c,
+                                                           float* __restrict__ hm, int silu, Q8 q,
+                                                           int* __restrict__ err) {
+    extern __shared__ float4 lds4[];
+    float* h = reinterpret_cast<float*>(lds4);
+    for (int i = threadIdx.x; i < ffn; i += QNT) {
+        const float xv = gu[i];
+        const float a = silu ? xv / (1.0f + libm::frq_expf(-xv))
+                             : 0.5f * xv * (1.0f + libm::frq_tanhf(c * (xv + 0.044715f * xv * xv * xv)));
+        const float hv = a * gu[ffn + i];
+        h[i] = hv;
+        hm[i] = hv;
+    }
+    __syncthreads();
+    quant_lds_row<NV4>(h, ffn, q, err);
 }
 
 // Checking hook of seq_sum_spec: out[r] = init + x[r][0] + ... + x[r][n-1],
@@ -724,6 +884,144 @@ __global__ __launch_bounds__(GT) void gm_dec_value_kernel(const float* __restric
     }
 }
 
+// ---- long-cache decode value chains through an LDS ring --------------------
+// gm_dec_value_kernel's work for CW = RB / es channels of one head per
+// workgroup (es the cache element size): the softmax as there, then every
+// channel's chain acc = fma(p[j], v[j][c], acc) in key order by wave 0,
+// with the value rows streamed into a ring of NB chunks of 16 KB by all
+// four waves' direct-to-LDS loads (global_load_lds, 16 loads a chunk, 4 a
+// wave): the first chunks are in flight during the softmax, and each
+// chunk's loads NB - 2 chunks ahead of the chain, which then reads LDS
+// rather than waiting on memory.  Per output the order is unchanged, so the
+// values are gm_dec_value_kernel's bit for bit.
+constexpr int VR_NB = 4, VR_CHUNK = 16384;
+
+typedef __attribute__((address_space(1))) void gm_gvoid_t;
+typedef __attribute__((address_space(3))) void gm_lvoid_t;
+__device__ __forceinline__ void gm_dma16(const void* g, void* lds_base) {
+    __builtin_amdgcn_global_load_lds((gm_gvoid_t*)g, (gm_lvoid_t*)lds_base, 16, 0, 0);
+}
+// s_waitcnt vmcnt(N) (gfx9 encoding; expcnt / lgkmcnt not waited on)
+template <int N>
+__device__ __forceinline__ void gm_wait_vm() {
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
+}
+
+template <bool KV8, int RB>
+__global__ __launch_bounds__(GT) void gm_dec_value_ring_kernel(const float* __restrict__ sc, int H, int KV, int hd,
+                                                               const int* __restrict__ curp,
+                                                               const float* __restrict__ vc,
+                                                               const int8_t* __restrict__ vq,
+                                                               const float* __restrict__ vs, int sliding, int window,
+                                                               int pstride, float* __restrict__ att) {
+    constexpr int ES = KV8 ? 1 : 4, CW = RB / ES, CK = VR_CHUNK / RB, KPI = 1024 / RB, PW = VR_CHUNK / 1024 / 4;
+    static_assert(PW == 4 && CK % 16 == 0, "four loads a wave a chunk; whole batches of 16 keys");
+    extern __shared__ float4 lds4[];
+    // p and sv hold key j at index j - j0, so a chunk's keys start 16-byte aligned
+    float* p = reinterpret_cast<float*>(lds4);
+    float* sv = p + pstride;
+    float* fsc = sv + pstride;
+    char* ring = reinterpret_cast<char*>(fsc + seq_sum_spec_scratch(GT));
+    __shared__ float red[4];
+    const int h = blockIdx.x, kv = h / (H / KV), kvd = KV * hd, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int ab = *curp, nk = ab + 1, j0 = (sliding && ab >= window) ? ab - window + 1 : 0;
+    const int n = nk - j0, nch = (n + CK - 1) / CK;
+    const int col0 = kv * hd + (int)blockIdx.y * CW;
+    const char* vbase = KV8 ? reinterpret_cast<const char*>(vq) : reinterpret_cast<const char*>(vc);
+    // this lane's 16 bytes of load i of chunk s: key j0 + s CK + i KPI + lane / (RB / 16), clamped
+    auto issue = [&](int s) {
+        char* st = ring + (s % VR_NB) * VR_CHUNK;
+#pragma unroll
+        for (int u = 0; u < PW; ++u) {
+            const int i = wave * PW + u;
+            const int key = min(j0 + s * CK + i * KPI + lane / (RB / 16), nk - 1);
+            const char* src = vbase + ((size_t)key * kvd + col0) * ES + (lane % (RB / 16)) * 16;
+            gm_dma16(src, st + i * 1024);
+        }
+    };
+#pragma unroll
+    for (int s = 0; s < VR_NB - 1; ++s)
+        if (s < nch) issue(s);
+    // the softmax, as gm_dec_value_kernel (the key-order sum from +0 over
+    // the keys j0 .. nk - 1)
+    float mx = -INFINITY;
+    for (int j = threadIdx.x; j < n; j += GT) {
+        const float v = sc[(size_t)h * pstride + j0 + j];
+        p[j] = v;
+        mx = fmaxf(mx, v);
+        if constexpr (KV8) sv[j] = vs[(size_t)(j0 + j) * KV + kv];
+    }
+    mx = gblock_max(mx, red);
+    if (j0 > 0) mx = fmaxf(mx, -1e30f);  // a masked entry joins the max
+    for (int j = threadIdx.x; j < n; j += GT) p[j] = libm::frq_expf(p[j] - mx);
+    __syncthreads();
+    const float sum = seq_sum_spec<GT>(p, n, 0.0f, fsc);
+    for (int j = threadIdx.x; j < n; j += GT) p[j] = p[j] / sum;
+    __syncthreads();  // the normalised p (the first chunks have long landed)
+    // the value chains: wave 0, a lane per channel; each batch of 16 keys'
+    // LDS reads issued a batch ahead of its FMAs
+    constexpr int B = 16;
+    float acc = 0.0f;
+    const int c = lane;
+    float vb[2][B], pb[2][B];
+    for (int s = 0; s < nch; ++s) {
+        // chunk s has landed once at most (chunks issued after s) x PW loads
+        // of this wave are outstanding; after the raw barrier (a
+        // __syncthreads would also wait for the loads still in flight) every
+        // wave's part is in LDS
+        const int ahead = min(nch - 1 - s, VR_NB - 2);
+        if (ahead >= 2) gm_wait_vm<2 * PW>();
+        else if (ahead == 1) gm_wait_vm<PW>();
+        else gm_wait_vm<0>();
+        __builtin_amdgcn_s_barrier();
+        // the slot refilled here held chunk s - 1, which wave 0 finished
+        // before this barrier
+        if (s + VR_NB - 1 < nch) issue(s + VR_NB - 1);
+        if (wave == 0 && c < CW) {
+            const char* st = ring + (s % VR_NB) * VR_CHUNK + c * ES;
+            const float* ps = p + s * CK;
+            const float* svs = sv + s * CK;
+            const int m = min(CK, n - s * CK), nb = m / B;
+            auto ld = [&](int b, int k) {
+#pragma unroll
+                for (int u = 0; u < B; u += 4) {
+                    const float4 p4 = *reinterpret_cast<const float4*>(ps + k * B + u);
+                    pb[b][u] = p4.x; pb[b][u + 1] = p4.y; pb[b][u + 2] = p4.z; pb[b][u + 3] = p4.w;
+                }
+#pragma unroll
+                for (int u = 0; u < B; ++u) {
+                    if constexpr (KV8) vb[b][u] = (float)*reinterpret_cast<const int8_t*>(st + (k * B + u) * RB) * svs[k * B + u];
+                    else vb[b][u] = *reinterpret_cast<const float*>(st + (k * B + u) * RB);
+                }
+            };
+            auto fm = [&](int b) {
+#pragma unroll
+                for (int u = 0; u < B; ++u) acc = __builtin_fmaf(pb[b][u], vb[b][u], acc);
+            };
+            if (nb > 0) {
+                ld(0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                int k = 0;
+                for (; k + 2 <= nb; k += 2) {
+                    ld(1, k + 1);
+                    __builtin_amdgcn_sched_barrier(0);
+                    fm(0);
+                    ld(0, min(k + 2, nb - 1));
+                    __builtin_amdgcn_sched_barrier(0);
+                    fm(1);
+                }
+                if (k < nb) fm(0);
+            }
+            for (int jj = nb * B; jj < m; ++jj) {
+                const float v = KV8 ? (float)*reinterpret_cast<const int8_t*>(st + jj * RB) * svs[jj]
+                                    : *reinterpret_cast<const float*>(st + jj * RB);
+                acc = __builtin_fmaf(ps[jj], v, acc);
+            }
+        }
+    }
+    if (wave == 0 && c < CW) att[(size_t)h * hd + blockIdx.y * CW + c] = acc;
+}
+
 // h = act(gate) * up over m rows of the [gate | up] buffer: gelu_tanh
 // (gemma.rs:31-34) or, silu, x / (1 + exp(-x)) (rope.rs:39-41).
 __global__ __launch_bounds__(GT) void gm_geglu_kernel(const float* __restrict__ gu, int ffn, size_t total,
@@ -780,6 +1078,12 @@ struct frq_gemma {
     unsigned long long* best = nullptr;
     int64_t *tok = nullptr, *ids = nullptr;
     float *qr = nullptr, *sc = nullptr;  // long-cache decode attention: roped q, scores
+    // the quantised decode rows of the int8 linears (d- and ffn-wide: the
+    // padding of each stays zero), their scales and outliers
+    int8_t *q8d = nullptr, *q8f = nullptr;
+    float* qsa = nullptr;   // [2]
+    uint32_t* qoi = nullptr;  // [2][32]
+    float* qov = nullptr;     // [2][32]
     ~frq_gemma() {
         for (auto* v : {&qkv, &o, &gu, &down})
             for (frq_w* w : *v) frq_w_free(w);
@@ -940,6 +1244,117 @@ hipError_t gm_allow_lds(size_t lds) {
     return hipSuccess;
 }
 
+// The ring value kernel's channels a workgroup (0: the kernel does not
+// apply to this head size) and its LDS for a padded position count ps.
+int value_ring_cw(size_t hd) {
+    // 16 channels a workgroup: a workgroup streams 64 bytes of f32 cache a
+    // key, which the ring's three chunks in flight deliver at the chain's
+    // pace; wider blocks leave the chain waiting on memory
+    return hd % 16 == 0 ? 16 : 0;
+}
+size_t value_ring_lds(size_t ps) {
+    return (2 * ps + seq_sum_spec_scratch(GT)) * sizeof(float) + (size_t)VR_NB * VR_CHUNK;
+}
+
+template <bool KV8, int RB>
+hipError_t value_ring_t(const frq_gemma* g, const float* sc, int sl, int win, int ps, const float* vc,
+                        const int8_t* vq, const float* vs, hipStream_t s) {
+    constexpr int CW = RB / (KV8 ? 1 : 4);
+    const size_t lds = value_ring_lds(ps);
+    gm_dec_value_ring_kernel<KV8, RB><<<dim3((unsigned)g->H, (unsigned)(g->hd / CW)), dim3(GT), lds, s>>>(
+        sc, (int)g->H, (int)g->KV, (int)g->hd, g->cur, vc, vq, vs, sl, win, ps, g->att);
+    return hipGetLastError();
+}
+
+// The long-cache value step through the LDS ring when the head size and the
+// LDS allow it; hipErrorNotSupported sends the caller to gm_dec_value_kernel.
+hipError_t launch_value_ring(const frq_gemma* g, int sl, int win, int ps, const float* vc, const int8_t* vq,
+                             const float* vs, hipStream_t s) {
+    const int cw = value_ring_cw(g->hd);
+    if (!cw || value_ring_lds(ps) > GM_LDS_MAX) return hipErrorNotSupported;
+    if (g->kv8) {
+        if (cw == 64) return value_ring_t<true, 64>(g, g->sc, sl, win, ps, vc, vq, vs, s);
+        if (cw == 32) return value_ring_t<true, 32>(g, g->sc, sl, win, ps, vc, vq, vs, s);
+        return value_ring_t<true, 16>(g, g->sc, sl, win, ps, vc, vq, vs, s);
+    }
+    if (cw == 64) return value_ring_t<false, 256>(g, g->sc, sl, win, ps, vc, vq, vs, s);
+    if (cw == 32) return value_ring_t<false, 128>(g, g->sc, sl, win, ps, vc, vq, vs, s);
+    return value_ring_t<false, 64>(g, g->sc, sl, win, ps, vc, vq, vs, s);
+}
+
+hipError_t allow_value_ring_lds(size_t ps) {
+    const size_t lds = value_ring_lds(ps);
+    if (lds > GM_LDS_MAX) return hipSuccess;  // the caller takes the other kernel
+    const void* ks[] = {(const void*)gm_dec_value_ring_kernel<false, 256>, (const void*)gm_dec_value_ring_kernel<false, 128>,
+                        (const void*)gm_dec_value_ring_kernel<false, 64>, (const void*)gm_dec_value_ring_kernel<true, 64>,
+                        (const void*)gm_dec_value_ring_kernel<true, 32>, (const void*)gm_dec_value_ring_kernel<true, 16>};
+    for (const void* k : ks)
+        if (hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds)) return e;
+    return hipSuccess;
+}
+
+// NV4 of the fused quant for a row of K: 0 when it does not apply.
+int quant_nv4(size_t k) {
+    if (k <= FRQ_T || k % 4 || k > (size_t)FRQ_QMAXK) return 0;
+    return (int)((k / 4 + QNT - 1) / QNT);
+}
+
+template <int NV4>
+hipError_t allow_quant_kernels(size_t nlds, size_t alds) {
+    // (their static LDS, the quant's selection state, counts against the
+    // same limit, so the attribute is set whatever the dynamic size)
+    if (hipError_t e = hipFuncSetAttribute((const void*)gm_norm_quant_kernel<NV4>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)nlds))
+        return e;
+    return hipFuncSetAttribute((const void*)gm_act_quant_kernel<NV4>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)alds);
+}
+
+// The fused quant kernels' dynamic LDS: the norm's rows and fold scratch, the
+// activation row.
+size_t norm_quant_lds(int d) { return gm_norm_lds_t<QNT>(d); }
+size_t act_quant_lds(int ffn) { return (size_t)((ffn + 3) & ~3) * sizeof(float); }
+
+hipError_t gm_allow_quant_lds(const frq_gemma* g) {
+    const size_t nl = norm_quant_lds((int)g->d), al = act_quant_lds((int)g->ffn);
+    for (hipError_t e : {allow_quant_kernels<1>(nl, al), allow_quant_kernels<2>(nl, al),
+                         allow_quant_kernels<3>(nl, al), allow_quant_kernels<4>(nl, al),
+                         allow_quant_kernels<5>(nl, al)})
+        if (e != hipSuccess) return e;
+    return hipSuccess;
+}
+
+Q8 gm_q8(frq_gemma* g, int which, size_t k) {
+    return Q8{which ? g->q8f : g->q8d, g->qsa + which, g->qoi + which * FRQ_T, g->qov + which * FRQ_T,
+              (int)round_up(k, FRQ_KALIGN)};
+}
+
+hipError_t launch_norm_quant(frq_gemma* g, const float* y, const float* wpost, const float* wnext, Q8 q,
+                             int* err, hipStream_t s) {
+    const int d = (int)g->d;
+    const size_t lds = norm_quant_lds(d);
+    switch (quant_nv4(g->d)) {
+        case 1: gm_norm_quant_kernel<1><<<1, QNT, lds, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, 0, q, err); break;
+        case 2: gm_norm_quant_kernel<2><<<1, QNT, lds, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, 0, q, err); break;
+        default: return hipErrorInvalidValue;  // d <= 8192
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_act_quant(frq_gemma* g, float c, Q8 q, int* err, hipStream_t s) {
+    const int f = (int)g->ffn, silu = g->arch == 1 ? 1 : 0;
+    const size_t lds = act_quant_lds(f);
+    switch (quant_nv4(g->ffn)) {
+        case 1: gm_act_quant_kernel<1><<<1, QNT, lds, s>>>(g->gub, f, c, g->hm, silu, q, err); break;
+        case 2: gm_act_quant_kernel<2><<<1, QNT, lds, s>>>(g->gub, f, c, g->hm, silu, q, err); break;
+        case 3: gm_act_quant_kernel<3><<<1, QNT, lds, s>>>(g->gub, f, c, g->hm, silu, q, err); break;
+        case 4: gm_act_quant_kernel<4><<<1, QNT, lds, s>>>(g->gub, f, c, g->hm, silu, q, err); break;
+        case 5: gm_act_quant_kernel<5><<<1, QNT, lds, s>>>(g->gub, f, c, g->hm, silu, q, err); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 // Points every buffer of the model at nothing and the capacities at zero:
 // the state after a failed reserve, so the next call reserves again.
 void gm_drop_buffers(frq_gemma* g) {
@@ -954,6 +1369,10 @@ void gm_drop_buffers(frq_gemma* g) {
     g->best = nullptr;
     g->tok = g->ids = nullptr;
     g->qr = g->sc = nullptr;
+    g->q8d = g->q8f = nullptr;
+    g->qsa = nullptr;
+    g->qoi = nullptr;
+    g->qov = nullptr;
 }
 
 // Device buffers for up to npos positions and rows prompt rows; the RoPE
@@ -977,6 +1396,8 @@ int gm_reserve(frq_ctx* c, frq_gemma* g, size_t npos, size_t rows) {
         GMCHK(hipFuncSetAttribute((const void*)gm_norm_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                   (int)gm_norm_lds((int)g->d)),
               "hipFuncSetAttribute(norm)");
+    GMCHK(gm_allow_quant_lds(g), "hipFuncSetAttribute(quant)");
+    GMCHK(allow_value_ring_lds(gm_pstride_n(N)), "hipFuncSetAttribute(value ring)");
     const size_t L = g->L, kvd = g->KV * g->hd, half = g->hd / 2;
     size_t off = 0;
     auto take = [&](size_t bytes) { const size_t o = off; off += round_up(bytes, 256); return o; };
@@ -992,7 +1413,9 @@ int gm_reserve(frq_ctx* c, frq_gemma* g, size_t npos, size_t rows) {
                  o_qkv = take(R * (g->H + 2 * g->KV) * g->hd * 4), o_att = take(R * g->H * g->hd * 4),
                  o_o = take(R * g->d * 4), o_gu = take(R * 2 * g->ffn * 4), o_hm = take(R * g->ffn * 4),
                  o_lg = take(g->vocab * 4), o_cur = take(4), o_best = take(8), o_tok = take(N * 8), o_ids = take(R * 8),
-                 o_qr = take(g->H * g->hd * 4), o_sc = take(g->H * gm_pstride_n(N) * 4);
+                 o_qr = take(g->H * g->hd * 4), o_sc = take(g->H * gm_pstride_n(N) * 4),
+                 o_q8d = take(round_up(g->d, FRQ_KALIGN)), o_q8f = take(round_up(g->ffn, FRQ_KALIGN)),
+                 o_qsa = take(2 * 4), o_qoi = take(2 * FRQ_T * 4), o_qov = take(2 * FRQ_T * 4);
     char* m = nullptr;
     GMCHK(hipMalloc(&m, off), "hipMalloc(gemma)");
     if (hipError_t e = hipMemsetAsync(m, 0, off, s)) {
@@ -1028,6 +1451,9 @@ int gm_reserve(frq_ctx* c, frq_gemma* g, size_t npos, size_t rows) {
     g->cur = reinterpret_cast<int*>(m + o_cur); g->best = reinterpret_cast<unsigned long long*>(m + o_best);
     g->tok = reinterpret_cast<int64_t*>(m + o_tok); g->ids = reinterpret_cast<int64_t*>(m + o_ids);
     g->qr = reinterpret_cast<float*>(m + o_qr); g->sc = reinterpret_cast<float*>(m + o_sc);
+    g->q8d = reinterpret_cast<int8_t*>(m + o_q8d); g->q8f = reinterpret_cast<int8_t*>(m + o_q8f);
+    g->qsa = reinterpret_cast<float*>(m + o_qsa); g->qoi = reinterpret_cast<uint32_t*>(m + o_qoi);
+    g->qov = reinterpret_cast<float*>(m + o_qov);
     return FRQ_OK;
 }
 
@@ -1036,17 +1462,41 @@ int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_o
     const int d = (int)g->d, H = (int)g->H, KV = (int)g->KV, hd = (int)g->hd, ffn = (int)g->ffn;
     const Weight& et = *weight_of(g->embed);
     const size_t nlds = gm_norm_lds(d);
-    auto norm = [&](const float* y, const float* wpost, const float* wnext, int rows, int row0) {
-        gm_norm_kernel<<<dim3(rows), dim3(NORM_NT), nlds, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, row0);
+    int* err = ctx_err(c);
+    // decode rows of int8 linears take their quant from the producing kernel
+    auto is_i8 = [&](const frq_w* w) { return weight_of(w)->dtype == FRQ_DT_I8; };
+    // (the rows feeding q|k|v and gate|up keep the fused M == 1 linear, whose
+    // per-workgroup quant overlaps its first weight loads: measured faster
+    // than quantising in the norm kernel)
+    const bool q8d = false;
+    const bool q8f = m == 1 && quant_nv4(g->ffn) > 0;
+    // quant: also quantise the normalised row for the int8 linear `next` reads
+    auto norm = [&](const float* y, const float* wpost, const float* wnext, int rows, int row0, bool quant) {
+        if (quant) return launch_norm_quant(g, y, wpost, wnext, gm_q8(g, 0, g->d), err, s);
+        const size_t n2 = gm_norm2_lds(d);
+        switch ((d / 4 + NORM_NT - 1) / NORM_NT) {
+            case 1: gm_norm2_kernel<1><<<dim3(rows), dim3(NORM_NT), n2, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, row0); break;
+            case 2: gm_norm2_kernel<2><<<dim3(rows), dim3(NORM_NT), n2, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, row0); break;
+            case 3: gm_norm2_kernel<3><<<dim3(rows), dim3(NORM_NT), n2, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, row0); break;
+            case 4: gm_norm2_kernel<4><<<dim3(rows), dim3(NORM_NT), n2, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, row0); break;
+            default: gm_norm_kernel<<<dim3(rows), dim3(NORM_NT), nlds, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, row0);
+        }
         return hipGetLastError();
+    };
+    // the linear of the row norm() left in g->a (its quantised form when
+    // quant)
+    auto mm_a = [&](const frq_w* w, bool quant, float* outp) -> int {
+        if (!quant) return gm_mm(c, w, g->a, m, outp);
+        const Q8 q = gm_q8(g, 0, g->d);
+        return frq_mm_i8_q_dev(c, w, q.a8, q.sa, q.oi, q.ov, 1, outp);
     };
     gm_embed_kernel<<<dim3((unsigned)m), dim3(GT), 0, s>>>(et.rowp, et.rpitch, d, g->escale, rel ? g->tok : g->ids,
                                                            rel, P, g->cur, g->x);
     GMCHK(hipGetLastError(), "launch embed");
-    GMCHK(norm(nullptr, nullptr, g->norm_of(0, 0), (int)m, 0), "launch norm");
+    GMCHK(norm(nullptr, nullptr, g->norm_of(0, 0), (int)m, 0, q8d && is_i8(g->qkv[0])), "launch norm");
     const size_t kvd = g->KV * g->hd;
     for (size_t l = 0; l < g->L; ++l) {
-        if (int rc = gm_mm(c, g->qkv[l], g->a, m, g->qkvb)) return rc;
+        if (int rc = mm_a(g->qkv[l], q8d && is_i8(g->qkv[l]), g->qkvb)) return rc;
         float* kc = g->kv8 ? nullptr : g->kc + l * g->cap_pos * kvd;
         float* vc = g->kv8 ? nullptr : g->vc + l * g->cap_pos * kvd;
         int8_t* kq = g->kv8 ? g->kq + l * g->cap_pos * kvd : nullptr;
@@ -1070,15 +1520,24 @@ int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_o
                     g->qkvb, H, KV, hd, g->cur, g->cs, kc, vc, kq, vq, ks, vs, qb, qn, kn, g->eps, g->qr);
                 gm_dec_score_kernel<true><<<sg, dim3(GT), hd4 * sizeof(float), s>>>(
                     g->qr, H, KV, hd, g->cur, kc, kq, ks, g->qscale, g->cap, sl, win, div, ps, g->sc);
-                gm_dec_value_kernel<true><<<dim3((unsigned)H), dim3(GT), vlds, s>>>(g->sc, H, KV, hd, g->cur, vc, vq,
-                                                                                    vs, sl, win, ps, g->att);
+                const hipError_t er = launch_value_ring(g, sl, win, ps, vc, vq, vs, s);
+                if (er == hipErrorNotSupported)
+                    gm_dec_value_kernel<true><<<dim3((unsigned)H), dim3(GT), vlds, s>>>(g->sc, H, KV, hd, g->cur, vc,
+                                                                                        vq, vs, sl, win, ps, g->att);
+                else
+                    GMCHK(er, "launch value ring");
             } else {
                 gm_dec_prep_kernel<false><<<dim3((unsigned)(H + KV)), dim3(GT), plds, s>>>(
                     g->qkvb, H, KV, hd, g->cur, g->cs, kc, vc, kq, vq, ks, vs, qb, qn, kn, g->eps, g->qr);
                 gm_dec_score_kernel<false><<<sg, dim3(GT), hd4 * sizeof(float), s>>>(
                     g->qr, H, KV, hd, g->cur, kc, kq, ks, g->qscale, g->cap, sl, win, div, ps, g->sc);
-                gm_dec_value_kernel<false><<<dim3((unsigned)H), dim3(GT), vlds, s>>>(g->sc, H, KV, hd, g->cur, vc,
-                                                                                     vq, vs, sl, win, ps, g->att);
+                const hipError_t er = launch_value_ring(g, sl, win, ps, vc, vq, vs, s);
+                if (er == hipErrorNotSupported)
+                    gm_dec_value_kernel<false><<<dim3((unsigned)H), dim3(GT), vlds, s>>>(g->sc, H, KV, hd, g->cur,
+                                                                                         vc, vq, vs, sl, win, ps,
+                                                                                         g->att);
+                else
+                    GMCHK(er, "launch value ring");
             }
         } else if (m == 1) {
             if (g->kv8)
@@ -1123,17 +1582,26 @@ int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_o
         }
         GMCHK(hipGetLastError(), "launch attention");
         if (int rc = gm_mm(c, g->o[l], g->att, m, g->ob)) return rc;
-        GMCHK(norm(g->ob, g->post_of(l, 1), g->norm_of(l, 2), (int)m, 0), "launch norm");
-        if (int rc = gm_mm(c, g->gu[l], g->a, m, g->gub)) return rc;
-        const size_t tot = m * g->ffn;
-        gm_geglu_kernel<<<dim3((unsigned)std::min<size_t>((tot + GT - 1) / GT, 4096)), dim3(GT), 0, s>>>(
-            g->gub, ffn, tot, sqrtf(2.0f / 3.14159274101257324f), g->hm, g->arch == 1 ? 1 : 0);
-        GMCHK(hipGetLastError(), "launch geglu");
-        if (int rc = gm_mm(c, g->down[l], g->hm, m, g->ob)) return rc;
+        const bool qg = q8d && is_i8(g->gu[l]);
+        GMCHK(norm(g->ob, g->post_of(l, 1), g->norm_of(l, 2), (int)m, 0, qg), "launch norm");
+        if (int rc = mm_a(g->gu[l], qg, g->gub)) return rc;
+        const float gc = sqrtf(2.0f / 3.14159274101257324f);
+        if (q8f && is_i8(g->down[l])) {  // act(gate) * up and its quant in one kernel
+            const Q8 q = gm_q8(g, 1, g->ffn);
+            GMCHK(launch_act_quant(g, gc, q, err, s), "launch act + quant");
+            if (int rc = frq_mm_i8_q_dev(c, g->down[l], q.a8, q.sa, q.oi, q.ov, 1, g->ob)) return rc;
+        } else {
+            const size_t tot = m * g->ffn;
+            gm_geglu_kernel<<<dim3((unsigned)std::min<size_t>((tot + GT - 1) / GT, 4096)), dim3(GT), 0, s>>>(
+                g->gub, ffn, tot, gc, g->hm, g->arch == 1 ? 1 : 0);
+            GMCHK(hipGetLastError(), "launch geglu");
+            if (int rc = gm_mm(c, g->down[l], g->hm, m, g->ob)) return rc;
+        }
         if (l + 1 < g->L)
-            GMCHK(norm(g->ob, g->post_of(l, 3), g->norm_of(l + 1, 0), (int)m, 0), "launch norm");
+            GMCHK(norm(g->ob, g->post_of(l, 3), g->norm_of(l + 1, 0), (int)m, 0, q8d && is_i8(g->qkv[l + 1])),
+                  "launch norm");
         else  // only the last row feeds the head
-            GMCHK(norm(g->ob, g->post_of(l, 3), g->final_norm(), 1, (int)m - 1), "launch norm");
+            GMCHK(norm(g->ob, g->post_of(l, 3), g->final_norm(), 1, (int)m - 1, false), "launch norm");
     }
     float* lg = logits_out ? logits_out : g->logits;
     const Weight& ut = g->unembed ? *weight_of(g->unembed) : et;
