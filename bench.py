@@ -540,6 +540,28 @@ def run_detail(args, ctx, fa, hip, synth, convert, time_loop, log, threads, cfx)
             "tok_s": round(256 / runs[256], 1), "decode_ms_per_token": round(dec_ms, 3),
             "decode_tok_s": round(1e3 / dec_ms, 1), "prefill_plus_first_ms": round(runs[1] * 1e3, 1),
             "tokens_identical_to_fixture": None if fx is None else cfx.compare(fx["sequences"][0], toks)[0]}
+        # batch 16: sixteen 64-token prompts decoded together (every sequence
+        # its own generate); decode tok/s over all sequences, and the step's
+        # weight stream (int4 linears + f16 scales + the f16 unembed) per step
+        pb = np.stack(cfx.WORKLOADS["config2_b16"]["prompts"]())
+        tb = g.generate_batch(pb, 256)
+        fxb = cfx.load_fixture("config2_b16")
+        runs = {}
+        for n_new in (1, 256):
+            t0 = time.perf_counter()
+            g.generate_batch(pb, n_new)
+            runs[n_new] = time.perf_counter() - t0
+        step_s = (runs[256] - runs[1]) / 255
+        L_, d_, ffn_, V_ = 26, 2304, 9216, 256000
+        lin = L_ * (d_ * (2048 + 1024 + 1024) + 2048 * d_ + d_ * 2 * ffn_ + ffn_ * d_)
+        step_bytes = lin // 2 + 2 * (lin // 32) + V_ * d_ * 2
+        detail["gemma2_decode"]["int4_kv_f32_batch16"] = {
+            "decode_tok_s": round(16 / step_s, 1), "step_ms": round(step_s * 1e3, 3),
+            "prefill_plus_first_ms": round(runs[1] * 1e3, 1),
+            "weight_GBps": round(step_bytes / step_s / 1e9, 1),
+            "weight_frac_hbm": round(step_bytes / step_s / 1e9 / HBM_PEAK_GBS, 3),
+            "tokens_identical_to_fixture": None if fxb is None else all(
+                cfx.compare(fxb["sequences"][i], tb[i])[0] for i in range(len(pb)))}
         log(f"gemma2 {detail['gemma2_decode']}")
         g.free()
         b.close()

@@ -92,6 +92,7 @@ SIGNATURES = {
     "frq_gemma_info": (_I, [_P, _P, _P, _P]),
     "frq_gemma_set_graphs": (_I, [_P, _I]),
     "frq_gemma_generate": (_I, [_P, _P, _P, _S, _S, _P, _P]),
+    "frq_gemma_generate_batch": (_I, [_P, _P, _P, _S, _S, _S, _P, _P]),
     "frq_gemma_predict": (_I, [_P, _P, _P, _S, _P, _P]),
 }
 
@@ -617,6 +618,18 @@ class Gemma:
         lg = np.empty((n_new, self.vocab), np.float32) if with_logits else None
         _check(lib.frq_gemma_generate(self.ctx.h, self.h, _ptr(prompt), len(prompt), n_new, _ptr(out),
                                       None if lg is None else _ptr(lg)))
+        return (out, lg) if with_logits else out
+
+    def generate_batch(self, prompts, n_new: int, with_logits: bool = False):
+        """Each row of prompts (nb, n_prompt) its own generate, the decode
+        steps of all rows together: tokens (nb, n_new) [and logits (nb,
+        n_new, vocab)] as nb calls of generate give them."""
+        prompts = np.ascontiguousarray(np.atleast_2d(prompts), dtype=np.int64)
+        nb, n_prompt = prompts.shape
+        out = np.empty((nb, n_new), np.int64)
+        lg = np.empty((nb, n_new, self.vocab), np.float32) if with_logits else None
+        _check(lib.frq_gemma_generate_batch(self.ctx.h, self.h, _ptr(prompts), nb, n_prompt, n_new, _ptr(out),
+                                            None if lg is None else _ptr(lg)))
         return (out, lg) if with_logits else out
 
     def predict(self, ids, with_logits: bool = False):

@@ -369,6 +369,8 @@ hipError_t launch_rowdot(const Weight& w, const float* x, const int64_t* cand, s
 // *best must start at 0.  A NaN output sets *err.
 hipError_t launch_rowdot_argmax(const Weight& w, const float* x, float* out, unsigned long long* best, int* err,
                                 hipStream_t s);
+hipError_t launch_rowdot_argmax_batch(const Weight& w, size_t nx, const float* x, size_t xs, float* out, size_t os,
+                                      unsigned long long* best, int* err, hipStream_t s);
 // int4 linear (any m).
 hipError_t launch_i4(const Weight& w, size_t m, const float* a, float* out,
                      float* wsf, unsigned* tickets, hipStream_t s);
@@ -379,6 +381,8 @@ hipError_t launch_i4_terms(const Weight& w, const float* a, float* out, hipStrea
 // int4 in the reference's orders for any m (M == 1 i4_dot_avx2, M > 1 the
 // dequantise + sequential-k GEMM): the paths decode engines use.
 hipError_t launch_i4_exact(const Weight& w, size_t m, const float* a, float* out, hipStream_t s);
+// m rows each in the M == 1 order (i4_dot_avx2), weights read once.
+hipError_t launch_i4_m1_rows(const Weight& w, size_t m, const float* a, float* out, hipStream_t s);
 // int4 (N, K/2) -> the MFMA layout (g == 32, K % 32 == 0); bytes of q4.
 size_t i4_blocked_bytes(size_t n, size_t k);
 hipError_t launch_i4_block(const uint8_t* raw, const uint16_t* sraw, size_t n,

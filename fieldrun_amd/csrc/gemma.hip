@@ -55,11 +55,13 @@ __device__ float gblock_max(float v, float* red) {
 
 // rows_f32("embed", ids) * escale (gemma.rs:424, 429): row t is token ids[t]
 // (rel: ids[cur - P + t], the token the last argmax wrote).
+// (tstride > 0: a batch step, row t is sequence t's last token, ids[t tstride + cur - P])
 __global__ __launch_bounds__(GT) void gm_embed_kernel(const uint8_t* __restrict__ tab, size_t pitch, int d,
                                                       float escale, const int64_t* __restrict__ ids, int rel, int P,
-                                                      const int* __restrict__ curp, float* __restrict__ x) {
+                                                      const int* __restrict__ curp, float* __restrict__ x,
+                                                      size_t tstride = 0) {
     const int t = blockIdx.x;
-    const int64_t id = ids[rel ? *curp - P + t : t];
+    const int64_t id = ids[rel ? (tstride ? t * tstride + *curp - P : *curp - P + t) : t];
     const uint16_t* row = reinterpret_cast<const uint16_t*>(tab + (size_t)id * pitch);
     for (int c = threadIdx.x; c < d; c += GT) x[(size_t)t * d + c] = h2f(row[c]) * escale;
 }
@@ -204,11 +206,13 @@ __global__ __launch_bounds__(NORM_NT) void gm_norm2_kernel(float* __restrict__ x
         if (valid(i)) reinterpret_cast<float4*>(out + r)[tid + NORM_NT * i] = mul(scl(nv[i], inv), wnv[i]);
 }
 
-// ---- the int8 decode linears' activation quant, fused into the kernel that
-// produces the row (the norm before q|k|v and gate|up, the activation before
-// down), so the linear that follows streams its weights with no quant of
-// its own (frq_mm_i8_q_dev).  The quant is quant_core.h's, by 16 waves:
-// the same bytes as the standalone quant and the fused M == 1 linear.
+// ---- the int8 down linear's activation quant, fused into the activation
+// kernel (act(gate) * up), so the down linear streams its weights with no
+// quant of its own (frq_mm_i8_q_dev).  The quant is quant_core.h's, by 16
+// waves: the same bytes as the standalone quant and the fused M == 1
+// linear.  (The rows feeding q|k|v and gate|up keep the fused M == 1
+// linear, whose per-workgroup quant overlaps its first weight loads:
+// measured faster than quantising in the norm kernel.)
 constexpr int QNT = 1024;
 constexpr int FRQ_QMAXK = 4 * QNT * 5;  // K of the fused quant (NV4 <= 5)
 
@@ -246,19 +250,6 @@ __device__ void quant_lds_row(const float* row, int K, const Q8& q, int* err) {
         q.ov[tid] = L.sel_v[tid];
     }
     if (tid == 0) *q.sa = sel.sa;
-}
-
-// gm_norm_kernel for one decode row, the normalised row also quantised.
-template <int NV4>
-__global__ __launch_bounds__(QNT) void gm_norm_quant_kernel(float* __restrict__ x, const float* __restrict__ y,
-                                                            const float* __restrict__ wpost,
-                                                            const float* __restrict__ wnext,
-                                                            float* __restrict__ out, int d, float eps, int row0,
-                                                            Q8 q, int* __restrict__ err) {
-    extern __shared__ float4 lds4[];
-    const float* t = gm_norm_body<QNT>(x, y, wpost, wnext, out, d, eps, (size_t)(row0 + blockIdx.x) * d,
-                                       reinterpret_cast<float*>(lds4));
-    quant_lds_row<NV4>(t, d, q, err);
 }
 
 // The down linear's input for one decode row, act(gate) * up as
@@ -386,7 +377,7 @@ __global__ __launch_bounds__(GT) void gm_attn_kernel(const float* __restrict__ q
                                                      float cap, int sliding, int window, int pstride,
                                                      float* __restrict__ att, int div,
                                                      const float* __restrict__ bias, const float* __restrict__ qn,
-                                                     const float* __restrict__ kn, float eps) {
+                                                     const float* __restrict__ kn, float eps, long long bst = 0) {
     extern __shared__ float4 lds4[];
     float* q = reinterpret_cast<float*>(lds4);
     float* kvs = q + ((hd + 3) & ~3);
@@ -394,7 +385,14 @@ __global__ __launch_bounds__(GT) void gm_attn_kernel(const float* __restrict__ q
     float* sv = p + pstride;
     __shared__ float red[4];
     const int h = blockIdx.x, i = blockIdx.y, rep = H / KV, kv = h / rep, half = hd / 2, kvd = KV * hd;
-    const int cur = *curp, ab = cur + i, klen = cur + (int)gridDim.y;
+    // bst > 0: a batch step, row i is sequence i's decode row (its own cache,
+    // bst elements further for each row; every sequence at position cur)
+    const int cur = *curp, ab = bst ? cur : cur + i, klen = bst ? cur + 1 : cur + (int)gridDim.y;
+    if (bst) {
+        const size_t o = (size_t)i * (size_t)bst, os = o / (size_t)hd;
+        if (kc) { kc += o; vc += o; }
+        if (kq) { kq += o; vq += o; ks += os; vs += os; }
+    }
     const float* row = qkv + (size_t)i * (H + 2 * KV) * hd;
     if constexpr (FUSED) {
         const size_t pos = (size_t)ab;
@@ -1037,6 +1035,19 @@ __global__ __launch_bounds__(GT) void gm_geglu_kernel(const float* __restrict__ 
 
 // The token the unembed's folded argmax chose goes to out[cur + m - P];
 // cur += m; the key is cleared.
+// A batch step's tokens: sequence b's argmax to out[b tstride + cur + 1 - P]
+// (after its previous token), then every sequence one position on.
+__global__ void gm_argmax_batch_kernel(unsigned long long* __restrict__ best, int* __restrict__ curp, int nb, int P,
+                                       int64_t* __restrict__ out, int tstride) {
+    const int cur = *curp;
+    for (int b = threadIdx.x; b < nb; b += blockDim.x) {
+        out[(size_t)b * tstride + cur + 1 - P] = (int64_t)(uint32_t)(best[b] & 0xffffffffull);
+        best[b] = 0ull;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) *curp = cur + 1;
+}
+
 __global__ void gm_argmax_done_kernel(unsigned long long* __restrict__ best, int* __restrict__ curp, int m, int P,
                                       int64_t* __restrict__ out) {
     if (threadIdx.x == 0) {
@@ -1080,10 +1091,13 @@ struct frq_gemma {
     float *qr = nullptr, *sc = nullptr;  // long-cache decode attention: roped q, scores
     // the quantised decode rows of the int8 linears (d- and ffn-wide: the
     // padding of each stays zero), their scales and outliers
-    int8_t *q8d = nullptr, *q8f = nullptr;
-    float* qsa = nullptr;   // [2]
-    uint32_t* qoi = nullptr;  // [2][32]
-    float* qov = nullptr;     // [2][32]
+    int8_t* q8f = nullptr;
+    float* qsa = nullptr;     // [1]
+    uint32_t* qoi = nullptr;  // [32]
+    float* qov = nullptr;     // [32]
+    // batches of sequences: the caches and token arrays hold cap_b
+    // sequences; seq is the sequence a one-sequence call (a prefill) works on
+    size_t cap_b = 0, seq = 0;
     ~frq_gemma() {
         for (auto* v : {&qkv, &o, &gu, &down})
             for (frq_w* w : *v) frq_w_free(w);
@@ -1221,6 +1235,27 @@ int gm_mm(frq_ctx* c, const frq_w* wh, const float* in, size_t m, float* outp) {
     return FRQ_OK;
 }
 
+// The linears of a batch step: m rows, each its own sequence's decode row,
+// so each row in the M == 1 order of its dtype (int8: the multi-row path is
+// bit-identical to M == 1 up to 16 rows; int4: i4_dot_avx2's order for every
+// row; q4a: one M == 1 call a row).
+int gm_mm_rows(frq_ctx* c, const frq_w* wh, const float* in, size_t m, float* outp) {
+    const Weight& w = *weight_of(wh);
+    hipStream_t s = (hipStream_t)frq_get_stream(c);
+    if (w.dtype == FRQ_DT_I4) {
+        GMCHK(launch_i4_m1_rows(w, m, in, outp, s), "launch i4 rows");
+        return FRQ_OK;
+    }
+    if (w.dtype == FRQ_DT_Q4A) {
+        for (size_t i = 0; i < m; ++i)
+            GMCHK(launch_q4a(w, 1, in + i * w.k, outp + i * w.n, s), "launch q4a");
+        return FRQ_OK;
+    }
+    for (size_t r0 = 0; r0 < m; r0 += 16)
+        if (int rc = frq_mm_dev(c, wh, in + r0 * w.k, std::min<size_t>(16, m - r0), outp + r0 * w.n)) return rc;
+    return FRQ_OK;
+}
+
 size_t gm_pstride_n(size_t npos) { return (npos + 3) & ~(size_t)3; }
 size_t gm_pstride(const frq_gemma* g) { return gm_pstride_n(g->cap_pos); }
 // LDS of the one-launch attention (gm_attn_kernel: q, two hd-vectors and
@@ -1258,28 +1293,28 @@ size_t value_ring_lds(size_t ps) {
 
 template <bool KV8, int RB>
 hipError_t value_ring_t(const frq_gemma* g, const float* sc, int sl, int win, int ps, const float* vc,
-                        const int8_t* vq, const float* vs, hipStream_t s) {
+                        const int8_t* vq, const float* vs, float* att, hipStream_t s) {
     constexpr int CW = RB / (KV8 ? 1 : 4);
     const size_t lds = value_ring_lds(ps);
     gm_dec_value_ring_kernel<KV8, RB><<<dim3((unsigned)g->H, (unsigned)(g->hd / CW)), dim3(GT), lds, s>>>(
-        sc, (int)g->H, (int)g->KV, (int)g->hd, g->cur, vc, vq, vs, sl, win, ps, g->att);
+        sc, (int)g->H, (int)g->KV, (int)g->hd, g->cur, vc, vq, vs, sl, win, ps, att);
     return hipGetLastError();
 }
 
 // The long-cache value step through the LDS ring when the head size and the
 // LDS allow it; hipErrorNotSupported sends the caller to gm_dec_value_kernel.
 hipError_t launch_value_ring(const frq_gemma* g, int sl, int win, int ps, const float* vc, const int8_t* vq,
-                             const float* vs, hipStream_t s) {
+                             const float* vs, float* att, hipStream_t s) {
     const int cw = value_ring_cw(g->hd);
     if (!cw || value_ring_lds(ps) > GM_LDS_MAX) return hipErrorNotSupported;
     if (g->kv8) {
-        if (cw == 64) return value_ring_t<true, 64>(g, g->sc, sl, win, ps, vc, vq, vs, s);
-        if (cw == 32) return value_ring_t<true, 32>(g, g->sc, sl, win, ps, vc, vq, vs, s);
-        return value_ring_t<true, 16>(g, g->sc, sl, win, ps, vc, vq, vs, s);
+        if (cw == 64) return value_ring_t<true, 64>(g, g->sc, sl, win, ps, vc, vq, vs, att, s);
+        if (cw == 32) return value_ring_t<true, 32>(g, g->sc, sl, win, ps, vc, vq, vs, att, s);
+        return value_ring_t<true, 16>(g, g->sc, sl, win, ps, vc, vq, vs, att, s);
     }
-    if (cw == 64) return value_ring_t<false, 256>(g, g->sc, sl, win, ps, vc, vq, vs, s);
-    if (cw == 32) return value_ring_t<false, 128>(g, g->sc, sl, win, ps, vc, vq, vs, s);
-    return value_ring_t<false, 64>(g, g->sc, sl, win, ps, vc, vq, vs, s);
+    if (cw == 64) return value_ring_t<false, 256>(g, g->sc, sl, win, ps, vc, vq, vs, att, s);
+    if (cw == 32) return value_ring_t<false, 128>(g, g->sc, sl, win, ps, vc, vq, vs, att, s);
+    return value_ring_t<false, 64>(g, g->sc, sl, win, ps, vc, vq, vs, att, s);
 }
 
 hipError_t allow_value_ring_lds(size_t ps) {
@@ -1300,45 +1335,27 @@ int quant_nv4(size_t k) {
 }
 
 template <int NV4>
-hipError_t allow_quant_kernels(size_t nlds, size_t alds) {
-    // (their static LDS, the quant's selection state, counts against the
-    // same limit, so the attribute is set whatever the dynamic size)
-    if (hipError_t e = hipFuncSetAttribute((const void*)gm_norm_quant_kernel<NV4>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)nlds))
-        return e;
+hipError_t allow_quant_kernel(size_t alds) {
+    // (its static LDS, the quant's selection state, counts against the same
+    // limit, so the attribute is set whatever the dynamic size)
     return hipFuncSetAttribute((const void*)gm_act_quant_kernel<NV4>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                (int)alds);
 }
 
-// The fused quant kernels' dynamic LDS: the norm's rows and fold scratch, the
-// activation row.
-size_t norm_quant_lds(int d) { return gm_norm_lds_t<QNT>(d); }
+// The activation + quant kernel's dynamic LDS: the activation row.
 size_t act_quant_lds(int ffn) { return (size_t)((ffn + 3) & ~3) * sizeof(float); }
 
 hipError_t gm_allow_quant_lds(const frq_gemma* g) {
-    const size_t nl = norm_quant_lds((int)g->d), al = act_quant_lds((int)g->ffn);
-    for (hipError_t e : {allow_quant_kernels<1>(nl, al), allow_quant_kernels<2>(nl, al),
-                         allow_quant_kernels<3>(nl, al), allow_quant_kernels<4>(nl, al),
-                         allow_quant_kernels<5>(nl, al)})
+    const size_t al = act_quant_lds((int)g->ffn);
+    for (hipError_t e : {allow_quant_kernel<1>(al), allow_quant_kernel<2>(al), allow_quant_kernel<3>(al),
+                         allow_quant_kernel<4>(al), allow_quant_kernel<5>(al)})
         if (e != hipSuccess) return e;
     return hipSuccess;
 }
 
 Q8 gm_q8(frq_gemma* g, int which, size_t k) {
-    return Q8{which ? g->q8f : g->q8d, g->qsa + which, g->qoi + which * FRQ_T, g->qov + which * FRQ_T,
-              (int)round_up(k, FRQ_KALIGN)};
-}
-
-hipError_t launch_norm_quant(frq_gemma* g, const float* y, const float* wpost, const float* wnext, Q8 q,
-                             int* err, hipStream_t s) {
-    const int d = (int)g->d;
-    const size_t lds = norm_quant_lds(d);
-    switch (quant_nv4(g->d)) {
-        case 1: gm_norm_quant_kernel<1><<<1, QNT, lds, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, 0, q, err); break;
-        case 2: gm_norm_quant_kernel<2><<<1, QNT, lds, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, 0, q, err); break;
-        default: return hipErrorInvalidValue;  // d <= 8192
-    }
-    return hipGetLastError();
+    (void)which;
+    return Q8{g->q8f, g->qsa, g->qoi, g->qov, (int)round_up(k, FRQ_KALIGN)};
 }
 
 hipError_t launch_act_quant(frq_gemma* g, float c, Q8 q, int* err, hipStream_t s) {
@@ -1360,7 +1377,7 @@ hipError_t launch_act_quant(frq_gemma* g, float c, Q8 q, int* err, hipStream_t s
 void gm_drop_buffers(frq_gemma* g) {
     if (g->buf) (void)hipFree(g->buf);
     g->buf = nullptr;
-    g->cap_pos = g->cap_rows = 0;
+    g->cap_pos = g->cap_rows = g->cap_b = 0;
     g->cs = nullptr;
     g->kc = g->vc = g->ks = g->vs = nullptr;
     g->kq = g->vq = nullptr;
@@ -1369,7 +1386,7 @@ void gm_drop_buffers(frq_gemma* g) {
     g->best = nullptr;
     g->tok = g->ids = nullptr;
     g->qr = g->sc = nullptr;
-    g->q8d = g->q8f = nullptr;
+    g->q8f = nullptr;
     g->qsa = nullptr;
     g->qoi = nullptr;
     g->qov = nullptr;
@@ -1380,9 +1397,9 @@ void gm_drop_buffers(frq_gemma* g) {
 // cos / sin).  A request the attention cannot serve is refused before
 // anything changes; any later failure leaves the model with no buffers
 // (capacities 0), never with pointers into freed memory.
-int gm_reserve(frq_ctx* c, frq_gemma* g, size_t npos, size_t rows) {
-    if (npos <= g->cap_pos && rows <= g->cap_rows && g->buf) return FRQ_OK;
-    const size_t N = std::max(npos, g->cap_pos), R = std::max(rows, g->cap_rows);
+int gm_reserve(frq_ctx* c, frq_gemma* g, size_t npos, size_t rows, size_t nb = 1) {
+    if (npos <= g->cap_pos && rows <= g->cap_rows && nb <= g->cap_b && g->buf) return FRQ_OK;
+    const size_t N = std::max(npos, g->cap_pos), R = std::max(rows, g->cap_rows), B = std::max(nb, g->cap_b);
     const size_t need = gm_attn_lds_n(g->hd, N);
     if (need > GM_LDS_MAX)
         return set_error(FRQ_ERR_ARG, "gemma: " + std::to_string(N) +
@@ -1404,18 +1421,19 @@ int gm_reserve(frq_ctx* c, frq_gemma* g, size_t npos, size_t rows) {
     const size_t o_cs = take(N * half * sizeof(float2));
     size_t o_kc, o_vc, o_ks = 0, o_vs = 0;
     if (g->kv8) {
-        o_kc = take(L * N * kvd); o_vc = take(L * N * kvd);
-        o_ks = take(L * N * g->KV * 4); o_vs = take(L * N * g->KV * 4);
+        o_kc = take(L * B * N * kvd); o_vc = take(L * B * N * kvd);
+        o_ks = take(L * B * N * g->KV * 4); o_vs = take(L * B * N * g->KV * 4);
     } else {
-        o_kc = take(L * N * kvd * 4); o_vc = take(L * N * kvd * 4);
+        o_kc = take(L * B * N * kvd * 4); o_vc = take(L * B * N * kvd * 4);
     }
     const size_t o_x = take(R * g->d * 4), o_a = take(R * g->d * 4),
                  o_qkv = take(R * (g->H + 2 * g->KV) * g->hd * 4), o_att = take(R * g->H * g->hd * 4),
                  o_o = take(R * g->d * 4), o_gu = take(R * 2 * g->ffn * 4), o_hm = take(R * g->ffn * 4),
-                 o_lg = take(g->vocab * 4), o_cur = take(4), o_best = take(8), o_tok = take(N * 8), o_ids = take(R * 8),
+                 o_lg = take(B * g->vocab * 4), o_cur = take(4), o_best = take(B * 8), o_tok = take(B * N * 8),
+                 o_ids = take(R * 8),
                  o_qr = take(g->H * g->hd * 4), o_sc = take(g->H * gm_pstride_n(N) * 4),
-                 o_q8d = take(round_up(g->d, FRQ_KALIGN)), o_q8f = take(round_up(g->ffn, FRQ_KALIGN)),
-                 o_qsa = take(2 * 4), o_qoi = take(2 * FRQ_T * 4), o_qov = take(2 * FRQ_T * 4);
+                 o_q8f = take(round_up(g->ffn, FRQ_KALIGN)), o_qsa = take(4), o_qoi = take(FRQ_T * 4),
+                 o_qov = take(FRQ_T * 4);
     char* m = nullptr;
     GMCHK(hipMalloc(&m, off), "hipMalloc(gemma)");
     if (hipError_t e = hipMemsetAsync(m, 0, off, s)) {
@@ -1437,6 +1455,7 @@ int gm_reserve(frq_ctx* c, frq_gemma* g, size_t npos, size_t rows) {
     g->buf = m;
     g->cap_pos = N;
     g->cap_rows = R;
+    g->cap_b = B;
     g->cs = reinterpret_cast<float2*>(m + o_cs);
     g->kc = g->kv8 ? nullptr : reinterpret_cast<float*>(m + o_kc);
     g->vc = g->kv8 ? nullptr : reinterpret_cast<float*>(m + o_vc);
@@ -1451,28 +1470,28 @@ int gm_reserve(frq_ctx* c, frq_gemma* g, size_t npos, size_t rows) {
     g->cur = reinterpret_cast<int*>(m + o_cur); g->best = reinterpret_cast<unsigned long long*>(m + o_best);
     g->tok = reinterpret_cast<int64_t*>(m + o_tok); g->ids = reinterpret_cast<int64_t*>(m + o_ids);
     g->qr = reinterpret_cast<float*>(m + o_qr); g->sc = reinterpret_cast<float*>(m + o_sc);
-    g->q8d = reinterpret_cast<int8_t*>(m + o_q8d); g->q8f = reinterpret_cast<int8_t*>(m + o_q8f);
+    g->q8f = reinterpret_cast<int8_t*>(m + o_q8f);
     g->qsa = reinterpret_cast<float*>(m + o_qsa); g->qoi = reinterpret_cast<uint32_t*>(m + o_qoi);
     g->qov = reinterpret_cast<float*>(m + o_qov);
     return FRQ_OK;
 }
 
-int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_out) {
+// One step of the model: m prompt rows (rel 0: ids; the prefill) or, rel 1,
+// the decode row of the last token; batch > 0: m = batch rows, row i the
+// decode row of sequence i, every sequence at the same position (logits
+// row i at logits_out + i los).
+int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_out, int batch = 0,
+             size_t los = 0) {
     hipStream_t s = (hipStream_t)frq_get_stream(c);
     const int d = (int)g->d, H = (int)g->H, KV = (int)g->KV, hd = (int)g->hd, ffn = (int)g->ffn;
     const Weight& et = *weight_of(g->embed);
     const size_t nlds = gm_norm_lds(d);
     int* err = ctx_err(c);
-    // decode rows of int8 linears take their quant from the producing kernel
     auto is_i8 = [&](const frq_w* w) { return weight_of(w)->dtype == FRQ_DT_I8; };
-    // (the rows feeding q|k|v and gate|up keep the fused M == 1 linear, whose
-    // per-workgroup quant overlaps its first weight loads: measured faster
-    // than quantising in the norm kernel)
-    const bool q8d = false;
-    const bool q8f = m == 1 && quant_nv4(g->ffn) > 0;
-    // quant: also quantise the normalised row for the int8 linear `next` reads
-    auto norm = [&](const float* y, const float* wpost, const float* wnext, int rows, int row0, bool quant) {
-        if (quant) return launch_norm_quant(g, y, wpost, wnext, gm_q8(g, 0, g->d), err, s);
+    // one decode row of an int8 down linear takes its quant from the
+    // activation kernel
+    const bool q8f = m == 1 && !batch && quant_nv4(g->ffn) > 0;
+    auto norm = [&](const float* y, const float* wpost, const float* wnext, int rows, int row0) {
         const size_t n2 = gm_norm2_lds(d);
         switch ((d / 4 + NORM_NT - 1) / NORM_NT) {
             case 1: gm_norm2_kernel<1><<<dim3(rows), dim3(NORM_NT), n2, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, row0); break;
@@ -1483,26 +1502,30 @@ int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_o
         }
         return hipGetLastError();
     };
-    // the linear of the row norm() left in g->a (its quantised form when
-    // quant)
-    auto mm_a = [&](const frq_w* w, bool quant, float* outp) -> int {
-        if (!quant) return gm_mm(c, w, g->a, m, outp);
-        const Q8 q = gm_q8(g, 0, g->d);
-        return frq_mm_i8_q_dev(c, w, q.a8, q.sa, q.oi, q.ov, 1, outp);
+    // the linears: in a batch step each row is its own sequence's decode row
+    auto mm = [&](const frq_w* w, const float* in, float* outp) -> int {
+        return batch ? gm_mm_rows(c, w, in, m, outp) : gm_mm(c, w, in, m, outp);
     };
-    gm_embed_kernel<<<dim3((unsigned)m), dim3(GT), 0, s>>>(et.rowp, et.rpitch, d, g->escale, rel ? g->tok : g->ids,
-                                                           rel, P, g->cur, g->x);
+    int64_t* tokp = g->tok + g->seq * g->cap_pos;  // this sequence's tokens (batch: sequence 0's)
+    gm_embed_kernel<<<dim3((unsigned)m), dim3(GT), 0, s>>>(et.rowp, et.rpitch, d, g->escale, rel ? tokp : g->ids,
+                                                           rel, P, g->cur, g->x, batch ? g->cap_pos : 0);
     GMCHK(hipGetLastError(), "launch embed");
-    GMCHK(norm(nullptr, nullptr, g->norm_of(0, 0), (int)m, 0, q8d && is_i8(g->qkv[0])), "launch norm");
+    GMCHK(norm(nullptr, nullptr, g->norm_of(0, 0), (int)m, 0), "launch norm");
     const size_t kvd = g->KV * g->hd;
+    // the caches: [layer][sequence][position][kv width]; a batch step's row i
+    // is sequence i (bst elements further per row)
+    const size_t bst = g->cap_pos * kvd;
     for (size_t l = 0; l < g->L; ++l) {
-        if (int rc = mm_a(g->qkv[l], q8d && is_i8(g->qkv[l]), g->qkvb)) return rc;
-        float* kc = g->kv8 ? nullptr : g->kc + l * g->cap_pos * kvd;
-        float* vc = g->kv8 ? nullptr : g->vc + l * g->cap_pos * kvd;
-        int8_t* kq = g->kv8 ? g->kq + l * g->cap_pos * kvd : nullptr;
-        int8_t* vq = g->kv8 ? g->vq + l * g->cap_pos * kvd : nullptr;
-        float* ks = g->kv8 ? g->ks + l * g->cap_pos * g->KV : nullptr;
-        float* vs = g->kv8 ? g->vs + l * g->cap_pos * g->KV : nullptr;
+        if (int rc = mm(g->qkv[l], g->a, g->qkvb)) return rc;
+        const size_t cb = (l * g->cap_b + g->seq) * g->cap_pos;  // this layer's (and sequence's) first position
+        float* kc0 = g->kv8 ? nullptr : g->kc + cb * kvd;
+        float* vc0 = g->kv8 ? nullptr : g->vc + cb * kvd;
+        int8_t* kq0 = g->kv8 ? g->kq + cb * kvd : nullptr;
+        int8_t* vq0 = g->kv8 ? g->vq + cb * kvd : nullptr;
+        float* ks0 = g->kv8 ? g->ks + cb * g->KV : nullptr;
+        float* vs0 = g->kv8 ? g->vs + cb * g->KV : nullptr;
+        float *kc = kc0, *vc = vc0, *ks = ks0, *vs = vs0;
+        int8_t *kq = kq0, *vq = vq0;
         const dim3 ag((unsigned)H, (unsigned)m);
         const size_t lds = gm_attn_lds(g);
         const int ps = (int)gm_pstride(g), sl = (g->arch == 0 && l % 2 == 0) ? 1 : 0, win = (int)g->window;
@@ -1510,44 +1533,55 @@ int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_o
         const float* qn = g->qn_of(l);
         const float* kn = g->kn_of(l);
         const int div = g->arch == 1;
-        if (m == 1 && g->cap_pos > 512) {  // long caches: the three-launch decode attention
+        if ((m == 1 || batch) && g->cap_pos > 512) {  // long caches: the three-launch decode attention
+          for (size_t bi = 0; bi < m; ++bi) {  // (a batch: each sequence in turn, on its own cache)
             const int hd4 = (hd + 3) & ~3;
             const size_t plds = (size_t)2 * hd4 * sizeof(float);
             const dim3 sg((unsigned)H, (unsigned)((g->cap_pos + GT - 1) / GT));
             const size_t vlds = ((size_t)2 * ps + seq_sum_spec_scratch(GT)) * sizeof(float);
+            float* qkvr = g->qkvb + bi * (H + 2 * KV) * hd;
+            float* attr = g->att + bi * H * hd;
+            float* kc = kc0 ? kc0 + bi * bst : nullptr;
+            float* vc = vc0 ? vc0 + bi * bst : nullptr;
+            int8_t* kq = kq0 ? kq0 + bi * bst : nullptr;
+            int8_t* vq = vq0 ? vq0 + bi * bst : nullptr;
+            float* ks = ks0 ? ks0 + bi * (bst / hd) : nullptr;
+            float* vs = vs0 ? vs0 + bi * (bst / hd) : nullptr;
             if (g->kv8) {
                 gm_dec_prep_kernel<true><<<dim3((unsigned)(H + KV)), dim3(GT), plds, s>>>(
-                    g->qkvb, H, KV, hd, g->cur, g->cs, kc, vc, kq, vq, ks, vs, qb, qn, kn, g->eps, g->qr);
+                    qkvr, H, KV, hd, g->cur, g->cs, kc, vc, kq, vq, ks, vs, qb, qn, kn, g->eps, g->qr);
                 gm_dec_score_kernel<true><<<sg, dim3(GT), hd4 * sizeof(float), s>>>(
                     g->qr, H, KV, hd, g->cur, kc, kq, ks, g->qscale, g->cap, sl, win, div, ps, g->sc);
-                const hipError_t er = launch_value_ring(g, sl, win, ps, vc, vq, vs, s);
+                const hipError_t er = launch_value_ring(g, sl, win, ps, vc, vq, vs, attr, s);
                 if (er == hipErrorNotSupported)
                     gm_dec_value_kernel<true><<<dim3((unsigned)H), dim3(GT), vlds, s>>>(g->sc, H, KV, hd, g->cur, vc,
-                                                                                        vq, vs, sl, win, ps, g->att);
+                                                                                        vq, vs, sl, win, ps, attr);
                 else
                     GMCHK(er, "launch value ring");
             } else {
                 gm_dec_prep_kernel<false><<<dim3((unsigned)(H + KV)), dim3(GT), plds, s>>>(
-                    g->qkvb, H, KV, hd, g->cur, g->cs, kc, vc, kq, vq, ks, vs, qb, qn, kn, g->eps, g->qr);
+                    qkvr, H, KV, hd, g->cur, g->cs, kc, vc, kq, vq, ks, vs, qb, qn, kn, g->eps, g->qr);
                 gm_dec_score_kernel<false><<<sg, dim3(GT), hd4 * sizeof(float), s>>>(
                     g->qr, H, KV, hd, g->cur, kc, kq, ks, g->qscale, g->cap, sl, win, div, ps, g->sc);
-                const hipError_t er = launch_value_ring(g, sl, win, ps, vc, vq, vs, s);
+                const hipError_t er = launch_value_ring(g, sl, win, ps, vc, vq, vs, attr, s);
                 if (er == hipErrorNotSupported)
                     gm_dec_value_kernel<false><<<dim3((unsigned)H), dim3(GT), vlds, s>>>(g->sc, H, KV, hd, g->cur,
                                                                                          vc, vq, vs, sl, win, ps,
-                                                                                         g->att);
+                                                                                         attr);
                 else
                     GMCHK(er, "launch value ring");
             }
-        } else if (m == 1) {
+          }
+        } else if (m == 1 || batch) {
+            const long long bs = batch ? (long long)bst : 0;
             if (g->kv8)
                 gm_attn_kernel<true, true><<<ag, dim3(GT), lds, s>>>(g->qkvb, H, KV, hd, g->cur, g->cs, kc, vc, kq,
                                                                      vq, ks, vs, g->qscale, g->cap, sl, win, ps,
-                                                                     g->att, div, qb, qn, kn, g->eps);
+                                                                     g->att, div, qb, qn, kn, g->eps, bs);
             else
                 gm_attn_kernel<false, true><<<ag, dim3(GT), lds, s>>>(g->qkvb, H, KV, hd, g->cur, g->cs, kc, vc, kq,
                                                                       vq, ks, vs, g->qscale, g->cap, sl, win, ps,
-                                                                      g->att, div, qb, qn, kn, g->eps);
+                                                                      g->att, div, qb, qn, kn, g->eps, bs);
         } else {
             if (g->kv8)
                 gm_qkv_kernel<true><<<dim3((unsigned)m), dim3(GT), 0, s>>>(g->qkvb, H, KV, hd, g->cur, g->cs, kc, vc,
@@ -1581,10 +1615,9 @@ int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_o
                                                                        g->eps);
         }
         GMCHK(hipGetLastError(), "launch attention");
-        if (int rc = gm_mm(c, g->o[l], g->att, m, g->ob)) return rc;
-        const bool qg = q8d && is_i8(g->gu[l]);
-        GMCHK(norm(g->ob, g->post_of(l, 1), g->norm_of(l, 2), (int)m, 0, qg), "launch norm");
-        if (int rc = mm_a(g->gu[l], qg, g->gub)) return rc;
+        if (int rc = mm(g->o[l], g->att, g->ob)) return rc;
+        GMCHK(norm(g->ob, g->post_of(l, 1), g->norm_of(l, 2), (int)m, 0), "launch norm");
+        if (int rc = mm(g->gu[l], g->a, g->gub)) return rc;
         const float gc = sqrtf(2.0f / 3.14159274101257324f);
         if (q8f && is_i8(g->down[l])) {  // act(gate) * up and its quant in one kernel
             const Q8 q = gm_q8(g, 1, g->ffn);
@@ -1595,18 +1628,25 @@ int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_o
             gm_geglu_kernel<<<dim3((unsigned)std::min<size_t>((tot + GT - 1) / GT, 4096)), dim3(GT), 0, s>>>(
                 g->gub, ffn, tot, gc, g->hm, g->arch == 1 ? 1 : 0);
             GMCHK(hipGetLastError(), "launch geglu");
-            if (int rc = gm_mm(c, g->down[l], g->hm, m, g->ob)) return rc;
+            if (int rc = mm(g->down[l], g->hm, g->ob)) return rc;
         }
         if (l + 1 < g->L)
-            GMCHK(norm(g->ob, g->post_of(l, 3), g->norm_of(l + 1, 0), (int)m, 0, q8d && is_i8(g->qkv[l + 1])),
-                  "launch norm");
+            GMCHK(norm(g->ob, g->post_of(l, 3), g->norm_of(l + 1, 0), (int)m, 0), "launch norm");
+        else if (batch)  // every sequence's row feeds the head
+            GMCHK(norm(g->ob, g->post_of(l, 3), g->final_norm(), (int)m, 0), "launch norm");
         else  // only the last row feeds the head
-            GMCHK(norm(g->ob, g->post_of(l, 3), g->final_norm(), 1, (int)m - 1, false), "launch norm");
+            GMCHK(norm(g->ob, g->post_of(l, 3), g->final_norm(), 1, (int)m - 1), "launch norm");
     }
     float* lg = logits_out ? logits_out : g->logits;
     const Weight& ut = g->unembed ? *weight_of(g->unembed) : et;
-    GMCHK(launch_rowdot_argmax(ut, g->a + (m - 1) * g->d, lg, g->best, ctx_err(c), s), "launch unembed");
-    gm_argmax_done_kernel<<<dim3(1), dim3(64), 0, s>>>(g->best, g->cur, (int)m, P, g->tok);
+    if (batch) {
+        GMCHK(launch_rowdot_argmax_batch(ut, m, g->a, g->d, lg, logits_out ? los : g->vocab, g->best, err, s),
+              "launch unembed");
+        gm_argmax_batch_kernel<<<dim3(1), dim3(64), 0, s>>>(g->best, g->cur, (int)m, P, g->tok, (int)g->cap_pos);
+    } else {
+        GMCHK(launch_rowdot_argmax(ut, g->a + (m - 1) * g->d, lg, g->best, err, s), "launch unembed");
+        gm_argmax_done_kernel<<<dim3(1), dim3(64), 0, s>>>(g->best, g->cur, (int)m, P, tokp);
+    }
     GMCHK(hipGetLastError(), "launch argmax");
     return FRQ_OK;
 }
@@ -1653,6 +1693,71 @@ int gm_run(frq_ctx* c, frq_gemma* g, const int64_t* prompt, size_t P, size_t n_n
     GMCHK(hipMemcpyAsync(out, g->tok, n_new * sizeof(int64_t), hipMemcpyDeviceToHost, s), "hipMemcpyAsync(tokens)");
     if (logits)
         GMCHK(hipMemcpyAsync(logits, lgd, n_new * g->vocab * sizeof(float), hipMemcpyDeviceToHost, s),
+              "hipMemcpyAsync(logits)");
+    return frq_sync(c);
+}
+
+// nb sequences (prompts nb x P), each its own Model::generate: every
+// sequence prefilled alone on its own cache, then the decode steps of all nb
+// at once, row i of a step being sequence i's.  Tokens out (nb x n_new),
+// logits (nb x n_new x vocab) as nb calls of gm_run give them.
+int gm_run_batch(frq_ctx* c, frq_gemma* g, const int64_t* prompts, size_t nb, size_t P, size_t n_new, int64_t* out,
+                 float* logits) {
+    if (!c || !g) return set_error(FRQ_ERR_ARG, "null context / model");
+    if (ctx_device(c) != g->device) return set_error(FRQ_ERR_ARG, "model lives on another device");
+    if (!nb || !P || !n_new) return set_error(FRQ_ERR_ARG, "no sequence, empty prompt or no tokens asked for");
+    if (!prompts || !out) return set_error(FRQ_ERR_ARG, "null prompts / output");
+    if (nb > 65535) return set_error(FRQ_ERR_ARG, "too many sequences");
+    for (size_t i = 0; i < nb * P; ++i)
+        if (prompts[i] < 0 || (size_t)prompts[i] >= g->vocab)
+            return set_error(FRQ_ERR_ARG, "token id " + std::to_string(prompts[i]) + " beyond the vocabulary");
+    GDev dv(g->device);
+    if (int rc = gm_reserve(c, g, P + n_new, std::max(P, nb), nb)) return rc;
+    hipStream_t s = (hipStream_t)frq_get_stream(c);
+    const size_t V = g->vocab;
+    float* lgd = nullptr;
+    if (logits) GMCHK(hipMalloc(&lgd, nb * n_new * V * sizeof(float)), "hipMalloc(logits)");
+    struct Free {
+        float* p;
+        ~Free() { if (p) (void)hipFree(p); }
+    } fr{lgd};
+    struct Seq0 {  // one-sequence calls of gm_block use sequence seq
+        frq_gemma* g;
+        ~Seq0() { g->seq = 0; }
+    } sq{g};
+    for (size_t b = 0; b < nb; ++b) {
+        g->seq = b;
+        GMCHK(hipMemcpyAsync(g->ids, prompts + b * P, P * sizeof(int64_t), hipMemcpyHostToDevice, s),
+              "hipMemcpyAsync(prompt)");
+        GMCHK(hipMemsetAsync(g->cur, 0, sizeof(int), s), "hipMemsetAsync(cur)");
+        if (int rc = gm_block(c, g, P, 0, (int)P, lgd ? lgd + b * n_new * V : nullptr)) return rc;
+    }
+    g->seq = 0;
+    const int B = (int)nb;
+    if (g->graphs && !logits && n_new > 2 && s != nullptr) {
+        hipGraph_t gr = nullptr;
+        hipGraphExec_t ex = nullptr;
+        GMCHK(hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed), "hipStreamBeginCapture");
+        const int rc = gm_block(c, g, nb, 1, (int)P, nullptr, B, 0);
+        const hipError_t e = hipStreamEndCapture(s, &gr);
+        if (rc) { if (gr) (void)hipGraphDestroy(gr); return rc; }
+        GMCHK(e, "hipStreamEndCapture");
+        const hipError_t ei = hipGraphInstantiate(&ex, gr, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(gr);
+        GMCHK(ei, "hipGraphInstantiate");
+        hipError_t el = hipSuccess;
+        for (size_t t = 1; t < n_new && el == hipSuccess; ++t) el = hipGraphLaunch(ex, s);
+        (void)hipGraphExecDestroy(ex);
+        GMCHK(el, "hipGraphLaunch");
+    } else {
+        for (size_t t = 1; t < n_new; ++t)
+            if (int rc = gm_block(c, g, nb, 1, (int)P, lgd ? lgd + t * V : nullptr, B, n_new * V)) return rc;
+    }
+    GMCHK(hipMemcpy2DAsync(out, n_new * sizeof(int64_t), g->tok, g->cap_pos * sizeof(int64_t),
+                           n_new * sizeof(int64_t), nb, hipMemcpyDeviceToHost, s),
+          "hipMemcpy2DAsync(tokens)");
+    if (logits)
+        GMCHK(hipMemcpyAsync(logits, lgd, nb * n_new * V * sizeof(float), hipMemcpyDeviceToHost, s),
               "hipMemcpyAsync(logits)");
     return frq_sync(c);
 }
@@ -1872,6 +1977,11 @@ int frq_seq_fold_f32(frq_ctx* c, const float* x, size_t rows, size_t n, float in
     GMCHK(hipMemcpyAsync(out, dx + rows * n, rows * sizeof(float), hipMemcpyDeviceToHost, s), "hipMemcpyAsync");
     GMCHK(hipStreamSynchronize(s), "hipStreamSynchronize");
     return FRQ_OK;
+}
+
+int frq_gemma_generate_batch(frq_ctx* c, frq_gemma* g, const int64_t* prompts, size_t nb, size_t n_prompt,
+                             size_t n_new, int64_t* out, float* logits) {
+    return gm_run_batch(c, g, prompts, nb, n_prompt, n_new, out, logits);
 }
 
 }  // extern "C"

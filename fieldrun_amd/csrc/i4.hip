@@ -155,6 +155,92 @@ __global__ __launch_bounds__(256) void i4_gemv_terms(const uint8_t* __restrict__
     for (int r = threadIdx.x; r < nr; r += 256) out[r0 + r] = lds_seq_sum(cg + r * ngp, ng, 0.0f);
 }
 
+// M independent rows (M <= 16), each in the M == 1 order (i4_dot_avx2): the
+// decode of a batch of sequences, where every sequence is its own
+// Gemma::generate.  A workgroup owns 16 weight rows; K goes in slices of 16
+// groups: the 16 token rows' activations of the slice are staged in LDS
+// (32-float units padded to 36 against bank conflicts), a thread takes one
+// (row, group) item, reads its nibbles once (the next slice's ahead) and
+// forms every token's group term scale * gsum in the AVX2 lane order, and
+// the thread of (token t, row r) then adds the slice's terms to its running
+// sum in group order (16 / G4 groups a slice, so the staged activations
+// take the same LDS for either group size).  Needs K % 32 == 0 and g == 32 G4.
+template <int G4>
+__global__ __launch_bounds__(256) void i4_terms_rows(const uint8_t* __restrict__ packed,
+                                                     const uint16_t* __restrict__ scale, int N, int K,
+                                                     const float* __restrict__ a, int M, float* __restrict__ out) {
+    constexpr int MT = 16, RB = 16, S = 16 / G4, U = 36;  // tokens, rows, groups a slice, floats a 32-unit
+    constexpr int g = 32 * G4, UPT = S * G4;          // 32-units of a token's slice
+    __shared__ __attribute__((aligned(16))) float act[MT][UPT * U];
+    __shared__ float term[MT][RB][S + 1];
+    const int tid = threadIdx.x, ng = K / g, pitch = K / 2, r0 = blockIdx.x * RB;
+    const int rr = tid / S, gl = tid % S;          // this thread's item: row r0 + rr, group sl S + gl
+    const int st = tid / RB, sr = tid % RB;        // this thread's sum: token st, row r0 + sr
+    const int row = min(r0 + rr, N - 1);           // clamped: the loads stay unconditional
+    const int nsl = (ng + S - 1) / S;
+    auto fetch = [&](int sl, uint4 (&w)[G4], float& sc) {
+        const int gi = min(sl * S + gl, ng - 1);
+        const uint8_t* pg = packed + (size_t)row * pitch + (size_t)gi * 16 * G4;
+#pragma unroll
+        for (int h = 0; h < G4; ++h) w[h] = *reinterpret_cast<const uint4*>(pg + 16 * h);
+        sc = h2f(scale[(size_t)row * ng + gi]);
+    };
+    uint4 wn[G4];
+    float sn;
+    fetch(0, wn, sn);
+    float sum = 0.0f;
+    for (int sl = 0; sl < nsl; ++sl) {
+        const int k0 = sl * S * g, kl = min(S * g, K - k0);  // this slice's k range
+        // stage the M token rows' k0 .. k0 + kl (float4 at a time)
+        for (int i = tid; i < MT * (S * g / 4); i += 256) {
+            const int t = i / (S * g / 4), q = i % (S * g / 4);
+            if (t < M && 4 * q < kl)
+                *reinterpret_cast<float4*>(&act[t][(4 * q) / 32 * U + (4 * q) % 32]) =
+                    *reinterpret_cast<const float4*>(a + (size_t)t * K + k0 + 4 * q);
+        }
+        uint4 wc[G4];
+#pragma unroll
+        for (int h = 0; h < G4; ++h) wc[h] = wn[h];
+        const float sc = sn;
+        if (sl + 1 < nsl) fetch(sl + 1, wn, sn);
+        __syncthreads();
+        const bool item = rr < RB && sl * S + gl < ng;
+        if (item) {
+            float wf[G4][32];
+#pragma unroll
+            for (int h = 0; h < G4; ++h) {
+                const uint32_t ws[4] = {wc[h].x, wc[h].y, wc[h].z, wc[h].w};
+#pragma unroll
+                for (int e = 0; e < 32; ++e) wf[h][e] = (float)((int)(ws[e / 8] << (28 - 4 * (e % 8))) >> 28);
+            }
+            for (int t = 0; t < M; ++t) {
+                float l[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+                for (int h = 0; h < G4; ++h) {
+                    const float* ab = &act[t][(gl * G4 + h) * U];
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const float4 a0 = *reinterpret_cast<const float4*>(ab + 8 * c);
+                        const float4 a1 = *reinterpret_cast<const float4*>(ab + 8 * c + 4);
+                        const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+                        for (int q = 0; q < 8; ++q) l[q] = __builtin_fmaf(wf[h][8 * c + q], av[q], l[q]);
+                    }
+                }
+                const float q0 = l[0] + l[4], q1 = l[1] + l[5], q2 = l[2] + l[6], q3 = l[3] + l[7];
+                term[t][rr][gl] = sc * ((q0 + q2) + (q1 + q3));
+            }
+        }
+        __syncthreads();
+        if (st < M) {
+            const int ns = min(S, ng - sl * S);
+            for (int j = 0; j < ns; ++j) sum = sum + term[st][sr][j];
+        }
+        __syncthreads();
+    }
+    if (st < M && r0 + sr < N) out[(size_t)st * N + r0 + sr] = sum;
+}
+
 // M > 1: dequantise w = s4 * scale (f32, exact) and run a sequential-k FMA
 // chain per output (the oracle's sgemm order).  One thread per column j and
 // up to 16 token rows; the token rows' activations are uniform across the
@@ -802,6 +888,23 @@ hipError_t launch_i4_terms(const Weight& w, const float* a, float* out, hipStrea
     else
         i4_gemv_terms<2><<<dim3(grid), dim3(256), cgb + asb, s>>>(w.q4raw, w.s4raw, (int)w.n, (int)w.k, rb, a, out);
     return hipGetLastError();
+}
+
+// m rows, each in the M == 1 order (bit-identical to m launches at M == 1).
+hipError_t launch_i4_m1_rows(const Weight& w, size_t m, const float* a, float* out, hipStream_t s) {
+    if (m == 0 || w.n == 0) return hipSuccess;
+    if (m <= 16 && w.k % 32 == 0 && (w.g == 32 || w.g == 64) && ((uintptr_t)a & 15) == 0 &&
+        w.k <= (size_t)INT32_MAX && w.n <= (size_t)INT32_MAX) {
+        const unsigned grid = (unsigned)((w.n + 15) / 16);
+        if (w.g == 32)
+            i4_terms_rows<1><<<dim3(grid), dim3(256), 0, s>>>(w.q4raw, w.s4raw, (int)w.n, (int)w.k, a, (int)m, out);
+        else
+            i4_terms_rows<2><<<dim3(grid), dim3(256), 0, s>>>(w.q4raw, w.s4raw, (int)w.n, (int)w.k, a, (int)m, out);
+        return hipGetLastError();
+    }
+    for (size_t i = 0; i < m; ++i)
+        if (hipError_t e = launch_i4_exact(w, 1, a + i * w.k, out + i * w.n, s)) return e;
+    return hipSuccess;
 }
 
 hipError_t launch_i4_exact(const Weight& w, size_t m, const float* a, float* out, hipStream_t s) {

@@ -43,12 +43,15 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int row) {
     return ((unsigned long long)u << 32) | (uint32_t)row;
 }
 
-template <int DT, bool SUB, int DEPTH, int WPB, bool ARG>  // DT: 0 f32, 1 f16, 2 rowi8; DEPTH chunks in
-                                                          // registers; WPB waves per block
+// NX x vectors at once (x + v xs, outputs out + v os, argmax best[v]): each
+// lane runs NX chains of its row, one per vector, so the table streams once
+// for all of them; every chain is the one-vector order.
+template <int DT, bool SUB, int DEPTH, int WPB, bool ARG, int NX = 1>  // DT: 0 f32, 1 f16, 2 rowi8; DEPTH
+                                                                      // chunks in registers; WPB waves
 __global__ __launch_bounds__(64 * WPB) void rowdot_kernel(
     const uint8_t* __restrict__ W, const float* __restrict__ rs, int rows, int d, size_t pitch,
     const float* __restrict__ x, const int64_t* __restrict__ cand, int nout, float* __restrict__ out,
-    unsigned long long* __restrict__ best, int* __restrict__ err) {
+    unsigned long long* __restrict__ best, int* __restrict__ err, size_t xs = 0, size_t os = 0) {
     constexpr int ES = DT == 0 ? 4 : (DT == 1 ? 2 : 1);  // bytes per element
     constexpr int CE = 128 / ES;                         // elements per chunk
     __shared__ __attribute__((aligned(16))) uint8_t tile[WPB][64 * TP];
@@ -82,8 +85,14 @@ __global__ __launch_bounds__(64 * WPB) void rowdot_kernel(
     const int own_row = row_of(o0 + lane, own_ok);
 
     const int nch = (int)(pitch / 128);
-    float acc = -0.0f;  // the fold (f32, f16, subset rowi8)
-    float l8[8] = {0, 0, 0, 0, 0, 0, 0, 0};  // the AVX2 lanes (full rowi8)
+    float acc[NX];  // the fold (f32, f16, subset rowi8)
+    float l8[NX][8];  // the AVX2 lanes (full rowi8)
+#pragma unroll
+    for (int v = 0; v < NX; ++v) {
+        acc[v] = -0.0f;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) l8[v][q] = 0.0f;
+    }
     auto load = [&](uint4 (&b)[8], int c) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) b[i] = ntload16u(src[i] + (size_t)c * 128);
@@ -95,16 +104,27 @@ __global__ __launch_bounds__(64 * WPB) void rowdot_kernel(
         if constexpr (DT == 0) {
 #pragma unroll
             for (int e = 0; e < CE; ++e)
-                if (!CHECK || k0 + e < d) acc = acc + __builtin_bit_cast(float, v[e]) * x[k0 + e];
+                if (!CHECK || k0 + e < d) {
+                    const float w = __builtin_bit_cast(float, v[e]);
+#pragma unroll
+                    for (int u = 0; u < NX; ++u) acc[u] = acc[u] + w * x[u * xs + k0 + e];
+                }
         } else if constexpr (DT == 1) {
 #pragma unroll
             for (int e = 0; e < CE; ++e)
-                if (!CHECK || k0 + e < d) acc = acc + h2f((uint16_t)(v[e >> 1] >> (16 * (e & 1)))) * x[k0 + e];
+                if (!CHECK || k0 + e < d) {
+                    const float w = h2f((uint16_t)(v[e >> 1] >> (16 * (e & 1))));
+#pragma unroll
+                    for (int u = 0; u < NX; ++u) acc[u] = acc[u] + w * x[u * xs + k0 + e];
+                }
         } else if constexpr (SUB) {
 #pragma unroll
             for (int e = 0; e < CE; ++e)
-                if (!CHECK || k0 + e < d)
-                    acc = acc + (float)(int8_t)(v[e >> 2] >> (8 * (e & 3))) * x[k0 + e];
+                if (!CHECK || k0 + e < d) {
+                    const float w = (float)(int8_t)(v[e >> 2] >> (8 * (e & 3)));
+#pragma unroll
+                    for (int u = 0; u < NX; ++u) acc[u] = acc[u] + w * x[u * xs + k0 + e];
+                }
         } else {
             // full 8-element groups only; the tail follows the lane sum
 #pragma unroll
@@ -112,8 +132,11 @@ __global__ __launch_bounds__(64 * WPB) void rowdot_kernel(
                 const int kb = k0 + 8 * gi;
                 if (!CHECK || kb + 8 <= d) {
 #pragma unroll
-                    for (int q = 0; q < 8; ++q)
-                        l8[q] = __builtin_fmaf((float)(int8_t)(v[2 * gi + (q >> 2)] >> (8 * (q & 3))), x[kb + q], l8[q]);
+                    for (int q = 0; q < 8; ++q) {
+                        const float w = (float)(int8_t)(v[2 * gi + (q >> 2)] >> (8 * (q & 3)));
+#pragma unroll
+                        for (int u = 0; u < NX; ++u) l8[u][q] = __builtin_fmaf(w, x[u * xs + kb + q], l8[u][q]);
+                    }
                 }
             }
         }
@@ -136,14 +159,21 @@ __global__ __launch_bounds__(64 * WPB) void rowdot_kernel(
         else run(v, k0, std::true_type{});
         if constexpr (DT == 2 && !SUB) {
             if (c == nch - 1) {
-                const float q0 = l8[0] + l8[4], q1 = l8[1] + l8[5], q2 = l8[2] + l8[6], q3 = l8[3] + l8[7];
-                acc = (q0 + q2) + (q1 + q3);
+#pragma unroll
+                for (int u = 0; u < NX; ++u) {
+                    const float q0 = l8[u][0] + l8[u][4], q1 = l8[u][1] + l8[u][5];
+                    const float q2 = l8[u][2] + l8[u][6], q3 = l8[u][3] + l8[u][7];
+                    acc[u] = (q0 + q2) + (q1 + q3);
+                }
                 const int kt = d & ~7;  // the tail lies in this chunk
                 if (kt < d) {
 #pragma unroll
                     for (int e = 0; e < CE; ++e)
-                        if (k0 + e >= kt && k0 + e < d)
-                            acc = acc + (float)(int8_t)(v[e >> 2] >> (8 * (e & 3))) * x[k0 + e];
+                        if (k0 + e >= kt && k0 + e < d) {
+                            const float w = (float)(int8_t)(v[e >> 2] >> (8 * (e & 3)));
+#pragma unroll
+                            for (int u = 0; u < NX; ++u) acc[u] = acc[u] + w * x[u * xs + k0 + e];
+                        }
                 }
             }
         }
@@ -177,22 +207,26 @@ __global__ __launch_bounds__(64 * WPB) void rowdot_kernel(
             }
         }
     }
-    if constexpr (DT == 2) {
-        if (!SUB && nch == 0) acc = 0.0f;  // d == 0: hsum of zero lanes
-        acc = rs[own_row] * acc;
-    }
     const int o = o0 + lane;
-    if (o < nout) out[o] = own_ok ? acc : -__builtin_inff();
-    if constexpr (ARG) {
-        unsigned long long key = o < nout ? argmax_key(acc, o) : 0ull;
-        const bool nan = o < nout && acc != acc;
 #pragma unroll
-        for (int sh = 32; sh > 0; sh >>= 1) {
-            const unsigned long long ok = __shfl_xor(key, sh);
-            key = ok > key ? ok : key;
+    for (int u = 0; u < NX; ++u) {
+        float a = acc[u];
+        if constexpr (DT == 2) {
+            if (!SUB && nch == 0) a = 0.0f;  // d == 0: hsum of zero lanes
+            a = rs[own_row] * a;
         }
-        if (__builtin_amdgcn_ballot_w64(nan) && lane == 0) atomicOr(err, 1);
-        if (lane == 0) atomicMax(best, key);
+        if (o < nout) out[u * os + o] = own_ok ? a : -__builtin_inff();
+        if constexpr (ARG) {
+            unsigned long long key = o < nout ? argmax_key(a, o) : 0ull;
+            const bool nan = o < nout && a != a;
+#pragma unroll
+            for (int sh = 32; sh > 0; sh >>= 1) {
+                const unsigned long long ok = __shfl_xor(key, sh);
+                key = ok > key ? ok : key;
+            }
+            if (__builtin_amdgcn_ballot_w64(nan) && lane == 0) atomicOr(err, 1);
+            if (lane == 0) atomicMax(best + u, key);
+        }
     }
 }
 
@@ -217,7 +251,55 @@ hipError_t launch_dt(const Weight& w, const float* x, const int64_t* cand, size_
     return hipGetLastError();
 }
 
+template <int DT, int NX>
+hipError_t launch_argmax_nx(const Weight& w, const float* x, size_t xs, float* out, size_t os,
+                            unsigned long long* best, int* err, hipStream_t s) {
+    const unsigned g4 = (unsigned)((w.n + 255) / 256);
+    rowdot_kernel<DT, false, 2, 4, true, NX><<<dim3(g4), dim3(256), 0, s>>>(
+        w.rowp, w.scale, (int)w.n, (int)w.k, w.rpitch, x, nullptr, (int)w.n, out, best, err, xs, os);
+    return hipGetLastError();
+}
+
+template <int DT>
+hipError_t launch_argmax_batch(const Weight& w, size_t nx, const float* x, size_t xs, float* out, size_t os,
+                               unsigned long long* best, int* err, hipStream_t s) {
+    // up to 16 vectors a pass (each a chain per lane), further passes for more
+    for (size_t v0 = 0; v0 < nx; v0 += 16) {
+        const size_t k = nx - v0 < 16 ? nx - v0 : 16;
+        const float* xv = x + v0 * xs;
+        float* ov = out + v0 * os;
+        hipError_t e;
+        switch (k) {
+            case 1: e = launch_argmax_nx<DT, 1>(w, xv, xs, ov, os, best + v0, err, s); break;
+            case 2: e = launch_argmax_nx<DT, 2>(w, xv, xs, ov, os, best + v0, err, s); break;
+            case 4: e = launch_argmax_nx<DT, 4>(w, xv, xs, ov, os, best + v0, err, s); break;
+            case 8: e = launch_argmax_nx<DT, 8>(w, xv, xs, ov, os, best + v0, err, s); break;
+            case 16: e = launch_argmax_nx<DT, 16>(w, xv, xs, ov, os, best + v0, err, s); break;
+            default:  // other counts: one vector at a time
+                e = hipSuccess;
+                for (size_t u = 0; u < k && e == hipSuccess; ++u)
+                    e = launch_argmax_nx<DT, 1>(w, xv + u * xs, xs, ov + u * os, os, best + v0 + u, err, s);
+        }
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
 }  // namespace
+
+// rowdot_f32 with the argmax fold for nx vectors x + v xs at once (outputs
+// out + v os, best[v]); each output's arithmetic is launch_rowdot_argmax's.
+hipError_t launch_rowdot_argmax_batch(const Weight& w, size_t nx, const float* x, size_t xs, float* out, size_t os,
+                                      unsigned long long* best, int* err, hipStream_t s) {
+    if (!w.n || !nx) return hipSuccess;
+    if (w.n > (size_t)INT32_MAX - 256 || w.k > (size_t)INT32_MAX) return hipErrorInvalidValue;
+    switch (w.dtype) {
+        case FRQ_DT_F32: return launch_argmax_batch<0>(w, nx, x, xs, out, os, best, err, s);
+        case FRQ_DT_F16: return launch_argmax_batch<1>(w, nx, x, xs, out, os, best, err, s);
+        case FRQ_DT_ROWI8: return launch_argmax_batch<2>(w, nx, x, xs, out, os, best, err, s);
+        default: return hipErrorInvalidValue;
+    }
+}
 
 size_t row_pitch(int dtype, size_t d) {
     const size_t es = dtype == FRQ_DT_F32 ? 4 : (dtype == FRQ_DT_F16 ? 2 : 1);

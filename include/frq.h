@@ -298,6 +298,15 @@ int frq_gemma_generate(frq_ctx* ctx, frq_gemma* g, const int64_t* prompt, size_t
 int frq_gemma_predict(frq_ctx* ctx, frq_gemma* g, const int64_t* ids, size_t n, int64_t* token,
                       float* logits);
 int frq_gemma_set_graphs(frq_gemma* g, int on);
+/* nb sequences at once (configs[2]'s batch 16): prompts (nb, n_prompt),
+ * each sequence its own Model::generate (src/gemma.rs:403-431; the reference
+ * has no batched generate, a batch is nb independent calls): out (nb, n_new)
+ * and logits (nb, n_new, vocab), nullable, are what nb calls of
+ * frq_gemma_generate give, bit for bit.  Each sequence has its own KV cache;
+ * the decode steps of all nb run together (the weights stream once a step,
+ * every row of an int4 linear in the M == 1 order of i4_dot_avx2). */
+int frq_gemma_generate_batch(frq_ctx* ctx, frq_gemma* g, const int64_t* prompts, size_t nb, size_t n_prompt,
+                             size_t n_new, int64_t* out, float* logits);
 /* Rope::new (src/rope.rs:56-64) over an arch "rope" bundle (Llama / Qwen2.5
  * / Qwen3 / Mistral: config [n_layer, H, nkv, hd, d, ffn, vocab, tied],
  * config_f [theta, eps]; arrays as convert_rope writes them,

@@ -8,11 +8,13 @@ configs[4]: Qwen2.5-7B-shaped int8, all 28 layers, the 2048-token prompt
 (the engine's MFMA prefill with the exact epilogue, grouped prefill
 attention over 2048 rows) and 128 greedy tokens (long-cache decode to 2175
 positions).  configs[2]: Gemma-2-2b-shaped int4, the 64-token prompt and
-256 greedy tokens, batch 1."""
+256 greedy tokens, batch 1, and batch 16 (sixteen prompts decoded together,
+each sequence against its own oracle generate)."""
 import os
 import sys
 import tempfile
 
+import numpy as np
 import pytest
 
 import fieldrun_amd as fa
@@ -27,7 +29,7 @@ def shm():
     return "/dev/shm" if os.path.isdir("/dev/shm") else None
 
 
-@pytest.mark.parametrize("name,engine", [("config4", fa.Rope), ("config2", fa.Gemma)])
+@pytest.mark.parametrize("name,engine", [("config4", fa.Rope), ("config2", fa.Gemma), ("config2_b16", fa.Gemma)])
 def test_config_full_length_vs_fixture(ctx, name, engine):
     fx = cfx.load_fixture(name)
     assert fx is not None, f"tests/golden/{name}.json missing: run tests/golden/make_config_fixtures.py"
@@ -37,10 +39,17 @@ def test_config_full_length_vs_fixture(ctx, name, engine):
         wl["write"](stem)
         b = fa.Bundle(stem, ctx)
         g = engine(b)
-        for seq, prompt in zip(fx["sequences"], wl["prompts"]()):
-            toks, lg = g.generate(prompt, fx["n_new"], with_logits=True)
-            same_tok, bad = cfx.compare(seq, toks, lg)
-            assert same_tok, "tokens differ"
-            assert bad is None, f"logits row {bad} differs"
+        prompts = wl["prompts"]()
+        if len(prompts) == 1:
+            toks, lg = g.generate(prompts[0], fx["n_new"], with_logits=True)
+            toks, lg = toks[None], lg[None]
+        else:  # the batch decode: every sequence its own generate
+            toks, lg = g.generate_batch(np.stack(prompts), fx["n_new"], with_logits=True)
+            g.set_graphs(True)
+            assert np.array_equal(g.generate_batch(np.stack(prompts), fx["n_new"]), toks)
+        for i, seq in enumerate(fx["sequences"]):
+            same_tok, bad = cfx.compare(seq, toks[i], lg[i])
+            assert same_tok, f"sequence {i}: tokens differ"
+            assert bad is None, f"sequence {i}: logits row {bad} differs"
         g.free()
         b.close()

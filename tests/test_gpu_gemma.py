@@ -172,3 +172,57 @@ def test_gemma_cache_past_64k_of_scores(ctx, tmp_path):
     assert same_bits(lg, rlg), first_diff(lg, rlg)
     g.free()
     b.close()
+
+
+@pytest.mark.parametrize("kv_int8", [False, True])
+def test_gemma_batch_matches_single_sequences(ctx, small, kv_int8):
+    """configs[2]'s batch decode: each row of a batch is its own
+    Gemma::generate (the reference has no batched generate), so the batch
+    gives, bit for bit, the tokens and logits of one call a sequence, and of
+    the oracle (int4 rows in i4_dot_avx2's order, q4a / int8 rows as at
+    M == 1); the captured-graph batch decode gives the same tokens."""
+    m, arrs = oracle.read_bundle(small)
+    ref = oracle.Gemma(m, arrs, nthreads=8)
+    b = fa.Bundle(small, ctx)
+    g = fa.Gemma(b, kv_int8)
+    prompts = np.stack([synth.gpt2_prompt(5, 500, 40 + i) for i in range(5)])
+    toks, lg = g.generate_batch(prompts, 12, with_logits=True)
+    for i in range(len(prompts)):
+        t1, l1 = g.generate(prompts[i], 12, with_logits=True)
+        assert np.array_equal(toks[i], t1), i
+        assert same_bits(lg[i], l1), (i, first_diff(lg[i], l1))
+        rt, rlg = ref.generate(prompts[i], 12, kv_int8=kv_int8, with_logits=True)
+        assert np.array_equal(toks[i], rt) and same_bits(lg[i], rlg), i
+    g.set_graphs(True)
+    assert np.array_equal(g.generate_batch(prompts, 12), toks)
+    g.free()
+    b.close()
+
+
+def test_gemma_batch_long_cache_and_sixteen_rows(ctx, tmp_path):
+    """A batch of 16 sequences (the int4 linears' widest batch in one pass)
+    past 512 positions (the long-cache attention, a sequence at a time)."""
+    stem = str(tmp_path / "g")
+    synth.write_gemma2_bundle(stem, 23, n_layer=2, n_head=4, n_kv=2, hd=32, d=128, ffn=256, vocab=500, std=0.05,
+                              norm_std=0.1)
+    b = fa.Bundle(stem, ctx)
+    g = fa.Gemma(b)
+    prompts = np.stack([synth.gpt2_prompt(520, 500, 60 + i) for i in range(16)])
+    toks, lg = g.generate_batch(prompts, 3, with_logits=True)
+    for i in (0, 7, 15):
+        t1, l1 = g.generate(prompts[i], 3, with_logits=True)
+        assert np.array_equal(toks[i], t1) and same_bits(lg[i], l1), i
+    g.set_graphs(True)
+    assert np.array_equal(g.generate_batch(prompts, 3), toks)
+    g.free()
+    b.close()
+
+
+def test_gemma_batch_errors(ctx, small):
+    b = fa.Bundle(small, ctx)
+    g = fa.Gemma(b)
+    with pytest.raises(fa.FrqError) as e:
+        g.generate_batch(np.array([[1, 2], [3, 500]]), 2)
+    assert e.value.code == fa.FRQ_ERR_ARG
+    g.free()
+    b.close()

@@ -112,3 +112,18 @@ def test_rope_long_cache_decode(ctx, tmp_path, kv_int8, hd):
     assert np.array_equal(g.generate(prompt, 6), toks)
     g.free()
     b.close()
+
+
+def test_rope_batch_matches_single_sequences(ctx, small):
+    """The batch decode on the Llama / Qwen family: every row its own
+    Rope::generate, bit for bit."""
+    b = fa.Bundle(small, ctx)
+    g = fa.Rope(b)
+    prompts = np.stack([synth.gpt2_prompt(6, 500, 70 + i) for i in range(4)])
+    toks, lg = g.generate_batch(prompts, 9, with_logits=True)
+    for i in range(len(prompts)):
+        t1, l1 = g.generate(prompts[i], 9, with_logits=True)
+        assert np.array_equal(toks[i], t1), i
+        assert same_bits(lg[i], l1), (i, first_diff(lg[i], l1))
+    g.free()
+    b.close()
