@@ -369,8 +369,8 @@ hipError_t launch_rowdot(const Weight& w, const float* x, const int64_t* cand, s
 // *best must start at 0.  A NaN output sets *err.
 hipError_t launch_rowdot_argmax(const Weight& w, const float* x, float* out, unsigned long long* best, int* err,
                                 hipStream_t s);
-hipError_t launch_rowdot_argmax_batch(const Weight& w, size_t nx, const float* x, size_t xs, float* out, size_t os,
-                                      unsigned long long* best, int* err, hipStream_t s);
+hipError_t launch_rowdot_argmax_batch(const Weight& w, size_t nx, const float* x, size_t xs, float* xt, float* out,
+                                      size_t os, unsigned long long* best, int* err, hipStream_t s);
 // int4 linear (any m).
 hipError_t launch_i4(const Weight& w, size_t m, const float* a, float* out,
                      float* wsf, unsigned* tickets, hipStream_t s);

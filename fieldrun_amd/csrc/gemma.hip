@@ -56,14 +56,26 @@ __device__ float gblock_max(float v, float* red) {
 // rows_f32("embed", ids) * escale (gemma.rs:424, 429): row t is token ids[t]
 // (rel: ids[cur - P + t], the token the last argmax wrote).
 // (tstride > 0: a batch step, row t is sequence t's last token, ids[t tstride + cur - P])
-__global__ __launch_bounds__(GT) void gm_embed_kernel(const uint8_t* __restrict__ tab, size_t pitch, int d,
-                                                      float escale, const int64_t* __restrict__ ids, int rel, int P,
+// The embedding rows (Bundle::rows_f32, src/bundle.rs:936-955: an f32, f16
+// or rowi8 table, a rowi8 element q as f32 times its row's scale rs[id])
+// times escale (gemma.rs:105; 1 on the Llama / Qwen family).
+__global__ __launch_bounds__(GT) void gm_embed_kernel(const uint8_t* __restrict__ tab, size_t pitch, int dt,
+                                                      const float* __restrict__ rs, int d, float escale,
+                                                      const int64_t* __restrict__ ids, int rel, int P,
                                                       const int* __restrict__ curp, float* __restrict__ x,
                                                       size_t tstride = 0) {
     const int t = blockIdx.x;
     const int64_t id = ids[rel ? (tstride ? t * tstride + *curp - P : *curp - P + t) : t];
-    const uint16_t* row = reinterpret_cast<const uint16_t*>(tab + (size_t)id * pitch);
-    for (int c = threadIdx.x; c < d; c += GT) x[(size_t)t * d + c] = h2f(row[c]) * escale;
+    const uint8_t* row = tab + (size_t)id * pitch;
+    float* xo = x + (size_t)t * d;
+    if (dt == FRQ_DT_F16) {
+        for (int c = threadIdx.x; c < d; c += GT) xo[c] = h2f(reinterpret_cast<const uint16_t*>(row)[c]) * escale;
+    } else if (dt == FRQ_DT_F32) {
+        for (int c = threadIdx.x; c < d; c += GT) xo[c] = reinterpret_cast<const float*>(row)[c] * escale;
+    } else {
+        const float sc = rs[id];
+        for (int c = threadIdx.x; c < d; c += GT) xo[c] = ((float)(int8_t)row[c] * sc) * escale;
+    }
 }
 
 // Threads of the norm kernel: eight waves, so the fold runs as eight
@@ -1089,6 +1101,7 @@ struct frq_gemma {
     unsigned long long* best = nullptr;
     int64_t *tok = nullptr, *ids = nullptr;
     float *qr = nullptr, *sc = nullptr;  // long-cache decode attention: roped q, scores
+    float* xt = nullptr;                 // batches: the head's input rows transposed (16 d)
     // the quantised decode rows of the int8 linears (d- and ffn-wide: the
     // padding of each stays zero), their scales and outliers
     int8_t* q8f = nullptr;
@@ -1385,7 +1398,7 @@ void gm_drop_buffers(frq_gemma* g) {
     g->cur = nullptr;
     g->best = nullptr;
     g->tok = g->ids = nullptr;
-    g->qr = g->sc = nullptr;
+    g->qr = g->sc = g->xt = nullptr;
     g->q8f = nullptr;
     g->qsa = nullptr;
     g->qoi = nullptr;
@@ -1432,6 +1445,7 @@ int gm_reserve(frq_ctx* c, frq_gemma* g, size_t npos, size_t rows, size_t nb = 1
                  o_lg = take(B * g->vocab * 4), o_cur = take(4), o_best = take(B * 8), o_tok = take(B * N * 8),
                  o_ids = take(R * 8),
                  o_qr = take(g->H * g->hd * 4), o_sc = take(g->H * gm_pstride_n(N) * 4),
+                 o_xt = take(B > 1 ? 16 * g->d * 4 : 0),
                  o_q8f = take(round_up(g->ffn, FRQ_KALIGN)), o_qsa = take(4), o_qoi = take(FRQ_T * 4),
                  o_qov = take(FRQ_T * 4);
     char* m = nullptr;
@@ -1470,6 +1484,7 @@ int gm_reserve(frq_ctx* c, frq_gemma* g, size_t npos, size_t rows, size_t nb = 1
     g->cur = reinterpret_cast<int*>(m + o_cur); g->best = reinterpret_cast<unsigned long long*>(m + o_best);
     g->tok = reinterpret_cast<int64_t*>(m + o_tok); g->ids = reinterpret_cast<int64_t*>(m + o_ids);
     g->qr = reinterpret_cast<float*>(m + o_qr); g->sc = reinterpret_cast<float*>(m + o_sc);
+    g->xt = B > 1 ? reinterpret_cast<float*>(m + o_xt) : nullptr;
     g->q8f = reinterpret_cast<int8_t*>(m + o_q8f);
     g->qsa = reinterpret_cast<float*>(m + o_qsa); g->qoi = reinterpret_cast<uint32_t*>(m + o_qoi);
     g->qov = reinterpret_cast<float*>(m + o_qov);
@@ -1507,8 +1522,9 @@ int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_o
         return batch ? gm_mm_rows(c, w, in, m, outp) : gm_mm(c, w, in, m, outp);
     };
     int64_t* tokp = g->tok + g->seq * g->cap_pos;  // this sequence's tokens (batch: sequence 0's)
-    gm_embed_kernel<<<dim3((unsigned)m), dim3(GT), 0, s>>>(et.rowp, et.rpitch, d, g->escale, rel ? tokp : g->ids,
-                                                           rel, P, g->cur, g->x, batch ? g->cap_pos : 0);
+    gm_embed_kernel<<<dim3((unsigned)m), dim3(GT), 0, s>>>(et.rowp, et.rpitch, et.dtype, et.scale, d, g->escale,
+                                                           rel ? tokp : g->ids, rel, P, g->cur, g->x,
+                                                           batch ? g->cap_pos : 0);
     GMCHK(hipGetLastError(), "launch embed");
     GMCHK(norm(nullptr, nullptr, g->norm_of(0, 0), (int)m, 0), "launch norm");
     const size_t kvd = g->KV * g->hd;
@@ -1640,7 +1656,7 @@ int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_o
     float* lg = logits_out ? logits_out : g->logits;
     const Weight& ut = g->unembed ? *weight_of(g->unembed) : et;
     if (batch) {
-        GMCHK(launch_rowdot_argmax_batch(ut, m, g->a, g->d, lg, logits_out ? los : g->vocab, g->best, err, s),
+        GMCHK(launch_rowdot_argmax_batch(ut, m, g->a, g->d, g->xt, lg, logits_out ? los : g->vocab, g->best, err, s),
               "launch unembed");
         gm_argmax_batch_kernel<<<dim3(1), dim3(64), 0, s>>>(g->best, g->cur, (int)m, P, g->tok, (int)g->cap_pos);
     } else {
@@ -1860,8 +1876,8 @@ static int decoder_load(frq_ctx* c, const frq_bundle* b, int kv_int8, int want_a
         int dt = 0;
         size_t n = 0, k = 0, gg = 0;
         (void)frq_w_info(*w, &dt, &n, &k, &gg);
-        if (dt != FRQ_DT_F16 || n != g->vocab || k != d)
-            return set_error(FRQ_ERR_FORMAT, std::string(nm) + ": expected an f16 (vocab, d) table");
+        if ((dt != FRQ_DT_F16 && dt != FRQ_DT_F32 && dt != FRQ_DT_ROWI8) || n != g->vocab || k != d)
+            return set_error(FRQ_ERR_FORMAT, std::string(nm) + ": expected an f32, f16 or rowi8 (vocab, d) table");
         return FRQ_OK;
     };
     if (int rc = table("embed", &g->embed)) return rc;

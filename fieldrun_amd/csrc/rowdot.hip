@@ -43,15 +43,17 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int row) {
     return ((unsigned long long)u << 32) | (uint32_t)row;
 }
 
-// NX x vectors at once (x + v xs, outputs out + v os, argmax best[v]): each
+// NX x vectors at once (outputs out + v os, argmax best[v], v < nv): each
 // lane runs NX chains of its row, one per vector, so the table streams once
-// for all of them; every chain is the one-vector order.
+// for all of them; every chain is the one-vector order.  For NX > 1, x is
+// the vectors transposed, x[k NX + v] (zero for v >= nv): element k's NX
+// values are adjacent, one wide scalar load feeding 2 NX VALU operations.
 template <int DT, bool SUB, int DEPTH, int WPB, bool ARG, int NX = 1>  // DT: 0 f32, 1 f16, 2 rowi8; DEPTH
                                                                       // chunks in registers; WPB waves
 __global__ __launch_bounds__(64 * WPB) void rowdot_kernel(
     const uint8_t* __restrict__ W, const float* __restrict__ rs, int rows, int d, size_t pitch,
     const float* __restrict__ x, const int64_t* __restrict__ cand, int nout, float* __restrict__ out,
-    unsigned long long* __restrict__ best, int* __restrict__ err, size_t xs = 0, size_t os = 0) {
+    unsigned long long* __restrict__ best, int* __restrict__ err, size_t os = 0, int nv = NX) {
     constexpr int ES = DT == 0 ? 4 : (DT == 1 ? 2 : 1);  // bytes per element
     constexpr int CE = 128 / ES;                         // elements per chunk
     __shared__ __attribute__((aligned(16))) uint8_t tile[WPB][64 * TP];
@@ -60,9 +62,10 @@ __global__ __launch_bounds__(64 * WPB) void rowdot_kernel(
     const int o0 = ((int)blockIdx.x * WPB + wave) * 64;
     if (o0 >= nout) return;  // wave-uniform; no block-wide barrier below
     uint8_t* tw = tile[wave];
+    auto xat = [&](int u, int k) __attribute__((always_inline)) -> float { return NX == 1 ? x[k] : x[(size_t)k * NX + u]; };
 
     // the row an output scores (row 0 stands in for invalid ones)
-    auto row_of = [&](int o, bool& ok) -> int {
+    auto row_of = [&](int o, bool& ok) __attribute__((always_inline)) -> int {
         ok = o < nout;
         if constexpr (SUB) {
             const int64_t c = ok ? cand[o] : 0;
@@ -93,13 +96,13 @@ __global__ __launch_bounds__(64 * WPB) void rowdot_kernel(
 #pragma unroll
         for (int q = 0; q < 8; ++q) l8[v][q] = 0.0f;
     }
-    auto load = [&](uint4 (&b)[8], int c) {
+    auto load = [&](uint4 (&b)[8], int c) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) b[i] = ntload16u(src[i] + (size_t)c * 128);
     };
     // the elements k0 .. k0 + CE of this lane's row, in order; CHECK: only
     // those below d (the last, partial chunk)
-    auto run = [&](const uint32_t (&v)[32], int k0, auto check) {
+    auto run = [&](const uint32_t (&v)[32], int k0, auto check) __attribute__((always_inline)) {
         constexpr bool CHECK = decltype(check)::value;
         if constexpr (DT == 0) {
 #pragma unroll
@@ -107,7 +110,7 @@ __global__ __launch_bounds__(64 * WPB) void rowdot_kernel(
                 if (!CHECK || k0 + e < d) {
                     const float w = __builtin_bit_cast(float, v[e]);
 #pragma unroll
-                    for (int u = 0; u < NX; ++u) acc[u] = acc[u] + w * x[u * xs + k0 + e];
+                    for (int u = 0; u < NX; ++u) acc[u] = acc[u] + w * xat(u, k0 + e);
                 }
         } else if constexpr (DT == 1) {
 #pragma unroll
@@ -115,7 +118,7 @@ __global__ __launch_bounds__(64 * WPB) void rowdot_kernel(
                 if (!CHECK || k0 + e < d) {
                     const float w = h2f((uint16_t)(v[e >> 1] >> (16 * (e & 1))));
 #pragma unroll
-                    for (int u = 0; u < NX; ++u) acc[u] = acc[u] + w * x[u * xs + k0 + e];
+                    for (int u = 0; u < NX; ++u) acc[u] = acc[u] + w * xat(u, k0 + e);
                 }
         } else if constexpr (SUB) {
 #pragma unroll
@@ -123,7 +126,7 @@ __global__ __launch_bounds__(64 * WPB) void rowdot_kernel(
                 if (!CHECK || k0 + e < d) {
                     const float w = (float)(int8_t)(v[e >> 2] >> (8 * (e & 3)));
 #pragma unroll
-                    for (int u = 0; u < NX; ++u) acc[u] = acc[u] + w * x[u * xs + k0 + e];
+                    for (int u = 0; u < NX; ++u) acc[u] = acc[u] + w * xat(u, k0 + e);
                 }
         } else {
             // full 8-element groups only; the tail follows the lane sum
@@ -135,14 +138,14 @@ __global__ __launch_bounds__(64 * WPB) void rowdot_kernel(
                     for (int q = 0; q < 8; ++q) {
                         const float w = (float)(int8_t)(v[2 * gi + (q >> 2)] >> (8 * (q & 3)));
 #pragma unroll
-                        for (int u = 0; u < NX; ++u) l8[u][q] = __builtin_fmaf(w, x[u * xs + kb + q], l8[u][q]);
+                        for (int u = 0; u < NX; ++u) l8[u][q] = __builtin_fmaf(w, xat(u, kb + q), l8[u][q]);
                     }
                 }
             }
         }
     };
     // one chunk: through the tile, then this lane's row
-    auto consume = [&](const uint4 (&b)[8], int c) {
+    auto consume = [&](const uint4 (&b)[8], int c) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < 8; ++i)
             *reinterpret_cast<uint4*>(tw + (8 * i + (lane >> 3)) * TP + (lane & 7) * 16) = b[i];
@@ -172,7 +175,7 @@ __global__ __launch_bounds__(64 * WPB) void rowdot_kernel(
                         if (k0 + e >= kt && k0 + e < d) {
                             const float w = (float)(int8_t)(v[e >> 2] >> (8 * (e & 3)));
 #pragma unroll
-                            for (int u = 0; u < NX; ++u) acc[u] = acc[u] + w * x[u * xs + k0 + e];
+                            for (int u = 0; u < NX; ++u) acc[u] = acc[u] + w * xat(u, k0 + e);
                         }
                 }
             }
@@ -215,6 +218,7 @@ __global__ __launch_bounds__(64 * WPB) void rowdot_kernel(
             if (!SUB && nch == 0) a = 0.0f;  // d == 0: hsum of zero lanes
             a = rs[own_row] * a;
         }
+        if (NX > 1 && u >= nv) break;  // the zero padding of the transposed x
         if (o < nout) out[u * os + o] = own_ok ? a : -__builtin_inff();
         if constexpr (ARG) {
             unsigned long long key = o < nout ? argmax_key(a, o) : 0ull;
@@ -251,35 +255,47 @@ hipError_t launch_dt(const Weight& w, const float* x, const int64_t* cand, size_
     return hipGetLastError();
 }
 
+// xt[k NX + v] = x[v xs + k] for v < nv, 0 for nv <= v < NX
+template <int NX>
+__global__ __launch_bounds__(256) void transpose_x_kernel(const float* __restrict__ x, size_t xs, int nv, int d,
+                                                          float* __restrict__ xt) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)d * NX) return;
+    const int k = (int)(i / NX), v = (int)(i % NX);
+    xt[i] = v < nv ? x[(size_t)v * xs + k] : 0.0f;
+}
+
 template <int DT, int NX>
-hipError_t launch_argmax_nx(const Weight& w, const float* x, size_t xs, float* out, size_t os,
+hipError_t launch_argmax_nx(const Weight& w, size_t nv, const float* x, size_t xs, float* xt, float* out, size_t os,
                             unsigned long long* best, int* err, hipStream_t s) {
     const unsigned g4 = (unsigned)((w.n + 255) / 256);
+    const float* xv = x;
+    if constexpr (NX > 1) {
+        const size_t tot = w.k * NX;
+        transpose_x_kernel<NX><<<dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s>>>(x, xs, (int)nv, (int)w.k,
+                                                                                         xt);
+        xv = xt;
+    }
     rowdot_kernel<DT, false, 2, 4, true, NX><<<dim3(g4), dim3(256), 0, s>>>(
-        w.rowp, w.scale, (int)w.n, (int)w.k, w.rpitch, x, nullptr, (int)w.n, out, best, err, xs, os);
+        w.rowp, w.scale, (int)w.n, (int)w.k, w.rpitch, xv, nullptr, (int)w.n, out, best, err, os, (int)nv);
     return hipGetLastError();
 }
 
 template <int DT>
-hipError_t launch_argmax_batch(const Weight& w, size_t nx, const float* x, size_t xs, float* out, size_t os,
-                               unsigned long long* best, int* err, hipStream_t s) {
-    // up to 16 vectors a pass (each a chain per lane), further passes for more
+hipError_t launch_argmax_batch(const Weight& w, size_t nx, const float* x, size_t xs, float* xt, float* out,
+                               size_t os, unsigned long long* best, int* err, hipStream_t s) {
+    // up to 16 vectors a pass (each a chain per lane), further passes for
+    // more; a count between the powers of two runs zero-padded
     for (size_t v0 = 0; v0 < nx; v0 += 16) {
         const size_t k = nx - v0 < 16 ? nx - v0 : 16;
         const float* xv = x + v0 * xs;
         float* ov = out + v0 * os;
         hipError_t e;
-        switch (k) {
-            case 1: e = launch_argmax_nx<DT, 1>(w, xv, xs, ov, os, best + v0, err, s); break;
-            case 2: e = launch_argmax_nx<DT, 2>(w, xv, xs, ov, os, best + v0, err, s); break;
-            case 4: e = launch_argmax_nx<DT, 4>(w, xv, xs, ov, os, best + v0, err, s); break;
-            case 8: e = launch_argmax_nx<DT, 8>(w, xv, xs, ov, os, best + v0, err, s); break;
-            case 16: e = launch_argmax_nx<DT, 16>(w, xv, xs, ov, os, best + v0, err, s); break;
-            default:  // other counts: one vector at a time
-                e = hipSuccess;
-                for (size_t u = 0; u < k && e == hipSuccess; ++u)
-                    e = launch_argmax_nx<DT, 1>(w, xv + u * xs, xs, ov + u * os, os, best + v0 + u, err, s);
-        }
+        if (k == 1) e = launch_argmax_nx<DT, 1>(w, 1, xv, xs, xt, ov, os, best + v0, err, s);
+        else if (k == 2) e = launch_argmax_nx<DT, 2>(w, k, xv, xs, xt, ov, os, best + v0, err, s);
+        else if (k <= 4) e = launch_argmax_nx<DT, 4>(w, k, xv, xs, xt, ov, os, best + v0, err, s);
+        else if (k <= 8) e = launch_argmax_nx<DT, 8>(w, k, xv, xs, xt, ov, os, best + v0, err, s);
+        else e = launch_argmax_nx<DT, 16>(w, k, xv, xs, xt, ov, os, best + v0, err, s);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
@@ -289,14 +305,15 @@ hipError_t launch_argmax_batch(const Weight& w, size_t nx, const float* x, size_
 
 // rowdot_f32 with the argmax fold for nx vectors x + v xs at once (outputs
 // out + v os, best[v]); each output's arithmetic is launch_rowdot_argmax's.
-hipError_t launch_rowdot_argmax_batch(const Weight& w, size_t nx, const float* x, size_t xs, float* out, size_t os,
-                                      unsigned long long* best, int* err, hipStream_t s) {
+// xt: device scratch of 16 w.k floats (the transposed vectors of a pass).
+hipError_t launch_rowdot_argmax_batch(const Weight& w, size_t nx, const float* x, size_t xs, float* xt, float* out,
+                                      size_t os, unsigned long long* best, int* err, hipStream_t s) {
     if (!w.n || !nx) return hipSuccess;
     if (w.n > (size_t)INT32_MAX - 256 || w.k > (size_t)INT32_MAX) return hipErrorInvalidValue;
     switch (w.dtype) {
-        case FRQ_DT_F32: return launch_argmax_batch<0>(w, nx, x, xs, out, os, best, err, s);
-        case FRQ_DT_F16: return launch_argmax_batch<1>(w, nx, x, xs, out, os, best, err, s);
-        case FRQ_DT_ROWI8: return launch_argmax_batch<2>(w, nx, x, xs, out, os, best, err, s);
+        case FRQ_DT_F32: return launch_argmax_batch<0>(w, nx, x, xs, xt, out, os, best, err, s);
+        case FRQ_DT_F16: return launch_argmax_batch<1>(w, nx, x, xs, xt, out, os, best, err, s);
+        case FRQ_DT_ROWI8: return launch_argmax_batch<2>(w, nx, x, xs, xt, out, os, best, err, s);
         default: return hipErrorInvalidValue;
     }
 }

@@ -152,7 +152,7 @@ def _f16_table_chunks(ss, rows: int, d: int, std: float):
 
 def write_gemma2_bundle(stem: str, s: int, n_layer: int = 26, n_head: int = 8, n_kv: int = 4, hd: int = 256,
                         d: int = 2304, ffn: int = 9216, vocab: int = 256000, std: float = 0.02,
-                        dtype: str = "int4", norm_std: float = 0.0, raw: bool = False) -> dict:
+                        dtype: str = "int4", norm_std: float = 0.0, raw: bool = False, embed: str = "f16") -> dict:
     """a Gemma-2-2b-shaped bundle as convert_gemma writes it
     (src/convert.rs:636-657 via write_layers 1266-1300): the f16 embed (tied
     unembed), the RMSNorm gains with the +1 baked in (1 + w, w = 0 at init,
@@ -161,7 +161,9 @@ def write_gemma2_bundle(stem: str, s: int, n_layer: int = 26, n_head: int = 8, n
     config [nl, H, nkv, hd, d, ffn, vocab, tied]; config_f [theta, eps,
     attn_cap, final_cap, query_pre_attn_scalar, sqrt(d)] as Gemma-2-2b.
     raw: the int4 linears as seeded random nibbles with f16 scales written
-    directly (the configs[2] size in seconds rather than minutes)."""
+    directly (the configs[2] size in seconds rather than minutes).
+    embed: the tied table's type when not raw, "f16", "f32" or "int8"
+    (rowi8 with f16 per-row scales, put_embed_i8)."""
     from .bundle import BundleWriter, manifest
     rng = np.random.default_rng(s)
     nrm = lambda *shape: (rng.standard_normal(shape, dtype=np.float32) * np.float32(std))
@@ -174,8 +176,10 @@ def write_gemma2_bundle(stem: str, s: int, n_layer: int = 26, n_head: int = 8, n
         nb = w._write(np.ascontiguousarray(emb.view(np.uint16)))
         w.entry("embed", "f16", emb.shape, nb)
         del emb
+    elif embed == "f32":
+        w.put_f32("embed", nrm(vocab, d))
     else:
-        w.put_embed("embed", nrm(vocab, d), "f16", dtype)
+        w.put_embed("embed", nrm(vocab, d), embed, dtype)
     w.put_small("norm", gain(), None, dtype)
     shapes = {"self_attn.q_proj": (n_head * hd, d), "self_attn.k_proj": (n_kv * hd, d),
               "self_attn.v_proj": (n_kv * hd, d), "self_attn.o_proj": (d, n_head * hd),

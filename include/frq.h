@@ -285,8 +285,9 @@ int frq_gpt2_set_graphs(frq_gpt2* g, int on);
  * [n_layer, H, nkv, hd, d, ffn, vocab, tied], config_f [theta, eps,
  * attn_cap, final_cap, query_pre_attn_scalar, escale]; arrays as
  * convert_gemma writes them, src/convert.rs:636-657): int4 / int8 / q4a
- * linears (q|k|v and gate|up uploaded side by side), the f16 embed (rows and
- * the tied unembed), the RMSNorm gains; kv_int8: the int8 cache of
+ * linears (q|k|v and gate|up uploaded side by side), the embed (rows and
+ * the tied unembed) as an f32, f16 or rowi8 table (Bundle::rows_f32 /
+ * rowdot_f32, src/bundle.rs:936-987), the RMSNorm gains; kv_int8: the int8 cache of
  * forward_block_q (293-363).  generate / predict as Model::generate
  * (403-431) / predict (436-441): tokens and logits as the reference's.
  * The cache and the RoPE table grow to the longest call. */

@@ -473,7 +473,7 @@ class _GemmaW(C.Structure):
                 ("theta", C.c_float), ("eps", C.c_float), ("attn_cap", C.c_float), ("qscale", C.c_float),
                 ("escale", C.c_float), ("embed", C.c_void_p), ("norm", C.c_void_p), ("norms", C.c_void_p),
                 ("lin", C.c_void_p), ("arch", C.c_int), ("bias", C.c_void_p), ("qk_norm", C.c_void_p),
-                ("unembed", C.c_void_p)]
+                ("unembed", C.c_void_p), ("embed_dt", C.c_int), ("embed_scale", C.c_void_p)]
 
 
 class Gemma:
@@ -536,7 +536,11 @@ class Gemma:
         ptrs = lambda lst: (C.c_void_p * max(len(lst), 1))(*[None if a is None else a.ctypes.data for a in lst])
         nptr, bptr, qptr = ptrs(norms), ptrs(biases), ptrs(qkn)
         self.keep += [lins, nptr, bptr, qptr]
-        self.embed = np.ascontiguousarray(arrs["embed"]).view(np.uint16)
+        # the embed table as stored: f32, f16 or rowi8 (+ f32 per-row scales)
+        edt = info["embed"].get("dtype", "f32")
+        self.embed = np.ascontiguousarray(arrs["embed"])
+        self.embed_scale = f32("embed__scale") if edt == "rowi8" else None
+        edt = {"f32": 3, "f16": 4, "rowi8": 5}[edt]
         tied = int(manifest["config"][7]) != 0
         self.unembed = None if (not rope or tied) else np.ascontiguousarray(arrs["lm_head"]).view(np.uint16)
         self.norm = f32("norm")
@@ -544,7 +548,8 @@ class Gemma:
                          np.float32(np.float32(qscalar) ** np.float32(-0.5)), np.float32(escale),
                          self.embed.ctypes.data, self.norm.ctypes.data, C.cast(nptr, C.c_void_p),
                          C.cast(lins, C.c_void_p), int(rope), C.cast(bptr, C.c_void_p), C.cast(qptr, C.c_void_p),
-                         None if self.unembed is None else self.unembed.ctypes.data)
+                         None if self.unembed is None else self.unembed.ctypes.data, edt,
+                         None if self.embed_scale is None else self.embed_scale.ctypes.data)
         self.vocab, self.nthreads = vocab, nthreads
 
     def generate(self, prompt, n_new: int, kv_int8: bool = False, with_logits: bool = False):

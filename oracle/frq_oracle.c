@@ -1302,8 +1302,18 @@ static int gm_block(gm_run* R, float* x, size_t m, size_t cur) {
 typedef struct { const fro_gemma_t* g; const float* x; float* out; size_t lo, hi; } gm_head_job;
 static void* gm_head_worker(void* p) {
     gm_head_job* J = (gm_head_job*)p;
-    const uint16_t* tab = J->g->unembed ? J->g->unembed : J->g->embed;
-    fro_rowdot_f32(FRO_DT_F16, tab + J->lo * J->g->d, NULL, J->hi - J->lo, J->g->d, J->x, J->out + J->lo);
+    const fro_gemma_t* g = J->g;
+    const size_t d = g->d, n = J->hi - J->lo;
+    if (g->unembed) {
+        fro_rowdot_f32(FRO_DT_F16, g->unembed + J->lo * d, NULL, n, d, J->x, J->out + J->lo);
+    } else if (g->embed_dt == FRO_DT_F32) {
+        fro_rowdot_f32(FRO_DT_F32, (const float*)(const void*)g->embed + J->lo * d, NULL, n, d, J->x, J->out + J->lo);
+    } else if (g->embed_dt == FRO_DT_ROWI8) {
+        fro_rowdot_f32(FRO_DT_ROWI8, (const int8_t*)(const void*)g->embed + J->lo * d, g->embed_scale + J->lo, n, d,
+                       J->x, J->out + J->lo);
+    } else {
+        fro_rowdot_f32(FRO_DT_F16, g->embed + J->lo * d, NULL, n, d, J->x, J->out + J->lo);
+    }
     return NULL;
 }
 
@@ -1330,10 +1340,21 @@ static int gm_head(gm_run* R, const float* xlast, float* logits, int64_t* tok) {
     return FRO_OK;
 }
 
+/* rows_f32 (src/bundle.rs:936-955): the row in f32 (a rowi8 element q as
+ * f32 times its row's scale), then times the embedding scale */
 static int gm_embed(const fro_gemma_t* g, const int64_t* ids, size_t m, float* x) {
+    const float* f = (const float*)(const void*)g->embed;
+    const int8_t* q = (const int8_t*)(const void*)g->embed;
     for (size_t t = 0; t < m; t++) {
         if (ids[t] < 0 || (size_t)ids[t] >= g->vocab) return FRO_ERR_ARG;
-        for (size_t c = 0; c < g->d; c++) x[t * g->d + c] = fro_f16_to_f32(g->embed[(size_t)ids[t] * g->d + c]) * g->escale;
+        const size_t r = (size_t)ids[t], b = r * g->d;
+        for (size_t c = 0; c < g->d; c++) {
+            float e;
+            if (g->embed_dt == FRO_DT_F32) e = f[b + c];
+            else if (g->embed_dt == FRO_DT_ROWI8) e = (float)q[b + c] * g->embed_scale[r];
+            else e = fro_f16_to_f32(g->embed[b + c]);
+            x[t * g->d + c] = e * g->escale;
+        }
     }
     return FRO_OK;
 }

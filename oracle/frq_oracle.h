@@ -65,7 +65,9 @@ extern "C" {
 #define FRO_OK 0
 #define FRO_ERR_ARG 1 /* an index the reference would panic on          */
 #define FRO_ERR_NAN 3 /* reference panics in partial_cmp().unwrap() */
+#define FRO_DT_F32 3 /* the row-dot table types (bundle.rs Arr) */
 #define FRO_DT_F16 4
+#define FRO_DT_ROWI8 5
 
 /* IEEE binary16 <-> binary32 (half 2.7.1 semantics: RNE, exact upcast). */
 float fro_f16_to_f32(uint16_t h);
@@ -240,6 +242,11 @@ typedef struct {
     const float* const* bias;
     const float* const* qk_norm;
     const uint16_t* unembed;
+    /* the embed table's type (Bundle::rows_f32 / rowdot_f32 take f32, f16
+     * and rowi8, src/bundle.rs:936-987): FRO_DT_F32, FRO_DT_F16 (or 0) or
+     * FRO_DT_ROWI8 with embed_scale its per-row f32 scales */
+    int embed_dt;
+    const float* embed_scale;
 } fro_gemma_t;
 
 /* RMSNorm with the baked (1 + w) gain (gemma.rs:66-77) over m rows. */

@@ -218,6 +218,30 @@ def test_gemma_batch_long_cache_and_sixteen_rows(ctx, tmp_path):
     b.close()
 
 
+@pytest.mark.parametrize("embed", ["f32", "int8"])
+def test_gemma_batch_head_table_types(ctx, tmp_path, embed):
+    """The batched head (the tied table's row dot and argmax for every
+    sequence in one pass, the vectors zero-padded to 4, 8 or 16) on f32 and
+    rowi8 tables: bit for bit the one-sequence head, and the oracle."""
+    stem = str(tmp_path / "g")
+    synth.write_gemma2_bundle(stem, 29, n_layer=2, n_head=4, n_kv=2, hd=32, d=132, ffn=256, vocab=700, std=0.05,
+                              norm_std=0.1, embed=embed)
+    m, arrs = oracle.read_bundle(stem)
+    ref = oracle.Gemma(m, arrs, nthreads=8)
+    b = fa.Bundle(stem, ctx)
+    g = fa.Gemma(b)
+    for nb in (3, 9):
+        prompts = np.stack([synth.gpt2_prompt(4, 700, 90 + nb + i) for i in range(nb)])
+        toks, lg = g.generate_batch(prompts, 4, with_logits=True)
+        for i in range(nb):
+            t1, l1 = g.generate(prompts[i], 4, with_logits=True)
+            assert np.array_equal(toks[i], t1) and same_bits(lg[i], l1), (nb, i, first_diff(lg[i], l1))
+        rt, rlg = ref.generate(prompts[nb - 1], 4, with_logits=True)
+        assert np.array_equal(toks[nb - 1], rt) and same_bits(lg[nb - 1], rlg), nb
+    g.free()
+    b.close()
+
+
 def test_gemma_batch_errors(ctx, small):
     b = fa.Bundle(small, ctx)
     g = fa.Gemma(b)
