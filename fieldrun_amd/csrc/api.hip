@@ -9,6 +9,7 @@
 //   int8, M >  16          -> quant kernel (blocked a8) + int8 MFMA GEMM
 //   int4                   -> blocked W4A32 GEMV (M == 1) / batched kernel
 // Every failure becomes an int status plus frq_last_error(); nothing throws.
+#include <atomic>
 #include <mutex>
 #include <new>
 #include <string>
@@ -284,6 +285,16 @@ int set_error(int code, const std::string& msg) { return fail(code, msg); }
 int last_code() { return g_code; }
 int ctx_device(const frq_ctx* c) { return c->device; }
 int* ctx_err(frq_ctx* c) { return c->err; }
+int device_cus(int dev) {
+    static std::atomic<int> cus[64];  // 0: not yet asked
+    if (dev < 0 || dev >= 64) return 256;
+    int v = cus[dev].load(std::memory_order_relaxed);
+    if (v <= 0) {
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+        cus[dev].store(v, std::memory_order_relaxed);
+    }
+    return v;
+}
 const Weight* weight_of(const frq_w* w) { return &w->w; }
 bool i8_rows_exact_ok(const frq_w* w, size_t m) { return rows_exact_ok(w, m); }
 int mm_i8_rows_exact(frq_ctx* c, const frq_w* w, const float* d_a, size_t m, float* d_out) {

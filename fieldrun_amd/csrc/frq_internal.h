@@ -193,6 +193,21 @@ __device__ inline void lds_seq_sum2(const float* p, int n, float& a0, float& a1)
     }
 }
 
+// Direct-to-LDS load (global_load_lds, 16 bytes a lane): lane l's 16 bytes
+// at g land at lds_base + 16 l (lds_base wave-uniform).  Counted by vmcnt;
+// the data is in LDS once the count has dropped past the load.
+typedef __attribute__((address_space(1))) void frq_gvoid_t;
+typedef __attribute__((address_space(3))) void frq_lvoid_t;
+__device__ __forceinline__ void dma16_lds(const void* g, void* lds_base) {
+    __builtin_amdgcn_global_load_lds((frq_gvoid_t*)g, (frq_lvoid_t*)lds_base, 16, 0, 0);
+}
+// s_waitcnt vmcnt(N) (gfx9 encoding; expcnt / lgkmcnt not waited on)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
+}
+
 // LDS floats of seq_sum_spec<NT>'s scratch (8-byte aligned).
 constexpr int seq_sum_spec_scratch(int nt) { return (nt / 64) * 128 + 2 * (nt / 64) + 4; }
 
@@ -345,6 +360,8 @@ hipError_t launch_i8_exact_epilogue(const Weight& w, size_t m, const float* sa, 
 // context's device, its NaN error word (reported by frq_sync) and a
 // weight's device layout.
 int ctx_device(const frq_ctx* c);
+// The device's compute units (hipDeviceAttributeMultiprocessorCount, cached).
+int device_cus(int dev);
 int* ctx_err(frq_ctx* c);
 const Weight* weight_of(const frq_w* w);
 // The int8 linear over m > 16 rows bit for bit as the skinny path gives it

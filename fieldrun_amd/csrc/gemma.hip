@@ -906,16 +906,9 @@ __global__ __launch_bounds__(GT) void gm_dec_value_kernel(const float* __restric
 // values are gm_dec_value_kernel's bit for bit.
 constexpr int VR_NB = 4, VR_CHUNK = 16384;
 
-typedef __attribute__((address_space(1))) void gm_gvoid_t;
-typedef __attribute__((address_space(3))) void gm_lvoid_t;
-__device__ __forceinline__ void gm_dma16(const void* g, void* lds_base) {
-    __builtin_amdgcn_global_load_lds((gm_gvoid_t*)g, (gm_lvoid_t*)lds_base, 16, 0, 0);
-}
-// s_waitcnt vmcnt(N) (gfx9 encoding; expcnt / lgkmcnt not waited on)
+__device__ __forceinline__ void gm_dma16(const void* g, void* lds_base) { dma16_lds(g, lds_base); }
 template <int N>
-__device__ __forceinline__ void gm_wait_vm() {
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
-}
+__device__ __forceinline__ void gm_wait_vm() { wait_vmcnt<N>(); }
 
 template <bool KV8, int RB>
 __global__ __launch_bounds__(GT) void gm_dec_value_ring_kernel(const float* __restrict__ sc, int H, int KV, int hd,

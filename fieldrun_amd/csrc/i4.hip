@@ -155,6 +155,125 @@ __global__ __launch_bounds__(256) void i4_gemv_terms(const uint8_t* __restrict__
     for (int r = threadIdx.x; r < nr; r += 256) out[r0 + r] = lds_seq_sum(cg + r * ngp, ng, 0.0f);
 }
 
+// M == 1 in i4_dot_avx2's order, streamed: a persistent grid of about one
+// workgroup per CU, each owning a contiguous range of R rows, so its
+// R * ng items (row, group) are one contiguous run of the packed weights
+// and of the scales.  A thread takes items tid + NT i; every one of its
+// nibble and scale loads is issued up front, right after the direct-to-LDS
+// loads of the activation row (32-float units padded to 36 against bank
+// conflicts), and items are consumed in issue order as the loads land.  A
+// group's term scale * gsum goes to LDS; after one barrier a lane per row
+// adds its row's terms in order.
+//   Nibbles to f32: (x & 0x000F000F) ^ 0x64086408 puts (q ^ 8) of nibbles
+// 0 and 4 of a word under the f16 exponent of 1024 (one bit operation),
+// a packed f16 add of -1032 leaves the exact signed values q - 16 [q >= 8]
+// in both halves, and v_fma_mix_f32 takes either half as an exactly
+// widened f32 operand of the FMA: the products and their rounding are
+// those of fma(float(s4), a, acc).
+__device__ __forceinline__ void nib_f16x2(uint32_t x, uint32_t (&d)[4]) {
+    d[0] = (x & 0x000F000Fu) ^ 0x64086408u;
+    d[1] = ((x >> 4) & 0x000F000Fu) ^ 0x64086408u;
+    d[2] = ((x >> 8) & 0x000F000Fu) ^ 0x64086408u;
+    d[3] = ((x >> 12) & 0x000F000Fu) ^ 0x64086408u;
+}
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// One 32-nibble unit (4 words) against 32 activations into the eight AVX2
+// lane chains l[q] (element 8c + q is nibble q of word c).
+__device__ __forceinline__ void unit_fma(const uint4 w, const float* __restrict__ ab, float (&l)[8]) {
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    const f16x2 off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        uint32_t d[4];
+        nib_f16x2(ws[c], d);
+        f16x2 h[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) h[j] = __builtin_bit_cast(f16x2, d[j]) + off;
+        const float4 a0 = *reinterpret_cast<const float4*>(ab + 8 * c);
+        const float4 a1 = *reinterpret_cast<const float4*>(ab + 8 * c + 4);
+        const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+        for (int q = 0; q < 8; ++q) l[q] = __builtin_fmaf((float)(q < 4 ? h[q].x : h[q - 4].y), av[q], l[q]);
+    }
+}
+
+// LDS bytes of the staged activation row: 16-byte slots of 9 a unit (8 of
+// data, 1 of padding), whole 1 KB loads of 64 slots.
+__host__ __device__ inline size_t i4_stream_as_bytes(int K) { return (size_t)(K / 32 * 9 + 63) / 64 * 1024; }
+
+template <int G4, int IPT, int NT>
+__global__ __launch_bounds__(NT) void i4_m1_stream(const uint8_t* __restrict__ packed,
+                                                    const uint16_t* __restrict__ scale, int N, int K, int R,
+                                                    const float* __restrict__ a, float* __restrict__ out) {
+    extern __shared__ float4 lds4[];
+    constexpr int g = 32 * G4;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, ng = K / g, nu = K / 32;
+    constexpr int NW = NT / 64;
+    const int r0 = blockIdx.x * R;
+    if (r0 >= N) return;  // workgroup-uniform, before any barrier
+    const int nr = min(R, N - r0), items = nr * ng;
+    const int ngp = (ng + 3) & ~3;  // terms row stride: 16-byte aligned rows
+    char* lds = reinterpret_cast<char*>(lds4);
+    const float* as = reinterpret_cast<const float*>(lds);                // unit u at 36 u floats
+    float* terms = reinterpret_cast<float*>(lds + i4_stream_as_bytes(K));  // nr rows of ngp floats, 1 dummy
+    const float4* a4 = reinterpret_cast<const float4*>(a);
+    // 1. the activation row straight into LDS (L2-resident, shared by every
+    //    workgroup): load q of the workgroup fills slots 64 q .. 64 q + 63,
+    //    slot k = 9 u + j holding float4 8 u + j (j == 8: padding, a dummy)
+    const int nslot = nu * 9, nld = (nslot + 63) / 64;
+    for (int q = wave; q < nld; q += NW) {
+        const int k = q * 64 + lane, u = k / 9, j = k - 9 * u;
+        dma16_lds(u < nu && j < 8 ? a4 + 8 * u + j : a4, lds + (size_t)q * 1024);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // 2. every item's nibbles and scale (indices clamped: unconditional)
+    const uint4* wp = reinterpret_cast<const uint4*>(packed + (size_t)r0 * ng * 16 * G4);
+    const uint16_t* sp = scale + (size_t)r0 * ng;
+    uint4 w[IPT][G4];
+    uint16_t sc[IPT];
+#pragma unroll
+    for (int i = 0; i < IPT; ++i) {
+        const int p = min(tid + NT * i, items - 1);
+#pragma unroll
+        for (int h = 0; h < G4; ++h) w[i][h] = wp[(size_t)p * G4 + h];
+        sc[i] = sp[p];
+    }
+    asm volatile("" ::: "memory");  // no load sinks below this point
+    __builtin_amdgcn_sched_barrier(0);
+    // 3. the row's loads were issued before these IPT (G4 + 1): once at most
+    //    that many are outstanding, this wave's share of the row is in LDS,
+    //    and after the barrier every wave's is
+    wait_vmcnt<IPT * (G4 + 1)>();
+    __builtin_amdgcn_s_barrier();
+    // item p = tid + NT i: row r = p / ng and group gi = p % ng, kept
+    // incrementally; every item is computed (past the end: a copy of the
+    // last, stored to a dummy slot)
+    const int q256 = NT / ng, m256 = NT % ng;
+    int r = tid / ng, gi = tid % ng;
+#pragma unroll
+    for (int i = 0; i < IPT; ++i) {
+        const int p = tid + NT * i;
+        const int gc = p < items ? gi : ng - 1;
+        float l[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int h = 0; h < G4; ++h) unit_fma(w[i][h], as + (gc * G4 + h) * 36, l);
+        const float q0 = l[0] + l[4], q1 = l[1] + l[5], q2 = l[2] + l[6], q3 = l[3] + l[7];
+        const float t = h2f(sc[i]) * ((q0 + q2) + (q1 + q3));
+        terms[p < items ? r * ngp + gi : nr * ngp] = t;  // past the end: a dummy slot (the compute
+                                                         // stays live, so its loads stay hoisted)
+        r += q256;
+        gi += m256;
+        if (gi >= ng) {
+            gi -= ng;
+            ++r;
+        }
+    }
+    __syncthreads();
+    for (int rr = tid; rr < nr; rr += NT) out[r0 + rr] = lds_seq_sum(terms + rr * ngp, ng, 0.0f);
+}
+
 // M independent rows (M <= 16), each in the M == 1 order (i4_dot_avx2): the
 // decode of a batch of sequences, where every sequence is its own
 // Gemma::generate.  A workgroup owns 16 weight rows; K goes in slices of 16
@@ -872,8 +991,60 @@ static hipError_t launch_fused(const Weight& w, size_t m, const float* a, float*
     }
 }
 
+template <int G4, int IPT, int NT>
+hipError_t launch_stream_t(const Weight& w, int R, unsigned grid, size_t lds, const float* a, float* out,
+                           hipStream_t s) {
+    if (lds > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute((const void*)i4_m1_stream<G4, IPT, NT>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    i4_m1_stream<G4, IPT, NT><<<dim3(grid), dim3(NT), lds, s>>>(w.q4raw, w.s4raw, (int)w.n, (int)w.k, R, a, out);
+    return hipGetLastError();
+}
+
+template <int G4, int NT>
+hipError_t launch_stream_g(const Weight& w, int ipt, int R, unsigned grid, size_t lds, const float* a, float* out,
+                           hipStream_t s) {
+    switch (ipt) {
+        case 2: return launch_stream_t<G4, 2, NT>(w, R, grid, lds, a, out, s);
+        case 4: return launch_stream_t<G4, 4, NT>(w, R, grid, lds, a, out, s);
+        case 6: return launch_stream_t<G4, 6, NT>(w, R, grid, lds, a, out, s);
+        case 8: return launch_stream_t<G4, 8, NT>(w, R, grid, lds, a, out, s);
+        case 12: return launch_stream_t<G4, 12, NT>(w, R, grid, lds, a, out, s);
+        default: return launch_stream_t<G4, 16, NT>(w, R, grid, lds, a, out, s);
+    }
+}
+
+// The streamed M == 1 kernel: rows split evenly over the workgroups (one a
+// CU, of 512 threads; more where a thread would hold over 16 items),
+// the activation row and the terms within 160 KB of LDS (else
+// hipErrorNotSupported).
+hipError_t launch_i4_stream(const Weight& w, const float* a, float* out, hipStream_t s) {
+    if (w.k % 32 || (w.g != 32 && w.g != 64) || w.k % w.g || w.k > (1u << 24) || w.n > (size_t)INT32_MAX ||
+        ((uintptr_t)a & 15))
+        return hipErrorNotSupported;
+    const size_t ng = w.k / w.g, n = w.n;
+    constexpr int nt = 512;  // 8 waves: two a SIMD, one activation row staged a CU
+    const size_t nwg = (size_t)device_cus(w.device);
+    size_t R = (n + nwg - 1) / nwg;
+    if (R * ng > (size_t)nt * 16) R = std::max<size_t>(1, (size_t)nt * 16 / ng);
+    const size_t items = R * ng, ipt0 = (items + nt - 1) / nt;
+    const int ipt = ipt0 <= 2 ? 2 : ipt0 <= 4 ? 4 : ipt0 <= 6 ? 6 : ipt0 <= 8 ? 8 : ipt0 <= 12 ? 12 : 16;
+    if (ipt0 > 16) return hipErrorNotSupported;
+    const size_t lds = i4_stream_as_bytes((int)w.k) + (R * ((ng + 3) & ~(size_t)3) + 4) * sizeof(float);
+    if (lds > 160 * 1024) return hipErrorNotSupported;
+    const unsigned grid = (unsigned)((n + R - 1) / R);
+    return w.g == 32 ? launch_stream_g<1, nt>(w, ipt, (int)R, grid, lds, a, out, s)
+                     : launch_stream_g<2, nt>(w, ipt, (int)R, grid, lds, a, out, s);
+}
+
 // The exact M == 1 kernel when the shape allows it (else hipErrorNotSupported).
 hipError_t launch_i4_terms(const Weight& w, const float* a, float* out, hipStream_t s) {
+    {
+        const hipError_t e = launch_i4_stream(w, a, out, s);
+        if (e != hipErrorNotSupported) return e;
+    }
     if (w.k % 32 || (w.g != 32 && w.g != 64) || w.k > (size_t)INT32_MAX || w.n > (size_t)INT32_MAX)
         return hipErrorNotSupported;
     const int ng = (int)(w.k / w.g);

@@ -258,6 +258,41 @@ def test_i8_device_entry_points_match_host(ctx, m, k, n):
     assert np.array_equal(out.numpy().view(np.uint32), out_h.view(np.uint32))
 
 
+def same_or_both_nan(x, y):
+    x, y = np.asarray(x, np.float32), np.asarray(y, np.float32)
+    nx, ny = np.isnan(x), np.isnan(y)
+    return np.array_equal(nx, ny) and np.array_equal(x[~nx].view(np.uint32), y[~ny].view(np.uint32))
+
+
+@pytest.mark.parametrize("n,k,g", [(9216, 2304, 32), (2304, 9216, 32), (300, 18944, 32), (5, 2304, 64),
+                                   (1000, 4096, 64), (257, 96, 32), (3, 64, 64), (4097, 2048, 32)])
+def test_i4_m1_stream_special_values(ctx, n, k, g):
+    """The streamed M == 1 kernel (nibbles widened through f16 into
+    v_fma_mix_f32) against i4_dot_avx2's order on raw random nibbles, f16
+    scales including subnormal ones, and activations holding +-inf, NaN,
+    +-0, f32 subnormals and values near the f32 maximum; g = 32 and 64,
+    ragged row ranges, one group a row, rows long enough to cap the items
+    a thread holds."""
+    rng = np.random.default_rng(n * 7 + k + g)
+    packed = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    ng = k // g
+    s16 = (rng.uniform(0.5, 1.5, (n, ng)) * 0.01).astype(np.float16)
+    s16.flat[rng.integers(0, s16.size, 8)] = np.float16(3e-7)  # f16 subnormals
+    a = rng.standard_normal((1, k)).astype(np.float32)
+    pos = rng.choice(k, 12, replace=False)
+    a[0, pos] = np.array([np.inf, -np.inf, np.nan, 0.0, -0.0, 1e-40, -3e-42, 3e38, -3e38, 1.5e-38, 7.0, -8.0],
+                         np.float32)
+    w = ctx.upload_i4(packed, s16, k, g)
+    got = w.mm(a)
+    ref = oracle.mm_i4(a, packed, s16.astype(np.float32), k, g)
+    assert same_or_both_nan(got, ref)
+    # a finite row: every bit
+    a2 = rng.standard_normal((1, k)).astype(np.float32)
+    a2[0, pos[:4]] = np.array([1e-40, -1e-39, 2e30, -2e30], np.float32)
+    assert np.array_equal(w.mm(a2).view(np.uint32), oracle.mm_i4(a2, packed, s16.astype(np.float32), k, g).view(np.uint32))
+    w.free()
+
+
 @pytest.mark.parametrize("n,k", [(9216, 2304), (2304, 9216), (2048, 2304), (1000, 4096), (7, 64)])
 def test_i4_m1_bit_exact_avx2_order(ctx, n, k):
     """M == 1 int4 with K % 32 == 0 and g = 32: bit-identical to
