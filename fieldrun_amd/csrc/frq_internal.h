@@ -111,7 +111,7 @@ __device__ __forceinline__ float h2f(uint16_t h) {
 // over LDS (p 16-byte aligned): loads run one 32-value batch ahead of the
 // adds (unconditional, the index clamped to the last batch) so the chain
 // waits on the adds, not on LDS latency.
-__device__ inline float lds_seq_sum(const float* p, int n, float acc) {
+__device__ __forceinline__ float lds_seq_sum(const float* p, int n, float acc) {
     constexpr int B = 8;  // float4 per batch
     const int nb = n / (4 * B);
     const float4* p4 = reinterpret_cast<const float4*>(p);
@@ -154,7 +154,7 @@ __device__ inline float lds_seq_sum(const float* p, int n, float acc) {
 
 // lds_seq_sum with two chains in the calling lane: a0 and a1 each get
 // p[0] + ... + p[n-1] added in index order (one LDS load feeds both).
-__device__ inline void lds_seq_sum2(const float* p, int n, float& a0, float& a1) {
+__device__ __forceinline__ void lds_seq_sum2(const float* p, int n, float& a0, float& a1) {
     constexpr int B = 8;
     const int nb = n / (4 * B);
     const float4* p4 = reinterpret_cast<const float4*>(p);
@@ -228,7 +228,7 @@ constexpr int seq_sum_spec_scratch(int nt) { return (nt / 64) * 128 + 2 * (nt / 
 // non-finite values) it folds segment k again from the true start.  The
 // result never depends on the estimates, only the time does.
 template <int NT>
-__device__ float seq_sum_spec(const float* p, int n, float init, float* sc) {
+__device__ __forceinline__ float seq_sum_spec(const float* p, int n, float init, float* sc) {
     constexpr int S = NT / 64, C = 128;
     const int tid = threadIdx.x, lane = tid & 63, k = tid >> 6;
     float* ends = sc;                                      // [S][C] candidate ends

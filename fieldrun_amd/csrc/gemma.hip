@@ -86,7 +86,7 @@ constexpr int NORM_NT = 512;
 // fold from -0.0 of v*v in index order / n (seq_sum_spec: bit-identical to
 // the one-lane chain), inv = 1 / sqrt(ms + eps), dst = v * inv * w.
 template <int NT>
-__device__ void rms_row(const float* v, float* sq, const float* __restrict__ w, int d, float eps, float* dst,
+__device__ __forceinline__ void rms_row(const float* v, float* sq, const float* __restrict__ w, int d, float eps, float* dst,
                         float* fsc) {
     for (int c = threadIdx.x; c < d; c += NT) sq[c] = v[c] * v[c];
     __syncthreads();
@@ -109,7 +109,7 @@ __host__ __device__ inline size_t gm_norm_lds(int d) { return gm_norm_lds_t<NORM
 // The norm kernel's body for NT threads; the normalised row is left in LDS
 // (returned) as well as written to out.
 template <int NT>
-__device__ float* gm_norm_body(float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ wpost,
+__device__ __forceinline__ float* gm_norm_body(float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ wpost,
                                const float* __restrict__ wnext, float* __restrict__ out, int d, float eps,
                                size_t r, float* lds) {
     const int dp = (d + 3) & ~3;
