@@ -236,18 +236,16 @@ struct Q8 {  // one quantised activation row as frq_mm_i8_q_dev takes it
     int kp;
 };
 
-// The row (K floats of LDS, 16-byte aligned, K % 4 == 0, 32 < K <= 4096 NV4)
+// The row (K floats of LDS, 16-byte aligned, K % 4 == 0, 32 < K <= 4096 NV4,
+// also held in v: v[i] = float4 tid + QNT i, entries past K / 4 ignored)
 // quantised into q by the QNT threads; a NaN row sets *err and writes the
 // standalone quant's placeholders.
 template <int NV4>
-__device__ void quant_lds_row(const float* row, int K, const Q8& q, int* err) {
+__device__ void quant_lds_row(const float* row, int K, const Q8& q, int* err, const float4 (&v)[NV4]) {
     __shared__ qc::RowLdsT<QNT> L;
     __shared__ unsigned long long cand[qc::FCAP];
     __shared__ uint32_t bitmap[FRQ_QMAXK / 32];
     const int tid = threadIdx.x, K4 = K >> 2;
-    float4 v[NV4];
-#pragma unroll
-    for (int i = 0; i < NV4; ++i) v[i] = reinterpret_cast<const float4*>(row)[min(tid + QNT * i, K4 - 1)];
     const qc::RowSel sel = qc::row_select<NV4, QNT>(row, K, v, L, cand, bitmap, (q.kp + 31) / 32);
     uint32_t* a8w = reinterpret_cast<uint32_t*>(q.a8);
     if (sel.nan) {  // the reference panics here; the call reports FRQ_ERR_NAN
@@ -271,17 +269,34 @@ __global__ __launch_bounds__(QNT) void gm_act_quant_kernel(const float* __restri
                                                            float* __restrict__ hm, int silu, Q8 q,
                                                            int* __restrict__ err) {
     extern __shared__ float4 lds4[];
-    float* h = reinterpret_cast<float*>(lds4);
-    for (int i = threadIdx.x; i < ffn; i += QNT) {
-        const float xv = gu[i];
-        const float a = silu ? xv / (1.0f + libm::frq_expf(-xv))
-                             : 0.5f * xv * (1.0f + libm::frq_tanhf(c * (xv + 0.044715f * xv * xv * xv)));
-        const float hv = a * gu[ffn + i];
-        h[i] = hv;
-        hm[i] = hv;
+    const int tid = threadIdx.x, f4 = ffn >> 2;
+    const float4* g4 = reinterpret_cast<const float4*>(gu);
+    const float4* u4 = reinterpret_cast<const float4*>(gu + ffn);
+    // every load issued before the first use (clamped: unconditional)
+    float4 gv[NV4], uv[NV4];
+#pragma unroll
+    for (int j = 0; j < NV4; ++j) {
+        const int q4 = min(tid + QNT * j, f4 - 1);
+        gv[j] = g4[q4];
+        uv[j] = u4[q4];
+    }
+    auto act = [&](float xv) {
+        return silu ? xv / (1.0f + libm::frq_expf(-xv))
+                    : 0.5f * xv * (1.0f + libm::frq_tanhf(c * (xv + 0.044715f * xv * xv * xv)));
+    };
+    float4 v[NV4];
+#pragma unroll
+    for (int j = 0; j < NV4; ++j) {
+        v[j] = make_float4(act(gv[j].x) * uv[j].x, act(gv[j].y) * uv[j].y, act(gv[j].z) * uv[j].z,
+                           act(gv[j].w) * uv[j].w);
+        const int q4 = tid + QNT * j;
+        if (q4 < f4) {
+            lds4[q4] = v[j];
+            reinterpret_cast<float4*>(hm)[q4] = v[j];
+        }
     }
     __syncthreads();
-    quant_lds_row<NV4>(h, ffn, q, err);
+    quant_lds_row<NV4>(reinterpret_cast<const float*>(lds4), ffn, q, err, v);
 }
 
 // Checking hook of seq_sum_spec: out[r] = init + x[r][0] + ... + x[r][n-1],
@@ -896,36 +911,40 @@ __global__ __launch_bounds__(GT) void gm_dec_value_kernel(const float* __restric
 
 // ---- long-cache decode value chains through an LDS ring --------------------
 // gm_dec_value_kernel's work for CW = RB / es channels of one head per
-// workgroup (es the cache element size): the softmax as there, then every
-// channel's chain acc = fma(p[j], v[j][c], acc) in key order by wave 0,
-// with the value rows streamed into a ring of NB chunks of 16 KB by all
-// four waves' direct-to-LDS loads (global_load_lds, 16 loads a chunk, 4 a
-// wave): the first chunks are in flight during the softmax, and each
-// chunk's loads NB - 2 chunks ahead of the chain, which then reads LDS
-// rather than waiting on memory.  Per output the order is unchanged, so the
-// values are gm_dec_value_kernel's bit for bit.
-constexpr int VR_NB = 4, VR_CHUNK = 16384;
+// workgroup (es the cache element size): the softmax as there, by VT threads
+// (the in-order sum a speculative fold over VT / 64 segments), then every
+// channel's chain acc = fma(p[j], v[j][c], acc) in key order by wave 0, with
+// the value rows streamed into a ring of NB chunks of 16 KB by every wave's
+// direct-to-LDS loads (global_load_lds, 16 loads a chunk): the first chunks
+// are in flight during the softmax, and each chunk's loads NB - 2 chunks
+// ahead of the chain, which then reads LDS rather than waiting on memory.
+// The f32 chain of a whole chunk is unrolled in batches of 8 keys (4 paired
+// value reads and 2 probability reads each) with two batches in flight, so
+// the chain waits on the FMA latency rather than on LDS.  Per output the
+// order is unchanged, so the values are gm_dec_value_kernel's bit for bit.
+constexpr int VR_NB = 4, VR_CHUNK = 16384, VT = 1024;
 
 __device__ __forceinline__ void gm_dma16(const void* g, void* lds_base) { dma16_lds(g, lds_base); }
 template <int N>
 __device__ __forceinline__ void gm_wait_vm() { wait_vmcnt<N>(); }
 
 template <bool KV8, int RB>
-__global__ __launch_bounds__(GT) void gm_dec_value_ring_kernel(const float* __restrict__ sc, int H, int KV, int hd,
+__global__ __launch_bounds__(VT) void gm_dec_value_ring_kernel(const float* __restrict__ sc, int H, int KV, int hd,
                                                                const int* __restrict__ curp,
                                                                const float* __restrict__ vc,
                                                                const int8_t* __restrict__ vq,
                                                                const float* __restrict__ vs, int sliding, int window,
                                                                int pstride, float* __restrict__ att) {
-    constexpr int ES = KV8 ? 1 : 4, CW = RB / ES, CK = VR_CHUNK / RB, KPI = 1024 / RB, PW = VR_CHUNK / 1024 / 4;
-    static_assert(PW == 4 && CK % 16 == 0, "four loads a wave a chunk; whole batches of 16 keys");
+    constexpr int ES = KV8 ? 1 : 4, CW = RB / ES, CK = VR_CHUNK / RB, KPI = 1024 / RB, NW = VT / 64;
+    constexpr int PW = VR_CHUNK / 1024 / NW;  // 1 KB loads a wave a chunk
+    static_assert(PW >= 1 && PW * NW * 1024 == VR_CHUNK && CK % 16 == 0, "whole loads; whole batches of keys");
     extern __shared__ float4 lds4[];
     // p and sv hold key j at index j - j0, so a chunk's keys start 16-byte aligned
     float* p = reinterpret_cast<float*>(lds4);
     float* sv = p + pstride;
     float* fsc = sv + pstride;
-    char* ring = reinterpret_cast<char*>(fsc + seq_sum_spec_scratch(GT));
-    __shared__ float red[4];
+    char* ring = reinterpret_cast<char*>(fsc + seq_sum_spec_scratch(VT));
+    __shared__ float red[NW];
     const int h = blockIdx.x, kv = h / (H / KV), kvd = KV * hd, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int ab = *curp, nk = ab + 1, j0 = (sliding && ab >= window) ? ab - window + 1 : 0;
     const int n = nk - j0, nch = (n + CK - 1) / CK;
@@ -946,27 +965,43 @@ __global__ __launch_bounds__(GT) void gm_dec_value_ring_kernel(const float* __re
     for (int s = 0; s < VR_NB - 1; ++s)
         if (s < nch) issue(s);
     // the softmax, as gm_dec_value_kernel (the key-order sum from +0 over
-    // the keys j0 .. nk - 1)
+    // the keys j0 .. nk - 1); the scores SB to a thread at a time, every
+    // load of a batch issued before the first is used
+    constexpr int SB = 4;
     float mx = -INFINITY;
-    for (int j = threadIdx.x; j < n; j += GT) {
-        const float v = sc[(size_t)h * pstride + j0 + j];
-        p[j] = v;
-        mx = fmaxf(mx, v);
-        if constexpr (KV8) sv[j] = vs[(size_t)(j0 + j) * KV + kv];
+    for (int b0 = 0; b0 < n; b0 += SB * VT) {
+        float vv[SB], ss[SB];
+#pragma unroll
+        for (int u = 0; u < SB; ++u) {
+            const int j = min(b0 + (int)threadIdx.x + u * VT, n - 1);
+            vv[u] = sc[(size_t)h * pstride + j0 + j];
+            if constexpr (KV8) ss[u] = vs[(size_t)(j0 + j) * KV + kv];
+        }
+#pragma unroll
+        for (int u = 0; u < SB; ++u) {
+            const int j = b0 + (int)threadIdx.x + u * VT;
+            if (j < n) {
+                p[j] = vv[u];
+                mx = fmaxf(mx, vv[u]);
+                if constexpr (KV8) sv[j] = ss[u];
+            }
+        }
     }
-    mx = gblock_max(mx, red);
-    if (j0 > 0) mx = fmaxf(mx, -1e30f);  // a masked entry joins the max
-    for (int j = threadIdx.x; j < n; j += GT) p[j] = libm::frq_expf(p[j] - mx);
+    mx = gwave_max(mx);
+    if (lane == 0) red[wave] = mx;
     __syncthreads();
-    const float sum = seq_sum_spec<GT>(p, n, 0.0f, fsc);
-    for (int j = threadIdx.x; j < n; j += GT) p[j] = p[j] / sum;
+    mx = red[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) mx = fmaxf(mx, red[w]);
+    if (j0 > 0) mx = fmaxf(mx, -1e30f);  // a masked entry joins the max
+    for (int j = threadIdx.x; j < n; j += VT) p[j] = libm::frq_expf(p[j] - mx);
+    __syncthreads();
+    const float sum = seq_sum_spec<VT>(p, n, 0.0f, fsc);
+    for (int j = threadIdx.x; j < n; j += VT) p[j] = p[j] / sum;
     __syncthreads();  // the normalised p (the first chunks have long landed)
-    // the value chains: wave 0, a lane per channel; each batch of 16 keys'
-    // LDS reads issued a batch ahead of its FMAs
-    constexpr int B = 16;
+    // the value chains: wave 0, a lane per channel
     float acc = 0.0f;
     const int c = lane;
-    float vb[2][B], pb[2][B];
     for (int s = 0; s < nch; ++s) {
         // chunk s has landed once at most (chunks issued after s) x PW loads
         // of this wave are outstanding; after the raw barrier (a
@@ -984,41 +1019,75 @@ __global__ __launch_bounds__(GT) void gm_dec_value_ring_kernel(const float* __re
             const char* st = ring + (s % VR_NB) * VR_CHUNK + c * ES;
             const float* ps = p + s * CK;
             const float* svs = sv + s * CK;
-            const int m = min(CK, n - s * CK), nb = m / B;
-            auto ld = [&](int b, int k) {
+            const int m = min(CK, n - s * CK);
+            if constexpr (!KV8) {
+                // batch k: keys 8k .. 8k + 7 of the chunk
+                float vb[3][8], pb[3][8];
+                auto ld = [&](int b, int k) __attribute__((always_inline)) {
 #pragma unroll
-                for (int u = 0; u < B; u += 4) {
-                    const float4 p4 = *reinterpret_cast<const float4*>(ps + k * B + u);
-                    pb[b][u] = p4.x; pb[b][u + 1] = p4.y; pb[b][u + 2] = p4.z; pb[b][u + 3] = p4.w;
+                    for (int u = 0; u < 8; ++u) vb[b][u] = *reinterpret_cast<const float*>(st + (8 * k + u) * RB);
+                    const float4 p0 = *reinterpret_cast<const float4*>(ps + 8 * k);
+                    const float4 p1 = *reinterpret_cast<const float4*>(ps + 8 * k + 4);
+                    pb[b][0] = p0.x; pb[b][1] = p0.y; pb[b][2] = p0.z; pb[b][3] = p0.w;
+                    pb[b][4] = p1.x; pb[b][5] = p1.y; pb[b][6] = p1.z; pb[b][7] = p1.w;
+                };
+                auto fm = [&](int b) __attribute__((always_inline)) {
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(pb[b][u], vb[b][u], acc);
+                };
+                if (m == CK) {  // a whole chunk: straight-line, two batches in flight
+                    constexpr int NB = CK / 8;
+                    ld(0, 0);
+                    ld(1, 1);
+#pragma unroll
+                    for (int k = 0; k < NB; ++k) {
+                        __builtin_amdgcn_sched_barrier(0);
+                        fm(k % 3);
+                        if (k + 2 < NB) ld((k + 2) % 3, k + 2);
+                    }
+                } else {  // the last, partial chunk: a batch at a time, then key by key
+                    int k = 0;
+                    for (; 8 * k + 8 <= m; ++k) {
+                        ld(0, k);
+                        fm(0);
+                    }
+                    for (int jj = 8 * k; jj < m; ++jj)
+                        acc = __builtin_fmaf(ps[jj], *reinterpret_cast<const float*>(st + jj * RB), acc);
                 }
+            } else {
+                constexpr int B = 16;
+                float vb[2][B], pb[2][B];
+                const int nb = m / B;
+                auto ld = [&](int b, int k) {
 #pragma unroll
-                for (int u = 0; u < B; ++u) {
-                    if constexpr (KV8) vb[b][u] = (float)*reinterpret_cast<const int8_t*>(st + (k * B + u) * RB) * svs[k * B + u];
-                    else vb[b][u] = *reinterpret_cast<const float*>(st + (k * B + u) * RB);
-                }
-            };
-            auto fm = [&](int b) {
+                    for (int u = 0; u < B; u += 4) {
+                        const float4 p4 = *reinterpret_cast<const float4*>(ps + k * B + u);
+                        pb[b][u] = p4.x; pb[b][u + 1] = p4.y; pb[b][u + 2] = p4.z; pb[b][u + 3] = p4.w;
+                    }
 #pragma unroll
-                for (int u = 0; u < B; ++u) acc = __builtin_fmaf(pb[b][u], vb[b][u], acc);
-            };
-            if (nb > 0) {
-                ld(0, 0);
-                __builtin_amdgcn_sched_barrier(0);
-                int k = 0;
-                for (; k + 2 <= nb; k += 2) {
-                    ld(1, k + 1);
+                    for (int u = 0; u < B; ++u)
+                        vb[b][u] = (float)*reinterpret_cast<const int8_t*>(st + (k * B + u) * RB) * svs[k * B + u];
+                };
+                auto fm = [&](int b) {
+#pragma unroll
+                    for (int u = 0; u < B; ++u) acc = __builtin_fmaf(pb[b][u], vb[b][u], acc);
+                };
+                if (nb > 0) {
+                    ld(0, 0);
                     __builtin_amdgcn_sched_barrier(0);
-                    fm(0);
-                    ld(0, min(k + 2, nb - 1));
-                    __builtin_amdgcn_sched_barrier(0);
-                    fm(1);
+                    int k = 0;
+                    for (; k + 2 <= nb; k += 2) {
+                        ld(1, k + 1);
+                        __builtin_amdgcn_sched_barrier(0);
+                        fm(0);
+                        ld(0, min(k + 2, nb - 1));
+                        __builtin_amdgcn_sched_barrier(0);
+                        fm(1);
+                    }
+                    if (k < nb) fm(0);
                 }
-                if (k < nb) fm(0);
-            }
-            for (int jj = nb * B; jj < m; ++jj) {
-                const float v = KV8 ? (float)*reinterpret_cast<const int8_t*>(st + jj * RB) * svs[jj]
-                                    : *reinterpret_cast<const float*>(st + jj * RB);
-                acc = __builtin_fmaf(ps[jj], v, acc);
+                for (int jj = nb * B; jj < m; ++jj)
+                    acc = __builtin_fmaf(ps[jj], (float)*reinterpret_cast<const int8_t*>(st + jj * RB) * svs[jj], acc);
             }
         }
     }
@@ -1294,7 +1363,7 @@ int value_ring_cw(size_t hd) {
     return hd % 16 == 0 ? 16 : 0;
 }
 size_t value_ring_lds(size_t ps) {
-    return (2 * ps + seq_sum_spec_scratch(GT)) * sizeof(float) + (size_t)VR_NB * VR_CHUNK;
+    return (2 * ps + seq_sum_spec_scratch(VT)) * sizeof(float) + (size_t)VR_NB * VR_CHUNK;
 }
 
 template <bool KV8, int RB>
@@ -1302,7 +1371,7 @@ hipError_t value_ring_t(const frq_gemma* g, const float* sc, int sl, int win, in
                         const int8_t* vq, const float* vs, float* att, hipStream_t s) {
     constexpr int CW = RB / (KV8 ? 1 : 4);
     const size_t lds = value_ring_lds(ps);
-    gm_dec_value_ring_kernel<KV8, RB><<<dim3((unsigned)g->H, (unsigned)(g->hd / CW)), dim3(GT), lds, s>>>(
+    gm_dec_value_ring_kernel<KV8, RB><<<dim3((unsigned)g->H, (unsigned)(g->hd / CW)), dim3(VT), lds, s>>>(
         sc, (int)g->H, (int)g->KV, (int)g->hd, g->cur, vc, vq, vs, sl, win, ps, att);
     return hipGetLastError();
 }
@@ -1313,22 +1382,14 @@ hipError_t launch_value_ring(const frq_gemma* g, int sl, int win, int ps, const 
                              const float* vs, float* att, hipStream_t s) {
     const int cw = value_ring_cw(g->hd);
     if (!cw || value_ring_lds(ps) > GM_LDS_MAX) return hipErrorNotSupported;
-    if (g->kv8) {
-        if (cw == 64) return value_ring_t<true, 64>(g, g->sc, sl, win, ps, vc, vq, vs, att, s);
-        if (cw == 32) return value_ring_t<true, 32>(g, g->sc, sl, win, ps, vc, vq, vs, att, s);
-        return value_ring_t<true, 16>(g, g->sc, sl, win, ps, vc, vq, vs, att, s);
-    }
-    if (cw == 64) return value_ring_t<false, 256>(g, g->sc, sl, win, ps, vc, vq, vs, att, s);
-    if (cw == 32) return value_ring_t<false, 128>(g, g->sc, sl, win, ps, vc, vq, vs, att, s);
+    if (g->kv8) return value_ring_t<true, 16>(g, g->sc, sl, win, ps, vc, vq, vs, att, s);
     return value_ring_t<false, 64>(g, g->sc, sl, win, ps, vc, vq, vs, att, s);
 }
 
 hipError_t allow_value_ring_lds(size_t ps) {
     const size_t lds = value_ring_lds(ps);
     if (lds > GM_LDS_MAX) return hipSuccess;  // the caller takes the other kernel
-    const void* ks[] = {(const void*)gm_dec_value_ring_kernel<false, 256>, (const void*)gm_dec_value_ring_kernel<false, 128>,
-                        (const void*)gm_dec_value_ring_kernel<false, 64>, (const void*)gm_dec_value_ring_kernel<true, 64>,
-                        (const void*)gm_dec_value_ring_kernel<true, 32>, (const void*)gm_dec_value_ring_kernel<true, 16>};
+    const void* ks[] = {(const void*)gm_dec_value_ring_kernel<false, 64>, (const void*)gm_dec_value_ring_kernel<true, 16>};
     for (const void* k : ks)
         if (hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds)) return e;
     return hipSuccess;

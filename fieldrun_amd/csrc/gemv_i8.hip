@@ -490,7 +490,13 @@ hipError_t launch_linear_m1(const Weight& w, const float* a, float* out, int32_t
         return launch_lm1<8, 8, true, 1>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 768, s);
     if (nch <= 64) return launch_lm1<16, 4, true, 1>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 768, s);
     if (nch <= 128) return launch_lm1<64, 2, true, 2>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 1024, s);
-    if (nch <= 256) return launch_lm1<64, 4, true, 4>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 1024, s);
+    if (nch <= 256) {
+        // about two 4-row groups a workgroup, both in flight during the
+        // quant (more workgroups each repeat the quant for less streaming)
+        const size_t n_rg = (w.n + 3) / 4;
+        const int gd = n_rg <= 1280 ? 512 : n_rg <= 2560 ? 768 : 1024;
+        return launch_lm1<64, 4, true, 4>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : gd, s);
+    }
     if (nch <= 512) return launch_lm1<64, 8, true, 8>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 512, s);
     // long rows: 1024 threads (a quarter of the quant per thread), every
     // workgroup's first group in flight during the quant
