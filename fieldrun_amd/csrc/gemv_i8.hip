@@ -500,9 +500,10 @@ hipError_t launch_linear_m1(const Weight& w, const float* a, float* out, int32_t
     if (nch <= 512) return launch_lm1<64, 8, true, 8>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 512, s);
     // long rows: 1024 threads (a quarter of the quant per thread), every
     // workgroup's first group in flight during the quant
-    // (128 lanes, two waves, per row: 8 rows per group)
-    if (nch <= 1024) return launch_lm1<128, 8, false, 4, 1024>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 256, s);
-    return launch_lm1<128, 10, false, 5, 1024>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 256, s);
+    // (256 lanes, four waves, per row: 4 rows per group, at most 5 chunks a
+    // lane — 116 VGPRs; 128 lanes with 10 chunks spilled to scratch)
+    if (nch <= 1024) return launch_lm1<256, 4, false, 4, 1024>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 256, s);
+    return launch_lm1<256, 5, false, 5, 1024>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 256, s);
 }
 
 }  // namespace frq
