@@ -1689,7 +1689,10 @@ int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_o
         GMCHK(norm(g->ob, g->post_of(l, 1), g->norm_of(l, 2), (int)m, 0), "launch norm");
         if (int rc = mm(g->gu[l], g->a, g->gub)) return rc;
         const float gc = sqrtf(2.0f / 3.14159274101257324f);
-        if (q8f && is_i8(g->down[l])) {  // act(gate) * up and its quant in one kernel
+        // rows the fused quant + GEMV covers take the elementwise act, then
+        // that linear; longer int8 rows the act + quant kernel, then the
+        // GEMV on the quantised row
+        if (q8f && is_i8(g->down[l]) && !linear_m1_ok(*weight_of(g->down[l]), g->hm)) {
             const Q8 q = gm_q8(g, 1, g->ffn);
             GMCHK(launch_act_quant(g, gc, q, err, s), "launch act + quant");
             if (int rc = frq_mm_i8_q_dev(c, g->down[l], q.a8, q.sa, q.oi, q.ov, 1, g->ob)) return rc;
