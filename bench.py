@@ -283,6 +283,7 @@ def main():
     gbs = lay_bytes / (lay_us * 1e-6) / 1e9
     roofline = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from("linear_m1_config4_pmc.md"),
+                "traffic_per": "one launch of each of the layer's four shapes (FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
                 "kernel": "linear_m1_kernel (fused quant + GEMV, M=1), one configs[4] layer's four launches",
                 "bytes_per_layer": lay_bytes, "us_per_layer": round(lay_us, 2), "launches": lin}
     log(f"decode linears: {lin}")

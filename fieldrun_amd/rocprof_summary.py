@@ -15,6 +15,14 @@
       (FETCH_SIZE, then WRITE_SIZE; *_counter_collection.csv).  Each counter
       (KiB per dispatch) is scaled by the factor that makes the same counter
       read N bytes on the device-to-device copy of N bytes in the same run.
+
+  python3 -m fieldrun_amd.rocprof_summary pmc-layer --fetch CSV --write CSV
+          --kernel PREFIX --per-shape R --shapes S --copy-bytes N
+          --algo-bytes B [--command-fetch CMD] [--command-write CMD]
+      The same for a workload that launches S shapes of kernels named
+      PREFIX... R times each, in order: the dispatches are split into S runs
+      of R by dispatch order, each run's mean taken, and the S means summed
+      (one launch of each shape, e.g. one model layer's linears).
 """
 from __future__ import annotations
 
@@ -138,6 +146,50 @@ def pmc(args) -> str:
     return "\n".join(lines) + "\n"
 
 
+def _dispatches(path: str, counter: str, prefix: str):
+    """(dispatch id, counter value) of the kernels whose short name starts
+    with `prefix`, in dispatch order."""
+    out = []
+    for r in _rows(path):
+        if r.get("Counter_Name", "").strip() != counter:
+            continue
+        if short_name(r["Kernel_Name"]).startswith(prefix):
+            out.append((int(r.get("Dispatch_Id", 0) or 0), float(r["Counter_Value"]), short_name(r["Kernel_Name"])))
+    out.sort()
+    return out
+
+
+def pmc_layer(args) -> str:
+    lines = []
+    total = 0.0
+    for counter, path, cmd in (("FETCH_SIZE", args.fetch, args.command_fetch),
+                               ("WRITE_SIZE", args.write, args.command_write)):
+        table = _per_kernel(path, counter, largest_grid=(args.copy_kernel,))
+        cname, (cval, cn) = _pick(table, args.copy_kernel, counter + " copy")
+        factor = args.copy_bytes / (cval * 1024.0)
+        ds = _dispatches(path, counter, args.kernel)
+        if len(ds) != args.per_shape * args.shapes:
+            sys.exit(f"{counter}: {len(ds)} dispatches of {args.kernel}..., expected {args.per_shape * args.shapes}")
+        if cmd:
+            lines += [f"{counter} run:", "", "    " + cmd, ""]
+        lines.append(f"- `{cname}` ({cn} dispatches of {args.copy_bytes} bytes): {counter} = {cval:.0f} KiB"
+                     f" per dispatch, scale factor {factor:.4f}")
+        sub = 0.0
+        for i in range(args.shapes):
+            run = ds[i * args.per_shape:(i + 1) * args.per_shape]
+            kv = sum(x[1] for x in run) / len(run)
+            b = kv * 1024.0 * factor
+            sub += b
+            lines.append(f"- shape {i} `{run[0][2]}` ({len(run)} dispatches): {counter} = {kv:.0f} KiB per dispatch"
+                         f" -> {b:.0f} bytes")
+        lines += [f"- {counter} over one launch of each shape: {sub:.0f} bytes", ""]
+        total += sub
+    lines += [f"Algorithmic bytes (one launch of each shape): {args.algo_bytes}",
+              f"Measured HBM traffic / algorithmic: {total / args.algo_bytes:.3f}", "",
+              f"traffic_bytes_per_launch: {int(round(total))}"]
+    return "\n".join(lines) + "\n"
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     sub = ap.add_subparsers(dest="mode", required=True)
@@ -158,8 +210,19 @@ def main(argv=None):
     p.add_argument("--algo-bytes", type=int, required=True)
     p.add_argument("--command-fetch", default="")
     p.add_argument("--command-write", default="")
+    pl = sub.add_parser("pmc-layer")
+    pl.add_argument("--fetch", required=True)
+    pl.add_argument("--write", required=True)
+    pl.add_argument("--kernel", required=True)
+    pl.add_argument("--per-shape", type=int, required=True)
+    pl.add_argument("--shapes", type=int, required=True)
+    pl.add_argument("--copy-kernel", default="copyBuffer")
+    pl.add_argument("--copy-bytes", type=int, required=True)
+    pl.add_argument("--algo-bytes", type=int, required=True)
+    pl.add_argument("--command-fetch", default="")
+    pl.add_argument("--command-write", default="")
     a = ap.parse_args(argv)
-    sys.stdout.write({"stats": stats, "trace": trace, "pmc": pmc}[a.mode](a))
+    sys.stdout.write({"stats": stats, "trace": trace, "pmc": pmc, "pmc-layer": pmc_layer}[a.mode](a))
 
 
 if __name__ == "__main__":
