@@ -198,7 +198,7 @@ int rows_exact(frq_ctx* c, const frq_w* wh, const float* d_a, size_t m, float* d
     void* gws = cv.take<char>(gemm_ws_bytes(m, w.kp, w.np));
     int32_t* acc = reinterpret_cast<int32_t*>((char*)c->ws + base);
     HIPCHK(launch_quant(d_a, m, w.k, w.kp, a8, sa, oi, ov, c->err, c->stream, mp), "launch quant");
-    HIPCHK(launch_gemm_i8(w, m, a8, sa, oi, ov, d_out, acc, gws, c->stream), "launch gemm_i8");
+    HIPCHK(launch_gemm_i8(w, m, a8, sa, oi, ov, d_out, acc, gws, c->stream, true), "launch gemm_i8");
     HIPCHK(launch_i8_exact_epilogue(w, m, sa, oi, ov, acc, d_out, c->stream), "launch i8 epilogue");
     return FRQ_OK;
 }

@@ -351,9 +351,10 @@ size_t gemm_ws_bytes(size_t m, size_t kp, size_t np);
 hipError_t launch_gemm_i8(const Weight& w, size_t m, const int8_t* a8b,
                           const float* sa, const uint32_t* oidx,
                           const float* oval, float* out, int32_t* acc, void* ws,
-                          hipStream_t s);
+                          hipStream_t s, bool acc_only = false);
 // out = scale * (sa * acc + corr) from the GEMM's i32 sums with the
-// reference's sequential outlier correction (the skinny kernel's order)
+// reference's sequential outlier correction (the skinny kernel's order);
+// acc_only above skips the GEMM's own approximate correction for this
 hipError_t launch_i8_exact_epilogue(const Weight& w, size_t m, const float* sa, const uint32_t* oidx,
                                     const float* oval, const int32_t* acc, float* out, hipStream_t s);
 // Context and weight internals, for engines built on the entry points: the

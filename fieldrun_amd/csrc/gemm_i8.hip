@@ -292,8 +292,9 @@ __device__ __forceinline__ void tr4(const uint32_t* in, uint32_t* out) {
 // MODE 0: the whole K range, then the epilogue.  MODE 1 (split K): workgroup
 // b runs k-split b % nsplit of tile b / nsplit and stores its int32 tile to
 // part.  MODE 2: one workgroup per tile adds the tile's nsplit partial tiles
-// in split order (exact) and runs the epilogue.
-template <int BN, int NST, int MODE>
+// in split order (exact) and runs the epilogue.  AO: the epilogue only
+// stores the exact int32 sums to acc (i8_exact_epilogue then forms out).
+template <int BN, int NST, int MODE, bool AO>
 __global__ __launch_bounds__(256, 2) void gemm_i8_kernel(
     const int8_t* __restrict__ Ab, const int8_t* __restrict__ Wb,
     const int8_t* __restrict__ Wkn, const int8_t* __restrict__ Wrow,
@@ -390,6 +391,20 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_kernel(
 #pragma unroll
                 for (int bn = 0; bn < TN; ++bn)
                     acc[bm][bn] += *reinterpret_cast<const v4i*>(pt + ((size_t)q * TM * TN + bm * TN + bn) * 1024);
+    }
+    if constexpr (AO) {
+        // 16 lanes cover 64 contiguous bytes of a row per store
+#pragma unroll
+        for (int bm = 0; bm < TM; ++bm)
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int bn = 0; bn < TN; ++bn) {
+                    const int i = m0 + wm * 64 + bm * 16 + (lane >> 4) * 4 + c;
+                    const int j = n0 + wn * (BN / 2) + bn * 16 + (lane & 15);
+                    if (i < M && j < N) acc_dbg[(size_t)i * N + j] = acc[bm][bn][c];
+                }
+        return;
     }
     __syncthreads();  // every fragment read; the ring is free for the epilogue
 
@@ -655,14 +670,14 @@ Prep carve_prep(void* ws, size_t mp, size_t kp) {
     return p;
 }
 
-template <int BN, int NST, int MODE>
+template <int BN, int NST, int MODE, bool AO>
 hipError_t launch_k(const Weight& w, size_t m, const int8_t* a8b, const float* sa,
                     const uint32_t* oidx, const float* oval, float* out, int32_t* acc,
                     const Prep& p, int split, hipStream_t s) {
     const int MT = (int)((m + GBM - 1) / GBM), NT = (int)(w.np / BN);
     const size_t lds = (size_t)NST * (GBM + BN) / 16 * 1024;
     const int t = (int)(w.k < FRQ_T ? w.k : FRQ_T);
-    auto kern = gemm_i8_kernel<BN, NST, MODE>;
+    auto kern = gemm_i8_kernel<BN, NST, MODE, AO>;
     static bool attr_set = false;  // per process; the attribute is per function
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -677,45 +692,118 @@ hipError_t launch_k(const Weight& w, size_t m, const int8_t* a8b, const float* s
     return hipGetLastError();
 }
 
-template <int BN, int NST>
+template <int BN, int NST, bool AO>
 hipError_t launch_t(const Weight& w, size_t m, const int8_t* a8b, const float* sa,
                     const uint32_t* oidx, const float* oval, float* out, int32_t* acc,
                     const Prep& p, int split, hipStream_t s) {
-    if (split <= 1) return launch_k<BN, NST, 0>(w, m, a8b, sa, oidx, oval, out, acc, p, 1, s);
-    if (hipError_t e = launch_k<BN, NST, 1>(w, m, a8b, sa, oidx, oval, out, acc, p, split, s); e != hipSuccess)
+    if (split <= 1) return launch_k<BN, NST, 0, AO>(w, m, a8b, sa, oidx, oval, out, acc, p, 1, s);
+    if (hipError_t e = launch_k<BN, NST, 1, AO>(w, m, a8b, sa, oidx, oval, out, acc, p, split, s); e != hipSuccess)
         return e;
-    return launch_k<BN, NST, 2>(w, m, a8b, sa, oidx, oval, out, acc, p, split, s);
+    return launch_k<BN, NST, 2, AO>(w, m, a8b, sa, oidx, oval, out, acc, p, split, s);
 }
 
-// out[i, j] = scale[j] * (sa[i] * (acc[i, j] as f32) + corr), corr the
-// reference's M > 1 sum over row i's outliers (ascending channel, from -0.0,
-// each product rounded before its add: bundle.rs:732-743), from the GEMM's
-// exact i32 sums: the skinny kernel's arithmetic, bit for bit.  A thread takes
-// four adjacent columns of one row (blockIdx.y); an outlier's four weights
-// are one 32-bit word of the (Kp, Np) copy, the row's outliers uniform loads.
-__global__ __launch_bounds__(256) void i8_exact_epilogue(const int8_t* __restrict__ wkn, int Np, int Kp,
-                                                         const float* __restrict__ scale, int N, int t,
-                                                         const float* __restrict__ sa,
-                                                         const uint32_t* __restrict__ oidx,
-                                                         const float* __restrict__ oval,
-                                                         const int32_t* __restrict__ acc, float* __restrict__ out) {
-    const int i = blockIdx.y, j0 = 4 * (blockIdx.x * 256 + threadIdx.x);
-    if (j0 >= N) return;
-    const uint32_t* oi = oidx + (size_t)i * FRQ_T;
-    const float* ov = oval + (size_t)i * FRQ_T;
-    float corr[4] = {-0.0f, -0.0f, -0.0f, -0.0f};
-    for (int q = 0; q < t; ++q) {
-        const uint32_t ch = min(oi[q], (uint32_t)(Kp - 1));
-        const uint32_t wq = *reinterpret_cast<const uint32_t*>(wkn + (size_t)ch * Np + j0);  // j0 + 3 < Np
-        const float o = ov[q];
+// The engines' exact epilogue for M > 16 rows: out[i, j] = scale[j] *
+// (sa[i] * (acc[i, j] as f32) + corr), corr the reference's M > 1 sum over
+// row i's outliers (ascending channel, from -0.0, each product rounded
+// before its add: bundle.rs:732-743), from the GEMM's exact i32 sums: the
+// skinny kernel's arithmetic, bit for bit.  A workgroup owns JB adjacent
+// columns for a share of the rows.  Their weights, Kp x JB bytes from the
+// (Np, Kp) rows, sit in LDS channel-major, SW words a channel (an odd
+// number, so the random channels of 64 rows spread over the banks): each
+// outlier's JB weights are JB / 4 word reads, and the weights of a column
+// block come from HBM once however dense the rows' outlier channels are.
+// A thread takes one row at a time with its 32 (channel, value) pairs in
+// registers.  Workgroup b: row chunk b / nblk, column block b % nblk, which
+// within whole runs of 64 blocks puts 8 adjacent blocks on one XCD (16- and
+// 32-byte row segments of acc and out share their lines there).
+constexpr size_t EPI_LDS = 80 * 1024;
+__host__ __device__ constexpr int epi_sw(int jb) { return (jb / 4) % 2 ? jb / 4 : jb / 4 + 1; }
+inline size_t epi_lds(int jb, size_t kp) { return kp * (size_t)epi_sw(jb) * 4; }
+
+template <int JB, int NT>
+__global__ __launch_bounds__(NT) void i8_exact_epilogue(const int8_t* __restrict__ wt, int Kp,
+                                                        const float* __restrict__ scale, int N, int M, int t,
+                                                        const float* __restrict__ sa,
+                                                        const uint32_t* __restrict__ oidx,
+                                                        const float* __restrict__ oval,
+                                                        const int32_t* __restrict__ acc, float* __restrict__ out,
+                                                        int nblk, int rch) {
+    constexpr int SW = epi_sw(JB), JQ = JB / 4;
+    extern __shared__ uint32_t wl[];
+    const int tid = threadIdx.x;
+    const int b = (int)blockIdx.x, rc = b / nblk, xb = b % nblk;
+    const int cb = (nblk % 8 == 0 && (xb / 64 + 1) * 64 <= nblk) ? (xb / 64) * 64 + (xb % 8) * 8 + (xb % 64) / 8 : xb;
+    const int n0 = JB * cb;
+    // the block's weights: 4 rows x 4 channels a thread, transposed to 4
+    // channel words (byte x of word y: column 4jq + x of channel 4cq + y)
+    const int nq = Kp >> 2;
+    for (int x = tid; x < JQ * nq; x += NT) {
+        const int jq = x / nq, cq = x - jq * nq;
+        const int8_t* src = wt + (size_t)(n0 + 4 * jq) * Kp + 4 * cq;
+        uint32_t r[4], o[4];
 #pragma unroll
-        for (int b = 0; b < 4; ++b) corr[b] = corr[b] + o * (float)(int8_t)(wq >> (8 * b));
+        for (int u = 0; u < 4; ++u) r[u] = *reinterpret_cast<const uint32_t*>(src + (size_t)u * Kp);
+        tr4(r, o);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) wl[(4 * cq + u) * SW + jq] = o[u];
     }
-    const float s = sa[i];
+    float scl[JB];
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-        const int j = j0 + b;
-        if (j < N) out[(size_t)i * N + j] = scale[j] * (s * (float)acc[(size_t)i * N + j] + corr[b]);
+    for (int j = 0; j < JB; ++j) scl[j] = scale[n0 + j];  // Np entries
+    __syncthreads();
+    const bool vec = (N & 3) == 0 && n0 + JB <= N;
+    for (int i = rc * NT + tid; i < M; i += rch * NT) {
+        uint32_t ch[FRQ_T];
+        float ov[FRQ_T];
+#pragma unroll
+        for (int v = 0; v < FRQ_T / 4; ++v) {
+            const uint4 c4 = reinterpret_cast<const uint4*>(oidx + (size_t)i * FRQ_T)[v];
+            const float4 o4 = reinterpret_cast<const float4*>(oval + (size_t)i * FRQ_T)[v];
+            ch[4 * v] = c4.x; ch[4 * v + 1] = c4.y; ch[4 * v + 2] = c4.z; ch[4 * v + 3] = c4.w;
+            ov[4 * v] = o4.x; ov[4 * v + 1] = o4.y; ov[4 * v + 2] = o4.z; ov[4 * v + 3] = o4.w;
+        }
+        int32_t a[JB];
+        const int32_t* ar = acc + (size_t)i * N + n0;
+        if (vec) {
+#pragma unroll
+            for (int q = 0; q < JQ; ++q) {
+                const int4 v = reinterpret_cast<const int4*>(ar)[q];
+                a[4 * q] = v.x; a[4 * q + 1] = v.y; a[4 * q + 2] = v.z; a[4 * q + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < JB; ++j) a[j] = n0 + j < N ? ar[j] : 0;
+        }
+        float corr[JB];
+#pragma unroll
+        for (int j = 0; j < JB; ++j) corr[j] = -0.0f;
+#pragma unroll
+        for (int q = 0; q < FRQ_T; ++q) {
+            if (q < t) {  // uniform: t = min(K, 32)
+                const uint32_t* wq = wl + min(ch[q], (uint32_t)(Kp - 1)) * SW;
+#pragma unroll
+                for (int m = 0; m < JQ; ++m) {
+                    const uint32_t wv = wq[m];
+#pragma unroll
+                    for (int x = 0; x < 4; ++x)
+                        corr[4 * m + x] = corr[4 * m + x] + ov[q] * (float)(int8_t)(wv >> (8 * x));
+                }
+            }
+        }
+        const float s = sa[i];
+        float r[JB];
+#pragma unroll
+        for (int j = 0; j < JB; ++j) r[j] = scl[j] * (s * (float)a[j] + corr[j]);
+        float* orow = out + (size_t)i * N + n0;
+        if (vec) {
+#pragma unroll
+            for (int q = 0; q < JQ; ++q)
+                reinterpret_cast<float4*>(orow)[q] = make_float4(r[4 * q], r[4 * q + 1], r[4 * q + 2], r[4 * q + 3]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < JB; ++j)
+                if (n0 + j < N) orow[j] = r[j];
+        }
     }
 }
 
@@ -741,14 +829,20 @@ size_t gemm_ws_bytes(size_t m, size_t kp, size_t np) {
 hipError_t launch_gemm_i8(const Weight& w, size_t m, const int8_t* a8b,
                           const float* sa, const uint32_t* oidx,
                           const float* oval, float* out, int32_t* acc, void* ws,
-                          hipStream_t s) {
+                          hipStream_t s, bool acc_only) {
     // a8b holds round_up(m, 128) blocked rows; wblk / wkn are padded to Np
     // (a multiple of 256) and Kp (a multiple of 128); Kp <= 20480 keeps the
     // channel bitmap within its 640 LDS words; ws holds
     // gemm_ws_bytes(m, Kp, Np)
-    if (w.kp > 20480 || !w.wblk || !ws) return hipErrorInvalidValue;
+    if (w.kp > 20480 || !w.wblk || !ws || (acc_only && !acc)) return hipErrorInvalidValue;
     const size_t mp = round_up(m, GBM);
     const Prep p = carve_prep(ws, mp, w.kp);
+    const Plan pl = plan_of(m, w.kp, w.np);
+    if (acc_only) {  // no correction operands: the exact epilogue follows
+        if (pl.bn == 256) return launch_t<256, 3, true>(w, m, a8b, sa, oidx, oval, out, acc, p, pl.split, s);
+        if (pl.bn == 224) return launch_t<224, 3, true>(w, m, a8b, sa, oidx, oval, out, acc, p, pl.split, s);
+        return launch_t<128, 4, true>(w, m, a8b, sa, oidx, oval, out, acc, p, pl.split, s);
+    }
     const int MT = (int)(mp / GBM), nchmax = p.cap / CH;
     const int t = (int)(w.k < FRQ_T ? w.k : FRQ_T);
     // chunk groups: enough workgroups to build a dense union's chunks in
@@ -757,21 +851,44 @@ hipError_t launch_gemm_i8(const Weight& w, size_t m, const int8_t* a8b,
     gemm_prep_kernel<<<dim3((unsigned)MT, (unsigned)ncg), dim3(256), 0, s>>>(
         (int)m, (int)w.k, (int)w.kp, t, oidx, oval, p.cap, p.nu, p.uch, p.so, p.fin, p.D);
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-    const Plan pl = plan_of(m, w.kp, w.np);
-    if (pl.bn == 256) return launch_t<256, 3>(w, m, a8b, sa, oidx, oval, out, acc, p, pl.split, s);
-    if (pl.bn == 224) return launch_t<224, 3>(w, m, a8b, sa, oidx, oval, out, acc, p, pl.split, s);
-    return launch_t<128, 4>(w, m, a8b, sa, oidx, oval, out, acc, p, pl.split, s);
+    if (pl.bn == 256) return launch_t<256, 3, false>(w, m, a8b, sa, oidx, oval, out, acc, p, pl.split, s);
+    if (pl.bn == 224) return launch_t<224, 3, false>(w, m, a8b, sa, oidx, oval, out, acc, p, pl.split, s);
+    return launch_t<128, 4, false>(w, m, a8b, sa, oidx, oval, out, acc, p, pl.split, s);
+}
+
+template <int JB>
+hipError_t launch_epi(const Weight& w, size_t m, const float* sa, const uint32_t* oidx, const float* oval,
+                      const int32_t* acc, float* out, hipStream_t s) {
+    constexpr int NT = 512;
+    const int t = (int)(w.k < FRQ_T ? w.k : FRQ_T);
+    const int nblk = (int)((w.n + JB - 1) / JB);
+    // row chunks so that about two rounds of workgroups fill the chip
+    const int rch = (int)std::max<size_t>(1, std::min<size_t>((m + NT - 1) / NT, (size_t)(1024 + nblk - 1) / nblk));
+    const size_t lds = epi_lds(JB, w.kp);
+    auto kern = i8_exact_epilogue<JB, NT>;
+    static bool attr_set = false;  // per process; the attribute is per function
+    if (!attr_set) {
+        if (hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               (int)EPI_LDS);
+            e != hipSuccess)
+            return e;
+        attr_set = true;
+    }
+    kern<<<dim3((unsigned)(nblk * rch)), dim3(NT), lds, s>>>(w.wt, (int)w.kp, w.scale, (int)w.n, (int)m, t, sa,
+                                                            oidx, oval, acc, out, nblk, rch);
+    return hipGetLastError();
 }
 
 hipError_t launch_i8_exact_epilogue(const Weight& w, size_t m, const float* sa, const uint32_t* oidx,
                                     const float* oval, const int32_t* acc, float* out, hipStream_t s) {
     if (m == 0 || w.n == 0) return hipSuccess;
-    if (!w.wkn || m > 65535 || w.np % 4 || w.np < w.n || w.kp == 0) return hipErrorInvalidValue;
-    const int t = (int)(w.k < FRQ_T ? w.k : FRQ_T);
-    const size_t n4 = (w.n + 3) / 4;
-    i8_exact_epilogue<<<dim3((unsigned)((n4 + 255) / 256), (unsigned)m), dim3(256), 0, s>>>(
-        w.wkn, (int)w.np, (int)w.kp, w.scale, (int)w.n, t, sa, oidx, oval, acc, out);
-    return hipGetLastError();
+    // the weight block comes from the (Np, Kp) rows (Np a multiple of 256,
+    // Kp of 128: whole blocks, whole channel quads, in bounds)
+    if (!w.wt || m > 65535 || w.np % 256 || w.np < w.n || w.kp == 0 || w.kp % 128 || w.kp > 20480)
+        return hipErrorInvalidValue;
+    if (epi_lds(16, w.kp) <= EPI_LDS) return launch_epi<16>(w, m, sa, oidx, oval, acc, out, s);
+    if (epi_lds(8, w.kp) <= EPI_LDS) return launch_epi<8>(w, m, sa, oidx, oval, acc, out, s);
+    return launch_epi<4>(w, m, sa, oidx, oval, acc, out, s);
 }
 
 }  // namespace frq

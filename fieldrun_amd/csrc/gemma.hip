@@ -2027,6 +2027,19 @@ int frq_gemma_predict(frq_ctx* c, frq_gemma* g, const int64_t* ids, size_t n, in
     return gm_run(c, g, ids, n, 1, token, logits);
 }
 
+int frq_mm_exact_dev(frq_ctx* c, const frq_w* w, const float* d_a, size_t m, float* d_out) {
+    if (!c) return set_error(FRQ_ERR_ARG, "null context");
+    if (!w) return set_error(FRQ_ERR_ARG, "null weight");
+    const Weight& ww = *weight_of(w);
+    if (ww.dtype != FRQ_DT_I8 && ww.dtype != FRQ_DT_I4 && ww.dtype != FRQ_DT_Q4A)
+        return set_error(FRQ_ERR_DTYPE, "frq_mm_exact_dev: not a linear weight");
+    if (ww.device != ctx_device(c)) return set_error(FRQ_ERR_ARG, "weight lives on another device");
+    if (m == 0 || ww.n == 0) return FRQ_OK;
+    if (!d_a || !d_out) return set_error(FRQ_ERR_ARG, "null activation/output pointer");
+    GDev dv(ctx_device(c));
+    return gm_mm(c, w, d_a, m, d_out);
+}
+
 int frq_seq_fold_f32(frq_ctx* c, const float* x, size_t rows, size_t n, float init, float* out) {
     if (!c) return set_error(FRQ_ERR_ARG, "null context");
     if (!rows) return FRQ_OK;

@@ -127,6 +127,16 @@ int frq_mm(frq_ctx* ctx, const frq_w* w, const float* a, size_t m,
            float* out);
 int frq_mm_dev(frq_ctx* ctx, const frq_w* w, const float* d_a, size_t m,
                float* d_out);
+/* Bundle::mm (src/bundle.rs:644-919) with every output bit-identical to the
+ * reference's order at any M, on device pointers: int8 at M <= 16 as
+ * frq_mm_dev; at M > 16 the MFMA GEMM's exact int32 sums, then the M > 1
+ * arm's sequential f32 outlier correction and epilogue (732-756); int4 in
+ * i4_dot_avx2's order at M = 1 and the M > 1 arm's per-row order (760-799);
+ * q4a likewise (802-845).  frq_mm_dev's int8 results at M > 16 are within
+ * 1e-6 sum|terms| instead (the correction on the f16 MFMA).  The decode
+ * engines run this linear. */
+int frq_mm_exact_dev(frq_ctx* ctx, const frq_w* w, const float* d_a, size_t m,
+                     float* d_out);
 /* No counterpart in the reference.  frq_mm_dev that allocates nothing, for
  * callers that cannot call hipMalloc (code under HIP graph capture, tight
  * serving loops, harnesses that forbid allocation).  The per-call scratch

@@ -59,6 +59,22 @@ def test_i8_gemv_bit_exact(ctx, m, k, n):
     assert np.array_equal(w.mm(a).view(np.uint32), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("m,k,n", [(17, 896, 4864), (130, 512, 301), (64, 37, 50), (20, 20, 30), (200, 128, 129),
+                                   (1024, 3584, 512), (300, 5000, 257), (600, 18944, 300), (40, 20480, 64),
+                                   (2048, 4096, 256), (1100, 1000, 1001)])
+def test_i8_mm_exact_bit_exact(ctx, m, k, n):
+    """frq_mm_exact_dev at M > 16: the GEMM's exact int32 sums, then the
+    M > 1 arm's sequential outlier correction with every column block's
+    weights in LDS (16, 8 or 4 columns by K; ragged N and M, K below the
+    outlier count), bit for bit against the oracle."""
+    a, wt, scale = case(m, k, n, 300 + m + k + n)
+    w = ctx.upload_i8(wt, scale)
+    ref = oracle.mm_i8_mt(a, wt, scale, 16)
+    got = w.mm_exact(a)
+    bad = np.argwhere(got.view(np.uint32) != ref.view(np.uint32))
+    assert len(bad) == 0, (len(bad), bad[:4].tolist())
+
+
 @pytest.mark.parametrize("m,k,n", [(5, 896, 4864), (16, 4096, 1024), (128, 896, 640), (130, 512, 300),
                                    (64, 37, 50), (16, 14336, 256), (33, 4864, 896), (200, 128, 129),
                                    (128, 14336, 512), (2048, 128, 14336)])
