@@ -589,7 +589,7 @@ def seq_fold_f32(ctx: "Context", x: np.ndarray, init: float = -0.0) -> np.ndarra
     return out
 
 
-LIBM_FNS = {"expf": 0, "expm1f": 1, "tanhf": 2}
+LIBM_FNS = {"expf": 0, "expm1f": 1, "tanhf": 2, "expf_sel": 3}
 
 
 def libm_f32(fn: str, x: np.ndarray, ctx: "Context | None" = None) -> np.ndarray:

@@ -729,6 +729,214 @@ __global__ __launch_bounds__(GT) void gm_attn_group_kernel(const float* __restri
     }
 }
 
+// ---- multi-row attention over an f32 cache, register-tiled ----
+// gm_attn_group_kernel<false>'s arithmetic per output (score = sequential
+// FMA chain over the head dims, max, exp, the key-order sum, divide, value
+// chain in key order), so the same bits, laid out for throughput:
+// - scores: a lane takes two adjacent keys for every head of the group
+//   (RP >= R; heads past R are computed on other q values and never
+//   leave the kernel), so each q value feeds two chains and each key value
+//   RP chains; q is wave-uniform and comes through scalar loads (SGPR
+//   operands), the key rows straight from memory a 32-dim block (one
+//   128-byte line a key) at a time, the next block in flight;
+// - p holds RP rows (rows past R never leave the kernel) so the exps,
+//   divides and stores run RP at a time without per-head tests (the exps
+//   branch-free, their table loads all in flight); its rows are prow apart
+//   with prow % 64 == 4 so the sum lanes' reads spread over the banks;
+// - values: a lane takes 2 dims of 4 heads (hd / 2 lanes a head group),
+//   so a value load feeds 4 heads' chains; the value loads run three 4-key
+//   batches ahead.
+// Needs hd % 32 == 0, hd <= 2 GT and R <= RP <= R + 2 KV (the q reads of
+// heads past R stay inside the qkv row).
+template <int RP>
+__global__ __launch_bounds__(GT) void gm_attn_tile_kernel(const float* __restrict__ qkv, int H, int KV, int hd,
+                                                          const int* __restrict__ curp,
+                                                          const float* __restrict__ kc, const float* __restrict__ vc,
+                                                          float qscale, float cap, int sliding, int window, int prow,
+                                                          float* __restrict__ att, int div) {
+    extern __shared__ float4 lds4[];
+    const int R = H / KV, kvd = KV * hd;
+    float* p = reinterpret_cast<float*>(lds4);  // [RP][prow]
+    __shared__ float red[RP][GT / 64];
+    __shared__ float sums[RP];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kv = blockIdx.x, i = blockIdx.y;
+    const int cur = *curp, ab = cur + i, klen = cur + (int)gridDim.y;
+    const float* row = qkv + (size_t)i * (H + 2 * KV) * hd;
+    const int j0 = (sliding && ab >= window) ? ab - window + 1 : 0;
+    const int nk = ab + 1;
+    float mx[RP];
+#pragma unroll
+    for (int r = 0; r < RP; ++r) mx[r] = -INFINITY;
+    const int nblk = hd >> 5;
+    const float* qrow = row + (size_t)kv * R * hd;  // uniform: scalar loads
+    for (int pb = j0; pb < nk; pb += 2 * GT) {
+        const int ja = pb + 2 * tid;
+        const float* kra = kc + (size_t)min(ja, nk - 1) * kvd + (size_t)kv * hd;
+        const float* krb = kc + (size_t)min(ja + 1, nk - 1) * kvd + (size_t)kv * hd;
+        float acc[2][RP];
+#pragma unroll
+        for (int r = 0; r < RP; ++r) acc[0][r] = acc[1][r] = 0.0f;
+        float4 ka[2][8], kb[2][8];
+        auto ld = [&](int buf, int b) __attribute__((always_inline)) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                ka[buf][u] = *reinterpret_cast<const float4*>(kra + 32 * b + 4 * u);
+                kb[buf][u] = *reinterpret_cast<const float4*>(krb + 32 * b + 4 * u);
+            }
+        };
+        auto fm = [&](int buf, int b) __attribute__((always_inline)) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+#pragma unroll
+                for (int r = 0; r < RP; ++r) {
+                    const float4 q4 = *reinterpret_cast<const float4*>(qrow + r * hd + 32 * b + 4 * u);
+                    acc[0][r] = __builtin_fmaf(q4.x, ka[buf][u].x, acc[0][r]);
+                    acc[0][r] = __builtin_fmaf(q4.y, ka[buf][u].y, acc[0][r]);
+                    acc[0][r] = __builtin_fmaf(q4.z, ka[buf][u].z, acc[0][r]);
+                    acc[0][r] = __builtin_fmaf(q4.w, ka[buf][u].w, acc[0][r]);
+                    acc[1][r] = __builtin_fmaf(q4.x, kb[buf][u].x, acc[1][r]);
+                    acc[1][r] = __builtin_fmaf(q4.y, kb[buf][u].y, acc[1][r]);
+                    acc[1][r] = __builtin_fmaf(q4.z, kb[buf][u].z, acc[1][r]);
+                    acc[1][r] = __builtin_fmaf(q4.w, kb[buf][u].w, acc[1][r]);
+                }
+            }
+        };
+        ld(0, 0);
+        for (int b = 0; b < nblk; b += 2) {
+            ld(1, min(b + 1, nblk - 1));
+            __builtin_amdgcn_sched_barrier(0);
+            fm(0, b);
+            ld(0, min(b + 2, nblk - 1));
+            __builtin_amdgcn_sched_barrier(0);
+            if (b + 1 < nblk) fm(1, b + 1);
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int j = ja + u;
+            if (j < nk) {
+#pragma unroll
+                for (int r = 0; r < RP; ++r) {
+                    float sj = div ? acc[u][r] / qscale : acc[u][r] * qscale;
+                    if (cap > 0.0f) sj = cap * libm::frq_tanhf(sj / cap);
+                    p[(size_t)r * prow + j] = sj;
+                    mx[r] = fmaxf(mx[r], sj);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RP; ++r) {
+        float v = mx[r];
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+        if (lane == 0) red[r][wave] = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < RP; ++r) {
+        float v = red[r][0];
+#pragma unroll
+        for (int w = 1; w < GT / 64; ++w) v = fmaxf(v, red[r][w]);
+        if (j0 > 0 || nk < klen) v = fmaxf(v, -1e30f);  // a masked entry joins the max
+        mx[r] = v;
+    }
+    for (int j = j0 + tid; j < nk; j += GT) {
+        float e[RP];
+#pragma unroll
+        for (int r = 0; r < RP; ++r) e[r] = p[(size_t)r * prow + j];
+#pragma unroll
+        for (int r = 0; r < RP; ++r) e[r] = libm::frq_expf_sel(e[r] - mx[r]);
+#pragma unroll
+        for (int r = 0; r < RP; ++r) p[(size_t)r * prow + j] = e[r];
+    }
+    __syncthreads();
+    if (tid < RP) {  // one lane per head, in key order; the lanes run in step
+        const float* pr = p + (size_t)tid * prow;
+        const int ja = min((j0 + 3) & ~3, nk);
+        float sum = 0.0f;
+        for (int j = j0; j < ja; ++j) sum = sum + pr[j];
+        sums[tid] = lds_seq_sum(pr + ja, nk - ja, sum);
+    }
+    __syncthreads();
+    for (int j = j0 + tid; j < nk; j += GT) {
+        float e[RP];
+#pragma unroll
+        for (int r = 0; r < RP; ++r) e[r] = p[(size_t)r * prow + j];
+#pragma unroll
+        for (int r = 0; r < RP; ++r) p[(size_t)r * prow + j] = e[r] / sums[r];
+    }
+    __syncthreads();
+    // values: lane (dims 2dg, 2dg + 1 of heads r4 .. r4 + 3), keys in order from +0
+    const int DG = hd >> 1, HG = GT / DG;  // lanes a head group, head groups a pass
+    const int ja = min((j0 + 3) & ~3, nk);  // keys before ja one at a time, then 4-key batches
+    const int nb = (nk - ja) >> 2;
+    for (int g0 = 0; 4 * g0 < R; g0 += HG) {
+        const int r4 = 4 * (g0 + tid / DG), dg = tid % DG;
+        if (r4 < R) {
+            const float* pr = p + (size_t)r4 * prow;
+            const float* vb = vc + (size_t)kv * hd + 2 * dg;
+            float2 a[4];
+#pragma unroll
+            for (int h = 0; h < 4; ++h) a[h] = make_float2(0.0f, 0.0f);
+            auto step = [&](int h, float pj, float2 v) __attribute__((always_inline)) {
+                a[h].x = __builtin_fmaf(pj, v.x, a[h].x);
+                a[h].y = __builtin_fmaf(pj, v.y, a[h].y);
+            };
+            for (int j = j0; j < ja; ++j) {
+                const float2 v = *reinterpret_cast<const float2*>(vb + (size_t)j * kvd);
+#pragma unroll
+                for (int h = 0; h < 4; ++h) step(h, pr[(size_t)h * prow + j], v);
+            }
+            float2 vv[3][4];
+            auto vld = [&](int buf, int k) __attribute__((always_inline)) {
+                const int jb = ja + 4 * min(k, nb - 1);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) vv[buf][u] = *reinterpret_cast<const float2*>(vb + (size_t)(jb + u) * kvd);
+            };
+            auto vfm = [&](int buf, int k) __attribute__((always_inline)) {
+#pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    const float4 p4 = *reinterpret_cast<const float4*>(pr + (size_t)h * prow + ja + 4 * k);
+                    step(h, p4.x, vv[buf][0]);
+                    step(h, p4.y, vv[buf][1]);
+                    step(h, p4.z, vv[buf][2]);
+                    step(h, p4.w, vv[buf][3]);
+                }
+            };
+            if (nb > 0) {  // three batches in flight, each consumed unconditionally
+                vld(0, 0);
+                vld(1, 1);
+                vld(2, 2);
+                __builtin_amdgcn_sched_barrier(0);
+                int k = 0;
+                for (; k + 3 <= nb; k += 3) {
+                    vfm(0, k);
+                    vld(0, k + 3);
+                    __builtin_amdgcn_sched_barrier(0);
+                    vfm(1, k + 1);
+                    vld(1, k + 4);
+                    __builtin_amdgcn_sched_barrier(0);
+                    vfm(2, k + 2);
+                    vld(2, k + 5);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                if (k < nb) vfm(0, k);
+                if (k + 1 < nb) vfm(1, k + 1);
+            }
+            for (int j = ja + 4 * nb; j < nk; ++j) {
+                const float2 v = *reinterpret_cast<const float2*>(vb + (size_t)j * kvd);
+#pragma unroll
+                for (int h = 0; h < 4; ++h) step(h, pr[(size_t)h * prow + j], v);
+            }
+#pragma unroll
+            for (int h = 0; h < 4; ++h)
+                if (r4 + h < R)
+                    *reinterpret_cast<float2*>(att + (size_t)i * H * hd + (size_t)(kv * R + r4 + h) * hd + 2 * dg) = a[h];
+        }
+    }
+}
+
 // ---- decode attention for long caches, split into three launches ----
 // The scores of the keys are independent (each a sequential FMA chain over
 // the head dims), so they spread over many blocks; the softmax sum and the
@@ -1665,7 +1873,23 @@ int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_o
             const size_t glds = ((size_t)R * (((size_t)hd + 3) & ~(size_t)3) + (size_t)R * ps + (g->kv8 ? (size_t)ps : 0)) * sizeof(float);
             const bool grouped = R > 1 && R <= 16 && GT % hd == 0 && R <= 4 * (GT / hd) && glds + 1024 <= 160 * 1024 &&
                                  m <= 65535;
-            if (grouped) {
+            // the register-tiled kernel for the f32 cache: p rows prow apart
+            // (prow % 64 == 4), RP >= R query heads a lane
+            const size_t prow = (ps + 59) / 64 * 64 + 4;
+            const int RP = R <= 2 ? 2 : R <= 4 ? 4 : 8;
+            const size_t tlds = (size_t)RP * prow * sizeof(float);
+            const bool tiled = !g->kv8 && R > 1 && R <= 8 && hd % 32 == 0 && hd <= 2 * GT && RP <= R + 2 * KV &&
+                               tlds + 1024 <= GM_LDS_MAX && m <= 65535;
+            if (tiled) {
+                auto kern = RP == 2 ? gm_attn_tile_kernel<2> : RP == 4 ? gm_attn_tile_kernel<4> : gm_attn_tile_kernel<8>;
+                if (tlds > 64 * 1024)
+                    GMCHK(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                              (int)tlds),
+                          "hipFuncSetAttribute");
+                kern<<<dim3((unsigned)KV, (unsigned)m), dim3(GT), tlds, s>>>(g->qkvb, H, KV, hd, g->cur, kc, vc,
+                                                                             g->qscale, g->cap, sl, win, (int)prow,
+                                                                             g->att, div);
+            } else if (grouped) {
                 auto kern = g->kv8 ? gm_attn_group_kernel<true> : gm_attn_group_kernel<false>;
                 if (glds > 64 * 1024)
                     GMCHK(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,

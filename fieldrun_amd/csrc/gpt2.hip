@@ -363,7 +363,8 @@ __global__ void argmax_done_kernel(unsigned long long* __restrict__ best, int* _
 float gelu_c() { return sqrtf(2.0f / 3.14159274101257324f); }  // (2/PI as f32).sqrt()
 
 __host__ __device__ inline float libm_fn(int fn, float x) {
-    return fn == 0 ? libm::frq_expf(x) : (fn == 1 ? libm::frq_expm1f(x) : libm::frq_tanhf(x));
+    return fn == 0 ? libm::frq_expf(x)
+                   : fn == 1 ? libm::frq_expm1f(x) : fn == 2 ? libm::frq_tanhf(x) : libm::frq_expf_sel(x);
 }
 __global__ __launch_bounds__(NT) void libm_kernel(int fn, const float* __restrict__ x, size_t n,
                                                   float* __restrict__ out) {
@@ -756,7 +757,7 @@ int frq_gpt2_info(const frq_gpt2* g, size_t* n_layer, size_t* n_head, size_t* d,
 }
 
 int frq_libm_f32(frq_ctx* c, int fn, const float* x, size_t n, float* out) {
-    if (fn < 0 || fn > 2) return set_error(FRQ_ERR_ARG, "fn: 0 expf, 1 expm1f, 2 tanhf");
+    if (fn < 0 || fn > 3) return set_error(FRQ_ERR_ARG, "fn: 0 expf, 1 expm1f, 2 tanhf, 3 expf (branch-free form)");
     if (!n) return FRQ_OK;
     if (!x || !out) return set_error(FRQ_ERR_ARG, "null input / output");
     if (!c) {

@@ -40,7 +40,9 @@ __host__ __device__ inline uint64_t d2u(double x) { uint64_t u; memcpy(&u, &x, 8
 __host__ __device__ inline double u2d(uint64_t u) { double x; memcpy(&x, &u, 8); return x; }
 
 
-__host__ __device__ inline float frq_expf(float x) {
+// frq_expf's arithmetic away from the special cases, for any x (inputs the
+// special cases take give an unused value; the table index stays in range).
+__host__ __device__ inline float frq_expf_core(float x) {
     // tab[i] = bits(RN(2^(i/32))) - (i << 47): the double nearest 2^(i/32)
     // with its exponent field pre-subtracted, so adding k << 47 scales it by
     // 2^(k/32).
@@ -57,13 +59,6 @@ __host__ __device__ inline float frq_expf(float x) {
     constexpr double shift = 0x1.8p+52, invln2n = 0x1.71547652b82fep+0 * 32;
     constexpr double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
                      c2 = 0x1.62e42ff0c52d6p-1 / 32;
-    const uint32_t abstop = (f2u(x) >> 20) & 0x7ff;
-    if (abstop >= (0x42b00000u >> 20)) {          // |x| >= 88 or NaN
-        if (f2u(x) == 0xff800000u) return 0.0f;  // -inf
-        if (abstop >= (0x7f800000u >> 20)) return x + x;
-        if (x > 0x1.62e42ep6f) return u2f(0x7f800000u);   // overflow
-        if (x < -0x1.9fe368p6f) return 0.0f;              // underflow
-    }
     const double xd = (double)x;
     double kd = __builtin_fma(invln2n, xd, shift);
     const uint64_t ki = d2u(kd);
@@ -76,6 +71,32 @@ __host__ __device__ inline float frq_expf(float x) {
     y = __builtin_fma(z, r2, y);
     y = y * s;
     return (float)y;
+}
+
+__host__ __device__ inline float frq_expf(float x) {
+    const uint32_t abstop = (f2u(x) >> 20) & 0x7ff;
+    if (abstop >= (0x42b00000u >> 20)) {          // |x| >= 88 or NaN
+        if (f2u(x) == 0xff800000u) return 0.0f;  // -inf
+        if (abstop >= (0x7f800000u >> 20)) return x + x;
+        if (x > 0x1.62e42ep6f) return u2f(0x7f800000u);   // overflow
+        if (x < -0x1.9fe368p6f) return 0.0f;              // underflow
+    }
+    return frq_expf_core(x);
+}
+
+// frq_expf without branches: the core always runs and the special cases
+// replace its value by selects, so a run of these in one thread keeps all
+// their table loads in flight together.  Same value as frq_expf for every x.
+__host__ __device__ inline float frq_expf_sel(float x) {
+    // every special input has |x| >= 88, so the selects need no outer test;
+    // applied lowest precedence first
+    const uint32_t ux = f2u(x);
+    float r = frq_expf_core(x);
+    r = x < -0x1.9fe368p6f ? 0.0f : r;              // underflow
+    r = x > 0x1.62e42ep6f ? u2f(0x7f800000u) : r;   // overflow
+    r = (ux & 0x7fffffffu) >= 0x7f800000u ? x + x : r;  // inf, NaN
+    r = ux == 0xff800000u ? 0.0f : r;               // -inf
+    return r;
 }
 
 __host__ __device__ inline float frq_expm1f(float x) {

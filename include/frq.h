@@ -327,7 +327,8 @@ int frq_gemma_generate_batch(frq_ctx* ctx, frq_gemma* g, const int64_t* prompts,
  * rope.rs:1147-1170; predict 730-734). */
 int frq_rope_load(frq_ctx* ctx, const frq_bundle* b, int kv_int8, frq_gemma** out);
 /* The f32 libm functions the decode kernels use (fn 0 expf, 1 expm1f, 2
- * tanhf), bit-identical to the libm behind Rust's f32::exp / f32::tanh
+ * tanhf, 3 expf in the branch-free form the attention kernels use),
+ * bit-identical to the libm behind Rust's f32::exp / f32::tanh
  * (glibc's expf and fdlibm's expm1f / tanhf): out[i] = f(x[i]) for n host
  * values, on ctx's device, or on the host when ctx is NULL. */
 int frq_libm_f32(frq_ctx* ctx, int fn, const float* x, size_t n, float* out);
