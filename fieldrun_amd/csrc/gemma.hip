@@ -937,6 +937,372 @@ __global__ __launch_bounds__(GT) void gm_attn_tile_kernel(const float* __restric
     }
 }
 
+// ---- prefill attention over an f32 cache in two tiled launches ----
+// The per-output arithmetic of gm_attn_group_kernel<false> (score =
+// sequential FMA chain over the head dims, scale / cap, max over the row's
+// keys, exp, the key-order sum from +0, p = e / sum, value chain in key
+// order from +0), so the same bits, with each key and value row read once
+// per block of rows rather than once per row.  A block is AP (row, head)
+// pairs: AP / RP consecutive rows times RP >= R heads of one kv head (pair
+// p = row * RP + head; heads past R and rows past m are computed on zeros
+// and never leave).  The scores go through a key-major buffer
+// st[kv][block][key][pair] (kpad keys a block) that the second launch turns
+// into exps in place.
+constexpr int PF_AP = 64, PF_KT = 128, PF_VK = 64, PF_NT = 256;
+constexpr size_t PF_MIN_ROWS = 1024;  // shorter prompts take the one-launch kernels (more workgroups)
+__host__ __device__ inline int pf_rows(int rp) { return PF_AP / rp; }
+
+struct PfRow {
+    int nk, j0, ok;  // keys [j0, nk) of the row; ok: a row of the launch
+};
+__device__ __forceinline__ PfRow pf_row(int i, int cur, int m, int sliding, int window) {
+    const int ab = cur + i;
+    return {ab + 1, (sliding && ab >= window) ? ab - window + 1 : 0, i < m};
+}
+
+// 1. scores: workgroup (kv, block b), heaviest blocks first; the block's q
+// pairs in LDS, then its key tiles in order, each tile's 128 key rows in
+// LDS (rows HD + 4 floats apart) while the next tile's rows load into
+// registers; a lane 8 pairs x 4 keys (keys kg + 32u); writes the scaled
+// (capped) scores and each pair's max over every tile key its row sees.
+template <int RP, int RV, int HD>
+__global__ __launch_bounds__(PF_NT) void gm_pf_scores_kernel(const float* __restrict__ qkv, int H, int KV,
+                                                             const int* __restrict__ curp, int m,
+                                                             const float* __restrict__ kc, float qscale, float cap,
+                                                             int sliding, int window, int nrb, int nkt, int kpad,
+                                                             float* __restrict__ st, float* __restrict__ pmax,
+                                                             int div) {
+    constexpr int RB = PF_AP / RP, HP = HD + 4, H4 = HD / 4;
+    constexpr int QN = PF_AP * H4 / PF_NT, KN = PF_KT * H4 / PF_NT;  // float4 loads a thread
+    static_assert(QN * PF_NT == PF_AP * H4 && KN * PF_NT == PF_KT * H4, "whole loads");
+    extern __shared__ float4 lds4[];
+    float* Qs = reinterpret_cast<float*>(lds4);  // [PF_AP][HP]
+    float* Ks = Qs + PF_AP * HP;                  // [PF_KT][HP]
+    const int R = H / KV, kvd = KV * HD, tid = threadIdx.x;
+    const int bx = (int)(gridDim.x - 1 - blockIdx.x);  // the longest blocks start first
+    const int b = bx % nrb, kv = bx / nrb;
+    const int cur = *curp, r0 = b * RB, klen = cur + m;
+    const int ntile = (cur + min(r0 + RB, m) + PF_KT - 1) / PF_KT;
+    float4 qv[QN];
+#pragma unroll
+    for (int u = 0; u < QN; ++u) {
+        const int x = tid + u * PF_NT, pq = x / H4, c4 = x % H4, h = pq % RP, i = r0 + pq / RP;
+        qv[u] = (h < R && i < m)
+                    ? *reinterpret_cast<const float4*>(qkv + (size_t)i * (H + 2 * KV) * HD + (size_t)(kv * R + h) * HD + 4 * c4)
+                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    float4 kv4[KN];
+    auto kload = [&](int c) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < KN; ++u) {
+            const int x = tid + u * PF_NT, t = x / H4, c4 = x % H4, j = c * PF_KT + t;
+            kv4[u] = j < klen ? *reinterpret_cast<const float4*>(kc + (size_t)j * kvd + (size_t)kv * HD + 4 * c4)
+                              : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    };
+    kload(0);
+#pragma unroll
+    for (int u = 0; u < QN; ++u) {
+        const int x = tid + u * PF_NT;
+        *reinterpret_cast<float4*>(Qs + (x / H4) * HP + 4 * (x % H4)) = qv[u];
+    }
+    const int kg = tid & 31, pg = tid >> 5;
+    float* sb = st + ((size_t)kv * nrb + b) * (size_t)kpad * PF_AP;
+    // rows of this lane's pairs: keys [j0, nk) (nk 0 past m)
+    int rj0[8], rnk[8];
+#pragma unroll
+    for (int a = 0; a < 8; ++a) {
+        const PfRow rw = pf_row(r0 + (8 * pg + a) / RP, cur, m, sliding, window);
+        rj0[a] = rw.j0;
+        rnk[a] = rw.ok ? rw.nk : 0;
+    }
+    float mxl[8];
+#pragma unroll
+    for (int a = 0; a < 8; ++a) mxl[a] = -INFINITY;
+    for (int c = 0; c < ntile; ++c) {
+        __syncthreads();  // the previous tile is consumed
+#pragma unroll
+        for (int u = 0; u < KN; ++u) {
+            const int x = tid + u * PF_NT;
+            *reinterpret_cast<float4*>(Ks + (x / H4) * HP + 4 * (x % H4)) = kv4[u];
+        }
+        __syncthreads();
+        if (c + 1 < ntile) kload(c + 1);  // in flight during this tile
+        float acc[8][4];
+#pragma unroll
+        for (int a = 0; a < 8; ++a)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc[a][u] = 0.0f;
+        const float* qb = Qs + (8 * pg) * HP;
+        const float* kb = Ks + kg * HP;
+#pragma unroll 2
+        for (int sd = 0; sd < H4; ++sd) {
+            float4 q4[8], k4[4];
+#pragma unroll
+            for (int a = 0; a < 8; ++a)
+                if (a % RP < RV) q4[a] = *reinterpret_cast<const float4*>(qb + a * HP + 4 * sd);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) k4[u] = *reinterpret_cast<const float4*>(kb + 32 * u * HP + 4 * sd);
+#pragma unroll
+            for (int a = 0; a < 8; ++a)
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    if (a % RP >= RV) continue;  // a spare head: never leaves the kernel
+                    acc[a][u] = __builtin_fmaf(q4[a].x, k4[u].x, acc[a][u]);
+                    acc[a][u] = __builtin_fmaf(q4[a].y, k4[u].y, acc[a][u]);
+                    acc[a][u] = __builtin_fmaf(q4[a].z, k4[u].z, acc[a][u]);
+                    acc[a][u] = __builtin_fmaf(q4[a].w, k4[u].w, acc[a][u]);
+                }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int j = c * PF_KT + kg + 32 * u;
+            float sv[8];
+#pragma unroll
+            for (int a = 0; a < 8; ++a) {
+                float sj = div ? acc[a][u] / qscale : acc[a][u] * qscale;
+                if (cap > 0.0f) sj = cap * libm::frq_tanhf(sj / cap);
+                sv[a] = sj;
+                if (j >= rj0[a] && j < rnk[a]) mxl[a] = fmaxf(mxl[a], sj);
+            }
+            float4* dst = reinterpret_cast<float4*>(sb + (size_t)j * PF_AP + 8 * pg);
+            dst[0] = make_float4(sv[0], sv[1], sv[2], sv[3]);
+            dst[1] = make_float4(sv[4], sv[5], sv[6], sv[7]);
+        }
+    }
+#pragma unroll
+    for (int a = 0; a < 8; ++a) {
+        float v = mxl[a];
+#pragma unroll
+        for (int off = 16; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+        if (kg == 0) pmax[((size_t)kv * nrb + b) * PF_AP + 8 * pg + a] = v;
+    }
+}
+
+// 2. workgroup (kv, block b), heaviest first: the pairs' maxes (one per
+// pair from the first launch); per key tile the exps (branch-free) into LDS
+// and, in place of the scores, into st, then wave 0 adds them in key order
+// (a lane a pair); then the value chains, a lane 8 pairs x 4 dims, over
+// 64-key chunks of p = e / sum and the value rows staged in LDS, the next
+// chunk loading into registers meanwhile (chunks every row of the block
+// sees entirely run without per-key tests).
+template <int RP, int RV, int HD>
+__global__ __launch_bounds__(PF_NT) void gm_pf_values_kernel(int H, int KV, const int* __restrict__ curp, int m,
+                                                             const float* __restrict__ vc, int sliding, int window,
+                                                             int nrb, int kpad, float* __restrict__ st,
+                                                             const float* __restrict__ pmax,
+                                                             float* __restrict__ att) {
+    constexpr int RB = PF_AP / RP, HP = HD + 4, H4 = HD / 4;
+    constexpr int PN = PF_VK * PF_AP / PF_NT, VN = (PF_VK * H4 + PF_NT - 1) / PF_NT;
+    extern __shared__ float4 lds4[];
+    __shared__ float mx[PF_AP], sums[PF_AP];
+    const int R = H / KV, kvd = KV * HD, tid = threadIdx.x;
+    const int bx = (int)(gridDim.x - 1 - blockIdx.x);
+    const int b = bx % nrb, kv = bx / nrb;
+    const int cur = *curp, r0 = b * RB, klen = cur + m;
+    const int kend = cur + min(r0 + RB, m);  // keys [0, kend) cover every row of the block
+    const int ntile = (kend + PF_KT - 1) / PF_KT;
+    float* sb = st + ((size_t)kv * nrb + b) * (size_t)kpad * PF_AP;
+    if (tid < PF_AP) {
+        const PfRow rw = pf_row(r0 + tid / RP, cur, m, sliding, window);
+        float v = pmax[((size_t)kv * nrb + b) * PF_AP + tid];
+        if (rw.j0 > 0 || rw.nk < klen) v = fmaxf(v, -1e30f);  // a masked entry joins the max
+        mx[tid] = v;
+    }
+    __syncthreads();
+    float* Es = reinterpret_cast<float*>(lds4);  // [PF_KT][PF_AP]
+    float sm = 0.0f;                              // wave 0: pair tid's sum
+    const PfRow rs = pf_row(r0 + (tid & (PF_AP - 1)) / RP, cur, m, sliding, window);
+    const int pq = tid & (PF_AP - 1);             // the pair of every element this thread touches
+    const PfRow rq = rs;
+    const float mxq = mx[pq];
+    for (int c = 0; c < ntile; ++c) {
+        const int jt = c * PF_KT;
+        constexpr int EN = PF_KT * PF_AP / PF_NT;  // 32 exps a thread, loads first
+        float e[EN];
+#pragma unroll
+        for (int u = 0; u < EN; ++u) e[u] = sb[(size_t)jt * PF_AP + tid + u * PF_NT];
+#pragma unroll
+        for (int u = 0; u < EN; ++u) {
+            const int x = tid + u * PF_NT, j = jt + x / PF_AP;
+            const float ev = libm::frq_expf_sel(e[u] - mxq);
+            e[u] = (rq.ok && j >= rq.j0 && j < rq.nk) ? ev : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < EN; ++u) {
+            Es[tid + u * PF_NT] = e[u];
+            sb[(size_t)jt * PF_AP + tid + u * PF_NT] = e[u];
+        }
+        __syncthreads();
+        if (tid < PF_AP && rs.ok) {
+            // the tile's keys of this pair's row in order, reads 16 ahead
+            const int ja = max(rs.j0, jt), jb = min(rs.nk, jt + PF_KT);
+            const float* ep = Es + tid;
+            int j = ja;
+            for (; j + 16 <= jb; j += 16) {
+                float ev[16];
+#pragma unroll
+                for (int u = 0; u < 16; ++u) ev[u] = ep[(j - jt + u) * PF_AP];
+#pragma unroll
+                for (int u = 0; u < 16; ++u) sm = sm + ev[u];
+            }
+            for (; j < jb; ++j) sm = sm + ep[(j - jt) * PF_AP];
+        }
+        __syncthreads();
+    }
+    if (tid < PF_AP) sums[tid] = sm;
+    __syncthreads();
+    // values
+    float* Ps = reinterpret_cast<float*>(lds4);  // [PF_VK][PF_AP]
+    float* Vs = Ps + PF_VK * PF_AP;              // [PF_VK][HP]
+    const int pg = tid >> 5, dg = tid & 31;
+    const bool lane_on = dg < H4;
+    int rj0[8], rnk[8];
+#pragma unroll
+    for (int a = 0; a < 8; ++a) {
+        const PfRow rw = pf_row(r0 + (8 * pg + a) / RP, cur, m, sliding, window);
+        rj0[a] = rw.j0;
+        rnk[a] = rw.ok ? rw.nk : 0;
+    }
+    // keys every row of the block sees: [j0 of the last row, nk of the first)
+    const PfRow rfirst = pf_row(r0, cur, m, sliding, window);
+    const PfRow rlast = pf_row(min(r0 + RB, m) - 1, cur, m, sliding, window);
+    const float rsum = sums[pq];
+    float acc[8][4];
+#pragma unroll
+    for (int a = 0; a < 8; ++a)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) acc[a][d] = 0.0f;
+    const int nvc = (kend + PF_VK - 1) / PF_VK;
+    float pn[PN];
+    float4 vn[VN];
+    auto cload = [&](int c) __attribute__((always_inline)) {
+        const int jc = c * PF_VK;
+#pragma unroll
+        for (int u = 0; u < PN; ++u) {
+            const int x = tid + u * PF_NT;
+            pn[u] = jc + x / PF_AP < kend ? sb[(size_t)jc * PF_AP + x] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < VN; ++u) {
+            const int x = tid + u * PF_NT, t = x / H4, c4 = x % H4, j = jc + t;
+            vn[u] = (x < PF_VK * H4 && j < kend)
+                        ? *reinterpret_cast<const float4*>(vc + (size_t)j * kvd + (size_t)kv * HD + 4 * c4)
+                        : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    };
+    cload(0);
+    for (int c = 0; c < nvc; ++c) {
+        const int jc = c * PF_VK;
+        __syncthreads();  // the previous chunk is consumed
+#pragma unroll
+        for (int u = 0; u < PN; ++u) Ps[tid + u * PF_NT] = pn[u] / rsum;  // pair tid % 64 throughout
+#pragma unroll
+        for (int u = 0; u < VN; ++u) {
+            const int x = tid + u * PF_NT;
+            if (x < PF_VK * H4) *reinterpret_cast<float4*>(Vs + (x / H4) * HP + 4 * (x % H4)) = vn[u];
+        }
+        __syncthreads();
+        if (c + 1 < nvc) cload(c + 1);
+        const bool full = jc >= rlast.j0 && jc + PF_VK <= rfirst.nk;
+        if (lane_on && full) {
+            for (int t = 0; t < PF_VK; ++t) {
+                const float4 pa = *reinterpret_cast<const float4*>(Ps + t * PF_AP + 8 * pg);
+                const float4 pb = *reinterpret_cast<const float4*>(Ps + t * PF_AP + 8 * pg + 4);
+                const float4 v = *reinterpret_cast<const float4*>(Vs + t * HP + 4 * dg);
+                const float pv[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+                const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int a = 0; a < 8; ++a) {
+                    if (a % RP >= RV) continue;
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) acc[a][d] = __builtin_fmaf(pv[a], vv[d], acc[a][d]);
+                }
+            }
+        } else if (lane_on) {
+            for (int t = 0; t < PF_VK; ++t) {
+                const int j = jc + t;
+                const float4 pa = *reinterpret_cast<const float4*>(Ps + t * PF_AP + 8 * pg);
+                const float4 pb = *reinterpret_cast<const float4*>(Ps + t * PF_AP + 8 * pg + 4);
+                const float4 v = *reinterpret_cast<const float4*>(Vs + t * HP + 4 * dg);
+                const float pv[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+                const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int a = 0; a < 8; ++a) {
+                    if (a % RP >= RV) continue;
+                    const bool on = j >= rj0[a] && j < rnk[a];
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        const float n = __builtin_fmaf(pv[a], vv[d], acc[a][d]);
+                        acc[a][d] = on ? n : acc[a][d];
+                    }
+                }
+            }
+        }
+    }
+    if (lane_on) {
+#pragma unroll
+        for (int a = 0; a < 8; ++a) {
+            const int pp = 8 * pg + a, h = pp % RP, i = r0 + pp / RP;
+            if (h < R && i < m)
+                *reinterpret_cast<float4*>(att + (size_t)i * H * HD + (size_t)(kv * R + h) * HD + 4 * dg) =
+                    make_float4(acc[a][0], acc[a][1], acc[a][2], acc[a][3]);
+        }
+    }
+}
+
+// LDS and scratch of the two-launch prefill attention
+inline size_t pf_scores_lds(int hd) { return (size_t)(PF_AP + PF_KT) * (hd + 4) * sizeof(float); }
+inline size_t pf_values_lds(int hd) {
+    return std::max((size_t)PF_KT * PF_AP, (size_t)PF_VK * PF_AP + (size_t)PF_VK * (hd + 4)) * sizeof(float);
+}
+inline size_t pf_kpad(size_t npos) { return (npos + PF_KT - 1) / PF_KT * PF_KT; }
+
+template <int RP, int RV, int HD>
+hipError_t launch_pf_t(const float* qkv, int H, int KV, const int* cur, int m, const float* kc, const float* vc,
+                       float qscale, float cap, int sl, int win, int nrb, int nkt, int kpad, float* st, float* pmx,
+                       float* att, int div, hipStream_t s) {
+    const size_t l1 = pf_scores_lds(HD), l2 = pf_values_lds(HD);
+    static bool attr = false;  // per process; the attribute is per function
+    if (!attr) {
+        if (hipError_t e = hipFuncSetAttribute((const void*)gm_pf_scores_kernel<RP, RV, HD>,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)l1))
+            return e;
+        if (hipError_t e = hipFuncSetAttribute((const void*)gm_pf_values_kernel<RP, RV, HD>,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)l2))
+            return e;
+        attr = true;
+    }
+    gm_pf_scores_kernel<RP, RV, HD><<<dim3((unsigned)(KV * nrb)), dim3(PF_NT), l1, s>>>(
+        qkv, H, KV, cur, m, kc, qscale, cap, sl, win, nrb, nkt, kpad, st, pmx, div);
+    if (hipError_t e = hipGetLastError()) return e;
+    gm_pf_values_kernel<RP, RV, HD><<<dim3((unsigned)(KV * nrb)), dim3(PF_NT), l2, s>>>(H, KV, cur, m, vc, sl, win, nrb,
+                                                                                 kpad, st, pmx, att);
+    return hipGetLastError();
+}
+
+template <int HD>
+hipError_t launch_pf_h(int rp, const float* qkv, int H, int KV, const int* cur, int m, const float* kc,
+                       const float* vc, float qscale, float cap, int sl, int win, int nrb, int nkt, int kpad, float* st,
+                       float* pmx, float* att, int div, hipStream_t s) {
+    // RV: the heads the FMAs run on (the spare ones of RP > R only where
+    // R == 7, the Qwen2.5-7B group; elsewhere they run on zero q)
+    const int R = H / KV;
+    if (rp == 2) return launch_pf_t<2, 2, HD>(qkv, H, KV, cur, m, kc, vc, qscale, cap, sl, win, nrb, nkt, kpad, st, pmx, att, div, s);
+    if (rp == 4) return launch_pf_t<4, 4, HD>(qkv, H, KV, cur, m, kc, vc, qscale, cap, sl, win, nrb, nkt, kpad, st, pmx, att, div, s);
+    if (R == 7) return launch_pf_t<8, 7, HD>(qkv, H, KV, cur, m, kc, vc, qscale, cap, sl, win, nrb, nkt, kpad, st, pmx, att, div, s);
+    return launch_pf_t<8, 8, HD>(qkv, H, KV, cur, m, kc, vc, qscale, cap, sl, win, nrb, nkt, kpad, st, pmx, att, div, s);
+}
+
+hipError_t launch_pf_attention(int rp, int hd, const float* qkv, int H, int KV, const int* cur, int m,
+                               const float* kc, const float* vc, float qscale, float cap, int sl, int win, int nrb,
+                               int nkt, int kpad, float* st, float* pmx, float* att, int div, hipStream_t s) {
+    if (hd == 32) return launch_pf_h<32>(rp, qkv, H, KV, cur, m, kc, vc, qscale, cap, sl, win, nrb, nkt, kpad, st, pmx, att, div, s);
+    if (hd == 64) return launch_pf_h<64>(rp, qkv, H, KV, cur, m, kc, vc, qscale, cap, sl, win, nrb, nkt, kpad, st, pmx, att, div, s);
+    if (hd == 128) return launch_pf_h<128>(rp, qkv, H, KV, cur, m, kc, vc, qscale, cap, sl, win, nrb, nkt, kpad, st, pmx, att, div, s);
+    return hipErrorInvalidValue;
+}
+
 // ---- decode attention for long caches, split into three launches ----
 // The scores of the keys are independent (each a sequential FMA chain over
 // the head dims), so they spread over many blocks; the softmax sum and the
@@ -1372,6 +1738,8 @@ struct frq_gemma {
     int64_t *tok = nullptr, *ids = nullptr;
     float *qr = nullptr, *sc = nullptr;  // long-cache decode attention: roped q, scores
     float* xt = nullptr;                 // batches: the head's input rows transposed (16 d)
+    float* pst = nullptr;                // prefill attention: scores / exps, [KV][block][kpad][64]
+    float* pmx = nullptr;                // prefill attention: the pairs' maxima, [KV][block][64]
     // the quantised decode rows of the int8 linears (d- and ffn-wide: the
     // padding of each stays zero), their scales and outliers
     int8_t* q8f = nullptr;
@@ -1661,6 +2029,7 @@ void gm_drop_buffers(frq_gemma* g) {
     g->best = nullptr;
     g->tok = g->ids = nullptr;
     g->qr = g->sc = g->xt = nullptr;
+    g->pst = g->pmx = nullptr;
     g->q8f = nullptr;
     g->qsa = nullptr;
     g->qoi = nullptr;
@@ -1672,6 +2041,16 @@ void gm_drop_buffers(frq_gemma* g) {
 // cos / sin).  A request the attention cannot serve is refused before
 // anything changes; any later failure leaves the model with no buffers
 // (capacities 0), never with pointers into freed memory.
+// RP of the two-launch prefill attention for this model (0: not served):
+// the f32 cache, 2 <= R <= 8 query heads a kv head, hd a multiple of 32 up
+// to 128, and RP - R spare heads' q reads inside the qkv row.
+int gm_pf_rp(const frq_gemma* g) {
+    const size_t R = g->H / g->KV;
+    if (g->kv8 || R < 2 || R > 8 || (g->hd != 32 && g->hd != 64 && g->hd != 128)) return 0;
+    const int rp = R <= 2 ? 2 : R <= 4 ? 4 : 8;
+    return (size_t)rp <= R + 2 * g->KV ? rp : 0;
+}
+
 int gm_reserve(frq_ctx* c, frq_gemma* g, size_t npos, size_t rows, size_t nb = 1) {
     if (npos <= g->cap_pos && rows <= g->cap_rows && nb <= g->cap_b && g->buf) return FRQ_OK;
     const size_t N = std::max(npos, g->cap_pos), R = std::max(rows, g->cap_rows), B = std::max(nb, g->cap_b);
@@ -1710,6 +2089,10 @@ int gm_reserve(frq_ctx* c, frq_gemma* g, size_t npos, size_t rows, size_t nb = 1
                  o_xt = take(B > 1 ? 16 * g->d * 4 : 0),
                  o_q8f = take(round_up(g->ffn, FRQ_KALIGN)), o_qsa = take(4), o_qoi = take(FRQ_T * 4),
                  o_qov = take(FRQ_T * 4);
+    // the two-launch prefill attention's scores and tile maxima
+    const int rp = gm_pf_rp(g);
+    const size_t pf_nrb = rp ? (R + pf_rows(rp) - 1) / pf_rows(rp) : 0, kpad = pf_kpad(N);
+    const size_t o_pst = take(pf_nrb * g->KV * kpad * PF_AP * 4), o_pmx = take(pf_nrb * g->KV * PF_AP * 4);
     char* m = nullptr;
     GMCHK(hipMalloc(&m, off), "hipMalloc(gemma)");
     if (hipError_t e = hipMemsetAsync(m, 0, off, s)) {
@@ -1747,6 +2130,8 @@ int gm_reserve(frq_ctx* c, frq_gemma* g, size_t npos, size_t rows, size_t nb = 1
     g->tok = reinterpret_cast<int64_t*>(m + o_tok); g->ids = reinterpret_cast<int64_t*>(m + o_ids);
     g->qr = reinterpret_cast<float*>(m + o_qr); g->sc = reinterpret_cast<float*>(m + o_sc);
     g->xt = B > 1 ? reinterpret_cast<float*>(m + o_xt) : nullptr;
+    g->pst = pf_nrb ? reinterpret_cast<float*>(m + o_pst) : nullptr;
+    g->pmx = pf_nrb ? reinterpret_cast<float*>(m + o_pmx) : nullptr;
     g->q8f = reinterpret_cast<int8_t*>(m + o_q8f);
     g->qsa = reinterpret_cast<float*>(m + o_qsa); g->qoi = reinterpret_cast<uint32_t*>(m + o_qoi);
     g->qov = reinterpret_cast<float*>(m + o_qov);
@@ -1880,7 +2265,15 @@ int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_o
             const size_t tlds = (size_t)RP * prow * sizeof(float);
             const bool tiled = !g->kv8 && R > 1 && R <= 8 && hd % 32 == 0 && hd <= 2 * GT && RP <= R + 2 * KV &&
                                tlds + 1024 <= GM_LDS_MAX && m <= 65535;
-            if (tiled) {
+            const int prp = gm_pf_rp(g);
+            if (prp && g->pst && m >= PF_MIN_ROWS && m <= 65535) {
+                // the two-launch form: each key / value row read once a block of rows
+                const int nrb = (int)((m + pf_rows(prp) - 1) / pf_rows(prp));
+                const int kpad = (int)pf_kpad(g->cap_pos), nkt = kpad / PF_KT;
+                GMCHK(launch_pf_attention(prp, hd, g->qkvb, H, KV, g->cur, (int)m, kc, vc, g->qscale, g->cap, sl, win,
+                                          nrb, nkt, kpad, g->pst, g->pmx, g->att, div, s),
+                      "launch prefill attention");
+            } else if (tiled) {
                 auto kern = RP == 2 ? gm_attn_tile_kernel<2> : RP == 4 ? gm_attn_tile_kernel<4> : gm_attn_tile_kernel<8>;
                 if (tlds > 64 * 1024)
                     GMCHK(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,

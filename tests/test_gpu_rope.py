@@ -127,3 +127,25 @@ def test_rope_batch_matches_single_sequences(ctx, small):
         assert same_bits(lg[i], l1), (i, first_diff(lg[i], l1))
     g.free()
     b.close()
+
+
+@pytest.mark.parametrize("n_head,n_kv,hd", [(8, 2, 64), (20, 4, 32)])
+def test_rope_long_prompt_two_launch_attention(ctx, tmp_path, n_head, n_kv, hd):
+    """Prompts of 1024 rows and more take the two-launch prefill attention
+    (scores tiled over blocks of rows and 128-key tiles, then the exps,
+    key-order sums and value chains per block of rows): tokens and logits
+    bit for bit against the oracle, at 4 and 5 query heads a kv head."""
+    stem = str(tmp_path / "r")
+    synth.write_rope_bundle(stem, 21, n_layer=2, n_head=n_head, n_kv=n_kv, hd=hd, d=n_head * hd, ffn=256,
+                            vocab=500, std=0.1, norm_std=0.1, dtype="int8")
+    m, arrs = oracle.read_bundle(stem)
+    ref = oracle.Rope(m, arrs, nthreads=16)
+    b = fa.Bundle(stem, ctx)
+    g = fa.Rope(b)
+    prompt = synth.gpt2_prompt(1100, 500, 23)
+    toks, lg = g.generate(prompt, 4, with_logits=True)
+    rt, rlg = ref.generate(prompt, 4, with_logits=True)
+    assert np.array_equal(toks, rt)
+    assert same_bits(lg, rlg), first_diff(lg, rlg)
+    g.free()
+    b.close()
