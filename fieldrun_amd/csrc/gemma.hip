@@ -1362,7 +1362,7 @@ __global__ __launch_bounds__(GT) void gm_dec_prep_kernel(const float* __restrict
 
 // 2. Scores: grid (H, key chunks of GT): thread j of chunk z scores key
 // z GT + j of the window [j0, cur] into sc[h * pstride + j].
-template <bool KV8>
+template <bool KV8, int HD = 0>
 __global__ __launch_bounds__(GT) void gm_dec_score_kernel(const float* __restrict__ qr, int H, int KV, int hd,
                                                           const int* __restrict__ curp, const float* __restrict__ kc,
                                                           const int8_t* __restrict__ kq, const float* __restrict__ ks,
@@ -1378,7 +1378,21 @@ __global__ __launch_bounds__(GT) void gm_dec_score_kernel(const float* __restric
     __syncthreads();
     if (j < j0 || j >= nk) return;
     float acc = 0.0f;
-    if constexpr (!KV8) {
+    if constexpr (!KV8 && HD > 0) {
+        // the whole key row requested at once (the old rows come from HBM)
+        const float* kr = kc + (size_t)j * kvd + (size_t)kv * HD;
+        float4 k4[HD / 4];
+#pragma unroll
+        for (int u = 0; u < HD / 4; ++u) k4[u] = *reinterpret_cast<const float4*>(kr + 4 * u);
+        __builtin_amdgcn_sched_barrier(0);  // every load issued before the chain starts
+#pragma unroll
+        for (int u = 0; u < HD / 4; ++u) {
+            acc = __builtin_fmaf(q[4 * u], k4[u].x, acc);
+            acc = __builtin_fmaf(q[4 * u + 1], k4[u].y, acc);
+            acc = __builtin_fmaf(q[4 * u + 2], k4[u].z, acc);
+            acc = __builtin_fmaf(q[4 * u + 3], k4[u].w, acc);
+        }
+    } else if constexpr (!KV8) {
         const float* kr = kc + (size_t)j * kvd + (size_t)kv * hd;
         for (int c = 0; c < hd; c += 4) {
             const float4 k4 = *reinterpret_cast<const float4*>(kr + c);
@@ -1396,6 +1410,82 @@ __global__ __launch_bounds__(GT) void gm_dec_score_kernel(const float* __restric
             acc = __builtin_fmaf(q[c + 1], (float)k4.y * sk, acc);
             acc = __builtin_fmaf(q[c + 2], (float)k4.z * sk, acc);
             acc = __builtin_fmaf(q[c + 3], (float)k4.w * sk, acc);
+        }
+    }
+    float sj = div ? acc / qscale : acc * qscale;
+    if (cap > 0.0f) sj = cap * libm::frq_tanhf(sj / cap);
+    sc[(size_t)h * pstride + j] = sj;
+}
+
+// 1 + 2 fused for the f32 cache: grid (H, key chunks of GT).  Every
+// workgroup prepares its own q head as gm_dec_prep_kernel does (bias,
+// QK-norm, RoPE at position cur) and scores its chunk's keys; the chunk
+// holding key cur prepares that key's k as well and scores it from LDS,
+// and for the first head of each kv group also appends k and v at cache
+// row cur (read by the value step, a launch later; no workgroup of this
+// launch reads that row from the cache).  Same arithmetic, so the same
+// bits; key rows requested whole before each chain.
+template <int HD>
+__global__ __launch_bounds__(GT) void gm_dec_qks_kernel(const float* __restrict__ qkv, int H, int KV,
+                                                        const int* __restrict__ curp, const float2* __restrict__ cs,
+                                                        float* __restrict__ kc, float* __restrict__ vc,
+                                                        const float* __restrict__ bias, const float* __restrict__ qn,
+                                                        const float* __restrict__ kn, float eps, float qscale,
+                                                        float cap, int sliding, int window, int div, int pstride,
+                                                        float* __restrict__ sc) {
+    __shared__ float qs[HD], kl[HD];
+    constexpr int half = HD / 2;
+    const int h = blockIdx.x, R = H / KV, kv = h / R, kvd = KV * HD, tid = threadIdx.x;
+    const int ab = *curp, nk = ab + 1, j0 = (sliding && ab >= window) ? ab - window + 1 : 0;
+    const int zb = (int)blockIdx.y * GT;
+    if (zb >= nk) return;  // block-uniform: past the cache
+    const bool last = zb + GT >= nk;  // this chunk holds key ab
+    const size_t pos = (size_t)ab;
+    for (int c = tid; c < HD; c += GT) {
+        float v = qkv[h * HD + c];
+        if (bias) v = v + bias[h * HD + c];
+        qs[c] = v;
+        if (last) {
+            float w = qkv[(H + kv) * HD + c];
+            if (bias) w = w + bias[(H + kv) * HD + c];
+            kl[c] = w;
+        }
+    }
+    __syncthreads();
+    if (qn) {
+        if (tid == 0) head_norm_lane(qs, HD, qn, eps);
+        if (last && tid == 64) head_norm_lane(kl, HD, kn, eps);
+        __syncthreads();
+    }
+    const float2* csp = cs + pos * half;
+    for (int t = tid; t < (last ? 2 : 1) * half; t += GT) rope_pair(t < half ? qs : kl, t % half, half, csp);
+    __syncthreads();
+    if (last && h % R == 0) {
+        for (int c = tid; c < HD; c += GT) {
+            float w = qkv[(H + KV + kv) * HD + c];
+            if (bias) w = w + bias[(H + KV + kv) * HD + c];
+            kc[pos * kvd + (size_t)kv * HD + c] = kl[c];
+            vc[pos * kvd + (size_t)kv * HD + c] = w;
+        }
+    }
+    const int j = zb + tid;
+    if (j < j0 || j >= nk) return;
+    float acc = 0.0f;
+    if (j == ab) {
+#pragma unroll 8
+        for (int c = 0; c < HD; ++c) acc = __builtin_fmaf(qs[c], kl[c], acc);
+    } else {
+        const float* kr = kc + (size_t)j * kvd + (size_t)kv * HD;
+        float4 k4[HD / 4];
+#pragma unroll
+        for (int u = 0; u < HD / 4; ++u) k4[u] = *reinterpret_cast<const float4*>(kr + 4 * u);
+        __builtin_amdgcn_sched_barrier(0);  // every load issued before the chain starts
+#pragma unroll
+        for (int u = 0; u < HD / 4; ++u) {
+            acc = __builtin_fmaf(qs[4 * u], k4[u].x, acc);
+            acc = __builtin_fmaf(qs[4 * u + 1], k4[u].y, acc);
+            acc = __builtin_fmaf(qs[4 * u + 2], k4[u].z, acc);
+            acc = __builtin_fmaf(qs[4 * u + 3], k4[u].w, acc);
         }
     }
     float sj = div ? acc / qscale : acc * qscale;
@@ -2236,10 +2326,16 @@ int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_o
                 else
                     GMCHK(er, "launch value ring");
             } else {
-                gm_dec_prep_kernel<false><<<dim3((unsigned)(H + KV)), dim3(GT), plds, s>>>(
-                    qkvr, H, KV, hd, g->cur, g->cs, kc, vc, kq, vq, ks, vs, qb, qn, kn, g->eps, g->qr);
-                gm_dec_score_kernel<false><<<sg, dim3(GT), hd4 * sizeof(float), s>>>(
-                    g->qr, H, KV, hd, g->cur, kc, kq, ks, g->qscale, g->cap, sl, win, div, ps, g->sc);
+                if (hd == 128 || hd == 64 || hd == 32) {  // prep fused into the scores
+                    auto qk = hd == 128 ? gm_dec_qks_kernel<128> : hd == 64 ? gm_dec_qks_kernel<64> : gm_dec_qks_kernel<32>;
+                    qk<<<sg, dim3(GT), 0, s>>>(qkvr, H, KV, g->cur, g->cs, kc, vc, qb, qn, kn, g->eps, g->qscale,
+                                               g->cap, sl, win, div, ps, g->sc);
+                } else {
+                    gm_dec_prep_kernel<false><<<dim3((unsigned)(H + KV)), dim3(GT), plds, s>>>(
+                        qkvr, H, KV, hd, g->cur, g->cs, kc, vc, kq, vq, ks, vs, qb, qn, kn, g->eps, g->qr);
+                    gm_dec_score_kernel<false><<<sg, dim3(GT), hd4 * sizeof(float), s>>>(
+                        g->qr, H, KV, hd, g->cur, kc, kq, ks, g->qscale, g->cap, sl, win, div, ps, g->sc);
+                }
                 const hipError_t er = launch_value_ring(g, sl, win, ps, vc, vq, vs, attr, s);
                 if (er == hipErrorNotSupported)
                     gm_dec_value_kernel<false><<<dim3((unsigned)H), dim3(GT), vlds, s>>>(g->sc, H, KV, hd, g->cur,
@@ -2321,7 +2417,8 @@ int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_o
         if (int rc = mm(g->gu[l], g->a, g->gub)) return rc;
         const float gc = sqrtf(2.0f / 3.14159274101257324f);
         // rows the fused quant + GEMV covers take the elementwise act, then
-        // that linear; longer int8 rows the act + quant kernel, then the
+        // that linear (an act inside it would be recomputed by every one of
+        // its workgroups); longer int8 rows the act + quant kernel, then the
         // GEMV on the quantised row
         if (q8f && is_i8(g->down[l]) && !linear_m1_ok(*weight_of(g->down[l]), g->hm)) {
             const Q8 q = gm_q8(g, 1, g->ffn);

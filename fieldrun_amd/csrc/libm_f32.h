@@ -40,13 +40,9 @@ __host__ __device__ inline uint64_t d2u(double x) { uint64_t u; memcpy(&u, &x, 8
 __host__ __device__ inline double u2d(uint64_t u) { double x; memcpy(&x, &u, 8); return x; }
 
 
-// frq_expf's arithmetic away from the special cases, for any x (inputs the
-// special cases take give an unused value; the table index stays in range).
-__host__ __device__ inline float frq_expf_core(float x) {
-    // tab[i] = bits(RN(2^(i/32))) - (i << 47): the double nearest 2^(i/32)
-    // with its exponent field pre-subtracted, so adding k << 47 scales it by
-    // 2^(k/32).
-    constexpr uint64_t tab[32] = {
+// tab[i] = bits(RN(2^(i/32))) - (i << 47): the double nearest 2^(i/32) with
+// its exponent field pre-subtracted, so adding k << 47 scales it by 2^(k/32).
+constexpr uint64_t kExp2Tab[32] = {
     0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
     0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
     0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
@@ -54,8 +50,13 @@ __host__ __device__ inline float frq_expf_core(float x) {
     0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
     0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
     0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
-    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull, \
-    };
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
+};
+
+// frq_expf's arithmetic away from the special cases, for any x (inputs the
+// special cases take give an unused value; the table index stays in range),
+// with the table read from tab (kExp2Tab's 32 entries, e.g. a copy in LDS).
+__host__ __device__ inline float frq_expf_core_t(float x, const uint64_t* tab) {
     constexpr double shift = 0x1.8p+52, invln2n = 0x1.71547652b82fep+0 * 32;
     constexpr double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
                      c2 = 0x1.62e42ff0c52d6p-1 / 32;
@@ -73,6 +74,8 @@ __host__ __device__ inline float frq_expf_core(float x) {
     return (float)y;
 }
 
+__host__ __device__ inline float frq_expf_core(float x) { return frq_expf_core_t(x, kExp2Tab); }
+
 __host__ __device__ inline float frq_expf(float x) {
     const uint32_t abstop = (f2u(x) >> 20) & 0x7ff;
     if (abstop >= (0x42b00000u >> 20)) {          // |x| >= 88 or NaN
@@ -87,17 +90,18 @@ __host__ __device__ inline float frq_expf(float x) {
 // frq_expf without branches: the core always runs and the special cases
 // replace its value by selects, so a run of these in one thread keeps all
 // their table loads in flight together.  Same value as frq_expf for every x.
-__host__ __device__ inline float frq_expf_sel(float x) {
+__host__ __device__ inline float frq_expf_sel_t(float x, const uint64_t* tab) {
     // every special input has |x| >= 88, so the selects need no outer test;
     // applied lowest precedence first
     const uint32_t ux = f2u(x);
-    float r = frq_expf_core(x);
+    float r = frq_expf_core_t(x, tab);
     r = x < -0x1.9fe368p6f ? 0.0f : r;              // underflow
     r = x > 0x1.62e42ep6f ? u2f(0x7f800000u) : r;   // overflow
     r = (ux & 0x7fffffffu) >= 0x7f800000u ? x + x : r;  // inf, NaN
     r = ux == 0xff800000u ? 0.0f : r;               // -inf
     return r;
 }
+__host__ __device__ inline float frq_expf_sel(float x) { return frq_expf_sel_t(x, kExp2Tab); }
 
 __host__ __device__ inline float frq_expm1f(float x) {
     const float one = 1.0f, huge = 1.0e+30f, tiny = 1.0e-30f, o_threshold = 8.8721679688e+01f,
