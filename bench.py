@@ -119,6 +119,9 @@ def main():
                          "rocprofv3's kernel trace does not survive graph capture on this image)")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="only the counter-collection workload (run under rocprofv3 --pmc)")
+    ap.add_argument("--pmc-what", default="layer", choices=["layer", "int4", "m128"],
+                    help="counter workload: the configs[4] layer's four decode linears (default), the int4 "
+                         "M=1 GEMV at the Gemma-2 shapes, or the int8 linear at M=128")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path "
@@ -176,6 +179,33 @@ def main():
             hip.copy_d2d(dst.ptr, src.ptr, PMC_COPY_BYTES)
         hip.synchronize()
         log(f"pmc: 3 copies of {PMC_COPY_BYTES} bytes")
+        if args.pmc_what == "int4":
+            for (k, n) in [(2304, 9216), (9216, 2304)]:
+                reps = []
+                for r in range(3):
+                    packed, s16, g = synth.int4_weight(n, k, synth.seed(2, r))
+                    reps.append(ctx.upload_i4(packed, s16, k, g))
+                a = hip.DeviceArray.from_numpy(synth.activations(1, k, synth.seed(2, 9), outlier_scale=1.0))
+                o = hip.DeviceArray((1, n), np.float32)
+                for i in range(9):
+                    reps[i % 3].mm_dev(a.ptr, 1, o.ptr)
+                ctx.sync()
+                log(f"pmc: 9 int4 M=1 launches at K={k} N={n}, {int4_bytes(1, k, n)} algorithmic bytes each")
+                for w in reps:
+                    w.free()
+            return
+        if args.pmc_what == "m128":
+            for (k, n) in [(896, 151936), (4096, 14336)]:
+                reps = [ctx.upload_i8(*synth.int8_weight(n, k, synth.seed(1, r) + k)) for r in range(3)]
+                a = hip.DeviceArray.from_numpy(synth.activations(128, k, synth.seed(1) + k))
+                o = hip.DeviceArray((128, n), np.float32)
+                for i in range(9):
+                    reps[i % 3].mm_dev(a.ptr, 128, o.ptr)
+                ctx.sync()
+                log(f"pmc: 9 int8 M=128 linears at K={k} N={n}, {int8_linear_bytes(128, k, n)} algorithmic bytes each")
+                for w in reps:
+                    w.free()
+            return
         for si, (k, n) in enumerate(C4_SHAPES):
             reps = [ctx.upload_i8(*synth.int8_weight(n, k, synth.seed(4, r) + si)) for r in range(3)]
             a = hip.DeviceArray.from_numpy(synth.activations(1, k, synth.seed(4) + si))
