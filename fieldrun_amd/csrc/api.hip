@@ -865,6 +865,7 @@ int frq_moe_dev(frq_ctx* c, const frq_moe_w* h, const float* d_x, size_t T,
     const MoeBank& b = h->b;
     if (b.device != c->device) return fail(FRQ_ERR_ARG, "MoE bank lives on another device");
     if (topk == 0 || topk > b.n_exp) return fail(FRQ_ERR_ARG, "topk must be in [1, n_exp]");
+    if (topk > 256) return fail(FRQ_ERR_ARG, "topk above 256 slots a token");
     if (T == 0) return FRQ_OK;
     if (!d_x || !d_logits || !d_out) return fail(FRQ_ERR_ARG, "null pointer");
     DeviceGuard g(c->device);
@@ -880,6 +881,7 @@ int frq_moe(frq_ctx* c, const frq_moe_w* h, const float* x, size_t T, const floa
     if (!h) return fail(FRQ_ERR_ARG, "null MoE bank");
     const MoeBank& b = h->b;
     if (topk == 0 || topk > b.n_exp) return fail(FRQ_ERR_ARG, "topk must be in [1, n_exp]");
+    if (topk > 256) return fail(FRQ_ERR_ARG, "topk above 256 slots a token");
     if (T == 0) return FRQ_OK;
     if (!x || !logits || !out) return fail(FRQ_ERR_ARG, "null pointer");
     DeviceGuard g(c->device);

@@ -70,7 +70,7 @@ size_t ntile_max(size_t T, size_t k, size_t E, size_t tr) {
     return P / tr + (E < P ? E : P) + 1;
 }
 
-size_t moe_tile_rows(size_t T) { return T <= 4 ? 4 : 16; }
+size_t moe_tile_rows(size_t T) { return T <= 4 ? 4 : 64; }
 
 MoeWs moe_view(void* base, const MoeBank& b, size_t T, size_t k) {
     const size_t P = T * k, E = b.n_exp, nt = ntile_max(T, k, E, moe_tile_rows(T));
@@ -108,35 +108,133 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 }
 
 // ---- routing: one wave per token ----------------------------------------
-// Routing of one token by one wave: softmax (max, exp, sequential sum,
-// divide), k rounds of arg-max by (p desc, expert asc), renormalised
-// weights.  p: E floats of LDS; picks go to pe / pw (k entries of LDS, pick
-// order).  Returns true (uniformly) when the row holds a NaN: the reference
-// panics; the picks are then experts 0..k-1 with weight 0.
-__device__ bool route_wave(const float* __restrict__ row, int E, int topk, int norm_topk,
-                           const float* __restrict__ pes, float* p, int* pe, float* pw) {
+// Wave-wide max of a float (every lane gets it), VALU lane exchanges only.
+__device__ __forceinline__ float wave_fmax(float v) {
+    v = fmaxf(v, __uint_as_float(xshfl<1>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(xshfl<2>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(xshfl<4>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(xshfl<8>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(xshfl<16>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(xshfl<32>(__float_as_uint(v))));
+    return v;
+}
+
+// A row has no probabilities the reference can sort when a logit is NaN or
+// the max is +-inf (inf - inf in an exponent makes every p NaN): its
+// partial_cmp().unwrap() panics.  The picks are then experts 0..k-1 with
+// weight 0, and the caller raises the error.
+__device__ __forceinline__ void route_fail(int topk, int* pe, float* pw) {
+    for (int i = threadIdx.x & 63; i < topk; i += 64) { pe[i] = i; pw[i] = 0.0f; }
+    wave_sync();
+}
+
+// The sequential sum p[0] + ... + p[E-1] from +0 (the reference's order),
+// the same chain in every lane; reads batched ahead of it where p is
+// 16-byte aligned.
+__device__ __forceinline__ float route_sum(const float* p, int E) {
+    if ((reinterpret_cast<uintptr_t>(p) & 15) == 0) return lds_seq_sum(p, E, 0.0f);
+    float s = 0.0f;
+    for (int e = 0; e < E; ++e) s = s + p[e];
+    return s;
+}
+
+// Renormalised weights, one pick per lane (each the same operations as a
+// sequential pass): p / denom (when renormalising) then * per_expert_scale.
+__device__ __forceinline__ void route_weights(int topk, int norm_topk, const float* __restrict__ pes,
+                                              float denom, const int* pe, float* pw) {
+    const bool renorm = norm_topk || pes != nullptr;
+    for (int i = threadIdx.x & 63; i < topk; i += 64) {
+        float w = renorm ? pw[i] / denom : pw[i];
+        if (pes) w = w * pes[pe[i]];
+        pw[i] = w;
+    }
+    wave_sync();
+}
+
+// Routing of one token by one wave, E <= 64 * NC: the probabilities stay
+// in registers (expert lane + 64 c in chunk c); softmax (max, exp,
+// sequential sum, divide), then k rounds of arg-max by (p desc, expert
+// asc): the wave max of p, and the lowest expert holding it from one
+// ballot per chunk (chunks ascend in expert id).  p: E floats of LDS (the
+// sum's operand); picks go to pe / pw (k entries of LDS, pick order).
+// Returns true (uniformly) for a row the reference cannot sort.
+template <int NC>
+__device__ bool route_wave_r(const float* __restrict__ row, int E, int topk, int norm_topk,
+                             const float* __restrict__ pes, float* p, int* pe, float* pw) {
     const int lane = threadIdx.x & 63;
+    float v[NC];
     float m = -INFINITY;
-    int bad = 0;
-    for (int e = lane; e < E; e += 64) {
-        const float v = row[e];
-        bad |= (v != v);
-        m = fmaxf(m, v);
+    bool nan = false;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int e = lane + 64 * c;
+        v[c] = e < E ? row[e] : -INFINITY;
+        nan |= v[c] != v[c];
+        m = fmaxf(m, v[c]);
+    }
+    m = wave_fmax(m);
+    if (__builtin_amdgcn_ballot_w64(nan) != 0 || !(fabsf(m) <= 3.40282347e38f)) {
+        route_fail(topk, pe, pw);
+        return true;
     }
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        m = fmaxf(m, __shfl_xor(m, off, 64));
-        bad |= __shfl_xor(bad, off, 64);
+    for (int c = 0; c < NC; ++c) {
+        const int e = lane + 64 * c;
+        if (e < E) {
+            v[c] = libm::frq_expf(v[c] - m);
+            p[e] = v[c];
+        }
     }
-    if (bad) {
-        for (int i = lane; i < topk; i += 64) { pe[i] = i; pw[i] = 0.0f; }
-        wave_sync();
+    wave_sync();
+    const float s = route_sum(p, E);
+    // taken experts become -1, lanes past E -2: both below every p >= +0
+#pragma unroll
+    for (int c = 0; c < NC; ++c) v[c] = lane + 64 * c < E ? v[c] / s : -2.0f;
+    float denom = -0.0f;
+    for (int i = 0; i < topk; ++i) {
+        float bl = v[0];
+#pragma unroll
+        for (int c = 1; c < NC; ++c) bl = fmaxf(bl, v[c]);
+        const float bv = wave_fmax(bl);
+        int be = -1;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const unsigned long long msk = __builtin_amdgcn_ballot_w64(v[c] == bv);
+            if (be < 0 && msk != 0) be = 64 * c + __builtin_ctzll(msk);
+        }
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+            if (be == lane + 64 * c) v[c] = -1.0f;
+        if (lane == 0) {
+            pe[i] = be;
+            pw[i] = bv;
+        }
+        denom = denom + bv;
+    }
+    wave_sync();
+    route_weights(topk, norm_topk, pes, denom, pe, pw);
+    return false;
+}
+
+// Any E: the probabilities in LDS p (E floats), arg-max rounds over them.
+__device__ bool route_wave_lds(const float* __restrict__ row, int E, int topk, int norm_topk,
+                               const float* __restrict__ pes, float* p, int* pe, float* pw) {
+    const int lane = threadIdx.x & 63;
+    float m = -INFINITY;
+    bool nan = false;
+    for (int e = lane; e < E; e += 64) {
+        const float v = row[e];
+        nan |= v != v;
+        m = fmaxf(m, v);
+    }
+    m = wave_fmax(m);
+    if (__builtin_amdgcn_ballot_w64(nan) != 0 || !(fabsf(m) <= 3.40282347e38f)) {
+        route_fail(topk, pe, pw);
         return true;
     }
     for (int e = lane; e < E; e += 64) p[e] = libm::frq_expf(row[e] - m);
     wave_sync();
-    float s = 0.0f;  // sequential sum in expert order, as the reference
-    for (int e = 0; e < E; ++e) s = s + p[e];
+    const float s = route_sum(p, E);
     wave_sync();
     for (int e = lane; e < E; e += 64) p[e] = p[e] / s;
     wave_sync();
@@ -163,16 +261,17 @@ __device__ bool route_wave(const float* __restrict__ row, int E, int topk, int n
         wave_sync();
         denom = denom + bv;
     }
-    // renormalised weights, one pick per lane (each the same operations as a
-    // sequential pass)
-    const bool renorm = norm_topk || pes != nullptr;
-    for (int i = lane; i < topk; i += 64) {
-        float w = renorm ? pw[i] / denom : pw[i];
-        if (pes) w = w * pes[pe[i]];
-        pw[i] = w;
-    }
-    wave_sync();
+    route_weights(topk, norm_topk, pes, denom, pe, pw);
     return false;
+}
+
+// Routing of one token by one wave (see route_wave_r); picks in pick order.
+__device__ bool route_wave(const float* __restrict__ row, int E, int topk, int norm_topk,
+                           const float* __restrict__ pes, float* p, int* pe, float* pw) {
+    if (E <= 64) return route_wave_r<1>(row, E, topk, norm_topk, pes, p, pe, pw);
+    if (E <= 128) return route_wave_r<2>(row, E, topk, norm_topk, pes, p, pe, pw);
+    if (E <= 256) return route_wave_r<4>(row, E, topk, norm_topk, pes, p, pe, pw);
+    return route_wave_lds(row, E, topk, norm_topk, pes, p, pe, pw);
 }
 
 // One wave per token (4 per workgroup); every step stays inside the wave.
@@ -180,7 +279,7 @@ __global__ __launch_bounds__(256) void route_kernel(
     const float* __restrict__ logits, int T, int E, int topk, int norm_topk,
     const float* __restrict__ pes, int32_t* __restrict__ sel,
     float* __restrict__ wout, int* __restrict__ err) {
-    extern __shared__ float sp[];  // [4][E] probabilities, [4][topk] picks (expert, w)
+    extern __shared__ __attribute__((aligned(16))) float sp[];  // [4][E] probabilities, [4][topk] picks (expert, w)
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int t = blockIdx.x * 4 + wv;
     if (t >= T) return;  // whole waves only
@@ -206,6 +305,7 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(
     uint32_t* run = sm + (size_t)E * nwc;  // [E] running count
     uint32_t* pre = run + E;               // [E][nwc] prefix popcounts
     uint32_t* offl = pre + (size_t)E * nwc;  // [E] expert row offsets
+    uint32_t* toff = offl + E;               // [E] expert tile offsets
     const int tid = threadIdx.x;
     for (int e = tid; e < E; e += 1024) run[e] = 0;
     __syncthreads();
@@ -215,18 +315,39 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(
         if (e >= 0 && e < E) atomicAdd(&run[e], 1u);
     }
     __syncthreads();
-    if (tid == 0) {
-        int acc = 0, nt = 0;
-        for (int e = 0; e < E; ++e) {
-            const int c = (int)run[e];
-            ws.cnt[e] = c;
-            ws.off[e] = acc;
-            offl[e] = (uint32_t)acc;
-            for (int r = 0; r < c; r += tr) { ws.tile_e[nt] = e; ws.tile_r[nt] = r; ++nt; }
-            acc += c;
+    // row and tile offsets: exclusive scans over the experts by wave 0, 64
+    // experts a step
+    if (tid < 64) {
+        int cr = 0, ct = 0;  // running totals of the steps before
+        for (int e0 = 0; e0 < E; e0 += 64) {
+            const int e = e0 + tid;
+            const int c = e < E ? (int)run[e] : 0, nt = (c + tr - 1) / tr;
+            int ic = c, it = nt;  // inclusive scans
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int yc = __shfl_up(ic, o, 64), yt = __shfl_up(it, o, 64);
+                if (tid >= o) { ic += yc; it += yt; }
+            }
+            if (e < E) {
+                ws.cnt[e] = c;
+                ws.off[e] = cr + ic - c;
+                offl[e] = (uint32_t)(cr + ic - c);
+                toff[e] = (uint32_t)(ct + it - nt);
+            }
+            cr += __shfl(ic, 63, 64);
+            ct += __shfl(it, 63, 64);
         }
-        ws.off[E] = acc;
-        ws.ntile[0] = nt;
+        if (tid == 0) {
+            ws.off[E] = cr;
+            ws.ntile[0] = ct;
+        }
+    }
+    __syncthreads();
+    // the tile list: (expert, first row) in ascending expert, then row
+    for (int e = tid; e < E; e += 1024) {
+        const int c = (int)run[e];
+        int t = (int)toff[e];
+        for (int r = 0; r < c; r += tr, ++t) { ws.tile_e[t] = e; ws.tile_r[t] = r; }
     }
     __syncthreads();
     for (int e = tid; e < E; e += 1024) run[e] = 0;
@@ -307,12 +428,64 @@ __device__ void row_digits(const float* __restrict__ v, int K, int Kp, int8_t* _
     if (tid == 0) *so_out = ok ? s : -1.0f;
 }
 
+// row_digits over values produced by val(k), held in registers (thread
+// tid takes k = tid + 256 i): one pass over the source, Kp <= 256 * NV.
+template <int NV, typename F>
+__device__ __forceinline__ void row_digits_r(F val, int K, int Kp, int8_t* __restrict__ D,
+                                             float* __restrict__ so_out, float* red) {
+    const int tid = threadIdx.x;
+    float v[NV];
+    float mx = 0.0f;
+    bool nf = false;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int k = tid + 256 * i;
+        v[i] = k < K ? val(k) : 0.0f;
+        nf |= !(fabsf(v[i]) <= 3.0e38f);
+        mx = fmaxf(mx, fabsf(v[i]));
+    }
+    mx = wave_fmax(mx);
+    const bool wnf = __builtin_amdgcn_ballot_w64(nf) != 0;
+    if ((tid & 63) == 0) { red[tid >> 6] = mx; red[4 + (tid >> 6)] = wnf ? 1.0f : 0.0f; }
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const bool anf = (red[4] + red[5] + red[6] + red[7]) != 0.0f;
+    const float s = mx > 0.0f ? mx / XMAXD : 1.0f;
+    const bool ok = !anf && s >= 1.0e-30f && s <= 1.0e28f;
+    const float r = 1.0f / s;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int k = tid + 256 * i;
+        if (k >= Kp) break;
+        int d2 = 0, d1 = 0, d0 = 0;
+        if (ok && k < K) {
+            float xf = rintf(v[i] * r);
+            xf = fminf(fmaxf(xf, -XMAXD), XMAXD);
+            const int X = (int)xf;
+            d0 = (int)(int8_t)(X & 0xFF);
+            const int X1 = (X - d0) >> 8;
+            d1 = (int)(int8_t)(X1 & 0xFF);
+            d2 = (X1 - d1) >> 8;
+        }
+        D[k] = (int8_t)d2;
+        D[Kp + k] = (int8_t)d1;
+        D[2 * Kp + k] = (int8_t)d0;
+    }
+    if (tid == 0) *so_out = ok ? s : -1.0f;
+}
+
+constexpr int RD_NV = 8;  // register-held rows: Kp <= 2048
+
 // One workgroup per token row of x.
 __global__ __launch_bounds__(256) void x_digits_kernel(const float* __restrict__ x, int K, int Kp,
                                                        int8_t* __restrict__ D, float* __restrict__ so) {
     __shared__ float red[8];
     const int r = blockIdx.x;
-    row_digits(x + (size_t)r * K, K, Kp, D + (size_t)r * 3 * Kp, so + r, red);
+    const float* xr = x + (size_t)r * K;
+    if (Kp <= 256 * RD_NV)
+        row_digits_r<RD_NV>([&](int k) { return xr[k]; }, K, Kp, D + (size_t)r * 3 * Kp, so + r, red);
+    else
+        row_digits(xr, K, Kp, D + (size_t)r * 3 * Kp, so + r, red);
 }
 
 // h = silu(g) * u  or  gelu_tanh(g[:mi]) * g[mi:], one workgroup per
@@ -327,6 +500,17 @@ __global__ __launch_bounds__(256) void act_digits_kernel(
     if (r >= off[E]) return;  // uniform
     const float* gr = g + (size_t)r * gw;
     float* hr = h + (size_t)r * mi;
+    if (kpm <= 256 * RD_NV) {
+        row_digits_r<RD_NV>(
+            [&](int c) {
+                const float hv = act == FRQ_ACT_SILU ? silu(gr[c]) * u[(size_t)r * mi + c]
+                                                     : gelu_tanh(gr[c]) * gr[c + mi];
+                hr[c] = hv;
+                return hv;
+            },
+            mi, kpm, hd + (size_t)r * 3 * kpm, hso + r, red);
+        return;
+    }
     for (int c = threadIdx.x; c < mi; c += 256)
         hr[c] = act == FRQ_ACT_SILU ? silu(gr[c]) * u[(size_t)r * mi + c] : gelu_tanh(gr[c]) * gr[c + mi];
     __syncthreads();
@@ -448,6 +632,167 @@ __global__ __launch_bounds__(64 * KS) void moe_mm_kernel(
             y[(size_t)prow * N + j] = v;
         }
     }
+}
+
+// ---- expert-stationary grouped digit GEMM (batched rows) -------------------
+// Workgroup = (tile of up to 64 permuted rows of one expert, 128 columns):
+// the expert's 128-column weight block streams from HBM once per tile, each
+// of the 4 waves taking 32 columns (two 16-column blocks); the tile's digit
+// rows pass through LDS one k-block at a time (double-buffered), and every
+// A operand read from LDS feeds two MFMAs.  The A items and B operands of
+// k-block kb sit in register slot kb % GM_BP from their load until use, so
+// both stream GM_BP k-blocks ahead (the wait counter is in order: A, needed
+// first, must not trail B).  Every load is unconditional, from a clamped
+// address, so the waits stay exact.  A operand of row group g: lane
+// 16 kq + 4 tl + d holds digit d of row 4 g + tl, k-bytes 16 kq..16 kq + 15
+// of the k-block (LDS keeps the 48 lanes d < 3; d = 3 reads a copy of
+// d = 2, whose product row acc[3] is not used); C lane l holds row
+// 4 g + l / 16, digit c in acc[c], column l % 16.  Output as
+// moe_mm_kernel's.  NGT = row groups the tile's rows need (4, 8 or 16).
+constexpr int GM_TR = 64;  // rows a tile
+constexpr int GM_BP = 6;   // k-blocks of A and B in flight a wave
+constexpr int GM_AS = (GM_TR / 4) * 48 + 256;  // A slots a buffer (+ one spare a thread)
+
+struct GmmArgs {
+    const int8_t* D;
+    const float* dso;
+    int Kp, Np, N, K;
+    const int8_t* Wb;
+    const float* wsc;
+    const float* xf;
+    const int8_t* wkn;
+    float* y;
+};
+
+template <int NGT>
+__device__ __forceinline__ void gmm_body(const GmmArgs& A, v4i (*As)[GM_AS], const int* srcs, int e,
+                                         int rows, int pbase, int cg) {
+    constexpr int NIT = 48 * NGT, UA = (NIT + 255) / 256;  // A items a k-block, a thread
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nkb = A.Kp / 64;
+    const int8_t* asrc[UA];
+    int adst[UA];
+#pragma unroll
+    for (int u = 0; u < UA; ++u) {
+        const int it = tid + 256 * u, kq = it & 3, rd = it >> 2, i = rd / 3, dg = rd - 3 * i;
+        const bool on = it < NIT;
+        asrc[u] = A.D + ((size_t)srcs[on ? min(i, rows - 1) : 0] * 3 + (on ? dg : 0)) * A.Kp + 16 * kq;
+        adst[u] = on ? (i >> 2) * 48 + kq * 12 + (i & 3) * 3 + dg : (GM_TR / 4) * 48 + tid;
+    }
+    const int cb0 = cg * 8 + 2 * wave, ncb = A.Np / 16;  // this wave's column blocks
+    const int8_t* wb0 = A.Wb + (size_t)e * A.Np * A.Kp + (size_t)min(cb0, ncb - 1) * 1024 + lane * 16;
+    const int8_t* wb1 = A.Wb + (size_t)e * A.Np * A.Kp + (size_t)min(cb0 + 1, ncb - 1) * 1024 + lane * 16;
+    const size_t ks = (size_t)ncb * 1024;
+    v4i ar[GM_BP][UA], bq[GM_BP][2];
+    // k-blocks past the last (the loop runs whole rounds of GM_BP) multiply
+    // a zero B operand
+    auto ld = [&](int sl, int kb) {
+        const size_t k = (size_t)min(kb, nkb - 1);
+#pragma unroll
+        for (int u = 0; u < UA; ++u) ar[sl][u] = *reinterpret_cast<const v4i*>(asrc[u] + k * 64);
+        const v4i b0 = *reinterpret_cast<const v4i*>(wb0 + k * ks);
+        const v4i b1 = *reinterpret_cast<const v4i*>(wb1 + k * ks);
+        const v4i z = v4i{0, 0, 0, 0};
+        bq[sl][0] = kb < nkb ? b0 : z;
+        bq[sl][1] = kb < nkb ? b1 : z;
+    };
+    auto sta = [&](int sl, int buf) {
+#pragma unroll
+        for (int u = 0; u < UA; ++u) As[buf][adst[u]] = ar[sl][u];
+    };
+    v4i acc[NGT][2];
+#pragma unroll
+    for (int g = 0; g < NGT; ++g) acc[g][0] = acc[g][1] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int sl = 0; sl < GM_BP; ++sl) ld(sl, sl);
+    sta(0, 0);
+    const int rr = lane & 15, tl = rr >> 2, dgl = rr & 3, kql = lane >> 4;
+    const int aidx = kql * 12 + tl * 3 + (dgl < 3 ? dgl : 2);
+    for (int kb0 = 0; kb0 < nkb; kb0 += GM_BP) {
+#pragma unroll
+        for (int sl = 0; sl < GM_BP; ++sl) {
+            const int kb = kb0 + sl;
+            __syncthreads();  // As[kb & 1] written by every wave, As[~kb & 1] read
+            const v4i* ab = As[kb & 1];
+            // every A read issued before the MFMAs (one LDS latency a
+            // k-block; the scheduler would pair reads with their MFMAs)
+            v4i av[NGT];
+#pragma unroll
+            for (int g = 0; g < NGT; ++g) av[g] = ab[g * 48 + aidx];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int g = 0; g < NGT; ++g) {
+                acc[g][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[g], bq[sl][0], acc[g][0], 0, 0, 0);
+                acc[g][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[g], bq[sl][1], acc[g][1], 0, 0, 0);
+            }
+            // k-block kb + 1's A into the other buffer; slot sl is then spent
+            // (its A stored an iteration ago, its B used now): reload it
+            const int sn = (sl + 1) % GM_BP;
+            if (kb + 1 < nkb) sta(sn, (kb + 1) & 1);
+            ld(sl, kb + GM_BP);
+        }
+    }
+    // y = s * (C2 * 2^16 + C1 * 2^8 + C0) * wsc[e, j]; rows whose digits do not
+    // carry them take the reference's sequential sum x . (q * s)
+    const int col = lane & 15, tok = lane >> 4;
+    const float* __restrict__ se = A.wsc + (size_t)e * A.N;
+#pragma unroll
+    for (int g = 0; g < NGT; ++g) {
+        const int i = 4 * g + tok;
+        if (i < rows) {  // predicated, not continue: acc stays statically indexed
+            const int prow = pbase + i, src = srcs[i];
+            const float so = A.dso[src];
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                const int j = (cb0 + c) * 16 + col;
+                if (j < A.N) {
+                    float v;
+                    if (so >= 0.0f) {
+                        const v4i a4 = acc[g][c];
+                        v = so * ((float)a4[0] * 65536.0f + ((float)a4[1] * 256.0f + (float)a4[2])) * se[j];
+                    } else {
+                        const float* xr = A.xf + (size_t)src * A.K;
+                        const int8_t* qe = A.wkn + (size_t)e * A.K * A.N;
+                        const float sj = se[j];
+                        v = 0.0f;
+                        for (int k = 0; k < A.K; ++k)
+                            v = __builtin_fmaf(xr[k], (float)qe[(size_t)k * A.N + j] * sj, v);
+                    }
+                    A.y[(size_t)prow * A.N + j] = v;
+                }
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void moe_gmm_kernel(GmmArgs A, int gather, const int32_t* __restrict__ ptok,
+                                                      const int32_t* __restrict__ off,
+                                                      const int32_t* __restrict__ cnt,
+                                                      const int32_t* __restrict__ tile_e,
+                                                      const int32_t* __restrict__ tile_r,
+                                                      const int32_t* __restrict__ ntile) {
+    __shared__ v4i As[2][GM_AS];
+    __shared__ int srcs[GM_TR];
+    // XCD-aware order: workgroup id goes to XCD id % 8, and XCD x runs
+    // tiles x, x + 8, ... with all ncg column groups of a tile in a row, so
+    // the tile's digit rows are fetched into that XCD's L2 once
+    const int ncg = (A.Np / 16 + 7) / 8;
+    const int xcd = blockIdx.x & 7, j = blockIdx.x >> 3;
+    const int tix = xcd + 8 * (j / ncg), cg = j % ncg;
+    if (tix >= ntile[0]) return;  // uniform
+    const int e = tile_e[tix], r0 = tile_r[tix];
+    const int rows = min(GM_TR, cnt[e] - r0);
+    const int pbase = off[e] + r0;
+    const int tid = threadIdx.x;
+    if (tid < GM_TR) {
+        const int prow = pbase + min(tid, rows - 1);
+        srcs[tid] = gather ? ptok[prow] : prow;
+    }
+    __syncthreads();
+    if (rows <= 16) gmm_body<4>(A, As, srcs, e, rows, pbase, cg);
+    else if (rows <= 32) gmm_body<8>(A, As, srcs, e, rows, pbase, cg);
+    else gmm_body<16>(A, As, srcs, e, rows, pbase, cg);
 }
 
 // ---- decode (T == 1): three launches ---------------------------------------
@@ -596,27 +941,302 @@ __global__ __launch_bounds__(1024) void moe_dec_down_kernel(
     }
 }
 
-__global__ void combine_kernel(const float* __restrict__ dn, const int32_t* __restrict__ sel,
-                               const float* __restrict__ w, const int32_t* __restrict__ pos,
-                               int topk, int d, float* __restrict__ out) {
-    const int t = blockIdx.y;
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= d) return;
-    // the token's slots in ascending expert id (experts within a token are
-    // distinct: top-k of a permutation)
-    const int32_t* st = sel + (size_t)t * topk;
-    float acc = 0.0f;
-    int last = -1;
-    for (int i = 0; i < topk; ++i) {
-        int best = -1, be = 0x7FFFFFFF;
-        for (int q = 0; q < topk; ++q) {
-            const int ev = st[q];
-            if (ev > last && ev < be) { be = ev; best = q; }
+// ---- decode (T == 1): two launches ----------------------------------------
+// D1: workgroup (slot s of the k picks in ascending expert id, 16 columns
+// of h).  Wave 0 routes the token while waves 1..3 take max|x| of its row;
+// then every wave issues its share (a quarter of K) of the expert's two
+// weight blocks, gate and up (or the two halves of the packed gate_up),
+// before the token's digit row is formed in LDS, so the row's second pass
+// over x overlaps the weight stream.  The two digit GEMMs end in wave 0,
+// whose lanes 0..15 write h = act(g) * u for their columns.  Workgroup
+// (0, 0) publishes the picks in ascending expert id (ws.sel / ws.w).
+// Matrix a holds g (columns 0..mi), matrix b holds u at column boff.
+constexpr int DEC_U = 8;  // k-blocks per wave and load batch
+
+__global__ __launch_bounds__(256) void moe_dec_gua_kernel(
+    const float* __restrict__ x, int d, int kpd, const float* __restrict__ logits, int E, int topk,
+    int norm_topk, const float* __restrict__ pes, const int8_t* __restrict__ a_b, int npa,
+    const float* __restrict__ a_s, int na, const int8_t* __restrict__ a_q,
+    const int8_t* __restrict__ b_b, int npb, const float* __restrict__ b_s, int nbw,
+    const int8_t* __restrict__ b_q, int boff, int act, int mi, float* __restrict__ h, MoeWs ws,
+    int* __restrict__ err) {
+    constexpr int KS = 4;
+    extern __shared__ __attribute__((aligned(16))) float dsm[];
+    float* p = dsm;                                        // [E]
+    int* pe = reinterpret_cast<int*>(dsm + E);             // [topk] picks, pick order
+    float* pw = dsm + E + topk;
+    int* se = reinterpret_cast<int*>(dsm + E + 2 * topk);  // [topk] ascending expert id
+    float* sw = dsm + E + 3 * topk;
+    float* red = dsm + E + 4 * topk;                       // [8]
+    int* bad_l = reinterpret_cast<int*>(red + 9);
+    int8_t* Dl = reinterpret_cast<int8_t*>(dsm + ((E + 4 * topk + 10 + 3) & ~3));  // [3][kpd]
+    __shared__ v4i rv[KS - 1][2][64];
+
+    const int slot = blockIdx.x, cbk = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    if (wave == 0) {
+        const bool bad = route_wave(logits, E, topk, norm_topk, pes, p, pe, pw);
+        for (int i = lane; i < topk; i += 64) {
+            int r = 0;
+            for (int j = 0; j < topk; ++j) r += pe[j] < pe[i];
+            se[r] = pe[i];
+            sw[r] = pw[i];
         }
-        if (best < 0) break;
-        last = be;
-        acc = acc + w[(size_t)t * topk + best] * dn[(size_t)pos[(size_t)t * topk + best] * d + c];
+        if (lane == 0) *bad_l = bad;
+    } else {
+        float mx = 0.0f;
+        bool nf = false;
+        for (int k = tid - 64; k < d; k += 192) {
+            const float xv = x[k];
+            nf |= !(fabsf(xv) <= 3.0e38f);
+            mx = fmaxf(mx, fabsf(xv));
+        }
+        mx = wave_fmax(mx);
+        const bool wnf = __builtin_amdgcn_ballot_w64(nf) != 0;
+        if (lane == 0) {
+            red[wave - 1] = mx;
+            red[4 + wave - 1] = wnf ? 1.0f : 0.0f;
+        }
     }
+    __syncthreads();
+    if (slot == 0 && cbk == 0) {
+        if (tid < topk) { ws.sel[tid] = se[tid]; ws.w[tid] = sw[tid]; }
+        if (tid == 0 && *bad_l) atomicOr(err, 1);
+    }
+    const int e = se[slot];
+    const int nkb = kpd / 64, kb0 = nkb * wave / KS, kb1 = nkb * (wave + 1) / KS;
+    const int rr = lane & 15, dg = rr & 3, kq = lane >> 4;
+    const bool aval = rr < 3;  // token 0, digits 0..2
+    const int8_t* wa = a_b + (size_t)e * npa * kpd + (size_t)cbk * 1024 + lane * 16;
+    const int8_t* wb = b_b + (size_t)e * npb * kpd + (size_t)(boff / 16 + cbk) * 1024 + lane * 16;
+    const size_t ksa = (size_t)(npa / 16) * 1024, ksb = (size_t)(npb / 16) * 1024;
+    v4i ba[DEC_U], bb[DEC_U];
+    auto ldw = [&](int kb) {
+#pragma unroll
+        for (int q = 0; q < DEC_U; ++q) {
+            const bool in = kb + q < kb1;
+            ba[q] = in ? *reinterpret_cast<const v4i*>(wa + (size_t)(kb + q) * ksa) : v4i{0, 0, 0, 0};
+            bb[q] = in ? *reinterpret_cast<const v4i*>(wb + (size_t)(kb + q) * ksb) : v4i{0, 0, 0, 0};
+        }
+    };
+    ldw(kb0);
+    const int j = cbk * 16 + lane;
+    const bool jout = wave == 0 && lane < 16 && j < mi;
+    const float sa = jout ? a_s[(size_t)e * na + j] : 0.0f;
+    const float sb = jout ? b_s[(size_t)e * nbw + boff + j] : 0.0f;
+    __builtin_amdgcn_sched_barrier(0);
+    // the token's digit row (as row_digits), from the maxima of waves 1..3
+    const float mxx = fmaxf(fmaxf(red[0], red[1]), red[2]);
+    const bool xnf = (red[4] + red[5] + red[6]) != 0.0f;
+    const float sx = mxx > 0.0f ? mxx / XMAXD : 1.0f;
+    const bool ok = !xnf && sx >= 1.0e-30f && sx <= 1.0e28f;
+    const float rx = 1.0f / sx;
+    for (int k = tid; k < kpd; k += 256) {
+        int d2 = 0, d1 = 0, d0 = 0;
+        if (ok && k < d) {
+            float xf = rintf(x[k] * rx);
+            xf = fminf(fmaxf(xf, -XMAXD), XMAXD);
+            const int X = (int)xf;
+            d0 = (int)(int8_t)(X & 0xFF);
+            const int X1 = (X - d0) >> 8;
+            d1 = (int)(int8_t)(X1 & 0xFF);
+            d2 = (X1 - d1) >> 8;
+        }
+        Dl[k] = (int8_t)d2;
+        Dl[kpd + k] = (int8_t)d1;
+        Dl[2 * kpd + k] = (int8_t)d0;
+    }
+    __syncthreads();
+    const int8_t* arow = Dl + (dg < 3 ? dg : 0) * kpd + 16 * kq;
+    v4i acca = v4i{0, 0, 0, 0}, accb = v4i{0, 0, 0, 0};
+    for (int kb = kb0; kb < kb1; kb += DEC_U) {
+        v4i av[DEC_U];
+#pragma unroll
+        for (int q = 0; q < DEC_U; ++q)
+            av[q] = (kb + q < kb1 && aval) ? *reinterpret_cast<const v4i*>(arow + (size_t)(kb + q) * 64)
+                                           : v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int q = 0; q < DEC_U; ++q) {
+            acca = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[q], ba[q], acca, 0, 0, 0);
+            accb = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[q], bb[q], accb, 0, 0, 0);
+        }
+        if (kb + DEC_U < kb1) ldw(kb + DEC_U);
+    }
+    if (wave > 0) {
+        rv[wave - 1][0][lane] = acca;
+        rv[wave - 1][1][lane] = accb;
+    }
+    __syncthreads();
+    if (wave > 0 || lane >= 16) return;
+#pragma unroll
+    for (int q = 0; q < KS - 1; ++q) {
+        acca += rv[q][0][lane];
+        accb += rv[q][1][lane];
+    }
+    // lanes 0..15: the token's digit sums in acc[0..2], column lane
+    if (!jout) return;
+    float ga, gb;
+    if (ok) {
+        ga = sx * ((float)acca[0] * 65536.0f + ((float)acca[1] * 256.0f + (float)acca[2])) * sa;
+        gb = sx * ((float)accb[0] * 65536.0f + ((float)accb[1] * 256.0f + (float)accb[2])) * sb;
+    } else {
+        const int8_t* qa = a_q + (size_t)e * d * na;
+        const int8_t* qb = b_q + (size_t)e * d * nbw;
+        ga = 0.0f;
+        gb = 0.0f;
+        for (int k = 0; k < d; ++k) {
+            ga = __builtin_fmaf(x[k], (float)qa[(size_t)k * na + j] * sa, ga);
+            gb = __builtin_fmaf(x[k], (float)qb[(size_t)k * nbw + boff + j] * sb, gb);
+        }
+    }
+    h[(size_t)slot * mi + j] = act == FRQ_ACT_SILU ? silu(ga) * gb : gelu_tanh(ga) * gb;
+}
+
+// D2: down GEMM of all k rows and the combine; wave s takes slot s
+// (ascending expert id), each workgroup 16 output columns.  Every wave
+// issues its expert's first weight batch, then forms its row's digits (as
+// row_digits) from h in its own LDS slab, four channels a lane and step;
+// the combine adds the slots' w * down in ascending expert id from +0, as
+// combine_kernel does.
+constexpr int DEC_HV = 4;   // h quads a lane: kpm <= 1024
+constexpr int DEC_DU = 16;  // k-blocks a load batch: all of kpm <= 1024
+
+__global__ __launch_bounds__(1024) void moe_dec_dn_kernel(
+    const float* __restrict__ h, int mi, int kpm, const int8_t* __restrict__ down_b, int dp,
+    const float* __restrict__ down_s, const int8_t* __restrict__ down, int d,
+    const int32_t* __restrict__ sel, const float* __restrict__ wsel, int topk,
+    float* __restrict__ out) {
+    extern __shared__ __attribute__((aligned(16))) uint32_t dw[];  // [topk][3][kpm / 4]
+    __shared__ float vs[16][16];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int slot = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nb0 = blockIdx.x;
+    const int e = sel[slot];
+    const int nkb = kpm / 64;
+    const int8_t* wb = down_b + (size_t)e * dp * kpm + (size_t)nb0 * 1024 + lane * 16;
+    const size_t kstride = (size_t)(dp / 16) * 1024;
+    v4i bv[DEC_DU];
+    auto ldw = [&](int kb) {
+#pragma unroll
+        for (int q = 0; q < DEC_DU; ++q)
+            bv[q] = kb + q < nkb ? *reinterpret_cast<const v4i*>(wb + (size_t)(kb + q) * kstride)
+                                 : v4i{0, 0, 0, 0};
+    };
+    ldw(0);
+    const int j = nb0 * 16 + lane;
+    const bool jout = lane < 16 && j < d;
+    const float sj = jout ? down_s[(size_t)e * d + j] : 0.0f;
+    __builtin_amdgcn_sched_barrier(0);
+    // the row's digits: lane takes channels 4 lane + 256 i .. + 3
+    const float* hr = h + (size_t)slot * mi;
+    float hv[DEC_HV][4];
+    float mx = 0.0f;
+    bool nf = false;
+#pragma unroll
+    for (int i = 0; i < DEC_HV; ++i)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int k = 256 * i + 4 * lane + c;
+            hv[i][c] = k < mi ? hr[k] : 0.0f;
+            nf |= !(fabsf(hv[i][c]) <= 3.0e38f);
+            mx = fmaxf(mx, fabsf(hv[i][c]));
+        }
+    mx = wave_fmax(mx);
+    nf = __builtin_amdgcn_ballot_w64(nf) != 0;
+    const float so = mx > 0.0f ? mx / XMAXD : 1.0f;
+    const bool ok = !nf && so >= 1.0e-30f && so <= 1.0e28f;
+    const float r = 1.0f / so;
+    uint32_t* dr = dw + (size_t)slot * 3 * (kpm / 4);
+#pragma unroll
+    for (int i = 0; i < DEC_HV; ++i) {
+        const int k4 = 64 * i + lane;  // word of 4 channels
+        if (4 * k4 >= kpm) break;
+        uint32_t w2 = 0, w1 = 0, w0 = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            int d2 = 0, d1 = 0, d0 = 0;
+            if (ok && 4 * k4 + c < mi) {
+                float xf = rintf(hv[i][c] * r);
+                xf = fminf(fmaxf(xf, -XMAXD), XMAXD);
+                const int X = (int)xf;
+                d0 = (int)(int8_t)(X & 0xFF);
+                const int X1 = (X - d0) >> 8;
+                d1 = (int)(int8_t)(X1 & 0xFF);
+                d2 = (X1 - d1) >> 8;
+            }
+            w2 |= (uint32_t)(d2 & 0xFF) << (8 * c);
+            w1 |= (uint32_t)(d1 & 0xFF) << (8 * c);
+            w0 |= (uint32_t)(d0 & 0xFF) << (8 * c);
+        }
+        dr[k4] = w2;
+        dr[kpm / 4 + k4] = w1;
+        dr[2 * (kpm / 4) + k4] = w0;
+    }
+    wave_sync();
+    const int rr = lane & 15, dg = rr & 3, kq = lane >> 4;
+    const bool aval = rr < 3;
+    const int8_t* arow = reinterpret_cast<const int8_t*>(dr) + (size_t)(dg < 3 ? dg : 0) * kpm + 16 * kq;
+    v4i acc = v4i{0, 0, 0, 0};
+    for (int kb = 0; kb < nkb; kb += DEC_DU) {
+#pragma unroll
+        for (int q0 = 0; q0 < DEC_DU; q0 += 4) {  // A operands four at a time (VGPR budget)
+            v4i av[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                av[q] = (kb + q0 + q < nkb && aval)
+                            ? *reinterpret_cast<const v4i*>(arow + (size_t)(kb + q0 + q) * 64)
+                            : v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[q], bv[q0 + q], acc, 0, 0, 0);
+        }
+        if (kb + DEC_DU < nkb) ldw(kb + DEC_DU);
+    }
+    if (jout) {
+        float v;
+        if (ok) {
+            v = so * ((float)acc[0] * 65536.0f + ((float)acc[1] * 256.0f + (float)acc[2])) * sj;
+        } else {
+            const int8_t* qe = down + (size_t)e * mi * d;
+            v = 0.0f;
+            for (int k = 0; k < mi; ++k) v = __builtin_fmaf(hr[k], (float)qe[(size_t)k * d + j] * sj, v);
+        }
+        vs[slot][lane] = v;
+    }
+    __syncthreads();
+    if (tid < 16 && nb0 * 16 + tid < d) {
+        float a = 0.0f;
+        for (int q = 0; q < topk; ++q) a = a + wsel[q] * vs[q][tid];
+        out[nb0 * 16 + tid] = a;
+    }
+}
+
+// out[t, :] = sum over t's slots in ascending expert id of w * down, from
+// +0.  Workgroup (column block, token): the token's k slots are ranked by
+// expert id into LDS (experts within a token are distinct: top-k of a
+// permutation), then every thread adds its column's k terms in that order.
+constexpr int CMB_K = 256;  // slots a token
+
+__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ dn, const int32_t* __restrict__ sel,
+                                                      const float* __restrict__ w, const int32_t* __restrict__ pos,
+                                                      int topk, int d, float* __restrict__ out) {
+    __shared__ int srow[CMB_K];
+    __shared__ float swt[CMB_K];
+    const int t = blockIdx.y;
+    const int32_t* st = sel + (size_t)t * topk;
+    for (int i = threadIdx.x; i < topk; i += 256) {
+        const int ev = st[i];
+        int r = 0;
+        for (int q = 0; q < topk; ++q) r += st[q] < ev;
+        srow[r] = pos[(size_t)t * topk + i];
+        swt[r] = w[(size_t)t * topk + i];
+    }
+    __syncthreads();
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= d) return;
+    float acc = 0.0f;
+    for (int i = 0; i < topk; ++i) acc = acc + swt[i] * dn[(size_t)srow[i] * d + c];
     out[(size_t)t * d + c] = acc;
 }
 
@@ -639,9 +1259,9 @@ hipError_t launch_moe_route(const float* logits, size_t T, size_t E,
     return hipGetLastError();
 }
 
-// One grouped digit GEMM: decode (tiles of 4 rows) splits K over 4 waves per
-// 16-column block; prefill (tiles of 16 rows) takes 64 columns per 1-wave
-// workgroup.
+// One grouped digit GEMM: a few tokens (tiles of 4 rows) split K over 4
+// waves per 16-column block; batches (tiles of 64 rows) run the
+// expert-stationary kernel, 128 columns a workgroup.
 static hipError_t moe_mm(bool dec, unsigned nt, const int8_t* D, const float* dso, size_t kp,
                          int gather, const MoeWs& ws, const int8_t* wb, size_t np, const float* wsc,
                          size_t n, const float* xf, size_t k, const int8_t* wkn, float* y,
@@ -651,9 +1271,9 @@ static hipError_t moe_mm(bool dec, unsigned nt, const int8_t* D, const float* ds
             D, dso, (int)kp, gather, ws.ptok, wb, (int)np, wsc, (int)n, xf, (int)k, wkn, ws.off,
             ws.cnt, ws.tile_e, ws.tile_r, ws.ntile, y);
     } else {
-        moe_mm_kernel<4, 4, 1><<<dim3(nt, (unsigned)((np / 16 + 3) / 4)), dim3(64), 0, s>>>(
-            D, dso, (int)kp, gather, ws.ptok, wb, (int)np, wsc, (int)n, xf, (int)k, wkn, ws.off,
-            ws.cnt, ws.tile_e, ws.tile_r, ws.ntile, y);
+        const GmmArgs ga{D, dso, (int)kp, (int)np, (int)n, (int)k, wb, wsc, xf, wkn, y};
+        moe_gmm_kernel<<<dim3((unsigned)(8 * ((nt + 7) / 8) * ((np / 16 + 7) / 8))), dim3(256), 0, s>>>(
+            ga, gather, ws.ptok, ws.off, ws.cnt, ws.tile_e, ws.tile_r, ws.ntile);
     }
     return hipGetLastError();
 }
@@ -668,8 +1288,26 @@ hipError_t launch_moe(const MoeBank& b, const float* x, size_t T,
     const size_t tr = moe_tile_rows(T);
     const bool dec = tr == 4;
     const size_t gwp = round_up(b.gw, 16), mip = round_up(b.mi, 16), dp = round_up(b.d, 16);
+    const bool gelu_split = b.act != FRQ_ACT_SILU && b.mi % 16 == 0;  // u at a block edge
+    if (T == 1 && topk <= 16 && (b.act == FRQ_ACT_SILU || gelu_split) && b.kpm <= 256 * DEC_HV &&
+        topk * 3 * b.kpm <= 65536) {
+        // decode in two launches: route + digits + gate/up + act, then the
+        // down digits + down GEMM + combine
+        const bool silu_ = b.act == FRQ_ACT_SILU;
+        const size_t nbh = (b.mi + 15) / 16;
+        const size_t lds1 = ((size_t)((E + 4 * (int)topk + 10 + 3) & ~3)) * 4 + 3 * b.kpd;
+        moe_dec_gua_kernel<<<dim3((unsigned)topk, (unsigned)nbh), dim3(256), lds1, s>>>(
+            x, d, (int)b.kpd, logits, E, (int)topk, norm_topk, pes, b.gate_b, (int)gwp, b.gate_s, gw,
+            b.gate, silu_ ? b.up_b : b.gate_b, (int)(silu_ ? mip : gwp), silu_ ? b.up_s : b.gate_s,
+            silu_ ? mi : gw, silu_ ? b.up : b.gate, silu_ ? 0 : mi, b.act, mi, ws.h, ws, err);
+        hipError_t e1 = hipGetLastError();
+        if (e1 != hipSuccess) return e1;
+        moe_dec_dn_kernel<<<dim3((unsigned)(dp / 16)), dim3((unsigned)(64 * topk)), topk * 3 * b.kpm, s>>>(
+            ws.h, mi, (int)b.kpm, b.down_b, (int)dp, b.down_s, b.down, d, ws.sel, ws.w, (int)topk, out);
+        return hipGetLastError();
+    }
     if (T == 1 && topk <= 16) {
-        // decode: route + digits + gate/up, act digits, down + combine
+        // decode, three launches: route + digits + gate/up, act digits, down + combine
         const int nbg = (int)(gwp / 16), nbu = b.act == FRQ_ACT_SILU ? (int)(mip / 16) : 0;
         const size_t lds1 = ((size_t)((E + 4 * (int)topk + 10 + 3) & ~3)) * 4 + 3 * b.kpd;
         moe_dec_gu_kernel<<<dim3((unsigned)topk, (unsigned)(nbg + nbu)), dim3(256), lds1, s>>>(
@@ -688,7 +1326,7 @@ hipError_t launch_moe(const MoeBank& b, const float* x, size_t T,
     hipError_t e = launch_moe_route(logits, T, b.n_exp, topk, norm_topk, pes, ws.sel, ws.w, err, s);
     if (e != hipSuccess) return e;
     const size_t nwc = (std::min(T, (size_t)TC) + 31) / 32;
-    const size_t dlds = ((size_t)E * nwc * 2 + 2 * E) * sizeof(uint32_t);
+    const size_t dlds = ((size_t)E * nwc * 2 + 3 * E) * sizeof(uint32_t);
     dispatch_kernel<<<dim3(1), dim3(1024), dlds, s>>>(ws.sel, (int)T, (int)topk, E, (int)tr, ws);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     x_digits_kernel<<<dim3((unsigned)T), dim3(256), 0, s>>>(x, d, (int)b.kpd, ws.xd, ws.xso);

@@ -210,7 +210,9 @@ void frq_moe_free(frq_moe_w* m);
 /* Routed expert layer: softmax over the router logits (T,E), stable top-k,
  * renormalise (norm_topk; per_expert_scale non-NULL selects the gemma4
  * weighting p/sum*pes[e]), per-expert W8A32 matmuls with SwiGLU or
- * gelu_tanh gating, weighted combine into out (T,d).  x, logits, out f32. */
+ * gelu_tanh gating, weighted combine into out (T,d).  x, logits, out f32.
+ * topk in [1, min(n_exp, 256)] (FRQ_ERR_ARG otherwise); a NaN logit, or a
+ * row whose max is +-inf, is FRQ_ERR_NAN (the reference's sort panics). */
 int frq_moe(frq_ctx* ctx, const frq_moe_w* m, const float* x, size_t T,
             const float* logits, size_t topk, int norm_topk,
             const float* per_expert_scale, float* out);

@@ -58,7 +58,8 @@ def moe_term_bound(x, sel, w, gate, gs, up, us, down, ds, act):
 
 
 @pytest.mark.parametrize("T,E,k,norm", [(1, 128, 8, True), (512, 128, 8, True), (37, 60, 4, False),
-                                        (5, 8, 8, True), (64, 128, 1, True)])
+                                        (5, 8, 8, True), (64, 128, 1, True), (9, 300, 5, True),
+                                        (6, 200, 12, False)])
 def test_route_parity(ctx, T, E, k, norm):
     rng = np.random.default_rng(T * 31 + E)
     logits = rng.standard_normal((T, E)).astype(np.float32)
@@ -83,6 +84,23 @@ def test_route_nan_is_an_error(ctx):
     assert ei.value.code == fa.FRQ_ERR_NAN
 
 
+@pytest.mark.parametrize("E", [16, 100, 300])
+def test_route_infinite_max_is_an_error(ctx, E):
+    """A +inf logit (inf - inf in its exponent) or a row of -inf makes the
+    reference's probabilities NaN, and its sort's partial_cmp().unwrap()
+    panics (src/qwen3moe.rs:47-51, 129): an error, as for a NaN logit."""
+    logits = np.zeros((3, E), np.float32)
+    logits[1, E - 1] = np.inf
+    with pytest.raises(fa.FrqError) as ei:
+        ctx.moe_route(logits, 2)
+    assert ei.value.code == fa.FRQ_ERR_NAN
+    logits = np.zeros((2, E), np.float32)
+    logits[0, :] = -np.inf
+    with pytest.raises(fa.FrqError) as ei:
+        ctx.moe_route(logits, 2)
+    assert ei.value.code == fa.FRQ_ERR_NAN
+
+
 @pytest.mark.parametrize("act", [0, 1])
 def test_expert_mm_bit_exact(ctx, act):
     E, d, mi = 4, 256, 96
@@ -102,7 +120,9 @@ def test_expert_mm_bit_exact(ctx, act):
                                             (7, 8, 128, 32, 8, 1), (1, 128, 2048, 768, 8, 0),
                                             (64, 128, 2048, 768, 8, 0), (1, 8, 128, 32, 8, 1),
                                             (1, 60, 256, 64, 4, 0), (1, 32, 320, 96, 16, 1),
-                                            (512, 128, 2048, 768, 8, 0)])
+                                            (512, 128, 2048, 768, 8, 0), (1, 16, 256, 40, 4, 1),
+                                            (1, 300, 256, 64, 6, 0), (300, 8, 256, 64, 4, 0),
+                                            (90, 12, 320, 48, 3, 1)])
 def test_moe_layer_parity(ctx, T, E, d, mi, k, act):
     gate, gs, up, us, down, ds = synth.moe_layer(E, d, mi, synth.seed(3) + T + act, act)
     bank = ctx.upload_moe_i8(gate, gs, up, us, down, ds, act)
@@ -122,7 +142,7 @@ def test_moe_layer_parity(ctx, T, E, d, mi, k, act):
 
 @pytest.mark.parametrize("act", [0, 1])
 def test_moe_decode_matches_batched_row(ctx, act):
-    """T == 1 runs the three-launch decode path; the same token inside a
+    """T == 1 runs the two-launch decode path; the same token inside a
     batch runs the general pipeline.  Both compute the same digit GEMMs and
     the same ascending-expert combine, so the row is bit-identical."""
     E, d, mi, k = 32, 512, 128, 8
@@ -170,5 +190,8 @@ def test_moe_decode_nan_logits_is_an_error(ctx):
     x = np.ones((1, d), np.float32)
     logits = np.zeros((1, E), np.float32)
     logits[0, 2] = np.nan
+    with pytest.raises(Exception):
+        bank.forward(x, logits, k, True)
+    logits[0, 2] = np.inf
     with pytest.raises(Exception):
         bank.forward(x, logits, k, True)
