@@ -70,7 +70,7 @@ size_t ntile_max(size_t T, size_t k, size_t E, size_t tr) {
     return P / tr + (E < P ? E : P) + 1;
 }
 
-size_t moe_tile_rows(size_t T) { return T <= 4 ? 4 : 64; }
+size_t moe_tile_rows(size_t T) { return T <= 4 ? 4 : 32; }
 
 MoeWs moe_view(void* base, const MoeBank& b, size_t T, size_t k) {
     const size_t P = T * k, E = b.n_exp, nt = ntile_max(T, k, E, moe_tile_rows(T));
@@ -635,11 +635,11 @@ __global__ __launch_bounds__(64 * KS) void moe_mm_kernel(
 }
 
 // ---- expert-stationary grouped digit GEMM (batched rows) -------------------
-// Workgroup = (tile of up to 64 permuted rows of one expert, 128 columns):
+// Workgroup = (tile of up to 32 permuted rows of one expert, 128 columns):
 // the expert's 128-column weight block streams from HBM once per tile, each
 // of the 4 waves taking 32 columns (two 16-column blocks); the tile's digit
-// rows pass through LDS one k-block at a time (double-buffered), and every
-// A operand read from LDS feeds two MFMAs.  The A items and B operands of
+// rows pass through LDS GM_KC k-blocks at a time (double-buffered), and
+// every A operand read from LDS feeds two MFMAs.  The A items and B operands of
 // k-block kb sit in register slot kb % GM_BP from their load until use, so
 // both stream GM_BP k-blocks ahead (the wait counter is in order: A, needed
 // first, must not trail B).  Every load is unconditional, from a clamped
@@ -648,10 +648,13 @@ __global__ __launch_bounds__(64 * KS) void moe_mm_kernel(
 // of the k-block (LDS keeps the 48 lanes d < 3; d = 3 reads a copy of
 // d = 2, whose product row acc[3] is not used); C lane l holds row
 // 4 g + l / 16, digit c in acc[c], column l % 16.  Output as
-// moe_mm_kernel's.  NGT = row groups the tile's rows need (4, 8 or 16).
-constexpr int GM_TR = 64;  // rows a tile
-constexpr int GM_BP = 6;   // k-blocks of A and B in flight a wave
-constexpr int GM_AS = (GM_TR / 4) * 48 + 256;  // A slots a buffer (+ one spare a thread)
+// moe_mm_kernel's.  NGT = row groups the tile's rows need (4 or 8); 32-row
+// tiles keep a wave within 256 registers, two workgroups a CU.
+constexpr int GM_TR = 32;  // rows a tile
+constexpr int GM_BP = 4;   // k-blocks of A and B in flight a wave
+constexpr int GM_KC = 1;   // k-blocks a barrier (GM_BP a multiple; 2 needs 260 registers: one wave a SIMD, slower)
+constexpr int GM_NS = (GM_TR / 4) * 48;        // A slots a k-block
+constexpr int GM_AS = GM_KC * GM_NS + 256;     // A slots a buffer (+ one spare a thread)
 
 struct GmmArgs {
     const int8_t* D;
@@ -678,7 +681,7 @@ __device__ __forceinline__ void gmm_body(const GmmArgs& A, v4i (*As)[GM_AS], con
         const int it = tid + 256 * u, kq = it & 3, rd = it >> 2, i = rd / 3, dg = rd - 3 * i;
         const bool on = it < NIT;
         asrc[u] = A.D + ((size_t)srcs[on ? min(i, rows - 1) : 0] * 3 + (on ? dg : 0)) * A.Kp + 16 * kq;
-        adst[u] = on ? (i >> 2) * 48 + kq * 12 + (i & 3) * 3 + dg : (GM_TR / 4) * 48 + tid;
+        adst[u] = on ? (i >> 2) * 48 + kq * 12 + (i & 3) * 3 + dg : -1;
     }
     const int cb0 = cg * 8 + 2 * wave, ncb = A.Np / 16;  // this wave's column blocks
     const int8_t* wb0 = A.Wb + (size_t)e * A.Np * A.Kp + (size_t)min(cb0, ncb - 1) * 1024 + lane * 16;
@@ -697,40 +700,51 @@ __device__ __forceinline__ void gmm_body(const GmmArgs& A, v4i (*As)[GM_AS], con
         bq[sl][0] = kb < nkb ? b0 : z;
         bq[sl][1] = kb < nkb ? b1 : z;
     };
-    auto sta = [&](int sl, int buf) {
+    // k-block q of a buffer's GM_KC; items past the tile's go to a spare slot
+    auto sta = [&](int sl, int buf, int q) {
 #pragma unroll
-        for (int u = 0; u < UA; ++u) As[buf][adst[u]] = ar[sl][u];
+        for (int u = 0; u < UA; ++u) As[buf][adst[u] >= 0 ? q * GM_NS + adst[u] : GM_KC * GM_NS + tid] = ar[sl][u];
     };
     v4i acc[NGT][2];
 #pragma unroll
     for (int g = 0; g < NGT; ++g) acc[g][0] = acc[g][1] = v4i{0, 0, 0, 0};
 #pragma unroll
     for (int sl = 0; sl < GM_BP; ++sl) ld(sl, sl);
-    sta(0, 0);
+#pragma unroll
+    for (int q = 0; q < GM_KC; ++q) sta(q, 0, q);
     const int rr = lane & 15, tl = rr >> 2, dgl = rr & 3, kql = lane >> 4;
     const int aidx = kql * 12 + tl * 3 + (dgl < 3 ? dgl : 2);
+    // chunks of GM_KC k-blocks; chunk ch's A in As[ch & 1]
     for (int kb0 = 0; kb0 < nkb; kb0 += GM_BP) {
 #pragma unroll
-        for (int sl = 0; sl < GM_BP; ++sl) {
-            const int kb = kb0 + sl;
-            __syncthreads();  // As[kb & 1] written by every wave, As[~kb & 1] read
-            const v4i* ab = As[kb & 1];
+        for (int c = 0; c < GM_BP / GM_KC; ++c) {
+            const int kbc = kb0 + c * GM_KC, ch = kbc / GM_KC;
+            __syncthreads();  // As[ch & 1] written by every wave, As[~ch & 1] read
+            const v4i* ab = As[ch & 1];
             // every A read issued before the MFMAs (one LDS latency a
-            // k-block; the scheduler would pair reads with their MFMAs)
-            v4i av[NGT];
+            // chunk; the scheduler would pair reads with their MFMAs)
+            v4i av[GM_KC][NGT];
 #pragma unroll
-            for (int g = 0; g < NGT; ++g) av[g] = ab[g * 48 + aidx];
+            for (int q = 0; q < GM_KC; ++q)
+#pragma unroll
+                for (int g = 0; g < NGT; ++g) av[q][g] = ab[q * GM_NS + g * 48 + aidx];
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int g = 0; g < NGT; ++g) {
-                acc[g][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[g], bq[sl][0], acc[g][0], 0, 0, 0);
-                acc[g][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[g], bq[sl][1], acc[g][1], 0, 0, 0);
+            for (int q = 0; q < GM_KC; ++q)
+#pragma unroll
+                for (int g = 0; g < NGT; ++g) {
+                    const int sl = c * GM_KC + q;
+                    acc[g][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[q][g], bq[sl][0], acc[g][0], 0, 0, 0);
+                    acc[g][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[q][g], bq[sl][1], acc[g][1], 0, 0, 0);
+                }
+            // the next chunk's A into the other buffer; this chunk's slots are
+            // then spent (their A stored a chunk ago, their B used now): reload
+            if (kbc + GM_KC < nkb) {
+#pragma unroll
+                for (int q = 0; q < GM_KC; ++q) sta(((c + 1) * GM_KC + q) % GM_BP, (ch + 1) & 1, q);
             }
-            // k-block kb + 1's A into the other buffer; slot sl is then spent
-            // (its A stored an iteration ago, its B used now): reload it
-            const int sn = (sl + 1) % GM_BP;
-            if (kb + 1 < nkb) sta(sn, (kb + 1) & 1);
-            ld(sl, kb + GM_BP);
+#pragma unroll
+            for (int q = 0; q < GM_KC; ++q) ld(c * GM_KC + q, kbc + q + GM_BP);
         }
     }
     // y = s * (C2 * 2^16 + C1 * 2^8 + C0) * wsc[e, j]; rows whose digits do not
@@ -791,8 +805,7 @@ __global__ __launch_bounds__(256) void moe_gmm_kernel(GmmArgs A, int gather, con
     }
     __syncthreads();
     if (rows <= 16) gmm_body<4>(A, As, srcs, e, rows, pbase, cg);
-    else if (rows <= 32) gmm_body<8>(A, As, srcs, e, rows, pbase, cg);
-    else gmm_body<16>(A, As, srcs, e, rows, pbase, cg);
+    else gmm_body<8>(A, As, srcs, e, rows, pbase, cg);
 }
 
 // ---- decode (T == 1): three launches ---------------------------------------
@@ -1260,7 +1273,7 @@ hipError_t launch_moe_route(const float* logits, size_t T, size_t E,
 }
 
 // One grouped digit GEMM: a few tokens (tiles of 4 rows) split K over 4
-// waves per 16-column block; batches (tiles of 64 rows) run the
+// waves per 16-column block; batches (tiles of 32 rows) run the
 // expert-stationary kernel, 128 columns a workgroup.
 static hipError_t moe_mm(bool dec, unsigned nt, const int8_t* D, const float* dso, size_t kp,
                          int gather, const MoeWs& ws, const int8_t* wb, size_t np, const float* wsc,
