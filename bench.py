@@ -119,9 +119,10 @@ def main():
                          "rocprofv3's kernel trace does not survive graph capture on this image)")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="only the counter-collection workload (run under rocprofv3 --pmc)")
-    ap.add_argument("--pmc-what", default="layer", choices=["layer", "int4", "m128"],
+    ap.add_argument("--pmc-what", default="layer", choices=["layer", "int4", "m128", "moe"],
                     help="counter workload: the configs[4] layer's four decode linears (default), the int4 "
-                         "M=1 GEMV at the Gemma-2 shapes, or the int8 linear at M=128")
+                         "M=1 GEMV at the Gemma-2 shapes, the int8 linear at M=128, or configs[3]'s MoE "
+                         "layer at T=1 and T=512")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path "
@@ -193,6 +194,22 @@ def main():
                 log(f"pmc: 9 int4 M=1 launches at K={k} N={n}, {int4_bytes(1, k, n)} algorithmic bytes each")
                 for w in reps:
                     w.free()
+            return
+        if args.pmc_what == "moe":
+            # the Qwen3-MoE routed layer at T=1 and T=512, 9 calls each
+            E, d, mi, topk = 128, 2048, 768, 8
+            gate, gs, up, us_, down, ds = synth.moe_layer(E, d, mi, synth.seed(3))
+            bank = ctx.upload_moe_i8(gate, gs, up, us_, down, ds)
+            for T in (1, 512):
+                rng = np.random.default_rng(synth.seed(3, T))
+                x = hip.DeviceArray.from_numpy(rng.standard_normal((T, d), dtype=np.float32))
+                lg = hip.DeviceArray.from_numpy(rng.standard_normal((T, E), dtype=np.float32))
+                o = hip.DeviceArray((T, d), np.float32)
+                for i in range(9):
+                    bank.forward_dev(x.ptr, T, lg.ptr, topk, True, None, o.ptr)
+                ctx.sync()
+                log(f"pmc: 9 MoE layer calls at T={T} (E={E}, d={d}, mi={mi}, k={topk})")
+            bank.free()
             return
         if args.pmc_what == "m128":
             for (k, n) in [(896, 151936), (4096, 14336)]:
