@@ -100,7 +100,9 @@ MoeWs moe_view(void* base, const MoeBank& b, size_t T, size_t k) {
 // The gates and the softmax use the restated glibc expf / fdlibm tanhf
 // (libm_f32.h), which Rust's f32::exp / f32::tanh reach on the reference's
 // host, so route weights and gated activations are the reference's bits.
-__device__ __forceinline__ float silu(float x) { return x / (1.0f + libm::frq_expf(-x)); }
+// (frq_expf_sel: frq_expf's value for every input, with selects for its
+// special cases instead of branches)
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + libm::frq_expf_sel(-x)); }
 
 __device__ __forceinline__ float gelu_tanh(float x) {
     const float c = sqrtf(2.0f / 3.14159274101257324f);
@@ -476,6 +478,20 @@ __device__ __forceinline__ void row_digits_r(F val, int K, int Kp, int8_t* __res
 
 constexpr int RD_NV = 8;  // register-held rows: Kp <= 2048
 
+// row_digits_r with the fewest registers that hold the row (Kp <= 2048)
+template <typename F>
+__device__ __forceinline__ void row_digits_nv(F val, int K, int Kp, int8_t* __restrict__ D,
+                                              float* __restrict__ so_out, float* red) {
+    switch ((Kp + 255) / 256) {
+        case 1: row_digits_r<1>(val, K, Kp, D, so_out, red); break;
+        case 2: row_digits_r<2>(val, K, Kp, D, so_out, red); break;
+        case 3: row_digits_r<3>(val, K, Kp, D, so_out, red); break;
+        case 4: row_digits_r<4>(val, K, Kp, D, so_out, red); break;
+        case 5: case 6: row_digits_r<6>(val, K, Kp, D, so_out, red); break;
+        default: row_digits_r<8>(val, K, Kp, D, so_out, red); break;
+    }
+}
+
 // One workgroup per token row of x.
 __global__ __launch_bounds__(256) void x_digits_kernel(const float* __restrict__ x, int K, int Kp,
                                                        int8_t* __restrict__ D, float* __restrict__ so) {
@@ -483,7 +499,7 @@ __global__ __launch_bounds__(256) void x_digits_kernel(const float* __restrict__
     const int r = blockIdx.x;
     const float* xr = x + (size_t)r * K;
     if (Kp <= 256 * RD_NV)
-        row_digits_r<RD_NV>([&](int k) { return xr[k]; }, K, Kp, D + (size_t)r * 3 * Kp, so + r, red);
+        row_digits_nv([&](int k) { return xr[k]; }, K, Kp, D + (size_t)r * 3 * Kp, so + r, red);
     else
         row_digits(xr, K, Kp, D + (size_t)r * 3 * Kp, so + r, red);
 }
@@ -501,7 +517,7 @@ __global__ __launch_bounds__(256) void act_digits_kernel(
     const float* gr = g + (size_t)r * gw;
     float* hr = h + (size_t)r * mi;
     if (kpm <= 256 * RD_NV) {
-        row_digits_r<RD_NV>(
+        row_digits_nv(
             [&](int c) {
                 const float hv = act == FRQ_ACT_SILU ? silu(gr[c]) * u[(size_t)r * mi + c]
                                                      : gelu_tanh(gr[c]) * gr[c + mi];
