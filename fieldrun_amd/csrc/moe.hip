@@ -665,9 +665,10 @@ __global__ __launch_bounds__(64 * KS) void moe_mm_kernel(
 // d = 2, whose product row acc[3] is not used); C lane l holds row
 // 4 g + l / 16, digit c in acc[c], column l % 16.  Output as
 // moe_mm_kernel's.  NGT = row groups the tile's rows need (4 or 8); 32-row
-// tiles keep a wave within 256 registers, two workgroups a CU.
+// tiles and a ring 3 deep fit a wave in 160 registers, three workgroups a
+// CU (the MFMA issue waits on latency: occupancy is what hides it).
 constexpr int GM_TR = 32;  // rows a tile
-constexpr int GM_BP = 4;   // k-blocks of A and B in flight a wave
+constexpr int GM_BP = 3;   // k-blocks of A and B in flight a wave
 constexpr int GM_KC = 1;   // k-blocks a barrier (GM_BP a multiple; 2 needs 260 registers: one wave a SIMD, slower)
 constexpr int GM_NS = (GM_TR / 4) * 48;        // A slots a k-block
 constexpr int GM_AS = GM_KC * GM_NS + 256;     // A slots a buffer (+ one spare a thread)
@@ -796,7 +797,7 @@ __device__ __forceinline__ void gmm_body(const GmmArgs& A, v4i (*As)[GM_AS], con
     }
 }
 
-__global__ __launch_bounds__(256) void moe_gmm_kernel(GmmArgs A, int gather, const int32_t* __restrict__ ptok,
+__global__ __launch_bounds__(256, 3) void moe_gmm_kernel(GmmArgs A, int gather, const int32_t* __restrict__ ptok,
                                                       const int32_t* __restrict__ off,
                                                       const int32_t* __restrict__ cnt,
                                                       const int32_t* __restrict__ tile_e,
