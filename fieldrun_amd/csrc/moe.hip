@@ -826,6 +826,8 @@ __global__ __launch_bounds__(256, 3) void moe_gmm_kernel(GmmArgs A, int gather, 
 }
 
 // ---- decode (T == 1): three launches ---------------------------------------
+// (the form for shapes the two-launch decode below does not take: gelu with
+// mi % 16 != 0, mi > 1024, k > 16)
 // K1: every workgroup (slot s of the k picks in ascending expert id, 16
 // columns of gate or up) routes the token in its wave 0 and builds the
 // token's digit row in LDS itself (a few KB from L2, no launch in between),
