@@ -797,7 +797,10 @@ __device__ __forceinline__ void gmm_body(const GmmArgs& A, v4i (*As)[GM_AS], con
     }
 }
 
-__global__ __launch_bounds__(256, 3) void moe_gmm_kernel(GmmArgs A, int gather, const int32_t* __restrict__ ptok,
+// A1 (ncg1 = 0: none) is a second linear over the same rows (up beside
+// gate): column groups ncg0 .. ncg0 + ncg1 - 1 of a tile are its.
+__global__ __launch_bounds__(256, 3) void moe_gmm_kernel(GmmArgs A0, GmmArgs A1, int ncg1, int gather,
+                                                         const int32_t* __restrict__ ptok,
                                                       const int32_t* __restrict__ off,
                                                       const int32_t* __restrict__ cnt,
                                                       const int32_t* __restrict__ tile_e,
@@ -808,9 +811,12 @@ __global__ __launch_bounds__(256, 3) void moe_gmm_kernel(GmmArgs A, int gather, 
     // XCD-aware order: workgroup id goes to XCD id % 8, and XCD x runs
     // tiles x, x + 8, ... with all ncg column groups of a tile in a row, so
     // the tile's digit rows are fetched into that XCD's L2 once
-    const int ncg = (A.Np / 16 + 7) / 8;
+    const int ncg0 = (A0.Np / 16 + 7) / 8, ncg = ncg0 + ncg1;
     const int xcd = blockIdx.x & 7, j = blockIdx.x >> 3;
-    const int tix = xcd + 8 * (j / ncg), cg = j % ncg;
+    const int tix = xcd + 8 * (j / ncg), cgt = j % ncg;
+    const bool second = cgt >= ncg0;  // uniform
+    const GmmArgs& A = second ? A1 : A0;
+    const int cg = second ? cgt - ncg0 : cgt;
     if (tix >= ntile[0]) return;  // uniform
     const int e = tile_e[tix], r0 = tile_r[tix];
     const int rows = min(GM_TR, cnt[e] - r0);
@@ -1305,8 +1311,16 @@ static hipError_t moe_mm(bool dec, unsigned nt, const int8_t* D, const float* ds
     } else {
         const GmmArgs ga{D, dso, (int)kp, (int)np, (int)n, (int)k, wb, wsc, xf, wkn, y};
         moe_gmm_kernel<<<dim3((unsigned)(8 * ((nt + 7) / 8) * ((np / 16 + 7) / 8))), dim3(256), 0, s>>>(
-            ga, gather, ws.ptok, ws.off, ws.cnt, ws.tile_e, ws.tile_r, ws.ntile);
+            ga, ga, 0, gather, ws.ptok, ws.off, ws.cnt, ws.tile_e, ws.tile_r, ws.ntile);
     }
+    return hipGetLastError();
+}
+
+// The batched gate and up GEMMs in one launch (the same digit rows).
+static hipError_t moe_gmm_pair(unsigned nt, const GmmArgs& g0, const GmmArgs& g1, const MoeWs& ws, hipStream_t s) {
+    const int ncg0 = (g0.Np / 16 + 7) / 8, ncg1 = (g1.Np / 16 + 7) / 8;
+    moe_gmm_kernel<<<dim3((unsigned)(8 * ((nt + 7) / 8) * (ncg0 + ncg1))), dim3(256), 0, s>>>(
+        g0, g1, ncg1, 1, ws.ptok, ws.off, ws.cnt, ws.tile_e, ws.tile_r, ws.ntile);
     return hipGetLastError();
 }
 
@@ -1364,13 +1378,19 @@ hipError_t launch_moe(const MoeBank& b, const float* x, size_t T,
     x_digits_kernel<<<dim3((unsigned)T), dim3(256), 0, s>>>(x, d, (int)b.kpd, ws.xd, ws.xso);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const unsigned nt = (unsigned)ntile_max(T, topk, b.n_exp, tr);
-    if ((e = moe_mm(dec, nt, ws.xd, ws.xso, b.kpd, 1, ws, b.gate_b, gwp, b.gate_s, b.gw, x, b.d,
-                    b.gate, ws.g, s)) != hipSuccess)
-        return e;
-    if (b.act == FRQ_ACT_SILU &&
-        (e = moe_mm(dec, nt, ws.xd, ws.xso, b.kpd, 1, ws, b.up_b, mip, b.up_s, b.mi, x, b.d, b.up,
-                    ws.u, s)) != hipSuccess)
-        return e;
+    if (!dec && b.act == FRQ_ACT_SILU) {
+        const GmmArgs gg{ws.xd, ws.xso, (int)b.kpd, (int)gwp, (int)b.gw, (int)b.d, b.gate_b, b.gate_s, x, b.gate, ws.g};
+        const GmmArgs gu{ws.xd, ws.xso, (int)b.kpd, (int)mip, (int)b.mi, (int)b.d, b.up_b, b.up_s, x, b.up, ws.u};
+        if ((e = moe_gmm_pair(nt, gg, gu, ws, s)) != hipSuccess) return e;
+    } else {
+        if ((e = moe_mm(dec, nt, ws.xd, ws.xso, b.kpd, 1, ws, b.gate_b, gwp, b.gate_s, b.gw, x, b.d,
+                        b.gate, ws.g, s)) != hipSuccess)
+            return e;
+        if (b.act == FRQ_ACT_SILU &&
+            (e = moe_mm(dec, nt, ws.xd, ws.xso, b.kpd, 1, ws, b.up_b, mip, b.up_s, b.mi, x, b.d, b.up,
+                        ws.u, s)) != hipSuccess)
+            return e;
+    }
     act_digits_kernel<<<dim3((unsigned)(T * topk)), dim3(256), 0, s>>>(
         ws.g, ws.u, b.act, mi, gw, (int)b.kpm, ws.off, E, ws.h, ws.hd, ws.hso);
     if ((e = hipGetLastError()) != hipSuccess) return e;
