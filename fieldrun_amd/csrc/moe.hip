@@ -1271,6 +1271,21 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
         swt[r] = w[(size_t)t * topk + i];
     }
     __syncthreads();
+    if ((d & 3) == 0) {  // four columns a thread, each in the same order
+        const int c4 = blockIdx.x * 256 + threadIdx.x;
+        if (4 * c4 >= d) return;
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int i = 0; i < topk; ++i) {
+            const float4 v = reinterpret_cast<const float4*>(dn + (size_t)srow[i] * d)[c4];
+            const float wi = swt[i];
+            acc.x = acc.x + wi * v.x;
+            acc.y = acc.y + wi * v.y;
+            acc.z = acc.z + wi * v.z;
+            acc.w = acc.w + wi * v.w;
+        }
+        reinterpret_cast<float4*>(out + (size_t)t * d)[c4] = acc;
+        return;
+    }
     const int c = blockIdx.x * 256 + threadIdx.x;
     if (c >= d) return;
     float acc = 0.0f;
@@ -1397,7 +1412,7 @@ hipError_t launch_moe(const MoeBank& b, const float* x, size_t T,
     if ((e = moe_mm(dec, nt, ws.hd, ws.hso, b.kpm, 0, ws, b.down_b, dp, b.down_s, b.d, ws.h, b.mi,
                     b.down, ws.dn, s)) != hipSuccess)
         return e;
-    combine_kernel<<<dim3((unsigned)((d + 255) / 256), (unsigned)T), dim3(256), 0, s>>>(
+    combine_kernel<<<dim3((unsigned)(((d % 4 ? d : d / 4) + 255) / 256), (unsigned)T), dim3(256), 0, s>>>(
         ws.dn, ws.sel, ws.w, ws.pos, (int)topk, d, out);
     return hipGetLastError();
 }
