@@ -75,7 +75,7 @@ def q4a_bytes(m, k, n, g=32):
 
 
 def moe_bytes(T, E, d, mi, active):
-    # SURVEY's MoE formula: active experts' int8 gate/up/down + f32 scales, x, out, logits
+    # the MoE layer's bytes: active experts' int8 gate/up/down + f32 scales, x, out, logits
     return active * (3 * d * mi + 4 * (mi + mi + d)) + 4 * T * d + 4 * T * d + 4 * T * E
 
 

@@ -1,4 +1,4 @@
-"""Seeded synthetic workloads of the BASELINE configs (host-side numpy).
+"""Seeded synthetic workloads of the benchmark configs (host-side numpy).
 
 Seeds are 0xF1E1D000 + config_index*1000 + replica.  Generated once on the
 host; the same arrays feed the HIP path and the CPU oracle.
@@ -70,7 +70,7 @@ def moe_layer(E: int, d: int, mi: int, s: int, act: int = 0, std: float = 0.02):
     return gate, gs, up, us, down, ds
 
 
-# ---- synthetic random-init bundles in the reference format (the BASELINE
+# ---- synthetic random-init bundles in the reference format (the benchmark
 # configs; array names and layouts as src/convert.rs writes them) ----------
 
 def gpt2_prompt(n: int, vocab: int, s: int) -> np.ndarray:

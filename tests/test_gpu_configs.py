@@ -1,4 +1,4 @@
-"""The BASELINE configs end to end at their full size and length on the
+"""The benchmark configs end to end at their full size and length on the
 device, against the oracle's golden fixtures (tests/golden, written by
 make_config_fixtures.py with the C restatement of Gemma::generate /
 Rope::generate on the same seeded bundles and prompts): the greedy tokens,
