@@ -1058,6 +1058,17 @@ __global__ __launch_bounds__(256) void moe_dec_gua_kernel(
             bb[q] = in ? *reinterpret_cast<const v4i*>(wb + (size_t)(kb + q) * ksb) : v4i{0, 0, 0, 0};
         }
     };
+    // this thread's x channels for the digit row first: vector loads retire
+    // in issue order, so the digits then wait on these, not on the weights
+    constexpr int XR = 8;  // registers: kpd <= 2048
+    const bool xreg = kpd <= 256 * XR;
+    float xk[XR];
+#pragma unroll
+    for (int i = 0; i < XR; ++i) {
+        const int k = tid + 256 * i;
+        xk[i] = (xreg && k < d) ? x[k] : 0.0f;
+    }
+    __builtin_amdgcn_sched_barrier(0);
     ldw(kb0);
     const int j = cbk * 16 + lane;
     const bool jout = wave == 0 && lane < 16 && j < mi;
@@ -1070,10 +1081,10 @@ __global__ __launch_bounds__(256) void moe_dec_gua_kernel(
     const float sx = mxx > 0.0f ? mxx / XMAXD : 1.0f;
     const bool ok = !xnf && sx >= 1.0e-30f && sx <= 1.0e28f;
     const float rx = 1.0f / sx;
-    for (int k = tid; k < kpd; k += 256) {
+    auto digit = [&](int k, float xv) {
         int d2 = 0, d1 = 0, d0 = 0;
         if (ok && k < d) {
-            float xf = rintf(x[k] * rx);
+            float xf = rintf(xv * rx);
             xf = fminf(fmaxf(xf, -XMAXD), XMAXD);
             const int X = (int)xf;
             d0 = (int)(int8_t)(X & 0xFF);
@@ -1084,6 +1095,13 @@ __global__ __launch_bounds__(256) void moe_dec_gua_kernel(
         Dl[k] = (int8_t)d2;
         Dl[kpd + k] = (int8_t)d1;
         Dl[2 * kpd + k] = (int8_t)d0;
+    };
+    if (xreg) {
+#pragma unroll
+        for (int i = 0; i < XR; ++i)
+            if (tid + 256 * i < kpd) digit(tid + 256 * i, xk[i]);
+    } else {
+        for (int k = tid; k < kpd; k += 256) digit(k, k < d ? x[k] : 0.0f);
     }
     __syncthreads();
     const int8_t* arow = Dl + (dg < 3 ? dg : 0) * kpd + 16 * kq;
@@ -1150,6 +1168,19 @@ __global__ __launch_bounds__(1024) void moe_dec_dn_kernel(
     const int tid = threadIdx.x, lane = tid & 63;
     const int slot = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nb0 = blockIdx.x;
+    // the row's values first (lane takes channels 4 lane + 256 i .. + 3):
+    // vector loads retire in issue order, so the digits then wait on these
+    // and not on the weight stream issued after them
+    const float* hr = h + (size_t)slot * mi;
+    float hv[DEC_HV][4];
+#pragma unroll
+    for (int i = 0; i < DEC_HV; ++i)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int k = 256 * i + 4 * lane + c;
+            hv[i][c] = k < mi ? hr[k] : 0.0f;
+        }
+    __builtin_amdgcn_sched_barrier(0);
     const int e = sel[slot];
     const int nkb = kpm / 64;
     const int8_t* wb = down_b + (size_t)e * dp * kpm + (size_t)nb0 * 1024 + lane * 16;
@@ -1166,17 +1197,13 @@ __global__ __launch_bounds__(1024) void moe_dec_dn_kernel(
     const bool jout = lane < 16 && j < d;
     const float sj = jout ? down_s[(size_t)e * d + j] : 0.0f;
     __builtin_amdgcn_sched_barrier(0);
-    // the row's digits: lane takes channels 4 lane + 256 i .. + 3
-    const float* hr = h + (size_t)slot * mi;
-    float hv[DEC_HV][4];
+    // the row's digits
     float mx = 0.0f;
     bool nf = false;
 #pragma unroll
     for (int i = 0; i < DEC_HV; ++i)
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            const int k = 256 * i + 4 * lane + c;
-            hv[i][c] = k < mi ? hr[k] : 0.0f;
             nf |= !(fabsf(hv[i][c]) <= 3.0e38f);
             mx = fmaxf(mx, fabsf(hv[i][c]));
         }
