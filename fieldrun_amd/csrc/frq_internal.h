@@ -107,6 +107,30 @@ __device__ __forceinline__ float h2f(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);
 }
 
+// The summation order of one element of the reference's a.dot (ndarray
+// 0.16.1 -> matrixmultiply 0.3.10 sgemm, Cargo.lock:1108, 1207): k is split
+// into blocks of MM_KC = 256 (S_KC) in order; in each block the FMA
+// micro-kernel chains the products from +0, k ascending; the first block's
+// result is stored, each later one added (C = C + AB).  An FMA chain from +0
+// never ends at -0, so C = +0 + AB_0 is AB_0 and one running sum from +0
+// covers both steps.
+constexpr int MM_KC = 256;
+
+// That order over the indices [j0, n) of a product whose terms outside are
+// exact zeros (masked keys with p = 0, padding): the block edges stay at
+// multiples of MM_KC from 0, and chain(s, e) returns the FMA chain from +0
+// over [s, e) (within one block).
+template <typename F>
+__device__ __forceinline__ float mm_blocks(int j0, int n, F chain) {
+    float c = 0.0f;
+    for (int s = j0; s < n;) {
+        const int e = min(n, (s / MM_KC + 1) * MM_KC);
+        c = c + chain(s, e);
+        s = e;
+    }
+    return c;
+}
+
 // acc + p[0] + p[1] + ... + p[n-1] in index order, in the calling lane,
 // over LDS (p 16-byte aligned): loads run one 32-value batch ahead of the
 // adds (unconditional, the index clamped to the last batch) so the chain

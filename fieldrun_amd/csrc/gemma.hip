@@ -20,10 +20,11 @@
 // the reference's bit for bit: the RMSNorm sum of squares is the fold from
 // -0.0 in index order; the RoPE cos / sin are the host libm's (the table is
 // computed on the host, where the reference computes them); scores and
-// values are sequential FMA chains; the soft-cap and GELU use the libm
+// values follow a.dot's order (MM_KC-key blocks, each an FMA chain from +0,
+// added in order; a head's scores are one block); the soft-cap and GELU use the libm
 // tanhf restatement, the softmax the expf one and a key-order sum; the
 // linears take their reference-order kernels (int4: i4_dot_avx2's order at
-// M = 1, dequantise + sequential GEMM above; int8: the bit-exact M <= 16
+// M = 1, dequantise + a.dot's blocked order above; int8: the bit-exact M <= 16
 // path, in chunks).
 #include "frq_internal.h"
 #include "libm_f32.h"
@@ -505,42 +506,47 @@ __global__ __launch_bounds__(GT) void gm_attn_kernel(const float* __restrict__ q
     __syncthreads();
     constexpr int B = 16;
     for (int c = threadIdx.x; c < hd; c += GT) {
-        float acc = 0.0f;
         const size_t col = (size_t)kv * hd + c;
-        const int n = nk - j0, nb = n / B;
-        float v0[B], v1[B];
-        auto ld = [&](float (&v)[B], int k) {
+        // one a.dot block of keys [s, e): the chain from +0, its value loads
+        // a 16-key batch ahead
+        auto chain = [&](int s, int e) {
+            float acc = 0.0f;
+            const int nb = (e - s) / B;
+            float v0[B], v1[B];
+            auto ld = [&](float (&v)[B], int k) {
 #pragma unroll
-            for (int u = 0; u < B; ++u) {
-                const size_t j = (size_t)(j0 + k * B + u);
-                if constexpr (!KV8) v[u] = vc[j * kvd + col];
-                else v[u] = (float)vq[j * kvd + col] * sv[j];
-            }
-        };
-        auto fma_b = [&](const float (&v)[B], int k) {
+                for (int u = 0; u < B; ++u) {
+                    const size_t j = (size_t)(s + k * B + u);
+                    if constexpr (!KV8) v[u] = vc[j * kvd + col];
+                    else v[u] = (float)vq[j * kvd + col] * sv[j];
+                }
+            };
+            auto fma_b = [&](const float (&v)[B], int k) {
 #pragma unroll
-            for (int u = 0; u < B; ++u) acc = __builtin_fmaf(p[j0 + k * B + u], v[u], acc);
-        };
-        if (nb > 0) {  // both batches of a trip consumed unconditionally, loads pinned a batch ahead
-            ld(v0, 0);
-            ld(v1, min(1, nb - 1));
-            __builtin_amdgcn_sched_barrier(0);
-            int k = 0;
-            for (; k + 2 <= nb; k += 2) {
-                fma_b(v0, k);
-                ld(v0, min(k + 2, nb - 1));
+                for (int u = 0; u < B; ++u) acc = __builtin_fmaf(p[s + k * B + u], v[u], acc);
+            };
+            if (nb > 0) {  // both batches of a trip consumed unconditionally, loads pinned a batch ahead
+                ld(v0, 0);
+                ld(v1, min(1, nb - 1));
                 __builtin_amdgcn_sched_barrier(0);
-                fma_b(v1, k + 1);
-                ld(v1, min(k + 3, nb - 1));
-                __builtin_amdgcn_sched_barrier(0);
+                int k = 0;
+                for (; k + 2 <= nb; k += 2) {
+                    fma_b(v0, k);
+                    ld(v0, min(k + 2, nb - 1));
+                    __builtin_amdgcn_sched_barrier(0);
+                    fma_b(v1, k + 1);
+                    ld(v1, min(k + 3, nb - 1));
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                if (k < nb) fma_b(v0, k);
             }
-            if (k < nb) fma_b(v0, k);
-        }
-        for (int j = j0 + nb * B; j < nk; ++j) {
-            const float v = KV8 ? (float)vq[(size_t)j * kvd + col] * sv[j] : vc[(size_t)j * kvd + col];
-            acc = __builtin_fmaf(p[j], v, acc);
-        }
-        att[(size_t)i * H * hd + (size_t)h * hd + c] = acc;
+            for (int j = s + nb * B; j < e; ++j) {
+                const float v = KV8 ? (float)vq[(size_t)j * kvd + col] * sv[j] : vc[(size_t)j * kvd + col];
+                acc = __builtin_fmaf(p[j], v, acc);
+            }
+            return acc;
+        };
+        att[(size_t)i * H * hd + (size_t)h * hd + c] = mm_blocks(j0, nk, chain);
     }
 }
 
@@ -549,8 +555,8 @@ __global__ __launch_bounds__(GT) void gm_attn_kernel(const float* __restrict__ q
 // value rows, so one workgroup takes all R for its query row: each key row
 // is loaded once for R score chains, each value element once for up to RC
 // (head, dim) chains.  The arithmetic per output is gm_attn_kernel<.., false>'s
-// (score = sequential FMA chain over the head dims, softmax max / exp /
-// key-order sum / divide, value chain in key order), so the bits are the same.
+// (score = FMA chain over the head dims, softmax max / exp / key-order sum /
+// divide, values in a.dot's blocked key order), so the bits are the same.
 // Needs GT % hd == 0 and R <= RC * (GT / hd).
 template <bool KV8>
 __global__ __launch_bounds__(GT) void gm_attn_group_kernel(const float* __restrict__ qkv, int H, int KV, int hd,
@@ -672,32 +678,36 @@ __global__ __launch_bounds__(GT) void gm_attn_group_kernel(const float* __restri
     // value chains: thread t takes dim c = t % hd of heads t / hd, t / hd + GT / hd, ...
     const int c = threadIdx.x % hd, r0 = threadIdx.x / hd, rs = GT / hd;
     const size_t col = (size_t)kv * hd + c;
-    float acc[RC];
+    float tot[RC], acc[RC];
 #pragma unroll
-    for (int u = 0; u < RC; ++u) acc[u] = 0.0f;
+    for (int u = 0; u < RC; ++u) tot[u] = 0.0f;
     constexpr int B = 16;
-    const int n = nk - j0, nb = n / B;
     float v0[B], v1[B];
-    auto ld = [&](float (&v)[B], int k) {
+    // a.dot's order: the keys in blocks of MM_KC at absolute multiples, each
+    // block's chains from +0 (value loads a 16-key batch ahead), then added
+    for (int s = j0; s < nk && r0 < R;) {
+        const int e = min(nk, (s / MM_KC + 1) * MM_KC), nb = (e - s) / B;
 #pragma unroll
-        for (int u = 0; u < B; ++u) {
-            const size_t j = (size_t)(j0 + k * B + u);
-            if constexpr (!KV8) v[u] = vc[j * kvd + col];
-            else v[u] = (float)vq[j * kvd + col] * sv[j];
-        }
-    };
-    auto fma_b = [&](const float (&v)[B], int k) {
+        for (int u = 0; u < RC; ++u) acc[u] = 0.0f;
+        auto ld = [&](float (&v)[B], int k) {
 #pragma unroll
-        for (int w = 0; w < RC; ++w) {
-            const int r = r0 + w * rs;
-            if (r < R) {
-                const float* pr = p + (size_t)r * pstride + j0 + k * B;
-#pragma unroll
-                for (int u = 0; u < B; ++u) acc[w] = __builtin_fmaf(pr[u], v[u], acc[w]);
+            for (int u = 0; u < B; ++u) {
+                const size_t j = (size_t)(s + k * B + u);
+                if constexpr (!KV8) v[u] = vc[j * kvd + col];
+                else v[u] = (float)vq[j * kvd + col] * sv[j];
             }
-        }
-    };
-    if (r0 < R) {
+        };
+        auto fma_b = [&](const float (&v)[B], int k) {
+#pragma unroll
+            for (int w = 0; w < RC; ++w) {
+                const int r = r0 + w * rs;
+                if (r < R) {
+                    const float* pr = p + (size_t)r * pstride + s + k * B;
+#pragma unroll
+                    for (int u = 0; u < B; ++u) acc[w] = __builtin_fmaf(pr[u], v[u], acc[w]);
+                }
+            }
+        };
         if (nb > 0) {  // both batches of a trip consumed unconditionally, loads pinned a batch ahead
             ld(v0, 0);
             ld(v1, min(1, nb - 1));
@@ -713,7 +723,7 @@ __global__ __launch_bounds__(GT) void gm_attn_group_kernel(const float* __restri
             }
             if (k < nb) fma_b(v0, k);
         }
-        for (int j = j0 + nb * B; j < nk; ++j) {
+        for (int j = s + nb * B; j < e; ++j) {
             const float v = KV8 ? (float)vq[(size_t)j * kvd + col] * sv[j] : vc[(size_t)j * kvd + col];
 #pragma unroll
             for (int w = 0; w < RC; ++w) {
@@ -722,17 +732,22 @@ __global__ __launch_bounds__(GT) void gm_attn_group_kernel(const float* __restri
             }
         }
 #pragma unroll
+        for (int u = 0; u < RC; ++u) tot[u] = tot[u] + acc[u];
+        s = e;
+    }
+    if (r0 < R) {
+#pragma unroll
         for (int w = 0; w < RC; ++w) {
             const int r = r0 + w * rs;
-            if (r < R) att[(size_t)i * H * hd + (size_t)(kv * R + r) * hd + c] = acc[w];
+            if (r < R) att[(size_t)i * H * hd + (size_t)(kv * R + r) * hd + c] = tot[w];
         }
     }
 }
 
 // ---- multi-row attention over an f32 cache, register-tiled ----
-// gm_attn_group_kernel<false>'s arithmetic per output (score = sequential
-// FMA chain over the head dims, max, exp, the key-order sum, divide, value
-// chain in key order), so the same bits, laid out for throughput:
+// gm_attn_group_kernel<false>'s arithmetic per output (score = FMA chain
+// over the head dims, max, exp, the key-order sum, divide, values in a.dot's
+// blocked key order), so the same bits, laid out for throughput:
 // - scores: a lane takes two adjacent keys for every head of the group
 //   (RP >= R; heads past R are computed on other q values and never
 //   leave the kernel), so each q value feeds two chains and each key value
@@ -867,23 +882,28 @@ __global__ __launch_bounds__(GT) void gm_attn_tile_kernel(const float* __restric
         for (int r = 0; r < RP; ++r) p[(size_t)r * prow + j] = e[r] / sums[r];
     }
     __syncthreads();
-    // values: lane (dims 2dg, 2dg + 1 of heads r4 .. r4 + 3), keys in order from +0
+    // values: lane (dims 2dg, 2dg + 1 of heads r4 .. r4 + 3); a.dot's order:
+    // blocks of MM_KC keys at absolute multiples, each chained from +0, added
     const int DG = hd >> 1, HG = GT / DG;  // lanes a head group, head groups a pass
-    const int ja = min((j0 + 3) & ~3, nk);  // keys before ja one at a time, then 4-key batches
-    const int nb = (nk - ja) >> 2;
     for (int g0 = 0; 4 * g0 < R; g0 += HG) {
         const int r4 = 4 * (g0 + tid / DG), dg = tid % DG;
         if (r4 < R) {
             const float* pr = p + (size_t)r4 * prow;
             const float* vb = vc + (size_t)kv * hd + 2 * dg;
-            float2 a[4];
+            float2 a[4], tot[4];
+#pragma unroll
+            for (int h = 0; h < 4; ++h) tot[h] = make_float2(0.0f, 0.0f);
+          for (int s = j0; s < nk;) {
+            const int e = min(nk, (s / MM_KC + 1) * MM_KC);
+            const int ja = min((s + 3) & ~3, e);  // keys before ja one at a time, then 4-key batches
+            const int nb = (e - ja) >> 2;
 #pragma unroll
             for (int h = 0; h < 4; ++h) a[h] = make_float2(0.0f, 0.0f);
             auto step = [&](int h, float pj, float2 v) __attribute__((always_inline)) {
                 a[h].x = __builtin_fmaf(pj, v.x, a[h].x);
                 a[h].y = __builtin_fmaf(pj, v.y, a[h].y);
             };
-            for (int j = j0; j < ja; ++j) {
+            for (int j = s; j < ja; ++j) {
                 const float2 v = *reinterpret_cast<const float2*>(vb + (size_t)j * kvd);
 #pragma unroll
                 for (int h = 0; h < 4; ++h) step(h, pr[(size_t)h * prow + j], v);
@@ -924,24 +944,31 @@ __global__ __launch_bounds__(GT) void gm_attn_tile_kernel(const float* __restric
                 if (k < nb) vfm(0, k);
                 if (k + 1 < nb) vfm(1, k + 1);
             }
-            for (int j = ja + 4 * nb; j < nk; ++j) {
+            for (int j = ja + 4 * nb; j < e; ++j) {
                 const float2 v = *reinterpret_cast<const float2*>(vb + (size_t)j * kvd);
 #pragma unroll
                 for (int h = 0; h < 4; ++h) step(h, pr[(size_t)h * prow + j], v);
             }
 #pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                tot[h].x = tot[h].x + a[h].x;
+                tot[h].y = tot[h].y + a[h].y;
+            }
+            s = e;
+          }
+#pragma unroll
             for (int h = 0; h < 4; ++h)
                 if (r4 + h < R)
-                    *reinterpret_cast<float2*>(att + (size_t)i * H * hd + (size_t)(kv * R + r4 + h) * hd + 2 * dg) = a[h];
+                    *reinterpret_cast<float2*>(att + (size_t)i * H * hd + (size_t)(kv * R + r4 + h) * hd + 2 * dg) = tot[h];
         }
     }
 }
 
 // ---- prefill attention over an f32 cache in two tiled launches ----
 // The per-output arithmetic of gm_attn_group_kernel<false> (score =
-// sequential FMA chain over the head dims, scale / cap, max over the row's
-// keys, exp, the key-order sum from +0, p = e / sum, value chain in key
-// order from +0), so the same bits, with each key and value row read once
+// FMA chain over the head dims, scale / cap, max over the row's keys, exp,
+// the key-order sum from +0, p = e / sum, values in a.dot's blocked key
+// order), so the same bits, with each key and value row read once
 // per block of rows rather than once per row.  A block is AP (row, head)
 // pairs: AP / RP consecutive rows times RP >= R heads of one kv head (pair
 // p = row * RP + head; heads past R and rows past m are computed on zeros
@@ -949,6 +976,7 @@ __global__ __launch_bounds__(GT) void gm_attn_tile_kernel(const float* __restric
 // st[kv][block][key][pair] (kpad keys a block) that the second launch turns
 // into exps in place.
 constexpr int PF_AP = 64, PF_KT = 128, PF_VK = 64, PF_NT = 256;
+static_assert(MM_KC % PF_VK == 0, "a value chunk lies in one a.dot block");
 constexpr size_t PF_MIN_ROWS = 1024;  // shorter prompts take the one-launch kernels (more workgroups)
 __host__ __device__ inline int pf_rows(int rp) { return PF_AP / rp; }
 
@@ -1168,11 +1196,13 @@ __global__ __launch_bounds__(PF_NT) void gm_pf_values_kernel(int H, int KV, cons
     const PfRow rfirst = pf_row(r0, cur, m, sliding, window);
     const PfRow rlast = pf_row(min(r0 + RB, m) - 1, cur, m, sliding, window);
     const float rsum = sums[pq];
-    float acc[8][4];
+    // a.dot's order: each MM_KC-key block (chunks from 0, MM_KC a multiple
+    // of PF_VK) chained from +0 in acc, the blocks added in order into tot
+    float acc[8][4], tot[8][4];
 #pragma unroll
     for (int a = 0; a < 8; ++a)
 #pragma unroll
-        for (int d = 0; d < 4; ++d) acc[a][d] = 0.0f;
+        for (int d = 0; d < 4; ++d) acc[a][d] = tot[a][d] = 0.0f;
     const int nvc = (kend + PF_VK - 1) / PF_VK;
     float pn[PN];
     float4 vn[VN];
@@ -1204,6 +1234,15 @@ __global__ __launch_bounds__(PF_NT) void gm_pf_values_kernel(int H, int KV, cons
         }
         __syncthreads();
         if (c + 1 < nvc) cload(c + 1);
+        if (jc > 0 && jc % MM_KC == 0) {
+#pragma unroll
+            for (int a = 0; a < 8; ++a)
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    tot[a][d] = tot[a][d] + acc[a][d];
+                    acc[a][d] = 0.0f;
+                }
+        }
         const bool full = jc >= rlast.j0 && jc + PF_VK <= rfirst.nk;
         if (lane_on && full) {
             for (int t = 0; t < PF_VK; ++t) {
@@ -1246,7 +1285,8 @@ __global__ __launch_bounds__(PF_NT) void gm_pf_values_kernel(int H, int KV, cons
             const int pp = 8 * pg + a, h = pp % RP, i = r0 + pp / RP;
             if (h < R && i < m)
                 *reinterpret_cast<float4*>(att + (size_t)i * H * HD + (size_t)(kv * R + h) * HD + 4 * dg) =
-                    make_float4(acc[a][0], acc[a][1], acc[a][2], acc[a][3]);
+                    make_float4(tot[a][0] + acc[a][0], tot[a][1] + acc[a][1], tot[a][2] + acc[a][2],
+                                tot[a][3] + acc[a][3]);
         }
     }
 }
@@ -1529,105 +1569,84 @@ __global__ __launch_bounds__(GT) void gm_dec_value_kernel(const float* __restric
     // wave's vector-memory counter tracks): the cache is read from L2 / HBM
     constexpr int B = 16;
     for (int c = threadIdx.x; c < hd; c += GT) {
-        float acc = 0.0f;
         const size_t col = (size_t)kv * hd + c;
-        const int n = nk - j0, nb = n / B;
-        float v0[B], v1[B], v2[B];
-        auto ld = [&](float (&v)[B], int k) {
+        // one a.dot block of keys [s, e), chained from +0
+        auto chain = [&](int s, int e) {
+            float acc = 0.0f;
+            const int nb = (e - s) / B;
+            float v0[B], v1[B], v2[B];
+            auto ld = [&](float (&v)[B], int k) {
 #pragma unroll
-            for (int u = 0; u < B; ++u) {
-                const size_t j = (size_t)(j0 + k * B + u);
-                if constexpr (!KV8) v[u] = vc[j * kvd + col];
-                else v[u] = (float)vq[j * kvd + col] * sv[j];
-            }
-        };
-        auto fma_b = [&](const float (&v)[B], int k) {
+                for (int u = 0; u < B; ++u) {
+                    const size_t j = (size_t)(s + k * B + u);
+                    if constexpr (!KV8) v[u] = vc[j * kvd + col];
+                    else v[u] = (float)vq[j * kvd + col] * sv[j];
+                }
+            };
+            auto fma_b = [&](const float (&v)[B], int k) {
 #pragma unroll
-            for (int u = 0; u < B; ++u) acc = __builtin_fmaf(p[j0 + k * B + u], v[u], acc);
-        };
-        if (nb > 0) {
-            ld(v0, 0);
-            ld(v1, min(1, nb - 1));
-            ld(v2, min(2, nb - 1));
-            __builtin_amdgcn_sched_barrier(0);
-            int k = 0;
-            for (; k + 3 <= nb; k += 3) {
-                fma_b(v0, k);
-                ld(v0, min(k + 3, nb - 1));
+                for (int u = 0; u < B; ++u) acc = __builtin_fmaf(p[s + k * B + u], v[u], acc);
+            };
+            if (nb > 0) {
+                ld(v0, 0);
+                ld(v1, min(1, nb - 1));
+                ld(v2, min(2, nb - 1));
                 __builtin_amdgcn_sched_barrier(0);
-                fma_b(v1, k + 1);
-                ld(v1, min(k + 4, nb - 1));
-                __builtin_amdgcn_sched_barrier(0);
-                fma_b(v2, k + 2);
-                ld(v2, min(k + 5, nb - 1));
-                __builtin_amdgcn_sched_barrier(0);
+                int k = 0;
+                for (; k + 3 <= nb; k += 3) {
+                    fma_b(v0, k);
+                    ld(v0, min(k + 3, nb - 1));
+                    __builtin_amdgcn_sched_barrier(0);
+                    fma_b(v1, k + 1);
+                    ld(v1, min(k + 4, nb - 1));
+                    __builtin_amdgcn_sched_barrier(0);
+                    fma_b(v2, k + 2);
+                    ld(v2, min(k + 5, nb - 1));
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                if (k < nb) fma_b(v0, k);
+                if (k + 1 < nb) fma_b(v1, k + 1);
             }
-            if (k < nb) fma_b(v0, k);
-            if (k + 1 < nb) fma_b(v1, k + 1);
-        }
-        for (int j = j0 + nb * B; j < nk; ++j) {
-            const float v = KV8 ? (float)vq[(size_t)j * kvd + col] * sv[j] : vc[(size_t)j * kvd + col];
-            acc = __builtin_fmaf(p[j], v, acc);
-        }
-        att[(size_t)h * hd + c] = acc;
+            for (int j = s + nb * B; j < e; ++j) {
+                const float v = KV8 ? (float)vq[(size_t)j * kvd + col] * sv[j] : vc[(size_t)j * kvd + col];
+                acc = __builtin_fmaf(p[j], v, acc);
+            }
+            return acc;
+        };
+        att[(size_t)h * hd + c] = mm_blocks(j0, nk, chain);
     }
 }
 
-// ---- long-cache decode value chains through an LDS ring --------------------
-// gm_dec_value_kernel's work for CW = RB / es channels of one head per
-// workgroup (es the cache element size): the softmax as there, by VT threads
-// (the in-order sum a speculative fold over VT / 64 segments), then every
-// channel's chain acc = fma(p[j], v[j][c], acc) in key order by wave 0, with
-// the value rows streamed into a ring of NB chunks of 16 KB by every wave's
-// direct-to-LDS loads (global_load_lds, 16 loads a chunk): the first chunks
-// are in flight during the softmax, and each chunk's loads NB - 2 chunks
-// ahead of the chain, which then reads LDS rather than waiting on memory.
-// The f32 chain of a whole chunk is unrolled in batches of 8 keys (4 paired
-// value reads and 2 probability reads each) with two batches in flight, so
-// the chain waits on the FMA latency rather than on LDS.  Per output the
-// order is unchanged, so the values are gm_dec_value_kernel's bit for bit.
-constexpr int VR_NB = 4, VR_CHUNK = 16384, VT = 1024;
+// ---- long-cache decode value step, a.dot's blocks in parallel -------------
+// gm_dec_value_kernel's work for VB_CW channels of one head per workgroup:
+// the softmax as there, by VT threads (the in-order sum a speculative fold
+// over VT / 64 segments), then the value product in a.dot's order, whose
+// blocks of MM_KC keys (at absolute multiples) are independent chains from
+// +0: thread t takes channel t % VB_CW of block t / VB_CW (and every
+// VT / VB_CW-th block after it), its chain fed by 16-key batches of value
+// loads two batches ahead (a key's VB_CW channels one coalesced row piece);
+// the block results go to LDS and the first VB_CW threads add them in block
+// order.  Per output the arithmetic is gm_dec_value_kernel's, bit for bit.
+constexpr int VT = 1024, VB_CW = 32;
 
-__device__ __forceinline__ void gm_dma16(const void* g, void* lds_base) { dma16_lds(g, lds_base); }
-template <int N>
-__device__ __forceinline__ void gm_wait_vm() { wait_vmcnt<N>(); }
-
-template <bool KV8, int RB>
-__global__ __launch_bounds__(VT) void gm_dec_value_ring_kernel(const float* __restrict__ sc, int H, int KV, int hd,
-                                                               const int* __restrict__ curp,
-                                                               const float* __restrict__ vc,
-                                                               const int8_t* __restrict__ vq,
-                                                               const float* __restrict__ vs, int sliding, int window,
-                                                               int pstride, float* __restrict__ att) {
-    constexpr int ES = KV8 ? 1 : 4, CW = RB / ES, CK = VR_CHUNK / RB, KPI = 1024 / RB, NW = VT / 64;
-    constexpr int PW = VR_CHUNK / 1024 / NW;  // 1 KB loads a wave a chunk
-    static_assert(PW >= 1 && PW * NW * 1024 == VR_CHUNK && CK % 16 == 0, "whole loads; whole batches of keys");
+template <bool KV8>
+__global__ __launch_bounds__(VT) void gm_dec_value_blk_kernel(const float* __restrict__ sc, int H, int KV, int hd,
+                                                              const int* __restrict__ curp,
+                                                              const float* __restrict__ vc,
+                                                              const int8_t* __restrict__ vq,
+                                                              const float* __restrict__ vs, int sliding, int window,
+                                                              int pstride, float* __restrict__ att) {
+    constexpr int NW = VT / 64, BPP = VT / VB_CW;
     extern __shared__ float4 lds4[];
-    // p and sv hold key j at index j - j0, so a chunk's keys start 16-byte aligned
+    // p and sv hold key j at index j - j0
     float* p = reinterpret_cast<float*>(lds4);
     float* sv = p + pstride;
     float* fsc = sv + pstride;
-    char* ring = reinterpret_cast<char*>(fsc + seq_sum_spec_scratch(VT));
+    float* part = fsc + seq_sum_spec_scratch(VT);  // [block][VB_CW]
     __shared__ float red[NW];
     const int h = blockIdx.x, kv = h / (H / KV), kvd = KV * hd, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int ab = *curp, nk = ab + 1, j0 = (sliding && ab >= window) ? ab - window + 1 : 0;
-    const int n = nk - j0, nch = (n + CK - 1) / CK;
-    const int col0 = kv * hd + (int)blockIdx.y * CW;
-    const char* vbase = KV8 ? reinterpret_cast<const char*>(vq) : reinterpret_cast<const char*>(vc);
-    // this lane's 16 bytes of load i of chunk s: key j0 + s CK + i KPI + lane / (RB / 16), clamped
-    auto issue = [&](int s) {
-        char* st = ring + (s % VR_NB) * VR_CHUNK;
-#pragma unroll
-        for (int u = 0; u < PW; ++u) {
-            const int i = wave * PW + u;
-            const int key = min(j0 + s * CK + i * KPI + lane / (RB / 16), nk - 1);
-            const char* src = vbase + ((size_t)key * kvd + col0) * ES + (lane % (RB / 16)) * 16;
-            gm_dma16(src, st + i * 1024);
-        }
-    };
-#pragma unroll
-    for (int s = 0; s < VR_NB - 1; ++s)
-        if (s < nch) issue(s);
+    const int n = nk - j0;
     // the softmax, as gm_dec_value_kernel (the key-order sum from +0 over
     // the keys j0 .. nk - 1); the scores SB to a thread at a time, every
     // load of a batch issued before the first is used
@@ -1662,100 +1681,55 @@ __global__ __launch_bounds__(VT) void gm_dec_value_ring_kernel(const float* __re
     __syncthreads();
     const float sum = seq_sum_spec<VT>(p, n, 0.0f, fsc);
     for (int j = threadIdx.x; j < n; j += VT) p[j] = p[j] / sum;
-    __syncthreads();  // the normalised p (the first chunks have long landed)
-    // the value chains: wave 0, a lane per channel
-    float acc = 0.0f;
-    const int c = lane;
-    for (int s = 0; s < nch; ++s) {
-        // chunk s has landed once at most (chunks issued after s) x PW loads
-        // of this wave are outstanding; after the raw barrier (a
-        // __syncthreads would also wait for the loads still in flight) every
-        // wave's part is in LDS
-        const int ahead = min(nch - 1 - s, VR_NB - 2);
-        if (ahead >= 2) gm_wait_vm<2 * PW>();
-        else if (ahead == 1) gm_wait_vm<PW>();
-        else gm_wait_vm<0>();
-        __builtin_amdgcn_s_barrier();
-        // the slot refilled here held chunk s - 1, which wave 0 finished
-        // before this barrier
-        if (s + VR_NB - 1 < nch) issue(s + VR_NB - 1);
-        if (wave == 0 && c < CW) {
-            const char* st = ring + (s % VR_NB) * VR_CHUNK + c * ES;
-            const float* ps = p + s * CK;
-            const float* svs = sv + s * CK;
-            const int m = min(CK, n - s * CK);
-            if constexpr (!KV8) {
-                // batch k: keys 8k .. 8k + 7 of the chunk
-                float vb[3][8], pb[3][8];
-                auto ld = [&](int b, int k) __attribute__((always_inline)) {
+    __syncthreads();
+    // the blocks of keys [j0, nk)
+    const int bf = j0 / MM_KC, nblk = (nk - 1) / MM_KC - bf + 1;
+    const int c = threadIdx.x % VB_CW;
+    const size_t col = (size_t)kv * hd + blockIdx.y * VB_CW + c;
+    constexpr int B = 16;
+    for (int bi = threadIdx.x / VB_CW; bi < nblk; bi += BPP) {
+        const int s = max(j0, (bf + bi) * MM_KC), e = min(nk, (bf + bi + 1) * MM_KC), nb = (e - s) / B;
+        float acc = 0.0f;
+        float v0[B], v1[B];
+        auto ld = [&](float (&v)[B], int k) __attribute__((always_inline)) {
 #pragma unroll
-                    for (int u = 0; u < 8; ++u) vb[b][u] = *reinterpret_cast<const float*>(st + (8 * k + u) * RB);
-                    const float4 p0 = *reinterpret_cast<const float4*>(ps + 8 * k);
-                    const float4 p1 = *reinterpret_cast<const float4*>(ps + 8 * k + 4);
-                    pb[b][0] = p0.x; pb[b][1] = p0.y; pb[b][2] = p0.z; pb[b][3] = p0.w;
-                    pb[b][4] = p1.x; pb[b][5] = p1.y; pb[b][6] = p1.z; pb[b][7] = p1.w;
-                };
-                auto fm = [&](int b) __attribute__((always_inline)) {
-#pragma unroll
-                    for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(pb[b][u], vb[b][u], acc);
-                };
-                if (m == CK) {  // a whole chunk: straight-line, two batches in flight
-                    constexpr int NB = CK / 8;
-                    ld(0, 0);
-                    ld(1, 1);
-#pragma unroll
-                    for (int k = 0; k < NB; ++k) {
-                        __builtin_amdgcn_sched_barrier(0);
-                        fm(k % 3);
-                        if (k + 2 < NB) ld((k + 2) % 3, k + 2);
-                    }
-                } else {  // the last, partial chunk: a batch at a time, then key by key
-                    int k = 0;
-                    for (; 8 * k + 8 <= m; ++k) {
-                        ld(0, k);
-                        fm(0);
-                    }
-                    for (int jj = 8 * k; jj < m; ++jj)
-                        acc = __builtin_fmaf(ps[jj], *reinterpret_cast<const float*>(st + jj * RB), acc);
-                }
-            } else {
-                constexpr int B = 16;
-                float vb[2][B], pb[2][B];
-                const int nb = m / B;
-                auto ld = [&](int b, int k) {
-#pragma unroll
-                    for (int u = 0; u < B; u += 4) {
-                        const float4 p4 = *reinterpret_cast<const float4*>(ps + k * B + u);
-                        pb[b][u] = p4.x; pb[b][u + 1] = p4.y; pb[b][u + 2] = p4.z; pb[b][u + 3] = p4.w;
-                    }
-#pragma unroll
-                    for (int u = 0; u < B; ++u)
-                        vb[b][u] = (float)*reinterpret_cast<const int8_t*>(st + (k * B + u) * RB) * svs[k * B + u];
-                };
-                auto fm = [&](int b) {
-#pragma unroll
-                    for (int u = 0; u < B; ++u) acc = __builtin_fmaf(pb[b][u], vb[b][u], acc);
-                };
-                if (nb > 0) {
-                    ld(0, 0);
-                    __builtin_amdgcn_sched_barrier(0);
-                    int k = 0;
-                    for (; k + 2 <= nb; k += 2) {
-                        ld(1, k + 1);
-                        __builtin_amdgcn_sched_barrier(0);
-                        fm(0);
-                        ld(0, min(k + 2, nb - 1));
-                        __builtin_amdgcn_sched_barrier(0);
-                        fm(1);
-                    }
-                    if (k < nb) fm(0);
-                }
-                for (int jj = nb * B; jj < m; ++jj)
-                    acc = __builtin_fmaf(ps[jj], (float)*reinterpret_cast<const int8_t*>(st + jj * RB) * svs[jj], acc);
+            for (int u = 0; u < B; ++u) {
+                const size_t j = (size_t)(s + k * B + u);
+                if constexpr (!KV8) v[u] = vc[j * kvd + col];
+                else v[u] = (float)vq[j * kvd + col] * sv[j - j0];
             }
+        };
+        auto fma_b = [&](const float (&v)[B], int k) __attribute__((always_inline)) {
+#pragma unroll
+            for (int u = 0; u < B; ++u) acc = __builtin_fmaf(p[s - j0 + k * B + u], v[u], acc);
+        };
+        if (nb > 0) {  // both batches of a trip consumed unconditionally, loads pinned a batch ahead
+            ld(v0, 0);
+            ld(v1, min(1, nb - 1));
+            __builtin_amdgcn_sched_barrier(0);
+            int k = 0;
+            for (; k + 2 <= nb; k += 2) {
+                fma_b(v0, k);
+                ld(v0, min(k + 2, nb - 1));
+                __builtin_amdgcn_sched_barrier(0);
+                fma_b(v1, k + 1);
+                ld(v1, min(k + 3, nb - 1));
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (k < nb) fma_b(v0, k);
         }
+        for (int j = s + nb * B; j < e; ++j) {
+            const float v = KV8 ? (float)vq[(size_t)j * kvd + col] * sv[j - j0] : vc[(size_t)j * kvd + col];
+            acc = __builtin_fmaf(p[j - j0], v, acc);
+        }
+        part[bi * VB_CW + c] = acc;
     }
-    if (wave == 0 && c < CW) att[(size_t)h * hd + blockIdx.y * CW + c] = acc;
+    __syncthreads();
+    if (threadIdx.x < VB_CW) {
+        float t = 0.0f;
+        for (int bi = 0; bi < nblk; ++bi) t = t + part[bi * VB_CW + threadIdx.x];
+        att[(size_t)h * hd + blockIdx.y * VB_CW + threadIdx.x] = t;
+    }
 }
 
 // h = act(gate) * up over m rows of the [gate | up] buffer: gelu_tanh
@@ -2034,42 +2008,32 @@ hipError_t gm_allow_lds(size_t lds) {
     return hipSuccess;
 }
 
-// The ring value kernel's channels a workgroup (0: the kernel does not
-// apply to this head size) and its LDS for a padded position count ps.
-int value_ring_cw(size_t hd) {
-    // 16 channels a workgroup: a workgroup streams 64 bytes of f32 cache a
-    // key, which the ring's three chunks in flight deliver at the chain's
-    // pace; wider blocks leave the chain waiting on memory
-    return hd % 16 == 0 ? 16 : 0;
-}
-size_t value_ring_lds(size_t ps) {
-    return (2 * ps + seq_sum_spec_scratch(VT)) * sizeof(float) + (size_t)VR_NB * VR_CHUNK;
+// LDS of the block-parallel value kernel for a padded position count ps:
+// p and sv, the fold's scratch, and a VB_CW-float row per block of keys.
+size_t value_blk_lds(size_t ps) {
+    return (2 * ps + seq_sum_spec_scratch(VT) + (ps / MM_KC + 2) * VB_CW) * sizeof(float);
 }
 
-template <bool KV8, int RB>
-hipError_t value_ring_t(const frq_gemma* g, const float* sc, int sl, int win, int ps, const float* vc,
-                        const int8_t* vq, const float* vs, float* att, hipStream_t s) {
-    constexpr int CW = RB / (KV8 ? 1 : 4);
-    const size_t lds = value_ring_lds(ps);
-    gm_dec_value_ring_kernel<KV8, RB><<<dim3((unsigned)g->H, (unsigned)(g->hd / CW)), dim3(VT), lds, s>>>(
-        sc, (int)g->H, (int)g->KV, (int)g->hd, g->cur, vc, vq, vs, sl, win, ps, att);
+// The long-cache value step, blocks in parallel, when the head size and the
+// LDS allow it; hipErrorNotSupported sends the caller to gm_dec_value_kernel.
+hipError_t launch_value_blk(const frq_gemma* g, int sl, int win, int ps, const float* vc, const int8_t* vq,
+                            const float* vs, float* att, hipStream_t s) {
+    const size_t lds = value_blk_lds(ps);
+    if (g->hd % VB_CW || lds > GM_LDS_MAX) return hipErrorNotSupported;
+    const dim3 grid((unsigned)g->H, (unsigned)(g->hd / VB_CW));
+    if (g->kv8)
+        gm_dec_value_blk_kernel<true><<<grid, dim3(VT), lds, s>>>(g->sc, (int)g->H, (int)g->KV, (int)g->hd, g->cur,
+                                                                   vc, vq, vs, sl, win, ps, att);
+    else
+        gm_dec_value_blk_kernel<false><<<grid, dim3(VT), lds, s>>>(g->sc, (int)g->H, (int)g->KV, (int)g->hd, g->cur,
+                                                                    vc, vq, vs, sl, win, ps, att);
     return hipGetLastError();
 }
 
-// The long-cache value step through the LDS ring when the head size and the
-// LDS allow it; hipErrorNotSupported sends the caller to gm_dec_value_kernel.
-hipError_t launch_value_ring(const frq_gemma* g, int sl, int win, int ps, const float* vc, const int8_t* vq,
-                             const float* vs, float* att, hipStream_t s) {
-    const int cw = value_ring_cw(g->hd);
-    if (!cw || value_ring_lds(ps) > GM_LDS_MAX) return hipErrorNotSupported;
-    if (g->kv8) return value_ring_t<true, 16>(g, g->sc, sl, win, ps, vc, vq, vs, att, s);
-    return value_ring_t<false, 64>(g, g->sc, sl, win, ps, vc, vq, vs, att, s);
-}
-
-hipError_t allow_value_ring_lds(size_t ps) {
-    const size_t lds = value_ring_lds(ps);
-    if (lds > GM_LDS_MAX) return hipSuccess;  // the caller takes the other kernel
-    const void* ks[] = {(const void*)gm_dec_value_ring_kernel<false, 64>, (const void*)gm_dec_value_ring_kernel<true, 16>};
+hipError_t allow_value_blk_lds(size_t ps) {
+    const size_t lds = value_blk_lds(ps);
+    if (lds > GM_LDS_MAX || lds <= 64 * 1024) return hipSuccess;  // the caller takes the other kernel / the default
+    const void* ks[] = {(const void*)gm_dec_value_blk_kernel<false>, (const void*)gm_dec_value_blk_kernel<true>};
     for (const void* k : ks)
         if (hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds)) return e;
     return hipSuccess;
@@ -2172,7 +2136,7 @@ int gm_reserve(frq_ctx* c, frq_gemma* g, size_t npos, size_t rows, size_t nb = 1
                                   (int)gm_norm_lds((int)g->d)),
               "hipFuncSetAttribute(norm)");
     GMCHK(gm_allow_quant_lds(g), "hipFuncSetAttribute(quant)");
-    GMCHK(allow_value_ring_lds(gm_pstride_n(N)), "hipFuncSetAttribute(value ring)");
+    GMCHK(allow_value_blk_lds(gm_pstride_n(N)), "hipFuncSetAttribute(value blocks)");
     const size_t L = g->L, kvd = g->KV * g->hd, half = g->hd / 2;
     size_t off = 0;
     auto take = [&](size_t bytes) { const size_t o = off; off += round_up(bytes, 256); return o; };
@@ -2319,12 +2283,12 @@ int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_o
                     qkvr, H, KV, hd, g->cur, g->cs, kc, vc, kq, vq, ks, vs, qb, qn, kn, g->eps, g->qr);
                 gm_dec_score_kernel<true><<<sg, dim3(GT), hd4 * sizeof(float), s>>>(
                     g->qr, H, KV, hd, g->cur, kc, kq, ks, g->qscale, g->cap, sl, win, div, ps, g->sc);
-                const hipError_t er = launch_value_ring(g, sl, win, ps, vc, vq, vs, attr, s);
+                const hipError_t er = launch_value_blk(g, sl, win, ps, vc, vq, vs, attr, s);
                 if (er == hipErrorNotSupported)
                     gm_dec_value_kernel<true><<<dim3((unsigned)H), dim3(GT), vlds, s>>>(g->sc, H, KV, hd, g->cur, vc,
                                                                                         vq, vs, sl, win, ps, attr);
                 else
-                    GMCHK(er, "launch value ring");
+                    GMCHK(er, "launch value blocks");
             } else {
                 if (hd == 128 || hd == 64 || hd == 32) {  // prep fused into the scores
                     auto qk = hd == 128 ? gm_dec_qks_kernel<128> : hd == 64 ? gm_dec_qks_kernel<64> : gm_dec_qks_kernel<32>;
@@ -2336,13 +2300,13 @@ int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_o
                     gm_dec_score_kernel<false><<<sg, dim3(GT), hd4 * sizeof(float), s>>>(
                         g->qr, H, KV, hd, g->cur, kc, kq, ks, g->qscale, g->cap, sl, win, div, ps, g->sc);
                 }
-                const hipError_t er = launch_value_ring(g, sl, win, ps, vc, vq, vs, attr, s);
+                const hipError_t er = launch_value_blk(g, sl, win, ps, vc, vq, vs, attr, s);
                 if (er == hipErrorNotSupported)
                     gm_dec_value_kernel<false><<<dim3((unsigned)H), dim3(GT), vlds, s>>>(g->sc, H, KV, hd, g->cur,
                                                                                          vc, vq, vs, sl, win, ps,
                                                                                          attr);
                 else
-                    GMCHK(er, "launch value ring");
+                    GMCHK(er, "launch value blocks");
             }
           }
         } else if (m == 1 || batch) {
@@ -2626,9 +2590,10 @@ static int decoder_load(frq_ctx* c, const frq_bundle* b, int kv_int8, int want_a
     g->L = cfg[0]; g->H = cfg[1]; g->KV = cfg[2]; g->hd = cfg[3]; g->d = cfg[4]; g->ffn = cfg[5]; g->vocab = cfg[6];
     g->kv8 = kv_int8 ? 1 : 0;
     g->arch = want_arch;
-    if (g->H % g->KV || g->hd % 4 || g->d % 4 || g->d > 8192 || g->hd > 1024)
+    // a head's scores are one a.dot block (hd <= MM_KC): a single FMA chain
+    if (g->H % g->KV || g->hd % 4 || g->d % 4 || g->d > 8192 || g->hd > (size_t)MM_KC)
         return set_error(FRQ_ERR_ARG, "gemma shape outside this build's kernels (H % nkv, head dim and d % 4, "
-                                      "d <= 8192)");
+                                      "head dim <= 256, d <= 8192)");
     // Gemma::new (52-60): f32 of the f64 config values; RoPE frequencies and
     // the query scale through the host libm's powf, as the reference
     const float theta = (float)cff[0];

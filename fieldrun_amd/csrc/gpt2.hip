@@ -26,8 +26,9 @@
 // top-32 |a| as outliers), so a one-ulp difference in an activation can
 // flip an int8 value and move the logits by ~1e-3.  Hence: layernorm's mean
 // is ndarray's eight-lane sum and its variance a sequential fold; the
-// softmax sum runs in key order; the score and value products are
-// sequential-k FMA chains (matrixmultiply's kernel order); exp and tanh
+// softmax sum runs in key order; the score and value products follow
+// matrixmultiply's order (MM_KC-long k blocks, each an FMA chain from +0,
+// added in order; a head's scores are one block); exp and tanh
 // are the libm algorithms Rust's f32::exp / f32::tanh reach (libm_f32.h);
 // and prefill rows go through the bit-exact M <= 16 linear in chunks.
 #include "frq_internal.h"
@@ -200,9 +201,10 @@ __global__ __launch_bounds__(NT) void qkv_kernel(float* __restrict__ qkv, const 
 // Causal attention of row i (position cur + i) and head h over cache rows
 // 0 .. cur + i (forward_block 189-201): s_j = (q . k_j) / sqrt(hd) as a
 // sequential FMA chain over the head dims (one thread per key), softmax
-// (max, expf, the sum in key order, divide), then out_c = sum_j p_j v_jc as
-// a sequential FMA chain over j (one lane per output dim, its loads a
-// 16-key batch ahead).  Keys past cur + i carry the reference's -1e10
+// (max, expf, the sum in key order, divide), then out_c = sum_j p_j v_jc in
+// a.dot's order (each MM_KC-key block an FMA chain over j from +0, the
+// blocks added in order; one lane per output dim, its loads a 16-key batch
+// ahead).  Keys past cur + i carry the reference's -1e10
 // mask: it joins the max, and its exp is exactly 0 (for any max above
 // -1e10 + 104), so those keys add nothing and are skipped.
 // FUSED (decode, one row): the block also adds the bias to its head's q, k,
@@ -298,42 +300,46 @@ __global__ __launch_bounds__(NT) void attn_kernel(const float* __restrict__ qkv,
     // run one 16-key batch ahead of the chain
     constexpr int B = 16;
     for (int c = threadIdx.x; c < hd; c += NT) {
-        float acc = 0.0f;
         const size_t col = (size_t)h * hd + c;
-        const int nb = nk / B;
-        float v0[B], v1[B];
-        auto ld = [&](float (&v)[B], int k) {
+        // one a.dot block of keys [s, e), chained from +0
+        auto chain = [&](int s, int e) {
+            float acc = 0.0f;
+            const int nb = (e - s) / B;
+            float v0[B], v1[B];
+            auto ld = [&](float (&v)[B], int k) {
 #pragma unroll
-            for (int u = 0; u < B; ++u) {
-                const size_t j = (size_t)(k * B + u);
-                if constexpr (!KV8) v[u] = vc[j * d + col];
-                else v[u] = (float)vq[j * d + col] * sv[j];
-            }
-        };
-        auto fma_b = [&](const float (&v)[B], int k) {
+                for (int u = 0; u < B; ++u) {
+                    const size_t j = (size_t)(s + k * B + u);
+                    if constexpr (!KV8) v[u] = vc[j * d + col];
+                    else v[u] = (float)vq[j * d + col] * sv[j];
+                }
+            };
+            auto fma_b = [&](const float (&v)[B], int k) {
 #pragma unroll
-            for (int u = 0; u < B; ++u) acc = __builtin_fmaf(p[k * B + u], v[u], acc);
-        };
-        if (nb > 0) {  // both batches of a trip consumed unconditionally, loads pinned a batch ahead
-            ld(v0, 0);
-            ld(v1, min(1, nb - 1));
-            __builtin_amdgcn_sched_barrier(0);
-            int k = 0;
-            for (; k + 2 <= nb; k += 2) {
-                fma_b(v0, k);
-                ld(v0, min(k + 2, nb - 1));
+                for (int u = 0; u < B; ++u) acc = __builtin_fmaf(p[s + k * B + u], v[u], acc);
+            };
+            if (nb > 0) {  // both batches of a trip consumed unconditionally, loads pinned a batch ahead
+                ld(v0, 0);
+                ld(v1, min(1, nb - 1));
                 __builtin_amdgcn_sched_barrier(0);
-                fma_b(v1, k + 1);
-                ld(v1, min(k + 3, nb - 1));
-                __builtin_amdgcn_sched_barrier(0);
+                int k = 0;
+                for (; k + 2 <= nb; k += 2) {
+                    fma_b(v0, k);
+                    ld(v0, min(k + 2, nb - 1));
+                    __builtin_amdgcn_sched_barrier(0);
+                    fma_b(v1, k + 1);
+                    ld(v1, min(k + 3, nb - 1));
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                if (k < nb) fma_b(v0, k);
             }
-            if (k < nb) fma_b(v0, k);
-        }
-        for (int j = nb * B; j < nk; ++j) {
-            const float v = KV8 ? (float)vq[(size_t)j * d + col] * sv[j] : vc[(size_t)j * d + col];
-            acc = __builtin_fmaf(p[j], v, acc);
-        }
-        att[(size_t)i * d + col] = acc;
+            for (int j = s + nb * B; j < e; ++j) {
+                const float v = KV8 ? (float)vq[(size_t)j * d + col] * sv[j] : vc[(size_t)j * d + col];
+                acc = __builtin_fmaf(p[j], v, acc);
+            }
+            return acc;
+        };
+        att[(size_t)i * d + col] = mm_blocks(0, nk, chain);
     }
 }
 
@@ -652,9 +658,10 @@ int frq_gpt2_load(frq_ctx* c, const frq_bundle* b, int kv_int8, frq_gpt2** out) 
     g->kv8 = kv_int8 ? 1 : 0;
     if (g->d % g->H) return set_error(FRQ_ERR_FORMAT, "n_embd not a multiple of n_head");
     g->hd = g->d / g->H;
-    if (g->hd % 4 || g->d > 2048 || attn_lds(g.get()) > 64 * 1024 || g->npos > (1u << 20))
-        return set_error(FRQ_ERR_ARG, "gpt2 shape outside this build's kernels (head dim % 4, n_embd <= 2048, "
-                                      "n_positions within 64 KB of scores)");
+    // a head's scores are one a.dot block (hd <= MM_KC): a single FMA chain
+    if (g->hd % 4 || g->hd > (size_t)MM_KC || g->d > 2048 || attn_lds(g.get()) > 64 * 1024 || g->npos > (1u << 20))
+        return set_error(FRQ_ERR_ARG, "gpt2 shape outside this build's kernels (head dim % 4 and <= 256, "
+                                      "n_embd <= 2048, n_positions within 64 KB of scores)");
     const size_t L = g->L, d = g->d;
     // linears and the row table
     static const char* names[4] = {"attn.c_attn", "attn.c_proj", "mlp.c_fc", "mlp.c_proj"};

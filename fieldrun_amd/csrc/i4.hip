@@ -5,9 +5,10 @@
 //    (199-225): per group, 8 lane accumulators each an FMA chain over the
 //    group's 8-nibble chunks, then hsum256 ((l0+l4)+(l2+l6))+((l1+l5)+(l3+l7))
 //    (146-153), a scalar mul+add tail, then sum += scale[g] * gsum.
-//  M > 1 (777-798): w[kk,j] = s4 * scale[j, kk/g] (f32) then a.dot(w); the
-//    oracle's stand-in for matrixmultiply's sgemm is a sequential-k FMA chain
-//    per output, which the batched kernel below reproduces.
+//  M > 1 (777-798): w[kk,j] = s4 * scale[j, kk/g] (f32) then a.dot(w),
+//    matrixmultiply's sgemm: per output, k in blocks of MM_KC, each an FMA
+//    chain from +0, the blocks added in order; the exact M > 1 kernels below
+//    reproduce that order.
 //
 // Blocked shapes (g == 32, K % 32 == 0, 1 <= M <= 16) run on the int8
 // MFMA.  At upload the nibbles are re-laid out so that the B operand of
@@ -360,8 +361,9 @@ __global__ __launch_bounds__(256) void i4_terms_rows(const uint8_t* __restrict__
     if (st < M && r0 + sr < N) out[(size_t)st * N + r0 + sr] = sum;
 }
 
-// M > 1: dequantise w = s4 * scale (f32, exact) and run a sequential-k FMA
-// chain per output (the oracle's sgemm order).  One thread per column j and
+// M > 1: dequantise w = s4 * scale (f32, exact) and sum in a.dot's order
+// (MM_KC-long k blocks, each an FMA chain from +0, added in order).  One
+// thread per column j and
 // up to 16 token rows; the token rows' activations are uniform across the
 // wave (scalar loads), the weight row is the thread's own packed row.
 template <int MT>
@@ -375,28 +377,34 @@ __global__ __launch_bounds__(256) void i4_gemm_rows(
     const int rb = (K + 1) / 2, ng = (K + g - 1) / g;
     const uint8_t* prow = packed + (size_t)j * rb;
     const uint16_t* srow = scale + (size_t)j * ng;
-    float acc[MT];
+    float acc[MT], tot[MT];
 #pragma unroll
-    for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
-    for (int kk = 0; kk < K; ++kk) {
-        const uint8_t byte = prow[kk >> 1];
-        const int v = (kk & 1) ? (byte >> 4) : (byte & 0x0F);
-        const float w = (float)((int)((uint32_t)v << 28) >> 28) * h2f(srow[kk / g]);
+    for (int m = 0; m < MT; ++m) tot[m] = 0.0f;
+    for (int k0 = 0; k0 < K; k0 += MM_KC) {
 #pragma unroll
-        for (int m = 0; m < MT; ++m)
-            if (m0 + m < M) acc[m] = __builtin_fmaf(a[(size_t)(m0 + m) * K + kk], w, acc[m]);
+        for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
+        for (int kk = k0; kk < min(K, k0 + MM_KC); ++kk) {
+            const uint8_t byte = prow[kk >> 1];
+            const int v = (kk & 1) ? (byte >> 4) : (byte & 0x0F);
+            const float w = (float)((int)((uint32_t)v << 28) >> 28) * h2f(srow[kk / g]);
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+                if (m0 + m < M) acc[m] = __builtin_fmaf(a[(size_t)(m0 + m) * K + kk], w, acc[m]);
+        }
+#pragma unroll
+        for (int m = 0; m < MT; ++m) tot[m] = tot[m] + acc[m];
     }
 #pragma unroll
     for (int m = 0; m < MT; ++m)
-        if (m0 + m < M) out[(size_t)(m0 + m) * N + j] = acc[m];
+        if (m0 + m < M) out[(size_t)(m0 + m) * N + j] = tot[m];
 }
 
 // The same chain with one thread per (column j, token row blockIdx.y), for
 // K % 32 == 0, g % 32 == 0 and 16-byte aligned activation rows: the thread
 // reads its packed row 32 nibbles (16 bytes) at a time and the token's 32
 // activations (uniform across the workgroup) with them, one chunk ahead of
-// the chain, so the K-long FMA chain is the only serial part.  The order per
-// output is i4_gemm_rows' (kk ascending, w = s4 * scale), bit for bit.
+// the chain, so the FMA chain is the only serial part.  The order per output
+// is i4_gemm_rows' (a.dot's blocks over kk, w = s4 * scale), bit for bit.
 __global__ __launch_bounds__(256) void i4_rows_chain(const uint8_t* __restrict__ packed,
                                                      const uint16_t* __restrict__ scale, int N, int K, int g,
                                                      const float* __restrict__ a, float* __restrict__ out) {
@@ -428,12 +436,23 @@ __global__ __launch_bounds__(256) void i4_rows_chain(const uint8_t* __restrict__
             for (int q = 0; q < 8; ++q) acc = __builtin_fmaf(x[q], s4f(ws[c4], q) * c.s, acc);
         }
     };
+    // a.dot's blocks: MM_KC / 32 chunks (an even count) each, so a block
+    // starts on an even chunk, where the running block sum is folded in
+    static_assert(MM_KC % 64 == 0, "blocks start on even chunks");
+    float tot = 0.0f;
+    auto fold = [&](int i) {
+        if (i > 0 && i % (MM_KC / 32) == 0) {
+            tot = tot + acc;
+            acc = 0.0f;
+        }
+    };
     Chunk c0, c1;
     ld(c0, 0);
     ld(c1, min(1, nc - 1));
     __builtin_amdgcn_sched_barrier(0);
     int i = 0;
     for (; i + 2 <= nc; i += 2) {
+        fold(i);
         chain(c0);
         ld(c0, min(i + 2, nc - 1));
         __builtin_amdgcn_sched_barrier(0);
@@ -441,8 +460,11 @@ __global__ __launch_bounds__(256) void i4_rows_chain(const uint8_t* __restrict__
         ld(c1, min(i + 3, nc - 1));
         __builtin_amdgcn_sched_barrier(0);
     }
-    if (i < nc) chain(c0);
-    if (j < N) out[(size_t)m * N + j] = acc;
+    if (i < nc) {
+        fold(i);
+        chain(c0);
+    }
+    if (j < N) out[(size_t)m * N + j] = tot + acc;
 }
 
 constexpr float XMAX4 = 8323072.0f;  // 127 * 2^16

@@ -25,7 +25,7 @@
 //             (|C| < 127 * 127 * K) and y = s * (C2*2^16 + C1*2^8 + C0) * s[j].
 //             The rounding of x to 24 bits keeps y within ~1e-7 of
 //             max|x| * sum|q*s|; a row with a non-finite or extreme value
-//             takes the reference's sequential f32 sum (expert_mm order).
+//             takes expert_mm's own f32 sum (a.dot's blocked order).
 //   act       h = silu(g) * u   or   gelu_tanh(g[:mi]) * g[mi:], written
 //             directly as the digits (and f32 copy) the down GEMM reads.
 //   combine   out[t,:] = sum over t's experts in ascending expert id of
@@ -95,6 +95,21 @@ MoeWs moe_view(void* base, const MoeBank& b, size_t T, size_t k) {
     v.hso = (float*)take(P * 4);
     v.dn = (float*)take(P * b.d * 4);
     return v;
+}
+
+// y_j = x . (q[:, j] * s) over K in a.dot's order (expert_mm's x.dot(&wv):
+// MM_KC-long k blocks, each an FMA chain from +0, added in order), q an
+// (in, out) int8 matrix with row pitch ldq: the exact rows, whose digits
+// cannot carry the activations.
+__device__ __forceinline__ float exact_col(const float* __restrict__ x, const int8_t* __restrict__ q, int ldq, int j,
+                                           float s, int K) {
+    float c = 0.0f;
+    for (int k0 = 0; k0 < K; k0 += MM_KC) {
+        float ab = 0.0f;
+        for (int k = k0; k < min(K, k0 + MM_KC); ++k) ab = __builtin_fmaf(x[k], (float)q[(size_t)k * ldq + j] * s, ab);
+        c = c + ab;
+    }
+    return c;
 }
 
 // The gates and the softmax use the restated glibc expf / fdlibm tanhf
@@ -620,7 +635,7 @@ __global__ __launch_bounds__(64 * KS) void moe_mm_kernel(
                 for (int c = 0; c < CB; ++c) acc[t][c] += red[q][t][c][lane];
     }
     // y = s * (C2 * 2^16 + C1 * 2^8 + C0) * wsc[e, j]; rows whose digits do not
-    // carry them take the reference's sequential sum x . (q * s)
+    // carry them take expert_mm's own sum x . (q * s), a.dot's order
     const int col = lane & 15, tok = lane >> 4;
     const float* __restrict__ se = wsc + (size_t)e * N;
 #pragma unroll
@@ -639,11 +654,7 @@ __global__ __launch_bounds__(64 * KS) void moe_mm_kernel(
                 const v4i a4 = acc[t][c];
                 v = so * ((float)a4[0] * 65536.0f + ((float)a4[1] * 256.0f + (float)a4[2])) * se[j];
             } else {
-                const float* xr = xf + (size_t)src * K;
-                const int8_t* qe = wkn + (size_t)e * K * N;
-                const float sj = se[j];
-                v = 0.0f;
-                for (int k = 0; k < K; ++k) v = __builtin_fmaf(xr[k], (float)qe[(size_t)k * N + j] * sj, v);
+                v = exact_col(xf + (size_t)src * K, wkn + (size_t)e * K * N, N, j, se[j], K);
             }
             y[(size_t)prow * N + j] = v;
         }
@@ -765,7 +776,7 @@ __device__ __forceinline__ void gmm_body(const GmmArgs& A, v4i (*As)[GM_AS], con
         }
     }
     // y = s * (C2 * 2^16 + C1 * 2^8 + C0) * wsc[e, j]; rows whose digits do not
-    // carry them take the reference's sequential sum x . (q * s)
+    // carry them take expert_mm's own sum x . (q * s), a.dot's order
     const int col = lane & 15, tok = lane >> 4;
     const float* __restrict__ se = A.wsc + (size_t)e * A.N;
 #pragma unroll
@@ -784,11 +795,7 @@ __device__ __forceinline__ void gmm_body(const GmmArgs& A, v4i (*As)[GM_AS], con
                         v = so * ((float)a4[0] * 65536.0f + ((float)a4[1] * 256.0f + (float)a4[2])) * se[j];
                     } else {
                         const float* xr = A.xf + (size_t)src * A.K;
-                        const int8_t* qe = A.wkn + (size_t)e * A.K * A.N;
-                        const float sj = se[j];
-                        v = 0.0f;
-                        for (int k = 0; k < A.K; ++k)
-                            v = __builtin_fmaf(xr[k], (float)qe[(size_t)k * A.N + j] * sj, v);
+                        v = exact_col(xr, A.wkn + (size_t)e * A.K * A.N, A.N, j, se[j], A.K);
                     }
                     A.y[(size_t)prow * A.N + j] = v;
                 }
@@ -918,9 +925,7 @@ __global__ __launch_bounds__(256) void moe_dec_gu_kernel(
     if (so >= 0.0f) {
         v = so * ((float)acc[0] * 65536.0f + ((float)acc[1] * 256.0f + (float)acc[2])) * sj;
     } else {
-        const int8_t* qe = (isg ? gate : up) + (size_t)e * d * N;
-        v = 0.0f;
-        for (int k = 0; k < d; ++k) v = __builtin_fmaf(x[k], (float)qe[(size_t)k * N + j] * sj, v);
+        v = exact_col(x, (isg ? gate : up) + (size_t)e * d * N, N, j, sj, d);
     }
     (isg ? g : u)[(size_t)slot * N + j] = v;
 }
@@ -964,10 +969,7 @@ __global__ __launch_bounds__(1024) void moe_dec_down_kernel(
         if (so >= 0.0f) {
             v = so * ((float)acc[0] * 65536.0f + ((float)acc[1] * 256.0f + (float)acc[2])) * sj;
         } else {
-            const float* xr = h + (size_t)slot * mi;
-            const int8_t* qe = down + (size_t)e * mi * d;
-            v = 0.0f;
-            for (int k = 0; k < mi; ++k) v = __builtin_fmaf(xr[k], (float)qe[(size_t)k * d + j] * sj, v);
+            v = exact_col(h + (size_t)slot * mi, down + (size_t)e * mi * d, d, j, sj, mi);
         }
         vs[slot][lane] = v;
     }
@@ -1137,14 +1139,8 @@ __global__ __launch_bounds__(256) void moe_dec_gua_kernel(
         ga = sx * ((float)acca[0] * 65536.0f + ((float)acca[1] * 256.0f + (float)acca[2])) * sa;
         gb = sx * ((float)accb[0] * 65536.0f + ((float)accb[1] * 256.0f + (float)accb[2])) * sb;
     } else {
-        const int8_t* qa = a_q + (size_t)e * d * na;
-        const int8_t* qb = b_q + (size_t)e * d * nbw;
-        ga = 0.0f;
-        gb = 0.0f;
-        for (int k = 0; k < d; ++k) {
-            ga = __builtin_fmaf(x[k], (float)qa[(size_t)k * na + j] * sa, ga);
-            gb = __builtin_fmaf(x[k], (float)qb[(size_t)k * nbw + boff + j] * sb, gb);
-        }
+        ga = exact_col(x, a_q + (size_t)e * d * na, na, j, sa, d);
+        gb = exact_col(x, b_q + (size_t)e * d * nbw, nbw, boff + j, sb, d);
     }
     h[(size_t)slot * mi + j] = act == FRQ_ACT_SILU ? silu(ga) * gb : gelu_tanh(ga) * gb;
 }
@@ -1263,9 +1259,7 @@ __global__ __launch_bounds__(1024) void moe_dec_dn_kernel(
         if (ok) {
             v = so * ((float)acc[0] * 65536.0f + ((float)acc[1] * 256.0f + (float)acc[2])) * sj;
         } else {
-            const int8_t* qe = down + (size_t)e * mi * d;
-            v = 0.0f;
-            for (int k = 0; k < mi; ++k) v = __builtin_fmaf(hr[k], (float)qe[(size_t)k * d + j] * sj, v);
+            v = exact_col(hr, down + (size_t)e * mi * d, d, j, sj, mi);
         }
         vs[slot][lane] = v;
     }
@@ -1471,10 +1465,7 @@ __global__ void expert_mm_kernel(const float* __restrict__ x, int m, const int8_
     const int j = blockIdx.x * blockDim.x + threadIdx.x;
     const int i = blockIdx.y;
     if (j >= N || i >= m) return;
-    float acc = 0.0f;
-    for (int k = 0; k < K; ++k)
-        acc = __builtin_fmaf(x[(size_t)i * K + k], (float)q[(size_t)k * N + j] * s[j], acc);
-    y[(size_t)i * N + j] = acc;
+    y[(size_t)i * N + j] = exact_col(x + (size_t)i * K, q, N, j, s[j], K);
 }
 
 hipError_t launch_expert_mm(const int8_t* q, const float* s, size_t inp,

@@ -9,9 +9,10 @@
 //           q * a, a lanes add chains of a), each folded by hsum256
 //           ((l0+l4)+(l2+l6)) + ((l1+l5)+(l3+l7)), a mul+add tail, then
 //           sum += scale*qsum + min*asum across the groups in order.
-//   M > 1:  the dequantised weight (scale*q + min, a mul then an add) and a
-//           sequential-k FMA chain per output (the order the oracle takes
-//           for ndarray's sgemm): q4a_rows_chain, a thread per (row, token),
+//   M > 1:  the dequantised weight (scale*q + min, a mul then an add) and
+//           a.dot's order per output (matrixmultiply's sgemm: MM_KC-long k
+//           blocks, each an FMA chain from +0, added in order):
+//           q4a_rows_chain, a thread per (row, token),
 //           where K and g are multiples of 32, else q4a_gemm_rows.
 // Both bit-exact to the oracle.
 //
@@ -150,28 +151,35 @@ __global__ __launch_bounds__(QT) void q4a_gemm_rows(const uint8_t* __restrict__ 
     const int ng = (K + g - 1) / g;
     const uint8_t* prow = packed + (size_t)j * pitch;
     const uint32_t* srow = sm + (size_t)j * ng;
-    float acc[MT];
+    float acc[MT], tot[MT];
 #pragma unroll
-    for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
-    for (int kk = 0; kk < K; ++kk) {
-        const uint8_t byte = prow[kk >> 1];
-        const uint32_t s = srow[kk / g];
-        const float w = h2f((uint16_t)(s & 0xffffu)) * (float)((kk & 1) ? (byte >> 4) : (byte & 15)) +
-                        h2f((uint16_t)(s >> 16));
+    for (int m = 0; m < MT; ++m) tot[m] = 0.0f;
+    for (int k0 = 0; k0 < K; k0 += MM_KC) {
 #pragma unroll
-        for (int m = 0; m < MT; ++m)
-            if (m0 + m < M) acc[m] = __builtin_fmaf(a[(size_t)(m0 + m) * K + kk], w, acc[m]);
+        for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
+        for (int kk = k0; kk < min(K, k0 + MM_KC); ++kk) {
+            const uint8_t byte = prow[kk >> 1];
+            const uint32_t s = srow[kk / g];
+            const float w = h2f((uint16_t)(s & 0xffffu)) * (float)((kk & 1) ? (byte >> 4) : (byte & 15)) +
+                            h2f((uint16_t)(s >> 16));
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+                if (m0 + m < M) acc[m] = __builtin_fmaf(a[(size_t)(m0 + m) * K + kk], w, acc[m]);
+        }
+#pragma unroll
+        for (int m = 0; m < MT; ++m) tot[m] = tot[m] + acc[m];
     }
 #pragma unroll
     for (int m = 0; m < MT; ++m)
-        if (m0 + m < M) out[(size_t)(m0 + m) * N + j] = acc[m];
+        if (m0 + m < M) out[(size_t)(m0 + m) * N + j] = tot[m];
 }
 
 // M > 1 with K % 32 == 0, g % 32 == 0 and 16-byte aligned activation rows:
 // one thread per (column j, token row blockIdx.y), the packed row read 16
 // bytes (32 nibbles) and the token's 32 activations (uniform across the
 // workgroup) at a time, one chunk ahead of the chain.  The order per output
-// is q4a_gemm_rows' (kk ascending, w = scale * q + min), bit for bit.
+// is q4a_gemm_rows' (a.dot's blocks over kk, w = scale * q + min), bit for
+// bit.
 __global__ __launch_bounds__(QT) void q4a_rows_chain(const uint8_t* __restrict__ packed, size_t pitch,
                                                      const uint32_t* __restrict__ sm, int N, int K, int g,
                                                      const float* __restrict__ a, float* __restrict__ out) {
@@ -205,12 +213,23 @@ __global__ __launch_bounds__(QT) void q4a_rows_chain(const uint8_t* __restrict__
                 acc = __builtin_fmaf(x[q], sc * (float)((ws[c4] >> (4 * q)) & 15u) + mn, acc);
         }
     };
+    // a.dot's blocks: MM_KC / 32 chunks (an even count) each, folded in
+    // where a block starts (an even chunk)
+    static_assert(MM_KC % 64 == 0, "blocks start on even chunks");
+    float tot = 0.0f;
+    auto fold = [&](int i) {
+        if (i > 0 && i % (MM_KC / 32) == 0) {
+            tot = tot + acc;
+            acc = 0.0f;
+        }
+    };
     Chunk c0, c1;
     ld(c0, 0);
     ld(c1, min(1, nc - 1));
     __builtin_amdgcn_sched_barrier(0);
     int i = 0;
     for (; i + 2 <= nc; i += 2) {
+        fold(i);
         chain(c0);
         ld(c0, min(i + 2, nc - 1));
         __builtin_amdgcn_sched_barrier(0);
@@ -218,8 +237,11 @@ __global__ __launch_bounds__(QT) void q4a_rows_chain(const uint8_t* __restrict__
         ld(c1, min(i + 3, nc - 1));
         __builtin_amdgcn_sched_barrier(0);
     }
-    if (i < nc) chain(c0);
-    if (j < N) out[(size_t)m * N + j] = acc;
+    if (i < nc) {
+        fold(i);
+        chain(c0);
+    }
+    if (j < N) out[(size_t)m * N + j] = tot + acc;
 }
 
 }  // namespace

@@ -47,6 +47,10 @@ def _load():
         "fro_i4_dot_avx2": (F, [P, P, P, S, S]),
         "fro_mm_i4": (I, [P, S, S, P, P, S, S, P]),
         "fro_expert_mm_i8": (None, [P, S, P, P, S, S, P]),
+        "fro_expert_f32": (I, [P, S, S, P]),
+        "fro_expert_mm": (I, [P, P, S, S, S, P]),
+        "fro_moe_ex_mt": (I, [P, S, S, P, S, S, I, P, S, I, P, P, P, P, I]),
+        "fro_mm_dot": (F, [P, S, P, S, S]),
         "fro_sgemm": (None, [P, S, S, P, S, P]),
         "fro_silu": (F, [F]),
         "fro_gelu_tanh": (F, [F]),
@@ -232,6 +236,82 @@ def expert_mm_i8(x, raw_in_out, scale):
     y = np.empty((m, out), np.float32)
     lib.fro_expert_mm_i8(_p(x), m, _p(raw_in_out), _p(scale), inp, out, _p(y))
     return y
+
+
+class _Expert(C.Structure):
+    _fields_ = [("dtype", C.c_int), ("raw", C.c_void_p), ("scale", C.c_void_p), ("mins", C.c_void_p),
+                ("g", C.c_size_t)]
+
+
+EXPERT_DTYPES = {"i8": 1, "i4": 2, "f32": 3, "f16": 4, "q4a": 6}
+
+
+def expert(dtype, raw, scale=None, mins=None, g=0, inp=None, out=None):
+    """One stored expert weight (fro_expert_t) as a dict:
+    i8  raw (in,out) int8, scale f32 [out];
+    i4  raw (out, ceil(in/2)) uint8 nibbles, scale f32 (out, ceil(in/g)), g, inp;
+    q4a as i4 plus mins f32 (out, ceil(in/g));
+    f16 raw (in,out) uint16 f16 bits;  f32 raw (in,out) float32."""
+    if dtype in ("i8", "f16", "f32"):
+        dt = {"i8": np.int8, "f16": np.uint16, "f32": np.float32}[dtype]
+        raw = _c(raw, dt)
+        inp, out = raw.shape
+    else:
+        raw = _c(raw, np.uint8)
+        out = raw.shape[0]
+        assert inp is not None and g > 0
+    return {"dtype": dtype, "raw": raw, "scale": None if scale is None else _c(scale, np.float32),
+            "mins": None if mins is None else _c(mins, np.float32), "g": int(g), "inp": int(inp), "out": int(out)}
+
+
+def _ex_struct(e):
+    return _Expert(EXPERT_DTYPES[e["dtype"]], e["raw"].ctypes.data, None if e["scale"] is None else e["scale"].ctypes.data,
+                   None if e["mins"] is None else e["mins"].ctypes.data, e["g"])
+
+
+def expert_f32(e):
+    """expert_f32 (src/bundle.rs:404-454): the weight as f32 (in, out)."""
+    v = np.empty((e["inp"], e["out"]), np.float32)
+    st = _ex_struct(e)
+    if lib.fro_expert_f32(C.byref(st), e["inp"], e["out"], _p(v)) != 0:
+        raise ValueError(f"expert dtype {e['dtype']!r} unsupported")
+    return v
+
+
+def expert_mm(x, e):
+    """expert_mm (src/bundle.rs:457-461): x (m, in) . expert_f32."""
+    x = _c(x, np.float32)
+    m = x.shape[0]
+    y = np.empty((m, e["out"]), np.float32)
+    st = _ex_struct(e)
+    if lib.fro_expert_mm(C.byref(st), _p(x), m, e["inp"], e["out"], _p(y)) != 0:
+        raise ValueError(f"expert dtype {e['dtype']!r} unsupported")
+    return y
+
+
+def mm_dot(x, w):
+    """One element of a.dot: matrixmultiply 0.3.10's order over k (fro_mm_dot)."""
+    x, w = _c(x, np.float32), _c(w, np.float32)
+    return float(lib.fro_mm_dot(_p(x), 1, _p(w), 1, x.size))
+
+
+def moe_ex(x, logits, topk, norm_topk, gate, up, down, act=0, per_expert_scale=None, nthreads: int = 1):
+    """The routed expert layer over experts of any stored dtype (lists of
+    expert() dicts; up unused for act 1): fro_moe_ex_mt."""
+    x, logits = _c(x, np.float32), _c(logits, np.float32)
+    T, d = x.shape
+    E = logits.shape[1]
+    mi = down[0]["inp"]
+    arr = lambda lst: (_Expert * E)(*[_ex_struct(e) for e in lst])  # noqa: E731
+    g_, d_ = arr(gate), arr(down)
+    u_ = arr(up) if act == 0 else None
+    pes = None if per_expert_scale is None else _c(per_expert_scale, np.float32)
+    out = np.empty((T, d), np.float32)
+    rc = lib.fro_moe_ex_mt(_p(x), T, d, _p(logits), E, topk, int(norm_topk), _p(pes), mi, act, g_, u_, d_, _p(out),
+                           int(nthreads))
+    if rc != 0:
+        raise ValueError("unsupported expert dtype")
+    return out
 
 
 def silu(x: float) -> float:

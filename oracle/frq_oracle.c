@@ -25,6 +25,12 @@
 /* half::f16::from_f32 (src/convert.rs:147-155; round-to-nearest-even).       */
 /* ------------------------------------------------------------------------ */
 static size_t nz(size_t x) { return x ? x : 1; }
+/* The reference's FMA code paths are compiled for FMA hardware
+ * (#[target_feature(enable = "avx2,fma")] on i4_dot_avx2 / q4a_dot_avx2 /
+ * rowi8_dot_avx2, src/bundle.rs:158-258; matrixmultiply selects its FMA
+ * micro-kernel at run time): the functions that restate them use the FMA
+ * instruction for fmaf too (same values as the libm call, which is exact). */
+#define FRO_FMA __attribute__((target("fma")))
 static uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
 static float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
 
@@ -409,7 +415,7 @@ float fro_i4_dot(const uint8_t* prow, const float* a, const float* scale,
  * kk/2, i.e. nibbles 2*(kk/2)..+8), then hsum256 (146-153):
  * ((l0+l4)+(l2+l6)) + ((l1+l5)+(l3+l7)), then a scalar mul+add tail, then
  * sum += scale*gsum. */
-float fro_i4_dot_avx2(const uint8_t* prow, const float* a, const float* scale,
+FRO_FMA float fro_i4_dot_avx2(const uint8_t* prow, const float* a, const float* scale,
                       size_t g, size_t k) {
     float sum = 0.0f;
     size_t gi = 0, kk = 0;
@@ -432,18 +438,33 @@ float fro_i4_dot_avx2(const uint8_t* prow, const float* a, const float* scale,
     return sum;
 }
 
-/* f32 GEMM used where the reference calls ndarray's a.dot (matrixmultiply
- * 0.3.10 sgemm, Cargo.lock:1207).  Its k-blocking order is not visible in
- * the reference tree (parity unpinned); this is the sequential-k FMA order
- * of one register-blocked micro-kernel pass. */
+/* f32 GEMM where the reference calls ndarray's a.dot: ndarray 0.16.1 hands
+ * every f32 Array2 product to matrixmultiply 0.3.10's sgemm (Cargo.lock:1108,
+ * 1207; the default build has no BLAS feature, Cargo.toml:27).  That crate's
+ * published algorithm (gemm.rs gemm_loop, the BLIS loop nest) fixes each
+ * output element's summation order, whatever m, n and the strides:
+ *   - k is split into blocks of KC = 256 (archparam S_KC), in order;
+ *   - per block, the micro-kernel (the FMA one on an x86-64 host with
+ *     avx + fma, selected at run time) accumulates each C element in its own
+ *     register lane from +0, k ascending, one fused multiply-add a step;
+ *   - the first block stores C = AB (beta = 0), every later one C = C + AB
+ *     (beta = 1, alpha = 1: one rounding).
+ * fro_mm_dot is that order for one element (x stride xs, w stride ws). */
+FRO_FMA float fro_mm_dot(const float* x, size_t xs, const float* w, size_t ws, size_t k) {
+    float c = 0.0f;
+    for (size_t k0 = 0; k0 < k; k0 += FRO_MM_KC) {
+        const size_t k1 = k - k0 > FRO_MM_KC ? k0 + FRO_MM_KC : k;
+        float ab = 0.0f;
+        for (size_t kk = k0; kk < k1; kk++) ab = fmaf(x[kk * xs], w[kk * ws], ab);
+        c = k0 == 0 ? ab : c + ab;
+    }
+    return c;
+}
+
 void fro_sgemm(const float* x, size_t m, size_t k, const float* w, size_t n,
                float* y) {
     for (size_t i = 0; i < m; i++)
-        for (size_t j = 0; j < n; j++) {
-            float acc = 0.0f;
-            for (size_t kk = 0; kk < k; kk++) acc = fmaf(x[i * k + kk], w[kk * n + j], acc);
-            y[i * n + j] = acc;
-        }
+        for (size_t j = 0; j < n; j++) y[i * n + j] = fro_mm_dot(x + i * k, 1, w + j, n, k);
 }
 
 /* Bundle::mm I4 arm: src/bundle.rs:760-799.  M==1 -> i4_dot per output
@@ -462,9 +483,7 @@ int fro_mm_i4(const float* a, size_t m, size_t k, const uint8_t* packed,
         for (size_t kk = 0; kk < k; kk++)
             wcol[kk] = (float)nib_s4(packed + j * rb, kk) * scale[j * ng + kk / g];
         for (size_t i = 0; i < m; i++) {
-            float acc = 0.0f;
-            for (size_t kk = 0; kk < k; kk++) acc = fmaf(a[i * k + kk], wcol[kk], acc);
-            out[i * n + j] = acc;
+            out[i * n + j] = fro_mm_dot(a + i * k, 1, wcol, 1, k);
         }
     }
     free(wcol);
@@ -475,11 +494,8 @@ int fro_mm_i4(const float* a, size_t m, size_t k, const uint8_t* packed,
  * v[i,j] = (raw[i,j] as f32) * scale[j]; y = x . v  (W8A32). */
 void fro_expert_mm_i8(const float* x, size_t m, const int8_t* raw,
                       const float* scale, size_t inp, size_t out, float* y) {
-    float* v = (float*)malloc(nz(inp * out) * sizeof(float));
-    for (size_t i = 0; i < inp; i++)
-        for (size_t j = 0; j < out; j++) v[i * out + j] = (float)raw[i * out + j] * scale[j];
-    fro_sgemm(x, m, inp, v, out, y);
-    free(v);
+    const fro_expert_t e = {FRO_DT_I8, raw, scale, NULL, 0};
+    fro_expert_mm(&e, x, m, inp, out, y);
 }
 
 /* silu: src/qwen3moe.rs:38-40. */
@@ -547,9 +563,7 @@ void fro_moe_route(const float* logits, size_t T, size_t E, size_t topk,
 typedef struct {
     const float* x; size_t T, d, topk, mi, E; int act;
     const int32_t* sel; const float* w;
-    const int8_t* const* gate; const float* const* gate_scale;
-    const int8_t* const* up; const float* const* up_scale;
-    const int8_t* const* down; const float* const* down_scale;
+    const fro_expert_t* gate; const fro_expert_t* up; const fro_expert_t* down;
     float* dn;  /* (T*topk, d): the down output of (t, slot) */
     int w0, nw;
 } moe_job;
@@ -571,28 +585,26 @@ static void* moe_worker(void* arg) {
                 if ((size_t)J->sel[t * topk + i] == e) tok[nt++] = t * topk + i;
         if (!nt) continue;
         for (size_t r = 0; r < nt; r++) memcpy(rows + r * d, J->x + tok[r] / topk * d, d * sizeof(float));
-        fro_expert_mm_i8(rows, nt, J->gate[e], J->gate_scale[e], d, gw, g);
+        fro_expert_mm(&J->gate[e], rows, nt, d, gw, g);
         if (J->act == 0) {
-            fro_expert_mm_i8(rows, nt, J->up[e], J->up_scale[e], d, mi, u);
+            fro_expert_mm(&J->up[e], rows, nt, d, mi, u);
             for (size_t i = 0; i < nt * mi; i++) h[i] = fro_silu(g[i]) * u[i];
         } else {
             for (size_t r = 0; r < nt; r++)
                 for (size_t c = 0; c < mi; c++)
                     h[r * mi + c] = fro_gelu_tanh(g[r * gw + c]) * g[r * gw + c + mi];
         }
-        fro_expert_mm_i8(h, nt, J->down[e], J->down_scale[e], mi, d, dn);
+        fro_expert_mm(&J->down[e], h, nt, mi, d, dn);
         for (size_t r = 0; r < nt; r++) memcpy(J->dn + tok[r] * d, dn + r * d, d * sizeof(float));
     }
     free(rows); free(g); free(u); free(h); free(dn); free(tok);
     return NULL;
 }
 
-int fro_moe_mt(const float* x, size_t T, size_t d, const float* logits, size_t E,
-               size_t topk, int norm_topk, const float* pes, size_t mi, int act,
-               const int8_t* const* gate, const float* const* gate_scale,
-               const int8_t* const* up, const float* const* up_scale,
-               const int8_t* const* down, const float* const* down_scale,
-               float* out, int nthreads) {
+int fro_moe_ex_mt(const float* x, size_t T, size_t d, const float* logits, size_t E,
+                  size_t topk, int norm_topk, const float* pes, size_t mi, int act,
+                  const fro_expert_t* gate, const fro_expert_t* up, const fro_expert_t* down,
+                  float* out, int nthreads) {
     if (nthreads < 1) nthreads = 1;
     if (nthreads > 64) nthreads = 64;
     int32_t* sel = (int32_t*)malloc(nz(T * topk) * sizeof(int32_t));
@@ -602,8 +614,7 @@ int fro_moe_mt(const float* x, size_t T, size_t d, const float* logits, size_t E
     moe_job jobs[64];
     pthread_t th[64];
     for (int i = 0; i < nthreads; i++) {
-        moe_job J = {x, T, d, topk, mi, E, act, sel, w, gate, gate_scale, up, up_scale,
-                     down, down_scale, dn, i, nthreads};
+        moe_job J = {x, T, d, topk, mi, E, act, sel, w, gate, up, down, dn, i, nthreads};
         jobs[i] = J;
     }
     if (nthreads == 1) {
@@ -623,6 +634,25 @@ int fro_moe_mt(const float* x, size_t T, size_t d, const float* logits, size_t E
                 }
     free(sel); free(w); free(dn);
     return FRO_OK;
+}
+
+/* The int8 bank (every expert an i8 (in,out) array with f32 scales). */
+int fro_moe_mt(const float* x, size_t T, size_t d, const float* logits, size_t E,
+               size_t topk, int norm_topk, const float* pes, size_t mi, int act,
+               const int8_t* const* gate, const float* const* gate_scale,
+               const int8_t* const* up, const float* const* up_scale,
+               const int8_t* const* down, const float* const* down_scale,
+               float* out, int nthreads) {
+    fro_expert_t* ex = (fro_expert_t*)calloc(nz(3 * E), sizeof(fro_expert_t));
+    for (size_t e = 0; e < E; e++) {
+        ex[e] = (fro_expert_t){FRO_DT_I8, gate[e], gate_scale[e], NULL, 0};
+        if (act == 0) ex[E + e] = (fro_expert_t){FRO_DT_I8, up[e], up_scale[e], NULL, 0};
+        ex[2 * E + e] = (fro_expert_t){FRO_DT_I8, down[e], down_scale[e], NULL, 0};
+    }
+    int rc = fro_moe_ex_mt(x, T, d, logits, E, topk, norm_topk, pes, mi, act, ex, ex + E, ex + 2 * E, out,
+                           nthreads);
+    free(ex);
+    return rc;
 }
 
 int fro_moe(const float* x, size_t T, size_t d, const float* logits, size_t E,
@@ -646,7 +676,7 @@ int fro_moe(const float* x, size_t T, size_t d, const float* logits, size_t E,
  * lane q an FMA chain over k = 8i + q, hsum256 (146-153), then a mul + add
  * tail.  rowi8, subset (or a host without AVX2+FMA, 980): scale * the fold
  * from -0.0 (1011). */
-static float row_dot(int dtype, const void* data, const float* scale, size_t r,
+FRO_FMA static float row_dot(int dtype, const void* data, const float* scale, size_t r,
                      size_t d, const float* x, int avx2) {
     if (dtype == 3) {
         const float* w = (const float*)data + r * d;
@@ -760,7 +790,7 @@ static int8_t kv_q8(float v, float sc) {
 /* forward_block / forward_block_q: m rows at absolute positions cur..cur+m
  * through every layer; x (m, d) in, the pre-final-LN hidden states out (in
  * place).  The attention products are matrixmultiply sgemms in the
- * reference; here each is a sequential-k FMA chain (fro_sgemm's order). */
+ * reference; each output element here is fro_mm_dot (their order). */
 static int g2_block(g2_run* R, float* x, size_t m, size_t cur) {
     const fro_gpt2_t* g = R->g;
     const size_t d = g->d, H = g->n_head, hd = d / H, klen = cur + m;
@@ -823,16 +853,12 @@ static int g2_block(g2_run* R, float* x, size_t m, size_t cur) {
                 const float* q = qkv + i * 3 * d + h * hd;
                 float* s = sc + i * klen;
                 for (size_t j = 0; j < klen; j++) {
-                    float acc = 0.0f;
-                    for (size_t c = 0; c < hd; c++) acc = fmaf(q[c], kh[j * hd + c], acc);
-                    s[j] = acc / rs;
+                    s[j] = fro_mm_dot(q, 1, kh + j * hd, 1, hd) / rs;
                 }
                 for (size_t j = cur + i + 1; j < klen; j++) s[j] = -1e10f;  /* causal mask */
                 softmax_row(s, klen);
                 for (size_t c = 0; c < hd; c++) {
-                    float acc = 0.0f;
-                    for (size_t j = 0; j < klen; j++) acc = fmaf(s[j], vh[j * hd + c], acc);
-                    att[i * d + h * hd + c] = acc;
+                    att[i * d + h * hd + c] = fro_mm_dot(s, 1, vh + c, hd, klen);
                 }
             }
         }
@@ -1028,7 +1054,7 @@ float fro_q4a_dot(const uint8_t* prow, const float* a, const float* scale, const
  * (q * a), a lanes an add chain, over the 8-nibble chunks read from byte
  * kk/2 (unpack8_nibbles); each set through hsum256; a mul+add tail; then
  * sum += scale*qsum + min*asum. */
-float fro_q4a_dot_avx2(const uint8_t* prow, const float* a, const float* scale, const float* mins, size_t g,
+FRO_FMA float fro_q4a_dot_avx2(const uint8_t* prow, const float* a, const float* scale, const float* mins, size_t g,
                        size_t k) {
     float sum = 0.0f;
     size_t gi = 0, kk = 0;
@@ -1057,7 +1083,7 @@ float fro_q4a_dot_avx2(const uint8_t* prow, const float* a, const float* scale, 
 
 /* Bundle::mm Q4A arm: src/bundle.rs:802-845.  M==1 -> q4a_dot per output
  * column (AVX2 order); M>1 -> w[kk,col] = scale*q + min (f32, mul then
- * add, 826-829) then a.dot(w) (the sequential-k FMA order of fro_sgemm). */
+ * add, 826-829) then a.dot(w) (fro_mm_dot: matrixmultiply's order). */
 int fro_mm_q4a(const float* a, size_t m, size_t k, const uint8_t* packed, const float* scale, const float* mins,
                size_t n, size_t g, float* out) {
     size_t ng = (k + g - 1) / g, rb = (k + 1) / 2;
@@ -1073,13 +1099,59 @@ int fro_mm_q4a(const float* a, size_t m, size_t k, const uint8_t* packed, const 
             wcol[kk] = scale[gi] * (float)nib_u4(packed + j * rb, kk) + mins[gi];
         }
         for (size_t i = 0; i < m; i++) {
-            float acc = 0.0f;
-            for (size_t kk = 0; kk < k; kk++) acc = fmaf(a[i * k + kk], wcol[kk], acc);
-            out[i * n + j] = acc;
+            out[i * n + j] = fro_mm_dot(a + i * k, 1, wcol, 1, k);
         }
     }
     free(wcol);
     return FRO_OK;
+}
+
+/* expert_f32: src/bundle.rs:404-454, one arm per stored dtype, each value
+ * as the reference forms it (f32 arithmetic, no contraction):
+ *   i8  (410-420)  v[i,j] = (q[i,j] as f32) * scale[j]
+ *   i4  (421-433)  v[i,j] = (s4(nib(j,i)) as f32) * scale[j*ng + i/g]
+ *                  (stored (out,in), transposed while dequantising)
+ *   q4a (434-448)  v[i,j] = scale[gi] * (u4(nib(j,i)) as f32) + mins[gi]
+ *   f16 (449)      v = f16 -> f32;  f32 (450) as stored. */
+int fro_expert_f32(const fro_expert_t* e, size_t inp, size_t out, float* v) {
+    switch (e->dtype) {
+        case FRO_DT_I8: {
+            const int8_t* q = (const int8_t*)e->raw;
+            for (size_t i = 0; i < inp; i++)
+                for (size_t j = 0; j < out; j++) v[i * out + j] = (float)q[i * out + j] * e->scale[j];
+            return FRO_OK;
+        }
+        case FRO_DT_I4:
+        case FRO_DT_Q4A: {
+            const uint8_t* p = (const uint8_t*)e->raw;
+            const size_t g = e->g, ng = (inp + g - 1) / g, rb = (inp + 1) / 2;
+            for (size_t j = 0; j < out; j++)
+                for (size_t i = 0; i < inp; i++) {
+                    const size_t gi = j * ng + i / g;
+                    v[i * out + j] = e->dtype == FRO_DT_I4
+                                         ? (float)nib_s4(p + j * rb, i) * e->scale[gi]
+                                         : e->scale[gi] * (float)nib_u4(p + j * rb, i) + e->mins[gi];
+                }
+            return FRO_OK;
+        }
+        case FRO_DT_F16:
+            fro_f16_to_f32_n((const uint16_t*)e->raw, v, inp * out);
+            return FRO_OK;
+        case FRO_DT_F32:
+            memcpy(v, e->raw, inp * out * sizeof(float));
+            return FRO_OK;
+        default:
+            return FRO_ERR_ARG;
+    }
+}
+
+/* expert_mm: src/bundle.rs:457-461, x.dot(&expert_f32) (fro_sgemm). */
+int fro_expert_mm(const fro_expert_t* e, const float* x, size_t m, size_t inp, size_t out, float* y) {
+    float* v = (float*)malloc(nz(inp * out) * sizeof(float));
+    int rc = fro_expert_f32(e, inp, out, v);
+    if (rc == FRO_OK) fro_sgemm(x, m, inp, v, out, y);
+    free(v);
+    return rc;
 }
 
 /* fro_mm_i4 with the output columns split over nthreads threads (each
@@ -1099,9 +1171,7 @@ static void* i4_worker(void* p) {
         for (size_t kk = 0; kk < J->k; kk++)
             wcol[kk] = (float)nib_s4(J->packed + j * rb, kk) * J->scale[j * ng + kk / J->g];
         for (size_t i = 0; i < J->m; i++) {
-            float acc = 0.0f;
-            for (size_t kk = 0; kk < J->k; kk++) acc = fmaf(J->a[i * J->k + kk], wcol[kk], acc);
-            J->out[i * J->n + j] = acc;
+            J->out[i * J->n + j] = fro_mm_dot(J->a + i * J->k, 1, wcol, 1, J->k);
         }
     }
     free(wcol);
@@ -1261,8 +1331,7 @@ static int gm_block(gm_run* R, float* x, size_t m, size_t cur) {
                 const float* qr = q + i * H * hd + h * hd;
                 const size_t abs_ = cur + i;
                 for (size_t j = 0; j < klen; j++) {
-                    float acc = 0.0f;
-                    for (size_t c = 0; c < hd; c++) acc = fmaf(qr[c], kh[j * hd + c], acc);
+                    const float acc = fro_mm_dot(qr, 1, kh + j * hd, 1, hd);
                     float s = g->arch == 1 ? acc / sqrtf((float)hd) : acc * g->qscale;
                     if (g->arch == 0 && g->attn_cap > 0.0f) s = g->attn_cap * tanhf(s / g->attn_cap);
                     if (j > abs_ || (sliding && abs_ >= g->window && j <= abs_ - g->window)) s = -1e30f;
@@ -1270,9 +1339,7 @@ static int gm_block(gm_run* R, float* x, size_t m, size_t cur) {
                 }
                 softmax_row(sc, klen);
                 for (size_t c = 0; c < hd; c++) {
-                    float acc = 0.0f;
-                    for (size_t j = 0; j < klen; j++) acc = fmaf(sc[j], vh[j * hd + c], acc);
-                    att[i * H * hd + h * hd + c] = acc;
+                    att[i * H * hd + h * hd + c] = fro_mm_dot(sc, 1, vh + c, hd, klen);
                 }
             }
         }

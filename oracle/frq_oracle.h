@@ -65,6 +65,9 @@ extern "C" {
 #define FRO_OK 0
 #define FRO_ERR_ARG 1 /* an index the reference would panic on          */
 #define FRO_ERR_NAN 3 /* reference panics in partial_cmp().unwrap() */
+#define FRO_DT_I8 1  /* expert / linear weight types (bundle.rs Arr) */
+#define FRO_DT_I4 2
+#define FRO_DT_Q4A 6
 #define FRO_DT_F32 3 /* the row-dot table types (bundle.rs Arr) */
 #define FRO_DT_F16 4
 #define FRO_DT_ROWI8 5
@@ -130,7 +133,32 @@ int fro_mm_q4a(const float* a, size_t m, size_t k, const uint8_t* packed, const 
 /* expert_f32 (i8 arm) + expert_mm: raw (in,out) i8, scale f32 [out]. */
 void fro_expert_mm_i8(const float* x, size_t m, const int8_t* raw,
                       const float* scale, size_t inp, size_t out, float* y);
-/* f32 GEMM y(m,n) = x(m,k) . w(k,n), sequential-k FMA order. */
+/* One MoE expert weight as the bundle stores it (src/bundle.rs:288-294,
+ * 404-454): dtype FRO_DT_I8 (raw (in,out) i8, scale [out]), FRO_DT_I4
+ * (raw (out, ceil(in/2)) packed nibbles, even input index low, scale
+ * (out, ceil(in/g))), FRO_DT_Q4A (as i4 with unsigned nibbles and mins
+ * (out, ceil(in/g))), FRO_DT_F16 (raw (in,out) f16 bits) or FRO_DT_F32
+ * (raw (in,out) f32).  Scales and mins are the f32 upcasts of the f16
+ * __scale / __min siblings (arr1o). */
+typedef struct {
+    int dtype;
+    const void* raw;
+    const float* scale;
+    const float* mins;
+    size_t g;
+} fro_expert_t;
+/* expert_f32: the weight dequantised to f32 (in, out) row-major (v has
+ * inp*out entries).  FRO_ERR_ARG for an unknown dtype (the reference
+ * panics, :452). */
+int fro_expert_f32(const fro_expert_t* e, size_t inp, size_t out, float* v);
+/* expert_mm (src/bundle.rs:457-461): y (m,out) = x (m,inp) . expert_f32. */
+int fro_expert_mm(const fro_expert_t* e, const float* x, size_t m, size_t inp, size_t out, float* y);
+/* One element of a.dot (matrixmultiply 0.3.10 sgemm): k split into blocks
+ * of FRO_MM_KC in order, each an FMA chain from +0, the block results added
+ * in order (the first stored as is). */
+#define FRO_MM_KC 256
+float fro_mm_dot(const float* x, size_t xs, const float* w, size_t ws, size_t k);
+/* f32 GEMM y(m,n) = x(m,k) . w(k,n), each element fro_mm_dot. */
 void fro_sgemm(const float* x, size_t m, size_t k, const float* w, size_t n,
                float* y);
 
@@ -162,6 +190,12 @@ int fro_moe_mt(const float* x, size_t T, size_t d, const float* logits, size_t E
             const float* const* gate_scale, const int8_t* const* up,
             const float* const* up_scale, const int8_t* const* down,
             const float* const* down_scale, float* out, int nthreads);
+/* The same layer over experts of any stored dtype (fro_expert_t, arrays of
+ * E each; up is ignored for act 1), on nthreads threads. */
+int fro_moe_ex_mt(const float* x, size_t T, size_t d, const float* logits, size_t E,
+                  size_t topk, int norm_topk, const float* per_expert_scale,
+                  size_t mi, int act, const fro_expert_t* gate, const fro_expert_t* up,
+                  const fro_expert_t* down, float* out, int nthreads);
 
 /* Bundle::rowdot_f32 / rowdot_f32_subset over a row-major (rows, d) table:
  * dtype 3 f32 (float data), 4 f16 (uint16 bits), 5 rowi8 (int8 data +
