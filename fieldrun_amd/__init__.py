@@ -63,6 +63,8 @@ SIGNATURES = {
     "frq_quant_i8_dev": (_I, [_P, _P, _S, _S, _P, _P, _P, _P]),
     "frq_mm_i8_q_dev": (_I, [_P, _P, _P, _P, _P, _P, _S, _P]),
     "frq_moe_upload_i8": (_P, [_P, _S, _S, _S, _I, _P, _P, _P, _P, _P, _P]),
+    "frq_moe_upload": (_P, [_P, _I, _S, _S, _S, _I, _S, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "frq_moe_info": (_I, [_P, _P, _P, _P, _P, _P]),
     "frq_moe_free": (None, [_P]),
     "frq_moe": (_I, [_P, _P, _P, _S, _P, _S, _I, _P, _P]),
     "frq_moe_dev": (_I, [_P, _P, _P, _S, _P, _S, _I, _P, _P]),
@@ -258,6 +260,38 @@ class Context:
             raise FrqError(FRQ_ERR_HIP, lib.frq_last_error().decode())
         return MoeBank(self, h, E, d, mi, act)
 
+    def upload_moe(self, dtype: str, d: int, mi: int, gate, down, up=None, gate_scale=None, up_scale=None,
+                   down_scale=None, gate_min=None, up_min=None, down_min=None, act: int = FRQ_ACT_SILU,
+                   g: int = 0) -> "MoeBank":
+        """An expert bank in the dtype its bundle stores (frq_moe_upload):
+        lists over experts of the stored arrays.  'i8': (in, out) int8 with
+        f16-bit [out] scales; 'i4' / 'q4a': packed (out, ceil(in/2)) uint8 with
+        f16-bit (out, ceil(in/g)) scales (and q4a mins); 'f16': (in, out)
+        f16 bits; 'f32': (in, out) float32.  d / mi: the layer's widths."""
+        code, raw_dt = {"i8": (FRQ_DT_I8, np.int8), "i4": (FRQ_DT_I4, np.uint8), "q4a": (FRQ_DT_Q4A, np.uint8),
+                        "f16": (FRQ_DT_F16, np.uint16), "f32": (FRQ_DT_F32, np.float32)}[dtype]
+        E = len(gate)
+        keep = []
+
+        def arr(lst, dt):
+            if lst is None:
+                return None
+            ptrs = (C.c_void_p * E)()
+            for i, a in enumerate(lst):
+                a = np.ascontiguousarray(a, dtype=dt)
+                keep.append(a)
+                ptrs[i] = a.ctypes.data
+            return ptrs
+
+        silu = act == FRQ_ACT_SILU
+        h = lib.frq_moe_upload(self.h, code, E, d, mi, act, g, arr(gate, raw_dt), arr(gate_scale, np.uint16),
+                               arr(gate_min, np.uint16), arr(up, raw_dt) if silu else None,
+                               arr(up_scale, np.uint16) if silu else None, arr(up_min, np.uint16) if silu else None,
+                               arr(down, raw_dt), arr(down_scale, np.uint16), arr(down_min, np.uint16))
+        if not h:
+            raise FrqError(FRQ_ERR_ARG, lib.frq_last_error().decode())
+        return MoeBank(self, h, E, d, mi, act)
+
     def moe_route(self, logits: np.ndarray, topk: int, norm_topk: bool = True,
                   per_expert_scale: np.ndarray | None = None):
         logits = np.ascontiguousarray(logits, dtype=np.float32)
@@ -381,6 +415,9 @@ class MoeBank:
 
     def __init__(self, ctx, h, E, d, mi, act):
         self.ctx, self.h, self.E, self.d, self.mi, self.act = ctx, h, E, d, mi, act
+        dt, g = C.c_int(), C.c_size_t()
+        _check(lib.frq_moe_info(h, C.byref(dt), None, None, None, C.byref(g)))
+        self.dtype, self.g = dt.value, g.value
 
     def free(self):
         if self.h:
@@ -524,9 +561,9 @@ class Bundle:
         out = C.c_void_p()
         _check(lib.frq_bundle_moe(self.ctx.h, self.h, prefix.encode(), n_exp, act, C.byref(out)))
         h = out.value
-        _, shape, _, _ = self.info(prefix + "experts.0.down")
-        mi, d = shape
-        return MoeBank(self.ctx, h, n_exp, d, mi, act)
+        d, mi = C.c_size_t(), C.c_size_t()
+        _check(lib.frq_moe_info(h, None, None, C.byref(d), C.byref(mi), None))
+        return MoeBank(self.ctx, h, n_exp, d.value, mi.value, act)
 
 
 class Gpt2:

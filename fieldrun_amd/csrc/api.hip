@@ -10,6 +10,7 @@
 //   int4                   -> blocked W4A32 GEMV (M == 1) / batched kernel
 // Every failure becomes an int status plus frq_last_error(); nothing throws.
 #include <atomic>
+#include <cstring>
 #include <mutex>
 #include <new>
 #include <string>
@@ -847,6 +848,127 @@ frq_moe_w* frq_moe_upload_i8(frq_ctx* c, size_t n_exp, size_t d, size_t mi, int 
     return h;
 }
 
+// A bank whose experts are stored as i4, q4a, f16 or f32 (the arms of
+// expert_f32, src/bundle.rs:404-454): each matrix of every expert copied as
+// stored, plus the int4 MFMA operand copy where g % 32 == 0.
+static frq_moe_w* moe_upload_ex(frq_ctx* c, int dtype, size_t n_exp, size_t d, size_t mi, int act, size_t g,
+                                const void* const* gate, const uint16_t* const* gate_scale,
+                                const uint16_t* const* gate_min, const void* const* up,
+                                const uint16_t* const* up_scale, const uint16_t* const* up_min,
+                                const void* const* down, const uint16_t* const* down_scale,
+                                const uint16_t* const* down_min) {
+    const bool q = dtype == FRQ_DT_I4 || dtype == FRQ_DT_Q4A;
+    if (q && g == 0) {
+        fail(FRQ_ERR_ARG, "frq_moe_upload: an i4 / q4a bank needs its group size");
+        return nullptr;
+    }
+    DeviceGuard dg(c->device);
+    frq_moe_w* h = new (std::nothrow) frq_moe_w;
+    if (!h) { fail(FRQ_ERR_ARG, "out of host memory"); return nullptr; }
+    MoeBank& b = h->b;
+    b.device = c->device; b.n_exp = n_exp; b.d = d; b.mi = mi; b.act = act; b.dtype = dtype; b.g = q ? g : 0;
+    b.gw = act == FRQ_ACT_SILU ? mi : 2 * mi;
+    const bool mfma = dtype == FRQ_DT_I4 && g % 32 == 0;
+    // digit rows of whole group quads for the int4 MFMA kernel (as the int8
+    // bank's, 64-input blocks, otherwise)
+    b.kpd = round_up(d, mfma ? 128 : 64);
+    b.kpm = round_up(mi, mfma ? 128 : 64);
+    hipError_t e = hipSuccess;
+    auto one = [&](ExpMat& m, size_t in, size_t out, const void* const* raw, const uint16_t* const* sc,
+                   const uint16_t* const* mn) {
+        m.in = in;
+        m.out = out;
+        const size_t ng = q ? (in + g - 1) / g : 0;
+        const size_t per = q ? out * ((in + 1) / 2) : in * out * (dtype == FRQ_DT_F16 ? 2 : 4);
+        e = hipMalloc(&m.raw, n_exp * per);
+        if (e == hipSuccess && q) e = hipMalloc(&m.sc, n_exp * out * ng * 2);
+        if (e == hipSuccess && dtype == FRQ_DT_Q4A) e = hipMalloc(&m.mn, n_exp * out * ng * 2);
+        for (size_t x = 0; x < n_exp && e == hipSuccess; ++x) {
+            if (!raw[x] || (q && !sc[x]) || (dtype == FRQ_DT_Q4A && !mn[x])) {
+                e = hipErrorInvalidValue;
+                break;
+            }
+            e = hipMemcpyAsync((char*)m.raw + x * per, raw[x], per, hipMemcpyHostToDevice, c->stream);
+            if (e == hipSuccess && q)
+                e = hipMemcpyAsync(m.sc + x * out * ng, sc[x], out * ng * 2, hipMemcpyHostToDevice, c->stream);
+            if (e == hipSuccess && dtype == FRQ_DT_Q4A)
+                e = hipMemcpyAsync(m.mn + x * out * ng, mn[x], out * ng * 2, hipMemcpyHostToDevice, c->stream);
+        }
+        if (e == hipSuccess && mfma) {
+            const size_t nrb = (out + 15) / 16, ng4 = (in + 127) / 128;
+            e = hipMalloc(&m.q4e, n_exp * nrb * ng4 * 1024);
+            if (e == hipSuccess) e = hipMalloc(&m.s4e, n_exp * nrb * ng4 * 128);
+            if (e == hipSuccess) e = launch_moe_i4_block(m, n_exp, g, c->stream);
+        }
+    };
+    one(b.mg, d, b.gw, gate, gate_scale, gate_min);
+    if (e == hipSuccess && act == FRQ_ACT_SILU) one(b.mu, d, mi, up, up_scale, up_min);
+    if (e == hipSuccess) one(b.md, mi, d, down, down_scale, down_min);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) {
+        hip_fail(e, "frq_moe_upload");
+        frq_moe_free(h);
+        return nullptr;
+    }
+    return h;
+}
+
+frq_moe_w* frq_moe_upload(frq_ctx* c, int dtype, size_t n_exp, size_t d, size_t mi, int act, size_t g,
+                          const void* const* gate, const uint16_t* const* gate_scale,
+                          const uint16_t* const* gate_min, const void* const* up, const uint16_t* const* up_scale,
+                          const uint16_t* const* up_min, const void* const* down,
+                          const uint16_t* const* down_scale, const uint16_t* const* down_min) {
+    const bool silu_ = act == FRQ_ACT_SILU;
+    if (check_ctx(c) || !n_exp || !d || !mi || !gate || !down || (silu_ && !up) ||
+        (act != FRQ_ACT_SILU && act != FRQ_ACT_GELU_TANH)) {
+        fail(FRQ_ERR_ARG, "frq_moe_upload: bad argument");
+        return nullptr;
+    }
+    if (dtype == FRQ_DT_I8) {  // the int8 bank, its f16 scales upcast (arr1o)
+        if (!gate_scale || !down_scale || (silu_ && !up_scale)) {
+            fail(FRQ_ERR_ARG, "frq_moe_upload: an i8 bank needs its scales");
+            return nullptr;
+        }
+        const size_t gw = silu_ ? mi : 2 * mi;
+        std::vector<std::vector<float>> gs(n_exp), us(n_exp), ds(n_exp);
+        std::vector<const float*> gsp(n_exp), usp(n_exp, nullptr), dsp(n_exp);
+        std::vector<const int8_t*> gp(n_exp), upp(n_exp, nullptr), dpp(n_exp);
+        auto up16 = [](const uint16_t* h16, size_t n, std::vector<float>& out) {
+            out.resize(n);
+            for (size_t i = 0; i < n; ++i) {  // the bundle's f16 arrays need not be 2-byte aligned
+                uint16_t v;
+                std::memcpy(&v, reinterpret_cast<const char*>(h16) + 2 * i, 2);
+                out[i] = h2f_host(v);
+            }
+        };
+        for (size_t x = 0; x < n_exp; ++x) {
+            if (!gate_scale[x] || !down_scale[x] || (silu_ && !up_scale[x])) {
+                fail(FRQ_ERR_ARG, "frq_moe_upload: null scale");
+                return nullptr;
+            }
+            up16(gate_scale[x], gw, gs[x]);
+            up16(down_scale[x], d, ds[x]);
+            gsp[x] = gs[x].data();
+            dsp[x] = ds[x].data();
+            gp[x] = (const int8_t*)gate[x];
+            dpp[x] = (const int8_t*)down[x];
+            if (silu_) {
+                up16(up_scale[x], mi, us[x]);
+                usp[x] = us[x].data();
+                upp[x] = (const int8_t*)up[x];
+            }
+        }
+        return frq_moe_upload_i8(c, n_exp, d, mi, act, gp.data(), gsp.data(), silu_ ? upp.data() : nullptr,
+                                 silu_ ? usp.data() : nullptr, dpp.data(), dsp.data());
+    }
+    if (dtype != FRQ_DT_I4 && dtype != FRQ_DT_Q4A && dtype != FRQ_DT_F16 && dtype != FRQ_DT_F32) {
+        fail(FRQ_ERR_DTYPE, "frq_moe_upload: expert dtype must be i8, i4, q4a, f16 or f32");
+        return nullptr;
+    }
+    return moe_upload_ex(c, dtype, n_exp, d, mi, act, g, gate, gate_scale, gate_min, up, up_scale, up_min, down,
+                         down_scale, down_min);
+}
+
 void frq_moe_free(frq_moe_w* h) {
     if (!h) return;
     MoeBank& b = h->b;
@@ -854,7 +976,20 @@ void frq_moe_free(frq_moe_w* h) {
     for (void* p : {(void*)b.gate, (void*)b.gate_s, (void*)b.up, (void*)b.up_s, (void*)b.down, (void*)b.down_s,
                     (void*)b.gate_b, (void*)b.up_b, (void*)b.down_b})
         if (p) (void)hipFree(p);
+    for (ExpMat* m : {&b.mg, &b.mu, &b.md})
+        for (void* p : {m->raw, (void*)m->sc, (void*)m->mn, (void*)m->q4e, (void*)m->s4e})
+            if (p) (void)hipFree(p);
     delete h;
+}
+
+int frq_moe_info(const frq_moe_w* h, int* dtype, size_t* n_exp, size_t* d, size_t* mi, size_t* g) {
+    if (!h) return fail(FRQ_ERR_ARG, "null MoE bank");
+    if (dtype) *dtype = h->b.dtype;
+    if (n_exp) *n_exp = h->b.n_exp;
+    if (d) *d = h->b.d;
+    if (mi) *mi = h->b.mi;
+    if (g) *g = h->b.g;
+    return FRQ_OK;
 }
 
 int frq_moe_dev(frq_ctx* c, const frq_moe_w* h, const float* d_x, size_t T,
@@ -936,13 +1071,20 @@ int frq_expert_mm(frq_ctx* c, const frq_moe_w* h, int which, size_t e, const flo
     if (!h) return fail(FRQ_ERR_ARG, "null MoE bank");
     const MoeBank& b = h->b;
     if (e >= b.n_exp) return fail(FRQ_ERR_MISSING, "expert index out of range");
-    const int8_t* q;
-    const float* s;
+    const int8_t* q = nullptr;
+    const float* s = nullptr;
+    const ExpMat* mt = nullptr;
     size_t inp, out;
-    if (which == 0) { q = b.gate + e * b.d * b.gw; s = b.gate_s + e * b.gw; inp = b.d; out = b.gw; }
-    else if (which == 1 && b.up) { q = b.up + e * b.d * b.mi; s = b.up_s + e * b.mi; inp = b.d; out = b.mi; }
-    else if (which == 2) { q = b.down + e * b.mi * b.d; s = b.down_s + e * b.d; inp = b.mi; out = b.d; }
-    else return fail(FRQ_ERR_MISSING, "no such expert bank");
+    const bool ex = b.dtype != FRQ_DT_I8;
+    if (which == 0) {
+        q = b.gate + e * b.d * b.gw; s = b.gate_s + e * b.gw; inp = b.d; out = b.gw; mt = &b.mg;
+    } else if (which == 1 && b.act == FRQ_ACT_SILU) {
+        q = b.up + e * b.d * b.mi; s = b.up_s + e * b.mi; inp = b.d; out = b.mi; mt = &b.mu;
+    } else if (which == 2) {
+        q = b.down + e * b.mi * b.d; s = b.down_s + e * b.d; inp = b.mi; out = b.d; mt = &b.md;
+    } else {
+        return fail(FRQ_ERR_MISSING, "no such expert bank");
+    }
     if (m == 0) return FRQ_OK;
     if (!x || !y) return fail(FRQ_ERR_ARG, "null pointer");
     DeviceGuard g(c->device);
@@ -951,7 +1093,8 @@ int frq_expert_mm(frq_ctx* c, const frq_moe_w* h, int which, size_t e, const flo
     float* dx = (float*)c->ws;
     float* dy = (float*)((char*)c->ws + xb);
     HIPCHK(hipMemcpyAsync(dx, x, m * inp * 4, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync");
-    HIPCHK(launch_expert_mm(q, s, inp, out, dx, m, dy, c->stream), "launch expert_mm");
+    if (ex) HIPCHK(launch_expert_mm_ex(b, *mt, e, dx, m, dy, c->stream), "launch expert_mm");
+    else HIPCHK(launch_expert_mm(q, s, inp, out, dx, m, dy, c->stream), "launch expert_mm");
     HIPCHK(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
     HIPCHK(hipMemcpy(y, dy, m * out * 4, hipMemcpyDeviceToHost), "hipMemcpy(y)");
     return FRQ_OK;

@@ -219,26 +219,6 @@ struct ArrSpec {
     size_t offset = 0, bytes = 0, group = 0;  // group 0: none
 };
 
-float f16_to_f32(uint16_t h) {
-    const uint32_t s = (uint32_t)(h >> 15) << 31, ex = (h >> 10) & 0x1F, m = h & 0x3FF;
-    uint32_t u;
-    if (ex == 0) {
-        if (!m) u = s;
-        else {  // subnormal: m * 2^-24
-            float f = std::ldexp((float)m, -24);
-            std::memcpy(&u, &f, 4);
-            u |= s;
-        }
-    } else if (ex == 31) {
-        u = s | 0x7F800000u | (m << 13);
-    } else {
-        u = s | ((ex + 112) << 23) | (m << 13);
-    }
-    float f;
-    std::memcpy(&f, &u, 4);
-    return f;
-}
-
 }  // namespace
 
 struct frq_bundle {
@@ -416,7 +396,7 @@ std::vector<float> upcast(const frq_bundle* b, const ArrSpec* s) {
     const size_t n = s->bytes / 2;
     std::vector<float> v(n);
     const uint8_t* p = b->blob + s->offset;
-    for (size_t i = 0; i < n; ++i) v[i] = f16_to_f32((uint16_t)(p[2 * i] | (p[2 * i + 1] << 8)));
+    for (size_t i = 0; i < n; ++i) v[i] = frq::h2f_host((uint16_t)(p[2 * i] | (p[2 * i + 1] << 8)));
     return v;
 }
 
@@ -566,54 +546,74 @@ static frq_moe_w* bundle_moe(frq_ctx* ctx, const frq_bundle* b, const char* pref
         return nullptr;
     }
     const std::string p(prefix);
-    std::vector<const int8_t*> gate(n_exp), up(n_exp, nullptr), down(n_exp);
-    std::vector<std::vector<float>> gs(n_exp), us(n_exp), ds(n_exp);
-    std::vector<const float*> gsp(n_exp), usp(n_exp, nullptr), dsp(n_exp);
-    size_t d = 0, mi = 0;
-    // one int8 (in, out) expert matrix with its f16 scales, shape checked
-    auto take = [&](const std::string& nm, size_t in, size_t out, const int8_t*& w, std::vector<float>& sc) {
-        const ArrSpec* s = need(b, nm, "i8", 2);
-        if (!s) return false;
-        if (s->shape[0] != in || s->shape[1] != out) {
-            frq::set_error(FRQ_ERR_FORMAT, nm + ": shape differs from the other experts'");
-            return false;
-        }
-        const ArrSpec* c = need(b, nm + "__scale", "f16", 1);
-        if (!c) return false;
-        if (c->shape[0] != out) {
-            frq::set_error(FRQ_ERR_FORMAT, nm + "__scale: one scale per output column expected");
-            return false;
-        }
-        w = reinterpret_cast<const int8_t*>(b->blob + s->offset);
-        sc = upcast(b, c);
-        return true;
-    };
-    const std::string g0 = p + "experts.0." + (act == FRQ_ACT_SILU ? "gate" : "gate_up");
-    const ArrSpec* s0 = need(b, g0, "i8", 2);
+    const bool silu_ = act == FRQ_ACT_SILU;
+    // the bank's dtype is the first expert's (expert_f32's arms, src/bundle.rs:408-452)
+    const std::string g0 = p + "experts.0." + (silu_ ? "gate" : "gate_up");
+    const ArrSpec* s0 = find(b, g0);
     if (!s0) return nullptr;
-    d = s0->shape[0];
-    mi = act == FRQ_ACT_SILU ? s0->shape[1] : s0->shape[1] / 2;
-    if (act == FRQ_ACT_GELU_TANH && s0->shape[1] % 2) {
+    const std::string dt = s0->dtype;
+    int dtype;
+    if (dt == "i8") dtype = FRQ_DT_I8;
+    else if (dt == "i4") dtype = FRQ_DT_I4;
+    else if (dt == "q4a") dtype = FRQ_DT_Q4A;
+    else if (dt == "f16") dtype = FRQ_DT_F16;
+    else if (dt == "f32") dtype = FRQ_DT_F32;
+    else {
+        frq::set_error(FRQ_ERR_DTYPE, g0 + ": expert dtype " + dt + " unsupported");  // :452
+        return nullptr;
+    }
+    const bool q = dtype == FRQ_DT_I4 || dtype == FRQ_DT_Q4A;
+    if (!need(b, g0, dt.c_str(), 2)) return nullptr;
+    // i8 / f16 / f32 store (in, out), i4 / q4a (out, in) (src/convert.rs:174-260)
+    const size_t d = q ? s0->shape[1] : s0->shape[0], gwid = q ? s0->shape[0] : s0->shape[1];
+    if (!silu_ && gwid % 2) {
         frq::set_error(FRQ_ERR_FORMAT, g0 + ": gate_up width must be even");
         return nullptr;
     }
+    const size_t mi = silu_ ? gwid : gwid / 2;
+    // i4 / q4a group: the manifest's, else the loader's defaults (32 / 64, src/bundle.rs:422, 435)
+    const size_t g = q ? (s0->group ? s0->group : (dtype == FRQ_DT_I4 ? 32 : 64)) : 0;
+    std::vector<const void*> gate(n_exp), up(n_exp, nullptr), down(n_exp);
+    std::vector<const uint16_t*> gs(n_exp, nullptr), us(n_exp, nullptr), ds(n_exp, nullptr);
+    std::vector<const uint16_t*> gm(n_exp, nullptr), um(n_exp, nullptr), dm(n_exp, nullptr);
+    // one expert matrix of logical (in, out), its siblings checked against it
+    auto take = [&](const std::string& nm, size_t in, size_t out, const void*& w, const uint16_t*& sc,
+                    const uint16_t*& mn) {
+        const ArrSpec* a = need(b, nm, dt.c_str(), 2);
+        if (!a) return false;
+        const size_t r0 = q ? out : in, r1 = q ? in : out;
+        if (a->shape[0] != r0 || a->shape[1] != r1 || (q && (a->group ? a->group : g) != g)) {
+            frq::set_error(FRQ_ERR_FORMAT, nm + ": shape or group differs from the other experts'");
+            return false;
+        }
+        w = b->blob + a->offset;
+        if (dtype == FRQ_DT_F16 || dtype == FRQ_DT_F32) return true;
+        const size_t ns = dtype == FRQ_DT_I8 ? out : out * ((in + g - 1) / g);
+        for (int which = 0; which < (dtype == FRQ_DT_Q4A ? 2 : 1); ++which) {
+            const std::string sn = nm + (which ? "__min" : "__scale");
+            const ArrSpec* c = need(b, sn, "f16", dtype == FRQ_DT_I8 ? 1 : 2);
+            if (!c) return false;
+            if (c->bytes != 2 * ns) {
+                frq::set_error(FRQ_ERR_FORMAT, sn + ": " + std::to_string(ns) + " f16 values expected");
+                return false;
+            }
+            (which ? mn : sc) = reinterpret_cast<const uint16_t*>(b->blob + c->offset);
+        }
+        return true;
+    };
     for (size_t e = 0; e < n_exp; ++e) {
         const std::string pe = p + "experts." + std::to_string(e) + ".";
-        if (act == FRQ_ACT_SILU) {
-            if (!take(pe + "gate", d, mi, gate[e], gs[e]) || !take(pe + "up", d, mi, up[e], us[e])) return nullptr;
-            usp[e] = us[e].data();
-        } else if (!take(pe + "gate_up", d, 2 * mi, gate[e], gs[e])) {
+        if (silu_) {
+            if (!take(pe + "gate", d, mi, gate[e], gs[e], gm[e]) || !take(pe + "up", d, mi, up[e], us[e], um[e]))
+                return nullptr;
+        } else if (!take(pe + "gate_up", d, 2 * mi, gate[e], gs[e], gm[e])) {
             return nullptr;
         }
-        if (!take(pe + "down", mi, d, down[e], ds[e])) return nullptr;
-        gsp[e] = gs[e].data();
-        dsp[e] = ds[e].data();
+        if (!take(pe + "down", mi, d, down[e], ds[e], dm[e])) return nullptr;
     }
-    return frq_moe_upload_i8(ctx, n_exp, d, mi, act, gate.data(), gsp.data(),
-                             act == FRQ_ACT_SILU ? up.data() : nullptr, act == FRQ_ACT_SILU ? usp.data() : nullptr,
-                             down.data(), dsp.data());
+    return frq_moe_upload(ctx, dtype, n_exp, d, mi, act, g, gate.data(), gs.data(), gm.data(),
+                          silu_ ? up.data() : nullptr, us.data(), um.data(), down.data(), ds.data(), dm.data());
 }
-
 int frq_bundle_weight(frq_ctx* ctx, const frq_bundle* b, const char* name, frq_w** out) {
     if (!out) return frq::set_error(FRQ_ERR_ARG, "frq_bundle_weight: null out");
     *out = bundle_weight(ctx, b, name);

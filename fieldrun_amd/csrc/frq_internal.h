@@ -40,6 +40,25 @@ namespace frq {
 
 inline size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+// IEEE binary16 -> binary32 on the host (exact; the arr1o upcast).
+inline float h2f_host(uint16_t h) {
+    const uint32_t s = (uint32_t)(h >> 15) << 31, ex = (h >> 10) & 0x1F, m = h & 0x3FF;
+    uint32_t u;
+    if (ex == 0) {
+        if (!m) {
+            u = s;
+        } else {  // subnormal: m * 2^-24, exact in f32
+            const float f = (float)m * 5.9604644775390625e-08f;
+            u = __builtin_bit_cast(uint32_t, f) | s;
+        }
+    } else if (ex == 31) {
+        u = s | 0x7F800000u | (m << 13);
+    } else {
+        u = s | ((ex + 112) << 23) | (m << 13);
+    }
+    return __builtin_bit_cast(float, u);
+}
+
 // Blocked MFMA-operand layout of an (R, Kp) int8 matrix (R % 16 == 0,
 // Kp % 64 == 0): the v_mfma_i32_16x16x64_i8 operand of rows 16rb..16rb+15
 // and k-bytes 64kb..64kb+63 is one contiguous 1 KB block in lane order
@@ -96,13 +115,13 @@ __device__ __forceinline__ unsigned long long xshfl64(unsigned long long v) {
     return ((unsigned long long)hi << 32) | lo;
 }
 
-// IEEE binary16 -> binary32 (exact).
 // Orders a wave's LDS accesses before and after (no other wave waits).
 __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     __builtin_amdgcn_wave_barrier();
 }
 
+// IEEE binary16 -> binary32 (exact).
 __device__ __forceinline__ float h2f(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);
 }
@@ -321,10 +340,34 @@ struct Weight {
     uint32_t* q4a_sm = nullptr;  // q4a: (N, ng) words, f16 scale | f16 min << 16
 };
 
+// One matrix (gate / gate_up, up or down) of every expert of a bank whose
+// experts are not int8, as the bundle stores it (src/bundle.rs:404-454,
+// src/convert.rs:174-260): f16 / f32 (E, in, out) row-major; i4 / q4a
+// (E, out, ceil(in/2)) packed nibbles, even input index low, with f16 scales
+// (and q4a mins) (E, out, ceil(in/g)).  An i4 matrix with g % 32 == 0 also
+// has the MFMA operand copy q4e / s4e: per expert, 16-row block rb and group
+// quad g4 (four 32-input groups) one 1 KB block, lane 16 q + r holding row
+// 16 rb + r's nibbles of inputs 8 q .. 8 q + 7 of each of the four groups,
+// four bytes a group with input 8 q + b in the low and 8 q + 4 + b in the
+// high half of byte b (so a shift and a mask give 16 x the sign-extended
+// values in input order); s4e the rows' f16 scales (rb, g4, r, 4), one per
+// 32-input group (zero past in).
+struct ExpMat {
+    void* raw = nullptr;
+    uint16_t* sc = nullptr;
+    uint16_t* mn = nullptr;
+    uint8_t* q4e = nullptr;
+    uint16_t* s4e = nullptr;
+    size_t in = 0, out = 0;
+};
+
 struct MoeBank {
     int device = 0;
     size_t n_exp = 0, d = 0, mi = 0;
     int act = 0;
+    int dtype = FRQ_DT_I8;       // the experts' stored dtype
+    size_t g = 0;                // i4 / q4a group
+    ExpMat mg, mu, md;           // non-int8 banks: gate (or gate_up), up, down
     size_t gw = 0;               // gate width: mi (SiLU) or 2*mi (gate_up)
     int8_t* gate = nullptr;      // (E, d, gw) i8 (in,out) row-major per expert
     float* gate_s = nullptr;     // (E, gw)
@@ -448,5 +491,10 @@ hipError_t launch_moe_block(const int8_t* src, size_t E, size_t K, size_t N, siz
 hipError_t launch_expert_mm(const int8_t* q, const float* s, size_t inp,
                             size_t out, const float* x, size_t m, float* y,
                             hipStream_t st);
+// expert_mm of expert e of a non-int8 bank matrix (dtype / g of the bank).
+hipError_t launch_expert_mm_ex(const MoeBank& b, const ExpMat& mt, size_t e, const float* x, size_t m, float* y,
+                               hipStream_t st);
+// The i4 MFMA operand copy of an i4 bank matrix (mt.raw / mt.sc filled).
+hipError_t launch_moe_i4_block(ExpMat& mt, size_t E, size_t g, hipStream_t st);
 
 }  // namespace frq

@@ -1314,6 +1314,330 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
     out[(size_t)t * d + c] = acc;
 }
 
+// ---- experts stored in other dtypes (i4, q4a, f16, f32) ---------------------
+// expert_f32 (src/bundle.rs:404-454) forms W[k, j] of every arm in f32 before
+// x.dot(&wv): i4 s4 * scale[j, k / g], q4a scale * u4 + min (a mul then an
+// add), f16 the exact upcast, f32 as stored.  The kernels below read the
+// stored bytes and form the same values in registers.
+struct ExpView {
+    const void* raw;
+    const uint16_t* sc;
+    const uint16_t* mn;
+    int in, out, g, ng, rb;  // rb: bytes a packed row
+    size_t per, sper;        // raw elements (bytes for i4 / q4a) and scales an expert
+};
+
+ExpView exp_view(const MoeBank& b, const ExpMat& m) {
+    ExpView v;
+    v.raw = m.raw; v.sc = m.sc; v.mn = m.mn;
+    v.in = (int)m.in; v.out = (int)m.out;
+    v.g = (int)(b.g ? b.g : 1);
+    v.ng = (int)((m.in + v.g - 1) / v.g);
+    v.rb = (int)((m.in + 1) / 2);
+    v.per = (b.dtype == FRQ_DT_I4 || b.dtype == FRQ_DT_Q4A) ? m.out * (size_t)v.rb : m.in * m.out;
+    v.sper = m.out * (size_t)v.ng;
+    return v;
+}
+
+template <int DT>
+__device__ __forceinline__ float wval(const ExpView& v, size_t e, int k, int j) {
+    if constexpr (DT == FRQ_DT_F32) {
+        return reinterpret_cast<const float*>(v.raw)[e * v.per + (size_t)k * v.out + j];
+    } else if constexpr (DT == FRQ_DT_F16) {
+        return h2f(reinterpret_cast<const uint16_t*>(v.raw)[e * v.per + (size_t)k * v.out + j]);
+    } else {
+        const uint8_t byte = reinterpret_cast<const uint8_t*>(v.raw)[e * v.per + (size_t)j * v.rb + (k >> 1)];
+        const int nib = (k & 1) ? (byte >> 4) : (byte & 15);
+        const size_t gi = e * v.sper + (size_t)j * v.ng + k / v.g;
+        if constexpr (DT == FRQ_DT_I4) return (float)((nib ^ 8) - 8) * h2f(v.sc[gi]);
+        else return h2f(v.sc[gi]) * (float)nib + h2f(v.mn[gi]);
+    }
+}
+
+// x . W_e[:, j] in a.dot's order (MM_KC-long k blocks, each an FMA chain
+// from +0, added in order).
+template <int DT>
+__device__ float exact_ex(const float* __restrict__ x, const ExpView& v, size_t e, int j) {
+    float c = 0.0f;
+    for (int k0 = 0; k0 < v.in; k0 += MM_KC) {
+        float ab = 0.0f;
+        for (int k = k0; k < min(v.in, k0 + MM_KC); ++k) ab = __builtin_fmaf(x[k], wval<DT>(v, e, k, j), ab);
+        c = c + ab;
+    }
+    return c;
+}
+
+// expert_mm of one expert: a thread per (row, output column).
+template <int DT>
+__global__ __launch_bounds__(256) void expert_mm_ex_kernel(const float* __restrict__ x, int m, ExpView v, int e,
+                                                           float* __restrict__ y) {
+    const int j = blockIdx.x * 256 + threadIdx.x, i = blockIdx.y;
+    if (j >= v.out || i >= m) return;
+    y[(size_t)i * v.out + j] = exact_ex<DT>(x + (size_t)i * v.in, v, (size_t)e, j);
+}
+
+// Grouped expert matmul over the tile list in expert_mm's own order, for any
+// stored dtype: workgroup (tile of up to GM_TR rows of one expert, 64
+// output columns); a lane per column, wave w the tile's rows w, w + 4, ...;
+// the tile's x rows pass through LDS one a.dot block at a time, each weight
+// value formed once for all of the wave's rows.  src = ptok[prow] when gather
+// (rows of x), else prow.
+constexpr int EX_RW = GM_TR / 4;  // rows a wave
+
+template <int DT>
+__global__ __launch_bounds__(256) void moe_ex_kernel(ExpView v, const float* __restrict__ x, int gather,
+                                                     const int32_t* __restrict__ ptok,
+                                                     const int32_t* __restrict__ off,
+                                                     const int32_t* __restrict__ cnt,
+                                                     const int32_t* __restrict__ tile_e,
+                                                     const int32_t* __restrict__ tile_r,
+                                                     const int32_t* __restrict__ ntile, float* __restrict__ y) {
+    __shared__ float xs[GM_TR][MM_KC + 1];
+    __shared__ int srcs[GM_TR];
+    const int tix = blockIdx.x;
+    if (tix >= ntile[0]) return;  // uniform
+    const int e = tile_e[tix], r0 = tile_r[tix];
+    const int rows = min(GM_TR, cnt[e] - r0), pbase = off[e] + r0;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid < GM_TR) {
+        const int prow = pbase + min(tid, rows - 1);
+        srcs[tid] = gather ? ptok[prow] : prow;
+    }
+    const int j = blockIdx.y * 64 + lane, jc = min(j, v.out - 1);
+    const int K = v.in;
+    float tot[EX_RW], acc[EX_RW];
+#pragma unroll
+    for (int u = 0; u < EX_RW; ++u) tot[u] = 0.0f;
+    for (int k0 = 0; k0 < K; k0 += MM_KC) {
+        const int kn = min(MM_KC, K - k0);
+        __syncthreads();  // srcs written / the previous block's xs read
+        for (int idx = tid; idx < rows * kn; idx += 256) {
+            const int r = idx / kn, kk = idx - r * kn;
+            xs[r][kk] = x[(size_t)srcs[r] * K + k0 + kk];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < EX_RW; ++u) acc[u] = 0.0f;
+        for (int kk = 0; kk < kn; ++kk) {
+            const float w = wval<DT>(v, (size_t)e, k0 + kk, jc);
+#pragma unroll
+            for (int u = 0; u < EX_RW; ++u) {
+                const int r = wave + 4 * u;
+                if (r < rows) acc[u] = __builtin_fmaf(xs[r][kk], w, acc[u]);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < EX_RW; ++u) tot[u] = tot[u] + acc[u];
+    }
+    if (j < v.out) {
+#pragma unroll
+        for (int u = 0; u < EX_RW; ++u) {
+            const int r = wave + 4 * u;
+            if (r < rows) y[(size_t)(pbase + r) * v.out + j] = tot[u];
+        }
+    }
+}
+
+// ---- int4 experts on the int8 MFMA ------------------------------------------
+// Expert-stationary grouped digit GEMM for i4 banks with g % 32 == 0:
+// workgroup (tile of up to GM_TR rows of one expert, 128 output columns), 4
+// waves x two 16-column blocks.  Per group quad (128 inputs) the tile's
+// digit rows (24-bit fixed point per row, as the int8 bank's) pass through
+// LDS, laid out as the v_mfma_i32_16x16x32_i8 A operands: token group t,
+// group gi, lane 16 q + 4 tl + d holds digit d of row 4 t + tl, inputs
+// 8 q .. 8 q + 7 of the group (d == 3 lanes read zeros).  B is one 16-byte
+// load a lane and block (the quad's four groups of q4e), each 4-byte group
+// word two shifts / masks away from 16 x the sign-extended nibbles.  A group
+// gives the exact integer dots C_d of the three digits; the f32 sum over
+// the groups is acc += scale[j, g] * (C2 * 2^16 + C1 * 2^8 + C0), and
+// y = (so / 16) * acc.  The next quad's A and B loads are in flight during
+// the MFMAs.  Rows whose digits cannot carry the activations take
+// expert_mm's own order over the stored nibbles.
+constexpr int I4_AS = 8 * 4 * 4 * 4 * 3;  // A slots (8 bytes) of a quad: t, gi, q, tl, d
+
+struct I4Args {
+    const int8_t* D;     // digit rows [src][3][Kp]
+    const float* dso;    // their scales (-1: exact row)
+    int Kp, nrb, ng4, N, K;
+    const uint8_t* q4e;
+    const uint16_t* s4e;
+    ExpView raw;
+    const float* xf;     // f32 rows (exact rows)
+    float* y;
+};
+
+__device__ __forceinline__ long i4_bop(uint32_t w) {
+    const uint32_t lo = (w & 0x0F0F0F0Fu) << 4, hi = w & 0xF0F0F0F0u;
+    return (long)(((unsigned long long)hi << 32) | lo);
+}
+
+template <int NGT>
+__device__ __forceinline__ void i4_body(const I4Args& A, uint2 (*As)[I4_AS], const int* srcs, int e, int rows,
+                                        int pbase, int cg) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int cb0 = cg * 8 + 2 * wave;  // this wave's two 16-column blocks (clamped loads past the last)
+    const size_t eb = (size_t)e * A.nrb;
+    const uint8_t* qb0 = A.q4e + (eb + min(cb0, A.nrb - 1)) * A.ng4 * 1024 + lane * 16;
+    const uint8_t* qb1 = A.q4e + (eb + min(cb0 + 1, A.nrb - 1)) * A.ng4 * 1024 + lane * 16;
+    const uint16_t* sb0 = A.s4e + (eb + min(cb0, A.nrb - 1)) * A.ng4 * 64 + (lane & 15) * 4;
+    const uint16_t* sb1 = A.s4e + (eb + min(cb0 + 1, A.nrb - 1)) * A.ng4 * 64 + (lane & 15) * 4;
+    // A staging: 3 items a thread, item = (row, digit, 16-byte chunk of the quad)
+    constexpr int NIT = 24 * 4 * NGT, UA = (NIT + 255) / 256;
+    const int8_t* asrc[UA];
+    int adst[UA];
+#pragma unroll
+    for (int u = 0; u < UA; ++u) {
+        const int it = min(tid + 256 * u, NIT - 1), r = it / 24, dg = (it % 24) / 8, ch = it % 8;
+        asrc[u] = A.D + ((size_t)srcs[min(r, rows - 1)] * 3 + dg) * A.Kp + 16 * ch;
+        adst[u] = tid + 256 * u < NIT ? ((((r >> 2) * 4 + (ch >> 1)) * 4 + 2 * (ch & 1)) * 4 + (r & 3)) * 3 + dg : -1;
+    }
+    uint4 an[UA], bn0, bn1, bc0, bc1;
+    uint2 sn0, sn1, sc0, sc1;
+    auto ldq = [&](int q4) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < UA; ++u) an[u] = *reinterpret_cast<const uint4*>(asrc[u] + (size_t)q4 * 128);
+        bn0 = *reinterpret_cast<const uint4*>(qb0 + (size_t)q4 * 1024);
+        bn1 = *reinterpret_cast<const uint4*>(qb1 + (size_t)q4 * 1024);
+        sn0 = *reinterpret_cast<const uint2*>(sb0 + (size_t)q4 * 64);
+        sn1 = *reinterpret_cast<const uint2*>(sb1 + (size_t)q4 * 64);
+    };
+    auto sta = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < UA; ++u)
+            if (adst[u] >= 0) {
+                As[buf][adst[u]] = make_uint2(an[u].x, an[u].y);
+                As[buf][adst[u] + 12] = make_uint2(an[u].z, an[u].w);
+            }
+    };
+    float acc[NGT][2];
+#pragma unroll
+    for (int t = 0; t < NGT; ++t) acc[t][0] = acc[t][1] = 0.0f;
+    ldq(0);
+    sta(0);
+    bc0 = bn0; bc1 = bn1; sc0 = sn0; sc1 = sn1;
+    __syncthreads();
+    const int ql = lane >> 4, tll = (lane >> 2) & 3, dgl = lane & 3;
+    const int abase = (ql * 4 + tll) * 3 + min(dgl, 2);
+    for (int q4 = 0; q4 < A.ng4; ++q4) {
+        const int buf = q4 & 1;
+        if (q4 + 1 < A.ng4) ldq(q4 + 1);
+        const uint32_t w0[4] = {bc0.x, bc0.y, bc0.z, bc0.w}, w1[4] = {bc1.x, bc1.y, bc1.z, bc1.w};
+        const uint32_t s0[2] = {sc0.x, sc0.y}, s1[2] = {sc1.x, sc1.y};
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi) {
+            const long b0 = i4_bop(w0[gi]), b1 = i4_bop(w1[gi]);
+            const float f0 = h2f((uint16_t)(s0[gi >> 1] >> (16 * (gi & 1))));
+            const float f1 = h2f((uint16_t)(s1[gi >> 1] >> (16 * (gi & 1))));
+#pragma unroll
+            for (int t = 0; t < NGT; ++t) {
+                uint2 a = As[buf][(t * 4 + gi) * 48 + abase];
+                if (dgl == 3) a = make_uint2(0u, 0u);
+                const long aop = (long)(((unsigned long long)a.y << 32) | a.x);
+                const v4i c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, b0, v4i{0, 0, 0, 0}, 0, 0, 0);
+                const v4i c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, b1, v4i{0, 0, 0, 0}, 0, 0, 0);
+                acc[t][0] = __builtin_fmaf(f0, (float)c0[0] * 65536.0f + ((float)c0[1] * 256.0f + (float)c0[2]),
+                                           acc[t][0]);
+                acc[t][1] = __builtin_fmaf(f1, (float)c1[0] * 65536.0f + ((float)c1[1] * 256.0f + (float)c1[2]),
+                                           acc[t][1]);
+            }
+        }
+        if (q4 + 1 < A.ng4) {
+            sta(buf ^ 1);
+            bc0 = bn0; bc1 = bn1; sc0 = sn0; sc1 = sn1;
+        }
+        __syncthreads();
+    }
+    const int col = lane & 15, tok = lane >> 4;
+#pragma unroll
+    for (int t = 0; t < NGT; ++t) {
+        const int i = 4 * t + tok;
+        if (i < rows) {
+            const int prow = pbase + i, src = srcs[i];
+            const float so = A.dso[src];
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                const int j = (cb0 + c) * 16 + col;
+                if (j < A.N) {
+                    const float v = so >= 0.0f ? (so * 0.0625f) * acc[t][c]
+                                               : exact_ex<FRQ_DT_I4>(A.xf + (size_t)src * A.K, A.raw, (size_t)e, j);
+                    A.y[(size_t)prow * A.N + j] = v;
+                }
+            }
+        }
+    }
+}
+
+// A1 (ncg1 = 0: none) is a second matrix over the same rows (up beside gate).
+__global__ __launch_bounds__(256) void moe_i4_kernel(I4Args A0, I4Args A1, int ncg1, int gather,
+                                                     const int32_t* __restrict__ ptok,
+                                                     const int32_t* __restrict__ off,
+                                                     const int32_t* __restrict__ cnt,
+                                                     const int32_t* __restrict__ tile_e,
+                                                     const int32_t* __restrict__ tile_r,
+                                                     const int32_t* __restrict__ ntile) {
+    __shared__ uint2 As[2][I4_AS];
+    __shared__ int srcs[GM_TR];
+    // XCD-aware order (as moe_gmm_kernel): a tile's column groups on one XCD
+    const int ncg0 = (A0.nrb + 7) / 8, ncg = ncg0 + ncg1;
+    const int xcd = blockIdx.x & 7, jb = blockIdx.x >> 3;
+    const int tix = xcd + 8 * (jb / ncg), cgt = jb % ncg;
+    const bool second = cgt >= ncg0;  // uniform
+    const I4Args& A = second ? A1 : A0;
+    const int cg = second ? cgt - ncg0 : cgt;
+    if (tix >= ntile[0]) return;  // uniform
+    const int e = tile_e[tix], r0 = tile_r[tix];
+    const int rows = min(GM_TR, cnt[e] - r0);
+    const int pbase = off[e] + r0;
+    const int tid = threadIdx.x;
+    if (tid < GM_TR) {
+        const int prow = pbase + min(tid, rows - 1);
+        srcs[tid] = gather ? ptok[prow] : prow;
+    }
+    __syncthreads();
+    if (rows <= 4) i4_body<1>(A, As, srcs, e, rows, pbase, cg);
+    else if (rows <= 16) i4_body<4>(A, As, srcs, e, rows, pbase, cg);
+    else i4_body<8>(A, As, srcs, e, rows, pbase, cg);
+}
+
+// (E, out, ceil(in/2)) i4 rows + (E, out, ceil(in/g)) f16 scales -> q4e / s4e.
+__global__ void moe_i4_block_kernel(const uint8_t* __restrict__ raw, const uint16_t* __restrict__ sc, int E,
+                                    int in, int out, int g, int nrb, int ng4, uint8_t* __restrict__ q4e,
+                                    uint16_t* __restrict__ s4e) {
+    const int rb_ = (in + 1) / 2, ng = (in + g - 1) / g;
+    const size_t total = (size_t)E * nrb * ng4 * 64;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+        const int L = (int)(i % 64), q = L >> 4, r = L & 15;
+        const size_t blk = i / 64;
+        const int g4 = (int)(blk % ng4);
+        const size_t er = blk / ng4;
+        const int rb = (int)(er % nrb), e = (int)(er / nrb), j = 16 * rb + r;
+        uint32_t words[4];
+        for (int gi = 0; gi < 4; ++gi) {
+            const int k0 = 32 * (4 * g4 + gi) + 8 * q;
+            uint32_t wd = 0;
+            for (int b = 0; b < 4; ++b) {
+                uint32_t lo = 0, hi = 0;
+                if (j < out && k0 + b < in) {
+                    const uint8_t by = raw[((size_t)e * out + j) * rb_ + ((k0 + b) >> 1)];
+                    lo = ((k0 + b) & 1) ? (by >> 4) : (by & 15);
+                }
+                if (j < out && k0 + 4 + b < in) {
+                    const uint8_t by = raw[((size_t)e * out + j) * rb_ + ((k0 + 4 + b) >> 1)];
+                    hi = ((k0 + 4 + b) & 1) ? (by >> 4) : (by & 15);
+                }
+                wd |= (lo | (hi << 4)) << (8 * b);
+            }
+            words[gi] = wd;
+            if (q == 0) {
+                const int kg = 32 * (4 * g4 + gi);
+                s4e[(blk * 16 + r) * 4 + gi] = (j < out && kg < in) ? sc[((size_t)e * out + j) * ng + kg / g] : 0;
+            }
+        }
+        *reinterpret_cast<uint4*>(q4e + i * 16) = make_uint4(words[0], words[1], words[2], words[3]);
+    }
+}
+
 }  // namespace
 
 size_t moe_ws_bytes(const MoeBank& b, size_t T, size_t topk) {
@@ -1360,11 +1684,112 @@ static hipError_t moe_gmm_pair(unsigned nt, const GmmArgs& g0, const GmmArgs& g1
     return hipGetLastError();
 }
 
+// One grouped matmul of a non-int8 bank matrix: the int4 MFMA kernel where
+// the bank has the operand copy (g % 32 == 0), else expert_mm's own order.
+static hipError_t moe_ex_mm(const MoeBank& b, const ExpMat& m, unsigned nt, int gather, const int8_t* D,
+                            const float* dso, size_t kp, const float* xf, const MoeWs& ws, float* y,
+                            const ExpMat* m2, float* y2, hipStream_t s) {
+    const ExpView v = exp_view(b, m);
+    if (m.q4e) {
+        const int nrb = (int)((m.out + 15) / 16), ng4 = (int)((m.in + 127) / 128);
+        const I4Args a{D, dso, (int)kp, nrb, ng4, (int)m.out, (int)m.in, m.q4e, m.s4e, v, xf, y};
+        I4Args a2 = a;
+        int ncg1 = 0;
+        if (m2) {
+            a2 = I4Args{D, dso, (int)kp, (int)((m2->out + 15) / 16), ng4, (int)m2->out, (int)m2->in, m2->q4e,
+                        m2->s4e, exp_view(b, *m2), xf, y2};
+            ncg1 = (a2.nrb + 7) / 8;
+        }
+        const int ncg = (nrb + 7) / 8 + ncg1;
+        moe_i4_kernel<<<dim3((unsigned)(8 * ((nt + 7) / 8) * ncg)), dim3(256), 0, s>>>(
+            a, a2, ncg1, gather, ws.ptok, ws.off, ws.cnt, ws.tile_e, ws.tile_r, ws.ntile);
+        return hipGetLastError();
+    }
+    const dim3 grid(nt, (unsigned)((m.out + 63) / 64));
+    switch (b.dtype) {
+        case FRQ_DT_I4:
+            moe_ex_kernel<FRQ_DT_I4><<<grid, dim3(256), 0, s>>>(v, xf, gather, ws.ptok, ws.off, ws.cnt, ws.tile_e,
+                                                                ws.tile_r, ws.ntile, y);
+            break;
+        case FRQ_DT_Q4A:
+            moe_ex_kernel<FRQ_DT_Q4A><<<grid, dim3(256), 0, s>>>(v, xf, gather, ws.ptok, ws.off, ws.cnt, ws.tile_e,
+                                                                 ws.tile_r, ws.ntile, y);
+            break;
+        case FRQ_DT_F16:
+            moe_ex_kernel<FRQ_DT_F16><<<grid, dim3(256), 0, s>>>(v, xf, gather, ws.ptok, ws.off, ws.cnt, ws.tile_e,
+                                                                 ws.tile_r, ws.ntile, y);
+            break;
+        default:
+            moe_ex_kernel<FRQ_DT_F32><<<grid, dim3(256), 0, s>>>(v, xf, gather, ws.ptok, ws.off, ws.cnt, ws.tile_e,
+                                                                 ws.tile_r, ws.ntile, y);
+            break;
+    }
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess && m2) return moe_ex_mm(b, *m2, nt, gather, D, dso, kp, xf, ws, y2, nullptr, nullptr, s);
+    return e;
+}
+
+// The routed layer over a non-int8 bank: route, dispatch, (int4: the x
+// digit rows), gate and up, act (and the h digit rows), down, combine.
+static hipError_t launch_moe_ex(const MoeBank& b, const float* x, size_t T, const float* logits, size_t topk,
+                                int norm_topk, const float* pes, float* out, void* wsp, int* err, hipStream_t s) {
+    MoeWs ws = moe_view(wsp, b, T, topk);
+    const int E = (int)b.n_exp, d = (int)b.d, mi = (int)b.mi, gw = (int)b.gw;
+    const size_t tr = moe_tile_rows(T);
+    hipError_t e = launch_moe_route(logits, T, b.n_exp, topk, norm_topk, pes, ws.sel, ws.w, err, s);
+    if (e != hipSuccess) return e;
+    const size_t nwc = (std::min(T, (size_t)TC) + 31) / 32;
+    const size_t dlds = ((size_t)E * nwc * 2 + 3 * E) * sizeof(uint32_t);
+    dispatch_kernel<<<dim3(1), dim3(1024), dlds, s>>>(ws.sel, (int)T, (int)topk, E, (int)tr, ws);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    const unsigned nt = (unsigned)ntile_max(T, topk, b.n_exp, tr);
+    const bool mf = b.mg.q4e != nullptr;
+    if (mf) {
+        x_digits_kernel<<<dim3((unsigned)T), dim3(256), 0, s>>>(x, d, (int)b.kpd, ws.xd, ws.xso);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    const bool silu_ = b.act == FRQ_ACT_SILU;
+    if ((e = moe_ex_mm(b, b.mg, nt, 1, ws.xd, ws.xso, b.kpd, x, ws, ws.g, silu_ ? &b.mu : nullptr, ws.u, s)) !=
+        hipSuccess)
+        return e;
+    act_digits_kernel<<<dim3((unsigned)(T * topk)), dim3(256), 0, s>>>(
+        ws.g, ws.u, b.act, mi, gw, (int)b.kpm, ws.off, E, ws.h, ws.hd, ws.hso);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if ((e = moe_ex_mm(b, b.md, nt, 0, ws.hd, ws.hso, b.kpm, ws.h, ws, ws.dn, nullptr, nullptr, s)) != hipSuccess)
+        return e;
+    combine_kernel<<<dim3((unsigned)(((d % 4 ? d : d / 4) + 255) / 256), (unsigned)T), dim3(256), 0, s>>>(
+        ws.dn, ws.sel, ws.w, ws.pos, (int)topk, d, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_expert_mm_ex(const MoeBank& b, const ExpMat& mt, size_t e, const float* x, size_t m, float* y,
+                               hipStream_t st) {
+    if (m == 0) return hipSuccess;
+    const ExpView v = exp_view(b, mt);
+    const dim3 grid((unsigned)((mt.out + 255) / 256), (unsigned)m);
+    switch (b.dtype) {
+        case FRQ_DT_I4: expert_mm_ex_kernel<FRQ_DT_I4><<<grid, dim3(256), 0, st>>>(x, (int)m, v, (int)e, y); break;
+        case FRQ_DT_Q4A: expert_mm_ex_kernel<FRQ_DT_Q4A><<<grid, dim3(256), 0, st>>>(x, (int)m, v, (int)e, y); break;
+        case FRQ_DT_F16: expert_mm_ex_kernel<FRQ_DT_F16><<<grid, dim3(256), 0, st>>>(x, (int)m, v, (int)e, y); break;
+        case FRQ_DT_F32: expert_mm_ex_kernel<FRQ_DT_F32><<<grid, dim3(256), 0, st>>>(x, (int)m, v, (int)e, y); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_i4_block(ExpMat& mt, size_t E, size_t g, hipStream_t st) {
+    const size_t nrb = (mt.out + 15) / 16, ng4 = (mt.in + 127) / 128;
+    moe_i4_block_kernel<<<dim3(2048), dim3(256), 0, st>>>((const uint8_t*)mt.raw, mt.sc, (int)E, (int)mt.in,
+                                                          (int)mt.out, (int)g, (int)nrb, (int)ng4, mt.q4e, mt.s4e);
+    return hipGetLastError();
+}
+
 hipError_t launch_moe(const MoeBank& b, const float* x, size_t T,
                       const float* logits, size_t topk, int norm_topk,
                       const float* pes, float* out, void* wsp, int* err,
                       hipStream_t s) {
     if (T == 0) return hipSuccess;
+    if (b.dtype != FRQ_DT_I8) return launch_moe_ex(b, x, T, logits, topk, norm_topk, pes, out, wsp, err, s);
     MoeWs ws = moe_view(wsp, b, T, topk);
     const int E = (int)b.n_exp, d = (int)b.d, mi = (int)b.mi, gw = (int)b.gw;
     const size_t tr = moe_tile_rows(T);

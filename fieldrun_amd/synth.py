@@ -70,6 +70,38 @@ def moe_layer(E: int, d: int, mi: int, s: int, act: int = 0, std: float = 0.02):
     return gate, gs, up, us, down, ds
 
 
+def moe_layer_ex(E: int, d: int, mi: int, s: int, dtype: str, act: int = 0, std: float = 0.02):
+    """Experts as put_lin stores them in `dtype` ("int4", "q4a", "f16" or
+    "f32", src/convert.rs:174-260): per matrix a dict with raw (the stored
+    array: packed (out, ceil(in/2)) nibbles for int4 / q4a, (in, out) f16
+    bits or f32 otherwise), scale / min (f16 bits, (out, ceil(in/g)); None
+    where the dtype has none), g, inp and out.  Returns (gate, up, down),
+    lists over experts (up empty for the packed gate_up of act 1)."""
+    rng = np.random.default_rng(s + 5)
+    gw = mi if act == 0 else 2 * mi
+
+    def lin(out, inp):
+        src = (rng.standard_normal((out, inp), dtype=np.float32) * np.float32(std)).astype(np.float32)
+        if dtype == "int4":
+            packed, s16, g = convert.put_i4(src, transpose=True)
+            return {"raw": packed, "scale": s16.view(np.uint16), "min": None, "g": g, "inp": inp, "out": out}
+        if dtype == "q4a":
+            packed, s16, m16, g = convert.put_q4a(src, transpose=True)
+            return {"raw": packed, "scale": s16.view(np.uint16), "min": m16.view(np.uint16), "g": g, "inp": inp,
+                    "out": out}
+        t = np.ascontiguousarray(src.T)  # (in, out)
+        raw = t.astype(np.float16).view(np.uint16) if dtype == "f16" else t
+        return {"raw": raw, "scale": None, "min": None, "g": 0, "inp": inp, "out": out}
+
+    gate, up, down = [], [], []
+    for _ in range(E):
+        gate.append(lin(gw, d))
+        if act == 0:
+            up.append(lin(mi, d))
+        down.append(lin(d, mi))
+    return gate, up, down
+
+
 # ---- synthetic random-init bundles in the reference format (the benchmark
 # configs; array names and layouts as src/convert.rs writes them) ----------
 
@@ -106,22 +138,23 @@ def write_gpt2_bundle(stem: str, s: int, n_layer: int = 12, n_head: int = 12, d:
 
 
 def write_qwen3moe_layer_bundle(stem: str, s: int, n_exp: int = 128, d: int = 2048, mi: int = 768,
-                                topk: int = 8, std: float = 0.02) -> dict:
+                                topk: int = 8, std: float = 0.02, dtype: str = "int8") -> dict:
     """one Qwen3-MoE routed layer as convert_qwen3moe writes it
-    (src/convert.rs:872-936, dtype int8): the router l0.gate and the experts
-    l0.experts.{e}.gate / .up / .down, each put_lin from an (out, in)
-    Linear source -> int8 (in, out) + f16 __scale.  The manifest's config
-    follows that converter's vector for a one-layer model (Qwen3-30B-A3B
-    attention dims, all of its arrays but the MoE layer absent)."""
+    (src/convert.rs:872-936, every linear put_lin at the converter's dtype:
+    "int8", "int4", "q4a", "f16" or "f32"): the router l0.gate and the
+    experts l0.experts.{e}.gate / .up / .down, each from an (out, in) Linear
+    source.  The manifest's config follows that converter's vector for a
+    one-layer model (Qwen3-30B-A3B attention dims, all of its arrays but the
+    MoE layer absent)."""
     from .bundle import BundleWriter, manifest
     rng = np.random.default_rng(s)
     nrm = lambda *shape: (rng.standard_normal(shape, dtype=np.float32) * np.float32(std))
     w = BundleWriter(stem)
-    w.put_lin("l0.gate", nrm(n_exp, d), "int8")
+    w.put_lin("l0.gate", nrm(n_exp, d), dtype)
     for e in range(n_exp):
-        w.put_lin(f"l0.experts.{e}.gate", nrm(mi, d), "int8")
-        w.put_lin(f"l0.experts.{e}.up", nrm(mi, d), "int8")
-        w.put_lin(f"l0.experts.{e}.down", nrm(d, mi), "int8")
+        w.put_lin(f"l0.experts.{e}.gate", nrm(mi, d), dtype)
+        w.put_lin(f"l0.experts.{e}.up", nrm(mi, d), dtype)
+        w.put_lin(f"l0.experts.{e}.down", nrm(d, mi), dtype)
     nh, nkv, hd, vocab = 32, 4, 128, 151936
     cfg = [1, nh, nkv, hd, d, 6144, vocab, 0, n_exp, topk, mi, 1, 1, 0]
     m = manifest("qwen3moe", cfg, [1e6, 1e-6])

@@ -127,14 +127,17 @@ int frq_mm(frq_ctx* ctx, const frq_w* w, const float* a, size_t m,
            float* out);
 int frq_mm_dev(frq_ctx* ctx, const frq_w* w, const float* d_a, size_t m,
                float* d_out);
-/* Bundle::mm (src/bundle.rs:644-919) with every output bit-identical to the
- * reference's order at any M, on device pointers: int8 at M <= 16 as
- * frq_mm_dev; at M > 16 the MFMA GEMM's exact int32 sums, then the M > 1
- * arm's sequential f32 outlier correction and epilogue (732-756); int4 in
- * i4_dot_avx2's order at M = 1 and the M > 1 arm's per-row order (760-799);
- * q4a likewise (802-845).  frq_mm_dev's int8 results at M > 16 are within
- * 1e-6 sum|terms| instead (the correction on the f16 MFMA).  The decode
- * engines run this linear. */
+/* Bundle::mm (src/bundle.rs:644-919) with every output in one fixed f32
+ * order at any M (the order the CPU oracle restates, bit for bit), on device
+ * pointers: int8 at M <= 16 as frq_mm_dev; at M > 16 the MFMA GEMM's exact
+ * int32 sums, then the M > 1 arm's f32 outlier correction and epilogue
+ * (732-756), the correction summed over the outliers in ascending channel
+ * (the reference sums them in select_nth_unstable_by's permutation, which
+ * its source does not fix); int4 in i4_dot_avx2's order at M = 1 and a.dot's
+ * (matrixmultiply 0.3.10's blocked sgemm) at M > 1 (760-799); q4a likewise
+ * (802-845).  frq_mm_dev's int8 results at M > 16 are within 1e-6
+ * sum|terms| instead (the correction on the f16 MFMA).  The decode engines
+ * run this linear. */
 int frq_mm_exact_dev(frq_ctx* ctx, const frq_w* w, const float* d_a, size_t m,
                      float* d_out);
 /* No counterpart in the reference.  frq_mm_dev that allocates nothing, for
@@ -205,7 +208,28 @@ frq_moe_w* frq_moe_upload_i8(frq_ctx* ctx, size_t n_exp, size_t d, size_t mi,
                              const float* const* up_scale,
                              const int8_t* const* down,
                              const float* const* down_scale);
+/* The expert bank of one layer in the dtype its bundle stores (the arms of
+ * expert_f32, src/bundle.rs:404-454; written by put_lin,
+ * src/convert.rs:174-260): dtype FRQ_DT_I8 (gate[e] etc. int8 (in, out),
+ * *_scale f16 [out]), FRQ_DT_I4 (packed (out, ceil(in/2)) nibbles, even
+ * input index low, *_scale f16 (out, ceil(in/g))), FRQ_DT_Q4A (as i4 with
+ * unsigned nibbles and *_min f16 (out, ceil(in/g))), FRQ_DT_F16 (f16 bits,
+ * (in, out)) or FRQ_DT_F32 ((in, out)); *_min only for q4a, g only for
+ * i4 / q4a (the loader's defaults are 32 and 64).  Shapes and act as
+ * frq_moe_upload_i8 (gate = the packed gate_up for FRQ_ACT_GELU_TANH).  The
+ * weights stay in their stored precision in HBM and are dequantised in
+ * registers, each value as expert_f32 forms it; i4 banks with g % 32 == 0
+ * also keep an MFMA operand copy of the nibbles.  FRQ_ERR_DTYPE for another
+ * dtype (the reference panics, :452). */
+frq_moe_w* frq_moe_upload(frq_ctx* ctx, int dtype, size_t n_exp, size_t d, size_t mi, int act, size_t g,
+                          const void* const* gate, const uint16_t* const* gate_scale,
+                          const uint16_t* const* gate_min, const void* const* up,
+                          const uint16_t* const* up_scale, const uint16_t* const* up_min,
+                          const void* const* down, const uint16_t* const* down_scale,
+                          const uint16_t* const* down_min);
 void frq_moe_free(frq_moe_w* m);
+/* dtype (FRQ_DT_*), n_exp, d, mi and the int4 group (0 for other dtypes). */
+int frq_moe_info(const frq_moe_w* m, int* dtype, size_t* n_exp, size_t* d, size_t* mi, size_t* g);
 
 /* Routed expert layer: softmax over the router logits (T,E), stable top-k,
  * renormalise (norm_topk; per_expert_scale non-NULL selects the gemma4
@@ -225,8 +249,9 @@ int frq_moe_route(frq_ctx* ctx, const float* logits, size_t T, size_t E,
                   size_t topk, int norm_topk, const float* per_expert_scale,
                   int32_t* sel, float* w);
 /* One expert matmul, expert_mm (src/bundle.rs:457-461): y (M,out) =
- * x (M,in) @ (q * scale) for expert `e` of bank `which` (0 gate/gate_up,
- * 1 up, 2 down). */
+ * x (M,in) @ expert_f32 for expert `e` of bank `which` (0 gate/gate_up,
+ * 1 up, 2 down), any bank dtype, in a.dot's order (matrixmultiply 0.3.10's
+ * sgemm: 256-long k blocks, each an FMA chain from +0, added in order). */
 int frq_expert_mm(frq_ctx* ctx, const frq_moe_w* m, int which, size_t e,
                   const float* x, size_t mrows, float* y);
 
@@ -260,8 +285,10 @@ int frq_bundle_weight(frq_ctx* ctx, const frq_bundle* b, const char* name,
                       frq_w** out);
 /* The routed expert bank of one MoE layer: n_exp experts named
  * {prefix}experts.{e}.gate / .up / .down (FRQ_ACT_SILU, qwen3moe) or
- * .gate_up / .down (FRQ_ACT_GELU_TANH, gemma4), int8 (in, out) with f16
- * __scale siblings (src/qwen3moe.rs:148-152, src/gemma4.rs:174-181). */
+ * .gate_up / .down (FRQ_ACT_GELU_TANH, gemma4) (src/qwen3moe.rs:148-152,
+ * src/gemma4.rs:174-181), in any dtype expert_f32 reads (i8 / i4 / q4a
+ * with their f16 __scale (and __min) siblings, f16, f32; the first
+ * expert's dtype, every expert alike), uploaded as frq_moe_upload. */
 int frq_bundle_moe(frq_ctx* ctx, const frq_bundle* b, const char* prefix,
                    size_t n_exp, int act, frq_moe_w** out);
 

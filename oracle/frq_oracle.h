@@ -31,9 +31,19 @@
  *                                     cases, hand-derived lane-order case;
  *                                     fro_put_q4a by closed forms (min/max
  *                                     nibbles, reconstruction bound)
- *   fro_mm_i4 (M>1), fro_expert_mm    f64 brute force only; the reference
- *                                     has no test for these (its sgemm order
- *                                     is matrixmultiply's): tolerance parity
+ *   fro_mm_dot / fro_sgemm            a hand-derived case that separates the
+ *                                     256-long blocks from one chain and from
+ *                                     other block lengths, exact integers;
+ *                                     that it is matrixmultiply 0.3.10's order
+ *                                     (restated from that crate's published
+ *                                     gemm loop) no reference test pins
+ *   fro_mm_i4 (M>1), fro_expert_mm    f64 brute force and exact integers; the
+ *                                     reference has no test for these
+ *   fro_expert_f32                    closed forms per arm (i4 nibble order and
+ *                                     group index, q4a mul then add, f16, f32,
+ *                                     i8); fro_moe_ex_mt over f32 experts holding
+ *                                     an int8 bank's q * s is that bank's layer
+ *                                     bit for bit
  *   fro_moe_route / fro_moe           closed-form softmax + brute-force
  *                                     stable sort, f64 combine bound
  *   fro_nd_sum / fro_layernorm        hand-derived order case (the eight-lane

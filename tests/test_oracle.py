@@ -628,3 +628,105 @@ def test_put_q4a_closed_forms():
     assert np.array_equal(s2.view(np.uint16), s16) and np.array_equal(m2.view(np.uint16), m16)
     p3, s3, m3, _ = convert.put_q4a(np.ascontiguousarray(w.T), False)
     assert np.array_equal(p3, packed) and np.array_equal(s3, s2) and np.array_equal(m3, m2)
+
+
+# ---- a.dot's order (matrixmultiply 0.3.10 sgemm) and expert_f32's arms ----
+
+def test_mm_dot_blocks_of_256():
+    """matrixmultiply's gemm_loop: k in blocks of 256 (S_KC), each an FMA
+    chain from +0, the block results added in order.  x = [2^24, 0 x 255,
+    1 x 256] against ones: the sequential chain stays at 2^24 (each + 1 is
+    a tie to even), the blocked sum is 2^24 + 256 (block two sums to 256
+    exactly); a 128-long block, or a chain that carried on, gives 2^24."""
+    x = np.zeros(512, np.float32)
+    x[0] = 2.0 ** 24
+    x[256:] = 1.0
+    w = np.ones(512, np.float32)
+    assert oracle.mm_dot(x, w) == 2.0 ** 24 + 256
+    assert oracle.mm_dot(x[:256], w[:256]) == 2.0 ** 24  # one block: one chain
+    x2 = x.copy()
+    x2[256:384] = 0.0  # block two sums to 128
+    assert oracle.mm_dot(x2, w) == 2.0 ** 24 + 128
+    # exact small integers: any order gives the integer dot
+    rng = np.random.default_rng(0)
+    a = rng.integers(-50, 50, 1000).astype(np.float32)
+    b = rng.integers(-50, 50, 1000).astype(np.float32)
+    assert oracle.mm_dot(a, b) == float(np.dot(a.astype(np.int64), b.astype(np.int64)))
+
+
+def _i4_dequant_closed_form(packed, scale16, k, g):
+    from fieldrun_amd import convert
+    s4 = convert.unpack_i4(packed, k).astype(np.float32)  # (out, k)
+    sc = np.repeat(oracle.f16_to_f32(scale16), g, axis=1)[:, :k]
+    return np.ascontiguousarray((s4 * sc).T)  # (in, out); s4 * f16 scale is exact in f32
+
+
+@pytest.mark.parametrize("k,out", [(256, 48), (130, 9), (37, 5)])
+def test_expert_f32_arms_closed_forms(k, out):
+    """expert_f32 (src/bundle.rs:404-454) per arm against a closed form:
+    i4 = sign-extended nibble * scale[j, i / g] transposed to (in, out)
+    (even input in the low nibble); q4a = scale * u4 + min (one f32 mul,
+    one f32 add); f16 = the IEEE upcast; f32 as stored; i8 = q * scale[j]."""
+    from fieldrun_amd import convert
+    rng = np.random.default_rng(k)
+    src = (rng.standard_normal((out, k)) * 0.05).astype(np.float32)
+    packed, s16, g = convert.put_i4(src, True)
+    e = oracle.expert("i4", packed, oracle.f16_to_f32(s16.view(np.uint16)), None, g, k, out)
+    assert np.array_equal(oracle.expert_f32(e), _i4_dequant_closed_form(packed, s16.view(np.uint16), k, g))
+    qp, qs16, qm16, qg = convert.put_q4a(src, True)
+    lo, hi = (qp & 0x0F).astype(np.float32), (qp >> 4).astype(np.float32)
+    u4 = np.stack([lo, hi], axis=2).reshape(out, -1)[:, :k]
+    sc = np.repeat(qs16.astype(np.float32), qg, axis=1)[:, :k]
+    mn = np.repeat(qm16.astype(np.float32), qg, axis=1)[:, :k]
+    want = np.ascontiguousarray(((sc * u4).astype(np.float32) + mn).astype(np.float32).T)
+    e = oracle.expert("q4a", qp, qs16.astype(np.float32), qm16.astype(np.float32), qg, k, out)
+    assert np.array_equal(oracle.expert_f32(e), want)
+    t = np.ascontiguousarray(src.T)
+    h = t.astype(np.float16)
+    assert np.array_equal(oracle.expert_f32(oracle.expert("f16", h.view(np.uint16))), h.astype(np.float32))
+    assert np.array_equal(oracle.expert_f32(oracle.expert("f32", t)), t)
+    w8, s8 = convert.put_i8(src, True)
+    s8f = s8.astype(np.float32)
+    assert np.array_equal(oracle.expert_f32(oracle.expert("i8", w8, s8f)), (w8.astype(np.float32) * s8f).astype(np.float32))
+
+
+def test_expert_mm_any_dtype_f64_and_exact_integers():
+    """expert_mm = x . expert_f32: within f32 rounding of the f64 product,
+    and exact for small-integer activations against integer-valued f32
+    weights; the i8 arm equals fro_expert_mm_i8."""
+    from fieldrun_amd import convert
+    rng = np.random.default_rng(7)
+    src = (rng.standard_normal((40, 300)) * 0.05).astype(np.float32)
+    x = rng.standard_normal((6, 300)).astype(np.float32)
+    packed, s16, g = convert.put_i4(src, True)
+    e = oracle.expert("i4", packed, oracle.f16_to_f32(s16.view(np.uint16)), None, g, 300, 40)
+    W = oracle.expert_f32(e).astype(np.float64)
+    y = oracle.expert_mm(x, e)
+    ref = x.astype(np.float64) @ W
+    assert np.all(np.abs(y - ref) <= 1e-5 * (np.abs(x).astype(np.float64) @ np.abs(W)) + 1e-30)
+    xi = rng.integers(-9, 9, (4, 300)).astype(np.float32)
+    wi = rng.integers(-30, 30, (300, 17)).astype(np.float32)
+    yi = oracle.expert_mm(xi, oracle.expert("f32", wi))
+    assert np.array_equal(yi, (xi.astype(np.int64) @ wi.astype(np.int64)).astype(np.float32))
+    w8, s8 = convert.put_i8(src, True)
+    assert np.array_equal(oracle.expert_mm(x, oracle.expert("i8", w8, s8.astype(np.float32))),
+                          oracle.expert_mm_i8(x, w8, s8.astype(np.float32)))
+
+
+@pytest.mark.parametrize("act", [0, 1])
+def test_moe_ex_reduces_to_the_int8_bank(act):
+    """The layer over f32 experts that hold exactly the int8 bank's
+    dequantised values (q * s) is the int8 layer bit for bit: the generic
+    expert path adds nothing of its own to routing, gating or combine."""
+    from fieldrun_amd import synth
+    E, d, mi, k, T = 8, 96, 40, 3, 11
+    gate, gs, up, us, down, ds = synth.moe_layer(E, d, mi, 21 + act, act)
+    rng = np.random.default_rng(act)
+    x = rng.standard_normal((T, d)).astype(np.float32)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    pes = rng.uniform(0.5, 1.5, E).astype(np.float32) if act else None
+    f32 = lambda W, S: [oracle.expert("f32", (w.astype(np.float32) * s[None, :]).astype(np.float32))  # noqa: E731
+                        for w, s in zip(W, S)]
+    r8 = oracle.moe(x, lg, k, True, gate, gs, up, us, down, ds, act, pes)
+    rx = oracle.moe_ex(x, lg, k, True, f32(gate, gs), f32(up, us) if act == 0 else [], f32(down, ds), act, pes)
+    assert np.array_equal(r8.view(np.uint32), rx.view(np.uint32))
