@@ -19,7 +19,8 @@ and the first token), in tok/s; `ms_per_step` the whole call.
 four launches at the engine's shapes (q|k|v 3584->4608, o 3584->3584,
 gate|up 3584->37888, down 18944->3584): algorithmic bytes (N*K + 4N + 4K + 4N
 each) over the launches' summed average durations, HIP events on the
-library's stream, weights rotated over 3 replicas (beyond the 256 MB MALL).
+library's stream, weights rotated over at least 4 sets of more than 640 MB
+in all for each shape (beyond the 256 MB MALL).
 `roofline_prefill`: the prefill's dominant kernel, the int8 MFMA GEMM at the
 gate|up shape (M=2048, K=3584, N=37888) on pre-quantised rows, 2*M*N*K ops
 over its average duration, against the dense int8 peak.
@@ -79,6 +80,20 @@ def moe_bytes(T, E, d, mi, active):
     return active * (3 * d * mi + 4 * (mi + mi + d)) + 4 * T * d + 4 * T * d + 4 * T * E
 
 
+def moe_i4_bytes(T, E, d, mi, active, g=32):
+    # int4 experts: packed nibbles + f16 group scales of gate / up / down, x, out, logits
+    return active * (3 * d * mi // 2 + 2 * 3 * d * mi // g) + 4 * T * d + 4 * T * d + 4 * T * E
+
+
+ROT_BYTES = 640 << 20  # weight bytes a timed shape rotates over (beyond the 256 MB MALL)
+
+
+def n_rot(bytes_each):
+    """Weight sets a timed shape rotates over: at least 4, together more
+    than ROT_BYTES, so no repeat can be served from the MALL."""
+    return max(4, -(-ROT_BYTES // bytes_each))
+
+
 def host_threads():
     """Threads for the CPU baseline: the cores this process may run on (what
     rayon's default pool uses), at most 16 (the GPU box's CPU share)."""
@@ -111,7 +126,6 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3, help="timed configs[4] generate calls")
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--replicas", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-detail", action="store_true")
     ap.add_argument("--no-graphs", action="store_true",
@@ -149,23 +163,24 @@ def main():
         ctx.sync()
         return e0.elapsed_ms(e1) / iters
 
-    R = args.replicas
-
     def decode_linears():
         """The configs[4] layer's four linear shapes at M=1 (the engine's
-        kernel), 3 weight replicas each: per-launch us and algorithmic bytes."""
+        kernel), each rotated over n_rot sets: per-launch us and algorithmic
+        bytes."""
         rows = []
         for si, (k, n) in enumerate(C4_SHAPES):
             reps = []
-            for r in range(R):
+            nr = n_rot(n * k)
+            for r in range(nr):
                 wt, scale = synth.int8_weight(n, k, synth.seed(4, r) + si)
                 reps.append(ctx.upload_i8(wt, scale))
                 del wt
             a = synth.activations(1, k, synth.seed(4) + si)
             da, do = hip.DeviceArray.from_numpy(a), hip.DeviceArray((1, n), np.float32)
-            us = time_loop(lambda i: reps[i % R].mm_dev(da.ptr, 1, do.ptr), 60) * 1e3
+            us = time_loop(lambda i: reps[i % nr].mm_dev(da.ptr, 1, do.ptr), max(60, 2 * nr)) * 1e3
             rows.append({"K": k, "N": n, "us": round(us, 2), "bytes": int8_linear_bytes(1, k, n),
-                         "GBps": round(int8_linear_bytes(1, k, n) / (us * 1e-6) / 1e9, 1)})
+                         "GBps": round(int8_linear_bytes(1, k, n) / (us * 1e-6) / 1e9, 1),
+                         "rotation": {"sets": nr, "bytes": nr * n * k}})
             for w in reps:
                 w.free()
         return rows
@@ -391,18 +406,20 @@ def main():
 
 def run_detail(args, ctx, fa, hip, synth, convert, time_loop, log, threads, cfx):
     detail = {}
-    R = args.replicas
     # ---------------- the isolated int8 sweep ----------------
     shapes = list(synth.SWEEP_KN)
     weights, acts = [], []
     for si, (k, n) in enumerate(shapes):
-        weights.append([ctx.upload_i8(*synth.int8_weight(n, k, synth.seed(1, r) + si)) for r in range(R)])
+        weights.append([ctx.upload_i8(*synth.int8_weight(n, k, synth.seed(1, r) + si)) for r in range(n_rot(n * k))])
         a = synth.activations(1, k, synth.seed(1) + si)
         acts.append((a, hip.DeviceArray.from_numpy(a)))
-    detail["int8_sweep_m1"] = {"full_linear": {}, "gemv_kernel": {}}
+    detail["int8_sweep_m1"] = {"full_linear": {}, "gemv_kernel": {},
+                               "rotation": {f"K{k}_N{n}": {"sets": len(weights[si]), "bytes": len(weights[si]) * n * k}
+                                            for si, (k, n) in enumerate(shapes)}}
     for si, (k, n) in enumerate(shapes):
+        R = len(weights[si])
         o = hip.DeviceArray((1, n), np.float32)
-        us = time_loop(lambda i, si=si: weights[si][i % R].mm_dev(acts[si][1].ptr, 1, o.ptr), 60) * 1e3
+        us = time_loop(lambda i, si=si: weights[si][i % R].mm_dev(acts[si][1].ptr, 1, o.ptr), max(60, 2 * R)) * 1e3
         gb = int8_linear_bytes(1, k, n) / (us * 1e-6) / 1e9
         detail["int8_sweep_m1"]["full_linear"][f"K{k}_N{n}"] = {"us": round(us, 2), "GBps": round(gb, 1),
                                                                 "frac": round(gb / HBM_PEAK_GBS, 3)}
@@ -411,7 +428,7 @@ def run_detail(args, ctx, fa, hip, synth, convert, time_loop, log, threads, cfx)
         oi, ov = hip.DeviceArray((1, 32), np.uint32), hip.DeviceArray((1, 32), np.float32)
         ctx.quant_dev(acts[si][1].ptr, 1, k, a8.ptr, sa.ptr, oi.ptr, ov.ptr)
         gus = time_loop(lambda i, si=si: weights[si][i % R].mm_q_dev(a8.ptr, sa.ptr, oi.ptr, ov.ptr, 1, o.ptr),
-                        60) * 1e3
+                        max(60, 2 * R)) * 1e3
         qus = time_loop(lambda i, si=si: ctx.quant_dev(acts[si][1].ptr, 1, k, a8.ptr, sa.ptr, oi.ptr, ov.ptr),
                         60) * 1e3
         detail["int8_sweep_m1"]["gemv_kernel"][f"K{k}_N{n}"] = {
@@ -423,9 +440,10 @@ def run_detail(args, ctx, fa, hip, synth, convert, time_loop, log, threads, cfx)
     for m in (4, 16, 128):
         row = {}
         for si, (k, n) in enumerate(shapes):
+            R = len(weights[si])
             a = synth.activations(m, k, synth.seed(1, 20 + m) + si)
             da, do = hip.DeviceArray.from_numpy(a), hip.DeviceArray((m, n), np.float32)
-            us = time_loop(lambda i, si=si: weights[si][i % R].mm_dev(da.ptr, m, do.ptr), 30) * 1e3
+            us = time_loop(lambda i, si=si: weights[si][i % R].mm_dev(da.ptr, m, do.ptr), max(30, 2 * R)) * 1e3
             row[f"K{k}_N{n}"] = {"full_linear_us": round(us, 2),
                                  "full_linear_GBps": round(int8_linear_bytes(m, k, n) / (us * 1e-6) / 1e9, 1)}
         detail["int8_sweep_m"][f"M{m}"] = row
@@ -460,28 +478,32 @@ def run_detail(args, ctx, fa, hip, synth, convert, time_loop, log, threads, cfx)
     # ---------------- int4 / q4a decode GEMV (Gemma-2-2b shapes) ----------------
     detail["int4_m1_gemv"], detail["q4a_m1_gemv"] = {}, {}
     for (k, n) in [(2304, 9216), (9216, 2304), (2304, 2048)]:
-        reps = []
-        for r in range(3):
-            packed, s16, g = synth.int4_weight(n, k, synth.seed(2, r))
-            reps.append(ctx.upload_i4(packed, s16, k, g))
+        # the rotation: distinct weight buffers over the same few seeded
+        # sets (the bytes, not the values, decide what the MALL can serve)
+        nr = n_rot(int4_bytes(0, k, n))
+        base = [synth.int4_weight(n, k, synth.seed(2, r)) for r in range(3)]
+        reps = [ctx.upload_i4(base[r % 3][0], base[r % 3][1], k, base[r % 3][2]) for r in range(nr)]
         a = synth.activations(1, k, synth.seed(2, 9), outlier_scale=1.0)
         da, do = hip.DeviceArray.from_numpy(a), hip.DeviceArray((1, n), np.float32)
-        us = time_loop(lambda i: reps[i % 3].mm_dev(da.ptr, 1, do.ptr), 60) * 1e3
+        us = time_loop(lambda i: reps[i % nr].mm_dev(da.ptr, 1, do.ptr), max(60, 2 * nr)) * 1e3
         gb = int4_bytes(1, k, n) / (us * 1e-6) / 1e9
         detail["int4_m1_gemv"][f"K{k}_N{n}"] = {"us": round(us, 2), "GBps": round(gb, 1),
-                                                "frac": round(gb / HBM_PEAK_GBS, 3)}
+                                                "frac": round(gb / HBM_PEAK_GBS, 3),
+                                                "rotation": {"sets": nr, "bytes": nr * int4_bytes(0, k, n)}}
         for w in reps:
             w.free()
-        reps = []
+        base = []
         for r in range(3):
             rng = np.random.default_rng(synth.seed(5, r))
-            packed, s16, m16, g = convert.put_q4a(rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02),
-                                                  True)
-            reps.append(ctx.upload_q4a(packed, s16, m16, k, g))
-        us = time_loop(lambda i: reps[i % 3].mm_dev(da.ptr, 1, do.ptr), 60) * 1e3
+            base.append(convert.put_q4a(rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02), True))
+        g = base[0][3]
+        nr = n_rot(q4a_bytes(0, k, n, g))
+        reps = [ctx.upload_q4a(base[r % 3][0], base[r % 3][1], base[r % 3][2], k, g) for r in range(nr)]
+        us = time_loop(lambda i: reps[i % nr].mm_dev(da.ptr, 1, do.ptr), max(60, 2 * nr)) * 1e3
         gb = q4a_bytes(1, k, n, g) / (us * 1e-6) / 1e9
         detail["q4a_m1_gemv"][f"K{k}_N{n}"] = {"us": round(us, 2), "GBps": round(gb, 1),
-                                               "frac": round(gb / HBM_PEAK_GBS, 3)}
+                                               "frac": round(gb / HBM_PEAK_GBS, 3),
+                                               "rotation": {"sets": nr, "bytes": nr * q4a_bytes(0, k, n, g)}}
         for w in reps:
             w.free()
     log(f"int4 {detail['int4_m1_gemv']}; q4a {detail['q4a_m1_gemv']}")
@@ -528,6 +550,29 @@ def run_detail(args, ctx, fa, hip, synth, convert, time_loop, log, threads, cfx)
                                               "TFLOPs": round(2 * T * topk * 3 * d * mi / (us * 1e-6) / 1e12, 2)}
     bank.free()
     log(f"moe {detail['moe_qwen3_layer']}")
+    # the same layer with int4 experts (convert --dtype int4: put_i4, g = 32)
+    detail["moe_qwen3_layer_int4"] = {}
+    gate, up, down = synth.moe_layer_ex(E, d, mi, synth.seed(3), "int4")
+    pick = lambda lst, key: [m[key] for m in lst]  # noqa: E731
+    bank = ctx.upload_moe("i4", d, mi, pick(gate, "raw"), pick(down, "raw"), pick(up, "raw"), pick(gate, "scale"),
+                          pick(up, "scale"), pick(down, "scale"), g=32)
+    del gate, up, down
+    for T in (1, 512):
+        rng = np.random.default_rng(synth.seed(3, T))
+        xh = rng.standard_normal((T, d), dtype=np.float32)
+        lgh = rng.standard_normal((T, E), dtype=np.float32)
+        x, lg = hip.DeviceArray.from_numpy(xh), hip.DeviceArray.from_numpy(lgh)
+        o = hip.DeviceArray((T, d), np.float32)
+        us = time_loop(lambda i: bank.forward_dev(x.ptr, T, lg.ptr, topk, True, None, o.ptr), 10) * 1e3
+        sel, _ = ctx.moe_route(lgh, topk, True)
+        active = len(np.unique(sel))
+        nb = moe_i4_bytes(T, E, d, mi, active)
+        gb = nb / (us * 1e-6) / 1e9
+        detail["moe_qwen3_layer_int4"][f"T{T}"] = {"us": round(us, 1), "active_experts": active, "bytes": nb,
+                                                   "GBps": round(gb, 1), "frac_hbm": round(gb / HBM_PEAK_GBS, 3),
+                                                   "TFLOPs": round(2 * T * topk * 3 * d * mi / (us * 1e-6) / 1e12, 2)}
+    bank.free()
+    log(f"moe int4 {detail['moe_qwen3_layer_int4']}")
     # ---------------- GPT-2 small greedy decode ----------------
     detail["gpt2_decode"] = {}
     with tempfile.TemporaryDirectory(dir=shm_dir()) as tmp:

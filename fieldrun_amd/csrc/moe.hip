@@ -1443,17 +1443,19 @@ __global__ __launch_bounds__(256) void moe_ex_kernel(ExpView v, const float* __r
 // workgroup (tile of up to GM_TR rows of one expert, 128 output columns), 4
 // waves x two 16-column blocks.  Per group quad (128 inputs) the tile's
 // digit rows (24-bit fixed point per row, as the int8 bank's) pass through
-// LDS, laid out as the v_mfma_i32_16x16x32_i8 A operands: token group t,
-// group gi, lane 16 q + 4 tl + d holds digit d of row 4 t + tl, inputs
-// 8 q .. 8 q + 7 of the group (d == 3 lanes read zeros).  B is one 16-byte
+// LDS, laid out as the v_mfma_i32_16x16x32_i8 A operands in lane order:
+// token group t, group gi, lane 16 q + 4 tl + d holds digit d of row
+// 4 t + tl, inputs 8 q .. 8 q + 7 of the group (the d == 3 slots stay zero),
+// so a wave's operand is one linear 512-byte LDS read.  B is one 16-byte
 // load a lane and block (the quad's four groups of q4e), each 4-byte group
-// word two shifts / masks away from 16 x the sign-extended nibbles.  A group
-// gives the exact integer dots C_d of the three digits; the f32 sum over
-// the groups is acc += scale[j, g] * (C2 * 2^16 + C1 * 2^8 + C0), and
-// y = (so / 16) * acc.  The next quad's A and B loads are in flight during
-// the MFMAs.  Rows whose digits cannot carry the activations take
-// expert_mm's own order over the stored nibbles.
-constexpr int I4_AS = 8 * 4 * 4 * 4 * 3;  // A slots (8 bytes) of a quad: t, gi, q, tl, d
+// word sign-extended into eight int8 values in input order.  A group gives
+// the exact integer dots C_d of the three digits, and their combination
+// G = C2 * 2^16 + C1 * 2^8 + C0 is exact in int32 (|C2| <= 32 * 127 * 8,
+// |C1|, |C0| <= 32 * 128 * 8: |G| < 2^31); the f32 sum over the groups is
+// acc += scale[j, g] * G and y = so * acc.  The next quad's A and B loads
+// are in flight during the MFMAs.  Rows whose digits cannot carry the
+// activations take expert_mm's own order over the stored nibbles.
+constexpr int I4_AS = 8 * 4 * 64;  // A slots (8 bytes) of a quad: t, gi, lane
 
 struct I4Args {
     const int8_t* D;     // digit rows [src][3][Kp]
@@ -1466,9 +1468,19 @@ struct I4Args {
     float* y;
 };
 
+// The eight nibbles of a q4e group word (input 8 q + b in the low, 8 q + 4 + b
+// in the high half of byte b) as sign-extended int8 in input order: per byte
+// with y = x ^ 8, ((y + 0x78) ^ 0x80) is x as a signed nibble, and y + 0x78
+// <= 0x87 never carries into the next byte.
 __device__ __forceinline__ long i4_bop(uint32_t w) {
-    const uint32_t lo = (w & 0x0F0F0F0Fu) << 4, hi = w & 0xF0F0F0F0u;
+    const uint32_t y = w ^ 0x88888888u;
+    const uint32_t lo = ((y & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
+    const uint32_t hi = (((y >> 4) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
     return (long)(((unsigned long long)hi << 32) | lo);
+}
+
+__device__ __attribute__((noinline)) float i4_exact(const float* __restrict__ x, const ExpView& v, size_t e, int j) {
+    return exact_ex<FRQ_DT_I4>(x, v, e, j);
 }
 
 template <int NGT>
@@ -1482,7 +1494,8 @@ __device__ __forceinline__ void i4_body(const I4Args& A, uint2 (*As)[I4_AS], con
     const uint8_t* qb1 = A.q4e + (eb + min(cb0 + 1, A.nrb - 1)) * A.ng4 * 1024 + lane * 16;
     const uint16_t* sb0 = A.s4e + (eb + min(cb0, A.nrb - 1)) * A.ng4 * 64 + (lane & 15) * 4;
     const uint16_t* sb1 = A.s4e + (eb + min(cb0 + 1, A.nrb - 1)) * A.ng4 * 64 + (lane & 15) * 4;
-    // A staging: 3 items a thread, item = (row, digit, 16-byte chunk of the quad)
+    // A staging: item = (row, digit, 16-byte chunk of the quad), two 8-byte
+    // operand pieces each (q and q + 1 of group ch / 2)
     constexpr int NIT = 24 * 4 * NGT, UA = (NIT + 255) / 256;
     const int8_t* asrc[UA];
     int adst[UA];
@@ -1490,8 +1503,10 @@ __device__ __forceinline__ void i4_body(const I4Args& A, uint2 (*As)[I4_AS], con
     for (int u = 0; u < UA; ++u) {
         const int it = min(tid + 256 * u, NIT - 1), r = it / 24, dg = (it % 24) / 8, ch = it % 8;
         asrc[u] = A.D + ((size_t)srcs[min(r, rows - 1)] * 3 + dg) * A.Kp + 16 * ch;
-        adst[u] = tid + 256 * u < NIT ? ((((r >> 2) * 4 + (ch >> 1)) * 4 + 2 * (ch & 1)) * 4 + (r & 3)) * 3 + dg : -1;
+        adst[u] = tid + 256 * u < NIT ? ((r >> 2) * 4 + (ch >> 1)) * 64 + 32 * (ch & 1) + 4 * (r & 3) + dg : -1;
     }
+    // the d == 3 slots of both buffers: zero for good
+    for (int i = tid; i < 2 * NGT * 4 * 16; i += 256) As[i / (NGT * 64)][(i % (NGT * 64)) * 4 + 3] = make_uint2(0u, 0u);
     uint4 an[UA], bn0, bn1, bc0, bc1;
     uint2 sn0, sn1, sc0, sc1;
     auto ldq = [&](int q4) __attribute__((always_inline)) {
@@ -1507,7 +1522,7 @@ __device__ __forceinline__ void i4_body(const I4Args& A, uint2 (*As)[I4_AS], con
         for (int u = 0; u < UA; ++u)
             if (adst[u] >= 0) {
                 As[buf][adst[u]] = make_uint2(an[u].x, an[u].y);
-                As[buf][adst[u] + 12] = make_uint2(an[u].z, an[u].w);
+                As[buf][adst[u] + 16] = make_uint2(an[u].z, an[u].w);
             }
     };
     float acc[NGT][2];
@@ -1517,30 +1532,40 @@ __device__ __forceinline__ void i4_body(const I4Args& A, uint2 (*As)[I4_AS], con
     sta(0);
     bc0 = bn0; bc1 = bn1; sc0 = sn0; sc1 = sn1;
     __syncthreads();
-    const int ql = lane >> 4, tll = (lane >> 2) & 3, dgl = lane & 3;
-    const int abase = (ql * 4 + tll) * 3 + min(dgl, 2);
     for (int q4 = 0; q4 < A.ng4; ++q4) {
         const int buf = q4 & 1;
         if (q4 + 1 < A.ng4) ldq(q4 + 1);
-        const uint32_t w0[4] = {bc0.x, bc0.y, bc0.z, bc0.w}, w1[4] = {bc1.x, bc1.y, bc1.z, bc1.w};
-        const uint32_t s0[2] = {sc0.x, sc0.y}, s1[2] = {sc1.x, sc1.y};
+        long b0[4], b1[4];
+        float f0[4], f1[4];
+        {
+            const uint32_t w0[4] = {bc0.x, bc0.y, bc0.z, bc0.w}, w1[4] = {bc1.x, bc1.y, bc1.z, bc1.w};
+            const uint32_t s0[2] = {sc0.x, sc0.y}, s1[2] = {sc1.x, sc1.y};
 #pragma unroll
-        for (int gi = 0; gi < 4; ++gi) {
-            const long b0 = i4_bop(w0[gi]), b1 = i4_bop(w1[gi]);
-            const float f0 = h2f((uint16_t)(s0[gi >> 1] >> (16 * (gi & 1))));
-            const float f1 = h2f((uint16_t)(s1[gi >> 1] >> (16 * (gi & 1))));
-#pragma unroll
-            for (int t = 0; t < NGT; ++t) {
-                uint2 a = As[buf][(t * 4 + gi) * 48 + abase];
-                if (dgl == 3) a = make_uint2(0u, 0u);
-                const long aop = (long)(((unsigned long long)a.y << 32) | a.x);
-                const v4i c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, b0, v4i{0, 0, 0, 0}, 0, 0, 0);
-                const v4i c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, b1, v4i{0, 0, 0, 0}, 0, 0, 0);
-                acc[t][0] = __builtin_fmaf(f0, (float)c0[0] * 65536.0f + ((float)c0[1] * 256.0f + (float)c0[2]),
-                                           acc[t][0]);
-                acc[t][1] = __builtin_fmaf(f1, (float)c1[0] * 65536.0f + ((float)c1[1] * 256.0f + (float)c1[2]),
-                                           acc[t][1]);
+            for (int gi = 0; gi < 4; ++gi) {
+                b0[gi] = i4_bop(w0[gi]);
+                b1[gi] = i4_bop(w1[gi]);
+                f0[gi] = h2f((uint16_t)(s0[gi >> 1] >> (16 * (gi & 1))));
+                f1[gi] = h2f((uint16_t)(s1[gi >> 1] >> (16 * (gi & 1))));
             }
+        }
+#pragma unroll
+        for (int t = 0; t < NGT; ++t) {
+#pragma unroll
+            for (int gi = 0; gi < 4; ++gi) {
+                uint2 a = As[buf][(t * 4 + gi) * 64 + lane];
+                // the operand passes an ordered (volatile) point, so this
+                // token group's MFMAs cannot be hoisted above the previous
+                // group's sums: every MFMA of the quad in flight at once
+                // would hold 64 result registers a token group
+                asm volatile("" : "+v"(a.x), "+v"(a.y));
+                const long aop = (long)(((unsigned long long)a.y << 32) | a.x);
+                const v4i c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, b0[gi], v4i{0, 0, 0, 0}, 0, 0, 0);
+                const v4i c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, b1[gi], v4i{0, 0, 0, 0}, 0, 0, 0);
+                const int g0 = c0[0] * 65536 + c0[1] * 256 + c0[2], g1 = c1[0] * 65536 + c1[1] * 256 + c1[2];
+                acc[t][0] = __builtin_fmaf(f0[gi], (float)g0, acc[t][0]);
+                acc[t][1] = __builtin_fmaf(f1[gi], (float)g1, acc[t][1]);
+            }
+            asm volatile("" : "+v"(acc[t][0]), "+v"(acc[t][1]));
         }
         if (q4 + 1 < A.ng4) {
             sta(buf ^ 1);
@@ -1559,8 +1584,8 @@ __device__ __forceinline__ void i4_body(const I4Args& A, uint2 (*As)[I4_AS], con
             for (int c = 0; c < 2; ++c) {
                 const int j = (cb0 + c) * 16 + col;
                 if (j < A.N) {
-                    const float v = so >= 0.0f ? (so * 0.0625f) * acc[t][c]
-                                               : exact_ex<FRQ_DT_I4>(A.xf + (size_t)src * A.K, A.raw, (size_t)e, j);
+                    const float v = so >= 0.0f ? so * acc[t][c]
+                                               : i4_exact(A.xf + (size_t)src * A.K, A.raw, (size_t)e, j);
                     A.y[(size_t)prow * A.N + j] = v;
                 }
             }
@@ -1583,21 +1608,28 @@ __global__ __launch_bounds__(256) void moe_i4_kernel(I4Args A0, I4Args A1, int n
     const int xcd = blockIdx.x & 7, jb = blockIdx.x >> 3;
     const int tix = xcd + 8 * (jb / ncg), cgt = jb % ncg;
     const bool second = cgt >= ncg0;  // uniform
-    const I4Args& A = second ? A1 : A0;
     const int cg = second ? cgt - ncg0 : cgt;
     if (tix >= ntile[0]) return;  // uniform
-    const int e = tile_e[tix], r0 = tile_r[tix];
-    const int rows = min(GM_TR, cnt[e] - r0);
-    const int pbase = off[e] + r0;
+    // the tile's expert and rows, wave-uniform (scalar, so the branches on
+    // them stay scalar)
+    const int e = __builtin_amdgcn_readfirstlane(tile_e[tix]), r0 = __builtin_amdgcn_readfirstlane(tile_r[tix]);
+    const int rows = __builtin_amdgcn_readfirstlane(min(GM_TR, cnt[e] - r0));
+    const int pbase = __builtin_amdgcn_readfirstlane(off[e] + r0);
     const int tid = threadIdx.x;
     if (tid < GM_TR) {
         const int prow = pbase + min(tid, rows - 1);
         srcs[tid] = gather ? ptok[prow] : prow;
     }
     __syncthreads();
-    if (rows <= 4) i4_body<1>(A, As, srcs, e, rows, pbase, cg);
-    else if (rows <= 16) i4_body<4>(A, As, srcs, e, rows, pbase, cg);
-    else i4_body<8>(A, As, srcs, e, rows, pbase, cg);
+    // each argument block read in place (a reference chosen between the two
+    // at run time would copy both to scratch)
+    auto run = [&](const I4Args& A) __attribute__((always_inline)) {
+        if (rows <= 4) i4_body<1>(A, As, srcs, e, rows, pbase, cg);
+        else if (rows <= 16) i4_body<4>(A, As, srcs, e, rows, pbase, cg);
+        else i4_body<8>(A, As, srcs, e, rows, pbase, cg);
+    };
+    if (second) run(A1);
+    else run(A0);
 }
 
 // (E, out, ceil(in/2)) i4 rows + (E, out, ceil(in/g)) f16 scales -> q4e / s4e.
