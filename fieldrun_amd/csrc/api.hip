@@ -33,9 +33,6 @@ struct frq_ctx {
     void* ws = nullptr;
     size_t ws_bytes = 0;
     int* err = nullptr;  // device word: kernels atomically OR 1 on NaN input
-    // arrival counters of split-K reductions (last workgroup folds); zeroed
-    // at init and left zero by every kernel that uses them
-    unsigned* tickets = nullptr;
 };
 
 // Scratch of frq_mm_dev_noalloc: one static array per GPU (each device that
@@ -332,11 +329,10 @@ frq_ctx* frq_init(int device) {
     hipError_t e = hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipMalloc(&c->err, 256);
     if (e == hipSuccess) e = hipMemset(c->err, 0, 256);
-    if (e == hipSuccess) e = hipMalloc(&c->tickets, FRQ_TICKETS * sizeof(unsigned));
-    if (e == hipSuccess) e = hipMemset(c->tickets, 0, FRQ_TICKETS * sizeof(unsigned));
     if (e == hipSuccess) e = scratch_setup(device);
     if (e != hipSuccess) {
         hip_fail(e, "frq_init");
+        if (c->err) (void)hipFree(c->err);
         if (c->own) (void)hipStreamDestroy(c->own);
         delete c;
         return nullptr;
@@ -351,7 +347,6 @@ void frq_free(frq_ctx* c) {
     (void)hipStreamSynchronize(c->stream);
     if (c->ws) (void)hipFree(c->ws);
     if (c->err) (void)hipFree(c->err);
-    if (c->tickets) (void)hipFree(c->tickets);
     if (c->own) (void)hipStreamDestroy(c->own);
     delete c;
 }
@@ -572,7 +567,7 @@ int frq_mm_dev(frq_ctx* c, const frq_w* wh, const float* d_a, size_t m, float* d
     }
     if (w.dtype == FRQ_DT_I4) {
         if (int rc = ws_reserve(c, i4_ws_floats(w, m) * sizeof(float) + 256)) return rc;
-        HIPCHK(launch_i4(w, m, d_a, d_out, (float*)c->ws, c->tickets, c->stream), "launch i4");
+        HIPCHK(launch_i4(w, m, d_a, d_out, (float*)c->ws, c->stream), "launch i4");
         return FRQ_OK;
     }
     if (w.dtype == FRQ_DT_Q4A) {
@@ -605,7 +600,7 @@ int frq_mm_dev_noalloc(frq_ctx* c, const frq_w* wh, const float* d_a, size_t m, 
     if (w.dtype == FRQ_DT_I4) {
         const size_t need = i4_ws_floats(w, m) * sizeof(float) + 256;
         if (need > FRQ_NOALLOC_SCRATCH_BYTES) return too_big(need);
-        HIPCHK(launch_i4(w, m, d_a, d_out, reinterpret_cast<float*>(sp), c->tickets, c->stream), "launch i4");
+        HIPCHK(launch_i4(w, m, d_a, d_out, reinterpret_cast<float*>(sp), c->stream), "launch i4");
         return FRQ_OK;
     }
     if (w.dtype == FRQ_DT_Q4A) {
@@ -699,7 +694,7 @@ static int mm_host(frq_ctx* c, const frq_w* wh, const float* a, size_t m, float*
     } else if (w.dtype == FRQ_DT_Q4A) {
         HIPCHK(launch_q4a(w, m, d_a, d_out, c->stream), "launch q4a");
     } else {
-        HIPCHK(launch_i4(w, m, d_a, d_out, (float*)scratch, c->tickets, c->stream), "launch i4");
+        HIPCHK(launch_i4(w, m, d_a, d_out, (float*)scratch, c->stream), "launch i4");
     }
     HIPCHK(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
     if (int rc = check_err_word(c)) return rc;

@@ -34,7 +34,6 @@
 #define FRQ_KALIGN 128      // Kp alignment (a multiple of the GEMM k-step)
 #define FRQ_NALIGN 256      // Np alignment (a multiple of every N tile)
 #define FRQ_MALIGN 128      // Mp alignment of the a8 workspace (GEMM M tile)
-#define FRQ_TICKETS (1 << 20)  // per-context split-K arrival counters
 
 namespace frq {
 
@@ -458,7 +457,7 @@ hipError_t launch_rowdot_argmax_batch(const Weight& w, size_t nx, const float* x
                                       size_t os, unsigned long long* best, int* err, hipStream_t s);
 // int4 linear (any m).
 hipError_t launch_i4(const Weight& w, size_t m, const float* a, float* out,
-                     float* wsf, unsigned* tickets, hipStream_t s);
+                     float* wsf, hipStream_t s);
 size_t i4_ws_floats(const Weight& w, size_t m);
 // int4 at M == 1 in i4_dot_avx2's order (bit-exact) with coalesced loads, for
 // K % 32 == 0 and g in {32, 64}; hipErrorNotSupported for other shapes.

@@ -978,6 +978,7 @@ __global__ __launch_bounds__(GT) void gm_attn_tile_kernel(const float* __restric
 constexpr int PF_AP = 64, PF_KT = 128, PF_VK = 64, PF_NT = 256;
 static_assert(MM_KC % PF_VK == 0, "a value chunk lies in one a.dot block");
 constexpr size_t PF_MIN_ROWS = 1024;  // shorter prompts take the one-launch kernels (more workgroups)
+constexpr size_t PF_MAX_BYTES = (size_t)2 << 30;  // score buffer cap (570 MB at configs[4]'s 2048 + 128)
 __host__ __device__ inline int pf_rows(int rp) { return PF_AP / rp; }
 
 struct PfRow {
@@ -2157,9 +2158,14 @@ int gm_reserve(frq_ctx* c, frq_gemma* g, size_t npos, size_t rows, size_t nb = 1
                  o_xt = take(B > 1 ? 16 * g->d * 4 : 0),
                  o_q8f = take(round_up(g->ffn, FRQ_KALIGN)), o_qsa = take(4), o_qoi = take(FRQ_T * 4),
                  o_qov = take(FRQ_T * 4);
-    // the two-launch prefill attention's scores and tile maxima
+    // the two-launch prefill attention's scores and tile maxima: only for
+    // prompts that take it (PF_MIN_ROWS rows or more), and only while the
+    // buffer stays within PF_MAX_BYTES (longer prompts take the one-launch
+    // kernels, which need no buffer)
     const int rp = gm_pf_rp(g);
-    const size_t pf_nrb = rp ? (R + pf_rows(rp) - 1) / pf_rows(rp) : 0, kpad = pf_kpad(N);
+    const size_t kpad = pf_kpad(N);
+    size_t pf_nrb = (rp && R >= PF_MIN_ROWS) ? (R + pf_rows(rp) - 1) / pf_rows(rp) : 0;
+    if (pf_nrb * g->KV * kpad * PF_AP * 4 > PF_MAX_BYTES) pf_nrb = 0;
     const size_t o_pst = take(pf_nrb * g->KV * kpad * PF_AP * 4), o_pmx = take(pf_nrb * g->KV * PF_AP * 4);
     char* m = nullptr;
     GMCHK(hipMalloc(&m, off), "hipMalloc(gemma)");

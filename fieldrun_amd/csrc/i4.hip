@@ -1016,10 +1016,14 @@ static hipError_t launch_fused(const Weight& w, size_t m, const float* a, float*
 template <int G4, int IPT, int NT>
 hipError_t launch_stream_t(const Weight& w, int R, unsigned grid, size_t lds, const float* a, float* out,
                            hipStream_t s) {
-    if (lds > 64 * 1024) {
+    // the attribute once per instantiation, at the full 160 KB (later calls
+    // issue the launch only)
+    static bool attr = false;
+    if (lds > 64 * 1024 && !attr) {
         const hipError_t e = hipFuncSetAttribute((const void*)i4_m1_stream<G4, IPT, NT>,
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         if (e != hipSuccess) return e;
+        attr = true;
     }
     i4_m1_stream<G4, IPT, NT><<<dim3(grid), dim3(NT), lds, s>>>(w.q4raw, w.s4raw, (int)w.n, (int)w.k, R, a, out);
     return hipGetLastError();
@@ -1120,8 +1124,7 @@ hipError_t launch_i4_exact(const Weight& w, size_t m, const float* a, float* out
 }
 
 hipError_t launch_i4(const Weight& w, size_t m, const float* a, float* out,
-                     float* wsf, unsigned* tickets, hipStream_t s) {
-    (void)tickets;
+                     float* wsf, hipStream_t s) {
     if (m == 0) return hipSuccess;
     if (m == 1) {  // the reference's decode order, bit for bit, where the shape allows
         const hipError_t e = launch_i4_terms(w, a, out, s);

@@ -28,6 +28,7 @@ for _name, _res, _args in [
     ("hipEventSynchronize", C.c_int, [_P]),
     ("hipEventElapsedTime", C.c_int, [C.POINTER(C.c_float), _P, _P]),
     ("hipGetErrorString", C.c_char_p, [C.c_int]),
+    ("hipMemGetInfo", C.c_int, [C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]),
 ]:
     _f = getattr(_hip, _name)
     _f.restype = _res
@@ -112,3 +113,10 @@ def synchronize():
 def copy_d2d(dst: int, src: int, nbytes: int):
     """Device-to-device copy (the runtime's blit kernel), synchronous."""
     _chk(_hip.hipMemcpy(dst, src, nbytes, D2D), "hipMemcpy D2D")
+
+
+def mem_info():
+    """(free, total) bytes of the current device."""
+    f, t = C.c_size_t(), C.c_size_t()
+    _chk(_hip.hipMemGetInfo(C.byref(f), C.byref(t)), "hipMemGetInfo")
+    return f.value, t.value

@@ -227,9 +227,9 @@ def test_i4_blocked_nonfinite_and_extreme_groups(ctx):
     assert np.all(np.abs(out[ok] - ref[ok]) <= 1e-5 * mag[ok] + 1e-30)
 
 
-def test_i4_repeated_calls_rearm_tickets(ctx):
-    """The split-K fold re-arms its per-row-block counters: back-to-back
-    calls of different shapes give the same results as fresh ones."""
+def test_i4_repeated_calls_of_other_shapes(ctx):
+    """Back-to-back int4 calls of different shapes (sharing the context's
+    workspace) give the same results as fresh ones."""
     shapes = [(1, 9216, 2304), (16, 2304, 9216), (1, 2048, 2304)]
     ws, refs, acts = [], [], []
     for i, (m, n, k) in enumerate(shapes):

@@ -3,7 +3,11 @@ callers that cannot allocate) against frq_mm_dev, through the C ABI: the
 same bits for int8 decode batches, the int8 MFMA GEMM, int4 and q4a, over
 two calls in a row, the second with a smaller input (the static scratch
 keeps the first call's contents); a call that needs more scratch than the
-static array holds is refused with FRQ_ERR_ARG."""
+static array holds is refused with FRQ_ERR_ARG; and on a fresh context the
+calls leave the device's free memory unchanged, where frq_mm_dev grows the
+context's workspace."""
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -70,3 +74,40 @@ def test_noalloc_refuses_what_does_not_fit(ctx):
     a = synth.activations(4, k, 11)
     assert same_bits(run(w, a, True), run(w, a, False))
     w.free()
+
+
+def test_noalloc_allocates_nothing(ctx):
+    """The defining property: calls on a fresh context (its workspace still
+    empty) through the int8 decode batch, the int8 MFMA GEMM, int4 and q4a
+    leave the device's free memory where it was; the same calls through
+    frq_mm_dev on that context allocate its workspace (the control that
+    the measurement sees an allocation)."""
+    rng = np.random.default_rng(13)
+    wt, scale = synth.int8_weight(4864, 896, 61)
+    w8 = ctx.upload_i8(wt, scale)
+    packed, s16, g = synth.int4_weight(1024, 2304, 62)
+    w4 = ctx.upload_i4(packed, s16, 2304, g)
+    qp, qs, qm, qg = convert.put_q4a(rng.standard_normal((1024, 2304), dtype=np.float32) * np.float32(0.02), True)
+    wq = ctx.upload_q4a(qp, qs, qm, 2304, qg)
+    calls = []
+    for w, m, k, n, so in ((w8, 8, 896, 4864, 20.0), (w8, 64, 896, 4864, 20.0), (w4, 8, 2304, 1024, 1.0),
+                           (wq, 2, 2304, 1024, 1.0)):
+        da = hip.DeviceArray.from_numpy(synth.activations(m, k, 70 + m, outlier_scale=so))
+        do = hip.DeviceArray((m, n), np.float32)
+        calls.append((w, m, da, do))
+    for w, m, da, do in calls:  # the kernels' code loaded, on the test's context
+        w.mm_dev_noalloc(da.ptr, m, do.ptr)
+    ctx.sync()
+    fresh = fa.Context(0)
+    before = hip.mem_info()[0]
+    for w, m, da, do in calls:
+        assert fa.lib.frq_mm_dev_noalloc(fresh.h, w.h, C.c_void_p(da.ptr), m, C.c_void_p(do.ptr)) == 0
+    assert fa.lib.frq_sync(fresh.h) == 0
+    assert hip.mem_info()[0] == before
+    for w, m, da, do in calls:
+        assert fa.lib.frq_mm_dev(fresh.h, w.h, C.c_void_p(da.ptr), m, C.c_void_p(do.ptr)) == 0
+    assert fa.lib.frq_sync(fresh.h) == 0
+    assert hip.mem_info()[0] < before
+    fresh.close()
+    for w in (w8, w4, wq):
+        w.free()
