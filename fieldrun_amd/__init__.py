@@ -57,6 +57,7 @@ SIGNATURES = {
     "frq_mm": (_I, [_P, _P, _P, _S, _P]),
     "frq_mm_dev": (_I, [_P, _P, _P, _S, _P]),
     "frq_mm_exact_dev": (_I, [_P, _P, _P, _S, _P]),
+    "frq_mm_rows_dev": (_I, [_P, _P, _P, _S, _P]),
     "frq_mm_dev_noalloc": (_I, [_P, _P, _P, _S, _P]),
     "frq_mm_i8_debug": (_I, [_P, _P, _P, _S, _P, _P, _P, _P, _P, _P]),
     "frq_quant_pitch": (_S, [_S]),
@@ -338,6 +339,27 @@ class Weight:
         """Bundle::mm bit-identical to the reference's order at any M
         (frq_mm_exact_dev), enqueued on the context stream."""
         _check(lib.frq_mm_exact_dev(self.ctx.h, self.h, a_ptr, m, out_ptr))
+
+    def mm_rows_dev(self, a_ptr: int, m: int, out_ptr: int):
+        """m independent rows, each bit-identical to Bundle::mm at M == 1
+        (frq_mm_rows_dev), enqueued on the context stream."""
+        _check(lib.frq_mm_rows_dev(self.ctx.h, self.h, a_ptr, m, out_ptr))
+
+    def mm_rows(self, a: np.ndarray) -> np.ndarray:
+        """mm_rows_dev on host arrays: (M,K) f32 -> (M,N) f32."""
+        from . import hip
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        if a.ndim != 2 or a.shape[1] != self.k:
+            raise FrqError(FRQ_ERR_ARG, f"activation shape {a.shape} does not match K={self.k}")
+        da = hip.DeviceArray.from_numpy(a)
+        do = hip.DeviceArray((a.shape[0], self.n), np.float32)
+        try:
+            self.mm_rows_dev(da.ptr, a.shape[0], do.ptr)
+            self.ctx.sync()
+            return do.numpy()
+        finally:
+            da.free()
+            do.free()
 
     def mm_exact(self, a: np.ndarray) -> np.ndarray:
         """mm_exact_dev on host arrays: (M,K) f32 -> (M,N) f32."""

@@ -283,6 +283,11 @@ int set_error(int code, const std::string& msg) { return fail(code, msg); }
 int last_code() { return g_code; }
 int ctx_device(const frq_ctx* c) { return c->device; }
 int* ctx_err(frq_ctx* c) { return c->err; }
+int ctx_ws(frq_ctx* c, size_t bytes, void** ws) {
+    if (int rc = ws_reserve(c, bytes)) return rc;
+    *ws = c->ws;
+    return FRQ_OK;
+}
 int device_cus(int dev) {
     static std::atomic<int> cus[64];  // 0: not yet asked
     if (dev < 0 || dev >= 64) return 256;

@@ -430,6 +430,9 @@ int ctx_device(const frq_ctx* c);
 // The device's compute units (hipDeviceAttributeMultiprocessorCount, cached).
 int device_cus(int dev);
 int* ctx_err(frq_ctx* c);
+// The context workspace, grown to at least `bytes` (synchronises when it
+// grows, so not under graph capture).
+int ctx_ws(frq_ctx* c, size_t bytes, void** ws);
 const Weight* weight_of(const frq_w* w);
 // The int8 linear over m > 16 rows bit for bit as the skinny path gives it
 // (the reference's M > 1 arm), in one pass: the MFMA GEMM's exact i32 sums
@@ -466,7 +469,16 @@ hipError_t launch_i4_terms(const Weight& w, const float* a, float* out, hipStrea
 // dequantise + sequential-k GEMM): the paths decode engines use.
 hipError_t launch_i4_exact(const Weight& w, size_t m, const float* a, float* out, hipStream_t s);
 // m rows each in the M == 1 order (i4_dot_avx2), weights read once.
-hipError_t launch_i4_m1_rows(const Weight& w, size_t m, const float* a, float* out, hipStream_t s);
+// Batched decode rows (m independent rows, each in the M == 1 order):
+// i4_rows_a4_ok says whether the weight takes the broadcast kernel, which
+// reads its <= 16 rows in the a4 layout (launch_rows_to_a4: the rows
+// interleaved by k-quads, i4_a4_floats(K) floats); launch_i4_m1_rows takes
+// row-major rows and a4 scratch (or NULL: one M == 1 launch a row).
+bool i4_rows_a4_ok(const Weight& w);
+size_t i4_a4_floats(size_t k);
+hipError_t launch_rows_to_a4(const float* a, size_t m, size_t k, float* a4, hipStream_t s);
+hipError_t launch_i4_rows_a4(const Weight& w, size_t m, const float* a4, float* out, hipStream_t s);
+hipError_t launch_i4_m1_rows(const Weight& w, size_t m, const float* a, float* out, float* a4, hipStream_t s);
 // int4 (N, K/2) -> the MFMA layout (g == 32, K % 32 == 0); bytes of q4.
 size_t i4_blocked_bytes(size_t n, size_t k);
 hipError_t launch_i4_block(const uint8_t* raw, const uint16_t* sraw, size_t n,

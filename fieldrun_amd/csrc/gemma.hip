@@ -1816,7 +1816,8 @@ struct frq_gemma {
     unsigned long long* best = nullptr;
     int64_t *tok = nullptr, *ids = nullptr;
     float *qr = nullptr, *sc = nullptr;  // long-cache decode attention: roped q, scores
-    float* xt = nullptr;                 // batches: the head's input rows transposed (16 d)
+    float* xt = nullptr;                 // batches: 16 staging rows (the head's input transposed,
+                                         // the int4 linears' a4 layout), 16 max(d, ffn, H hd)
     float* pst = nullptr;                // prefill attention: scores / exps, [KV][block][kpad][64]
     float* pmx = nullptr;                // prefill attention: the pairs' maxima, [KV][block][64]
     // the quantised decode rows of the int8 linears (d- and ffn-wide: the
@@ -1968,12 +1969,13 @@ int gm_mm(frq_ctx* c, const frq_w* wh, const float* in, size_t m, float* outp) {
 // The linears of a batch step: m rows, each its own sequence's decode row,
 // so each row in the M == 1 order of its dtype (int8: the multi-row path is
 // bit-identical to M == 1 up to 16 rows; int4: i4_dot_avx2's order for every
-// row; q4a: one M == 1 call a row).
-int gm_mm_rows(frq_ctx* c, const frq_w* wh, const float* in, size_t m, float* outp) {
+// row, a4 the broadcast kernel's staging of i4_a4_floats(K) floats; q4a: one
+// M == 1 call a row).
+int gm_mm_rows(frq_ctx* c, const frq_w* wh, const float* in, size_t m, float* outp, float* a4) {
     const Weight& w = *weight_of(wh);
     hipStream_t s = (hipStream_t)frq_get_stream(c);
     if (w.dtype == FRQ_DT_I4) {
-        GMCHK(launch_i4_m1_rows(w, m, in, outp, s), "launch i4 rows");
+        GMCHK(launch_i4_m1_rows(w, m, in, outp, a4, s), "launch i4 rows");
         return FRQ_OK;
     }
     if (w.dtype == FRQ_DT_Q4A) {
@@ -2155,7 +2157,7 @@ int gm_reserve(frq_ctx* c, frq_gemma* g, size_t npos, size_t rows, size_t nb = 1
                  o_lg = take(B * g->vocab * 4), o_cur = take(4), o_best = take(B * 8), o_tok = take(B * N * 8),
                  o_ids = take(R * 8),
                  o_qr = take(g->H * g->hd * 4), o_sc = take(g->H * gm_pstride_n(N) * 4),
-                 o_xt = take(B > 1 ? 16 * g->d * 4 : 0),
+                 o_xt = take(B > 1 ? 16 * std::max({g->d, g->ffn, g->H * g->hd}) * 4 : 0),
                  o_q8f = take(round_up(g->ffn, FRQ_KALIGN)), o_qsa = take(4), o_qoi = take(FRQ_T * 4),
                  o_qov = take(FRQ_T * 4);
     // the two-launch prefill attention's scores and tile maxima: only for
@@ -2240,7 +2242,7 @@ int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_o
     };
     // the linears: in a batch step each row is its own sequence's decode row
     auto mm = [&](const frq_w* w, const float* in, float* outp) -> int {
-        return batch ? gm_mm_rows(c, w, in, m, outp) : gm_mm(c, w, in, m, outp);
+        return batch ? gm_mm_rows(c, w, in, m, outp, g->xt) : gm_mm(c, w, in, m, outp);
     };
     int64_t* tokp = g->tok + g->seq * g->cap_pos;  // this sequence's tokens (batch: sequence 0's)
     gm_embed_kernel<<<dim3((unsigned)m), dim3(GT), 0, s>>>(et.rowp, et.rpitch, et.dtype, et.scale, d, g->escale,
@@ -2737,6 +2739,22 @@ int frq_mm_exact_dev(frq_ctx* c, const frq_w* w, const float* d_a, size_t m, flo
     if (!d_a || !d_out) return set_error(FRQ_ERR_ARG, "null activation/output pointer");
     GDev dv(ctx_device(c));
     return gm_mm(c, w, d_a, m, d_out);
+}
+
+int frq_mm_rows_dev(frq_ctx* c, const frq_w* w, const float* d_a, size_t m, float* d_out) {
+    if (!c) return set_error(FRQ_ERR_ARG, "null context");
+    if (!w) return set_error(FRQ_ERR_ARG, "null weight");
+    const Weight& ww = *weight_of(w);
+    if (ww.dtype != FRQ_DT_I8 && ww.dtype != FRQ_DT_I4 && ww.dtype != FRQ_DT_Q4A)
+        return set_error(FRQ_ERR_DTYPE, "frq_mm_rows_dev: not a linear weight");
+    if (ww.device != ctx_device(c)) return set_error(FRQ_ERR_ARG, "weight lives on another device");
+    if (m == 0 || ww.n == 0) return FRQ_OK;
+    if (!d_a || !d_out) return set_error(FRQ_ERR_ARG, "null activation/output pointer");
+    GDev dv(ctx_device(c));
+    void* a4 = nullptr;
+    if (ww.dtype == FRQ_DT_I4)
+        if (int rc = ctx_ws(c, i4_a4_floats(ww.k) * sizeof(float), &a4)) return rc;
+    return gm_mm_rows(c, w, d_a, m, d_out, (float*)a4);
 }
 
 int frq_seq_fold_f32(frq_ctx* c, const float* x, size_t rows, size_t n, float init, float* out) {

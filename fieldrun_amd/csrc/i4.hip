@@ -275,90 +275,204 @@ __global__ __launch_bounds__(NT) void i4_m1_stream(const uint8_t* __restrict__ p
     for (int rr = tid; rr < nr; rr += NT) out[r0 + rr] = lds_seq_sum(terms + rr * ngp, ng, 0.0f);
 }
 
-// M independent rows (M <= 16), each in the M == 1 order (i4_dot_avx2): the
-// decode of a batch of sequences, where every sequence is its own
-// Gemma::generate.  A workgroup owns 16 weight rows; K goes in slices of 16
-// groups: the 16 token rows' activations of the slice are staged in LDS
-// (32-float units padded to 36 against bank conflicts), a thread takes one
-// (row, group) item, reads its nibbles once (the next slice's ahead) and
-// forms every token's group term scale * gsum in the AVX2 lane order, and
-// the thread of (token t, row r) then adds the slice's terms to its running
-// sum in group order (16 / G4 groups a slice, so the staged activations
-// take the same LDS for either group size).  Needs K % 32 == 0 and g == 32 G4.
-template <int G4>
-__global__ __launch_bounds__(256) void i4_terms_rows(const uint8_t* __restrict__ packed,
-                                                     const uint16_t* __restrict__ scale, int N, int K,
-                                                     const float* __restrict__ a, int M, float* __restrict__ out) {
-    constexpr int MT = 16, RB = 16, S = 16 / G4, U = 36;  // tokens, rows, groups a slice, floats a 32-unit
-    constexpr int g = 32 * G4, UPT = S * G4;          // 32-units of a token's slice
-    __shared__ __attribute__((aligned(16))) float act[MT][UPT * U];
-    __shared__ float term[MT][RB][S + 1];
-    const int tid = threadIdx.x, ng = K / g, pitch = K / 2, r0 = blockIdx.x * RB;
-    const int rr = tid / S, gl = tid % S;          // this thread's item: row r0 + rr, group sl S + gl
-    const int st = tid / RB, sr = tid % RB;        // this thread's sum: token st, row r0 + sr
-    const int row = min(r0 + rr, N - 1);           // clamped: the loads stay unconditional
-    const int nsl = (ng + S - 1) / S;
-    auto fetch = [&](int sl, uint4 (&w)[G4], float& sc) {
-        const int gi = min(sl * S + gl, ng - 1);
-        const uint8_t* pg = packed + (size_t)row * pitch + (size_t)gi * 16 * G4;
+// 16 FMAs of one weight register v of a 32-unit into lane chains
+// l[4 v .. 4 v + 3]: v_fmac_f32_dpp with row_newbcast:n gives each token
+// lane of a 16-lane DPP row the weight held by lane n of that row.  Lane n
+// holds element e = 8 (n & 3) + (n >> 2) + 4 v, which is nibble
+// (n >> 2) + 4 v of word n & 3 (chain q = e & 7, chunk c = e >> 3), and its
+// product takes av[e]; the FMAs go c-major so each chain advances in chunk
+// order.  START begins the chains: chunk 0 is a v_mul_f32_dpp, which
+// differs from fma(w, a, +0) only in giving -0 for a -0 product; a chain
+// is exact otherwise, the lane sums of i4_dot_avx2 then differ at most in
+// the sign of a zero, and so does a group term, which the running sum from
+// +0 absorbs (+0 + -0 == +0): the row sums are bit-identical.  The s_nop
+// gives the two wait states a DPP read needs after the VALU write of w,
+// which the compiler does not see inside the asm.
+#define FRQ_DPPF(op, acc, n, src) #op "_f32_dpp %" #acc ", %4, %" #src " row_newbcast:" #n " row_mask:0xf bank_mask:0xf\n\t"
+#define FRQ_DPP_C0(op) FRQ_DPPF(op, 0, 0, 5) FRQ_DPPF(op, 1, 4, 9) FRQ_DPPF(op, 2, 8, 13) FRQ_DPPF(op, 3, 12, 17)
+#define FRQ_DPP_C123                                                                                          \
+    FRQ_DPPF(v_fmac, 0, 1, 6) FRQ_DPPF(v_fmac, 1, 5, 10) FRQ_DPPF(v_fmac, 2, 9, 14) FRQ_DPPF(v_fmac, 3, 13, 18) \
+    FRQ_DPPF(v_fmac, 0, 2, 7) FRQ_DPPF(v_fmac, 1, 6, 11) FRQ_DPPF(v_fmac, 2, 10, 15)                            \
+    FRQ_DPPF(v_fmac, 3, 14, 19) FRQ_DPPF(v_fmac, 0, 3, 8) FRQ_DPPF(v_fmac, 1, 7, 12)                            \
+    FRQ_DPPF(v_fmac, 2, 11, 16) FRQ_DPPF(v_fmac, 3, 15, 20)
+#define FRQ_DPP_OPS(V)                                                                              \
+    : "+v"(l[4 * V]), "+v"(l[4 * V + 1]), "+v"(l[4 * V + 2]), "+v"(l[4 * V + 3])                    \
+    : "v"(w), "v"(av[4 * V]), "v"(av[8 + 4 * V]), "v"(av[16 + 4 * V]), "v"(av[24 + 4 * V]),         \
+      "v"(av[1 + 4 * V]), "v"(av[9 + 4 * V]), "v"(av[17 + 4 * V]), "v"(av[25 + 4 * V]),             \
+      "v"(av[2 + 4 * V]), "v"(av[10 + 4 * V]), "v"(av[18 + 4 * V]), "v"(av[26 + 4 * V]),            \
+      "v"(av[3 + 4 * V]), "v"(av[11 + 4 * V]), "v"(av[19 + 4 * V]), "v"(av[27 + 4 * V])
+template <int V, bool START>
+__device__ __forceinline__ void dpp_fma16(float (&l)[8], float w, const float (&av)[32]) {
+    if constexpr (START)
+        asm("s_nop 1\n\t" FRQ_DPP_C0(v_mul) FRQ_DPP_C123 FRQ_DPP_OPS(V));
+    else
+        asm("s_nop 1\n\t" FRQ_DPP_C0(v_fmac) FRQ_DPP_C123 FRQ_DPP_OPS(V));
+}
+#undef FRQ_DPP_OPS
+#undef FRQ_DPP_C123
+#undef FRQ_DPP_C0
+#undef FRQ_DPPF
+
+// The activation layout of i4_rows_dpp: the 16 token rows interleaved by
+// k-quads, a4[64 (k / 4) + 4 t + k % 4] = a[t][k] (rows t >= M zero), so
+// that the 16 token lanes of a DPP row read 256 contiguous bytes a load.
+__global__ void rows_to_a4_kernel(const float* __restrict__ a, int M, int K, float* __restrict__ a4) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;  // float4 i of a4: k-quad i / 16, token i % 16
+    const int kq = i >> 4, t = i & 15;
+    if (kq >= K / 4) return;
+    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (t < M) v = *reinterpret_cast<const float4*>(a + (size_t)t * K + 4 * kq);
+    reinterpret_cast<float4*>(a4)[i] = v;
+}
+
+// M independent rows (M <= 16), each in the M == 1 order (i4_dot_avx2),
+// with the weights broadcast across tokens: lane 16 d + t of a wave is token
+// t in DPP row d, and the workgroup's ND = 4 NW DPP rows D = 4 wave + d take
+// a slice of 2 ND groups in two rounds (groups 2 ND s + ND i + D, i = 0, 1).
+// A lane holds its token's 32 activations of the current 32-unit (read from
+// the a4 layout) and, for each of the workgroup's R weight rows, the packed
+// word t & 3 of the unit, whose nibbles t >> 2 and 4 + (t >> 2) become its
+// two f32 weight registers (dpp_fma16): each activation register serves R
+// rows and each weight register 16 tokens.  A group's term scale * gsum goes
+// to LDS (+0 for the groups past the end, which the running sum absorbs
+// exactly: it is never -0); after the slice's one barrier the lane of (row,
+// token) adds the slice's 2 ND terms to its running sum in group order (two
+// term buffers, so the next slice's writes never meet this slice's reads).
+// Activations and scales are loaded one step ahead, weights two.  Needs
+// K % (32 G4) == 0 and a matrix under 4 GB (32-bit offsets from each row's
+// base).
+template <int G4, int R, int NW>
+__global__ __launch_bounds__(64 * NW) void i4_rows_dpp(const uint8_t* __restrict__ packed,
+                                                       const uint16_t* __restrict__ scale, int N, int K,
+                                                       const float* __restrict__ a4, int M, float* __restrict__ out) {
+    static_assert(G4 == 1 || G4 == 2, "a group is one or two 32-units");
+    constexpr int ND = 4 * NW;                 // DPP rows
+    constexpr int GPS = 3 - G4;                // groups a DPP row takes a slice (two steps a slice)
+    constexpr int SG = ND * GPS;               // groups a slice
+    constexpr int TS = SG + 1;                 // term row stride (floats), odd: conflict-free reads
+    constexpr int L = (16 * R + NW - 1) / NW;  // serial lanes a wave
+    static_assert(L <= 64, "one (row, token) pair a lane");
+    __shared__ float tb[2][16 * R][TS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int t = lane & 15, D = 4 * wave + (lane >> 4);
+    const int ng = K / (32 * G4), r0 = blockIdx.x * R;
+    const int nst = (ng + SG - 1) / SG * 2;  // unit steps: two a slice
+    const int sh = 4 * (t >> 2);
+    const size_t pitch = (size_t)K / 2;
+    const uint8_t* wrow[R];
+    const uint16_t* srow[R];
 #pragma unroll
-        for (int h = 0; h < G4; ++h) w[h] = *reinterpret_cast<const uint4*>(pg + 16 * h);
-        sc = h2f(scale[(size_t)row * ng + gi]);
-    };
-    uint4 wn[G4];
-    float sn;
-    fetch(0, wn, sn);
-    float sum = 0.0f;
-    for (int sl = 0; sl < nsl; ++sl) {
-        const int k0 = sl * S * g, kl = min(S * g, K - k0);  // this slice's k range
-        // stage the M token rows' k0 .. k0 + kl (float4 at a time)
-        for (int i = tid; i < MT * (S * g / 4); i += 256) {
-            const int t = i / (S * g / 4), q = i % (S * g / 4);
-            if (t < M && 4 * q < kl)
-                *reinterpret_cast<float4*>(&act[t][(4 * q) / 32 * U + (4 * q) % 32]) =
-                    *reinterpret_cast<const float4*>(a + (size_t)t * K + k0 + 4 * q);
-        }
-        uint4 wc[G4];
-#pragma unroll
-        for (int h = 0; h < G4; ++h) wc[h] = wn[h];
-        const float sc = sn;
-        if (sl + 1 < nsl) fetch(sl + 1, wn, sn);
-        __syncthreads();
-        const bool item = rr < RB && sl * S + gl < ng;
-        if (item) {
-            float wf[G4][32];
-#pragma unroll
-            for (int h = 0; h < G4; ++h) {
-                const uint32_t ws[4] = {wc[h].x, wc[h].y, wc[h].z, wc[h].w};
-#pragma unroll
-                for (int e = 0; e < 32; ++e) wf[h][e] = (float)((int)(ws[e / 8] << (28 - 4 * (e % 8))) >> 28);
-            }
-            for (int t = 0; t < M; ++t) {
-                float l[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-                for (int h = 0; h < G4; ++h) {
-                    const float* ab = &act[t][(gl * G4 + h) * U];
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        const float4 a0 = *reinterpret_cast<const float4*>(ab + 8 * c);
-                        const float4 a1 = *reinterpret_cast<const float4*>(ab + 8 * c + 4);
-                        const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-#pragma unroll
-                        for (int q = 0; q < 8; ++q) l[q] = __builtin_fmaf(wf[h][8 * c + q], av[q], l[q]);
-                    }
-                }
-                const float q0 = l[0] + l[4], q1 = l[1] + l[5], q2 = l[2] + l[6], q3 = l[3] + l[7];
-                term[t][rr][gl] = sc * ((q0 + q2) + (q1 + q3));
-            }
-        }
-        __syncthreads();
-        if (st < M) {
-            const int ns = min(S, ng - sl * S);
-            for (int j = 0; j < ns; ++j) sum = sum + term[st][sr][j];
-        }
-        __syncthreads();
+    for (int r = 0; r < R; ++r) {
+        const size_t row = (size_t)min(r0 + r, N - 1);  // clamped: loads stay unconditional
+        wrow[r] = packed + row * pitch;
+        srow[r] = scale + row * ng;
     }
-    if (st < M && r0 + sr < N) out[(size_t)st * N + r0 + sr] = sum;
+    const float* at = a4 + 4 * t;
+    // serial lane: pair p = wave L + lane -> (row p >> 4, token p & 15)
+    const int p = wave * L + lane;
+    const bool ser = lane < L && p < 16 * R;
+    float sum = 0.0f;
+    struct WB {
+        uint32_t w[R];
+    };
+    struct AB {
+        float4 a[8];
+        uint32_t sc[R];
+    };
+    // step j: slice j / 2; with G4 == 1 round j % 2 of the slice, with G4 == 2
+    // unit j % 2 of the DPP row's one group
+    auto group_of = [&](int j) { return (j >> 1) * SG + (G4 == 1 ? (j & 1) * ND : 0) + D; };
+    auto unit_of = [&](int j, int gi) { return min(gi, ng - 1) * G4 + (G4 == 2 ? (j & 1) : 0); };
+    auto load_w = [&](int j, WB& b) {
+        const uint32_t wo = (uint32_t)unit_of(j, group_of(j)) * 16 + 4 * (t & 3);
+#pragma unroll
+        for (int r = 0; r < R; ++r) b.w[r] = *reinterpret_cast<const uint32_t*>(wrow[r] + wo);
+    };
+    auto load_a = [&](int j, AB& b) {
+        const int gi = group_of(j);
+        const float* ap = at + (size_t)unit_of(j, gi) * 512;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) b.a[i] = *reinterpret_cast<const float4*>(ap + 64 * i);
+        const uint32_t so = 2 * (uint32_t)min(gi, ng - 1);
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            b.sc[r] = *reinterpret_cast<const uint16_t*>(reinterpret_cast<const uint8_t*>(srow[r]) + so);
+    };
+    float l[R][8];  // each group's chains start with a product (dpp_fma16<., true>)
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int q = 0; q < 8; ++q) l[r][q] = 0.0f;  // defined inputs for the first asm
+    // ODD: the slice's second step, which ends every chain and the slice
+    auto step = [&](auto odd, int j, const WB& wb, const AB& ab) {
+        constexpr bool O = decltype(odd)::value;
+        constexpr bool START = G4 == 1 || !O;
+        float av[32];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            av[4 * i] = ab.a[i].x;
+            av[4 * i + 1] = ab.a[i].y;
+            av[4 * i + 2] = ab.a[i].z;
+            av[4 * i + 3] = ab.a[i].w;
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float w0 = (float)(int)__builtin_amdgcn_sbfe((int)wb.w[r], sh, 4);
+            const float w1 = (float)(int)__builtin_amdgcn_sbfe((int)wb.w[r], sh + 16, 4);
+            dpp_fma16<0, START>(l[r], w0, av);
+            dpp_fma16<1, START>(l[r], w1, av);
+        }
+        if constexpr (G4 == 2 && !O) return;  // the group goes on in the odd step
+        float(&tbs)[16 * R][TS] = tb[(j >> 1) & 1];
+        const int gi = group_of(j);
+        const int col = gi - (j >> 1) * SG;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float q0 = l[r][0] + l[r][4], q1 = l[r][1] + l[r][5], q2 = l[r][2] + l[r][6],
+                        q3 = l[r][3] + l[r][7];
+            const float term = h2f((uint16_t)ab.sc[r]) * ((q0 + q2) + (q1 + q3));
+            tbs[r * 16 + t][col] = gi < ng ? term : 0.0f;
+        }
+        if constexpr (!O) return;
+        __syncthreads();
+        if (ser) {
+            float v[SG];
+#pragma unroll
+            for (int i = 0; i < SG; ++i) v[i] = tbs[p][i];
+#pragma unroll
+            for (int i = 0; i < SG; ++i) sum = sum + v[i];
+        }
+    };
+    using T = std::true_type;
+    using F = std::false_type;
+    // The loads are unconditional (past the end: the last step again), so
+    // the wait for a step's data never covers a later one's, and fenced so
+    // that they issue before the step they run ahead of.
+    auto issued = [] {
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    WB wc, wn, w2;
+    AB a0, a1;
+    load_w(0, wc);
+    load_a(0, a0);
+    load_w(1, wn);
+    for (int j = 0; j < nst; j += 2) {
+        load_w(min(j + 2, nst - 1), w2);
+        load_a(j + 1, a1);
+        issued();
+        step(F{}, j, wc, a0);
+        load_w(min(j + 3, nst - 1), wc);
+        load_a(min(j + 2, nst - 1), a0);
+        issued();
+        step(T{}, j + 1, wn, a1);
+        wn = wc;
+        wc = w2;
+    }
+    if (ser) {
+        const int pr = p >> 4, pt = p & 15;
+        if (pt < M && r0 + pr < N) out[(size_t)pt * N + r0 + pr] = sum;
+    }
 }
 
 // M > 1: dequantise w = s4 * scale (f32, exact) and sum in a.dot's order
@@ -1087,20 +1201,62 @@ hipError_t launch_i4_terms(const Weight& w, const float* a, float* out, hipStrea
     return hipGetLastError();
 }
 
-// m rows, each in the M == 1 order (bit-identical to m launches at M == 1).
-hipError_t launch_i4_m1_rows(const Weight& w, size_t m, const float* a, float* out, hipStream_t s) {
+// Whether launch_i4_rows_a4 takes this weight (else launch_i4_m1_rows runs
+// the rows one M == 1 launch at a time).
+bool i4_rows_a4_ok(const Weight& w) {
+    return (w.g == 32 || w.g == 64) && w.k % w.g == 0 && w.k <= (size_t)INT32_MAX &&
+           w.n <= (size_t)INT32_MAX && w.n * w.k / 2 < ((size_t)1 << 32);
+}
+
+size_t i4_a4_floats(size_t k) { return 16 * k; }
+
+hipError_t launch_rows_to_a4(const float* a, size_t m, size_t k, float* a4, hipStream_t s) {
+    const size_t n4 = 4 * k;  // float4 of a4
+    rows_to_a4_kernel<<<dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s>>>(a, (int)m, (int)k, a4);
+    return hipGetLastError();
+}
+
+namespace {
+template <int G4, int R>
+hipError_t rows_dpp(const Weight& w, int nw, size_t m, const float* a4, float* out, hipStream_t s) {
+    const unsigned grid = (unsigned)((w.n + R - 1) / R);
+    if (nw == 3)
+        i4_rows_dpp<G4, R, 3><<<dim3(grid), dim3(192), 0, s>>>(w.q4raw, w.s4raw, (int)w.n, (int)w.k, a4, (int)m, out);
+    else
+        i4_rows_dpp<G4, R, 4><<<dim3(grid), dim3(256), 0, s>>>(w.q4raw, w.s4raw, (int)w.n, (int)w.k, a4, (int)m, out);
+    return hipGetLastError();
+}
+}  // namespace
+
+// m <= 16 rows in the a4 layout (launch_rows_to_a4), each in the M == 1
+// order.  Workgroups of 3 or 4 waves (12 or 16 DPP rows, whichever leaves
+// the fewer idle groups in the last slice; 4 on a tie) and 6 rows (each
+// activation register used 6 times) for wide outputs, 4 below 8192 rows,
+// where more workgroups matter more (measured on the Gemma-2 2B shapes).
+hipError_t launch_i4_rows_a4(const Weight& w, size_t m, const float* a4, float* out, hipStream_t s) {
     if (m == 0 || w.n == 0) return hipSuccess;
-    if (m <= 16 && w.k % 32 == 0 && (w.g == 32 || w.g == 64) && ((uintptr_t)a & 15) == 0 &&
-        w.k <= (size_t)INT32_MAX && w.n <= (size_t)INT32_MAX) {
-        const unsigned grid = (unsigned)((w.n + 15) / 16);
-        if (w.g == 32)
-            i4_terms_rows<1><<<dim3(grid), dim3(256), 0, s>>>(w.q4raw, w.s4raw, (int)w.n, (int)w.k, a, (int)m, out);
-        else
-            i4_terms_rows<2><<<dim3(grid), dim3(256), 0, s>>>(w.q4raw, w.s4raw, (int)w.n, (int)w.k, a, (int)m, out);
-        return hipGetLastError();
+    if (m > 16 || !i4_rows_a4_ok(w)) return hipErrorNotSupported;
+    const size_t ng = w.k / w.g, gps = w.g == 32 ? 2 : 1;  // groups a DPP row takes a slice
+    const int nw = (ng + 12 * gps - 1) / (12 * gps) * 12 < (ng + 16 * gps - 1) / (16 * gps) * 16 ? 3 : 4;
+    const bool r6 = w.n >= 8192;
+    if (w.g == 32) return r6 ? rows_dpp<1, 6>(w, nw, m, a4, out, s) : rows_dpp<1, 4>(w, nw, m, a4, out, s);
+    return r6 ? rows_dpp<2, 6>(w, nw, m, a4, out, s) : rows_dpp<2, 4>(w, nw, m, a4, out, s);
+}
+
+// m rows, each in the M == 1 order (bit-identical to m launches at M == 1);
+// a4 is scratch of i4_a4_floats(K) floats (16-byte aligned).
+hipError_t launch_i4_m1_rows(const Weight& w, size_t m, const float* a, float* out, float* a4, hipStream_t s) {
+    if (m == 0 || w.n == 0) return hipSuccess;
+    for (size_t r0 = 0; r0 < m; r0 += 16) {
+        const size_t mm = std::min<size_t>(16, m - r0);
+        if (a4 && i4_rows_a4_ok(w)) {
+            if (hipError_t e = launch_rows_to_a4(a + r0 * w.k, mm, w.k, a4, s)) return e;
+            if (hipError_t e = launch_i4_rows_a4(w, mm, a4, out + r0 * w.n, s)) return e;
+            continue;
+        }
+        for (size_t i = r0; i < r0 + mm; ++i)
+            if (hipError_t e = launch_i4_exact(w, 1, a + i * w.k, out + i * w.n, s)) return e;
     }
-    for (size_t i = 0; i < m; ++i)
-        if (hipError_t e = launch_i4_exact(w, 1, a + i * w.k, out + i * w.n, s)) return e;
     return hipSuccess;
 }
 

@@ -140,6 +140,14 @@ int frq_mm_dev(frq_ctx* ctx, const frq_w* w, const float* d_a, size_t m,
  * run this linear. */
 int frq_mm_exact_dev(frq_ctx* ctx, const frq_w* w, const float* d_a, size_t m,
                      float* d_out);
+/* m independent rows, each Bundle::mm at M == 1 (src/bundle.rs:644-919):
+ * row i of d_out is bit-identical to frq_mm_dev(ctx, w, d_a + i*K, 1, ...)
+ * (int8: 688-756 at M == 1; int4: i4_dot_avx2's order, 767-776; q4a:
+ * 802-845 at M == 1).  The reference reaches this when each of m sequences
+ * runs its own decode step (Gemma::generate, src/gemma.rs:416, once per
+ * sequence); the batched decode engine runs its linears through it. */
+int frq_mm_rows_dev(frq_ctx* ctx, const frq_w* w, const float* d_a, size_t m,
+                    float* d_out);
 /* No counterpart in the reference.  frq_mm_dev that allocates nothing, for
  * callers that cannot call hipMalloc (code under HIP graph capture, tight
  * serving loops, harnesses that forbid allocation).  The per-call scratch
