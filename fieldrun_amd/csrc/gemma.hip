@@ -145,10 +145,12 @@ __device__ __forceinline__ float* gm_norm_body(float* __restrict__ x, const floa
 __global__ __launch_bounds__(NORM_NT) void gm_norm_kernel(float* __restrict__ x, const float* __restrict__ y,
                                                           const float* __restrict__ wpost,
                                                           const float* __restrict__ wnext, float* __restrict__ out,
-                                                          int d, float eps, int row0) {
+                                                          int d, float eps, int row0, float* __restrict__ a4) {
     extern __shared__ float4 lds4[];
-    gm_norm_body<NORM_NT>(x, y, wpost, wnext, out, d, eps, (size_t)(row0 + blockIdx.x) * d,
-                          reinterpret_cast<float*>(lds4));
+    const float* t = gm_norm_body<NORM_NT>(x, y, wpost, wnext, out, d, eps, (size_t)(row0 + blockIdx.x) * d,
+                                           reinterpret_cast<float*>(lds4));
+    if (a4)
+        for (int c = threadIdx.x; c < d; c += NORM_NT) a4[(c >> 2) * 64 + 4 * (row0 + blockIdx.x) + (c & 3)] = t[c];
 }
 
 // The norm kernel with the row in registers: float4 q = tid + NORM_NT i of
@@ -163,7 +165,7 @@ template <int NV>
 __global__ __launch_bounds__(NORM_NT) void gm_norm2_kernel(float* __restrict__ x, const float* __restrict__ y,
                                                            const float* __restrict__ wpost,
                                                            const float* __restrict__ wnext, float* __restrict__ out,
-                                                           int d, float eps, int row0) {
+                                                           int d, float eps, int row0, float* __restrict__ a4) {
     extern __shared__ float4 lds4[];
     float4* sq4 = lds4;
     float* sq = reinterpret_cast<float*>(lds4);
@@ -216,7 +218,11 @@ __global__ __launch_bounds__(NORM_NT) void gm_norm2_kernel(float* __restrict__ x
     const float inv = inv_of(nv);
 #pragma unroll
     for (int i = 0; i < NV; ++i)
-        if (valid(i)) reinterpret_cast<float4*>(out + r)[tid + NORM_NT * i] = mul(scl(nv[i], inv), wnv[i]);
+        if (valid(i)) {
+            const float4 o = mul(scl(nv[i], inv), wnv[i]);
+            reinterpret_cast<float4*>(out + r)[tid + NORM_NT * i] = o;
+            if (a4) reinterpret_cast<float4*>(a4)[(size_t)(tid + NORM_NT * i) * 16 + row0 + blockIdx.x] = o;
+        }
 }
 
 // ---- the int8 down linear's activation quant, fused into the activation
@@ -405,7 +411,8 @@ __global__ __launch_bounds__(GT) void gm_attn_kernel(const float* __restrict__ q
                                                      float cap, int sliding, int window, int pstride,
                                                      float* __restrict__ att, int div,
                                                      const float* __restrict__ bias, const float* __restrict__ qn,
-                                                     const float* __restrict__ kn, float eps, long long bst = 0) {
+                                                     const float* __restrict__ kn, float eps, long long bst = 0,
+                                                     float* __restrict__ a4 = nullptr) {
     extern __shared__ float4 lds4[];
     float* q = reinterpret_cast<float*>(lds4);
     float* kvs = q + ((hd + 3) & ~3);
@@ -546,7 +553,12 @@ __global__ __launch_bounds__(GT) void gm_attn_kernel(const float* __restrict__ q
             }
             return acc;
         };
-        att[(size_t)i * H * hd + (size_t)h * hd + c] = mm_blocks(j0, nk, chain);
+        const float o = mm_blocks(j0, nk, chain);
+        att[(size_t)i * H * hd + (size_t)h * hd + c] = o;
+        if (a4) {
+            const size_t k = (size_t)h * hd + c;
+            a4[(k >> 2) * 64 + 4 * i + (k & 3)] = o;
+        }
     }
 }
 
@@ -1735,8 +1747,11 @@ __global__ __launch_bounds__(VT) void gm_dec_value_blk_kernel(const float* __res
 
 // h = act(gate) * up over m rows of the [gate | up] buffer: gelu_tanh
 // (gemma.rs:31-34) or, silu, x / (1 + exp(-x)) (rope.rs:39-41).
+// a4 (a batch's rows, <= 16, feeding an int4 linear): the rows also in the
+// k-quad interleaved layout of launch_i4_rows_a4.
 __global__ __launch_bounds__(GT) void gm_geglu_kernel(const float* __restrict__ gu, int ffn, size_t total,
-                                                      float c, float* __restrict__ hm, int silu) {
+                                                      float c, float* __restrict__ hm, int silu,
+                                                      float* __restrict__ a4 = nullptr) {
     auto act = [&](float x) __attribute__((always_inline)) {
         return silu ? x / (1.0f + libm::frq_expf_sel(-x))
                     : 0.5f * x * (1.0f + libm::frq_tanhf(c * (x + 0.044715f * x * x * x)));
@@ -1749,14 +1764,17 @@ __global__ __launch_bounds__(GT) void gm_geglu_kernel(const float* __restrict__ 
             const size_t r = i / f4, c4 = i - r * f4;
             const float4 g = reinterpret_cast<const float4*>(gu + r * 2 * ffn)[c4];
             const float4 u = reinterpret_cast<const float4*>(gu + r * 2 * ffn + ffn)[c4];
-            reinterpret_cast<float4*>(hm)[i] = make_float4(act(g.x) * u.x, act(g.y) * u.y, act(g.z) * u.z,
-                                                           act(g.w) * u.w);
+            const float4 h = make_float4(act(g.x) * u.x, act(g.y) * u.y, act(g.z) * u.z, act(g.w) * u.w);
+            reinterpret_cast<float4*>(hm)[i] = h;
+            if (a4) reinterpret_cast<float4*>(a4)[c4 * 16 + r] = h;
         }
         return;
     }
     for (size_t i = (size_t)blockIdx.x * GT + threadIdx.x; i < total; i += (size_t)gridDim.x * GT) {
         const size_t r = i / ffn, col = i - r * ffn;
-        hm[i] = act(gu[r * 2 * ffn + col]) * gu[r * 2 * ffn + ffn + col];
+        const float h = act(gu[r * 2 * ffn + col]) * gu[r * 2 * ffn + ffn + col];
+        hm[i] = h;
+        if (a4) a4[(col >> 2) * 64 + 4 * r + (col & 3)] = h;
     }
 }
 
@@ -2229,33 +2247,47 @@ int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_o
     // one decode row of an int8 down linear takes its quant from the
     // activation kernel
     const bool q8f = m == 1 && !batch && quant_nv4(g->ffn) > 0;
-    auto norm = [&](const float* y, const float* wpost, const float* wnext, int rows, int row0) {
+    // A batch step's int4 linears read their rows in the k-quad interleaved
+    // layout, which the kernel producing those rows also writes (into the
+    // staging rows xt): a4_for(w) is where, or NULL when w does not take it.
+    auto a4_for = [&](const frq_w* w) -> float* {
+        return batch && m <= 16 && g->xt && weight_of(w)->dtype == FRQ_DT_I4 && i4_rows_a4_ok(*weight_of(w))
+                   ? g->xt
+                   : nullptr;
+    };
+    auto norm = [&](const float* y, const float* wpost, const float* wnext, int rows, int row0, float* a4) {
         const size_t n2 = gm_norm2_lds(d);
         switch ((d / 4 + NORM_NT - 1) / NORM_NT) {
-            case 1: gm_norm2_kernel<1><<<dim3(rows), dim3(NORM_NT), n2, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, row0); break;
-            case 2: gm_norm2_kernel<2><<<dim3(rows), dim3(NORM_NT), n2, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, row0); break;
-            case 3: gm_norm2_kernel<3><<<dim3(rows), dim3(NORM_NT), n2, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, row0); break;
-            case 4: gm_norm2_kernel<4><<<dim3(rows), dim3(NORM_NT), n2, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, row0); break;
-            default: gm_norm_kernel<<<dim3(rows), dim3(NORM_NT), nlds, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, row0);
+            case 1: gm_norm2_kernel<1><<<dim3(rows), dim3(NORM_NT), n2, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, row0, a4); break;
+            case 2: gm_norm2_kernel<2><<<dim3(rows), dim3(NORM_NT), n2, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, row0, a4); break;
+            case 3: gm_norm2_kernel<3><<<dim3(rows), dim3(NORM_NT), n2, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, row0, a4); break;
+            case 4: gm_norm2_kernel<4><<<dim3(rows), dim3(NORM_NT), n2, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, row0, a4); break;
+            default: gm_norm_kernel<<<dim3(rows), dim3(NORM_NT), nlds, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, row0, a4);
         }
         return hipGetLastError();
     };
-    // the linears: in a batch step each row is its own sequence's decode row
-    auto mm = [&](const frq_w* w, const float* in, float* outp) -> int {
-        return batch ? gm_mm_rows(c, w, in, m, outp, g->xt) : gm_mm(c, w, in, m, outp);
+    // the linears: in a batch step each row is its own sequence's decode row;
+    // a4 set: the rows are already staged there (a4_for)
+    auto mm = [&](const frq_w* w, const float* in, float* outp, const float* a4) -> int {
+        if (!batch) return gm_mm(c, w, in, m, outp);
+        if (a4) {
+            GMCHK(launch_i4_rows_a4(*weight_of(w), m, a4, outp, s), "launch i4 rows");
+            return FRQ_OK;
+        }
+        return gm_mm_rows(c, w, in, m, outp, g->xt);
     };
     int64_t* tokp = g->tok + g->seq * g->cap_pos;  // this sequence's tokens (batch: sequence 0's)
     gm_embed_kernel<<<dim3((unsigned)m), dim3(GT), 0, s>>>(et.rowp, et.rpitch, et.dtype, et.scale, d, g->escale,
                                                            rel ? tokp : g->ids, rel, P, g->cur, g->x,
                                                            batch ? g->cap_pos : 0);
     GMCHK(hipGetLastError(), "launch embed");
-    GMCHK(norm(nullptr, nullptr, g->norm_of(0, 0), (int)m, 0), "launch norm");
+    GMCHK(norm(nullptr, nullptr, g->norm_of(0, 0), (int)m, 0, a4_for(g->qkv[0])), "launch norm");
     const size_t kvd = g->KV * g->hd;
     // the caches: [layer][sequence][position][kv width]; a batch step's row i
     // is sequence i (bst elements further per row)
     const size_t bst = g->cap_pos * kvd;
     for (size_t l = 0; l < g->L; ++l) {
-        if (int rc = mm(g->qkv[l], g->a, g->qkvb)) return rc;
+        if (int rc = mm(g->qkv[l], g->a, g->qkvb, a4_for(g->qkv[l]))) return rc;
         const size_t cb = (l * g->cap_b + g->seq) * g->cap_pos;  // this layer's (and sequence's) first position
         float* kc0 = g->kv8 ? nullptr : g->kc + cb * kvd;
         float* vc0 = g->kv8 ? nullptr : g->vc + cb * kvd;
@@ -2272,6 +2304,8 @@ int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_o
         const float* qn = g->qn_of(l);
         const float* kn = g->kn_of(l);
         const int div = g->arch == 1;
+        // the one-launch decode attention also stages o's rows
+        float* a4o = (m == 1 || batch) && g->cap_pos <= 512 ? a4_for(g->o[l]) : nullptr;
         if ((m == 1 || batch) && g->cap_pos > 512) {  // long caches: the three-launch decode attention
           for (size_t bi = 0; bi < m; ++bi) {  // (a batch: each sequence in turn, on its own cache)
             const int hd4 = (hd + 3) & ~3;
@@ -2322,11 +2356,11 @@ int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_o
             if (g->kv8)
                 gm_attn_kernel<true, true><<<ag, dim3(GT), lds, s>>>(g->qkvb, H, KV, hd, g->cur, g->cs, kc, vc, kq,
                                                                      vq, ks, vs, g->qscale, g->cap, sl, win, ps,
-                                                                     g->att, div, qb, qn, kn, g->eps, bs);
+                                                                     g->att, div, qb, qn, kn, g->eps, bs, a4o);
             else
                 gm_attn_kernel<false, true><<<ag, dim3(GT), lds, s>>>(g->qkvb, H, KV, hd, g->cur, g->cs, kc, vc, kq,
                                                                       vq, ks, vs, g->qscale, g->cap, sl, win, ps,
-                                                                      g->att, div, qb, qn, kn, g->eps, bs);
+                                                                      g->att, div, qb, qn, kn, g->eps, bs, a4o);
         } else {
             if (g->kv8)
                 gm_qkv_kernel<true><<<dim3((unsigned)m), dim3(GT), 0, s>>>(g->qkvb, H, KV, hd, g->cur, g->cs, kc, vc,
@@ -2384,9 +2418,9 @@ int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_o
                                                                        g->eps);
         }
         GMCHK(hipGetLastError(), "launch attention");
-        if (int rc = mm(g->o[l], g->att, g->ob)) return rc;
-        GMCHK(norm(g->ob, g->post_of(l, 1), g->norm_of(l, 2), (int)m, 0), "launch norm");
-        if (int rc = mm(g->gu[l], g->a, g->gub)) return rc;
+        if (int rc = mm(g->o[l], g->att, g->ob, a4o)) return rc;
+        GMCHK(norm(g->ob, g->post_of(l, 1), g->norm_of(l, 2), (int)m, 0, a4_for(g->gu[l])), "launch norm");
+        if (int rc = mm(g->gu[l], g->a, g->gub, a4_for(g->gu[l]))) return rc;
         const float gc = sqrtf(2.0f / 3.14159274101257324f);
         // rows the fused quant + GEMV covers take the elementwise act, then
         // that linear (an act inside it would be recomputed by every one of
@@ -2399,16 +2433,17 @@ int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_o
         } else {
             const size_t tot = m * g->ffn, items = g->arch == 1 && g->ffn % 4 == 0 && m >= 16 ? tot / 4 : tot;
             gm_geglu_kernel<<<dim3((unsigned)std::min<size_t>((items + GT - 1) / GT, 4096)), dim3(GT), 0, s>>>(
-                g->gub, ffn, tot, gc, g->hm, g->arch == 1 ? 1 : 0);
+                g->gub, ffn, tot, gc, g->hm, g->arch == 1 ? 1 : 0, a4_for(g->down[l]));
             GMCHK(hipGetLastError(), "launch geglu");
-            if (int rc = mm(g->down[l], g->hm, g->ob)) return rc;
+            if (int rc = mm(g->down[l], g->hm, g->ob, a4_for(g->down[l]))) return rc;
         }
         if (l + 1 < g->L)
-            GMCHK(norm(g->ob, g->post_of(l, 3), g->norm_of(l + 1, 0), (int)m, 0), "launch norm");
+            GMCHK(norm(g->ob, g->post_of(l, 3), g->norm_of(l + 1, 0), (int)m, 0, a4_for(g->qkv[l + 1])),
+                  "launch norm");
         else if (batch)  // every sequence's row feeds the head
-            GMCHK(norm(g->ob, g->post_of(l, 3), g->final_norm(), (int)m, 0), "launch norm");
+            GMCHK(norm(g->ob, g->post_of(l, 3), g->final_norm(), (int)m, 0, nullptr), "launch norm");
         else  // only the last row feeds the head
-            GMCHK(norm(g->ob, g->post_of(l, 3), g->final_norm(), 1, (int)m - 1), "launch norm");
+            GMCHK(norm(g->ob, g->post_of(l, 3), g->final_norm(), 1, (int)m - 1, nullptr), "launch norm");
     }
     float* lg = logits_out ? logits_out : g->logits;
     const Weight& ut = g->unembed ? *weight_of(g->unembed) : et;
