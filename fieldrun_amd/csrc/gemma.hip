@@ -158,11 +158,13 @@ __global__ __launch_bounds__(NORM_NT) void gm_norm_kernel(float* __restrict__ x,
 // gains) is issued up front, the squares go to LDS for the fold.  The
 // arithmetic is gm_norm_body's, operation for operation.  LDS: d floats and
 // the fold's scratch.
+// NT threads.
+template <int NT = NORM_NT>
 __host__ __device__ inline size_t gm_norm2_lds(int d) {
-    return ((size_t)((d + 3) & ~3) + seq_sum_spec_scratch(NORM_NT)) * sizeof(float);
+    return ((size_t)((d + 3) & ~3) + seq_sum_spec_scratch(NT)) * sizeof(float);
 }
-template <int NV>
-__global__ __launch_bounds__(NORM_NT) void gm_norm2_kernel(float* __restrict__ x, const float* __restrict__ y,
+template <int NV, int NT>
+__global__ __launch_bounds__(NT) void gm_norm2_kernel(float* __restrict__ x, const float* __restrict__ y,
                                                            const float* __restrict__ wpost,
                                                            const float* __restrict__ wnext, float* __restrict__ out,
                                                            int d, float eps, int row0, float* __restrict__ a4) {
@@ -179,13 +181,13 @@ __global__ __launch_bounds__(NORM_NT) void gm_norm2_kernel(float* __restrict__ x
     float4 xv[NV], yv[NV], wpv[NV], wnv[NV];
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-        const int q = min(tid + NORM_NT * i, d4 - 1);  // clamped: unconditional loads
+        const int q = min(tid + NT * i, d4 - 1);  // clamped: unconditional loads
         xv[i] = x4[q];
         wnv[i] = wn4[q];
         if (y) yv[i] = y4[q];
         if (y && wpost) wpv[i] = wp4[q];
     }
-    auto valid = [&](int i) { return tid + NORM_NT * i < d4; };
+    auto valid = [&](int i) { return tid + NT * i < d4; };
     auto mul = [](float4 a, float4 b) { return make_float4(a.x * b.x, a.y * b.y, a.z * b.z, a.w * b.w); };
     auto scl = [](float4 a, float s) { return make_float4(a.x * s, a.y * s, a.z * s, a.w * s); };
     auto add = [](float4 a, float4 b) { return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w); };
@@ -193,9 +195,9 @@ __global__ __launch_bounds__(NORM_NT) void gm_norm2_kernel(float* __restrict__ x
     auto inv_of = [&](const float4 (&v)[NV]) {
 #pragma unroll
         for (int i = 0; i < NV; ++i)
-            if (valid(i)) sq4[tid + NORM_NT * i] = mul(v[i], v[i]);
+            if (valid(i)) sq4[tid + NT * i] = mul(v[i], v[i]);
         __syncthreads();
-        const float ms = seq_sum_spec<NORM_NT>(sq, d, -0.0f, fsc) / (float)d;
+        const float ms = seq_sum_spec<NT>(sq, d, -0.0f, fsc) / (float)d;
         return 1.0f / sqrtf(ms + eps);
     };
     float4 nv[NV];
@@ -213,15 +215,15 @@ __global__ __launch_bounds__(NORM_NT) void gm_norm2_kernel(float* __restrict__ x
     if (y) {
 #pragma unroll
         for (int i = 0; i < NV; ++i)
-            if (valid(i)) reinterpret_cast<float4*>(x + r)[tid + NORM_NT * i] = nv[i];
+            if (valid(i)) reinterpret_cast<float4*>(x + r)[tid + NT * i] = nv[i];
     }
     const float inv = inv_of(nv);
 #pragma unroll
     for (int i = 0; i < NV; ++i)
         if (valid(i)) {
             const float4 o = mul(scl(nv[i], inv), wnv[i]);
-            reinterpret_cast<float4*>(out + r)[tid + NORM_NT * i] = o;
-            if (a4) reinterpret_cast<float4*>(a4)[(size_t)(tid + NORM_NT * i) * 16 + row0 + blockIdx.x] = o;
+            reinterpret_cast<float4*>(out + r)[tid + NT * i] = o;
+            if (a4) reinterpret_cast<float4*>(a4)[(size_t)(tid + NT * i) * 16 + row0 + blockIdx.x] = o;
         }
 }
 
@@ -1835,7 +1837,7 @@ struct frq_gemma {
     int64_t *tok = nullptr, *ids = nullptr;
     float *qr = nullptr, *sc = nullptr;  // long-cache decode attention: roped q, scores
     float* xt = nullptr;                 // batches: 16 staging rows (the head's input transposed,
-                                         // the int4 linears' a4 layout), 16 max(d, ffn, H hd)
+                                         // the int4 linears' a4 layout), 16 (max(d, ffn, H hd) + 4)
     float* pst = nullptr;                // prefill attention: scores / exps, [KV][block][kpad][64]
     float* pmx = nullptr;                // prefill attention: the pairs' maxima, [KV][block][64]
     // the quantised decode rows of the int8 linears (d- and ffn-wide: the
@@ -2175,7 +2177,7 @@ int gm_reserve(frq_ctx* c, frq_gemma* g, size_t npos, size_t rows, size_t nb = 1
                  o_lg = take(B * g->vocab * 4), o_cur = take(4), o_best = take(B * 8), o_tok = take(B * N * 8),
                  o_ids = take(R * 8),
                  o_qr = take(g->H * g->hd * 4), o_sc = take(g->H * gm_pstride_n(N) * 4),
-                 o_xt = take(B > 1 ? 16 * std::max({g->d, g->ffn, g->H * g->hd}) * 4 : 0),
+                 o_xt = take(B > 1 ? 16 * (std::max({g->d, g->ffn, g->H * g->hd}) + 4) * 4 : 0),
                  o_q8f = take(round_up(g->ffn, FRQ_KALIGN)), o_qsa = take(4), o_qoi = take(FRQ_T * 4),
                  o_qov = take(FRQ_T * 4);
     // the two-launch prefill attention's scores and tile maxima: only for
@@ -2258,10 +2260,10 @@ int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_o
     auto norm = [&](const float* y, const float* wpost, const float* wnext, int rows, int row0, float* a4) {
         const size_t n2 = gm_norm2_lds(d);
         switch ((d / 4 + NORM_NT - 1) / NORM_NT) {
-            case 1: gm_norm2_kernel<1><<<dim3(rows), dim3(NORM_NT), n2, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, row0, a4); break;
-            case 2: gm_norm2_kernel<2><<<dim3(rows), dim3(NORM_NT), n2, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, row0, a4); break;
-            case 3: gm_norm2_kernel<3><<<dim3(rows), dim3(NORM_NT), n2, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, row0, a4); break;
-            case 4: gm_norm2_kernel<4><<<dim3(rows), dim3(NORM_NT), n2, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, row0, a4); break;
+            case 1: gm_norm2_kernel<1, NORM_NT><<<dim3(rows), dim3(NORM_NT), n2, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, row0, a4); break;
+            case 2: gm_norm2_kernel<2, NORM_NT><<<dim3(rows), dim3(NORM_NT), n2, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, row0, a4); break;
+            case 3: gm_norm2_kernel<3, NORM_NT><<<dim3(rows), dim3(NORM_NT), n2, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, row0, a4); break;
+            case 4: gm_norm2_kernel<4, NORM_NT><<<dim3(rows), dim3(NORM_NT), n2, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, row0, a4); break;
             default: gm_norm_kernel<<<dim3(rows), dim3(NORM_NT), nlds, s>>>(g->x, y, wpost, wnext, g->a, d, g->eps, row0, a4);
         }
         return hipGetLastError();

@@ -255,6 +255,167 @@ hipError_t launch_dt(const Weight& w, const float* x, const int64_t* cand, size_
     return hipGetLastError();
 }
 
+// Products w * x[u] for vectors u = U, U + 1 of one element: x (a VGPR)
+// holds vector u's value in lane u of each 16-lane DPP row, and
+// v_mul_f32_dpp row_newbcast:u hands every lane that value times its own w.
+// NOP: the two wait states a DPP read needs after a VALU write of x (the
+// compiler does not see into the asm).
+#define FRQ_DPPM(dst, n) "v_mul_f32_dpp %" #dst ", %2, %3 row_newbcast:" #n " row_mask:0xf bank_mask:0xf\n\t"
+template <int U, bool NOP>
+__device__ __forceinline__ void dpp_mul2(float& p0, float& p1, float x, float w) {
+    static_assert(U >= 0 && U <= 14 && U % 2 == 0, "lane pair");
+#define FRQ_DPPM_CASE(u0, u1)                                                                        \
+    if constexpr (U == u0) {                                                                         \
+        if constexpr (NOP) asm("s_nop 1\n\t" FRQ_DPPM(0, u0) FRQ_DPPM(1, u1) : "=&v"(p0), "=&v"(p1) : "v"(x), "v"(w)); \
+        else asm(FRQ_DPPM(0, u0) FRQ_DPPM(1, u1) : "=&v"(p0), "=&v"(p1) : "v"(x), "v"(w));              \
+    }
+    FRQ_DPPM_CASE(0, 1) FRQ_DPPM_CASE(2, 3) FRQ_DPPM_CASE(4, 5) FRQ_DPPM_CASE(6, 7)
+    FRQ_DPPM_CASE(8, 9) FRQ_DPPM_CASE(10, 11) FRQ_DPPM_CASE(12, 13) FRQ_DPPM_CASE(14, 15)
+#undef FRQ_DPPM_CASE
+}
+#undef FRQ_DPPM
+
+// The f32 / f16 fold for 2 <= NX <= 16 vectors with the argmax (the
+// batched head): each output is rowdot_kernel's fold (acc = acc + w * x
+// from -0.0, k ascending).  A lane owns a row (read from the LDS tile 16
+// bytes at a time); an element's NX products come from dpp_mul2 (x
+// broadcast from a register, no scalar loads: their latency, not the
+// arithmetic, bounded the scalar-x form), then its NX adds.  x is in the
+// k-quad interleaved layout xq[64 (k / 4) + 4 v + k % 4] (16 vector slots,
+// k < d + 4; lane l loads the quad of vector l % 16), one quad ahead.  The
+// next chunk's row tile loads into the registers the current one was
+// staged from.
+template <int DT, int NX>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void rowdot_nx_kernel(const uint8_t* __restrict__ W, int rows, int d, size_t pitch,
+                                                        const float* __restrict__ xq, float* __restrict__ out,
+                                                        unsigned long long* __restrict__ best, int* __restrict__ err,
+                                                        size_t os, int nv) {
+    static_assert(DT == 0 || DT == 1, "the fold arms");
+    static_assert(NX >= 2 && NX <= 16 && NX % 2 == 0, "vector pairs");
+    constexpr int ES = DT == 0 ? 4 : 2;  // bytes per element
+    constexpr int EQ = 16 / ES;          // elements per 16-byte piece
+    __shared__ __attribute__((aligned(16))) uint8_t tile[4][64 * TP];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int o0 = ((int)blockIdx.x * 4 + wave) * 64;
+    if (o0 >= rows) return;  // wave-uniform; no block-wide barrier below
+    uint8_t* tw = tile[wave];
+    // load instruction i of a chunk: row o0 + 8 i + lane / 8 (the last row
+    // past the end), bytes 16 (lane % 8); 32-bit offsets from the wave's
+    // first row (64 rows of one table)
+    const uint8_t* wb = W + (size_t)o0 * pitch;
+    uint32_t lo[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        lo[i] = (uint32_t)min(8 * i + (lane >> 3), rows - 1 - o0) * (uint32_t)pitch + (lane & 7) * 16;
+    const int nch = (int)(pitch / 128);
+    const float* xl = xq + 4 * (lane & 15);
+    const int nq = (d + 3) / 4;  // quads of x
+    float acc[NX];
+#pragma unroll
+    for (int u = 0; u < NX; ++u) acc[u] = -0.0f;
+    // element e of piece q (a uint4 of the lane's row) as f32
+    auto elem = [&](const uint4& q, int e) __attribute__((always_inline)) -> float {
+        const uint32_t wd = e / (4 / ES) == 0 ? q.x : e / (4 / ES) == 1 ? q.y : e / (4 / ES) == 2 ? q.z : q.w;
+        if constexpr (DT == 0) return __builtin_bit_cast(float, wd);
+        else return h2f((uint16_t)(wd >> (16 * (e & 1))));
+    };
+    // one element: w times its x (component i of the quad xv); ADD: k < d
+    auto fold = [&](float w, const float4& xv, int i, bool add) __attribute__((always_inline)) {
+        const float xi = i == 0 ? xv.x : i == 1 ? xv.y : i == 2 ? xv.z : xv.w;
+        float pr[NX];
+        dpp_mul2<0, true>(pr[0], pr[1], xi, w);
+        if constexpr (NX > 2) dpp_mul2<2, false>(pr[2], pr[3], xi, w);
+        if constexpr (NX > 4) {
+            dpp_mul2<4, false>(pr[4], pr[5], xi, w);
+            dpp_mul2<6, false>(pr[6], pr[7], xi, w);
+        }
+        if constexpr (NX > 8) {
+            dpp_mul2<8, false>(pr[8], pr[9], xi, w);
+            dpp_mul2<10, false>(pr[10], pr[11], xi, w);
+            dpp_mul2<12, false>(pr[12], pr[13], xi, w);
+            dpp_mul2<14, false>(pr[14], pr[15], xi, w);
+        }
+        if (add) {
+#pragma unroll
+            for (int u = 0; u < NX; ++u) acc[u] = acc[u] + pr[u];
+        }
+    };
+    auto xload = [&](int kq) __attribute__((always_inline)) {
+        return *reinterpret_cast<const float4*>(xl + (size_t)min(kq, nq - 1) * 64);
+    };
+    // a chunk's elements k0 .. k0 + 128 / ES; CHECK: only k < d.  The quads
+    // alternate two register sets (an even count a chunk).
+    float4 xa = xload(0), xb;
+    auto run = [&](auto check, int k0) __attribute__((always_inline)) {
+        constexpr bool CHECK = decltype(check)::value;
+        const int kq0 = k0 / 4;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint4 q = *reinterpret_cast<const uint4*>(tw + lane * TP + 16 * j);
+#pragma unroll
+            for (int h = 0; h < EQ / 4; ++h) {
+                const int qi = j * (EQ / 4) + h;  // quad of the chunk
+                if (qi % 2 == 0) {
+                    xb = xload(kq0 + qi + 1);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) fold(elem(q, 4 * h + i), xa, i, !CHECK || k0 + 4 * qi + i < d);
+                } else {
+                    xa = xload(kq0 + qi + 1);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) fold(elem(q, 4 * h + i), xb, i, !CHECK || k0 + 4 * qi + i < d);
+                }
+            }
+        }
+    };
+    uint4 b[8];
+    auto load = [&](int c) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) b[i] = ntload16u(wb + (size_t)c * 128 + lo[i]);
+    };
+    if (nch > 0) {
+        load(0);
+        for (int c = 0; c < nch; ++c) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                *reinterpret_cast<uint4*>(tw + (8 * i + (lane >> 3)) * TP + (lane & 7) * 16) = b[i];
+            load(min(c + 1, nch - 1));  // the next chunk, under this one's arithmetic
+            wave_sync();
+            const int k0 = c * (128 / ES);
+            if (k0 + 128 / ES <= d) run(std::false_type{}, k0);  // wave-uniform
+            else run(std::true_type{}, k0);
+            wave_sync();  // the tile is read before the next chunk is written
+        }
+    }
+    const int o = o0 + lane;
+#pragma unroll
+    for (int u = 0; u < NX; ++u) {
+        if (u >= nv) break;  // the zero padding of the transposed x
+        const float a = acc[u];
+        if (o < rows) out[u * os + o] = a;
+        unsigned long long key = o < rows ? argmax_key(a, o) : 0ull;
+        const bool nan = o < rows && a != a;
+#pragma unroll
+        for (int sh = 32; sh > 0; sh >>= 1) {
+            const unsigned long long ok = __shfl_xor(key, sh);
+            key = ok > key ? ok : key;
+        }
+        if (__builtin_amdgcn_ballot_w64(nan) && lane == 0) atomicOr(err, 1);
+        if (lane == 0) atomicMax(best + u, key);
+    }
+}
+
+// xq[64 (k / 4) + 4 v + k % 4] = x[v xs + k] for v < nv and k < d, else 0,
+// over the (d + 3) / 4 quads (rowdot_nx_kernel's x layout)
+__global__ __launch_bounds__(256) void quad_x_kernel(const float* __restrict__ x, size_t xs, int nv, int d,
+                                                     float* __restrict__ xq) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t nq = ((size_t)d + 3) / 4;
+    if (i >= nq * 64) return;
+    const int kq = (int)(i / 64), v = (int)(i % 64) / 4, k = 4 * kq + (int)(i % 4);
+    xq[i] = v < nv && k < d ? x[(size_t)v * xs + k] : 0.0f;
+}
+
 // xt[k NX + v] = x[v xs + k] for v < nv, 0 for nv <= v < NX
 template <int NX>
 __global__ __launch_bounds__(256) void transpose_x_kernel(const float* __restrict__ x, size_t xs, int nv, int d,
@@ -269,15 +430,22 @@ template <int DT, int NX>
 hipError_t launch_argmax_nx(const Weight& w, size_t nv, const float* x, size_t xs, float* xt, float* out, size_t os,
                             unsigned long long* best, int* err, hipStream_t s) {
     const unsigned g4 = (unsigned)((w.n + 255) / 256);
-    const float* xv = x;
-    if constexpr (NX > 1) {
-        const size_t tot = w.k * NX;
-        transpose_x_kernel<NX><<<dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s>>>(x, xs, (int)nv, (int)w.k,
-                                                                                         xt);
-        xv = xt;
+    if constexpr (NX > 1 && DT != 2) {
+        const size_t nq = (w.k + 3) / 4;
+        quad_x_kernel<<<dim3((unsigned)((nq * 64 + 255) / 256)), dim3(256), 0, s>>>(x, xs, (int)nv, (int)w.k, xt);
+        rowdot_nx_kernel<DT, NX><<<dim3(g4), dim3(256), 0, s>>>(w.rowp, (int)w.n, (int)w.k, w.rpitch, xt, out, best,
+                                                                 err, os, (int)nv);
+    } else {
+        const float* xv = x;
+        if constexpr (NX > 1) {
+            const size_t tot = w.k * NX;
+            transpose_x_kernel<NX><<<dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s>>>(x, xs, (int)nv,
+                                                                                             (int)w.k, xt);
+            xv = xt;
+        }
+        rowdot_kernel<DT, false, 2, 4, true, NX><<<dim3(g4), dim3(256), 0, s>>>(
+            w.rowp, w.scale, (int)w.n, (int)w.k, w.rpitch, xv, nullptr, (int)w.n, out, best, err, os, (int)nv);
     }
-    rowdot_kernel<DT, false, 2, 4, true, NX><<<dim3(g4), dim3(256), 0, s>>>(
-        w.rowp, w.scale, (int)w.n, (int)w.k, w.rpitch, xv, nullptr, (int)w.n, out, best, err, os, (int)nv);
     return hipGetLastError();
 }
 
@@ -305,7 +473,7 @@ hipError_t launch_argmax_batch(const Weight& w, size_t nx, const float* x, size_
 
 // rowdot_f32 with the argmax fold for nx vectors x + v xs at once (outputs
 // out + v os, best[v]); each output's arithmetic is launch_rowdot_argmax's.
-// xt: device scratch of 16 w.k floats (the transposed vectors of a pass).
+// xt: device scratch of 16 (w.k + 4) floats (the vectors of a pass, transposed or in quads).
 hipError_t launch_rowdot_argmax_batch(const Weight& w, size_t nx, const float* x, size_t xs, float* xt, float* out,
                                       size_t os, unsigned long long* best, int* err, hipStream_t s) {
     if (!w.n || !nx) return hipSuccess;

@@ -218,13 +218,14 @@ def test_gemma_batch_long_cache_and_sixteen_rows(ctx, tmp_path):
     b.close()
 
 
-@pytest.mark.parametrize("embed", ["f32", "int8"])
-def test_gemma_batch_head_table_types(ctx, tmp_path, embed):
+@pytest.mark.parametrize("embed,d", [("f32", 132), ("int8", 132), ("f16", 132), ("f16", 196)])
+def test_gemma_batch_head_table_types(ctx, tmp_path, embed, d):
     """The batched head (the tied table's row dot and argmax for every
-    sequence in one pass, the vectors zero-padded to 4, 8 or 16) on f32 and
-    rowi8 tables: bit for bit the one-sequence head, and the oracle."""
+    sequence in one pass, the vectors zero-padded to 4, 8 or 16) on f32, f16
+    and rowi8 tables, rows ending inside a 128-byte chunk: bit for bit the
+    one-sequence head, and the oracle."""
     stem = str(tmp_path / "g")
-    synth.write_gemma2_bundle(stem, 29, n_layer=2, n_head=4, n_kv=2, hd=32, d=132, ffn=256, vocab=700, std=0.05,
+    synth.write_gemma2_bundle(stem, 29, n_layer=2, n_head=4, n_kv=2, hd=32, d=d, ffn=256, vocab=700, std=0.05,
                               norm_std=0.1, embed=embed)
     m, arrs = oracle.read_bundle(stem)
     ref = oracle.Gemma(m, arrs, nthreads=8)
