@@ -313,6 +313,151 @@ __device__ __forceinline__ void dpp_fma16(float (&l)[8], float w, const float (&
 #undef FRQ_DPP_C0
 #undef FRQ_DPPF
 
+// One k of R FMA chains: c[r] = fma(w_r(lane n), a, c[r]) for r < R, where
+// v_fmac_f32_dpp row_newbcast:n gives every token lane of a 16-lane DPP row
+// the weight held by lane n of that row (lane n: k0 + n).  The s_nop gives
+// the two wait states a DPP read needs after the VALU write of the weights.
+#define FRQ_CHF(acc, w, a, n) "v_fmac_f32_dpp %" #acc ", %" #w ", %" #a " row_newbcast:" #n " row_mask:0xf bank_mask:0xf\n\t"
+#define FRQ_CH8(n)                                                                                       \
+    FRQ_CHF(0, 8, 16, n) FRQ_CHF(1, 9, 16, n) FRQ_CHF(2, 10, 16, n) FRQ_CHF(3, 11, 16, n) FRQ_CHF(4, 12, 16, n) \
+    FRQ_CHF(5, 13, 16, n) FRQ_CHF(6, 14, 16, n) FRQ_CHF(7, 15, 16, n)
+#define FRQ_CH8_OPS                                                                                          \
+    : "+v"(c[0]), "+v"(c[1]), "+v"(c[2]), "+v"(c[3]), "+v"(c[4]), "+v"(c[5]), "+v"(c[6]), "+v"(c[7])         \
+    : "v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]), "v"(w[4]), "v"(w[5]), "v"(w[6]), "v"(w[7]), "v"(a)
+#define FRQ_CH8_CASE(n) \
+    if constexpr (N == n) asm("s_nop 1\n\t" FRQ_CH8(n) FRQ_CH8_OPS);
+template <int N>
+__device__ __forceinline__ void dpp_chain8(float (&c)[8], const float (&w)[8], float a) {
+    FRQ_CH8_CASE(0) FRQ_CH8_CASE(1) FRQ_CH8_CASE(2) FRQ_CH8_CASE(3) FRQ_CH8_CASE(4) FRQ_CH8_CASE(5)
+    FRQ_CH8_CASE(6) FRQ_CH8_CASE(7) FRQ_CH8_CASE(8) FRQ_CH8_CASE(9) FRQ_CH8_CASE(10) FRQ_CH8_CASE(11)
+    FRQ_CH8_CASE(12) FRQ_CH8_CASE(13) FRQ_CH8_CASE(14) FRQ_CH8_CASE(15)
+}
+#undef FRQ_CH8_CASE
+#undef FRQ_CH8_OPS
+#undef FRQ_CH8
+#undef FRQ_CHF
+
+// M > 1 rows in a.dot's order (each output: MM_KC-long k blocks, each an
+// FMA chain from +0 over k with w = s4 * scale, the blocks added in order)
+// with the weights broadcast across tokens: lane 16 d + t of a wave is
+// token t of the workgroup's 16-row tile (blockIdx.y) in DPP row d.  The
+// ND = 4 NW DPP rows D = BP rs + ph form ND / BP row sets of BP block
+// phases: row set rs owns the R weight rows r0 + R rs .. + R - 1, phase ph
+// takes blocks ph, ph + BP, ... .  For each 16-k chunk a lane dequantises
+// its rows' 16 weights into one register a row (lane n: k0 + n, exact
+// s4 * scale) and dpp_chain8 advances the R chains one k at a time; the
+// chunk's activations are the lane's own 16 (row-major), one chunk ahead.
+// A block's chain values go to LDS; after a slice of BP blocks, one barrier,
+// and the lane of each (row, token) adds them to its running sum in block
+// order (blocks past the end add +0, which a sum from +0 absorbs: no chain
+// from +0 ends at -0).  Needs K % 32 == 0, g % 16 == 0, M rows of K floats
+// 16-byte aligned.
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void i4_mm_dpp(const uint8_t* __restrict__ packed,
+                                                     const uint16_t* __restrict__ scale, int N, int K, int g,
+                                                     const float* __restrict__ a, int M, float* __restrict__ out,
+                                                     int BP) {
+    constexpr int R = 8, ND = 4 * NW;
+    constexpr int TB = ND * R * 16 * 2;  // term floats a buffer (RS R 16 pairs, BP + 1 apart)
+    __shared__ float tb[2][TB];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int t = lane & 15, D = 4 * wave + (lane >> 4);
+    const int RS = ND / BP, rs = D / BP, ph = D - rs * BP, TS = BP + 1;
+    const int nb = (K + MM_KC - 1) / MM_KC, nsl = (nb + BP - 1) / BP;
+    const int rows = RS * R, r0 = blockIdx.x * rows + rs * R, m0 = blockIdx.y * 16;
+    const int ng = (K + g - 1) / g;
+    const size_t pitch = (size_t)K / 2;
+    const uint8_t* wrow[R];
+    const uint16_t* srow[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const size_t row = (size_t)min(r0 + r, N - 1);  // clamped: loads stay unconditional
+        wrow[r] = packed + row * pitch + 4 * (t >> 3);
+        srow[r] = scale + row * ng;
+    }
+    const float* ar = a + (size_t)min(m0 + t, M - 1) * K;
+    const int sh = 4 * (t & 7);
+    // this lane's chunk sequence: slice s, chunk q of block s BP + ph
+    // (clamped to the last chunk of the row past the end: its values go
+    // unused)
+    const int nck = (K / 16);
+    auto chunk_k = [&](int s, int q) { return min((s * BP + ph) * MM_KC + 16 * q, 16 * (nck - 1)); };
+    struct Ld {
+        uint32_t w[R];
+        uint32_t sc[R];
+        float4 a[4];
+    };
+    auto load = [&](int k0, Ld& b) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) b.w[r] = *reinterpret_cast<const uint32_t*>(wrow[r] + (uint32_t)k0 / 2);
+        const uint32_t so = 2 * (uint32_t)(k0 / g);
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            b.sc[r] = *reinterpret_cast<const uint16_t*>(reinterpret_cast<const uint8_t*>(srow[r]) + so);
+        const float4* ap = reinterpret_cast<const float4*>(ar + k0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) b.a[i] = ap[i];
+    };
+    auto issued = [] {
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    float c[R];
+    auto chunk = [&](const Ld& b) {
+        float wv[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            wv[r] = (float)(int)__builtin_amdgcn_sbfe((int)b.w[r], sh, 4) * h2f((uint16_t)b.sc[r]);
+        const float av[16] = {b.a[0].x, b.a[0].y, b.a[0].z, b.a[0].w, b.a[1].x, b.a[1].y, b.a[1].z, b.a[1].w,
+                              b.a[2].x, b.a[2].y, b.a[2].z, b.a[2].w, b.a[3].x, b.a[3].y, b.a[3].z, b.a[3].w};
+        dpp_chain8<0>(c, wv, av[0]); dpp_chain8<1>(c, wv, av[1]); dpp_chain8<2>(c, wv, av[2]);
+        dpp_chain8<3>(c, wv, av[3]); dpp_chain8<4>(c, wv, av[4]); dpp_chain8<5>(c, wv, av[5]);
+        dpp_chain8<6>(c, wv, av[6]); dpp_chain8<7>(c, wv, av[7]); dpp_chain8<8>(c, wv, av[8]);
+        dpp_chain8<9>(c, wv, av[9]); dpp_chain8<10>(c, wv, av[10]); dpp_chain8<11>(c, wv, av[11]);
+        dpp_chain8<12>(c, wv, av[12]); dpp_chain8<13>(c, wv, av[13]); dpp_chain8<14>(c, wv, av[14]);
+        dpp_chain8<15>(c, wv, av[15]);
+    };
+    const int P = rows * 16;  // (row, token) pairs: pair p = (row p / 16, token p % 16)
+    float sum[(ND * R * 16 + 64 * NW - 1) / (64 * NW)];
+    constexpr int PPT = (ND * R * 16 + 64 * NW - 1) / (64 * NW);  // pairs a thread at most
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) sum[i] = 0.0f;
+    Ld b0, b1;
+    load(chunk_k(0, 0), b0);
+    for (int s = 0; s < nsl; ++s) {
+        const int blk = s * BP + ph;
+        const int nq = blk < nb ? min(16, (K - blk * MM_KC) / 16) : 16;  // past the end: any 16, unused
+#pragma unroll
+        for (int r = 0; r < R; ++r) c[r] = 0.0f;
+        // chunks in pairs (K % 32 == 0: every block has an even count); the
+        // last pair's second load is the next slice's first chunk
+        for (int q = 0; q < nq; q += 2) {
+            load(chunk_k(s, q + 1), b1);
+            issued();
+            chunk(b0);
+            load(q + 2 < nq ? chunk_k(s, q + 2) : chunk_k(s + 1, 0), b0);
+            issued();
+            chunk(b1);
+        }
+        float* tbs = tb[s & 1];
+#pragma unroll
+        for (int r = 0; r < R; ++r) tbs[((rs * R + r) * 16 + t) * TS + ph] = blk < nb ? c[r] : 0.0f;
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) {
+            const int p = tid + 64 * NW * i;
+            if (p < P)
+                for (int j = 0; j < BP; ++j) sum[i] = sum[i] + tbs[p * TS + j];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+        const int p = tid + 64 * NW * i;
+        const int row = blockIdx.x * rows + p / 16, tok = m0 + p % 16;
+        if (p < P && row < N && tok < M) out[(size_t)tok * N + row] = sum[i];
+    }
+}
+
 // The activation layout of i4_rows_dpp: the 16 token rows interleaved by
 // k-quads, a4[64 (k / 4) + 4 t + k % 4] = a[t][k] (rows t >= M zero), so
 // that the 16 token lanes of a DPP row read 256 contiguous bytes a load.
@@ -1267,6 +1412,34 @@ hipError_t launch_i4_exact(const Weight& w, size_t m, const float* a, float* out
         if (e != hipErrorNotSupported) return e;
         i4_gemv_generic<<<dim3((unsigned)((w.n + 255) / 256)), dim3(256), 0, s>>>(
             w.q4raw, w.s4raw, (int)w.n, (int)w.k, (int)w.g, a, out);
+        return hipGetLastError();
+    }
+    if (w.k % 32 == 0 && w.g % 16 == 0 && ((uintptr_t)a & 15) == 0 && (m + 15) / 16 <= 65535 &&
+        w.k <= (size_t)INT32_MAX && w.n <= (size_t)INT32_MAX && w.n * w.k / 2 < ((size_t)1 << 32)) {
+        // workgroups of NW waves (4 NW DPP rows) in BP block phases: the
+        // most blocks used of the slices run, then the longer slice (fewer
+        // rows a workgroup, fewer barriers), then four waves
+        const int nb = (int)((w.k + MM_KC - 1) / MM_KC);
+        int bnw = 4, bbp = 1;
+        double best = -1.0;
+        for (int nw : {4, 3})
+            for (int bp = 1; bp <= 4 * nw; ++bp) {
+                if ((4 * nw) % bp) continue;
+                const double eff = (double)nb / ((nb + bp - 1) / bp * bp);
+                if (eff > best + 1e-9 || (eff > best - 1e-9 && bp > bbp)) {
+                    best = eff;
+                    bnw = nw;
+                    bbp = bp;
+                }
+            }
+        const unsigned rows = (unsigned)(4 * bnw / bbp * 8);
+        const dim3 grid((unsigned)((w.n + rows - 1) / rows), (unsigned)((m + 15) / 16));
+        if (bnw == 3)
+            i4_mm_dpp<3><<<grid, dim3(192), 0, s>>>(w.q4raw, w.s4raw, (int)w.n, (int)w.k, (int)w.g, a, (int)m, out,
+                                                    bbp);
+        else
+            i4_mm_dpp<4><<<grid, dim3(256), 0, s>>>(w.q4raw, w.s4raw, (int)w.n, (int)w.k, (int)w.g, a, (int)m, out,
+                                                    bbp);
         return hipGetLastError();
     }
     if (w.k % 32 == 0 && w.g % 32 == 0 && ((uintptr_t)a & 15) == 0 && m <= 65535) {
