@@ -250,67 +250,120 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
 }
 
-// LDS floats of seq_sum_spec<NT>'s scratch (8-byte aligned).
-constexpr int seq_sum_spec_scratch(int nt) { return (nt / 64) * 128 + 2 * (nt / 64) + 4; }
+// LDS floats of seq_sum_spec<NT>'s scratch.
+constexpr int seq_sum_spec_scratch(int nt) { return 2 * ((nt / 64) * 128) + 6 * (nt / 64) + 4; }
 
 // init + p[0] + p[1] + ... + p[n-1], the sequential f32 fold in index order
 // (p in LDS, 16-byte aligned), bit-identical to lds_seq_sum, by all NT
-// threads of the workgroup (every thread calls it and gets the result) in
-// about 64/NT of its time.  Each of the NT/64 waves takes one contiguous
-// segment.  Segment 0 is folded from init.  Segment k > 0 is folded from 128
-// start values at once, two chains per lane: the f32 values within 64 steps
-// (one unit in the last place each) either side of f32(init + the exact
-// sum of the earlier segments, added in double).  The true start of segment
-// k is the fold's value at its first index, which differs from that
-// estimate only by the accumulated rounding, a few dozen units in the last
-// place on activation rows.  Then one thread chains the segments: when
-// segment k's true start (segment k-1's true end) is among its candidates,
-// bit for bit, that candidate's end is segment k's true end, by
-// determinism; otherwise (rows whose rounding drifts further, constant rows,
-// non-finite values) it folds segment k again from the true start.  The
-// result never depends on the estimates, only the time does.
+// threads of the workgroup (every thread calls it and gets the result).
+// The row is cut into S = 2 NT / 64 contiguous segments of a multiple of 32
+// elements, one a half-wave.  Segment 0 is folded from init.  Segment k > 0
+// is folded from 64 start values at once, two chains in each of the
+// half-wave's 32 lanes: the f32 values within 32 steps (one unit in the
+// last place each) either side of its estimate f32(init + the sum of the
+// earlier segments), each segment summed in f32 by its half-wave and the
+// sums added in double.  The true start of segment k is the fold's value at
+// its first index, which differs from the estimate only by the accumulated
+// rounding (a few dozen units in the last place at most on activation rows,
+// typically fewer).  Wave 0 then resolves the chain: lane j computes, for
+// every segment k, which candidate of segment k the end of segment k-1's
+// candidate j selects (its index, or none), so that following the true
+// candidates from segment 0 is one lane read a segment; where the true
+// start is not among the candidates (rows whose rounding drifts further,
+// constant rows, non-finite values) the remaining segments are folded again
+// from the true value.  The result never depends on the estimates, only the
+// time does.
 template <int NT>
 __device__ __forceinline__ float seq_sum_spec(const float* p, int n, float init, float* sc) {
-    constexpr int S = NT / 64, C = 128;
-    const int tid = threadIdx.x, lane = tid & 63, k = tid >> 6;
+    constexpr int S = 2 * (NT / 64), C = 64;
+    static_assert(S <= 64, "a lane of wave 0 a segment");
+    const int tid = threadIdx.x, lane = tid & 63, hl = lane & 31;
+    const int k = 2 * (tid >> 6) + (lane >> 5);  // this half-wave's segment
     float* ends = sc;                                      // [S][C] candidate ends
-    double* psum = reinterpret_cast<double*>(sc + S * C);  // [S] segment sums
-    float* res = sc + S * C + 2 * S;                       // [1] the result
-    if (n < 64 * S) {  // short: the plain chain
+    float* psum = sc + S * C;                              // [S] segment sums (estimates)
+    uint32_t* est = reinterpret_cast<uint32_t*>(psum + S);  // [S] start estimates (f32 bits)
+    float* res = psum + 2 * S;                             // [1] the result
+    if (n < 256) {  // short: the plain chain
         if (tid == 0) res[0] = lds_seq_sum(p, n, init);
         __syncthreads();
         const float r = res[0];
         __syncthreads();
         return r;
     }
-    const int L = ((n + S - 1) / S + 3) & ~3;  // segment length, a multiple of 4
-    const int lo = k * L, hi = min(n, lo + L);
-    double ps = 0.0;
-    for (int i = lo + lane; i < hi; i += 64) ps += (double)p[i];
+    const int L = ((n + S - 1) / S + 31) & ~31;  // segment length, whole 32-element batches
+    const int lo = min(n, k * L), hi = min(n, lo + L);
+    // the segment's sum by its half-wave (an estimate: any order will do)
+    float ps = 0.0f;
+    for (int i = lo + hl; i < hi; i += 32) ps += p[i];
+    ps += __builtin_bit_cast(float, xshfl<16>(__builtin_bit_cast(uint32_t, ps)));
+    ps += __builtin_bit_cast(float, xshfl<8>(__builtin_bit_cast(uint32_t, ps)));
+    ps += __builtin_bit_cast(float, xshfl<4>(__builtin_bit_cast(uint32_t, ps)));
+    ps += __builtin_bit_cast(float, xshfl<2>(__builtin_bit_cast(uint32_t, ps)));
+    ps += __builtin_bit_cast(float, xshfl<1>(__builtin_bit_cast(uint32_t, ps)));
+    if (hl == 0) psum[k] = ps;
+    __syncthreads();
+    float pv[S];  // every segment's sum, read at once
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) ps += __shfl_xor(ps, off, 64);
-    if (lane == 0) psum[k] = ps;
-    __syncthreads();
+    for (int kk = 0; kk < S; ++kk) pv[kk] = psum[kk];
     double pre = (double)init;
-    for (int kk = 0; kk < k; ++kk) pre += psum[kk];
+#pragma unroll
+    for (int kk = 0; kk < S; ++kk)
+        if (kk < k) pre += (double)pv[kk];
     const uint32_t eb = __float_as_uint((float)pre);
-    float c0 = k == 0 ? init : __uint_as_float(eb + (uint32_t)lane - (uint32_t)(C / 2));
-    float c1 = k == 0 ? init : __uint_as_float(eb + (uint32_t)lane + 64u - (uint32_t)(C / 2));
+    const uint32_t ebn = __float_as_uint((float)(pre + (double)pv[k < S - 1 ? k : 0]));  // segment k+1's
+    if (hl == 0) est[k] = eb;
+    float c0 = k == 0 ? init : __uint_as_float(eb + (uint32_t)hl - (uint32_t)(C / 2));
+    float c1 = k == 0 ? init : __uint_as_float(eb + (uint32_t)hl);
     if (lo < hi) lds_seq_sum2(p + lo, hi - lo, c0, c1);
-    ends[k * C + lane] = c0;
-    ends[k * C + lane + 64] = c1;
+    ends[k * C + hl] = c0;  // candidate start eb + hl - C/2
+    ends[k * C + hl + C / 2] = c1;
+    // the candidate of segment k+1 that each of these ends selects (or -1)
+    int* nxs = reinterpret_cast<int*>(ends + S * C) + 3 * S + 1;  // [S][C]
+    auto sel = [&](float e) {
+        const int64_t d = (int64_t)__float_as_uint(e) - (int64_t)ebn + C / 2;
+        return d >= 0 && d < C ? (int)d : -1;
+    };
+    if (k + 1 < S) {
+        nxs[(k + 1) * C + hl] = sel(c0);
+        nxs[(k + 1) * C + hl + C / 2] = sel(c1);
+    }
     __syncthreads();
-    if (tid == 0) {
-        float s = ends[0];
-        double pp = (double)init;
-        for (int kk = 1; kk < S; ++kk) {
-            pp += psum[kk - 1];
-            const int64_t d = (int64_t)__float_as_uint(s) - (int64_t)__float_as_uint((float)pp) + C / 2;
-            const int lo2 = kk * L, hi2 = min(n, lo2 + L);
-            if (d >= 0 && d < C) s = ends[kk * C + (int)d];
-            else if (lo2 < hi2) s = lds_seq_sum(p + lo2, hi2 - lo2, s);
+    if (tid < 64) {
+        // wave 0: lane j holds candidate j's end of every segment, and
+        // nx[kk] = the candidate of segment kk that candidate j of segment
+        // kk - 1 selects (or -1)
+        float e[S];
+        int nx[S];
+#pragma unroll
+        for (int kk = 0; kk < S; ++kk) e[kk] = ends[kk * C + lane];
+#pragma unroll
+        for (int kk = 1; kk < S; ++kk) nx[kk] = nxs[kk * C + lane];
+        // follow the true candidates: segment 0's is any (all start at init)
+        int d = 0, kk = 1;
+#pragma unroll
+        for (int j = 1; j < S; ++j) {
+            if (kk == j) {
+                const int dn = __builtin_amdgcn_readlane(nx[j], d);
+                if (dn >= 0) {
+                    d = dn;
+                    ++kk;
+                }
+            }
         }
-        res[0] = s;
+        float s = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e[kk - 1]), d));
+        // from the first segment whose start was missed: folded again, or
+        // its candidate where the refolded start is one
+        for (; kk < S; ++kk) {
+            const int64_t dd = (int64_t)__float_as_uint(s) - (int64_t)est[kk] + C / 2;
+            const int lo2 = min(n, kk * L), hi2 = min(n, lo2 + L);
+            if (dd >= 0 && dd < C) {
+                const float ek = ends[kk * C + (int)dd];
+                s = ek;
+            } else if (lo2 < hi2) {
+                s = lds_seq_sum(p + lo2, hi2 - lo2, s);
+            }
+        }
+        if (tid == 0) res[0] = s;
     }
     __syncthreads();
     const float r = res[0];
