@@ -133,6 +133,9 @@ def main():
                          "rocprofv3's kernel trace does not survive graph capture on this image)")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="only the counter-collection workload (run under rocprofv3 --pmc)")
+    ap.add_argument("--only-gemma2", action="store_true",
+                    help="only configs[2]'s Gemma-2 decode (batch 1 and batch 16) and print its detail entry "
+                         "(for profiling those runs; combine with --no-graphs under rocprofv3)")
     ap.add_argument("--pmc-what", default="layer", choices=["layer", "int4", "m128", "moe"],
                     help="counter workload: the configs[4] layer's four decode linears (default), the int4 "
                          "M=1 GEMV at the Gemma-2 shapes, the int8 linear at M=128, or configs[3]'s MoE "
@@ -253,6 +256,10 @@ def main():
     threads, visible = host_threads()
     detail = {}
     import config_fixtures as cfx
+
+    if args.only_gemma2:
+        print(json.dumps({"gemma2_decode": gemma2_detail(args, ctx, fa, cfx, log)}))
+        return
 
     # ======================= headline: configs[4] =======================
     with tempfile.TemporaryDirectory(dir=shm_dir()) as tmp:
@@ -612,8 +619,13 @@ def run_detail(args, ctx, fa, hip, synth, convert, time_loop, log, threads, cfx)
             g.free()
         b.close()
     log(f"gpt2 {detail['gpt2_decode']}")
-    # ---------------- Gemma-2-2b int4 greedy decode ----------------
-    detail["gemma2_decode"] = {}
+    detail["gemma2_decode"] = gemma2_detail(args, ctx, fa, cfx, log)
+    return detail
+
+
+def gemma2_detail(args, ctx, fa, cfx, log):
+    """Gemma-2-2b int4 greedy decode, batch 1 and batch 16."""
+    out = {}
     with tempfile.TemporaryDirectory(dir=shm_dir()) as tmp:
         stem = os.path.join(tmp, "gemma2")
         cfx.WORKLOADS["config2"]["write"](stem)
@@ -629,7 +641,7 @@ def run_detail(args, ctx, fa, hip, synth, convert, time_loop, log, threads, cfx)
             g.generate(prompt, n_new)
             runs[n_new] = time.perf_counter() - t0
         dec_ms = (runs[256] - runs[1]) / 255 * 1e3
-        detail["gemma2_decode"]["int4_kv_f32_batch1"] = {
+        out["int4_kv_f32_batch1"] = {
             "tok_s": round(256 / runs[256], 1), "decode_ms_per_token": round(dec_ms, 3),
             "decode_tok_s": round(1e3 / dec_ms, 1), "prefill_plus_first_ms": round(runs[1] * 1e3, 1),
             "tokens_identical_to_fixture": None if fx is None else cfx.compare(fx["sequences"][0], toks)[0]}
@@ -648,17 +660,22 @@ def run_detail(args, ctx, fa, hip, synth, convert, time_loop, log, threads, cfx)
         L_, d_, ffn_, V_ = 26, 2304, 9216, 256000
         lin = L_ * (d_ * (2048 + 1024 + 1024) + 2048 * d_ + d_ * 2 * ffn_ + ffn_ * d_)
         step_bytes = lin // 2 + 2 * (lin // 32) + V_ * d_ * 2
-        detail["gemma2_decode"]["int4_kv_f32_batch16"] = {
+        out["int4_kv_f32_batch16"] = {
             "decode_tok_s": round(16 / step_s, 1), "step_ms": round(step_s * 1e3, 3),
             "prefill_plus_first_ms": round(runs[1] * 1e3, 1),
             "weight_GBps": round(step_bytes / step_s / 1e9, 1),
             "weight_frac_hbm": round(step_bytes / step_s / 1e9 / HBM_PEAK_GBS, 3),
+            # the exact per-sequence orders make the batch step VALU-bound:
+            # one f32 FMA (linears) or mul + add (the f16 head) per weight
+            # element and sequence
+            "fma_per_step": 16 * (lin + V_ * d_),
+            "fma_T_per_s": round(16 * (lin + V_ * d_) / step_s / 1e12, 2),
             "tokens_identical_to_fixture": None if fxb is None else all(
                 cfx.compare(fxb["sequences"][i], tb[i])[0] for i in range(len(pb)))}
-        log(f"gemma2 {detail['gemma2_decode']}")
+        log(f"gemma2 {out}")
         g.free()
         b.close()
-    return detail
+    return out
 
 
 if __name__ == "__main__":

@@ -8,6 +8,14 @@
       the same per (kernel, workgroup count) from *_kernel_trace.csv, with
       register / LDS / scratch use.
 
+  python3 -m fieldrun_amd.rocprof_summary steps KERNEL_TRACE_CSV --marker SUBSTR
+          [--exclude SUBSTR ...] [--command CMD]
+      per-step time of each (kernel, workgroup count) over a run of decode
+      steps: the trace (in start order) is cut at each launch of the kernel
+      whose name contains the marker (one a step, e.g. the head), intervals
+      holding a kernel whose name contains an --exclude string (a prefill's)
+      are dropped, and each kernel's time is averaged over the kept steps.
+
   python3 -m fieldrun_amd.rocprof_summary pmc --fetch CSV --write CSV
           --kernel NAME --copy-bytes N --algo-bytes B [--command-fetch CMD]
           [--command-write CMD]
@@ -91,6 +99,38 @@ def trace(args) -> str:
         v = acc[k]
         out.append("| `%s` | %d | %d | %.2f | %.2f | %.2f | %s | %s | %s | %s | %s |" % (
             k[0], k[1], len(v), sum(v) / len(v), min(v), max(v), *meta[k]))
+    return "\n".join(out) + "\n"
+
+
+def steps(args) -> str:
+    """Per-step kernel times between consecutive marker launches."""
+    rows = sorted(_rows(args.csv), key=lambda r: int(r["Start_Timestamp"]))
+    marks = [i for i, r in enumerate(rows) if args.marker in r["Kernel_Name"]]
+    acc = defaultdict(float)
+    cnt = defaultdict(int)
+    kept, span = 0, 0.0
+    for a, b in zip(marks, marks[1:]):
+        seg = rows[a + 1:b + 1]  # a step ends with its head launch
+        if any(x in r["Kernel_Name"] for r in seg for x in args.exclude):
+            continue
+        kept += 1
+        span += (int(seg[-1]["End_Timestamp"]) - int(seg[0]["Start_Timestamp"])) / 1e3
+        for r in seg:
+            key = (short_name(r["Kernel_Name"]), int(r["Grid_Size_X"]) // max(1, int(r["Workgroup_Size_X"])))
+            acc[key] += (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+            cnt[key] += 1
+    out = []
+    if args.command:
+        out += ["Command:", "", "    " + args.command, ""]
+    if not kept:
+        return "\n".join(out + ["no complete step between markers"]) + "\n"
+    busy = sum(acc.values()) / kept
+    out += [f"{kept} steps: {busy:.1f} us of kernel time a step ({span / kept:.1f} us first start to last end)", "",
+            "| kernel | workgroups | launches a step | us a step | avg us | share |",
+            "|---|---:|---:|---:|---:|---:|"]
+    for k in sorted(acc, key=lambda k: -acc[k])[: args.top]:
+        out.append("| `%s` | %d | %.1f | %.1f | %.2f | %.1f%% |" % (
+            k[0], k[1], cnt[k] / kept, acc[k] / kept, acc[k] / cnt[k], 100 * acc[k] / kept / busy))
     return "\n".join(out) + "\n"
 
 
@@ -201,6 +241,12 @@ def main(argv=None):
     t.add_argument("csv")
     t.add_argument("--command", default="")
     t.add_argument("--top", type=int, default=40)
+    st = sub.add_parser("steps")
+    st.add_argument("csv")
+    st.add_argument("--marker", required=True)
+    st.add_argument("--exclude", action="append", default=[])
+    st.add_argument("--top", type=int, default=25)
+    st.add_argument("--command", default="")
     p = sub.add_parser("pmc")
     p.add_argument("--fetch", required=True)
     p.add_argument("--write", required=True)
@@ -222,7 +268,7 @@ def main(argv=None):
     pl.add_argument("--command-fetch", default="")
     pl.add_argument("--command-write", default="")
     a = ap.parse_args(argv)
-    sys.stdout.write({"stats": stats, "trace": trace, "pmc": pmc, "pmc-layer": pmc_layer}[a.mode](a))
+    sys.stdout.write({"stats": stats, "trace": trace, "steps": steps, "pmc": pmc, "pmc-layer": pmc_layer}[a.mode](a))
 
 
 if __name__ == "__main__":
