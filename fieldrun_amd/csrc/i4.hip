@@ -32,7 +32,9 @@
 // workgroups would need device-scope fences, which on this part write back
 // and invalidate the whole L2.
 // Other shapes run i4_gemv_generic (M == 1, bit-identical to i4_dot_avx2)
-// or, M > 1, i4_rows_chain (K and g multiples of 32) or i4_gemm_rows.
+// or, M > 1 in the exact order, i4_mm_dpp (K % 32 == 0, g % 16 == 0),
+// i4_rows_chain (K and g multiples of 32) or i4_gemm_rows.  Up to 16
+// independent M == 1 rows (a batched decode) run i4_rows_dpp.
 #include "frq_internal.h"
 
 namespace frq {
