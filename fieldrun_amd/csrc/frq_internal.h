@@ -454,6 +454,19 @@ bool linear_m1_ok(const Weight& w, const float* a);
 hipError_t launch_linear_m1(const Weight& w, const float* a, float* out, int32_t* acc,
                             int8_t* a8o, float* sao, uint32_t* oio, float* ovo, int* err,
                             hipStream_t s, int gmax = 0);
+// The fused linear of a gated pair with the activation in its epilogue:
+// w's rows interleaved in runs of hr (gated_rows: gate columns hr p ..
+// hr p + hr - 1, then the same up columns), hr = linear_m1_rpp(Kp, N) / 2;
+// out[c] = act(gate[c]) * up[c] for the N / 2 columns, act SiLU (silu) or
+// gelu_tanh with constant gc, the separate activation kernel's values bit
+// for bit.
+int linear_m1_rpp(size_t kp, size_t n);
+bool linear_m1_act_ok(const Weight& w, const float* a, int hr);
+hipError_t launch_linear_m1_act(const Weight& w, const float* a, float* out, int hr, int silu, float gc, int* err,
+                                hipStream_t s);
+// Position of gate column c (up: + hr) in a gated pair interleaved in runs
+// of hr (hr == 0: [gate | up], up at + half).
+__host__ __device__ inline size_t gated_col(size_t c, size_t hr) { return hr ? 2 * hr * (c / hr) + c % hr : c; }
 // int8 linear for 1 <= m <= 16 on row-major a8 (pitch kp) from the blocked
 // weight copy; outputs bit-exact to the reference's M > 1 order.
 hipError_t launch_skinny_i8(const Weight& w, size_t m, const int8_t* a8, const float* sa,

@@ -1751,21 +1751,38 @@ __global__ __launch_bounds__(VT) void gm_dec_value_blk_kernel(const float* __res
 // (gemma.rs:31-34) or, silu, x / (1 + exp(-x)) (rope.rs:39-41).
 // a4 (a batch's rows, <= 16, feeding an int4 linear): the rows also in the
 // k-quad interleaved layout of launch_i4_rows_a4.
+// hr > 0: the pair's columns interleaved in runs of hr (gated_col: gate
+// column col at gated_col(col, hr), up hr further), else [gate | up].
 __global__ __launch_bounds__(GT) void gm_geglu_kernel(const float* __restrict__ gu, int ffn, size_t total,
-                                                      float c, float* __restrict__ hm, int silu,
+                                                      float c, float* __restrict__ hm, int silu, int hr,
                                                       float* __restrict__ a4 = nullptr) {
     auto act = [&](float x) __attribute__((always_inline)) {
         return silu ? x / (1.0f + libm::frq_expf_sel(-x))
                     : 0.5f * x * (1.0f + libm::frq_tanhf(c * (x + 0.044715f * x * x * x)));
     };
-    if (silu && (ffn & 3) == 0 && total >= (size_t)16 * ffn) {
+    const size_t up = hr ? (size_t)hr : (size_t)ffn;  // up column's offset from its gate column
+    if (silu && (ffn & 3) == 0 && hr == 2 && total >= (size_t)16 * ffn) {
+        // prefill SiLU on pairs in runs of 2: columns 4 c4 .. 4 c4 + 3 are
+        // the gates and ups of two float4s, [g g u u][g g u u]
+        const size_t f4 = (size_t)ffn >> 2, t4 = total >> 2;
+        for (size_t i = (size_t)blockIdx.x * GT + threadIdx.x; i < t4; i += (size_t)gridDim.x * GT) {
+            const size_t r = i / f4, c4 = i - r * f4;
+            const float4 p = *reinterpret_cast<const float4*>(gu + r * 2 * ffn + 8 * c4);
+            const float4 q = *reinterpret_cast<const float4*>(gu + r * 2 * ffn + 8 * c4 + 4);
+            const float4 h = make_float4(act(p.x) * p.z, act(p.y) * p.w, act(q.x) * q.z, act(q.y) * q.w);
+            reinterpret_cast<float4*>(hm)[i] = h;
+            if (a4) reinterpret_cast<float4*>(a4)[c4 * 16 + r] = h;
+        }
+        return;
+    }
+    if (silu && (ffn & 3) == 0 && (hr & 3) == 0 && total >= (size_t)16 * ffn) {
         // prefill SiLU: four adjacent columns a thread, float4 loads, four
         // independent exps (decode rows keep a column a thread: more threads)
         const size_t f4 = (size_t)ffn >> 2, t4 = total >> 2;
         for (size_t i = (size_t)blockIdx.x * GT + threadIdx.x; i < t4; i += (size_t)gridDim.x * GT) {
-            const size_t r = i / f4, c4 = i - r * f4;
-            const float4 g = reinterpret_cast<const float4*>(gu + r * 2 * ffn)[c4];
-            const float4 u = reinterpret_cast<const float4*>(gu + r * 2 * ffn + ffn)[c4];
+            const size_t r = i / f4, c4 = i - r * f4, gcol = gated_col(4 * c4, (size_t)hr);  // 4 | hr
+            const float4 g = *reinterpret_cast<const float4*>(gu + r * 2 * ffn + gcol);
+            const float4 u = *reinterpret_cast<const float4*>(gu + r * 2 * ffn + gcol + up);
             const float4 h = make_float4(act(g.x) * u.x, act(g.y) * u.y, act(g.z) * u.z, act(g.w) * u.w);
             reinterpret_cast<float4*>(hm)[i] = h;
             if (a4) reinterpret_cast<float4*>(a4)[c4 * 16 + r] = h;
@@ -1773,8 +1790,8 @@ __global__ __launch_bounds__(GT) void gm_geglu_kernel(const float* __restrict__ 
         return;
     }
     for (size_t i = (size_t)blockIdx.x * GT + threadIdx.x; i < total; i += (size_t)gridDim.x * GT) {
-        const size_t r = i / ffn, col = i - r * ffn;
-        const float h = act(gu[r * 2 * ffn + col]) * gu[r * 2 * ffn + ffn + col];
+        const size_t r = i / ffn, col = i - r * ffn, gcol = gated_col(col, (size_t)hr);
+        const float h = act(gu[r * 2 * ffn + gcol]) * gu[r * 2 * ffn + gcol + up];
         hm[i] = h;
         if (a4) a4[(col >> 2) * 64 + 4 * r + (col & 3)] = h;
     }
@@ -1819,6 +1836,10 @@ struct frq_gemma {
     int arch = 0;                    // 0 gemma (gemma.rs), 1 the Llama / Qwen family (rope.rs)
     std::vector<float> inv;          // RoPE inverse frequencies
     std::vector<frq_w*> qkv, o, gu, down;
+    // per layer: the int8 gate|up pair's rows interleaved in runs of gu_hr
+    // (gated_col; the decode row's activation then runs in the fused
+    // linear's epilogue), or 0: [gate | up]
+    std::vector<int> gu_hr;
     frq_w* embed = nullptr;
     frq_w* unembed = nullptr;        // rope, untied: lm_head (else the embed table)
     float* norms = nullptr;          // 4 per layer + the final norm, f32 (d each)
@@ -1891,7 +1912,12 @@ struct GDev {
 // Two or three linears with the same input concatenated along the output:
 // the stored arrays' output rows (int4 / q4a: rows of the (out, in) store;
 // int8: columns of the (in, out) store) side by side, scales likewise.
-int concat_linear(frq_ctx* c, const frq_bundle* b, const std::vector<std::string>& names, size_t k, frq_w** out) {
+// hr > 0, int8, two linears of equal width divisible by hr (a gated pair):
+// their columns interleaved in runs of hr instead (gated_col), *hr_out = hr;
+// else *hr_out = 0.
+int concat_linear(frq_ctx* c, const frq_bundle* b, const std::vector<std::string>& names, size_t k, frq_w** out,
+                  size_t hr = 0, int* hr_out = nullptr) {
+    if (hr_out) *hr_out = 0;
     struct Arr {
         std::string dt;
         size_t shape[4], nd = 4, grp = 0, bytes = 0;
@@ -1921,13 +1947,33 @@ int concat_linear(frq_ctx* c, const frq_bundle* b, const std::vector<std::string
     if (dt == "i8") {
         std::vector<int8_t> cat(k * ntot);
         std::vector<uint16_t> sc(ntot);
-        size_t off = 0;
-        for (size_t i = 0; i < names.size(); ++i) {
-            const size_t n = w[i].shape[1];
-            const int8_t* src = static_cast<const int8_t*>(w[i].data);
-            for (size_t r = 0; r < k; ++r) std::memcpy(&cat[r * ntot + off], src + r * n, n);
-            std::memcpy(&sc[off], s[i].data, n * 2);
-            off += n;
+        const size_t h = w[0].shape[1];
+        if (hr && names.size() == 2 && w[1].shape[1] == h && h % hr == 0) {
+            // a gated pair in runs of hr: gate column c at gated_col(c, hr),
+            // up column c hr further
+            const int8_t* gs = static_cast<const int8_t*>(w[0].data);
+            const int8_t* us = static_cast<const int8_t*>(w[1].data);
+            const uint16_t* gsc = static_cast<const uint16_t*>(s[0].data);
+            const uint16_t* usc = static_cast<const uint16_t*>(s[1].data);
+            for (size_t p0 = 0; p0 < h; p0 += hr) {
+                const size_t dst = gated_col(p0, hr);
+                for (size_t r = 0; r < k; ++r) {
+                    std::memcpy(&cat[r * ntot + dst], gs + r * h + p0, hr);
+                    std::memcpy(&cat[r * ntot + dst + hr], us + r * h + p0, hr);
+                }
+                std::memcpy(&sc[dst], gsc + p0, hr * 2);
+                std::memcpy(&sc[dst + hr], usc + p0, hr * 2);
+            }
+            if (hr_out) *hr_out = (int)hr;
+        } else {
+            size_t off = 0;
+            for (size_t i = 0; i < names.size(); ++i) {
+                const size_t n = w[i].shape[1];
+                const int8_t* src = static_cast<const int8_t*>(w[i].data);
+                for (size_t r = 0; r < k; ++r) std::memcpy(&cat[r * ntot + off], src + r * n, n);
+                std::memcpy(&sc[off], s[i].data, n * 2);
+                off += n;
+            }
         }
         *out = frq_upload_i8_bundle(c, cat.data(), sc.data(), k, ntot);
     } else if (dt == "i4" || dt == "q4a") {
@@ -2422,21 +2468,32 @@ int gm_block(frq_ctx* c, frq_gemma* g, size_t m, int rel, int P, float* logits_o
         GMCHK(hipGetLastError(), "launch attention");
         if (int rc = mm(g->o[l], g->att, g->ob, a4o)) return rc;
         GMCHK(norm(g->ob, g->post_of(l, 1), g->norm_of(l, 2), (int)m, 0, a4_for(g->gu[l])), "launch norm");
-        if (int rc = mm(g->gu[l], g->a, g->gub, a4_for(g->gu[l]))) return rc;
         const float gc = sqrtf(2.0f / 3.14159274101257324f);
         // rows the fused quant + GEMV covers take the elementwise act, then
         // that linear (an act inside it would be recomputed by every one of
         // its workgroups); longer int8 rows the act + quant kernel, then the
         // GEMV on the quantised row
-        if (q8f && is_i8(g->down[l]) && !linear_m1_ok(*weight_of(g->down[l]), g->hm)) {
+        const bool down_q = q8f && is_i8(g->down[l]) && !linear_m1_ok(*weight_of(g->down[l]), g->hm);
+        // one decode row of an int8 gate|up pair otherwise: the activation in
+        // the fused linear's epilogue (no separate act launch)
+        const int hr = g->gu_hr[l];
+        const bool act_fused = m == 1 && !batch && !down_q && hr && linear_m1_act_ok(*weight_of(g->gu[l]), g->a, hr);
+        if (act_fused)
+            GMCHK(launch_linear_m1_act(*weight_of(g->gu[l]), g->a, g->hm, hr, g->arch == 1 ? 1 : 0, gc, err, s),
+                  "launch gate|up + act");
+        else if (int rc = mm(g->gu[l], g->a, g->gub, a4_for(g->gu[l])))
+            return rc;
+        if (down_q) {
             const Q8 q = gm_q8(g, 1, g->ffn);
             GMCHK(launch_act_quant(g, gc, q, err, s), "launch act + quant");
             if (int rc = frq_mm_i8_q_dev(c, g->down[l], q.a8, q.sa, q.oi, q.ov, 1, g->ob)) return rc;
         } else {
-            const size_t tot = m * g->ffn, items = g->arch == 1 && g->ffn % 4 == 0 && m >= 16 ? tot / 4 : tot;
-            gm_geglu_kernel<<<dim3((unsigned)std::min<size_t>((items + GT - 1) / GT, 4096)), dim3(GT), 0, s>>>(
-                g->gub, ffn, tot, gc, g->hm, g->arch == 1 ? 1 : 0, a4_for(g->down[l]));
-            GMCHK(hipGetLastError(), "launch geglu");
+            if (!act_fused) {
+                const size_t tot = m * g->ffn, items = g->arch == 1 && g->ffn % 4 == 0 && m >= 16 ? tot / 4 : tot;
+                gm_geglu_kernel<<<dim3((unsigned)std::min<size_t>((items + GT - 1) / GT, 4096)), dim3(GT), 0, s>>>(
+                    g->gub, ffn, tot, gc, g->hm, g->arch == 1 ? 1 : 0, hr, a4_for(g->down[l]));
+                GMCHK(hipGetLastError(), "launch geglu");
+            }
             if (int rc = mm(g->down[l], g->hm, g->ob, a4_for(g->down[l]))) return rc;
         }
         if (l + 1 < g->L)
@@ -2661,8 +2718,16 @@ static int decoder_load(frq_ctx* c, const frq_bundle* b, int kv_int8, int want_a
         g->qkv.push_back(w);
         if (int rc = one_linear(c, b, p + "self_attn.o_proj", qd, d, &w)) return rc;
         g->o.push_back(w);
-        if (int rc = concat_linear(c, b, {p + "mlp.gate_proj", p + "mlp.up_proj"}, d, &w)) return rc;
+        // the decode row of an int8 pair takes the fused linear with the
+        // activation in its epilogue where both linears fit the fused form
+        // (d and ffn multiples of 4 in (32, 20480]): rows in runs of its RPP / 2
+        const bool fuse = g->d % 4 == 0 && g->d > 32 && round_up(g->d, 128) <= 20480 && g->ffn % 4 == 0 &&
+                          g->ffn > 32 && round_up(g->ffn, 128) <= 20480;
+        const size_t hr = fuse ? (size_t)linear_m1_rpp(round_up(g->d, 128), 2 * g->ffn) / 2 : 0;
+        int ghr = 0;
+        if (int rc = concat_linear(c, b, {p + "mlp.gate_proj", p + "mlp.up_proj"}, d, &w, hr, &ghr)) return rc;
         g->gu.push_back(w);
+        g->gu_hr.push_back(ghr);
         if (int rc = one_linear(c, b, p + "mlp.down_proj", g->ffn, d, &w)) return rc;
         g->down.push_back(w);
     }

@@ -15,6 +15,8 @@
 // group's waves through LDS.  The activations (M x Kp bytes) sit in LDS and
 // each 16-byte activation chunk is reused for the R weight rows.
 #include "quant_core.h"
+// after the HIP runtime (quant_core.h): its memcpy is the device one
+#include "libm_f32.h"
 
 #include <algorithm>
 
@@ -296,19 +298,43 @@ __host__ __device__ inline size_t lm1_urow(size_t kp) {
     return kp > (size_t)qc::FCAP * 8 ? kp : (size_t)qc::FCAP * 8;
 }
 
-template <int L, int CPL, bool DB, int NV4, int NT>
+constexpr int LM1_ACT_IT = 16;  // groups a workgroup of the ACT form at most
+
+// ACT: the weight is a gated pair whose rows are interleaved in runs of
+// RPP/2 (gate columns RPP/2 g .., then the same up columns, in group g:
+// gated_rows), and the output is act(gate) * up (N / 2 values); each
+// group's row values stay in LDS and after the loop every thread takes some
+// (gate, up) pairs (in the loop the activation would delay every group
+// behind its barrier).  act: SiLU, x / (1 +
+// exp(-x)) (rope.rs:39-41), or, silu == 0, gelu_tanh with constant gc
+// (gemma.rs:31-34), the operations of the separate activation kernel.
+// (etab: expf's 32-entry table, a copy in LDS: a global table read in the
+// epilogue would stall every group behind its barrier)
+__device__ __forceinline__ float gated_act(float x, int silu, float gc, const uint64_t* etab) {
+    return silu ? x / (1.0f + libm::frq_expf_sel_t(-x, etab))
+                : 0.5f * x * (1.0f + libm::frq_tanhf(gc * (x + 0.044715f * x * x * x)));
+}
+
+template <int L, int CPL, bool DB, int NV4, int NT, bool ACT = false>
 __global__ __launch_bounds__(NT) void linear_m1_kernel(
     const int8_t* __restrict__ W, const int8_t* __restrict__ Wkn,
     const float* __restrict__ scale, int N, int Np, int Kp, int K,
     const float* __restrict__ A, float* __restrict__ out, int32_t* __restrict__ acc_dbg,
     int8_t* __restrict__ a8o, float* __restrict__ sao, uint32_t* __restrict__ oio,
-    float* __restrict__ ovo, int* __restrict__ err, int n_rg) {
-    constexpr int RPP = NT / L;
+    float* __restrict__ ovo, int* __restrict__ err, int n_rg, int silu = 1, float gc_act = 0.0f) {
+    constexpr int RPP = NT / L, HR = RPP / 2;
     constexpr int LW = L < 64 ? L : 64, WPR = L / LW;  // lanes per wave of a row, waves per row
     constexpr int NQW = FRQ_T * (RPP / 4);  // outlier words per group
     static_assert(NQW <= NT && RPP % 4 == 0, "one outlier word per thread");
     __shared__ qc::RowLdsT<NT> Q;
     __shared__ int accs[2][RPP * WPR];
+    // ACT: each visited group's RPP row values (and the group), for the
+    // activation after the loop (at most LM1_ACT_IT groups a workgroup)
+    __shared__ float actv[ACT ? LM1_ACT_IT * RPP : 1];
+    __shared__ int actg[ACT ? LM1_ACT_IT : 1];
+    __shared__ uint64_t etab[ACT ? 32 : 1];
+    if (ACT && threadIdx.x < 32) etab[threadIdx.x] = libm::kExp2Tab[threadIdx.x];
+    int it = 0;
     extern __shared__ __align__(16) unsigned char dyn[];
     const int nbw = Kp >> 5;  // Kp % 128 == 0
     uint32_t* bitmap = reinterpret_cast<uint32_t*>(dyn);
@@ -421,7 +447,19 @@ __global__ __launch_bounds__(NT) void linear_m1_kernel(
             scn = load_s(gn);
         }
         __syncthreads();
-        if (tid < RPP) {
+        if constexpr (ACT) {
+            if (tid < RPP) {  // the group's RPP row values, kept for after the loop
+                float corr = -0.0f;
+#pragma unroll
+                for (int qq = 0; qq < FRQ_T; ++qq) corr = corr + prod[buf][tid][qq];
+                int total = accs[buf][tid * WPR];
+#pragma unroll
+                for (int h = 1; h < WPR; ++h) total += accs[buf][tid * WPR + h];
+                actv[it * RPP + tid] = sc * (sam * (float)total + corr);
+                if (tid == 0) actg[it] = gc;
+            }
+            ++it;
+        } else if (tid < RPP) {
             const int j = gc * RPP + tid;
             if (j < N) {
                 float corr = -0.0f;
@@ -444,20 +482,76 @@ __global__ __launch_bounds__(NT) void linear_m1_kernel(
         gc = gn;
         rg = rgn;
     }
+    if constexpr (ACT) {  // out = act(gate) * up for every kept group, all threads at once
+        __syncthreads();
+        for (int x = tid; x < it * HR; x += NT) {
+            const int i = x / HR, r = x - i * HR;
+            out[HR * actg[i] + r] = gated_act(actv[i * RPP + r], silu, gc_act, etab) * actv[i * RPP + HR + r];
+        }
+    }
 }
 
-template <int L, int CPL, bool DB, int NV4, int NT = 256>
+template <int L, int CPL, bool DB, int NV4, int NT = 256, bool ACT = false>
 hipError_t launch_lm1(const Weight& w, const float* a, float* out, int32_t* acc, int8_t* a8o,
-                      float* sao, uint32_t* oio, float* ovo, int* err, int gmax, hipStream_t s) {
+                      float* sao, uint32_t* oio, float* ovo, int* err, int gmax, hipStream_t s, int silu = 1,
+                      float gc = 0.0f) {
     constexpr int RPP = NT / L;
     const int n_rg = (int)((w.n + RPP - 1) / RPP);  // rows < Np (RPP divides 256)
-    const int grid = n_rg < gmax ? n_rg : gmax;
+    int grid = n_rg < gmax ? n_rg : gmax;
+    if (ACT && (n_rg + grid - 1) / grid > LM1_ACT_IT) grid = (n_rg + LM1_ACT_IT - 1) / LM1_ACT_IT;
     const size_t prod = (size_t)2 * RPP * (FRQ_T + 1) * 4;
     const size_t lds = w.kp / 8 + (DB ? std::max(lm1_urow(w.kp), prod) : lm1_urow(w.kp) + prod);
-    linear_m1_kernel<L, CPL, DB, NV4, NT><<<dim3((unsigned)grid), dim3(NT), lds, s>>>(
+    linear_m1_kernel<L, CPL, DB, NV4, NT, ACT><<<dim3((unsigned)grid), dim3(NT), lds, s>>>(
         w.wt, w.wkn, w.scale, (int)w.n, (int)w.np, (int)w.kp, (int)w.k, a, out, acc, a8o, sao, oio,
-        ovo, err, n_rg);
+        ovo, err, n_rg, silu, gc);
     return hipGetLastError();
+}
+
+// The two launches lm1_dispatch makes: the plain fused linear and the one
+// with the gated activation in its epilogue.
+struct Lm1Call {
+    const Weight& w; const float* a; float* out; int32_t* acc; int8_t* a8o; float* sao; uint32_t* oio;
+    float* ovo; int* err; hipStream_t s;
+    template <int L, int CPL, bool DB, int NV4, int NT>
+    hipError_t operator()(int g) const {
+        return launch_lm1<L, CPL, DB, NV4, NT>(w, a, out, acc, a8o, sao, oio, ovo, err, g, s);
+    }
+};
+struct Lm1ActCall {
+    const Weight& w; const float* a; float* out; int silu; float gc; int* err; hipStream_t s;
+    template <int L, int CPL, bool DB, int NV4, int NT>
+    hipError_t operator()(int g) const {
+        return launch_lm1<L, CPL, DB, NV4, NT, true>(w, a, out, nullptr, nullptr, nullptr, nullptr, nullptr, err, g,
+                                                     s, silu, gc);
+    }
+};
+
+// The fused linear's configuration for a row of nch 16-byte chunks and N
+// outputs, as a call of f<L, CPL, DB, NV4, NT>(gmax default).
+template <typename F>
+hipError_t lm1_dispatch(const Weight& w, int g, F f) {
+    const size_t nch = w.kp / 16;
+    // grid caps: about the workgroups resident at once (256 CUs times the
+    // occupancy each variant's registers allow), measured best on MI355X
+    // short rows: 8 lanes a row (32-row groups) when N is large, 16 lanes
+    // (16-row groups: twice the groups, a shorter quant-bound tail) below
+    if (nch <= 64 && w.n >= 65536) return f.template operator()<8, 8, true, 1, 256>(g ? g : 768);
+    if (nch <= 64) return f.template operator()<16, 4, true, 1, 256>(g ? g : 768);
+    if (nch <= 128) return f.template operator()<64, 2, true, 2, 256>(g ? g : 1024);
+    if (nch <= 256) {
+        // about two 4-row groups a workgroup, both in flight during the
+        // quant (more workgroups each repeat the quant for less streaming)
+        const size_t n_rg = (w.n + 3) / 4;
+        const int gd = n_rg <= 1280 ? 512 : n_rg <= 2560 ? 768 : 1024;
+        return f.template operator()<64, 4, true, 4, 256>(g ? g : gd);
+    }
+    if (nch <= 512) return f.template operator()<64, 8, true, 8, 256>(g ? g : 512);
+    // long rows: 1024 threads (a quarter of the quant per thread), every
+    // workgroup's first group in flight during the quant
+    // (256 lanes, four waves, per row: 4 rows per group, at most 5 chunks a
+    // lane — 116 VGPRs; 128 lanes with 10 chunks spilled to scratch)
+    if (nch <= 1024) return f.template operator()<256, 4, false, 4, 1024>(g ? g : 256);
+    return f.template operator()<256, 5, false, 5, 1024>(g ? g : 256);
 }
 
 }  // namespace
@@ -480,30 +574,23 @@ hipError_t launch_linear_m1(const Weight& w, const float* a, float* out, int32_t
                             int8_t* a8o, float* sao, uint32_t* oio, float* ovo, int* err,
                             hipStream_t s, int gmax) {
     if (!linear_m1_ok(w, a)) return hipErrorInvalidValue;
-    const size_t nch = w.kp / 16;
-    // grid caps: about the workgroups resident at once (256 CUs times the
-    // occupancy each variant's registers allow), measured best on MI355X
-    const int g = gmax;
-    // short rows: 8 lanes a row (32-row groups) when N is large, 16 lanes
-    // (16-row groups: twice the groups, a shorter quant-bound tail) below
-    if (nch <= 64 && w.n >= 65536)
-        return launch_lm1<8, 8, true, 1>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 768, s);
-    if (nch <= 64) return launch_lm1<16, 4, true, 1>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 768, s);
-    if (nch <= 128) return launch_lm1<64, 2, true, 2>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 1024, s);
-    if (nch <= 256) {
-        // about two 4-row groups a workgroup, both in flight during the
-        // quant (more workgroups each repeat the quant for less streaming)
-        const size_t n_rg = (w.n + 3) / 4;
-        const int gd = n_rg <= 1280 ? 512 : n_rg <= 2560 ? 768 : 1024;
-        return launch_lm1<64, 4, true, 4>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : gd, s);
-    }
-    if (nch <= 512) return launch_lm1<64, 8, true, 8>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 512, s);
-    // long rows: 1024 threads (a quarter of the quant per thread), every
-    // workgroup's first group in flight during the quant
-    // (256 lanes, four waves, per row: 4 rows per group, at most 5 chunks a
-    // lane — 116 VGPRs; 128 lanes with 10 chunks spilled to scratch)
-    if (nch <= 1024) return launch_lm1<256, 4, false, 4, 1024>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 256, s);
-    return launch_lm1<256, 5, false, 5, 1024>(w, a, out, acc, a8o, sao, oio, ovo, err, g ? g : 256, s);
+    return lm1_dispatch(w, gmax, Lm1Call{w, a, out, acc, a8o, sao, oio, ovo, err, s});
+}
+
+int linear_m1_rpp(size_t kp, size_t n) {
+    const size_t nch = kp / 16;  // as lm1_dispatch: NT / L
+    return nch <= 64 ? (n >= 65536 ? 32 : 16) : 4;
+}
+
+bool linear_m1_act_ok(const Weight& w, const float* a, int hr) {
+    // whole groups of hr gate and hr up rows, hr the dispatch's RPP / 2
+    return linear_m1_ok(w, a) && hr > 0 && 2 * hr == linear_m1_rpp(w.kp, w.n) && w.n % (2 * (size_t)hr) == 0;
+}
+
+hipError_t launch_linear_m1_act(const Weight& w, const float* a, float* out, int hr, int silu, float gc, int* err,
+                                hipStream_t s) {
+    if (!linear_m1_act_ok(w, a, hr)) return hipErrorInvalidValue;
+    return lm1_dispatch(w, 0, Lm1ActCall{w, a, out, silu, gc, err, s});
 }
 
 }  // namespace frq
