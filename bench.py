@@ -21,9 +21,11 @@ gate|up 3584->37888, down 18944->3584): algorithmic bytes (N*K + 4N + 4K + 4N
 each) over the launches' summed average durations, HIP events on the
 library's stream, weights rotated over at least 4 sets of more than 640 MB
 in all for each shape (beyond the 256 MB MALL).
-`roofline_prefill`: the prefill's dominant kernel, the int8 MFMA GEMM at the
-gate|up shape (M=2048, K=3584, N=37888) on pre-quantised rows, 2*M*N*K ops
-over its average duration, against the dense int8 peak.
+`roofline_prefill`: the prefill's dominant kernel, the int8 MFMA GEMM the
+engine's prefill runs (its exact int32 sums), at the gate|up shape (M=2048,
+K=3584, N=37888) on pre-quantised rows, 2*M*N*K ops over its average
+duration, against the dense int8 peak; beside it the whole exact linear
+(quant + GEMM + exact epilogue) and the union-correction GEMM.
 `cpu_baseline`: the oracle's restatement of Rope::generate (the reference's
 scalar int8 path, the `_scalar_i8_bench` build, -O3 -march=x86-64) on the
 same bundle, decode tok/s over a bounded sample; `cpu_baseline_avx512` the
@@ -133,6 +135,9 @@ def main():
                          "rocprofv3's kernel trace does not survive graph capture on this image)")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="only the counter-collection workload (run under rocprofv3 --pmc)")
+    ap.add_argument("--vendor", action="store_true",
+                    help="also time hipBLASLt's int8 GEMM (torch._int_mm) at the prefill GEMM shapes, a speed "
+                         "reference for roofline_prefill (imports torch: not in the default run)")
     ap.add_argument("--only-gemma2", action="store_true",
                     help="only configs[2]'s Gemma-2 decode (batch 1 and batch 16) and print its detail entry "
                          "(for profiling those runs; combine with --no-graphs under rocprofv3)")
@@ -357,31 +362,55 @@ def main():
                 "bytes_per_layer": lay_bytes, "us_per_layer": round(lay_us, 2), "launches": lin}
     log(f"decode linears: {lin}")
 
-    # prefill GEMM roofline: M=2048 at the gate|up shape, pre-quantised rows
+    # prefill GEMM roofline: M=2048 at the gate|up shape, pre-quantised rows,
+    # the GEMM the engine's prefill runs (int32 sums for the exact epilogue)
     k, n, M = 3584, 2 * 18944, C4["prompt"]
-    wt, scale = synth.int8_weight(n, k, synth.seed(4, 9))
-    w = ctx.upload_i8(wt, scale)
-    del wt
+    nr = max(2, n_rot(n * k))  # weight sets rotated (each 136 MB)
+    ws_ = []
+    for r in range(nr):
+        wt, scale = synth.int8_weight(n, k, synth.seed(4, 9) + r)
+        ws_.append(ctx.upload_i8(wt, scale))
+        del wt
     a = synth.activations(M, k, synth.seed(4, 10))
     da, do = hip.DeviceArray.from_numpy(a), hip.DeviceArray((M, n), np.float32)
+    dacc = hip.DeviceArray((M, n), np.int32)
     kp = fa.quant_pitch(k)
     a8, sa = hip.DeviceArray((M, kp), np.int8), hip.DeviceArray((M,), np.float32)
     oi, ov = hip.DeviceArray((M, 32), np.uint32), hip.DeviceArray((M, 32), np.float32)
     ctx.quant_dev(da.ptr, M, k, a8.ptr, sa.ptr, oi.ptr, ov.ptr)
-    gus = float(np.median([time_loop(lambda i: w.mm_q_dev(a8.ptr, sa.ptr, oi.ptr, ov.ptr, M, do.ptr), 10,
-                                     warm=5 if r == 0 else 0) for r in range(3)])) * 1e3
-    fus = float(np.median([time_loop(lambda i: w.mm_dev(da.ptr, M, do.ptr), 10, warm=0) for _ in range(3)])) * 1e3
+    gus = float(np.median([time_loop(lambda i: ws_[i % nr].mm_acc_dev(a8.ptr, M, dacc.ptr), 2 * nr,
+                                     warm=2 if r == 0 else 0) for r in range(3)])) * 1e3
+    fus = float(np.median([time_loop(lambda i: ws_[i % nr].mm_exact_dev(da.ptr, M, do.ptr), 2 * nr, warm=1)
+                           for _ in range(3)])) * 1e3
+    uus = float(np.median([time_loop(lambda i: ws_[i % nr].mm_q_dev(a8.ptr, sa.ptr, oi.ptr, ov.ptr, M, do.ptr),
+                                     2 * nr, warm=1) for _ in range(3)])) * 1e3
     ops = 2.0 * M * n * k
     tops = ops / (gus * 1e-6) / 1e12
     roofline_prefill = {"bound": "mfma", "achieved": round(tops, 1), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
                         "frac": round(tops / INT8_PEAK_TOPS, 4), "traffic": None,
-                        "kernel": "gemm_i8_kernel (+ its correction pre-pass) on pre-quantised rows, "
-                                  f"M={M} K={k} N={n}",
-                        "us_per_launch": round(gus, 1), "full_linear_us": round(fus, 1),
-                        "full_linear_TOPS": round(ops / (fus * 1e-6) / 1e12, 1)}
-    w.free()
-    del a, da, do, a8, sa, oi, ov
+                        "kernel": "gemm_i8_kernel, the int32-sum MFMA GEMM the engine's prefill runs "
+                                  f"(frq_mm_i8_acc_dev: blockify + GEMM on pre-quantised rows), M={M} K={k} N={n}",
+                        "us_per_launch": round(gus, 1),
+                        "rotation": {"sets": nr, "bytes": nr * n * k},
+                        "exact_linear_us": round(fus, 1),
+                        "exact_linear_TOPS": round(ops / (fus * 1e-6) / 1e12, 1),
+                        "exact_linear_note": "frq_mm_exact_dev: quant, this GEMM, the exact sequential outlier "
+                                             "epilogue (the engine's prefill linear, bit-exact)",
+                        "union_gemm_us": round(uus, 1),
+                        "union_gemm_note": "frq_mm_i8_q_dev at M > 16: the GEMM with the outlier correction as "
+                                           "f16 hi/lo MFMAs (within 1e-6 of the exact sum)"}
+    for w in ws_:
+        w.free()
+    del a, da, do, dacc, a8, sa, oi, ov
     log(f"prefill GEMM: {roofline_prefill}")
+    if args.vendor:  # in a child process: torch's own HIP runtime does not start beside libfrq's
+        import subprocess
+        r = subprocess.run([sys.executable, os.path.abspath(__file__), "--vendor-child"], capture_output=True,
+                           text=True, timeout=600)
+        lines = [l for l in r.stdout.splitlines() if l.startswith("{")]
+        roofline_prefill["vendor"] = json.loads(lines[-1]) if r.returncode == 0 and lines else {
+            "error": (r.stderr or "")[-400:]}
+        log(f"vendor int8 GEMM: {roofline_prefill['vendor']}")
 
     if not args.no_detail:
         detail.update(run_detail(args, ctx, fa, hip, synth, convert, time_loop, log, threads, cfx))
@@ -409,6 +438,37 @@ def main():
         "detail": detail,
     }
     print(json.dumps(line))
+
+
+def vendor_int8_gemm(log=lambda *a: None):
+    """hipBLASLt's int8 GEMM through torch._int_mm (A (M,K) i8 row-major, B
+    (K,N) the transpose of an (N,K) row-major i8 weight, i32 out) at the
+    configs[4] prefill shapes, weights rotated over >= 4 sets: a speed
+    reference for the MFMA GEMM, not a parity path."""
+    import torch
+    res = {}
+    for (m, k, n) in [(2048, 3584, 37888), (2048, 3584, 4608), (2048, 18944, 3584), (2048, 4096, 14336)]:
+        a = torch.randint(-127, 128, (m, k), dtype=torch.int8, device="cuda:0")
+        nr = n_rot(n * k)
+        bs = [torch.randint(-127, 128, (n, k), dtype=torch.int8, device="cuda:0").t() for _ in range(nr)]
+        for i in range(3):
+            torch._int_mm(a, bs[i % nr])
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        it = 4 * nr
+        e0.record()
+        for i in range(it):
+            torch._int_mm(a, bs[i % nr])
+        e1.record()
+        e1.synchronize()
+        us = e0.elapsed_time(e1) / it * 1e3
+        tops = 2.0 * m * n * k / (us * 1e-6) / 1e12
+        res[f"M{m}_K{k}_N{n}"] = {"us": round(us, 1), "TOPS": round(tops, 1),
+                                  "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+        del a, bs
+        torch.cuda.empty_cache()
+    log(f"vendor int8 GEMM (torch._int_mm / hipBLASLt): {res}")
+    return {"library": "hipBLASLt via torch._int_mm", "shapes": res}
 
 
 def run_detail(args, ctx, fa, hip, synth, convert, time_loop, log, threads, cfx):
@@ -679,4 +739,7 @@ def gemma2_detail(args, ctx, fa, cfx, log):
 
 
 if __name__ == "__main__":
-    main()
+    if "--vendor-child" in sys.argv:
+        print(json.dumps(vendor_int8_gemm()))
+    else:
+        main()

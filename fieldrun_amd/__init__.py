@@ -63,6 +63,7 @@ SIGNATURES = {
     "frq_quant_pitch": (_S, [_S]),
     "frq_quant_i8_dev": (_I, [_P, _P, _S, _S, _P, _P, _P, _P]),
     "frq_mm_i8_q_dev": (_I, [_P, _P, _P, _P, _P, _P, _S, _P]),
+    "frq_mm_i8_acc_dev": (_I, [_P, _P, _P, _S, _P]),
     "frq_moe_upload_i8": (_P, [_P, _S, _S, _S, _I, _P, _P, _P, _P, _P, _P]),
     "frq_moe_upload": (_P, [_P, _I, _S, _S, _S, _I, _S, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "frq_moe_info": (_I, [_P, _P, _P, _P, _P, _P]),
@@ -386,6 +387,11 @@ class Weight:
     def mm_q_dev(self, a8_ptr: int, sa_ptr: int, oidx_ptr: int, oval_ptr: int, m: int, out_ptr: int):
         """int8 dot + epilogue on a batch quantised by Context.quant_dev."""
         _check(lib.frq_mm_i8_q_dev(self.ctx.h, self.h, a8_ptr, sa_ptr, oidx_ptr, oval_ptr, m, out_ptr))
+
+    def mm_acc_dev(self, a8_ptr: int, m: int, acc_ptr: int):
+        """int8: the i32 sums alone (the exact path's GEMM at m > 16) on a
+        batch quantised by Context.quant_dev."""
+        _check(lib.frq_mm_i8_acc_dev(self.ctx.h, self.h, a8_ptr, m, acc_ptr))
 
     def mm_debug(self, a: np.ndarray):
         """int8: (out, acc, a8, sa, oidx, oval) — the reference's locals."""

@@ -666,6 +666,50 @@ int frq_mm_i8_q_dev(frq_ctx* c, const frq_w* wh, const int8_t* d_a8, const float
     return FRQ_OK;
 }
 
+int frq_mm_i8_acc_dev(frq_ctx* c, const frq_w* wh, const int8_t* d_a8, size_t m, int32_t* d_acc) {
+    if (int rc = check_ctx(c)) return rc;
+    if (!wh) return fail(FRQ_ERR_ARG, "null weight");
+    const Weight& w = wh->w;
+    if (w.dtype != FRQ_DT_I8) return fail(FRQ_ERR_DTYPE, "frq_mm_i8_acc_dev: not an int8 weight");
+    if (w.device != c->device) return fail(FRQ_ERR_ARG, "weight lives on another device");
+    if (m == 0 || w.n == 0) return FRQ_OK;
+    if (!d_a8 || !d_acc) return fail(FRQ_ERR_ARG, "null pointer");
+    DeviceGuard g(c->device);
+    if (w.k == 0) {
+        HIPCHK(hipMemsetAsync(d_acc, 0, m * w.n * sizeof(int32_t), c->stream), "hipMemsetAsync");
+        return FRQ_OK;
+    }
+    // the dot kernels need the quant's outputs only for their epilogues:
+    // placeholders (sa = 1, no outliers) in the workspace, the sums to d_acc
+    const bool gemm = rows_exact_ok(wh, m);
+    const size_t mp = round_up(m, FRQ_MALIGN);
+    const size_t base = round_up(mp * w.kp, 256) + round_up(mp * sizeof(float), 256) +
+                        round_up(mp * FRQ_T * sizeof(uint32_t), 256) + round_up(mp * FRQ_T * sizeof(float), 256);
+    const size_t gwb = gemm ? gemm_ws_bytes(m, w.kp, w.np) : 0;
+    if (int rc = ws_reserve(c, base + gwb + round_up(m * w.n * sizeof(float), 256))) return rc;
+    Carve cv{(char*)c->ws};
+    int8_t* a8 = cv.take<int8_t>(mp * w.kp);
+    float* sa = cv.take<float>(mp);
+    uint32_t* oi = cv.take<uint32_t>(mp * FRQ_T);
+    float* ov = cv.take<float>(mp * FRQ_T);
+    void* gws = gemm ? cv.take<char>(gwb) : nullptr;
+    float* out = cv.take<float>(m * w.n);
+    HIPCHK(hipMemsetAsync(sa, 0, mp * sizeof(float), c->stream), "hipMemsetAsync");
+    HIPCHK(hipMemsetAsync(oi, 0, mp * FRQ_T * sizeof(uint32_t), c->stream), "hipMemsetAsync");
+    HIPCHK(hipMemsetAsync(ov, 0, mp * FRQ_T * sizeof(float), c->stream), "hipMemsetAsync");
+    if (gemm) {
+        HIPCHK(launch_blockify(d_a8, m, mp, w.kp, w.kp, a8, c->stream), "launch blockify");
+        HIPCHK(launch_gemm_i8(w, m, a8, sa, oi, ov, out, d_acc, gws, c->stream, true), "launch gemm_i8");
+    } else if (m == 1) {
+        HIPCHK(launch_gemv_i8(w, m, d_a8, sa, oi, ov, out, d_acc, c->stream), "launch gemv_i8");
+    } else if (m <= 16) {
+        HIPCHK(launch_skinny_i8(w, m, d_a8, sa, oi, ov, out, d_acc, c->stream), "launch skinny_i8");
+    } else {
+        return fail(FRQ_ERR_ARG, "frq_mm_i8_acc_dev: shape not supported (K beyond 20480 at M > 16)");
+    }
+    return FRQ_OK;
+}
+
 static int mm_host(frq_ctx* c, const frq_w* wh, const float* a, size_t m, float* out,
                    int32_t* acc, int8_t* a8h, float* sah, uint32_t* oih, float* ovh) {
     if (int rc = check_ctx(c)) return rc;

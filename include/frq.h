@@ -184,6 +184,13 @@ int frq_quant_i8_dev(frq_ctx* ctx, const float* d_a, size_t m, size_t k,
 int frq_mm_i8_q_dev(frq_ctx* ctx, const frq_w* w, const int8_t* d_a8,
                     const float* d_sa, const uint32_t* d_oidx,
                     const float* d_oval, size_t m, float* d_out);
+/* The dot alone on such a quantised batch: acc (M,N) i32 = i8dot(a8[i],
+ * wt[j]) for every row and column (src/bundle.rs:710 / 745, the exact sums
+ * the epilogue scales), on device pointers.  M > 16 runs the MFMA GEMM whose
+ * int32 sums frq_mm_exact_dev's epilogue takes (the engines' prefill GEMM);
+ * M <= 16 the skinny / GEMV dot. */
+int frq_mm_i8_acc_dev(frq_ctx* ctx, const frq_w* w, const int8_t* d_a8, size_t m,
+                      int32_t* d_acc);
 
 /* ---- the unembed: Bundle::rowdot_f32 (src/bundle.rs:958-987) -----------
  * out[r] = dot(W[r], x) for every row of a frq_upload_rows table (out has

@@ -274,6 +274,31 @@ def test_i8_device_entry_points_match_host(ctx, m, k, n):
     assert np.array_equal(out.numpy().view(np.uint32), out_h.view(np.uint32))
 
 
+@pytest.mark.parametrize("m,k,n", [(1, 896, 4864), (4, 4864, 896), (16, 300, 257), (17, 896, 4864),
+                                   (128, 3584, 640), (300, 5000, 257), (2048, 3584, 512), (40, 20480, 64)])
+def test_i8_acc_dev_matches_oracle(ctx, m, k, n):
+    """frq_mm_i8_acc_dev on frq_quant_i8_dev's rows: the i32 sums of every
+    (row, column) bit for bit against the oracle's i8dot (the GEMV, skinny
+    and MFMA GEMM dots; the GEMM is the exact path's, whose sums
+    frq_mm_exact_dev's epilogue scales)."""
+    import fieldrun_amd as fa
+    from fieldrun_amd import hip
+    a, wt, scale = case(m, k, n, 700 + m + k + n)
+    w = ctx.upload_i8(wt, scale)
+    kp = fa.quant_pitch(k)
+    da = hip.DeviceArray.from_numpy(a)
+    a8 = hip.DeviceArray((m, kp), np.int8)
+    sa = hip.DeviceArray((m,), np.float32)
+    oi = hip.DeviceArray((m, 32), np.uint32)
+    ov = hip.DeviceArray((m, 32), np.float32)
+    acc = hip.DeviceArray((m, n), np.int32)
+    ctx.quant_dev(da.ptr, m, k, a8.ptr, sa.ptr, oi.ptr, ov.ptr)
+    w.mm_acc_dev(a8.ptr, m, acc.ptr)
+    ctx.sync()
+    _, racc = oracle.mm_i8(a, wt, scale, with_acc=True)
+    assert np.array_equal(acc.numpy(), racc)
+
+
 def same_or_both_nan(x, y):
     x, y = np.asarray(x, np.float32), np.asarray(y, np.float32)
     nx, ny = np.isnan(x), np.isnan(y)
