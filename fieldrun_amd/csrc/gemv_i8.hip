@@ -315,7 +315,7 @@ __device__ __forceinline__ float gated_act(float x, int silu, float gc, const ui
                 : 0.5f * x * (1.0f + libm::frq_tanhf(gc * (x + 0.044715f * x * x * x)));
 }
 
-template <int L, int CPL, bool DB, int NV4, int NT, bool ACT = false>
+template <int L, int CPL, bool DB, int NV4, int NT, bool ACT = false, bool PB = false>
 __global__ __launch_bounds__(NT) void linear_m1_kernel(
     const int8_t* __restrict__ W, const int8_t* __restrict__ Wkn,
     const float* __restrict__ scale, int N, int Np, int Kp, int K,
@@ -345,7 +345,7 @@ __global__ __launch_bounds__(NT) void linear_m1_kernel(
     const int nch = Kp >> 4, K4 = K >> 2;
     const int G = (int)gridDim.x;
     int rg = blockIdx.x;
-    int4 w[CPL], wn[DB ? CPL : 1];
+    int4 w[CPL], wn[(DB || PB) ? CPL : 1];
     // chunks past the row are clamped, not skipped (no branches between the
     // loads); the activation chunk they meet is zero
     auto load_w = [&](int g, int4* dst) {
@@ -410,8 +410,11 @@ __global__ __launch_bounds__(NT) void linear_m1_kernel(
     int gc = xcd_group<RPP>(rg, n_rg);  // rg < n_rg: the grid is at most n_rg
     uint32_t ow = load_o(gc), own = 0;
     float sc = load_s(gc), scn = 0.0f;
-    if (DB && rg + G < n_rg) {
+    if ((DB || PB) && rg + G < n_rg) {
         const int g1 = xcd_group<RPP>(rg + G, n_rg);
+        // PB: the second group goes out once the selection has freed its
+        // registers (both groups in flight through the stream)
+        if (PB) load_w(g1, wn);
         own = load_o(g1);
         scn = load_s(g1);
     }
@@ -420,7 +423,7 @@ __global__ __launch_bounds__(NT) void linear_m1_kernel(
     while (rg < n_rg) {
         const int rgn = rg + G;
         const int gn = rgn < n_rg ? xcd_group<RPP>(rgn, n_rg) : 0;
-        if (DB && !first && rgn < n_rg) {
+        if ((DB || PB) && !first && rgn < n_rg) {
             load_w(gn, wn);
             own = load_o(gn);
             scn = load_s(gn);
@@ -434,7 +437,7 @@ __global__ __launch_bounds__(NT) void linear_m1_kernel(
         }
         // single-buffered: the next group's weights go out as soon as the dot
         // has consumed these, overlapping the reduction and the epilogue
-        if (!DB && rgn < n_rg) load_w(gn, w);
+        if (!DB && !PB && rgn < n_rg) load_w(gn, w);
 #pragma unroll
         for (int off = LW / 2; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
         if (sub % LW == 0) accs[buf][rloc * WPR + sub / LW] = acc;
@@ -442,7 +445,7 @@ __global__ __launch_bounds__(NT) void linear_m1_kernel(
 #pragma unroll
             for (int b = 0; b < 4; ++b) prod[buf][4 * r4 + b][q] = ovq * (float)(int8_t)(ow >> (8 * b));
         }
-        if (!DB && rgn < n_rg) {
+        if (!DB && !PB && rgn < n_rg) {
             own = load_o(gn);
             scn = load_s(gn);
         }
@@ -473,7 +476,7 @@ __global__ __launch_bounds__(NT) void linear_m1_kernel(
             }
         }
         buf ^= 1;
-        if (DB) {
+        if (DB || PB) {
 #pragma unroll
             for (int i = 0; i < CPL; ++i) w[i] = wn[i];
         }
@@ -491,7 +494,7 @@ __global__ __launch_bounds__(NT) void linear_m1_kernel(
     }
 }
 
-template <int L, int CPL, bool DB, int NV4, int NT = 256, bool ACT = false>
+template <int L, int CPL, bool DB, int NV4, int NT = 256, bool ACT = false, bool PB = false>
 hipError_t launch_lm1(const Weight& w, const float* a, float* out, int32_t* acc, int8_t* a8o,
                       float* sao, uint32_t* oio, float* ovo, int* err, int gmax, hipStream_t s, int silu = 1,
                       float gc = 0.0f) {
@@ -501,7 +504,7 @@ hipError_t launch_lm1(const Weight& w, const float* a, float* out, int32_t* acc,
     if (ACT && (n_rg + grid - 1) / grid > LM1_ACT_IT) grid = (n_rg + LM1_ACT_IT - 1) / LM1_ACT_IT;
     const size_t prod = (size_t)2 * RPP * (FRQ_T + 1) * 4;
     const size_t lds = w.kp / 8 + (DB ? std::max(lm1_urow(w.kp), prod) : lm1_urow(w.kp) + prod);
-    linear_m1_kernel<L, CPL, DB, NV4, NT, ACT><<<dim3((unsigned)grid), dim3(NT), lds, s>>>(
+    linear_m1_kernel<L, CPL, DB, NV4, NT, ACT, PB><<<dim3((unsigned)grid), dim3(NT), lds, s>>>(
         w.wt, w.wkn, w.scale, (int)w.n, (int)w.np, (int)w.kp, (int)w.k, a, out, acc, a8o, sao, oio,
         ovo, err, n_rg, silu, gc);
     return hipGetLastError();
@@ -514,15 +517,15 @@ struct Lm1Call {
     float* ovo; int* err; hipStream_t s;
     template <int L, int CPL, bool DB, int NV4, int NT>
     hipError_t operator()(int g) const {
-        return launch_lm1<L, CPL, DB, NV4, NT>(w, a, out, acc, a8o, sao, oio, ovo, err, g, s);
+        return launch_lm1<L, CPL, DB, NV4, NT, false, !DB>(w, a, out, acc, a8o, sao, oio, ovo, err, g, s);
     }
 };
 struct Lm1ActCall {
     const Weight& w; const float* a; float* out; int silu; float gc; int* err; hipStream_t s;
     template <int L, int CPL, bool DB, int NV4, int NT>
     hipError_t operator()(int g) const {
-        return launch_lm1<L, CPL, DB, NV4, NT, true>(w, a, out, nullptr, nullptr, nullptr, nullptr, nullptr, err, g,
-                                                     s, silu, gc);
+        return launch_lm1<L, CPL, DB, NV4, NT, true, !DB>(w, a, out, nullptr, nullptr, nullptr, nullptr, nullptr, err,
+                                                          g, s, silu, gc);
     }
 };
 
