@@ -541,18 +541,18 @@ hipError_t lm1_dispatch(const Weight& w, int g, F f) {
     if (nch <= 64 && w.n >= 65536) return f.template operator()<8, 8, true, 1, 256>(g ? g : 768);
     if (nch <= 64) return f.template operator()<16, 4, true, 1, 256>(g ? g : 768);
     if (nch <= 128) return f.template operator()<64, 2, true, 2, 256>(g ? g : 1024);
-    if (nch <= 256) {
-        // about two 4-row groups a workgroup, both in flight during the
-        // quant (more workgroups each repeat the quant for less streaming)
-        const size_t n_rg = (w.n + 3) / 4;
-        const int gd = n_rg <= 1280 ? 512 : n_rg <= 2560 ? 768 : 1024;
-        return f.template operator()<64, 4, true, 4, 256>(g ? g : gd);
-    }
+    // rows of 2049..4096 bytes: one 512-thread workgroup a CU (8-row groups,
+    // two in flight during the quant; the quant once a CU, half the
+    // elements a thread), two a CU for long outputs (N >= 16384: gate|up);
+    // measured against two / four 256-thread workgroups a CU: o 9.64 ->
+    // 8.3 us, q|k|v 9.78 -> 9.56, gate|up 27.3 -> 26.0 (configs[4] shapes)
+    if (nch <= 256) return f.template operator()<64, 4, true, 2, 512>(g ? g : (w.n >= 16384 ? 512 : 256));
     if (nch <= 512) return f.template operator()<64, 8, true, 8, 256>(g ? g : 512);
     // long rows: 1024 threads (a quarter of the quant per thread), every
     // workgroup's first group in flight during the quant
     // (256 lanes, four waves, per row: 4 rows per group, at most 5 chunks a
-    // lane — 116 VGPRs; 128 lanes with 10 chunks spilled to scratch)
+    // lane — 110 VGPRs with the second buffer issued after the quant; 128
+    // lanes with 10 chunks spilled to scratch)
     if (nch <= 1024) return f.template operator()<256, 4, false, 4, 1024>(g ? g : 256);
     return f.template operator()<256, 5, false, 5, 1024>(g ? g : 256);
 }
@@ -582,7 +582,7 @@ hipError_t launch_linear_m1(const Weight& w, const float* a, float* out, int32_t
 
 int linear_m1_rpp(size_t kp, size_t n) {
     const size_t nch = kp / 16;  // as lm1_dispatch: NT / L
-    return nch <= 64 ? (n >= 65536 ? 32 : 16) : 4;
+    return nch <= 64 ? (n >= 65536 ? 32 : 16) : nch <= 128 ? 4 : nch <= 256 ? 8 : 4;
 }
 
 bool linear_m1_act_ok(const Weight& w, const float* a, int hr) {

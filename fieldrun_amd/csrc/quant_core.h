@@ -13,13 +13,14 @@
 // in ascending channel order.
 //
 // The routines here cover rows with K % 4 == 0 and 32 < K <= 4 NT NV4 for a
-// workgroup of NT = 256 or 1024 threads, the row held as
+// workgroup of NT = 256, 512 or 1024 threads, the row held as
 // v[i] = a[4 (tid + NT i) ..] (float4, entries past K ignored):
 //   row_select:   1. each thread's max |a|;
 //                 2. tau: with 4 waves the 33rd largest thread max (every
 //                    wave sorts its 64 maxima with a bitonic network on DPP /
 //                    permlane lane exchanges, and every wave merges the four
-//                    lists keeping the top 64); with 16 waves the 33rd
+//                    lists keeping the top 64; 8 waves: the eight lists
+//                    merged pairwise the same way); with 16 waves the 33rd
 //                    largest of the waves' top-3 lane maxima.  At least t+1
 //                    elements are >= tau, so bulk_max >= tau;
 //                 3. the elements >= tau (a few dozen on real rows) are
@@ -244,7 +245,8 @@ template <int NV4, int NT = BLOCK>
 __device__ RowSel row_select(const float* __restrict__ a, int K, const float4 (&v)[NV4], RowLdsT<NT>& L,
                              unsigned long long* cand, uint32_t* bitmap, int nbw) {
     constexpr int NW = NT / 64, BLOCK = NT;
-    static_assert(NW == 4 || NW == 16, "4 or 16 waves");
+    static_assert(NW == 4 || NW == 8 || NW == 16, "4, 8 or 16 waves");
+    constexpr int TOPW = 3;  // lane maxima a wave contributes (16 waves)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int K4 = K >> 2;
     uint32_t mx = 0;  // max |a| bits; NaN shows as > 0x7F800000
@@ -262,7 +264,7 @@ __device__ RowSel row_select(const float* __restrict__ a, int K, const float4 (&
     // rides on the same barrier.
     const bool wnan = __builtin_amdgcn_ballot_w64(mx > 0x7F800000u) != 0;  // NaN bits
     const uint32_t srt = wave_sort_desc(mx);
-    if (NW == 4 || lane < 3) L.ws[wave][lane] = srt;
+    if (NW <= 8 || lane < TOPW) L.ws[wave][lane] = srt;
     if (lane == 0) L.wn[wave] = wnan;
     for (int w = tid; w < nbw; w += BLOCK) bitmap[w] = 0u;
     if (tid < 64) L.rank[tid] = 0u;
@@ -280,10 +282,19 @@ __device__ RowSel row_select(const float* __restrict__ a, int K, const float4 (&
         const uint32_t mx01 = merge_top64(L.ws[0][lane], L.ws[1][63 - lane]);
         const uint32_t mx23 = merge_top64(L.ws[2][lane], L.ws[3][63 - lane]);
         tau = __builtin_amdgcn_readlane(merge_top64(mx01, __shfl(mx23, 63 - lane, 64)), FRQ_T);
+    } else if constexpr (NW == 8) {
+        // the 33rd largest thread maximum, the eight lists merged pairwise
+        const uint32_t mx01 = merge_top64(L.ws[0][lane], L.ws[1][63 - lane]);
+        const uint32_t mx23 = merge_top64(L.ws[2][lane], L.ws[3][63 - lane]);
+        const uint32_t mx45 = merge_top64(L.ws[4][lane], L.ws[5][63 - lane]);
+        const uint32_t mx67 = merge_top64(L.ws[6][lane], L.ws[7][63 - lane]);
+        const uint32_t mx03 = merge_top64(mx01, __shfl(mx23, 63 - lane, 64));
+        const uint32_t mx47 = merge_top64(mx45, __shfl(mx67, 63 - lane, 64));
+        tau = __builtin_amdgcn_readlane(merge_top64(mx03, __shfl(mx47, 63 - lane, 64)), FRQ_T);
     } else {
         // the 33rd largest of the waves' top-3 lane maxima: 48 distinct
         // elements, so at least 33 elements are >= it
-        const uint32_t t3 = lane < 3 * NW ? L.ws[lane / 3][lane % 3] : 0u;
+        const uint32_t t3 = lane < TOPW * NW ? L.ws[lane / TOPW][lane % TOPW] : 0u;
         tau = __builtin_amdgcn_readlane(wave_sort_desc(t3), FRQ_T);
     }
     // compact candidates into per-wave regions of cand[] (FCAP/4 keys each),
