@@ -9,12 +9,13 @@
       register / LDS / scratch use.
 
   python3 -m fieldrun_amd.rocprof_summary steps KERNEL_TRACE_CSV --marker SUBSTR
-          [--exclude SUBSTR ...] [--command CMD]
+          [--exclude SUBSTR ...] [--by-prev] [--command CMD]
       per-step time of each (kernel, workgroup count) over a run of decode
       steps: the trace (in start order) is cut at each launch of the kernel
       whose name contains the marker (one a step, e.g. the head), intervals
       holding a kernel whose name contains an --exclude string (a prefill's)
-      are dropped, and each kernel's time is averaged over the kept steps.
+      are dropped, and each kernel's time is averaged over the kept steps
+      (--by-prev: each (kernel, grid) split by the kernel launched before it).
 
   python3 -m fieldrun_amd.rocprof_summary pmc --fetch CSV --write CSV
           --kernel NAME --copy-bytes N --algo-bytes B [--command-fetch CMD]
@@ -115,10 +116,16 @@ def steps(args) -> str:
             continue
         kept += 1
         span += (int(seg[-1]["End_Timestamp"]) - int(seg[0]["Start_Timestamp"])) / 1e3
+        prev = short_name(rows[a]["Kernel_Name"])
         for r in seg:
-            key = (short_name(r["Kernel_Name"]), int(r["Grid_Size_X"]) // max(1, int(r["Workgroup_Size_X"])))
+            name = short_name(r["Kernel_Name"])
+            # --by-prev: launches of one kernel and grid told apart by the
+            # kernel launched before them (e.g. two linears of a layer)
+            key = (name if not args.by_prev else f"{name} after {prev.split('<')[0]}",
+                   int(r["Grid_Size_X"]) // max(1, int(r["Workgroup_Size_X"])))
             acc[key] += (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
             cnt[key] += 1
+            prev = name
     out = []
     if args.command:
         out += ["Command:", "", "    " + args.command, ""]
@@ -247,6 +254,7 @@ def main(argv=None):
     st.add_argument("--exclude", action="append", default=[])
     st.add_argument("--top", type=int, default=25)
     st.add_argument("--command", default="")
+    st.add_argument("--by-prev", action="store_true")
     p = sub.add_parser("pmc")
     p.add_argument("--fetch", required=True)
     p.add_argument("--write", required=True)
