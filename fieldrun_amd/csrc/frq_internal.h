@@ -272,11 +272,15 @@ constexpr int seq_sum_spec_scratch(int nt) { return 2 * ((nt / 64) * 128) + 6 * 
 // start is not among the candidates (rows whose rounding drifts further,
 // constant rows, non-finite values) the remaining segments are folded again
 // from the true value.  The result never depends on the estimates, only the
-// time does.
-template <int NT>
+// time does.  NF < NT: only the first NF threads fold (S = 2 NF / 64), the
+// others take part in the barriers only (the candidate chains are VALU
+// work, 64 adds an element whatever S is, while the barriers and the
+// resolve grow with S).
+template <int NT, int NF = NT>
 __device__ __forceinline__ float seq_sum_spec(const float* p, int n, float init, float* sc) {
-    constexpr int S = 2 * (NT / 64), C = 64;
+    constexpr int S = 2 * (NF / 64), C = 64;
     static_assert(S <= 64, "a lane of wave 0 a segment");
+    static_assert(NF <= NT && NF % 64 == 0, "whole waves of the workgroup");
     const int tid = threadIdx.x, lane = tid & 63, hl = lane & 31;
     const int k = 2 * (tid >> 6) + (lane >> 5);  // this half-wave's segment
     float* ends = sc;                                      // [S][C] candidate ends
@@ -300,7 +304,7 @@ __device__ __forceinline__ float seq_sum_spec(const float* p, int n, float init,
     ps += __builtin_bit_cast(float, xshfl<4>(__builtin_bit_cast(uint32_t, ps)));
     ps += __builtin_bit_cast(float, xshfl<2>(__builtin_bit_cast(uint32_t, ps)));
     ps += __builtin_bit_cast(float, xshfl<1>(__builtin_bit_cast(uint32_t, ps)));
-    if (hl == 0) psum[k] = ps;
+    if (hl == 0 && k < S) psum[k] = ps;
     __syncthreads();
     float pv[S];  // every segment's sum, read at once
 #pragma unroll
@@ -311,12 +315,14 @@ __device__ __forceinline__ float seq_sum_spec(const float* p, int n, float init,
         if (kk < k) pre += (double)pv[kk];
     const uint32_t eb = __float_as_uint((float)pre);
     const uint32_t ebn = __float_as_uint((float)(pre + (double)pv[k < S - 1 ? k : 0]));  // segment k+1's
-    if (hl == 0) est[k] = eb;
+    if (hl == 0 && k < S) est[k] = eb;
     float c0 = k == 0 ? init : __uint_as_float(eb + (uint32_t)hl - (uint32_t)(C / 2));
     float c1 = k == 0 ? init : __uint_as_float(eb + (uint32_t)hl);
     if (lo < hi) lds_seq_sum2(p + lo, hi - lo, c0, c1);
-    ends[k * C + hl] = c0;  // candidate start eb + hl - C/2
-    ends[k * C + hl + C / 2] = c1;
+    if (k < S) {
+        ends[k * C + hl] = c0;  // candidate start eb + hl - C/2
+        ends[k * C + hl + C / 2] = c1;
+    }
     // the candidate of segment k+1 that each of these ends selects (or -1)
     int* nxs = reinterpret_cast<int*>(ends + S * C) + 3 * S + 1;  // [S][C]
     auto sel = [&](float e) {

@@ -32,6 +32,20 @@ __device__ __forceinline__ int dot16(const int4 a, const int4 w, int acc) {
     return acc;
 }
 
+// Sum over aligned runs of LW lanes (LW a power of two <= 64), every lane
+// of a run getting it: butterfly exchanges in DPP / permlane (xshfl), no
+// LDS round trips.
+template <int LW>
+__device__ __forceinline__ int lane_sum(int v) {
+    if constexpr (LW >= 64) v += (int)xshfl<32>((uint32_t)v);
+    if constexpr (LW >= 32) v += (int)xshfl<16>((uint32_t)v);
+    if constexpr (LW >= 16) v += (int)xshfl<8>((uint32_t)v);
+    if constexpr (LW >= 8) v += (int)xshfl<4>((uint32_t)v);
+    if constexpr (LW >= 4) v += (int)xshfl<2>((uint32_t)v);
+    if constexpr (LW >= 2) v += (int)xshfl<1>((uint32_t)v);
+    return v;
+}
+
 __device__ __forceinline__ int wave_sum(int v) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
@@ -209,8 +223,7 @@ __global__ __launch_bounds__(256) void gemv3_i8_kernel(
         int acc = 0;
 #pragma unroll
         for (int i = 0; i < CPL; ++i) acc = dot16(x[i], w[i], acc);
-#pragma unroll
-        for (int off = L / 2; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+        acc = lane_sum<L>(acc);
         if (sub == 0) accs[buf][rloc] = acc;
         if (qw) {
 #pragma unroll
@@ -438,8 +451,7 @@ __global__ __launch_bounds__(NT) void linear_m1_kernel(
         // single-buffered: the next group's weights go out as soon as the dot
         // has consumed these, overlapping the reduction and the epilogue
         if (!DB && !PB && rgn < n_rg) load_w(gn, w);
-#pragma unroll
-        for (int off = LW / 2; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+        acc = lane_sum<LW>(acc);
         if (sub % LW == 0) accs[buf][rloc * WPR + sub / LW] = acc;
         if (qw) {
 #pragma unroll
