@@ -1479,9 +1479,6 @@ __device__ __forceinline__ long i4_bop(uint32_t w) {
     return (long)(((unsigned long long)hi << 32) | lo);
 }
 
-__device__ __attribute__((noinline)) float i4_exact(const float* __restrict__ x, const ExpView& v, size_t e, int j) {
-    return exact_ex<FRQ_DT_I4>(x, v, e, j);
-}
 
 template <int NGT>
 __device__ __forceinline__ void i4_body(const I4Args& A, uint2 (*As)[I4_AS], const int* srcs, int e, int rows,
@@ -1585,9 +1582,96 @@ __device__ __forceinline__ void i4_body(const I4Args& A, uint2 (*As)[I4_AS], con
                 const int j = (cb0 + c) * 16 + col;
                 if (j < A.N) {
                     const float v = so >= 0.0f ? so * acc[t][c]
-                                               : i4_exact(A.xf + (size_t)src * A.K, A.raw, (size_t)e, j);
+                                               : exact_ex<FRQ_DT_I4>(A.xf + (size_t)src * A.K, A.raw, (size_t)e, j);
                     A.y[(size_t)prow * A.N + j] = v;
                 }
+            }
+        }
+    }
+}
+
+// i4_body<1> for tiles of at most 4 rows and at most I4_SQ quads (the
+// decode): every quad's A operands are staged into LDS up front (one
+// barrier, 2 KB a quad: token group 0 of the As layout, quad q at 256 q),
+// and the B words and scales run I4_PF quads ahead in a register ring, so
+// the loop waits on no load it has just issued and has no barrier; the
+// operations and their order are i4_body's, so the values are the same bits.
+constexpr int I4_SQ = 2 * I4_AS / 256, I4_PF = 4;
+
+__device__ __forceinline__ void i4_body_s(const I4Args& A, uint2* As, const int* srcs, int e, int rows, int pbase,
+                                          int cg) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int cb0 = cg * 8 + 2 * wave;
+    const size_t eb = (size_t)e * A.nrb;
+    const uint8_t* qb0 = A.q4e + (eb + min(cb0, A.nrb - 1)) * A.ng4 * 1024 + lane * 16;
+    const uint8_t* qb1 = A.q4e + (eb + min(cb0 + 1, A.nrb - 1)) * A.ng4 * 1024 + lane * 16;
+    const uint16_t* sb0 = A.s4e + (eb + min(cb0, A.nrb - 1)) * A.ng4 * 64 + (lane & 15) * 4;
+    const uint16_t* sb1 = A.s4e + (eb + min(cb0 + 1, A.nrb - 1)) * A.ng4 * 64 + (lane & 15) * 4;
+    const int ng4 = A.ng4;
+    uint4 B0[I4_PF], B1[I4_PF];
+    uint2 S0[I4_PF], S1[I4_PF];
+    auto ldb = [&](int p, int q4) __attribute__((always_inline)) {
+        const int q = min(q4, ng4 - 1);  // clamped: the loads stay unconditional
+        B0[p] = *reinterpret_cast<const uint4*>(qb0 + (size_t)q * 1024);
+        B1[p] = *reinterpret_cast<const uint4*>(qb1 + (size_t)q * 1024);
+        S0[p] = *reinterpret_cast<const uint2*>(sb0 + (size_t)q * 64);
+        S1[p] = *reinterpret_cast<const uint2*>(sb1 + (size_t)q * 64);
+    };
+#pragma unroll
+    for (int p = 0; p < I4_PF; ++p) ldb(p, p);
+    // A of every quad: item (quad, row < 4, digit, 16-byte chunk), as i4_body
+    for (int it = tid; it < 96 * ng4; it += 256) {
+        const int q4 = it / 96, rem = it - 96 * q4, r = rem / 24, dg = (rem % 24) / 8, ch = rem % 8;
+        const uint4 a = *reinterpret_cast<const uint4*>(A.D + ((size_t)srcs[min(r, rows - 1)] * 3 + dg) * A.Kp +
+                                                         (size_t)q4 * 128 + 16 * ch);
+        const int dst = q4 * 256 + (ch >> 1) * 64 + 32 * (ch & 1) + 4 * r + dg;
+        As[dst] = make_uint2(a.x, a.y);
+        As[dst + 16] = make_uint2(a.z, a.w);
+    }
+    for (int i = tid; i < 64 * ng4; i += 256) As[4 * i + 3] = make_uint2(0u, 0u);  // the d == 3 slots
+    __syncthreads();
+    float acc0 = 0.0f, acc1 = 0.0f;
+    for (int q0 = 0; q0 < ng4; q0 += I4_PF) {
+#pragma unroll
+        for (int p = 0; p < I4_PF; ++p) {
+            const int q4 = q0 + p;
+            if (q4 >= ng4) break;  // uniform
+            const uint32_t w0[4] = {B0[p].x, B0[p].y, B0[p].z, B0[p].w}, w1[4] = {B1[p].x, B1[p].y, B1[p].z, B1[p].w};
+            const uint32_t s0[2] = {S0[p].x, S0[p].y}, s1[2] = {S1[p].x, S1[p].y};
+            long b0[4], b1[4];
+            float f0[4], f1[4];
+#pragma unroll
+            for (int gi = 0; gi < 4; ++gi) {
+                b0[gi] = i4_bop(w0[gi]);
+                b1[gi] = i4_bop(w1[gi]);
+                f0[gi] = h2f((uint16_t)(s0[gi >> 1] >> (16 * (gi & 1))));
+                f1[gi] = h2f((uint16_t)(s1[gi >> 1] >> (16 * (gi & 1))));
+            }
+            ldb(p, q4 + I4_PF);  // this slot's next quad
+#pragma unroll
+            for (int gi = 0; gi < 4; ++gi) {
+                const uint2 a = As[q4 * 256 + gi * 64 + lane];
+                const long aop = (long)(((unsigned long long)a.y << 32) | a.x);
+                const v4i c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, b0[gi], v4i{0, 0, 0, 0}, 0, 0, 0);
+                const v4i c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, b1[gi], v4i{0, 0, 0, 0}, 0, 0, 0);
+                const int g0 = c0[0] * 65536 + c0[1] * 256 + c0[2], g1 = c1[0] * 65536 + c1[1] * 256 + c1[2];
+                acc0 = __builtin_fmaf(f0[gi], (float)g0, acc0);
+                acc1 = __builtin_fmaf(f1[gi], (float)g1, acc1);
+            }
+        }
+    }
+    const int col = lane & 15, i = lane >> 4;
+    if (i < rows) {
+        const int prow = pbase + i, src = srcs[i];
+        const float so = A.dso[src];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const int j = (cb0 + c) * 16 + col;
+            if (j < A.N) {
+                const float v = so >= 0.0f ? so * (c ? acc1 : acc0)
+                                           : exact_ex<FRQ_DT_I4>(A.xf + (size_t)src * A.K, A.raw, (size_t)e, j);
+                A.y[(size_t)prow * A.N + j] = v;
             }
         }
     }
@@ -1624,12 +1708,219 @@ __global__ __launch_bounds__(256) void moe_i4_kernel(I4Args A0, I4Args A1, int n
     // each argument block read in place (a reference chosen between the two
     // at run time would copy both to scratch)
     auto run = [&](const I4Args& A) __attribute__((always_inline)) {
-        if (rows <= 4) i4_body<1>(A, As, srcs, e, rows, pbase, cg);
+        if (rows <= 4 && A.ng4 <= I4_SQ) i4_body_s(A, &As[0][0], srcs, e, rows, pbase, cg);
+        else if (rows <= 4) i4_body<1>(A, As, srcs, e, rows, pbase, cg);
         else if (rows <= 16) i4_body<4>(A, As, srcs, e, rows, pbase, cg);
         else i4_body<8>(A, As, srcs, e, rows, pbase, cg);
     };
     if (second) run(A1);
     else run(A0);
+}
+
+// ---- int4 decode (T == 1, SiLU): two launches -------------------------------
+// The batched path's values (digit rows as row_digits, i4_body's group order
+// and epilogue, act_digits's h, combine_kernel's order), so the same bits,
+// in two launches instead of seven.  A lane's MFMA A operand is read from a
+// compact digit row in LDS (rows dr[dg][k], dg 0..2 = d2, d1, d0; token row 0
+// only, the other rows of the operand zero).
+__device__ __forceinline__ long i4_dec_aop(const int8_t* dr, int kp, int q4, int gi, int lane) {
+    const int dg = lane & 3, tl = (lane >> 2) & 3, qq = lane >> 4;
+    if (tl != 0 || dg == 3) return 0;
+    const uint2 a = *reinterpret_cast<const uint2*>(dr + (size_t)dg * kp + q4 * 128 + gi * 32 + 8 * qq);
+    return (long)(((unsigned long long)a.y << 32) | a.x);
+}
+
+// the three digits of v at scale reciprocal r (row_digits), zero unless ok
+__device__ __forceinline__ void i4_dec_digits(float v, float r, bool ok, int8_t* dr, int kp, int k) {
+    int d2 = 0, d1 = 0, d0 = 0;
+    if (ok) {
+        float xf = rintf(v * r);
+        xf = fminf(fmaxf(xf, -XMAXD), XMAXD);
+        const int X = (int)xf;
+        d0 = (int)(int8_t)(X & 0xFF);
+        const int X1 = (X - d0) >> 8;
+        d1 = (int)(int8_t)(X1 & 0xFF);
+        d2 = (X1 - d1) >> 8;
+    }
+    dr[k] = (int8_t)d2;
+    dr[kp + k] = (int8_t)d1;
+    dr[2 * kp + k] = (int8_t)d0;
+}
+
+// i4_body's quad loop for one token row over two 16-column blocks (B words
+// of block b at qb[b] / scales sb[b], I4_PF quads ahead in registers):
+// acc[b] += scale * G over the groups in order.
+__device__ __forceinline__ void i4_dec_loop(const uint8_t* const (&qb)[2], const uint16_t* const (&sb)[2],
+                                            const int8_t* dr, int kp, int ng4, int lane, float (&acc)[2]) {
+    uint4 B0[I4_PF], B1[I4_PF];
+    uint2 S0[I4_PF], S1[I4_PF];
+    auto ldb = [&](int p, int q4) __attribute__((always_inline)) {
+        const int q = min(q4, ng4 - 1);
+        B0[p] = *reinterpret_cast<const uint4*>(qb[0] + (size_t)q * 1024);
+        B1[p] = *reinterpret_cast<const uint4*>(qb[1] + (size_t)q * 1024);
+        S0[p] = *reinterpret_cast<const uint2*>(sb[0] + (size_t)q * 64);
+        S1[p] = *reinterpret_cast<const uint2*>(sb[1] + (size_t)q * 64);
+    };
+#pragma unroll
+    for (int p = 0; p < I4_PF; ++p) ldb(p, p);
+    acc[0] = acc[1] = 0.0f;
+    for (int q0 = 0; q0 < ng4; q0 += I4_PF) {
+#pragma unroll
+        for (int p = 0; p < I4_PF; ++p) {
+            const int q4 = q0 + p;
+            if (q4 >= ng4) break;  // uniform
+            const uint32_t w0[4] = {B0[p].x, B0[p].y, B0[p].z, B0[p].w}, w1[4] = {B1[p].x, B1[p].y, B1[p].z, B1[p].w};
+            const uint32_t s0[2] = {S0[p].x, S0[p].y}, s1[2] = {S1[p].x, S1[p].y};
+            long b0[4], b1[4];
+            float f0[4], f1[4];
+#pragma unroll
+            for (int gi = 0; gi < 4; ++gi) {
+                b0[gi] = i4_bop(w0[gi]);
+                b1[gi] = i4_bop(w1[gi]);
+                f0[gi] = h2f((uint16_t)(s0[gi >> 1] >> (16 * (gi & 1))));
+                f1[gi] = h2f((uint16_t)(s1[gi >> 1] >> (16 * (gi & 1))));
+            }
+            ldb(p, q4 + I4_PF);
+#pragma unroll
+            for (int gi = 0; gi < 4; ++gi) {
+                const long aop = i4_dec_aop(dr, kp, q4, gi, lane);
+                const v4i c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, b0[gi], v4i{0, 0, 0, 0}, 0, 0, 0);
+                const v4i c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, b1[gi], v4i{0, 0, 0, 0}, 0, 0, 0);
+                const int g0 = c0[0] * 65536 + c0[1] * 256 + c0[2], g1 = c1[0] * 65536 + c1[1] * 256 + c1[2];
+                acc[0] = __builtin_fmaf(f0[gi], (float)g0, acc[0]);
+                acc[1] = __builtin_fmaf(f1[gi], (float)g1, acc[1]);
+            }
+        }
+    }
+}
+
+// I1: workgroup (slot s of the k picks in ascending expert id, 4 column
+// blocks of h).  Wave 0 routes the token while waves 1..3 take max|x|; every
+// thread then forms digits of x into LDS, and wave w runs the quad loop over
+// gate and up column block 4 by + w, then lanes 0..15 write h = silu(g) * u.
+// Workgroup (0, 0) publishes the picks (ws.sel / ws.w, ascending expert id).
+__global__ __launch_bounds__(256) void moe_i4_dec_gu_kernel(
+    const float* __restrict__ x, const float* __restrict__ logits, int E, int topk, int norm_topk,
+    const float* __restrict__ pes, I4Args G, I4Args U, int mi, float* __restrict__ h, MoeWs ws,
+    int* __restrict__ err) {
+    extern __shared__ __attribute__((aligned(16))) float dsm[];
+    float* p = dsm;                                        // [E]
+    int* pe = reinterpret_cast<int*>(dsm + E);             // [topk] picks, pick order
+    float* pw = dsm + E + topk;
+    int* se = reinterpret_cast<int*>(dsm + E + 2 * topk);  // [topk] ascending expert id
+    float* sw = dsm + E + 3 * topk;
+    float* red = dsm + E + 4 * topk;                       // [8]
+    int* bad_l = reinterpret_cast<int*>(red + 9);
+    int8_t* dr = reinterpret_cast<int8_t*>(dsm + ((E + 4 * topk + 10 + 3) & ~3));  // [3][kp]
+    const int slot = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int d = G.K, ng4 = G.ng4, kp = 128 * ng4;
+    if (wave == 0) {
+        const bool bad = route_wave(logits, E, topk, norm_topk, pes, p, pe, pw);
+        for (int i = lane; i < topk; i += 64) {
+            int r = 0;
+            for (int j = 0; j < topk; ++j) r += pe[j] < pe[i];
+            se[r] = pe[i];
+            sw[r] = pw[i];
+        }
+        if (lane == 0) *bad_l = bad;
+    } else {
+        float mx = 0.0f;
+        bool nf = false;
+        for (int k = tid - 64; k < d; k += 192) {
+            const float xv = x[k];
+            nf |= !(fabsf(xv) <= 3.0e38f);
+            mx = fmaxf(mx, fabsf(xv));
+        }
+        mx = wave_fmax(mx);
+        const bool wnf = __builtin_amdgcn_ballot_w64(nf) != 0;
+        if (lane == 0) {
+            red[wave - 1] = mx;
+            red[4 + wave - 1] = wnf ? 1.0f : 0.0f;
+        }
+    }
+    __syncthreads();
+    if (slot == 0 && blockIdx.y == 0) {
+        if (tid < topk) { ws.sel[tid] = se[tid]; ws.w[tid] = sw[tid]; }
+        if (tid == 0 && *bad_l) atomicOr(err, 1);
+    }
+    const int e = se[slot];
+    const int cb = blockIdx.y * 4 + wave, cbc = min(cb, G.nrb - 1);
+    const size_t eb = (size_t)e * G.nrb;
+    const uint8_t* const qb[2] = {G.q4e + (eb + cbc) * ng4 * 1024 + lane * 16, U.q4e + (eb + cbc) * ng4 * 1024 + lane * 16};
+    const uint16_t* const sb[2] = {G.s4e + (eb + cbc) * ng4 * 64 + (lane & 15) * 4,
+                                   U.s4e + (eb + cbc) * ng4 * 64 + (lane & 15) * 4};
+    // the token's digit row (x_digits_kernel's values)
+    const float mxx = fmaxf(fmaxf(red[0], red[1]), red[2]);
+    const bool xnf = (red[4] + red[5] + red[6]) != 0.0f;
+    const float sx = mxx > 0.0f ? mxx / XMAXD : 1.0f;
+    const bool ok = !xnf && sx >= 1.0e-30f && sx <= 1.0e28f;
+    const float rx = 1.0f / sx;
+    for (int k = tid; k < kp; k += 256) i4_dec_digits(k < d ? x[k] : 0.0f, rx, ok && k < d, dr, kp, k);
+    __syncthreads();
+    float acc[2];
+    i4_dec_loop(qb, sb, dr, kp, ng4, lane, acc);
+    const int j = cb * 16 + lane;
+    if (lane < 16 && j < mi) {
+        const float gv = ok ? sx * acc[0] : exact_ex<FRQ_DT_I4>(x, G.raw, (size_t)e, j);
+        const float uv = ok ? sx * acc[1] : exact_ex<FRQ_DT_I4>(x, U.raw, (size_t)e, j);
+        h[(size_t)slot * mi + j] = silu(gv) * uv;
+    }
+}
+
+// I2: the down rows of all k slots and the combine: wave s takes slot s
+// (ascending expert id), a workgroup two column blocks of the output; each
+// wave forms its row's digits (row_digits's values, act_digits's scale) in
+// its own LDS slab, runs the quad loop over its expert's two down blocks,
+// and the first 32 threads add the slots' w * down in ascending expert id
+// from +0 (combine_kernel's order).
+__global__ __launch_bounds__(1024) void moe_i4_dec_dn_kernel(const float* __restrict__ h, int mi, I4Args D,
+                                                             const int32_t* __restrict__ sel,
+                                                             const float* __restrict__ wsel, int topk,
+                                                             float* __restrict__ out) {
+    extern __shared__ __attribute__((aligned(16))) int8_t dsl[];  // [topk][3][kp]
+    __shared__ float vs[16][32];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int slot = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ng4 = D.ng4, kp = 128 * ng4, dn = D.N;
+    int8_t* dr = dsl + (size_t)slot * 3 * kp;
+    const int e = sel[slot];
+    const int cb0 = blockIdx.x * 2;
+    const size_t eb = (size_t)e * D.nrb;
+    const int c0 = min(cb0, D.nrb - 1), c1 = min(cb0 + 1, D.nrb - 1);
+    const uint8_t* const qb[2] = {D.q4e + (eb + c0) * ng4 * 1024 + lane * 16, D.q4e + (eb + c1) * ng4 * 1024 + lane * 16};
+    const uint16_t* const sb[2] = {D.s4e + (eb + c0) * ng4 * 64 + (lane & 15) * 4,
+                                   D.s4e + (eb + c1) * ng4 * 64 + (lane & 15) * 4};
+    const float* hr = h + (size_t)slot * mi;
+    float mx = 0.0f;
+    bool nf = false;
+    for (int k = lane; k < mi; k += 64) {
+        const float v = hr[k];
+        nf |= !(fabsf(v) <= 3.0e38f);
+        mx = fmaxf(mx, fabsf(v));
+    }
+    mx = wave_fmax(mx);
+    nf = __builtin_amdgcn_ballot_w64(nf) != 0;
+    const float so = mx > 0.0f ? mx / XMAXD : 1.0f;
+    const bool ok = !nf && so >= 1.0e-30f && so <= 1.0e28f;
+    const float r = 1.0f / so;
+    for (int k = lane; k < kp; k += 64) i4_dec_digits(k < mi ? hr[k] : 0.0f, r, ok && k < mi, dr, kp, k);
+    wave_sync();
+    float acc[2];
+    i4_dec_loop(qb, sb, dr, kp, ng4, lane, acc);
+    if (lane < 16) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const int j = (cb0 + c) * 16 + lane;
+            if (j < dn) vs[slot][16 * c + lane] = ok ? so * acc[c] : exact_ex<FRQ_DT_I4>(hr, D.raw, (size_t)e, j);
+        }
+    }
+    __syncthreads();
+    if (tid < 32 && cb0 * 16 + tid < dn) {
+        float a = 0.0f;
+        for (int q = 0; q < topk; ++q) a = a + wsel[q] * vs[q][tid];
+        out[cb0 * 16 + tid] = a;
+    }
 }
 
 // (E, out, ceil(in/2)) i4 rows + (E, out, ceil(in/g)) f16 scales -> q4e / s4e.
@@ -1767,6 +2058,29 @@ static hipError_t launch_moe_ex(const MoeBank& b, const float* x, size_t T, cons
                                 int norm_topk, const float* pes, float* out, void* wsp, int* err, hipStream_t s) {
     MoeWs ws = moe_view(wsp, b, T, topk);
     const int E = (int)b.n_exp, d = (int)b.d, mi = (int)b.mi, gw = (int)b.gw;
+    if (T == 1 && topk <= 16 && b.act == FRQ_ACT_SILU && b.mg.q4e && b.mu.q4e && b.md.q4e) {
+        // int4 decode in two launches (route + digits + gate / up + act,
+        // then the down rows + combine), where the digit rows fit in LDS
+        const ExpMat &mg = b.mg, &mu = b.mu, &md = b.md;
+        const int ng4g = (int)((mg.in + 127) / 128), ng4d = (int)((md.in + 127) / 128);
+        const size_t lds1 = (size_t)((E + 4 * (int)topk + 10 + 3) & ~3) * 4 + 3 * 128 * (size_t)ng4g;
+        const size_t lds2 = topk * 3 * 128 * (size_t)ng4d;
+        if (mg.out == (size_t)mi && mu.out == (size_t)mi && mg.in == (size_t)d && md.in == (size_t)mi &&
+            md.out == (size_t)d && lds1 <= 65536 && lds2 <= 65536) {
+            const I4Args G{nullptr, nullptr, 0, (int)((mg.out + 15) / 16), ng4g, (int)mg.out, (int)mg.in,
+                           mg.q4e, mg.s4e, exp_view(b, mg), x, nullptr};
+            const I4Args U{nullptr, nullptr, 0, (int)((mu.out + 15) / 16), ng4g, (int)mu.out, (int)mu.in,
+                           mu.q4e, mu.s4e, exp_view(b, mu), x, nullptr};
+            const I4Args Dn{nullptr, nullptr, 0, (int)((md.out + 15) / 16), ng4d, (int)md.out, (int)md.in,
+                            md.q4e, md.s4e, exp_view(b, md), ws.h, nullptr};
+            moe_i4_dec_gu_kernel<<<dim3((unsigned)topk, (unsigned)((G.nrb + 3) / 4)), dim3(256), lds1, s>>>(
+                x, logits, E, (int)topk, norm_topk, pes, G, U, mi, ws.h, ws, err);
+            if (hipError_t e1 = hipGetLastError()) return e1;
+            moe_i4_dec_dn_kernel<<<dim3((unsigned)((Dn.nrb + 1) / 2)), dim3((unsigned)(64 * topk)), lds2, s>>>(
+                ws.h, mi, Dn, ws.sel, ws.w, (int)topk, out);
+            return hipGetLastError();
+        }
+    }
     const size_t tr = moe_tile_rows(T);
     hipError_t e = launch_moe_route(logits, T, b.n_exp, topk, norm_topk, pes, ws.sel, ws.w, err, s);
     if (e != hipSuccess) return e;
