@@ -141,7 +141,7 @@ def main():
     ap.add_argument("--only-gemma2", action="store_true",
                     help="only configs[2]'s Gemma-2 decode (batch 1 and batch 16) and print its detail entry "
                          "(for profiling those runs; combine with --no-graphs under rocprofv3)")
-    ap.add_argument("--pmc-what", default="layer", choices=["layer", "int4", "m128", "moe"],
+    ap.add_argument("--pmc-what", default="layer", choices=["layer", "int4", "m128", "moe", "moe4"],
                     help="counter workload: the configs[4] layer's four decode linears (default), the int4 "
                          "M=1 GEMV at the Gemma-2 shapes, the int8 linear at M=128, or configs[3]'s MoE "
                          "layer at T=1 and T=512")
@@ -218,11 +218,18 @@ def main():
                 for w in reps:
                     w.free()
             return
-        if args.pmc_what == "moe":
-            # the Qwen3-MoE routed layer at T=1 and T=512, 9 calls each
+        if args.pmc_what in ("moe", "moe4"):
+            # the Qwen3-MoE routed layer at T=1 and T=512, 9 calls each (moe4: int4 experts, g 32)
             E, d, mi, topk = 128, 2048, 768, 8
-            gate, gs, up, us_, down, ds = synth.moe_layer(E, d, mi, synth.seed(3))
-            bank = ctx.upload_moe_i8(gate, gs, up, us_, down, ds)
+            if args.pmc_what == "moe":
+                gate, gs, up, us_, down, ds = synth.moe_layer(E, d, mi, synth.seed(3))
+                bank = ctx.upload_moe_i8(gate, gs, up, us_, down, ds)
+            else:
+                gate, up, down = synth.moe_layer_ex(E, d, mi, synth.seed(3), "int4")
+                pick = lambda lst, key: [m[key] for m in lst]  # noqa: E731
+                bank = ctx.upload_moe("i4", d, mi, pick(gate, "raw"), pick(down, "raw"), pick(up, "raw"),
+                                      pick(gate, "scale"), pick(up, "scale"), pick(down, "scale"), g=32)
+                del gate, up, down
             for T in (1, 512):
                 rng = np.random.default_rng(synth.seed(3, T))
                 x = hip.DeviceArray.from_numpy(rng.standard_normal((T, d), dtype=np.float32))
