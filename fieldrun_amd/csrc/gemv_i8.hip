@@ -555,10 +555,12 @@ hipError_t lm1_dispatch(const Weight& w, int g, F f) {
     if (nch <= 128) return f.template operator()<64, 2, true, 2, 256>(g ? g : 1024);
     // rows of 2049..4096 bytes: one 512-thread workgroup a CU (8-row groups,
     // two in flight during the quant; the quant once a CU, half the
-    // elements a thread), two a CU for long outputs (N >= 16384: gate|up);
+    // elements a thread), two a CU for long outputs (N >= 12288: gate|up);
     // measured against two / four 256-thread workgroups a CU: o 9.64 ->
-    // 8.3 us, q|k|v 9.78 -> 9.56, gate|up 27.3 -> 26.0 (configs[4] shapes)
-    if (nch <= 256) return f.template operator()<64, 4, true, 2, 512>(g ? g : (w.n >= 16384 ? 512 : 256));
+    // 8.3 us, q|k|v 9.78 -> 9.56, gate|up 27.3 -> 26.0 (configs[4] shapes);
+    // the two-a-CU threshold: K 4096 N 14336 16.2 -> 15.2 us, K 3584 N
+    // 12288 14.5 -> 14.2, but N 8192 11.5 -> 12.5
+    if (nch <= 256) return f.template operator()<64, 4, true, 2, 512>(g ? g : (w.n >= 12288 ? 512 : 256));
     if (nch <= 512) return f.template operator()<64, 8, true, 8, 256>(g ? g : 512);
     // long rows: 1024 threads (a quarter of the quant per thread), every
     // workgroup's first group in flight during the quant
