@@ -172,9 +172,10 @@ def test_i8_sweep_full_shapes(ctx, k, n):
         assert np.array_equal(acc[r], racc)
         mag = corr_mag(a[r], wt, scale, racc)
         assert np.all(np.abs(out[r].astype(np.float64) - ref) <= 1e-6 * mag + 1e-30)
-    # the decode batches (M = 4 and 16): every row bit-exact (the multi-row
-    # MFMA path keeps the reference's epilogue order)
-    for m in (4, 16):
+    # the decode batches (M = 2 .. 16, ragged ones included: token rows past
+    # M are zero lanes of the 16-row MFMA tile): every row bit-exact (the
+    # multi-row MFMA path keeps the reference's epilogue order)
+    for m in (2, 3, 4, 7, 16):
         ref = oracle.mm_i8_mt(a[:m], wt, scale, 16)
         assert np.array_equal(w.mm(a[:m]).view(np.uint32), ref.view(np.uint32)), m
 
